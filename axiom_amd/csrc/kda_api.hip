@@ -1,0 +1,306 @@
+// C ABI of the KDA hot path: argument validation, workspace layout, dispatch.
+#include "../../include/kda_mi355x.h"
+
+#include <cmath>
+#include <cstdarg>
+#include <cstdio>
+#include <cstring>
+
+#include "kda_common.h"
+#include "kda_internal.h"
+
+namespace {
+
+thread_local char g_err[512] = "";
+
+int fail(int code, const char* fmt, ...) {
+  va_list ap;
+  va_start(ap, fmt);
+  std::vsnprintf(g_err, sizeof(g_err), fmt, ap);
+  va_end(ap);
+  return code;
+}
+
+int hip_fail(hipError_t e, const char* what) {
+  return fail(KDA_ERR_HIP, "%s: %s", what, hipGetErrorString(e));
+}
+
+constexpr int kC = 64;
+constexpr size_t kAlign = 256;
+
+size_t align_up(size_t x) { return (x + kAlign - 1) / kAlign * kAlign; }
+
+struct WsLayout {
+  size_t W, U, AQ, GQ, LK, GC;
+  size_t cu_clamped, chunk_off, n_units, order, flags;
+  size_t total;
+  int64_t units_bound;
+};
+
+bool is_exact(int in_dtype) { return in_dtype == KDA_DTYPE_F32; }
+
+// n_seqs <= 0: dense
+WsLayout ws_layout(int B, int T, int H, int dk, int dv, int32_t n_seqs, int in_dtype) {
+  WsLayout L{};
+  const size_t es = is_exact(in_dtype) ? 4 : 2;
+  int64_t units;
+  if (n_seqs > 0) {
+    units = (static_cast<int64_t>(T) + 63LL * n_seqs) / kC;
+  } else {
+    units = static_cast<int64_t>(B) * ((static_cast<int64_t>(T) + kC - 1) / kC);
+  }
+  L.units_bound = units;
+  const int64_t ch = units * H;
+  size_t off = 0;
+  auto take = [&](size_t bytes) { size_t at = off; off = align_up(off + bytes); return at; };
+  L.W = take(static_cast<size_t>(ch) * kC * dk * es);
+  L.GQ = take(static_cast<size_t>(ch) * kC * dk * es);
+  L.LK = take(static_cast<size_t>(ch) * kC * dk * es);
+  L.U = take(static_cast<size_t>(ch) * kC * dv * es);
+  L.AQ = take(static_cast<size_t>(ch) * kC * kC * es);
+  L.GC = take(static_cast<size_t>(ch) * dk * 4);
+  if (n_seqs > 0) {
+    L.cu_clamped = take(static_cast<size_t>(n_seqs + 1) * 4);
+    L.chunk_off = take(static_cast<size_t>(n_seqs + 1) * 4);
+    L.n_units = take(4);
+    L.order = take(static_cast<size_t>(n_seqs) * 4);
+    L.flags = take(4);
+  }
+  L.total = off;
+  return L;
+}
+
+bool dim_ok(int d) { return d == 64 || d == 128; }
+
+int check_dims(int H, int dk, int dv) {
+  if (H < 1) return fail(KDA_ERR_INVALID_ARGUMENT, "H=%d must be >= 1", H);
+  if (dk < 1 || dv < 1) return fail(KDA_ERR_INVALID_ARGUMENT, "dk=%d, dv=%d must be >= 1", dk, dv);
+  if (!dim_ok(dk) || dk != dv)
+    return fail(KDA_ERR_UNSUPPORTED, "head dims dk=%d, dv=%d: this build runs dk == dv in {64, 128}", dk, dv);
+  return KDA_OK;
+}
+
+template <typename T>
+T* at(void* base, size_t off) { return reinterpret_cast<T*>(static_cast<char*>(base) + off); }
+
+int chunk_fwd_impl(hipStream_t stream, const void* q, const void* k, const void* v,
+                   const void* g, const void* beta, const float* h0,
+                   const int32_t* cu_seqlens, int32_t n_seqs, void* o, float* ht,
+                   int B, int T, int H, int dk, int dv, int chunk, float scale,
+                   int in_dtype, int out_dtype, void* ws, size_t ws_bytes) {
+  if (!q || !k || !v || !g || !beta) return fail(KDA_ERR_INVALID_ARGUMENT, "null input pointer");
+  if (!o && T > 0) return fail(KDA_ERR_INVALID_ARGUMENT, "null output pointer o");
+  if (B < 1) return fail(KDA_ERR_INVALID_ARGUMENT, "B=%d must be >= 1", B);
+  if (T < 0) return fail(KDA_ERR_INVALID_ARGUMENT, "T=%d must be >= 0", T);
+  if (int rc = check_dims(H, dk, dv)) return rc;
+  if (chunk != kC) return fail(KDA_ERR_UNSUPPORTED, "chunk=%d: this build runs chunk == 64", chunk);
+  if (in_dtype < KDA_DTYPE_F32 || in_dtype > KDA_DTYPE_BF16_F32GATES)
+    return fail(KDA_ERR_INVALID_ARGUMENT, "in_dtype=%d is not a kda_dtype_t", in_dtype);
+  if (out_dtype != KDA_DTYPE_F32 && out_dtype != KDA_DTYPE_BF16)
+    return fail(KDA_ERR_INVALID_ARGUMENT, "out_dtype=%d: o is emitted as F32 or BF16", out_dtype);
+  if (!std::isfinite(scale)) return fail(KDA_ERR_INVALID_ARGUMENT, "scale must be finite");
+  const bool varlen = cu_seqlens != nullptr;
+  if (varlen) {
+    if (B != 1) return fail(KDA_ERR_INVALID_ARGUMENT, "cu_seqlens requires B == 1 (got B=%d)", B);
+    if (n_seqs < 1) return fail(KDA_ERR_INVALID_ARGUMENT, "n_seqs=%d must be >= 1 with cu_seqlens", n_seqs);
+  }
+  const int64_t elems = static_cast<int64_t>(B) * T * H * (dk > dv ? dk : dv);
+  if (elems >= (1LL << 40)) return fail(KDA_ERR_INVALID_ARGUMENT, "problem too large");
+  const WsLayout L = ws_layout(B, T, H, dk, dv, varlen ? n_seqs : 0, in_dtype);
+  if (L.units_bound * H > 0x7FFFFFFFLL) return fail(KDA_ERR_INVALID_ARGUMENT, "too many chunk-heads");
+  if (ws == nullptr || ws_bytes < L.total)
+    return fail(KDA_ERR_WORKSPACE, "workspace of %zu bytes is too small (need %zu)", ws_bytes, L.total);
+
+  const bool exact = is_exact(in_dtype);
+  int dtq, dtg;
+  switch (in_dtype) {
+    case KDA_DTYPE_F32: dtq = 0; dtg = 0; break;
+    case KDA_DTYPE_BF16: dtq = 1; dtg = 1; break;
+    case KDA_DTYPE_F16: dtq = 2; dtg = 2; break;
+    default: dtq = 1; dtg = 0; break;
+  }
+
+  kda::Geom G{};
+  G.B = B; G.T = T; G.H = H;
+  G.NT = (T + kC - 1) / kC;
+  G.N = varlen ? n_seqs : B;
+  if (varlen) {
+    G.cu = cu_seqlens;
+    G.cu_clamped = at<int32_t>(ws, L.cu_clamped);
+    G.chunk_off = at<int32_t>(ws, L.chunk_off);
+    G.n_units = at<int32_t>(ws, L.n_units);
+    G.order = at<int32_t>(ws, L.order);
+    hipError_t e = kda::launch_varlen_prep(cu_seqlens, n_seqs, T, at<int32_t>(ws, L.cu_clamped),
+                                           at<int32_t>(ws, L.chunk_off), at<int32_t>(ws, L.n_units),
+                                           at<int32_t>(ws, L.order), at<int32_t>(ws, L.flags), stream);
+    if (e != hipSuccess) return hip_fail(e, "varlen prep launch");
+  }
+
+  kda::IntraArgs ia{};
+  ia.geom = G;
+  ia.q = q; ia.k = k; ia.v = v; ia.g = g; ia.beta = beta;
+  ia.scale = scale;
+  ia.W = at<void>(ws, L.W);
+  ia.U = at<void>(ws, L.U);
+  ia.AQ = at<void>(ws, L.AQ);
+  ia.GQ = at<void>(ws, L.GQ);
+  ia.LK = at<void>(ws, L.LK);
+  ia.GC = at<float>(ws, L.GC);
+  const int64_t intra_grid = L.units_bound * H;
+  if (intra_grid > 0) {
+    hipError_t e = kda::launch_intra(ia, dk, dtq, dtg, static_cast<int>(intra_grid), stream);
+    if (e != hipSuccess) return hip_fail(e, "intra kernel launch");
+  }
+
+  kda::StateArgs sa{};
+  sa.geom = G;
+  sa.W = ia.W; sa.U = ia.U; sa.AQ = ia.AQ; sa.GQ = ia.GQ; sa.LK = ia.LK; sa.GC = ia.GC;
+  sa.h0 = h0;
+  sa.o = o;
+  sa.ht = ht;
+  const int splits = dv / 32;
+  const int64_t chains = static_cast<int64_t>(G.N) * H;
+  const int64_t state_grid = ((chains + 7) / 8) * 8 * splits;
+  if (state_grid > 0x7FFFFFFFLL) return fail(KDA_ERR_INVALID_ARGUMENT, "too many chains");
+  hipError_t e = kda::launch_state(sa, dk, exact, out_dtype == KDA_DTYPE_BF16 ? 1 : 0,
+                                   static_cast<int>(state_grid), stream);
+  if (e != hipSuccess) return hip_fail(e, "state kernel launch");
+  return KDA_OK;
+}
+
+}  // namespace
+
+// ----------------------------------------------------------------------------
+// cc_scan adapter kernel: g = log(alpha), beta = mean(beta32 over 32 columns)
+// ----------------------------------------------------------------------------
+namespace kda {
+
+__global__ __launch_bounds__(256) void kda_adapt_kernel(AdaptArgs a) {
+  const int64_t i = static_cast<int64_t>(blockIdx.x) * 256 + threadIdx.x;  // token-head
+  if (i >= a.n_tok_heads) return;
+  const float* al = a.alpha + i * a.dk;
+  float* go = a.g_out + i * a.dk;
+  for (int d = 0; d < a.dk; ++d) go[d] = logf(al[d]);
+  const float* b = a.beta32 + i * 32;
+  float s = 0.f;
+  for (int j = 0; j < 32; ++j) s += b[j];
+  a.beta_out[i] = s * (1.0f / 32.0f);
+}
+
+hipError_t launch_adapt(const AdaptArgs& a, hipStream_t s) {
+  if (a.n_tok_heads == 0) return hipSuccess;
+  const int64_t grid = (a.n_tok_heads + 255) / 256;
+  hipLaunchKernelGGL(kda_adapt_kernel, dim3(static_cast<unsigned>(grid)), dim3(256), 0, s, a);
+  return hipGetLastError();
+}
+
+}  // namespace kda
+
+// ----------------------------------------------------------------------------
+// exported entry points
+// ----------------------------------------------------------------------------
+extern "C" {
+
+int kda_abi_version(void) { return 100; }
+
+const char* kda_last_error(void) { return g_err; }
+
+size_t kda_chunk_fwd_workspace(int B, int T, int H, int dk, int dv, int chunk, int32_t n_seqs,
+                               int in_dtype) {
+  if (B < 1 || T < 0 || H < 1 || !dim_ok(dk) || dk != dv || chunk != kC) return 0;
+  if (in_dtype < KDA_DTYPE_F32 || in_dtype > KDA_DTYPE_BF16_F32GATES) return 0;
+  return ws_layout(B, T, H, dk, dv, n_seqs > 0 ? n_seqs : 0, in_dtype).total;
+}
+
+int kda_chunk_fwd(hipStream_t stream, const void* q, const void* k, const void* v,
+                  const void* g, const void* beta, const float* h0,
+                  const int32_t* cu_seqlens, int32_t n_seqs, void* o, float* ht,
+                  int B, int T, int H, int dk, int dv, int chunk, float scale,
+                  int in_dtype, int out_dtype, void* workspace, size_t workspace_bytes) {
+  g_err[0] = '\0';
+  return chunk_fwd_impl(stream, q, k, v, g, beta, h0, cu_seqlens, n_seqs, o, ht, B, T, H, dk, dv,
+                        chunk, scale, in_dtype, out_dtype, workspace, workspace_bytes);
+}
+
+int kda_varlen_status(hipStream_t stream, const void* workspace, size_t workspace_bytes,
+                      int B, int T, int H, int dk, int dv, int chunk, int32_t n_seqs,
+                      int in_dtype, int32_t* flags_out) {
+  g_err[0] = '\0';
+  if (!workspace || !flags_out) return fail(KDA_ERR_INVALID_ARGUMENT, "null pointer");
+  if (n_seqs < 1) return fail(KDA_ERR_INVALID_ARGUMENT, "n_seqs=%d must be >= 1", n_seqs);
+  const size_t need = kda_chunk_fwd_workspace(B, T, H, dk, dv, chunk, n_seqs, in_dtype);
+  if (need == 0 || workspace_bytes < need) return fail(KDA_ERR_WORKSPACE, "workspace does not match");
+  const WsLayout L = ws_layout(B, T, H, dk, dv, n_seqs, in_dtype);
+  hipError_t e = hipMemcpyAsync(flags_out, static_cast<const char*>(workspace) + L.flags, 4,
+                                hipMemcpyDeviceToHost, stream);
+  if (e != hipSuccess) return hip_fail(e, "flags copy");
+  e = hipStreamSynchronize(stream);
+  if (e != hipSuccess) return hip_fail(e, "stream synchronize");
+  return KDA_OK;
+}
+
+int kda_recurrent_step(hipStream_t stream, const void* q, const void* k, const void* v,
+                       const void* g, const void* beta, float* state, void* o,
+                       int B, int H, int dk, int dv, float scale, int in_dtype, int out_dtype) {
+  g_err[0] = '\0';
+  if (!q || !k || !v || !g || !beta || !state || !o)
+    return fail(KDA_ERR_INVALID_ARGUMENT, "null pointer");
+  if (B < 1) return fail(KDA_ERR_INVALID_ARGUMENT, "B=%d must be >= 1", B);
+  if (int rc = check_dims(H, dk, dv)) return rc;
+  if (in_dtype < KDA_DTYPE_F32 || in_dtype > KDA_DTYPE_F16)
+    return fail(KDA_ERR_INVALID_ARGUMENT, "in_dtype=%d: decode takes F32, BF16 or F16", in_dtype);
+  if (out_dtype != KDA_DTYPE_F32 && out_dtype != KDA_DTYPE_BF16)
+    return fail(KDA_ERR_INVALID_ARGUMENT, "out_dtype=%d: o is emitted as F32 or BF16", out_dtype);
+  if (!std::isfinite(scale)) return fail(KDA_ERR_INVALID_ARGUMENT, "scale must be finite");
+  const int64_t grid = static_cast<int64_t>(B) * H;
+  if (grid > 0x7FFFFFFFLL) return fail(KDA_ERR_INVALID_ARGUMENT, "B*H too large");
+  kda::DecodeArgs a{};
+  a.q = q; a.k = k; a.v = v; a.g = g; a.beta = beta;
+  a.state = state; a.o = o; a.scale = scale;
+  hipError_t e = kda::launch_decode(a, dk, in_dtype, out_dtype == KDA_DTYPE_BF16 ? 1 : 0,
+                                    static_cast<int>(grid), stream);
+  if (e != hipSuccess) return hip_fail(e, "decode kernel launch");
+  return KDA_OK;
+}
+
+size_t kda_cc_scan_workspace(int T, int H, int dk, int dv, int chunk) {
+  if (T < 0 || H < 1 || !dim_ok(dk) || dk != dv || chunk < 1) return 0;
+  const size_t adapt = align_up(static_cast<size_t>(T) * H * dk * 4) +
+                       align_up(static_cast<size_t>(T) * H * 4);
+  return adapt + ws_layout(1, T, H, dk, dv, 0, KDA_DTYPE_BF16_F32GATES).total;
+}
+
+int kda_cc_scan(hipStream_t stream, const void* q, const void* k, const void* v,
+                const float* alpha, const float* beta32, const float* S_in,
+                float* o, float* S_out, int T, int H, int dk, int dv, int tile, int chunk,
+                void* workspace, size_t workspace_bytes) {
+  g_err[0] = '\0';
+  if (!q || !k || !v || !alpha || !beta32 || !S_in || !o || !S_out)
+    return fail(KDA_ERR_INVALID_ARGUMENT, "null pointer");
+  if (T < 0) return fail(KDA_ERR_INVALID_ARGUMENT, "T=%d must be >= 0", T);
+  if (chunk < 1) return fail(KDA_ERR_INVALID_ARGUMENT, "chunk=%d must be >= 1", chunk);
+  if (T % chunk)
+    return fail(KDA_ERR_INVALID_ARGUMENT, "T=%d must be a multiple of the chunk width C=%d", T, chunk);
+  if (tile < 1 || tile > 16)
+    return fail(KDA_ERR_INVALID_ARGUMENT, "tile=%d outside [1, 16] (the _cc_tile bound)", tile);
+  if (int rc = check_dims(H, dk, dv)) return rc;
+  const size_t need = kda_cc_scan_workspace(T, H, dk, dv, chunk);
+  if (workspace == nullptr || workspace_bytes < need)
+    return fail(KDA_ERR_WORKSPACE, "workspace of %zu bytes is too small (need %zu)", workspace_bytes, need);
+  const size_t g_bytes = align_up(static_cast<size_t>(T) * H * dk * 4);
+  const size_t b_bytes = align_up(static_cast<size_t>(T) * H * 4);
+  float* g32 = reinterpret_cast<float*>(workspace);
+  float* b32 = reinterpret_cast<float*>(static_cast<char*>(workspace) + g_bytes);
+  kda::AdaptArgs aa{};
+  aa.alpha = alpha; aa.beta32 = beta32; aa.g_out = g32; aa.beta_out = b32;
+  aa.n_tok_heads = static_cast<int64_t>(T) * H;
+  aa.dk = dk;
+  hipError_t e = kda::launch_adapt(aa, stream);
+  if (e != hipSuccess) return hip_fail(e, "cc_scan adapter launch");
+  void* rest = static_cast<char*>(workspace) + g_bytes + b_bytes;
+  return chunk_fwd_impl(stream, q, k, v, g32, b32, S_in, nullptr, 0, o, S_out, 1, T, H, dk, dv,
+                        kC, 1.0f, KDA_DTYPE_BF16_F32GATES, KDA_DTYPE_F32, rest,
+                        workspace_bytes - g_bytes - b_bytes);
+}
+
+}  // extern "C"

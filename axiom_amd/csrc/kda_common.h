@@ -1,0 +1,181 @@
+// Shared device helpers for the KDA kernels (gfx950 / CDNA4 only).
+//
+// Fragment conventions used by every kernel in this library (64-lane waves):
+//   lane l, row-in-tile r = l & 15, lane group gq = l >> 4 (0..3).
+//   * MFMA 16x16x32 (f16/bf16): lane holds A[r][k-slots of group gq] (8 values)
+//     and B[k-slots of group gq][r]; D (4 fp32) holds rows 4*gq+i, column r.
+//   * MFMA 16x16x16 (f16): lane holds A[r][4*gq .. 4*gq+3] and
+//     B[4*gq .. 4*gq+3][r]; same D layout.
+//   * fp32 "exact" mode replaces one 16x16x32 by eight 16x16x4f32 MFMAs on the
+//     same registers (slot e of every lane group forms one K=4 step), so the
+//     register layouts are identical in both precisions.
+//   * Channel slots.  Inside a 32-wide K step j, slot (gq, e), e = 0..7, carries
+//     channel 32*j + 4*gq + (e & 3) + 16*(e >> 2).  With this order the D
+//     layouts of two 16x16 tiles (rows 4*gq+i of tile 2j and of tile 2j+1) are
+//     exactly the A fragment of one 16x16x32 MFMA, so kernels can hand results
+//     to each other through HBM in fragment order with no transpose.
+#pragma once
+
+#include <hip/hip_runtime.h>
+#include <hip/hip_fp16.h>
+#include <hip/hip_bf16.h>
+#include <stdint.h>
+
+namespace kda {
+
+typedef _Float16 h4 __attribute__((ext_vector_type(4)));
+typedef _Float16 h8 __attribute__((ext_vector_type(8)));
+typedef __bf16 b8 __attribute__((ext_vector_type(8)));
+typedef float f4 __attribute__((ext_vector_type(4)));
+typedef float f8 __attribute__((ext_vector_type(8)));
+typedef uint16_t u16;
+
+constexpr float kLog2e = 1.4426950408889634f;
+
+// ----------------------------------------------------------------------------
+// element conversions
+// ----------------------------------------------------------------------------
+__device__ __forceinline__ float bf16_to_f32(u16 b) {
+  return __uint_as_float(static_cast<uint32_t>(b) << 16);
+}
+__device__ __forceinline__ float f16bits_to_f32(u16 b) {
+  _Float16 h;
+  __builtin_memcpy(&h, &b, 2);
+  return static_cast<float>(h);
+}
+// round-to-nearest-even fp32 -> bf16 bits (finite inputs)
+__device__ __forceinline__ u16 f32_to_bf16_bits(float x) {
+  uint32_t u = __float_as_uint(x);
+  u += 0x7FFFu + ((u >> 16) & 1u);
+  return static_cast<u16>(u >> 16);
+}
+
+// Input element types: 0 = fp32, 1 = bf16, 2 = fp16.
+template <int DT> struct InT;
+template <> struct InT<0> { typedef float t; };
+template <> struct InT<1> { typedef u16 t; };
+template <> struct InT<2> { typedef u16 t; };
+
+template <int DT>
+__device__ __forceinline__ float ld1(const void* p, int64_t i) {
+  if constexpr (DT == 0) return static_cast<const float*>(p)[i];
+  else if constexpr (DT == 1) return bf16_to_f32(static_cast<const u16*>(p)[i]);
+  else return f16bits_to_f32(static_cast<const u16*>(p)[i]);
+}
+
+// Four consecutive elements starting at element index i (i multiple of 4).
+template <int DT>
+__device__ __forceinline__ f4 ld4(const void* p, int64_t i) {
+  if constexpr (DT == 0) {
+    return *reinterpret_cast<const f4*>(static_cast<const float*>(p) + i);
+  } else {
+    uint2 w = *reinterpret_cast<const uint2*>(static_cast<const u16*>(p) + i);
+    f4 r;
+    if constexpr (DT == 1) {
+      r[0] = __uint_as_float(w.x << 16);
+      r[1] = __uint_as_float(w.x & 0xFFFF0000u);
+      r[2] = __uint_as_float(w.y << 16);
+      r[3] = __uint_as_float(w.y & 0xFFFF0000u);
+    } else {
+      r[0] = f16bits_to_f32(static_cast<u16>(w.x & 0xFFFFu));
+      r[1] = f16bits_to_f32(static_cast<u16>(w.x >> 16));
+      r[2] = f16bits_to_f32(static_cast<u16>(w.y & 0xFFFFu));
+      r[3] = f16bits_to_f32(static_cast<u16>(w.y >> 16));
+    }
+    return r;
+  }
+}
+
+// ----------------------------------------------------------------------------
+// operand precision: fast (fp16 operands) or exact (fp32 operands)
+// ----------------------------------------------------------------------------
+template <bool EXACT> struct Prec;
+template <> struct Prec<false> {
+  typedef _Float16 st;  // storage / operand element
+  typedef h8 v8;
+  typedef h4 v4;
+};
+template <> struct Prec<true> {
+  typedef float st;
+  typedef f8 v8;
+  typedef f4 v4;
+};
+
+template <bool EXACT>
+__device__ __forceinline__ typename Prec<EXACT>::v8 cvt8(const f8& x) {
+  if constexpr (EXACT) {
+    return x;
+  } else {
+    h8 r;
+#pragma unroll
+    for (int i = 0; i < 8; ++i) r[i] = static_cast<_Float16>(x[i]);
+    return r;
+  }
+}
+template <bool EXACT>
+__device__ __forceinline__ typename Prec<EXACT>::v4 cvt4(const f4& x) {
+  if constexpr (EXACT) {
+    return x;
+  } else {
+    h4 r;
+#pragma unroll
+    for (int i = 0; i < 4; ++i) r[i] = static_cast<_Float16>(x[i]);
+    return r;
+  }
+}
+
+// ----------------------------------------------------------------------------
+// MFMA wrappers
+// ----------------------------------------------------------------------------
+__device__ __forceinline__ f4 mma32(f4 acc, h8 a, h8 b) {
+  return __builtin_amdgcn_mfma_f32_16x16x32_f16(a, b, acc, 0, 0, 0);
+}
+__device__ __forceinline__ f4 mma32(f4 acc, const f8& a, const f8& b) {
+#pragma unroll
+  for (int e = 0; e < 8; ++e) acc = __builtin_amdgcn_mfma_f32_16x16x4f32(a[e], b[e], acc, 0, 0, 0);
+  return acc;
+}
+__device__ __forceinline__ f4 mma32_bf16(f4 acc, b8 a, b8 b) {
+  return __builtin_amdgcn_mfma_f32_16x16x32_bf16(a, b, acc, 0, 0, 0);
+}
+__device__ __forceinline__ f4 mma16(f4 acc, h4 a, h4 b) {
+  return __builtin_amdgcn_mfma_f32_16x16x16f16(a, b, acc, 0, 0, 0);
+}
+__device__ __forceinline__ f4 mma16(f4 acc, const f4& a, const f4& b) {
+#pragma unroll
+  for (int e = 0; e < 4; ++e) acc = __builtin_amdgcn_mfma_f32_16x16x4f32(a[e], b[e], acc, 0, 0, 0);
+  return acc;
+}
+
+// ----------------------------------------------------------------------------
+// DPP helpers inside 16-lane rows
+// ----------------------------------------------------------------------------
+// Value of lane (row_base + N) of this lane's 16-lane row.
+template <int N>
+__device__ __forceinline__ float row_bcast(float x) {
+  return __builtin_bit_cast(float, __builtin_amdgcn_update_dpp(
+      0, __builtin_bit_cast(int, x), 0x150 + N, 0xF, 0xF, false));
+}
+// Value of lane (lane - N) in this 16-lane row, 0 for the first N lanes.
+template <int N>
+__device__ __forceinline__ float row_shr(float x) {
+  return __builtin_bit_cast(float, __builtin_amdgcn_update_dpp(
+      0, __builtin_bit_cast(int, x), 0x110 + N, 0xF, 0xF, false));
+}
+// Inclusive prefix sum over the 16 lanes of each DPP row.
+__device__ __forceinline__ float row_scan16(float x) {
+  x += row_shr<1>(x);
+  x += row_shr<2>(x);
+  x += row_shr<4>(x);
+  x += row_shr<8>(x);
+  return x;
+}
+
+__device__ __forceinline__ float fast_exp2(float x) { return __builtin_amdgcn_exp2f(x); }
+
+// channel carried by slot (gq, e) of 32-wide K step j
+__device__ __forceinline__ int slot_channel(int j, int gq, int e) {
+  return 32 * j + 4 * gq + (e & 3) + 16 * (e >> 2);
+}
+
+}  // namespace kda

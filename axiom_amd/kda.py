@@ -1,0 +1,219 @@
+"""Host-side API of the MI355X KDA path (torch tensors in device memory).
+
+Mirrors the reference's interface for this path (romannekrasovaillm/axiom):
+
+* :func:`cc_scan` -- the whole-sequence KDA scan seam
+  ``net/kernels/kda_cc_fused_persist.py:920`` with the same arguments,
+  layouts, outputs and error classes (``ValueError`` for dtype / ``T % C`` /
+  unsupported configuration, ``RuntimeError`` when no GPU is present, as
+  ``net/kda.py:818-822``).
+* :func:`kda_chunk_fwd` -- the FLA-style generalisation ``(q, k, v, g, beta,
+  initial_state, cu_seqlens) -> (o, final_state)`` of that seam with explicit
+  batch, ragged lengths and varlen packing.
+* :func:`kda_recurrent_step` -- one decode token, the delta rule of
+  ``net/kda.py:298-310`` plus the read-out ``net/kda.py:293``, state in place.
+
+Every function calls the HIP library through its C ABI on torch's current
+stream; nothing here computes on the CPU.
+"""
+
+from __future__ import annotations
+
+import ctypes
+
+import torch
+
+from . import _lib
+
+_IN_CODES = {torch.float32: _lib.KDA_DTYPE_F32, torch.bfloat16: _lib.KDA_DTYPE_BF16,
+             torch.float16: _lib.KDA_DTYPE_F16}
+_OUT_CODES = {torch.float32: _lib.KDA_DTYPE_F32, torch.bfloat16: _lib.KDA_DTYPE_BF16}
+SUPPORTED_HEAD_DIMS = (64, 128)
+CHUNK = 64
+
+
+def _ptr(t):
+    return ctypes.c_void_p(0 if t is None else t.data_ptr())
+
+
+def _stream(device) -> ctypes.c_void_p:
+    return ctypes.c_void_p(torch.cuda.current_stream(device).cuda_stream)
+
+
+def _require_gpu(tensors, what: str) -> torch.device:
+    devs = {t.device for t in tensors if t is not None}
+    if len(devs) != 1:
+        raise ValueError(f"{what}: all tensors must be on one device, got {sorted(map(str, devs))}")
+    dev = devs.pop()
+    if dev.type != "cuda" or not torch.cuda.is_available():
+        raise RuntimeError(
+            f"{what}: the KDA kernels run only on the GPU (HIP, gfx950); got tensors on {dev}. "
+            "There is no CPU fallback.")
+    return dev
+
+
+def _contig(name, t):
+    if not t.is_contiguous():
+        raise ValueError(f"{name} must be contiguous")
+
+
+def _check_dims(dk, dv, what):
+    if dk != dv or dk not in SUPPORTED_HEAD_DIMS:
+        raise ValueError(f"{what}: head dims dk={dk}, dv={dv} unsupported "
+                         f"(this build runs dk == dv in {SUPPORTED_HEAD_DIMS})")
+
+
+def chunk_fwd_workspace_bytes(B, T, H, dk, dv, n_seqs=0, in_code=_lib.KDA_DTYPE_BF16) -> int:
+    return int(_lib.lib().kda_chunk_fwd_workspace(B, T, H, dk, dv, CHUNK, n_seqs, in_code))
+
+
+def kda_chunk_fwd(q, k, v, g, beta, initial_state=None, cu_seqlens=None, chunk_size: int = 64,
+                  scale: float = 1.0, output_final_state: bool = True,
+                  out_dtype=torch.float32, workspace=None):
+    """Chunked KDA forward; returns ``(o, final_state)`` (``final_state`` None if not requested).
+
+    ``q, k, g [B,T,H,dk]``, ``v [B,T,H,dv]``, ``beta [B,T,H]``; q/k/v share one
+    dtype (bf16, fp16 or fp32).  g and beta have the same dtype as q, or fp32
+    with bf16 q/k/v.  ``initial_state [N,H,dk,dv]`` fp32 or None (zeros);
+    ``cu_seqlens`` int32 ``[N+1]`` on the device (requires B == 1).  fp32
+    inputs select the exact (fp32 MFMA) kernels.
+    """
+    what = "kda_chunk_fwd"
+    if q.dim() != 4 or k.shape != q.shape or g.shape != q.shape:
+        raise ValueError(f"{what}: q, k, g must share a [B,T,H,dk] shape")
+    B, T, H, dk = q.shape
+    if v.dim() != 4 or v.shape[:3] != q.shape[:3]:
+        raise ValueError(f"{what}: v must be [B,T,H,dv] matching q")
+    dv = v.shape[3]
+    if tuple(beta.shape) != (B, T, H):
+        raise ValueError(f"{what}: beta must be [B,T,H] = {(B, T, H)}, got {tuple(beta.shape)}")
+    if chunk_size != CHUNK:
+        raise ValueError(f"{what}: chunk_size={chunk_size} unsupported (this build runs {CHUNK})")
+    _check_dims(dk, dv, what)
+    if q.dtype not in _IN_CODES or k.dtype != q.dtype or v.dtype != q.dtype:
+        raise ValueError(f"{what}: q, k, v must share a dtype in bf16/fp16/fp32")
+    if g.dtype == q.dtype and beta.dtype == q.dtype:
+        in_code = _IN_CODES[q.dtype]
+    elif q.dtype == torch.bfloat16 and g.dtype == torch.float32 and beta.dtype == torch.float32:
+        in_code = _lib.KDA_DTYPE_BF16_F32GATES
+    else:
+        raise ValueError(f"{what}: g/beta dtype must equal q's, or be fp32 with bf16 q/k/v")
+    if out_dtype not in _OUT_CODES:
+        raise ValueError(f"{what}: out_dtype must be fp32 or bf16")
+    n_seqs = 0
+    N = B
+    if cu_seqlens is not None:
+        if cu_seqlens.dtype != torch.int32 or cu_seqlens.dim() != 1 or cu_seqlens.numel() < 2:
+            raise ValueError(f"{what}: cu_seqlens must be a 1-D int32 tensor of N+1 >= 2 offsets")
+        if B != 1:
+            raise ValueError(f"{what}: cu_seqlens requires B == 1, got B={B}")
+        n_seqs = cu_seqlens.numel() - 1
+        N = n_seqs
+    if initial_state is not None:
+        if initial_state.dtype != torch.float32 or tuple(initial_state.shape) != (N, H, dk, dv):
+            raise ValueError(f"{what}: initial_state must be fp32 [{N},{H},{dk},{dv}]")
+    for name, t in (("q", q), ("k", k), ("v", v), ("g", g), ("beta", beta),
+                    ("initial_state", initial_state), ("cu_seqlens", cu_seqlens)):
+        if t is not None:
+            _contig(name, t)
+    dev = _require_gpu([q, k, v, g, beta, initial_state, cu_seqlens], what)
+    L = _lib.lib()
+    ws_bytes = int(L.kda_chunk_fwd_workspace(B, T, H, dk, dv, CHUNK, n_seqs, in_code))
+    if ws_bytes == 0:
+        raise ValueError(f"{what}: unsupported configuration")
+    if workspace is None or workspace.numel() * workspace.element_size() < ws_bytes:
+        workspace = torch.empty(ws_bytes, dtype=torch.uint8, device=dev)
+    o = torch.empty((B, T, H, dv), dtype=out_dtype, device=dev)
+    ht = torch.empty((N, H, dk, dv), dtype=torch.float32, device=dev) if output_final_state else None
+    rc = L.kda_chunk_fwd(_stream(dev), _ptr(q), _ptr(k), _ptr(v), _ptr(g), _ptr(beta),
+                         _ptr(initial_state), _ptr(cu_seqlens), n_seqs, _ptr(o), _ptr(ht),
+                         B, T, H, dk, dv, CHUNK, float(scale), in_code, _OUT_CODES[out_dtype],
+                         _ptr(workspace), ws_bytes)
+    _lib.check(rc, what)
+    return o, ht
+
+
+def varlen_status(workspace, B, T, H, dk, dv, n_seqs, in_code=_lib.KDA_DTYPE_BF16) -> int:
+    """Validation bits of the last varlen call that used ``workspace`` (synchronises)."""
+    flags = ctypes.c_int32(0)
+    rc = _lib.lib().kda_varlen_status(_stream(workspace.device), _ptr(workspace),
+                                      workspace.numel() * workspace.element_size(),
+                                      B, T, H, dk, dv, CHUNK, n_seqs, in_code, ctypes.byref(flags))
+    _lib.check(rc, "kda_varlen_status")
+    return int(flags.value)
+
+
+def kda_recurrent_step(q, k, v, g, beta, state, scale: float = 1.0, out_dtype=torch.float32):
+    """One decode token per chain; ``state [B,H,dk,dv]`` fp32 is updated in place.
+
+    ``q, k, g [B,H,dk]``, ``v [B,H,dv]``, ``beta [B,H]`` (one dtype: bf16, fp16
+    or fp32).  Returns ``o [B,H,dv]`` in ``out_dtype``.
+    """
+    what = "kda_recurrent_step"
+    if q.dim() != 3 or k.shape != q.shape or g.shape != q.shape:
+        raise ValueError(f"{what}: q, k, g must share a [B,H,dk] shape")
+    B, H, dk = q.shape
+    if v.dim() != 3 or v.shape[:2] != q.shape[:2]:
+        raise ValueError(f"{what}: v must be [B,H,dv]")
+    dv = v.shape[2]
+    if tuple(beta.shape) != (B, H):
+        raise ValueError(f"{what}: beta must be [B,H]")
+    _check_dims(dk, dv, what)
+    if q.dtype not in _IN_CODES or any(t.dtype != q.dtype for t in (k, v, g, beta)):
+        raise ValueError(f"{what}: q, k, v, g, beta must share a dtype in bf16/fp16/fp32")
+    if state.dtype != torch.float32 or tuple(state.shape) != (B, H, dk, dv):
+        raise ValueError(f"{what}: state must be fp32 [{B},{H},{dk},{dv}]")
+    if out_dtype not in _OUT_CODES:
+        raise ValueError(f"{what}: out_dtype must be fp32 or bf16")
+    for name, t in (("q", q), ("k", k), ("v", v), ("g", g), ("beta", beta), ("state", state)):
+        _contig(name, t)
+    dev = _require_gpu([q, k, v, g, beta, state], what)
+    o = torch.empty((B, H, dv), dtype=out_dtype, device=dev)
+    rc = _lib.lib().kda_recurrent_step(_stream(dev), _ptr(q), _ptr(k), _ptr(v), _ptr(g), _ptr(beta),
+                                       _ptr(state), _ptr(o), B, H, dk, dv, float(scale),
+                                       _IN_CODES[q.dtype], _OUT_CODES[out_dtype])
+    _lib.check(rc, what)
+    return o
+
+
+def cc_scan(q, k, v, alpha, beta32, S, tile: int = 16, chunk: int = 32):
+    """The reference seam ``cc_scan`` (``net/kernels/kda_cc_fused_persist.py:920``).
+
+    ``q, k (T, H*dk)`` bf16, ``v (T, H*dv)`` bf16, ``alpha (T, H*dk)`` fp32,
+    ``beta32 (T, H*32)`` fp32, ``S (H, dk, dv)`` fp32.  Returns
+    ``(o (T, H*dv) fp32, S_new (H, dk, dv) fp32)``.  Raises ``ValueError`` for
+    a non-bf16 q/v (``:737-740``), ``T % chunk != 0`` (``:741-742``) or an
+    unsupported configuration (``:743-749``), ``RuntimeError`` without a GPU.
+    """
+    T = q.shape[0]
+    if S.dim() != 3:
+        raise ValueError("cc_scan: S must be (H, dk, dv)")
+    H, dk, dv = S.shape
+    dt = q.dtype
+    if v.dtype != dt or dt != torch.bfloat16:
+        raise ValueError(
+            f"persistent kernel consumes bf16 q/k/v; got q.dtype={dt}, v.dtype={v.dtype}")
+    C = int(chunk)
+    if C < 1 or T % C:
+        raise ValueError(f"T={T} must be a multiple of the chunk width C={C}")
+    if not (1 <= int(tile) <= 16):
+        raise ValueError(f"cc_scan: tile={tile} outside [1, 16]")
+    _check_dims(dk, dv, "cc_scan")
+    if (tuple(q.shape) != (T, H * dk) or tuple(k.shape) != (T, H * dk) or k.dtype != dt
+            or tuple(v.shape) != (T, H * dv) or tuple(alpha.shape) != (T, H * dk)
+            or tuple(beta32.shape) != (T, H * 32)):
+        raise ValueError("cc_scan: shapes must be q,k,alpha (T,H*dk), v (T,H*dv), beta32 (T,H*32)")
+    if alpha.dtype != torch.float32 or beta32.dtype != torch.float32 or S.dtype != torch.float32:
+        raise ValueError("cc_scan: alpha, beta32 and S must be fp32")
+    for name, t in (("q", q), ("k", k), ("v", v), ("alpha", alpha), ("beta32", beta32), ("S", S)):
+        _contig(name, t)
+    dev = _require_gpu([q, k, v, alpha, beta32, S], "cc_scan")
+    L = _lib.lib()
+    ws_bytes = int(L.kda_cc_scan_workspace(T, H, dk, dv, C))
+    workspace = torch.empty(max(ws_bytes, 1), dtype=torch.uint8, device=dev)
+    o = torch.empty((T, H * dv), dtype=torch.float32, device=dev)
+    S_new = torch.empty((H, dk, dv), dtype=torch.float32, device=dev)
+    rc = L.kda_cc_scan(_stream(dev), _ptr(q), _ptr(k), _ptr(v), _ptr(alpha), _ptr(beta32), _ptr(S),
+                       _ptr(o), _ptr(S_new), T, H, dk, dv, int(tile), C, _ptr(workspace), ws_bytes)
+    _lib.check(rc, "cc_scan")
+    return o, S_new

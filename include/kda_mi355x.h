@@ -1,0 +1,154 @@
+/*
+ * kda_mi355x.h -- C ABI of the MI355X (gfx950) KDA hot path.
+ *
+ * Drop-in boundary for the chunked Kimi-Delta-Attention forward (WY/UT form),
+ * the single-token recurrent decode step and varlen (cu_seqlens) scheduling.
+ *
+ * Conventions (all entry points):
+ *   - every tensor pointer is device memory; work is enqueued on `stream` and
+ *     is stream-ordered; nothing is allocated by the library (the chunked
+ *     forward takes a caller-provided workspace);
+ *   - tensors are row-major, token-major: q, k, g are [B, T, H, dk], v and o
+ *     are [B, T, H, dv], beta is [B, T, H]; states are [N, H, dk, dv] fp32;
+ *   - g is the per-channel log-decay (g = log alpha <= 0), beta in (0, 1);
+ *     no 1/sqrt(d) scale is applied unless `scale` says so (1.0 reproduces
+ *     the reference, which applies none: net/kda.py:293, :693-696);
+ *   - return value 0 on success, a negative kda_status_t otherwise; the
+ *     message of the last failure on the calling thread is kda_last_error().
+ *     Invalid arguments are rejected before anything is enqueued; there is
+ *     no fallback path of any kind.
+ *
+ * Reference = romannekrasovaillm/axiom.  Each entry point names the reference
+ * interface it replaces.
+ */
+#ifndef KDA_MI355X_H_
+#define KDA_MI355X_H_
+
+#include <stddef.h>
+#include <stdint.h>
+#include <hip/hip_runtime_api.h>
+
+#if defined(__GNUC__)
+#define KDA_API __attribute__((visibility("default")))
+#else
+#define KDA_API
+#endif
+
+#ifdef __cplusplus
+extern "C" {
+#endif
+
+typedef enum kda_status_t {
+  KDA_OK = 0,
+  KDA_ERR_INVALID_ARGUMENT = -1, /* bad pointer, shape or value            */
+  KDA_ERR_UNSUPPORTED = -2,      /* valid request this build does not run  */
+  KDA_ERR_WORKSPACE = -3,        /* workspace missing or too small         */
+  KDA_ERR_HIP = -4               /* HIP runtime / launch failure           */
+} kda_status_t;
+
+typedef enum kda_dtype_t {
+  KDA_DTYPE_F32 = 0,             /* all inputs fp32: exact (fp32 MFMA) mode */
+  KDA_DTYPE_BF16 = 1,            /* q, k, v, g, beta bf16                   */
+  KDA_DTYPE_F16 = 2,             /* q, k, v, g, beta fp16                   */
+  KDA_DTYPE_BF16_F32GATES = 3    /* q, k, v bf16; g, beta fp32              */
+} kda_dtype_t;
+
+/*
+ * Chunked KDA forward.
+ *
+ * Replaces the reference's whole-sequence KDA scan seam
+ *   net/kernels/kda_cc_fused_persist.py:920  cc_scan(q, k, v, alpha, beta32, S, tile, chunk)
+ * and the jax scan it stands in for, net/kda.py:856-926 (apply_chunked_cc,
+ * body cc_chunk_step net/kda.py:634-705), called from net/kda.py:844 with the
+ * batch axis vmapped at net/model.py:341.  Generalised to the FLA-style
+ * signature (q, k, v, g, beta, h0, cu_seqlens) -> (o, ht):
+ *   - g replaces alpha (g = log alpha), beta is [B,T,H] (not replicated),
+ *   - the batch is explicit instead of vmapped,
+ *   - h0 (nullable, zeros if null; the reference passes zeros at
+ *     net/kda.py:850) and ht (nullable) are [N, H, dk, dv] fp32 with N = B,
+ *     or N = n_seqs when cu_seqlens is given,
+ *   - cu_seqlens (nullable, int32 [n_seqs+1], requires B == 1) packs n_seqs
+ *     independent sequences into one stream (absent in the reference; defined
+ *     by "packed run == independent per-sequence runs"),
+ *   - T need not be a multiple of `chunk`: a ragged tail is handled in place
+ *     and ht is the state after the last real token.
+ * o is written in out_dtype (KDA_DTYPE_F32 or KDA_DTYPE_BF16); the reference
+ * seam emits fp32 (net/kernels/kda_cc_fused_persist.py:660).
+ * Supported: dk == dv in {64, 128}, chunk == 64, in_dtype any kda_dtype_t.
+ * cu_seqlens values are clamped on the device into a non-decreasing sequence
+ * inside [0, T] so no access can leave the tensors; kda_varlen_status reports
+ * whether a repair was needed.
+ */
+KDA_API int kda_chunk_fwd(hipStream_t stream,
+                  const void* q, const void* k, const void* v,
+                  const void* g, const void* beta,
+                  const float* h0,
+                  const int32_t* cu_seqlens, int32_t n_seqs,
+                  void* o, float* ht,
+                  int B, int T, int H, int dk, int dv, int chunk, float scale,
+                  int in_dtype, int out_dtype,
+                  void* workspace, size_t workspace_bytes);
+
+/* Workspace bytes kda_chunk_fwd needs for these arguments (0 on bad input).
+ * n_seqs <= 0 means dense (no cu_seqlens).  Host-only; no HIP call. */
+KDA_API size_t kda_chunk_fwd_workspace(int B, int T, int H, int dk, int dv, int chunk,
+                               int32_t n_seqs, int in_dtype);
+
+/*
+ * After a varlen kda_chunk_fwd on `stream`, copy the device-side validation
+ * word of its workspace to *flags_out (synchronising the stream).  Bits:
+ * 1 cu[0] != 0, 2 cu[n] != T, 4 decreasing entry, 8 entry outside [0, T].
+ */
+KDA_API int kda_varlen_status(hipStream_t stream, const void* workspace, size_t workspace_bytes,
+                      int B, int T, int H, int dk, int dv, int chunk, int32_t n_seqs,
+                      int in_dtype, int32_t* flags_out);
+
+/*
+ * One recurrent decode step for B*H chains, state updated in place.
+ *
+ * Replaces net/kda.py:298-310 (_delta_step) followed by the read-out
+ * net/kda.py:293 (o = S^T q) inside recurrent_step (net/kda.py:277-295):
+ *   S <- (I - beta k k^T) diag(alpha) S + beta k v^T,  o = S^T (scale q).
+ * q, k, g: [B, H, dk]; v: [B, H, dv]; beta: [B, H]; state: [B, H, dk, dv] fp32
+ * (in place); o: [B, H, dv] in out_dtype.  in_dtype: F32, BF16 or F16.
+ */
+KDA_API int kda_recurrent_step(hipStream_t stream,
+                       const void* q, const void* k, const void* v,
+                       const void* g, const void* beta,
+                       float* state, void* o,
+                       int B, int H, int dk, int dv, float scale,
+                       int in_dtype, int out_dtype);
+
+/*
+ * The reference seam verbatim:
+ *   net/kernels/kda_cc_fused_persist.py:920  cc_scan(q, k, v, alpha, beta32, S, tile=16, chunk=32)
+ * q, k: (T, H*dk) bf16; v: (T, H*dv) bf16; alpha: (T, H*dk) fp32 in (0, 1];
+ * beta32: (T, H*32) fp32 (beta replicated over 32 columns, recovered as the
+ * mean, :435); S_in: (H, dk, dv) fp32.  Outputs o: (T, H*dv) fp32 and S_out:
+ * (H, dk, dv) fp32 (functional: S_in is not modified unless S_out == S_in).
+ * Errors as the reference (net/kernels/kda_cc_fused_persist.py:737-749):
+ * T % chunk != 0 -> KDA_ERR_INVALID_ARGUMENT; tile outside [1, 16] ->
+ * KDA_ERR_INVALID_ARGUMENT.  The result does not depend on chunk or tile in
+ * exact arithmetic; the kernels always run with C = 64 and 16-row tiles.
+ */
+KDA_API int kda_cc_scan(hipStream_t stream,
+                const void* q, const void* k, const void* v,
+                const float* alpha, const float* beta32, const float* S_in,
+                float* o, float* S_out,
+                int T, int H, int dk, int dv, int tile, int chunk,
+                void* workspace, size_t workspace_bytes);
+
+/* Workspace bytes kda_cc_scan needs (0 on bad input).  Host-only. */
+KDA_API size_t kda_cc_scan_workspace(int T, int H, int dk, int dv, int chunk);
+
+/* Message of the last failure on the calling thread ("" if none). */
+KDA_API const char* kda_last_error(void);
+
+/* ABI version of this library (major * 100 + minor). */
+KDA_API int kda_abi_version(void);
+
+#ifdef __cplusplus
+}
+#endif
+
+#endif /* KDA_MI355X_H_ */

@@ -1,0 +1,281 @@
+"""CPU restatement of the reference KDA algebra (TEST INFRASTRUCTURE ONLY).
+
+Reference = romannekrasovaillm/axiom.  Notation per head: chunk length ``C``,
+``g = log(alpha) <= 0`` per channel, ``G = cumsum_c(g)`` (inclusive),
+``gamma = exp(G)``, ``beta in (0, 1)``.
+
+Functions and what each restates
+--------------------------------
+``recurrent_fwd`` / ``decode_step`` (numpy, float64)
+    The delta rule of ``net/kda.py:298-310`` (``_delta_step``):
+    ``S <- (I - beta k k^T) Diag(alpha) S + beta k v^T`` with the read taken
+    against ``Diag(alpha) S``, and the output ``o = S^T q`` of ``net/kda.py:293``.
+    This is the ground truth every other form is checked against.
+``cc_scores``
+    Tile-wise decay-weighted scores, ``net/kda.py:588-631`` (``_cc_scores``),
+    tile width rule ``net/kda.py:570-585`` (``_cc_tile``: 16 at ``g_min = -5``).
+``ut_solve``
+    ``(I + L)^{-1}`` as an explicit inverse, ``net/kda.py:434-438``
+    (``_solve_pair_jax``).
+``chunk_fwd`` (torch CPU, float64 or float32)
+    The chunk body ``cc_chunk_step`` core, ``net/kda.py:669-702``: scores,
+    ``L = beta * Akk``, ``W = T(beta gamma k)``, ``U = T(beta v)``,
+    ``v~ = U - W S``, ``o = (gamma q) S + Aqk v~``,
+    ``S' = gamma_C S + (lambda k)^T v~``; scanned over chunks as
+    ``net/kda.py:924`` and batched over (B, H) as ``net/model.py:341``.
+    Padding of a ragged tail follows ``net/kda.py:829-831`` in spirit (zero
+    k/v/q rows) with ``g = 0, beta = 0`` so padded rows leave the state alone;
+    the returned final state is the state after the last real token, which is
+    what the recurrence defines.  ``cu_seqlens`` (absent in the reference) is
+    defined by the invariant "packed run == independent per-sequence runs".
+
+How each is pinned (tests/test_oracle.py)
+----------------------------------------
+* recurrence: closed forms (beta=0 decay-only, g=0 & beta=0 identity,
+  alpha->0 overwrite, single token from S0=0 gives ``o = beta (k.q) v``,
+  orthonormal keys with beta=1 store ``S^T k_i = v_i`` exactly) and a scalar
+  brute-force loop on tiny inputs;
+* chunked form: equals the recurrence within 1e-4 for C in {16, 32, 64, 128}
+  (the reference's own bar, ``net/tests/test_kda_chunked_cc.py:189-208``),
+  chunk-size invariance, per-chunk states, T < C and ragged tails
+  (``net/tests/test_kda_chunked_cc.py:270-288``, ``:413-427``);
+* scores: brute-force ``(C, C, dk)`` decay-ratio tensor
+  (``net/tests/test_kda_chunked_cc.py:221-247``);
+* UT solve: ``scipy.linalg.solve_triangular(unit_diagonal=True)`` and the
+  Neumann product identity (``net/kernels/kda_ut_solve.py:20-27``);
+* varlen: packed == per-sequence; decode: T decode steps == chunked forward.
+* mutation tests plant a dropped term, a sign flip, a transposed operand and an
+  off-by-one in the decay into copies of these functions and show that at
+  least one pin fails for each.
+No function here is "parity unpinned".
+"""
+
+from __future__ import annotations
+
+import numpy as np
+import torch
+
+# ---------------------------------------------------------------------------
+# Recurrent form (ground truth)
+# ---------------------------------------------------------------------------
+
+
+def decode_step(q, k, v, g, beta, S, scale: float = 1.0):
+    """One token per chain: ``net/kda.py:298-310`` then ``o = S'^T q`` (``:293``).
+
+    Shapes: ``q, k, g [..., dk]``, ``v [..., dv]``, ``beta [...]``,
+    ``S [..., dk, dv]``.  float64 throughout; returns ``(o, S_new)``.
+    """
+    q = np.asarray(q, np.float64) * scale
+    k = np.asarray(k, np.float64)
+    v = np.asarray(v, np.float64)
+    alpha = np.exp(np.asarray(g, np.float64))
+    beta = np.asarray(beta, np.float64)
+    S = np.asarray(S, np.float64)
+    decayed = alpha[..., :, None] * S                      # Diag(alpha) S
+    read = np.einsum("...d,...de->...e", alpha * k, S)     # (alpha*k)^T S
+    S_new = decayed + beta[..., None, None] * k[..., :, None] * (v - read)[..., None, :]
+    o = np.einsum("...d,...de->...e", q, S_new)            # S'^T q
+    return o, S_new
+
+
+def recurrent_fwd(q, k, v, g, beta, h0=None, cu_seqlens=None, scale: float = 1.0):
+    """Token-by-token recurrence over ``[B, T, H, d]`` inputs (float64).
+
+    Returns ``(o [B,T,H,dv], ht [N,H,dk,dv])`` with ``N = B`` or the number of
+    sequences when ``cu_seqlens`` is given (then ``B`` must be 1).
+    """
+    q, k, v, g, beta = (np.asarray(x, np.float64) for x in (q, k, v, g, beta))
+    B, T, H, dk = q.shape
+    dv = v.shape[-1]
+    if cu_seqlens is None:
+        S = np.zeros((B, H, dk, dv)) if h0 is None else np.array(h0, np.float64)
+        o = np.zeros((B, T, H, dv))
+        for t in range(T):
+            o[:, t], S = decode_step(q[:, t], k[:, t], v[:, t], g[:, t], beta[:, t], S, scale)
+        return o, S
+    if B != 1:
+        raise ValueError("cu_seqlens requires B == 1")
+    cu = np.asarray(cu_seqlens, np.int64)
+    n = len(cu) - 1
+    o = np.zeros((1, T, H, dv))
+    hts = np.zeros((n, H, dk, dv))
+    for i in range(n):
+        a, b = int(cu[i]), int(cu[i + 1])
+        h0_i = None if h0 is None else np.asarray(h0)[i:i + 1]
+        o_i, ht_i = recurrent_fwd(q[:, a:b], k[:, a:b], v[:, a:b], g[:, a:b], beta[:, a:b],
+                                  h0=h0_i, scale=scale)
+        o[:, a:b] = o_i
+        hts[i] = ht_i[0]
+    return o, hts
+
+
+# ---------------------------------------------------------------------------
+# Chunked WY/UT form (net/kda.py:570-705), torch CPU
+# ---------------------------------------------------------------------------
+
+
+def cc_tile(g_min: float = -5.0) -> int:
+    """Row-tile width of the decay factors, ``net/kda.py:577-585``."""
+    step = abs(float(g_min))
+    cap = int(80.0 / step) if step > 0 else 16
+    return max(1, min(16, cap))
+
+
+def cc_scores(row: torch.Tensor, col: torch.Tensor, G: torch.Tensor, tile: int,
+              strict: bool) -> torch.Tensor:
+    """``sum_d exp(G_c - G_i) row_c[d] col_i[d]`` masked to ``c >= i`` (``c > i``).
+
+    Restates ``net/kda.py:588-631``: each row tile measures its decay against
+    its own first position ``p``, ``exp(G_c - G_i) = exp(G_c - G_p) exp(G_p - G_i)``.
+    ``row, col, G``: ``[N, C, dk]``; returns ``[N, C, C]``.
+    """
+    N, C, _ = row.shape
+    out = torch.zeros((N, C, C), dtype=row.dtype)
+    for p in range(0, C, tile):
+        b = min(tile, C - p)
+        ref = G[:, p:p + 1, :]
+        rows = row[:, p:p + b, :] * torch.exp(G[:, p:p + b, :] - ref)
+        cols = col[:, :p + b, :] * torch.exp(ref - G[:, :p + b, :])
+        blk = rows @ cols.transpose(1, 2)
+        ri = torch.arange(p, p + b)[:, None]
+        ci = torch.arange(p + b)[None, :]
+        keep = (ri > ci) if strict else (ri >= ci)
+        out[:, p:p + b, :p + b] = torch.where(keep, blk, torch.zeros((), dtype=blk.dtype))
+    return out
+
+
+def ut_solve(L: torch.Tensor) -> torch.Tensor:
+    """``T = (I + L)^{-1}`` for strictly-lower ``L [N, C, C]`` (``net/kda.py:434-438``)."""
+    C = L.shape[-1]
+    eye = torch.eye(C, dtype=L.dtype).expand_as(L)
+    return torch.linalg.inv(eye + L)
+
+
+def chunk_step(q, k, v, G, beta, S, tile: int = 16):
+    """One chunk for ``N`` chains: ``net/kda.py:669-702``.
+
+    ``q, k, G [N, C, dk]``, ``v [N, C, dv]``, ``beta [N, C]``, ``S [N, dk, dv]``
+    (``G`` is the in-chunk inclusive cumsum of ``g``).  Returns ``(o, S_new)``.
+    """
+    aqk = cc_scores(q, k, G, tile, strict=False)                  # :677
+    akk = cc_scores(k, k, G, tile, strict=True)                   # :678
+    L = akk * beta[:, :, None]                                    # :681
+    gamma = torch.exp(G)                                          # :684
+    xw = gamma * k * beta[:, :, None]                             # :685
+    vw = v * beta[:, :, None]                                     # :686
+    Tm = ut_solve(L)                                              # :687
+    w = Tm @ xw
+    u = Tm @ vw
+    v_tilde = u - w @ S                                           # :690
+    o = (gamma * q) @ S + aqk @ v_tilde                           # :693-696
+    G_last = G[:, -1:, :]
+    lam = torch.exp(torch.clamp(G_last - G, max=0.0))             # :700
+    S_new = gamma[:, -1, :, None] * S + (lam * k).transpose(1, 2) @ v_tilde   # :701-702
+    return o, S_new
+
+
+def _to_torch(x, dtype):
+    return torch.as_tensor(np.ascontiguousarray(x)).to(dtype)
+
+
+def _chunk_fwd_dense(q, k, v, g, beta, h0, C, tile, dtype, scale, return_chunk_states=False):
+    """Chunked forward for equal-length chains: inputs ``[B, T, H, d]`` numpy."""
+    B, T, H, dk = q.shape
+    dv = v.shape[-1]
+    n_chunks = (T + C - 1) // C
+    Tp = n_chunks * C
+    pad = Tp - T
+
+    def prep(x, d):
+        t = _to_torch(x, dtype).permute(0, 2, 1, 3).reshape(B * H, T, d)
+        if pad:
+            t = torch.cat([t, torch.zeros((B * H, pad, d), dtype=dtype)], dim=1)
+        return t.reshape(B * H, n_chunks, C, d)
+
+    qc = prep(np.asarray(q) * scale, dk)
+    kc = prep(k, dk)
+    vc = prep(v, dv)
+    gc = prep(g, dk)
+    bt = _to_torch(beta, dtype).permute(0, 2, 1).reshape(B * H, T)
+    if pad:
+        bt = torch.cat([bt, torch.zeros((B * H, pad), dtype=dtype)], dim=1)
+    bc = bt.reshape(B * H, n_chunks, C)
+    if h0 is None:
+        S = torch.zeros((B * H, dk, dv), dtype=dtype)
+    else:
+        S = _to_torch(h0, dtype).reshape(B * H, dk, dv).clone()
+    o = torch.empty((B * H, n_chunks, C, dv), dtype=dtype)
+    states = []
+    for n in range(n_chunks):                                     # net/kda.py:924 scan
+        G = torch.cumsum(gc[:, n], dim=1)                         # net/kda.py:397-399
+        if return_chunk_states:
+            states.append(S.clone())
+        o[:, n], S = chunk_step(qc[:, n], kc[:, n], vc[:, n], G, bc[:, n], S, tile)
+    o = o.reshape(B, H, Tp, dv)[:, :, :T].permute(0, 2, 1, 3)
+    out = (o.contiguous(), S.reshape(B, H, dk, dv))
+    if return_chunk_states:
+        out = out + (torch.stack(states, 1).reshape(B, H, n_chunks, dk, dv),)
+    return out
+
+
+def chunk_fwd(q, k, v, g, beta, h0=None, cu_seqlens=None, chunk: int = 64, tile: int = 16,
+              dtype=torch.float64, scale: float = 1.0, return_chunk_states: bool = False):
+    """Chunked WY/UT forward (``net/kda.py:856-926`` scan of ``cc_chunk_step``).
+
+    Inputs are numpy ``[B, T, H, d]`` (``beta [B, T, H]``), ``h0 [N, H, dk, dv]``
+    or None, ``cu_seqlens [N+1]`` or None (then ``B == 1``).  Returns torch
+    tensors ``(o [B,T,H,dv], ht [N,H,dk,dv])`` in ``dtype``.
+    """
+    if cu_seqlens is None:
+        return _chunk_fwd_dense(q, k, v, g, beta, h0, chunk, tile, dtype, scale,
+                                return_chunk_states)
+    B, T, H, dk = q.shape
+    dv = v.shape[-1]
+    if B != 1:
+        raise ValueError("cu_seqlens requires B == 1")
+    cu = np.asarray(cu_seqlens, np.int64)
+    n = len(cu) - 1
+    o = torch.zeros((1, T, H, dv), dtype=dtype)
+    hts = torch.zeros((n, H, dk, dv), dtype=dtype)
+    for i in range(n):
+        a, b = int(cu[i]), int(cu[i + 1])
+        if b == a:
+            hts[i] = torch.zeros((H, dk, dv), dtype=dtype) if h0 is None else _to_torch(h0[i], dtype)
+            continue
+        h0_i = None if h0 is None else np.asarray(h0)[i:i + 1]
+        o_i, ht_i = _chunk_fwd_dense(q[:, a:b], k[:, a:b], v[:, a:b], g[:, a:b], beta[:, a:b],
+                                     h0_i, chunk, tile, dtype, scale)
+        o[:, a:b] = o_i
+        hts[i] = ht_i[0]
+    return o, hts
+
+
+def decode_steps(q, k, v, g, beta, S, scale: float = 1.0):
+    """``steps`` successive decode steps: inputs ``[steps, B, H, d]``, state ``[B,H,dk,dv]``."""
+    outs = []
+    S = np.asarray(S, np.float64)
+    for t in range(q.shape[0]):
+        o, S = decode_step(q[t], k[t], v[t], g[t], beta[t], S, scale)
+        outs.append(o)
+    return np.stack(outs, 0), S
+
+
+# ---------------------------------------------------------------------------
+# Error metrics used by every parity test
+# ---------------------------------------------------------------------------
+
+
+def rel_l2(x, ref) -> float:
+    x = np.asarray(x, np.float64)
+    ref = np.asarray(ref, np.float64)
+    den = np.linalg.norm(ref.ravel())
+    return float(np.linalg.norm((x - ref).ravel()) / max(den, 1e-30))
+
+
+def max_abs(x, ref) -> float:
+    x = np.asarray(x, np.float64)
+    ref = np.asarray(ref, np.float64)
+    if x.size == 0:
+        return 0.0
+    return float(np.max(np.abs(x - ref)))
