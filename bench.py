@@ -1,0 +1,241 @@
+#!/usr/bin/env python
+"""Benchmark of the MI355X KDA hot path (one GPU).
+
+Headline (the ``value``): chunked KDA forward throughput in tokens/s at
+B=4, T=4096, H=16, dk=dv=128, C=64, bf16 inputs, fp32 o and fp32 final state
+(``configs[1]`` of the benchmark definition), inputs resident in HBM.  One
+"step" = one ``kda_chunk_fwd`` over the whole batch.
+
+Also reported on the same JSON line:
+* TFLOP/s and % of bf16 dense MFMA peak with the algorithmic count
+  ``8*C*d + 6*d^2`` FLOP per token-head;
+* ``roofline``: algorithmic bytes (read q, k, v, g, beta; write o fp32 and the
+  final state fp32 = 407.4 MB) over the average duration of the forward's
+  kernels, measured with HIP events on the stream they are launched on;
+* ``decode``: the recurrent decode step at B=256, H=16, d=128 (fp32 state
+  read-modified-written in place, bf16 inputs), iterated 128 steps, as GB/s
+  against the 8 TB/s HBM peak (``configs[4]``);
+* ``cpu_baseline``: the oracle's fp32 restatement of the reference jax body
+  (torch CPU, all available cores) timed on a bounded sample of the same
+  workload on this host.
+
+``--gpus N`` with N > 1 exits: this build measures one GPU.
+"""
+
+from __future__ import annotations
+
+import argparse
+import json
+import math
+import os
+import platform
+import statistics
+import sys
+import time
+
+import torch
+
+HBM_PEAK_GBPS = 8000.0
+MFMA_BF16_PEAK_TFLOPS = 2516.6
+
+CFG = dict(B=4, T=4096, H=16, dk=128, dv=128, C=64)
+
+
+def flops_per_token_head(C, d):
+    return 8 * C * d + 6 * d * d
+
+
+def fwd_bytes(B, T, H, dk, dv, in_bytes=2, o_bytes=4):
+    n = B * T * H
+    return n * (3 * dk + dv) * in_bytes + n * in_bytes + n * dv * o_bytes + B * H * dk * dv * 4
+
+
+def decode_bytes(B, H, dk, dv, in_bytes=2, o_bytes=4):
+    n = B * H
+    return 2 * n * dk * dv * 4 + n * (3 * dk + dv + 1) * in_bytes + n * dv * o_bytes
+
+
+def make_inputs_gpu(B, T, H, dk, dv, seed, device, dtype=torch.bfloat16):
+    """Config distributions on the GPU: q,k = l2norm(N(0,1)); v ~ N(0,1);
+    beta = sigmoid(N(0,1)); g = -softplus(N(0,1)) * exp(a_h), a_h ~ U(-2,0)."""
+    gen = torch.Generator(device=device)
+    gen.manual_seed(seed)
+
+    def l2n(x):
+        return x / (x.norm(dim=-1, keepdim=True) + 1e-12)
+
+    q = l2n(torch.randn(B, T, H, dk, device=device, generator=gen)).to(dtype)
+    k = l2n(torch.randn(B, T, H, dk, device=device, generator=gen)).to(dtype)
+    v = torch.randn(B, T, H, dv, device=device, generator=gen).to(dtype)
+    beta = torch.sigmoid(torch.randn(B, T, H, device=device, generator=gen)).to(dtype)
+    gz = torch.randn(B, T, H, dk, device=device, generator=gen)
+    a = torch.rand(H, device=device, generator=gen) * -2.0
+    g = (-torch.nn.functional.softplus(gz) * torch.exp(a)[None, None, :, None]).to(dtype)
+    return q, k, v, g, beta
+
+
+def copy_bandwidth(device, nbytes=1 << 30, reps=10):
+    x = torch.empty(nbytes // 4, dtype=torch.float32, device=device)
+    y = torch.empty_like(x)
+    y.copy_(x)
+    torch.cuda.synchronize()
+    e0, e1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+    e0.record()
+    for _ in range(reps):
+        y.copy_(x)
+    e1.record()
+    torch.cuda.synchronize()
+    t = e0.elapsed_time(e1) / 1e3 / reps
+    return 2 * nbytes / t / 1e9
+
+
+def bench_forward(args, device):
+    import axiom_amd
+    from axiom_amd import kda as kmod
+    B, T, H, dk, dv, C = (CFG[k] for k in ("B", "T", "H", "dk", "dv", "C"))
+    q, k, v, g, beta = make_inputs_gpu(B, T, H, dk, dv, args.seed, device)
+    ws = torch.empty(kmod.chunk_fwd_workspace_bytes(B, T, H, dk, dv), dtype=torch.uint8, device=device)
+    for _ in range(args.warmup):
+        axiom_amd.kda_chunk_fwd(q, k, v, g, beta, workspace=ws)
+    torch.cuda.synchronize()
+    stream = torch.cuda.current_stream(device)
+    ev = [(torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True))
+          for _ in range(args.steps)]
+    t0 = time.perf_counter()
+    for i in range(args.steps):
+        ev[i][0].record(stream)
+        o, ht = axiom_amd.kda_chunk_fwd(q, k, v, g, beta, workspace=ws)
+        ev[i][1].record(stream)
+    torch.cuda.synchronize()
+    wall = time.perf_counter() - t0
+    per_launch = [a.elapsed_time(b) / 1e3 for a, b in ev]
+    return dict(wall=wall, per_launch=per_launch, o=o, ht=ht, inputs=(q, k, v, g, beta))
+
+
+def bench_decode(args, device):
+    import axiom_amd
+    B, H, d, steps = 256, 16, 128, args.decode_steps
+    gen = torch.Generator(device=device)
+    gen.manual_seed(args.seed + 1)
+    q, k, v, g, beta = make_inputs_gpu(steps, B, H, d, d, args.seed + 2, device)
+    S = torch.randn(B, H, d, d, device=device, generator=gen) * 0.02
+    stream = torch.cuda.current_stream(device)
+    for t in range(min(8, steps)):                       # warm-up on a scratch copy
+        axiom_amd.kda_recurrent_step(q[t], k[t], v[t], g[t], beta[t], S.clone())
+    torch.cuda.synchronize()
+    e0, e1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+    e0.record(stream)
+    for t in range(steps):
+        axiom_amd.kda_recurrent_step(q[t], k[t], v[t], g[t], beta[t], S)
+    e1.record(stream)
+    torch.cuda.synchronize()
+    t_step = e0.elapsed_time(e1) / 1e3 / steps
+    nbytes = decode_bytes(B, H, d, d)
+    gbps = nbytes / t_step / 1e9
+    return dict(us_per_step=t_step * 1e6, gbps=gbps, frac=gbps / HBM_PEAK_GBPS,
+                bytes_per_step=nbytes, steps=steps, config="B256 H16 d128 bf16, fp32 state in place")
+
+
+def cpu_baseline(fwd_inputs, seconds):
+    """Oracle port (fp32, torch CPU) of the reference jax body on a bounded sample."""
+    from oracle import kda_oracle as K
+    n_threads = len(os.sched_getaffinity(0)) if hasattr(os, "sched_getaffinity") else os.cpu_count()
+    torch.set_num_threads(n_threads)
+    q, k, v, g, beta = (x.float().cpu().numpy() for x in fwd_inputs)
+    B, T, H = q.shape[:3]
+
+    def run():
+        t0 = time.perf_counter()
+        K.chunk_fwd(q, k, v, g, beta, chunk=64, dtype=torch.float32)
+        return time.perf_counter() - t0
+
+    run()                                                 # warm-up round
+    times = [run()]
+    budget = time.perf_counter() + seconds
+    while time.perf_counter() < budget or len(times) < 3:
+        times.append(run())
+    med = statistics.median(times)
+    T_s = B * T
+    cpu_model = platform.processor() or ""
+    try:
+        with open("/proc/cpuinfo") as f:
+            for line in f:
+                if line.startswith("model name"):
+                    cpu_model = line.split(":", 1)[1].strip()
+                    break
+    except OSError:
+        pass
+    return {"value": T_s / med, "unit": "tokens/s", "cores": n_threads, "kind": "port",
+            "sample": f"the full workload B={B} T={T} H={H} d=128 C=64 in fp32 (the bench inputs "
+                      f"upcast), median of {len(times)} rounds, {med:.2f} s/round",
+            "cpu_model": cpu_model}
+
+
+def main():
+    ap = argparse.ArgumentParser(description=__doc__.split("\n")[0])
+    ap.add_argument("--gpus", type=int, default=1)
+    ap.add_argument("--steps", type=int, default=20)
+    ap.add_argument("--warmup", type=int, default=5)
+    ap.add_argument("--decode-steps", type=int, default=128)
+    ap.add_argument("--seed", type=int, default=0)
+    ap.add_argument("--cpu-seconds", type=float, default=10.0)
+    ap.add_argument("--no-cpu-baseline", action="store_true")
+    ap.add_argument("--no-decode", action="store_true")
+    args = ap.parse_args()
+    if args.gpus != 1 or int(os.environ.get("WORLD_SIZE", "1")) != 1:
+        print("bench.py measures one GPU only: every (batch, head) chain of this path is "
+              "independent, multi-GPU sharding is described but not run here.", file=sys.stderr)
+        sys.exit(2)
+    if not torch.cuda.is_available():
+        print("bench.py needs a GPU", file=sys.stderr)
+        sys.exit(1)
+    device = torch.device("cuda:0")
+    B, T, H, dk, dv, C = (CFG[k] for k in ("B", "T", "H", "dk", "dv", "C"))
+
+    fwd = bench_forward(args, device)
+    steps = args.steps
+    ms_per_step = fwd["wall"] / steps * 1e3
+    t_launch = statistics.mean(fwd["per_launch"])
+    tokens = B * T
+    flops = tokens * H * flops_per_token_head(C, dk)
+    nbytes = fwd_bytes(B, T, H, dk, dv)
+    value = tokens / (fwd["wall"] / steps)
+    tflops = flops / t_launch / 1e12
+    achieved = nbytes / t_launch / 1e9
+    line = {
+        "metric": "KDA fwd tokens/s + TFLOP/s (% MFMA peak) at B4 T4096 H16 d128; decode HBM GB/s",
+        "value": value,
+        "unit": "tokens/s",
+        "n_gpus": 1,
+        "steps": steps,
+        "warmup": args.warmup,
+        "ms_per_step": ms_per_step,
+        "higher_is_better": True,
+        "scaling": "weak",
+        "vs_baseline": None,
+        "dtype": "bf16",
+        "data": "synthetic",
+        "config": {"workload": "chunked KDA forward B=4 T=4096 H=16 dk=dv=128 C=64, bf16 in, "
+                               "fp32 o and final state, zero initial state",
+                   "global_batch": B, "seq_len": T, "heads": H, "head_dim": dk, "chunk": C},
+        "tflops": tflops,
+        "mfma_peak_frac": tflops / MFMA_BF16_PEAK_TFLOPS,
+        "us_per_launch": t_launch * 1e6,
+        "roofline": {"bound": "hbm", "achieved": achieved, "peak": HBM_PEAK_GBPS, "unit": "GB/s",
+                     "frac": achieved / HBM_PEAK_GBPS, "traffic": None,
+                     "kernels": "kda_intra_kernel + kda_state_kernel (one kda_chunk_fwd)",
+                     "algorithmic_bytes_per_launch": nbytes},
+    }
+    try:
+        line["copy_gbps_measured"] = copy_bandwidth(device)
+    except RuntimeError:
+        line["copy_gbps_measured"] = None
+    if not args.no_decode:
+        line["decode"] = bench_decode(args, device)
+    if not args.no_cpu_baseline:
+        line["cpu_baseline"] = cpu_baseline(fwd["inputs"], args.cpu_seconds)
+    print(json.dumps(line), flush=True)
+
+
+if __name__ == "__main__":
+    main()
