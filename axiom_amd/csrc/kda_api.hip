@@ -1,5 +1,5 @@
 // C ABI of the KDA hot path: argument validation, workspace layout, dispatch.
-#include "../../include/kda_mi355x.h"
+#include "kda_mi355x.h"
 
 #include <cmath>
 #include <cstdarg>

@@ -9,20 +9,31 @@
 //   v~ = U - W S,  o = (gamma q) S + Aqk v~,
 //   S' = diag(gamma_C) S + (lambda k)^T v~,  lambda = exp(G_C - G)
 //
-// Two kernels:
-//  * kda_intra_kernel  -- one workgroup per chunk-head, fully parallel.  Builds
-//    the decay-gated scores on MFMA (off-diagonal 16x16 tiles with both decay
-//    factors <= 1 in fp16; diagonal tiles with a mid-tile anchor in a bf16
-//    hi/lo split, 3 MFMAs, ~fp32 accuracy), solves T = (I+L)^-1 in LDS
-//    (column substitution for the 16x16 diagonal blocks, MFMA for the
-//    off-diagonal blocks), forms W and U, and writes W, U, Aqk, gamma*q,
-//    lambda*k and gamma_C to the workspace in MFMA fragment order.
-//  * kda_state_kernel  -- one workgroup per (chain, 32-column dv slice); walks
-//    the chunks of its chain in order with the fp32 state slice S[dk x 32]
-//    held in MFMA accumulators, and emits o.
+// Decay factors.  The chunk is cut into four 16-row tiles.  With Gt the
+// tile-local inclusive cumsum (log2 units) and D the tile total, every lane
+// needs only R = 2^Gt (<= 1) and Cf = 2^(D - Gt) (<= 1):
+//   off-diagonal tile pair (r > s):  2^(G_c - G_i) = R_c * M_rs * Cf_i,
+//     M_rs = 2^(sum of the totals of the tiles strictly between) <= 1,
+//     so both MFMA operands stay in [0, 1] and run in fp16;
+//   diagonal tile (c >= i):  2^(G_c - G_i) = (R_c 2^-D) * Cf_i, operands up
+//     to 2^|D|, run as fp32 MFMA (16x16x4); a tile whose total decay passes
+//     2^-100 takes a slower mid-tile-anchored path with the same result;
+//   gamma = R * 2^(totals before the tile), lambda = Cf * 2^(totals after).
+// The per-channel constants (2^pre, 2^post, 2^-D, M) are computed once per
+// wave into LDS.
 //
-// Exact mode (fp32 inputs) uses the same code with fp32 operands and
-// 16x16x4 fp32 MFMAs.
+// Work split: wave w of a 256-thread workgroup owns rows 16w..16w+15 (its
+// code is compiled per w so tile-dependent loops are static), lane
+// (r = l & 15, gq = l >> 4) owns row 16w + r and the 8 channel slots of lane
+// group gq in every 32-wide K step (see kda_common.h).
+//
+// Kernels:
+//  * kda_intra_kernel -- one workgroup per chunk-head; writes W, U, Aqk,
+//    gamma*q, lambda*k and gamma_C to the workspace in MFMA fragment order.
+//  * kda_state_kernel -- one workgroup per (chain, 32-column dv slice); walks
+//    the chunks of its chain with the fp32 state slice in MFMA accumulators,
+//    prefetching three chunks ahead, and emits o and the final state.
+// Exact mode (fp32 inputs) runs the same code with fp32 operands.
 
 #include "kda_common.h"
 #include "kda_internal.h"
@@ -65,26 +76,38 @@ __device__ __forceinline__ UnitRef unit_ref(const Geom& G, int u) {
 }
 
 // ----------------------------------------------------------------------------
-// Intra-chunk kernel
+// Intra-chunk work of one chunk-head (device function, per wave W)
 // ----------------------------------------------------------------------------
 template <int DK, int DV, bool EXACT>
 struct IntraSmem {
   typedef typename Prec<EXACT>::st st;
   static constexpr int PK = DK + 8;   // row pitch (elements) of [C][DK] buffers
   static constexpr int PC = kC + 8;   // row pitch of [*][C] buffers
-  st KC[kC * PK];         // k*Cf (slot order); later the lambda*k transpose stage
-  st BWt[DK * PC];        // (beta*gamma*k)^T, rows = channel
-  st BVt[DV * PC];        // (beta*v)^T
-  st Lm[kC * PC];         // L (off-diagonal blocks)
-  st Tm[kC * PC];         // T = (I+L)^-1
-  float Ld[4][16][17];    // diagonal blocks of L, fp32
+  static constexpr int R1 = (kC * PK > DK * PC) ? kC * PK : DK * PC;
+  // region 1, two lives: k*Cf (scores) -> (beta*gamma*k)^T (W product)
+  st r1[R1];
+  st BVt[DV * PC];        // (beta*v)^T, rows = channel
+  st Tm[kC * PC];         // T = (I+L)^-1; wave w writes row block w
+  st Lmb[6][16][20];      // off-diagonal L blocks, row-major; block (R,j) at R(R-1)/2+j
+  st Tdg[4][16][20];      // diagonal T blocks, row-major
+  float Ld[4][16][20];    // diagonal L blocks, fp32
   float tot[4][DK];       // per-tile log2 decay totals, slot order
-  float beta_s[kC];
+  float fac[4][5][DK];    // per tile: 2^pre, 2^post, 2^-D, M(w,w-2), M(w,w-3)
 };
 
-template <int DK, int DV, int DTQ, int DTG, bool EXACT>
-__global__ __launch_bounds__(256, EXACT ? 1 : 2)
-void kda_intra_kernel(IntraArgs a) {
+// slot index (position in a lane-group-major row) of channel d
+__device__ __forceinline__ int channel_slot(int d) {
+  const int jd = d >> 5, wd = d & 31;
+  return 32 * jd + 8 * ((wd & 15) >> 2) + 4 * (wd >> 4) + (wd & 3);
+}
+// channel of slot index s
+__device__ __forceinline__ int slot_index_channel(int s) {
+  return slot_channel(s >> 5, (s >> 3) & 3, s & 7);
+}
+
+template <int DK, int DV, int DTQ, int DTG, bool EXACT, int W>
+__device__ __forceinline__ void intra_chunk(const IntraArgs& a, const UnitRef& U, const int h,
+                                            const int64_t chead, IntraSmem<DK, DV, EXACT>& sm) {
   typedef typename Prec<EXACT>::st st;
   typedef typename Prec<EXACT>::v8 v8;
   typedef typename Prec<EXACT>::v4 v4;
@@ -93,34 +116,24 @@ void kda_intra_kernel(IntraArgs a) {
   constexpr int NJV = DV / 32;
   constexpr int PK = SM::PK;
   constexpr int PC = SM::PC;
-  __shared__ SM sm;
-
   const int tid = threadIdx.x;
-  const int w = tid >> 6, l = tid & 63, r = l & 15, gq = l >> 4;
+  const int l = tid & 63, r = l & 15, gq = l >> 4;
   const int H = a.geom.H;
-  const int u = blockIdx.x / H;
-  const int h = blockIdx.x - u * H;
-  if (a.geom.cu != nullptr && u >= *a.geom.n_units) return;  // uniform per workgroup
-  const UnitRef U = unit_ref(a.geom, u);
-  const int64_t chead = static_cast<int64_t>(u) * H + h;
   st* const oW = static_cast<st*>(a.W);
   st* const oU = static_cast<st*>(a.U);
   st* const oAQ = static_cast<st*>(a.AQ);
   st* const oGQ = static_cast<st*>(a.GQ);
   st* const oLK = static_cast<st*>(a.LK);
 
-  const int c = 16 * w + r;           // my row inside the chunk
+  const int c = 16 * W + r;           // my row inside the chunk
   const bool valid = c < U.len;
   const int64_t tok = U.row0 + c;
-
-  // zero T (its above-diagonal blocks are read as zeros by the W/U products)
-  for (int i = tid; i < kC * PC; i += 256) sm.Tm[i] = st(0);
+  const int64_t bq = (tok * H + h) * DK;
 
   // ---- loads (slot order), masked rows are zero -----------------------------
-  float qv[NJ][8], kv[NJ][8], Gt[NJ][8];
+  float kr[NJ][8], qr[NJ][8], kc[NJ][8], Gt[NJ][8];
   float beta_c = 0.f;
   {
-    const int64_t bq = (tok * H + h) * DK;
 #pragma unroll
     for (int j = 0; j < NJ; ++j) {
 #pragma unroll
@@ -134,8 +147,8 @@ void kda_intra_kernel(IntraArgs a) {
         }
 #pragma unroll
         for (int e = 0; e < 4; ++e) {
-          qv[j][4 * hf + e] = x[e] * a.scale;
-          kv[j][4 * hf + e] = y[e];
+          qr[j][4 * hf + e] = x[e] * a.scale;
+          kr[j][4 * hf + e] = y[e];
           Gt[j][4 * hf + e] = z[e] * kLog2e;
         }
       }
@@ -143,7 +156,7 @@ void kda_intra_kernel(IntraArgs a) {
     if (valid) beta_c = ld1<DTG>(a.beta, tok * H + h);
   }
 
-  // beta * v  -> BVt (channel-major), done early so v is not kept live
+  // beta * v  -> BVt (channel-major)
   {
     const int64_t bv = (tok * H + h) * DV;
 #pragma unroll
@@ -159,319 +172,447 @@ void kda_intra_kernel(IntraArgs a) {
     }
   }
 
-  // ---- tile-local inclusive cumsum (16 rows = 16 lanes of a DPP row) --------
-#pragma unroll
-  for (int j = 0; j < NJ; ++j)
-#pragma unroll
-    for (int e = 0; e < 8; ++e) Gt[j][e] = row_scan16(Gt[j][e]);
-
-  // k * exp2(Dw - Gt) -> KC (column operand of the off-diagonal score tiles)
+  // ---- tile-local cumsum and the two decay factors ---------------------------
+  float dmin = 0.f;
 #pragma unroll
   for (int j = 0; j < NJ; ++j) {
     f8 x;
 #pragma unroll
     for (int e = 0; e < 8; ++e) {
-      const float dw = row_bcast<15>(Gt[j][e]);
-      x[e] = kv[j][e] * fast_exp2(dw - Gt[j][e]);
-      if (r == 15) sm.tot[w][32 * j + 8 * gq + e] = Gt[j][e];
-    }
-    *reinterpret_cast<v8*>(&sm.KC[c * PK + 32 * j + 8 * gq]) = cvt8<EXACT>(x);
-  }
-  if (gq == 0) sm.beta_s[c] = beta_c;
-  __syncthreads();  // #1: tot, KC, BVt, beta_s
-
-  // ---- scores: wave w computes Akk^T / Aqk^T tiles (s, w), s <= w -----------
-  f4 accK[4], accQ[4];
-#pragma unroll
-  for (int s = 0; s < 4; ++s) { accK[s] = f4{0, 0, 0, 0}; accQ[s] = f4{0, 0, 0, 0}; }
-  typedef typename Prec<EXACT>::st stt;
-  stt lk[NJ][8];  // lambda*k, written to the stage after the scores
-
-#pragma unroll
-  for (int j = 0; j < NJ; ++j) {
-    float tt[4][8];
-#pragma unroll
-    for (int t = 0; t < 4; ++t)
-#pragma unroll
-      for (int e = 0; e < 8; ++e) tt[t][e] = sm.tot[t][32 * j + 8 * gq + e];
-
-    f8 kr, qr;         // row operands k*exp2(Gt), q*exp2(Gt)
-    f8 dk_row, dq_row, dk_col;  // diagonal-tile operands (mid-tile anchor)
-#pragma unroll
-    for (int e = 0; e < 8; ++e) {
-      const float gt = Gt[j][e];
-      const float g7 = row_bcast<7>(gt);
-      const float R = fast_exp2(gt);
-      kr[e] = kv[j][e] * R;
-      qr[e] = qv[j][e] * R;
-      const float fr = fast_exp2(gt - g7);
-      const float fc = fast_exp2(g7 - gt);
-      dk_row[e] = kv[j][e] * fr;
-      dq_row[e] = qv[j][e] * fr;
-      dk_col[e] = kv[j][e] * fc;
-    }
-    // off-diagonal tiles s < w
-#pragma unroll
-    for (int s = 0; s < 3; ++s) {
-      if (s < w) {
-        f8 bk = kr, bqv = qr;
-        if (s < w - 1) {
-#pragma unroll
-          for (int e = 0; e < 8; ++e) {
-            float m = 0.f;
-#pragma unroll
-            for (int t = 1; t < 3; ++t)
-              if (t > s && t < w) m += tt[t][e];
-            const float M = fast_exp2(m);
-            bk[e] *= M;
-            bqv[e] *= M;
-          }
-        }
-        const v8 A = *reinterpret_cast<const v8*>(&sm.KC[(16 * s + r) * PK + 32 * j + 8 * gq]);
-        accK[s] = mma32(accK[s], A, cvt8<EXACT>(bk));
-        accQ[s] = mma32(accQ[s], A, cvt8<EXACT>(bqv));
-      }
-    }
-    // diagonal tile s == w
-    {
-      f4 ak = f4{0, 0, 0, 0}, aq = f4{0, 0, 0, 0};
-#pragma unroll
-      for (int s = 0; s < 4; ++s) { if (s == w) { ak = accK[s]; aq = accQ[s]; } }
-      if constexpr (EXACT) {
-        ak = mma32(ak, dk_col, dk_row);
-        aq = mma32(aq, dk_col, dq_row);
-      } else {
-        b8 ah, al, kh, kl, qh, ql;
-#pragma unroll
-        for (int e = 0; e < 8; ++e) {
-          const __bf16 a0 = static_cast<__bf16>(dk_col[e]);
-          ah[e] = a0;
-          al[e] = static_cast<__bf16>(dk_col[e] - static_cast<float>(a0));
-          const __bf16 k0 = static_cast<__bf16>(dk_row[e]);
-          kh[e] = k0;
-          kl[e] = static_cast<__bf16>(dk_row[e] - static_cast<float>(k0));
-          const __bf16 q0 = static_cast<__bf16>(dq_row[e]);
-          qh[e] = q0;
-          ql[e] = static_cast<__bf16>(dq_row[e] - static_cast<float>(q0));
-        }
-        ak = mma32_bf16(ak, ah, kh);
-        ak = mma32_bf16(ak, ah, kl);
-        ak = mma32_bf16(ak, al, kh);
-        aq = mma32_bf16(aq, ah, qh);
-        aq = mma32_bf16(aq, ah, ql);
-        aq = mma32_bf16(aq, al, qh);
-      }
-#pragma unroll
-      for (int s = 0; s < 4; ++s) { if (s == w) { accK[s] = ak; accQ[s] = aq; } }
-    }
-
-    // gamma, lambda for this K step: q*gamma -> GQ (fragment order), the W
-    // right-hand side beta*gamma*k -> BWt, lambda*k kept for the stage
-    f8 gqv;
-#pragma unroll
-    for (int e = 0; e < 8; ++e) {
-      float pre = 0.f, post = 0.f;
-#pragma unroll
-      for (int t = 0; t < 4; ++t) {
-        if (t < w) pre += tt[t][e];
-        if (t > w) post += tt[t][e];
-      }
-      const float gt = Gt[j][e];
+      const float gt = row_scan16(Gt[j][e]);
+      Gt[j][e] = gt;
       const float dw = row_bcast<15>(gt);
-      const float gam = fast_exp2(pre + gt);
-      const float lam = fast_exp2(post + dw - gt);
-      gqv[e] = gam * qv[j][e];
-      lk[j][e] = stt(lam * kv[j][e]);
-      sm.BWt[slot_channel(j, gq, e) * PC + c] = st(beta_c * gam * kv[j][e]);
+      dmin = fminf(dmin, dw);
+      const float R = fast_exp2(gt);
+      kc[j][e] = kr[j][e] * fast_exp2(dw - gt);
+      kr[j][e] *= R;
+      qr[j][e] *= R;
+      x[e] = kc[j][e];
+      if (r == 15) sm.tot[W][32 * j + 8 * gq + e] = gt;
     }
-    *reinterpret_cast<v8*>(oGQ + (chead * (kC / 16) * NJ + (w * NJ + j)) * 512 + l * 8) =
-        cvt8<EXACT>(gqv);
-    if (w == 0 && r == 0) {
-#pragma unroll
-      for (int e = 0; e < 8; ++e)
-        a.GC[chead * DK + slot_channel(j, gq, e)] =
-            fast_exp2(tt[0][e] + tt[1][e] + tt[2][e] + tt[3][e]);
-    }
+    *reinterpret_cast<v8*>(&sm.r1[c * PK + 32 * j + 8 * gq]) = cvt8<EXACT>(x);
   }
+  // a tile whose decay total passes 2^-100 in some channel: anchored path
+  const bool extreme = __any(dmin < -100.f);
+  lds_barrier();  // #1: tot, k*Cf, BVt
 
-  // masks, L and Aqk fragments
-  {
+  // ---- per-channel constants of this tile (wave-local) -----------------------
 #pragma unroll
-    for (int s = 0; s < 4; ++s) {
-      if (s <= w) {
+  for (int s0 = l; s0 < DK; s0 += 64) {
+    const float tt[4] = {sm.tot[0][s0], sm.tot[1][s0], sm.tot[2][s0], sm.tot[3][s0]};
+    float pre = 0.f, post = 0.f;
 #pragma unroll
-        for (int i = 0; i < 4; ++i) {
-          const int ii = 4 * gq + i;  // row of the tile = key index i
-          if (s == w) {
-            if (!(r > ii)) accK[s][i] = 0.f;
-            if (!(r >= ii)) accQ[s][i] = 0.f;
-          }
-        }
-        if (s < w) {
-          v4 lv;
-#pragma unroll
-          for (int i = 0; i < 4; ++i) lv[i] = st(beta_c * accK[s][i]);
-          *reinterpret_cast<v4*>(&sm.Lm[c * PC + 16 * s + 4 * gq]) = lv;
-        } else {
-#pragma unroll
-          for (int i = 0; i < 4; ++i) sm.Ld[w][r][4 * gq + i] = beta_c * accK[s][i];
-        }
-      }
+    for (int t = 0; t < 4; ++t) {
+      if (t < W) pre += tt[t];
+      if (t > W) post += tt[t];
     }
-    // Aqk fragments for the state kernel: row tile w, K step jj pairs key tiles (2jj, 2jj+1)
-#pragma unroll
-    for (int jj = 0; jj < 2; ++jj) {
-      f8 x;
-#pragma unroll
-      for (int hf = 0; hf < 2; ++hf) {
-        const int s = 2 * jj + hf;
-#pragma unroll
-        for (int i = 0; i < 4; ++i) x[4 * hf + i] = (s <= w) ? accQ[s][i] : 0.f;
-      }
-      *reinterpret_cast<v8*>(oAQ + (chead * (kC / 16) * 2 + (w * 2 + jj)) * 512 + l * 8) =
-          cvt8<EXACT>(x);
-    }
+    sm.fac[W][0][s0] = fast_exp2(pre);
+    sm.fac[W][1][s0] = fast_exp2(post);
+    sm.fac[W][2][s0] = fast_exp2(-tt[W]);
+    if constexpr (W >= 2) sm.fac[W][3][s0] = fast_exp2(tt[W - 1]);
+    if constexpr (W >= 3) sm.fac[W][4][s0] = fast_exp2(tt[W - 1] + tt[W - 2]);
+    if constexpr (W == 0) a.GC[chead * DK + slot_index_channel(s0)] = fast_exp2(tt[0] + tt[1] + tt[2] + tt[3]);
   }
-  __syncthreads();  // #2: Lm, Ld ready; KC free
+  __builtin_amdgcn_wave_barrier();  // this wave reads back its own fac[W] below
 
-  // lambda*k -> stage (reuses KC)
+  // ---- scores: Akk^T / Aqk^T tiles (s, W), s <= W ----------------------------
+  f4 accK[W + 1], accQ[W + 1];
+#pragma unroll
+  for (int s = 0; s <= W; ++s) { accK[s] = f4{0, 0, 0, 0}; accQ[s] = f4{0, 0, 0, 0}; }
+  st lk[NJ][8];  // lambda*k
+  st bw[NJ][8];  // beta*gamma*k
+
 #pragma unroll
   for (int j = 0; j < NJ; ++j) {
-    v8 x;
+    const int sb = 32 * j + 8 * gq;
+    const f8 P = *reinterpret_cast<const f8*>(&sm.fac[W][0][sb]);
+    const f8 Q = *reinterpret_cast<const f8*>(&sm.fac[W][1][sb]);
+    const f8 iD = *reinterpret_cast<const f8*>(&sm.fac[W][2][sb]);
+    f8 krj, qrj;
 #pragma unroll
-    for (int e = 0; e < 8; ++e) x[e] = lk[j][e];
-    *reinterpret_cast<v8*>(&sm.KC[c * PK + 32 * j + 8 * gq]) = x;
-  }
+    for (int e = 0; e < 8; ++e) { krj[e] = kr[j][e]; qrj[e] = qr[j][e]; }
 
-  // diagonal block inverse: lane (any group) computes column r of T_ww
-  {
-    float x[16];
-#pragma unroll
-    for (int i = 0; i < 16; ++i) {
-      float acc = 0.f;
-#pragma unroll
-      for (int m = 0; m < i; ++m) acc += sm.Ld[w][i][m] * x[m];
-      x[i] = (i < r) ? 0.f : ((i == r) ? 1.f : -acc);
+    // off-diagonal tiles: A = k*Cf of key tile s (LDS), B = row operand of tile W
+    if constexpr (W >= 1) {
+      constexpr int s = W - 1;
+      const v8 A = *reinterpret_cast<const v8*>(&sm.r1[(16 * s + r) * PK + sb]);
+      accK[s] = mma32(accK[s], A, cvt8<EXACT>(krj));
+      accQ[s] = mma32(accQ[s], A, cvt8<EXACT>(qrj));
     }
-    if (gq == 0) {
-#pragma unroll
-      for (int i = 0; i < 16; ++i) sm.Tm[(16 * w + i) * PC + 16 * w + r] = st(x[i]);
+    if constexpr (W >= 2) {
+      constexpr int s = W - 2;
+      const f8 M2 = *reinterpret_cast<const f8*>(&sm.fac[W][3][sb]);
+      const v8 A = *reinterpret_cast<const v8*>(&sm.r1[(16 * s + r) * PK + sb]);
+      accK[s] = mma32(accK[s], A, cvt8<EXACT>(krj * M2));
+      accQ[s] = mma32(accQ[s], A, cvt8<EXACT>(qrj * M2));
     }
-  }
-  __syncthreads();  // #3: diagonal T blocks, lambda*k stage
-
-  // lambda*k fragments for the state update: (lambda k)^T tile rows = channel
-  {
-    constexpr int DTW = DK / 64;  // channel tiles per wave
+    if constexpr (W >= 3) {
+      constexpr int s = W - 3;
+      const f8 M3 = *reinterpret_cast<const f8*>(&sm.fac[W][4][sb]);
+      const v8 A = *reinterpret_cast<const v8*>(&sm.r1[(16 * s + r) * PK + sb]);
+      accK[s] = mma32(accK[s], A, cvt8<EXACT>(krj * M3));
+      accQ[s] = mma32(accQ[s], A, cvt8<EXACT>(qrj * M3));
+    }
+    // diagonal tile in fp32
+    {
+      f8 ad, bk, bqd;
+      if (!extreme) {
 #pragma unroll
-    for (int t = 0; t < DTW; ++t) {
-      const int dt = w * DTW + t;
-      const int d = 16 * dt + r;
-      const int jd = d >> 5, wd = d & 31;
-      const int sidx = 32 * jd + 8 * ((wd & 15) >> 2) + 4 * (wd >> 4) + (wd & 3);
+        for (int e = 0; e < 8; ++e) { ad[e] = kc[j][e]; bk[e] = krj[e] * iD[e]; bqd[e] = qrj[e] * iD[e]; }
+      } else {
+        // mid-tile anchor: 2^(Gt_c - Gt_7) * 2^(Gt_7 - Gt_i); k and q are reloaded
 #pragma unroll
-      for (int jj = 0; jj < 2; ++jj) {
-        v8 x;
+        for (int hf = 0; hf < 2; ++hf) {
+          const int ch0 = 32 * j + 4 * gq + 16 * hf;
+          f4 x = {0, 0, 0, 0}, y = {0, 0, 0, 0};
+          if (valid) { x = ld4<DTQ>(a.q, bq + ch0); y = ld4<DTQ>(a.k, bq + ch0); }
 #pragma unroll
-        for (int e = 0; e < 8; ++e) {
-          const int cc = slot_channel(jj, gq, e);
-          x[e] = sm.KC[cc * PK + sidx];
+          for (int e = 0; e < 4; ++e) {
+            const int ee = 4 * hf + e;
+            const float gt = Gt[j][ee];
+            const float g7 = row_bcast<7>(gt);
+            const float fr = fast_exp2(gt - g7);
+            ad[ee] = y[e] * fast_exp2(g7 - gt);
+            bk[ee] = y[e] * fr;
+            bqd[ee] = x[e] * a.scale * fr;
+          }
         }
-        *reinterpret_cast<v8*>(oLK + (chead * (DK / 16) * 2 + (dt * 2 + jj)) * 512 + l * 8) = x;
       }
+      accK[W] = mma32(accK[W], ad, bk);
+      accQ[W] = mma32(accQ[W], ad, bqd);
     }
+
+    // q*gamma -> GQ (fragment order); beta*gamma*k and lambda*k kept
+    f8 gqv;
+    const float bc = beta_c;
+#pragma unroll
+    for (int e = 0; e < 8; ++e) {
+      gqv[e] = qrj[e] * P[e];
+      lk[j][e] = st(kc[j][e] * Q[e]);
+      bw[j][e] = st(krj[e] * (bc * P[e]));
+    }
+    *reinterpret_cast<v8*>(oGQ + (chead * (kC / 16) * NJ + (W * NJ + j)) * 512 + l * 8) =
+        cvt8<EXACT>(gqv);
   }
 
-  // off-diagonal blocks of T by increasing distance:
-  //   T_ws = -T_ww * sum_{j=s}^{w-1} L_wj T_js
+  // masks; L = beta_c * Akk stays in registers (Lk[s] = 16x16x16 A fragment of L_{W,s})
 #pragma unroll
-  for (int dist = 1; dist < 4; ++dist) {
-    if (w >= dist) {
-      const int s = w - dist;
+  for (int i = 0; i < 4; ++i) {
+    const int ii = 4 * gq + i;  // key row of the tile
+    if (!(r > ii)) accK[W][i] = 0.f;
+    if (!(r >= ii)) accQ[W][i] = 0.f;
+  }
+  f4 Lk[W + 1];
+#pragma unroll
+  for (int s = 0; s <= W; ++s) Lk[s] = accK[s] * beta_c;
+  // Aqk fragments for the state kernel: row tile W, K step jj pairs key tiles (2jj, 2jj+1)
+#pragma unroll
+  for (int jj = 0; jj < 2; ++jj) {
+    f8 x;
+#pragma unroll
+    for (int hf = 0; hf < 2; ++hf) {
+      const int s = 2 * jj + hf;
+#pragma unroll
+      for (int i = 0; i < 4; ++i) x[4 * hf + i] = (s <= W) ? accQ[s <= W ? s : 0][i] : 0.f;
+    }
+    *reinterpret_cast<v8*>(oAQ + (chead * (kC / 16) * 2 + (W * 2 + jj)) * 512 + l * 8) =
+        cvt8<EXACT>(x);
+  }
+
+  // lambda*k fragments for the state update, transposed by an MFMA against a
+  // selection matrix: D[c][d] = sum_slot lk[c][slot] I[slot][d] lands in the D
+  // layout (lane = channel d, rows c), which is half of the (lambda k)^T A
+  // fragment of K step W/2.
+#pragma unroll
+  for (int dt = 0; dt < DK / 16; ++dt) {
+    const int j = dt >> 1;
+    v8 A, Isel;
+#pragma unroll
+    for (int e = 0; e < 8; ++e) {
+      A[e] = lk[j][e];
+      Isel[e] = st((gq == (r >> 2) && e == 4 * (dt & 1) + (r & 3)) ? 1.f : 0.f);
+    }
+    const f4 D = mma32(f4{0, 0, 0, 0}, A, Isel);
+    *reinterpret_cast<v4*>(oLK + (chead * (DK / 16) * 2 + (dt * 2 + (W >> 1))) * 512 + l * 8 +
+                           (W & 1) * 4) = cvt4<EXACT>(D);
+  }
+
+  // L blocks -> LDS: off-diagonal ones for the other waves' T rows, the own
+  // diagonal one in fp32 for the substitution below
+#pragma unroll
+  for (int s = 0; s < W; ++s)
+    *reinterpret_cast<v4*>(&sm.Lmb[W * (W - 1) / 2 + s][r][4 * gq]) = cvt4<EXACT>(Lk[s]);
+  *reinterpret_cast<f4*>(&sm.Ld[W][r][4 * gq]) = Lk[W];
+  __builtin_amdgcn_wave_barrier();
+
+  // diagonal block inverse: column r of T_WW by forward substitution
+  float x[16];
+#pragma unroll
+  for (int i = 0; i < 16; ++i) {
+    float acc = 0.f;
+#pragma unroll
+    for (int m4 = 0; m4 < i; m4 += 4) {
+      const f4 Lrow = *reinterpret_cast<const f4*>(&sm.Ld[W][i][m4]);
+#pragma unroll
+      for (int t = 0; t < 4; ++t)
+        if (m4 + t < i) acc += Lrow[t] * x[m4 + t];
+    }
+    x[i] = (i < r) ? 0.f : ((i == r) ? 1.f : -acc);
+  }
+  if (gq == 0) {
+#pragma unroll
+    for (int i = 0; i < 16; ++i) sm.Tdg[W][i][r] = st(x[i]);
+  }
+  lds_barrier();  // #2: Lmb, Tdg of every wave; region 1 free
+
+  // beta*gamma*k -> region 1, channel-major (the W product's A operand)
+#pragma unroll
+  for (int j = 0; j < NJ; ++j)
+#pragma unroll
+    for (int e = 0; e < 8; ++e) sm.r1[slot_channel(j, gq, e) * PC + c] = bw[j][e];
+
+  // rows 1..W of T in registers (each wave recomputes the earlier rows it needs):
+  //   T_Rs = -T_RR sum_{j=s}^{R-1} L_Rj T_js,  T_js in the D layout (= B layout)
+  f4 Toff[6];
+#pragma unroll
+  for (int R = 1; R <= W; ++R) {
+#pragma unroll
+    for (int s = R - 1; s >= 0; --s) {
       f4 X = {0, 0, 0, 0};
-      for (int jb = s; jb < w; ++jb) {
-        v4 A = *reinterpret_cast<const v4*>(&sm.Lm[(16 * w + r) * PC + 16 * jb + 4 * gq]);
-        v4 Bm;
 #pragma unroll
-        for (int i = 0; i < 4; ++i) Bm[i] = sm.Tm[(16 * jb + 4 * gq + i) * PC + 16 * s + r];
+      for (int jb = s; jb < R; ++jb) {
+        v4 A;
+        if (R == W) A = cvt4<EXACT>(Lk[jb]);
+        else A = *reinterpret_cast<const v4*>(&sm.Lmb[R * (R - 1) / 2 + jb][r][4 * gq]);
+        v4 Bm;
+        if (jb == s) {
+#pragma unroll
+          for (int i = 0; i < 4; ++i) Bm[i] = sm.Tdg[s][4 * gq + i][r];
+        } else {
+          Bm = cvt4<EXACT>(Toff[jb * (jb - 1) / 2 + s]);
+        }
         X = mma16(X, A, Bm);
       }
-      v4 A2 = *reinterpret_cast<const v4*>(&sm.Tm[(16 * w + r) * PC + 16 * w + 4 * gq]);
-      f4 Y = mma16(f4{0, 0, 0, 0}, A2, cvt4<EXACT>(X));
-#pragma unroll
-      for (int i = 0; i < 4; ++i) sm.Tm[(16 * w + 4 * gq + i) * PC + 16 * s + r] = st(-Y[i]);
+      const v4 A2 = *reinterpret_cast<const v4*>(&sm.Tdg[R][r][4 * gq]);
+      Toff[R * (R - 1) / 2 + s] = -mma16(f4{0, 0, 0, 0}, A2, cvt4<EXACT>(X));
     }
-    __syncthreads();  // #4..#6
   }
+  // own row block of T -> Tm (read back by this wave only)
+#pragma unroll
+  for (int s = 0; s < W; ++s)
+#pragma unroll
+    for (int i = 0; i < 4; ++i)
+      sm.Tm[(16 * W + 4 * gq + i) * PC + 16 * s + r] = st(Toff[W * (W - 1) / 2 + s][i]);
+  if constexpr ((W & 1) == 0) {
+    // the next tile's columns are inside this row's K range and must read as zero
+#pragma unroll
+    for (int i = 0; i < 4; ++i) sm.Tm[(16 * W + 4 * gq + i) * PC + 16 * (W + 1) + r] = st(0);
+  }
+  if (gq == 0) {
+#pragma unroll
+    for (int i = 0; i < 16; ++i) sm.Tm[(16 * W + i) * PC + 16 * W + r] = st(x[i]);
+  }
+  lds_barrier();  // #3: (beta*gamma*k)^T of every wave; own T rows
 
-  // ---- W^T tiles and U tiles for row tile w ---------------------------------
-  const int nk = (w < 2) ? 1 : 2;
+  // ---- W^T tiles and U tiles for row tile W ---------------------------------
+  constexpr int nk = (W < 2) ? 1 : 2;
 #pragma unroll
   for (int dt = 0; dt < DK / 16; ++dt) {
     f4 acc = {0, 0, 0, 0};
+#pragma unroll
     for (int jc = 0; jc < nk; ++jc) {
-      const v8 A = *reinterpret_cast<const v8*>(&sm.BWt[(16 * dt + r) * PC + 32 * jc + 8 * gq]);
-      const v8 B = *reinterpret_cast<const v8*>(&sm.Tm[(16 * w + r) * PC + 32 * jc + 8 * gq]);
+      const v8 A = *reinterpret_cast<const v8*>(&sm.r1[(16 * dt + r) * PC + 32 * jc + 8 * gq]);
+      const v8 B = *reinterpret_cast<const v8*>(&sm.Tm[(16 * W + r) * PC + 32 * jc + 8 * gq]);
       acc = mma32(acc, A, B);
     }
-    *reinterpret_cast<v4*>(oW + (chead * (kC / 16) * NJ + (w * NJ + (dt >> 1))) * 512 + l * 8 +
+    *reinterpret_cast<v4*>(oW + (chead * (kC / 16) * NJ + (W * NJ + (dt >> 1))) * 512 + l * 8 +
                            (dt & 1) * 4) = cvt4<EXACT>(acc);
   }
 #pragma unroll
   for (int et = 0; et < DV / 16; ++et) {
     f4 acc = {0, 0, 0, 0};
+#pragma unroll
     for (int jc = 0; jc < nk; ++jc) {
-      const v8 A = *reinterpret_cast<const v8*>(&sm.Tm[(16 * w + r) * PC + 32 * jc + 8 * gq]);
+      const v8 A = *reinterpret_cast<const v8*>(&sm.Tm[(16 * W + r) * PC + 32 * jc + 8 * gq]);
       const v8 B = *reinterpret_cast<const v8*>(&sm.BVt[(16 * et + r) * PC + 32 * jc + 8 * gq]);
       acc = mma32(acc, A, B);
     }
-    *reinterpret_cast<v4*>(oU + (chead * (kC / 16) * (DV / 16) + (w * (DV / 16) + et)) * 256 +
+    *reinterpret_cast<v4*>(oU + (chead * (kC / 16) * (DV / 16) + (W * (DV / 16) + et)) * 256 +
                            l * 4) = cvt4<EXACT>(acc);
   }
 }
 
+template <int DK, int DV, int DTQ, int DTG, bool EXACT>
+__global__ __launch_bounds__(256, EXACT ? 1 : 2)
+void kda_intra_kernel(IntraArgs a) {
+  __shared__ IntraSmem<DK, DV, EXACT> sm;
+  const int H = a.geom.H;
+  const int u = blockIdx.x / H;
+  const int h = blockIdx.x - u * H;
+  if (a.geom.cu != nullptr && u >= *a.geom.n_units) return;  // uniform per workgroup
+  const UnitRef U = unit_ref(a.geom, u);
+  const int64_t chead = static_cast<int64_t>(u) * H + h;
+  switch (threadIdx.x >> 6) {
+    case 0: intra_chunk<DK, DV, DTQ, DTG, EXACT, 0>(a, U, h, chead, sm); break;
+    case 1: intra_chunk<DK, DV, DTQ, DTG, EXACT, 1>(a, U, h, chead, sm); break;
+    case 2: intra_chunk<DK, DV, DTQ, DTG, EXACT, 2>(a, U, h, chead, sm); break;
+    default: intra_chunk<DK, DV, DTQ, DTG, EXACT, 3>(a, U, h, chead, sm); break;
+  }
+}
+
 // ----------------------------------------------------------------------------
-// State kernel: serial over the chunks of one chain, 32 value columns per WG
+// State step: one chunk of one chain for a 32-column value slice
 // ----------------------------------------------------------------------------
-template <int DK, int DV, bool EXACT, int OUT_DT>
-__global__ __launch_bounds__(256, 1)
-void kda_state_kernel(StateArgs a) {
+template <int DK, bool EXACT>
+struct StateFrags {
+  typedef typename Prec<EXACT>::v8 v8;
+  typedef typename Prec<EXACT>::v4 v4;
+  static constexpr int NJ = DK / 32;
+  static constexpr int DTW = DK / 64;
+  v8 W[NJ], Q[NJ], A[2], L[DTW][2];
+  v4 U[2];
+  f4 gc[DTW];
+};
+
+template <int DK, int DV, bool EXACT>
+struct StateSmem {
+  typedef typename Prec<EXACT>::st st;
+  static constexpr int PK = DK + 8;
+  static constexpr int PC = kC + 8;
+  st St[32 * PK];   // S^T slice: [value col][channel]
+  st Vt[32 * PC];   // v~^T: [value col][row]
+};
+
+template <int DK, int DV, bool EXACT, int W>
+__device__ __forceinline__ void load_frags(StateFrags<DK, EXACT>& f, const StateArgs& a,
+                                           int64_t chead, int split, int l, int gq) {
   typedef typename Prec<EXACT>::st st;
   typedef typename Prec<EXACT>::v8 v8;
   typedef typename Prec<EXACT>::v4 v4;
   constexpr int NJ = DK / 32;
-  constexpr int SPLITS = DV / 32;
-  constexpr int DTW = DK / 64;          // state channel tiles per wave
+  constexpr int DTW = DK / 64;
+  const st* iW = static_cast<const st*>(a.W);
+  const st* iQ = static_cast<const st*>(a.GQ);
+  const st* iA = static_cast<const st*>(a.AQ);
+  const st* iL = static_cast<const st*>(a.LK);
+  const st* iU = static_cast<const st*>(a.U);
+#pragma unroll
+  for (int j = 0; j < NJ; ++j) {
+    f.W[j] = *reinterpret_cast<const v8*>(iW + (chead * (kC / 16) * NJ + (W * NJ + j)) * 512 + l * 8);
+    f.Q[j] = *reinterpret_cast<const v8*>(iQ + (chead * (kC / 16) * NJ + (W * NJ + j)) * 512 + l * 8);
+  }
+  constexpr int NA = (W < 2) ? 1 : 2;  // Aqk row tile W has no keys past tile W
+#pragma unroll
+  for (int jj = 0; jj < NA; ++jj)
+    f.A[jj] = *reinterpret_cast<const v8*>(iA + (chead * (kC / 16) * 2 + (W * 2 + jj)) * 512 + l * 8);
+#pragma unroll
+  for (int et = 0; et < 2; ++et)
+    f.U[et] = *reinterpret_cast<const v4*>(
+        iU + (chead * (kC / 16) * (DV / 16) + (W * (DV / 16) + 2 * split + et)) * 256 + l * 4);
+#pragma unroll
+  for (int t = 0; t < DTW; ++t) {
+    const int dt = W * DTW + t;
+#pragma unroll
+    for (int jj = 0; jj < 2; ++jj)
+      f.L[t][jj] = *reinterpret_cast<const v8*>(iL + (chead * (DK / 16) * 2 + (dt * 2 + jj)) * 512 + l * 8);
+    f.gc[t] = *reinterpret_cast<const f4*>(a.GC + chead * DK + 16 * dt + 4 * gq);
+  }
+}
+
+template <int DK, int DV, bool EXACT, int OUT_DT, int W>
+__device__ __forceinline__ void state_step(f4 (&S)[DK / 64][2], const StateFrags<DK, EXACT>& f,
+                                           StateSmem<DK, DV, EXACT>& sm, const StateArgs& a,
+                                           int64_t row0, int len, int h, int split,
+                                           int r, int gq) {
+  typedef typename Prec<EXACT>::st st;
+  typedef typename Prec<EXACT>::v8 v8;
+  typedef typename Prec<EXACT>::v4 v4;
+  constexpr int NJ = DK / 32;
+  constexpr int DTW = DK / 64;
   constexpr int PK = DK + 8;
   constexpr int PC = kC + 8;
-  __shared__ st St[32 * PK];            // S^T slice: [value col][channel]
-  __shared__ st Vt[32 * PC];            // v~^T: [value col][row]
+  const int H = a.geom.H;
 
-  const int tid = threadIdx.x;
-  const int w = tid >> 6, l = tid & 63, r = l & 15, gq = l >> 4;
+  // 1. S^T slice -> LDS (operand precision)
+#pragma unroll
+  for (int t = 0; t < DTW; ++t)
+#pragma unroll
+    for (int et = 0; et < 2; ++et)
+      *reinterpret_cast<v4*>(&sm.St[(16 * et + r) * PK + 16 * (W * DTW + t) + 4 * gq]) = cvt4<EXACT>(S[t][et]);
+  lds_barrier();
+
+  // 2. P = W S, O = (gamma q) S, v~ = U - P
+  f4 O[2];
+#pragma unroll
+  for (int et = 0; et < 2; ++et) {
+    f4 P = {0, 0, 0, 0};
+    O[et] = f4{0, 0, 0, 0};
+#pragma unroll
+    for (int j = 0; j < NJ; ++j) {
+      v8 Sf;
+      const st* row = &sm.St[(16 * et + r) * PK + 32 * j + 4 * gq];
+      const v4 s0 = *reinterpret_cast<const v4*>(row);
+      const v4 s1 = *reinterpret_cast<const v4*>(row + 16);
+#pragma unroll
+      for (int i = 0; i < 4; ++i) { Sf[i] = s0[i]; Sf[4 + i] = s1[i]; }
+      P = mma32(P, f.W[j], Sf);
+      O[et] = mma32(O[et], f.Q[j], Sf);
+    }
+    f4 vt;
+#pragma unroll
+    for (int i = 0; i < 4; ++i) vt[i] = static_cast<float>(f.U[et][i]) - P[i];
+    *reinterpret_cast<v4*>(&sm.Vt[(16 * et + r) * PC + 16 * W + 4 * gq]) = cvt4<EXACT>(vt);
+  }
+  lds_barrier();
+
+  // 3. O += Aqk v~ ; 4. S <- gamma_C S + (lambda k)^T v~
+  constexpr int NA = (W < 2) ? 1 : 2;
+#pragma unroll
+  for (int et = 0; et < 2; ++et) {
+    v8 Vf[2];
+#pragma unroll
+    for (int jj = 0; jj < 2; ++jj) {
+      const st* row = &sm.Vt[(16 * et + r) * PC + 32 * jj + 4 * gq];
+      const v4 s0 = *reinterpret_cast<const v4*>(row);
+      const v4 s1 = *reinterpret_cast<const v4*>(row + 16);
+#pragma unroll
+      for (int i = 0; i < 4; ++i) { Vf[jj][i] = s0[i]; Vf[jj][4 + i] = s1[i]; }
+    }
+#pragma unroll
+    for (int jj = 0; jj < NA; ++jj) O[et] = mma32(O[et], f.A[jj], Vf[jj]);
+#pragma unroll
+    for (int t = 0; t < DTW; ++t) {
+      f4 s = S[t][et] * f.gc[t];
+      s = mma32(s, f.L[t][0], Vf[0]);
+      s = mma32(s, f.L[t][1], Vf[1]);
+      S[t][et] = s;
+    }
+  }
+  // o stores last: nothing in this step reuses their source registers, so the
+  // caller's next prefetch is younger than every pending store
+#pragma unroll
+  for (int et = 0; et < 2; ++et)
+#pragma unroll
+    for (int i = 0; i < 4; ++i) {
+      const int cr = 16 * W + 4 * gq + i;
+      if (cr < len) {
+        const int64_t oi = ((row0 + cr) * H + h) * (int64_t)DV + 32 * split + 16 * et + r;
+        if constexpr (OUT_DT == 0) static_cast<float*>(a.o)[oi] = O[et][i];
+        else static_cast<u16*>(a.o)[oi] = f32_to_bf16_bits(O[et][i]);
+      }
+    }
+  // (the next step's first barrier orders St/Vt reuse)
+}
+
+template <int DK, int DV, bool EXACT, int OUT_DT, int W>
+__device__ __forceinline__ void state_chain(const StateArgs& a, StateSmem<DK, DV, EXACT>& sm,
+                                            int seq, int h, int split) {
+  constexpr int DTW = DK / 64;
   const Geom& G = a.geom;
   const int H = G.H;
-
-  // XCD-aware mapping: the SPLITS workgroups of one chain share an XCD (and L2)
-  const st* const iW = static_cast<const st*>(a.W);
-  const st* const iU = static_cast<const st*>(a.U);
-  const st* const iAQ = static_cast<const st*>(a.AQ);
-  const st* const iGQ = static_cast<const st*>(a.GQ);
-  const st* const iLK = static_cast<const st*>(a.LK);
-  const int x = blockIdx.x;
-  const int xcd = x & 7;
-  const int kk = x >> 3;
-  const int slot = kk / SPLITS;
-  const int split = kk - slot * SPLITS;
-  const int chain = slot * 8 + xcd;
-  if (chain >= G.N * H) return;
-  const int seq_rank = chain / H;
-  const int h = chain - seq_rank * H;
-  const int seq = (G.order != nullptr) ? G.order[seq_rank] : seq_rank;
-
-  int u0, nchunks;
+  const int l = threadIdx.x & 63, r = l & 15, gq = l >> 4;
+  int u0, nchunks, seq_len;
   int64_t tok0;
-  int seq_len;
   if (G.cu == nullptr) {
     u0 = seq * G.NT;
     nchunks = G.NT;
@@ -484,7 +625,6 @@ void kda_state_kernel(StateArgs a) {
     seq_len = G.cu_clamped[seq + 1] - G.cu_clamped[seq];
   }
 
-  // state accumulators: tiles (dt = w*DTW + t, et), rows 4*gq+i, column r
   f4 S[DTW][2];
   const int64_t sbase = (static_cast<int64_t>(seq) * H + h) * DK * DV;
 #pragma unroll
@@ -493,107 +633,35 @@ void kda_state_kernel(StateArgs a) {
     for (int et = 0; et < 2; ++et)
 #pragma unroll
       for (int i = 0; i < 4; ++i) {
-        const int d = 16 * (w * DTW + t) + 4 * gq + i;
+        const int d = 16 * (W * DTW + t) + 4 * gq + i;
         const int e = 32 * split + 16 * et + r;
         S[t][et][i] = (a.h0 != nullptr) ? a.h0[sbase + static_cast<int64_t>(d) * DV + e] : 0.f;
       }
 
-  for (int n = 0; n < nchunks; ++n) {
-    const int64_t chead = static_cast<int64_t>(u0 + n) * H + h;
+  auto chead_of = [&](int n) { return static_cast<int64_t>(u0 + n) * H + h; };
+  auto step = [&](const StateFrags<DK, EXACT>& f, int n) {
     const int64_t row0 = tok0 + static_cast<int64_t>(n) * kC;
-    const int len = min(kC, static_cast<int>(seq_len - static_cast<int64_t>(n) * kC));
-
-    // operands of this chunk (fragment order, written by the intra kernel)
-    v8 Wf[NJ], Qf[NJ], Af[2], Lf[DTW][2];
-    v4 Uf[2];
-    f4 gc[DTW];
-#pragma unroll
-    for (int j = 0; j < NJ; ++j) {
-      Wf[j] = *reinterpret_cast<const v8*>(iW + (chead * (kC / 16) * NJ + (w * NJ + j)) * 512 + l * 8);
-      Qf[j] = *reinterpret_cast<const v8*>(iGQ + (chead * (kC / 16) * NJ + (w * NJ + j)) * 512 + l * 8);
-    }
-#pragma unroll
-    for (int jj = 0; jj < 2; ++jj)
-      Af[jj] = *reinterpret_cast<const v8*>(iAQ + (chead * (kC / 16) * 2 + (w * 2 + jj)) * 512 + l * 8);
-#pragma unroll
-    for (int et = 0; et < 2; ++et)
-      Uf[et] = *reinterpret_cast<const v4*>(
-          iU + (chead * (kC / 16) * (DV / 16) + (w * (DV / 16) + 2 * split + et)) * 256 + l * 4);
-#pragma unroll
-    for (int t = 0; t < DTW; ++t) {
-      const int dt = w * DTW + t;
-#pragma unroll
-      for (int jj = 0; jj < 2; ++jj)
-        Lf[t][jj] = *reinterpret_cast<const v8*>(iLK + (chead * (DK / 16) * 2 + (dt * 2 + jj)) * 512 + l * 8);
-      gc[t] = *reinterpret_cast<const f4*>(a.GC + chead * DK + 16 * dt + 4 * gq);
-    }
-
-    // 1. S^T slice -> LDS (operand precision)
-#pragma unroll
-    for (int t = 0; t < DTW; ++t)
-#pragma unroll
-      for (int et = 0; et < 2; ++et)
-        *reinterpret_cast<v4*>(&St[(16 * et + r) * PK + 16 * (w * DTW + t) + 4 * gq]) = cvt4<EXACT>(S[t][et]);
-    __syncthreads();
-
-    // 2. P = W S, O = (gamma q) S, v~ = U - P
-    f4 O[2];
-#pragma unroll
-    for (int et = 0; et < 2; ++et) {
-      f4 P = {0, 0, 0, 0};
-      O[et] = f4{0, 0, 0, 0};
-#pragma unroll
-      for (int j = 0; j < NJ; ++j) {
-        v8 Sf;
-        const st* row = &St[(16 * et + r) * PK + 32 * j + 4 * gq];
-        const v4 s0 = *reinterpret_cast<const v4*>(row);
-        const v4 s1 = *reinterpret_cast<const v4*>(row + 16);
-#pragma unroll
-        for (int i = 0; i < 4; ++i) { Sf[i] = s0[i]; Sf[4 + i] = s1[i]; }
-        P = mma32(P, Wf[j], Sf);
-        O[et] = mma32(O[et], Qf[j], Sf);
-      }
-      f4 vt;
-#pragma unroll
-      for (int i = 0; i < 4; ++i) vt[i] = static_cast<float>(Uf[et][i]) - P[i];
-      *reinterpret_cast<v4*>(&Vt[(16 * et + r) * PC + 16 * w + 4 * gq]) = cvt4<EXACT>(vt);
-    }
-    __syncthreads();
-
-    // 3. O += Aqk v~ ; 4. S <- gamma_C S + (lambda k)^T v~
-    const int nk2 = (w < 2) ? 1 : 2;
-#pragma unroll
-    for (int et = 0; et < 2; ++et) {
-      v8 Vf[2];
-#pragma unroll
-      for (int jj = 0; jj < 2; ++jj) {
-        const st* row = &Vt[(16 * et + r) * PC + 32 * jj + 4 * gq];
-        const v4 s0 = *reinterpret_cast<const v4*>(row);
-        const v4 s1 = *reinterpret_cast<const v4*>(row + 16);
-#pragma unroll
-        for (int i = 0; i < 4; ++i) { Vf[jj][i] = s0[i]; Vf[jj][4 + i] = s1[i]; }
-      }
-      for (int jj = 0; jj < nk2; ++jj) O[et] = mma32(O[et], Af[jj], Vf[jj]);
-#pragma unroll
-      for (int i = 0; i < 4; ++i) {
-        const int cr = 16 * w + 4 * gq + i;
-        if (cr < len) {
-          const int64_t oi = ((row0 + cr) * H + h) * DV + 32 * split + 16 * et + r;
-          if constexpr (OUT_DT == 0) static_cast<float*>(a.o)[oi] = O[et][i];
-          else static_cast<u16*>(a.o)[oi] = f32_to_bf16_bits(O[et][i]);
-        }
-      }
-#pragma unroll
-      for (int t = 0; t < DTW; ++t) {
-        f4 s = S[t][et];
-#pragma unroll
-        for (int i = 0; i < 4; ++i) s[i] *= gc[t][i];
-        s = mma32(s, Lf[t][0], Vf[0]);
-        s = mma32(s, Lf[t][1], Vf[1]);
-        S[t][et] = s;
-      }
-    }
-    // (the next iteration's first barrier orders Vt/St reuse)
+    const int len = min(kC, seq_len - n * kC);
+    state_step<DK, DV, EXACT, OUT_DT, W>(S, f, sm, a, row0, len, h, split, r, gq);
+  };
+  // Three fragment sets in fixed registers.  The loads for chunk n+3 are issued
+  // right after step n (and its o stores), so they are younger than every
+  // store the next steps must retire before reusing registers: vmcnt retires
+  // in order on this architecture, and a prefetch issued before the stores
+  // would have to complete before them.
+  StateFrags<DK, EXACT> f0, f1, f2;
+  if (nchunks > 0) load_frags<DK, DV, EXACT, W>(f0, a, chead_of(0), split, l, gq);
+  if (nchunks > 1) load_frags<DK, DV, EXACT, W>(f1, a, chead_of(1), split, l, gq);
+  if (nchunks > 2) load_frags<DK, DV, EXACT, W>(f2, a, chead_of(2), split, l, gq);
+  for (int n = 0; n < nchunks; n += 3) {
+    step(f0, n);
+    if (n + 3 < nchunks) load_frags<DK, DV, EXACT, W>(f0, a, chead_of(n + 3), split, l, gq);
+    if (n + 1 >= nchunks) break;
+    step(f1, n + 1);
+    if (n + 4 < nchunks) load_frags<DK, DV, EXACT, W>(f1, a, chead_of(n + 4), split, l, gq);
+    if (n + 2 >= nchunks) break;
+    step(f2, n + 2);
+    if (n + 5 < nchunks) load_frags<DK, DV, EXACT, W>(f2, a, chead_of(n + 5), split, l, gq);
   }
 
   if (a.ht != nullptr) {
@@ -603,111 +671,36 @@ void kda_state_kernel(StateArgs a) {
       for (int et = 0; et < 2; ++et)
 #pragma unroll
         for (int i = 0; i < 4; ++i) {
-          const int d = 16 * (w * DTW + t) + 4 * gq + i;
+          const int d = 16 * (W * DTW + t) + 4 * gq + i;
           const int e = 32 * split + 16 * et + r;
           a.ht[sbase + static_cast<int64_t>(d) * DV + e] = S[t][et][i];
         }
   }
 }
 
-// ----------------------------------------------------------------------------
-// varlen preparation: clamp cu_seqlens, chunk offsets, longest-first order
-// ----------------------------------------------------------------------------
-__global__ __launch_bounds__(1024)
-void kda_varlen_prep_kernel(const int32_t* cu, int N, int T, int32_t* cu_clamped,
-                            int32_t* chunk_off, int32_t* n_units, int32_t* order,
-                            int32_t* flags) {
-  __shared__ int32_t scan[1024];
-  __shared__ int32_t carry;
-  __shared__ int32_t bad;
-  __shared__ int64_t keys[2048];
-  const int tid = threadIdx.x;
-  if (tid == 0) { carry = 0; bad = 0; }
-  __syncthreads();
-  // clamp: 0 <= cu[i] <= T and non-decreasing; flag any repair
-  for (int base = 0; base <= N; base += 1024) {
-    const int i = base + tid;
-    int v = 0;
-    if (i <= N) {
-      v = cu[i];
-      int lo = (i == 0) ? 0 : cu[i - 1];
-      if (i == 0 && v != 0) atomicOr(&bad, 1);
-      if (i == N && v != T) atomicOr(&bad, 2);
-      if (v < lo) { atomicOr(&bad, 4); }
-      if (v < 0 || v > T) atomicOr(&bad, 8);
-    }
-    (void)v;
-  }
-  __syncthreads();
-  // serial-safe clamp in one thread group pass (running max)
-  for (int base = 0; base <= N; base += 1024) {
-    const int i = base + tid;
-    int v = 0;
-    if (i <= N) v = min(max(cu[i], 0), T);
-    if (i == 0) v = 0;
-    scan[tid] = v;
-    __syncthreads();
-    // inclusive running max (Hillis-Steele)
-    for (int off = 1; off < 1024; off <<= 1) {
-      int t = (tid >= off) ? scan[tid - off] : 0;
-      __syncthreads();
-      scan[tid] = max(scan[tid], t);
-      __syncthreads();
-    }
-    const int m = max(scan[tid], carry);
-    if (i <= N) cu_clamped[i] = m;
-    __syncthreads();
-    if (tid == 1023) carry = m;
-    __syncthreads();
-  }
-  if (tid == 0) carry = 0;
-  __syncthreads();
-  // chunk offsets: exclusive scan of ceil(len/64)
-  for (int base = 0; base < N; base += 1024) {
-    const int i = base + tid;
-    int cnt = 0;
-    if (i < N) cnt = (cu_clamped[i + 1] - cu_clamped[i] + kC - 1) / kC;
-    scan[tid] = cnt;
-    __syncthreads();
-    for (int off = 1; off < 1024; off <<= 1) {
-      int t = (tid >= off) ? scan[tid - off] : 0;
-      __syncthreads();
-      scan[tid] += t;
-      __syncthreads();
-    }
-    if (i < N) chunk_off[i] = carry + scan[tid] - cnt;
-    __syncthreads();
-    if (tid == 1023) carry += scan[1023];
-    __syncthreads();
-  }
-  if (tid == 0) { chunk_off[N] = carry; *n_units = carry; flags[0] = bad; }
-  // longest-first order (bitonic sort of (-len, idx)); identity for large N
-  if (N <= 2048) {
-    for (int i = tid; i < 2048; i += 1024) {
-      if (i < N) {
-        const int64_t len = cu_clamped[i + 1] - cu_clamped[i];
-        keys[i] = ((int64_t)(0x7FFFFFFF - len) << 32) | (uint32_t)i;
-      } else {
-        keys[i] = INT64_MAX;
-      }
-    }
-    __syncthreads();
-    for (int k = 2; k <= 2048; k <<= 1) {
-      for (int j = k >> 1; j > 0; j >>= 1) {
-        for (int i = tid; i < 2048; i += 1024) {
-          const int ixj = i ^ j;
-          if (ixj > i) {
-            const bool up = ((i & k) == 0);
-            const int64_t a0 = keys[i], a1 = keys[ixj];
-            if ((a0 > a1) == up) { keys[i] = a1; keys[ixj] = a0; }
-          }
-        }
-        __syncthreads();
-      }
-    }
-    for (int i = tid; i < N; i += 1024) order[i] = (int32_t)(keys[i] & 0xFFFFFFFF);
-  } else {
-    for (int i = tid; i < N; i += 1024) order[i] = i;
+template <int DK, int DV, bool EXACT, int OUT_DT>
+__global__ __launch_bounds__(256, 1)
+void kda_state_kernel(StateArgs a) {
+  constexpr int SPLITS = DV / 32;
+  __shared__ StateSmem<DK, DV, EXACT> sm;
+  const Geom& G = a.geom;
+  const int H = G.H;
+  // XCD-aware mapping: the SPLITS workgroups of one chain share an XCD (and L2)
+  const int x = blockIdx.x;
+  const int xcd = x & 7;
+  const int kk = x >> 3;
+  const int slot = kk / SPLITS;
+  const int split = kk - slot * SPLITS;
+  const int chain = slot * 8 + xcd;
+  if (chain >= G.N * H) return;
+  const int seq_rank = chain / H;
+  const int h = chain - seq_rank * H;
+  const int seq = (G.order != nullptr) ? G.order[seq_rank] : seq_rank;
+  switch (threadIdx.x >> 6) {
+    case 0: state_chain<DK, DV, EXACT, OUT_DT, 0>(a, sm, seq, h, split); break;
+    case 1: state_chain<DK, DV, EXACT, OUT_DT, 1>(a, sm, seq, h, split); break;
+    case 2: state_chain<DK, DV, EXACT, OUT_DT, 2>(a, sm, seq, h, split); break;
+    default: state_chain<DK, DV, EXACT, OUT_DT, 3>(a, sm, seq, h, split); break;
   }
 }
 
@@ -754,14 +747,6 @@ hipError_t launch_state(const StateArgs& a, int d, bool exact, int out_dt, int g
   KDA_STATE(64, true, 1)
 #undef KDA_STATE
   return hipErrorInvalidValue;
-}
-
-hipError_t launch_varlen_prep(const int32_t* cu, int N, int T, int32_t* cu_clamped,
-                              int32_t* chunk_off, int32_t* n_units, int32_t* order,
-                              int32_t* flags, hipStream_t s) {
-  hipLaunchKernelGGL(kda_varlen_prep_kernel, dim3(1), dim3(1024), 0, s, cu, N, T, cu_clamped,
-                     chunk_off, n_units, order, flags);
-  return hipGetLastError();
 }
 
 }  // namespace kda

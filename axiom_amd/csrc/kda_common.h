@@ -173,6 +173,16 @@ __device__ __forceinline__ float row_scan16(float x) {
 
 __device__ __forceinline__ float fast_exp2(float x) { return __builtin_amdgcn_exp2f(x); }
 
+// Workgroup barrier that orders LDS only.  __syncthreads() also releases
+// global memory, which makes every wave wait for its outstanding global loads
+// (prefetches) and stores at each barrier; the kernels here never communicate
+// through global memory inside a workgroup phase, so they use this one.
+__device__ __forceinline__ void lds_barrier() {
+  __builtin_amdgcn_fence(__ATOMIC_RELEASE, "workgroup", "local");
+  __builtin_amdgcn_s_barrier();
+  __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "workgroup", "local");
+}
+
 // channel carried by slot (gq, e) of 32-wide K step j
 __device__ __forceinline__ int slot_channel(int j, int gq, int e) {
   return 32 * j + 4 * gq + (e & 3) + 16 * (e >> 2);

@@ -251,6 +251,51 @@ def chunk_fwd(q, k, v, g, beta, h0=None, cu_seqlens=None, chunk: int = 64, tile:
     return o, hts
 
 
+def chunk_intermediates(q, k, v, g, beta, chunk: int = 64, tile: int = 16, scale: float = 1.0):
+    """Per-chunk intermediates of ``cc_chunk_step`` (``net/kda.py:669-702``), dense inputs.
+
+    Returns a dict of float64 arrays indexed ``[B, H, n_chunks, ...]``:
+    ``W [C, dk]``, ``U [C, dv]``, ``Aqk [C, C]``, ``GQ = gamma*q [C, dk]``,
+    ``LK = lambda*k [C, dk]``, ``GC = gamma_C [dk]`` and ``T = (I+L)^-1 [C, C]``
+    (T depends only on the chunk's own inputs, not on the carried state).
+    """
+    B, Tn, H, dk = q.shape
+    dv = v.shape[-1]
+    n = (Tn + chunk - 1) // chunk
+    pad = n * chunk - Tn
+    dt = torch.float64
+
+    def prep(x, d):
+        t = _to_torch(x, dt).permute(0, 2, 1, 3).reshape(B * H, Tn, d)
+        if pad:
+            t = torch.cat([t, torch.zeros((B * H, pad, d), dtype=dt)], dim=1)
+        return t.reshape(B * H, n, chunk, d)
+
+    qc, kc, vc, gc = prep(np.asarray(q) * scale, dk), prep(k, dk), prep(v, dv), prep(g, dk)
+    bt = _to_torch(beta, dt).permute(0, 2, 1).reshape(B * H, Tn)
+    if pad:
+        bt = torch.cat([bt, torch.zeros((B * H, pad), dtype=dt)], dim=1)
+    bc = bt.reshape(B * H, n, chunk)
+    out = {name: [] for name in ("W", "U", "Aqk", "GQ", "LK", "GC", "T")}
+    for i in range(n):
+        G = torch.cumsum(gc[:, i], dim=1)
+        qq, kk, vv, bb = qc[:, i], kc[:, i], vc[:, i], bc[:, i]
+        aqk = cc_scores(qq, kk, G, tile, strict=False)
+        L = cc_scores(kk, kk, G, tile, strict=True) * bb[:, :, None]
+        gamma = torch.exp(G)
+        Tm = ut_solve(L)
+        lam = torch.exp(torch.clamp(G[:, -1:, :] - G, max=0.0))
+        out["W"].append(Tm @ (gamma * kk * bb[:, :, None]))
+        out["U"].append(Tm @ (vv * bb[:, :, None]))
+        out["Aqk"].append(aqk)
+        out["GQ"].append(gamma * qq)
+        out["LK"].append(lam * kk)
+        out["GC"].append(gamma[:, -1, :])
+        out["T"].append(Tm)
+    return {name: torch.stack(vals, 1).reshape(B, H, n, *vals[0].shape[1:]).numpy()
+            for name, vals in out.items()}
+
+
 def decode_steps(q, k, v, g, beta, S, scale: float = 1.0):
     """``steps`` successive decode steps: inputs ``[steps, B, H, d]``, state ``[B,H,dk,dv]``."""
     outs = []
