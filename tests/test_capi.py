@@ -1,0 +1,224 @@
+"""CPU: the C-ABI library loads, exports exactly what ``include/kda_mi355x.h``
+declares, and rejects invalid requests before any HIP call.
+
+Nothing here launches a kernel or touches device memory: every call either
+only computes sizes or fails argument validation, which the library does on
+the host before it enqueues anything.  The Python layer's refusal to run on
+CPU tensors (no fallback) is checked too.
+"""
+
+from __future__ import annotations
+
+import ctypes
+import subprocess
+
+import pytest
+import torch
+
+from axiom_amd import _lib
+from axiom_amd import kda as kmod
+
+C = 64
+
+
+@pytest.fixture(scope="module")
+def L():
+    if not _lib.LIB_PATH.exists():
+        from axiom_amd import build
+        build.build()
+    return _lib.lib()
+
+
+def _align(x):
+    return (x + 255) // 256 * 256
+
+
+def dense_ws_bytes(B, T, H, dk, dv, es):
+    """Dense workspace size: W, gamma*q, lambda*k [units*H][C][dk], U [..][C][dv],
+    Aqk [..][C][C] in operand precision, gamma_C [..][dk] fp32, each 256-B aligned."""
+    ch = B * ((T + C - 1) // C) * H
+    return sum(_align(n) for n in (ch * C * dk * es, ch * C * dk * es, ch * C * dk * es,
+                                   ch * C * dv * es, ch * C * C * es, ch * dk * 4))
+
+
+def varlen_ws_bytes(T, N, H, dk, dv, es):
+    units = (T + 63 * N) // C   # upper bound on sum(ceil(len_i / C))
+    ch = units * H
+    arrays = (ch * C * dk * es, ch * C * dk * es, ch * C * dk * es, ch * C * dv * es,
+              ch * C * C * es, ch * dk * 4, (N + 1) * 4, (N + 1) * 4, 4, N * 4, 4)
+    return sum(_align(n) for n in arrays)
+
+
+def test_header_declares_the_abi():
+    names = _lib.header_symbols()
+    assert set(names) == set(_lib._SIGNATURES), names
+    assert len(names) == len(set(names)) == 8
+
+
+def test_library_exports_every_declared_symbol(L):
+    for name in _lib.header_symbols():
+        assert hasattr(L, name), f"{name} declared in the header but not exported"
+    out = subprocess.run(["nm", "-D", "--defined-only", str(_lib.LIB_PATH)],
+                         capture_output=True, text=True, check=True).stdout
+    exported = {ln.split()[-1] for ln in out.splitlines() if " T " in ln}
+    kda_exported = {s for s in exported if s.startswith("kda_")}
+    assert kda_exported == set(_lib.header_symbols()), kda_exported ^ set(_lib.header_symbols())
+
+
+def test_abi_version(L):
+    assert L.kda_abi_version() == 100
+
+
+@pytest.mark.parametrize("B,T,H,d", [(1, 512, 4, 64), (4, 4096, 16, 128), (2, 1, 3, 128),
+                                     (3, 65, 2, 64), (1, 0, 1, 64)])
+@pytest.mark.parametrize("code,es", [(0, 4), (1, 2), (2, 2), (3, 2)])
+def test_dense_workspace_size(L, B, T, H, d, code, es):
+    assert L.kda_chunk_fwd_workspace(B, T, H, d, d, C, 0, code) == dense_ws_bytes(B, T, H, d, d, es)
+
+
+@pytest.mark.parametrize("T,N", [(262144, 64), (108, 4), (1, 1), (0, 3)])
+def test_varlen_workspace_size(L, T, N):
+    assert L.kda_chunk_fwd_workspace(1, T, 16, 128, 128, C, N, 1) == varlen_ws_bytes(T, N, 16, 128, 128, 2)
+
+
+def test_varlen_workspace_covers_every_split():
+    # sum_i ceil(len_i / C) <= (T + (C-1) N) / C for any N lengths summing to T
+    import numpy as np
+    rng = np.random.default_rng(0)
+    for _ in range(200):
+        N = int(rng.integers(1, 40))
+        lens = rng.integers(0, 300, size=N)
+        T = int(lens.sum())
+        assert int(np.sum((lens + C - 1) // C)) <= (T + (C - 1) * N) // C
+
+
+@pytest.mark.parametrize("args", [
+    (1, 64, 1, 96, 96, C, 0, 1),     # head dim
+    (1, 64, 1, 64, 128, C, 0, 1),    # dk != dv
+    (1, 64, 1, 64, 64, 32, 0, 1),    # chunk
+    (0, 64, 1, 64, 64, C, 0, 1),     # B
+    (1, -1, 1, 64, 64, C, 0, 1),     # T
+    (1, 64, 0, 64, 64, C, 0, 1),     # H
+    (1, 64, 1, 64, 64, C, 0, 7),     # dtype
+])
+def test_workspace_size_rejects_unsupported(L, args):
+    assert L.kda_chunk_fwd_workspace(*args) == 0
+
+
+def test_cc_scan_workspace_size(L):
+    T, H, d = 512, 4, 64
+    adapt = _align(T * H * d * 4) + _align(T * H * 4)
+    assert L.kda_cc_scan_workspace(T, H, d, d, 32) == adapt + dense_ws_bytes(1, T, H, d, d, 2)
+    assert L.kda_cc_scan_workspace(T, H, 96, 96, 32) == 0
+
+
+_FAKE = ctypes.c_void_p(0x1000)   # never dereferenced: every call below fails validation
+_NULL = ctypes.c_void_p(0)
+
+
+def _chunk_fwd(L, **kw):
+    a = dict(q=_FAKE, k=_FAKE, v=_FAKE, g=_FAKE, beta=_FAKE, h0=_NULL, cu=_NULL, n_seqs=0,
+             o=_FAKE, ht=_NULL, B=1, T=64, H=1, dk=64, dv=64, chunk=C, scale=1.0, in_dt=1,
+             out_dt=0, ws=_FAKE, ws_bytes=1 << 40)
+    a.update(kw)
+    rc = L.kda_chunk_fwd(_NULL, a["q"], a["k"], a["v"], a["g"], a["beta"], a["h0"], a["cu"],
+                         a["n_seqs"], a["o"], a["ht"], a["B"], a["T"], a["H"], a["dk"], a["dv"],
+                         a["chunk"], a["scale"], a["in_dt"], a["out_dt"], a["ws"], a["ws_bytes"])
+    return rc, _lib.last_error()
+
+
+@pytest.mark.parametrize("kw,status,needle", [
+    (dict(q=_NULL), _lib.KDA_ERR_INVALID_ARGUMENT, "null input"),
+    (dict(o=_NULL), _lib.KDA_ERR_INVALID_ARGUMENT, "null output"),
+    (dict(B=0), _lib.KDA_ERR_INVALID_ARGUMENT, "B=0"),
+    (dict(T=-5), _lib.KDA_ERR_INVALID_ARGUMENT, "T=-5"),
+    (dict(dk=96, dv=96), _lib.KDA_ERR_UNSUPPORTED, "dk=96"),
+    (dict(dk=128, dv=64), _lib.KDA_ERR_UNSUPPORTED, "dk=128, dv=64"),
+    (dict(chunk=32), _lib.KDA_ERR_UNSUPPORTED, "chunk=32"),
+    (dict(in_dt=9), _lib.KDA_ERR_INVALID_ARGUMENT, "in_dtype=9"),
+    (dict(out_dt=2), _lib.KDA_ERR_INVALID_ARGUMENT, "out_dtype=2"),
+    (dict(scale=float("nan")), _lib.KDA_ERR_INVALID_ARGUMENT, "scale"),
+    (dict(cu=_FAKE, n_seqs=2, B=2), _lib.KDA_ERR_INVALID_ARGUMENT, "requires B == 1"),
+    (dict(cu=_FAKE, n_seqs=0), _lib.KDA_ERR_INVALID_ARGUMENT, "n_seqs=0"),
+    (dict(ws=_NULL), _lib.KDA_ERR_WORKSPACE, "workspace"),
+    (dict(ws_bytes=100), _lib.KDA_ERR_WORKSPACE, "too small"),
+])
+def test_chunk_fwd_validation(L, kw, status, needle):
+    rc, msg = _chunk_fwd(L, **kw)
+    assert rc == status, msg
+    assert needle in msg, msg
+
+
+def test_error_message_is_cleared_by_next_call(L):
+    rc, msg = _chunk_fwd(L, chunk=32)
+    assert rc != 0 and msg
+    assert L.kda_chunk_fwd_workspace(1, 64, 1, 64, 64, C, 0, 1) > 0
+    rc, msg = _chunk_fwd(L, dk=96, dv=96)
+    assert "dk=96" in msg and "chunk" not in msg
+
+
+def test_recurrent_step_validation(L):
+    def call(**kw):
+        a = dict(q=_FAKE, state=_FAKE, B=4, H=2, dk=128, dv=128, scale=1.0, in_dt=1, out_dt=0)
+        a.update(kw)
+        rc = L.kda_recurrent_step(_NULL, a["q"], _FAKE, _FAKE, _FAKE, _FAKE, a["state"], _FAKE,
+                                  a["B"], a["H"], a["dk"], a["dv"], a["scale"], a["in_dt"], a["out_dt"])
+        return rc, _lib.last_error()
+    assert call(state=_NULL)[0] == _lib.KDA_ERR_INVALID_ARGUMENT
+    assert call(B=0)[0] == _lib.KDA_ERR_INVALID_ARGUMENT
+    assert call(dk=32, dv=32)[0] == _lib.KDA_ERR_UNSUPPORTED
+    rc, msg = call(in_dt=3)
+    assert rc == _lib.KDA_ERR_INVALID_ARGUMENT and "decode takes" in msg
+    assert call(out_dt=2)[0] == _lib.KDA_ERR_INVALID_ARGUMENT
+
+
+def test_cc_scan_validation_messages(L):
+    def call(T=96, H=1, d=64, tile=16, chunk=32, ws_bytes=1 << 40):
+        rc = L.kda_cc_scan(_NULL, _FAKE, _FAKE, _FAKE, _FAKE, _FAKE, _FAKE, _FAKE, _FAKE,
+                           T, H, d, d, tile, chunk, _FAKE, ws_bytes)
+        return rc, _lib.last_error()
+    rc, msg = call(T=100)
+    assert rc == _lib.KDA_ERR_INVALID_ARGUMENT
+    assert msg == "T=100 must be a multiple of the chunk width C=32"   # net/kernels/kda_cc_fused_persist.py:741-742
+    assert call(tile=17)[0] == _lib.KDA_ERR_INVALID_ARGUMENT
+    assert call(tile=0)[0] == _lib.KDA_ERR_INVALID_ARGUMENT
+    assert call(d=96)[0] == _lib.KDA_ERR_UNSUPPORTED
+    assert call(ws_bytes=10)[0] == _lib.KDA_ERR_WORKSPACE
+
+
+def test_python_layer_refuses_cpu_tensors():
+    q = torch.zeros(1, 64, 1, 64, dtype=torch.bfloat16)
+    beta = torch.zeros(1, 64, 1, dtype=torch.bfloat16)
+    with pytest.raises(RuntimeError, match="no CPU fallback"):
+        kmod.kda_chunk_fwd(q, q, q, q, beta)
+    with pytest.raises(RuntimeError, match="no CPU fallback"):
+        kmod.kda_recurrent_step(q[:, 0], q[:, 0], q[:, 0], q[:, 0], beta[:, 0],
+                                torch.zeros(1, 1, 64, 64))
+
+
+def test_python_layer_argument_errors():
+    q = torch.zeros(1, 64, 1, 64, dtype=torch.bfloat16)
+    beta = torch.zeros(1, 64, 1, dtype=torch.bfloat16)
+    with pytest.raises(ValueError, match="chunk_size"):
+        kmod.kda_chunk_fwd(q, q, q, q, beta, chunk_size=32)
+    with pytest.raises(ValueError, match="head dims"):
+        q96 = torch.zeros(1, 64, 1, 96, dtype=torch.bfloat16)
+        kmod.kda_chunk_fwd(q96, q96, q96, q96, beta)
+    with pytest.raises(ValueError, match="requires B == 1"):
+        q2 = torch.zeros(2, 64, 1, 64, dtype=torch.bfloat16)
+        kmod.kda_chunk_fwd(q2, q2, q2, q2, torch.zeros(2, 64, 1, dtype=torch.bfloat16),
+                           cu_seqlens=torch.tensor([0, 64], dtype=torch.int32))
+    with pytest.raises(ValueError, match="initial_state"):
+        kmod.kda_chunk_fwd(q, q, q, q, beta, initial_state=torch.zeros(1, 1, 64, 32))
+
+
+def test_cc_scan_reference_errors():
+    T, H, d = 100, 1, 64
+    q = torch.zeros(T, H * d, dtype=torch.bfloat16)
+    a = torch.ones(T, H * d)
+    b = torch.ones(T, H * 32)
+    S = torch.zeros(H, d, d)
+    with pytest.raises(ValueError, match="persistent kernel consumes bf16 q/k/v"):
+        kmod.cc_scan(q.float(), q.float(), q.float(), a, b, S)
+    with pytest.raises(ValueError, match="T=100 must be a multiple of the chunk width C=32"):
+        kmod.cc_scan(q, q, q, a, b, S)
