@@ -705,6 +705,297 @@ void kda_state_kernel(StateArgs a) {
 }
 
 // ----------------------------------------------------------------------------
+// State kernel, column-owner form (fp16 operands)
+//
+// A workgroup of two waves owns 32 value columns of one chain; wave w owns
+// the 16 columns of value tile et = 2*split + w for ALL dk channels, so every
+// product of the step has its state / v~ operand in this wave's registers:
+//   * S tile dt in the MFMA D layout (rows 4gq+i, column r) is, two tiles at a
+//     time, the B fragment of a 32-wide K step over channels (slot order);
+//   * v~ row tiles, two at a time, are the B fragment over 32 keys.
+// Only the dv-independent A operands (W, gamma*q, Aqk, lambda*k) and gamma_C
+// are shared: per chunk a third, producer-only wave copies them once per
+// workgroup from the workspace into one of two LDS buffers by direct
+// global->LDS loads (16 B per lane, fragment order, so every LDS read is a
+// conflict-free 16 B per lane), one chunk ahead.  The compute waves issue no
+// copies of their own (a wave issues memory instructions in order, so a deep
+// copy queue would stall its MFMAs).  One barrier per chunk.
+// ----------------------------------------------------------------------------
+template <int DK>
+struct ColLayout {
+  static constexpr int NJ = DK / 32;
+  static constexpr int FW = 4 * NJ;          // W (and gamma*q) fragments per chunk-head
+  static constexpr int FL = 2 * (DK / 16);   // lambda*k fragments
+  static constexpr int FA = 6;               // Aqk fragments (ct, jj) with jj <= ct / 2
+  static constexpr int OFF_Q = FW;
+  static constexpr int OFF_L = 2 * FW;
+  static constexpr int OFF_A = 2 * FW + FL;
+  static constexpr int NF = 2 * FW + FL + FA;  // 1-KiB fragments per chunk-head
+  static constexpr int OFF_G = NF * 1024;      // gamma_C (DK floats)
+  static constexpr int BYTES = NF * 1024 + DK * 4;
+};
+
+template <int DK>
+struct ColSmem {
+  alignas(16) unsigned char buf[2][ColLayout<DK>::BYTES];
+};
+
+// s_waitcnt vmcnt(0), other counters untouched (gfx9 encoding)
+__device__ __forceinline__ void wait_vmem_all() { __builtin_amdgcn_s_waitcnt(0x0F70); }
+
+
+// Copy the shared operands of chunk-head ch into an LDS buffer
+// (fragment-ordered 1 KiB blocks: lane l moves bytes 16l..16l+15) and gamma_C.
+template <int DK>
+__device__ __forceinline__ void col_stage(const StateArgs& a, int64_t ch, unsigned char* dst, int l) {
+  typedef ColLayout<DK> LY;
+  const _Float16* iW = static_cast<const _Float16*>(a.W);
+  const _Float16* iQ = static_cast<const _Float16*>(a.GQ);
+  const _Float16* iL = static_cast<const _Float16*>(a.LK);
+  const _Float16* iA = static_cast<const _Float16*>(a.AQ);
+#pragma unroll
+  for (int f = 0; f < LY::NF; ++f) {
+    const _Float16* src;
+    if (f < LY::OFF_Q) src = iW + (ch * LY::FW + f) * 512;
+    else if (f < LY::OFF_L) src = iQ + (ch * LY::FW + (f - LY::OFF_Q)) * 512;
+    else if (f < LY::OFF_A) src = iL + (ch * LY::FL + (f - LY::OFF_L)) * 512;
+    else {
+      const int ai = f - LY::OFF_A;                 // 0..5 -> (ct, jj) = 00 10 20 21 30 31
+      const int gidx = (ai < 2) ? 2 * ai : ai + 2;  // index ct*2 + jj in the workspace
+      src = iA + (ch * 8 + gidx) * 512;
+    }
+    __builtin_amdgcn_global_load_lds(src + l * 8, dst + f * 1024, 16, 0, 0);
+  }
+  const _Float16* gsrc = reinterpret_cast<const _Float16*>(a.GC + ch * DK + l * 4);
+  unsigned char* gdst = dst + LY::OFF_G;
+  if (l < DK / 4) __builtin_amdgcn_global_load_lds(gsrc, gdst, 16, 0, 0);
+}
+
+struct ChainRef {
+  int u0, nchunks, seq_len;
+  int64_t tok0;
+};
+
+__device__ __forceinline__ ChainRef chain_ref(const Geom& G, int seq) {
+  ChainRef c;
+  if (G.cu == nullptr) {
+    c.u0 = seq * G.NT;
+    c.nchunks = G.NT;
+    c.tok0 = static_cast<int64_t>(seq) * G.T;
+    c.seq_len = G.T;
+  } else {
+    c.u0 = G.chunk_off[seq];
+    c.nchunks = G.chunk_off[seq + 1] - c.u0;
+    c.tok0 = G.cu_clamped[seq];
+    c.seq_len = G.cu_clamped[seq + 1] - G.cu_clamped[seq];
+  }
+  return c;
+}
+
+// Producer wave: fills the buffer of chunk n+1 while the compute waves work on
+// chunk n, and joins the one barrier per chunk once its copies have landed.
+template <int DK>
+__device__ __forceinline__ void col_producer(const StateArgs& a, ColSmem<DK>& sm, int seq, int h) {
+  const ChainRef c = chain_ref(a.geom, seq);
+  const int H = a.geom.H;
+  const int l = threadIdx.x & 63;
+  if (c.nchunks > 0) {
+    col_stage<DK>(a, static_cast<int64_t>(c.u0) * H + h, sm.buf[0], l);
+    wait_vmem_all();
+    lds_barrier();
+  }
+  for (int n = 0; n + 1 < c.nchunks; ++n) {
+    col_stage<DK>(a, static_cast<int64_t>(c.u0 + n + 1) * H + h, sm.buf[(n + 1) & 1], l);
+    wait_vmem_all();
+    lds_barrier();
+  }
+}
+
+__device__ __forceinline__ h8 lds_frag(const unsigned char* buf, int f, int l) {
+  return *reinterpret_cast<const h8*>(buf + f * 1024 + l * 16);
+}
+
+template <int DK, int DV, int OUT_DT>
+__device__ __forceinline__ void col_store_o(const StateArgs& a, const f4 (&O)[4], int64_t row0, int len,
+                                            int h, int et, int r, int gq) {
+  const int H = a.geom.H;
+#pragma unroll
+  for (int ct = 0; ct < 4; ++ct)
+#pragma unroll
+    for (int i = 0; i < 4; ++i) {
+      const int cr = 16 * ct + 4 * gq + i;
+      if (cr < len) {
+        const int64_t oi = ((row0 + cr) * H + h) * (int64_t)DV + 16 * et + r;
+        if constexpr (OUT_DT == 0) static_cast<float*>(a.o)[oi] = O[ct][i];
+        else static_cast<u16*>(a.o)[oi] = f32_to_bf16_bits(O[ct][i]);
+      }
+    }
+}
+
+template <int DK, int DV, int OUT_DT, int W>
+__device__ __forceinline__ void col_chain(const StateArgs& a, ColSmem<DK>& sm, int seq, int h, int split) {
+  typedef ColLayout<DK> LY;
+  constexpr int NJ = DK / 32;
+  constexpr int NT = DK / 16;
+  const Geom& G = a.geom;
+  const int H = G.H;
+  const int l = threadIdx.x & 63, r = l & 15, gq = l >> 4;
+  const int et = 2 * split + W;
+  const ChainRef c = chain_ref(G, seq);
+  const int u0 = c.u0, nchunks = c.nchunks, seq_len = c.seq_len;
+  const int64_t tok0 = c.tok0;
+
+  f4 S[NT];
+  const int64_t sbase = (static_cast<int64_t>(seq) * H + h) * DK * DV;
+#pragma unroll
+  for (int dt = 0; dt < NT; ++dt)
+#pragma unroll
+    for (int i = 0; i < 4; ++i)
+      S[dt][i] = (a.h0 != nullptr)
+                     ? a.h0[sbase + static_cast<int64_t>(16 * dt + 4 * gq + i) * DV + 16 * et + r]
+                     : 0.f;
+
+  const _Float16* iU = static_cast<const _Float16*>(a.U);
+  auto chead_of = [&](int n) { return static_cast<int64_t>(u0 + n) * H + h; };
+  auto load_u = [&](h4 (&U)[4], int64_t ch) {
+#pragma unroll
+    for (int ct = 0; ct < 4; ++ct)
+      U[ct] = *reinterpret_cast<const h4*>(iU + (ch * 4 * (DV / 16) + ct * (DV / 16) + et) * 256 + l * 4);
+  };
+
+  h4 Ucur[4], Unext[4];
+  if (nchunks > 0) {
+    load_u(Ucur, chead_of(0));
+    lds_barrier();  // chunk 0 staged by the producer wave
+  }
+  for (int n = 0; n < nchunks; ++n) {
+    const unsigned char* cur = sm.buf[n & 1];
+    const bool more = n + 1 < nchunks;
+    if (more) load_u(Unext, chead_of(n + 1));
+
+    // The step is a fixed sequence of MFMA groups; each group's A fragments
+    // are read from LDS two groups ahead into a 3-slot register ring, and a
+    // scheduling barrier keeps the reads there.  Groups: 2ct = W rows of tile
+    // ct (P), 2ct+1 = gamma*q rows (O), 8 = Aqk, 9 + dt = lambda*k of channel
+    // tile dt with gamma_C.
+    constexpr int NG = 9 + NT;
+    h8 Rf[3][6];
+    f4 Rg[3];
+    auto load_group = [&](int g) {
+      const int sl = g % 3;
+      if (g < 8) {
+        const int base = ((g & 1) ? LY::OFF_Q : 0) + (g >> 1) * NJ;
+#pragma unroll
+        for (int j = 0; j < NJ; ++j) Rf[sl][j] = lds_frag(cur, base + j, l);
+      } else if (g == 8) {
+#pragma unroll
+        for (int f = 0; f < LY::FA; ++f) Rf[sl][f] = lds_frag(cur, LY::OFF_A + f, l);
+      } else {
+        const int dt = g - 9;
+        Rf[sl][0] = lds_frag(cur, LY::OFF_L + 2 * dt, l);
+        Rf[sl][1] = lds_frag(cur, LY::OFF_L + 2 * dt + 1, l);
+        Rg[sl] = *reinterpret_cast<const f4*>(cur + LY::OFF_G + (16 * dt + 4 * gq) * 4);
+      }
+    };
+    load_group(0);
+    load_group(1);
+    // S as B fragments over channels
+    h8 Sb[NJ];
+#pragma unroll
+    for (int j = 0; j < NJ; ++j)
+#pragma unroll
+      for (int i = 0; i < 4; ++i) {
+        Sb[j][i] = static_cast<_Float16>(S[2 * j][i]);
+        Sb[j][4 + i] = static_cast<_Float16>(S[2 * j + 1][i]);
+      }
+    f4 O[4], Vt[4];
+    h8 Vb[2];
+#pragma unroll
+    for (int g = 0; g < NG; ++g) {
+      if (g + 2 < NG) load_group(g + 2);
+      __builtin_amdgcn_sched_barrier(0);
+      const int sl = g % 3;
+      if (g < 8) {
+        // P = W S (then v~ = U - P) or O = (gamma q) S for row tile ct
+        const int ct = g >> 1;
+        f4 acc = {0, 0, 0, 0};
+#pragma unroll
+        for (int j = 0; j < NJ; ++j) acc = mma32(acc, Rf[sl][j], Sb[j]);
+        if ((g & 1) == 0) {
+#pragma unroll
+          for (int i = 0; i < 4; ++i) Vt[ct][i] = static_cast<float>(Ucur[ct][i]) - acc[i];
+        } else {
+          O[ct] = acc;
+        }
+      } else if (g == 8) {
+        // v~ as B fragments over keys; O += Aqk v~ (keys at or before the row tile)
+#pragma unroll
+        for (int jj = 0; jj < 2; ++jj)
+#pragma unroll
+          for (int i = 0; i < 4; ++i) {
+            Vb[jj][i] = static_cast<_Float16>(Vt[2 * jj][i]);
+            Vb[jj][4 + i] = static_cast<_Float16>(Vt[2 * jj + 1][i]);
+          }
+        O[0] = mma32(O[0], Rf[sl][0], Vb[0]);
+        O[1] = mma32(O[1], Rf[sl][1], Vb[0]);
+        O[2] = mma32(O[2], Rf[sl][2], Vb[0]);
+        O[2] = mma32(O[2], Rf[sl][3], Vb[1]);
+        O[3] = mma32(O[3], Rf[sl][4], Vb[0]);
+        O[3] = mma32(O[3], Rf[sl][5], Vb[1]);
+      } else {
+        // S <- gamma_C S + (lambda k)^T v~ for channel tile dt
+        const int dt = g - 9;
+        f4 sv = S[dt] * Rg[sl];
+        sv = mma32(sv, Rf[sl][0], Vb[0]);
+        sv = mma32(sv, Rf[sl][1], Vb[1]);
+        S[dt] = sv;
+      }
+    }
+
+    col_store_o<DK, DV, OUT_DT>(a, O, tok0 + static_cast<int64_t>(n) * kC, min(kC, seq_len - n * kC),
+                                h, et, r, gq);
+#pragma unroll
+    for (int ct = 0; ct < 4; ++ct) Ucur[ct] = Unext[ct];
+    // the producer has landed the next buffer, and both compute waves are
+    // done with this one before it is refilled
+    if (more) lds_barrier();
+  }
+
+  if (a.ht != nullptr) {
+#pragma unroll
+    for (int dt = 0; dt < NT; ++dt)
+#pragma unroll
+      for (int i = 0; i < 4; ++i)
+        a.ht[sbase + static_cast<int64_t>(16 * dt + 4 * gq + i) * DV + 16 * et + r] = S[dt][i];
+  }
+}
+
+template <int DK, int DV, int OUT_DT>
+__global__ __launch_bounds__(192, 1)
+void kda_state_col_kernel(StateArgs a) {
+  constexpr int SPLITS = DV / 32;
+  __shared__ ColSmem<DK> sm;
+  const Geom& G = a.geom;
+  const int H = G.H;
+  // XCD-aware mapping: the SPLITS workgroups of one chain share an XCD (and L2)
+  const int x = blockIdx.x;
+  const int xcd = x & 7;
+  const int kk = x >> 3;
+  const int slot = kk / SPLITS;
+  const int split = kk - slot * SPLITS;
+  const int chain = slot * 8 + xcd;
+  if (chain >= G.N * H) return;
+  const int seq_rank = chain / H;
+  const int h = chain - seq_rank * H;
+  const int seq = (G.order != nullptr) ? G.order[seq_rank] : seq_rank;
+  switch (threadIdx.x >> 6) {
+    case 0: col_chain<DK, DV, OUT_DT, 0>(a, sm, seq, h, split); break;
+    case 1: col_chain<DK, DV, OUT_DT, 1>(a, sm, seq, h, split); break;
+    default: col_producer<DK>(a, sm, seq, h); break;
+  }
+}
+
+// ----------------------------------------------------------------------------
 // host-side launchers
 // ----------------------------------------------------------------------------
 template <int DK, int DV, int DTQ, int DTG, bool EXACT>
@@ -715,7 +1006,11 @@ static hipError_t launch_intra_t(const IntraArgs& a, int grid, hipStream_t s) {
 
 template <int DK, int DV, bool EXACT, int OUT>
 static hipError_t launch_state_t(const StateArgs& a, int grid, hipStream_t s) {
-  hipLaunchKernelGGL((kda_state_kernel<DK, DV, EXACT, OUT>), dim3(grid), dim3(256), 0, s, a);
+  if constexpr (EXACT) {
+    hipLaunchKernelGGL((kda_state_kernel<DK, DV, EXACT, OUT>), dim3(grid), dim3(256), 0, s, a);
+  } else {
+    hipLaunchKernelGGL((kda_state_col_kernel<DK, DV, OUT>), dim3(grid), dim3(192), 0, s, a);
+  }
   return hipGetLastError();
 }
 
