@@ -131,7 +131,50 @@ __device__ __forceinline__ void intra_chunk(const IntraArgs& a, const UnitRef& U
   const int64_t bq = (tok * H + h) * DK;
 
   // ---- loads (slot order), masked rows are zero -----------------------------
+  // 16-bit q, k, v (and g) rows are first copied into LDS by direct
+  // global->LDS loads: each instruction moves whole rows (1 KiB, fully
+  // coalesced), where per-lane loads of the slot order would touch 16 rows x
+  // 32 B per instruction.  Each wave copies only its own 16 rows, so a
+  // wave-local wait suffices; 16-byte chunks are XOR-swizzled by row so the
+  // slot-order reads below are spread over the LDS banks.  The staging area
+  // aliases the buffers of the later phases (barrier before their first use).
+  // fp32 tensors are loaded per lane as before.
+  constexpr bool STQ = (DTQ != 0);
+  constexpr bool STG = (DTG != 0);
+  constexpr int ROWB = DK * 2;          // bytes per staged row
+  constexpr int NCH = ROWB / 16;        // 16-byte chunks per row
+  constexpr int RPI = 1024 / ROWB;      // rows per copy instruction
+  static_assert(!(STQ || STG) || sizeof(SM) >= 4 * kC * ROWB, "staging area exceeds the shared buffers");
+  static_assert(DK == DV, "staging assumes dk == dv");
+  unsigned char* const stg = reinterpret_cast<unsigned char*>(&sm);
+  auto stg_row = [&](int t, int row) { return stg + (t * kC + row) * ROWB; };
+  if constexpr (STQ || STG) {
+#pragma unroll
+    for (int t = 0; t < 4; ++t) {  // 0 q, 1 k, 2 g, 3 v
+      if ((t == 2) ? !STG : !STQ) continue;
+      const u16* src = static_cast<const u16*>(t == 0 ? a.q : t == 1 ? a.k : t == 2 ? a.g : a.v);
+#pragma unroll
+      for (int i = 0; i < 16 / RPI; ++i) {
+        const int row = 16 * W + RPI * i + l / NCH;                 // chunk row this lane copies
+        const int cidx = (l % NCH) ^ (row & (NCH - 1));             // source chunk of LDS chunk l % NCH
+        const int64_t srow = U.row0 + min(row, U.len - 1);          // rows past the end re-read a valid row
+        const u16* gsrc = src + (srow * H + h) * DK + cidx * 8;
+        unsigned char* ldst = stg_row(t, 16 * W + RPI * i);
+        __builtin_amdgcn_global_load_lds(gsrc, ldst, 16, 0, 0);
+      }
+    }
+    wait_vmem_all();
+    __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "workgroup", "local");
+  }
+  // four channels ch0 = 32j + 16hf + 4gq .. +3 of this lane's row from staging
+  auto stg_read4 = [&](int t, int j, int hf) -> uint2 {
+    const int ci = 4 * j + 2 * hf + (gq >> 1);
+    const int pc = ci ^ (c & (NCH - 1));
+    return *reinterpret_cast<const uint2*>(stg_row(t, c) + pc * 16 + (gq & 1) * 8);
+  };
+
   float kr[NJ][8], qr[NJ][8], kc[NJ][8], Gt[NJ][8];
+  float vr[NJV][8];
   float beta_c = 0.f;
   {
 #pragma unroll
@@ -139,38 +182,41 @@ __device__ __forceinline__ void intra_chunk(const IntraArgs& a, const UnitRef& U
 #pragma unroll
       for (int hf = 0; hf < 2; ++hf) {
         const int ch0 = 32 * j + 4 * gq + 16 * hf;
-        f4 x = {0, 0, 0, 0}, y = {0, 0, 0, 0}, z = {0, 0, 0, 0};
-        if (valid) {
+        f4 x = {0, 0, 0, 0}, y = {0, 0, 0, 0}, z = {0, 0, 0, 0}, w = {0, 0, 0, 0};
+        if constexpr (STQ) {
+          x = unpack4<DTQ>(stg_read4(0, j, hf));
+          y = unpack4<DTQ>(stg_read4(1, j, hf));
+          w = unpack4<DTQ>(stg_read4(3, j, hf));
+        } else if (valid) {
           x = ld4<DTQ>(a.q, bq + ch0);
           y = ld4<DTQ>(a.k, bq + ch0);
-          z = ld4<DTG>(a.g, bq + ch0);
+          w = ld4<DTQ>(a.v, (tok * H + h) * DV + ch0);
         }
+        if constexpr (STG) z = unpack4<DTG>(stg_read4(2, j, hf));
+        else if (valid) z = ld4<DTG>(a.g, bq + ch0);
 #pragma unroll
         for (int e = 0; e < 4; ++e) {
-          qr[j][4 * hf + e] = x[e] * a.scale;
-          kr[j][4 * hf + e] = y[e];
-          Gt[j][4 * hf + e] = z[e] * kLog2e;
+          qr[j][4 * hf + e] = valid ? x[e] * a.scale : 0.f;
+          kr[j][4 * hf + e] = valid ? y[e] : 0.f;
+          Gt[j][4 * hf + e] = valid ? z[e] * kLog2e : 0.f;
+          vr[j][4 * hf + e] = valid ? w[e] : 0.f;
         }
       }
     }
     if (valid) beta_c = ld1<DTG>(a.beta, tok * H + h);
   }
+  // every wave has read its staged rows before any buffer they alias is written
+  if constexpr (STQ || STG) lds_barrier();
 
   // beta * v  -> BVt (channel-major)
-  {
-    const int64_t bv = (tok * H + h) * DV;
 #pragma unroll
-    for (int j = 0; j < NJV; ++j) {
+  for (int j = 0; j < NJV; ++j)
 #pragma unroll
-      for (int hf = 0; hf < 2; ++hf) {
-        const int ch0 = 32 * j + 4 * gq + 16 * hf;
-        f4 x = {0, 0, 0, 0};
-        if (valid) x = ld4<DTQ>(a.v, bv + ch0);
+    for (int hf = 0; hf < 2; ++hf) {
+      const int ch0 = 32 * j + 4 * gq + 16 * hf;
 #pragma unroll
-        for (int e = 0; e < 4; ++e) sm.BVt[(ch0 + e) * PC + c] = st(beta_c * x[e]);
-      }
+      for (int e = 0; e < 4; ++e) sm.BVt[(ch0 + e) * PC + c] = st(beta_c * vr[j][4 * hf + e]);
     }
-  }
 
   // ---- tile-local cumsum and the two decay factors ---------------------------
   float dmin = 0.f;
@@ -714,7 +760,7 @@ void kda_state_kernel(StateArgs a) {
 //     time, the B fragment of a 32-wide K step over channels (slot order);
 //   * v~ row tiles, two at a time, are the B fragment over 32 keys.
 // Only the dv-independent A operands (W, gamma*q, Aqk, lambda*k) and gamma_C
-// are shared: per chunk a third, producer-only wave copies them once per
+// are shared: per chunk four producer-only waves copy them once per
 // workgroup from the workspace into one of two LDS buffers by direct
 // global->LDS loads (16 B per lane, fragment order, so every LDS read is a
 // conflict-free 16 B per lane), one chunk ahead.  The compute waves issue no
@@ -740,13 +786,16 @@ struct ColSmem {
   alignas(16) unsigned char buf[2][ColLayout<DK>::BYTES];
 };
 
-// s_waitcnt vmcnt(0), other counters untouched (gfx9 encoding)
-__device__ __forceinline__ void wait_vmem_all() { __builtin_amdgcn_s_waitcnt(0x0F70); }
 
+// Producer waves per state workgroup.  One wave moves only ~22 GB/s from L2
+// on this part (measured); four together move the 56 KiB a chunk needs in
+// well under a chunk's compute time.
+constexpr int kColProducers = 4;
 
-// Copy the shared operands of chunk-head ch into an LDS buffer
-// (fragment-ordered 1 KiB blocks: lane l moves bytes 16l..16l+15) and gamma_C.
-template <int DK>
+// Copy producer P's share of the shared operands of chunk-head ch into an
+// LDS buffer (fragment-ordered 1 KiB blocks: lane l moves bytes 16l..16l+15);
+// the last producer also copies gamma_C.
+template <int DK, int P>
 __device__ __forceinline__ void col_stage(const StateArgs& a, int64_t ch, unsigned char* dst, int l) {
   typedef ColLayout<DK> LY;
   const _Float16* iW = static_cast<const _Float16*>(a.W);
@@ -754,7 +803,7 @@ __device__ __forceinline__ void col_stage(const StateArgs& a, int64_t ch, unsign
   const _Float16* iL = static_cast<const _Float16*>(a.LK);
   const _Float16* iA = static_cast<const _Float16*>(a.AQ);
 #pragma unroll
-  for (int f = 0; f < LY::NF; ++f) {
+  for (int f = P; f < LY::NF; f += kColProducers) {
     const _Float16* src;
     if (f < LY::OFF_Q) src = iW + (ch * LY::FW + f) * 512;
     else if (f < LY::OFF_L) src = iQ + (ch * LY::FW + (f - LY::OFF_Q)) * 512;
@@ -766,9 +815,11 @@ __device__ __forceinline__ void col_stage(const StateArgs& a, int64_t ch, unsign
     }
     __builtin_amdgcn_global_load_lds(src + l * 8, dst + f * 1024, 16, 0, 0);
   }
-  const _Float16* gsrc = reinterpret_cast<const _Float16*>(a.GC + ch * DK + l * 4);
-  unsigned char* gdst = dst + LY::OFF_G;
-  if (l < DK / 4) __builtin_amdgcn_global_load_lds(gsrc, gdst, 16, 0, 0);
+  if constexpr (P == kColProducers - 1) {
+    const _Float16* gsrc = reinterpret_cast<const _Float16*>(a.GC + ch * DK + l * 4);
+    unsigned char* gdst = dst + LY::OFF_G;
+    if (l < DK / 4) __builtin_amdgcn_global_load_lds(gsrc, gdst, 16, 0, 0);
+  }
 }
 
 struct ChainRef {
@@ -792,20 +843,21 @@ __device__ __forceinline__ ChainRef chain_ref(const Geom& G, int seq) {
   return c;
 }
 
-// Producer wave: fills the buffer of chunk n+1 while the compute waves work on
-// chunk n, and joins the one barrier per chunk once its copies have landed.
-template <int DK>
+// Producer wave P: fills its share of the buffer of chunk n+1 while the
+// compute waves work on chunk n, and joins the one barrier per chunk once its
+// copies have landed.
+template <int DK, int P>
 __device__ __forceinline__ void col_producer(const StateArgs& a, ColSmem<DK>& sm, int seq, int h) {
   const ChainRef c = chain_ref(a.geom, seq);
   const int H = a.geom.H;
   const int l = threadIdx.x & 63;
   if (c.nchunks > 0) {
-    col_stage<DK>(a, static_cast<int64_t>(c.u0) * H + h, sm.buf[0], l);
+    col_stage<DK, P>(a, static_cast<int64_t>(c.u0) * H + h, sm.buf[0], l);
     wait_vmem_all();
     lds_barrier();
   }
   for (int n = 0; n + 1 < c.nchunks; ++n) {
-    col_stage<DK>(a, static_cast<int64_t>(c.u0 + n + 1) * H + h, sm.buf[(n + 1) & 1], l);
+    col_stage<DK, P>(a, static_cast<int64_t>(c.u0 + n + 1) * H + h, sm.buf[(n + 1) & 1], l);
     wait_vmem_all();
     lds_barrier();
   }
@@ -971,7 +1023,7 @@ __device__ __forceinline__ void col_chain(const StateArgs& a, ColSmem<DK>& sm, i
 }
 
 template <int DK, int DV, int OUT_DT>
-__global__ __launch_bounds__(192, 1)
+__global__ __launch_bounds__(64 * (2 + kColProducers), 1)
 void kda_state_col_kernel(StateArgs a) {
   constexpr int SPLITS = DV / 32;
   __shared__ ColSmem<DK> sm;
@@ -991,7 +1043,10 @@ void kda_state_col_kernel(StateArgs a) {
   switch (threadIdx.x >> 6) {
     case 0: col_chain<DK, DV, OUT_DT, 0>(a, sm, seq, h, split); break;
     case 1: col_chain<DK, DV, OUT_DT, 1>(a, sm, seq, h, split); break;
-    default: col_producer<DK>(a, sm, seq, h); break;
+    case 2: col_producer<DK, 0>(a, sm, seq, h); break;
+    case 3: col_producer<DK, 1>(a, sm, seq, h); break;
+    case 4: col_producer<DK, 2>(a, sm, seq, h); break;
+    default: col_producer<DK, 3>(a, sm, seq, h); break;
   }
 }
 
@@ -1009,7 +1064,7 @@ static hipError_t launch_state_t(const StateArgs& a, int grid, hipStream_t s) {
   if constexpr (EXACT) {
     hipLaunchKernelGGL((kda_state_kernel<DK, DV, EXACT, OUT>), dim3(grid), dim3(256), 0, s, a);
   } else {
-    hipLaunchKernelGGL((kda_state_col_kernel<DK, DV, OUT>), dim3(grid), dim3(192), 0, s, a);
+    hipLaunchKernelGGL((kda_state_col_kernel<DK, DV, OUT>), dim3(grid), dim3(64 * (2 + kColProducers)), 0, s, a);
   }
   return hipGetLastError();
 }

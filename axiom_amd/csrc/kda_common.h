@@ -63,26 +63,31 @@ __device__ __forceinline__ float ld1(const void* p, int64_t i) {
   else return f16bits_to_f32(static_cast<const u16*>(p)[i]);
 }
 
+// Four packed 16-bit elements (DT 1 = bf16, 2 = fp16) to fp32.
+template <int DT>
+__device__ __forceinline__ f4 unpack4(uint2 w) {
+  f4 r;
+  if constexpr (DT == 1) {
+    r[0] = __uint_as_float(w.x << 16);
+    r[1] = __uint_as_float(w.x & 0xFFFF0000u);
+    r[2] = __uint_as_float(w.y << 16);
+    r[3] = __uint_as_float(w.y & 0xFFFF0000u);
+  } else {
+    r[0] = f16bits_to_f32(static_cast<u16>(w.x & 0xFFFFu));
+    r[1] = f16bits_to_f32(static_cast<u16>(w.x >> 16));
+    r[2] = f16bits_to_f32(static_cast<u16>(w.y & 0xFFFFu));
+    r[3] = f16bits_to_f32(static_cast<u16>(w.y >> 16));
+  }
+  return r;
+}
+
 // Four consecutive elements starting at element index i (i multiple of 4).
 template <int DT>
 __device__ __forceinline__ f4 ld4(const void* p, int64_t i) {
   if constexpr (DT == 0) {
     return *reinterpret_cast<const f4*>(static_cast<const float*>(p) + i);
   } else {
-    uint2 w = *reinterpret_cast<const uint2*>(static_cast<const u16*>(p) + i);
-    f4 r;
-    if constexpr (DT == 1) {
-      r[0] = __uint_as_float(w.x << 16);
-      r[1] = __uint_as_float(w.x & 0xFFFF0000u);
-      r[2] = __uint_as_float(w.y << 16);
-      r[3] = __uint_as_float(w.y & 0xFFFF0000u);
-    } else {
-      r[0] = f16bits_to_f32(static_cast<u16>(w.x & 0xFFFFu));
-      r[1] = f16bits_to_f32(static_cast<u16>(w.x >> 16));
-      r[2] = f16bits_to_f32(static_cast<u16>(w.y & 0xFFFFu));
-      r[3] = f16bits_to_f32(static_cast<u16>(w.y >> 16));
-    }
-    return r;
+    return unpack4<DT>(*reinterpret_cast<const uint2*>(static_cast<const u16*>(p) + i));
   }
 }
 
@@ -172,6 +177,11 @@ __device__ __forceinline__ float row_scan16(float x) {
 }
 
 __device__ __forceinline__ float fast_exp2(float x) { return __builtin_amdgcn_exp2f(x); }
+
+// s_waitcnt vmcnt(0), other counters untouched (gfx9 encoding).  Direct
+// global->LDS loads are not tracked by the compiler's own waits, so code that
+// reads what they wrote waits with this (then orders its LDS reads after it).
+__device__ __forceinline__ void wait_vmem_all() { __builtin_amdgcn_s_waitcnt(0x0F70); }
 
 // Workgroup barrier that orders LDS only.  __syncthreads() also releases
 // global memory, which makes every wave wait for its outstanding global loads
