@@ -324,8 +324,24 @@ __device__ __forceinline__ void intra_chunk(const IntraArgs& a, const UnitRef& U
           }
         }
       }
-      accK[W] = mma32(accK[W], ad, bk);
-      accQ[W] = mma32(accQ[W], ad, bqd);
+      if constexpr (EXACT) {
+        accK[W] = mma32(accK[W], ad, bk);
+        accQ[W] = mma32(accQ[W], ad, bqd);
+      } else {
+        // x*y ~ xh*yh + xh*yl + xl*yh with bf16 halves (x = xh + xl): ~16
+        // significant bits per operand on the bf16 MFMA, with the fp32
+        // exponent range the 2^|D| factor of the diagonal tile needs
+        b8 ah, al, kh, kl, qh, ql;
+        split_bf16(ad, ah, al);
+        split_bf16(bk, kh, kl);
+        split_bf16(bqd, qh, ql);
+        accK[W] = mma32_bf16(accK[W], ah, kh);
+        accQ[W] = mma32_bf16(accQ[W], ah, qh);
+        accK[W] = mma32_bf16(accK[W], ah, kl);
+        accQ[W] = mma32_bf16(accQ[W], ah, ql);
+        accK[W] = mma32_bf16(accK[W], al, kh);
+        accQ[W] = mma32_bf16(accQ[W], al, qh);
+      }
     }
 
     // q*gamma -> GQ (fragment order); beta*gamma*k and lambda*k kept

@@ -143,6 +143,15 @@ __device__ __forceinline__ f4 mma32(f4 acc, const f8& a, const f8& b) {
 __device__ __forceinline__ f4 mma32_bf16(f4 acc, b8 a, b8 b) {
   return __builtin_amdgcn_mfma_f32_16x16x32_bf16(a, b, acc, 0, 0, 0);
 }
+// x = hi + lo with both halves bf16 (hi = x rounded to nearest even)
+__device__ __forceinline__ void split_bf16(const f8& x, b8& hi, b8& lo) {
+#pragma unroll
+  for (int e = 0; e < 8; ++e) {
+    const __bf16 h = static_cast<__bf16>(x[e]);
+    hi[e] = h;
+    lo[e] = static_cast<__bf16>(x[e] - static_cast<float>(h));
+  }
+}
 __device__ __forceinline__ f4 mma16(f4 acc, h4 a, h4 b) {
   return __builtin_amdgcn_mfma_f32_16x16x16f16(a, b, acc, 0, 0, 0);
 }

@@ -29,10 +29,32 @@ void kda_decode_kernel(DecodeArgs a) {
   const int tid = threadIdx.x;
   const int bh = blockIdx.x;             // b * H + h
   const int64_t vec = static_cast<int64_t>(bh);
-  for (int d = tid; d < DK; d += 256) {
-    qs[d] = ld1<DT>(a.q, vec * DK + d) * a.scale;
-    ks[d] = ld1<DT>(a.k, vec * DK + d);
-    as[d] = fast_exp2(ld1<DT>(a.g, vec * DK + d) * kLog2e);
+  // The small per-token loads (q, k, g, beta, v) are issued first and the
+  // state read right after: memory operations retire in order, so waiting on
+  // the small loads does not wait for the state, whose latency then overlaps
+  // the exp, the barrier and the k.q reduction.  Every thread loads an
+  // in-range q/k/g element; threads >= DK drop theirs.
+  static_assert(DK <= 256, "one q/k/g element per thread");
+  const int td = tid % DK;
+  const float q_t = ld1<DT>(a.q, vec * DK + td);
+  const float k_t = ld1<DT>(a.k, vec * DK + td);
+  const float g_t = ld1<DT>(a.g, vec * DK + td);
+  const int cq = tid % NCQ;
+  const int rg = tid / NCQ;
+  const float beta = ld1<DT>(a.beta, vec);
+  const f4 vv = ld4<DT>(a.v, vec * DV + 4 * cq);
+  __builtin_amdgcn_sched_barrier(0);  // keep the small loads ahead of the state read
+  float* S = a.state + static_cast<int64_t>(bh) * DK * DV;
+  f4 sv[RPT];
+#pragma unroll
+  for (int i = 0; i < RPT; ++i) {
+    const int d = rg + RG * i;
+    sv[i] = __builtin_nontemporal_load(reinterpret_cast<const f4*>(S + static_cast<int64_t>(d) * DV) + cq);
+  }
+  if (tid < DK) {
+    qs[tid] = q_t * a.scale;
+    ks[tid] = k_t;
+    as[tid] = fast_exp2(g_t * kLog2e);
   }
   __syncthreads();
   if (tid < 64) {
@@ -43,15 +65,6 @@ void kda_decode_kernel(DecodeArgs a) {
     if (tid == 0) kq_s = p;
   }
 
-  const int cq = tid % NCQ;
-  const int rg = tid / NCQ;
-  float* S = a.state + static_cast<int64_t>(bh) * DK * DV;
-  f4 sv[RPT];
-#pragma unroll
-  for (int i = 0; i < RPT; ++i) {
-    const int d = rg + RG * i;
-    sv[i] = __builtin_nontemporal_load(reinterpret_cast<const f4*>(S + static_cast<int64_t>(d) * DV) + cq);
-  }
   f4 pu = {0, 0, 0, 0}, pw = {0, 0, 0, 0};
 #pragma unroll
   for (int i = 0; i < RPT; ++i) {
@@ -67,8 +80,6 @@ void kda_decode_kernel(DecodeArgs a) {
   f4 uu = {0, 0, 0, 0}, ww = {0, 0, 0, 0};
 #pragma unroll
   for (int g = 0; g < RG; ++g) { uu += red_u[g][cq]; ww += red_w[g][cq]; }
-  const float beta = ld1<DT>(a.beta, vec);
-  const f4 vv = ld4<DT>(a.v, vec * DV + 4 * cq);
   const f4 delta = beta * (vv - uu);              // beta (v - u)
   const float kq = kq_s;
 #pragma unroll
