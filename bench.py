@@ -10,8 +10,11 @@ Also reported on the same JSON line:
 * TFLOP/s and % of bf16 dense MFMA peak with the algorithmic count
   ``8*C*d + 6*d^2`` FLOP per token-head;
 * ``roofline``: algorithmic bytes (read q, k, v, g, beta; write o fp32 and the
-  final state fp32 = 407.4 MB) over the average duration of the forward's
-  kernels, measured with HIP events on the stream they are launched on;
+  final state fp32 = 407.4 MB) over the average duration of one forward call
+  (its two kernels), measured with HIP events on the stream they are launched
+  on; ``traffic`` is the HBM bytes per call measured by rocprofv3
+  (FETCH_SIZE + WRITE_SIZE, calibrated), read from the committed summary
+  under ``profiles/``;
 * ``decode``: the recurrent decode step at B=256, H=16, d=128 (fp32 state
   read-modified-written in place, bf16 inputs), iterated 128 steps, as GB/s
   against the 8 TB/s HBM peak (``configs[4]``);
@@ -36,6 +39,8 @@ import time
 import torch
 
 HBM_PEAK_GBPS = 8000.0
+TRAFFIC_PROFILE = os.path.join(os.path.dirname(os.path.abspath(__file__)), "profiles",
+                               "kda_fwd_decode_config1_config4_hbm_traffic.md")
 MFMA_BF16_PEAK_TFLOPS = 2516.6
 
 CFG = dict(B=4, T=4096, H=16, dk=128, dv=128, C=64)
@@ -53,6 +58,19 @@ def fwd_bytes(B, T, H, dk, dv, in_bytes=2, o_bytes=4):
 def decode_bytes(B, H, dk, dv, in_bytes=2, o_bytes=4):
     n = B * H
     return 2 * n * dk * dv * 4 + n * (3 * dk + dv + 1) * in_bytes + n * dv * o_bytes
+
+
+def measured_traffic(key):
+    """HBM bytes per call from the committed rocprofv3 FETCH_SIZE / WRITE_SIZE
+    summary (calibrated against a device copy of known size), or None."""
+    try:
+        with open(TRAFFIC_PROFILE) as f:
+            for line in f:
+                if line.startswith(key + ":"):
+                    return int(line.split(":", 1)[1])
+    except (OSError, ValueError):
+        pass
+    return None
 
 
 def make_inputs_gpu(B, T, H, dk, dv, seed, device, dtype=torch.bfloat16):
@@ -133,7 +151,8 @@ def bench_decode(args, device):
     nbytes = decode_bytes(B, H, d, d)
     gbps = nbytes / t_step / 1e9
     return dict(us_per_step=t_step * 1e6, gbps=gbps, frac=gbps / HBM_PEAK_GBPS,
-                bytes_per_step=nbytes, steps=steps, config="B256 H16 d128 bf16, fp32 state in place")
+                bytes_per_step=nbytes, traffic=measured_traffic("decode_traffic_bytes_per_step"),
+                steps=steps, config="B256 H16 d128 bf16, fp32 state in place")
 
 
 def cpu_baseline(fwd_inputs, seconds):
@@ -222,8 +241,9 @@ def main():
         "mfma_peak_frac": tflops / MFMA_BF16_PEAK_TFLOPS,
         "us_per_launch": t_launch * 1e6,
         "roofline": {"bound": "hbm", "achieved": achieved, "peak": HBM_PEAK_GBPS, "unit": "GB/s",
-                     "frac": achieved / HBM_PEAK_GBPS, "traffic": None,
-                     "kernels": "kda_intra_kernel + kda_state_kernel (one kda_chunk_fwd)",
+                     "frac": achieved / HBM_PEAK_GBPS,
+                     "traffic": measured_traffic("traffic_bytes_per_call"),
+                     "kernels": "kda_intra_kernel + kda_state_col_kernel (one kda_chunk_fwd)",
                      "algorithmic_bytes_per_launch": nbytes},
     }
     try:
