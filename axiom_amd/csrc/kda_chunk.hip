@@ -794,12 +794,14 @@ struct ColLayout {
   static constexpr int OFF_A = 2 * FW + FL;
   static constexpr int NF = 2 * FW + FL + FA;  // 1-KiB fragments per chunk-head
   static constexpr int OFF_G = NF * 1024;      // gamma_C (DK floats)
-  static constexpr int BYTES = NF * 1024 + DK * 4;
+  static constexpr int OFF_U = NF * 1024 + DK * 4;  // U of the workgroup's two value tiles, [ct][w][64][4]
+  static constexpr int BYTES = OFF_U + 4 * 1024;
 };
 
 template <int DK>
 struct ColSmem {
   alignas(16) unsigned char buf[2][ColLayout<DK>::BYTES];
+  alignas(16) unsigned char obuf[2][kC * 32 * 4];  // o rows of the workgroup's 32 columns
 };
 
 
@@ -808,11 +810,13 @@ struct ColSmem {
 // well under a chunk's compute time.
 constexpr int kColProducers = 4;
 
-// Copy producer P's share of the shared operands of chunk-head ch into an
-// LDS buffer (fragment-ordered 1 KiB blocks: lane l moves bytes 16l..16l+15);
-// the last producer also copies gamma_C.
-template <int DK, int P>
-__device__ __forceinline__ void col_stage(const StateArgs& a, int64_t ch, unsigned char* dst, int l) {
+// Copy producer P's share of the operands of chunk-head ch into an LDS buffer
+// (fragment-ordered 1 KiB blocks: lane l moves bytes 16l..16l+15): every
+// fourth shared fragment, the U block of row tile P for this workgroup's two
+// value tiles, and (last producer) gamma_C.
+template <int DK, int DV, int P>
+__device__ __forceinline__ void col_stage(const StateArgs& a, int64_t ch, int split, unsigned char* dst,
+                                          int l) {
   typedef ColLayout<DK> LY;
   const _Float16* iW = static_cast<const _Float16*>(a.W);
   const _Float16* iQ = static_cast<const _Float16*>(a.GQ);
@@ -831,10 +835,41 @@ __device__ __forceinline__ void col_stage(const StateArgs& a, int64_t ch, unsign
     }
     __builtin_amdgcn_global_load_lds(src + l * 8, dst + f * 1024, 16, 0, 0);
   }
+  {
+    static_assert(kColProducers == 4, "one U row tile per producer");
+    const _Float16* usrc = static_cast<const _Float16*>(a.U) +
+                           (ch * 4 * (DV / 16) + P * (DV / 16) + 2 * split) * 256 + l * 8;
+    unsigned char* udst = dst + LY::OFF_U + P * 1024;
+    __builtin_amdgcn_global_load_lds(usrc, udst, 16, 0, 0);
+  }
   if constexpr (P == kColProducers - 1) {
     const _Float16* gsrc = reinterpret_cast<const _Float16*>(a.GC + ch * DK + l * 4);
     unsigned char* gdst = dst + LY::OFF_G;
     if (l < DK / 4) __builtin_amdgcn_global_load_lds(gsrc, gdst, 16, 0, 0);
+  }
+}
+
+// Producer P's share of the o rows of one chunk: LDS [64 rows][32 columns]
+// (fp32, or bf16 when OUT_DT == 1) to the workgroup's 32 columns of o, 16 B
+// per lane, rows past the chunk's end skipped.
+template <int DV, int OUT_DT, int P>
+__device__ __forceinline__ void col_store_rows(const StateArgs& a, const unsigned char* ob, int64_t row0,
+                                               int len, int h, int split, int l) {
+  constexpr int ES = (OUT_DT == 0) ? 4 : 2;
+  constexpr int LPR = 32 * ES / 16;            // lanes per row
+  constexpr int RPI = 64 / LPR;                // rows per instruction
+  constexpr int NI = kC / RPI;                 // instructions per chunk
+  const int H = a.geom.H;
+#pragma unroll
+  for (int ins = P; ins < NI; ins += kColProducers) {
+    const int row = RPI * ins + l / LPR;
+    const int cb = (l % LPR) * 16;             // byte offset inside the 32-column row
+    const uint4 v = *reinterpret_cast<const uint4*>(ob + row * (32 * ES) + cb);
+    if (row < len) {
+      unsigned char* dst = static_cast<unsigned char*>(a.o) +
+                           (((row0 + row) * H + h) * static_cast<int64_t>(DV) + 32 * split) * ES + cb;
+      *reinterpret_cast<uint4*>(dst) = v;
+    }
   }
 }
 
@@ -859,44 +894,51 @@ __device__ __forceinline__ ChainRef chain_ref(const Geom& G, int seq) {
   return c;
 }
 
-// Producer wave P: fills its share of the buffer of chunk n+1 while the
-// compute waves work on chunk n, and joins the one barrier per chunk once its
-// copies have landed.
-template <int DK, int P>
-__device__ __forceinline__ void col_producer(const StateArgs& a, ColSmem<DK>& sm, int seq, int h) {
+// Producer wave P: while the compute waves work on chunk n it stores o of
+// chunk n-1 (from LDS) and fills its share of the buffer of chunk n+1, then
+// joins the one barrier per chunk once all of it has landed.  The compute
+// waves issue no global memory operation inside the chunk loop: a wave issues
+// memory instructions in order, so queueing behind these copies would stall
+// their MFMAs.
+template <int DK, int DV, int OUT_DT, int P>
+__device__ __forceinline__ void col_producer(const StateArgs& a, ColSmem<DK>& sm, int seq, int h,
+                                             int split) {
   const ChainRef c = chain_ref(a.geom, seq);
   const int H = a.geom.H;
   const int l = threadIdx.x & 63;
-  if (c.nchunks > 0) {
-    col_stage<DK, P>(a, static_cast<int64_t>(c.u0) * H + h, sm.buf[0], l);
+  if (c.nchunks <= 0) return;
+  col_stage<DK, DV, P>(a, static_cast<int64_t>(c.u0) * H + h, split, sm.buf[0], l);
+  wait_vmem_all();
+  lds_barrier();
+  for (int n = 0; n < c.nchunks; ++n) {
+    if (n > 0)
+      col_store_rows<DV, OUT_DT, P>(a, sm.obuf[(n - 1) & 1], c.tok0 + static_cast<int64_t>(n - 1) * kC,
+                                    min(kC, c.seq_len - (n - 1) * kC), h, split, l);
+    if (n + 1 < c.nchunks)
+      col_stage<DK, DV, P>(a, static_cast<int64_t>(c.u0 + n + 1) * H + h, split, sm.buf[(n + 1) & 1], l);
     wait_vmem_all();
     lds_barrier();
   }
-  for (int n = 0; n + 1 < c.nchunks; ++n) {
-    col_stage<DK, P>(a, static_cast<int64_t>(c.u0 + n + 1) * H + h, sm.buf[(n + 1) & 1], l);
-    wait_vmem_all();
-    lds_barrier();
-  }
+  const int nl = c.nchunks - 1;
+  col_store_rows<DV, OUT_DT, P>(a, sm.obuf[nl & 1], c.tok0 + static_cast<int64_t>(nl) * kC,
+                                min(kC, c.seq_len - nl * kC), h, split, l);
 }
 
 __device__ __forceinline__ h8 lds_frag(const unsigned char* buf, int f, int l) {
   return *reinterpret_cast<const h8*>(buf + f * 1024 + l * 16);
 }
 
-template <int DK, int DV, int OUT_DT>
-__device__ __forceinline__ void col_store_o(const StateArgs& a, const f4 (&O)[4], int64_t row0, int len,
-                                            int h, int et, int r, int gq) {
-  const int H = a.geom.H;
+// o of row tiles 0..3 (D layout: rows 16ct + 4gq + i, column r of value tile
+// W) into the LDS o rows of the workgroup's 32 columns.
+template <int OUT_DT, int W>
+__device__ __forceinline__ void col_put_o(unsigned char* ob, const f4 (&O)[4], int r, int gq) {
 #pragma unroll
   for (int ct = 0; ct < 4; ++ct)
 #pragma unroll
     for (int i = 0; i < 4; ++i) {
-      const int cr = 16 * ct + 4 * gq + i;
-      if (cr < len) {
-        const int64_t oi = ((row0 + cr) * H + h) * (int64_t)DV + 16 * et + r;
-        if constexpr (OUT_DT == 0) static_cast<float*>(a.o)[oi] = O[ct][i];
-        else static_cast<u16*>(a.o)[oi] = f32_to_bf16_bits(O[ct][i]);
-      }
+      const int row = 16 * ct + 4 * gq + i;
+      if constexpr (OUT_DT == 0) reinterpret_cast<float*>(ob)[row * 32 + 16 * W + r] = O[ct][i];
+      else reinterpret_cast<u16*>(ob)[row * 32 + 16 * W + r] = f32_to_bf16_bits(O[ct][i]);
     }
 }
 
@@ -910,8 +952,7 @@ __device__ __forceinline__ void col_chain(const StateArgs& a, ColSmem<DK>& sm, i
   const int l = threadIdx.x & 63, r = l & 15, gq = l >> 4;
   const int et = 2 * split + W;
   const ChainRef c = chain_ref(G, seq);
-  const int u0 = c.u0, nchunks = c.nchunks, seq_len = c.seq_len;
-  const int64_t tok0 = c.tok0;
+  const int nchunks = c.nchunks;
 
   f4 S[NT];
   const int64_t sbase = (static_cast<int64_t>(seq) * H + h) * DK * DV;
@@ -923,23 +964,13 @@ __device__ __forceinline__ void col_chain(const StateArgs& a, ColSmem<DK>& sm, i
                      ? a.h0[sbase + static_cast<int64_t>(16 * dt + 4 * gq + i) * DV + 16 * et + r]
                      : 0.f;
 
-  const _Float16* iU = static_cast<const _Float16*>(a.U);
-  auto chead_of = [&](int n) { return static_cast<int64_t>(u0 + n) * H + h; };
-  auto load_u = [&](h4 (&U)[4], int64_t ch) {
-#pragma unroll
-    for (int ct = 0; ct < 4; ++ct)
-      U[ct] = *reinterpret_cast<const h4*>(iU + (ch * 4 * (DV / 16) + ct * (DV / 16) + et) * 256 + l * 4);
-  };
-
-  h4 Ucur[4], Unext[4];
-  if (nchunks > 0) {
-    load_u(Ucur, chead_of(0));
-    lds_barrier();  // chunk 0 staged by the producer wave
-  }
+  if (nchunks > 0) lds_barrier();  // chunk 0 staged by the producer waves
   for (int n = 0; n < nchunks; ++n) {
     const unsigned char* cur = sm.buf[n & 1];
-    const bool more = n + 1 < nchunks;
-    if (more) load_u(Unext, chead_of(n + 1));
+    h4 Ucur[4];
+#pragma unroll
+    for (int ct = 0; ct < 4; ++ct)
+      Ucur[ct] = *reinterpret_cast<const h4*>(cur + LY::OFF_U + (2 * ct + W) * 512 + l * 8);
 
     // The step is a fixed sequence of MFMA groups; each group's A fragments
     // are read from LDS two groups ahead into a 3-slot register ring, and a
@@ -1020,13 +1051,10 @@ __device__ __forceinline__ void col_chain(const StateArgs& a, ColSmem<DK>& sm, i
       }
     }
 
-    col_store_o<DK, DV, OUT_DT>(a, O, tok0 + static_cast<int64_t>(n) * kC, min(kC, seq_len - n * kC),
-                                h, et, r, gq);
-#pragma unroll
-    for (int ct = 0; ct < 4; ++ct) Ucur[ct] = Unext[ct];
-    // the producer has landed the next buffer, and both compute waves are
-    // done with this one before it is refilled
-    if (more) lds_barrier();
+    col_put_o<OUT_DT, W>(sm.obuf[n & 1], O, r, gq);
+    // the producers have landed the next buffer and may store these o rows;
+    // both compute waves are done with this buffer before it is refilled
+    lds_barrier();
   }
 
   if (a.ht != nullptr) {
@@ -1059,10 +1087,10 @@ void kda_state_col_kernel(StateArgs a) {
   switch (threadIdx.x >> 6) {
     case 0: col_chain<DK, DV, OUT_DT, 0>(a, sm, seq, h, split); break;
     case 1: col_chain<DK, DV, OUT_DT, 1>(a, sm, seq, h, split); break;
-    case 2: col_producer<DK, 0>(a, sm, seq, h); break;
-    case 3: col_producer<DK, 1>(a, sm, seq, h); break;
-    case 4: col_producer<DK, 2>(a, sm, seq, h); break;
-    default: col_producer<DK, 3>(a, sm, seq, h); break;
+    case 2: col_producer<DK, DV, OUT_DT, 0>(a, sm, seq, h, split); break;
+    case 3: col_producer<DK, DV, OUT_DT, 1>(a, sm, seq, h, split); break;
+    case 4: col_producer<DK, DV, OUT_DT, 2>(a, sm, seq, h, split); break;
+    default: col_producer<DK, DV, OUT_DT, 3>(a, sm, seq, h, split); break;
   }
 }
 
