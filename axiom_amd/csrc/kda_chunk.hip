@@ -194,16 +194,26 @@ __device__ __forceinline__ void intra_chunk(const IntraArgs& a, const UnitRef& U
         }
         if constexpr (STG) z = unpack4<DTG>(stg_read4(2, j, hf));
         else if (valid) z = ld4<DTG>(a.g, bq + ch0);
+        // Rows past the chunk's end (staged copies of a real row) need no
+        // masking except g and beta: beta = 0 zeroes their rows of L, W and U
+        // and hence of v~, and their o rows are never stored; g = 0 keeps them
+        // out of the chunk's decay.
 #pragma unroll
         for (int e = 0; e < 4; ++e) {
-          qr[j][4 * hf + e] = valid ? x[e] * a.scale : 0.f;
-          kr[j][4 * hf + e] = valid ? y[e] : 0.f;
+          qr[j][4 * hf + e] = x[e];
+          kr[j][4 * hf + e] = y[e];
           Gt[j][4 * hf + e] = valid ? z[e] * kLog2e : 0.f;
-          vr[j][4 * hf + e] = valid ? w[e] : 0.f;
+          vr[j][4 * hf + e] = w[e];
         }
       }
     }
     if (valid) beta_c = ld1<DTG>(a.beta, tok * H + h);
+    if (a.scale != 1.f) {
+#pragma unroll
+      for (int j = 0; j < NJ; ++j)
+#pragma unroll
+        for (int e = 0; e < 8; ++e) qr[j][e] *= a.scale;
+    }
   }
   // every wave has read its staged rows before any buffer they alias is written
   if constexpr (STQ || STG) lds_barrier();
@@ -222,7 +232,7 @@ __device__ __forceinline__ void intra_chunk(const IntraArgs& a, const UnitRef& U
   float dmin = 0.f;
 #pragma unroll
   for (int j = 0; j < NJ; ++j) {
-    f8 x;
+    f8 x, tj;
 #pragma unroll
     for (int e = 0; e < 8; ++e) {
       const float gt = row_scan16(Gt[j][e]);
@@ -234,12 +244,26 @@ __device__ __forceinline__ void intra_chunk(const IntraArgs& a, const UnitRef& U
       kr[j][e] *= R;
       qr[j][e] *= R;
       x[e] = kc[j][e];
-      if (r == 15) sm.tot[W][32 * j + 8 * gq + e] = gt;
+      tj[e] = gt;
     }
+    if (r == 15) *reinterpret_cast<f8*>(&sm.tot[W][32 * j + 8 * gq]) = tj;
     *reinterpret_cast<v8*>(&sm.r1[c * PK + 32 * j + 8 * gq]) = cvt8<EXACT>(x);
   }
   // a tile whose decay total passes 2^-100 in some channel: anchored path
   const bool extreme = __any(dmin < -100.f);
+  // The diagonal tile's operands are k*Cf and (k or q)*R*2^-D.  When every
+  // channel's tile total D is above -12 and |k*Cf|, |k*R|, |q*R| <= 8 they
+  // fit fp16 (< 2^15) and the tile runs on one fp16 MFMA pair like the
+  // off-diagonal ones; otherwise on bf16 hi/lo.
+  bool diag16 = false;
+  if constexpr (!EXACT) {
+    float mx = 0.f;
+#pragma unroll
+    for (int j = 0; j < NJ; ++j)
+#pragma unroll
+      for (int e = 0; e < 8; ++e) mx = fmaxf(mx, fmaxf(fabsf(kc[j][e]), fmaxf(fabsf(kr[j][e]), fabsf(qr[j][e]))));
+    diag16 = !__any(dmin < -12.f || !(mx <= 8.f));
+  }
   lds_barrier();  // #1: tot, k*Cf, BVt
 
   // ---- per-channel constants of this tile (wave-local) -----------------------
@@ -327,6 +351,10 @@ __device__ __forceinline__ void intra_chunk(const IntraArgs& a, const UnitRef& U
       if constexpr (EXACT) {
         accK[W] = mma32(accK[W], ad, bk);
         accQ[W] = mma32(accQ[W], ad, bqd);
+      } else if (diag16 && !extreme) {
+        const v8 a16 = cvt8<EXACT>(ad);
+        accK[W] = mma32(accK[W], a16, cvt8<EXACT>(bk));
+        accQ[W] = mma32(accQ[W], a16, cvt8<EXACT>(bqd));
       } else {
         // x*y ~ xh*yh + xh*yl + xl*yh with bf16 halves (x = xh + xl): ~16
         // significant bits per operand on the bf16 MFMA, with the fp32
