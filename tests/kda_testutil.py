@@ -33,3 +33,39 @@ def assert_close(name: str, got, ref, tol: tuple[float, float]):
     assert rel <= rel_tol and mx <= abs_tol, (
         f"{name}: rel_l2={rel:.3e} (tol {rel_tol:g}) max_abs={mx:.3e} (tol {abs_tol:g})")
     return rel, mx
+
+
+def make_inputs_device(B, T, H, dk, dv, seed, device, h0_std=0.0, n_states=None):
+    """The config distributions drawn on the GPU (torch generator), bf16:
+    q, k = l2norm(N(0,1)); v ~ N(0,1); beta = sigmoid(N(0,1));
+    g = -softplus(N(0,1)) * exp(a_h), a_h ~ U(-2, 0); h0 ~ N(0, h0_std^2) fp32.
+    For full-size cases whose inputs are too large to draw on the host; the
+    oracle then sees the exact bf16 values of the chains it checks."""
+    gen = torch.Generator(device=device)
+    gen.manual_seed(seed)
+
+    def l2n(x):
+        return x / (x.norm(dim=-1, keepdim=True) + 1e-12)
+
+    q = l2n(torch.randn(B, T, H, dk, device=device, generator=gen)).to(torch.bfloat16)
+    k = l2n(torch.randn(B, T, H, dk, device=device, generator=gen)).to(torch.bfloat16)
+    v = torch.randn(B, T, H, dv, device=device, generator=gen).to(torch.bfloat16)
+    beta = torch.sigmoid(torch.randn(B, T, H, device=device, generator=gen)).to(torch.bfloat16)
+    gz = torch.randn(B, T, H, dk, device=device, generator=gen)
+    a = torch.rand(H, device=device, generator=gen) * -2.0
+    g = (-torch.nn.functional.softplus(gz) * torch.exp(a)[None, None, :, None]).to(torch.bfloat16)
+    out = dict(q=q, k=k, v=v, g=g, beta=beta)
+    if h0_std > 0.0:
+        n = B if n_states is None else n_states
+        out["h0"] = torch.randn(n, H, dk, dv, device=device, generator=gen) * h0_std
+    return out
+
+
+def host_chains(d, b, heads, t0=0, t1=None):
+    """float32 numpy copies of batch row b, tokens [t0, t1), the given heads."""
+    sl = slice(t0, t1)
+    res = {}
+    for n in ("q", "k", "v", "g"):
+        res[n] = d[n][b:b + 1, sl][:, :, heads].float().cpu().numpy()
+    res["beta"] = d["beta"][b:b + 1, sl][:, :, heads].float().cpu().numpy()
+    return res

@@ -1,0 +1,120 @@
+"""GPU parity at the full sizes of the benchmark configurations.
+
+The fp64 oracle cannot run these sizes whole, so each test combines
+* exact oracle checks on a sample of chains (heads and sequences are
+  independent chains, so a sample is checked at its full length), and
+* size-independent properties checked on everything: splitting a sequence and
+  carrying the final state across gives the same result bit for bit; a packed
+  varlen run equals the per-sequence runs bit for bit; no non-finite values.
+
+Config 1: B4 T4096 H16 d128; config 2: B1 T65536 H16 d128 (1024 serial
+chunks per chain); config 3: 64 sequences of U[128, 8192] tokens packed with
+cu_seqlens, H16 d128, per-sequence h0 ~ N(0, 0.02^2); config 4: decode B256
+H16 d128 with the fp32 state updated in place for 128 steps.
+"""
+
+from __future__ import annotations
+
+import numpy as np
+import pytest
+import torch
+
+from oracle import inputs, kda_oracle as K
+from tests.kda_testutil import TOL, assert_close, host_chains, make_inputs_device
+
+pytestmark = pytest.mark.gpu
+
+
+def _fwd(d, h0=None, cu=None):
+    import axiom_amd
+    o, ht = axiom_amd.kda_chunk_fwd(d["q"], d["k"], d["v"], d["g"], d["beta"], initial_state=h0,
+                                    cu_seqlens=cu)
+    torch.cuda.synchronize()
+    return o, ht
+
+
+def _slice(d, t0, t1):
+    return {n: d[n][:, t0:t1].contiguous() for n in ("q", "k", "v", "g", "beta")}
+
+
+def test_config1_full(cuda):
+    B, T, H, dd = 4, 4096, 16, 128
+    d = make_inputs_device(B, T, H, dd, dd, seed=101, device=cuda)
+    print("[full] config 1 forward", flush=True)
+    o, ht = _fwd(d)
+    assert torch.isfinite(o).all() and torch.isfinite(ht).all()
+    for b, heads in ((0, [0, 7]), (3, [15])):
+        hc = host_chains(d, b, heads)
+        o_ref, ht_ref = K.chunk_fwd(hc["q"], hc["k"], hc["v"], hc["g"], hc["beta"], chunk=64)
+        assert_close(f"o[b={b}]", o[b:b + 1][:, :, heads], o_ref, TOL["bf16"])
+        assert_close(f"ht[b={b}]", ht[b:b + 1][:, heads], ht_ref, TOL["bf16"])
+
+
+def test_config2_full(cuda):
+    B, T, H, dd = 1, 65536, 16, 128
+    d = make_inputs_device(B, T, H, dd, dd, seed=102, device=cuda)
+    print("[full] config 2 forward", flush=True)
+    o, ht = _fwd(d)
+    assert torch.isfinite(o).all() and torch.isfinite(ht).all()
+    heads = [0, 9]
+    hc = host_chains(d, 0, heads)
+    o_ref, ht_ref = K.chunk_fwd(hc["q"], hc["k"], hc["v"], hc["g"], hc["beta"], chunk=64)
+    assert_close("o", o[:, :, heads], o_ref, TOL["bf16"])
+    assert_close("ht", ht[:, heads], ht_ref, TOL["bf16"])
+    # state carry: [0, T/2) then [T/2, T) from its final state == the whole run
+    half = T // 2
+    o1, ht1 = _fwd(_slice(d, 0, half))
+    o2, ht2 = _fwd(_slice(d, half, T), h0=ht1)
+    assert torch.equal(o1, o[:, :half]) and torch.equal(o2, o[:, half:])
+    assert torch.equal(ht2, ht)
+
+
+def test_config3_varlen_full(cuda):
+    H, dd = 16, 128
+    lengths = inputs.make_varlen_lengths(64, 128, 8192, seed=3)
+    cu = inputs.cu_seqlens_from_lengths(lengths)
+    T = int(cu[-1])
+    d = make_inputs_device(1, T, H, dd, dd, seed=103, device=cuda, h0_std=0.02, n_states=len(lengths))
+    cu_t = torch.from_numpy(cu).to(cuda)
+    print(f"[full] config 3 varlen forward T={T}", flush=True)
+    o, ht = _fwd(d, h0=d["h0"], cu=cu_t)
+    assert torch.isfinite(o).all() and torch.isfinite(ht).all()
+    order = np.argsort(lengths)
+    picks = sorted({int(order[0]), int(order[-1]), 0, len(lengths) - 1})
+    for i in picks:
+        a, b = int(cu[i]), int(cu[i + 1])
+        oi, hi = _fwd(_slice(d, a, b), h0=d["h0"][i:i + 1].contiguous())
+        assert torch.equal(oi, o[:, a:b]), f"sequence {i}: packed o differs from its own run"
+        assert torch.equal(hi[0], ht[i]), f"sequence {i}: packed state differs from its own run"
+    for i in (int(order[0]), int(order[-1])):
+        a, b = int(cu[i]), int(cu[i + 1])
+        heads = [2, 13]
+        hc = host_chains(d, 0, heads, a, b)
+        h0 = d["h0"][i:i + 1][:, heads].cpu().numpy()
+        o_ref, ht_ref = K.chunk_fwd(hc["q"], hc["k"], hc["v"], hc["g"], hc["beta"], h0=h0, chunk=64)
+        assert_close(f"o[seq {i}]", o[:, a:b][:, :, heads], o_ref, TOL["bf16"])
+        assert_close(f"ht[seq {i}]", ht[i:i + 1][:, heads], ht_ref, TOL["bf16"])
+
+
+def test_config4_decode_full(cuda):
+    import axiom_amd
+    B, H, dd, steps = 256, 16, 128, 128
+    d = make_inputs_device(steps, B, H, dd, dd, seed=104, device=cuda)   # [steps, B, H, d]
+    gen = torch.Generator(device=cuda)
+    gen.manual_seed(105)
+    S = torch.randn(B, H, dd, dd, device=cuda, generator=gen) * 0.02
+    pick = [(0, 0), (17, 5), (255, 15)]
+    S0 = np.stack([S[b, h].cpu().numpy() for b, h in pick])          # [n, d, d]
+    print("[full] config 4 decode", flush=True)
+    outs = []
+    for t in range(steps):
+        outs.append(axiom_amd.kda_recurrent_step(d["q"][t], d["k"][t], d["v"][t], d["g"][t], d["beta"][t], S))
+    torch.cuda.synchronize()
+    assert torch.isfinite(S).all()
+    bs = [b for b, _ in pick]
+    hs = [h for _, h in pick]
+    sub = {n: d[n][:, bs, hs].float().cpu().numpy()[:, :, None] for n in ("q", "k", "v", "g", "beta")}
+    o_ref, S_ref = K.decode_steps(sub["q"], sub["k"], sub["v"], sub["g"], sub["beta"], S0[:, None])
+    o_got = torch.stack([o[bs, hs] for o in outs]).cpu().numpy()[:, :, None]
+    assert_close("o", o_got, o_ref, (1e-5, 1e-5))
+    assert_close("S", torch.stack([S[b, h] for b, h in pick]).cpu().numpy()[:, None], S_ref, (1e-5, 1e-5))
