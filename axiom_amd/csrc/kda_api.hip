@@ -253,7 +253,7 @@ int kda_recurrent_step(hipStream_t stream, const void* q, const void* k, const v
     return fail(KDA_ERR_INVALID_ARGUMENT, "out_dtype=%d: o is emitted as F32 or BF16", out_dtype);
   if (!std::isfinite(scale)) return fail(KDA_ERR_INVALID_ARGUMENT, "scale must be finite");
   const int64_t grid = static_cast<int64_t>(B) * H;
-  if (grid > 0x7FFFFFFFLL) return fail(KDA_ERR_INVALID_ARGUMENT, "B*H too large");
+  if (grid > 0x3FFFFFFFLL) return fail(KDA_ERR_INVALID_ARGUMENT, "B*H too large");
   kda::DecodeArgs a{};
   a.q = q; a.k = k; a.v = v; a.g = g; a.beta = beta;
   a.state = state; a.o = o; a.scale = scale;

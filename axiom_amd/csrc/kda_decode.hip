@@ -6,19 +6,26 @@
 // with o computed as  S~^T q + beta (v - u) (k . q)  so S is read once and
 // written once (in place).
 //
-// One workgroup of 256 threads per (b, h).  Thread t owns value columns
-// 4*(t & 31) .. +3 and channel rows (t >> 5) + 8*i; the column partial sums of
-// u = S~^T k and w = S~^T q are reduced across the 8 row groups through LDS.
+// Two workgroups of 256 threads per (b, h), each owning half of the value
+// columns for all channels (the column sums u = S~^T k and w = S~^T q need no
+// data from the other half; q, k, alpha are read by both).  Thread t owns
+// columns 4*(t % NCQ) .. +3 of its half and channel rows t / NCQ + RG*i; the
+// column partial sums are reduced across the RG row groups through LDS.
+// Half-width workgroups keep the state slice in 32 registers per thread, so
+// more workgroups are resident per CU.
 
 #include "kda_common.h"
 #include "kda_internal.h"
 
 namespace kda {
 
+constexpr int kDecodeColSplit = 2;
+
 template <int DK, int DV, int DT, int OUT_DT>
 __global__ __launch_bounds__(256)
 void kda_decode_kernel(DecodeArgs a) {
-  constexpr int NCQ = DV / 4;            // float4 column groups per row
+  constexpr int DVW = DV / kDecodeColSplit;  // value columns of this workgroup
+  constexpr int NCQ = DVW / 4;           // float4 column groups per row
   constexpr int RG = 256 / NCQ;          // row groups
   constexpr int RPT = DK / RG;           // rows per thread
   static_assert(256 % NCQ == 0 && DK % RG == 0, "decode tiling");
@@ -27,7 +34,8 @@ void kda_decode_kernel(DecodeArgs a) {
   __shared__ float kq_s;
 
   const int tid = threadIdx.x;
-  const int bh = blockIdx.x;             // b * H + h
+  const int bh = blockIdx.x / kDecodeColSplit;   // b * H + h
+  const int c0 = (blockIdx.x % kDecodeColSplit) * DVW;
   const int64_t vec = static_cast<int64_t>(bh);
   // The small per-token loads (q, k, g, beta, v) are issued first and the
   // state read right after: memory operations retire in order, so waiting on
@@ -42,9 +50,9 @@ void kda_decode_kernel(DecodeArgs a) {
   const int cq = tid % NCQ;
   const int rg = tid / NCQ;
   const float beta = ld1<DT>(a.beta, vec);
-  const f4 vv = ld4<DT>(a.v, vec * DV + 4 * cq);
+  const f4 vv = ld4<DT>(a.v, vec * DV + c0 + 4 * cq);
   __builtin_amdgcn_sched_barrier(0);  // keep the small loads ahead of the state read
-  float* S = a.state + static_cast<int64_t>(bh) * DK * DV;
+  float* S = a.state + static_cast<int64_t>(bh) * DK * DV + c0;
   f4 sv[RPT];
 #pragma unroll
   for (int i = 0; i < RPT; ++i) {
@@ -90,7 +98,7 @@ void kda_decode_kernel(DecodeArgs a) {
   }
   if (rg == 0) {
     const f4 o = ww + kq * delta;
-    const int64_t oi = vec * DV + 4 * cq;
+    const int64_t oi = vec * DV + c0 + 4 * cq;
     if constexpr (OUT_DT == 0) {
       *reinterpret_cast<f4*>(static_cast<float*>(a.o) + oi) = o;
     } else {
@@ -104,7 +112,7 @@ void kda_decode_kernel(DecodeArgs a) {
 
 template <int D, int DT, int OUT>
 static hipError_t launch_decode_t(const DecodeArgs& a, int grid, hipStream_t s) {
-  hipLaunchKernelGGL((kda_decode_kernel<D, D, DT, OUT>), dim3(grid), dim3(256), 0, s, a);
+  hipLaunchKernelGGL((kda_decode_kernel<D, D, DT, OUT>), dim3(grid * kDecodeColSplit), dim3(256), 0, s, a);
   return hipGetLastError();
 }
 
