@@ -35,6 +35,8 @@
 //    prefetching three chunks ahead, and emits o and the final state.
 // Exact mode (fp32 inputs) runs the same code with fp32 operands.
 
+#include <type_traits>
+
 #include "kda_common.h"
 #include "kda_internal.h"
 
@@ -952,6 +954,16 @@ __device__ __forceinline__ void col_producer(const StateArgs& a, ColSmem<DK>& sm
                                 min(kC, c.seq_len - nl * kC), h, split, l);
 }
 
+// Calls f(std::integral_constant<int, I>{}) for I = B .. E-1, expanded at
+// compile time (a loop over a long, branchy body is not always unrolled).
+template <int B, int E, typename F>
+__device__ __forceinline__ void static_for(F&& f) {
+  if constexpr (B < E) {
+    f(std::integral_constant<int, B>{});
+    static_for<B + 1, E>(f);
+  }
+}
+
 __device__ __forceinline__ h8 lds_frag(const unsigned char* buf, int f, int l) {
   return *reinterpret_cast<const h8*>(buf + f * 1024 + l * 16);
 }
@@ -1000,32 +1012,39 @@ __device__ __forceinline__ void col_chain(const StateArgs& a, ColSmem<DK>& sm, i
     for (int ct = 0; ct < 4; ++ct)
       Ucur[ct] = *reinterpret_cast<const h4*>(cur + LY::OFF_U + (2 * ct + W) * 512 + l * 8);
 
-    // The step is a fixed sequence of MFMA groups; each group's A fragments
-    // are read from LDS two groups ahead into a 3-slot register ring, and a
-    // scheduling barrier keeps the reads there.  Groups: 2ct = W rows of tile
-    // ct (P), 2ct+1 = gamma*q rows (O), 8 = Aqk, 9 + dt = lambda*k of channel
-    // tile dt with gamma_C.
-    constexpr int NG = 9 + NT;
-    h8 Rf[3][6];
-    f4 Rg[3];
-    auto load_group = [&](int g) {
-      const int sl = g % 3;
-      if (g < 8) {
-        const int base = ((g & 1) ? LY::OFF_Q : 0) + (g >> 1) * NJ;
-#pragma unroll
-        for (int j = 0; j < NJ; ++j) Rf[sl][j] = lds_frag(cur, base + j, l);
-      } else if (g == 8) {
-#pragma unroll
-        for (int f = 0; f < LY::FA; ++f) Rf[sl][f] = lds_frag(cur, LY::OFF_A + f, l);
+    // The step is one stream of 16-byte LDS reads consumed in order:
+    //   items 0 .. 8*NJ-1    W and gamma*q fragments of row tile ct = i / (2*NJ)
+    //                        (alternating: P and O products of K step j),
+    //   next FA items        Aqk fragments,
+    //   next NT items        gamma_C of channel tile dt (one float4 per lane),
+    //   last 2*NT items      lambda*k fragments of channel tile dt, K steps 0, 1.
+    // Each read is issued DEPTH items ahead of its use into a register ring,
+    // so up to DEPTH reads are in flight at every wait (the lgkm counter
+    // tracks 15), and a scheduling barrier per item keeps that order.
+    constexpr int N_ROW = 8 * NJ;
+    constexpr int I_AQ = N_ROW;
+    constexpr int I_GC = I_AQ + LY::FA;
+    constexpr int I_LK = I_GC + NT;
+    constexpr int NIT = I_LK + 2 * NT;
+    constexpr int DEPTH = 12;
+    constexpr int RING = DEPTH + 1;
+    auto item_read = [&](auto ic) -> uint4 {
+      constexpr int i = decltype(ic)::value;
+      const unsigned char* p;
+      if constexpr (i < N_ROW) {
+        constexpr int ct = i / (2 * NJ), j = (i % (2 * NJ)) >> 1;
+        p = cur + (((i & 1) ? LY::OFF_Q : 0) + ct * NJ + j) * 1024 + l * 16;
+      } else if constexpr (i < I_GC) {
+        p = cur + (LY::OFF_A + (i - I_AQ)) * 1024 + l * 16;
+      } else if constexpr (i < I_LK) {
+        p = cur + LY::OFF_G + (16 * (i - I_GC) + 4 * gq) * 4;
       } else {
-        const int dt = g - 9;
-        Rf[sl][0] = lds_frag(cur, LY::OFF_L + 2 * dt, l);
-        Rf[sl][1] = lds_frag(cur, LY::OFF_L + 2 * dt + 1, l);
-        Rg[sl] = *reinterpret_cast<const f4*>(cur + LY::OFF_G + (16 * dt + 4 * gq) * 4);
+        p = cur + (LY::OFF_L + (i - I_LK)) * 1024 + l * 16;
       }
+      return *reinterpret_cast<const uint4*>(p);
     };
-    load_group(0);
-    load_group(1);
+    uint4 ring[RING];
+    static_for<0, DEPTH>([&](auto ic) { ring[decltype(ic)::value % RING] = item_read(ic); });
     // S as B fragments over channels
     h8 Sb[NJ];
 #pragma unroll
@@ -1035,49 +1054,49 @@ __device__ __forceinline__ void col_chain(const StateArgs& a, ColSmem<DK>& sm, i
         Sb[j][i] = static_cast<_Float16>(S[2 * j][i]);
         Sb[j][4 + i] = static_cast<_Float16>(S[2 * j + 1][i]);
       }
-    f4 O[4], Vt[4];
+    f4 O[4], P[4], Vt[4], Gc[NT];
     h8 Vb[2];
 #pragma unroll
-    for (int g = 0; g < NG; ++g) {
-      if (g + 2 < NG) load_group(g + 2);
+    for (int ct = 0; ct < 4; ++ct) { P[ct] = f4{0, 0, 0, 0}; O[ct] = f4{0, 0, 0, 0}; }
+    static_for<0, NIT>([&](auto ic) {
+      constexpr int i = decltype(ic)::value;
+      if constexpr (i + DEPTH < NIT) ring[(i + DEPTH) % RING] = item_read(std::integral_constant<int, i + DEPTH>{});
       __builtin_amdgcn_sched_barrier(0);
-      const int sl = g % 3;
-      if (g < 8) {
-        // P = W S (then v~ = U - P) or O = (gamma q) S for row tile ct
-        const int ct = g >> 1;
-        f4 acc = {0, 0, 0, 0};
+      const uint4 it = ring[i % RING];
+      if constexpr (i < N_ROW) {
+        // P = W S and O = (gamma q) S, row tile ct; v~ = U - P once P is complete
+        constexpr int ct = i / (2 * NJ), j = (i % (2 * NJ)) >> 1;
+        const h8 A = __builtin_bit_cast(h8, it);
+        if constexpr (i & 1) O[ct] = mma32(O[ct], A, Sb[j]);
+        else P[ct] = mma32(P[ct], A, Sb[j]);
+        if constexpr (i % (2 * NJ) == 2 * NJ - 1) {
 #pragma unroll
-        for (int j = 0; j < NJ; ++j) acc = mma32(acc, Rf[sl][j], Sb[j]);
-        if ((g & 1) == 0) {
-#pragma unroll
-          for (int i = 0; i < 4; ++i) Vt[ct][i] = static_cast<float>(Ucur[ct][i]) - acc[i];
-        } else {
-          O[ct] = acc;
+          for (int e = 0; e < 4; ++e) Vt[ct][e] = static_cast<float>(Ucur[ct][e]) - P[ct][e];
         }
-      } else if (g == 8) {
-        // v~ as B fragments over keys; O += Aqk v~ (keys at or before the row tile)
+      } else if constexpr (i < I_GC) {
+        // O += Aqk v~ (keys at or before the row tile); fragments (ct,jj) = 00 10 20 21 30 31
+        constexpr int f = i - I_AQ;
+        if constexpr (f == 0) {
 #pragma unroll
-        for (int jj = 0; jj < 2; ++jj)
+          for (int jj = 0; jj < 2; ++jj)
 #pragma unroll
-          for (int i = 0; i < 4; ++i) {
-            Vb[jj][i] = static_cast<_Float16>(Vt[2 * jj][i]);
-            Vb[jj][4 + i] = static_cast<_Float16>(Vt[2 * jj + 1][i]);
-          }
-        O[0] = mma32(O[0], Rf[sl][0], Vb[0]);
-        O[1] = mma32(O[1], Rf[sl][1], Vb[0]);
-        O[2] = mma32(O[2], Rf[sl][2], Vb[0]);
-        O[2] = mma32(O[2], Rf[sl][3], Vb[1]);
-        O[3] = mma32(O[3], Rf[sl][4], Vb[0]);
-        O[3] = mma32(O[3], Rf[sl][5], Vb[1]);
+            for (int e = 0; e < 4; ++e) {
+              Vb[jj][e] = static_cast<_Float16>(Vt[2 * jj][e]);
+              Vb[jj][4 + e] = static_cast<_Float16>(Vt[2 * jj + 1][e]);
+            }
+        }
+        constexpr int ct = (f < 2) ? f : 2 + ((f - 2) >> 1);
+        constexpr int jj = (f < 2) ? 0 : ((f - 2) & 1);
+        O[ct] = mma32(O[ct], __builtin_bit_cast(h8, it), Vb[jj]);
+      } else if constexpr (i < I_LK) {
+        Gc[i - I_GC] = __builtin_bit_cast(f4, it);
       } else {
         // S <- gamma_C S + (lambda k)^T v~ for channel tile dt
-        const int dt = g - 9;
-        f4 sv = S[dt] * Rg[sl];
-        sv = mma32(sv, Rf[sl][0], Vb[0]);
-        sv = mma32(sv, Rf[sl][1], Vb[1]);
-        S[dt] = sv;
+        constexpr int dt = (i - I_LK) >> 1, jj = (i - I_LK) & 1;
+        if constexpr (jj == 0) S[dt] = S[dt] * Gc[dt];
+        S[dt] = mma32(S[dt], __builtin_bit_cast(h8, it), Vb[jj]);
       }
-    }
+    });
 
     col_put_o<OUT_DT, W>(sm.obuf[n & 1], O, r, gq);
     // the producers have landed the next buffer and may store these o rows;
