@@ -839,6 +839,12 @@ struct ColSmem {
 // on this part (measured); four together move the 56 KiB a chunk needs in
 // well under a chunk's compute time.
 constexpr int kColProducers = 4;
+// Compute waves per state workgroup; each owns 2 / kColComputeWaves of the
+// workgroup's two 16-column value tiles.  (One wave owning both reads every
+// shared fragment once and feeds two MFMAs; measured slower: its MFMA time
+// per chunk doubles.)
+constexpr int kColComputeWaves = 2;
+constexpr int kColTilesPerWave = 2 / kColComputeWaves;
 
 // Copy producer P's share of the operands of chunk-head ch into an LDS buffer
 // (fragment-ordered 1 KiB blocks: lane l moves bytes 16l..16l+15): every
@@ -969,16 +975,16 @@ __device__ __forceinline__ h8 lds_frag(const unsigned char* buf, int f, int l) {
 }
 
 // o of row tiles 0..3 (D layout: rows 16ct + 4gq + i, column r of value tile
-// W) into the LDS o rows of the workgroup's 32 columns.
-template <int OUT_DT, int W>
-__device__ __forceinline__ void col_put_o(unsigned char* ob, const f4 (&O)[4], int r, int gq) {
+// `tile` of the workgroup) into the LDS o rows of the workgroup's 32 columns.
+template <int OUT_DT>
+__device__ __forceinline__ void col_put_o(unsigned char* ob, const f4 (&O)[4], int tile, int r, int gq) {
 #pragma unroll
   for (int ct = 0; ct < 4; ++ct)
 #pragma unroll
     for (int i = 0; i < 4; ++i) {
       const int row = 16 * ct + 4 * gq + i;
-      if constexpr (OUT_DT == 0) reinterpret_cast<float*>(ob)[row * 32 + 16 * W + r] = O[ct][i];
-      else reinterpret_cast<u16*>(ob)[row * 32 + 16 * W + r] = f32_to_bf16_bits(O[ct][i]);
+      if constexpr (OUT_DT == 0) reinterpret_cast<float*>(ob)[row * 32 + 16 * tile + r] = O[ct][i];
+      else reinterpret_cast<u16*>(ob)[row * 32 + 16 * tile + r] = f32_to_bf16_bits(O[ct][i]);
     }
 }
 
@@ -987,32 +993,39 @@ __device__ __forceinline__ void col_chain(const StateArgs& a, ColSmem<DK>& sm, i
   typedef ColLayout<DK> LY;
   constexpr int NJ = DK / 32;
   constexpr int NT = DK / 16;
+  constexpr int NC = kColTilesPerWave;
   const Geom& G = a.geom;
   const int H = G.H;
   const int l = threadIdx.x & 63, r = l & 15, gq = l >> 4;
-  const int et = 2 * split + W;
+  const int tile0 = W * NC;                 // first value tile of this wave inside the workgroup
   const ChainRef c = chain_ref(G, seq);
   const int nchunks = c.nchunks;
 
-  f4 S[NT];
+  f4 S[NC][NT];
   const int64_t sbase = (static_cast<int64_t>(seq) * H + h) * DK * DV;
 #pragma unroll
-  for (int dt = 0; dt < NT; ++dt)
+  for (int cc = 0; cc < NC; ++cc)
 #pragma unroll
-    for (int i = 0; i < 4; ++i)
-      S[dt][i] = (a.h0 != nullptr)
-                     ? a.h0[sbase + static_cast<int64_t>(16 * dt + 4 * gq + i) * DV + 16 * et + r]
-                     : 0.f;
+    for (int dt = 0; dt < NT; ++dt)
+#pragma unroll
+      for (int i = 0; i < 4; ++i)
+        S[cc][dt][i] = (a.h0 != nullptr)
+                           ? a.h0[sbase + static_cast<int64_t>(16 * dt + 4 * gq + i) * DV +
+                                  16 * (2 * split + tile0 + cc) + r]
+                           : 0.f;
 
   if (nchunks > 0) lds_barrier();  // chunk 0 staged by the producer waves
   for (int n = 0; n < nchunks; ++n) {
     const unsigned char* cur = sm.buf[n & 1];
-    h4 Ucur[4];
+    h4 Ucur[NC][4];
 #pragma unroll
-    for (int ct = 0; ct < 4; ++ct)
-      Ucur[ct] = *reinterpret_cast<const h4*>(cur + LY::OFF_U + (2 * ct + W) * 512 + l * 8);
+    for (int cc = 0; cc < NC; ++cc)
+#pragma unroll
+      for (int ct = 0; ct < 4; ++ct)
+        Ucur[cc][ct] = *reinterpret_cast<const h4*>(cur + LY::OFF_U + (2 * ct + tile0 + cc) * 512 + l * 8);
 
-    // The step is one stream of 16-byte LDS reads consumed in order:
+    // The step is one stream of 16-byte LDS reads consumed in order (each
+    // fragment feeds one MFMA per value tile of this wave):
     //   items 0 .. 8*NJ-1    W and gamma*q fragments of row tile ct = i / (2*NJ)
     //                        (alternating: P and O products of K step j),
     //   next FA items        Aqk fragments,
@@ -1046,18 +1059,22 @@ __device__ __forceinline__ void col_chain(const StateArgs& a, ColSmem<DK>& sm, i
     uint4 ring[RING];
     static_for<0, DEPTH>([&](auto ic) { ring[decltype(ic)::value % RING] = item_read(ic); });
     // S as B fragments over channels
-    h8 Sb[NJ];
+    h8 Sb[NC][NJ];
 #pragma unroll
-    for (int j = 0; j < NJ; ++j)
+    for (int cc = 0; cc < NC; ++cc)
 #pragma unroll
-      for (int i = 0; i < 4; ++i) {
-        Sb[j][i] = static_cast<_Float16>(S[2 * j][i]);
-        Sb[j][4 + i] = static_cast<_Float16>(S[2 * j + 1][i]);
-      }
-    f4 O[4], P[4], Vt[4], Gc[NT];
-    h8 Vb[2];
+      for (int j = 0; j < NJ; ++j)
 #pragma unroll
-    for (int ct = 0; ct < 4; ++ct) { P[ct] = f4{0, 0, 0, 0}; O[ct] = f4{0, 0, 0, 0}; }
+        for (int i = 0; i < 4; ++i) {
+          Sb[cc][j][i] = static_cast<_Float16>(S[cc][2 * j][i]);
+          Sb[cc][j][4 + i] = static_cast<_Float16>(S[cc][2 * j + 1][i]);
+        }
+    f4 O[NC][4], P[NC][4], Vt[NC][4], Gc[NT];
+    h8 Vb[NC][2];
+#pragma unroll
+    for (int cc = 0; cc < NC; ++cc)
+#pragma unroll
+      for (int ct = 0; ct < 4; ++ct) { P[cc][ct] = f4{0, 0, 0, 0}; O[cc][ct] = f4{0, 0, 0, 0}; }
     static_for<0, NIT>([&](auto ic) {
       constexpr int i = decltype(ic)::value;
       if constexpr (i + DEPTH < NIT) ring[(i + DEPTH) % RING] = item_read(std::integral_constant<int, i + DEPTH>{});
@@ -1067,54 +1084,71 @@ __device__ __forceinline__ void col_chain(const StateArgs& a, ColSmem<DK>& sm, i
         // P = W S and O = (gamma q) S, row tile ct; v~ = U - P once P is complete
         constexpr int ct = i / (2 * NJ), j = (i % (2 * NJ)) >> 1;
         const h8 A = __builtin_bit_cast(h8, it);
-        if constexpr (i & 1) O[ct] = mma32(O[ct], A, Sb[j]);
-        else P[ct] = mma32(P[ct], A, Sb[j]);
+#pragma unroll
+        for (int cc = 0; cc < NC; ++cc) {
+          if constexpr (i & 1) O[cc][ct] = mma32(O[cc][ct], A, Sb[cc][j]);
+          else P[cc][ct] = mma32(P[cc][ct], A, Sb[cc][j]);
+        }
         if constexpr (i % (2 * NJ) == 2 * NJ - 1) {
 #pragma unroll
-          for (int e = 0; e < 4; ++e) Vt[ct][e] = static_cast<float>(Ucur[ct][e]) - P[ct][e];
+          for (int cc = 0; cc < NC; ++cc)
+#pragma unroll
+            for (int e = 0; e < 4; ++e) Vt[cc][ct][e] = static_cast<float>(Ucur[cc][ct][e]) - P[cc][ct][e];
         }
       } else if constexpr (i < I_GC) {
         // O += Aqk v~ (keys at or before the row tile); fragments (ct,jj) = 00 10 20 21 30 31
         constexpr int f = i - I_AQ;
         if constexpr (f == 0) {
 #pragma unroll
-          for (int jj = 0; jj < 2; ++jj)
+          for (int cc = 0; cc < NC; ++cc)
 #pragma unroll
-            for (int e = 0; e < 4; ++e) {
-              Vb[jj][e] = static_cast<_Float16>(Vt[2 * jj][e]);
-              Vb[jj][4 + e] = static_cast<_Float16>(Vt[2 * jj + 1][e]);
-            }
+            for (int jj = 0; jj < 2; ++jj)
+#pragma unroll
+              for (int e = 0; e < 4; ++e) {
+                Vb[cc][jj][e] = static_cast<_Float16>(Vt[cc][2 * jj][e]);
+                Vb[cc][jj][4 + e] = static_cast<_Float16>(Vt[cc][2 * jj + 1][e]);
+              }
         }
         constexpr int ct = (f < 2) ? f : 2 + ((f - 2) >> 1);
         constexpr int jj = (f < 2) ? 0 : ((f - 2) & 1);
-        O[ct] = mma32(O[ct], __builtin_bit_cast(h8, it), Vb[jj]);
+        const h8 A = __builtin_bit_cast(h8, it);
+#pragma unroll
+        for (int cc = 0; cc < NC; ++cc) O[cc][ct] = mma32(O[cc][ct], A, Vb[cc][jj]);
       } else if constexpr (i < I_LK) {
         Gc[i - I_GC] = __builtin_bit_cast(f4, it);
       } else {
         // S <- gamma_C S + (lambda k)^T v~ for channel tile dt
         constexpr int dt = (i - I_LK) >> 1, jj = (i - I_LK) & 1;
-        if constexpr (jj == 0) S[dt] = S[dt] * Gc[dt];
-        S[dt] = mma32(S[dt], __builtin_bit_cast(h8, it), Vb[jj]);
+        const h8 A = __builtin_bit_cast(h8, it);
+#pragma unroll
+        for (int cc = 0; cc < NC; ++cc) {
+          if constexpr (jj == 0) S[cc][dt] = S[cc][dt] * Gc[dt];
+          S[cc][dt] = mma32(S[cc][dt], A, Vb[cc][jj]);
+        }
       }
     });
 
-    col_put_o<OUT_DT, W>(sm.obuf[n & 1], O, r, gq);
+#pragma unroll
+    for (int cc = 0; cc < NC; ++cc) col_put_o<OUT_DT>(sm.obuf[n & 1], O[cc], tile0 + cc, r, gq);
     // the producers have landed the next buffer and may store these o rows;
-    // both compute waves are done with this buffer before it is refilled
+    // the compute waves are done with this buffer before it is refilled
     lds_barrier();
   }
 
   if (a.ht != nullptr) {
 #pragma unroll
-    for (int dt = 0; dt < NT; ++dt)
+    for (int cc = 0; cc < NC; ++cc)
 #pragma unroll
-      for (int i = 0; i < 4; ++i)
-        a.ht[sbase + static_cast<int64_t>(16 * dt + 4 * gq + i) * DV + 16 * et + r] = S[dt][i];
+      for (int dt = 0; dt < NT; ++dt)
+#pragma unroll
+        for (int i = 0; i < 4; ++i)
+          a.ht[sbase + static_cast<int64_t>(16 * dt + 4 * gq + i) * DV + 16 * (2 * split + tile0 + cc) + r] =
+              S[cc][dt][i];
   }
 }
 
 template <int DK, int DV, int OUT_DT>
-__global__ __launch_bounds__(64 * (2 + kColProducers), 1)
+__global__ __launch_bounds__(64 * (kColComputeWaves + kColProducers), 1)
 void kda_state_col_kernel(StateArgs a) {
   constexpr int SPLITS = DV / 32;
   __shared__ ColSmem<DK> sm;
@@ -1131,13 +1165,18 @@ void kda_state_col_kernel(StateArgs a) {
   const int seq_rank = chain / H;
   const int h = chain - seq_rank * H;
   const int seq = (G.order != nullptr) ? G.order[seq_rank] : seq_rank;
-  switch (threadIdx.x >> 6) {
-    case 0: col_chain<DK, DV, OUT_DT, 0>(a, sm, seq, h, split); break;
-    case 1: col_chain<DK, DV, OUT_DT, 1>(a, sm, seq, h, split); break;
-    case 2: col_producer<DK, DV, OUT_DT, 0>(a, sm, seq, h, split); break;
-    case 3: col_producer<DK, DV, OUT_DT, 1>(a, sm, seq, h, split); break;
-    case 4: col_producer<DK, DV, OUT_DT, 2>(a, sm, seq, h, split); break;
-    default: col_producer<DK, DV, OUT_DT, 3>(a, sm, seq, h, split); break;
+  const int wave = threadIdx.x >> 6;
+  if (wave < kColComputeWaves) {
+    if constexpr (kColComputeWaves == 1) col_chain<DK, DV, OUT_DT, 0>(a, sm, seq, h, split);
+    else if (wave == 0) col_chain<DK, DV, OUT_DT, 0>(a, sm, seq, h, split);
+    else col_chain<DK, DV, OUT_DT, 1>(a, sm, seq, h, split);
+  } else {
+    switch (wave - kColComputeWaves) {
+      case 0: col_producer<DK, DV, OUT_DT, 0>(a, sm, seq, h, split); break;
+      case 1: col_producer<DK, DV, OUT_DT, 1>(a, sm, seq, h, split); break;
+      case 2: col_producer<DK, DV, OUT_DT, 2>(a, sm, seq, h, split); break;
+      default: col_producer<DK, DV, OUT_DT, 3>(a, sm, seq, h, split); break;
+    }
   }
 }
 
@@ -1155,7 +1194,8 @@ static hipError_t launch_state_t(const StateArgs& a, int grid, hipStream_t s) {
   if constexpr (EXACT) {
     hipLaunchKernelGGL((kda_state_kernel<DK, DV, EXACT, OUT>), dim3(grid), dim3(256), 0, s, a);
   } else {
-    hipLaunchKernelGGL((kda_state_col_kernel<DK, DV, OUT>), dim3(grid), dim3(64 * (2 + kColProducers)), 0, s, a);
+    hipLaunchKernelGGL((kda_state_col_kernel<DK, DV, OUT>), dim3(grid), dim3(64 * (kColComputeWaves + kColProducers)), 0,
+                       s, a);
   }
   return hipGetLastError();
 }
