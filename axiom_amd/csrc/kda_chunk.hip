@@ -57,8 +57,9 @@ struct UnitRef {
 __device__ __forceinline__ UnitRef unit_ref(const Geom& G, int u) {
   UnitRef R;
   if (G.cu == nullptr) {
-    R.seq = u / G.NT;
-    R.n = u - R.seq * G.NT;
+    // dense: units are (sequence, chunk) of the segment [n0, n0 + NTS)
+    R.seq = u / G.NTS;
+    R.n = G.n0 + (u - R.seq * G.NTS);
     R.row0 = static_cast<int64_t>(R.seq) * G.T + static_cast<int64_t>(R.n) * kC;
     R.len = min(kC, G.T - R.n * kC);
   } else {
@@ -706,10 +707,10 @@ __device__ __forceinline__ void state_chain(const StateArgs& a, StateSmem<DK, DV
   int u0, nchunks, seq_len;
   int64_t tok0;
   if (G.cu == nullptr) {
-    u0 = seq * G.NT;
-    nchunks = G.NT;
-    tok0 = static_cast<int64_t>(seq) * G.T;
-    seq_len = G.T;
+    u0 = seq * G.NTS;
+    nchunks = G.NTS;
+    tok0 = static_cast<int64_t>(seq) * G.T + static_cast<int64_t>(G.n0) * kC;
+    seq_len = G.T - G.n0 * kC;
   } else {
     u0 = G.chunk_off[seq];
     nchunks = G.chunk_off[seq + 1] - u0;
@@ -917,10 +918,10 @@ struct ChainRef {
 __device__ __forceinline__ ChainRef chain_ref(const Geom& G, int seq) {
   ChainRef c;
   if (G.cu == nullptr) {
-    c.u0 = seq * G.NT;
-    c.nchunks = G.NT;
-    c.tok0 = static_cast<int64_t>(seq) * G.T;
-    c.seq_len = G.T;
+    c.u0 = seq * G.NTS;
+    c.nchunks = G.NTS;
+    c.tok0 = static_cast<int64_t>(seq) * G.T + static_cast<int64_t>(G.n0) * kC;
+    c.seq_len = G.T - G.n0 * kC;
   } else {
     c.u0 = G.chunk_off[seq];
     c.nchunks = G.chunk_off[seq + 1] - c.u0;

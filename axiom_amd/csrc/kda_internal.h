@@ -11,6 +11,8 @@ namespace kda {
 struct Geom {
   int B, T, H;
   int NT;                       // dense: chunks per sequence
+  int n0;                       // dense: first chunk of the segment this launch covers
+  int NTS;                      // dense: chunks in that segment (workspace units per sequence)
   int N;                        // number of sequences (dense: B)
   const int32_t* cu;            // original cu_seqlens (varlen) or null
   const int32_t* cu_clamped;    // validated copy (varlen)

@@ -33,12 +33,37 @@ def _align(x):
     return (x + 255) // 256 * 256
 
 
+SEGMENT_BUDGET = 100 * 1048576   # bytes of intra-chunk results per segment of a dense call
+
+
+def dense_segments(B, T, H, dk, dv, es):
+    NT = (T + C - 1) // C
+    if NT <= 1:
+        return 1, NT
+    total = B * NT * H * (C * (3 * dk + dv + C) * es + dk * 4)
+    s = min(max(-(-total // SEGMENT_BUDGET), 1), NT)
+    seg = -(-NT // s)
+    return -(-NT // seg), seg
+
+
 def dense_ws_bytes(B, T, H, dk, dv, es):
     """Dense workspace size: W, gamma*q, lambda*k [units*H][C][dk], U [..][C][dv],
-    Aqk [..][C][C] in operand precision, gamma_C [..][dk] fp32, each 256-B aligned."""
-    ch = B * ((T + C - 1) // C) * H
-    return sum(_align(n) for n in (ch * C * dk * es, ch * C * dk * es, ch * C * dk * es,
-                                   ch * C * dv * es, ch * C * C * es, ch * dk * 4))
+    Aqk [..][C][C] in operand precision, gamma_C [..][dk] fp32, each 256-B aligned,
+    for one segment's units; plus the carried state when the call is segmented."""
+    segments, seg = dense_segments(B, T, H, dk, dv, es)
+    ch = B * seg * H
+    arrays = [ch * C * dk * es, ch * C * dk * es, ch * C * dk * es, ch * C * dv * es, ch * C * C * es,
+              ch * dk * 4]
+    if segments > 1:
+        arrays.append(B * H * dk * dv * 4)
+    return sum(_align(n) for n in arrays)
+
+
+def test_segment_policy():
+    # config 1: 304 MB of intra-chunk results -> 3 segments of 22 chunks
+    assert dense_segments(4, 4096, 16, 128, 128, 2) == (3, 22)
+    assert dense_segments(2, 1000, 2, 128, 128, 2) == (1, 16)
+    assert dense_segments(1, 65536, 16, 128, 128, 2) == (12, 86)
 
 
 def varlen_ws_bytes(T, N, H, dk, dv, es):

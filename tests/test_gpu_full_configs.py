@@ -48,6 +48,14 @@ def test_config1_full(cuda):
         o_ref, ht_ref = K.chunk_fwd(hc["q"], hc["k"], hc["v"], hc["g"], hc["beta"], chunk=64)
         assert_close(f"o[b={b}]", o[b:b + 1][:, :, heads], o_ref, TOL["bf16"])
         assert_close(f"ht[b={b}]", ht[b:b + 1][:, heads], ht_ref, TOL["bf16"])
+    # The whole call runs in 3 segments of 22 chunks (its intra-chunk results
+    # exceed the per-segment budget); four calls of 16 chunks each run whole
+    # and carry the state between them: same result bit for bit.
+    h, outs = None, []
+    for t0 in range(0, T, 1024):
+        oi, h = _fwd(_slice(d, t0, t0 + 1024), h0=h)
+        outs.append(oi)
+    assert torch.equal(torch.cat(outs, dim=1), o) and torch.equal(h, ht)
 
 
 def test_config2_full(cuda):

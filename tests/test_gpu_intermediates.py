@@ -28,7 +28,8 @@ def _align(x):
 
 
 def ws_offsets(B, T, H, dk, dv, es):
-    """Mirror of the C ABI's dense workspace layout (kda_api.hip: ws_layout)."""
+    """Mirror of the C ABI's dense workspace layout (kda_api.hip: ws_layout) for a
+    call that runs in one segment (its intra-chunk results fit the segment budget)."""
     units = B * ((T + C - 1) // C)
     ch = units * H
     off, res = 0, {}
