@@ -151,13 +151,23 @@ __device__ __forceinline__ void intra_chunk(const IntraArgs& a, const UnitRef& U
   static_assert(DK == DV, "staging assumes dk == dv");
   unsigned char* const stg = reinterpret_cast<unsigned char*>(&sm);
   auto stg_row = [&](int t, int row) { return stg + (t * kC + row) * ROWB; };
+  // beta first: its latency hides behind the row copies.  Copy order g, k, q,
+  // v: with all four staged (SPLIT) the waits below are partial (vmcnt retires
+  // in issue order), so the decay scan runs while k, q and v are still
+  // arriving and the k/q decay factors while v is.
+  constexpr bool SPLIT = STQ && STG;
+  constexpr int NPER = 16 / RPI;        // copies per tensor per wave
+  // (unconditional load of a valid row, masked after the waits: a load
+  // inside a branch is waited for at the branch's end)
+  float beta_c = ld1<DTG>(a.beta, (U.row0 + min(c, U.len - 1)) * H + h);
   if constexpr (STQ || STG) {
 #pragma unroll
-    for (int t = 0; t < 4; ++t) {  // 0 q, 1 k, 2 g, 3 v
+    for (int oi = 0; oi < 4; ++oi) {
+      const int t = (oi == 0) ? 2 : (oi == 1) ? 1 : (oi == 2) ? 0 : 3;  // 0 q, 1 k, 2 g, 3 v
       if ((t == 2) ? !STG : !STQ) continue;
       const u16* src = static_cast<const u16*>(t == 0 ? a.q : t == 1 ? a.k : t == 2 ? a.g : a.v);
 #pragma unroll
-      for (int i = 0; i < 16 / RPI; ++i) {
+      for (int i = 0; i < NPER; ++i) {
         const int row = 16 * W + RPI * i + l / NCH;                 // chunk row this lane copies
         const int cidx = (l % NCH) ^ (row & (NCH - 1));             // source chunk of LDS chunk l % NCH
         const int64_t srow = U.row0 + min(row, U.len - 1);          // rows past the end re-read a valid row
@@ -166,62 +176,123 @@ __device__ __forceinline__ void intra_chunk(const IntraArgs& a, const UnitRef& U
         __builtin_amdgcn_global_load_lds(gsrc, ldst, 16, 0, 0);
       }
     }
-    wait_vmem_all();
-    __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "workgroup", "local");
+    if constexpr (!SPLIT) {
+      wait_vmem_all();
+      __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "workgroup", "local");
+    }
   }
-  // four channels ch0 = 32j + 16hf + 4gq .. +3 of this lane's row from staging
-  auto stg_read4 = [&](int t, int j, int hf) -> uint2 {
-    const int ci = 4 * j + 2 * hf + (gq >> 1);
-    const int pc = ci ^ (c & (NCH - 1));
-    return *reinterpret_cast<const uint2*>(stg_row(t, c) + pc * 16 + (gq & 1) * 8);
-  };
-
-  float kr[NJ][8], qr[NJ][8], kc[NJ][8], Gt[NJ][8];
-  float vr[NJV][8];
-  float beta_c = 0.f;
-  {
+  // four channels ch0 = 32j + 16hf + 4gq .. +3 of this lane's row from
+  // staging, all 2 NJ of them for tensor t (read untracked, then settled)
+  auto stg_read_all = [&](int t, uint2 (&w)[2 * NJ]) {
 #pragma unroll
-    for (int j = 0; j < NJ; ++j) {
+    for (int j = 0; j < NJ; ++j)
 #pragma unroll
       for (int hf = 0; hf < 2; ++hf) {
-        const int ch0 = 32 * j + 4 * gq + 16 * hf;
-        f4 x = {0, 0, 0, 0}, y = {0, 0, 0, 0}, z = {0, 0, 0, 0}, w = {0, 0, 0, 0};
-        if constexpr (STQ) {
-          x = unpack4<DTQ>(stg_read4(0, j, hf));
-          y = unpack4<DTQ>(stg_read4(1, j, hf));
-          w = unpack4<DTQ>(stg_read4(3, j, hf));
-        } else if (valid) {
-          x = ld4<DTQ>(a.q, bq + ch0);
-          y = ld4<DTQ>(a.k, bq + ch0);
-          w = ld4<DTQ>(a.v, (tok * H + h) * DV + ch0);
-        }
-        if constexpr (STG) z = unpack4<DTG>(stg_read4(2, j, hf));
-        else if (valid) z = ld4<DTG>(a.g, bq + ch0);
-        // Rows past the chunk's end (staged copies of a real row) need no
-        // masking except g and beta: beta = 0 zeroes their rows of L, W and U
-        // and hence of v~, and their o rows are never stored; g = 0 keeps them
-        // out of the chunk's decay.
+        const int ci = 4 * j + 2 * hf + (gq >> 1);
+        const int pc = ci ^ (c & (NCH - 1));
+        w[2 * j + hf] = ds_read_b64_raw(stg_row(t, c) + pc * 16 + (gq & 1) * 8);
+      }
+    lds_settle(w);
+  };
+  // Rows past the chunk's end (staged copies of a real row) need no masking
+  // except g and beta: beta = 0 zeroes their rows of L, W and U and hence of
+  // v~, and their o rows are never stored; g = 0 keeps them out of the
+  // chunk's decay.
+  float kr[NJ][8], qr[NJ][8], kc[NJ][8], Gt[NJ][8];
+  float vr[NJV][8];
+
+  // g -> log2 decay, then the tile-local inclusive scan
+  if constexpr (SPLIT) {
+    wait_vmem<3 * NPER>();
+    __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "workgroup", "local");
+  }
+  uint2 sw[2 * NJ];
+  if constexpr (STG) stg_read_all(2, sw);
 #pragma unroll
-        for (int e = 0; e < 4; ++e) {
-          qr[j][4 * hf + e] = x[e];
-          kr[j][4 * hf + e] = y[e];
-          Gt[j][4 * hf + e] = valid ? z[e] * kLog2e : 0.f;
-          vr[j][4 * hf + e] = w[e];
-        }
+  for (int j = 0; j < NJ; ++j)
+#pragma unroll
+    for (int hf = 0; hf < 2; ++hf) {
+      f4 z = {0, 0, 0, 0};
+      if constexpr (STG) z = unpack4<DTG>(sw[2 * j + hf]);
+      else if (valid) z = ld4<DTG>(a.g, bq + 32 * j + 4 * gq + 16 * hf);
+#pragma unroll
+      for (int e = 0; e < 4; ++e) Gt[j][4 * hf + e] = valid ? z[e] * kLog2e : 0.f;
+    }
+#pragma unroll
+  for (int j = 0; j < NJ; ++j)
+#pragma unroll
+    for (int e = 0; e < 8; ++e) Gt[j][e] = row_scan16(Gt[j][e]);
+
+  // k, q and the two decay factors
+  if constexpr (SPLIT) {
+    wait_vmem<NPER>();
+    __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "workgroup", "local");
+  }
+  uint2 sq[2 * NJ];
+  if constexpr (STQ) {
+    stg_read_all(0, sq);
+    stg_read_all(1, sw);
+  }
+#pragma unroll
+  for (int j = 0; j < NJ; ++j)
+#pragma unroll
+    for (int hf = 0; hf < 2; ++hf) {
+      const int ch0 = 32 * j + 4 * gq + 16 * hf;
+      f4 x = {0, 0, 0, 0}, y = {0, 0, 0, 0};
+      if constexpr (STQ) {
+        x = unpack4<DTQ>(sq[2 * j + hf]);
+        y = unpack4<DTQ>(sw[2 * j + hf]);
+      } else if (valid) {
+        x = ld4<DTQ>(a.q, bq + ch0);
+        y = ld4<DTQ>(a.k, bq + ch0);
+      }
+#pragma unroll
+      for (int e = 0; e < 4; ++e) {
+        qr[j][4 * hf + e] = x[e];
+        kr[j][4 * hf + e] = y[e];
       }
     }
-    if (valid) beta_c = ld1<DTG>(a.beta, tok * H + h);
-    if (a.scale != 1.f) {
+  if (a.scale != 1.f) {
 #pragma unroll
-      for (int j = 0; j < NJ; ++j)
+    for (int j = 0; j < NJ; ++j)
 #pragma unroll
-        for (int e = 0; e < 8; ++e) qr[j][e] *= a.scale;
-    }
+      for (int e = 0; e < 8; ++e) qr[j][e] *= a.scale;
   }
+  float dmin = 0.f;
+#pragma unroll
+  for (int j = 0; j < NJ; ++j)
+#pragma unroll
+    for (int e = 0; e < 8; ++e) {
+      const float gt = Gt[j][e];
+      const float dw = row_bcast<15>(gt);
+      dmin = fminf(dmin, dw);
+      const float R = fast_exp2(gt);
+      kc[j][e] = kr[j][e] * fast_exp2(dw - gt);
+      kr[j][e] *= R;
+      qr[j][e] *= R;
+    }
+
+  // v
+  if constexpr (SPLIT) {
+    wait_vmem<0>();
+    __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "workgroup", "local");
+  }
+  if constexpr (STQ) stg_read_all(3, sw);
+#pragma unroll
+  for (int j = 0; j < NJV; ++j)
+#pragma unroll
+    for (int hf = 0; hf < 2; ++hf) {
+      f4 w = {0, 0, 0, 0};
+      if constexpr (STQ) w = unpack4<DTQ>(sw[2 * j + hf]);
+      else if (valid) w = ld4<DTQ>(a.v, (tok * H + h) * DV + 32 * j + 4 * gq + 16 * hf);
+#pragma unroll
+      for (int e = 0; e < 4; ++e) vr[j][4 * hf + e] = w[e];
+    }
+  if (!valid) beta_c = 0.f;
   // every wave has read its staged rows before any buffer they alias is written
   if constexpr (STQ || STG) lds_barrier();
 
-  // beta * v  -> BVt (channel-major)
+  // beta * v  -> BVt (channel-major); tile totals; k*Cf -> region 1
 #pragma unroll
   for (int j = 0; j < NJV; ++j)
 #pragma unroll
@@ -230,25 +301,11 @@ __device__ __forceinline__ void intra_chunk(const IntraArgs& a, const UnitRef& U
 #pragma unroll
       for (int e = 0; e < 4; ++e) sm.BVt[(ch0 + e) * PC + c] = st(beta_c * vr[j][4 * hf + e]);
     }
-
-  // ---- tile-local cumsum and the two decay factors ---------------------------
-  float dmin = 0.f;
 #pragma unroll
   for (int j = 0; j < NJ; ++j) {
     f8 x, tj;
 #pragma unroll
-    for (int e = 0; e < 8; ++e) {
-      const float gt = row_scan16(Gt[j][e]);
-      Gt[j][e] = gt;
-      const float dw = row_bcast<15>(gt);
-      dmin = fminf(dmin, dw);
-      const float R = fast_exp2(gt);
-      kc[j][e] = kr[j][e] * fast_exp2(dw - gt);
-      kr[j][e] *= R;
-      qr[j][e] *= R;
-      x[e] = kc[j][e];
-      tj[e] = gt;
-    }
+    for (int e = 0; e < 8; ++e) { x[e] = kc[j][e]; tj[e] = Gt[j][e]; }
     if (r == 15) *reinterpret_cast<f8*>(&sm.tot[W][32 * j + 8 * gq]) = tj;
     *reinterpret_cast<v8*>(&sm.r1[c * PK + 32 * j + 8 * gq]) = cvt8<EXACT>(x);
   }
@@ -490,7 +547,7 @@ __device__ __forceinline__ void intra_chunk(const IntraArgs& a, const UnitRef& U
       Toff[R * (R - 1) / 2 + s] = -mma16(f4{0, 0, 0, 0}, A2, cvt4<EXACT>(X));
     }
   }
-  // own row block of T -> Tm (read back by this wave only)
+  // own row block of T -> Tm (every wave reads all four after barrier #3)
 #pragma unroll
   for (int s = 0; s < W; ++s)
 #pragma unroll
@@ -505,33 +562,59 @@ __device__ __forceinline__ void intra_chunk(const IntraArgs& a, const UnitRef& U
 #pragma unroll
     for (int i = 0; i < 16; ++i) sm.Tm[(16 * W + i) * PC + 16 * W + r] = st(x[i]);
   }
-  lds_barrier();  // #3: (beta*gamma*k)^T of every wave; own T rows
+  lds_barrier();  // #3: (beta*gamma*k)^T and the T row blocks of every wave
 
-  // ---- W^T tiles and U tiles for row tile W ---------------------------------
-  constexpr int nk = (W < 2) ? 1 : 2;
+  // ---- W^T and U tiles -------------------------------------------------------
+  // Balanced over the waves: wave W computes column tiles {2W, 2W+1} (of W^T's
+  // dk and of U's dv) for all four row tiles, so every wave issues the same
+  // 2 x (1 + 1 + 2 + 2) MFMA pairs (row tiles 0, 1 have a 32-wide K range, 2 and
+  // 3 a 64-wide one) instead of the last row tile's wave doing twice the
+  // first's.  A W^T pair of column tiles is one 16-byte fragment per lane.
+  static_assert(DK / 16 == 8 && DV / 16 == 8 || DK / 16 == 4 && DV / 16 == 4, "column tiles per wave");
+  constexpr int CT = DK / 64;          // column tiles per wave (2 at d = 128, 1 at d = 64)
+  v8 Aw[CT][2], Bv[CT][2];
 #pragma unroll
-  for (int dt = 0; dt < DK / 16; ++dt) {
-    f4 acc = {0, 0, 0, 0};
+  for (int i = 0; i < CT; ++i)
 #pragma unroll
-    for (int jc = 0; jc < nk; ++jc) {
-      const v8 A = *reinterpret_cast<const v8*>(&sm.r1[(16 * dt + r) * PC + 32 * jc + 8 * gq]);
-      const v8 B = *reinterpret_cast<const v8*>(&sm.Tm[(16 * W + r) * PC + 32 * jc + 8 * gq]);
-      acc = mma32(acc, A, B);
+    for (int jc = 0; jc < 2; ++jc) {
+      const int t = CT * W + i;
+      Aw[i][jc] = *reinterpret_cast<const v8*>(&sm.r1[(16 * t + r) * PC + 32 * jc + 8 * gq]);
+      Bv[i][jc] = *reinterpret_cast<const v8*>(&sm.BVt[(16 * t + r) * PC + 32 * jc + 8 * gq]);
     }
-    *reinterpret_cast<v4*>(oW + (chead * (kC / 16) * NJ + (W * NJ + (dt >> 1))) * 512 + l * 8 +
-                           (dt & 1) * 4) = cvt4<EXACT>(acc);
-  }
 #pragma unroll
-  for (int et = 0; et < DV / 16; ++et) {
-    f4 acc = {0, 0, 0, 0};
+  for (int R = 0; R < 4; ++R) {
+    const int nk = (R < 2) ? 1 : 2;
+    v8 Tr[2];
 #pragma unroll
-    for (int jc = 0; jc < nk; ++jc) {
-      const v8 A = *reinterpret_cast<const v8*>(&sm.Tm[(16 * W + r) * PC + 32 * jc + 8 * gq]);
-      const v8 B = *reinterpret_cast<const v8*>(&sm.BVt[(16 * et + r) * PC + 32 * jc + 8 * gq]);
-      acc = mma32(acc, A, B);
+    for (int jc = 0; jc < 2; ++jc)
+      if (jc < nk) Tr[jc] = *reinterpret_cast<const v8*>(&sm.Tm[(16 * R + r) * PC + 32 * jc + 8 * gq]);
+    f4 accW[CT], accU[CT];
+#pragma unroll
+    for (int i = 0; i < CT; ++i) {
+      accW[i] = f4{0, 0, 0, 0};
+      accU[i] = f4{0, 0, 0, 0};
+#pragma unroll
+      for (int jc = 0; jc < 2; ++jc)
+        if (jc < nk) {
+          accW[i] = mma32(accW[i], Aw[i][jc], Tr[jc]);
+          accU[i] = mma32(accU[i], Tr[jc], Bv[i][jc]);
+        }
     }
-    *reinterpret_cast<v4*>(oU + (chead * (kC / 16) * (DV / 16) + (W * (DV / 16) + et)) * 256 +
-                           l * 4) = cvt4<EXACT>(acc);
+    if constexpr (CT == 2) {
+      // dk tiles 2W, 2W+1 = the two halves of K step j = W of row tile R
+      v8 wf;
+      const v4 w0 = cvt4<EXACT>(accW[0]), w1 = cvt4<EXACT>(accW[1]);
+#pragma unroll
+      for (int e = 0; e < 4; ++e) { wf[e] = w0[e]; wf[4 + e] = w1[e]; }
+      *reinterpret_cast<v8*>(oW + (chead * (kC / 16) * NJ + (R * NJ + W)) * 512 + l * 8) = wf;
+    } else {
+      *reinterpret_cast<v4*>(oW + (chead * (kC / 16) * NJ + (R * NJ + (W >> 1))) * 512 + l * 8 +
+                             (W & 1) * 4) = cvt4<EXACT>(accW[0]);
+    }
+#pragma unroll
+    for (int i = 0; i < CT; ++i)
+      *reinterpret_cast<v4*>(oU + (chead * (kC / 16) * (DV / 16) + (R * (DV / 16) + CT * W + i)) * 256 +
+                             l * 4) = cvt4<EXACT>(accU[i]);
   }
 }
 

@@ -191,6 +191,31 @@ __device__ __forceinline__ float fast_exp2(float x) { return __builtin_amdgcn_ex
 // global->LDS loads are not tracked by the compiler's own waits, so code that
 // reads what they wrote waits with this (then orders its LDS reads after it).
 __device__ __forceinline__ void wait_vmem_all() { __builtin_amdgcn_s_waitcnt(0x0F70); }
+// 8-byte LDS read issued by inline assembly.  The compiler does not see it as
+// an LDS access, so it does not make it wait for every outstanding direct
+// global->LDS copy of the wave (vmcnt(0)), which it does before each LDS read
+// it does see; the caller waits for the copies it needs with wait_vmem<N>()
+// first and calls lds_settle() before using the values.
+__device__ __forceinline__ uint2 ds_read_b64_raw(const void* p) {
+  uint2 v;
+  const unsigned addr = static_cast<unsigned>(reinterpret_cast<uintptr_t>(p));
+  asm volatile("ds_read_b64 %0, %1" : "=v"(v) : "v"(addr));
+  return v;
+}
+// Waits for all outstanding LDS reads and ties the values to the wait, so no
+// use of them is scheduled before it.
+template <int N>
+__device__ __forceinline__ void lds_settle(uint2 (&v)[N]) {
+  asm volatile("s_waitcnt lgkmcnt(0)" ::: "memory");
+#pragma unroll
+  for (int i = 0; i < N; ++i) asm volatile("" : "+v"(v[i]));
+}
+// s_waitcnt vmcnt(N): all but the N most recently issued memory operations done
+template <int N>
+__device__ __forceinline__ void wait_vmem() {
+  static_assert(N >= 0 && N < 16, "vmcnt field (low 4 bits)");
+  __builtin_amdgcn_s_waitcnt(0x0F70 | N);
+}
 
 // Workgroup barrier that orders LDS only.  __syncthreads() also releases
 // global memory, which makes every wave wait for its outstanding global loads
