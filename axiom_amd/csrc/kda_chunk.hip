@@ -223,8 +223,15 @@ __device__ __forceinline__ void intra_chunk(const IntraArgs& a, const UnitRef& U
 #pragma unroll
     for (int e = 0; e < 8; ++e) Gt[j][e] = row_scan16(Gt[j][e]);
 
-  // k, q and the two decay factors
+  // k, q and the two decay factors.  Each group's results are tied to an
+  // empty asm statement before the next group's wait: otherwise the compiler
+  // sinks the arithmetic to its first use, past the staging barrier, and the
+  // copies still in flight hide nothing.
   if constexpr (SPLIT) {
+#pragma unroll
+    for (int j = 0; j < NJ; ++j)
+#pragma unroll
+      for (int e = 0; e < 8; ++e) asm volatile("" : "+v"(Gt[j][e]));
     wait_vmem<NPER>();
     __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "workgroup", "local");
   }
@@ -274,6 +281,10 @@ __device__ __forceinline__ void intra_chunk(const IntraArgs& a, const UnitRef& U
 
   // v
   if constexpr (SPLIT) {
+#pragma unroll
+    for (int j = 0; j < NJ; ++j)
+#pragma unroll
+      for (int e = 0; e < 8; ++e) asm volatile("" : "+v"(kc[j][e]), "+v"(kr[j][e]), "+v"(qr[j][e]));
     wait_vmem<0>();
     __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "workgroup", "local");
   }
