@@ -251,6 +251,143 @@ def chunk_fwd(q, k, v, g, beta, h0=None, cu_seqlens=None, chunk: int = 64, tile:
     return o, hts
 
 
+# ---------------------------------------------------------------------------
+# Chunked backward: the analytic adjoint per chunk, scanned in reverse
+# ---------------------------------------------------------------------------
+
+
+def chunk_step_bwd(q, k, v, G, beta, S, do, dS_next):
+    """Adjoint of ``chunk_step`` for ``N`` chains, one chunk.
+
+    Transcribes the equations of ``net/kernels/kda_cc_fused_bwd.py:30-55``
+    (code ``:139-228``) with the decay written through ``G`` (the in-chunk
+    inclusive cumsum of ``g``) instead of ``alpha``: the returned ``dG`` is
+    the cotangent of ``G`` (its reverse cumsum is ``dg``, done by the caller).
+    Shapes as ``chunk_step``; ``do [N, C, dv]``, ``dS_next [N, dk, dv]``.
+    Returns ``(dq, dk, dv, dG, dbeta, dS_in)``.
+    """
+    N, C, dk = q.shape
+    ar = torch.arange(C)
+    tril = (ar[:, None] >= ar[None, :]).to(q.dtype)
+    strict = (ar[:, None] > ar[None, :]).to(q.dtype)
+    b = beta[:, :, None]
+    # E[c, i, d] = exp(G_c - G_i), clamped at 0 above the diagonal (masked there)
+    E = torch.exp(torch.clamp(G[:, :, None, :] - G[:, None, :, :], max=0.0))
+    aqk = tril * torch.einsum("ncid,ncd,nid->nci", E, q, k)
+    L = strict * torch.einsum("ncid,ncd,nid->nci", E, k * b, k)
+    gamma = torch.exp(G)
+    xw = gamma * k * b
+    vw = v * b
+    SM = torch.linalg.inv(torch.eye(C, dtype=q.dtype) + L)
+    W = SM @ xw
+    U = SM @ vw
+    vt = U - W @ S
+    gc = gamma[:, -1, :]                                      # exp(sum_c la)
+    lam = torch.exp(G[:, -1:, :] - G)
+    y = lam * k
+
+    dS_acc = gc[:, :, None] * dS_next                         # :176-177
+    dgc = (S * dS_next).sum(-1)
+    dY = vt @ dS_next.transpose(1, 2)                         # :178-180
+    dvt = y @ dS_next + aqk.transpose(1, 2) @ do
+    daqk = (do @ vt.transpose(1, 2)) * tril
+    dS_acc = dS_acc + (gamma * q).transpose(1, 2) @ do        # :181-184
+    dgq = do @ S.transpose(1, 2)
+    dgamma = dgq * q
+    dq = dgq * gamma
+    dU = dvt                                                  # :187-196
+    dW = -(dvt @ S.transpose(1, 2))
+    dS_acc = dS_acc - W.transpose(1, 2) @ dvt
+    Yw = SM.transpose(1, 2) @ dW
+    Yu = SM.transpose(1, 2) @ dU
+    dL = -(Yw @ W.transpose(1, 2) + Yu @ U.transpose(1, 2)) * strict
+    dgamma = dgamma + Yw * (k * b)
+    dk_ = Yw * (gamma * b)
+    dv_ = Yu * b
+    db = (Yw * gamma * k).sum(-1) + (Yu * v).sum(-1)
+    dr_a = torch.einsum("nci,ncid,nid->ncd", daqk, E, k)      # :199-211
+    dc_a = torch.einsum("nci,ncid,ncd->nid", daqk, E, q)
+    dq = dq + dr_a
+    dk_ = dk_ + dc_a
+    dr_k = torch.einsum("nci,ncid,nid->ncd", dL, E, k)
+    dc_k = torch.einsum("nci,ncid,ncd->nid", dL, E, k * b)
+    dk_ = dk_ + dr_k * b + dc_k
+    db = db + (dr_k * k).sum(-1)
+    dG = (dr_a * q - dc_a * k) + (dr_k * (k * b) - dc_k * k)
+    dG = dG + dgamma * gamma                                  # through exp(G)
+    dlam = dY * k                                             # :214-217
+    dk_ = dk_ + dY * lam
+    dz = dlam * lam                                           # lam = exp(G_C - G)
+    dG = dG - dz
+    dG[:, -1, :] += dz.sum(1) + gc * dgc                      # G_C = G[C-1] (:218-220)
+    return dq, dk_, dv_, dG, db, dS_acc
+
+
+def chunk_bwd(q, k, v, g, beta, do, dht=None, h0=None, chunk: int = 64, dtype=torch.float64,
+              scale: float = 1.0):
+    """Gradients of the chunked forward for dense ``[B, T, H, d]`` inputs.
+
+    The reverse scan of ``net/kernels/kda_cc_fused_persist.py:794-842``
+    (``reference_bwd_scan``): a forward scan recomputes each chunk's incoming
+    state, a reverse scan runs ``chunk_step_bwd`` per chunk and hands the
+    state cotangent to the previous chunk.  ``do [B,T,H,dv]`` and ``dht
+    [B,H,dk,dv]`` (None = 0) are the cotangents of ``o`` and of the final
+    state.  A ragged tail is zero-padded with ``g = 0, beta = 0, do = 0``,
+    which leaves every real row's gradient unchanged.  ``scale`` multiplies q
+    as in the forward.  Returns numpy float64 ``(dq, dk, dv, dg, dbeta, dh0)``
+    in the input layouts (``dg`` is the cotangent of the log-decay ``g``:
+    ``dalpha = dg / alpha`` in the reference's ``alpha`` form).
+    """
+    B, T, H, dk = q.shape
+    dv = v.shape[-1]
+    C = chunk
+    n = (T + C - 1) // C
+    Tp = n * C
+    pad = Tp - T
+
+    def prep(x, d):
+        t = _to_torch(x, dtype).permute(0, 2, 1, 3).reshape(B * H, T, d)
+        if pad:
+            t = torch.cat([t, torch.zeros((B * H, pad, d), dtype=dtype)], dim=1)
+        return t.reshape(B * H, n, C, d)
+
+    qc = prep(np.asarray(q) * scale, dk)
+    kc = prep(k, dk)
+    vc = prep(v, dv)
+    gcs = torch.cumsum(prep(g, dk), dim=2)
+    doc = prep(do, dv)
+    bt = _to_torch(beta, dtype).permute(0, 2, 1).reshape(B * H, T)
+    if pad:
+        bt = torch.cat([bt, torch.zeros((B * H, pad), dtype=dtype)], dim=1)
+    bc = bt.reshape(B * H, n, C)
+    S = (torch.zeros((B * H, dk, dv), dtype=dtype) if h0 is None
+         else _to_torch(h0, dtype).reshape(B * H, dk, dv).clone())
+    states = []
+    for i in range(n):
+        states.append(S)
+        _, S = chunk_step(qc[:, i], kc[:, i], vc[:, i], gcs[:, i], bc[:, i], S, tile=C)
+    dS = (torch.zeros((B * H, dk, dv), dtype=dtype) if dht is None
+          else _to_torch(dht, dtype).reshape(B * H, dk, dv))
+    outs = {x: torch.zeros((B * H, n, C, d), dtype=dtype)
+            for x, d in (("dq", dk), ("dk", dk), ("dv", dv), ("dg", dk))}
+    dbeta = torch.zeros((B * H, n, C), dtype=dtype)
+    for i in reversed(range(n)):
+        dq_, dk_, dv_, dG, db, dS = chunk_step_bwd(qc[:, i], kc[:, i], vc[:, i], gcs[:, i], bc[:, i],
+                                                   states[i], doc[:, i], dS)
+        outs["dq"][:, i] = dq_ * scale
+        outs["dk"][:, i] = dk_
+        outs["dv"][:, i] = dv_
+        outs["dg"][:, i] = torch.flip(torch.cumsum(torch.flip(dG, [1]), 1), [1])   # G = cumsum(g)
+        dbeta[:, i] = db
+
+    def back(t, d):
+        return t.reshape(B, H, Tp, d)[:, :, :T].permute(0, 2, 1, 3).contiguous().numpy()
+
+    return (back(outs["dq"], dk), back(outs["dk"], dk), back(outs["dv"], dv), back(outs["dg"], dk),
+            dbeta.reshape(B, H, Tp)[:, :, :T].permute(0, 2, 1).contiguous().numpy(),
+            dS.reshape(B, H, dk, dv).numpy())
+
+
 def chunk_intermediates(q, k, v, g, beta, chunk: int = 64, tile: int = 16, scale: float = 1.0):
     """Per-chunk intermediates of ``cc_chunk_step`` (``net/kda.py:669-702``), dense inputs.
 
