@@ -1,11 +1,12 @@
 """axiom_amd -- MI355X-native (gfx950) KDA hot path.
 
 Chunked Kimi-Delta-Attention forward in WY/UT form, the single-token recurrent
-decode step and varlen scheduling, as hand-written HIP kernels behind the C ABI
-of ``include/kda_mi355x.h``.  The Python layer (:mod:`axiom_amd.kda`) only
+decode step, varlen scheduling and the chunked backward, as hand-written HIP
+kernels behind the C ABI of ``include/kda_mi355x.h``.  The Python layer (:mod:`axiom_amd.kda`) only
 validates arguments and hands device pointers to that library.
 """
 
-from .kda import cc_scan, kda_chunk_fwd, kda_recurrent_step, varlen_status  # noqa: F401
+from .kda import (cc_scan, kda_chunk, kda_chunk_bwd, kda_chunk_fwd, kda_recurrent_step,  # noqa: F401
+                  varlen_status)
 
-__all__ = ["cc_scan", "kda_chunk_fwd", "kda_recurrent_step", "varlen_status"]
+__all__ = ["cc_scan", "kda_chunk", "kda_chunk_bwd", "kda_chunk_fwd", "kda_recurrent_step", "varlen_status"]

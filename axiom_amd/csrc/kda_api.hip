@@ -249,6 +249,33 @@ hipError_t launch_adapt(const AdaptArgs& a, hipStream_t s) {
 // ----------------------------------------------------------------------------
 // exported entry points
 // ----------------------------------------------------------------------------
+// Backward workspace: fp32 arrays per chunk-head (see kda_internal.h: BwdArgs).
+struct BwdLayout {
+  size_t GL, QG, KL, GCV, AQ, TM, WM, UM, SI, VT, DS, DVT, total;
+};
+
+BwdLayout bwd_layout(int B, int T, int H, int d) {
+  BwdLayout L{};
+  const size_t ch = static_cast<size_t>(B) * ((T + kC - 1) / kC) * H;
+  size_t off = 0;
+  auto take = [&](size_t bytes) { size_t at = off; off = align_up(off + bytes); return at; };
+  const size_t cd = ch * kC * d * 4, cc = ch * kC * kC * 4, dd = ch * d * d * 4;
+  L.GL = take(cd);
+  L.QG = take(cd);
+  L.KL = take(cd);
+  L.GCV = take(ch * d * 4);
+  L.AQ = take(cc);
+  L.TM = take(cc);
+  L.WM = take(cd);
+  L.UM = take(cd);
+  L.SI = take(dd);
+  L.VT = take(cd);
+  L.DS = take(dd);
+  L.DVT = take(cd);
+  L.total = off;
+  return L;
+}
+
 extern "C" {
 
 int kda_abi_version(void) { return 100; }
@@ -351,6 +378,70 @@ int kda_cc_scan(hipStream_t stream, const void* q, const void* k, const void* v,
   return chunk_fwd_impl(stream, q, k, v, g32, b32, S_in, nullptr, 0, o, S_out, 1, T, H, dk, dv,
                         kC, 1.0f, KDA_DTYPE_BF16_F32GATES, KDA_DTYPE_F32, rest,
                         workspace_bytes - g_bytes - b_bytes);
+}
+
+size_t kda_chunk_bwd_workspace(int B, int T, int H, int dk, int dv, int chunk) {
+  if (B < 1 || T < 0 || H < 1 || !dim_ok(dk) || dk != dv || chunk != kC) return 0;
+  const size_t total = bwd_layout(B, T, H, dk).total;
+  return total > 0 ? total : kAlign;   // 0 is reserved for "bad input"
+}
+
+int kda_chunk_bwd(hipStream_t stream, const void* q, const void* k, const void* v, const void* g,
+                  const void* beta, const float* h0, const void* dout, const float* dht,
+                  float* dq, float* dk, float* dv, float* dg, float* dbeta, float* dh0,
+                  int B, int T, int H, int dk_dim, int dv_dim, int chunk, float scale,
+                  int in_dtype, int dout_dtype, void* workspace, size_t workspace_bytes) {
+  g_err[0] = 0;
+  if (B < 1) return fail(KDA_ERR_INVALID_ARGUMENT, "B=%d must be >= 1", B);
+  if (T < 0) return fail(KDA_ERR_INVALID_ARGUMENT, "T=%d must be >= 0", T);
+  // (with T == 0 the per-token tensors are empty and may be null)
+  if (T > 0 && (!q || !k || !v || !g || !beta || !dout))
+    return fail(KDA_ERR_INVALID_ARGUMENT, "null input pointer");
+  if (T > 0 && (!dq || !dk || !dv || !dg || !dbeta))
+    return fail(KDA_ERR_INVALID_ARGUMENT, "null gradient pointer");
+  if (int rc = check_dims(H, dk_dim, dv_dim)) return rc;
+  if (chunk != kC) return fail(KDA_ERR_UNSUPPORTED, "chunk=%d: this build runs chunk == 64", chunk);
+  if (in_dtype < KDA_DTYPE_F32 || in_dtype > KDA_DTYPE_BF16_F32GATES)
+    return fail(KDA_ERR_INVALID_ARGUMENT, "in_dtype=%d is not a kda_dtype_t", in_dtype);
+  if (dout_dtype != KDA_DTYPE_F32 && dout_dtype != KDA_DTYPE_BF16)
+    return fail(KDA_ERR_INVALID_ARGUMENT, "dout_dtype=%d: dout is F32 or BF16", dout_dtype);
+  if (!std::isfinite(scale)) return fail(KDA_ERR_INVALID_ARGUMENT, "scale must be finite");
+  const int64_t elems = static_cast<int64_t>(B) * T * H * dk_dim;
+  if (elems >= (1LL << 40)) return fail(KDA_ERR_INVALID_ARGUMENT, "problem too large");
+  const int64_t NT = (T + kC - 1) / kC;
+  if (static_cast<int64_t>(B) * NT * H > 0x7FFFFFFFLL) return fail(KDA_ERR_INVALID_ARGUMENT, "too many chunk-heads");
+  const BwdLayout L = bwd_layout(B, T, H, dk_dim);
+  if (!workspace || workspace_bytes < L.total)
+    return fail(KDA_ERR_WORKSPACE, "workspace of %zu bytes is too small (need %zu)", workspace_bytes, L.total);
+  if (T == 0) {
+    // no tokens: the state passes through unchanged, dh0 = dht
+    if (dh0 != nullptr) {
+      const hipError_t e = kda::launch_copy_or_zero(dh0, dht, static_cast<int64_t>(B) * H * dk_dim * dv_dim, stream);
+      if (e != hipSuccess) return hip_fail(e, "dh0 for T == 0");
+    }
+    return KDA_OK;
+  }
+  unsigned char* ws = static_cast<unsigned char*>(workspace);
+  kda::BwdArgs a{};
+  a.B = B; a.T = T; a.H = H; a.NT = static_cast<int>(NT);
+  a.q = q; a.k = k; a.v = v; a.g = g; a.beta = beta;
+  a.h0 = h0; a.dout = dout; a.dht = dht; a.scale = scale;
+  a.dq = dq; a.dk = dk; a.dv = dv; a.dg = dg; a.dbeta = dbeta; a.dh0 = dh0;
+  a.GL = reinterpret_cast<float*>(ws + L.GL);
+  a.QG = reinterpret_cast<float*>(ws + L.QG);
+  a.KL = reinterpret_cast<float*>(ws + L.KL);
+  a.GCV = reinterpret_cast<float*>(ws + L.GCV);
+  a.AQ = reinterpret_cast<float*>(ws + L.AQ);
+  a.TM = reinterpret_cast<float*>(ws + L.TM);
+  a.WM = reinterpret_cast<float*>(ws + L.WM);
+  a.UM = reinterpret_cast<float*>(ws + L.UM);
+  a.SI = reinterpret_cast<float*>(ws + L.SI);
+  a.VT = reinterpret_cast<float*>(ws + L.VT);
+  a.DS = reinterpret_cast<float*>(ws + L.DS);
+  a.DVT = reinterpret_cast<float*>(ws + L.DVT);
+  const hipError_t e = kda::launch_bwd(a, dk_dim, in_dtype, dout_dtype, stream);
+  if (e != hipSuccess) return hip_fail(e, "backward kernel launch");
+  return KDA_OK;
 }
 
 }  // extern "C"

@@ -1,0 +1,870 @@
+// Chunked KDA backward (dense [B, T, H, d] inputs), fp32 throughout.
+//
+// Gradients of o = chunk_fwd(q, k, v, g, beta, h0) and of the final state
+// with respect to q, k, v, g (the log decay), beta and h0, following the
+// reference's analytic adjoint per chunk (net/kernels/kda_cc_fused_bwd.py:30-55,
+// code :139-228) scanned in reverse over the chunks
+// (net/kernels/kda_cc_fused_persist.py:794-842, reference_bwd_scan).  Four
+// launches:
+//   kda_bwd_prep_kernel   one workgroup per chunk-head: in-chunk log2 cumsum G,
+//                         gamma*q, lambda*k, gamma_C, Aqk, T = (I+L)^-1, W, U;
+//   kda_bwd_fscan_kernel  one workgroup per (chain, 32 value columns): the
+//                         forward state scan, keeping every chunk's incoming
+//                         state S and its v~ = U - W S;
+//   kda_bwd_rscan_kernel  same grid, chunks in reverse: the state cotangent
+//                         dS entering each chunk from the right, and
+//                         dv~ = (lambda k) dS + Aqk^T do;
+//                         dS <- gamma_C dS + (gamma q)^T do - W^T dv~; dh0;
+//   kda_bwd_chunk_kernel  one workgroup per chunk-head: the rest of the adjoint
+//                         (dY, dgq, dW, the two transposed solves, dL, dAqk, the
+//                         score adjoints, the cumsum adjoint) and the outputs.
+// Every matrix product is an LDS-tiled fp32 FMA loop (each of the 256 threads
+// owns rows r0 + 16i and columns c0 + 16j of the product); decay factors of
+// off-diagonal 16-row tiles are anchored at the row tile's first row
+// (2^(G_c - G_a) * 2^(G_a - G_i), both <= 1), diagonal tiles use
+// 2^(G_c - G_i) directly.  Workspace arrays are fp32, row-major, per
+// chunk-head ch = (b * NT + n) * H + h.
+#include <hip/hip_runtime.h>
+
+#include <cstdint>
+
+#include "kda_common.h"
+#include "kda_internal.h"
+
+namespace kda {
+namespace {
+
+constexpr int kC = 64;
+constexpr int kThreads = 256;
+
+__device__ __forceinline__ float ex2(float x) { return __builtin_amdgcn_exp2f(x); }
+
+template <int D>
+struct BwdDims {
+  static constexpr int P = D + 1;     // LDS pitch of [rows][D] arrays
+  static constexpr int PC = kC + 1;   // LDS pitch of [rows][64] arrays
+  static constexpr int NJ = D / 16;   // columns per thread of a [64][D] product
+};
+
+// Token row of chunk row c (dense layout) and whether it exists.
+struct ChunkRows {
+  int64_t row0;   // b * T + n * 64
+  int len;        // valid rows of this chunk
+};
+
+__device__ __forceinline__ ChunkRows chunk_rows(const BwdArgs& a, int u) {
+  const int b = u / a.NT, n = u - b * a.NT;
+  ChunkRows r;
+  r.row0 = static_cast<int64_t>(b) * a.T + static_cast<int64_t>(n) * kC;
+  r.len = min(kC, a.T - n * kC);
+  return r;
+}
+
+// [64][D] block of a row-major fp32 workspace array into LDS (pitch P).
+template <int D>
+__device__ __forceinline__ void lds_load_rows(float* dst, int pitch, const float* src, int rows, int cols,
+                                              int src_ld, int col0) {
+  for (int e = threadIdx.x; e < rows * cols; e += kThreads) {
+    const int r = e / cols, c = e - r * cols;
+    dst[r * pitch + c] = src[static_cast<int64_t>(r) * src_ld + col0 + c];
+  }
+}
+
+// ---------------------------------------------------------------------------
+// prep: G, gamma*q, lambda*k, gamma_C, Aqk, T, W, U of one chunk-head
+// ---------------------------------------------------------------------------
+template <int D, int DTQ, int DTG>
+__global__ __launch_bounds__(kThreads) void kda_bwd_prep_kernel(BwdArgs a) {
+  typedef BwdDims<D> BD;
+  constexpr int P = BD::P, PC = BD::PC;
+  __shared__ float sQ[kC * P], sK[kC * P], sG[kC * P];
+  __shared__ float sL[kC * PC], sT[kC * PC];
+  __shared__ float sX0[16 * P], sX1[16 * P], sKf[16 * P];
+  __shared__ float sB[kC];
+  const int t = threadIdx.x;
+  const int H = a.H;
+  const int u = blockIdx.x / H, h = blockIdx.x - u * H;
+  const ChunkRows cr = chunk_rows(a, u);
+  const int64_t ch = static_cast<int64_t>(u) * H + h;
+
+  for (int e = t; e < kC * D; e += kThreads) {
+    const int c = e / D, d = e - c * D;
+    float qv = 0.f, kv = 0.f, gv = 0.f;
+    if (c < cr.len) {
+      const int64_t idx = ((cr.row0 + c) * H + h) * D + d;
+      qv = ld1<DTQ>(a.q, idx) * a.scale;
+      kv = ld1<DTQ>(a.k, idx);
+      gv = ld1<DTG>(a.g, idx);
+    }
+    sQ[c * P + d] = qv;
+    sK[c * P + d] = kv;
+    sG[c * P + d] = gv;
+  }
+  if (t < kC) sB[t] = (t < cr.len) ? ld1<DTG>(a.beta, (cr.row0 + t) * H + h) : 0.f;
+  __syncthreads();
+  // in-chunk inclusive cumsum of g, in log2 units
+  if (t < D) {
+    float acc = 0.f;
+    for (int c = 0; c < kC; ++c) {
+      acc += sG[c * P + t];
+      sG[c * P + t] = acc * kLog2e;
+    }
+  }
+  __syncthreads();
+  {
+    float* GL = a.GL + ch * kC * D;
+    float* QG = a.QG + ch * kC * D;
+    float* KL = a.KL + ch * kC * D;
+    for (int e = t; e < kC * D; e += kThreads) {
+      const int c = e / D, d = e - c * D;
+      const float gl = sG[c * P + d];
+      const float glast = sG[(kC - 1) * P + d];
+      GL[e] = gl;
+      QG[e] = ex2(gl) * sQ[c * P + d];
+      KL[e] = ex2(glast - gl) * sK[c * P + d];
+    }
+    if (t < D) a.GCV[ch * D + t] = ex2(sG[(kC - 1) * P + t]);
+  }
+
+  // scores: Aqk (c >= i) straight to the workspace, L = beta_c Akk (c > i) to LDS
+  float* AQ = a.AQ + ch * kC * kC;
+  const int r = t >> 4, i16 = t & 15;   // output (r, i16) of a 16 x 16 tile pair
+  for (int R = 0; R < 4; ++R) {
+    const int a0 = 16 * R;
+    // row operands of tile R with the factor 2^(G_c - G_a)
+    for (int e = t; e < 16 * D; e += kThreads) {
+      const int rr = e / D, d = e - rr * D;
+      const float fr = ex2(sG[(a0 + rr) * P + d] - sG[a0 * P + d]);
+      sX0[rr * P + d] = sQ[(a0 + rr) * P + d] * fr;
+      sX1[rr * P + d] = sK[(a0 + rr) * P + d] * sB[a0 + rr] * fr;
+    }
+    for (int s = 0; s < R; ++s) {
+      __syncthreads();  // sX0/sX1 written; previous sKf readers done
+      for (int e = t; e < 16 * D; e += kThreads) {
+        const int ii = e / D, d = e - ii * D;
+        sKf[ii * P + d] = sK[(16 * s + ii) * P + d] * ex2(sG[a0 * P + d] - sG[(16 * s + ii) * P + d]);
+      }
+      __syncthreads();
+      float accA = 0.f, accL = 0.f;
+      for (int d = 0; d < D; ++d) {
+        const float kf = sKf[i16 * P + d];
+        accA = fmaf(sX0[r * P + d], kf, accA);
+        accL = fmaf(sX1[r * P + d], kf, accL);
+      }
+      AQ[(a0 + r) * kC + 16 * s + i16] = accA;
+      sL[(a0 + r) * PC + 16 * s + i16] = accL;
+    }
+    // diagonal tile, 2^(G_c - G_i) directly
+    {
+      const int c = a0 + r, i = a0 + i16;
+      float accA = 0.f, accL = 0.f;
+      if (i16 <= r) {
+        for (int d = 0; d < D; ++d) {
+          const float e = ex2(sG[c * P + d] - sG[i * P + d]);
+          const float ki = sK[i * P + d] * e;
+          accA = fmaf(sQ[c * P + d], ki, accA);
+          accL = fmaf(sK[c * P + d], ki, accL);
+        }
+      }
+      AQ[c * kC + i] = accA;
+      sL[c * PC + i] = (i16 < r) ? accL * sB[c] : 0.f;
+      // upper triangle of the row band: zero
+      for (int s = R + 1; s < 4; ++s) {
+        AQ[c * kC + 16 * s + i16] = 0.f;
+        sL[c * PC + 16 * s + i16] = 0.f;
+      }
+    }
+    __syncthreads();  // sX0/sX1 reused by the next row tile
+  }
+
+  // T = (I + L)^-1: diagonal 16 x 16 blocks by forward substitution (one
+  // column per thread), then T_Rs = -T_RR sum_{j=s}^{R-1} L_Rj T_js.
+  for (int e = t; e < kC * kC; e += kThreads) {
+    const int c = e / kC, i = e - c * kC;
+    sT[c * PC + i] = 0.f;
+  }
+  __syncthreads();
+  if (t < kC) {
+    const int R = t >> 4, j = t & 15, a0 = 16 * R;
+    sT[(a0 + j) * PC + a0 + j] = 1.f;
+    for (int i = j + 1; i < 16; ++i) {
+      float acc = 0.f;
+      for (int m = j; m < i; ++m) acc = fmaf(sL[(a0 + i) * PC + a0 + m], sT[(a0 + m) * PC + a0 + j], acc);
+      sT[(a0 + i) * PC + a0 + j] = -acc;
+    }
+  }
+  __syncthreads();
+  for (int R = 1; R < 4; ++R) {
+    // X_s = sum_{j=s}^{R-1} L_Rj T_js for s < R (into sX0 rows 16s..), then T_Rs = -T_RR X_s
+    for (int e = t; e < 16 * 16 * R; e += kThreads) {
+      const int s = e >> 8, rr = (e >> 4) & 15, cc = e & 15;
+      float acc = 0.f;
+      for (int m = 16 * s; m < 16 * R; ++m) acc = fmaf(sL[(16 * R + rr) * PC + m], sT[m * PC + 16 * s + cc], acc);
+      sX0[s * 256 + rr * 16 + cc] = acc;
+    }
+    __syncthreads();
+    for (int e = t; e < 16 * 16 * R; e += kThreads) {
+      const int s = e >> 8, rr = (e >> 4) & 15, cc = e & 15;
+      float acc = 0.f;
+      for (int m = 0; m < 16; ++m) acc = fmaf(sT[(16 * R + rr) * PC + 16 * R + m], sX0[s * 256 + m * 16 + cc], acc);
+      sT[(16 * R + rr) * PC + 16 * s + cc] = -acc;
+    }
+    __syncthreads();
+  }
+  {
+    float* TM = a.TM + ch * kC * kC;
+    for (int e = t; e < kC * kC; e += kThreads) {
+      const int c = e / kC, i = e - c * kC;
+      TM[e] = sT[c * PC + i];
+    }
+  }
+  // W = T (beta gamma k), U = T (beta v)
+  for (int e = t; e < kC * D; e += kThreads) {
+    const int c = e / D, d = e - c * D;
+    sK[c * P + d] *= sB[c] * ex2(sG[c * P + d]);
+    float vv = 0.f;
+    if (c < cr.len) vv = ld1<DTQ>(a.v, ((cr.row0 + c) * H + h) * D + d);
+    sQ[c * P + d] = vv * sB[c];
+  }
+  __syncthreads();
+  {
+    constexpr int NJ = BD::NJ;
+    const int rm = t >> 4, cn = t & 15;
+    float accW[4][NJ], accU[4][NJ];
+#pragma unroll
+    for (int i = 0; i < 4; ++i)
+#pragma unroll
+      for (int j = 0; j < NJ; ++j) accW[i][j] = accU[i][j] = 0.f;
+    for (int m = 0; m < kC; ++m) {
+      float tv[4];
+#pragma unroll
+      for (int i = 0; i < 4; ++i) tv[i] = sT[(rm + 16 * i) * PC + m];
+#pragma unroll
+      for (int j = 0; j < NJ; ++j) {
+        const float x = sK[m * P + cn + 16 * j], y = sQ[m * P + cn + 16 * j];
+#pragma unroll
+        for (int i = 0; i < 4; ++i) {
+          accW[i][j] = fmaf(tv[i], x, accW[i][j]);
+          accU[i][j] = fmaf(tv[i], y, accU[i][j]);
+        }
+      }
+    }
+    float* WM = a.WM + ch * kC * D;
+    float* UM = a.UM + ch * kC * D;
+#pragma unroll
+    for (int i = 0; i < 4; ++i)
+#pragma unroll
+      for (int j = 0; j < NJ; ++j) {
+        WM[(rm + 16 * i) * D + cn + 16 * j] = accW[i][j];
+        UM[(rm + 16 * i) * D + cn + 16 * j] = accU[i][j];
+      }
+  }
+}
+
+// ---------------------------------------------------------------------------
+// forward state scan of one (chain, 32-column slice): S_in and v~ per chunk
+// ---------------------------------------------------------------------------
+template <int D>
+__global__ __launch_bounds__(kThreads) void kda_bwd_fscan_kernel(BwdArgs a) {
+  typedef BwdDims<D> BD;
+  constexpr int P = BD::P;
+  constexpr int NS = D / 32;
+  constexpr int NI = D / 16;   // state rows per thread
+  __shared__ float sW[kC * P], sKL[kC * P];
+  __shared__ float sS[D * 33], sU[kC * 33], sV[kC * 33], sGC[D];
+  const int t = threadIdx.x, rm = t >> 4, cn = t & 15;
+  const int chain = blockIdx.x / NS, split = blockIdx.x - chain * NS;
+  const int H = a.H;
+  const int b = chain / H, h = chain - b * H;
+  const int c0 = 32 * split;
+  float S[NI][2];
+#pragma unroll
+  for (int i = 0; i < NI; ++i)
+#pragma unroll
+    for (int j = 0; j < 2; ++j)
+      S[i][j] = (a.h0 != nullptr) ? a.h0[(static_cast<int64_t>(chain) * D + rm + 16 * i) * D + c0 + cn + 16 * j]
+                                  : 0.f;
+  for (int n = 0; n < a.NT; ++n) {
+    const int64_t ch = (static_cast<int64_t>(b) * a.NT + n) * H + h;
+    float* SI = a.SI + ch * D * D;
+#pragma unroll
+    for (int i = 0; i < NI; ++i)
+#pragma unroll
+      for (int j = 0; j < 2; ++j) {
+        SI[(rm + 16 * i) * D + c0 + cn + 16 * j] = S[i][j];
+        sS[(rm + 16 * i) * 33 + cn + 16 * j] = S[i][j];
+      }
+    lds_load_rows<D>(sW, P, a.WM + ch * kC * D, kC, D, D, 0);
+    lds_load_rows<D>(sKL, P, a.KL + ch * kC * D, kC, D, D, 0);
+    lds_load_rows<D>(sU, 33, a.UM + ch * kC * D, kC, 32, D, c0);
+    if (t < D) sGC[t] = a.GCV[ch * D + t];
+    __syncthreads();
+    // v~ = U - W S: rows rm + 16i (i < 4), columns cn + 16j (j < 2)
+    {
+      float acc[4][2];
+#pragma unroll
+      for (int i = 0; i < 4; ++i)
+#pragma unroll
+        for (int j = 0; j < 2; ++j) acc[i][j] = sU[(rm + 16 * i) * 33 + cn + 16 * j];
+      for (int d = 0; d < D; ++d) {
+        const float s0 = sS[d * 33 + cn], s1 = sS[d * 33 + cn + 16];
+#pragma unroll
+        for (int i = 0; i < 4; ++i) {
+          const float w = sW[(rm + 16 * i) * P + d];
+          acc[i][0] = fmaf(-w, s0, acc[i][0]);
+          acc[i][1] = fmaf(-w, s1, acc[i][1]);
+        }
+      }
+      float* VT = a.VT + ch * kC * D;
+#pragma unroll
+      for (int i = 0; i < 4; ++i)
+#pragma unroll
+        for (int j = 0; j < 2; ++j) {
+          sV[(rm + 16 * i) * 33 + cn + 16 * j] = acc[i][j];
+          VT[(rm + 16 * i) * D + c0 + cn + 16 * j] = acc[i][j];
+        }
+    }
+    __syncthreads();
+    // S <- gamma_C S + (lambda k)^T v~
+#pragma unroll
+    for (int i = 0; i < NI; ++i) {
+      const float gcv = sGC[rm + 16 * i];
+      S[i][0] *= gcv;
+      S[i][1] *= gcv;
+    }
+    for (int c = 0; c < kC; ++c) {
+      const float v0 = sV[c * 33 + cn], v1 = sV[c * 33 + cn + 16];
+#pragma unroll
+      for (int i = 0; i < NI; ++i) {
+        const float kl = sKL[c * P + rm + 16 * i];
+        S[i][0] = fmaf(kl, v0, S[i][0]);
+        S[i][1] = fmaf(kl, v1, S[i][1]);
+      }
+    }
+    __syncthreads();
+  }
+}
+
+// ---------------------------------------------------------------------------
+// reverse scan of one (chain, 32-column slice): dS per chunk, dv~, dh0
+// ---------------------------------------------------------------------------
+template <int D, int DO>
+__global__ __launch_bounds__(kThreads) void kda_bwd_rscan_kernel(BwdArgs a) {
+  typedef BwdDims<D> BD;
+  constexpr int P = BD::P, PC = BD::PC;
+  constexpr int NS = D / 32;
+  constexpr int NI = D / 16;
+  __shared__ float sX[kC * P], sY[kC * P], sA[kC * PC];
+  __shared__ float sS[D * 33], sDo[kC * 33], sDv[kC * 33], sGC[D];
+  const int t = threadIdx.x, rm = t >> 4, cn = t & 15;
+  const int chain = blockIdx.x / NS, split = blockIdx.x - chain * NS;
+  const int H = a.H;
+  const int b = chain / H, h = chain - b * H;
+  const int c0 = 32 * split;
+  float dS[NI][2];
+#pragma unroll
+  for (int i = 0; i < NI; ++i)
+#pragma unroll
+    for (int j = 0; j < 2; ++j)
+      dS[i][j] = (a.dht != nullptr) ? a.dht[(static_cast<int64_t>(chain) * D + rm + 16 * i) * D + c0 + cn + 16 * j]
+                                    : 0.f;
+  for (int n = a.NT - 1; n >= 0; --n) {
+    const int u = b * a.NT + n;
+    const int64_t ch = static_cast<int64_t>(u) * H + h;
+    const ChunkRows cr = chunk_rows(a, u);
+    float* DS = a.DS + ch * D * D;
+#pragma unroll
+    for (int i = 0; i < NI; ++i)
+#pragma unroll
+      for (int j = 0; j < 2; ++j) {
+        DS[(rm + 16 * i) * D + c0 + cn + 16 * j] = dS[i][j];
+        sS[(rm + 16 * i) * 33 + cn + 16 * j] = dS[i][j];
+      }
+    lds_load_rows<D>(sX, P, a.KL + ch * kC * D, kC, D, D, 0);
+    lds_load_rows<D>(sA, PC, a.AQ + ch * kC * kC, kC, kC, kC, 0);
+    for (int e = t; e < kC * 32; e += kThreads) {
+      const int c = e >> 5, j = e & 31;
+      sDo[c * 33 + j] = (c < cr.len) ? ld1<DO>(a.dout, ((cr.row0 + c) * H + h) * D + c0 + j) : 0.f;
+    }
+    if (t < D) sGC[t] = a.GCV[ch * D + t];
+    __syncthreads();
+    // dv~ = (lambda k) dS + Aqk^T do
+    {
+      float acc[4][2];
+#pragma unroll
+      for (int i = 0; i < 4; ++i) acc[i][0] = acc[i][1] = 0.f;
+      for (int d = 0; d < D; ++d) {
+        const float s0 = sS[d * 33 + cn], s1 = sS[d * 33 + cn + 16];
+#pragma unroll
+        for (int i = 0; i < 4; ++i) {
+          const float kl = sX[(rm + 16 * i) * P + d];
+          acc[i][0] = fmaf(kl, s0, acc[i][0]);
+          acc[i][1] = fmaf(kl, s1, acc[i][1]);
+        }
+      }
+      for (int c = 0; c < kC; ++c) {
+        const float o0 = sDo[c * 33 + cn], o1 = sDo[c * 33 + cn + 16];
+#pragma unroll
+        for (int i = 0; i < 4; ++i) {
+          const float av = sA[c * PC + rm + 16 * i];
+          acc[i][0] = fmaf(av, o0, acc[i][0]);
+          acc[i][1] = fmaf(av, o1, acc[i][1]);
+        }
+      }
+      float* DVT = a.DVT + ch * kC * D;
+#pragma unroll
+      for (int i = 0; i < 4; ++i)
+#pragma unroll
+        for (int j = 0; j < 2; ++j) {
+          sDv[(rm + 16 * i) * 33 + cn + 16 * j] = acc[i][j];
+          DVT[(rm + 16 * i) * D + c0 + cn + 16 * j] = acc[i][j];
+        }
+    }
+    __syncthreads();
+    lds_load_rows<D>(sX, P, a.QG + ch * kC * D, kC, D, D, 0);
+    lds_load_rows<D>(sY, P, a.WM + ch * kC * D, kC, D, D, 0);
+    __syncthreads();
+    // dS <- gamma_C dS + (gamma q)^T do - W^T dv~
+#pragma unroll
+    for (int i = 0; i < NI; ++i) {
+      const float gcv = sGC[rm + 16 * i];
+      dS[i][0] *= gcv;
+      dS[i][1] *= gcv;
+    }
+    for (int c = 0; c < kC; ++c) {
+      const float o0 = sDo[c * 33 + cn], o1 = sDo[c * 33 + cn + 16];
+      const float v0 = sDv[c * 33 + cn], v1 = sDv[c * 33 + cn + 16];
+#pragma unroll
+      for (int i = 0; i < NI; ++i) {
+        const float qg = sX[c * P + rm + 16 * i], w = sY[c * P + rm + 16 * i];
+        dS[i][0] = fmaf(qg, o0, fmaf(-w, v0, dS[i][0]));
+        dS[i][1] = fmaf(qg, o1, fmaf(-w, v1, dS[i][1]));
+      }
+    }
+    __syncthreads();
+  }
+  if (a.dh0 != nullptr) {
+#pragma unroll
+    for (int i = 0; i < NI; ++i)
+#pragma unroll
+      for (int j = 0; j < 2; ++j)
+        a.dh0[(static_cast<int64_t>(chain) * D + rm + 16 * i) * D + c0 + cn + 16 * j] = dS[i][j];
+  }
+}
+
+// ---------------------------------------------------------------------------
+// per chunk-head adjoint
+// ---------------------------------------------------------------------------
+template <int D, int DTQ, int DTG, int DO>
+__global__ __launch_bounds__(kThreads) void kda_bwd_chunk_kernel(BwdArgs a) {
+  typedef BwdDims<D> BD;
+  constexpr int P = BD::P, PC = BD::PC, NJ = BD::NJ;
+  constexpr int HW = 64;             // value columns per pass of phase 1
+  constexpr int NH = D / HW;
+  // phase 4 is the largest: dL, dAqk [64][65]; q, k, G [64][P]; three [16][P]
+  constexpr int SMEM_FLOATS = 2 * kC * PC + 3 * kC * P + 3 * 16 * P + kC;
+  __shared__ float sm[SMEM_FLOATS];
+  const int t = threadIdx.x, rm = t >> 4, cn = t & 15;
+  const int H = a.H;
+  const int u = blockIdx.x / H, h = blockIdx.x - u * H;
+  const ChunkRows cr = chunk_rows(a, u);
+  const int64_t ch = static_cast<int64_t>(u) * H + h;
+  const float* GL = a.GL + ch * kC * D;
+  auto in_idx = [&](int c, int d) { return ((cr.row0 + c) * H + h) * D + d; };
+  auto ld_q = [&](int c, int d) { return (c < cr.len) ? ld1<DTQ>(a.q, in_idx(c, d)) * a.scale : 0.f; };
+  auto ld_k = [&](int c, int d) { return (c < cr.len) ? ld1<DTQ>(a.k, in_idx(c, d)) : 0.f; };
+  auto ld_v = [&](int c, int d) { return (c < cr.len) ? ld1<DTQ>(a.v, in_idx(c, d)) : 0.f; };
+  auto ld_b = [&](int c) { return (c < cr.len) ? ld1<DTG>(a.beta, (cr.row0 + c) * H + h) : 0.f; };
+  auto ld_do = [&](int c, int d) { return (c < cr.len) ? ld1<DO>(a.dout, in_idx(c, d)) : 0.f; };
+
+  float dq[4][NJ], dk[4][NJ], dG[4][NJ], dbr[4], dzp[NJ];
+#pragma unroll
+  for (int i = 0; i < 4; ++i) {
+    dbr[i] = 0.f;
+#pragma unroll
+    for (int j = 0; j < NJ; ++j) dq[i][j] = dk[i][j] = dG[i][j] = 0.f;
+  }
+  float dgc = 0.f;   // thread t < D: sum_n S[t][n] dS'[t][n]
+
+  // ---- phase 1: dY = v~ dS'^T, dgq = do S^T, dW = -dv~ S^T (K = dv in passes of 64)
+  float dW[4][NJ];
+  {
+    float dY[4][NJ], dgq[4][NJ];
+#pragma unroll
+    for (int i = 0; i < 4; ++i)
+#pragma unroll
+      for (int j = 0; j < NJ; ++j) dY[i][j] = dgq[i][j] = dW[i][j] = 0.f;
+    float* sVt = sm;
+    float* sDo = sVt + kC * PC;
+    float* sDv = sDo + kC * PC;
+    float* sS = sDv + kC * PC;
+    float* sDS = sS + D * PC;
+    for (int hp = 0; hp < NH; ++hp) {
+      const int n0 = HW * hp;
+      lds_load_rows<D>(sVt, PC, a.VT + ch * kC * D, kC, HW, D, n0);
+      lds_load_rows<D>(sDv, PC, a.DVT + ch * kC * D, kC, HW, D, n0);
+      lds_load_rows<D>(sS, PC, a.SI + ch * D * D, D, HW, D, n0);
+      lds_load_rows<D>(sDS, PC, a.DS + ch * D * D, D, HW, D, n0);
+      for (int e = t; e < kC * HW; e += kThreads) {
+        const int c = e / HW, j = e - c * HW;
+        sDo[c * PC + j] = ld_do(c, n0 + j);
+      }
+      __syncthreads();
+      for (int nn = 0; nn < HW; ++nn) {
+        float va[4], oa[4], wa[4];
+#pragma unroll
+        for (int i = 0; i < 4; ++i) {
+          va[i] = sVt[(rm + 16 * i) * PC + nn];
+          oa[i] = sDo[(rm + 16 * i) * PC + nn];
+          wa[i] = sDv[(rm + 16 * i) * PC + nn];
+        }
+#pragma unroll
+        for (int j = 0; j < NJ; ++j) {
+          const float sv = sS[(cn + 16 * j) * PC + nn], dsv = sDS[(cn + 16 * j) * PC + nn];
+#pragma unroll
+          for (int i = 0; i < 4; ++i) {
+            dY[i][j] = fmaf(va[i], dsv, dY[i][j]);
+            dgq[i][j] = fmaf(oa[i], sv, dgq[i][j]);
+            dW[i][j] = fmaf(-wa[i], sv, dW[i][j]);
+          }
+        }
+      }
+      if (t < D) {
+        for (int nn = 0; nn < HW; ++nn) dgc = fmaf(sS[t * PC + nn], sDS[t * PC + nn], dgc);
+      }
+      __syncthreads();
+    }
+    // elementwise: dq = dgq gamma; dG += dgq q gamma; dk += dY lambda; dG -= dY k lambda
+#pragma unroll
+    for (int j = 0; j < NJ; ++j) dzp[j] = 0.f;
+#pragma unroll
+    for (int i = 0; i < 4; ++i) {
+      const int c = rm + 16 * i;
+#pragma unroll
+      for (int j = 0; j < NJ; ++j) {
+        const int d = cn + 16 * j;
+        const float gl = GL[c * D + d], glast = GL[(kC - 1) * D + d];
+        const float gam = ex2(gl), lam = ex2(glast - gl);
+        const float qv = ld_q(c, d), kv = ld_k(c, d);
+        dq[i][j] += dgq[i][j] * gam;
+        dG[i][j] += dgq[i][j] * qv * gam;
+        dk[i][j] += dY[i][j] * lam;
+        const float dz = dY[i][j] * kv * lam;
+        dG[i][j] -= dz;
+        dzp[j] += dz;
+      }
+    }
+  }
+
+  // ---- phase 2: Yw = T^T dW, Yu = T^T dv~
+  float Yw[4][NJ], Yu[4][NJ];
+  {
+    float* sT = sm;
+    float* sX = sT + kC * PC;
+    float* sY = sX + kC * P;
+#pragma unroll
+    for (int i = 0; i < 4; ++i)
+#pragma unroll
+      for (int j = 0; j < NJ; ++j) sX[(rm + 16 * i) * P + cn + 16 * j] = dW[i][j];
+    lds_load_rows<D>(sT, PC, a.TM + ch * kC * kC, kC, kC, kC, 0);
+    lds_load_rows<D>(sY, P, a.DVT + ch * kC * D, kC, D, D, 0);
+    __syncthreads();
+#pragma unroll
+    for (int i = 0; i < 4; ++i)
+#pragma unroll
+      for (int j = 0; j < NJ; ++j) Yw[i][j] = Yu[i][j] = 0.f;
+    for (int m = 0; m < kC; ++m) {
+      float tv[4];
+#pragma unroll
+      for (int i = 0; i < 4; ++i) tv[i] = sT[m * PC + rm + 16 * i];
+#pragma unroll
+      for (int j = 0; j < NJ; ++j) {
+        const float x = sX[m * P + cn + 16 * j], y = sY[m * P + cn + 16 * j];
+#pragma unroll
+        for (int i = 0; i < 4; ++i) {
+          Yw[i][j] = fmaf(tv[i], x, Yw[i][j]);
+          Yu[i][j] = fmaf(tv[i], y, Yu[i][j]);
+        }
+      }
+    }
+    __syncthreads();
+    // dgamma += Yw k beta; dk += Yw gamma beta; dv = Yu beta; dbeta += Yw gamma k + Yu v
+#pragma unroll
+    for (int i = 0; i < 4; ++i) {
+      const int c = rm + 16 * i;
+      const float bc = ld_b(c);
+#pragma unroll
+      for (int j = 0; j < NJ; ++j) {
+        const int d = cn + 16 * j;
+        const float gam = ex2(GL[c * D + d]);
+        const float kv = ld_k(c, d), vv = ld_v(c, d);
+        dG[i][j] += Yw[i][j] * kv * bc * gam;
+        dk[i][j] += Yw[i][j] * gam * bc;
+        dbr[i] += Yw[i][j] * gam * kv + Yu[i][j] * vv;
+        if (c < cr.len) a.dv[in_idx(c, d)] = Yu[i][j] * bc;
+      }
+    }
+  }
+
+  // ---- phase 3: dL = strict(-(Yw W^T + Yu U^T)), dAqk = tril(do v~^T)
+  float dLr[4][4], dAr[4][4];   // rows rm + 16i, columns cn + 16j
+  {
+    float* sX = sm;
+    float* sY = sX + kC * P;
+    float* sW = sY + kC * P;
+    float* sU = sW + kC * P;
+#pragma unroll
+    for (int i = 0; i < 4; ++i)
+#pragma unroll
+      for (int j = 0; j < NJ; ++j) {
+        sX[(rm + 16 * i) * P + cn + 16 * j] = Yw[i][j];
+        sY[(rm + 16 * i) * P + cn + 16 * j] = Yu[i][j];
+      }
+    lds_load_rows<D>(sW, P, a.WM + ch * kC * D, kC, D, D, 0);
+    lds_load_rows<D>(sU, P, a.UM + ch * kC * D, kC, D, D, 0);
+    __syncthreads();
+#pragma unroll
+    for (int i = 0; i < 4; ++i)
+#pragma unroll
+      for (int j = 0; j < 4; ++j) dLr[i][j] = dAr[i][j] = 0.f;
+    for (int d = 0; d < D; ++d) {
+      float yw[4], yu[4];
+#pragma unroll
+      for (int i = 0; i < 4; ++i) {
+        yw[i] = sX[(rm + 16 * i) * P + d];
+        yu[i] = sY[(rm + 16 * i) * P + d];
+      }
+#pragma unroll
+      for (int j = 0; j < 4; ++j) {
+        const float w = sW[(cn + 16 * j) * P + d], uu = sU[(cn + 16 * j) * P + d];
+#pragma unroll
+        for (int i = 0; i < 4; ++i) dLr[i][j] = fmaf(yw[i], w, fmaf(yu[i], uu, dLr[i][j]));
+      }
+    }
+    __syncthreads();
+    // do and v~ into the W / U slots
+    for (int e = t; e < kC * D; e += kThreads) {
+      const int c = e / D, d = e - c * D;
+      sW[c * P + d] = ld_do(c, d);
+    }
+    lds_load_rows<D>(sU, P, a.VT + ch * kC * D, kC, D, D, 0);
+    __syncthreads();
+    for (int d = 0; d < D; ++d) {
+      float ov[4];
+#pragma unroll
+      for (int i = 0; i < 4; ++i) ov[i] = sW[(rm + 16 * i) * P + d];
+#pragma unroll
+      for (int j = 0; j < 4; ++j) {
+        const float vv = sU[(cn + 16 * j) * P + d];
+#pragma unroll
+        for (int i = 0; i < 4; ++i) dAr[i][j] = fmaf(ov[i], vv, dAr[i][j]);
+      }
+    }
+    __syncthreads();
+  }
+
+  // ---- phase 4: score adjoints (Aqk with rows q, columns k; L with rows k beta, columns k)
+  {
+    float* sDL = sm;
+    float* sDA = sDL + kC * PC;
+    float* sQ = sDA + kC * PC;
+    float* sK = sQ + kC * P;
+    float* sG = sK + kC * P;
+    float* sXq = sG + kC * P;
+    float* sXk = sXq + 16 * P;
+    float* sKf = sXk + 16 * P;
+    float* sB = sKf + 16 * P;
+#pragma unroll
+    for (int i = 0; i < 4; ++i)
+#pragma unroll
+      for (int j = 0; j < 4; ++j) {
+        const int c = rm + 16 * i, ii = cn + 16 * j;
+        sDL[c * PC + ii] = (ii < c) ? -dLr[i][j] : 0.f;
+        sDA[c * PC + ii] = (ii <= c) ? dAr[i][j] : 0.f;
+      }
+    for (int e = t; e < kC * D; e += kThreads) {
+      const int c = e / D, d = e - c * D;
+      sQ[c * P + d] = ld_q(c, d);
+      sK[c * P + d] = ld_k(c, d);
+      sG[c * P + d] = GL[e];
+    }
+    if (t < kC) sB[t] = ld_b(t);
+    __syncthreads();
+#pragma unroll
+    for (int R = 0; R < 4; ++R) {
+      const int a0 = 16 * R;
+      for (int e = t; e < 16 * D; e += kThreads) {
+        const int rr = e / D, d = e - rr * D;
+        const float fr = ex2(sG[(a0 + rr) * P + d] - sG[a0 * P + d]);
+        sXq[rr * P + d] = sQ[(a0 + rr) * P + d] * fr;
+        sXk[rr * P + d] = sK[(a0 + rr) * P + d] * sB[a0 + rr] * fr;
+      }
+      float drA[NJ], drK[NJ];   // row c = a0 + rm: factorised part (times 2^(G_c - G_a) at the end)
+#pragma unroll
+      for (int j = 0; j < NJ; ++j) drA[j] = drK[j] = 0.f;
+      const int c = a0 + rm;
+#pragma unroll
+      for (int s = 0; s < R; ++s) {
+        __syncthreads();
+        for (int e = t; e < 16 * D; e += kThreads) {
+          const int ii = e / D, d = e - ii * D;
+          sKf[ii * P + d] = sK[(16 * s + ii) * P + d] * ex2(sG[a0 * P + d] - sG[(16 * s + ii) * P + d]);
+        }
+        __syncthreads();
+        // row side: dr[c] += sum_{i in s} D[c][i] k_i 2^(G_a - G_i)
+        for (int ii = 0; ii < 16; ++ii) {
+          const float da = sDA[c * PC + 16 * s + ii], dl = sDL[c * PC + 16 * s + ii];
+#pragma unroll
+          for (int j = 0; j < NJ; ++j) {
+            const float kf = sKf[ii * P + cn + 16 * j];
+            drA[j] = fmaf(da, kf, drA[j]);
+            drK[j] = fmaf(dl, kf, drK[j]);
+          }
+        }
+        // column side for key row i = 16s + rm: sum_{c' in R} D[c'][i] x_c' 2^(G_c' - G_a), times 2^(G_a - G_i)
+        {
+          const int i = 16 * s + rm;
+          float dcA[NJ], dcK[NJ];
+#pragma unroll
+          for (int j = 0; j < NJ; ++j) dcA[j] = dcK[j] = 0.f;
+          for (int rr = 0; rr < 16; ++rr) {
+            const float da = sDA[(a0 + rr) * PC + i], dl = sDL[(a0 + rr) * PC + i];
+#pragma unroll
+            for (int j = 0; j < NJ; ++j) {
+              dcA[j] = fmaf(da, sXq[rr * P + cn + 16 * j], dcA[j]);
+              dcK[j] = fmaf(dl, sXk[rr * P + cn + 16 * j], dcK[j]);
+            }
+          }
+#pragma unroll
+          for (int j = 0; j < NJ; ++j) {
+            const int d = cn + 16 * j;
+            const float fk = ex2(sG[a0 * P + d] - sG[i * P + d]);
+            const float sum = (dcA[j] + dcK[j]) * fk;
+            dk[s][j] += sum;
+            dG[s][j] -= sum * sK[i * P + d];
+          }
+        }
+      }
+      // diagonal tile and the row-side totals
+      {
+        const int i = a0 + rm;   // the same row, as a key row of the diagonal tile
+#pragma unroll
+        for (int j = 0; j < NJ; ++j) {
+          const int d = cn + 16 * j;
+          const float gc = sG[c * P + d];
+          float rA = drA[j] * ex2(gc - sG[a0 * P + d]);
+          float rK = drK[j] * ex2(gc - sG[a0 * P + d]);
+          float cA = 0.f, cK = 0.f;
+          for (int ii = 0; ii <= rm; ++ii) {
+            const int ik = a0 + ii;
+            const float e = ex2(gc - sG[ik * P + d]);
+            const float ke = sK[ik * P + d] * e;
+            rA = fmaf(sDA[c * PC + ik], ke, rA);
+            rK = fmaf(sDL[c * PC + ik], ke, rK);
+          }
+          const float gi = sG[i * P + d];
+          for (int rr = rm; rr < 16; ++rr) {
+            const int cc = a0 + rr;
+            const float e = ex2(sG[cc * P + d] - gi);
+            cA = fmaf(sDA[cc * PC + i], sQ[cc * P + d] * e, cA);
+            cK = fmaf(sDL[cc * PC + i], sK[cc * P + d] * sB[cc] * e, cK);
+          }
+          const float qv = sQ[c * P + d], kv = sK[c * P + d], bc = sB[c];
+          dq[R][j] += rA;
+          dG[R][j] += rA * qv + rK * kv * bc;
+          dk[R][j] += rK * bc + cA + cK;
+          dbr[R] += rK * kv;
+          dG[R][j] -= (cA + cK) * kv;
+        }
+      }
+      __syncthreads();
+    }
+  }
+
+  // ---- outputs: dq, dk, dbeta, dg (reverse cumsum of dG plus the G_C terms)
+  {
+    float* sDG = sm;                   // [64][P]
+    float* sRed = sDG + kC * P;        // [16][D] column partial sums of dz
+    float* sDb = sRed + 16 * D;        // [64][16] row partial sums of dbeta
+#pragma unroll
+    for (int i = 0; i < 4; ++i) {
+      const int c = rm + 16 * i;
+#pragma unroll
+      for (int j = 0; j < NJ; ++j) {
+        const int d = cn + 16 * j;
+        sDG[c * P + d] = dG[i][j];
+        if (c < cr.len) {
+          a.dq[in_idx(c, d)] = dq[i][j] * a.scale;
+          a.dk[in_idx(c, d)] = dk[i][j];
+        }
+      }
+      sDb[c * 16 + cn] = dbr[i];
+    }
+#pragma unroll
+    for (int j = 0; j < NJ; ++j) sRed[rm * D + cn + 16 * j] = dzp[j];
+    __syncthreads();
+    if (t < D) {
+      float acc = dgc * ex2(GL[(kC - 1) * D + t]);
+      for (int r = 0; r < 16; ++r) acc += sRed[r * D + t];
+      for (int c = kC - 1; c >= 0; --c) {
+        acc += sDG[c * P + t];
+        if (c < cr.len) a.dg[in_idx(c, t)] = acc;
+      }
+    }
+    if (t < kC && t < cr.len) {
+      float acc = 0.f;
+      for (int j = 0; j < 16; ++j) acc += sDb[t * 16 + j];
+      a.dbeta[(cr.row0 + t) * H + h] = acc;
+    }
+  }
+}
+
+template <int D, int DTQ, int DTG, int DO>
+hipError_t launch_bwd_t(const BwdArgs& a, hipStream_t s) {
+  const int chunk_heads = a.B * a.NT * a.H;
+  const int chains = a.B * a.H;
+  hipLaunchKernelGGL((kda_bwd_prep_kernel<D, DTQ, DTG>), dim3(chunk_heads), dim3(kThreads), 0, s, a);
+  hipError_t e = hipGetLastError();
+  if (e != hipSuccess) return e;
+  hipLaunchKernelGGL((kda_bwd_fscan_kernel<D>), dim3(chains * (D / 32)), dim3(kThreads), 0, s, a);
+  e = hipGetLastError();
+  if (e != hipSuccess) return e;
+  hipLaunchKernelGGL((kda_bwd_rscan_kernel<D, DO>), dim3(chains * (D / 32)), dim3(kThreads), 0, s, a);
+  e = hipGetLastError();
+  if (e != hipSuccess) return e;
+  hipLaunchKernelGGL((kda_bwd_chunk_kernel<D, DTQ, DTG, DO>), dim3(chunk_heads), dim3(kThreads), 0, s, a);
+  return hipGetLastError();
+}
+
+template <int D, int DO>
+hipError_t launch_bwd_dt(const BwdArgs& a, int in_dtype, hipStream_t s) {
+  switch (in_dtype) {
+    case 0: return launch_bwd_t<D, 0, 0, DO>(a, s);
+    case 1: return launch_bwd_t<D, 1, 1, DO>(a, s);
+    case 2: return launch_bwd_t<D, 2, 2, DO>(a, s);
+    default: return launch_bwd_t<D, 1, 0, DO>(a, s);
+  }
+}
+
+__global__ __launch_bounds__(kThreads) void kda_copy_or_zero_kernel(float* dst, const float* src, int64_t n) {
+  for (int64_t i = static_cast<int64_t>(blockIdx.x) * kThreads + threadIdx.x; i < n;
+       i += static_cast<int64_t>(gridDim.x) * kThreads)
+    dst[i] = (src != nullptr) ? src[i] : 0.f;
+}
+
+}  // namespace
+
+hipError_t launch_copy_or_zero(float* dst, const float* src, int64_t n, hipStream_t s) {
+  if (n <= 0) return hipSuccess;
+  const int64_t blocks = (n + kThreads - 1) / kThreads;
+  const int grid = static_cast<int>(blocks < 4096 ? blocks : 4096);
+  hipLaunchKernelGGL(kda_copy_or_zero_kernel, dim3(grid), dim3(kThreads), 0, s, dst, src, n);
+  return hipGetLastError();
+}
+
+hipError_t launch_bwd(const BwdArgs& a, int d, int in_dtype, int do_dtype, hipStream_t s) {
+  if (d == 128) return do_dtype == 0 ? launch_bwd_dt<128, 0>(a, in_dtype, s) : launch_bwd_dt<128, 1>(a, in_dtype, s);
+  return do_dtype == 0 ? launch_bwd_dt<64, 0>(a, in_dtype, s) : launch_bwd_dt<64, 1>(a, in_dtype, s);
+}
+
+}  // namespace kda

@@ -70,6 +70,42 @@ struct AdaptArgs {
   int dk;
 };
 
+// Chunked backward (dense inputs; all workspace arrays fp32, row-major,
+// per chunk-head ch = (b * NT + n) * H + h).
+struct BwdArgs {
+  int B, T, H, NT;
+  const void* q;
+  const void* k;
+  const void* v;
+  const void* g;
+  const void* beta;
+  const float* h0;      // [B,H,dk,dv] or null
+  const void* dout;     // cotangent of o, [B,T,H,dv] (fp32 or bf16)
+  const float* dht;     // cotangent of the final state, [B,H,dk,dv] or null
+  float scale;
+  float* dq;            // [B,T,H,dk]
+  float* dk;
+  float* dv;            // [B,T,H,dv]
+  float* dg;            // [B,T,H,dk]
+  float* dbeta;         // [B,T,H]
+  float* dh0;           // [B,H,dk,dv] or null
+  float* GL;            // [ch][C][dk] in-chunk cumsum of g, log2 units
+  float* QG;            // [ch][C][dk] gamma * q (scaled)
+  float* KL;            // [ch][C][dk] lambda * k
+  float* GCV;           // [ch][dk]    gamma_C
+  float* AQ;            // [ch][C][C]  Aqk
+  float* TM;            // [ch][C][C]  (I + L)^-1
+  float* WM;            // [ch][C][dk]
+  float* UM;            // [ch][C][dv]
+  float* SI;            // [ch][dk][dv] state entering the chunk
+  float* VT;            // [ch][C][dv] v~
+  float* DS;            // [ch][dk][dv] cotangent of the state leaving the chunk
+  float* DVT;           // [ch][C][dv] cotangent of v~
+};
+
+hipError_t launch_bwd(const BwdArgs& a, int d, int in_dtype, int do_dtype, hipStream_t s);
+// dst[0..n) = src (or 0 when src is null), by a kernel (no memset/memcpy node)
+hipError_t launch_copy_or_zero(float* dst, const float* src, int64_t n, hipStream_t s);
 hipError_t launch_intra(const IntraArgs& a, int d, int dtq, int dtg, int grid, hipStream_t s);
 hipError_t launch_state(const StateArgs& a, int d, bool exact, int out_dt, int grid, hipStream_t s);
 hipError_t launch_varlen_prep(const int32_t* cu, int N, int T, int32_t* cu_clamped,

@@ -12,6 +12,9 @@ Mirrors the reference's interface for this path (romannekrasovaillm/axiom):
   batch, ragged lengths and varlen packing.
 * :func:`kda_recurrent_step` -- one decode token, the delta rule of
   ``net/kda.py:298-310`` plus the read-out ``net/kda.py:293``, state in place.
+* :func:`kda_chunk_bwd` / :func:`kda_chunk` -- the chunked backward (the
+  ``cc_scan`` custom_vjp's backward rule, ``net/kernels/kda_cc_fused_persist.py:1707``)
+  and a differentiable ``torch.autograd.Function`` over forward + backward.
 
 Every function calls the HIP library through its C ABI on torch's current
 stream; nothing here computes on the CPU.
@@ -131,6 +134,107 @@ def kda_chunk_fwd(q, k, v, g, beta, initial_state=None, cu_seqlens=None, chunk_s
                          _ptr(workspace), ws_bytes)
     _lib.check(rc, what)
     return o, ht
+
+
+def chunk_bwd_workspace_bytes(B, T, H, dk, dv) -> int:
+    return int(_lib.lib().kda_chunk_bwd_workspace(B, T, H, dk, dv, CHUNK))
+
+
+def kda_chunk_bwd(q, k, v, g, beta, do, dht=None, initial_state=None, scale: float = 1.0,
+                  chunk_size: int = 64, need_dh0: bool = True, workspace=None):
+    """Gradients of ``kda_chunk_fwd`` (dense inputs, no ``cu_seqlens``).
+
+    ``do [B,T,H,dv]`` (fp32 or bf16) and ``dht [B,H,dk,dv]`` fp32 (None = 0)
+    are the cotangents of ``o`` and of the final state.  Returns fp32
+    ``(dq, dk, dv, dg, dbeta, dh0)`` (``dh0`` None unless ``need_dh0``);
+    ``dg`` is the cotangent of the log decay ``g``.  The backward rule of the
+    reference's ``cc_scan`` (``net/kernels/kda_cc_fused_persist.py:1707``).
+    """
+    what = "kda_chunk_bwd"
+    if q.dim() != 4 or k.shape != q.shape or g.shape != q.shape:
+        raise ValueError(f"{what}: q, k, g must share a [B,T,H,dk] shape")
+    B, T, H, dk = q.shape
+    if v.dim() != 4 or v.shape[:3] != q.shape[:3]:
+        raise ValueError(f"{what}: v must be [B,T,H,dv] matching q")
+    dv = v.shape[3]
+    if tuple(beta.shape) != (B, T, H):
+        raise ValueError(f"{what}: beta must be [B,T,H] = {(B, T, H)}, got {tuple(beta.shape)}")
+    if chunk_size != CHUNK:
+        raise ValueError(f"{what}: chunk_size={chunk_size} unsupported (this build runs {CHUNK})")
+    _check_dims(dk, dv, what)
+    if q.dtype not in _IN_CODES or k.dtype != q.dtype or v.dtype != q.dtype:
+        raise ValueError(f"{what}: q, k, v must share a dtype in bf16/fp16/fp32")
+    if g.dtype == q.dtype and beta.dtype == q.dtype:
+        in_code = _IN_CODES[q.dtype]
+    elif q.dtype == torch.bfloat16 and g.dtype == torch.float32 and beta.dtype == torch.float32:
+        in_code = _lib.KDA_DTYPE_BF16_F32GATES
+    else:
+        raise ValueError(f"{what}: g/beta dtype must equal q's, or be fp32 with bf16 q/k/v")
+    if tuple(do.shape) != (B, T, H, dv) or do.dtype not in _OUT_CODES:
+        raise ValueError(f"{what}: do must be fp32 or bf16 [{B},{T},{H},{dv}]")
+    for name, st in (("dht", dht), ("initial_state", initial_state)):
+        if st is not None and (st.dtype != torch.float32 or tuple(st.shape) != (B, H, dk, dv)):
+            raise ValueError(f"{what}: {name} must be fp32 [{B},{H},{dk},{dv}]")
+    for name, t in (("q", q), ("k", k), ("v", v), ("g", g), ("beta", beta), ("do", do),
+                    ("dht", dht), ("initial_state", initial_state)):
+        if t is not None:
+            _contig(name, t)
+    dev = _require_gpu([q, k, v, g, beta, do, dht, initial_state], what)
+    L = _lib.lib()
+    ws_bytes = int(L.kda_chunk_bwd_workspace(B, T, H, dk, dv, CHUNK))
+    if ws_bytes == 0:
+        raise ValueError(f"{what}: unsupported configuration")
+    if workspace is None or workspace.numel() * workspace.element_size() < ws_bytes:
+        workspace = torch.empty(max(ws_bytes, 1), dtype=torch.uint8, device=dev)
+    f32 = torch.float32
+    dq = torch.empty((B, T, H, dk), dtype=f32, device=dev)
+    dk_ = torch.empty((B, T, H, dk), dtype=f32, device=dev)
+    dv_ = torch.empty((B, T, H, dv), dtype=f32, device=dev)
+    dg = torch.empty((B, T, H, dk), dtype=f32, device=dev)
+    dbeta = torch.empty((B, T, H), dtype=f32, device=dev)
+    dh0 = torch.empty((B, H, dk, dv), dtype=f32, device=dev) if need_dh0 else None
+    rc = L.kda_chunk_bwd(_stream(dev), _ptr(q), _ptr(k), _ptr(v), _ptr(g), _ptr(beta),
+                         _ptr(initial_state), _ptr(do), _ptr(dht),
+                         _ptr(dq), _ptr(dk_), _ptr(dv_), _ptr(dg), _ptr(dbeta), _ptr(dh0),
+                         B, T, H, dk, dv, CHUNK, float(scale), in_code, _OUT_CODES[do.dtype],
+                         _ptr(workspace), ws_bytes)
+    _lib.check(rc, what)
+    return dq, dk_, dv_, dg, dbeta, dh0
+
+
+class _KDAChunk(torch.autograd.Function):
+    """``(o, final_state)`` of the chunked forward with the HIP backward as its VJP."""
+
+    @staticmethod
+    def forward(ctx, q, k, v, g, beta, initial_state, scale):
+        o, ht = kda_chunk_fwd(q, k, v, g, beta, initial_state=initial_state, scale=scale)
+        ctx.save_for_backward(q, k, v, g, beta, initial_state)
+        ctx.scale = scale
+        return o, ht
+
+    @staticmethod
+    def backward(ctx, do, dht):
+        q, k, v, g, beta, h0 = ctx.saved_tensors
+        if do is None:
+            do = torch.zeros(q.shape[:3] + (v.shape[3],), dtype=torch.float32, device=q.device)
+        do = do.contiguous()
+        if do.dtype not in _OUT_CODES:
+            do = do.float()
+        dht = None if dht is None else dht.float().contiguous()
+        dq, dk, dv, dg, dbeta, dh0 = kda_chunk_bwd(q, k, v, g, beta, do, dht=dht, initial_state=h0,
+                                                   scale=ctx.scale, need_dh0=ctx.needs_input_grad[5])
+        return (dq.to(q.dtype), dk.to(k.dtype), dv.to(v.dtype), dg.to(g.dtype), dbeta.to(beta.dtype),
+                dh0, None)
+
+
+def kda_chunk(q, k, v, g, beta, initial_state=None, scale: float = 1.0):
+    """Differentiable chunked KDA: ``(o, final_state)`` with the HIP backward.
+
+    Dense ``[B,T,H,d]`` inputs as :func:`kda_chunk_fwd`; gradients flow to q,
+    k, v, g, beta and ``initial_state`` (cast back to their dtypes, as the
+    reference's ``custom_vjp`` returns primal dtypes).
+    """
+    return _KDAChunk.apply(q, k, v, g, beta, initial_state, scale)
 
 
 def varlen_status(workspace, B, T, H, dk, dv, n_seqs, in_code=_lib.KDA_DTYPE_BF16) -> int:

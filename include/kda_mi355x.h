@@ -141,6 +141,32 @@ KDA_API int kda_cc_scan(hipStream_t stream,
 /* Workspace bytes kda_cc_scan needs (0 on bad input).  Host-only. */
 KDA_API size_t kda_cc_scan_workspace(int T, int H, int dk, int dv, int chunk);
 
+/*
+ * Chunked backward: gradients of (o, final state) = kda_chunk_fwd(q, k, v, g,
+ * beta, h0) for dense [B,T,H,d] inputs (no cu_seqlens).  Replaces the
+ * reference's backward rule of the cc_scan custom_vjp,
+ *   net/kernels/kda_cc_fused_persist.py:1707  kernel_bwd(q, k, v, alpha, beta32, S, do, dS)
+ *   (the reverse scan of the per-chunk adjoint, :794-842 and
+ *   net/kernels/kda_cc_fused_bwd.py:117-228),
+ * in the FLA-style layout of kda_chunk_fwd.  dout [B,T,H,dv] is the cotangent
+ * of o (dout_dtype KDA_DTYPE_F32 or KDA_DTYPE_BF16), dht [B,H,dk,dv] fp32 the
+ * cotangent of the final state (null = 0), h0 as in the forward (null = 0).
+ * Outputs, all fp32: dq, dk, dg [B,T,H,dk], dv [B,T,H,dv], dbeta [B,T,H] and,
+ * when dh0 is not null, dh0 [B,H,dk,dv].  dg is the cotangent of the log
+ * decay g (the reference's alpha form has dalpha = dg / alpha).  q, k, v, g,
+ * beta, in_dtype, scale and chunk as in kda_chunk_fwd; the workspace is
+ * caller-owned, kda_chunk_bwd_workspace bytes.
+ */
+KDA_API int kda_chunk_bwd(hipStream_t stream,
+                const void* q, const void* k, const void* v, const void* g, const void* beta,
+                const float* h0, const void* dout, const float* dht,
+                float* dq, float* dk, float* dv, float* dg, float* dbeta, float* dh0,
+                int B, int T, int H, int dk_dim, int dv_dim, int chunk, float scale,
+                int in_dtype, int dout_dtype, void* workspace, size_t workspace_bytes);
+
+/* Workspace bytes kda_chunk_bwd needs (0 on bad input).  Host-only. */
+KDA_API size_t kda_chunk_bwd_workspace(int B, int T, int H, int dk_dim, int dv_dim, int chunk);
+
 /* Message of the last failure on the calling thread ("" if none). */
 KDA_API const char* kda_last_error(void);
 
