@@ -36,6 +36,9 @@ namespace {
 
 constexpr int kC = 64;
 constexpr int kThreads = 256;
+// The per-chunk adjoint runs 512 threads (two waves per SIMD): it is bound by
+// latency at one workgroup per CU (its LDS), so the second wave per SIMD hides it.
+constexpr int kChunkThreads = 512;
 
 __device__ __forceinline__ float ex2(float x) { return __builtin_amdgcn_exp2f(x); }
 
@@ -60,13 +63,82 @@ __device__ __forceinline__ ChunkRows chunk_rows(const BwdArgs& a, int u) {
   return r;
 }
 
-// [64][D] block of a row-major fp32 workspace array into LDS (pitch P).
-template <int D>
-__device__ __forceinline__ void lds_load_rows(float* dst, int pitch, const float* src, int rows, int cols,
-                                              int src_ld, int col0) {
-  for (int e = threadIdx.x; e < rows * cols; e += kThreads) {
-    const int r = e / cols, c = e - r * cols;
-    dst[r * pitch + c] = src[static_cast<int64_t>(r) * src_ld + col0 + c];
+// ROWS x COLS block of a row-major fp32 array (row stride src_ld floats,
+// first column col0) into LDS rows of pitch PITCH.  All of a thread's 16-byte
+// loads are issued before its LDS writes, so they are in flight together.
+template <int ROWS, int COLS, int PITCH, int NTH = kThreads>
+__device__ __forceinline__ void lds_load(float* dst, const float* src, int src_ld, int col0) {
+  constexpr int V = COLS / 4;
+  constexpr int N = ROWS * V;
+  constexpr int PER = (N + NTH - 1) / NTH;
+  static_assert(COLS % 4 == 0, "16-byte loads");
+  float4 tmp[PER];
+#pragma unroll
+  for (int p = 0; p < PER; ++p) {
+    const int e = threadIdx.x + p * NTH;
+    if (N % NTH == 0 || e < N) {
+      const int r = e / V, c4 = e - r * V;
+      tmp[p] = *reinterpret_cast<const float4*>(src + static_cast<int64_t>(r) * src_ld + col0 + 4 * c4);
+    }
+  }
+#pragma unroll
+  for (int p = 0; p < PER; ++p) {
+    const int e = threadIdx.x + p * NTH;
+    if (N % NTH == 0 || e < N) {
+      const int r = e / V, c4 = e - r * V;
+      float* d = dst + r * PITCH + 4 * c4;
+      d[0] = tmp[p].x;
+      d[1] = tmp[p].y;
+      d[2] = tmp[p].z;
+      d[3] = tmp[p].w;
+    }
+  }
+}
+
+// Eight consecutive elements of an input tensor (DT 0 fp32, 1 bf16, 2 fp16)
+// as fp32.
+template <int DT>
+__device__ __forceinline__ void ld8(const void* p, int64_t i, float (&o)[8]) {
+  if constexpr (DT == 0) {
+    const float4 a = *reinterpret_cast<const float4*>(static_cast<const float*>(p) + i);
+    const float4 b = *reinterpret_cast<const float4*>(static_cast<const float*>(p) + i + 4);
+    o[0] = a.x; o[1] = a.y; o[2] = a.z; o[3] = a.w;
+    o[4] = b.x; o[5] = b.y; o[6] = b.z; o[7] = b.w;
+  } else {
+    const uint4 w = *reinterpret_cast<const uint4*>(static_cast<const u16*>(p) + i);
+    const f4 lo = unpack4<DT>(make_uint2(w.x, w.y)), hi = unpack4<DT>(make_uint2(w.z, w.w));
+#pragma unroll
+    for (int e = 0; e < 4; ++e) { o[e] = lo[e]; o[4 + e] = hi[e]; }
+  }
+}
+
+// Columns [col0, col0 + COLS) of the 64 rows of a chunk of a token-major
+// input tensor [*, H, D] (rows past `len` read as zero), times mul, into LDS
+// rows of pitch PITCH.  Loads issued together, 8 elements per load.
+template <int DT, int D, int COLS, int PITCH, int NTH = kThreads>
+__device__ __forceinline__ void lds_load_in(float* dst, const void* src, int64_t row0, int len, int H, int h,
+                                            int col0, float mul) {
+  constexpr int V = COLS / 8;
+  constexpr int N = kC * V;
+  constexpr int PER = (N + NTH - 1) / NTH;
+  static_assert(COLS % 8 == 0, "8-element loads");
+  float tmp[PER][8];
+#pragma unroll
+  for (int p = 0; p < PER; ++p) {
+    const int e = threadIdx.x + p * NTH;
+    const int r = e / V, c8 = e - r * V;
+#pragma unroll
+    for (int x = 0; x < 8; ++x) tmp[p][x] = 0.f;
+    if ((N % NTH == 0 || e < N) && r < len) ld8<DT>(src, ((row0 + r) * H + h) * D + col0 + 8 * c8, tmp[p]);
+  }
+#pragma unroll
+  for (int p = 0; p < PER; ++p) {
+    const int e = threadIdx.x + p * NTH;
+    if (N % NTH == 0 || e < N) {
+      const int r = e / V, c8 = e - r * V;
+#pragma unroll
+      for (int x = 0; x < 8; ++x) dst[r * PITCH + 8 * c8 + x] = tmp[p][x] * mul;
+    }
   }
 }
 
@@ -87,19 +159,9 @@ __global__ __launch_bounds__(kThreads) void kda_bwd_prep_kernel(BwdArgs a) {
   const ChunkRows cr = chunk_rows(a, u);
   const int64_t ch = static_cast<int64_t>(u) * H + h;
 
-  for (int e = t; e < kC * D; e += kThreads) {
-    const int c = e / D, d = e - c * D;
-    float qv = 0.f, kv = 0.f, gv = 0.f;
-    if (c < cr.len) {
-      const int64_t idx = ((cr.row0 + c) * H + h) * D + d;
-      qv = ld1<DTQ>(a.q, idx) * a.scale;
-      kv = ld1<DTQ>(a.k, idx);
-      gv = ld1<DTG>(a.g, idx);
-    }
-    sQ[c * P + d] = qv;
-    sK[c * P + d] = kv;
-    sG[c * P + d] = gv;
-  }
+  lds_load_in<DTQ, D, D, P>(sQ, a.q, cr.row0, cr.len, H, h, 0, a.scale);
+  lds_load_in<DTQ, D, D, P>(sK, a.k, cr.row0, cr.len, H, h, 0, 1.f);
+  lds_load_in<DTG, D, D, P>(sG, a.g, cr.row0, cr.len, H, h, 0, 1.f);
   if (t < kC) sB[t] = (t < cr.len) ? ld1<DTG>(a.beta, (cr.row0 + t) * H + h) : 0.f;
   __syncthreads();
   // in-chunk inclusive cumsum of g, in log2 units
@@ -146,6 +208,7 @@ __global__ __launch_bounds__(kThreads) void kda_bwd_prep_kernel(BwdArgs a) {
       }
       __syncthreads();
       float accA = 0.f, accL = 0.f;
+      #pragma unroll 4
       for (int d = 0; d < D; ++d) {
         const float kf = sKf[i16 * P + d];
         accA = fmaf(sX0[r * P + d], kf, accA);
@@ -159,6 +222,7 @@ __global__ __launch_bounds__(kThreads) void kda_bwd_prep_kernel(BwdArgs a) {
       const int c = a0 + r, i = a0 + i16;
       float accA = 0.f, accL = 0.f;
       if (i16 <= r) {
+        #pragma unroll 4
         for (int d = 0; d < D; ++d) {
           const float e = ex2(sG[c * P + d] - sG[i * P + d]);
           const float ki = sK[i * P + d] * e;
@@ -219,12 +283,12 @@ __global__ __launch_bounds__(kThreads) void kda_bwd_prep_kernel(BwdArgs a) {
     }
   }
   // W = T (beta gamma k), U = T (beta v)
+  lds_load_in<DTQ, D, D, P>(sQ, a.v, cr.row0, cr.len, H, h, 0, 1.f);
+  __syncthreads();
   for (int e = t; e < kC * D; e += kThreads) {
     const int c = e / D, d = e - c * D;
     sK[c * P + d] *= sB[c] * ex2(sG[c * P + d]);
-    float vv = 0.f;
-    if (c < cr.len) vv = ld1<DTQ>(a.v, ((cr.row0 + c) * H + h) * D + d);
-    sQ[c * P + d] = vv * sB[c];
+    sQ[c * P + d] *= sB[c];
   }
   __syncthreads();
   {
@@ -235,6 +299,7 @@ __global__ __launch_bounds__(kThreads) void kda_bwd_prep_kernel(BwdArgs a) {
     for (int i = 0; i < 4; ++i)
 #pragma unroll
       for (int j = 0; j < NJ; ++j) accW[i][j] = accU[i][j] = 0.f;
+    #pragma unroll 4
     for (int m = 0; m < kC; ++m) {
       float tv[4];
 #pragma unroll
@@ -294,9 +359,9 @@ __global__ __launch_bounds__(kThreads) void kda_bwd_fscan_kernel(BwdArgs a) {
         SI[(rm + 16 * i) * D + c0 + cn + 16 * j] = S[i][j];
         sS[(rm + 16 * i) * 33 + cn + 16 * j] = S[i][j];
       }
-    lds_load_rows<D>(sW, P, a.WM + ch * kC * D, kC, D, D, 0);
-    lds_load_rows<D>(sKL, P, a.KL + ch * kC * D, kC, D, D, 0);
-    lds_load_rows<D>(sU, 33, a.UM + ch * kC * D, kC, 32, D, c0);
+    lds_load<kC, D, P>(sW, a.WM + ch * kC * D, D, 0);
+    lds_load<kC, D, P>(sKL, a.KL + ch * kC * D, D, 0);
+    lds_load<kC, 32, 33>(sU, a.UM + ch * kC * D, D, c0);
     if (t < D) sGC[t] = a.GCV[ch * D + t];
     __syncthreads();
     // v~ = U - W S: rows rm + 16i (i < 4), columns cn + 16j (j < 2)
@@ -306,6 +371,7 @@ __global__ __launch_bounds__(kThreads) void kda_bwd_fscan_kernel(BwdArgs a) {
       for (int i = 0; i < 4; ++i)
 #pragma unroll
         for (int j = 0; j < 2; ++j) acc[i][j] = sU[(rm + 16 * i) * 33 + cn + 16 * j];
+      #pragma unroll 4
       for (int d = 0; d < D; ++d) {
         const float s0 = sS[d * 33 + cn], s1 = sS[d * 33 + cn + 16];
 #pragma unroll
@@ -332,6 +398,7 @@ __global__ __launch_bounds__(kThreads) void kda_bwd_fscan_kernel(BwdArgs a) {
       S[i][0] *= gcv;
       S[i][1] *= gcv;
     }
+    #pragma unroll 4
     for (int c = 0; c < kC; ++c) {
       const float v0 = sV[c * 33 + cn], v1 = sV[c * 33 + cn + 16];
 #pragma unroll
@@ -380,12 +447,9 @@ __global__ __launch_bounds__(kThreads) void kda_bwd_rscan_kernel(BwdArgs a) {
         DS[(rm + 16 * i) * D + c0 + cn + 16 * j] = dS[i][j];
         sS[(rm + 16 * i) * 33 + cn + 16 * j] = dS[i][j];
       }
-    lds_load_rows<D>(sX, P, a.KL + ch * kC * D, kC, D, D, 0);
-    lds_load_rows<D>(sA, PC, a.AQ + ch * kC * kC, kC, kC, kC, 0);
-    for (int e = t; e < kC * 32; e += kThreads) {
-      const int c = e >> 5, j = e & 31;
-      sDo[c * 33 + j] = (c < cr.len) ? ld1<DO>(a.dout, ((cr.row0 + c) * H + h) * D + c0 + j) : 0.f;
-    }
+    lds_load<kC, D, P>(sX, a.KL + ch * kC * D, D, 0);
+    lds_load<kC, kC, PC>(sA, a.AQ + ch * kC * kC, kC, 0);
+    lds_load_in<DO, D, 32, 33>(sDo, a.dout, cr.row0, cr.len, H, h, c0, 1.f);
     if (t < D) sGC[t] = a.GCV[ch * D + t];
     __syncthreads();
     // dv~ = (lambda k) dS + Aqk^T do
@@ -393,6 +457,7 @@ __global__ __launch_bounds__(kThreads) void kda_bwd_rscan_kernel(BwdArgs a) {
       float acc[4][2];
 #pragma unroll
       for (int i = 0; i < 4; ++i) acc[i][0] = acc[i][1] = 0.f;
+      #pragma unroll 4
       for (int d = 0; d < D; ++d) {
         const float s0 = sS[d * 33 + cn], s1 = sS[d * 33 + cn + 16];
 #pragma unroll
@@ -402,6 +467,7 @@ __global__ __launch_bounds__(kThreads) void kda_bwd_rscan_kernel(BwdArgs a) {
           acc[i][1] = fmaf(kl, s1, acc[i][1]);
         }
       }
+      #pragma unroll 4
       for (int c = 0; c < kC; ++c) {
         const float o0 = sDo[c * 33 + cn], o1 = sDo[c * 33 + cn + 16];
 #pragma unroll
@@ -421,8 +487,8 @@ __global__ __launch_bounds__(kThreads) void kda_bwd_rscan_kernel(BwdArgs a) {
         }
     }
     __syncthreads();
-    lds_load_rows<D>(sX, P, a.QG + ch * kC * D, kC, D, D, 0);
-    lds_load_rows<D>(sY, P, a.WM + ch * kC * D, kC, D, D, 0);
+    lds_load<kC, D, P>(sX, a.QG + ch * kC * D, D, 0);
+    lds_load<kC, D, P>(sY, a.WM + ch * kC * D, D, 0);
     __syncthreads();
     // dS <- gamma_C dS + (gamma q)^T do - W^T dv~
 #pragma unroll
@@ -431,6 +497,7 @@ __global__ __launch_bounds__(kThreads) void kda_bwd_rscan_kernel(BwdArgs a) {
       dS[i][0] *= gcv;
       dS[i][1] *= gcv;
     }
+    #pragma unroll 4
     for (int c = 0; c < kC; ++c) {
       const float o0 = sDo[c * 33 + cn], o1 = sDo[c * 33 + cn + 16];
       const float v0 = sDv[c * 33 + cn], v1 = sDv[c * 33 + cn + 16];
@@ -456,15 +523,19 @@ __global__ __launch_bounds__(kThreads) void kda_bwd_rscan_kernel(BwdArgs a) {
 // per chunk-head adjoint
 // ---------------------------------------------------------------------------
 template <int D, int DTQ, int DTG, int DO>
-__global__ __launch_bounds__(kThreads) void kda_bwd_chunk_kernel(BwdArgs a) {
+__global__ __launch_bounds__(kChunkThreads) void kda_bwd_chunk_kernel(BwdArgs a) {
   typedef BwdDims<D> BD;
-  constexpr int P = BD::P, PC = BD::PC, NJ = BD::NJ;
+  constexpr int P = BD::P, PC = BD::PC;
+  constexpr int NTH = kChunkThreads;
+  constexpr int TC = NTH / 16;        // threads per row group: columns cn + TC j
+  constexpr int NJ = D / TC;          // columns per thread of a [64][D] product
+  constexpr int NJC = kC / TC;        // of a [64][64] product
   constexpr int HW = 64;             // value columns per pass of phase 1
   constexpr int NH = D / HW;
   // phase 4 is the largest: dL, dAqk [64][65]; q, k, G [64][P]; three [16][P]
   constexpr int SMEM_FLOATS = 2 * kC * PC + 3 * kC * P + 3 * 16 * P + kC;
   __shared__ float sm[SMEM_FLOATS];
-  const int t = threadIdx.x, rm = t >> 4, cn = t & 15;
+  const int t = threadIdx.x, rm = t / TC, cn = t % TC;
   const int H = a.H;
   const int u = blockIdx.x / H, h = blockIdx.x - u * H;
   const ChunkRows cr = chunk_rows(a, u);
@@ -475,15 +546,20 @@ __global__ __launch_bounds__(kThreads) void kda_bwd_chunk_kernel(BwdArgs a) {
   auto ld_k = [&](int c, int d) { return (c < cr.len) ? ld1<DTQ>(a.k, in_idx(c, d)) : 0.f; };
   auto ld_v = [&](int c, int d) { return (c < cr.len) ? ld1<DTQ>(a.v, in_idx(c, d)) : 0.f; };
   auto ld_b = [&](int c) { return (c < cr.len) ? ld1<DTG>(a.beta, (cr.row0 + c) * H + h) : 0.f; };
-  auto ld_do = [&](int c, int d) { return (c < cr.len) ? ld1<DO>(a.dout, in_idx(c, d)) : 0.f; };
+  // The gradients of q, k and G accumulate in place in dq, dk and dg (dg
+  // holds dG until the final reverse cumsum): each thread owns the positions
+  // (rm + 16i, cn + 16j) of its row tile i = 0..3, so its own read-modify-
+  // writes need no synchronisation; pad rows (c >= len) are never stored
+  // (their dG is zero: every term carries a factor q_c or k_c).
+  float* const gq_ = a.dq;
+  float* const gk_ = a.dk;
+  float* const gG_ = a.dg;
 
-  float dq[4][NJ], dk[4][NJ], dG[4][NJ], dbr[4], dzp[NJ];
+  float dbr[4], dzp[NJ];
 #pragma unroll
-  for (int i = 0; i < 4; ++i) {
-    dbr[i] = 0.f;
+  for (int i = 0; i < 4; ++i) dbr[i] = 0.f;
 #pragma unroll
-    for (int j = 0; j < NJ; ++j) dq[i][j] = dk[i][j] = dG[i][j] = 0.f;
-  }
+  for (int j = 0; j < NJ; ++j) dzp[j] = 0.f;
   float dgc = 0.f;   // thread t < D: sum_n S[t][n] dS'[t][n]
 
   // ---- phase 1: dY = v~ dS'^T, dgq = do S^T, dW = -dv~ S^T (K = dv in passes of 64)
@@ -501,15 +577,13 @@ __global__ __launch_bounds__(kThreads) void kda_bwd_chunk_kernel(BwdArgs a) {
     float* sDS = sS + D * PC;
     for (int hp = 0; hp < NH; ++hp) {
       const int n0 = HW * hp;
-      lds_load_rows<D>(sVt, PC, a.VT + ch * kC * D, kC, HW, D, n0);
-      lds_load_rows<D>(sDv, PC, a.DVT + ch * kC * D, kC, HW, D, n0);
-      lds_load_rows<D>(sS, PC, a.SI + ch * D * D, D, HW, D, n0);
-      lds_load_rows<D>(sDS, PC, a.DS + ch * D * D, D, HW, D, n0);
-      for (int e = t; e < kC * HW; e += kThreads) {
-        const int c = e / HW, j = e - c * HW;
-        sDo[c * PC + j] = ld_do(c, n0 + j);
-      }
+      lds_load<kC, HW, PC, NTH>(sVt, a.VT + ch * kC * D, D, n0);
+      lds_load<kC, HW, PC, NTH>(sDv, a.DVT + ch * kC * D, D, n0);
+      lds_load<D, HW, PC, NTH>(sS, a.SI + ch * D * D, D, n0);
+      lds_load<D, HW, PC, NTH>(sDS, a.DS + ch * D * D, D, n0);
+      lds_load_in<DO, D, HW, PC, NTH>(sDo, a.dout, cr.row0, cr.len, H, h, n0, 1.f);
       __syncthreads();
+      #pragma unroll 4
       for (int nn = 0; nn < HW; ++nn) {
         float va[4], oa[4], wa[4];
 #pragma unroll
@@ -520,7 +594,7 @@ __global__ __launch_bounds__(kThreads) void kda_bwd_chunk_kernel(BwdArgs a) {
         }
 #pragma unroll
         for (int j = 0; j < NJ; ++j) {
-          const float sv = sS[(cn + 16 * j) * PC + nn], dsv = sDS[(cn + 16 * j) * PC + nn];
+          const float sv = sS[(cn + TC * j) * PC + nn], dsv = sDS[(cn + TC * j) * PC + nn];
 #pragma unroll
           for (int i = 0; i < 4; ++i) {
             dY[i][j] = fmaf(va[i], dsv, dY[i][j]);
@@ -534,24 +608,33 @@ __global__ __launch_bounds__(kThreads) void kda_bwd_chunk_kernel(BwdArgs a) {
       }
       __syncthreads();
     }
-    // elementwise: dq = dgq gamma; dG += dgq q gamma; dk += dY lambda; dG -= dY k lambda
+    // dq = dgq gamma; dG = dgq q gamma - dY k lambda; dk = dY lambda.  Each
+    // row tile's loads are issued before its stores (the compiler cannot move
+    // a load above a store to a pointer it may alias).
+    float glast[NJ];
 #pragma unroll
-    for (int j = 0; j < NJ; ++j) dzp[j] = 0.f;
+    for (int j = 0; j < NJ; ++j) glast[j] = GL[(kC - 1) * D + cn + TC * j];
 #pragma unroll
     for (int i = 0; i < 4; ++i) {
       const int c = rm + 16 * i;
+      float gl[NJ], qv[NJ], kv[NJ];
 #pragma unroll
       for (int j = 0; j < NJ; ++j) {
-        const int d = cn + 16 * j;
-        const float gl = GL[c * D + d], glast = GL[(kC - 1) * D + d];
-        const float gam = ex2(gl), lam = ex2(glast - gl);
-        const float qv = ld_q(c, d), kv = ld_k(c, d);
-        dq[i][j] += dgq[i][j] * gam;
-        dG[i][j] += dgq[i][j] * qv * gam;
-        dk[i][j] += dY[i][j] * lam;
-        const float dz = dY[i][j] * kv * lam;
-        dG[i][j] -= dz;
+        gl[j] = GL[c * D + cn + TC * j];
+        qv[j] = ld_q(c, cn + TC * j);
+        kv[j] = ld_k(c, cn + TC * j);
+      }
+#pragma unroll
+      for (int j = 0; j < NJ; ++j) {
+        const int d = cn + TC * j;
+        const float gam = ex2(gl[j]), lam = ex2(glast[j] - gl[j]);
+        const float dz = dY[i][j] * kv[j] * lam;
         dzp[j] += dz;
+        if (c < cr.len) {
+          gq_[in_idx(c, d)] = dgq[i][j] * gam * a.scale;
+          gk_[in_idx(c, d)] = dY[i][j] * lam;
+          gG_[in_idx(c, d)] = dgq[i][j] * qv[j] * gam - dz;
+        }
       }
     }
   }
@@ -565,21 +648,22 @@ __global__ __launch_bounds__(kThreads) void kda_bwd_chunk_kernel(BwdArgs a) {
 #pragma unroll
     for (int i = 0; i < 4; ++i)
 #pragma unroll
-      for (int j = 0; j < NJ; ++j) sX[(rm + 16 * i) * P + cn + 16 * j] = dW[i][j];
-    lds_load_rows<D>(sT, PC, a.TM + ch * kC * kC, kC, kC, kC, 0);
-    lds_load_rows<D>(sY, P, a.DVT + ch * kC * D, kC, D, D, 0);
+      for (int j = 0; j < NJ; ++j) sX[(rm + 16 * i) * P + cn + TC * j] = dW[i][j];
+    lds_load<kC, kC, PC, NTH>(sT, a.TM + ch * kC * kC, kC, 0);
+    lds_load<kC, D, P, NTH>(sY, a.DVT + ch * kC * D, D, 0);
     __syncthreads();
 #pragma unroll
     for (int i = 0; i < 4; ++i)
 #pragma unroll
       for (int j = 0; j < NJ; ++j) Yw[i][j] = Yu[i][j] = 0.f;
+    #pragma unroll 4
     for (int m = 0; m < kC; ++m) {
       float tv[4];
 #pragma unroll
       for (int i = 0; i < 4; ++i) tv[i] = sT[m * PC + rm + 16 * i];
 #pragma unroll
       for (int j = 0; j < NJ; ++j) {
-        const float x = sX[m * P + cn + 16 * j], y = sY[m * P + cn + 16 * j];
+        const float x = sX[m * P + cn + TC * j], y = sY[m * P + cn + TC * j];
 #pragma unroll
         for (int i = 0; i < 4; ++i) {
           Yw[i][j] = fmaf(tv[i], x, Yw[i][j]);
@@ -588,26 +672,38 @@ __global__ __launch_bounds__(kThreads) void kda_bwd_chunk_kernel(BwdArgs a) {
       }
     }
     __syncthreads();
-    // dgamma += Yw k beta; dk += Yw gamma beta; dv = Yu beta; dbeta += Yw gamma k + Yu v
+    // dG += Yw k beta gamma; dk += Yw gamma beta; dv = Yu beta; dbeta += Yw gamma k + Yu v
 #pragma unroll
     for (int i = 0; i < 4; ++i) {
       const int c = rm + 16 * i;
+      const bool live = c < cr.len;
       const float bc = ld_b(c);
+      float gl[NJ], kv[NJ], vv[NJ], oG[NJ], ok[NJ];
 #pragma unroll
       for (int j = 0; j < NJ; ++j) {
-        const int d = cn + 16 * j;
-        const float gam = ex2(GL[c * D + d]);
-        const float kv = ld_k(c, d), vv = ld_v(c, d);
-        dG[i][j] += Yw[i][j] * kv * bc * gam;
-        dk[i][j] += Yw[i][j] * gam * bc;
-        dbr[i] += Yw[i][j] * gam * kv + Yu[i][j] * vv;
-        if (c < cr.len) a.dv[in_idx(c, d)] = Yu[i][j] * bc;
+        const int d = cn + TC * j;
+        gl[j] = GL[c * D + d];
+        kv[j] = ld_k(c, d);
+        vv[j] = ld_v(c, d);
+        oG[j] = live ? gG_[in_idx(c, d)] : 0.f;
+        ok[j] = live ? gk_[in_idx(c, d)] : 0.f;
+      }
+#pragma unroll
+      for (int j = 0; j < NJ; ++j) {
+        const int d = cn + TC * j;
+        const float gam = ex2(gl[j]);
+        dbr[i] += Yw[i][j] * gam * kv[j] + Yu[i][j] * vv[j];
+        if (live) {
+          gG_[in_idx(c, d)] = oG[j] + Yw[i][j] * kv[j] * bc * gam;
+          gk_[in_idx(c, d)] = ok[j] + Yw[i][j] * gam * bc;
+          a.dv[in_idx(c, d)] = Yu[i][j] * bc;
+        }
       }
     }
   }
 
   // ---- phase 3: dL = strict(-(Yw W^T + Yu U^T)), dAqk = tril(do v~^T)
-  float dLr[4][4], dAr[4][4];   // rows rm + 16i, columns cn + 16j
+  float dLr[4][NJC], dAr[4][NJC];   // rows rm + 16i, columns cn + TC j
   {
     float* sX = sm;
     float* sY = sX + kC * P;
@@ -617,16 +713,17 @@ __global__ __launch_bounds__(kThreads) void kda_bwd_chunk_kernel(BwdArgs a) {
     for (int i = 0; i < 4; ++i)
 #pragma unroll
       for (int j = 0; j < NJ; ++j) {
-        sX[(rm + 16 * i) * P + cn + 16 * j] = Yw[i][j];
-        sY[(rm + 16 * i) * P + cn + 16 * j] = Yu[i][j];
+        sX[(rm + 16 * i) * P + cn + TC * j] = Yw[i][j];
+        sY[(rm + 16 * i) * P + cn + TC * j] = Yu[i][j];
       }
-    lds_load_rows<D>(sW, P, a.WM + ch * kC * D, kC, D, D, 0);
-    lds_load_rows<D>(sU, P, a.UM + ch * kC * D, kC, D, D, 0);
+    lds_load<kC, D, P, NTH>(sW, a.WM + ch * kC * D, D, 0);
+    lds_load<kC, D, P, NTH>(sU, a.UM + ch * kC * D, D, 0);
     __syncthreads();
 #pragma unroll
     for (int i = 0; i < 4; ++i)
 #pragma unroll
-      for (int j = 0; j < 4; ++j) dLr[i][j] = dAr[i][j] = 0.f;
+      for (int j = 0; j < NJC; ++j) dLr[i][j] = dAr[i][j] = 0.f;
+    #pragma unroll 4
     for (int d = 0; d < D; ++d) {
       float yw[4], yu[4];
 #pragma unroll
@@ -635,27 +732,25 @@ __global__ __launch_bounds__(kThreads) void kda_bwd_chunk_kernel(BwdArgs a) {
         yu[i] = sY[(rm + 16 * i) * P + d];
       }
 #pragma unroll
-      for (int j = 0; j < 4; ++j) {
-        const float w = sW[(cn + 16 * j) * P + d], uu = sU[(cn + 16 * j) * P + d];
+      for (int j = 0; j < NJC; ++j) {
+        const float w = sW[(cn + TC * j) * P + d], uu = sU[(cn + TC * j) * P + d];
 #pragma unroll
         for (int i = 0; i < 4; ++i) dLr[i][j] = fmaf(yw[i], w, fmaf(yu[i], uu, dLr[i][j]));
       }
     }
     __syncthreads();
     // do and v~ into the W / U slots
-    for (int e = t; e < kC * D; e += kThreads) {
-      const int c = e / D, d = e - c * D;
-      sW[c * P + d] = ld_do(c, d);
-    }
-    lds_load_rows<D>(sU, P, a.VT + ch * kC * D, kC, D, D, 0);
+    lds_load_in<DO, D, D, P, NTH>(sW, a.dout, cr.row0, cr.len, H, h, 0, 1.f);
+    lds_load<kC, D, P, NTH>(sU, a.VT + ch * kC * D, D, 0);
     __syncthreads();
+    #pragma unroll 4
     for (int d = 0; d < D; ++d) {
       float ov[4];
 #pragma unroll
       for (int i = 0; i < 4; ++i) ov[i] = sW[(rm + 16 * i) * P + d];
 #pragma unroll
-      for (int j = 0; j < 4; ++j) {
-        const float vv = sU[(cn + 16 * j) * P + d];
+      for (int j = 0; j < NJC; ++j) {
+        const float vv = sU[(cn + TC * j) * P + d];
 #pragma unroll
         for (int i = 0; i < 4; ++i) dAr[i][j] = fmaf(ov[i], vv, dAr[i][j]);
       }
@@ -677,23 +772,19 @@ __global__ __launch_bounds__(kThreads) void kda_bwd_chunk_kernel(BwdArgs a) {
 #pragma unroll
     for (int i = 0; i < 4; ++i)
 #pragma unroll
-      for (int j = 0; j < 4; ++j) {
-        const int c = rm + 16 * i, ii = cn + 16 * j;
+      for (int j = 0; j < NJC; ++j) {
+        const int c = rm + 16 * i, ii = cn + TC * j;
         sDL[c * PC + ii] = (ii < c) ? -dLr[i][j] : 0.f;
         sDA[c * PC + ii] = (ii <= c) ? dAr[i][j] : 0.f;
       }
-    for (int e = t; e < kC * D; e += kThreads) {
-      const int c = e / D, d = e - c * D;
-      sQ[c * P + d] = ld_q(c, d);
-      sK[c * P + d] = ld_k(c, d);
-      sG[c * P + d] = GL[e];
-    }
+    lds_load_in<DTQ, D, D, P, NTH>(sQ, a.q, cr.row0, cr.len, H, h, 0, a.scale);
+    lds_load_in<DTQ, D, D, P, NTH>(sK, a.k, cr.row0, cr.len, H, h, 0, 1.f);
+    lds_load<kC, D, P, NTH>(sG, GL, D, 0);
     if (t < kC) sB[t] = ld_b(t);
     __syncthreads();
-#pragma unroll
     for (int R = 0; R < 4; ++R) {
       const int a0 = 16 * R;
-      for (int e = t; e < 16 * D; e += kThreads) {
+      for (int e = t; e < 16 * D; e += NTH) {
         const int rr = e / D, d = e - rr * D;
         const float fr = ex2(sG[(a0 + rr) * P + d] - sG[a0 * P + d]);
         sXq[rr * P + d] = sQ[(a0 + rr) * P + d] * fr;
@@ -703,20 +794,20 @@ __global__ __launch_bounds__(kThreads) void kda_bwd_chunk_kernel(BwdArgs a) {
 #pragma unroll
       for (int j = 0; j < NJ; ++j) drA[j] = drK[j] = 0.f;
       const int c = a0 + rm;
-#pragma unroll
       for (int s = 0; s < R; ++s) {
         __syncthreads();
-        for (int e = t; e < 16 * D; e += kThreads) {
+        for (int e = t; e < 16 * D; e += NTH) {
           const int ii = e / D, d = e - ii * D;
           sKf[ii * P + d] = sK[(16 * s + ii) * P + d] * ex2(sG[a0 * P + d] - sG[(16 * s + ii) * P + d]);
         }
         __syncthreads();
         // row side: dr[c] += sum_{i in s} D[c][i] k_i 2^(G_a - G_i)
+        #pragma unroll 4
         for (int ii = 0; ii < 16; ++ii) {
           const float da = sDA[c * PC + 16 * s + ii], dl = sDL[c * PC + 16 * s + ii];
 #pragma unroll
           for (int j = 0; j < NJ; ++j) {
-            const float kf = sKf[ii * P + cn + 16 * j];
+            const float kf = sKf[ii * P + cn + TC * j];
             drA[j] = fmaf(da, kf, drA[j]);
             drK[j] = fmaf(dl, kf, drK[j]);
           }
@@ -727,30 +818,48 @@ __global__ __launch_bounds__(kThreads) void kda_bwd_chunk_kernel(BwdArgs a) {
           float dcA[NJ], dcK[NJ];
 #pragma unroll
           for (int j = 0; j < NJ; ++j) dcA[j] = dcK[j] = 0.f;
+          #pragma unroll 4
           for (int rr = 0; rr < 16; ++rr) {
             const float da = sDA[(a0 + rr) * PC + i], dl = sDL[(a0 + rr) * PC + i];
 #pragma unroll
             for (int j = 0; j < NJ; ++j) {
-              dcA[j] = fmaf(da, sXq[rr * P + cn + 16 * j], dcA[j]);
-              dcK[j] = fmaf(dl, sXk[rr * P + cn + 16 * j], dcK[j]);
+              dcA[j] = fmaf(da, sXq[rr * P + cn + TC * j], dcA[j]);
+              dcK[j] = fmaf(dl, sXk[rr * P + cn + TC * j], dcK[j]);
             }
           }
+          if (i < cr.len) {
+            float ok[NJ], oG[NJ];
 #pragma unroll
-          for (int j = 0; j < NJ; ++j) {
-            const int d = cn + 16 * j;
-            const float fk = ex2(sG[a0 * P + d] - sG[i * P + d]);
-            const float sum = (dcA[j] + dcK[j]) * fk;
-            dk[s][j] += sum;
-            dG[s][j] -= sum * sK[i * P + d];
+            for (int j = 0; j < NJ; ++j) {
+              ok[j] = gk_[in_idx(i, cn + TC * j)];
+              oG[j] = gG_[in_idx(i, cn + TC * j)];
+            }
+#pragma unroll
+            for (int j = 0; j < NJ; ++j) {
+              const int d = cn + TC * j;
+              const float fk = ex2(sG[a0 * P + d] - sG[i * P + d]);
+              const float sum = (dcA[j] + dcK[j]) * fk;
+              gk_[in_idx(i, d)] = ok[j] + sum;
+              gG_[in_idx(i, d)] = oG[j] - sum * sK[i * P + d];
+            }
           }
         }
       }
       // diagonal tile and the row-side totals
       {
         const int i = a0 + rm;   // the same row, as a key row of the diagonal tile
+        float dbsum = 0.f;
+        float oq[NJ], oG[NJ], ok[NJ];
 #pragma unroll
         for (int j = 0; j < NJ; ++j) {
-          const int d = cn + 16 * j;
+          const bool live = c < cr.len;
+          oq[j] = live ? gq_[in_idx(c, cn + TC * j)] : 0.f;
+          oG[j] = live ? gG_[in_idx(c, cn + TC * j)] : 0.f;
+          ok[j] = live ? gk_[in_idx(c, cn + TC * j)] : 0.f;
+        }
+#pragma unroll
+        for (int j = 0; j < NJ; ++j) {
+          const int d = cn + TC * j;
           const float gc = sG[c * P + d];
           float rA = drA[j] * ex2(gc - sG[a0 * P + d]);
           float rK = drK[j] * ex2(gc - sG[a0 * P + d]);
@@ -770,38 +879,41 @@ __global__ __launch_bounds__(kThreads) void kda_bwd_chunk_kernel(BwdArgs a) {
             cK = fmaf(sDL[cc * PC + i], sK[cc * P + d] * sB[cc] * e, cK);
           }
           const float qv = sQ[c * P + d], kv = sK[c * P + d], bc = sB[c];
-          dq[R][j] += rA;
-          dG[R][j] += rA * qv + rK * kv * bc;
-          dk[R][j] += rK * bc + cA + cK;
-          dbr[R] += rK * kv;
-          dG[R][j] -= (cA + cK) * kv;
+          dbsum += rK * kv;
+          if (c < cr.len) {
+            gq_[in_idx(c, d)] = oq[j] + rA * a.scale;
+            gG_[in_idx(c, d)] = oG[j] + rA * qv + rK * kv * bc - (cA + cK) * kv;
+            gk_[in_idx(c, d)] = ok[j] + rK * bc + cA + cK;
+          }
         }
+        // dbr is indexed by the row tile: R is a runtime loop here, so add
+        // through the per-row LDS reduction below instead of a register array
+        dbr[0] += (R == 0) ? dbsum : 0.f;
+        dbr[1] += (R == 1) ? dbsum : 0.f;
+        dbr[2] += (R == 2) ? dbsum : 0.f;
+        dbr[3] += (R == 3) ? dbsum : 0.f;
       }
       __syncthreads();
     }
   }
 
-  // ---- outputs: dq, dk, dbeta, dg (reverse cumsum of dG plus the G_C terms)
+  // ---- outputs: dbeta, dg (reverse cumsum of dG plus the G_C terms)
   {
     float* sDG = sm;                   // [64][P]
     float* sRed = sDG + kC * P;        // [16][D] column partial sums of dz
-    float* sDb = sRed + 16 * D;        // [64][16] row partial sums of dbeta
+    float* sDb = sRed + 16 * D;        // [64][TC] row partial sums of dbeta
 #pragma unroll
     for (int i = 0; i < 4; ++i) {
       const int c = rm + 16 * i;
 #pragma unroll
       for (int j = 0; j < NJ; ++j) {
-        const int d = cn + 16 * j;
-        sDG[c * P + d] = dG[i][j];
-        if (c < cr.len) {
-          a.dq[in_idx(c, d)] = dq[i][j] * a.scale;
-          a.dk[in_idx(c, d)] = dk[i][j];
-        }
+        const int d = cn + TC * j;
+        sDG[c * P + d] = (c < cr.len) ? gG_[in_idx(c, d)] : 0.f;
       }
-      sDb[c * 16 + cn] = dbr[i];
+      sDb[c * TC + cn] = dbr[i];
     }
 #pragma unroll
-    for (int j = 0; j < NJ; ++j) sRed[rm * D + cn + 16 * j] = dzp[j];
+    for (int j = 0; j < NJ; ++j) sRed[rm * D + cn + TC * j] = dzp[j];
     __syncthreads();
     if (t < D) {
       float acc = dgc * ex2(GL[(kC - 1) * D + t]);
@@ -813,7 +925,7 @@ __global__ __launch_bounds__(kThreads) void kda_bwd_chunk_kernel(BwdArgs a) {
     }
     if (t < kC && t < cr.len) {
       float acc = 0.f;
-      for (int j = 0; j < 16; ++j) acc += sDb[t * 16 + j];
+      for (int j = 0; j < TC; ++j) acc += sDb[t * TC + j];
       a.dbeta[(cr.row0 + t) * H + h] = acc;
     }
   }
@@ -832,7 +944,7 @@ hipError_t launch_bwd_t(const BwdArgs& a, hipStream_t s) {
   hipLaunchKernelGGL((kda_bwd_rscan_kernel<D, DO>), dim3(chains * (D / 32)), dim3(kThreads), 0, s, a);
   e = hipGetLastError();
   if (e != hipSuccess) return e;
-  hipLaunchKernelGGL((kda_bwd_chunk_kernel<D, DTQ, DTG, DO>), dim3(chunk_heads), dim3(kThreads), 0, s, a);
+  hipLaunchKernelGGL((kda_bwd_chunk_kernel<D, DTQ, DTG, DO>), dim3(chunk_heads), dim3(kChunkThreads), 0, s, a);
   return hipGetLastError();
 }
 
