@@ -39,6 +39,9 @@ constexpr int kThreads = 256;
 // The per-chunk adjoint runs 512 threads (two waves per SIMD): it is bound by
 // latency at one workgroup per CU (its LDS), so the second wave per SIMD hides it.
 constexpr int kChunkThreads = 512;
+// Scan workgroups likewise: one per (chain, 32-column slice), 512 threads, one
+// state column per thread.
+constexpr int kScanThreads = 512;
 
 __device__ __forceinline__ float ex2(float x) { return __builtin_amdgcn_exp2f(x); }
 
@@ -66,33 +69,60 @@ __device__ __forceinline__ ChunkRows chunk_rows(const BwdArgs& a, int u) {
 // ROWS x COLS block of a row-major fp32 array (row stride src_ld floats,
 // first column col0) into LDS rows of pitch PITCH.  All of a thread's 16-byte
 // loads are issued before its LDS writes, so they are in flight together.
+// The two halves of lds_load: the loads into registers (a thread's share,
+// Tile::PER 16-byte pieces) and the LDS writes.  Split, a scan kernel issues
+// the next chunk's loads before the current chunk's arithmetic.
+template <int ROWS, int COLS, int NTH = kThreads>
+struct Tile {
+  static constexpr int V = COLS / 4;
+  static constexpr int N = ROWS * V;
+  static constexpr int PER = (N + NTH - 1) / NTH;
+  static_assert(COLS % 4 == 0, "16-byte loads");
+  float4 r[PER];
+  __device__ __forceinline__ void fetch(const float* src, int src_ld, int col0) {
+#pragma unroll
+    for (int p = 0; p < PER; ++p) {
+      const int e = threadIdx.x + p * NTH;
+      if (N % NTH == 0 || e < N) {
+        const int row = e / V, c4 = e - row * V;
+        r[p] = *reinterpret_cast<const float4*>(src + static_cast<int64_t>(row) * src_ld + col0 + 4 * c4);
+      }
+    }
+  }
+  template <int PITCH>
+  __device__ __forceinline__ void put(float* dst) const {
+#pragma unroll
+    for (int p = 0; p < PER; ++p) {
+      const int e = threadIdx.x + p * NTH;
+      if (N % NTH == 0 || e < N) {
+        const int row = e / V, c4 = e - row * V;
+        float* d = dst + row * PITCH + 4 * c4;
+        d[0] = r[p].x;
+        d[1] = r[p].y;
+        d[2] = r[p].z;
+        d[3] = r[p].w;
+      }
+    }
+  }
+};
+
 template <int ROWS, int COLS, int PITCH, int NTH = kThreads>
 __device__ __forceinline__ void lds_load(float* dst, const float* src, int src_ld, int col0) {
-  constexpr int V = COLS / 4;
-  constexpr int N = ROWS * V;
-  constexpr int PER = (N + NTH - 1) / NTH;
-  static_assert(COLS % 4 == 0, "16-byte loads");
-  float4 tmp[PER];
-#pragma unroll
-  for (int p = 0; p < PER; ++p) {
-    const int e = threadIdx.x + p * NTH;
-    if (N % NTH == 0 || e < N) {
-      const int r = e / V, c4 = e - r * V;
-      tmp[p] = *reinterpret_cast<const float4*>(src + static_cast<int64_t>(r) * src_ld + col0 + 4 * c4);
-    }
-  }
-#pragma unroll
-  for (int p = 0; p < PER; ++p) {
-    const int e = threadIdx.x + p * NTH;
-    if (N % NTH == 0 || e < N) {
-      const int r = e / V, c4 = e - r * V;
-      float* d = dst + r * PITCH + 4 * c4;
-      d[0] = tmp[p].x;
-      d[1] = tmp[p].y;
-      d[2] = tmp[p].z;
-      d[3] = tmp[p].w;
-    }
-  }
+  Tile<ROWS, COLS, NTH> t;
+  t.fetch(src, src_ld, col0);
+  t.template put<PITCH>(dst);
+}
+
+// Workgroup -> (chain, 32-column slice) of the scan kernels: the NS slices
+// of a chain on one XCD (workgroup x runs on XCD x % 8), so the operands all
+// of them read come from that XCD's L2.  Grid: ceil(chains / 8) * 8 * NS.
+template <int NS>
+__device__ __forceinline__ bool scan_slot(int nchains, int& chain, int& split) {
+  const int x = blockIdx.x, xcd = x & 7, kk = x >> 3;
+  const int slot = kk / NS;
+  split = kk - slot * NS;
+  chain = slot * 8 + xcd;
+  return chain < nchains;
 }
 
 // Eight consecutive elements of an input tensor (DT 0 fp32, 1 bf16, 2 fp16)
@@ -166,9 +196,13 @@ __global__ __launch_bounds__(kThreads) void kda_bwd_prep_kernel(BwdArgs a) {
   __syncthreads();
   // in-chunk inclusive cumsum of g, in log2 units
   if (t < D) {
+    float col[kC];
+#pragma unroll
+    for (int c = 0; c < kC; ++c) col[c] = sG[c * P + t];
     float acc = 0.f;
+#pragma unroll
     for (int c = 0; c < kC; ++c) {
-      acc += sG[c * P + t];
+      acc += col[c];
       sG[c * P + t] = acc * kLog2e;
     }
   }
@@ -249,13 +283,19 @@ __global__ __launch_bounds__(kThreads) void kda_bwd_prep_kernel(BwdArgs a) {
   }
   __syncthreads();
   if (t < kC) {
+    // column j of the block's inverse in registers: x_i = [i == j] - sum_{m<i} L_im x_m
+    // (x_m = 0 for m < j, so the sums may run over all m < i)
     const int R = t >> 4, j = t & 15, a0 = 16 * R;
-    sT[(a0 + j) * PC + a0 + j] = 1.f;
-    for (int i = j + 1; i < 16; ++i) {
+    float x[16];
+#pragma unroll
+    for (int i = 0; i < 16; ++i) {
       float acc = 0.f;
-      for (int m = j; m < i; ++m) acc = fmaf(sL[(a0 + i) * PC + a0 + m], sT[(a0 + m) * PC + a0 + j], acc);
-      sT[(a0 + i) * PC + a0 + j] = -acc;
+#pragma unroll
+      for (int m = 0; m < i; ++m) acc = fmaf(sL[(a0 + i) * PC + a0 + m], x[m], acc);
+      x[i] = (i < j) ? 0.f : ((i == j) ? 1.f : -acc);
     }
+#pragma unroll
+    for (int i = 0; i < 16; ++i) sT[(a0 + i) * PC + a0 + j] = x[i];
   }
   __syncthreads();
   for (int R = 1; R < 4; ++R) {
@@ -330,64 +370,82 @@ __global__ __launch_bounds__(kThreads) void kda_bwd_prep_kernel(BwdArgs a) {
 // forward state scan of one (chain, 32-column slice): S_in and v~ per chunk
 // ---------------------------------------------------------------------------
 template <int D>
-__global__ __launch_bounds__(kThreads) void kda_bwd_fscan_kernel(BwdArgs a) {
+__global__ __launch_bounds__(kScanThreads) void kda_bwd_fscan_kernel(BwdArgs a) {
   typedef BwdDims<D> BD;
   constexpr int P = BD::P;
   constexpr int NS = D / 32;
   constexpr int NI = D / 16;   // state rows per thread
   __shared__ float sW[kC * P], sKL[kC * P];
   __shared__ float sS[D * 33], sU[kC * 33], sV[kC * 33], sGC[D];
-  const int t = threadIdx.x, rm = t >> 4, cn = t & 15;
-  const int chain = blockIdx.x / NS, split = blockIdx.x - chain * NS;
+  constexpr int NTH = kScanThreads;
+  constexpr int TC = NTH / 16;   // threads per row group: slice columns cn + TC j
+  constexpr int CJ = 32 / TC;    // slice columns per thread
+  const int t = threadIdx.x, rm = t / TC, cn = t % TC;
   const int H = a.H;
+  int chain, split;
+  if (!scan_slot<NS>(a.B * H, chain, split)) return;   // uniform per workgroup
   const int b = chain / H, h = chain - b * H;
   const int c0 = 32 * split;
-  float S[NI][2];
+  float S[NI][CJ];
 #pragma unroll
   for (int i = 0; i < NI; ++i)
 #pragma unroll
-    for (int j = 0; j < 2; ++j)
-      S[i][j] = (a.h0 != nullptr) ? a.h0[(static_cast<int64_t>(chain) * D + rm + 16 * i) * D + c0 + cn + 16 * j]
+    for (int j = 0; j < CJ; ++j)
+      S[i][j] = (a.h0 != nullptr) ? a.h0[(static_cast<int64_t>(chain) * D + rm + 16 * i) * D + c0 + cn + TC * j]
                                   : 0.f;
+  // chunk n's W, lambda*k and U slice are loaded into registers during
+  // chunk n-1's arithmetic
+  Tile<kC, D, NTH> tW, tK;
+  Tile<kC, 32, NTH> tU;
+  auto fetch = [&](int n) {
+    const int64_t ch = (static_cast<int64_t>(b) * a.NT + n) * H + h;
+    tW.fetch(a.WM + ch * kC * D, D, 0);
+    tK.fetch(a.KL + ch * kC * D, D, 0);
+    tU.fetch(a.UM + ch * kC * D, D, c0);
+  };
+  if (a.NT > 0) fetch(0);
   for (int n = 0; n < a.NT; ++n) {
     const int64_t ch = (static_cast<int64_t>(b) * a.NT + n) * H + h;
     float* SI = a.SI + ch * D * D;
 #pragma unroll
     for (int i = 0; i < NI; ++i)
 #pragma unroll
-      for (int j = 0; j < 2; ++j) {
-        SI[(rm + 16 * i) * D + c0 + cn + 16 * j] = S[i][j];
-        sS[(rm + 16 * i) * 33 + cn + 16 * j] = S[i][j];
+      for (int j = 0; j < CJ; ++j) {
+        SI[(rm + 16 * i) * D + c0 + cn + TC * j] = S[i][j];
+        sS[(rm + 16 * i) * 33 + cn + TC * j] = S[i][j];
       }
-    lds_load<kC, D, P>(sW, a.WM + ch * kC * D, D, 0);
-    lds_load<kC, D, P>(sKL, a.KL + ch * kC * D, D, 0);
-    lds_load<kC, 32, 33>(sU, a.UM + ch * kC * D, D, c0);
+    tW.template put<P>(sW);
+    tK.template put<P>(sKL);
+    tU.template put<33>(sU);
     if (t < D) sGC[t] = a.GCV[ch * D + t];
+    if (n + 1 < a.NT) fetch(n + 1);
     __syncthreads();
     // v~ = U - W S: rows rm + 16i (i < 4), columns cn + 16j (j < 2)
     {
-      float acc[4][2];
+      float acc[4][CJ];
 #pragma unroll
       for (int i = 0; i < 4; ++i)
 #pragma unroll
-        for (int j = 0; j < 2; ++j) acc[i][j] = sU[(rm + 16 * i) * 33 + cn + 16 * j];
+        for (int j = 0; j < CJ; ++j) acc[i][j] = sU[(rm + 16 * i) * 33 + cn + TC * j];
       #pragma unroll 4
       for (int d = 0; d < D; ++d) {
-        const float s0 = sS[d * 33 + cn], s1 = sS[d * 33 + cn + 16];
+        float sv[CJ];
+#pragma unroll
+        for (int j = 0; j < CJ; ++j) sv[j] = sS[d * 33 + cn + TC * j];
 #pragma unroll
         for (int i = 0; i < 4; ++i) {
           const float w = sW[(rm + 16 * i) * P + d];
-          acc[i][0] = fmaf(-w, s0, acc[i][0]);
-          acc[i][1] = fmaf(-w, s1, acc[i][1]);
+#pragma unroll
+          for (int j = 0; j < CJ; ++j) acc[i][j] = fmaf(-w, sv[j], acc[i][j]);
         }
       }
       float* VT = a.VT + ch * kC * D;
 #pragma unroll
       for (int i = 0; i < 4; ++i)
 #pragma unroll
-        for (int j = 0; j < 2; ++j) {
-          sV[(rm + 16 * i) * 33 + cn + 16 * j] = acc[i][j];
-          VT[(rm + 16 * i) * D + c0 + cn + 16 * j] = acc[i][j];
+        for (int j = 0; j < CJ; ++j) {
+          sV[(rm + 16 * i) * 33 + cn + TC * j] = acc[i][j];
+          VT[(rm + 16 * i) * D + c0 + cn + TC * j] = acc[i][j];
         }
     }
     __syncthreads();
@@ -395,17 +453,19 @@ __global__ __launch_bounds__(kThreads) void kda_bwd_fscan_kernel(BwdArgs a) {
 #pragma unroll
     for (int i = 0; i < NI; ++i) {
       const float gcv = sGC[rm + 16 * i];
-      S[i][0] *= gcv;
-      S[i][1] *= gcv;
+#pragma unroll
+      for (int j = 0; j < CJ; ++j) S[i][j] *= gcv;
     }
     #pragma unroll 4
     for (int c = 0; c < kC; ++c) {
-      const float v0 = sV[c * 33 + cn], v1 = sV[c * 33 + cn + 16];
+      float vv[CJ];
+#pragma unroll
+      for (int j = 0; j < CJ; ++j) vv[j] = sV[c * 33 + cn + TC * j];
 #pragma unroll
       for (int i = 0; i < NI; ++i) {
         const float kl = sKL[c * P + rm + 16 * i];
-        S[i][0] = fmaf(kl, v0, S[i][0]);
-        S[i][1] = fmaf(kl, v1, S[i][1]);
+#pragma unroll
+        for (int j = 0; j < CJ; ++j) S[i][j] = fmaf(kl, vv[j], S[i][j]);
       }
     }
     __syncthreads();
@@ -416,25 +476,40 @@ __global__ __launch_bounds__(kThreads) void kda_bwd_fscan_kernel(BwdArgs a) {
 // reverse scan of one (chain, 32-column slice): dS per chunk, dv~, dh0
 // ---------------------------------------------------------------------------
 template <int D, int DO>
-__global__ __launch_bounds__(kThreads) void kda_bwd_rscan_kernel(BwdArgs a) {
+__global__ __launch_bounds__(kScanThreads) void kda_bwd_rscan_kernel(BwdArgs a) {
   typedef BwdDims<D> BD;
   constexpr int P = BD::P, PC = BD::PC;
   constexpr int NS = D / 32;
   constexpr int NI = D / 16;
   __shared__ float sX[kC * P], sY[kC * P], sA[kC * PC];
   __shared__ float sS[D * 33], sDo[kC * 33], sDv[kC * 33], sGC[D];
-  const int t = threadIdx.x, rm = t >> 4, cn = t & 15;
-  const int chain = blockIdx.x / NS, split = blockIdx.x - chain * NS;
+  constexpr int NTH = kScanThreads;
+  constexpr int TC = NTH / 16;   // threads per row group: slice columns cn + TC j
+  constexpr int CJ = 32 / TC;    // slice columns per thread
+  const int t = threadIdx.x, rm = t / TC, cn = t % TC;
   const int H = a.H;
+  int chain, split;
+  if (!scan_slot<NS>(a.B * H, chain, split)) return;   // uniform per workgroup
   const int b = chain / H, h = chain - b * H;
   const int c0 = 32 * split;
-  float dS[NI][2];
+  float dS[NI][CJ];
 #pragma unroll
   for (int i = 0; i < NI; ++i)
 #pragma unroll
-    for (int j = 0; j < 2; ++j)
-      dS[i][j] = (a.dht != nullptr) ? a.dht[(static_cast<int64_t>(chain) * D + rm + 16 * i) * D + c0 + cn + 16 * j]
+    for (int j = 0; j < CJ; ++j)
+      dS[i][j] = (a.dht != nullptr) ? a.dht[(static_cast<int64_t>(chain) * D + rm + 16 * i) * D + c0 + cn + TC * j]
                                     : 0.f;
+  // Operands of the two products of a chunk, loaded into registers one
+  // product ahead: lambda*k and Aqk (for dv~) during the previous chunk's dS
+  // update, gamma*q and W (for dS) during this chunk's dv~.
+  Tile<kC, D, NTH> tX, tY;
+  Tile<kC, kC, NTH> tA;
+  auto fetch_a = [&](int n) {
+    const int64_t ch = (static_cast<int64_t>(b) * a.NT + n) * H + h;
+    tX.fetch(a.KL + ch * kC * D, D, 0);
+    tA.fetch(a.AQ + ch * kC * kC, kC, 0);
+  };
+  if (a.NT > 0) fetch_a(a.NT - 1);
   for (int n = a.NT - 1; n >= 0; --n) {
     const int u = b * a.NT + n;
     const int64_t ch = static_cast<int64_t>(u) * H + h;
@@ -443,69 +518,82 @@ __global__ __launch_bounds__(kThreads) void kda_bwd_rscan_kernel(BwdArgs a) {
 #pragma unroll
     for (int i = 0; i < NI; ++i)
 #pragma unroll
-      for (int j = 0; j < 2; ++j) {
-        DS[(rm + 16 * i) * D + c0 + cn + 16 * j] = dS[i][j];
-        sS[(rm + 16 * i) * 33 + cn + 16 * j] = dS[i][j];
+      for (int j = 0; j < CJ; ++j) {
+        DS[(rm + 16 * i) * D + c0 + cn + TC * j] = dS[i][j];
+        sS[(rm + 16 * i) * 33 + cn + TC * j] = dS[i][j];
       }
-    lds_load<kC, D, P>(sX, a.KL + ch * kC * D, D, 0);
-    lds_load<kC, kC, PC>(sA, a.AQ + ch * kC * kC, kC, 0);
-    lds_load_in<DO, D, 32, 33>(sDo, a.dout, cr.row0, cr.len, H, h, c0, 1.f);
+    tX.template put<P>(sX);
+    tA.template put<PC>(sA);
+    lds_load_in<DO, D, 32, 33, NTH>(sDo, a.dout, cr.row0, cr.len, H, h, c0, 1.f);
     if (t < D) sGC[t] = a.GCV[ch * D + t];
+    tX.fetch(a.QG + ch * kC * D, D, 0);
+    tY.fetch(a.WM + ch * kC * D, D, 0);
     __syncthreads();
     // dv~ = (lambda k) dS + Aqk^T do
     {
-      float acc[4][2];
+      float acc[4][CJ];
 #pragma unroll
-      for (int i = 0; i < 4; ++i) acc[i][0] = acc[i][1] = 0.f;
+      for (int i = 0; i < 4; ++i)
+#pragma unroll
+        for (int j = 0; j < CJ; ++j) acc[i][j] = 0.f;
       #pragma unroll 4
       for (int d = 0; d < D; ++d) {
-        const float s0 = sS[d * 33 + cn], s1 = sS[d * 33 + cn + 16];
+        float sv[CJ];
+#pragma unroll
+        for (int j = 0; j < CJ; ++j) sv[j] = sS[d * 33 + cn + TC * j];
 #pragma unroll
         for (int i = 0; i < 4; ++i) {
           const float kl = sX[(rm + 16 * i) * P + d];
-          acc[i][0] = fmaf(kl, s0, acc[i][0]);
-          acc[i][1] = fmaf(kl, s1, acc[i][1]);
+#pragma unroll
+          for (int j = 0; j < CJ; ++j) acc[i][j] = fmaf(kl, sv[j], acc[i][j]);
         }
       }
       #pragma unroll 4
       for (int c = 0; c < kC; ++c) {
-        const float o0 = sDo[c * 33 + cn], o1 = sDo[c * 33 + cn + 16];
+        float ov[CJ];
+#pragma unroll
+        for (int j = 0; j < CJ; ++j) ov[j] = sDo[c * 33 + cn + TC * j];
 #pragma unroll
         for (int i = 0; i < 4; ++i) {
           const float av = sA[c * PC + rm + 16 * i];
-          acc[i][0] = fmaf(av, o0, acc[i][0]);
-          acc[i][1] = fmaf(av, o1, acc[i][1]);
+#pragma unroll
+          for (int j = 0; j < CJ; ++j) acc[i][j] = fmaf(av, ov[j], acc[i][j]);
         }
       }
       float* DVT = a.DVT + ch * kC * D;
 #pragma unroll
       for (int i = 0; i < 4; ++i)
 #pragma unroll
-        for (int j = 0; j < 2; ++j) {
-          sDv[(rm + 16 * i) * 33 + cn + 16 * j] = acc[i][j];
-          DVT[(rm + 16 * i) * D + c0 + cn + 16 * j] = acc[i][j];
+        for (int j = 0; j < CJ; ++j) {
+          sDv[(rm + 16 * i) * 33 + cn + TC * j] = acc[i][j];
+          DVT[(rm + 16 * i) * D + c0 + cn + TC * j] = acc[i][j];
         }
     }
     __syncthreads();
-    lds_load<kC, D, P>(sX, a.QG + ch * kC * D, D, 0);
-    lds_load<kC, D, P>(sY, a.WM + ch * kC * D, D, 0);
+    tX.template put<P>(sX);
+    tY.template put<P>(sY);
+    if (n > 0) fetch_a(n - 1);
     __syncthreads();
     // dS <- gamma_C dS + (gamma q)^T do - W^T dv~
 #pragma unroll
     for (int i = 0; i < NI; ++i) {
       const float gcv = sGC[rm + 16 * i];
-      dS[i][0] *= gcv;
-      dS[i][1] *= gcv;
+#pragma unroll
+      for (int j = 0; j < CJ; ++j) dS[i][j] *= gcv;
     }
     #pragma unroll 4
     for (int c = 0; c < kC; ++c) {
-      const float o0 = sDo[c * 33 + cn], o1 = sDo[c * 33 + cn + 16];
-      const float v0 = sDv[c * 33 + cn], v1 = sDv[c * 33 + cn + 16];
+      float ov[CJ], dvv[CJ];
+#pragma unroll
+      for (int j = 0; j < CJ; ++j) {
+        ov[j] = sDo[c * 33 + cn + TC * j];
+        dvv[j] = sDv[c * 33 + cn + TC * j];
+      }
 #pragma unroll
       for (int i = 0; i < NI; ++i) {
         const float qg = sX[c * P + rm + 16 * i], w = sY[c * P + rm + 16 * i];
-        dS[i][0] = fmaf(qg, o0, fmaf(-w, v0, dS[i][0]));
-        dS[i][1] = fmaf(qg, o1, fmaf(-w, v1, dS[i][1]));
+#pragma unroll
+        for (int j = 0; j < CJ; ++j) dS[i][j] = fmaf(qg, ov[j], fmaf(-w, dvv[j], dS[i][j]));
       }
     }
     __syncthreads();
@@ -514,8 +602,8 @@ __global__ __launch_bounds__(kThreads) void kda_bwd_rscan_kernel(BwdArgs a) {
 #pragma unroll
     for (int i = 0; i < NI; ++i)
 #pragma unroll
-      for (int j = 0; j < 2; ++j)
-        a.dh0[(static_cast<int64_t>(chain) * D + rm + 16 * i) * D + c0 + cn + 16 * j] = dS[i][j];
+      for (int j = 0; j < CJ; ++j)
+        a.dh0[(static_cast<int64_t>(chain) * D + rm + 16 * i) * D + c0 + cn + TC * j] = dS[i][j];
   }
 }
 
@@ -938,10 +1026,11 @@ hipError_t launch_bwd_t(const BwdArgs& a, hipStream_t s) {
   hipLaunchKernelGGL((kda_bwd_prep_kernel<D, DTQ, DTG>), dim3(chunk_heads), dim3(kThreads), 0, s, a);
   hipError_t e = hipGetLastError();
   if (e != hipSuccess) return e;
-  hipLaunchKernelGGL((kda_bwd_fscan_kernel<D>), dim3(chains * (D / 32)), dim3(kThreads), 0, s, a);
+  const int scan_grid = (chains + 7) / 8 * 8 * (D / 32);
+  hipLaunchKernelGGL((kda_bwd_fscan_kernel<D>), dim3(scan_grid), dim3(kScanThreads), 0, s, a);
   e = hipGetLastError();
   if (e != hipSuccess) return e;
-  hipLaunchKernelGGL((kda_bwd_rscan_kernel<D, DO>), dim3(chains * (D / 32)), dim3(kThreads), 0, s, a);
+  hipLaunchKernelGGL((kda_bwd_rscan_kernel<D, DO>), dim3(scan_grid), dim3(kScanThreads), 0, s, a);
   e = hipGetLastError();
   if (e != hipSuccess) return e;
   hipLaunchKernelGGL((kda_bwd_chunk_kernel<D, DTQ, DTG, DO>), dim3(chunk_heads), dim3(kChunkThreads), 0, s, a);
