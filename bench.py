@@ -18,6 +18,10 @@ Also reported on the same JSON line:
 * ``decode``: the recurrent decode step at B=256, H=16, d=128 (fp32 state
   read-modified-written in place, bf16 inputs), iterated 128 steps, as GB/s
   against the 8 TB/s HBM peak (``configs[4]``);
+* ``backward``: the chunked backward (``kda_chunk_bwd``: dq, dk, dv, dg,
+  dbeta, dh0 from fp32 do and dht) on the same config-1 inputs, per call, with
+  its algorithmic bytes (read q, k, v, g, beta bf16 and do fp32 plus dht;
+  write the five gradients and dh0 fp32) against the HBM peak;
 * ``cpu_baseline``: the oracle's fp32 restatement of the reference jax body
   (torch CPU, all available cores) timed on a bounded sample of the same
   workload on this host.
@@ -155,6 +159,44 @@ def bench_decode(args, device):
                 steps=steps, config="B256 H16 d128 bf16, fp32 state in place")
 
 
+def bwd_bytes(B, T, H, dk, dv, in_bytes=2):
+    n = B * T * H
+    read = n * ((3 * dk + dv) * in_bytes + in_bytes + dv * 4) + B * H * dk * dv * 4
+    write = n * ((3 * dk + dv) * 4 + 4) + B * H * dk * dv * 4
+    return read + write
+
+
+def bench_backward(args, fwd_inputs, device):
+    import axiom_amd
+    from axiom_amd import kda as kmod
+    q, k, v, g, beta = fwd_inputs
+    B, T, H, dk = q.shape
+    dv = v.shape[3]
+    gen = torch.Generator(device=device)
+    gen.manual_seed(args.seed + 3)
+    do = torch.randn(B, T, H, dv, device=device, generator=gen)
+    dht = torch.randn(B, H, dk, dv, device=device, generator=gen) * 0.1
+    ws = torch.empty(kmod.chunk_bwd_workspace_bytes(B, T, H, dk, dv), dtype=torch.uint8, device=device)
+    stream = torch.cuda.current_stream(device)
+    for _ in range(2):
+        axiom_amd.kda_chunk_bwd(q, k, v, g, beta, do, dht=dht, workspace=ws)
+    torch.cuda.synchronize()
+    e0, e1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+    e0.record(stream)
+    for _ in range(args.bwd_steps):
+        axiom_amd.kda_chunk_bwd(q, k, v, g, beta, do, dht=dht, workspace=ws)
+    e1.record(stream)
+    torch.cuda.synchronize()
+    t_call = e0.elapsed_time(e1) / 1e3 / args.bwd_steps
+    nbytes = bwd_bytes(B, T, H, dk, dv)
+    gbps = nbytes / t_call / 1e9
+    return dict(us_per_call=t_call * 1e6, tokens_per_s=B * T / t_call, calls=args.bwd_steps,
+                roofline={"bound": "hbm", "achieved": gbps, "peak": HBM_PEAK_GBPS, "unit": "GB/s",
+                          "frac": gbps / HBM_PEAK_GBPS, "algorithmic_bytes_per_call": nbytes},
+                kernels="kda_bwd_prep + kda_bwd_fscan + kda_bwd_rscan + kda_bwd_chunk (fp32)",
+                config="B4 T4096 H16 d128 bf16 inputs, fp32 do and dht, zero h0")
+
+
 def cpu_baseline(fwd_inputs, seconds):
     """Oracle port (fp32, torch CPU) of the reference jax body on a bounded sample."""
     from oracle import kda_oracle as K
@@ -200,6 +242,8 @@ def main():
     ap.add_argument("--cpu-seconds", type=float, default=10.0)
     ap.add_argument("--no-cpu-baseline", action="store_true")
     ap.add_argument("--no-decode", action="store_true")
+    ap.add_argument("--bwd-steps", type=int, default=5)
+    ap.add_argument("--no-backward", action="store_true")
     args = ap.parse_args()
     if args.gpus != 1 or int(os.environ.get("WORLD_SIZE", "1")) != 1:
         print("bench.py measures one GPU only: every (batch, head) chain of this path is "
@@ -252,6 +296,8 @@ def main():
         line["copy_gbps_measured"] = None
     if not args.no_decode:
         line["decode"] = bench_decode(args, device)
+    if not args.no_backward:
+        line["backward"] = bench_backward(args, fwd["inputs"], device)
     if not args.no_cpu_baseline:
         line["cpu_baseline"] = cpu_baseline(fwd["inputs"], args.cpu_seconds)
     print(json.dumps(line), flush=True)
