@@ -7,6 +7,7 @@ validates arguments and hands device pointers to that library.
 """
 
 from .kda import (cc_scan, kda_chunk, kda_chunk_bwd, kda_chunk_fwd, kda_recurrent_step,  # noqa: F401
-                  varlen_status)
+                  solve, solve_t, ut_solve, ut_solve_bwd, varlen_status)
 
-__all__ = ["cc_scan", "kda_chunk", "kda_chunk_bwd", "kda_chunk_fwd", "kda_recurrent_step", "varlen_status"]
+__all__ = ["cc_scan", "kda_chunk", "kda_chunk_bwd", "kda_chunk_fwd", "kda_recurrent_step", "solve", "solve_t",
+           "ut_solve", "ut_solve_bwd", "varlen_status"]

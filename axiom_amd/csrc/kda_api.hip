@@ -276,6 +276,16 @@ BwdLayout bwd_layout(int B, int T, int H, int d) {
   return L;
 }
 
+int ut_check(const void* a, const void* b, const void* x, int H, int C, int N, int dtype) {
+  if (!a || !b || !x) return fail(KDA_ERR_INVALID_ARGUMENT, "null pointer");
+  if (H < 1 || N < 1) return fail(KDA_ERR_INVALID_ARGUMENT, "H=%d, N=%d must be >= 1", H, N);
+  if (C < 1 || C > 64) return fail(KDA_ERR_UNSUPPORTED, "C=%d: this build solves 1 <= C <= 64", C);
+  if (dtype != KDA_DTYPE_F32 && dtype != KDA_DTYPE_BF16)
+    return fail(KDA_ERR_INVALID_ARGUMENT, "dtype=%d: a, b, x are F32 or BF16", dtype);
+  if (static_cast<int64_t>(H) * ((N + 63) / 64) > 0x7FFFFFFFLL) return fail(KDA_ERR_INVALID_ARGUMENT, "too large");
+  return KDA_OK;
+}
+
 extern "C" {
 
 int kda_abi_version(void) { return 100; }
@@ -441,6 +451,31 @@ int kda_chunk_bwd(hipStream_t stream, const void* q, const void* k, const void* 
   a.DVT = reinterpret_cast<float*>(ws + L.DVT);
   const hipError_t e = kda::launch_bwd(a, dk_dim, in_dtype, dout_dtype, stream);
   if (e != hipSuccess) return hip_fail(e, "backward kernel launch");
+  return KDA_OK;
+}
+
+
+int kda_ut_solve(hipStream_t stream, const void* a, const void* b, void* x, int H, int C, int N,
+                 int dtype, int transpose) {
+  g_err[0] = 0;
+  if (int rc = ut_check(a, b, x, H, C, N, dtype)) return rc;
+  kda::UtArgs u{};
+  u.a = a; u.b = b; u.x = x; u.H = H; u.C = C; u.N = N; u.ntiles = (N + 63) / 64;
+  const hipError_t e = kda::launch_ut(u, dtype == KDA_DTYPE_F32 ? 0 : 1, transpose != 0, false, stream);
+  if (e != hipSuccess) return hip_fail(e, "ut solve launch");
+  return KDA_OK;
+}
+
+int kda_ut_solve_bwd(hipStream_t stream, const void* a, const void* x, const void* dx, void* da, void* db,
+                     int H, int C, int N, int dtype, int transpose) {
+  g_err[0] = 0;
+  if (int rc = ut_check(a, dx, db, H, C, N, dtype)) return rc;
+  if (!x || !da) return fail(KDA_ERR_INVALID_ARGUMENT, "null pointer");
+  kda::UtArgs u{};
+  u.a = a; u.b = dx; u.x = db; u.xf = x; u.da = da; u.H = H; u.C = C; u.N = N; u.ntiles = (N + 63) / 64;
+  // the adjoint of the forward solve is the transposed solve, and vice versa
+  const hipError_t e = kda::launch_ut(u, dtype == KDA_DTYPE_F32 ? 0 : 1, transpose == 0, true, stream);
+  if (e != hipSuccess) return hip_fail(e, "ut solve backward launch");
   return KDA_OK;
 }
 

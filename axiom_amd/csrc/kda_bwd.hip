@@ -30,6 +30,7 @@
 
 #include "kda_common.h"
 #include "kda_internal.h"
+#include "kda_tri.h"
 
 namespace kda {
 namespace {
@@ -275,46 +276,8 @@ __global__ __launch_bounds__(kThreads) void kda_bwd_prep_kernel(BwdArgs a) {
     __syncthreads();  // sX0/sX1 reused by the next row tile
   }
 
-  // T = (I + L)^-1: diagonal 16 x 16 blocks by forward substitution (one
-  // column per thread), then T_Rs = -T_RR sum_{j=s}^{R-1} L_Rj T_js.
-  for (int e = t; e < kC * kC; e += kThreads) {
-    const int c = e / kC, i = e - c * kC;
-    sT[c * PC + i] = 0.f;
-  }
-  __syncthreads();
-  if (t < kC) {
-    // column j of the block's inverse in registers: x_i = [i == j] - sum_{m<i} L_im x_m
-    // (x_m = 0 for m < j, so the sums may run over all m < i)
-    const int R = t >> 4, j = t & 15, a0 = 16 * R;
-    float x[16];
-#pragma unroll
-    for (int i = 0; i < 16; ++i) {
-      float acc = 0.f;
-#pragma unroll
-      for (int m = 0; m < i; ++m) acc = fmaf(sL[(a0 + i) * PC + a0 + m], x[m], acc);
-      x[i] = (i < j) ? 0.f : ((i == j) ? 1.f : -acc);
-    }
-#pragma unroll
-    for (int i = 0; i < 16; ++i) sT[(a0 + i) * PC + a0 + j] = x[i];
-  }
-  __syncthreads();
-  for (int R = 1; R < 4; ++R) {
-    // X_s = sum_{j=s}^{R-1} L_Rj T_js for s < R (into sX0 rows 16s..), then T_Rs = -T_RR X_s
-    for (int e = t; e < 16 * 16 * R; e += kThreads) {
-      const int s = e >> 8, rr = (e >> 4) & 15, cc = e & 15;
-      float acc = 0.f;
-      for (int m = 16 * s; m < 16 * R; ++m) acc = fmaf(sL[(16 * R + rr) * PC + m], sT[m * PC + 16 * s + cc], acc);
-      sX0[s * 256 + rr * 16 + cc] = acc;
-    }
-    __syncthreads();
-    for (int e = t; e < 16 * 16 * R; e += kThreads) {
-      const int s = e >> 8, rr = (e >> 4) & 15, cc = e & 15;
-      float acc = 0.f;
-      for (int m = 0; m < 16; ++m) acc = fmaf(sT[(16 * R + rr) * PC + 16 * R + m], sX0[s * 256 + m * 16 + cc], acc);
-      sT[(16 * R + rr) * PC + 16 * s + cc] = -acc;
-    }
-    __syncthreads();
-  }
+  // T = (I + L)^-1
+  invert_unit_lower64<PC, kThreads>(sL, sT, sX0);
   {
     float* TM = a.TM + ch * kC * kC;
     for (int e = t; e < kC * kC; e += kThreads) {

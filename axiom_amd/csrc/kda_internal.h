@@ -103,7 +103,18 @@ struct BwdArgs {
   float* DVT;           // [ch][C][dv] cotangent of v~
 };
 
+// Standalone unit-triangular solve (kda_ut.hip); a [H][C][C], b/x/xf [H][C][N].
+struct UtArgs {
+  const void* a;
+  const void* b;    // right-hand side (the cotangent dX in the backward rule)
+  void* x;          // solution (dB in the backward rule)
+  const void* xf;   // backward rule: the forward solution X
+  void* da;         // backward rule: dA (strict lower), else unused
+  int H, C, N, ntiles;
+};
+
 hipError_t launch_bwd(const BwdArgs& a, int d, int in_dtype, int do_dtype, hipStream_t s);
+hipError_t launch_ut(const UtArgs& a, int dtype, bool transpose, bool with_da, hipStream_t s);
 // dst[0..n) = src (or 0 when src is null), by a kernel (no memset/memcpy node)
 hipError_t launch_copy_or_zero(float* dst, const float* src, int64_t n, hipStream_t s);
 hipError_t launch_intra(const IntraArgs& a, int d, int dtq, int dtg, int grid, hipStream_t s);

@@ -15,6 +15,9 @@ Mirrors the reference's interface for this path (romannekrasovaillm/axiom):
 * :func:`kda_chunk_bwd` / :func:`kda_chunk` -- the chunked backward (the
   ``cc_scan`` custom_vjp's backward rule, ``net/kernels/kda_cc_fused_persist.py:1707``)
   and a differentiable ``torch.autograd.Function`` over forward + backward.
+* :func:`ut_solve` / :func:`solve` / :func:`solve_t` -- the standalone batched
+  unit-triangular solve of ``net/kernels/kda_ut_solve.py`` (both orientations)
+  and its custom_vjp.
 
 Every function calls the HIP library through its C ABI on torch's current
 stream; nothing here computes on the CPU.
@@ -235,6 +238,82 @@ def kda_chunk(q, k, v, g, beta, initial_state=None, scale: float = 1.0):
     reference's ``custom_vjp`` returns primal dtypes).
     """
     return _KDAChunk.apply(q, k, v, g, beta, initial_state, scale)
+
+
+_UT_CODES = {torch.float32: _lib.KDA_DTYPE_F32, torch.bfloat16: _lib.KDA_DTYPE_BF16}
+
+
+def _ut_check(a, b, what):
+    if a.dim() != 3 or a.shape[1] != a.shape[2]:
+        raise ValueError(f"{what}: a must be (H, C, C), got {tuple(a.shape)}")
+    H, C = a.shape[0], a.shape[1]
+    if b.dim() != 3 or b.shape[0] != H or b.shape[1] != C:
+        raise ValueError(f"{what}: b must be (H, C, N) = ({H}, {C}, N), got {tuple(b.shape)}")
+    if a.dtype not in _UT_CODES or b.dtype != a.dtype:
+        raise ValueError(f"{what}: a and b must share a dtype in fp32/bf16")
+    if not 1 <= C <= 64:
+        raise ValueError(f"{what}: C={C} unsupported (this build solves 1 <= C <= 64)")
+    for name, t in (("a", a), ("b", b)):
+        _contig(name, t)
+    return H, C, b.shape[2]
+
+
+def ut_solve(a, b, transpose: bool = False):
+    """``X = (I + L)^-1 B`` (``transpose``: ``(I + L)^-T B``), ``L = tril(a, -1)`` per head.
+
+    The reference's ``kernel`` / ``kernel_t`` (``net/kernels/kda_ut_solve.py:525``,
+    ``:536``): ``a (H, C, C)`` unit lower triangular, ``b (H, C, N)``, fp32 or
+    bf16 (fp32 arithmetic), ``C <= 64``.
+    """
+    what = "ut_solve"
+    H, C, N = _ut_check(a, b, what)
+    dev = _require_gpu([a, b], what)
+    x = torch.empty_like(b)
+    rc = _lib.lib().kda_ut_solve(_stream(dev), _ptr(a), _ptr(b), _ptr(x), H, C, N, _UT_CODES[a.dtype],
+                                 1 if transpose else 0)
+    _lib.check(rc, what)
+    return x
+
+
+def ut_solve_bwd(a, x, dx, transpose: bool = False):
+    """``(dA, dB)`` of :func:`ut_solve` (``net/kernels/kda_ut_solve.py:563`` ``_backward``)."""
+    what = "ut_solve_bwd"
+    H, C, N = _ut_check(a, dx, what)
+    if x.shape != dx.shape or x.dtype != dx.dtype:
+        raise ValueError(f"{what}: x and dx must match")
+    _contig("x", x)
+    dev = _require_gpu([a, x, dx], what)
+    da = torch.empty_like(a)
+    db = torch.empty_like(dx)
+    rc = _lib.lib().kda_ut_solve_bwd(_stream(dev), _ptr(a), _ptr(x), _ptr(dx), _ptr(da), _ptr(db),
+                                     H, C, N, _UT_CODES[a.dtype], 1 if transpose else 0)
+    _lib.check(rc, what)
+    return da, db
+
+
+class _UTSolve(torch.autograd.Function):
+    @staticmethod
+    def forward(ctx, a, b, transpose):
+        x = ut_solve(a, b, transpose)
+        ctx.save_for_backward(a, x)
+        ctx.transpose = transpose
+        return x
+
+    @staticmethod
+    def backward(ctx, dx):
+        a, x = ctx.saved_tensors
+        da, db = ut_solve_bwd(a, x, dx.contiguous().to(x.dtype), ctx.transpose)
+        return da, db, None
+
+
+def solve(a, b):
+    """Differentiable ``(I + L)^-1 B`` (the reference's ``solve``, ``kda_ut_solve.py:628``)."""
+    return _UTSolve.apply(a, b, False)
+
+
+def solve_t(a, b):
+    """Differentiable ``(I + L)^-T B`` (the reference's ``solve_t``, ``kda_ut_solve.py:631``)."""
+    return _UTSolve.apply(a, b, True)
 
 
 def varlen_status(workspace, B, T, H, dk, dv, n_seqs, in_code=_lib.KDA_DTYPE_BF16) -> int:

@@ -167,6 +167,30 @@ KDA_API int kda_chunk_bwd(hipStream_t stream,
 /* Workspace bytes kda_chunk_bwd needs (0 on bad input).  Host-only. */
 KDA_API size_t kda_chunk_bwd_workspace(int B, int T, int H, int dk_dim, int dv_dim, int chunk);
 
+/*
+ * Standalone batched unit-triangular solve, per head h:
+ *   transpose == 0:  X = (I + L)^-1 B      net/kernels/kda_ut_solve.py:525  kernel(a, b)
+ *   transpose != 0:  X = (I + L)^-T B      net/kernels/kda_ut_solve.py:536  kernel_t(a, b)
+ * with L = the strictly lower part of a [H][C][C] (a's diagonal and upper
+ * part are not read: a is unit lower triangular in the reference's
+ * contract), b and x [H][C][N], all row-major, of one dtype KDA_DTYPE_F32 or
+ * KDA_DTYPE_BF16 (fp32 arithmetic).  1 <= C <= 64, N >= 1.
+ */
+KDA_API int kda_ut_solve(hipStream_t stream, const void* a, const void* b, void* x,
+                int H, int C, int N, int dtype, int transpose);
+
+/*
+ * Backward rule of the differentiable solve (the custom_vjp of
+ * net/kernels/kda_ut_solve.py:601-636, adjoint :563-588): given a, the
+ * forward solution x and its cotangent dx, writes db = the sibling solve of
+ * dx (transposed for the forward solve, plain for the transposed one) and
+ * da = strict_lower(-db x^T) (forward solve) or strict_lower(-x db^T)
+ * (transposed solve); da's diagonal and upper part are written as zero.
+ * Shapes, dtype and `transpose` (of the forward solve) as kda_ut_solve.
+ */
+KDA_API int kda_ut_solve_bwd(hipStream_t stream, const void* a, const void* x, const void* dx,
+                void* da, void* db, int H, int C, int N, int dtype, int transpose);
+
 /* Message of the last failure on the calling thread ("" if none). */
 KDA_API const char* kda_last_error(void);
 

@@ -77,7 +77,7 @@ def varlen_ws_bytes(T, N, H, dk, dv, es):
 def test_header_declares_the_abi():
     names = _lib.header_symbols()
     assert set(names) == set(_lib._SIGNATURES), names
-    assert len(names) == len(set(names)) == 10
+    assert len(names) == len(set(names)) == 12
 
 
 def test_library_exports_every_declared_symbol(L):
@@ -247,3 +247,27 @@ def test_cc_scan_reference_errors():
         kmod.cc_scan(q.float(), q.float(), q.float(), a, b, S)
     with pytest.raises(ValueError, match="T=100 must be a multiple of the chunk width C=32"):
         kmod.cc_scan(q, q, q, a, b, S)
+
+
+@pytest.mark.parametrize("args,status,needle", [
+    ((_NULL, _FAKE, _FAKE, 1, 64, 8, 0, 0), _lib.KDA_ERR_INVALID_ARGUMENT, "null"),
+    ((_FAKE, _FAKE, _FAKE, 1, 65, 8, 0, 0), _lib.KDA_ERR_UNSUPPORTED, "C=65"),
+    ((_FAKE, _FAKE, _FAKE, 1, 0, 8, 0, 0), _lib.KDA_ERR_UNSUPPORTED, "C=0"),
+    ((_FAKE, _FAKE, _FAKE, 0, 64, 8, 0, 0), _lib.KDA_ERR_INVALID_ARGUMENT, "H=0"),
+    ((_FAKE, _FAKE, _FAKE, 1, 64, 8, 2, 0), _lib.KDA_ERR_INVALID_ARGUMENT, "dtype=2"),
+])
+def test_ut_solve_validation(L, args, status, needle):
+    rc = L.kda_ut_solve(_NULL, *args)
+    msg = _lib.last_error()
+    assert rc == status and needle in msg, msg
+
+
+def test_chunk_bwd_workspace_size(L):
+    NT = (4096 + 63) // 64
+    ch = 4 * NT * 16
+    expected = sum(_align(n) for n in (ch * 64 * 128 * 4,) * 3 + (ch * 128 * 4, ch * 64 * 64 * 4, ch * 64 * 64 * 4)
+                   + (ch * 64 * 128 * 4,) * 2 + (ch * 128 * 128 * 4, ch * 64 * 128 * 4, ch * 128 * 128 * 4,
+                                                 ch * 64 * 128 * 4))
+    assert L.kda_chunk_bwd_workspace(4, 4096, 16, 128, 128, C) == expected
+    assert L.kda_chunk_bwd_workspace(1, 0, 1, 64, 64, C) > 0
+    assert L.kda_chunk_bwd_workspace(1, 64, 1, 96, 96, C) == 0
