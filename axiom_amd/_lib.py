@@ -48,6 +48,8 @@ _SIGNATURES = {
     "kda_chunk_bwd_workspace": (_sz, [_i, _i, _i, _i, _i, _i]),
     "kda_ut_solve": (_i, [_vp, _vp, _vp, _vp, _i, _i, _i, _i, _i]),
     "kda_ut_solve_bwd": (_i, [_vp, _vp, _vp, _vp, _vp, _vp, _i, _i, _i, _i, _i]),
+    "kda_prologue": (_i, [_vp] * 16 + [_i] * 7),
+    "kda_epilogue": (_i, [_vp, _vp, _vp, _vp, _i, _i, _i, _i, _f, _i, _i, _i]),
     "kda_last_error": (ctypes.c_char_p, []),
     "kda_abi_version": (_i, []),
 }

@@ -32,7 +32,7 @@ HIPCC_FLAGS = [
     "-Xclang", "-target-feature", "-Xclang", "-packed-fp32-ops",
     "-Wno-unused-command-line-argument",
 ]
-SOURCES = ["kda_chunk.hip", "kda_varlen.hip", "kda_decode.hip", "kda_bwd.hip", "kda_ut.hip", "kda_api.hip"]
+SOURCES = ["kda_chunk.hip", "kda_varlen.hip", "kda_decode.hip", "kda_bwd.hip", "kda_ut.hip", "kda_prologue.hip", "kda_api.hip"]
 
 
 def _hipcc() -> str:

@@ -479,4 +479,50 @@ int kda_ut_solve_bwd(hipStream_t stream, const void* a, const void* x, const voi
   return KDA_OK;
 }
 
+int kda_prologue(hipStream_t stream, const void* qp, const void* kp, const void* vp,
+                 const float* wq, const float* wk, const float* wv,
+                 const float* bq_in, const float* bk_in, const float* bv_in,
+                 float* bq_out, float* bk_out, float* bv_out,
+                 void* q, void* k, void* v,
+                 int B, int T, int H, int d, int K, int in_dtype, int out_dtype) {
+  g_err[0] = 0;
+  if (B < 1 || T < 0 || H < 1) return fail(KDA_ERR_INVALID_ARGUMENT, "B=%d, T=%d, H=%d out of range", B, T, H);
+  if (!dim_ok(d)) return fail(KDA_ERR_UNSUPPORTED, "d=%d: this build runs d in {64, 128}", d);
+  if (K < 1 || K > 8) return fail(KDA_ERR_UNSUPPORTED, "K=%d: conv kernels of 1..8 taps", K);
+  if ((in_dtype != KDA_DTYPE_F32 && in_dtype != KDA_DTYPE_BF16) ||
+      (out_dtype != KDA_DTYPE_F32 && out_dtype != KDA_DTYPE_BF16))
+    return fail(KDA_ERR_INVALID_ARGUMENT, "in_dtype=%d, out_dtype=%d: F32 or BF16", in_dtype, out_dtype);
+  if (!wq || !wk || !wv) return fail(KDA_ERR_INVALID_ARGUMENT, "null conv taps");
+  if (T > 0 && (!qp || !kp || !vp || !q || !k || !v)) return fail(KDA_ERR_INVALID_ARGUMENT, "null pointer");
+  if (static_cast<int64_t>(B) * T * H * 3 / 4 > 0x7FFFFFFFLL) return fail(KDA_ERR_INVALID_ARGUMENT, "too large");
+  kda::PrologueArgs a{};
+  a.qp = qp; a.kp = kp; a.vp = vp; a.wq = wq; a.wk = wk; a.wv = wv;
+  a.bq_in = bq_in; a.bk_in = bk_in; a.bv_in = bv_in; a.bq_out = bq_out; a.bk_out = bk_out; a.bv_out = bv_out;
+  a.q = q; a.k = k; a.v = v; a.B = B; a.T = T; a.H = H; a.K = K;
+  const hipError_t e = kda::launch_prologue(a, d, in_dtype == KDA_DTYPE_F32 ? 0 : 1,
+                                            out_dtype == KDA_DTYPE_F32 ? 0 : 1, stream);
+  if (e != hipSuccess) return hip_fail(e, "prologue launch");
+  return KDA_OK;
+}
+
+int kda_epilogue(hipStream_t stream, const void* o, const void* gate, void* y, int B, int T, int H, int dv,
+                 float eps, int o_dtype, int gate_dtype, int out_dtype) {
+  g_err[0] = 0;
+  if (B < 1 || T < 0 || H < 1) return fail(KDA_ERR_INVALID_ARGUMENT, "B=%d, T=%d, H=%d out of range", B, T, H);
+  if (!dim_ok(dv)) return fail(KDA_ERR_UNSUPPORTED, "dv=%d: this build runs dv in {64, 128}", dv);
+  auto ok = [](int dt) { return dt == KDA_DTYPE_F32 || dt == KDA_DTYPE_BF16; };
+  if (!ok(o_dtype) || !ok(gate_dtype) || !ok(out_dtype))
+    return fail(KDA_ERR_INVALID_ARGUMENT, "dtypes must be F32 or BF16");
+  if (!(eps >= 0.f) || !std::isfinite(eps)) return fail(KDA_ERR_INVALID_ARGUMENT, "eps must be finite and >= 0");
+  if (T > 0 && (!o || !gate || !y)) return fail(KDA_ERR_INVALID_ARGUMENT, "null pointer");
+  if (static_cast<int64_t>(B) * T * H / 4 > 0x7FFFFFFFLL) return fail(KDA_ERR_INVALID_ARGUMENT, "too large");
+  kda::EpilogueArgs a{};
+  a.o = o; a.gate = gate; a.y = y; a.B = B; a.T = T; a.H = H; a.eps = eps;
+  const hipError_t e = kda::launch_epilogue(a, dv, o_dtype == KDA_DTYPE_F32 ? 0 : 1,
+                                            gate_dtype == KDA_DTYPE_F32 ? 0 : 1, out_dtype == KDA_DTYPE_F32 ? 0 : 1,
+                                            stream);
+  if (e != hipSuccess) return hip_fail(e, "epilogue launch");
+  return KDA_OK;
+}
+
 }  // extern "C"

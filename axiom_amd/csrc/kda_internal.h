@@ -113,6 +113,36 @@ struct UtArgs {
   int H, C, N, ntiles;
 };
 
+// Prologue / epilogue around the chunked kernels (kda_prologue.hip).
+struct PrologueArgs {
+  const void* qp;          // [B,T,H*d] projections (fp32 or bf16)
+  const void* kp;
+  const void* vp;
+  const float* wq;         // [K, H*d] depthwise conv taps, w[i] weights x[t-i]
+  const float* wk;
+  const float* wv;
+  const float* bq_in;      // [B, K-1, H*d] history rows, oldest first, or null (zeros)
+  const float* bk_in;
+  const float* bv_in;
+  float* bq_out;           // last K-1 inputs after this call, or null
+  float* bk_out;
+  float* bv_out;
+  void* q;                 // [B,T,H,d] outputs (fp32 or bf16)
+  void* k;
+  void* v;
+  int B, T, H, K;
+};
+
+struct EpilogueArgs {
+  const void* o;           // [B,T,H,dv]
+  const void* gate;        // [B,T,H*dv] gate logits
+  void* y;                 // [B,T,H*dv]
+  int B, T, H;
+  float eps;
+};
+
+hipError_t launch_prologue(const PrologueArgs& a, int d, int in_dt, int out_dt, hipStream_t s);
+hipError_t launch_epilogue(const EpilogueArgs& a, int d, int o_dt, int g_dt, int y_dt, hipStream_t s);
 hipError_t launch_bwd(const BwdArgs& a, int d, int in_dtype, int do_dtype, hipStream_t s);
 hipError_t launch_ut(const UtArgs& a, int dtype, bool transpose, bool with_da, hipStream_t s);
 // dst[0..n) = src (or 0 when src is null), by a kernel (no memset/memcpy node)

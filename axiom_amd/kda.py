@@ -15,6 +15,8 @@ Mirrors the reference's interface for this path (romannekrasovaillm/axiom):
 * :func:`kda_chunk_bwd` / :func:`kda_chunk` -- the chunked backward (the
   ``cc_scan`` custom_vjp's backward rule, ``net/kernels/kda_cc_fused_persist.py:1707``)
   and a differentiable ``torch.autograd.Function`` over forward + backward.
+* :func:`kda_prologue` / :func:`kda_epilogue` -- short conv, swish and L2 norm
+  before the chunked kernels; head-wise RMSNorm and the sigmoid gate after.
 * :func:`ut_solve` / :func:`solve` / :func:`solve_t` -- the standalone batched
   unit-triangular solve of ``net/kernels/kda_ut_solve.py`` (both orientations)
   and its custom_vjp.
@@ -314,6 +316,80 @@ def solve(a, b):
 def solve_t(a, b):
     """Differentiable ``(I + L)^-T B`` (the reference's ``solve_t``, ``kda_ut_solve.py:631``)."""
     return _UTSolve.apply(a, b, True)
+
+
+def kda_prologue(qp, kp, vp, wq, wk, wv, num_heads: int, conv_state=None, return_state: bool = True,
+                 out_dtype=torch.bfloat16):
+    """Short conv -> swish -> (L2 norm for q, k) of the projections (``net/kda.py:194-202``).
+
+    ``qp, kp, vp [B, T, H*d]`` fp32 or bf16; ``wq, wk, wv [K, H*d]`` fp32 conv
+    taps (``w[i]`` weights the input ``i`` steps back); ``conv_state`` None or
+    a tuple of three fp32 ``[B, K-1, H*d]`` buffers (the previous ``K-1``
+    inputs).  Returns ``(q, k, v [B, T, H, d] in out_dtype, new_state)``
+    (``new_state`` None unless ``return_state``); the new buffers may be the
+    ones passed in (updated in place) -- a fresh tuple is returned here.
+    """
+    what = "kda_prologue"
+    if qp.dim() != 3 or kp.shape != qp.shape or vp.shape != qp.shape:
+        raise ValueError(f"{what}: qp, kp, vp must share a [B,T,H*d] shape")
+    B, T, HD = qp.shape
+    H = int(num_heads)
+    if H < 1 or HD % H:
+        raise ValueError(f"{what}: H*d={HD} is not a multiple of num_heads={H}")
+    d = HD // H
+    if d not in SUPPORTED_HEAD_DIMS:
+        raise ValueError(f"{what}: head dim {d} unsupported ({SUPPORTED_HEAD_DIMS})")
+    if qp.dtype not in _UT_CODES or kp.dtype != qp.dtype or vp.dtype != qp.dtype or out_dtype not in _UT_CODES:
+        raise ValueError(f"{what}: projections and out_dtype must be fp32 or bf16")
+    K = wq.shape[0]
+    for name, w in (("wq", wq), ("wk", wk), ("wv", wv)):
+        if w.dtype != torch.float32 or tuple(w.shape) != (K, HD):
+            raise ValueError(f"{what}: {name} must be fp32 [{K},{HD}]")
+    if conv_state is not None:
+        for st in conv_state:
+            if st.dtype != torch.float32 or tuple(st.shape) != (B, K - 1, HD):
+                raise ValueError(f"{what}: conv_state buffers must be fp32 [{B},{K - 1},{HD}]")
+    tensors = [qp, kp, vp, wq, wk, wv] + list(conv_state or [])
+    for i, t in enumerate(tensors):
+        _contig(f"arg{i}", t)
+    dev = _require_gpu(tensors, what)
+    q = torch.empty((B, T, H, d), dtype=out_dtype, device=dev)
+    k = torch.empty_like(q)
+    v = torch.empty_like(q)
+    new = tuple(torch.empty((B, K - 1, HD), dtype=torch.float32, device=dev) for _ in range(3)) \
+        if return_state else (None, None, None)
+    bin_ = conv_state if conv_state is not None else (None, None, None)
+    rc = _lib.lib().kda_prologue(_stream(dev), _ptr(qp), _ptr(kp), _ptr(vp), _ptr(wq), _ptr(wk), _ptr(wv),
+                                 *(_ptr(b) for b in bin_), *(_ptr(b) for b in new), _ptr(q), _ptr(k), _ptr(v),
+                                 B, T, H, d, K, _UT_CODES[qp.dtype], _UT_CODES[out_dtype])
+    _lib.check(rc, what)
+    return q, k, v, (new if return_state else None)
+
+
+def kda_epilogue(o, gate, eps: float = 1e-6, out_dtype=torch.bfloat16):
+    """``sigmoid(gate) * headwise_rms_norm(o)`` (``net/kda.py:205-214`` before ``W_o``).
+
+    ``o [B, T, H, dv]``, ``gate [B, T, H*dv]`` logits (fp32 or bf16); returns
+    ``[B, T, H*dv]`` in out_dtype.
+    """
+    what = "kda_epilogue"
+    if o.dim() != 4:
+        raise ValueError(f"{what}: o must be [B,T,H,dv]")
+    B, T, H, dv = o.shape
+    if tuple(gate.shape) != (B, T, H * dv):
+        raise ValueError(f"{what}: gate must be [{B},{T},{H * dv}]")
+    if dv not in SUPPORTED_HEAD_DIMS:
+        raise ValueError(f"{what}: dv={dv} unsupported ({SUPPORTED_HEAD_DIMS})")
+    if o.dtype not in _UT_CODES or gate.dtype not in _UT_CODES or out_dtype not in _UT_CODES:
+        raise ValueError(f"{what}: dtypes must be fp32 or bf16")
+    _contig("o", o)
+    _contig("gate", gate)
+    dev = _require_gpu([o, gate], what)
+    y = torch.empty((B, T, H * dv), dtype=out_dtype, device=dev)
+    rc = _lib.lib().kda_epilogue(_stream(dev), _ptr(o), _ptr(gate), _ptr(y), B, T, H, dv, float(eps),
+                                 _UT_CODES[o.dtype], _UT_CODES[gate.dtype], _UT_CODES[out_dtype])
+    _lib.check(rc, what)
+    return y
 
 
 def varlen_status(workspace, B, T, H, dk, dv, n_seqs, in_code=_lib.KDA_DTYPE_BF16) -> int:

@@ -191,6 +191,37 @@ KDA_API int kda_ut_solve(hipStream_t stream, const void* a, const void* b, void*
 KDA_API int kda_ut_solve_bwd(hipStream_t stream, const void* a, const void* x, const void* dx,
                 void* da, void* db, int H, int C, int N, int dtype, int transpose);
 
+/*
+ * Prologue of the KDA layer around kda_chunk_fwd: per channel the causal
+ * depthwise short convolution of the projections (net/shortconv.py:14-33,
+ * continued across calls by buffers as net/kda.py:383-389), swish
+ * (net/norm.py:15-17), and for q and k the per-head L2 normalisation
+ * x / (||x|| + 1e-12) (net/norm.py:53-66) -- net/kda.py:194-202.  qp, kp, vp
+ * [B,T,H*d] in in_dtype (KDA_DTYPE_F32 or KDA_DTYPE_BF16); conv taps wq, wk, wv
+ * [K, H*d] fp32 (w[i] weights the input i steps back, 1 <= K <= 8); buffers
+ * b*_in [B, K-1, H*d] fp32 (the previous K-1 inputs, oldest first; null =
+ * zeros) and b*_out (the last K-1 inputs after this call; null = not kept; may
+ * equal b*_in); outputs q, k, v [B,T,H,d] in out_dtype (KDA_DTYPE_F32 or
+ * KDA_DTYPE_BF16).  d = dk = dv in {64, 128}.
+ */
+KDA_API int kda_prologue(hipStream_t stream,
+                const void* qp, const void* kp, const void* vp,
+                const float* wq, const float* wk, const float* wv,
+                const float* bq_in, const float* bk_in, const float* bv_in,
+                float* bq_out, float* bk_out, float* bv_out,
+                void* q, void* k, void* v,
+                int B, int T, int H, int d, int K, int in_dtype, int out_dtype);
+
+/*
+ * Epilogue of the KDA layer before the output projection (net/kda.py:205-214
+ * without W_o): y = sigmoid(gate) * o / sqrt(mean over the head's dv
+ * channels of o^2 + eps) (net/norm.py:69-73, eps = 1e-6 there).  o
+ * [B,T,H,dv] and gate logits [B,T,H*dv] in their dtypes (F32 or BF16), y
+ * [B,T,H*dv] in out_dtype.  dv in {64, 128}.
+ */
+KDA_API int kda_epilogue(hipStream_t stream, const void* o, const void* gate, void* y,
+                int B, int T, int H, int dv, float eps, int o_dtype, int gate_dtype, int out_dtype);
+
 /* Message of the last failure on the calling thread ("" if none). */
 KDA_API const char* kda_last_error(void);
 
