@@ -50,6 +50,8 @@ _SIGNATURES = {
     "kda_ut_solve_bwd": (_i, [_vp, _vp, _vp, _vp, _vp, _vp, _i, _i, _i, _i, _i]),
     "kda_prologue": (_i, [_vp] * 16 + [_i] * 7),
     "kda_epilogue": (_i, [_vp, _vp, _vp, _vp, _i, _i, _i, _i, _f, _i, _i, _i]),
+    "kda_decode_layer_step": (_i, [_vp] * 15 + [_i, _i, _i, _i, _f, _f, _i, _i, _vp, _sz]),
+    "kda_decode_layer_workspace": (_sz, [_i, _i, _i, _i]),
     "kda_last_error": (ctypes.c_char_p, []),
     "kda_abi_version": (_i, []),
 }

@@ -525,4 +525,58 @@ int kda_epilogue(hipStream_t stream, const void* o, const void* gate, void* y, i
   return KDA_OK;
 }
 
+size_t kda_decode_layer_workspace(int B, int H, int d, int in_dtype) {
+  if (B < 1 || H < 1 || !dim_ok(d) || (in_dtype != KDA_DTYPE_F32 && in_dtype != KDA_DTYPE_BF16)) return 0;
+  const size_t n = static_cast<size_t>(B) * H * d;
+  const size_t es = in_dtype == KDA_DTYPE_F32 ? 4 : 2;
+  return 3 * align_up(n * es) + align_up(n * 4);
+}
+
+int kda_decode_layer_step(hipStream_t stream, const void* qp, const void* kp, const void* vp,
+                          const void* g, const void* beta, const void* gate,
+                          const float* wq, const float* wk, const float* wv,
+                          float* bq, float* bk, float* bv, float* state, void* y,
+                          int B, int H, int d, int K, float scale, float eps, int in_dtype, int out_dtype,
+                          void* workspace, size_t workspace_bytes) {
+  g_err[0] = 0;
+  if (!qp || !kp || !vp || !g || !beta || !gate || !wq || !wk || !wv || !state || !y)
+    return fail(KDA_ERR_INVALID_ARGUMENT, "null pointer");
+  if (K > 1 && (!bq || !bk || !bv)) return fail(KDA_ERR_INVALID_ARGUMENT, "null conv buffer");
+  if (B < 1 || H < 1) return fail(KDA_ERR_INVALID_ARGUMENT, "B=%d, H=%d must be >= 1", B, H);
+  if (!dim_ok(d)) return fail(KDA_ERR_UNSUPPORTED, "d=%d: this build runs d in {64, 128}", d);
+  if (K < 1 || K > 8) return fail(KDA_ERR_UNSUPPORTED, "K=%d: conv kernels of 1..8 taps", K);
+  if ((in_dtype != KDA_DTYPE_F32 && in_dtype != KDA_DTYPE_BF16) ||
+      (out_dtype != KDA_DTYPE_F32 && out_dtype != KDA_DTYPE_BF16))
+    return fail(KDA_ERR_INVALID_ARGUMENT, "in_dtype=%d, out_dtype=%d: F32 or BF16", in_dtype, out_dtype);
+  if (!std::isfinite(scale) || !std::isfinite(eps) || !(eps >= 0.f))
+    return fail(KDA_ERR_INVALID_ARGUMENT, "scale and eps must be finite (eps >= 0)");
+  if (static_cast<int64_t>(B) * H > 0x3FFFFFFFLL) return fail(KDA_ERR_INVALID_ARGUMENT, "B*H too large");
+  const size_t need = kda_decode_layer_workspace(B, H, d, in_dtype);
+  if (!workspace || workspace_bytes < need)
+    return fail(KDA_ERR_WORKSPACE, "workspace of %zu bytes is too small (need %zu)", workspace_bytes, need);
+  const size_t n = static_cast<size_t>(B) * H * d;
+  const size_t es = in_dtype == KDA_DTYPE_F32 ? 4 : 2;
+  unsigned char* ws = static_cast<unsigned char*>(workspace);
+  void* q = ws;
+  void* k = ws + align_up(n * es);
+  void* v = ws + 2 * align_up(n * es);
+  float* o = reinterpret_cast<float*>(ws + 3 * align_up(n * es));
+  const int dt = in_dtype == KDA_DTYPE_F32 ? 0 : 1;
+  kda::PrologueArgs p{};
+  p.qp = qp; p.kp = kp; p.vp = vp; p.wq = wq; p.wk = wk; p.wv = wv;
+  p.bq_in = bq; p.bk_in = bk; p.bv_in = bv; p.bq_out = bq; p.bk_out = bk; p.bv_out = bv;
+  p.q = q; p.k = k; p.v = v; p.B = B; p.T = 1; p.H = H; p.K = K;
+  hipError_t e = kda::launch_prologue(p, d, dt, dt, stream);
+  if (e != hipSuccess) return hip_fail(e, "layer step prologue launch");
+  kda::DecodeArgs a{};
+  a.q = q; a.k = k; a.v = v; a.g = g; a.beta = beta; a.state = state; a.o = o; a.scale = scale;
+  e = kda::launch_decode(a, d, in_dtype, 0, static_cast<int>(static_cast<int64_t>(B) * H), stream);
+  if (e != hipSuccess) return hip_fail(e, "layer step decode launch");
+  kda::EpilogueArgs ep{};
+  ep.o = o; ep.gate = gate; ep.y = y; ep.B = B; ep.T = 1; ep.H = H; ep.eps = eps;
+  e = kda::launch_epilogue(ep, d, 0, dt, out_dtype == KDA_DTYPE_F32 ? 0 : 1, stream);
+  if (e != hipSuccess) return hip_fail(e, "layer step epilogue launch");
+  return KDA_OK;
+}
+
 }  // extern "C"

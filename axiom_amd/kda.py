@@ -392,6 +392,43 @@ def kda_epilogue(o, gate, eps: float = 1e-6, out_dtype=torch.bfloat16):
     return y
 
 
+def kda_decode_layer_step(qp, kp, vp, g, beta, gate, wq, wk, wv, conv_state, state, scale: float = 1.0,
+                          eps: float = 1e-6, out_dtype=torch.float32, workspace=None):
+    """One decode token of the layer (``net/kda.py:277-295`` minus projections and ``W_o``).
+
+    ``qp, kp, vp [B, H*d]``, ``g [B, H, d]``, ``beta [B, H]``, ``gate [B, H*d]``
+    (logits) share a dtype (fp32 or bf16); ``wq, wk, wv [K, H*d]`` fp32;
+    ``conv_state`` three fp32 ``[B, K-1, H*d]`` buffers and ``state
+    [B, H, d, d]`` fp32 are updated in place.  Returns ``y [B, H*d]``.
+    """
+    what = "kda_decode_layer_step"
+    B, H, d = g.shape
+    if tuple(qp.shape) != (B, H * d) or kp.shape != qp.shape or vp.shape != qp.shape or gate.shape != qp.shape:
+        raise ValueError(f"{what}: qp, kp, vp, gate must be [{B},{H * d}]")
+    if tuple(beta.shape) != (B, H) or tuple(state.shape) != (B, H, d, d) or state.dtype != torch.float32:
+        raise ValueError(f"{what}: beta [B,H], state fp32 [B,H,d,d] expected")
+    dt = qp.dtype
+    if dt not in _UT_CODES or any(t.dtype != dt for t in (kp, vp, g, beta, gate)):
+        raise ValueError(f"{what}: qp, kp, vp, g, beta, gate must share a dtype in fp32/bf16")
+    K = wq.shape[0]
+    bq, bk, bv = conv_state
+    tensors = [qp, kp, vp, g, beta, gate, wq, wk, wv, bq, bk, bv, state]
+    for i, t in enumerate(tensors):
+        _contig(f"arg{i}", t)
+    dev = _require_gpu(tensors, what)
+    L = _lib.lib()
+    need = int(L.kda_decode_layer_workspace(B, H, d, _UT_CODES[dt]))
+    if need == 0:
+        raise ValueError(f"{what}: unsupported configuration")
+    if workspace is None or workspace.numel() * workspace.element_size() < need:
+        workspace = torch.empty(need, dtype=torch.uint8, device=dev)
+    y = torch.empty((B, H * d), dtype=out_dtype, device=dev)
+    rc = L.kda_decode_layer_step(_stream(dev), *(_ptr(t) for t in tensors), _ptr(y), B, H, d, K, float(scale),
+                                 float(eps), _UT_CODES[dt], _UT_CODES[out_dtype], _ptr(workspace), need)
+    _lib.check(rc, what)
+    return y
+
+
 def varlen_status(workspace, B, T, H, dk, dv, n_seqs, in_code=_lib.KDA_DTYPE_BF16) -> int:
     """Validation bits of the last varlen call that used ``workspace`` (synchronises)."""
     flags = ctypes.c_int32(0)

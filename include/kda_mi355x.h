@@ -222,6 +222,29 @@ KDA_API int kda_prologue(hipStream_t stream,
 KDA_API int kda_epilogue(hipStream_t stream, const void* o, const void* gate, void* y,
                 int B, int T, int H, int dv, float eps, int o_dtype, int gate_dtype, int out_dtype);
 
+/*
+ * One decode token of the whole KDA layer between its projections and W_o,
+ * with the short-conv buffers and the state carried in place: the streaming
+ * recurrent_step of net/kda.py:277-295 (conv steps net/shortconv.py:36-62,
+ * postprocess :194-202, delta rule :298-310, o = S^T q :293, output gate
+ * :205-214 without W_o).  qp, kp, vp [B, H*d], g [B,H,d] (log decay), beta
+ * [B,H], gate logits [B, H*d] in in_dtype (KDA_DTYPE_F32 or KDA_DTYPE_BF16);
+ * conv taps [K, H*d] fp32; buffers [B, K-1, H*d] fp32 and state [B,H,d,d]
+ * fp32 updated in place; y [B, H*d] in out_dtype (F32 or BF16).  Three
+ * launches (prologue, decode, epilogue) through a caller workspace of
+ * kda_decode_layer_workspace bytes.  d in {64, 128}, 1 <= K <= 8.
+ */
+KDA_API int kda_decode_layer_step(hipStream_t stream,
+                const void* qp, const void* kp, const void* vp,
+                const void* g, const void* beta, const void* gate,
+                const float* wq, const float* wk, const float* wv,
+                float* bq, float* bk, float* bv, float* state, void* y,
+                int B, int H, int d, int K, float scale, float eps, int in_dtype, int out_dtype,
+                void* workspace, size_t workspace_bytes);
+
+/* Workspace bytes kda_decode_layer_step needs (0 on bad input).  Host-only. */
+KDA_API size_t kda_decode_layer_workspace(int B, int H, int d, int in_dtype);
+
 /* Message of the last failure on the calling thread ("" if none). */
 KDA_API const char* kda_last_error(void);
 

@@ -103,3 +103,45 @@ def test_epilogue_matches_oracle(cuda, o_dt, g_dt, y_dt, dv):
     torch.cuda.synchronize()
     ref = Lr.epilogue(_as(o, o_dt), _as(gate, g_dt), eps=1e-6)
     _close(y, ref, o_dt == g_dt == y_dt == torch.float32)
+
+
+@pytest.mark.parametrize("dt,d", [(torch.float32, 128), (torch.bfloat16, 64)])
+def test_decode_layer_steps_equal_the_whole_sequence(cuda, dt, d):
+    """T layer steps (conv buffers and state carried in place) == prologue over the
+    T tokens, the recurrence, and the epilogue (the decode == chunked invariant of
+    the reference's generation path, net/kda.py:277-295)."""
+    import axiom_amd
+    from oracle import inputs, kda_oracle as K
+    B, T, H, Kc = 2, 12, 2, 4
+    rng = np.random.default_rng(d)
+    xs, ws, _ = _proj(B, T, H, d, Kc, seed=d + 1)
+    base = inputs.make_inputs(B, T, H, d, d, seed=d + 2, dtype="fp32")
+    gate = rng.standard_normal((B, T, H * d)).astype(np.float32)
+    S0 = (rng.standard_normal((B, H, d, d)) * 0.05).astype(np.float32)
+    xs_r = [_as(x, dt) for x in xs]
+    g_r, b_r, gate_r = _as(base["g"], dt), _as(base["beta"], dt), _as(gate, dt)
+    q, k, v, _ = Lr.prologue(*xs_r, *ws, H)
+    if dt == torch.bfloat16:   # the layer step hands bf16 q, k, v to the decode kernel
+        q, k, v = (_as(x.astype(np.float32), dt) for x in (q, k, v))
+    o, hT = K.recurrent_fwd(q, k, v, g_r, b_r, h0=S0)
+    y_ref = Lr.epilogue(o, gate_r)
+    state = torch.from_numpy(S0).to(cuda)
+    bufs = tuple(torch.zeros((B, Kc - 1, H * d), device=cuda) for _ in range(3))
+    ws_t = [torch.from_numpy(w).to(cuda) for w in ws]
+    ys = []
+    for t in range(T):
+        args = [torch.from_numpy(np.ascontiguousarray(x[:, t])).to(cuda, dt) for x in xs]
+        g_t = torch.from_numpy(np.ascontiguousarray(base["g"][:, t])).to(cuda, dt)
+        b_t = torch.from_numpy(np.ascontiguousarray(base["beta"][:, t])).to(cuda, dt)
+        gt_t = torch.from_numpy(np.ascontiguousarray(gate[:, t])).to(cuda, dt)
+        ys.append(axiom_amd.kda_decode_layer_step(*args, g_t, b_t, gt_t, *ws_t, bufs, state))
+    torch.cuda.synchronize()
+    y = torch.stack(ys, 1).double().cpu().numpy()
+    if dt == torch.float32:
+        assert np.abs(y - y_ref).max() <= 1e-4, np.abs(y - y_ref).max()
+        assert np.abs(state.cpu().numpy() - hT).max() <= 1e-5
+    else:
+        assert np.linalg.norm(y - y_ref) / np.linalg.norm(y_ref) <= 1e-2
+        assert np.linalg.norm(state.cpu().numpy() - hT) / np.linalg.norm(hT) <= 1e-2
+    for buf, x in zip(bufs, xs_r):
+        np.testing.assert_allclose(buf.cpu().numpy(), x[:, T - (Kc - 1):], rtol=0, atol=0)
