@@ -43,6 +43,9 @@ constexpr int kChunkThreads = 512;
 // Scan workgroups likewise: one per (chain, 32-column slice), 512 threads, one
 // state column per thread.
 constexpr int kScanThreads = 512;
+// The prep kernel likewise (the channel sums of a score tile pair split over
+// the two halves of the workgroup).
+constexpr int kPrepThreads = 512;
 
 __device__ __forceinline__ float ex2(float x) { return __builtin_amdgcn_exp2f(x); }
 
@@ -177,22 +180,24 @@ __device__ __forceinline__ void lds_load_in(float* dst, const void* src, int64_t
 // prep: G, gamma*q, lambda*k, gamma_C, Aqk, T, W, U of one chunk-head
 // ---------------------------------------------------------------------------
 template <int D, int DTQ, int DTG>
-__global__ __launch_bounds__(kThreads) void kda_bwd_prep_kernel(BwdArgs a) {
+__global__ __launch_bounds__(kPrepThreads) void kda_bwd_prep_kernel(BwdArgs a) {
   typedef BwdDims<D> BD;
   constexpr int P = BD::P, PC = BD::PC;
   __shared__ float sQ[kC * P], sK[kC * P], sG[kC * P];
   __shared__ float sL[kC * PC], sT[kC * PC];
   __shared__ float sX0[16 * P], sX1[16 * P], sKf[16 * P];
   __shared__ float sB[kC];
+  __shared__ float sRed[2 * 256];   // the second half's partial sums of a tile pair
+  constexpr int NTH = kPrepThreads;
   const int t = threadIdx.x;
   const int H = a.H;
   const int u = blockIdx.x / H, h = blockIdx.x - u * H;
   const ChunkRows cr = chunk_rows(a, u);
   const int64_t ch = static_cast<int64_t>(u) * H + h;
 
-  lds_load_in<DTQ, D, D, P>(sQ, a.q, cr.row0, cr.len, H, h, 0, a.scale);
-  lds_load_in<DTQ, D, D, P>(sK, a.k, cr.row0, cr.len, H, h, 0, 1.f);
-  lds_load_in<DTG, D, D, P>(sG, a.g, cr.row0, cr.len, H, h, 0, 1.f);
+  lds_load_in<DTQ, D, D, P, NTH>(sQ, a.q, cr.row0, cr.len, H, h, 0, a.scale);
+  lds_load_in<DTQ, D, D, P, NTH>(sK, a.k, cr.row0, cr.len, H, h, 0, 1.f);
+  lds_load_in<DTG, D, D, P, NTH>(sG, a.g, cr.row0, cr.len, H, h, 0, 1.f);
   if (t < kC) sB[t] = (t < cr.len) ? ld1<DTG>(a.beta, (cr.row0 + t) * H + h) : 0.f;
   __syncthreads();
   // in-chunk inclusive cumsum of g, in log2 units
@@ -212,7 +217,7 @@ __global__ __launch_bounds__(kThreads) void kda_bwd_prep_kernel(BwdArgs a) {
     float* GL = a.GL + ch * kC * D;
     float* QG = a.QG + ch * kC * D;
     float* KL = a.KL + ch * kC * D;
-    for (int e = t; e < kC * D; e += kThreads) {
+    for (int e = t; e < kC * D; e += NTH) {
       const int c = e / D, d = e - c * D;
       const float gl = sG[c * P + d];
       const float glast = sG[(kC - 1) * P + d];
@@ -225,11 +230,15 @@ __global__ __launch_bounds__(kThreads) void kda_bwd_prep_kernel(BwdArgs a) {
 
   // scores: Aqk (c >= i) straight to the workspace, L = beta_c Akk (c > i) to LDS
   float* AQ = a.AQ + ch * kC * kC;
-  const int r = t >> 4, i16 = t & 15;   // output (r, i16) of a 16 x 16 tile pair
+  // output (r, i16) of a 16 x 16 tile pair; the two halves of the workgroup
+  // sum over the two halves of the channels and add up through sRed
+  const int t2 = t & 255, half = t >> 8;
+  const int r = t2 >> 4, i16 = t2 & 15;
+  const int d0 = half * (D / 2);
   for (int R = 0; R < 4; ++R) {
     const int a0 = 16 * R;
     // row operands of tile R with the factor 2^(G_c - G_a)
-    for (int e = t; e < 16 * D; e += kThreads) {
+    for (int e = t; e < 16 * D; e += NTH) {
       const int rr = e / D, d = e - rr * D;
       const float fr = ex2(sG[(a0 + rr) * P + d] - sG[a0 * P + d]);
       sX0[rr * P + d] = sQ[(a0 + rr) * P + d] * fr;
@@ -237,20 +246,24 @@ __global__ __launch_bounds__(kThreads) void kda_bwd_prep_kernel(BwdArgs a) {
     }
     for (int s = 0; s < R; ++s) {
       __syncthreads();  // sX0/sX1 written; previous sKf readers done
-      for (int e = t; e < 16 * D; e += kThreads) {
+      for (int e = t; e < 16 * D; e += NTH) {
         const int ii = e / D, d = e - ii * D;
         sKf[ii * P + d] = sK[(16 * s + ii) * P + d] * ex2(sG[a0 * P + d] - sG[(16 * s + ii) * P + d]);
       }
       __syncthreads();
       float accA = 0.f, accL = 0.f;
       #pragma unroll 4
-      for (int d = 0; d < D; ++d) {
+      for (int d = d0; d < d0 + D / 2; ++d) {
         const float kf = sKf[i16 * P + d];
         accA = fmaf(sX0[r * P + d], kf, accA);
         accL = fmaf(sX1[r * P + d], kf, accL);
       }
-      AQ[(a0 + r) * kC + 16 * s + i16] = accA;
-      sL[(a0 + r) * PC + 16 * s + i16] = accL;
+      if (half) { sRed[t2] = accA; sRed[256 + t2] = accL; }
+      __syncthreads();
+      if (!half) {
+        AQ[(a0 + r) * kC + 16 * s + i16] = accA + sRed[t2];
+        sL[(a0 + r) * PC + 16 * s + i16] = accL + sRed[256 + t2];
+      }
     }
     // diagonal tile, 2^(G_c - G_i) directly
     {
@@ -258,45 +271,51 @@ __global__ __launch_bounds__(kThreads) void kda_bwd_prep_kernel(BwdArgs a) {
       float accA = 0.f, accL = 0.f;
       if (i16 <= r) {
         #pragma unroll 4
-        for (int d = 0; d < D; ++d) {
+        for (int d = d0; d < d0 + D / 2; ++d) {
           const float e = ex2(sG[c * P + d] - sG[i * P + d]);
           const float ki = sK[i * P + d] * e;
           accA = fmaf(sQ[c * P + d], ki, accA);
           accL = fmaf(sK[c * P + d], ki, accL);
         }
       }
-      AQ[c * kC + i] = accA;
-      sL[c * PC + i] = (i16 < r) ? accL * sB[c] : 0.f;
-      // upper triangle of the row band: zero
-      for (int s = R + 1; s < 4; ++s) {
-        AQ[c * kC + 16 * s + i16] = 0.f;
-        sL[c * PC + 16 * s + i16] = 0.f;
+      __syncthreads();   // the off-diagonal sums have been read out of sRed
+      if (half) { sRed[t2] = accA; sRed[256 + t2] = accL; }
+      __syncthreads();
+      if (!half) {
+        AQ[c * kC + i] = accA + sRed[t2];
+        sL[c * PC + i] = (i16 < r) ? (accL + sRed[256 + t2]) * sB[c] : 0.f;
+        // upper triangle of the row band: zero
+        for (int s = R + 1; s < 4; ++s) {
+          AQ[c * kC + 16 * s + i16] = 0.f;
+          sL[c * PC + 16 * s + i16] = 0.f;
+        }
       }
     }
     __syncthreads();  // sX0/sX1 reused by the next row tile
   }
 
   // T = (I + L)^-1
-  invert_unit_lower64<PC, kThreads>(sL, sT, sX0);
+  invert_unit_lower64<PC, NTH>(sL, sT, sX0);
   {
     float* TM = a.TM + ch * kC * kC;
-    for (int e = t; e < kC * kC; e += kThreads) {
+    for (int e = t; e < kC * kC; e += NTH) {
       const int c = e / kC, i = e - c * kC;
       TM[e] = sT[c * PC + i];
     }
   }
   // W = T (beta gamma k), U = T (beta v)
-  lds_load_in<DTQ, D, D, P>(sQ, a.v, cr.row0, cr.len, H, h, 0, 1.f);
+  lds_load_in<DTQ, D, D, P, NTH>(sQ, a.v, cr.row0, cr.len, H, h, 0, 1.f);
   __syncthreads();
-  for (int e = t; e < kC * D; e += kThreads) {
+  for (int e = t; e < kC * D; e += NTH) {
     const int c = e / D, d = e - c * D;
     sK[c * P + d] *= sB[c] * ex2(sG[c * P + d]);
     sQ[c * P + d] *= sB[c];
   }
   __syncthreads();
   {
-    constexpr int NJ = BD::NJ;
-    const int rm = t >> 4, cn = t & 15;
+    constexpr int TC = NTH / 16;
+    constexpr int NJ = D / TC;
+    const int rm = t / TC, cn = t % TC;
     float accW[4][NJ], accU[4][NJ];
 #pragma unroll
     for (int i = 0; i < 4; ++i)
@@ -309,7 +328,7 @@ __global__ __launch_bounds__(kThreads) void kda_bwd_prep_kernel(BwdArgs a) {
       for (int i = 0; i < 4; ++i) tv[i] = sT[(rm + 16 * i) * PC + m];
 #pragma unroll
       for (int j = 0; j < NJ; ++j) {
-        const float x = sK[m * P + cn + 16 * j], y = sQ[m * P + cn + 16 * j];
+        const float x = sK[m * P + cn + TC * j], y = sQ[m * P + cn + TC * j];
 #pragma unroll
         for (int i = 0; i < 4; ++i) {
           accW[i][j] = fmaf(tv[i], x, accW[i][j]);
@@ -323,8 +342,8 @@ __global__ __launch_bounds__(kThreads) void kda_bwd_prep_kernel(BwdArgs a) {
     for (int i = 0; i < 4; ++i)
 #pragma unroll
       for (int j = 0; j < NJ; ++j) {
-        WM[(rm + 16 * i) * D + cn + 16 * j] = accW[i][j];
-        UM[(rm + 16 * i) * D + cn + 16 * j] = accU[i][j];
+        WM[(rm + 16 * i) * D + cn + TC * j] = accW[i][j];
+        UM[(rm + 16 * i) * D + cn + TC * j] = accU[i][j];
       }
   }
 }
@@ -986,7 +1005,7 @@ template <int D, int DTQ, int DTG, int DO>
 hipError_t launch_bwd_t(const BwdArgs& a, hipStream_t s) {
   const int chunk_heads = a.B * a.NT * a.H;
   const int chains = a.B * a.H;
-  hipLaunchKernelGGL((kda_bwd_prep_kernel<D, DTQ, DTG>), dim3(chunk_heads), dim3(kThreads), 0, s, a);
+  hipLaunchKernelGGL((kda_bwd_prep_kernel<D, DTQ, DTG>), dim3(chunk_heads), dim3(kPrepThreads), 0, s, a);
   hipError_t e = hipGetLastError();
   if (e != hipSuccess) return e;
   const int scan_grid = (chains + 7) / 8 * 8 * (D / 32);
