@@ -22,6 +22,8 @@ Also reported on the same JSON line:
   dbeta, dh0 from fp32 do and dht) on the same config-1 inputs, per call, with
   its algorithmic bytes (read q, k, v, g, beta bf16 and do fp32 plus dht;
   write the five gradients and dh0 fp32) against the HBM peak;
+* ``ut_solve``: the standalone unit-triangular solve at the reference's case
+  (H=12, C=64, N=dk+dv=256, fp32), both orientations, per call;
 * ``cpu_baseline``: the oracle's fp32 restatement of the reference jax body
   (torch CPU, all available cores) timed on a bounded sample of the same
   workload on this host.
@@ -197,6 +199,30 @@ def bench_backward(args, fwd_inputs, device):
                 config="B4 T4096 H16 d128 bf16 inputs, fp32 do and dht, zero h0")
 
 
+def bench_ut_solve(args, device):
+    import axiom_amd
+    H, C, N = 12, 64, 256
+    gen = torch.Generator(device=device)
+    gen.manual_seed(args.seed + 4)
+    a = torch.eye(C, device=device) + torch.tril((torch.rand(H, C, C, device=device, generator=gen) - 0.5) * 0.5, -1)
+    b = torch.randn(H, C, N, device=device, generator=gen)
+    out = {}
+    stream = torch.cuda.current_stream(device)
+    for tr in (False, True):
+        for _ in range(3):
+            axiom_amd.ut_solve(a, b, transpose=tr)
+        torch.cuda.synchronize()
+        e0, e1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+        e0.record(stream)
+        for _ in range(50):
+            axiom_amd.ut_solve(a, b, transpose=tr)
+        e1.record(stream)
+        torch.cuda.synchronize()
+        out["us_per_call_t" if tr else "us_per_call"] = e0.elapsed_time(e1) / 50 * 1e3
+    out["config"] = "H12 C64 N256 fp32 (the reference's case)"
+    return out
+
+
 def cpu_baseline(fwd_inputs, seconds):
     """Oracle port (fp32, torch CPU) of the reference jax body on a bounded sample."""
     from oracle import kda_oracle as K
@@ -298,6 +324,7 @@ def main():
         line["decode"] = bench_decode(args, device)
     if not args.no_backward:
         line["backward"] = bench_backward(args, fwd["inputs"], device)
+    line["ut_solve"] = bench_ut_solve(args, device)
     if not args.no_cpu_baseline:
         line["cpu_baseline"] = cpu_baseline(fwd["inputs"], args.cpu_seconds)
     print(json.dumps(line), flush=True)
