@@ -4,7 +4,10 @@
 Headline (the ``value``): chunked KDA forward throughput in tokens/s at
 B=4, T=4096, H=16, dk=dv=128, C=64, bf16 inputs, fp32 o and fp32 final state
 (``configs[1]`` of the benchmark definition), inputs resident in HBM.  One
-"step" = one ``kda_chunk_fwd`` over the whole batch.
+"step" = one ``kda_chunk_fwd`` over the whole batch.  The default warm-up is
+100 untimed steps (~25 ms): after idle the GPU's clocks ramp up over the first
+~80 calls (336 us per call for the first 20, 244 us from the 80th on), and the
+timed steps are meant to see the steady state.
 
 Also reported on the same JSON line:
 * TFLOP/s and % of bf16 dense MFMA peak with the algorithmic count
@@ -262,7 +265,7 @@ def main():
     ap = argparse.ArgumentParser(description=__doc__.split("\n")[0])
     ap.add_argument("--gpus", type=int, default=1)
     ap.add_argument("--steps", type=int, default=20)
-    ap.add_argument("--warmup", type=int, default=5)
+    ap.add_argument("--warmup", type=int, default=100)
     ap.add_argument("--decode-steps", type=int, default=128)
     ap.add_argument("--seed", type=int, default=0)
     ap.add_argument("--cpu-seconds", type=float, default=10.0)
