@@ -7,8 +7,8 @@ validates arguments and hands device pointers to that library.
 """
 
 from .kda import (cc_scan, kda_chunk, kda_chunk_bwd, kda_chunk_fwd, kda_decode_layer_step,  # noqa: F401
-                  kda_epilogue, kda_prologue, kda_recurrent_step, solve, solve_t, ut_solve, ut_solve_bwd,
+                  kda_epilogue, kda_layer_fwd, kda_prologue, kda_recurrent_step, solve, solve_t, ut_solve, ut_solve_bwd,
                   varlen_status)
 
 __all__ = ["cc_scan", "kda_chunk", "kda_chunk_bwd", "kda_chunk_fwd", "kda_decode_layer_step", "kda_epilogue",
-           "kda_prologue", "kda_recurrent_step", "solve", "solve_t", "ut_solve", "ut_solve_bwd", "varlen_status"]
+           "kda_layer_fwd", "kda_prologue", "kda_recurrent_step", "solve", "solve_t", "ut_solve", "ut_solve_bwd", "varlen_status"]

@@ -118,11 +118,20 @@ int check_dims(int H, int dk, int dv) {
 template <typename T>
 T* at(void* base, size_t off) { return reinterpret_cast<T*>(static_cast<char*>(base) + off); }
 
+// The layer's short conv fused into the intra kernel (q, k, v are then the
+// raw projections): taps and first-chunk history per tensor, K taps.
+struct FusedPrologue {
+  const float* cw[3];
+  const float* cb[3];
+  int K;
+};
+
 int chunk_fwd_impl(hipStream_t stream, const void* q, const void* k, const void* v,
                    const void* g, const void* beta, const float* h0,
                    const int32_t* cu_seqlens, int32_t n_seqs, void* o, float* ht,
                    int B, int T, int H, int dk, int dv, int chunk, float scale,
-                   int in_dtype, int out_dtype, void* ws, size_t ws_bytes) {
+                   int in_dtype, int out_dtype, void* ws, size_t ws_bytes,
+                   const FusedPrologue* pro = nullptr) {
   if (!q || !k || !v || !g || !beta) return fail(KDA_ERR_INVALID_ARGUMENT, "null input pointer");
   if (!o && T > 0) return fail(KDA_ERR_INVALID_ARGUMENT, "null output pointer o");
   if (B < 1) return fail(KDA_ERR_INVALID_ARGUMENT, "B=%d must be >= 1", B);
@@ -183,6 +192,10 @@ int chunk_fwd_impl(hipStream_t stream, const void* q, const void* k, const void*
   ia.GQ = at<void>(ws, L.GQ);
   ia.LK = at<void>(ws, L.LK);
   ia.GC = at<float>(ws, L.GC);
+  if (pro != nullptr) {
+    for (int t = 0; t < 3; ++t) { ia.cw[t] = pro->cw[t]; ia.cb[t] = pro->cb[t]; }
+    ia.K = pro->K;
+  }
 
   kda::StateArgs sa{};
   sa.geom = G;
@@ -206,7 +219,8 @@ int chunk_fwd_impl(hipStream_t stream, const void* q, const void* k, const void*
     sa.geom = G;
     const int64_t intra_grid = varlen ? L.units_bound * H : static_cast<int64_t>(B) * G.NTS * H;
     if (intra_grid > 0) {
-      hipError_t e = kda::launch_intra(ia, dk, dtq, dtg, static_cast<int>(intra_grid), stream);
+      hipError_t e = (pro != nullptr) ? kda::launch_intra_prologue(ia, dk, dtg, static_cast<int>(intra_grid), stream)
+                                      : kda::launch_intra(ia, dk, dtq, dtg, static_cast<int>(intra_grid), stream);
       if (e != hipSuccess) return hip_fail(e, "intra kernel launch");
     }
     sa.h0 = (sgi == 0) ? h0 : carry;
@@ -576,6 +590,106 @@ int kda_decode_layer_step(hipStream_t stream, const void* qp, const void* kp, co
   ep.o = o; ep.gate = gate; ep.y = y; ep.B = B; ep.T = 1; ep.H = H; ep.eps = eps;
   e = kda::launch_epilogue(ep, d, 0, dt, out_dtype == KDA_DTYPE_F32 ? 0 : 1, stream);
   if (e != hipSuccess) return hip_fail(e, "layer step epilogue launch");
+  return KDA_OK;
+}
+
+}  // extern "C"
+
+namespace {
+
+// The chunked layer forward runs the prologue inside the intra kernel when the
+// projections are bf16 and the conv has at most kFusedConvTaps taps;
+// otherwise as its own pass into workspace q, k, v.
+bool layer_fused(int K, int in_dtype) {
+  return (in_dtype == KDA_DTYPE_BF16 || in_dtype == KDA_DTYPE_BF16_F32GATES) && K >= 1 && K <= kda::kFusedConvTaps;
+}
+
+struct LayerLayout {
+  size_t chunk_ws, o, qkv, total;
+};
+
+LayerLayout layer_layout(int B, int T, int H, int d, int K, int in_dtype) {
+  LayerLayout L{};
+  const size_t n = static_cast<size_t>(B) * T * H * d;
+  L.chunk_ws = 0;
+  size_t off = align_up(ws_layout(B, T, H, d, d, 0, in_dtype).total);
+  L.o = off;
+  off += align_up(n * 4);
+  L.qkv = off;
+  if (!layer_fused(K, in_dtype)) off += 3 * align_up(n * (in_dtype == KDA_DTYPE_F32 ? 4 : 2));
+  L.total = off;
+  return L;
+}
+
+}  // namespace
+
+extern "C" {
+
+size_t kda_layer_fwd_workspace(int B, int T, int H, int d, int K, int in_dtype) {
+  if (B < 1 || T < 0 || H < 1 || !dim_ok(d) || K < 1 || K > 8) return 0;
+  if (in_dtype < KDA_DTYPE_F32 || in_dtype > KDA_DTYPE_BF16_F32GATES || in_dtype == KDA_DTYPE_F16) return 0;
+  return layer_layout(B, T, H, d, K, in_dtype).total;
+}
+
+int kda_layer_fwd(hipStream_t stream, const void* qp, const void* kp, const void* vp,
+                  const void* g, const void* beta, const void* gate,
+                  const float* wq, const float* wk, const float* wv,
+                  const float* bq_in, const float* bk_in, const float* bv_in,
+                  float* bq_out, float* bk_out, float* bv_out,
+                  const float* h0, float* ht, void* y,
+                  int B, int T, int H, int d, int K, float scale, float eps,
+                  int in_dtype, int gate_dtype, int out_dtype, void* workspace, size_t workspace_bytes) {
+  g_err[0] = 0;
+  if (B < 1 || T < 0 || H < 1) return fail(KDA_ERR_INVALID_ARGUMENT, "B=%d, T=%d, H=%d out of range", B, T, H);
+  if (!dim_ok(d)) return fail(KDA_ERR_UNSUPPORTED, "d=%d: this build runs d in {64, 128}", d);
+  if (K < 1 || K > 8) return fail(KDA_ERR_UNSUPPORTED, "K=%d: conv kernels of 1..8 taps", K);
+  if (in_dtype != KDA_DTYPE_F32 && in_dtype != KDA_DTYPE_BF16 && in_dtype != KDA_DTYPE_BF16_F32GATES)
+    return fail(KDA_ERR_INVALID_ARGUMENT, "in_dtype=%d: F32, BF16 or BF16_F32GATES", in_dtype);
+  auto ok = [](int dt) { return dt == KDA_DTYPE_F32 || dt == KDA_DTYPE_BF16; };
+  if (!ok(gate_dtype) || !ok(out_dtype))
+    return fail(KDA_ERR_INVALID_ARGUMENT, "gate_dtype=%d, out_dtype=%d: F32 or BF16", gate_dtype, out_dtype);
+  if (!wq || !wk || !wv) return fail(KDA_ERR_INVALID_ARGUMENT, "null conv taps");
+  if (T > 0 && (!qp || !kp || !vp || !g || !beta || !gate || !y))
+    return fail(KDA_ERR_INVALID_ARGUMENT, "null input or output pointer");
+  if (!std::isfinite(scale) || !std::isfinite(eps) || !(eps >= 0.f))
+    return fail(KDA_ERR_INVALID_ARGUMENT, "scale and eps must be finite (eps >= 0)");
+  if (static_cast<int64_t>(B) * T * H * 3 / 4 > 0x7FFFFFFFLL) return fail(KDA_ERR_INVALID_ARGUMENT, "too large");
+  const LayerLayout L = layer_layout(B, T, H, d, K, in_dtype);
+  if (!workspace || workspace_bytes < L.total)
+    return fail(KDA_ERR_WORKSPACE, "workspace of %zu bytes is too small (need %zu)", workspace_bytes, L.total);
+  unsigned char* ws = static_cast<unsigned char*>(workspace);
+  float* o = reinterpret_cast<float*>(ws + L.o);
+  const size_t chunk_bytes = L.o;
+  kda::PrologueArgs p{};
+  p.qp = qp; p.kp = kp; p.vp = vp; p.wq = wq; p.wk = wk; p.wv = wv;
+  p.bq_in = bq_in; p.bk_in = bk_in; p.bv_in = bv_in; p.bq_out = bq_out; p.bk_out = bk_out; p.bv_out = bv_out;
+  p.B = B; p.T = T; p.H = H; p.K = K;
+  const int pdt = in_dtype == KDA_DTYPE_F32 ? 0 : 1;
+  hipError_t e;
+  if (layer_fused(K, in_dtype)) {
+    FusedPrologue fp{{wq, wk, wv}, {bq_in, bk_in, bv_in}, K};
+    const int rc = chunk_fwd_impl(stream, qp, kp, vp, g, beta, h0, nullptr, 0, o, ht, B, T, H, d, d, 64, scale,
+                                  in_dtype, KDA_DTYPE_F32, ws, chunk_bytes, &fp);
+    if (rc != KDA_OK) return rc;
+    // the buffers are rewritten after every read of the old ones
+    e = kda::launch_prologue_buffers(p, d, pdt, stream);
+    if (e != hipSuccess) return hip_fail(e, "layer conv buffer launch");
+  } else {
+    const size_t n = static_cast<size_t>(B) * T * H * d;
+    const size_t es = in_dtype == KDA_DTYPE_F32 ? 4 : 2;
+    p.q = ws + L.qkv;
+    p.k = ws + L.qkv + align_up(n * es);
+    p.v = ws + L.qkv + 2 * align_up(n * es);
+    e = kda::launch_prologue(p, d, pdt, pdt, stream);
+    if (e != hipSuccess) return hip_fail(e, "layer prologue launch");
+    const int rc = chunk_fwd_impl(stream, p.q, p.k, p.v, g, beta, h0, nullptr, 0, o, ht, B, T, H, d, d, 64, scale,
+                                  in_dtype, KDA_DTYPE_F32, ws, chunk_bytes);
+    if (rc != KDA_OK) return rc;
+  }
+  kda::EpilogueArgs ep{};
+  ep.o = o; ep.gate = gate; ep.y = y; ep.B = B; ep.T = T; ep.H = H; ep.eps = eps;
+  e = kda::launch_epilogue(ep, d, 0, gate_dtype == KDA_DTYPE_F32 ? 0 : 1, out_dtype == KDA_DTYPE_F32 ? 0 : 1, stream);
+  if (e != hipSuccess) return hip_fail(e, "layer epilogue launch");
   return KDA_OK;
 }
 

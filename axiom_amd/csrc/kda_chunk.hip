@@ -108,7 +108,7 @@ __device__ __forceinline__ int slot_index_channel(int s) {
   return slot_channel(s >> 5, (s >> 3) & 3, s & 7);
 }
 
-template <int DK, int DV, int DTQ, int DTG, bool EXACT, int W>
+template <int DK, int DV, int DTQ, int DTG, bool EXACT, int W, bool PRO>
 __device__ __forceinline__ void intra_chunk(const IntraArgs& a, const UnitRef& U, const int h,
                                             const int64_t chead, IntraSmem<DK, DV, EXACT>& sm) {
   typedef typename Prec<EXACT>::st st;
@@ -147,32 +147,98 @@ __device__ __forceinline__ void intra_chunk(const IntraArgs& a, const UnitRef& U
   constexpr int ROWB = DK * 2;          // bytes per staged row
   constexpr int NCH = ROWB / 16;        // 16-byte chunks per row
   constexpr int RPI = 1024 / ROWB;      // rows per copy instruction
-  static_assert(!(STQ || STG) || sizeof(SM) >= 4 * kC * ROWB, "staging area exceeds the shared buffers");
+  static_assert(PRO || !(STQ || STG) || sizeof(SM) >= 4 * kC * ROWB, "staging area exceeds the shared buffers");
   static_assert(DK == DV, "staging assumes dk == dv");
+  static_assert(!PRO || (DTQ == 1 && !EXACT), "the fused prologue stages bf16 projections");
   unsigned char* const stg = reinterpret_cast<unsigned char*>(&sm);
-  auto stg_row = [&](int t, int row) { return stg + (t * kC + row) * ROWB; };
+  // With the fused prologue (PRO) each wave stages, for q, k and v, RPI rows
+  // before its own 16 (the convolution's history) into rows of its own: HR
+  // rows per wave and tensor after the 64 rows of g.
+  constexpr int HR = 16 + RPI;
+  auto stg_row = [&](int t, int row) -> unsigned char* {
+    if constexpr (PRO) {
+      if (t == 2) return stg + row * ROWB;
+      const int tt = (t == 3) ? 2 : t;   // q, k, v
+      return stg + (kC + (tt * 4 + W) * HR + (row - 16 * W + RPI)) * ROWB;
+    } else {
+      return stg + (t * kC + row) * ROWB;
+    }
+  };
   // beta first: its latency hides behind the row copies.  Copy order g, k, q,
   // v: with all four staged (SPLIT) the waits below are partial (vmcnt retires
   // in issue order), so the decay scan runs while k, q and v are still
   // arriving and the k/q decay factors while v is.
   constexpr bool SPLIT = STQ && STG;
   constexpr int NPER = 16 / RPI;        // copies per tensor per wave
+  constexpr int NQKV = PRO ? NPER + 1 : NPER;   // copies per q, k, v (PRO: one of history rows)
   // (unconditional load of a valid row, masked after the waits: a load
   // inside a branch is waited for at the branch's end)
   float beta_c = ld1<DTG>(a.beta, (U.row0 + min(c, U.len - 1)) * H + h);
+  // PRO: conv taps of this lane's channels PL*l .. PL*l + PL-1 and, for the
+  // first chunk of a sequence (wave 0), the carried inputs before it; loaded
+  // before the row copies, so the copies' partial waits cover them
+  constexpr int PL = DK / 64;
+  constexpr int KM = kFusedConvTaps;
+  float cwv[3][KM][PL];
+  float hist[3][KM - 1][PL];
+  if constexpr (PRO) {
+    const int64_t HD = static_cast<int64_t>(H) * DK;
+#pragma unroll
+    for (int tt = 0; tt < 3; ++tt)
+#pragma unroll
+      for (int i = 0; i < KM; ++i) {
+        const float* wp = a.cw[tt] + min(i, a.K - 1) * HD + h * DK + PL * l;
+        if constexpr (PL == 2) {
+          const float2 w2 = *reinterpret_cast<const float2*>(wp);
+          cwv[tt][i][0] = w2.x;
+          cwv[tt][i][1] = w2.y;
+        } else {
+          cwv[tt][i][0] = *wp;
+        }
+      }
+    if constexpr (W == 0) {
+#pragma unroll
+      for (int tt = 0; tt < 3; ++tt)
+#pragma unroll
+        for (int j = 0; j < KM - 1; ++j)
+#pragma unroll
+          for (int p = 0; p < PL; ++p) hist[tt][j][p] = 0.f;
+      if (U.n == 0) {
+        // row j - (KM-1) of the chunk is buffer row K-1 + j - (KM-1) (oldest first)
+#pragma unroll
+        for (int tt = 0; tt < 3; ++tt) {
+          if (a.cb[tt] == nullptr) continue;
+#pragma unroll
+          for (int j = 0; j < KM - 1; ++j) {
+            const int br = a.K - 1 + j - (KM - 1);
+            if (br < 0) continue;
+            const float* bp = a.cb[tt] + (static_cast<int64_t>(U.seq) * (a.K - 1) + br) * HD + h * DK + PL * l;
+#pragma unroll
+            for (int p = 0; p < PL; ++p) hist[tt][j][p] = bp[p];
+          }
+        }
+      }
+    }
+  }
   if constexpr (STQ || STG) {
 #pragma unroll
     for (int oi = 0; oi < 4; ++oi) {
       const int t = (oi == 0) ? 2 : (oi == 1) ? 1 : (oi == 2) ? 0 : 3;  // 0 q, 1 k, 2 g, 3 v
       if ((t == 2) ? !STG : !STQ) continue;
       const u16* src = static_cast<const u16*>(t == 0 ? a.q : t == 1 ? a.k : t == 2 ? a.g : a.v);
+      const int nc = (t == 2) ? NPER : NQKV;
+      const int r0 = (PRO && t != 2) ? 16 * W - RPI : 16 * W;       // first row copied
 #pragma unroll
-      for (int i = 0; i < NPER; ++i) {
-        const int row = 16 * W + RPI * i + l / NCH;                 // chunk row this lane copies
+      for (int i = 0; i < nc; ++i) {
+        const int row = r0 + RPI * i + l / NCH;                     // chunk row this lane copies
         const int cidx = (l % NCH) ^ (row & (NCH - 1));             // source chunk of LDS chunk l % NCH
-        const int64_t srow = U.row0 + min(row, U.len - 1);          // rows past the end re-read a valid row
+        // rows past the end re-read a valid row; history rows before a
+        // sequence's first chunk (replaced by the carried inputs) read row 0
+        int rv = min(row, U.len - 1);
+        if (PRO && U.n == 0) rv = max(rv, 0);
+        const int64_t srow = U.row0 + rv;
         const u16* gsrc = src + (srow * H + h) * DK + cidx * 8;
-        unsigned char* ldst = stg_row(t, 16 * W + RPI * i);
+        unsigned char* ldst = stg_row(t, r0 + RPI * i);
         __builtin_amdgcn_global_load_lds(gsrc, ldst, 16, 0, 0);
       }
     }
@@ -203,7 +269,7 @@ __device__ __forceinline__ void intra_chunk(const IntraArgs& a, const UnitRef& U
 
   // g -> log2 decay, then the tile-local inclusive scan
   if constexpr (SPLIT) {
-    wait_vmem<3 * NPER>();
+    wait_vmem<3 * NQKV>();
     __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "workgroup", "local");
   }
   uint2 sw[2 * NJ];
@@ -232,8 +298,117 @@ __device__ __forceinline__ void intra_chunk(const IntraArgs& a, const UnitRef& U
     for (int j = 0; j < NJ; ++j)
 #pragma unroll
       for (int e = 0; e < 8; ++e) asm volatile("" : "+v"(Gt[j][e]));
-    wait_vmem<NPER>();
-    __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "workgroup", "local");
+    if constexpr (!PRO) {
+      wait_vmem<NPER>();
+      __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "workgroup", "local");
+    }
+  }
+  if constexpr (PRO) {
+    // Fused prologue, k first (its rows arrive first), then q, then v: per
+    // row out = sum_i w[i] x[row - i] (fp32, taps in order), swish, for q
+    // and k times 1 / (||row|| + 1e-12), rounded to bf16 and written over
+    // the staged row -- the arithmetic of kda_prologue_kernel, lane for lane.
+    auto conv = [&](const int t, const int tt, const bool nrm) {
+      constexpr int NR = 15 + KM;     // rows 16W - (KM-1) .. 16W + 15
+      const int ci = (PL * l) >> 3, cb = ((PL * l) & 7) * 2;
+      unsigned raw[NR];
+#pragma unroll
+      for (int j = 0; j < NR; ++j) {
+        const int row = 16 * W - (KM - 1) + j;
+        const unsigned char* p = stg_row(t, row) + (ci ^ (row & (NCH - 1))) * 16 + cb;
+        raw[j] = (PL == 2) ? ds_read_b32_raw(p) : ds_read_u16_raw(p);
+      }
+      lds_settle(raw);
+      float xs[NR][PL];
+#pragma unroll
+      for (int j = 0; j < NR; ++j) {
+        xs[j][0] = bf16_to_f32(static_cast<u16>(raw[j] & 0xFFFFu));
+        if constexpr (PL == 2) xs[j][1] = bf16_to_f32(static_cast<u16>(raw[j] >> 16));
+      }
+      if constexpr (W == 0) {
+        if (U.n == 0) {
+#pragma unroll
+          for (int j = 0; j < KM - 1; ++j)
+#pragma unroll
+            for (int p = 0; p < PL; ++p) xs[j][p] = hist[tt][j][p];
+        }
+      }
+      float sv[16][PL], ss[16];
+#pragma unroll
+      for (int r2 = 0; r2 < 16; ++r2) {
+        ss[r2] = 0.f;
+#pragma unroll
+        for (int p = 0; p < PL; ++p) {
+          float acc = 0.f;
+#pragma unroll
+          for (int i = 0; i < KM; ++i)
+            if (i < a.K) acc = fmaf(cwv[tt][i][p], xs[r2 + KM - 1 - i][p], acc);
+          sv[r2][p] = acc * sigmoid_f32(acc);
+          ss[r2] = fmaf(sv[r2][p], sv[r2][p], ss[r2]);
+        }
+      }
+      if (nrm) {
+        // Row sums over the 64 lanes as a reduce-scatter: after the steps at
+        // lane distance 32, 16, 8, 4 lane l holds row 8 b5 + 4 b4 + 2 b3 + b2
+        // (its lane bits), then two butterfly steps.  Every partial is the
+        // one an xor-butterfly over 32, 16, .., 1 forms, so each row total is
+        // that butterfly's, bit for bit.
+        float v8[8], v4[4], v2[2];
+        const bool b5 = (l & 32) != 0, b4 = (l & 16) != 0, b3 = (l & 8) != 0, b2 = (l & 4) != 0;
+#pragma unroll
+        for (int j = 0; j < 8; ++j) {
+          const float snd = b5 ? ss[j] : ss[8 + j];
+          v8[j] = (b5 ? ss[8 + j] : ss[j]) + __shfl_xor(snd, 32, 64);
+        }
+#pragma unroll
+        for (int j = 0; j < 4; ++j) {
+          const float snd = b4 ? v8[j] : v8[4 + j];
+          v4[j] = (b4 ? v8[4 + j] : v8[j]) + __shfl_xor(snd, 16, 64);
+        }
+#pragma unroll
+        for (int j = 0; j < 2; ++j) {
+          const float snd = b3 ? v4[j] : v4[2 + j];
+          v2[j] = (b3 ? v4[2 + j] : v4[j]) + __shfl_xor(snd, 8, 64);
+        }
+        float v1 = (b2 ? v2[1] : v2[0]) + __shfl_xor(b2 ? v2[0] : v2[1], 4, 64);
+        v1 += __shfl_xor(v1, 2, 64);
+        v1 += __shfl_xor(v1, 1, 64);
+#pragma unroll
+        for (int r2 = 0; r2 < 16; ++r2) {
+          const int src = 32 * ((r2 >> 3) & 1) + 16 * ((r2 >> 2) & 1) + 8 * ((r2 >> 1) & 1) + 4 * (r2 & 1);
+          const float tot = __builtin_bit_cast(float, __builtin_amdgcn_readlane(__builtin_bit_cast(int, v1), src));
+          const float sc = 1.f / (sqrtf(tot) + 1e-12f);
+#pragma unroll
+          for (int p = 0; p < PL; ++p) sv[r2][p] *= sc;
+        }
+      }
+#pragma unroll
+      for (int r2 = 0; r2 < 16; ++r2) {
+        const int row = 16 * W + r2;
+        unsigned char* p = stg_row(t, row) + (ci ^ (row & (NCH - 1))) * 16 + cb;
+        if constexpr (PL == 2) {
+          ds_write_b32_raw(p, static_cast<unsigned>(f32_to_bf16_bits(sv[r2][0])) |
+                                  (static_cast<unsigned>(f32_to_bf16_bits(sv[r2][1])) << 16));
+        } else {
+          ds_write_b16_raw(p, f32_to_bf16_bits(sv[r2][0]));
+        }
+      }
+    };
+    if constexpr (SPLIT) {
+      wait_vmem<2 * NQKV>();
+      __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "workgroup", "local");
+    }
+    conv(1, 1, true);
+    if constexpr (SPLIT) {
+      wait_vmem<NQKV>();
+      __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "workgroup", "local");
+    }
+    conv(0, 0, true);
+    if constexpr (SPLIT) {
+      wait_vmem<0>();
+      __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "workgroup", "local");
+    }
+    conv(3, 2, false);
   }
   uint2 sq[2 * NJ];
   if constexpr (STQ) {
@@ -629,10 +804,22 @@ __device__ __forceinline__ void intra_chunk(const IntraArgs& a, const UnitRef& U
   }
 }
 
-template <int DK, int DV, int DTQ, int DTG, bool EXACT>
+// Shared memory of the intra kernel: IntraSmem, or with the fused prologue
+// the larger staging area it needs (64 rows of g plus 4 waves x 3 tensors x
+// (16 + history) rows), whichever is bigger.
+template <int DK, int DV, bool EXACT, bool PRO>
+struct IntraLds {
+  static constexpr int ROWB = DK * 2;
+  static constexpr int RPI = 1024 / ROWB;
+  static constexpr size_t kStage = PRO ? static_cast<size_t>(kC + 12 * (16 + RPI)) * ROWB : 0;
+  static constexpr size_t kBytes = sizeof(IntraSmem<DK, DV, EXACT>) > kStage ? sizeof(IntraSmem<DK, DV, EXACT>) : kStage;
+};
+
+template <int DK, int DV, int DTQ, int DTG, bool EXACT, bool PRO>
 __global__ __launch_bounds__(256, EXACT ? 1 : 2)
 void kda_intra_kernel(IntraArgs a) {
-  __shared__ IntraSmem<DK, DV, EXACT> sm;
+  __shared__ __attribute__((aligned(16))) unsigned char lds[IntraLds<DK, DV, EXACT, PRO>::kBytes];
+  IntraSmem<DK, DV, EXACT>& sm = *reinterpret_cast<IntraSmem<DK, DV, EXACT>*>(lds);
   const int H = a.geom.H;
   const int u = blockIdx.x / H;
   const int h = blockIdx.x - u * H;
@@ -640,10 +827,10 @@ void kda_intra_kernel(IntraArgs a) {
   const UnitRef U = unit_ref(a.geom, u);
   const int64_t chead = static_cast<int64_t>(u) * H + h;
   switch (threadIdx.x >> 6) {
-    case 0: intra_chunk<DK, DV, DTQ, DTG, EXACT, 0>(a, U, h, chead, sm); break;
-    case 1: intra_chunk<DK, DV, DTQ, DTG, EXACT, 1>(a, U, h, chead, sm); break;
-    case 2: intra_chunk<DK, DV, DTQ, DTG, EXACT, 2>(a, U, h, chead, sm); break;
-    default: intra_chunk<DK, DV, DTQ, DTG, EXACT, 3>(a, U, h, chead, sm); break;
+    case 0: intra_chunk<DK, DV, DTQ, DTG, EXACT, 0, PRO>(a, U, h, chead, sm); break;
+    case 1: intra_chunk<DK, DV, DTQ, DTG, EXACT, 1, PRO>(a, U, h, chead, sm); break;
+    case 2: intra_chunk<DK, DV, DTQ, DTG, EXACT, 2, PRO>(a, U, h, chead, sm); break;
+    default: intra_chunk<DK, DV, DTQ, DTG, EXACT, 3, PRO>(a, U, h, chead, sm); break;
   }
 }
 
@@ -1278,9 +1465,9 @@ void kda_state_col_kernel(StateArgs a) {
 // ----------------------------------------------------------------------------
 // host-side launchers
 // ----------------------------------------------------------------------------
-template <int DK, int DV, int DTQ, int DTG, bool EXACT>
+template <int DK, int DV, int DTQ, int DTG, bool EXACT, bool PRO = false>
 static hipError_t launch_intra_t(const IntraArgs& a, int grid, hipStream_t s) {
-  hipLaunchKernelGGL((kda_intra_kernel<DK, DV, DTQ, DTG, EXACT>), dim3(grid), dim3(256), 0, s, a);
+  hipLaunchKernelGGL((kda_intra_kernel<DK, DV, DTQ, DTG, EXACT, PRO>), dim3(grid), dim3(256), 0, s, a);
   return hipGetLastError();
 }
 
@@ -1307,6 +1494,15 @@ hipError_t launch_intra(const IntraArgs& a, int d, int dtq, int dtg, int grid, h
   KDA_INTRA(64, 1, 0, false)
   KDA_INTRA(64, 0, 0, true)
 #undef KDA_INTRA
+  return hipErrorInvalidValue;
+}
+
+hipError_t launch_intra_prologue(const IntraArgs& a, int d, int dtg, int grid, hipStream_t s) {
+  if (a.K < 1 || a.K > kFusedConvTaps) return hipErrorInvalidValue;
+  if (d == 128 && dtg == 1) return launch_intra_t<128, 128, 1, 1, false, true>(a, grid, s);
+  if (d == 128 && dtg == 0) return launch_intra_t<128, 128, 1, 0, false, true>(a, grid, s);
+  if (d == 64 && dtg == 1) return launch_intra_t<64, 64, 1, 1, false, true>(a, grid, s);
+  if (d == 64 && dtg == 0) return launch_intra_t<64, 64, 1, 0, false, true>(a, grid, s);
   return hipErrorInvalidValue;
 }
 

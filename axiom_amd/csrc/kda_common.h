@@ -202,6 +202,29 @@ __device__ __forceinline__ uint2 ds_read_b64_raw(const void* p) {
   asm volatile("ds_read_b64 %0, %1" : "=v"(v) : "v"(addr));
   return v;
 }
+// 4- and 2-byte forms of the same (the 2-byte read zero-extends), and LDS
+// writes the compiler does not see either (it would otherwise wait for every
+// outstanding direct copy before them too).
+__device__ __forceinline__ unsigned ds_read_b32_raw(const void* p) {
+  unsigned v;
+  const unsigned addr = static_cast<unsigned>(reinterpret_cast<uintptr_t>(p));
+  asm volatile("ds_read_b32 %0, %1" : "=v"(v) : "v"(addr));
+  return v;
+}
+__device__ __forceinline__ unsigned ds_read_u16_raw(const void* p) {
+  unsigned v;
+  const unsigned addr = static_cast<unsigned>(reinterpret_cast<uintptr_t>(p));
+  asm volatile("ds_read_u16 %0, %1" : "=v"(v) : "v"(addr));
+  return v;
+}
+__device__ __forceinline__ void ds_write_b32_raw(void* p, unsigned v) {
+  const unsigned addr = static_cast<unsigned>(reinterpret_cast<uintptr_t>(p));
+  asm volatile("ds_write_b32 %0, %1" : : "v"(addr), "v"(v) : "memory");
+}
+__device__ __forceinline__ void ds_write_b16_raw(void* p, unsigned v) {
+  const unsigned addr = static_cast<unsigned>(reinterpret_cast<uintptr_t>(p));
+  asm volatile("ds_write_b16 %0, %1" : : "v"(addr), "v"(v) : "memory");
+}
 // Waits for all outstanding LDS reads and ties the values to the wait, so no
 // use of them is scheduled before it.
 template <int N>
@@ -210,6 +233,16 @@ __device__ __forceinline__ void lds_settle(uint2 (&v)[N]) {
 #pragma unroll
   for (int i = 0; i < N; ++i) asm volatile("" : "+v"(v[i]));
 }
+template <int N>
+__device__ __forceinline__ void lds_settle(unsigned (&v)[N]) {
+  asm volatile("s_waitcnt lgkmcnt(0)" ::: "memory");
+#pragma unroll
+  for (int i = 0; i < N; ++i) asm volatile("" : "+v"(v[i]));
+}
+
+// 1 / (1 + e^-x): the logistic function of the layer's swish and gates (one
+// definition, so the fused and the standalone prologue round alike)
+__device__ __forceinline__ float sigmoid_f32(float x) { return 1.f / (1.f + __expf(-x)); }
 // s_waitcnt vmcnt(N): all but the N most recently issued memory operations done
 template <int N>
 __device__ __forceinline__ void wait_vmem() {

@@ -35,6 +35,13 @@ struct IntraArgs {
   void* GQ;
   void* LK;
   float* GC;
+  // Fused prologue (K > 0): q, k, v are the raw projections qp, kp, vp and
+  // the kernel applies the short conv (taps cw[t] [K][H*dk] fp32, history of
+  // each sequence's first chunk cb[t] [N][K-1][H*dk] fp32 or null = zeros),
+  // swish and, for q and k, the L2 norm before everything else.
+  const float* cw[3];
+  const float* cb[3];
+  int K;
 };
 
 struct StateArgs {
@@ -142,12 +149,17 @@ struct EpilogueArgs {
 };
 
 hipError_t launch_prologue(const PrologueArgs& a, int d, int in_dt, int out_dt, hipStream_t s);
+// only the conv buffer update of launch_prologue (the last K-1 inputs)
+hipError_t launch_prologue_buffers(const PrologueArgs& a, int d, int in_dt, hipStream_t s);
 hipError_t launch_epilogue(const EpilogueArgs& a, int d, int o_dt, int g_dt, int y_dt, hipStream_t s);
 hipError_t launch_bwd(const BwdArgs& a, int d, int in_dtype, int do_dtype, hipStream_t s);
 hipError_t launch_ut(const UtArgs& a, int dtype, bool transpose, bool with_da, hipStream_t s);
 // dst[0..n) = src (or 0 when src is null), by a kernel (no memset/memcpy node)
 hipError_t launch_copy_or_zero(float* dst, const float* src, int64_t n, hipStream_t s);
 hipError_t launch_intra(const IntraArgs& a, int d, int dtq, int dtg, int grid, hipStream_t s);
+// the intra kernel with the fused prologue (a.K in [1, kFusedConvTaps], bf16 q, k, v)
+hipError_t launch_intra_prologue(const IntraArgs& a, int d, int dtg, int grid, hipStream_t s);
+constexpr int kFusedConvTaps = 4;
 hipError_t launch_state(const StateArgs& a, int d, bool exact, int out_dt, int grid, hipStream_t s);
 hipError_t launch_varlen_prep(const int32_t* cu, int N, int T, int32_t* cu_clamped,
                               int32_t* chunk_off, int32_t* n_units, int32_t* order,

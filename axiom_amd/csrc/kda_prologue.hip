@@ -11,9 +11,12 @@
 // Epilogue (net/kda.py:205-214 _output_gate without the W_o projection):
 // y = sigmoid(gate) * o / sqrt(mean_head(o^2) + eps) (net/norm.py:69-73).
 //
-// One wavefront per (tensor, b, t, h) row: the row's d channels sit d/64 per
-// lane, the head's sum of squares is a wavefront reduction.  The K input rows
-// a convolution reads are neighbouring rows of the same tensor (cache hits).
+// One wavefront per (tensor, b, t, h) row: lane l holds channels PL*l ..
+// PL*l + PL-1 (PL = d/64), the head's sum of squares is a wavefront xor-
+// butterfly.  The fused prologue of the intra kernel (kda_chunk.hip) uses the
+// same channel mapping, tap order and reduction order, so its q, k, v equal
+// this kernel's bit for bit.  The K input rows a convolution reads are
+// neighbouring rows of the same tensor (cache hits).
 #include <hip/hip_runtime.h>
 
 #include <cstdint>
@@ -44,8 +47,6 @@ __device__ __forceinline__ float wave_sum(float x) {
   return x;
 }
 
-__device__ __forceinline__ float sigmoidf_(float x) { return 1.f / (1.f + __expf(-x)); }
-
 template <int DI, int DO, int D>
 __global__ __launch_bounds__(64 * kRowsPerBlock) void kda_prologue_kernel(PrologueArgs a) {
   constexpr int PL = D / 64;   // channels per lane
@@ -68,7 +69,7 @@ __global__ __launch_bounds__(64 * kRowsPerBlock) void kda_prologue_kernel(Prolog
   float ss = 0.f;
 #pragma unroll
   for (int p = 0; p < PL; ++p) {
-    const int c = h * D + lane + 64 * p;            // channel in [0, H*D)
+    const int c = h * D + PL * lane + p;            // channel in [0, H*D)
     float acc = 0.f;
     for (int i = 0; i < a.K; ++i) {
       const int ti = t - i;
@@ -77,14 +78,14 @@ __global__ __launch_bounds__(64 * kRowsPerBlock) void kda_prologue_kernel(Prolog
       else if (buf != nullptr) xv = buf[(static_cast<int64_t>(b) * (a.K - 1) + (a.K - 1 + ti)) * HD + c];
       acc = fmaf(w[static_cast<int64_t>(i) * HD + c], xv, acc);
     }
-    const float sw = acc * sigmoidf_(acc);
+    const float sw = acc * sigmoid_f32(acc);
     s[p] = sw;
     ss = fmaf(sw, sw, ss);
   }
   float scale = 1.f;
   if (tensor < 2) scale = 1.f / (sqrtf(wave_sum(ss)) + 1e-12f);
 #pragma unroll
-  for (int p = 0; p < PL; ++p) pl_st<DO>(y, rr * D + lane + 64 * p, s[p] * scale);
+  for (int p = 0; p < PL; ++p) pl_st<DO>(y, rr * D + PL * lane + p, s[p] * scale);
 }
 
 // new conv buffers: the last K-1 inputs of (old buffer ++ x), one thread per
@@ -132,7 +133,7 @@ __global__ __launch_bounds__(64 * kRowsPerBlock) void kda_epilogue_kernel(Epilog
   const float inv = 1.f / sqrtf(wave_sum(ss) / D + a.eps);
 #pragma unroll
   for (int p = 0; p < PL; ++p) {
-    const float gt = sigmoidf_(pl_ld<DG>(a.gate, r * D + lane + 64 * p));
+    const float gt = sigmoid_f32(pl_ld<DG>(a.gate, r * D + lane + 64 * p));
     pl_st<DY>(a.y, r * D + lane + 64 * p, gt * ov[p] * inv);
   }
 }
@@ -160,6 +161,16 @@ hipError_t launch_prologue_d(const PrologueArgs& a, int in_dt, int out_dt, hipSt
 }
 
 template <int D>
+hipError_t launch_prologue_buffers_d(const PrologueArgs& a, int in_dt, hipStream_t s) {
+  if (!(a.bq_out || a.bk_out || a.bv_out) || a.K <= 1) return hipSuccess;
+  const int64_t n = 3LL * a.B * a.H * D;
+  const int g = static_cast<int>((n + 255) / 256);
+  if (in_dt == 0) hipLaunchKernelGGL((kda_prologue_buf_kernel<0, D>), dim3(g), dim3(256), 0, s, a);
+  else hipLaunchKernelGGL((kda_prologue_buf_kernel<1, D>), dim3(g), dim3(256), 0, s, a);
+  return hipGetLastError();
+}
+
+template <int D>
 hipError_t launch_epilogue_d(const EpilogueArgs& a, int o_dt, int g_dt, int y_dt, hipStream_t s) {
   const int64_t rows = static_cast<int64_t>(a.B) * a.T * a.H;
   if (rows == 0) return hipSuccess;
@@ -182,6 +193,10 @@ hipError_t launch_epilogue_d(const EpilogueArgs& a, int o_dt, int g_dt, int y_dt
 
 hipError_t launch_prologue(const PrologueArgs& a, int d, int in_dt, int out_dt, hipStream_t s) {
   return d == 128 ? launch_prologue_d<128>(a, in_dt, out_dt, s) : launch_prologue_d<64>(a, in_dt, out_dt, s);
+}
+
+hipError_t launch_prologue_buffers(const PrologueArgs& a, int d, int in_dt, hipStream_t s) {
+  return d == 128 ? launch_prologue_buffers_d<128>(a, in_dt, s) : launch_prologue_buffers_d<64>(a, in_dt, s);
 }
 
 hipError_t launch_epilogue(const EpilogueArgs& a, int d, int o_dt, int g_dt, int y_dt, hipStream_t s) {

@@ -429,6 +429,82 @@ def kda_decode_layer_step(qp, kp, vp, g, beta, gate, wq, wk, wv, conv_state, sta
     return y
 
 
+def layer_fwd_workspace_bytes(B, T, H, d, K, in_code=_lib.KDA_DTYPE_BF16) -> int:
+    """Workspace bytes :func:`kda_layer_fwd` needs (0 for an unsupported configuration)."""
+    return int(_lib.lib().kda_layer_fwd_workspace(B, T, H, d, K, in_code))
+
+
+def kda_layer_fwd(qp, kp, vp, g, beta, gate, wq, wk, wv, conv_state=None, initial_state=None,
+                  scale: float = 1.0, eps: float = 1e-6, output_final_state: bool = True,
+                  return_conv_state: bool = True, out_dtype=torch.bfloat16, workspace=None):
+    """The chunked KDA layer between its projections and ``W_o``.
+
+    ``net/kda.py:790-853`` (short conv -> postprocess -> chunked scan -> output
+    gate), with the conv history carried as ``chunk_step`` does
+    (``net/kda.py:356-358``).  ``qp, kp, vp [B, T, H*d]`` bf16 (or fp32),
+    ``g [B, T, H, d]`` log decay and ``beta [B, T, H]`` in the projections'
+    dtype or fp32 (with bf16 projections), ``gate [B, T, H*d]`` logits (fp32
+    or bf16), ``wq, wk, wv [K, H*d]`` fp32 conv taps, ``conv_state`` None or
+    three fp32 ``[B, K-1, H*d]`` buffers, ``initial_state`` None or fp32
+    ``[B, H, d, d]``.  Returns ``(y [B, T, H*d] in out_dtype, final_state or
+    None, new_conv_state or None)``.
+    """
+    what = "kda_layer_fwd"
+    if qp.dim() != 3 or kp.shape != qp.shape or vp.shape != qp.shape or gate.shape != qp.shape:
+        raise ValueError(f"{what}: qp, kp, vp, gate must share a [B,T,H*d] shape")
+    if g.dim() != 4:
+        raise ValueError(f"{what}: g must be [B,T,H,d]")
+    B, T, H, d = g.shape
+    if tuple(qp.shape) != (B, T, H * d) or tuple(beta.shape) != (B, T, H):
+        raise ValueError(f"{what}: qp [B,T,H*d], beta [B,T,H] expected for g {tuple(g.shape)}")
+    _check_dims(d, d, what)
+    if any(t.dtype != qp.dtype for t in (kp, vp)) or beta.dtype != g.dtype:
+        raise ValueError(f"{what}: qp, kp, vp share a dtype, and so do g and beta")
+    if qp.dtype == torch.bfloat16 and g.dtype == torch.bfloat16:
+        code = _lib.KDA_DTYPE_BF16
+    elif qp.dtype == torch.bfloat16 and g.dtype == torch.float32:
+        code = _lib.KDA_DTYPE_BF16_F32GATES
+    elif qp.dtype == torch.float32 and g.dtype == torch.float32:
+        code = _lib.KDA_DTYPE_F32
+    else:
+        raise ValueError(f"{what}: projections bf16 (gates bf16 or fp32) or everything fp32")
+    if gate.dtype not in _OUT_CODES or out_dtype not in _OUT_CODES:
+        raise ValueError(f"{what}: gate and out_dtype must be fp32 or bf16")
+    K = wq.shape[0]
+    for name, w in (("wq", wq), ("wk", wk), ("wv", wv)):
+        if w.dtype != torch.float32 or tuple(w.shape) != (K, H * d):
+            raise ValueError(f"{what}: {name} must be fp32 [{K},{H * d}]")
+    if conv_state is not None:
+        for st in conv_state:
+            if st.dtype != torch.float32 or tuple(st.shape) != (B, K - 1, H * d):
+                raise ValueError(f"{what}: conv_state buffers must be fp32 [{B},{K - 1},{H * d}]")
+    if initial_state is not None and (initial_state.dtype != torch.float32 or
+                                      tuple(initial_state.shape) != (B, H, d, d)):
+        raise ValueError(f"{what}: initial_state must be fp32 [{B},{H},{d},{d}]")
+    tensors = [qp, kp, vp, g, beta, gate, wq, wk, wv] + list(conv_state or []) + \
+        ([initial_state] if initial_state is not None else [])
+    for i, t in enumerate(tensors):
+        _contig(f"arg{i}", t)
+    dev = _require_gpu(tensors, what)
+    L = _lib.lib()
+    need = int(L.kda_layer_fwd_workspace(B, T, H, d, K, code))
+    if need == 0:
+        raise ValueError(f"{what}: unsupported configuration")
+    if workspace is None or workspace.numel() * workspace.element_size() < need:
+        workspace = torch.empty(need, dtype=torch.uint8, device=dev)
+    y = torch.empty((B, T, H * d), dtype=out_dtype, device=dev)
+    ht = torch.empty((B, H, d, d), dtype=torch.float32, device=dev) if output_final_state else None
+    new = tuple(torch.empty((B, K - 1, H * d), dtype=torch.float32, device=dev) for _ in range(3)) \
+        if return_conv_state else (None, None, None)
+    bin_ = conv_state if conv_state is not None else (None, None, None)
+    rc = L.kda_layer_fwd(_stream(dev), _ptr(qp), _ptr(kp), _ptr(vp), _ptr(g), _ptr(beta), _ptr(gate),
+                         _ptr(wq), _ptr(wk), _ptr(wv), *(_ptr(b) for b in bin_), *(_ptr(b) for b in new),
+                         _ptr(initial_state), _ptr(ht), _ptr(y), B, T, H, d, K, float(scale), float(eps),
+                         code, _OUT_CODES[gate.dtype], _OUT_CODES[out_dtype], _ptr(workspace), need)
+    _lib.check(rc, what)
+    return y, ht, (new if return_conv_state else None)
+
+
 def varlen_status(workspace, B, T, H, dk, dv, n_seqs, in_code=_lib.KDA_DTYPE_BF16) -> int:
     """Validation bits of the last varlen call that used ``workspace`` (synchronises)."""
     flags = ctypes.c_int32(0)

@@ -245,6 +245,34 @@ KDA_API int kda_decode_layer_step(hipStream_t stream,
 /* Workspace bytes kda_decode_layer_step needs (0 on bad input).  Host-only. */
 KDA_API size_t kda_decode_layer_workspace(int B, int H, int d, int in_dtype);
 
+/*
+ * The chunked (prefill / training-forward) KDA layer between its projections
+ * and W_o: replaces the body of net/kda.py:790-853 (_apply_chunked_cc_persistent:
+ * short_conv -> _postprocess -> cc_scan -> _output_gate, :839-853), with the
+ * conv history carried across calls as chunk_step does (net/kda.py:356-358,
+ * :383-389) and an optional initial state.  qp, kp, vp [B,T,H*d]; g [B,T,H,d]
+ * log decay; beta [B,T,H] -- in in_dtype (KDA_DTYPE_BF16, KDA_DTYPE_BF16_F32GATES
+ * or KDA_DTYPE_F32, as for kda_chunk_fwd); gate logits [B,T,H*d] in gate_dtype;
+ * conv taps, buffers as kda_prologue (1 <= K <= 8); h0 / ht as kda_chunk_fwd;
+ * y [B,T,H*d] = sigmoid(gate) * RMSNorm_head(o) in out_dtype (F32 or BF16).
+ * With bf16 projections and K <= 4 the prologue runs inside the intra kernel
+ * (no q, k, v round trip through memory; results equal kda_prologue followed
+ * by kda_chunk_fwd and kda_epilogue bit for bit); otherwise it is its own pass.
+ * Caller workspace of kda_layer_fwd_workspace bytes.  d in {64, 128}.
+ */
+KDA_API int kda_layer_fwd(hipStream_t stream,
+                const void* qp, const void* kp, const void* vp,
+                const void* g, const void* beta, const void* gate,
+                const float* wq, const float* wk, const float* wv,
+                const float* bq_in, const float* bk_in, const float* bv_in,
+                float* bq_out, float* bk_out, float* bv_out,
+                const float* h0, float* ht, void* y,
+                int B, int T, int H, int d, int K, float scale, float eps,
+                int in_dtype, int gate_dtype, int out_dtype, void* workspace, size_t workspace_bytes);
+
+/* Workspace bytes kda_layer_fwd needs (0 on bad input).  Host-only. */
+KDA_API size_t kda_layer_fwd_workspace(int B, int T, int H, int d, int K, int in_dtype);
+
 /* Message of the last failure on the calling thread ("" if none). */
 KDA_API const char* kda_last_error(void);
 

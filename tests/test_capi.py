@@ -77,7 +77,7 @@ def varlen_ws_bytes(T, N, H, dk, dv, es):
 def test_header_declares_the_abi():
     names = _lib.header_symbols()
     assert set(names) == set(_lib._SIGNATURES), names
-    assert len(names) == len(set(names)) == 16
+    assert len(names) == len(set(names)) == 18
 
 
 def test_library_exports_every_declared_symbol(L):
@@ -99,6 +99,24 @@ def test_abi_version(L):
 @pytest.mark.parametrize("code,es", [(0, 4), (1, 2), (2, 2), (3, 2)])
 def test_dense_workspace_size(L, B, T, H, d, code, es):
     assert L.kda_chunk_fwd_workspace(B, T, H, d, d, C, 0, code) == dense_ws_bytes(B, T, H, d, d, es)
+
+
+@pytest.mark.parametrize("B,T,H,d", [(4, 4096, 16, 128), (2, 37, 2, 64), (1, 0, 1, 128)])
+@pytest.mark.parametrize("K,code,es,fused", [(4, 1, 2, True), (4, 3, 2, True), (1, 1, 2, True),
+                                             (5, 1, 2, False), (4, 0, 4, False)])
+def test_layer_workspace_size(L, B, T, H, d, K, code, es, fused):
+    """chunk workspace + o fp32 (+ q, k, v when the prologue runs as its own pass)."""
+    n = B * T * H * d
+    want = _align(dense_ws_bytes(B, T, H, d, d, es)) + _align(n * 4)
+    if not fused:
+        want += 3 * _align(n * es)
+    assert L.kda_layer_fwd_workspace(B, T, H, d, K, code) == want
+
+
+@pytest.mark.parametrize("args", [(1, 64, 1, 96, 4, 1), (1, 64, 1, 64, 0, 1), (1, 64, 1, 64, 9, 1),
+                                  (1, 64, 1, 64, 4, 2), (0, 64, 1, 64, 4, 1), (1, -1, 1, 64, 4, 1)])
+def test_layer_workspace_rejects_unsupported(L, args):
+    assert L.kda_layer_fwd_workspace(*args) == 0
 
 
 @pytest.mark.parametrize("T,N", [(262144, 64), (108, 4), (1, 1), (0, 3)])
