@@ -348,36 +348,11 @@ __device__ __forceinline__ void intra_chunk(const IntraArgs& a, const UnitRef& U
         }
       }
       if (nrm) {
-        // Row sums over the 64 lanes as a reduce-scatter: after the steps at
-        // lane distance 32, 16, 8, 4 lane l holds row 8 b5 + 4 b4 + 2 b3 + b2
-        // (its lane bits), then two butterfly steps.  Every partial is the
-        // one an xor-butterfly over 32, 16, .., 1 forms, so each row total is
-        // that butterfly's, bit for bit.
-        float v8[8], v4[4], v2[2];
-        const bool b5 = (l & 32) != 0, b4 = (l & 16) != 0, b3 = (l & 8) != 0, b2 = (l & 4) != 0;
-#pragma unroll
-        for (int j = 0; j < 8; ++j) {
-          const float snd = b5 ? ss[j] : ss[8 + j];
-          v8[j] = (b5 ? ss[8 + j] : ss[j]) + __shfl_xor(snd, 32, 64);
-        }
-#pragma unroll
-        for (int j = 0; j < 4; ++j) {
-          const float snd = b4 ? v8[j] : v8[4 + j];
-          v4[j] = (b4 ? v8[4 + j] : v8[j]) + __shfl_xor(snd, 16, 64);
-        }
-#pragma unroll
-        for (int j = 0; j < 2; ++j) {
-          const float snd = b3 ? v4[j] : v4[2 + j];
-          v2[j] = (b3 ? v4[2 + j] : v4[j]) + __shfl_xor(snd, 8, 64);
-        }
-        float v1 = (b2 ? v2[1] : v2[0]) + __shfl_xor(b2 ? v2[0] : v2[1], 4, 64);
-        v1 += __shfl_xor(v1, 2, 64);
-        v1 += __shfl_xor(v1, 1, 64);
+        float tot[16];
+        wave_rowsums16(ss, tot);
 #pragma unroll
         for (int r2 = 0; r2 < 16; ++r2) {
-          const int src = 32 * ((r2 >> 3) & 1) + 16 * ((r2 >> 2) & 1) + 8 * ((r2 >> 1) & 1) + 4 * (r2 & 1);
-          const float tot = __builtin_bit_cast(float, __builtin_amdgcn_readlane(__builtin_bit_cast(int, v1), src));
-          const float sc = 1.f / (sqrtf(tot) + 1e-12f);
+          const float sc = inv_l2_f32(tot[r2]);
 #pragma unroll
           for (int p = 0; p < PL; ++p) sv[r2][p] *= sc;
         }
@@ -386,12 +361,8 @@ __device__ __forceinline__ void intra_chunk(const IntraArgs& a, const UnitRef& U
       for (int r2 = 0; r2 < 16; ++r2) {
         const int row = 16 * W + r2;
         unsigned char* p = stg_row(t, row) + (ci ^ (row & (NCH - 1))) * 16 + cb;
-        if constexpr (PL == 2) {
-          ds_write_b32_raw(p, static_cast<unsigned>(f32_to_bf16_bits(sv[r2][0])) |
-                                  (static_cast<unsigned>(f32_to_bf16_bits(sv[r2][1])) << 16));
-        } else {
-          ds_write_b16_raw(p, f32_to_bf16_bits(sv[r2][0]));
-        }
+        if constexpr (PL == 2) ds_write_b32_raw(p, pack_bf16x2(sv[r2][0], sv[r2][1]));
+        else ds_write_b16_raw(p, cvt_bf16(sv[r2][0]));
       }
     };
     if constexpr (SPLIT) {

@@ -240,9 +240,49 @@ __device__ __forceinline__ void lds_settle(unsigned (&v)[N]) {
   for (int i = 0; i < N; ++i) asm volatile("" : "+v"(v[i]));
 }
 
-// 1 / (1 + e^-x): the logistic function of the layer's swish and gates (one
-// definition, so the fused and the standalone prologue round alike)
-__device__ __forceinline__ float sigmoid_f32(float x) { return 1.f / (1.f + __expf(-x)); }
+// The layer's elementwise pieces, each defined once so the fused and the
+// standalone prologue round alike.  Hardware reciprocal and square root
+// (1 ulp) rather than the correctly rounded sequences (12 and 20 instructions).
+// 1 / (1 + e^-x): the logistic function of the swish and the output gate
+__device__ __forceinline__ float sigmoid_f32(float x) { return __builtin_amdgcn_rcpf(1.f + __expf(-x)); }
+// 1 / (sqrt(ss) + 1e-12): the L2 normalisation of a row with sum of squares ss
+__device__ __forceinline__ float inv_l2_f32(float ss) {
+  return __builtin_amdgcn_rcpf(__builtin_amdgcn_sqrtf(ss) + 1e-12f);
+}
+// two fp32 -> packed bf16 (round to nearest even, one instruction on gfx950)
+typedef float f2v __attribute__((ext_vector_type(2)));
+typedef __bf16 bf2v __attribute__((ext_vector_type(2)));
+__device__ __forceinline__ unsigned pack_bf16x2(float lo, float hi) {
+  const f2v v = {lo, hi};
+  return __builtin_bit_cast(unsigned, __builtin_convertvector(v, bf2v));
+}
+__device__ __forceinline__ u16 cvt_bf16(float x) { return __builtin_bit_cast(u16, static_cast<__bf16>(x)); }
+
+// Totals over the 64 lanes of a wavefront of 16 per-lane partial sums (row
+// r's partial in ss[r]), as wave-uniform values.  A reduce-scatter over lane
+// distances 32, 16, 8, 4 leaves lane l with row 8 b5 + 4 b4 + 2 b3 + b2 (its
+// lane bits), two butterfly steps finish it, and each row's total is read from
+// a lane holding it.  Every partial formed is the one an xor-butterfly sum
+// over distances 32, 16, .., 1 forms, so each total equals that sum bit for bit.
+__device__ __forceinline__ void wave_rowsums16(const float (&ss)[16], float (&tot)[16]) {
+  const int l = __lane_id();
+  const bool b5 = (l & 32) != 0, b4 = (l & 16) != 0, b3 = (l & 8) != 0, b2 = (l & 4) != 0;
+  float v8[8], v4[4], v2[2];
+#pragma unroll
+  for (int j = 0; j < 8; ++j) v8[j] = (b5 ? ss[8 + j] : ss[j]) + __shfl_xor(b5 ? ss[j] : ss[8 + j], 32, 64);
+#pragma unroll
+  for (int j = 0; j < 4; ++j) v4[j] = (b4 ? v8[4 + j] : v8[j]) + __shfl_xor(b4 ? v8[j] : v8[4 + j], 16, 64);
+#pragma unroll
+  for (int j = 0; j < 2; ++j) v2[j] = (b3 ? v4[2 + j] : v4[j]) + __shfl_xor(b3 ? v4[j] : v4[2 + j], 8, 64);
+  float v1 = (b2 ? v2[1] : v2[0]) + __shfl_xor(b2 ? v2[0] : v2[1], 4, 64);
+  v1 += __shfl_xor(v1, 2, 64);
+  v1 += __shfl_xor(v1, 1, 64);
+#pragma unroll
+  for (int r = 0; r < 16; ++r) {
+    const int src = 32 * ((r >> 3) & 1) + 16 * ((r >> 2) & 1) + 8 * ((r >> 1) & 1) + 4 * (r & 1);
+    tot[r] = __builtin_bit_cast(float, __builtin_amdgcn_readlane(__builtin_bit_cast(int, v1), src));
+  }
+}
 // s_waitcnt vmcnt(N): all but the N most recently issued memory operations done
 template <int N>
 __device__ __forceinline__ void wait_vmem() {

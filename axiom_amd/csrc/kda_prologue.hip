@@ -38,7 +38,7 @@ __device__ __forceinline__ float pl_ld(const void* p, int64_t i) {
 template <int DT>
 __device__ __forceinline__ void pl_st(void* p, int64_t i, float v) {
   if constexpr (DT == 0) static_cast<float*>(p)[i] = v;
-  else static_cast<u16*>(p)[i] = f32_to_bf16_bits(v);
+  else static_cast<u16*>(p)[i] = cvt_bf16(v);
 }
 
 __device__ __forceinline__ float wave_sum(float x) {
@@ -47,45 +47,116 @@ __device__ __forceinline__ float wave_sum(float x) {
   return x;
 }
 
-template <int DI, int DO, int D>
+constexpr int kProRows = 16;   // rows of one (tensor, b, h) per wavefront
+
+template <int DI, int PL>
+__device__ __forceinline__ void pl_ld_pl(const void* p, int64_t i, float (&o)[PL]) {
+  if constexpr (DI == 0) {
+    if constexpr (PL == 2) {
+      const float2 v = *reinterpret_cast<const float2*>(static_cast<const float*>(p) + i);
+      o[0] = v.x;
+      o[1] = v.y;
+    } else {
+      o[0] = static_cast<const float*>(p)[i];
+    }
+  } else {
+    if constexpr (PL == 2) {
+      const unsigned w = *reinterpret_cast<const unsigned*>(static_cast<const u16*>(p) + i);
+      o[0] = __uint_as_float(w << 16);
+      o[1] = __uint_as_float(w & 0xFFFF0000u);
+    } else {
+      o[0] = bf16_to_f32(static_cast<const u16*>(p)[i]);
+    }
+  }
+}
+
+// One wavefront per 16 consecutive rows of one (tensor, b, h): the rows and
+// the KW-1 before them are loaded once (16 + KW - 1 row loads, all in flight
+// together), the K taps run over them in registers, and the 16 row norms are
+// one wave_rowsums16.  Lane l holds channels PL*l .. PL*l + PL-1 of the head.
+template <int DI, int DO, int D, int KW>
 __global__ __launch_bounds__(64 * kRowsPerBlock) void kda_prologue_kernel(PrologueArgs a) {
   constexpr int PL = D / 64;   // channels per lane
   const int lane = threadIdx.x & 63;
-  const int64_t rows = static_cast<int64_t>(a.B) * a.T * a.H;
-  const int64_t r = static_cast<int64_t>(blockIdx.x) * kRowsPerBlock + (threadIdx.x >> 6);
-  if (r >= 3 * rows) return;                       // uniform per wavefront
-  const int tensor = static_cast<int>(r / rows);   // 0 q, 1 k, 2 v
-  const int64_t rr = r - tensor * rows;
-  const int h = static_cast<int>(rr % a.H);
-  const int64_t bt = rr / a.H;
-  const int t = static_cast<int>(bt % a.T);
-  const int b = static_cast<int>(bt / a.T);
+  const int nblk = (a.T + kProRows - 1) / kProRows;
+  const int64_t items = 3LL * a.B * a.H * nblk;
+  const int64_t w = static_cast<int64_t>(blockIdx.x) * kRowsPerBlock + (threadIdx.x >> 6);
+  if (w >= items) return;                          // uniform per wavefront
+  const int blk = static_cast<int>(w % nblk);
+  int64_t rest = w / nblk;
+  const int h = static_cast<int>(rest % a.H);
+  rest /= a.H;
+  const int b = static_cast<int>(rest % a.B);
+  const int tensor = static_cast<int>(rest / a.B);  // 0 q, 1 k, 2 v
   const void* x = tensor == 0 ? a.qp : tensor == 1 ? a.kp : a.vp;
-  const float* w = tensor == 0 ? a.wq : tensor == 1 ? a.wk : a.wv;
+  const float* wp = tensor == 0 ? a.wq : tensor == 1 ? a.wk : a.wv;
   const float* buf = tensor == 0 ? a.bq_in : tensor == 1 ? a.bk_in : a.bv_in;
   void* y = tensor == 0 ? a.q : tensor == 1 ? a.k : a.v;
-  const int HD = a.H * D;                          // channels of the tensor
-  float s[PL];
-  float ss = 0.f;
+  const int HD = a.H * D;
+  const int c0 = h * D + PL * lane;                // the lane's first channel in [0, H*D)
+  const int t0 = blk * kProRows;
+  float wt[KW][PL];
 #pragma unroll
-  for (int p = 0; p < PL; ++p) {
-    const int c = h * D + PL * lane + p;            // channel in [0, H*D)
-    float acc = 0.f;
-    for (int i = 0; i < a.K; ++i) {
-      const int ti = t - i;
-      float xv = 0.f;
-      if (ti >= 0) xv = pl_ld<DI>(x, (static_cast<int64_t>(b) * a.T + ti) * HD + c);
-      else if (buf != nullptr) xv = buf[(static_cast<int64_t>(b) * (a.K - 1) + (a.K - 1 + ti)) * HD + c];
-      acc = fmaf(w[static_cast<int64_t>(i) * HD + c], xv, acc);
-    }
-    const float sw = acc * sigmoid_f32(acc);
-    s[p] = sw;
-    ss = fmaf(sw, sw, ss);
+  for (int i = 0; i < KW; ++i) {
+    const float* p = wp + static_cast<int64_t>(min(i, a.K - 1)) * HD + c0;
+#pragma unroll
+    for (int q = 0; q < PL; ++q) wt[i][q] = p[q];
   }
-  float scale = 1.f;
-  if (tensor < 2) scale = 1.f / (sqrtf(wave_sum(ss)) + 1e-12f);
+  // xs[j] = input row t0 - (KW-1) + j; rows before the sequence from the
+  // buffer (or zero), rows past its end re-read the last row (never stored)
+  float xs[KW - 1 + kProRows][PL];
+  if (t0 == 0) {
 #pragma unroll
-  for (int p = 0; p < PL; ++p) pl_st<DO>(y, rr * D + PL * lane + p, s[p] * scale);
+    for (int j = 0; j < KW - 1; ++j) {
+      const int br = a.K - 1 + j - (KW - 1);      // buffer row (oldest first)
+#pragma unroll
+      for (int q = 0; q < PL; ++q)
+        xs[j][q] = (buf != nullptr && br >= 0) ? buf[(static_cast<int64_t>(b) * (a.K - 1) + br) * HD + c0 + q] : 0.f;
+    }
+  } else {
+#pragma unroll
+    for (int j = 0; j < KW - 1; ++j)
+      pl_ld_pl<DI, PL>(x, (static_cast<int64_t>(b) * a.T + t0 - (KW - 1) + j) * HD + c0, xs[j]);
+  }
+#pragma unroll
+  for (int r = 0; r < kProRows; ++r)
+    pl_ld_pl<DI, PL>(x, (static_cast<int64_t>(b) * a.T + min(t0 + r, a.T - 1)) * HD + c0, xs[KW - 1 + r]);
+  float sv[kProRows][PL], ss[kProRows];
+#pragma unroll
+  for (int r = 0; r < kProRows; ++r) {
+    ss[r] = 0.f;
+#pragma unroll
+    for (int q = 0; q < PL; ++q) {
+      float acc = 0.f;
+#pragma unroll
+      for (int i = 0; i < KW; ++i)
+        if (i < a.K) acc = fmaf(wt[i][q], xs[KW - 1 + r - i][q], acc);
+      sv[r][q] = acc * sigmoid_f32(acc);
+      ss[r] = fmaf(sv[r][q], sv[r][q], ss[r]);
+    }
+  }
+  if (tensor < 2) {
+    float tot[kProRows];
+    wave_rowsums16(ss, tot);
+#pragma unroll
+    for (int r = 0; r < kProRows; ++r) {
+      const float sc = inv_l2_f32(tot[r]);
+#pragma unroll
+      for (int q = 0; q < PL; ++q) sv[r][q] *= sc;
+    }
+  }
+#pragma unroll
+  for (int r = 0; r < kProRows; ++r) {
+    if (t0 + r >= a.T) break;
+    const int64_t o = ((static_cast<int64_t>(b) * a.T + t0 + r) * a.H + h) * D + PL * lane;
+    if constexpr (DO == 0) {
+      if constexpr (PL == 2) *reinterpret_cast<float2*>(static_cast<float*>(y) + o) = make_float2(sv[r][0], sv[r][1]);
+      else static_cast<float*>(y)[o] = sv[r][0];
+    } else {
+      if constexpr (PL == 2) *reinterpret_cast<unsigned*>(static_cast<u16*>(y) + o) = pack_bf16x2(sv[r][0], sv[r][1]);
+      else static_cast<u16*>(y)[o] = cvt_bf16(sv[r][0]);
+    }
+  }
 }
 
 // new conv buffers: the last K-1 inputs of (old buffer ++ x), one thread per
@@ -116,37 +187,73 @@ __global__ __launch_bounds__(256) void kda_prologue_buf_kernel(PrologueArgs a) {
   for (int j = 0; j < km1; ++j) bout[(static_cast<int64_t>(b) * km1 + j) * HD + c] = v[j];
 }
 
+// Four consecutive channels per lane: a row of D channels is D/4 lanes (a
+// half wavefront at D = 128), the head's sum of squares a butterfly inside
+// that lane group; 16-byte o loads, 8-byte bf16 gate loads and y stores.
+// kEpiRowsPerBlock rows per workgroup per step, grid-strided.
+constexpr int kEpiThreads = 256;
+
+template <int DT>
+__device__ __forceinline__ f4 ep_ld4(const void* p, int64_t i) {
+  if constexpr (DT == 0) {
+    const float4 v = *reinterpret_cast<const float4*>(static_cast<const float*>(p) + i);
+    return f4{v.x, v.y, v.z, v.w};
+  } else {
+    const uint2 w = *reinterpret_cast<const uint2*>(static_cast<const u16*>(p) + i);
+    return f4{__uint_as_float(w.x << 16), __uint_as_float(w.x & 0xFFFF0000u), __uint_as_float(w.y << 16),
+              __uint_as_float(w.y & 0xFFFF0000u)};
+  }
+}
+
+template <int DT>
+__device__ __forceinline__ void ep_st4(void* p, int64_t i, const f4& v) {
+  if constexpr (DT == 0) {
+    *reinterpret_cast<float4*>(static_cast<float*>(p) + i) = make_float4(v[0], v[1], v[2], v[3]);
+  } else {
+    *reinterpret_cast<uint2*>(static_cast<u16*>(p) + i) = make_uint2(pack_bf16x2(v[0], v[1]), pack_bf16x2(v[2], v[3]));
+  }
+}
+
 template <int DO_, int DG, int DY, int D>
-__global__ __launch_bounds__(64 * kRowsPerBlock) void kda_epilogue_kernel(EpilogueArgs a) {
-  constexpr int PL = D / 64;
-  const int lane = threadIdx.x & 63;
+__global__ __launch_bounds__(kEpiThreads) void kda_epilogue_kernel(EpilogueArgs a) {
+  constexpr int LPR = D / 4;                    // lanes per row
+  constexpr int RPB = kEpiThreads / LPR;        // rows per workgroup step
   const int64_t rows = static_cast<int64_t>(a.B) * a.T * a.H;
-  const int64_t r = static_cast<int64_t>(blockIdx.x) * kRowsPerBlock + (threadIdx.x >> 6);
-  if (r >= rows) return;
-  float ov[PL];
-  float ss = 0.f;
+  const int sub = threadIdx.x % LPR;
+  for (int64_t r = static_cast<int64_t>(blockIdx.x) * RPB + threadIdx.x / LPR; r < rows;
+       r += static_cast<int64_t>(gridDim.x) * RPB) {   // a row's lanes share r: uniform per group
+    const int64_t i = r * D + 4 * sub;
+    const f4 o = ep_ld4<DO_>(a.o, i);
+    const f4 g = ep_ld4<DG>(a.gate, i);
+    float ss = o[0] * o[0];
 #pragma unroll
-  for (int p = 0; p < PL; ++p) {
-    ov[p] = pl_ld<DO_>(a.o, r * D + lane + 64 * p);
-    ss = fmaf(ov[p], ov[p], ss);
-  }
-  const float inv = 1.f / sqrtf(wave_sum(ss) / D + a.eps);
+    for (int e = 1; e < 4; ++e) ss = fmaf(o[e], o[e], ss);
 #pragma unroll
-  for (int p = 0; p < PL; ++p) {
-    const float gt = sigmoid_f32(pl_ld<DG>(a.gate, r * D + lane + 64 * p));
-    pl_st<DY>(a.y, r * D + lane + 64 * p, gt * ov[p] * inv);
+    for (int off = LPR / 2; off >= 1; off >>= 1) ss += __shfl_xor(ss, off, 64);
+    const float inv = __builtin_amdgcn_rsqf(ss * (1.f / D) + a.eps);
+    f4 y;
+#pragma unroll
+    for (int e = 0; e < 4; ++e) y[e] = sigmoid_f32(g[e]) * o[e] * inv;
+    ep_st4<DY>(a.y, i, y);
   }
+}
+
+template <int D, int KW>
+void launch_prologue_main(const PrologueArgs& a, int in_dt, int out_dt, int grid, hipStream_t s) {
+  const dim3 g(grid), blk(64 * kRowsPerBlock);
+  if (in_dt == 0 && out_dt == 0) hipLaunchKernelGGL((kda_prologue_kernel<0, 0, D, KW>), g, blk, 0, s, a);
+  else if (in_dt == 0) hipLaunchKernelGGL((kda_prologue_kernel<0, 1, D, KW>), g, blk, 0, s, a);
+  else if (out_dt == 0) hipLaunchKernelGGL((kda_prologue_kernel<1, 0, D, KW>), g, blk, 0, s, a);
+  else hipLaunchKernelGGL((kda_prologue_kernel<1, 1, D, KW>), g, blk, 0, s, a);
 }
 
 template <int D>
 hipError_t launch_prologue_d(const PrologueArgs& a, int in_dt, int out_dt, hipStream_t s) {
-  const int64_t rows = 3LL * a.B * a.T * a.H;
-  const int grid = static_cast<int>((rows + kRowsPerBlock - 1) / kRowsPerBlock);
-  if (rows > 0) {
-    if (in_dt == 0 && out_dt == 0) hipLaunchKernelGGL((kda_prologue_kernel<0, 0, D>), dim3(grid), dim3(64 * kRowsPerBlock), 0, s, a);
-    else if (in_dt == 0) hipLaunchKernelGGL((kda_prologue_kernel<0, 1, D>), dim3(grid), dim3(64 * kRowsPerBlock), 0, s, a);
-    else if (out_dt == 0) hipLaunchKernelGGL((kda_prologue_kernel<1, 0, D>), dim3(grid), dim3(64 * kRowsPerBlock), 0, s, a);
-    else hipLaunchKernelGGL((kda_prologue_kernel<1, 1, D>), dim3(grid), dim3(64 * kRowsPerBlock), 0, s, a);
+  const int64_t items = 3LL * a.B * a.H * ((a.T + kProRows - 1) / kProRows);
+  if (items > 0) {
+    const int grid = static_cast<int>((items + kRowsPerBlock - 1) / kRowsPerBlock);
+    if (a.K <= 4) launch_prologue_main<D, 4>(a, in_dt, out_dt, grid, s);
+    else launch_prologue_main<D, 8>(a, in_dt, out_dt, grid, s);
     const hipError_t e = hipGetLastError();
     if (e != hipSuccess) return e;
   }
@@ -174,17 +281,19 @@ template <int D>
 hipError_t launch_epilogue_d(const EpilogueArgs& a, int o_dt, int g_dt, int y_dt, hipStream_t s) {
   const int64_t rows = static_cast<int64_t>(a.B) * a.T * a.H;
   if (rows == 0) return hipSuccess;
-  const int grid = static_cast<int>((rows + kRowsPerBlock - 1) / kRowsPerBlock);
+  constexpr int RPB = kEpiThreads / (D / 4);
+  const int64_t need = (rows + RPB - 1) / RPB;
+  const int grid = static_cast<int>(need < 8192 ? need : 8192);   // 32 workgroups per CU, grid-strided
   const int code = o_dt * 4 + g_dt * 2 + y_dt;
   switch (code) {
-    case 0: hipLaunchKernelGGL((kda_epilogue_kernel<0, 0, 0, D>), dim3(grid), dim3(64 * kRowsPerBlock), 0, s, a); break;
-    case 1: hipLaunchKernelGGL((kda_epilogue_kernel<0, 0, 1, D>), dim3(grid), dim3(64 * kRowsPerBlock), 0, s, a); break;
-    case 2: hipLaunchKernelGGL((kda_epilogue_kernel<0, 1, 0, D>), dim3(grid), dim3(64 * kRowsPerBlock), 0, s, a); break;
-    case 3: hipLaunchKernelGGL((kda_epilogue_kernel<0, 1, 1, D>), dim3(grid), dim3(64 * kRowsPerBlock), 0, s, a); break;
-    case 4: hipLaunchKernelGGL((kda_epilogue_kernel<1, 0, 0, D>), dim3(grid), dim3(64 * kRowsPerBlock), 0, s, a); break;
-    case 5: hipLaunchKernelGGL((kda_epilogue_kernel<1, 0, 1, D>), dim3(grid), dim3(64 * kRowsPerBlock), 0, s, a); break;
-    case 6: hipLaunchKernelGGL((kda_epilogue_kernel<1, 1, 0, D>), dim3(grid), dim3(64 * kRowsPerBlock), 0, s, a); break;
-    default: hipLaunchKernelGGL((kda_epilogue_kernel<1, 1, 1, D>), dim3(grid), dim3(64 * kRowsPerBlock), 0, s, a); break;
+    case 0: hipLaunchKernelGGL((kda_epilogue_kernel<0, 0, 0, D>), dim3(grid), dim3(kEpiThreads), 0, s, a); break;
+    case 1: hipLaunchKernelGGL((kda_epilogue_kernel<0, 0, 1, D>), dim3(grid), dim3(kEpiThreads), 0, s, a); break;
+    case 2: hipLaunchKernelGGL((kda_epilogue_kernel<0, 1, 0, D>), dim3(grid), dim3(kEpiThreads), 0, s, a); break;
+    case 3: hipLaunchKernelGGL((kda_epilogue_kernel<0, 1, 1, D>), dim3(grid), dim3(kEpiThreads), 0, s, a); break;
+    case 4: hipLaunchKernelGGL((kda_epilogue_kernel<1, 0, 0, D>), dim3(grid), dim3(kEpiThreads), 0, s, a); break;
+    case 5: hipLaunchKernelGGL((kda_epilogue_kernel<1, 0, 1, D>), dim3(grid), dim3(kEpiThreads), 0, s, a); break;
+    case 6: hipLaunchKernelGGL((kda_epilogue_kernel<1, 1, 0, D>), dim3(grid), dim3(kEpiThreads), 0, s, a); break;
+    default: hipLaunchKernelGGL((kda_epilogue_kernel<1, 1, 1, D>), dim3(grid), dim3(kEpiThreads), 0, s, a); break;
   }
   return hipGetLastError();
 }
