@@ -25,6 +25,9 @@ Also reported on the same JSON line:
   dbeta, dh0 from fp32 do and dht) on the same config-1 inputs, per call, with
   its algorithmic bytes (read q, k, v, g, beta bf16 and do fp32 plus dht;
   write the five gradients and dh0 fp32) against the HBM peak;
+* ``layer``: the chunked layer forward ``kda_layer_fwd`` (short conv, swish
+  and L2 norm fused into the intra kernel, the scan, the RMSNorm x sigmoid
+  gate epilogue) on config-1 shapes with K = 4, bf16 projections and output;
 * ``ut_solve``: the standalone unit-triangular solve at the reference's case
   (H=12, C=64, N=dk+dv=256, fp32), both orientations, per call;
 * ``cpu_baseline``: the oracle's fp32 restatement of the reference jax body
@@ -202,6 +205,60 @@ def bench_backward(args, fwd_inputs, device):
                 config="B4 T4096 H16 d128 bf16 inputs, fp32 do and dht, zero h0")
 
 
+def layer_bytes(B, T, H, d, K):
+    """Read qp, kp, vp, g, gate bf16, beta bf16, conv taps fp32; write y bf16 and hT fp32."""
+    n = B * T * H
+    return n * d * 5 * 2 + n * 2 + 3 * K * H * d * 4 + n * d * 2 + B * H * d * d * 4
+
+
+def bench_layer(args, fwd_inputs, device):
+    """The chunked layer forward (prologue fused into the intra kernel, scan, epilogue)."""
+    import axiom_amd
+    from axiom_amd import kda as kmod
+    q, k, v, g, beta = fwd_inputs
+    B, T, H, d = q.shape
+    K = 4
+    gen = torch.Generator(device=device)
+    gen.manual_seed(args.seed + 5)
+    xs = [torch.randn(B, T, H * d, device=device, generator=gen).to(torch.bfloat16) for _ in range(3)]
+    ws_ = [torch.randn(K, H * d, device=device, generator=gen) * 0.4 for _ in range(3)]
+    gate = torch.randn(B, T, H * d, device=device, generator=gen).to(torch.bfloat16)
+    ws = torch.empty(kmod.layer_fwd_workspace_bytes(B, T, H, d, K), dtype=torch.uint8, device=device)
+    stream = torch.cuda.current_stream(device)
+
+    cws = torch.empty(kmod.chunk_fwd_workspace_bytes(B, T, H, d, d), dtype=torch.uint8, device=device)
+
+    def call():
+        return axiom_amd.kda_layer_fwd(*xs, g, beta, gate, *ws_, out_dtype=torch.bfloat16,
+                                       return_conv_state=False, workspace=ws)
+
+    def unfused():   # the same layer as three entry points (q, k, v and o through memory)
+        qq, kk, vv, _ = axiom_amd.kda_prologue(*xs, *ws_, H, out_dtype=torch.bfloat16, return_state=False)
+        o, _ = axiom_amd.kda_chunk_fwd(qq, kk, vv, g, beta, workspace=cws)
+        return axiom_amd.kda_epilogue(o, gate, out_dtype=torch.bfloat16)
+
+    def timed(f):
+        for _ in range(5):
+            f()
+        torch.cuda.synchronize()
+        e0, e1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+        e0.record(stream)
+        for _ in range(args.steps):
+            f()
+        e1.record(stream)
+        torch.cuda.synchronize()
+        return e0.elapsed_time(e1) / 1e3 / args.steps
+    t_call = timed(call)
+    t_unfused = timed(unfused)
+    nbytes = layer_bytes(B, T, H, d, K)
+    gbps = nbytes / t_call / 1e9
+    return dict(us_per_call=t_call * 1e6, tokens_per_s=B * T / t_call, unfused_us_per_call=t_unfused * 1e6,
+                roofline={"bound": "hbm", "achieved": gbps, "peak": HBM_PEAK_GBPS, "unit": "GB/s",
+                          "frac": gbps / HBM_PEAK_GBPS, "algorithmic_bytes_per_call": nbytes},
+                kernels="kda_intra_kernel with the fused short conv + kda_state_col_kernel + kda_epilogue_kernel",
+                config="B4 T4096 H16 d128 K4, bf16 projections, gates and y, fp32 o inside, zero h0")
+
+
 def bench_ut_solve(args, device):
     import axiom_amd
     H, C, N = 12, 64, 256
@@ -327,6 +384,7 @@ def main():
         line["decode"] = bench_decode(args, device)
     if not args.no_backward:
         line["backward"] = bench_backward(args, fwd["inputs"], device)
+    line["layer"] = bench_layer(args, fwd["inputs"], device)
     line["ut_solve"] = bench_ut_solve(args, device)
     if not args.no_cpu_baseline:
         line["cpu_baseline"] = cpu_baseline(fwd["inputs"], args.cpu_seconds)
