@@ -349,32 +349,49 @@ __global__ __launch_bounds__(kPrepThreads) void kda_bwd_prep_kernel(BwdArgs a) {
 }
 
 // ---------------------------------------------------------------------------
-// forward state scan of one (chain, 32-column slice): S_in and v~ per chunk
+// The two scans run their products on the fp32 matrix cores
+// (v_mfma_f32_16x16x4f32, exact fp32 products): lane (r = l & 15, gq = l >> 4)
+// supplies A[r][4s + gq] and B[4s + gq][r] of K step s and holds D rows
+// 4 gq + i, column r.  Eight waves per workgroup; the 32-column state slice is
+// (D/16) x 2 tiles in accumulators, D/64 tiles per wave; the [64][32] results
+// of a chunk are 8 tiles, one per wave.  LDS pitches: PW = D + 2 for [64][D]
+// operands (row fragments conflict-free, column fragments 2-way), PB = 48 for
+// [*][32] B operands, PA = 80 for Aqk read by columns.
 // ---------------------------------------------------------------------------
+constexpr int kPB = 48;
+constexpr int kPA = kC + 16;
+
+__device__ __forceinline__ f4 mfma4(float a, float b, f4 c) {
+  return __builtin_amdgcn_mfma_f32_16x16x4f32(a, b, c, 0, 0, 0);
+}
+
+// forward state scan of one (chain, 32-column slice): S_in and v~ per chunk
 template <int D>
 __global__ __launch_bounds__(kScanThreads) void kda_bwd_fscan_kernel(BwdArgs a) {
-  typedef BwdDims<D> BD;
-  constexpr int P = BD::P;
+  constexpr int PW = D + 2;
   constexpr int NS = D / 32;
-  constexpr int NI = D / 16;   // state rows per thread
-  __shared__ float sW[kC * P], sKL[kC * P];
-  __shared__ float sS[D * 33], sU[kC * 33], sV[kC * 33], sGC[D];
+  constexpr int NST = D / 64;   // state tiles per wave
+  __shared__ float sW[kC * PW], sKL[kC * PW];
+  __shared__ float sS[D * kPB], sU[kC * kPB], sV[kC * kPB], sGC[D];
   constexpr int NTH = kScanThreads;
-  constexpr int TC = NTH / 16;   // threads per row group: slice columns cn + TC j
-  constexpr int CJ = 32 / TC;    // slice columns per thread
-  const int t = threadIdx.x, rm = t / TC, cn = t % TC;
+  const int t = threadIdx.x, wv = t >> 6, l = t & 63, r = l & 15, gq = l >> 4;
   const int H = a.H;
   int chain, split;
   if (!scan_slot<NS>(a.B * H, chain, split)) return;   // uniform per workgroup
   const int b = chain / H, h = chain - b * H;
   const int c0 = 32 * split;
-  float S[NI][CJ];
+  const int mt = wv >> 1, ct = wv & 1;                  // this wave's v~ tile
+  int rt[NST], cs[NST];                                 // this wave's state tiles
 #pragma unroll
-  for (int i = 0; i < NI; ++i)
+  for (int q = 0; q < NST; ++q) { rt[q] = (wv * NST + q) >> 1; cs[q] = (wv * NST + q) & 1; }
+  f4 S[NST];
 #pragma unroll
-    for (int j = 0; j < CJ; ++j)
-      S[i][j] = (a.h0 != nullptr) ? a.h0[(static_cast<int64_t>(chain) * D + rm + 16 * i) * D + c0 + cn + TC * j]
-                                  : 0.f;
+  for (int q = 0; q < NST; ++q)
+#pragma unroll
+    for (int i = 0; i < 4; ++i)
+      S[q][i] = (a.h0 != nullptr)
+                    ? a.h0[(static_cast<int64_t>(chain) * D + 16 * rt[q] + 4 * gq + i) * D + c0 + 16 * cs[q] + r]
+                    : 0.f;
   // chunk n's W, lambda*k and U slice are loaded into registers during
   // chunk n-1's arithmetic
   Tile<kC, D, NTH> tW, tK;
@@ -390,97 +407,80 @@ __global__ __launch_bounds__(kScanThreads) void kda_bwd_fscan_kernel(BwdArgs a) 
     const int64_t ch = (static_cast<int64_t>(b) * a.NT + n) * H + h;
     float* SI = a.SI + ch * D * D;
 #pragma unroll
-    for (int i = 0; i < NI; ++i)
+    for (int q = 0; q < NST; ++q)
 #pragma unroll
-      for (int j = 0; j < CJ; ++j) {
-        SI[(rm + 16 * i) * D + c0 + cn + TC * j] = S[i][j];
-        sS[(rm + 16 * i) * 33 + cn + TC * j] = S[i][j];
+      for (int i = 0; i < 4; ++i) {
+        const int row = 16 * rt[q] + 4 * gq + i, col = 16 * cs[q] + r;
+        SI[row * D + c0 + col] = S[q][i];
+        sS[row * kPB + col] = S[q][i];
       }
-    tW.template put<P>(sW);
-    tK.template put<P>(sKL);
-    tU.template put<33>(sU);
+    tW.template put<PW>(sW);
+    tK.template put<PW>(sKL);
+    tU.template put<kPB>(sU);
     if (t < D) sGC[t] = a.GCV[ch * D + t];
     if (n + 1 < a.NT) fetch(n + 1);
     __syncthreads();
-    // v~ = U - W S: rows rm + 16i (i < 4), columns cn + 16j (j < 2)
+    // v~ = U - W S (two accumulation chains over K = D)
     {
-      float acc[4][CJ];
+      f4 acc0, acc1 = {0.f, 0.f, 0.f, 0.f};
 #pragma unroll
-      for (int i = 0; i < 4; ++i)
-#pragma unroll
-        for (int j = 0; j < CJ; ++j) acc[i][j] = sU[(rm + 16 * i) * 33 + cn + TC * j];
-      #pragma unroll 4
-      for (int d = 0; d < D; ++d) {
-        float sv[CJ];
-#pragma unroll
-        for (int j = 0; j < CJ; ++j) sv[j] = sS[d * 33 + cn + TC * j];
-#pragma unroll
-        for (int i = 0; i < 4; ++i) {
-          const float w = sW[(rm + 16 * i) * P + d];
-#pragma unroll
-          for (int j = 0; j < CJ; ++j) acc[i][j] = fmaf(-w, sv[j], acc[i][j]);
-        }
+      for (int i = 0; i < 4; ++i) acc0[i] = sU[(16 * mt + 4 * gq + i) * kPB + 16 * ct + r];
+#pragma unroll 8
+      for (int k = 0; k < D / 4; k += 2) {
+        acc0 = mfma4(-sW[(16 * mt + r) * PW + 4 * k + gq], sS[(4 * k + gq) * kPB + 16 * ct + r], acc0);
+        acc1 = mfma4(-sW[(16 * mt + r) * PW + 4 * k + 4 + gq], sS[(4 * k + 4 + gq) * kPB + 16 * ct + r], acc1);
       }
       float* VT = a.VT + ch * kC * D;
 #pragma unroll
-      for (int i = 0; i < 4; ++i)
-#pragma unroll
-        for (int j = 0; j < CJ; ++j) {
-          sV[(rm + 16 * i) * 33 + cn + TC * j] = acc[i][j];
-          VT[(rm + 16 * i) * D + c0 + cn + TC * j] = acc[i][j];
-        }
+      for (int i = 0; i < 4; ++i) {
+        const int row = 16 * mt + 4 * gq + i, col = 16 * ct + r;
+        const float v = acc0[i] + acc1[i];
+        sV[row * kPB + col] = v;
+        VT[row * D + c0 + col] = v;
+      }
     }
     __syncthreads();
     // S <- gamma_C S + (lambda k)^T v~
 #pragma unroll
-    for (int i = 0; i < NI; ++i) {
-      const float gcv = sGC[rm + 16 * i];
+    for (int q = 0; q < NST; ++q)
 #pragma unroll
-      for (int j = 0; j < CJ; ++j) S[i][j] *= gcv;
-    }
-    #pragma unroll 4
-    for (int c = 0; c < kC; ++c) {
-      float vv[CJ];
+      for (int i = 0; i < 4; ++i) S[q][i] *= sGC[16 * rt[q] + 4 * gq + i];
+#pragma unroll 4
+    for (int k = 0; k < kC / 4; ++k)
 #pragma unroll
-      for (int j = 0; j < CJ; ++j) vv[j] = sV[c * 33 + cn + TC * j];
-#pragma unroll
-      for (int i = 0; i < NI; ++i) {
-        const float kl = sKL[c * P + rm + 16 * i];
-#pragma unroll
-        for (int j = 0; j < CJ; ++j) S[i][j] = fmaf(kl, vv[j], S[i][j]);
-      }
-    }
+      for (int q = 0; q < NST; ++q)
+        S[q] = mfma4(sKL[(4 * k + gq) * PW + 16 * rt[q] + r], sV[(4 * k + gq) * kPB + 16 * cs[q] + r], S[q]);
     __syncthreads();
   }
 }
 
-// ---------------------------------------------------------------------------
 // reverse scan of one (chain, 32-column slice): dS per chunk, dv~, dh0
-// ---------------------------------------------------------------------------
 template <int D, int DO>
 __global__ __launch_bounds__(kScanThreads) void kda_bwd_rscan_kernel(BwdArgs a) {
-  typedef BwdDims<D> BD;
-  constexpr int P = BD::P, PC = BD::PC;
+  constexpr int PW = D + 2;
   constexpr int NS = D / 32;
-  constexpr int NI = D / 16;
-  __shared__ float sX[kC * P], sY[kC * P], sA[kC * PC];
-  __shared__ float sS[D * 33], sDo[kC * 33], sDv[kC * 33], sGC[D];
+  constexpr int NST = D / 64;
+  __shared__ float sX[kC * PW], sY[kC * PW], sA[kC * kPA];
+  __shared__ float sS[D * kPB], sDo[kC * kPB], sDv[kC * kPB], sGC[D];
   constexpr int NTH = kScanThreads;
-  constexpr int TC = NTH / 16;   // threads per row group: slice columns cn + TC j
-  constexpr int CJ = 32 / TC;    // slice columns per thread
-  const int t = threadIdx.x, rm = t / TC, cn = t % TC;
+  const int t = threadIdx.x, wv = t >> 6, l = t & 63, r = l & 15, gq = l >> 4;
   const int H = a.H;
   int chain, split;
   if (!scan_slot<NS>(a.B * H, chain, split)) return;   // uniform per workgroup
   const int b = chain / H, h = chain - b * H;
   const int c0 = 32 * split;
-  float dS[NI][CJ];
+  const int mt = wv >> 1, ct = wv & 1;
+  int rt[NST], cs[NST];
 #pragma unroll
-  for (int i = 0; i < NI; ++i)
+  for (int q = 0; q < NST; ++q) { rt[q] = (wv * NST + q) >> 1; cs[q] = (wv * NST + q) & 1; }
+  f4 dS[NST];
 #pragma unroll
-    for (int j = 0; j < CJ; ++j)
-      dS[i][j] = (a.dht != nullptr) ? a.dht[(static_cast<int64_t>(chain) * D + rm + 16 * i) * D + c0 + cn + TC * j]
-                                    : 0.f;
+  for (int q = 0; q < NST; ++q)
+#pragma unroll
+    for (int i = 0; i < 4; ++i)
+      dS[q][i] = (a.dht != nullptr)
+                     ? a.dht[(static_cast<int64_t>(chain) * D + 16 * rt[q] + 4 * gq + i) * D + c0 + 16 * cs[q] + r]
+                     : 0.f;
   // Operands of the two products of a chunk, loaded into registers one
   // product ahead: lambda*k and Aqk (for dv~) during the previous chunk's dS
   // update, gamma*q and W (for dS) during this chunk's dv~.
@@ -498,94 +498,64 @@ __global__ __launch_bounds__(kScanThreads) void kda_bwd_rscan_kernel(BwdArgs a) 
     const ChunkRows cr = chunk_rows(a, u);
     float* DS = a.DS + ch * D * D;
 #pragma unroll
-    for (int i = 0; i < NI; ++i)
+    for (int q = 0; q < NST; ++q)
 #pragma unroll
-      for (int j = 0; j < CJ; ++j) {
-        DS[(rm + 16 * i) * D + c0 + cn + TC * j] = dS[i][j];
-        sS[(rm + 16 * i) * 33 + cn + TC * j] = dS[i][j];
+      for (int i = 0; i < 4; ++i) {
+        const int row = 16 * rt[q] + 4 * gq + i, col = 16 * cs[q] + r;
+        DS[row * D + c0 + col] = dS[q][i];
+        sS[row * kPB + col] = dS[q][i];
       }
-    tX.template put<P>(sX);
-    tA.template put<PC>(sA);
-    lds_load_in<DO, D, 32, 33, NTH>(sDo, a.dout, cr.row0, cr.len, H, h, c0, 1.f);
+    tX.template put<PW>(sX);
+    tA.template put<kPA>(sA);
+    lds_load_in<DO, D, 32, kPB, NTH>(sDo, a.dout, cr.row0, cr.len, H, h, c0, 1.f);
     if (t < D) sGC[t] = a.GCV[ch * D + t];
     tX.fetch(a.QG + ch * kC * D, D, 0);
     tY.fetch(a.WM + ch * kC * D, D, 0);
     __syncthreads();
     // dv~ = (lambda k) dS + Aqk^T do
     {
-      float acc[4][CJ];
-#pragma unroll
-      for (int i = 0; i < 4; ++i)
-#pragma unroll
-        for (int j = 0; j < CJ; ++j) acc[i][j] = 0.f;
-      #pragma unroll 4
-      for (int d = 0; d < D; ++d) {
-        float sv[CJ];
-#pragma unroll
-        for (int j = 0; j < CJ; ++j) sv[j] = sS[d * 33 + cn + TC * j];
-#pragma unroll
-        for (int i = 0; i < 4; ++i) {
-          const float kl = sX[(rm + 16 * i) * P + d];
-#pragma unroll
-          for (int j = 0; j < CJ; ++j) acc[i][j] = fmaf(kl, sv[j], acc[i][j]);
-        }
-      }
-      #pragma unroll 4
-      for (int c = 0; c < kC; ++c) {
-        float ov[CJ];
-#pragma unroll
-        for (int j = 0; j < CJ; ++j) ov[j] = sDo[c * 33 + cn + TC * j];
-#pragma unroll
-        for (int i = 0; i < 4; ++i) {
-          const float av = sA[c * PC + rm + 16 * i];
-#pragma unroll
-          for (int j = 0; j < CJ; ++j) acc[i][j] = fmaf(av, ov[j], acc[i][j]);
-        }
-      }
+      f4 acc0 = {0.f, 0.f, 0.f, 0.f}, acc1 = {0.f, 0.f, 0.f, 0.f};
+#pragma unroll 8
+      for (int k = 0; k < D / 4; ++k)
+        acc0 = mfma4(sX[(16 * mt + r) * PW + 4 * k + gq], sS[(4 * k + gq) * kPB + 16 * ct + r], acc0);
+#pragma unroll 8
+      for (int k = 0; k < kC / 4; ++k)
+        acc1 = mfma4(sA[(4 * k + gq) * kPA + 16 * mt + r], sDo[(4 * k + gq) * kPB + 16 * ct + r], acc1);
       float* DVT = a.DVT + ch * kC * D;
 #pragma unroll
-      for (int i = 0; i < 4; ++i)
-#pragma unroll
-        for (int j = 0; j < CJ; ++j) {
-          sDv[(rm + 16 * i) * 33 + cn + TC * j] = acc[i][j];
-          DVT[(rm + 16 * i) * D + c0 + cn + TC * j] = acc[i][j];
-        }
+      for (int i = 0; i < 4; ++i) {
+        const int row = 16 * mt + 4 * gq + i, col = 16 * ct + r;
+        const float v = acc0[i] + acc1[i];
+        sDv[row * kPB + col] = v;
+        DVT[row * D + c0 + col] = v;
+      }
     }
     __syncthreads();
-    tX.template put<P>(sX);
-    tY.template put<P>(sY);
+    tX.template put<PW>(sX);
+    tY.template put<PW>(sY);
     if (n > 0) fetch_a(n - 1);
     __syncthreads();
     // dS <- gamma_C dS + (gamma q)^T do - W^T dv~
 #pragma unroll
-    for (int i = 0; i < NI; ++i) {
-      const float gcv = sGC[rm + 16 * i];
+    for (int q = 0; q < NST; ++q)
 #pragma unroll
-      for (int j = 0; j < CJ; ++j) dS[i][j] *= gcv;
-    }
-    #pragma unroll 4
-    for (int c = 0; c < kC; ++c) {
-      float ov[CJ], dvv[CJ];
+      for (int i = 0; i < 4; ++i) dS[q][i] *= sGC[16 * rt[q] + 4 * gq + i];
+#pragma unroll 4
+    for (int k = 0; k < kC / 4; ++k)
 #pragma unroll
-      for (int j = 0; j < CJ; ++j) {
-        ov[j] = sDo[c * 33 + cn + TC * j];
-        dvv[j] = sDv[c * 33 + cn + TC * j];
+      for (int q = 0; q < NST; ++q) {
+        const int kr = (4 * k + gq) * PW + 16 * rt[q] + r, kb = (4 * k + gq) * kPB + 16 * cs[q] + r;
+        dS[q] = mfma4(sX[kr], sDo[kb], dS[q]);
+        dS[q] = mfma4(-sY[kr], sDv[kb], dS[q]);
       }
-#pragma unroll
-      for (int i = 0; i < NI; ++i) {
-        const float qg = sX[c * P + rm + 16 * i], w = sY[c * P + rm + 16 * i];
-#pragma unroll
-        for (int j = 0; j < CJ; ++j) dS[i][j] = fmaf(qg, ov[j], fmaf(-w, dvv[j], dS[i][j]));
-      }
-    }
     __syncthreads();
   }
   if (a.dh0 != nullptr) {
 #pragma unroll
-    for (int i = 0; i < NI; ++i)
+    for (int q = 0; q < NST; ++q)
 #pragma unroll
-      for (int j = 0; j < CJ; ++j)
-        a.dh0[(static_cast<int64_t>(chain) * D + rm + 16 * i) * D + c0 + cn + TC * j] = dS[i][j];
+      for (int i = 0; i < 4; ++i)
+        a.dh0[(static_cast<int64_t>(chain) * D + 16 * rt[q] + 4 * gq + i) * D + c0 + 16 * cs[q] + r] = dS[q][i];
   }
 }
 
