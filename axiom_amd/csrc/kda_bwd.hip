@@ -569,11 +569,11 @@ __global__ __launch_bounds__(kChunkThreads) void kda_bwd_chunk_kernel(BwdArgs a)
   constexpr int NTH = kChunkThreads;
   constexpr int TC = NTH / 16;        // threads per row group: columns cn + TC j
   constexpr int NJ = D / TC;          // columns per thread of a [64][D] product
-  constexpr int NJC = kC / TC;        // of a [64][64] product
   constexpr int HW = 64;             // value columns per pass of phase 1
   constexpr int NH = D / HW;
-  // phase 4 is the largest: dL, dAqk [64][65]; q, k, G [64][P]; three [16][P]
-  constexpr int SMEM_FLOATS = 2 * kC * PC + 3 * kC * P + 3 * 16 * P + kC;
+  // phase 4 is the largest: dL, dAqk [64][65]; q, k, G [64][P]; three [16][PF]
+  constexpr int PF = D + 16;          // column-fragment pitch of phase 4's factored operands
+  constexpr int SMEM_FLOATS = 2 * kC * PC + 3 * kC * P + 3 * 16 * PF + kC;
   __shared__ float sm[SMEM_FLOATS];
   const int t = threadIdx.x, rm = t / TC, cn = t % TC;
   const int H = a.H;
@@ -587,361 +587,365 @@ __global__ __launch_bounds__(kChunkThreads) void kda_bwd_chunk_kernel(BwdArgs a)
   auto ld_v = [&](int c, int d) { return (c < cr.len) ? ld1<DTQ>(a.v, in_idx(c, d)) : 0.f; };
   auto ld_b = [&](int c) { return (c < cr.len) ? ld1<DTG>(a.beta, (cr.row0 + c) * H + h) : 0.f; };
   // The gradients of q, k and G accumulate in place in dq, dk and dg (dg
-  // holds dG until the final reverse cumsum): each thread owns the positions
-  // (rm + 16i, cn + 16j) of its row tile i = 0..3, so its own read-modify-
-  // writes need no synchronisation; pad rows (c >= len) are never stored
-  // (their dG is zero: every term carries a factor q_c or k_c).
+  // holds dG until the final reverse cumsum).  Phases 1-3 run on the fp32
+  // matrix cores: wave wv owns row tile mt = wv / 2 and the NDT column tiles
+  // dt = (wv % 2) NDT + q of every [64][D] product (lane (r, gq) holds rows
+  // 16 mt + 4 gq + i, column 16 dt + r), so its read-modify-writes of phases
+  // 1 and 2 hit its own positions; phase 4 owns positions (rm + 16i, cn + TC j)
+  // and reads what other threads wrote, after the workgroup barriers between
+  // the phases.  Pad rows (c >= len) are never stored (their dG is zero: every
+  // term carries a factor q_c or k_c).
   float* const gq_ = a.dq;
   float* const gk_ = a.dk;
   float* const gG_ = a.dg;
+  constexpr int NDT = D / 32;          // column tiles per wave of a [64][D] product
+  const int wv = t >> 6, l = t & 63, r16 = l & 15, gq = l >> 4;
+  const int mt = wv >> 1, dg_ = wv & 1;
+  constexpr int PH = HW + 2;           // row-fragment pitch of phase 1's [*][HW] tiles
+  constexpr int PR = D + 2;            // row-fragment pitch of [64][D] operands
+  constexpr int PX = D + 16;           // column-fragment pitch of [64][D] operands
+  constexpr int PT = kC + 16;          // column-fragment pitch of T
 
-  float dbr[4], dzp[NJ];
+  float dbrD[4], dzp[NDT];             // dbeta partials (rows 16 mt + 4 gq + i), dz partials
 #pragma unroll
-  for (int i = 0; i < 4; ++i) dbr[i] = 0.f;
+  for (int i = 0; i < 4; ++i) dbrD[i] = 0.f;
 #pragma unroll
-  for (int j = 0; j < NJ; ++j) dzp[j] = 0.f;
+  for (int q = 0; q < NDT; ++q) dzp[q] = 0.f;
   float dgc = 0.f;   // thread t < D: sum_n S[t][n] dS'[t][n]
 
-  // ---- phase 1: dY = v~ dS'^T, dgq = do S^T, dW = -dv~ S^T (K = dv in passes of 64)
-  float dW[4][NJ];
+  // ---- phase 1: dY = v~ dS'^T, dgq = do S^T, dW = -dv~ S^T (K = dv in passes of HW)
+  f4 dW[NDT];
   {
-    float dY[4][NJ], dgq[4][NJ];
+    f4 dY[NDT], dgq[NDT];
 #pragma unroll
-    for (int i = 0; i < 4; ++i)
+    for (int q = 0; q < NDT; ++q)
 #pragma unroll
-      for (int j = 0; j < NJ; ++j) dY[i][j] = dgq[i][j] = dW[i][j] = 0.f;
+      for (int i = 0; i < 4; ++i) dY[q][i] = dgq[q][i] = dW[q][i] = 0.f;
     float* sVt = sm;
-    float* sDo = sVt + kC * PC;
-    float* sDv = sDo + kC * PC;
-    float* sS = sDv + kC * PC;
-    float* sDS = sS + D * PC;
+    float* sDo = sVt + kC * PH;
+    float* sDv = sDo + kC * PH;
+    float* sS = sDv + kC * PH;
+    float* sDS = sS + D * PH;
     for (int hp = 0; hp < NH; ++hp) {
       const int n0 = HW * hp;
-      lds_load<kC, HW, PC, NTH>(sVt, a.VT + ch * kC * D, D, n0);
-      lds_load<kC, HW, PC, NTH>(sDv, a.DVT + ch * kC * D, D, n0);
-      lds_load<D, HW, PC, NTH>(sS, a.SI + ch * D * D, D, n0);
-      lds_load<D, HW, PC, NTH>(sDS, a.DS + ch * D * D, D, n0);
-      lds_load_in<DO, D, HW, PC, NTH>(sDo, a.dout, cr.row0, cr.len, H, h, n0, 1.f);
+      lds_load<kC, HW, PH, NTH>(sVt, a.VT + ch * kC * D, D, n0);
+      lds_load<kC, HW, PH, NTH>(sDv, a.DVT + ch * kC * D, D, n0);
+      lds_load<D, HW, PH, NTH>(sS, a.SI + ch * D * D, D, n0);
+      lds_load<D, HW, PH, NTH>(sDS, a.DS + ch * D * D, D, n0);
+      lds_load_in<DO, D, HW, PH, NTH>(sDo, a.dout, cr.row0, cr.len, H, h, n0, 1.f);
       __syncthreads();
-      #pragma unroll 4
-      for (int nn = 0; nn < HW; ++nn) {
-        float va[4], oa[4], wa[4];
+#pragma unroll 4
+      for (int k = 0; k < HW / 4; ++k) {
+        const int ka = (16 * mt + r16) * PH + 4 * k + gq;
+        const float av = sVt[ka], ao = sDo[ka], aw = -sDv[ka];
 #pragma unroll
-        for (int i = 0; i < 4; ++i) {
-          va[i] = sVt[(rm + 16 * i) * PC + nn];
-          oa[i] = sDo[(rm + 16 * i) * PC + nn];
-          wa[i] = sDv[(rm + 16 * i) * PC + nn];
-        }
-#pragma unroll
-        for (int j = 0; j < NJ; ++j) {
-          const float sv = sS[(cn + TC * j) * PC + nn], dsv = sDS[(cn + TC * j) * PC + nn];
-#pragma unroll
-          for (int i = 0; i < 4; ++i) {
-            dY[i][j] = fmaf(va[i], dsv, dY[i][j]);
-            dgq[i][j] = fmaf(oa[i], sv, dgq[i][j]);
-            dW[i][j] = fmaf(-wa[i], sv, dW[i][j]);
-          }
+        for (int q = 0; q < NDT; ++q) {
+          const int kb = (16 * (dg_ * NDT + q) + r16) * PH + 4 * k + gq;
+          const float bs = sS[kb];
+          dY[q] = mfma4(av, sDS[kb], dY[q]);
+          dgq[q] = mfma4(ao, bs, dgq[q]);
+          dW[q] = mfma4(aw, bs, dW[q]);
         }
       }
       if (t < D) {
-        for (int nn = 0; nn < HW; ++nn) dgc = fmaf(sS[t * PC + nn], sDS[t * PC + nn], dgc);
+        for (int nn = 0; nn < HW; ++nn) dgc = fmaf(sS[t * PH + nn], sDS[t * PH + nn], dgc);
       }
       __syncthreads();
     }
-    // dq = dgq gamma; dG = dgq q gamma - dY k lambda; dk = dY lambda.  Each
-    // row tile's loads are issued before its stores (the compiler cannot move
-    // a load above a store to a pointer it may alias).
-    float glast[NJ];
+    // dq = dgq gamma; dG = dgq q gamma - dY k lambda; dk = dY lambda.  Loads
+    // of a tile are issued before its stores (the compiler cannot move a load
+    // above a store to a pointer it may alias).
 #pragma unroll
-    for (int j = 0; j < NJ; ++j) glast[j] = GL[(kC - 1) * D + cn + TC * j];
+    for (int q = 0; q < NDT; ++q) {
+      const int d = 16 * (dg_ * NDT + q) + r16;
+      const float glast = GL[(kC - 1) * D + d];
+      float gl[4], qv[4], kv[4];
 #pragma unroll
-    for (int i = 0; i < 4; ++i) {
-      const int c = rm + 16 * i;
-      float gl[NJ], qv[NJ], kv[NJ];
-#pragma unroll
-      for (int j = 0; j < NJ; ++j) {
-        gl[j] = GL[c * D + cn + TC * j];
-        qv[j] = ld_q(c, cn + TC * j);
-        kv[j] = ld_k(c, cn + TC * j);
+      for (int i = 0; i < 4; ++i) {
+        const int c = 16 * mt + 4 * gq + i;
+        gl[i] = GL[c * D + d];
+        qv[i] = ld_q(c, d);
+        kv[i] = ld_k(c, d);
       }
 #pragma unroll
-      for (int j = 0; j < NJ; ++j) {
-        const int d = cn + TC * j;
-        const float gam = ex2(gl[j]), lam = ex2(glast[j] - gl[j]);
-        const float dz = dY[i][j] * kv[j] * lam;
-        dzp[j] += dz;
+      for (int i = 0; i < 4; ++i) {
+        const int c = 16 * mt + 4 * gq + i;
+        const float gam = ex2(gl[i]), lam = ex2(glast - gl[i]);
+        const float dz = dY[q][i] * kv[i] * lam;
+        dzp[q] += dz;
         if (c < cr.len) {
-          gq_[in_idx(c, d)] = dgq[i][j] * gam * a.scale;
-          gk_[in_idx(c, d)] = dY[i][j] * lam;
-          gG_[in_idx(c, d)] = dgq[i][j] * qv[j] * gam - dz;
+          gq_[in_idx(c, d)] = dgq[q][i] * gam * a.scale;
+          gk_[in_idx(c, d)] = dY[q][i] * lam;
+          gG_[in_idx(c, d)] = dgq[q][i] * qv[i] * gam - dz;
         }
       }
     }
   }
 
-  // ---- phase 2: Yw = T^T dW, Yu = T^T dv~
-  float Yw[4][NJ], Yu[4][NJ];
+  // ---- phase 2: Yw = T^T dW, Yu = T^T dv~ (K = the chunk's 64 rows)
+  f4 Yw[NDT], Yu[NDT];
   {
     float* sT = sm;
-    float* sX = sT + kC * PC;
-    float* sY = sX + kC * P;
+    float* sX = sT + kC * PT;
+    float* sY = sX + kC * PX;
 #pragma unroll
-    for (int i = 0; i < 4; ++i)
+    for (int q = 0; q < NDT; ++q)
 #pragma unroll
-      for (int j = 0; j < NJ; ++j) sX[(rm + 16 * i) * P + cn + TC * j] = dW[i][j];
-    lds_load<kC, kC, PC, NTH>(sT, a.TM + ch * kC * kC, kC, 0);
-    lds_load<kC, D, P, NTH>(sY, a.DVT + ch * kC * D, D, 0);
+      for (int i = 0; i < 4; ++i) sX[(16 * mt + 4 * gq + i) * PX + 16 * (dg_ * NDT + q) + r16] = dW[q][i];
+    lds_load<kC, kC, PT, NTH>(sT, a.TM + ch * kC * kC, kC, 0);
+    lds_load<kC, D, PX, NTH>(sY, a.DVT + ch * kC * D, D, 0);
     __syncthreads();
 #pragma unroll
-    for (int i = 0; i < 4; ++i)
+    for (int q = 0; q < NDT; ++q)
 #pragma unroll
-      for (int j = 0; j < NJ; ++j) Yw[i][j] = Yu[i][j] = 0.f;
-    #pragma unroll 4
-    for (int m = 0; m < kC; ++m) {
-      float tv[4];
+      for (int i = 0; i < 4; ++i) Yw[q][i] = Yu[q][i] = 0.f;
+#pragma unroll 4
+    for (int k = 0; k < kC / 4; ++k) {
+      const float at = sT[(4 * k + gq) * PT + 16 * mt + r16];   // (T^T)[c][m] = T[m][c]
 #pragma unroll
-      for (int i = 0; i < 4; ++i) tv[i] = sT[m * PC + rm + 16 * i];
-#pragma unroll
-      for (int j = 0; j < NJ; ++j) {
-        const float x = sX[m * P + cn + TC * j], y = sY[m * P + cn + TC * j];
-#pragma unroll
-        for (int i = 0; i < 4; ++i) {
-          Yw[i][j] = fmaf(tv[i], x, Yw[i][j]);
-          Yu[i][j] = fmaf(tv[i], y, Yu[i][j]);
-        }
+      for (int q = 0; q < NDT; ++q) {
+        const int kb = (4 * k + gq) * PX + 16 * (dg_ * NDT + q) + r16;
+        Yw[q] = mfma4(at, sX[kb], Yw[q]);
+        Yu[q] = mfma4(at, sY[kb], Yu[q]);
       }
     }
     __syncthreads();
     // dG += Yw k beta gamma; dk += Yw gamma beta; dv = Yu beta; dbeta += Yw gamma k + Yu v
 #pragma unroll
     for (int i = 0; i < 4; ++i) {
-      const int c = rm + 16 * i;
+      const int c = 16 * mt + 4 * gq + i;
       const bool live = c < cr.len;
       const float bc = ld_b(c);
-      float gl[NJ], kv[NJ], vv[NJ], oG[NJ], ok[NJ];
+      float gl[NDT], kv[NDT], vv[NDT], oG[NDT], ok[NDT];
 #pragma unroll
-      for (int j = 0; j < NJ; ++j) {
-        const int d = cn + TC * j;
-        gl[j] = GL[c * D + d];
-        kv[j] = ld_k(c, d);
-        vv[j] = ld_v(c, d);
-        oG[j] = live ? gG_[in_idx(c, d)] : 0.f;
-        ok[j] = live ? gk_[in_idx(c, d)] : 0.f;
+      for (int q = 0; q < NDT; ++q) {
+        const int d = 16 * (dg_ * NDT + q) + r16;
+        gl[q] = GL[c * D + d];
+        kv[q] = ld_k(c, d);
+        vv[q] = ld_v(c, d);
+        oG[q] = live ? gG_[in_idx(c, d)] : 0.f;
+        ok[q] = live ? gk_[in_idx(c, d)] : 0.f;
       }
 #pragma unroll
-      for (int j = 0; j < NJ; ++j) {
-        const int d = cn + TC * j;
-        const float gam = ex2(gl[j]);
-        dbr[i] += Yw[i][j] * gam * kv[j] + Yu[i][j] * vv[j];
+      for (int q = 0; q < NDT; ++q) {
+        const int d = 16 * (dg_ * NDT + q) + r16;
+        const float gam = ex2(gl[q]);
+        dbrD[i] += Yw[q][i] * gam * kv[q] + Yu[q][i] * vv[q];
         if (live) {
-          gG_[in_idx(c, d)] = oG[j] + Yw[i][j] * kv[j] * bc * gam;
-          gk_[in_idx(c, d)] = ok[j] + Yw[i][j] * gam * bc;
-          a.dv[in_idx(c, d)] = Yu[i][j] * bc;
+          gG_[in_idx(c, d)] = oG[q] + Yw[q][i] * kv[q] * bc * gam;
+          gk_[in_idx(c, d)] = ok[q] + Yw[q][i] * gam * bc;
+          a.dv[in_idx(c, d)] = Yu[q][i] * bc;
         }
       }
     }
   }
 
-  // ---- phase 3: dL = strict(-(Yw W^T + Yu U^T)), dAqk = tril(do v~^T)
-  float dLr[4][NJC], dAr[4][NJC];   // rows rm + 16i, columns cn + TC j
+  // ---- phase 3: dL = strict(-(Yw W^T + Yu U^T)), dAqk = tril(do v~^T); [64][64]
+  // outputs, two 16 x 16 tiles per wave: row tile mt, key tiles 2 (wv % 2) + q
+  static_assert(3 * kC * PH + 2 * D * PH <= SMEM_FLOATS, "phase 1 LDS");
+  static_assert(kC * PT + 2 * kC * PX <= SMEM_FLOATS, "phase 2 LDS");
+  static_assert(4 * kC * PR <= SMEM_FLOATS, "phase 3 LDS");
+  float* const sDL = sm;                 // phase 4's operands, written at the end of phase 3
+  float* const sDA = sDL + kC * PC;
   {
-    float* sX = sm;
-    float* sY = sX + kC * P;
-    float* sW = sY + kC * P;
-    float* sU = sW + kC * P;
+    float* sA = sm;                      // Yw, then do
+    float* sB = sA + kC * PR;            // Yu, then v~
+    float* sW = sB + kC * PR;
+    float* sU = sW + kC * PR;
 #pragma unroll
-    for (int i = 0; i < 4; ++i)
-#pragma unroll
-      for (int j = 0; j < NJ; ++j) {
-        sX[(rm + 16 * i) * P + cn + TC * j] = Yw[i][j];
-        sY[(rm + 16 * i) * P + cn + TC * j] = Yu[i][j];
-      }
-    lds_load<kC, D, P, NTH>(sW, a.WM + ch * kC * D, D, 0);
-    lds_load<kC, D, P, NTH>(sU, a.UM + ch * kC * D, D, 0);
-    __syncthreads();
-#pragma unroll
-    for (int i = 0; i < 4; ++i)
-#pragma unroll
-      for (int j = 0; j < NJC; ++j) dLr[i][j] = dAr[i][j] = 0.f;
-    #pragma unroll 4
-    for (int d = 0; d < D; ++d) {
-      float yw[4], yu[4];
+    for (int q = 0; q < NDT; ++q)
 #pragma unroll
       for (int i = 0; i < 4; ++i) {
-        yw[i] = sX[(rm + 16 * i) * P + d];
-        yu[i] = sY[(rm + 16 * i) * P + d];
+        const int o = (16 * mt + 4 * gq + i) * PR + 16 * (dg_ * NDT + q) + r16;
+        sA[o] = Yw[q][i];
+        sB[o] = Yu[q][i];
       }
+    lds_load<kC, D, PR, NTH>(sW, a.WM + ch * kC * D, D, 0);
+    lds_load<kC, D, PR, NTH>(sU, a.UM + ch * kC * D, D, 0);
+    __syncthreads();
+    f4 dLa[2], dAa[2];
 #pragma unroll
-      for (int j = 0; j < NJC; ++j) {
-        const float w = sW[(cn + TC * j) * P + d], uu = sU[(cn + TC * j) * P + d];
+    for (int q = 0; q < 2; ++q)
 #pragma unroll
-        for (int i = 0; i < 4; ++i) dLr[i][j] = fmaf(yw[i], w, fmaf(yu[i], uu, dLr[i][j]));
+      for (int i = 0; i < 4; ++i) dLa[q][i] = dAa[q][i] = 0.f;
+#pragma unroll 4
+    for (int k = 0; k < D / 4; ++k) {
+      const int ka = (16 * mt + r16) * PR + 4 * k + gq;
+      const float yw = sA[ka], yu = sB[ka];
+#pragma unroll
+      for (int q = 0; q < 2; ++q) {
+        const int kb = (16 * (2 * dg_ + q) + r16) * PR + 4 * k + gq;
+        dLa[q] = mfma4(yw, sW[kb], dLa[q]);
+        dLa[q] = mfma4(yu, sU[kb], dLa[q]);
       }
     }
     __syncthreads();
-    // do and v~ into the W / U slots
-    lds_load_in<DO, D, D, P, NTH>(sW, a.dout, cr.row0, cr.len, H, h, 0, 1.f);
-    lds_load<kC, D, P, NTH>(sU, a.VT + ch * kC * D, D, 0);
+    // do and v~ into the Yw / Yu slots
+    lds_load_in<DO, D, D, PR, NTH>(sA, a.dout, cr.row0, cr.len, H, h, 0, 1.f);
+    lds_load<kC, D, PR, NTH>(sB, a.VT + ch * kC * D, D, 0);
     __syncthreads();
-    #pragma unroll 4
-    for (int d = 0; d < D; ++d) {
-      float ov[4];
+#pragma unroll 4
+    for (int k = 0; k < D / 4; ++k) {
+      const float ao = sA[(16 * mt + r16) * PR + 4 * k + gq];
 #pragma unroll
-      for (int i = 0; i < 4; ++i) ov[i] = sW[(rm + 16 * i) * P + d];
-#pragma unroll
-      for (int j = 0; j < NJC; ++j) {
-        const float vv = sU[(cn + TC * j) * P + d];
-#pragma unroll
-        for (int i = 0; i < 4; ++i) dAr[i][j] = fmaf(ov[i], vv, dAr[i][j]);
-      }
+      for (int q = 0; q < 2; ++q) dAa[q] = mfma4(ao, sB[(16 * (2 * dg_ + q) + r16) * PR + 4 * k + gq], dAa[q]);
     }
+    __syncthreads();   // every read of sA, sB done before sDL, sDA overwrite them
+    // phase 4's masked operands
+#pragma unroll
+    for (int q = 0; q < 2; ++q)
+#pragma unroll
+      for (int i = 0; i < 4; ++i) {
+        const int c = 16 * mt + 4 * gq + i, ii = 16 * (2 * dg_ + q) + r16;
+        sDL[c * PC + ii] = (ii < c) ? -dLa[q][i] : 0.f;
+        sDA[c * PC + ii] = (ii <= c) ? dAa[q][i] : 0.f;
+      }
     __syncthreads();
   }
 
-  // ---- phase 4: score adjoints (Aqk with rows q, columns k; L with rows k beta, columns k)
+  // ---- phase 4: score adjoints.  With dA = sDA, dL = sDL (masked):
+  //   row side  rA[c] = sum_i dA[c][i] k_i 2^(G_c - G_i),  rK likewise with dL;
+  //   col side  cS[i] = sum_c (dA[c][i] q_c + dL[c][i] beta_c k_c) 2^(G_c - G_i);
+  //   dq += rA; dk += rK beta + cS; dG += rA q + rK k beta - cS k; dbeta_c += sum_d rK k_c
+  // (q carries the scale).  Off-diagonal tile pairs (row tile R > key tile s)
+  // factor the decay at the row tile's first row a, 2^(G_c - G_a) 2^(G_a - G_i),
+  // both <= 1, and run on the matrix cores: (16 x 16 block) x (k_i 2^(G_a - G_i))
+  // for the row side, (block)^T x (q_c 2^(G_c - G_a)) for the column side.
+  // Diagonal tiles take 2^(min(G_c - G_i, 0)) per element (the clamp only
+  // reaches pairs whose cotangent is zero).  Wave wv < D/16 owns column tile
+  // wv: lane (r, gq) rows 4 gq + e of every row tile, column 16 wv + r; each
+  // position gets one read-modify-write.
+  constexpr int NCT = D / 16;
+  float* sDb4 = nullptr;             // [64][8] row partial sums of dbeta, per column tile
   {
-    float* sDL = sm;
-    float* sDA = sDL + kC * PC;
-    float* sQ = sDA + kC * PC;
+    float* sQ = sDA + kC * PC;       // q * scale
     float* sK = sQ + kC * P;
     float* sG = sK + kC * P;
-    float* sXq = sG + kC * P;
-    float* sXk = sXq + 16 * P;
-    float* sKf = sXk + 16 * P;
-    float* sB = sKf + 16 * P;
-#pragma unroll
-    for (int i = 0; i < 4; ++i)
-#pragma unroll
-      for (int j = 0; j < NJC; ++j) {
-        const int c = rm + 16 * i, ii = cn + TC * j;
-        sDL[c * PC + ii] = (ii < c) ? -dLr[i][j] : 0.f;
-        sDA[c * PC + ii] = (ii <= c) ? dAr[i][j] : 0.f;
-      }
+    float* sXq = sG + kC * P;        // [16][PF] q_c 2^(G_c - G_a), rows of tile R
+    float* sXk = sXq + 16 * PF;      // [16][PF] beta_c k_c 2^(G_c - G_a)
+    float* sKf = sXk + 16 * PF;      // [16][PF] k_i 2^(G_a - G_i), rows of key tile s
+    float* sB = sKf + 16 * PF;
     lds_load_in<DTQ, D, D, P, NTH>(sQ, a.q, cr.row0, cr.len, H, h, 0, a.scale);
     lds_load_in<DTQ, D, D, P, NTH>(sK, a.k, cr.row0, cr.len, H, h, 0, 1.f);
     lds_load<kC, D, P, NTH>(sG, GL, D, 0);
     if (t < kC) sB[t] = ld_b(t);
     __syncthreads();
-    for (int R = 0; R < 4; ++R) {
+    const bool mine = wv < NCT;
+    const int d = 16 * (wv % NCT) + r16;
+    // Row tiles in descending order: when tile R is finished (its diagonal and
+    // the read-modify-write of its rows), every row tile below it has already
+    // added its column-side terms to colS[R].
+    f4 colS[3];
+#pragma unroll
+    for (int q = 0; q < 3; ++q)
+#pragma unroll
+      for (int e = 0; e < 4; ++e) colS[q][e] = 0.f;
+    float dbq[4][4];
+#pragma unroll
+    for (int R = 3; R >= 0; --R) {
       const int a0 = 16 * R;
-      for (int e = t; e < 16 * D; e += NTH) {
-        const int rr = e / D, d = e - rr * D;
-        const float fr = ex2(sG[(a0 + rr) * P + d] - sG[a0 * P + d]);
-        sXq[rr * P + d] = sQ[(a0 + rr) * P + d] * fr;
-        sXk[rr * P + d] = sK[(a0 + rr) * P + d] * sB[a0 + rr] * fr;
-      }
-      float drA[NJ], drK[NJ];   // row c = a0 + rm: factorised part (times 2^(G_c - G_a) at the end)
-#pragma unroll
-      for (int j = 0; j < NJ; ++j) drA[j] = drK[j] = 0.f;
-      const int c = a0 + rm;
-      for (int s = 0; s < R; ++s) {
-        __syncthreads();
+      f4 accA = {0.f, 0.f, 0.f, 0.f}, accK = {0.f, 0.f, 0.f, 0.f};
+      if (R > 0) {
         for (int e = t; e < 16 * D; e += NTH) {
-          const int ii = e / D, d = e - ii * D;
-          sKf[ii * P + d] = sK[(16 * s + ii) * P + d] * ex2(sG[a0 * P + d] - sG[(16 * s + ii) * P + d]);
+          const int rr = e / D, dd = e - rr * D;
+          const float fr = ex2(sG[(a0 + rr) * P + dd] - sG[a0 * P + dd]);
+          sXq[rr * PF + dd] = sQ[(a0 + rr) * P + dd] * fr;
+          sXk[rr * PF + dd] = sK[(a0 + rr) * P + dd] * sB[a0 + rr] * fr;
+        }
+      }
+#pragma unroll
+      for (int sk = 0; sk < R; ++sk) {
+        for (int e = t; e < 16 * D; e += NTH) {
+          const int ii = e / D, dd = e - ii * D;
+          sKf[ii * PF + dd] = sK[(16 * sk + ii) * P + dd] * ex2(sG[a0 * P + dd] - sG[(16 * sk + ii) * P + dd]);
         }
         __syncthreads();
-        // row side: dr[c] += sum_{i in s} D[c][i] k_i 2^(G_a - G_i)
-        #pragma unroll 4
-        for (int ii = 0; ii < 16; ++ii) {
-          const float da = sDA[c * PC + 16 * s + ii], dl = sDL[c * PC + 16 * s + ii];
+        if (mine) {
+          f4 cS = {0.f, 0.f, 0.f, 0.f};
 #pragma unroll
-          for (int j = 0; j < NJ; ++j) {
-            const float kf = sKf[ii * P + cn + TC * j];
-            drA[j] = fmaf(da, kf, drA[j]);
-            drK[j] = fmaf(dl, kf, drK[j]);
+          for (int k = 0; k < 4; ++k) {
+            const int kr = (4 * k + gq) * PF + 16 * wv + r16;
+            const float kb = sKf[kr];
+            accA = mfma4(sDA[(a0 + r16) * PC + 16 * sk + 4 * k + gq], kb, accA);
+            accK = mfma4(sDL[(a0 + r16) * PC + 16 * sk + 4 * k + gq], kb, accK);
+            cS = mfma4(sDA[(a0 + 4 * k + gq) * PC + 16 * sk + r16], sXq[kr], cS);
+            cS = mfma4(sDL[(a0 + 4 * k + gq) * PC + 16 * sk + r16], sXk[kr], cS);
           }
+#pragma unroll
+          for (int e = 0; e < 4; ++e)
+            colS[sk][e] += cS[e] * ex2(sG[a0 * P + d] - sG[(16 * sk + 4 * gq + e) * P + d]);
         }
-        // column side for key row i = 16s + rm: sum_{c' in R} D[c'][i] x_c' 2^(G_c' - G_a), times 2^(G_a - G_i)
-        {
-          const int i = 16 * s + rm;
-          float dcA[NJ], dcK[NJ];
-#pragma unroll
-          for (int j = 0; j < NJ; ++j) dcA[j] = dcK[j] = 0.f;
-          #pragma unroll 4
-          for (int rr = 0; rr < 16; ++rr) {
-            const float da = sDA[(a0 + rr) * PC + i], dl = sDL[(a0 + rr) * PC + i];
-#pragma unroll
-            for (int j = 0; j < NJ; ++j) {
-              dcA[j] = fmaf(da, sXq[rr * P + cn + TC * j], dcA[j]);
-              dcK[j] = fmaf(dl, sXk[rr * P + cn + TC * j], dcK[j]);
-            }
-          }
-          if (i < cr.len) {
-            float ok[NJ], oG[NJ];
-#pragma unroll
-            for (int j = 0; j < NJ; ++j) {
-              ok[j] = gk_[in_idx(i, cn + TC * j)];
-              oG[j] = gG_[in_idx(i, cn + TC * j)];
-            }
-#pragma unroll
-            for (int j = 0; j < NJ; ++j) {
-              const int d = cn + TC * j;
-              const float fk = ex2(sG[a0 * P + d] - sG[i * P + d]);
-              const float sum = (dcA[j] + dcK[j]) * fk;
-              gk_[in_idx(i, d)] = ok[j] + sum;
-              gG_[in_idx(i, d)] = oG[j] - sum * sK[i * P + d];
-            }
-          }
-        }
+        __syncthreads();   // sKf, and after the last key tile sXq / sXk, free again
       }
-      // diagonal tile and the row-side totals
-      {
-        const int i = a0 + rm;   // the same row, as a key row of the diagonal tile
-        float dbsum = 0.f;
-        float oq[NJ], oG[NJ], ok[NJ];
+      if (mine) {
+        float gd[16], kd[16], qd[16];
 #pragma unroll
-        for (int j = 0; j < NJ; ++j) {
-          const bool live = c < cr.len;
-          oq[j] = live ? gq_[in_idx(c, cn + TC * j)] : 0.f;
-          oG[j] = live ? gG_[in_idx(c, cn + TC * j)] : 0.f;
-          ok[j] = live ? gk_[in_idx(c, cn + TC * j)] : 0.f;
+        for (int y = 0; y < 16; ++y) {
+          gd[y] = sG[(a0 + y) * P + d];
+          kd[y] = sK[(a0 + y) * P + d];
+          qd[y] = sQ[(a0 + y) * P + d];
         }
 #pragma unroll
-        for (int j = 0; j < NJ; ++j) {
-          const int d = cn + TC * j;
-          const float gc = sG[c * P + d];
-          float rA = drA[j] * ex2(gc - sG[a0 * P + d]);
-          float rK = drK[j] * ex2(gc - sG[a0 * P + d]);
-          float cA = 0.f, cK = 0.f;
-          for (int ii = 0; ii <= rm; ++ii) {
-            const int ik = a0 + ii;
-            const float e = ex2(gc - sG[ik * P + d]);
-            const float ke = sK[ik * P + d] * e;
-            rA = fmaf(sDA[c * PC + ik], ke, rA);
-            rK = fmaf(sDL[c * PC + ik], ke, rK);
+        for (int e = 0; e < 4; ++e) {
+          const int c = a0 + 4 * gq + e;
+          const float gc = sG[c * P + d], kc = sK[c * P + d], qc = sQ[c * P + d], bc = sB[c];
+          float rA = 0.f, rK = 0.f, cS = 0.f;
+#pragma unroll
+          for (int y = 0; y < 16; ++y) {
+            const float er = ex2(fminf(gc - gd[y], 0.f));   // row side pair (c, a0 + y)
+            const float ec = ex2(fminf(gd[y] - gc, 0.f));   // col side pair (a0 + y, c)
+            const float kr = kd[y] * er;
+            rA = fmaf(sDA[c * PC + a0 + y], kr, rA);
+            rK = fmaf(sDL[c * PC + a0 + y], kr, rK);
+            cS = fmaf(sDA[(a0 + y) * PC + c], qd[y] * ec, cS);
+            cS = fmaf(sDL[(a0 + y) * PC + c], sB[a0 + y] * kd[y] * ec, cS);
           }
-          const float gi = sG[i * P + d];
-          for (int rr = rm; rr < 16; ++rr) {
-            const int cc = a0 + rr;
-            const float e = ex2(sG[cc * P + d] - gi);
-            cA = fmaf(sDA[cc * PC + i], sQ[cc * P + d] * e, cA);
-            cK = fmaf(sDL[cc * PC + i], sK[cc * P + d] * sB[cc] * e, cK);
+          if (R > 0) {
+            const float f = ex2(sG[c * P + d] - sG[a0 * P + d]);
+            rA = fmaf(accA[e], f, rA);
+            rK = fmaf(accK[e], f, rK);
           }
-          const float qv = sQ[c * P + d], kv = sK[c * P + d], bc = sB[c];
-          dbsum += rK * kv;
+          if (R < 3) cS += colS[R < 3 ? R : 0][e];
+          dbq[R][e] = rK * kc;
           if (c < cr.len) {
-            gq_[in_idx(c, d)] = oq[j] + rA * a.scale;
-            gG_[in_idx(c, d)] = oG[j] + rA * qv + rK * kv * bc - (cA + cK) * kv;
-            gk_[in_idx(c, d)] = ok[j] + rK * bc + cA + cK;
+            const int64_t o = in_idx(c, d);
+            const float oq = gq_[o], oG = gG_[o], ok = gk_[o];
+            gq_[o] = oq + rA * a.scale;
+            gG_[o] = oG + rA * qc + rK * kc * bc - cS * kc;
+            gk_[o] = ok + rK * bc + cS;
           }
         }
-        // dbr is indexed by the row tile: R is a runtime loop here, so add
-        // through the per-row LDS reduction below instead of a register array
-        dbr[0] += (R == 0) ? dbsum : 0.f;
-        dbr[1] += (R == 1) ? dbsum : 0.f;
-        dbr[2] += (R == 2) ? dbsum : 0.f;
-        dbr[3] += (R == 3) ? dbsum : 0.f;
       }
-      __syncthreads();
+      asm volatile("" ::: "memory");   // keep each row tile's loads inside its iteration
+    }
+    if (mine) {
+      // dbeta partials: sum over the 16 columns of this wave's tile
+#pragma unroll
+      for (int R = 0; R < 4; ++R)
+#pragma unroll
+        for (int e = 0; e < 4; ++e) {
+          float v = dbq[R][e];
+#pragma unroll
+          for (int off = 8; off >= 1; off >>= 1) v += __shfl_xor(v, off, 64);
+          dbq[R][e] = v;
+        }
+    }
+    __syncthreads();   // phase 4's LDS reads done; every position written
+    sDb4 = sm + kC * P + 16 * D + kC * 32;   // outputs' layout (below)
+    if (mine && r16 == 0) {
+#pragma unroll
+      for (int R = 0; R < 4; ++R)
+#pragma unroll
+        for (int e = 0; e < 4; ++e) sDb4[(16 * R + 4 * gq + e) * 8 + wv] = dbq[R][e];
     }
   }
 
   // ---- outputs: dbeta, dg (reverse cumsum of dG plus the G_C terms)
   {
     float* sDG = sm;                   // [64][P]
-    float* sRed = sDG + kC * P;        // [16][D] column partial sums of dz
-    float* sDb = sRed + 16 * D;        // [64][TC] row partial sums of dbeta
+    float* sRed = sDG + kC * P;        // [16][D] column partial sums of dz (slot 4 mt + gq)
+    float* sDbD = sRed + 16 * D;       // [64][32] row partial sums of dbeta (phase 2)
+    // sDb4 = sDbD + 64 * 32: [64][8] row partial sums of dbeta (phase 4), written above
 #pragma unroll
     for (int i = 0; i < 4; ++i) {
       const int c = rm + 16 * i;
@@ -950,10 +954,10 @@ __global__ __launch_bounds__(kChunkThreads) void kda_bwd_chunk_kernel(BwdArgs a)
         const int d = cn + TC * j;
         sDG[c * P + d] = (c < cr.len) ? gG_[in_idx(c, d)] : 0.f;
       }
-      sDb[c * TC + cn] = dbr[i];
+      sDbD[(16 * mt + 4 * gq + i) * 32 + 16 * dg_ + r16] = dbrD[i];
     }
 #pragma unroll
-    for (int j = 0; j < NJ; ++j) sRed[rm * D + cn + TC * j] = dzp[j];
+    for (int q = 0; q < NDT; ++q) sRed[(4 * mt + gq) * D + 16 * (dg_ * NDT + q) + r16] = dzp[q];
     __syncthreads();
     if (t < D) {
       float acc = dgc * ex2(GL[(kC - 1) * D + t]);
@@ -965,7 +969,8 @@ __global__ __launch_bounds__(kChunkThreads) void kda_bwd_chunk_kernel(BwdArgs a)
     }
     if (t < kC && t < cr.len) {
       float acc = 0.f;
-      for (int j = 0; j < TC; ++j) acc += sDb[t * TC + j];
+      for (int j = 0; j < NCT; ++j) acc += sDb4[t * 8 + j];
+      for (int j = 0; j < 32; ++j) acc += sDbD[t * 32 + j];
       a.dbeta[(cr.row0 + t) * H + h] = acc;
     }
   }
