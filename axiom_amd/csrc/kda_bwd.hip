@@ -179,17 +179,21 @@ __device__ __forceinline__ void lds_load_in(float* dst, const void* src, int64_t
 // ---------------------------------------------------------------------------
 // prep: G, gamma*q, lambda*k, gamma_C, Aqk, T, W, U of one chunk-head
 // ---------------------------------------------------------------------------
+__device__ __forceinline__ f4 mfma4(float a, float b, f4 c) {
+  return __builtin_amdgcn_mfma_f32_16x16x4f32(a, b, c, 0, 0, 0);
+}
+
 template <int D, int DTQ, int DTG>
 __global__ __launch_bounds__(kPrepThreads) void kda_bwd_prep_kernel(BwdArgs a) {
-  typedef BwdDims<D> BD;
-  constexpr int P = BD::P, PC = BD::PC;
+  constexpr int P = D + 2;            // [64][D] pitch: row fragments conflict-free
+  constexpr int PC = kC + 1;
   __shared__ float sQ[kC * P], sK[kC * P], sG[kC * P];
   __shared__ float sL[kC * PC], sT[kC * PC];
-  __shared__ float sX0[16 * P], sX1[16 * P], sKf[16 * P];
+  __shared__ float sTmp[768];         // the triangular inversion's scratch
   __shared__ float sB[kC];
-  __shared__ float sRed[2 * 256];   // the second half's partial sums of a tile pair
   constexpr int NTH = kPrepThreads;
   const int t = threadIdx.x;
+  const int wv = t >> 6, l = t & 63, r16 = l & 15, gq = l >> 4;
   const int H = a.H;
   const int u = blockIdx.x / H, h = blockIdx.x - u * H;
   const ChunkRows cr = chunk_rows(a, u);
@@ -228,74 +232,64 @@ __global__ __launch_bounds__(kPrepThreads) void kda_bwd_prep_kernel(BwdArgs a) {
     if (t < D) a.GCV[ch * D + t] = ex2(sG[(kC - 1) * P + t]);
   }
 
-  // scores: Aqk (c >= i) straight to the workspace, L = beta_c Akk (c > i) to LDS
+  // scores: Aqk (c >= i) to the workspace, L = beta_c Akk (c > i) to LDS.
+  // Off-diagonal tile pairs (row tile R > key tile s) on the matrix cores,
+  // one pair per wave (waves 0..5), the decay factored at the row tile's
+  // first row a: 2^(G_c - G_i) = 2^(G_c - G_a) 2^(G_a - G_i), both <= 1,
+  // applied to each operand element as it is read.  Diagonal tiles take
+  // 2^(G_c - G_i) per element, (c, i) slots spread over all threads.
   float* AQ = a.AQ + ch * kC * kC;
-  // output (r, i16) of a 16 x 16 tile pair; the two halves of the workgroup
-  // sum over the two halves of the channels and add up through sRed
-  const int t2 = t & 255, half = t >> 8;
-  const int r = t2 >> 4, i16 = t2 & 15;
-  const int d0 = half * (D / 2);
-  for (int R = 0; R < 4; ++R) {
-    const int a0 = 16 * R;
-    // row operands of tile R with the factor 2^(G_c - G_a)
-    for (int e = t; e < 16 * D; e += NTH) {
-      const int rr = e / D, d = e - rr * D;
-      const float fr = ex2(sG[(a0 + rr) * P + d] - sG[a0 * P + d]);
-      sX0[rr * P + d] = sQ[(a0 + rr) * P + d] * fr;
-      sX1[rr * P + d] = sK[(a0 + rr) * P + d] * sB[a0 + rr] * fr;
+  if (wv < 6) {
+    const int R = (wv < 1) ? 1 : (wv < 3) ? 2 : 3;
+    const int sk = wv - R * (R - 1) / 2;
+    const int a0 = 16 * R, i = 16 * sk + r16;
+    f4 accA = {0.f, 0.f, 0.f, 0.f}, accL = {0.f, 0.f, 0.f, 0.f};
+#pragma unroll 8
+    for (int k = 0; k < D / 4; ++k) {
+      const int d = 4 * k + gq;
+      const float ga = sG[a0 * P + d];
+      const float fa = ex2(sG[(a0 + r16) * P + d] - ga);
+      const float bk = sK[i * P + d] * ex2(ga - sG[i * P + d]);
+      accA = mfma4(sQ[(a0 + r16) * P + d] * fa, bk, accA);
+      accL = mfma4(sK[(a0 + r16) * P + d] * fa, bk, accL);
     }
-    for (int s = 0; s < R; ++s) {
-      __syncthreads();  // sX0/sX1 written; previous sKf readers done
-      for (int e = t; e < 16 * D; e += NTH) {
-        const int ii = e / D, d = e - ii * D;
-        sKf[ii * P + d] = sK[(16 * s + ii) * P + d] * ex2(sG[a0 * P + d] - sG[(16 * s + ii) * P + d]);
-      }
-      __syncthreads();
-      float accA = 0.f, accL = 0.f;
-      #pragma unroll 4
-      for (int d = d0; d < d0 + D / 2; ++d) {
-        const float kf = sKf[i16 * P + d];
-        accA = fmaf(sX0[r * P + d], kf, accA);
-        accL = fmaf(sX1[r * P + d], kf, accL);
-      }
-      if (half) { sRed[t2] = accA; sRed[256 + t2] = accL; }
-      __syncthreads();
-      if (!half) {
-        AQ[(a0 + r) * kC + 16 * s + i16] = accA + sRed[t2];
-        sL[(a0 + r) * PC + 16 * s + i16] = accL + sRed[256 + t2];
-      }
+#pragma unroll
+    for (int e = 0; e < 4; ++e) {
+      const int c = a0 + 4 * gq + e;
+      AQ[c * kC + i] = accA[e];
+      sL[c * PC + i] = accL[e] * sB[c];
     }
-    // diagonal tile, 2^(G_c - G_i) directly
-    {
-      const int c = a0 + r, i = a0 + i16;
-      float accA = 0.f, accL = 0.f;
-      if (i16 <= r) {
-        #pragma unroll 4
-        for (int d = d0; d < d0 + D / 2; ++d) {
-          const float e = ex2(sG[c * P + d] - sG[i * P + d]);
-          const float ki = sK[i * P + d] * e;
-          accA = fmaf(sQ[c * P + d], ki, accA);
-          accL = fmaf(sK[c * P + d], ki, accL);
-        }
-      }
-      __syncthreads();   // the off-diagonal sums have been read out of sRed
-      if (half) { sRed[t2] = accA; sRed[256 + t2] = accL; }
-      __syncthreads();
-      if (!half) {
-        AQ[c * kC + i] = accA + sRed[t2];
-        sL[c * PC + i] = (i16 < r) ? (accL + sRed[256 + t2]) * sB[c] : 0.f;
-        // upper triangle of the row band: zero
-        for (int s = R + 1; s < 4; ++s) {
-          AQ[c * kC + 16 * s + i16] = 0.f;
-          sL[c * PC + 16 * s + i16] = 0.f;
-        }
-      }
-    }
-    __syncthreads();  // sX0/sX1 reused by the next row tile
   }
+#pragma unroll
+  for (int j = 0; j < 2; ++j) {
+    const int p = t + NTH * j;                 // 4 diagonal tiles x 256 slots
+    const int R = p >> 8, rc = (p >> 4) & 15, ri = p & 15;
+    const int c = 16 * R + rc, i = 16 * R + ri;
+    float accA = 0.f, accL = 0.f;
+    if (ri <= rc) {
+#pragma unroll 4
+      for (int d = 0; d < D; ++d) {
+        const float ki = sK[i * P + d] * ex2(sG[c * P + d] - sG[i * P + d]);
+        accA = fmaf(sQ[c * P + d], ki, accA);
+        accL = fmaf(sK[c * P + d], ki, accL);
+      }
+    }
+    AQ[c * kC + i] = accA;
+    sL[c * PC + i] = (ri < rc) ? accL * sB[c] : 0.f;
+  }
+  // blocks above the diagonal: zero
+  for (int e = t; e < 6 * 256; e += NTH) {
+    const int blk = e >> 8, rc = (e >> 4) & 15, ri = e & 15;
+    const int R = (blk < 3) ? 0 : (blk < 5) ? 1 : 2;             // (0,1) (0,2) (0,3) (1,2) (1,3) (2,3)
+    const int sk = (blk < 3) ? blk + 1 : (blk < 5) ? blk - 1 : 3;
+    const int c = 16 * R + rc, i = 16 * sk + ri;
+    AQ[c * kC + i] = 0.f;
+    sL[c * PC + i] = 0.f;
+  }
+  __syncthreads();
 
   // T = (I + L)^-1
-  invert_unit_lower64<PC, NTH>(sL, sT, sX0);
+  invert_unit_lower64<PC, NTH>(sL, sT, sTmp);
   {
     float* TM = a.TM + ch * kC * kC;
     for (int e = t; e < kC * kC; e += NTH) {
@@ -303,7 +297,8 @@ __global__ __launch_bounds__(kPrepThreads) void kda_bwd_prep_kernel(BwdArgs a) {
       TM[e] = sT[c * PC + i];
     }
   }
-  // W = T (beta gamma k), U = T (beta v)
+  // W = T (beta gamma k), U = T (beta v) on the matrix cores: wave wv owns
+  // row tile wv / 2 and column tiles (wv % 2) D/32 + q
   lds_load_in<DTQ, D, D, P, NTH>(sQ, a.v, cr.row0, cr.len, H, h, 0, 1.f);
   __syncthreads();
   for (int e = t; e < kC * D; e += NTH) {
@@ -313,37 +308,32 @@ __global__ __launch_bounds__(kPrepThreads) void kda_bwd_prep_kernel(BwdArgs a) {
   }
   __syncthreads();
   {
-    constexpr int TC = NTH / 16;
-    constexpr int NJ = D / TC;
-    const int rm = t / TC, cn = t % TC;
-    float accW[4][NJ], accU[4][NJ];
+    constexpr int NDT = D / 32;
+    const int mt = wv >> 1, dg = wv & 1;
+    f4 accW[NDT], accU[NDT];
 #pragma unroll
-    for (int i = 0; i < 4; ++i)
+    for (int q = 0; q < NDT; ++q)
 #pragma unroll
-      for (int j = 0; j < NJ; ++j) accW[i][j] = accU[i][j] = 0.f;
-    #pragma unroll 4
-    for (int m = 0; m < kC; ++m) {
-      float tv[4];
+      for (int e = 0; e < 4; ++e) accW[q][e] = accU[q][e] = 0.f;
+#pragma unroll 4
+    for (int k = 0; k < kC / 4; ++k) {
+      const float at = sT[(16 * mt + r16) * PC + 4 * k + gq];
 #pragma unroll
-      for (int i = 0; i < 4; ++i) tv[i] = sT[(rm + 16 * i) * PC + m];
-#pragma unroll
-      for (int j = 0; j < NJ; ++j) {
-        const float x = sK[m * P + cn + TC * j], y = sQ[m * P + cn + TC * j];
-#pragma unroll
-        for (int i = 0; i < 4; ++i) {
-          accW[i][j] = fmaf(tv[i], x, accW[i][j]);
-          accU[i][j] = fmaf(tv[i], y, accU[i][j]);
-        }
+      for (int q = 0; q < NDT; ++q) {
+        const int kb = (4 * k + gq) * P + 16 * (dg * NDT + q) + r16;
+        accW[q] = mfma4(at, sK[kb], accW[q]);
+        accU[q] = mfma4(at, sQ[kb], accU[q]);
       }
     }
     float* WM = a.WM + ch * kC * D;
     float* UM = a.UM + ch * kC * D;
 #pragma unroll
-    for (int i = 0; i < 4; ++i)
+    for (int q = 0; q < NDT; ++q)
 #pragma unroll
-      for (int j = 0; j < NJ; ++j) {
-        WM[(rm + 16 * i) * D + cn + TC * j] = accW[i][j];
-        UM[(rm + 16 * i) * D + cn + TC * j] = accU[i][j];
+      for (int e = 0; e < 4; ++e) {
+        const int o = (16 * mt + 4 * gq + e) * D + 16 * (dg * NDT + q) + r16;
+        WM[o] = accW[q][e];
+        UM[o] = accU[q][e];
       }
   }
 }
@@ -360,10 +350,6 @@ __global__ __launch_bounds__(kPrepThreads) void kda_bwd_prep_kernel(BwdArgs a) {
 // ---------------------------------------------------------------------------
 constexpr int kPB = 48;
 constexpr int kPA = kC + 16;
-
-__device__ __forceinline__ f4 mfma4(float a, float b, f4 c) {
-  return __builtin_amdgcn_mfma_f32_16x16x4f32(a, b, c, 0, 0, 0);
-}
 
 // forward state scan of one (chain, 32-column slice): S_in and v~ per chunk
 template <int D>
