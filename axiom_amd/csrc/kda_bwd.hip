@@ -176,6 +176,60 @@ __device__ __forceinline__ void lds_load_in(float* dst, const void* src, int64_t
   }
 }
 
+// lds_load_in split into its loads (fetch) and its LDS writes (put), so a
+// kernel can issue the loads of a later phase before this phase's arithmetic.
+template <int DT, int D, int COLS, int NTH>
+struct InTile {
+  static constexpr int V = COLS / 8;
+  static constexpr int N = kC * V;
+  static constexpr int PER = (N + NTH - 1) / NTH;
+  static_assert(COLS % 8 == 0, "8-element loads");
+  uint4 w[DT == 0 ? 2 * PER : PER];
+  __device__ __forceinline__ void fetch(const void* src, int64_t row0, int len, int H, int h, int col0) {
+#pragma unroll
+    for (int p = 0; p < PER; ++p) {
+      const int e = threadIdx.x + p * NTH;
+      const int r = e / V, c8 = e - r * V;
+      const bool ok = (N % NTH == 0 || e < N) && r < len;
+      const int64_t i = ((row0 + (ok ? r : 0)) * H + h) * D + col0 + 8 * c8;
+      // the address is valid for every thread (row 0 when masked): load
+      // unconditionally, then zero, so no load sits inside a branch
+      const uint4 z = make_uint4(0, 0, 0, 0);
+      if constexpr (DT == 0) {
+        const uint4* q = reinterpret_cast<const uint4*>(static_cast<const float*>(src) + i);
+        const uint4 v0 = q[0], v1 = q[1];
+        w[2 * p] = ok ? v0 : z;
+        w[2 * p + 1] = ok ? v1 : z;
+      } else {
+        const uint4 v = *reinterpret_cast<const uint4*>(static_cast<const u16*>(src) + i);
+        w[p] = ok ? v : z;
+      }
+    }
+  }
+  template <int PITCH>
+  __device__ __forceinline__ void put(float* dst, float mul) const {
+#pragma unroll
+    for (int p = 0; p < PER; ++p) {
+      const int e = threadIdx.x + p * NTH;
+      if (N % NTH == 0 || e < N) {
+        const int r = e / V, c8 = e - r * V;
+        float x[8];
+        if constexpr (DT == 0) {
+          const uint4 a = w[2 * p], b = w[2 * p + 1];
+          x[0] = __uint_as_float(a.x); x[1] = __uint_as_float(a.y); x[2] = __uint_as_float(a.z); x[3] = __uint_as_float(a.w);
+          x[4] = __uint_as_float(b.x); x[5] = __uint_as_float(b.y); x[6] = __uint_as_float(b.z); x[7] = __uint_as_float(b.w);
+        } else {
+          const f4 lo = unpack4<DT>(make_uint2(w[p].x, w[p].y)), hi = unpack4<DT>(make_uint2(w[p].z, w[p].w));
+#pragma unroll
+          for (int q = 0; q < 4; ++q) { x[q] = lo[q]; x[4 + q] = hi[q]; }
+        }
+#pragma unroll
+        for (int q = 0; q < 8; ++q) dst[r * PITCH + 8 * c8 + q] = x[q] * mul;
+      }
+    }
+  }
+};
+
 // ---------------------------------------------------------------------------
 // prep: G, gamma*q, lambda*k, gamma_C, Aqk, T, W, U of one chunk-head
 // ---------------------------------------------------------------------------
@@ -601,6 +655,8 @@ __global__ __launch_bounds__(kChunkThreads) void kda_bwd_chunk_kernel(BwdArgs a)
 
   // ---- phase 1: dY = v~ dS'^T, dgq = do S^T, dW = -dv~ S^T (K = dv in passes of HW)
   f4 dW[NDT];
+  Tile<kC, kC, NTH> tT;      // phase 2's T and dv~, loaded during phase 1's last pass
+  Tile<kC, D, NTH> tY;
   {
     f4 dY[NDT], dgq[NDT];
 #pragma unroll
@@ -612,14 +668,30 @@ __global__ __launch_bounds__(kChunkThreads) void kda_bwd_chunk_kernel(BwdArgs a)
     float* sDv = sDo + kC * PH;
     float* sS = sDv + kC * PH;
     float* sDS = sS + D * PH;
+    // a pass's operands are loaded during the previous pass's products
+    Tile<kC, HW, NTH> pV, pDv;
+    Tile<D, HW, NTH> pS, pDS;
+    InTile<DO, D, HW, NTH> pDo;
+    auto fetch_pass = [&](int n0) {
+      pV.fetch(a.VT + ch * kC * D, D, n0);
+      pDv.fetch(a.DVT + ch * kC * D, D, n0);
+      pS.fetch(a.SI + ch * D * D, D, n0);
+      pDS.fetch(a.DS + ch * D * D, D, n0);
+      pDo.fetch(a.dout, cr.row0, cr.len, H, h, n0);
+    };
+    fetch_pass(0);
     for (int hp = 0; hp < NH; ++hp) {
-      const int n0 = HW * hp;
-      lds_load<kC, HW, PH, NTH>(sVt, a.VT + ch * kC * D, D, n0);
-      lds_load<kC, HW, PH, NTH>(sDv, a.DVT + ch * kC * D, D, n0);
-      lds_load<D, HW, PH, NTH>(sS, a.SI + ch * D * D, D, n0);
-      lds_load<D, HW, PH, NTH>(sDS, a.DS + ch * D * D, D, n0);
-      lds_load_in<DO, D, HW, PH, NTH>(sDo, a.dout, cr.row0, cr.len, H, h, n0, 1.f);
+      pV.template put<PH>(sVt);
+      pDv.template put<PH>(sDv);
+      pS.template put<PH>(sS);
+      pDS.template put<PH>(sDS);
+      pDo.template put<PH>(sDo, 1.f);
       __syncthreads();
+      if (hp + 1 < NH) fetch_pass(HW * (hp + 1));
+      else {   // phase 2's operands
+        tT.fetch(a.TM + ch * kC * kC, kC, 0);
+        tY.fetch(a.DVT + ch * kC * D, D, 0);
+      }
 #pragma unroll 4
       for (int k = 0; k < HW / 4; ++k) {
         const int ka = (16 * mt + r16) * PH + 4 * k + gq;
@@ -670,6 +742,7 @@ __global__ __launch_bounds__(kChunkThreads) void kda_bwd_chunk_kernel(BwdArgs a)
 
   // ---- phase 2: Yw = T^T dW, Yu = T^T dv~ (K = the chunk's 64 rows)
   f4 Yw[NDT], Yu[NDT];
+  Tile<kC, D, NTH> tW3, tU3;
   {
     float* sT = sm;
     float* sX = sT + kC * PT;
@@ -678,9 +751,11 @@ __global__ __launch_bounds__(kChunkThreads) void kda_bwd_chunk_kernel(BwdArgs a)
     for (int q = 0; q < NDT; ++q)
 #pragma unroll
       for (int i = 0; i < 4; ++i) sX[(16 * mt + 4 * gq + i) * PX + 16 * (dg_ * NDT + q) + r16] = dW[q][i];
-    lds_load<kC, kC, PT, NTH>(sT, a.TM + ch * kC * kC, kC, 0);
-    lds_load<kC, D, PX, NTH>(sY, a.DVT + ch * kC * D, D, 0);
+    tT.template put<PT>(sT);
+    tY.template put<PX>(sY);
     __syncthreads();
+    tW3.fetch(a.WM + ch * kC * D, D, 0);     // phase 3's operands, during the products
+    tU3.fetch(a.UM + ch * kC * D, D, 0);
 #pragma unroll
     for (int q = 0; q < NDT; ++q)
 #pragma unroll
@@ -746,8 +821,8 @@ __global__ __launch_bounds__(kChunkThreads) void kda_bwd_chunk_kernel(BwdArgs a)
         sA[o] = Yw[q][i];
         sB[o] = Yu[q][i];
       }
-    lds_load<kC, D, PR, NTH>(sW, a.WM + ch * kC * D, D, 0);
-    lds_load<kC, D, PR, NTH>(sU, a.UM + ch * kC * D, D, 0);
+    tW3.template put<PR>(sW);
+    tU3.template put<PR>(sU);
     __syncthreads();
     f4 dLa[2], dAa[2];
 #pragma unroll
@@ -797,8 +872,7 @@ __global__ __launch_bounds__(kChunkThreads) void kda_bwd_chunk_kernel(BwdArgs a)
   // factor the decay at the row tile's first row a, 2^(G_c - G_a) 2^(G_a - G_i),
   // both <= 1, and run on the matrix cores: (16 x 16 block) x (k_i 2^(G_a - G_i))
   // for the row side, (block)^T x (q_c 2^(G_c - G_a)) for the column side.
-  // Diagonal tiles take 2^(min(G_c - G_i, 0)) per element (the clamp only
-  // reaches pairs whose cotangent is zero).  Wave wv < D/16 owns column tile
+  // Diagonal tiles take 2^-|G_c - G_i| per element.  Wave wv < D/16 owns column tile
   // wv: lane (r, gq) rows 4 gq + e of every row tile, column 16 wv + r; each
   // position gets one read-modify-write.
   constexpr int NCT = D / 16;
@@ -876,15 +950,18 @@ __global__ __launch_bounds__(kChunkThreads) void kda_bwd_chunk_kernel(BwdArgs a)
           const int c = a0 + 4 * gq + e;
           const float gc = sG[c * P + d], kc = sK[c * P + d], qc = sQ[c * P + d], bc = sB[c];
           float rA = 0.f, rK = 0.f, cS = 0.f;
+          // With G non-increasing (g <= 0), the pair (c, a0 + y) of the row
+          // side (y <= x) decays by 2^(G_c - G_y) and the pair (a0 + y, c) of
+          // the column side (y >= x) by 2^(G_y - G_c): both are 2^-|G_c - G_y|,
+          // and the masked cotangents zero the side a given y does not belong to.
 #pragma unroll
           for (int y = 0; y < 16; ++y) {
-            const float er = ex2(fminf(gc - gd[y], 0.f));   // row side pair (c, a0 + y)
-            const float ec = ex2(fminf(gd[y] - gc, 0.f));   // col side pair (a0 + y, c)
-            const float kr = kd[y] * er;
+            const float ev = ex2(-fabsf(gc - gd[y]));
+            const float kr = kd[y] * ev;
             rA = fmaf(sDA[c * PC + a0 + y], kr, rA);
             rK = fmaf(sDL[c * PC + a0 + y], kr, rK);
-            cS = fmaf(sDA[(a0 + y) * PC + c], qd[y] * ec, cS);
-            cS = fmaf(sDL[(a0 + y) * PC + c], sB[a0 + y] * kd[y] * ec, cS);
+            cS = fmaf(sDA[(a0 + y) * PC + c], qd[y] * ev, cS);
+            cS = fmaf(sDL[(a0 + y) * PC + c], sB[a0 + y] * kr, cS);
           }
           if (R > 0) {
             const float f = ex2(sG[c * P + d] - sG[a0 * P + d]);
