@@ -808,6 +808,8 @@ __global__ __launch_bounds__(kChunkThreads) void kda_bwd_chunk_kernel(BwdArgs a)
   static_assert(4 * kC * PR <= SMEM_FLOATS, "phase 3 LDS");
   float* const sDL = sm;                 // phase 4's operands, written at the end of phase 3
   float* const sDA = sDL + kC * PC;
+  InTile<DTQ, D, D, NTH> tQ4, tK4;
+  Tile<kC, D, NTH> tG4;
   {
     float* sA = sm;                      // Yw, then do
     float* sB = sA + kC * PR;            // Yu, then v~
@@ -829,6 +831,10 @@ __global__ __launch_bounds__(kChunkThreads) void kda_bwd_chunk_kernel(BwdArgs a)
     for (int q = 0; q < 2; ++q)
 #pragma unroll
       for (int i = 0; i < 4; ++i) dLa[q][i] = dAa[q][i] = 0.f;
+    InTile<DO, D, D, NTH> tDo;            // do and v~ for dAqk, during the dL products
+    Tile<kC, D, NTH> tVt;
+    tDo.fetch(a.dout, cr.row0, cr.len, H, h, 0);
+    tVt.fetch(a.VT + ch * kC * D, D, 0);
 #pragma unroll 4
     for (int k = 0; k < D / 4; ++k) {
       const int ka = (16 * mt + r16) * PR + 4 * k + gq;
@@ -842,9 +848,12 @@ __global__ __launch_bounds__(kChunkThreads) void kda_bwd_chunk_kernel(BwdArgs a)
     }
     __syncthreads();
     // do and v~ into the Yw / Yu slots
-    lds_load_in<DO, D, D, PR, NTH>(sA, a.dout, cr.row0, cr.len, H, h, 0, 1.f);
-    lds_load<kC, D, PR, NTH>(sB, a.VT + ch * kC * D, D, 0);
+    tDo.template put<PR>(sA, 1.f);
+    tVt.template put<PR>(sB);
     __syncthreads();
+    tQ4.fetch(a.q, cr.row0, cr.len, H, h, 0);   // phase 4's q, k, G, during the dAqk products
+    tK4.fetch(a.k, cr.row0, cr.len, H, h, 0);
+    tG4.fetch(GL, D, 0);
 #pragma unroll 4
     for (int k = 0; k < D / 4; ++k) {
       const float ao = sA[(16 * mt + r16) * PR + 4 * k + gq];
@@ -885,9 +894,9 @@ __global__ __launch_bounds__(kChunkThreads) void kda_bwd_chunk_kernel(BwdArgs a)
     float* sXk = sXq + 16 * PF;      // [16][PF] beta_c k_c 2^(G_c - G_a)
     float* sKf = sXk + 16 * PF;      // [16][PF] k_i 2^(G_a - G_i), rows of key tile s
     float* sB = sKf + 16 * PF;
-    lds_load_in<DTQ, D, D, P, NTH>(sQ, a.q, cr.row0, cr.len, H, h, 0, a.scale);
-    lds_load_in<DTQ, D, D, P, NTH>(sK, a.k, cr.row0, cr.len, H, h, 0, 1.f);
-    lds_load<kC, D, P, NTH>(sG, GL, D, 0);
+    tQ4.template put<P>(sQ, a.scale);
+    tK4.template put<P>(sK, 1.f);
+    tG4.template put<P>(sG);
     if (t < kC) sB[t] = ld_b(t);
     __syncthreads();
     const bool mine = wv < NCT;
