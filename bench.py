@@ -283,6 +283,51 @@ def bench_ut_solve(args, device):
     return out
 
 
+def bench_other_configs(args, device):
+    """Forward at configs 2 (B1 T65536, 1 024 serial chunks per chain) and 3
+    (64 packed sequences of U[128, 8192] tokens, per-sequence h0): the
+    parity-test configurations, timed on request (``--other-configs``)."""
+    import axiom_amd
+    from axiom_amd import kda as kmod
+    from oracle import inputs as oin
+    stream = torch.cuda.current_stream(device)
+
+    def timed(f, n=10):
+        for _ in range(3):
+            f()
+        torch.cuda.synchronize()
+        e0, e1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+        e0.record(stream)
+        for _ in range(n):
+            f()
+        e1.record(stream)
+        torch.cuda.synchronize()
+        return e0.elapsed_time(e1) / 1e3 / n
+
+    out = {}
+    H, d = CFG["H"], CFG["dk"]
+    T2 = 65536
+    q, k, v, g, beta = make_inputs_gpu(1, T2, H, d, d, args.seed + 6, device)
+    ws = torch.empty(kmod.chunk_fwd_workspace_bytes(1, T2, H, d, d), dtype=torch.uint8, device=device)
+    t = timed(lambda: axiom_amd.kda_chunk_fwd(q, k, v, g, beta, workspace=ws))
+    nb = fwd_bytes(1, T2, H, d, d)
+    out["config2"] = dict(us_per_call=t * 1e6, tokens_per_s=T2 / t, hbm_frac=nb / t / 1e9 / HBM_PEAK_GBPS,
+                          workload="B1 T65536 H16 d128 bf16, fp32 o")
+    del q, k, v, g, beta, ws
+    lengths = oin.make_varlen_lengths(64, 128, 8192, seed=3)
+    cu = torch.from_numpy(oin.cu_seqlens_from_lengths(lengths)).to(device)
+    T3 = int(lengths.sum())
+    q, k, v, g, beta = make_inputs_gpu(1, T3, H, d, d, args.seed + 7, device)
+    h0 = torch.randn(len(lengths), H, d, d, device=device) * 0.02
+    ws = torch.empty(kmod.chunk_fwd_workspace_bytes(1, T3, H, d, d, n_seqs=len(lengths)), dtype=torch.uint8,
+                     device=device)
+    t = timed(lambda: axiom_amd.kda_chunk_fwd(q, k, v, g, beta, initial_state=h0, cu_seqlens=cu, workspace=ws))
+    nb = fwd_bytes(1, T3, H, d, d) + 2 * len(lengths) * H * d * d * 4 - H * d * d * 4
+    out["config3"] = dict(us_per_call=t * 1e6, tokens_per_s=T3 / t, hbm_frac=nb / t / 1e9 / HBM_PEAK_GBPS,
+                          workload=f"varlen 64 sequences U[128, 8192] (T={T3}) H16 d128 bf16, h0 and hT per sequence")
+    return out
+
+
 def cpu_baseline(fwd_inputs, seconds):
     """Oracle port (fp32, torch CPU) of the reference jax body on a bounded sample."""
     from oracle import kda_oracle as K
@@ -330,6 +375,8 @@ def main():
     ap.add_argument("--no-decode", action="store_true")
     ap.add_argument("--bwd-steps", type=int, default=5)
     ap.add_argument("--no-backward", action="store_true")
+    ap.add_argument("--other-configs", action="store_true",
+                    help="also time the forward at configs 2 and 3 (parity-test shapes)")
     args = ap.parse_args()
     if args.gpus != 1 or int(os.environ.get("WORLD_SIZE", "1")) != 1:
         print("bench.py measures one GPU only: every (batch, head) chain of this path is "
@@ -386,6 +433,8 @@ def main():
         line["backward"] = bench_backward(args, fwd["inputs"], device)
     line["layer"] = bench_layer(args, fwd["inputs"], device)
     line["ut_solve"] = bench_ut_solve(args, device)
+    if args.other_configs:
+        line["other_configs"] = bench_other_configs(args, device)
     if not args.no_cpu_baseline:
         line["cpu_baseline"] = cpu_baseline(fwd["inputs"], args.cpu_seconds)
     print(json.dumps(line), flush=True)
