@@ -18,9 +18,9 @@
 //   kda_bwd_chunk_kernel  one workgroup per chunk-head: the rest of the adjoint
 //                         (dY, dgq, dW, the two transposed solves, dL, dAqk, the
 //                         score adjoints, the cumsum adjoint) and the outputs.
-// Every matrix product is an LDS-tiled fp32 FMA loop (each of the 256 threads
-// owns rows r0 + 16i and columns c0 + 16j of the product); decay factors of
-// off-diagonal 16-row tiles are anchored at the row tile's first row
+// Every dense product runs on the fp32 matrix cores (v_mfma_f32_16x16x4f32:
+// exact fp32 products, fp32 sums), operands staged through LDS; decay factors
+// of off-diagonal 16-row tiles are anchored at the row tile's first row
 // (2^(G_c - G_a) * 2^(G_a - G_i), both <= 1), diagonal tiles use
 // 2^(G_c - G_i) directly.  Workspace arrays are fp32, row-major, per
 // chunk-head ch = (b * NT + n) * H + h.
@@ -631,10 +631,11 @@ __global__ __launch_bounds__(kChunkThreads) void kda_bwd_chunk_kernel(BwdArgs a)
   // matrix cores: wave wv owns row tile mt = wv / 2 and the NDT column tiles
   // dt = (wv % 2) NDT + q of every [64][D] product (lane (r, gq) holds rows
   // 16 mt + 4 gq + i, column 16 dt + r), so its read-modify-writes of phases
-  // 1 and 2 hit its own positions; phase 4 owns positions (rm + 16i, cn + TC j)
-  // and reads what other threads wrote, after the workgroup barriers between
-  // the phases.  Pad rows (c >= len) are never stored (their dG is zero: every
-  // term carries a factor q_c or k_c).
+  // 1 and 2 hit its own positions; phase 4 (wave wv owns column tile wv, lane
+  // rows 4 gq + e of every row tile) and the outputs (thread (rm, cn) owns rows
+  // rm + 16i, columns cn + TC j) read what other threads wrote, after the
+  // workgroup barriers between the phases.  Pad rows (c >= len) are never
+  // stored (their dG is zero: every term carries a factor q_c or k_c).
   float* const gq_ = a.dq;
   float* const gk_ = a.dk;
   float* const gG_ = a.dg;
