@@ -28,6 +28,9 @@ Also reported on the same JSON line:
 * ``layer``: the chunked layer forward ``kda_layer_fwd`` (short conv, swish
   and L2 norm fused into the intra kernel, the scan, the RMSNorm x sigmoid
   gate epilogue) on config-1 shapes with K = 4, bf16 projections and output;
+* ``decode_layer``: the layer decode step (prologue, recurrent step,
+  epilogue) per token, eager against a HIP graph of 64 tokens, at B=1 and
+  B=256;
 * ``ut_solve``: the standalone unit-triangular solve at the reference's case
   (H=12, C=64, N=dk+dv=256, fp32), both orientations, per call;
 * ``cpu_baseline``: the oracle's fp32 restatement of the reference jax body
@@ -203,6 +206,60 @@ def bench_backward(args, fwd_inputs, device):
                           "frac": gbps / HBM_PEAK_GBPS, "algorithmic_bytes_per_call": nbytes},
                 kernels="kda_bwd_prep + kda_bwd_fscan + kda_bwd_rscan + kda_bwd_chunk (fp32)",
                 config="B4 T4096 H16 d128 bf16 inputs, fp32 do and dht, zero h0")
+
+
+def bench_decode_layer(args, device):
+    """Layer decode steps (prologue, recurrent step, epilogue; conv buffers and
+    state in place) per token: eager launches against one HIP graph replaying
+    64 tokens, at B=1 (launch-bound serving) and B=256 (configs[4]'s batch)."""
+    import axiom_amd
+    H, d, K, steps = 16, 128, 4, 64
+    out = {}
+    stream = torch.cuda.current_stream(device)
+    for B in (1, 256):
+        gen = torch.Generator(device=device)
+        gen.manual_seed(args.seed + 8)
+        bf = torch.bfloat16
+        toks = [[torch.randn(B, H * d, device=device, generator=gen).to(bf) for _ in range(4)] for _ in range(steps)]
+        gs = [(-torch.nn.functional.softplus(torch.randn(B, H, d, device=device, generator=gen))).to(bf)
+              for _ in range(steps)]
+        bs = [torch.sigmoid(torch.randn(B, H, device=device, generator=gen)).to(bf) for _ in range(steps)]
+        ws_ = [torch.randn(K, H * d, device=device, generator=gen) * 0.4 for _ in range(3)]
+        state = torch.randn(B, H, d, d, device=device, generator=gen) * 0.02
+        bufs = [torch.zeros(B, K - 1, H * d, device=device) for _ in range(3)]
+
+        def run():
+            return [axiom_amd.kda_decode_layer_step(qp, kp, vp, gs[t], bs[t], gt, *ws_, bufs, state)
+                    for t, (qp, kp, vp, gt) in enumerate(toks)]
+
+        run()
+        torch.cuda.synchronize()
+        e0, e1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+        e0.record(stream)
+        run()
+        e1.record(stream)
+        torch.cuda.synchronize()
+        t_eager = e0.elapsed_time(e1) / 1e3 / steps
+        side = torch.cuda.Stream()
+        side.wait_stream(stream)
+        with torch.cuda.stream(side):
+            run()
+        stream.wait_stream(side)
+        torch.cuda.synchronize()
+        graph = torch.cuda.CUDAGraph()
+        with torch.cuda.graph(graph):
+            run()
+        graph.replay()
+        torch.cuda.synchronize()
+        e0.record(stream)
+        for _ in range(5):
+            graph.replay()
+        e1.record(stream)
+        torch.cuda.synchronize()
+        t_graph = e0.elapsed_time(e1) / 1e3 / (5 * steps)
+        out[f"B{B}"] = dict(us_per_token_eager=t_eager * 1e6, us_per_token_graph=t_graph * 1e6)
+    out["config"] = "H16 d128 K4 bf16, 64 tokens per graph"
+    return out
 
 
 def layer_bytes(B, T, H, d, K):
@@ -432,6 +489,7 @@ def main():
     if not args.no_backward:
         line["backward"] = bench_backward(args, fwd["inputs"], device)
     line["layer"] = bench_layer(args, fwd["inputs"], device)
+    line["decode_layer"] = bench_decode_layer(args, device)
     line["ut_solve"] = bench_ut_solve(args, device)
     if args.other_configs:
         line["other_configs"] = bench_other_configs(args, device)
