@@ -47,7 +47,7 @@ __device__ __forceinline__ float wave_sum(float x) {
   return x;
 }
 
-constexpr int kProRows = 16;   // rows of one (tensor, b, h) per wavefront
+constexpr int kProRows = 16;   // rows of one (tensor, b, h) per wavefront (T >= 16)
 
 template <int DI, int PL>
 __device__ __forceinline__ void pl_ld_pl(const void* p, int64_t i, float (&o)[PL]) {
@@ -70,12 +70,17 @@ __device__ __forceinline__ void pl_ld_pl(const void* p, int64_t i, float (&o)[PL
   }
 }
 
-// One wavefront per 16 consecutive rows of one (tensor, b, h): the rows and
-// the KW-1 before them are loaded once (16 + KW - 1 row loads, all in flight
-// together), the K taps run over them in registers, and the 16 row norms are
-// one wave_rowsums16.  Lane l holds channels PL*l .. PL*l + PL-1 of the head.
-template <int DI, int DO, int D, int KW>
+// One wavefront per RW consecutive rows of one (tensor, b, h): the rows and
+// the KW-1 before them are loaded once (RW + KW - 1 row loads, all in flight
+// together), the K taps run over them in registers, and the row norms are one
+// wave_rowsums16 (RW = 16) or one xor-butterfly (RW = 1; the same sums bit for
+// bit).  Lane l holds channels PL*l .. PL*l + PL-1 of the head.  BUF (T == 1,
+// one wavefront per (tensor, b, h)): the wavefront also writes the new conv
+// buffer of its channels -- the old rows 1..K-2 and x -- after reading the old
+// one, so in-place buffers need no second launch.
+template <int DI, int DO, int D, int KW, int RW, bool BUF>
 __global__ __launch_bounds__(64 * kRowsPerBlock) void kda_prologue_kernel(PrologueArgs a) {
+  constexpr int kProRows = RW;
   constexpr int PL = D / 64;   // channels per lane
   const int lane = threadIdx.x & 63;
   const int nblk = (a.T + kProRows - 1) / kProRows;
@@ -105,18 +110,17 @@ __global__ __launch_bounds__(64 * kRowsPerBlock) void kda_prologue_kernel(Prolog
   // xs[j] = input row t0 - (KW-1) + j; rows before the sequence from the
   // buffer (or zero), rows past its end re-read the last row (never stored)
   float xs[KW - 1 + kProRows][PL];
-  if (t0 == 0) {
 #pragma unroll
-    for (int j = 0; j < KW - 1; ++j) {
-      const int br = a.K - 1 + j - (KW - 1);      // buffer row (oldest first)
+  for (int j = 0; j < KW - 1; ++j) {
+    const int tr = t0 - (KW - 1) + j;                // uniform per wavefront
+    if (tr >= 0) {
+      pl_ld_pl<DI, PL>(x, (static_cast<int64_t>(b) * a.T + tr) * HD + c0, xs[j]);
+    } else {
+      const int br = a.K - 1 + tr;                   // buffer row (oldest first)
 #pragma unroll
       for (int q = 0; q < PL; ++q)
         xs[j][q] = (buf != nullptr && br >= 0) ? buf[(static_cast<int64_t>(b) * (a.K - 1) + br) * HD + c0 + q] : 0.f;
     }
-  } else {
-#pragma unroll
-    for (int j = 0; j < KW - 1; ++j)
-      pl_ld_pl<DI, PL>(x, (static_cast<int64_t>(b) * a.T + t0 - (KW - 1) + j) * HD + c0, xs[j]);
   }
 #pragma unroll
   for (int r = 0; r < kProRows; ++r)
@@ -137,12 +141,26 @@ __global__ __launch_bounds__(64 * kRowsPerBlock) void kda_prologue_kernel(Prolog
   }
   if (tensor < 2) {
     float tot[kProRows];
-    wave_rowsums16(ss, tot);
+    if constexpr (RW == 16) wave_rowsums16(ss, tot);
+    else tot[0] = wave_sum(ss[0]);
 #pragma unroll
     for (int r = 0; r < kProRows; ++r) {
       const float sc = inv_l2_f32(tot[r]);
 #pragma unroll
       for (int q = 0; q < PL; ++q) sv[r][q] *= sc;
+    }
+  }
+  if constexpr (BUF) {
+    // new buffer row j = (old ++ x)[1 + j] = xs[KW - K + 1 + j]
+    float* bout = tensor == 0 ? a.bq_out : tensor == 1 ? a.bk_out : a.bv_out;
+    if (bout != nullptr) {
+#pragma unroll
+      for (int j = 0; j < KW - 1; ++j) {
+        if (j >= a.K - 1) break;
+#pragma unroll
+        for (int q = 0; q < PL; ++q)
+          bout[(static_cast<int64_t>(b) * (a.K - 1) + j) * HD + c0 + q] = xs[KW - a.K + 1 + j][q];
+      }
     }
   }
 #pragma unroll
@@ -238,22 +256,34 @@ __global__ __launch_bounds__(kEpiThreads) void kda_epilogue_kernel(EpilogueArgs 
   }
 }
 
-template <int D, int KW>
+template <int D, int KW, int RW, bool BUF>
 void launch_prologue_main(const PrologueArgs& a, int in_dt, int out_dt, int grid, hipStream_t s) {
   const dim3 g(grid), blk(64 * kRowsPerBlock);
-  if (in_dt == 0 && out_dt == 0) hipLaunchKernelGGL((kda_prologue_kernel<0, 0, D, KW>), g, blk, 0, s, a);
-  else if (in_dt == 0) hipLaunchKernelGGL((kda_prologue_kernel<0, 1, D, KW>), g, blk, 0, s, a);
-  else if (out_dt == 0) hipLaunchKernelGGL((kda_prologue_kernel<1, 0, D, KW>), g, blk, 0, s, a);
-  else hipLaunchKernelGGL((kda_prologue_kernel<1, 1, D, KW>), g, blk, 0, s, a);
+  if (in_dt == 0 && out_dt == 0) hipLaunchKernelGGL((kda_prologue_kernel<0, 0, D, KW, RW, BUF>), g, blk, 0, s, a);
+  else if (in_dt == 0) hipLaunchKernelGGL((kda_prologue_kernel<0, 1, D, KW, RW, BUF>), g, blk, 0, s, a);
+  else if (out_dt == 0) hipLaunchKernelGGL((kda_prologue_kernel<1, 0, D, KW, RW, BUF>), g, blk, 0, s, a);
+  else hipLaunchKernelGGL((kda_prologue_kernel<1, 1, D, KW, RW, BUF>), g, blk, 0, s, a);
+}
+
+template <int D, int RW, bool BUF>
+void launch_prologue_k(const PrologueArgs& a, int in_dt, int out_dt, hipStream_t s) {
+  const int64_t items = 3LL * a.B * a.H * ((a.T + RW - 1) / RW);
+  const int grid = static_cast<int>((items + kRowsPerBlock - 1) / kRowsPerBlock);
+  if (a.K <= 4) launch_prologue_main<D, 4, RW, BUF>(a, in_dt, out_dt, grid, s);
+  else launch_prologue_main<D, 8, RW, BUF>(a, in_dt, out_dt, grid, s);
 }
 
 template <int D>
 hipError_t launch_prologue_d(const PrologueArgs& a, int in_dt, int out_dt, hipStream_t s) {
-  const int64_t items = 3LL * a.B * a.H * ((a.T + kProRows - 1) / kProRows);
-  if (items > 0) {
-    const int grid = static_cast<int>((items + kRowsPerBlock - 1) / kRowsPerBlock);
-    if (a.K <= 4) launch_prologue_main<D, 4>(a, in_dt, out_dt, grid, s);
-    else launch_prologue_main<D, 8>(a, in_dt, out_dt, grid, s);
+  // T == 1 (a decode step): one wavefront per (tensor, b, h), buffers written
+  // by the same kernel; short sequences one row per wavefront; else 16.
+  if (a.T == 1) {
+    launch_prologue_k<D, 1, true>(a, in_dt, out_dt, s);
+    return hipGetLastError();
+  }
+  if (a.T > 0) {
+    if (a.T < kProRows) launch_prologue_k<D, 1, false>(a, in_dt, out_dt, s);
+    else launch_prologue_k<D, kProRows, false>(a, in_dt, out_dt, s);
     const hipError_t e = hipGetLastError();
     if (e != hipSuccess) return e;
   }
