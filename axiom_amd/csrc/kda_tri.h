@@ -2,7 +2,8 @@
 // workgroup: the four diagonal 16 x 16 blocks by forward substitution (one
 // column per thread, in registers), then the off-diagonal blocks by the
 // blocked recurrence T_Rs = -T_RR sum_{j=s}^{R-1} L_Rj T_js, block row by
-// block row.  Used by the backward's prep kernel and the standalone solve.
+// block row, on the fp32 matrix cores (exact fp32 products).  Used by the
+// backward's prep kernel and the standalone solve.
 #pragma once
 
 #include <hip/hip_runtime.h>
@@ -36,21 +37,35 @@ __device__ __forceinline__ void invert_unit_lower64(const float* sL, float* sT, 
     for (int i = 0; i < 16; ++i) sT[(a0 + i) * PC + a0 + j] = x[i];
   }
   __syncthreads();
+  // Off-diagonal blocks on the fp32 matrix cores, one block T_Rs per wave
+  // (wave s, s < R): X = sum_{j=s}^{R-1} L_Rj T_js, through the wave's 16 x 16
+  // of tmp into the B layout, then T_Rs = -T_RR X.  Lane (r = l & 15,
+  // gq = l >> 4) supplies A[r][4k + gq] and B[4k + gq][r] and holds rows
+  // 4 gq + e, column r of the result.
+  const int wv = t >> 6, l = t & 63, r = l & 15, gq = l >> 4;
   for (int R = 1; R < 4; ++R) {
-    // X_s = sum_{j=s}^{R-1} L_Rj T_js (s < R) into tmp, then T_Rs = -T_RR X_s
-    for (int e = t; e < 256 * R; e += NTH) {
-      const int s = e >> 8, rr = (e >> 4) & 15, cc = e & 15;
-      float acc = 0.f;
-      for (int m = 16 * s; m < 16 * R; ++m) acc = fmaf(sL[(16 * R + rr) * PC + m], sT[m * PC + 16 * s + cc], acc);
-      tmp[s * 256 + rr * 16 + cc] = acc;
-    }
-    __syncthreads();
-    for (int e = t; e < 256 * R; e += NTH) {
-      const int s = e >> 8, rr = (e >> 4) & 15, cc = e & 15;
-      float acc = 0.f;
+    if (wv < R) {
+      const int sb = wv;
+      float* X = tmp + 256 * sb;
+      typedef float f4_ __attribute__((ext_vector_type(4)));
+      f4_ acc = {0.f, 0.f, 0.f, 0.f};
+      for (int j = sb; j < R; ++j) {
 #pragma unroll
-      for (int m = 0; m < 16; ++m) acc = fmaf(sT[(16 * R + rr) * PC + 16 * R + m], tmp[s * 256 + m * 16 + cc], acc);
-      sT[(16 * R + rr) * PC + 16 * s + cc] = -acc;
+        for (int k = 0; k < 4; ++k)
+          acc = __builtin_amdgcn_mfma_f32_16x16x4f32(sL[(16 * R + r) * PC + 16 * j + 4 * k + gq],
+                                                     sT[(16 * j + 4 * k + gq) * PC + 16 * sb + r], acc, 0, 0, 0);
+      }
+#pragma unroll
+      for (int e = 0; e < 4; ++e) X[(4 * gq + e) * 16 + r] = acc[e];
+      __builtin_amdgcn_fence(__ATOMIC_RELEASE, "wavefront", "local");
+      __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "wavefront", "local");
+      f4_ out = {0.f, 0.f, 0.f, 0.f};
+#pragma unroll
+      for (int k = 0; k < 4; ++k)
+        out = __builtin_amdgcn_mfma_f32_16x16x4f32(sT[(16 * R + r) * PC + 16 * R + 4 * k + gq],
+                                                   X[(4 * k + gq) * 16 + r], out, 0, 0, 0);
+#pragma unroll
+      for (int e = 0; e < 4; ++e) sT[(16 * R + 4 * gq + e) * PC + 16 * sb + r] = -out[e];
     }
     __syncthreads();
   }
