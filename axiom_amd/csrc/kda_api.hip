@@ -539,6 +539,71 @@ int kda_epilogue(hipStream_t stream, const void* o, const void* gate, void* y, i
   return KDA_OK;
 }
 
+size_t kda_prologue_bwd_workspace(int B, int T, int H, int d, int K) {
+  if (B < 1 || T < 0 || H < 1 || !dim_ok(d) || K < 1 || K > 8) return 0;
+  const size_t hd = static_cast<size_t>(H) * d;
+  const size_t groups = (static_cast<size_t>(T) + 63) / 64;
+  const size_t n = align_up(3 * static_cast<size_t>(B) * T * hd * 4) + align_up(3 * B * groups * K * hd * 4);
+  return n > 0 ? n : 256;   // nonzero for T == 0: 0 means unsupported
+}
+
+int kda_prologue_bwd(hipStream_t stream, const void* qp, const void* kp, const void* vp,
+                     const float* wq, const float* wk, const float* wv,
+                     const float* bq_in, const float* bk_in, const float* bv_in,
+                     const float* dq, const float* dk, const float* dv,
+                     float* dqp, float* dkp, float* dvp, float* dwq, float* dwk, float* dwv,
+                     float* dbq, float* dbk, float* dbv,
+                     int B, int T, int H, int d, int K, int in_dtype, void* workspace, size_t workspace_bytes) {
+  g_err[0] = 0;
+  if (B < 1 || T < 0 || H < 1) return fail(KDA_ERR_INVALID_ARGUMENT, "B=%d, T=%d, H=%d out of range", B, T, H);
+  if (!dim_ok(d)) return fail(KDA_ERR_UNSUPPORTED, "d=%d: this build runs d in {64, 128}", d);
+  if (K < 1 || K > 8) return fail(KDA_ERR_UNSUPPORTED, "K=%d: conv kernels of 1..8 taps", K);
+  if (in_dtype != KDA_DTYPE_F32 && in_dtype != KDA_DTYPE_BF16)
+    return fail(KDA_ERR_INVALID_ARGUMENT, "in_dtype=%d: projections are F32 or BF16", in_dtype);
+  if (!wq || !wk || !wv || !dwq || !dwk || !dwv) return fail(KDA_ERR_INVALID_ARGUMENT, "null conv taps or dw");
+  if (T > 0 && (!qp || !kp || !vp || !dq || !dk || !dv || !dqp || !dkp || !dvp))
+    return fail(KDA_ERR_INVALID_ARGUMENT, "null pointer");
+  if (static_cast<int64_t>(B) * T * H * 3 / 4 > 0x7FFFFFFFLL) return fail(KDA_ERR_INVALID_ARGUMENT, "too large");
+  const size_t need = kda_prologue_bwd_workspace(B, T, H, d, K);
+  if (!workspace || workspace_bytes < need)
+    return fail(KDA_ERR_WORKSPACE, "workspace of %zu bytes is too small (need %zu)", workspace_bytes, need);
+  kda::PrologueBwdArgs a{};
+  a.x[0] = qp; a.x[1] = kp; a.x[2] = vp;
+  a.w[0] = wq; a.w[1] = wk; a.w[2] = wv;
+  a.bin[0] = bq_in; a.bin[1] = bk_in; a.bin[2] = bv_in;
+  a.dy[0] = dq; a.dy[1] = dk; a.dy[2] = dv;
+  a.dx[0] = dqp; a.dx[1] = dkp; a.dx[2] = dvp;
+  a.dw[0] = dwq; a.dw[1] = dwk; a.dw[2] = dwv;
+  a.db[0] = K > 1 ? dbq : nullptr; a.db[1] = K > 1 ? dbk : nullptr; a.db[2] = K > 1 ? dbv : nullptr;
+  a.B = B; a.T = T; a.H = H; a.K = K; a.G = (T + 63) / 64;
+  a.da = static_cast<float*>(workspace);
+  a.part = reinterpret_cast<float*>(static_cast<unsigned char*>(workspace) +
+                                    align_up(3 * static_cast<size_t>(B) * T * H * d * 4));
+  const hipError_t e = kda::launch_prologue_bwd(a, d, in_dtype == KDA_DTYPE_F32 ? 0 : 1, stream);
+  if (e != hipSuccess) return hip_fail(e, "prologue backward launch");
+  return KDA_OK;
+}
+
+int kda_epilogue_bwd(hipStream_t stream, const void* o, const void* gate, const void* dy, float* dout, void* dgate,
+                     int B, int T, int H, int dv, float eps, int o_dtype, int gate_dtype, int dy_dtype,
+                     int dgate_dtype) {
+  g_err[0] = 0;
+  if (B < 1 || T < 0 || H < 1) return fail(KDA_ERR_INVALID_ARGUMENT, "B=%d, T=%d, H=%d out of range", B, T, H);
+  if (!dim_ok(dv)) return fail(KDA_ERR_UNSUPPORTED, "dv=%d: this build runs dv in {64, 128}", dv);
+  auto ok = [](int dt) { return dt == KDA_DTYPE_F32 || dt == KDA_DTYPE_BF16; };
+  if (!ok(o_dtype) || !ok(gate_dtype) || !ok(dy_dtype) || !ok(dgate_dtype))
+    return fail(KDA_ERR_INVALID_ARGUMENT, "dtypes must be F32 or BF16");
+  if (!(eps >= 0.f) || !std::isfinite(eps)) return fail(KDA_ERR_INVALID_ARGUMENT, "eps must be finite and >= 0");
+  if (T > 0 && (!o || !gate || !dy || !dout || !dgate)) return fail(KDA_ERR_INVALID_ARGUMENT, "null pointer");
+  if (static_cast<int64_t>(B) * T * H / 4 > 0x7FFFFFFFLL) return fail(KDA_ERR_INVALID_ARGUMENT, "too large");
+  kda::EpilogueBwdArgs a{};
+  a.o = o; a.gate = gate; a.dy = dy; a.dout = dout; a.dgate = dgate; a.B = B; a.T = T; a.H = H; a.eps = eps;
+  auto c = [](int dt) { return dt == KDA_DTYPE_F32 ? 0 : 1; };
+  const hipError_t e = kda::launch_epilogue_bwd(a, dv, c(o_dtype), c(gate_dtype), c(dy_dtype), c(dgate_dtype), stream);
+  if (e != hipSuccess) return hip_fail(e, "epilogue backward launch");
+  return KDA_OK;
+}
+
 size_t kda_decode_layer_workspace(int B, int H, int d, int in_dtype) {
   if (B < 1 || H < 1 || !dim_ok(d) || (in_dtype != KDA_DTYPE_F32 && in_dtype != KDA_DTYPE_BF16)) return 0;
   const size_t n = static_cast<size_t>(B) * H * d;

@@ -148,7 +148,35 @@ struct EpilogueArgs {
   float eps;
 };
 
+// Backward of the prologue: cotangents dq, dk, dv [B,T,H,d] fp32 of its
+// outputs -> dx (projections), dw (conv taps), db (incoming buffers).
+struct PrologueBwdArgs {
+  const void* x[3];        // qp, kp, vp [B,T,H*d] (fp32 or bf16)
+  const float* w[3];       // [K, H*d]
+  const float* bin[3];     // [B, K-1, H*d] or null (zeros)
+  const float* dy[3];      // dq, dk, dv [B,T,H*d] fp32
+  float* dx[3];            // [B,T,H*d] fp32
+  float* dw[3];            // [K, H*d] fp32
+  float* db[3];            // [B, K-1, H*d] fp32 or null (not wanted)
+  float* da;               // workspace: [3][B][T][H*d] fp32, the conv output's cotangent
+  float* part;             // workspace: [3][B * G][K][H*d] fp32, dw partial sums (G groups of 64 rows)
+  int B, T, H, K, G;
+};
+
+struct EpilogueBwdArgs {
+  const void* o;           // [B,T,H,dv]
+  const void* gate;        // [B,T,H*dv] gate logits
+  const void* dy;          // [B,T,H*dv]
+  float* dout;             // [B,T,H,dv] fp32
+  void* dgate;             // [B,T,H*dv]
+  int B, T, H;
+  float eps;
+};
+
 hipError_t launch_prologue(const PrologueArgs& a, int d, int in_dt, int out_dt, hipStream_t s);
+hipError_t launch_prologue_bwd(const PrologueBwdArgs& a, int d, int in_dt, hipStream_t s);
+hipError_t launch_epilogue_bwd(const EpilogueBwdArgs& a, int d, int o_dt, int g_dt, int dy_dt, int dg_dt,
+                               hipStream_t s);
 // only the conv buffer update of launch_prologue (the last K-1 inputs)
 hipError_t launch_prologue_buffers(const PrologueArgs& a, int d, int in_dt, hipStream_t s);
 hipError_t launch_epilogue(const EpilogueArgs& a, int d, int o_dt, int g_dt, int y_dt, hipStream_t s);

@@ -328,6 +328,328 @@ hipError_t launch_epilogue_d(const EpilogueArgs& a, int o_dt, int g_dt, int y_dt
   return hipGetLastError();
 }
 
+// ---------------------------------------------------------------------------
+// Backward of the prologue.  With a = conv(x), sg = sigmoid(a), s = a sg and,
+// for q and k, y = s / (||s|| + 1e-12) (y = s for v):
+//   ds = dy / (n + eps) - s (s . dy) / (n (n + eps)^2), n = ||s|| (0 when n = 0:
+//        the reference's tangent convention at a zero row), or ds = dy for v;
+//   da = ds sg (1 + a (1 - sg));
+//   dx[t] = sum_i w[i] da[t + i];  dbuf[j] = the same sum at the history row
+//   j - (K-1);  dw[i] = sum_t da[t] x[t - i].
+// Three launches: da (forward recomputed, one wavefront per 16 rows), then dx,
+// dbuf and per-64-row dw partial sums (workgroup = four wavefronts = 64 rows of
+// one (tensor, b, h)), then the dw reduction.
+// ---------------------------------------------------------------------------
+template <int DI, int D, int KW>
+__global__ __launch_bounds__(64 * kRowsPerBlock) void kda_prologue_bwd_da_kernel(PrologueBwdArgs a) {
+  constexpr int RW = 16;
+  constexpr int PL = D / 64;
+  const int lane = threadIdx.x & 63;
+  const int nblk = (a.T + RW - 1) / RW;
+  const int64_t items = 3LL * a.B * a.H * nblk;
+  const int64_t w = static_cast<int64_t>(blockIdx.x) * kRowsPerBlock + (threadIdx.x >> 6);
+  if (w >= items) return;                          // uniform per wavefront
+  const int blk = static_cast<int>(w % nblk);
+  int64_t rest = w / nblk;
+  const int h = static_cast<int>(rest % a.H);
+  rest /= a.H;
+  const int b = static_cast<int>(rest % a.B);
+  const int tensor = static_cast<int>(rest / a.B);
+  const void* x = a.x[tensor];
+  const float* wp = a.w[tensor];
+  const float* buf = a.bin[tensor];
+  const float* dyp = a.dy[tensor];
+  const int HD = a.H * D;
+  const int c0 = h * D + PL * lane;
+  const int t0 = blk * RW;
+  float wt[KW][PL];
+#pragma unroll
+  for (int i = 0; i < KW; ++i)
+#pragma unroll
+    for (int q = 0; q < PL; ++q) wt[i][q] = wp[static_cast<int64_t>(min(i, a.K - 1)) * HD + c0 + q];
+  float xs[KW - 1 + RW][PL];
+#pragma unroll
+  for (int j = 0; j < KW - 1; ++j) {
+    const int tr = t0 - (KW - 1) + j;
+    if (tr >= 0) {
+      pl_ld_pl<DI, PL>(x, (static_cast<int64_t>(b) * a.T + tr) * HD + c0, xs[j]);
+    } else {
+      const int br = a.K - 1 + tr;
+#pragma unroll
+      for (int q = 0; q < PL; ++q)
+        xs[j][q] = (buf != nullptr && br >= 0) ? buf[(static_cast<int64_t>(b) * (a.K - 1) + br) * HD + c0 + q] : 0.f;
+    }
+  }
+#pragma unroll
+  for (int r = 0; r < RW; ++r)
+    pl_ld_pl<DI, PL>(x, (static_cast<int64_t>(b) * a.T + min(t0 + r, a.T - 1)) * HD + c0, xs[KW - 1 + r]);
+  float dy[RW][PL];
+#pragma unroll
+  for (int r = 0; r < RW; ++r) {
+    const bool live = t0 + r < a.T;
+    const int64_t o = (static_cast<int64_t>(b) * a.T + (live ? t0 + r : 0)) * HD + c0;
+#pragma unroll
+    for (int q = 0; q < PL; ++q) {
+      const float v = dyp[o + q];
+      dy[r][q] = live ? v : 0.f;
+    }
+  }
+  float av[RW][PL], sgv[RW][PL], sv[RW][PL], ss[RW], sd[RW];
+#pragma unroll
+  for (int r = 0; r < RW; ++r) {
+    ss[r] = 0.f;
+    sd[r] = 0.f;
+#pragma unroll
+    for (int q = 0; q < PL; ++q) {
+      float acc = 0.f;
+#pragma unroll
+      for (int i = 0; i < KW; ++i)
+        if (i < a.K) acc = fmaf(wt[i][q], xs[KW - 1 + r - i][q], acc);
+      av[r][q] = acc;
+      sgv[r][q] = sigmoid_f32(acc);
+      sv[r][q] = acc * sgv[r][q];
+      ss[r] = fmaf(sv[r][q], sv[r][q], ss[r]);
+      sd[r] = fmaf(sv[r][q], dy[r][q], sd[r]);
+    }
+  }
+  if (tensor < 2) {
+    float nn[RW], dd[RW];
+    wave_rowsums16(ss, nn);
+    wave_rowsums16(sd, dd);
+#pragma unroll
+    for (int r = 0; r < RW; ++r) {
+      const float n = __builtin_amdgcn_sqrtf(nn[r]);
+      const float npe = n + 1e-12f;
+      const float c1 = __builtin_amdgcn_rcpf(npe);
+      const float c2 = dd[r] * __builtin_amdgcn_rcpf(n * npe * npe);
+#pragma unroll
+      for (int q = 0; q < PL; ++q) dy[r][q] = (n > 0.f) ? dy[r][q] * c1 - sv[r][q] * c2 : 0.f;
+    }
+  }
+  float* dap = a.da + static_cast<int64_t>(tensor) * a.B * a.T * HD;
+#pragma unroll
+  for (int r = 0; r < RW; ++r) {
+    if (t0 + r >= a.T) break;
+    const int64_t o = (static_cast<int64_t>(b) * a.T + t0 + r) * HD + c0;
+#pragma unroll
+    for (int q = 0; q < PL; ++q)
+      dap[o + q] = dy[r][q] * sgv[r][q] * (1.f + av[r][q] * (1.f - sgv[r][q]));
+  }
+}
+
+template <int DI, int D, int KW>
+__global__ __launch_bounds__(64 * kRowsPerBlock) void kda_prologue_bwd_dx_kernel(PrologueBwdArgs a) {
+  constexpr int RW = 16;
+  constexpr int PL = D / 64;
+  __shared__ float sPart[kRowsPerBlock][KW][64 * PL];
+  const int lane = threadIdx.x & 63, wv = threadIdx.x >> 6;
+  const int g = blockIdx.x % a.G;                  // 64-row group
+  int rest = blockIdx.x / a.G;
+  const int h = rest % a.H;
+  rest /= a.H;
+  const int b = rest % a.B;
+  const int tensor = rest / a.B;
+  const void* x = a.x[tensor];
+  const float* wp = a.w[tensor];
+  const float* buf = a.bin[tensor];
+  const int HD = a.H * D;
+  const int c0 = h * D + PL * lane;
+  const int t0 = 64 * g + RW * wv;
+  const float* dap = a.da + static_cast<int64_t>(tensor) * a.B * a.T * HD;
+  float wt[KW][PL];
+#pragma unroll
+  for (int i = 0; i < KW; ++i)
+#pragma unroll
+    for (int q = 0; q < PL; ++q) wt[i][q] = wp[static_cast<int64_t>(min(i, a.K - 1)) * HD + c0 + q];
+  // da rows t0 .. t0 + RW + KW - 2 (zero past T); x rows t0 - (KW-1) .. t0 + RW - 1
+  float dav[RW + KW - 1][PL], xs[KW - 1 + RW][PL];
+#pragma unroll
+  for (int j = 0; j < RW + KW - 1; ++j) {
+    const bool live = t0 + j < a.T;
+    const int64_t o = (static_cast<int64_t>(b) * a.T + (live ? t0 + j : 0)) * HD + c0;
+#pragma unroll
+    for (int q = 0; q < PL; ++q) {
+      const float v = dap[o + q];
+      dav[j][q] = live ? v : 0.f;
+    }
+  }
+#pragma unroll
+  for (int j = 0; j < KW - 1 + RW; ++j) {
+    const int tr = t0 - (KW - 1) + j;
+    if (tr >= 0) {
+      pl_ld_pl<DI, PL>(x, (static_cast<int64_t>(b) * a.T + min(tr, a.T - 1)) * HD + c0, xs[j]);
+    } else {
+      const int br = a.K - 1 + tr;
+#pragma unroll
+      for (int q = 0; q < PL; ++q)
+        xs[j][q] = (buf != nullptr && br >= 0) ? buf[(static_cast<int64_t>(b) * (a.K - 1) + br) * HD + c0 + q] : 0.f;
+    }
+  }
+  // dx
+  float* dxp = a.dx[tensor];
+#pragma unroll
+  for (int r = 0; r < RW; ++r) {
+    if (t0 + r >= a.T) break;
+    const int64_t o = (static_cast<int64_t>(b) * a.T + t0 + r) * HD + c0;
+#pragma unroll
+    for (int q = 0; q < PL; ++q) {
+      float acc = 0.f;
+#pragma unroll
+      for (int i = 0; i < KW; ++i)
+        if (i < a.K) acc = fmaf(wt[i][q], dav[r + i][q], acc);
+      dxp[o + q] = acc;
+    }
+  }
+  // the incoming buffer's rows j (sequence row j - (K-1))
+  float* dbp = a.db[tensor];
+  if (t0 == 0 && dbp != nullptr) {
+#pragma unroll
+    for (int j = 0; j < KW - 1; ++j) {
+      if (j >= a.K - 1) break;
+#pragma unroll
+      for (int q = 0; q < PL; ++q) {
+        float acc = 0.f;
+#pragma unroll
+        for (int i = 0; i < KW; ++i) {
+          const int tr = j - (a.K - 1) + i;          // sequence row reached by tap i
+          if (i < a.K && tr >= 0) acc = fmaf(wt[i][q], dav[tr][q], acc);
+        }
+        dbp[(static_cast<int64_t>(b) * (a.K - 1) + j) * HD + c0 + q] = acc;
+      }
+    }
+  }
+  // dw partial sums over this wavefront's rows, then over the workgroup's four
+#pragma unroll
+  for (int i = 0; i < KW; ++i)
+#pragma unroll
+    for (int q = 0; q < PL; ++q) {
+      float acc = 0.f;
+#pragma unroll
+      for (int r = 0; r < RW; ++r) acc = fmaf(dav[r][q], xs[KW - 1 + r - i][q], acc);   // dav = 0 past T
+      sPart[wv][i][PL * lane + q] = acc;
+    }
+  __syncthreads();
+  if (wv == 0) {
+    float* pp = a.part + (static_cast<int64_t>(tensor) * a.B * a.G + static_cast<int64_t>(b) * a.G + g) * a.K * HD;
+#pragma unroll
+    for (int i = 0; i < KW; ++i) {
+      if (i >= a.K) break;
+#pragma unroll
+      for (int q = 0; q < PL; ++q) {
+        const int c = PL * lane + q;
+        pp[static_cast<int64_t>(i) * HD + h * D + c] = ((sPart[0][i][c] + sPart[1][i][c]) + sPart[2][i][c]) + sPart[3][i][c];
+      }
+    }
+  }
+}
+
+// dw[tensor][i][c] = sum over the B * G partial sums.  With T == 0 the same
+// launch also zeroes the buffers' gradients (no output reads them).
+__global__ __launch_bounds__(256) void kda_prologue_bwd_dw_kernel(PrologueBwdArgs a, int HD) {
+  const int64_t n = 3LL * a.K * HD;
+  const int64_t id = static_cast<int64_t>(blockIdx.x) * 256 + threadIdx.x;
+  if (id < n) {
+    const int tensor = static_cast<int>(id / (static_cast<int64_t>(a.K) * HD));
+    const int64_t ic = id - tensor * static_cast<int64_t>(a.K) * HD;     // i * HD + c
+    const float* pp = a.part + static_cast<int64_t>(tensor) * a.B * a.G * a.K * HD + ic;
+    const int np = a.B * a.G;
+    float acc = 0.f;
+    for (int p = 0; p < np; ++p) acc += pp[static_cast<int64_t>(p) * a.K * HD];
+    a.dw[tensor][ic] = acc;
+  } else if (a.T == 0) {
+    const int64_t per = static_cast<int64_t>(a.B) * (a.K - 1) * HD;
+    const int64_t j = id - n;
+    if (j < 3 * per) {
+      const int tensor = static_cast<int>(j / per);
+      if (a.db[tensor] != nullptr) a.db[tensor][j - tensor * per] = 0.f;
+    }
+  }
+}
+
+template <int D, int KW>
+hipError_t launch_prologue_bwd_k(const PrologueBwdArgs& a, int in_dt, hipStream_t s) {
+  const int nblk = (a.T + 15) / 16;
+  const int64_t items = 3LL * a.B * a.H * nblk;
+  if (items > 0) {
+    const int grid = static_cast<int>((items + kRowsPerBlock - 1) / kRowsPerBlock);
+    if (in_dt == 0) hipLaunchKernelGGL((kda_prologue_bwd_da_kernel<0, D, KW>), dim3(grid), dim3(64 * kRowsPerBlock), 0, s, a);
+    else hipLaunchKernelGGL((kda_prologue_bwd_da_kernel<1, D, KW>), dim3(grid), dim3(64 * kRowsPerBlock), 0, s, a);
+    hipError_t e = hipGetLastError();
+    if (e != hipSuccess) return e;
+    const int grid2 = 3 * a.B * a.H * a.G;
+    if (in_dt == 0) hipLaunchKernelGGL((kda_prologue_bwd_dx_kernel<0, D, KW>), dim3(grid2), dim3(64 * kRowsPerBlock), 0, s, a);
+    else hipLaunchKernelGGL((kda_prologue_bwd_dx_kernel<1, D, KW>), dim3(grid2), dim3(64 * kRowsPerBlock), 0, s, a);
+    e = hipGetLastError();
+    if (e != hipSuccess) return e;
+  }
+  const int HD = a.H * D;
+  const int64_t n = 3LL * a.K * HD + (a.T == 0 ? 3LL * a.B * (a.K - 1) * HD : 0);
+  hipLaunchKernelGGL(kda_prologue_bwd_dw_kernel, dim3(static_cast<int>((n + 255) / 256)), dim3(256), 0, s, a, HD);
+  return hipGetLastError();
+}
+
+// Epilogue backward: y = sg o r with sg = sigmoid(z), r = (mean(o^2) + eps)^-1/2:
+//   dz = dy o r sg (1 - sg);  do = sg r dy - o r^3 (sum_c dy sg o) / D.
+// Same layout as the epilogue: four channels per lane, D/4 lanes per row.
+template <int DO_, int DG, int DDY, int DDG, int D>
+__global__ __launch_bounds__(kEpiThreads) void kda_epilogue_bwd_kernel(EpilogueBwdArgs a) {
+  constexpr int LPR = D / 4;
+  constexpr int RPB = kEpiThreads / LPR;
+  const int64_t rows = static_cast<int64_t>(a.B) * a.T * a.H;
+  const int sub = threadIdx.x % LPR;
+  for (int64_t r = static_cast<int64_t>(blockIdx.x) * RPB + threadIdx.x / LPR; r < rows;
+       r += static_cast<int64_t>(gridDim.x) * RPB) {
+    const int64_t i = r * D + 4 * sub;
+    const f4 o = ep_ld4<DO_>(a.o, i);
+    const f4 z = ep_ld4<DG>(a.gate, i);
+    const f4 dy = ep_ld4<DDY>(a.dy, i);
+    f4 sg;
+    float ss = 0.f, sd = 0.f;
+#pragma unroll
+    for (int e = 0; e < 4; ++e) {
+      sg[e] = sigmoid_f32(z[e]);
+      ss = fmaf(o[e], o[e], ss);
+      sd = fmaf(dy[e] * sg[e], o[e], sd);
+    }
+#pragma unroll
+    for (int off = LPR / 2; off >= 1; off >>= 1) {
+      ss += __shfl_xor(ss, off, 64);
+      sd += __shfl_xor(sd, off, 64);
+    }
+    const float rr = __builtin_amdgcn_rsqf(ss * (1.f / D) + a.eps);
+    const float c3 = rr * rr * rr * sd * (1.f / D);
+    f4 dz, dout;
+#pragma unroll
+    for (int e = 0; e < 4; ++e) {
+      dz[e] = dy[e] * o[e] * rr * sg[e] * (1.f - sg[e]);
+      dout[e] = sg[e] * rr * dy[e] - o[e] * c3;
+    }
+    *reinterpret_cast<float4*>(a.dout + i) = make_float4(dout[0], dout[1], dout[2], dout[3]);
+    ep_st4<DDG>(a.dgate, i, dz);
+  }
+}
+
+template <int D>
+hipError_t launch_epilogue_bwd_d(const EpilogueBwdArgs& a, int o_dt, int g_dt, int dy_dt, int dg_dt, hipStream_t s) {
+  const int64_t rows = static_cast<int64_t>(a.B) * a.T * a.H;
+  if (rows == 0) return hipSuccess;
+  constexpr int RPB = kEpiThreads / (D / 4);
+  const int64_t need = (rows + RPB - 1) / RPB;
+  const dim3 grid(static_cast<int>(need < 8192 ? need : 8192)), blk(kEpiThreads);
+  const int code = o_dt * 8 + g_dt * 4 + dy_dt * 2 + dg_dt;
+#define KDA_EPB(C, A, B2, Cc, Dd) \
+  case C: hipLaunchKernelGGL((kda_epilogue_bwd_kernel<A, B2, Cc, Dd, D>), grid, blk, 0, s, a); break;
+  switch (code) {
+    KDA_EPB(0, 0, 0, 0, 0) KDA_EPB(1, 0, 0, 0, 1) KDA_EPB(2, 0, 0, 1, 0) KDA_EPB(3, 0, 0, 1, 1)
+    KDA_EPB(4, 0, 1, 0, 0) KDA_EPB(5, 0, 1, 0, 1) KDA_EPB(6, 0, 1, 1, 0) KDA_EPB(7, 0, 1, 1, 1)
+    KDA_EPB(8, 1, 0, 0, 0) KDA_EPB(9, 1, 0, 0, 1) KDA_EPB(10, 1, 0, 1, 0) KDA_EPB(11, 1, 0, 1, 1)
+    KDA_EPB(12, 1, 1, 0, 0) KDA_EPB(13, 1, 1, 0, 1) KDA_EPB(14, 1, 1, 1, 0) default:
+      hipLaunchKernelGGL((kda_epilogue_bwd_kernel<1, 1, 1, 1, D>), grid, blk, 0, s, a); break;
+  }
+#undef KDA_EPB
+  return hipGetLastError();
+}
+
 }  // namespace
 
 hipError_t launch_prologue(const PrologueArgs& a, int d, int in_dt, int out_dt, hipStream_t s) {
@@ -340,6 +662,21 @@ hipError_t launch_prologue_buffers(const PrologueArgs& a, int d, int in_dt, hipS
 
 hipError_t launch_epilogue(const EpilogueArgs& a, int d, int o_dt, int g_dt, int y_dt, hipStream_t s) {
   return d == 128 ? launch_epilogue_d<128>(a, o_dt, g_dt, y_dt, s) : launch_epilogue_d<64>(a, o_dt, g_dt, y_dt, s);
+}
+
+}  // namespace kda
+
+namespace kda {
+
+hipError_t launch_prologue_bwd(const PrologueBwdArgs& a, int d, int in_dt, hipStream_t s) {
+  if (d == 128) return a.K <= 4 ? launch_prologue_bwd_k<128, 4>(a, in_dt, s) : launch_prologue_bwd_k<128, 8>(a, in_dt, s);
+  return a.K <= 4 ? launch_prologue_bwd_k<64, 4>(a, in_dt, s) : launch_prologue_bwd_k<64, 8>(a, in_dt, s);
+}
+
+hipError_t launch_epilogue_bwd(const EpilogueBwdArgs& a, int d, int o_dt, int g_dt, int dy_dt, int dg_dt,
+                               hipStream_t s) {
+  return d == 128 ? launch_epilogue_bwd_d<128>(a, o_dt, g_dt, dy_dt, dg_dt, s)
+                  : launch_epilogue_bwd_d<64>(a, o_dt, g_dt, dy_dt, dg_dt, s);
 }
 
 }  // namespace kda

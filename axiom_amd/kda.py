@@ -505,6 +505,148 @@ def kda_layer_fwd(qp, kp, vp, g, beta, gate, wq, wk, wv, conv_state=None, initia
     return y, ht, (new if return_conv_state else None)
 
 
+def prologue_bwd_workspace_bytes(B, T, H, d, K) -> int:
+    """Workspace bytes :func:`kda_prologue_bwd` needs (0 for an unsupported configuration)."""
+    return int(_lib.lib().kda_prologue_bwd_workspace(B, T, H, d, K))
+
+
+def kda_prologue_bwd(qp, kp, vp, wq, wk, wv, dq, dk, dv, conv_state=None, workspace=None):
+    """Gradients of :func:`kda_prologue` (the VJP of ``net/kda.py:194-202``
+    after the convs of ``:383-389``).
+
+    Inputs as :func:`kda_prologue` plus the cotangents ``dq, dk, dv [B, T, H, d]``.
+    Returns fp32 ``((dqp, dkp, dvp) [B, T, H*d], (dwq, dwk, dwv) [K, H*d],
+    dconv_state)`` where ``dconv_state`` is three ``[B, K-1, H*d]`` buffer
+    gradients (None when ``conv_state`` is None or K == 1).  A row whose
+    swish output is all zeros gets a zero L2-norm gradient.
+    """
+    what = "kda_prologue_bwd"
+    if qp.dim() != 3 or kp.shape != qp.shape or vp.shape != qp.shape:
+        raise ValueError(f"{what}: qp, kp, vp must share a [B,T,H*d] shape")
+    B, T, HD = qp.shape
+    if dq.dim() != 4:
+        raise ValueError(f"{what}: dq must be [B,T,H,d]")
+    H, d = dq.shape[2], dq.shape[3]
+    if tuple(dq.shape) != (B, T, H, d) or H * d != HD or dk.shape != dq.shape or dv.shape != dq.shape:
+        raise ValueError(f"{what}: dq, dk, dv must be [{B},{T},H,d] with H*d = {HD}")
+    if any(t.dtype != torch.float32 for t in (dq, dk, dv)):
+        raise ValueError(f"{what}: dq, dk, dv must be fp32")
+    if d not in SUPPORTED_HEAD_DIMS:
+        raise ValueError(f"{what}: head dim {d} unsupported ({SUPPORTED_HEAD_DIMS})")
+    if qp.dtype not in _UT_CODES or kp.dtype != qp.dtype or vp.dtype != qp.dtype:
+        raise ValueError(f"{what}: projections must be fp32 or bf16")
+    K = wq.shape[0]
+    for name, w in (("wq", wq), ("wk", wk), ("wv", wv)):
+        if w.dtype != torch.float32 or tuple(w.shape) != (K, HD):
+            raise ValueError(f"{what}: {name} must be fp32 [{K},{HD}]")
+    if conv_state is not None:
+        for st in conv_state:
+            if st.dtype != torch.float32 or tuple(st.shape) != (B, K - 1, HD):
+                raise ValueError(f"{what}: conv_state buffers must be fp32 [{B},{K - 1},{HD}]")
+    tensors = [qp, kp, vp, wq, wk, wv, dq, dk, dv] + list(conv_state or [])
+    for i, t in enumerate(tensors):
+        _contig(f"arg{i}", t)
+    dev = _require_gpu(tensors, what)
+    L = _lib.lib()
+    need = int(L.kda_prologue_bwd_workspace(B, T, H, d, K))
+    if need == 0:
+        raise ValueError(f"{what}: unsupported configuration")
+    if workspace is None or workspace.numel() * workspace.element_size() < need:
+        workspace = torch.empty(need, dtype=torch.uint8, device=dev)
+    f32 = torch.float32
+    dx = tuple(torch.empty((B, T, HD), dtype=f32, device=dev) for _ in range(3))
+    dw = tuple(torch.empty((K, HD), dtype=f32, device=dev) for _ in range(3))
+    want_db = conv_state is not None and K > 1
+    db = tuple(torch.empty((B, K - 1, HD), dtype=f32, device=dev) for _ in range(3)) if want_db \
+        else (None, None, None)
+    bin_ = conv_state if conv_state is not None else (None, None, None)
+    rc = L.kda_prologue_bwd(_stream(dev), _ptr(qp), _ptr(kp), _ptr(vp), _ptr(wq), _ptr(wk), _ptr(wv),
+                            *(_ptr(b) for b in bin_), _ptr(dq), _ptr(dk), _ptr(dv),
+                            *(_ptr(t) for t in dx), *(_ptr(t) for t in dw), *(_ptr(t) for t in db),
+                            B, T, H, d, K, _UT_CODES[qp.dtype], _ptr(workspace), need)
+    _lib.check(rc, what)
+    return dx, dw, (db if want_db else None)
+
+
+def kda_epilogue_bwd(o, gate, dy, eps: float = 1e-6, dgate_dtype=None):
+    """Gradients of :func:`kda_epilogue`: ``(do [B, T, H, dv] fp32, dgate [B, T, H*dv])``.
+
+    ``dgate`` is in ``dgate_dtype`` (default: the gate's dtype).
+    """
+    what = "kda_epilogue_bwd"
+    if o.dim() != 4:
+        raise ValueError(f"{what}: o must be [B,T,H,dv]")
+    B, T, H, dv = o.shape
+    if tuple(gate.shape) != (B, T, H * dv) or tuple(dy.shape) != (B, T, H * dv):
+        raise ValueError(f"{what}: gate and dy must be [{B},{T},{H * dv}]")
+    if dv not in SUPPORTED_HEAD_DIMS:
+        raise ValueError(f"{what}: dv={dv} unsupported ({SUPPORTED_HEAD_DIMS})")
+    dgate_dtype = gate.dtype if dgate_dtype is None else dgate_dtype
+    if any(t not in _UT_CODES for t in (o.dtype, gate.dtype, dy.dtype, dgate_dtype)):
+        raise ValueError(f"{what}: dtypes must be fp32 or bf16")
+    for name, t in (("o", o), ("gate", gate), ("dy", dy)):
+        _contig(name, t)
+    dev = _require_gpu([o, gate, dy], what)
+    do = torch.empty((B, T, H, dv), dtype=torch.float32, device=dev)
+    dgate = torch.empty((B, T, H * dv), dtype=dgate_dtype, device=dev)
+    rc = _lib.lib().kda_epilogue_bwd(_stream(dev), _ptr(o), _ptr(gate), _ptr(dy), _ptr(do), _ptr(dgate),
+                                     B, T, H, dv, float(eps), _UT_CODES[o.dtype], _UT_CODES[gate.dtype],
+                                     _UT_CODES[dy.dtype], _UT_CODES[dgate_dtype])
+    _lib.check(rc, what)
+    return do, dgate
+
+
+class _KDALayer(torch.autograd.Function):
+    """``(y, final_state)`` of :func:`kda_layer_fwd` with a backward that runs on
+    the HIP kernels: q, k, v and o recomputed (prologue, chunked forward), then
+    epilogue backward -> chunked backward -> prologue backward."""
+
+    @staticmethod
+    def forward(ctx, qp, kp, vp, g, beta, gate, wq, wk, wv, bq, bk, bv, initial_state, scale, eps):
+        conv_state = None if bq is None else (bq, bk, bv)
+        y, ht, _ = kda_layer_fwd(qp, kp, vp, g, beta, gate, wq, wk, wv, conv_state=conv_state,
+                                 initial_state=initial_state, scale=scale, eps=eps, return_conv_state=False,
+                                 out_dtype=qp.dtype)
+        ctx.save_for_backward(qp, kp, vp, g, beta, gate, wq, wk, wv, bq, bk, bv, initial_state)
+        ctx.scale, ctx.eps = scale, eps
+        return y, ht
+
+    @staticmethod
+    def backward(ctx, dy, dht):
+        qp, kp, vp, g, beta, gate, wq, wk, wv, bq, bk, bv, h0 = ctx.saved_tensors
+        conv_state = None if bq is None else (bq, bk, bv)
+        B, T, H, d = g.shape
+        if dy is None:
+            dy = torch.zeros((B, T, H * d), dtype=torch.float32, device=qp.device)
+        dy = dy.contiguous()
+        if dy.dtype not in _OUT_CODES:
+            dy = dy.float()
+        q, k, v, _ = kda_prologue(qp, kp, vp, wq, wk, wv, H, conv_state=conv_state, return_state=False,
+                                  out_dtype=qp.dtype)
+        o, _ = kda_chunk_fwd(q, k, v, g, beta, initial_state=h0, scale=ctx.scale, output_final_state=False)
+        do, dgate = kda_epilogue_bwd(o, gate, dy, eps=ctx.eps)
+        dht = None if dht is None else dht.float().contiguous()
+        dq, dk, dv, dg, dbeta, dh0 = kda_chunk_bwd(q, k, v, g, beta, do, dht=dht, initial_state=h0,
+                                                   scale=ctx.scale, need_dh0=ctx.needs_input_grad[12])
+        dx, dw, db = kda_prologue_bwd(qp, kp, vp, wq, wk, wv, dq, dk, dv, conv_state=conv_state)
+        db = db if db is not None else (None, None, None)
+        return (dx[0].to(qp.dtype), dx[1].to(kp.dtype), dx[2].to(vp.dtype), dg.to(g.dtype),
+                dbeta.to(beta.dtype), dgate, dw[0], dw[1], dw[2], db[0], db[1], db[2], dh0, None, None)
+
+
+def kda_layer(qp, kp, vp, g, beta, gate, wq, wk, wv, conv_state=None, initial_state=None,
+              scale: float = 1.0, eps: float = 1e-6):
+    """Differentiable chunked KDA layer between the projections and ``W_o``:
+    ``(y [B, T, H*d] in the projections' dtype, final_state [B, H, d, d] fp32)``.
+
+    The forward is :func:`kda_layer_fwd`; gradients flow to the projections,
+    ``g``, ``beta``, the gate logits, the conv taps, the carried conv buffers
+    and ``initial_state`` (dense inputs, no ``cu_seqlens``).
+    """
+    bq, bk, bv = conv_state if conv_state is not None else (None, None, None)
+    return _KDALayer.apply(qp, kp, vp, g, beta, gate, wq, wk, wv, bq, bk, bv, initial_state, scale, eps)
+
+
 def varlen_status(workspace, B, T, H, dk, dv, n_seqs, in_code=_lib.KDA_DTYPE_BF16) -> int:
     """Validation bits of the last varlen call that used ``workspace`` (synchronises)."""
     flags = ctypes.c_int32(0)

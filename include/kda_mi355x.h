@@ -223,6 +223,42 @@ KDA_API int kda_epilogue(hipStream_t stream, const void* o, const void* gate, vo
                 int B, int T, int H, int dv, float eps, int o_dtype, int gate_dtype, int out_dtype);
 
 /*
+ * Backward of kda_prologue: the adjoint of net/kda.py:194-202 after the convs
+ * of :383-389 (autodiff through net/shortconv.py:14-33 and net/norm.py:15-17,
+ * 53-66 in the reference), written out: L2-norm adjoint (zero on a row whose
+ * norm is zero, the tangent convention net/tests/test_22_l2norm_padding_
+ * gradient.py pins), swish adjoint, conv transpose.  Inputs as kda_prologue
+ * (qp, kp, vp [B,T,H*d] in in_dtype, F32 or BF16; taps [K,H*d] fp32; incoming
+ * buffers [B,K-1,H*d] fp32 or NULL for zeros) plus dq, dk, dv [B,T,H,d] fp32.
+ * Outputs fp32: dqp, dkp, dvp [B,T,H*d]; dwq, dwk, dwv [K,H*d] (sums over the
+ * batch, overwritten); dbq, dbk, dbv [B,K-1,H*d], the incoming buffers'
+ * gradients (NULL to skip; unused when K == 1).  The forward is recomputed.
+ * Caller workspace of kda_prologue_bwd_workspace bytes.  d in {64, 128},
+ * 1 <= K <= 8.
+ */
+KDA_API int kda_prologue_bwd(hipStream_t stream, const void* qp, const void* kp, const void* vp,
+                const float* wq, const float* wk, const float* wv,
+                const float* bq_in, const float* bk_in, const float* bv_in,
+                const float* dq, const float* dk, const float* dv,
+                float* dqp, float* dkp, float* dvp, float* dwq, float* dwk, float* dwv,
+                float* dbq, float* dbk, float* dbv,
+                int B, int T, int H, int d, int K, int in_dtype, void* workspace, size_t workspace_bytes);
+
+/* Workspace bytes kda_prologue_bwd needs (0 on bad input).  Host-only. */
+KDA_API size_t kda_prologue_bwd_workspace(int B, int T, int H, int d, int K);
+
+/*
+ * Backward of kda_epilogue (net/kda.py:205-214 without W_o, and
+ * net/norm.py:69-73, differentiated by autodiff in the reference): given
+ * o [B,T,H,dv], gate logits [B,T,H*dv] and dy [B,T,H*dv], writes
+ * dout [B,T,H,dv] fp32 and dgate [B,T,H*dv] in dgate_dtype.  All input
+ * dtypes F32 or BF16.  One launch.  dv in {64, 128}.
+ */
+KDA_API int kda_epilogue_bwd(hipStream_t stream, const void* o, const void* gate, const void* dy,
+                float* dout, void* dgate, int B, int T, int H, int dv, float eps,
+                int o_dtype, int gate_dtype, int dy_dtype, int dgate_dtype);
+
+/*
  * One decode token of the whole KDA layer between its projections and W_o,
  * with the short-conv buffers and the state carried in place: the streaming
  * recurrent_step of net/kda.py:277-295 (conv steps net/shortconv.py:36-62,

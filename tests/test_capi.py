@@ -77,7 +77,7 @@ def varlen_ws_bytes(T, N, H, dk, dv, es):
 def test_header_declares_the_abi():
     names = _lib.header_symbols()
     assert set(names) == set(_lib._SIGNATURES), names
-    assert len(names) == len(set(names)) == 18
+    assert len(names) == len(set(names)) == 21
 
 
 def test_library_exports_every_declared_symbol(L):
@@ -289,3 +289,49 @@ def test_chunk_bwd_workspace_size(L):
     assert L.kda_chunk_bwd_workspace(4, 4096, 16, 128, 128, C) == expected
     assert L.kda_chunk_bwd_workspace(1, 0, 1, 64, 64, C) > 0
     assert L.kda_chunk_bwd_workspace(1, 64, 1, 96, 96, C) == 0
+
+
+@pytest.mark.parametrize("B,T,H,d,K", [(4, 4096, 16, 128, 4), (2, 37, 2, 64, 8), (1, 0, 1, 128, 4),
+                                       (3, 129, 2, 64, 1)])
+def test_prologue_bwd_workspace_size(L, B, T, H, d, K):
+    """da [3][B][T][H*d] fp32 + per-64-row dw partial sums [3][B][ceil(T/64)][K][H*d] fp32
+    (256 bytes when both are empty: 0 means unsupported)."""
+    hd = H * d
+    want = _align(3 * B * T * hd * 4) + _align(3 * B * ((T + 63) // 64) * K * hd * 4) or 256
+    assert L.kda_prologue_bwd_workspace(B, T, H, d, K) == want
+    for bad in ((0, T, H, d, K), (B, -1, H, d, K), (B, T, H, 96, K), (B, T, H, d, 0), (B, T, H, d, 9)):
+        assert L.kda_prologue_bwd_workspace(*bad) == 0
+
+
+def test_prologue_bwd_validation(L):
+    def call(**kw):
+        a = dict(x=_FAKE, w=_FAKE, dy=_FAKE, dx=_FAKE, dw=_FAKE, B=1, T=64, H=1, d=64, K=4, dt=1,
+                 ws=_FAKE, ws_bytes=1 << 30)
+        a.update(kw)
+        rc = L.kda_prologue_bwd(_NULL, a["x"], a["x"], a["x"], a["w"], a["w"], a["w"], _NULL, _NULL, _NULL,
+                                a["dy"], a["dy"], a["dy"], a["dx"], a["dx"], a["dx"], a["dw"], a["dw"], a["dw"],
+                                _NULL, _NULL, _NULL, a["B"], a["T"], a["H"], a["d"], a["K"], a["dt"],
+                                a["ws"], a["ws_bytes"])
+        return rc, _lib.last_error()
+    assert call(x=_NULL)[0] == _lib.KDA_ERR_INVALID_ARGUMENT
+    assert call(dw=_NULL)[0] == _lib.KDA_ERR_INVALID_ARGUMENT
+    assert call(d=96)[0] == _lib.KDA_ERR_UNSUPPORTED
+    assert call(K=9)[0] == _lib.KDA_ERR_UNSUPPORTED
+    assert call(dt=2)[0] == _lib.KDA_ERR_INVALID_ARGUMENT
+    rc, msg = call(ws_bytes=16)
+    assert rc == _lib.KDA_ERR_WORKSPACE and "too small" in msg
+
+
+def test_epilogue_bwd_validation(L):
+    def call(**kw):
+        a = dict(o=_FAKE, dout=_FAKE, B=1, T=8, H=1, dv=64, eps=1e-6, dts=(0, 0, 0, 0))
+        a.update(kw)
+        rc = L.kda_epilogue_bwd(_NULL, a["o"], _FAKE, _FAKE, a["dout"], _FAKE, a["B"], a["T"], a["H"], a["dv"],
+                                a["eps"], *a["dts"])
+        return rc, _lib.last_error()
+    assert call(o=_NULL)[0] == _lib.KDA_ERR_INVALID_ARGUMENT
+    assert call(dout=_NULL)[0] == _lib.KDA_ERR_INVALID_ARGUMENT
+    assert call(dv=32)[0] == _lib.KDA_ERR_UNSUPPORTED
+    assert call(eps=float("nan"))[0] == _lib.KDA_ERR_INVALID_ARGUMENT
+    assert call(dts=(0, 0, 0, 2))[0] == _lib.KDA_ERR_INVALID_ARGUMENT
+    assert call(B=0)[0] == _lib.KDA_ERR_INVALID_ARGUMENT

@@ -55,3 +55,67 @@ def test_l2_and_rms_closed_forms():
     r = Lr.headwise_rms_norm(x, eps=0.0)
     np.testing.assert_allclose(np.sqrt(np.mean(r * r, axis=-1)), 1.0, rtol=1e-12)
     np.testing.assert_allclose(Lr.swish(np.array([0.0, 1.0])), [0.0, 1.0 / (1.0 + np.exp(-1.0))])
+
+
+def _fd(f, x, direction, h=1e-6):
+    return (f(x + h * direction) - f(x - h * direction)) / (2 * h)
+
+
+def test_prologue_bwd_matches_finite_differences():
+    """<dL, dx> == directional derivative of L = <dy, prologue(x)> for every input."""
+    rng = np.random.default_rng(11)
+    B, T, H, d, K = 2, 9, 2, 6, 4
+    xs = [rng.standard_normal((B, T, H * d)) for _ in range(3)]
+    ws = [rng.standard_normal((K, H * d)) * 0.4 for _ in range(3)]
+    bufs = [rng.standard_normal((B, K - 1, H * d)) for _ in range(3)]
+    dys = [rng.standard_normal((B, T, H, d)) for _ in range(3)]
+
+    def loss(xs_, ws_, bufs_):
+        q, k, v, _ = Lr.prologue(*xs_, *ws_, H, bufs=bufs_)
+        return sum(np.sum(a * b) for a, b in zip((q, k, v), dys))
+
+    dx0, dx1, dx2, dws, dbs = Lr.prologue_bwd(*xs, *ws, H, *dys, bufs=bufs)
+    dxs = [dx0, dx1, dx2]
+    for n in range(3):
+        u = rng.standard_normal(xs[n].shape)
+        xs_p = [x.copy() for x in xs]
+        fd = (loss([x + 1e-6 * u if i == n else x for i, x in enumerate(xs)], ws, bufs)
+              - loss([x - 1e-6 * u if i == n else x for i, x in enumerate(xs)], ws, bufs)) / 2e-6
+        np.testing.assert_allclose(np.sum(dxs[n] * u), fd, rtol=1e-6, atol=1e-8)
+        u = rng.standard_normal(ws[n].shape)
+        fd = (loss(xs, [w + 1e-6 * u if i == n else w for i, w in enumerate(ws)], bufs)
+              - loss(xs, [w - 1e-6 * u if i == n else w for i, w in enumerate(ws)], bufs)) / 2e-6
+        np.testing.assert_allclose(np.sum(dws[n] * u), fd, rtol=1e-6, atol=1e-8)
+        u = rng.standard_normal(bufs[n].shape)
+        fd = (loss(xs, ws, [b + 1e-6 * u if i == n else b for i, b in enumerate(bufs)])
+              - loss(xs, ws, [b - 1e-6 * u if i == n else b for i, b in enumerate(bufs)])) / 2e-6
+        np.testing.assert_allclose(np.sum(dbs[n] * u), fd, rtol=1e-6, atol=1e-8)
+
+
+def test_epilogue_bwd_matches_finite_differences():
+    rng = np.random.default_rng(12)
+    B, T, H, dv = 2, 5, 3, 8
+    o = rng.standard_normal((B, T, H, dv))
+    z = rng.standard_normal((B, T, H * dv))
+    dy = rng.standard_normal((B, T, H * dv))
+    do, dz = Lr.epilogue_bwd(o, z, dy)
+    u = rng.standard_normal(o.shape)
+    fd = (np.sum(dy * Lr.epilogue(o + 1e-6 * u, z)) - np.sum(dy * Lr.epilogue(o - 1e-6 * u, z))) / 2e-6
+    np.testing.assert_allclose(np.sum(do * u), fd, rtol=1e-6, atol=1e-9)
+    u = rng.standard_normal(z.shape)
+    fd = (np.sum(dy * Lr.epilogue(o, z + 1e-6 * u)) - np.sum(dy * Lr.epilogue(o, z - 1e-6 * u))) / 2e-6
+    np.testing.assert_allclose(np.sum(dz * u), fd, rtol=1e-6, atol=1e-9)
+
+
+def test_l2_norm_gradient_at_a_zero_row_is_zero():
+    """net/tests/test_22_l2norm_padding_gradient.py: zero rows give exactly zero gradient and do
+    not change the other rows' gradients."""
+    x = np.array([[3.0, 4.0, 0.0, 0.0], [0.0, 0.0, 0.0, 0.0], [1.0, 0.0, 0.0, 0.0]])
+    dy = np.ones_like(x)
+    g = Lr.l2_norm_bwd(x, dy)
+    assert np.all(np.isfinite(g)) and np.all(g[1] == 0.0)
+    np.testing.assert_allclose(g[[0, 2]], Lr.l2_norm_bwd(x[[0, 2]], dy[[0, 2]]), rtol=0, atol=0)
+    # and the nonzero rows equal the finite-difference gradient of the plain expression
+    u = np.random.default_rng(13).standard_normal((2, 4))
+    fd = (np.sum(Lr.l2_norm(x[[0, 2]] + 1e-6 * u)) - np.sum(Lr.l2_norm(x[[0, 2]] - 1e-6 * u))) / 2e-6
+    np.testing.assert_allclose(np.sum(g[[0, 2]] * u), fd, rtol=1e-6)
