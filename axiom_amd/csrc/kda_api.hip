@@ -543,7 +543,7 @@ size_t kda_prologue_bwd_workspace(int B, int T, int H, int d, int K) {
   if (B < 1 || T < 0 || H < 1 || !dim_ok(d) || K < 1 || K > 8) return 0;
   const size_t hd = static_cast<size_t>(H) * d;
   const size_t groups = (static_cast<size_t>(T) + 63) / 64;
-  const size_t n = align_up(3 * static_cast<size_t>(B) * T * hd * 4) + align_up(3 * B * groups * K * hd * 4);
+  const size_t n = align_up(3 * B * groups * K * hd * 4);   // dw partial sums per 64-row group
   return n > 0 ? n : 256;   // nonzero for T == 0: 0 means unsupported
 }
 
@@ -576,9 +576,7 @@ int kda_prologue_bwd(hipStream_t stream, const void* qp, const void* kp, const v
   a.dw[0] = dwq; a.dw[1] = dwk; a.dw[2] = dwv;
   a.db[0] = K > 1 ? dbq : nullptr; a.db[1] = K > 1 ? dbk : nullptr; a.db[2] = K > 1 ? dbv : nullptr;
   a.B = B; a.T = T; a.H = H; a.K = K; a.G = (T + 63) / 64;
-  a.da = static_cast<float*>(workspace);
-  a.part = reinterpret_cast<float*>(static_cast<unsigned char*>(workspace) +
-                                    align_up(3 * static_cast<size_t>(B) * T * H * d * 4));
+  a.part = static_cast<float*>(workspace);
   const hipError_t e = kda::launch_prologue_bwd(a, d, in_dtype == KDA_DTYPE_F32 ? 0 : 1, stream);
   if (e != hipSuccess) return hip_fail(e, "prologue backward launch");
   return KDA_OK;

@@ -264,7 +264,10 @@ __device__ __forceinline__ u16 cvt_bf16(float x) { return __builtin_bit_cast(u16
 // lane bits), two butterfly steps finish it, and each row's total is read from
 // a lane holding it.  Every partial formed is the one an xor-butterfly sum
 // over distances 32, 16, .., 1 forms, so each total equals that sum bit for bit.
-__device__ __forceinline__ void wave_rowsums16(const float (&ss)[16], float (&tot)[16]) {
+// The reduce-scatter part alone: lane l ends with the total of row
+// rowsum16_row(l); a per-row function of the totals can then be evaluated once
+// per lane (one instruction for all 16 rows) and read back with readlane.
+__device__ __forceinline__ float wave_rowsums16_lanes(const float (&ss)[16]) {
   const int l = __lane_id();
   const bool b5 = (l & 32) != 0, b4 = (l & 16) != 0, b3 = (l & 8) != 0, b2 = (l & 4) != 0;
   float v8[8], v4[4], v2[2];
@@ -277,11 +280,19 @@ __device__ __forceinline__ void wave_rowsums16(const float (&ss)[16], float (&to
   float v1 = (b2 ? v2[1] : v2[0]) + __shfl_xor(b2 ? v2[0] : v2[1], 4, 64);
   v1 += __shfl_xor(v1, 2, 64);
   v1 += __shfl_xor(v1, 1, 64);
+  return v1;
+}
+// a lane that holds row r's total after wave_rowsums16_lanes
+__device__ __forceinline__ constexpr int rowsum16_lane(int r) {
+  return 32 * ((r >> 3) & 1) + 16 * ((r >> 2) & 1) + 8 * ((r >> 1) & 1) + 4 * (r & 1);
+}
+__device__ __forceinline__ float readlane_f32(float v, int lane) {
+  return __builtin_bit_cast(float, __builtin_amdgcn_readlane(__builtin_bit_cast(int, v), lane));
+}
+__device__ __forceinline__ void wave_rowsums16(const float (&ss)[16], float (&tot)[16]) {
+  const float v1 = wave_rowsums16_lanes(ss);
 #pragma unroll
-  for (int r = 0; r < 16; ++r) {
-    const int src = 32 * ((r >> 3) & 1) + 16 * ((r >> 2) & 1) + 8 * ((r >> 1) & 1) + 4 * (r & 1);
-    tot[r] = __builtin_bit_cast(float, __builtin_amdgcn_readlane(__builtin_bit_cast(int, v1), src));
-  }
+  for (int r = 0; r < 16; ++r) tot[r] = readlane_f32(v1, rowsum16_lane(r));
 }
 // s_waitcnt vmcnt(N): all but the N most recently issued memory operations done
 template <int N>

@@ -158,7 +158,6 @@ struct PrologueBwdArgs {
   float* dx[3];            // [B,T,H*d] fp32
   float* dw[3];            // [K, H*d] fp32
   float* db[3];            // [B, K-1, H*d] fp32 or null (not wanted)
-  float* da;               // workspace: [3][B][T][H*d] fp32, the conv output's cotangent
   float* part;             // workspace: [3][B * G][K][H*d] fp32, dw partial sums (G groups of 64 rows)
   int B, T, H, K, G;
 };

@@ -336,255 +336,285 @@ hipError_t launch_epilogue_d(const EpilogueArgs& a, int o_dt, int g_dt, int y_dt
 //   da = ds sg (1 + a (1 - sg));
 //   dx[t] = sum_i w[i] da[t + i];  dbuf[j] = the same sum at the history row
 //   j - (K-1);  dw[i] = sum_t da[t] x[t - i].
-// Three launches: da (forward recomputed, one wavefront per 16 rows), then dx,
-// dbuf and per-64-row dw partial sums (workgroup = four wavefronts = 64 rows of
-// one (tensor, b, h)), then the dw reduction.
+// One pass: a wavefront owns 16 rows of one (tensor, b, h) and recomputes the
+// forward, and da, for those rows and the K-1 rows after them (the halo its dx
+// sums reach), so da never goes through memory.  A workgroup is four
+// wavefronts on 64 consecutive rows; it adds its dw sums in LDS and writes one
+// partial sum per 64-row group, which a second launch reduces.
 // ---------------------------------------------------------------------------
-template <int DI, int D, int KW>
-__global__ __launch_bounds__(64 * kRowsPerBlock) void kda_prologue_bwd_da_kernel(PrologueBwdArgs a) {
-  constexpr int RW = 16;
-  constexpr int PL = D / 64;
-  const int lane = threadIdx.x & 63;
-  const int nblk = (a.T + RW - 1) / RW;
-  const int64_t items = 3LL * a.B * a.H * nblk;
-  const int64_t w = static_cast<int64_t>(blockIdx.x) * kRowsPerBlock + (threadIdx.x >> 6);
-  if (w >= items) return;                          // uniform per wavefront
-  const int blk = static_cast<int>(w % nblk);
-  int64_t rest = w / nblk;
-  const int h = static_cast<int>(rest % a.H);
-  rest /= a.H;
-  const int b = static_cast<int>(rest % a.B);
-  const int tensor = static_cast<int>(rest / a.B);
-  const void* x = a.x[tensor];
-  const float* wp = a.w[tensor];
-  const float* buf = a.bin[tensor];
-  const float* dyp = a.dy[tensor];
-  const int HD = a.H * D;
-  const int c0 = h * D + PL * lane;
-  const int t0 = blk * RW;
-  float wt[KW][PL];
-#pragma unroll
-  for (int i = 0; i < KW; ++i)
-#pragma unroll
-    for (int q = 0; q < PL; ++q) wt[i][q] = wp[static_cast<int64_t>(min(i, a.K - 1)) * HD + c0 + q];
-  float xs[KW - 1 + RW][PL];
-#pragma unroll
-  for (int j = 0; j < KW - 1; ++j) {
-    const int tr = t0 - (KW - 1) + j;
-    if (tr >= 0) {
-      pl_ld_pl<DI, PL>(x, (static_cast<int64_t>(b) * a.T + tr) * HD + c0, xs[j]);
+// arr[t] for a wave-uniform t < 3 by scalar selects (a runtime index into
+// the kernel-argument struct would read it through memory)
+template <typename P>
+__device__ __forceinline__ P pick3(const P (&arr)[3], int t) {
+  return t == 0 ? arr[0] : (t == 1 ? arr[1] : arr[2]);
+}
+
+// PL consecutive channels at element offset lo of a row whose address is
+// wave-uniform (scalar base + 32-bit lane offset).
+template <int DI, int PL>
+__device__ __forceinline__ void ld_row(const void* row, unsigned lo, float (&o)[PL]) {
+  if constexpr (DI == 0) {
+    const float* p = static_cast<const float*>(row) + lo;
+    if constexpr (PL == 2) {
+      const float2 v = *reinterpret_cast<const float2*>(p);
+      o[0] = v.x;
+      o[1] = v.y;
     } else {
-      const int br = a.K - 1 + tr;
-#pragma unroll
-      for (int q = 0; q < PL; ++q)
-        xs[j][q] = (buf != nullptr && br >= 0) ? buf[(static_cast<int64_t>(b) * (a.K - 1) + br) * HD + c0 + q] : 0.f;
+      o[0] = p[0];
     }
-  }
-#pragma unroll
-  for (int r = 0; r < RW; ++r)
-    pl_ld_pl<DI, PL>(x, (static_cast<int64_t>(b) * a.T + min(t0 + r, a.T - 1)) * HD + c0, xs[KW - 1 + r]);
-  float dy[RW][PL];
-#pragma unroll
-  for (int r = 0; r < RW; ++r) {
-    const bool live = t0 + r < a.T;
-    const int64_t o = (static_cast<int64_t>(b) * a.T + (live ? t0 + r : 0)) * HD + c0;
-#pragma unroll
-    for (int q = 0; q < PL; ++q) {
-      const float v = dyp[o + q];
-      dy[r][q] = live ? v : 0.f;
+  } else {
+    const u16* p = static_cast<const u16*>(row) + lo;
+    if constexpr (PL == 2) {
+      const unsigned w = *reinterpret_cast<const unsigned*>(p);
+      o[0] = __uint_as_float(w << 16);
+      o[1] = __uint_as_float(w & 0xFFFF0000u);
+    } else {
+      o[0] = bf16_to_f32(p[0]);
     }
-  }
-  float av[RW][PL], sgv[RW][PL], sv[RW][PL], ss[RW], sd[RW];
-#pragma unroll
-  for (int r = 0; r < RW; ++r) {
-    ss[r] = 0.f;
-    sd[r] = 0.f;
-#pragma unroll
-    for (int q = 0; q < PL; ++q) {
-      float acc = 0.f;
-#pragma unroll
-      for (int i = 0; i < KW; ++i)
-        if (i < a.K) acc = fmaf(wt[i][q], xs[KW - 1 + r - i][q], acc);
-      av[r][q] = acc;
-      sgv[r][q] = sigmoid_f32(acc);
-      sv[r][q] = acc * sgv[r][q];
-      ss[r] = fmaf(sv[r][q], sv[r][q], ss[r]);
-      sd[r] = fmaf(sv[r][q], dy[r][q], sd[r]);
-    }
-  }
-  if (tensor < 2) {
-    float nn[RW], dd[RW];
-    wave_rowsums16(ss, nn);
-    wave_rowsums16(sd, dd);
-#pragma unroll
-    for (int r = 0; r < RW; ++r) {
-      const float n = __builtin_amdgcn_sqrtf(nn[r]);
-      const float npe = n + 1e-12f;
-      const float c1 = __builtin_amdgcn_rcpf(npe);
-      const float c2 = dd[r] * __builtin_amdgcn_rcpf(n * npe * npe);
-#pragma unroll
-      for (int q = 0; q < PL; ++q) dy[r][q] = (n > 0.f) ? dy[r][q] * c1 - sv[r][q] * c2 : 0.f;
-    }
-  }
-  float* dap = a.da + static_cast<int64_t>(tensor) * a.B * a.T * HD;
-#pragma unroll
-  for (int r = 0; r < RW; ++r) {
-    if (t0 + r >= a.T) break;
-    const int64_t o = (static_cast<int64_t>(b) * a.T + t0 + r) * HD + c0;
-#pragma unroll
-    for (int q = 0; q < PL; ++q)
-      dap[o + q] = dy[r][q] * sgv[r][q] * (1.f + av[r][q] * (1.f - sgv[r][q]));
   }
 }
 
 template <int DI, int D, int KW>
-__global__ __launch_bounds__(64 * kRowsPerBlock) void kda_prologue_bwd_dx_kernel(PrologueBwdArgs a) {
+__global__ __launch_bounds__(64 * kRowsPerBlock) void kda_prologue_bwd_kernel(PrologueBwdArgs a) {
   constexpr int RW = 16;
+  constexpr int HW = KW - 1;      // halo rows (da after the block; x before it)
   constexpr int PL = D / 64;
+  constexpr int ES = DI == 0 ? 4 : 2;
   __shared__ float sPart[kRowsPerBlock][KW][64 * PL];
-  const int lane = threadIdx.x & 63, wv = threadIdx.x >> 6;
+  const int lane = threadIdx.x & 63;
+  const int wv = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
   const int g = blockIdx.x % a.G;                  // 64-row group
   int rest = blockIdx.x / a.G;
   const int h = rest % a.H;
   rest /= a.H;
   const int b = rest % a.B;
   const int tensor = rest / a.B;
-  const void* x = a.x[tensor];
-  const float* wp = a.w[tensor];
-  const float* buf = a.bin[tensor];
   const int HD = a.H * D;
-  const int c0 = h * D + PL * lane;
+  const unsigned lo = PL * lane;
   const int t0 = 64 * g + RW * wv;
-  const float* dap = a.da + static_cast<int64_t>(tensor) * a.B * a.T * HD;
-  float wt[KW][PL];
+  // wave-uniform bases at (b, row 0, channel h * D)
+  const int64_t rowbase = static_cast<int64_t>(b) * a.T * HD + h * D;
+  const char* xb = static_cast<const char*>(pick3(a.x, tensor)) + rowbase * ES;
+  const float* yb = pick3(a.dy, tensor) + rowbase;
+  const float* buf = pick3(a.bin, tensor);
+  const float* bb = buf == nullptr ? nullptr : buf + static_cast<int64_t>(b) * (a.K - 1) * HD + h * D;
+  float wt[KW][PL];                // taps K .. KW-1 are zero: every sum below runs over KW
 #pragma unroll
-  for (int i = 0; i < KW; ++i)
+  for (int i = 0; i < KW; ++i) {
+    float w[PL];
+    ld_row<0, PL>(pick3(a.w, tensor) + static_cast<int64_t>(min(i, a.K - 1)) * HD + h * D, lo, w);
 #pragma unroll
-    for (int q = 0; q < PL; ++q) wt[i][q] = wp[static_cast<int64_t>(min(i, a.K - 1)) * HD + c0 + q];
-  // da rows t0 .. t0 + RW + KW - 2 (zero past T); x rows t0 - (KW-1) .. t0 + RW - 1
-  float dav[RW + KW - 1][PL], xs[KW - 1 + RW][PL];
+    for (int q = 0; q < PL; ++q) wt[i][q] = i < a.K ? w[q] : 0.f;
+  }
+  // x rows t0 - HW .. t0 + RW + HW - 1 and dy rows t0 .. t0 + RW + HW - 1,
+  // loaded from clamped rows without branches (every load in flight at once);
+  // the few edge rows are fixed up after: before row 0 the carried buffer or
+  // zeros, dy zero from T on (so da is zero there)
+  float xs[RW + 2 * HW][PL];
+  float dd[RW + HW][PL];
 #pragma unroll
-  for (int j = 0; j < RW + KW - 1; ++j) {
-    const bool live = t0 + j < a.T;
-    const int64_t o = (static_cast<int64_t>(b) * a.T + (live ? t0 + j : 0)) * HD + c0;
+  for (int j = 0; j < RW + 2 * HW; ++j)
+    ld_row<DI, PL>(xb + static_cast<int64_t>(min(max(t0 - HW + j, 0), a.T - 1)) * HD * ES, lo, xs[j]);
+#pragma unroll
+  for (int r = 0; r < RW + HW; ++r) ld_row<0, PL>(yb + static_cast<int64_t>(min(t0 + r, a.T - 1)) * HD, lo, dd[r]);
+  if (t0 == 0) {
+#pragma unroll
+    for (int j = 0; j < HW; ++j) {
+      const int br = a.K - 1 - HW + j;      // buffer row of sequence row j - HW
+      if (bb != nullptr && br >= 0) {
+        ld_row<0, PL>(bb + static_cast<int64_t>(br) * HD, lo, xs[j]);
+      } else {
+#pragma unroll
+        for (int q = 0; q < PL; ++q) xs[j][q] = 0.f;
+      }
+    }
+  }
+  if (t0 + RW + HW > a.T) {
+#pragma unroll
+    for (int r = 0; r < RW + HW; ++r)
+      if (t0 + r >= a.T) {
+#pragma unroll
+        for (int q = 0; q < PL; ++q) dd[r][q] = 0.f;
+      }
+  }
+  // s = a sg and the swish derivative f = sg (1 + a (1 - sg)) per element
+  float sv[RW + HW][PL], fv[RW + HW][PL];
+#pragma unroll
+  for (int r = 0; r < RW + HW; ++r)
 #pragma unroll
     for (int q = 0; q < PL; ++q) {
-      const float v = dap[o + q];
-      dav[j][q] = live ? v : 0.f;
-    }
-  }
+      float av = 0.f;
 #pragma unroll
-  for (int j = 0; j < KW - 1 + RW; ++j) {
-    const int tr = t0 - (KW - 1) + j;
-    if (tr >= 0) {
-      pl_ld_pl<DI, PL>(x, (static_cast<int64_t>(b) * a.T + min(tr, a.T - 1)) * HD + c0, xs[j]);
-    } else {
-      const int br = a.K - 1 + tr;
-#pragma unroll
-      for (int q = 0; q < PL; ++q)
-        xs[j][q] = (buf != nullptr && br >= 0) ? buf[(static_cast<int64_t>(b) * (a.K - 1) + br) * HD + c0 + q] : 0.f;
+      for (int i = 0; i < KW; ++i) av = fmaf(wt[i][q], xs[HW + r - i][q], av);
+      const float sg = sigmoid_f32(av);
+      sv[r][q] = av * sg;
+      fv[r][q] = sg * fmaf(av, 1.f - sg, 1.f);
     }
+  if (tensor < 2) {
+    float c1[RW], c2[RW], h1[HW], h2[HW];
+#pragma unroll
+    for (int r = 0; r < RW + HW; ++r) {
+      float ss = 0.f, sd = 0.f;
+#pragma unroll
+      for (int q = 0; q < PL; ++q) {
+        ss = fmaf(sv[r][q], sv[r][q], ss);
+        sd = fmaf(sv[r][q], dd[r][q], sd);
+      }
+      if (r < RW) {
+        c1[r] = ss;
+        c2[r] = sd;
+      } else {
+        h1[r - RW] = wave_sum(ss);
+        h2[r - RW] = wave_sum(sd);
+      }
+    }
+    // ds = dy k1 - s k2 with k1 = 1 / (n + eps), k2 = (s . dy) / (n (n + eps)^2)
+    // (both 0 when n = 0), evaluated once per lane for the 16 rows it holds
+    auto coef = [](float nsq, float sdr, float& k1, float& k2) {
+      const float n = __builtin_amdgcn_sqrtf(nsq);
+      const float npe = n + 1e-12f;
+      k1 = n > 0.f ? __builtin_amdgcn_rcpf(npe) : 0.f;
+      k2 = n > 0.f ? sdr * __builtin_amdgcn_rcpf(n * npe * npe) : 0.f;
+    };
+    float k1v, k2v;
+    coef(wave_rowsums16_lanes(c1), wave_rowsums16_lanes(c2), k1v, k2v);
+#pragma unroll
+    for (int r = 0; r < RW + HW; ++r) {
+      float k1, k2;
+      if (r < RW) {
+        k1 = readlane_f32(k1v, rowsum16_lane(r));
+        k2 = readlane_f32(k2v, rowsum16_lane(r));
+      } else {
+        coef(h1[r - RW], h2[r - RW], k1, k2);
+      }
+#pragma unroll
+      for (int q = 0; q < PL; ++q) dd[r][q] = fmaf(dd[r][q], k1, -sv[r][q] * k2) * fv[r][q];
+    }
+  } else {
+#pragma unroll
+    for (int r = 0; r < RW + HW; ++r)
+#pragma unroll
+      for (int q = 0; q < PL; ++q) dd[r][q] *= fv[r][q];
   }
   // dx
-  float* dxp = a.dx[tensor];
+  float* xo = pick3(a.dx, tensor) + rowbase;
 #pragma unroll
   for (int r = 0; r < RW; ++r) {
     if (t0 + r >= a.T) break;
-    const int64_t o = (static_cast<int64_t>(b) * a.T + t0 + r) * HD + c0;
+    float acc[PL];
 #pragma unroll
     for (int q = 0; q < PL; ++q) {
-      float acc = 0.f;
+      acc[q] = 0.f;
 #pragma unroll
-      for (int i = 0; i < KW; ++i)
-        if (i < a.K) acc = fmaf(wt[i][q], dav[r + i][q], acc);
-      dxp[o + q] = acc;
+      for (int i = 0; i < KW; ++i) acc[q] = fmaf(wt[i][q], dd[r + i][q], acc[q]);
     }
+    float* p = xo + static_cast<int64_t>(t0 + r) * HD + lo;
+    if constexpr (PL == 2) *reinterpret_cast<float2*>(p) = make_float2(acc[0], acc[1]);
+    else p[0] = acc[0];
   }
-  // the incoming buffer's rows j (sequence row j - (K-1))
-  float* dbp = a.db[tensor];
+  // the incoming buffer: sequence row -m (m = 1 .. K-1) is its row K-1-m and
+  // reaches the outputs 0 .. KW-1-m through taps m .. KW-1
+  float* dbp = pick3(a.db, tensor);
   if (t0 == 0 && dbp != nullptr) {
+    float* dbb = dbp + static_cast<int64_t>(b) * (a.K - 1) * HD + h * D + lo;
 #pragma unroll
-    for (int j = 0; j < KW - 1; ++j) {
-      if (j >= a.K - 1) break;
+    for (int m = 1; m <= HW; ++m) {
+      if (m > a.K - 1) break;
 #pragma unroll
       for (int q = 0; q < PL; ++q) {
         float acc = 0.f;
 #pragma unroll
-        for (int i = 0; i < KW; ++i) {
-          const int tr = j - (a.K - 1) + i;          // sequence row reached by tap i
-          if (i < a.K && tr >= 0) acc = fmaf(wt[i][q], dav[tr][q], acc);
-        }
-        dbp[(static_cast<int64_t>(b) * (a.K - 1) + j) * HD + c0 + q] = acc;
+        for (int i = m; i < KW; ++i) acc = fmaf(wt[i][q], dd[i - m][q], acc);
+        dbb[static_cast<int64_t>(a.K - 1 - m) * HD + q] = acc;
       }
     }
   }
-  // dw partial sums over this wavefront's rows, then over the workgroup's four
+  // dw sums over this wavefront's rows (da = 0 from T on), then over the four
 #pragma unroll
   for (int i = 0; i < KW; ++i)
 #pragma unroll
     for (int q = 0; q < PL; ++q) {
       float acc = 0.f;
 #pragma unroll
-      for (int r = 0; r < RW; ++r) acc = fmaf(dav[r][q], xs[KW - 1 + r - i][q], acc);   // dav = 0 past T
-      sPart[wv][i][PL * lane + q] = acc;
+      for (int r = 0; r < RW; ++r) acc = fmaf(dd[r][q], xs[HW + r - i][q], acc);
+      sPart[wv][i][lo + q] = acc;
     }
   __syncthreads();
   if (wv == 0) {
-    float* pp = a.part + (static_cast<int64_t>(tensor) * a.B * a.G + static_cast<int64_t>(b) * a.G + g) * a.K * HD;
+    float* pp = a.part + (static_cast<int64_t>(tensor) * a.B * a.G + static_cast<int64_t>(b) * a.G + g) * a.K * HD +
+                h * D;
 #pragma unroll
     for (int i = 0; i < KW; ++i) {
       if (i >= a.K) break;
 #pragma unroll
       for (int q = 0; q < PL; ++q) {
-        const int c = PL * lane + q;
-        pp[static_cast<int64_t>(i) * HD + h * D + c] = ((sPart[0][i][c] + sPart[1][i][c]) + sPart[2][i][c]) + sPart[3][i][c];
+        const int c = lo + q;
+        pp[static_cast<int64_t>(i) * HD + c] = ((sPart[0][i][c] + sPart[1][i][c]) + sPart[2][i][c]) + sPart[3][i][c];
       }
     }
   }
 }
 
-// dw[tensor][i][c] = sum over the B * G partial sums.  With T == 0 the same
-// launch also zeroes the buffers' gradients (no output reads them).
-__global__ __launch_bounds__(256) void kda_prologue_bwd_dw_kernel(PrologueBwdArgs a, int HD) {
-  const int64_t n = 3LL * a.K * HD;
-  const int64_t id = static_cast<int64_t>(blockIdx.x) * 256 + threadIdx.x;
-  if (id < n) {
-    const int tensor = static_cast<int>(id / (static_cast<int64_t>(a.K) * HD));
-    const int64_t ic = id - tensor * static_cast<int64_t>(a.K) * HD;     // i * HD + c
-    const float* pp = a.part + static_cast<int64_t>(tensor) * a.B * a.G * a.K * HD + ic;
+// dw[tensor][i][c] = sum of the B * G partial sums.  A workgroup takes 64
+// columns of one (tensor, i); its eight wavefronts take every eighth partial
+// (four loads in flight each), then add in LDS.  With T == 0 the blocks after
+// those zero the buffers' gradients (no output reads the buffers).
+constexpr int kDwWaves = 8;
+
+__global__ __launch_bounds__(64 * kDwWaves) void kda_prologue_bwd_dw_kernel(PrologueBwdArgs a, int HD) {
+  __shared__ float sSum[kDwWaves][64];
+  const int lane = threadIdx.x & 63, wv = threadIdx.x >> 6;
+  const int cb = HD / 64;
+  const int ndw = 3 * a.K * cb;
+  if (static_cast<int>(blockIdx.x) < ndw) {
+    const int tensor = blockIdx.x / (a.K * cb);
+    const int rem = blockIdx.x % (a.K * cb);
+    const int i = rem / cb;
+    const int c = (rem % cb) * 64 + lane;
+    const int64_t stride = static_cast<int64_t>(a.K) * HD;
+    const float* pp = a.part + static_cast<int64_t>(tensor) * a.B * a.G * stride + static_cast<int64_t>(i) * HD + c;
     const int np = a.B * a.G;
-    float acc = 0.f;
-    for (int p = 0; p < np; ++p) acc += pp[static_cast<int64_t>(p) * a.K * HD];
-    a.dw[tensor][ic] = acc;
+    float s0 = 0.f, s1 = 0.f, s2 = 0.f, s3 = 0.f;
+    int p = wv;
+    for (; p + 3 * kDwWaves < np; p += 4 * kDwWaves) {
+      s0 += pp[p * stride];
+      s1 += pp[(p + kDwWaves) * stride];
+      s2 += pp[(p + 2 * kDwWaves) * stride];
+      s3 += pp[(p + 3 * kDwWaves) * stride];
+    }
+    for (; p < np; p += kDwWaves) s0 += pp[p * stride];
+    sSum[wv][lane] = (s0 + s1) + (s2 + s3);
+    __syncthreads();
+    if (wv == 0) {
+      float acc = 0.f;
+#pragma unroll
+      for (int w = 0; w < kDwWaves; ++w) acc += sSum[w][lane];
+      pick3(a.dw, tensor)[static_cast<int64_t>(i) * HD + c] = acc;
+    }
   } else if (a.T == 0) {
     const int64_t per = static_cast<int64_t>(a.B) * (a.K - 1) * HD;
-    const int64_t j = id - n;
+    const int64_t j = static_cast<int64_t>(blockIdx.x - ndw) * (64 * kDwWaves) + threadIdx.x;
     if (j < 3 * per) {
       const int tensor = static_cast<int>(j / per);
-      if (a.db[tensor] != nullptr) a.db[tensor][j - tensor * per] = 0.f;
+      float* dbp = pick3(a.db, tensor);
+      if (dbp != nullptr) dbp[j - tensor * per] = 0.f;
     }
   }
 }
 
 template <int D, int KW>
 hipError_t launch_prologue_bwd_k(const PrologueBwdArgs& a, int in_dt, hipStream_t s) {
-  const int nblk = (a.T + 15) / 16;
-  const int64_t items = 3LL * a.B * a.H * nblk;
-  if (items > 0) {
-    const int grid = static_cast<int>((items + kRowsPerBlock - 1) / kRowsPerBlock);
-    if (in_dt == 0) hipLaunchKernelGGL((kda_prologue_bwd_da_kernel<0, D, KW>), dim3(grid), dim3(64 * kRowsPerBlock), 0, s, a);
-    else hipLaunchKernelGGL((kda_prologue_bwd_da_kernel<1, D, KW>), dim3(grid), dim3(64 * kRowsPerBlock), 0, s, a);
-    hipError_t e = hipGetLastError();
-    if (e != hipSuccess) return e;
-    const int grid2 = 3 * a.B * a.H * a.G;
-    if (in_dt == 0) hipLaunchKernelGGL((kda_prologue_bwd_dx_kernel<0, D, KW>), dim3(grid2), dim3(64 * kRowsPerBlock), 0, s, a);
-    else hipLaunchKernelGGL((kda_prologue_bwd_dx_kernel<1, D, KW>), dim3(grid2), dim3(64 * kRowsPerBlock), 0, s, a);
-    e = hipGetLastError();
+  if (a.T > 0) {
+    const int grid = 3 * a.B * a.H * a.G;
+    if (in_dt == 0) hipLaunchKernelGGL((kda_prologue_bwd_kernel<0, D, KW>), dim3(grid), dim3(64 * kRowsPerBlock), 0, s, a);
+    else hipLaunchKernelGGL((kda_prologue_bwd_kernel<1, D, KW>), dim3(grid), dim3(64 * kRowsPerBlock), 0, s, a);
+    const hipError_t e = hipGetLastError();
     if (e != hipSuccess) return e;
   }
   const int HD = a.H * D;
-  const int64_t n = 3LL * a.K * HD + (a.T == 0 ? 3LL * a.B * (a.K - 1) * HD : 0);
-  hipLaunchKernelGGL(kda_prologue_bwd_dw_kernel, dim3(static_cast<int>((n + 255) / 256)), dim3(256), 0, s, a, HD);
+  int64_t blocks = 3LL * a.K * (HD / 64);
+  if (a.T == 0) blocks += (3LL * a.B * (a.K - 1) * HD + 64 * kDwWaves - 1) / (64 * kDwWaves);
+  hipLaunchKernelGGL(kda_prologue_bwd_dw_kernel, dim3(static_cast<int>(blocks)), dim3(64 * kDwWaves), 0, s, a, HD);
   return hipGetLastError();
 }
 

@@ -28,6 +28,11 @@ Also reported on the same JSON line:
 * ``layer``: the chunked layer forward ``kda_layer_fwd`` (short conv, swish
   and L2 norm fused into the intra kernel, the scan, the RMSNorm x sigmoid
   gate epilogue) on config-1 shapes with K = 4, bf16 projections and output;
+* ``layer_backward``: the layer's backward on the same shapes -- the
+  prologue and epilogue adjoints (``kda_prologue_bwd``, ``kda_epilogue_bwd``)
+  per call against their algorithmic bytes, and the whole backward of
+  ``kda_layer`` (q, k, v and o recomputed, then epilogue, chunked and
+  prologue backward);
 * ``decode_layer``: the layer decode step (prologue, recurrent step,
   epilogue) per token, eager against a HIP graph of 64 tokens, at B=1 and
   B=256;
@@ -316,6 +321,65 @@ def bench_layer(args, fwd_inputs, device):
                 config="B4 T4096 H16 d128 K4, bf16 projections, gates and y, fp32 o inside, zero h0")
 
 
+def bench_layer_bwd(args, fwd_inputs, device):
+    """The layer backward at config-1 shapes (K = 4, bf16 projections, gate and
+    dy): the two new entry points on their own, and the whole backward of
+    ``kda_layer`` (recompute q, k, v and o, epilogue backward, chunked
+    backward, prologue backward)."""
+    import axiom_amd
+    from axiom_amd import kda as kmod
+    q, k, v, g, beta = fwd_inputs
+    B, T, H, d = q.shape
+    K = 4
+    gen = torch.Generator(device=device)
+    gen.manual_seed(args.seed + 7)
+    bf = torch.bfloat16
+    xs = [torch.randn(B, T, H * d, device=device, generator=gen).to(bf) for _ in range(3)]
+    ws_ = [torch.randn(K, H * d, device=device, generator=gen) * 0.4 for _ in range(3)]
+    gate = torch.randn(B, T, H * d, device=device, generator=gen).to(bf)
+    dy = torch.randn(B, T, H * d, device=device, generator=gen).to(bf)
+    dqkv = [torch.randn(B, T, H, d, device=device, generator=gen) for _ in range(3)]
+    o = torch.randn(B, T, H, d, device=device, generator=gen)
+    pws = torch.empty(kmod.prologue_bwd_workspace_bytes(B, T, H, d, K), dtype=torch.uint8, device=device)
+    cws = torch.empty(kmod.chunk_fwd_workspace_bytes(B, T, H, d, d), dtype=torch.uint8, device=device)
+    bws = torch.empty(kmod.chunk_bwd_workspace_bytes(B, T, H, d, d), dtype=torch.uint8, device=device)
+    stream = torch.cuda.current_stream(device)
+
+    def timed(f, steps):
+        for _ in range(3):
+            f()
+        torch.cuda.synchronize()
+        e0, e1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+        e0.record(stream)
+        for _ in range(steps):
+            f()
+        e1.record(stream)
+        torch.cuda.synchronize()
+        return e0.elapsed_time(e1) / 1e3 / steps
+
+    def whole():
+        qq, kk, vv, _ = axiom_amd.kda_prologue(*xs, *ws_, H, out_dtype=bf, return_state=False)
+        oo, _ = axiom_amd.kda_chunk_fwd(qq, kk, vv, g, beta, output_final_state=False, workspace=cws)
+        do, _ = axiom_amd.kda_epilogue_bwd(oo, gate, dy)
+        dq, dk, dv, _, _, _ = axiom_amd.kda_chunk_bwd(qq, kk, vv, g, beta, do, need_dh0=False, workspace=bws)
+        return axiom_amd.kda_prologue_bwd(*xs, *ws_, dq, dk, dv, workspace=pws)
+
+    nd = B * T * H * d
+    t_pro = timed(lambda: axiom_amd.kda_prologue_bwd(*xs, *ws_, *dqkv, workspace=pws), args.steps)
+    t_epi = timed(lambda: axiom_amd.kda_epilogue_bwd(o, gate, dy), args.steps)
+    t_all = timed(whole, args.bwd_steps)
+    pro_bytes = 3 * nd * (2 + 4 + 4) + 6 * K * H * d * 4     # x bf16, dq/dk/dv fp32 in; dx fp32, taps, dw
+    epi_bytes = nd * (4 + 2 + 2 + 4 + 2)                    # o fp32, gate, dy bf16 in; do fp32, dgate bf16
+    return dict(
+        prologue_bwd={"us_per_call": t_pro * 1e6, "algorithmic_bytes": pro_bytes,
+                      "gbps": pro_bytes / t_pro / 1e9, "frac": pro_bytes / t_pro / 1e9 / HBM_PEAK_GBPS,
+                      "kernels": "kda_prologue_bwd_kernel (one pass) + kda_prologue_bwd_dw_kernel"},
+        epilogue_bwd={"us_per_call": t_epi * 1e6, "algorithmic_bytes": epi_bytes,
+                      "gbps": epi_bytes / t_epi / 1e9, "frac": epi_bytes / t_epi / 1e9 / HBM_PEAK_GBPS},
+        layer_bwd_us_per_call=t_all * 1e6, layer_bwd_tokens_per_s=B * T / t_all,
+        config="B4 T4096 H16 d128 K4, bf16 projections, gate and dy; the whole backward recomputes q, k, v, o")
+
+
 def bench_ut_solve(args, device):
     import axiom_amd
     H, C, N = 12, 64, 256
@@ -489,6 +553,8 @@ def main():
     if not args.no_backward:
         line["backward"] = bench_backward(args, fwd["inputs"], device)
     line["layer"] = bench_layer(args, fwd["inputs"], device)
+    if not args.no_backward:
+        line["layer_backward"] = bench_layer_bwd(args, fwd["inputs"], device)
     line["decode_layer"] = bench_decode_layer(args, device)
     line["ut_solve"] = bench_ut_solve(args, device)
     if args.other_configs:

@@ -294,10 +294,10 @@ def test_chunk_bwd_workspace_size(L):
 @pytest.mark.parametrize("B,T,H,d,K", [(4, 4096, 16, 128, 4), (2, 37, 2, 64, 8), (1, 0, 1, 128, 4),
                                        (3, 129, 2, 64, 1)])
 def test_prologue_bwd_workspace_size(L, B, T, H, d, K):
-    """da [3][B][T][H*d] fp32 + per-64-row dw partial sums [3][B][ceil(T/64)][K][H*d] fp32
-    (256 bytes when both are empty: 0 means unsupported)."""
+    """Per-64-row dw partial sums [3][B][ceil(T/64)][K][H*d] fp32 (256 bytes when
+    empty: 0 means unsupported)."""
     hd = H * d
-    want = _align(3 * B * T * hd * 4) + _align(3 * B * ((T + 63) // 64) * K * hd * 4) or 256
+    want = _align(3 * B * ((T + 63) // 64) * K * hd * 4) or 256
     assert L.kda_prologue_bwd_workspace(B, T, H, d, K) == want
     for bad in ((0, T, H, d, K), (B, -1, H, d, K), (B, T, H, 96, K), (B, T, H, d, 0), (B, T, H, d, 9)):
         assert L.kda_prologue_bwd_workspace(*bad) == 0
