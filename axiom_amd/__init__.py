@@ -7,10 +7,10 @@ kernels behind the C ABI of ``include/kda_mi355x.h``.  The Python layer (:mod:`a
 validates arguments and hands device pointers to that library.
 """
 
-from .kda import (cc_scan, kda_chunk, kda_chunk_bwd, kda_chunk_fwd, kda_decode_layer_step,  # noqa: F401
+from .kda import (cc_scan, cc_scan_bwd, kda_chunk, kda_chunk_bwd, kda_chunk_fwd, kda_decode_layer_step,  # noqa: F401
                   kda_epilogue, kda_epilogue_bwd, kda_layer, kda_layer_fwd, kda_prologue, kda_prologue_bwd,
                   kda_recurrent_step, solve, solve_t, ut_solve, ut_solve_bwd, varlen_status)
 
-__all__ = ["cc_scan", "kda_chunk", "kda_chunk_bwd", "kda_chunk_fwd", "kda_decode_layer_step", "kda_epilogue",
+__all__ = ["cc_scan", "cc_scan_bwd", "kda_chunk", "kda_chunk_bwd", "kda_chunk_fwd", "kda_decode_layer_step", "kda_epilogue",
            "kda_epilogue_bwd", "kda_layer", "kda_layer_fwd", "kda_prologue", "kda_prologue_bwd",
            "kda_recurrent_step", "solve", "solve_t", "ut_solve", "ut_solve_bwd", "varlen_status"]

@@ -258,6 +258,24 @@ hipError_t launch_adapt(const AdaptArgs& a, hipStream_t s) {
   return hipGetLastError();
 }
 
+__global__ __launch_bounds__(256) void kda_cc_finish_kernel(CcFinishArgs a) {
+  const int64_t i = static_cast<int64_t>(blockIdx.x) * 256 + threadIdx.x;
+  if (i < a.n) {
+    static_cast<u16*>(a.dq)[i] = cvt_bf16(a.dq32[i]);
+    static_cast<u16*>(a.dk)[i] = cvt_bf16(a.dk32[i]);
+    static_cast<u16*>(a.dv)[i] = cvt_bf16(a.dv32[i]);
+    a.dalpha[i] = a.dg[i] / a.alpha[i];
+  }
+  if (i < a.n_tok_heads * 32) a.dbeta32[i] = a.dbeta[i >> 5] * (1.0f / 32.0f);
+}
+
+hipError_t launch_cc_finish(const CcFinishArgs& a, hipStream_t s) {
+  const int64_t n = a.n > a.n_tok_heads * 32 ? a.n : a.n_tok_heads * 32;
+  if (n == 0) return hipSuccess;
+  hipLaunchKernelGGL(kda_cc_finish_kernel, dim3(static_cast<unsigned>((n + 255) / 256)), dim3(256), 0, s, a);
+  return hipGetLastError();
+}
+
 }  // namespace kda
 
 // ----------------------------------------------------------------------------
@@ -468,6 +486,68 @@ int kda_chunk_bwd(hipStream_t stream, const void* q, const void* k, const void* 
   return KDA_OK;
 }
 
+
+size_t kda_cc_scan_bwd_workspace(int T, int H, int dk, int dv, int chunk) {
+  if (T < 0 || H < 1 || !dim_ok(dk) || dk != dv || chunk < 1) return 0;
+  const size_t th = static_cast<size_t>(T) * H;
+  // g, beta (adapter) + dq, dk, dv, dg fp32 + dbeta fp32 + the dense backward's workspace
+  return align_up(th * dk * 4) + align_up(th * 4) + 4 * align_up(th * dk * 4) + align_up(th * 4) +
+         kda_chunk_bwd_workspace(1, T, H, dk, dv, kC);
+}
+
+int kda_cc_scan_bwd(hipStream_t stream, const void* q, const void* k, const void* v,
+                    const float* alpha, const float* beta32, const float* S_in,
+                    const float* d_o, const float* dS, void* dq, void* dk, void* dv,
+                    float* dalpha, float* dbeta32, float* dS_in,
+                    int T, int H, int dk_dim, int dv_dim, int tile, int chunk,
+                    void* workspace, size_t workspace_bytes) {
+  g_err[0] = '\0';
+  if (!q || !k || !v || !alpha || !beta32 || !S_in || !d_o || !dS || !dq || !dk || !dv || !dalpha ||
+      !dbeta32 || !dS_in)
+    return fail(KDA_ERR_INVALID_ARGUMENT, "null pointer");
+  if (T < 0) return fail(KDA_ERR_INVALID_ARGUMENT, "T=%d must be >= 0", T);
+  if (chunk < 1) return fail(KDA_ERR_INVALID_ARGUMENT, "chunk=%d must be >= 1", chunk);
+  if (T % chunk)
+    return fail(KDA_ERR_INVALID_ARGUMENT, "T=%d must be a multiple of the chunk width C=%d", T, chunk);
+  if (tile < 1 || tile > 16)
+    return fail(KDA_ERR_INVALID_ARGUMENT, "tile=%d outside [1, 16] (the _cc_tile bound)", tile);
+  if (int rc = check_dims(H, dk_dim, dv_dim)) return rc;
+  const size_t need = kda_cc_scan_bwd_workspace(T, H, dk_dim, dv_dim, chunk);
+  if (workspace == nullptr || workspace_bytes < need)
+    return fail(KDA_ERR_WORKSPACE, "workspace of %zu bytes is too small (need %zu)", workspace_bytes, need);
+  const size_t th = static_cast<size_t>(T) * H;
+  unsigned char* ws = static_cast<unsigned char*>(workspace);
+  float* g32 = reinterpret_cast<float*>(ws);
+  ws += align_up(th * dk_dim * 4);
+  float* b32 = reinterpret_cast<float*>(ws);
+  ws += align_up(th * 4);
+  float* f[4];
+  for (int i = 0; i < 4; ++i) {
+    f[i] = reinterpret_cast<float*>(ws);
+    ws += align_up(th * dk_dim * 4);
+  }
+  float* dbeta = reinterpret_cast<float*>(ws);
+  ws += align_up(th * 4);
+  const size_t rest = workspace_bytes - static_cast<size_t>(ws - static_cast<unsigned char*>(workspace));
+  kda::AdaptArgs aa{};
+  aa.alpha = alpha; aa.beta32 = beta32; aa.g_out = g32; aa.beta_out = b32;
+  aa.n_tok_heads = static_cast<int64_t>(th);
+  aa.dk = dk_dim;
+  hipError_t e = kda::launch_adapt(aa, stream);
+  if (e != hipSuccess) return hip_fail(e, "cc_scan backward adapter launch");
+  // the dense backward on the [1, T, H, d] view (the same memory layout)
+  const int rc = kda_chunk_bwd(stream, q, k, v, g32, b32, S_in, d_o, dS, f[0], f[1], f[2], f[3], dbeta, dS_in,
+                               1, T, H, dk_dim, dv_dim, kC, 1.0f, KDA_DTYPE_BF16_F32GATES, KDA_DTYPE_F32, ws, rest);
+  if (rc != KDA_OK) return rc;
+  kda::CcFinishArgs fa{};
+  fa.dq32 = f[0]; fa.dk32 = f[1]; fa.dv32 = f[2]; fa.dg = f[3]; fa.dbeta = dbeta; fa.alpha = alpha;
+  fa.dq = dq; fa.dk = dk; fa.dv = dv; fa.dalpha = dalpha; fa.dbeta32 = dbeta32;
+  fa.n = static_cast<int64_t>(th) * dk_dim;
+  fa.n_tok_heads = static_cast<int64_t>(th);
+  e = kda::launch_cc_finish(fa, stream);
+  if (e != hipSuccess) return hip_fail(e, "cc_scan backward finish launch");
+  return KDA_OK;
+}
 
 int kda_ut_solve(hipStream_t stream, const void* a, const void* b, void* x, int H, int C, int N,
                  int dtype, int transpose) {

@@ -194,4 +194,24 @@ hipError_t launch_varlen_prep(const int32_t* cu, int N, int T, int32_t* cu_clamp
 hipError_t launch_decode(const DecodeArgs& a, int d, int dt, int out_dt, int grid, hipStream_t s);
 hipError_t launch_adapt(const AdaptArgs& a, hipStream_t s);
 
+// cc_scan backward outputs from the dense backward's fp32 results: dq, dk, dv
+// rounded to bf16 (the primal dtype), dalpha = dg / alpha (g = log alpha),
+// dbeta32 = dbeta / 32 on each of the 32 columns (beta = their mean).
+struct CcFinishArgs {
+  const float* dq32;
+  const float* dk32;
+  const float* dv32;
+  const float* dg;
+  const float* dbeta;
+  const float* alpha;
+  void* dq;                // bf16
+  void* dk;
+  void* dv;
+  float* dalpha;
+  float* dbeta32;
+  int64_t n;               // T * H * d
+  int64_t n_tok_heads;     // T * H
+};
+hipError_t launch_cc_finish(const CcFinishArgs& a, hipStream_t s);
+
 }  // namespace kda

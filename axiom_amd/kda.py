@@ -690,37 +690,34 @@ def kda_recurrent_step(q, k, v, g, beta, state, scale: float = 1.0, out_dtype=to
     return o
 
 
-def cc_scan(q, k, v, alpha, beta32, S, tile: int = 16, chunk: int = 32):
-    """The reference seam ``cc_scan`` (``net/kernels/kda_cc_fused_persist.py:920``).
-
-    ``q, k (T, H*dk)`` bf16, ``v (T, H*dv)`` bf16, ``alpha (T, H*dk)`` fp32,
-    ``beta32 (T, H*32)`` fp32, ``S (H, dk, dv)`` fp32.  Returns
-    ``(o (T, H*dv) fp32, S_new (H, dk, dv) fp32)``.  Raises ``ValueError`` for
-    a non-bf16 q/v (``:737-740``), ``T % chunk != 0`` (``:741-742``) or an
-    unsupported configuration (``:743-749``), ``RuntimeError`` without a GPU.
-    """
+def _cc_check(q, k, v, alpha, beta32, S, tile, chunk, what, dtype_msg):
     T = q.shape[0]
     if S.dim() != 3:
-        raise ValueError("cc_scan: S must be (H, dk, dv)")
+        raise ValueError(f"{what}: S must be (H, dk, dv)")
     H, dk, dv = S.shape
     dt = q.dtype
     if v.dtype != dt or dt != torch.bfloat16:
-        raise ValueError(
-            f"persistent kernel consumes bf16 q/k/v; got q.dtype={dt}, v.dtype={v.dtype}")
+        raise ValueError(f"{dtype_msg}; got q.dtype={dt}, v.dtype={v.dtype}")
     C = int(chunk)
     if C < 1 or T % C:
         raise ValueError(f"T={T} must be a multiple of the chunk width C={C}")
     if not (1 <= int(tile) <= 16):
-        raise ValueError(f"cc_scan: tile={tile} outside [1, 16]")
-    _check_dims(dk, dv, "cc_scan")
+        raise ValueError(f"{what}: tile={tile} outside [1, 16]")
+    _check_dims(dk, dv, what)
     if (tuple(q.shape) != (T, H * dk) or tuple(k.shape) != (T, H * dk) or k.dtype != dt
             or tuple(v.shape) != (T, H * dv) or tuple(alpha.shape) != (T, H * dk)
             or tuple(beta32.shape) != (T, H * 32)):
-        raise ValueError("cc_scan: shapes must be q,k,alpha (T,H*dk), v (T,H*dv), beta32 (T,H*32)")
+        raise ValueError(f"{what}: shapes must be q,k,alpha (T,H*dk), v (T,H*dv), beta32 (T,H*32)")
     if alpha.dtype != torch.float32 or beta32.dtype != torch.float32 or S.dtype != torch.float32:
-        raise ValueError("cc_scan: alpha, beta32 and S must be fp32")
+        raise ValueError(f"{what}: alpha, beta32 and S must be fp32")
     for name, t in (("q", q), ("k", k), ("v", v), ("alpha", alpha), ("beta32", beta32), ("S", S)):
         _contig(name, t)
+    return T, H, dk, dv, C
+
+
+def _cc_scan_fwd(q, k, v, alpha, beta32, S, tile, chunk):
+    T, H, dk, dv, C = _cc_check(q, k, v, alpha, beta32, S, tile, chunk, "cc_scan",
+                                "persistent kernel consumes bf16 q/k/v")
     dev = _require_gpu([q, k, v, alpha, beta32, S], "cc_scan")
     L = _lib.lib()
     ws_bytes = int(L.kda_cc_scan_workspace(T, H, dk, dv, C))
@@ -731,3 +728,76 @@ def cc_scan(q, k, v, alpha, beta32, S, tile: int = 16, chunk: int = 32):
                        _ptr(o), _ptr(S_new), T, H, dk, dv, int(tile), C, _ptr(workspace), ws_bytes)
     _lib.check(rc, "cc_scan")
     return o, S_new
+
+
+def cc_scan_bwd(q, k, v, alpha, beta32, S, do, dS=None, tile: int = 16, chunk: int = 32):
+    """The seam's backward rule ``kernel_bwd`` (``net/kernels/kda_cc_fused_persist.py:1710``).
+
+    ``(q, k, v, alpha, beta32, S)`` as :func:`cc_scan`, ``do (T, H*dv)`` and
+    ``dS (H, dk, dv)`` (None = 0) the cotangents of ``o`` and ``S_new``.
+    Returns ``(dq, dk, dv, dalpha, dbeta32, dS_in)`` in the primal dtypes:
+    bf16 ``dq, dk, dv``, fp32 ``dalpha`` (``= d(log alpha) / alpha``),
+    ``dbeta32`` (the beta cotangent / 32 on each of the 32 columns) and
+    ``dS_in``.
+    """
+    what = "cc_scan_bwd"
+    T, H, dk, dv, C = _cc_check(q, k, v, alpha, beta32, S, tile, chunk, what,
+                                "persistent backward kernel consumes bf16 q/k/v (the same operand "
+                                "path as the forward kernel)")
+    if tuple(do.shape) != (T, H * dv):
+        raise ValueError(f"{what}: do must be (T, H*dv) = {(T, H * dv)}")
+    do = do.float().contiguous()
+    if dS is None:
+        dS = torch.zeros_like(S)
+    if tuple(dS.shape) != (H, dk, dv):
+        raise ValueError(f"{what}: dS must be (H, dk, dv)")
+    dS = dS.float().contiguous()
+    dev = _require_gpu([q, k, v, alpha, beta32, S, do, dS], what)
+    L = _lib.lib()
+    ws_bytes = int(L.kda_cc_scan_bwd_workspace(T, H, dk, dv, C))
+    workspace = torch.empty(max(ws_bytes, 1), dtype=torch.uint8, device=dev)
+    dq = torch.empty_like(q)
+    dk_ = torch.empty_like(k)
+    dv_ = torch.empty_like(v)
+    dalpha = torch.empty_like(alpha)
+    dbeta32 = torch.empty_like(beta32)
+    dS_in = torch.empty_like(S)
+    rc = L.kda_cc_scan_bwd(_stream(dev), _ptr(q), _ptr(k), _ptr(v), _ptr(alpha), _ptr(beta32), _ptr(S),
+                           _ptr(do), _ptr(dS), _ptr(dq), _ptr(dk_), _ptr(dv_), _ptr(dalpha), _ptr(dbeta32),
+                           _ptr(dS_in), T, H, dk, dv, int(tile), C, _ptr(workspace), ws_bytes)
+    _lib.check(rc, what)
+    return dq, dk_, dv_, dalpha, dbeta32, dS_in
+
+
+class _CCScan(torch.autograd.Function):
+    """``cc_scan`` with :func:`cc_scan_bwd` as its VJP, as the reference's
+    ``custom_vjp`` (``net/kernels/kda_cc_fused_persist.py:895-911``)."""
+
+    @staticmethod
+    def forward(ctx, q, k, v, alpha, beta32, S, tile, chunk):
+        o, S_new = _cc_scan_fwd(q, k, v, alpha, beta32, S, tile, chunk)
+        ctx.save_for_backward(q, k, v, alpha, beta32, S)
+        ctx.tile, ctx.chunk = tile, chunk
+        return o, S_new
+
+    @staticmethod
+    def backward(ctx, do, dS):
+        q, k, v, alpha, beta32, S = ctx.saved_tensors
+        if do is None:
+            do = torch.zeros((q.shape[0], v.shape[1]), dtype=torch.float32, device=q.device)
+        grads = cc_scan_bwd(q, k, v, alpha, beta32, S, do, dS, tile=ctx.tile, chunk=ctx.chunk)
+        return (*grads, None, None)
+
+
+def cc_scan(q, k, v, alpha, beta32, S, tile: int = 16, chunk: int = 32):
+    """The reference seam ``cc_scan`` (``net/kernels/kda_cc_fused_persist.py:920``).
+
+    ``q, k (T, H*dk)`` bf16, ``v (T, H*dv)`` bf16, ``alpha (T, H*dk)`` fp32,
+    ``beta32 (T, H*32)`` fp32, ``S (H, dk, dv)`` fp32.  Returns
+    ``(o (T, H*dv) fp32, S_new (H, dk, dv) fp32)``.  Raises ``ValueError`` for
+    a non-bf16 q/v (``:737-740``), ``T % chunk != 0`` (``:741-742``) or an
+    unsupported configuration (``:743-749``), ``RuntimeError`` without a GPU.
+    Differentiable: gradients reach all six inputs through
+    :func:`cc_scan_bwd`, like the reference's ``custom_vjp``.
+    """
+    return _CCScan.apply(q, k, v, alpha, beta32, S, tile, chunk)

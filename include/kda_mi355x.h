@@ -142,6 +142,28 @@ KDA_API int kda_cc_scan(hipStream_t stream,
 KDA_API size_t kda_cc_scan_workspace(int T, int H, int dk, int dv, int chunk);
 
 /*
+ * The seam's backward rule: kernel_bwd, net/kernels/kda_cc_fused_persist.py
+ * :1710-1763 (the custom_vjp backward of cc_scan, :895-911; the adjoint of
+ * net/kernels/kda_cc_fused_bwd.py:117-239 scanned in reverse, :794-842).
+ * Inputs as kda_cc_scan plus the cotangents d_o (T, H*dv) fp32 of o and dS
+ * (H, dk, dv) fp32 of S_out.  Outputs in the primal dtypes: dq, dk (T, H*dk)
+ * and dv (T, H*dv) bf16; dalpha (T, H*dk) fp32 (= d(log alpha) / alpha);
+ * dbeta32 (T, H*32) fp32 (the beta cotangent / 32 on each column); dS_in
+ * (H, dk, dv) fp32.  Errors as kda_cc_scan.  Caller workspace of
+ * kda_cc_scan_bwd_workspace bytes.
+ */
+KDA_API int kda_cc_scan_bwd(hipStream_t stream,
+                const void* q, const void* k, const void* v,
+                const float* alpha, const float* beta32, const float* S_in,
+                const float* d_o, const float* dS,
+                void* dq, void* dk, void* dv, float* dalpha, float* dbeta32, float* dS_in,
+                int T, int H, int dk_dim, int dv_dim, int tile, int chunk,
+                void* workspace, size_t workspace_bytes);
+
+/* Workspace bytes kda_cc_scan_bwd needs (0 on bad input).  Host-only. */
+KDA_API size_t kda_cc_scan_bwd_workspace(int T, int H, int dk, int dv, int chunk);
+
+/*
  * Chunked backward: gradients of (o, final state) = kda_chunk_fwd(q, k, v, g,
  * beta, h0) for dense [B,T,H,d] inputs (no cu_seqlens).  Replaces the
  * reference's backward rule of the cc_scan custom_vjp,

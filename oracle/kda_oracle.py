@@ -44,6 +44,9 @@ How each is pinned (tests/test_oracle.py)
 * UT solve: ``scipy.linalg.solve_triangular(unit_diagonal=True)`` and the
   Neumann product identity (``net/kernels/kda_ut_solve.py:20-27``);
 * varlen: packed == per-sequence; decode: T decode steps == chunked forward.
+* ``cc_scan`` / ``cc_scan_bwd`` (the seam's operands: alpha, beta32 as a
+  32-column mean): the backward against central finite differences of the
+  forward in every input, with unequal beta32 columns (tests/test_oracle_bwd.py).
 * mutation tests plant a dropped term, a sign flip, a transposed operand and an
   off-by-one in the decay into copies of these functions and show that at
   least one pin fails for each.
@@ -386,6 +389,41 @@ def chunk_bwd(q, k, v, g, beta, do, dht=None, h0=None, chunk: int = 64, dtype=to
     return (back(outs["dq"], dk), back(outs["dk"], dk), back(outs["dv"], dv), back(outs["dg"], dk),
             dbeta.reshape(B, H, Tp)[:, :, :T].permute(0, 2, 1).contiguous().numpy(),
             dS.reshape(B, H, dk, dv).numpy())
+
+
+def cc_scan(q, k, v, alpha, beta32, S, chunk: int = 64):
+    """The reference seam ``cc_scan`` (``net/kernels/kda_cc_fused_persist.py:920``)
+    in its own operands: ``q, k, alpha (T, H*dk)``, ``v (T, H*dv)``, ``beta32
+    (T, H*32)`` (beta = the mean of a head's 32 columns, ``:435``), ``S (H, dk,
+    dv)``.  ``g = log(alpha)``; returns numpy float64 ``(o (T, H*dv), S_new)``."""
+    H, dk, dv = np.asarray(S).shape
+    T = np.asarray(q).shape[0]
+    g = np.log(np.asarray(alpha, np.float64)).reshape(1, T, H, dk)
+    beta = np.asarray(beta32, np.float64).reshape(T, H, 32).mean(-1)[None]
+    o, ht = chunk_fwd(np.asarray(q, np.float64).reshape(1, T, H, dk), np.asarray(k, np.float64).reshape(1, T, H, dk),
+                      np.asarray(v, np.float64).reshape(1, T, H, dv), g, beta, h0=np.asarray(S, np.float64)[None],
+                      chunk=chunk)
+    return o.numpy().reshape(T, H * dv), ht.numpy()[0]
+
+
+def cc_scan_bwd(q, k, v, alpha, beta32, S, do, dS=None, chunk: int = 64):
+    """The seam's backward rule (``kernel_bwd``, ``net/kernels/kda_cc_fused_persist.py:1710``;
+    cotangent structure of ``net/kernels/kda_cc_fused_bwd.py:228-239``):
+    ``(dq, dk, dv, dalpha, dbeta32, dS_in)`` in float64, ``dalpha = dg / alpha``
+    and ``dbeta32`` = the beta cotangent / 32 on each column."""
+    H, dk, dv = np.asarray(S).shape
+    T = np.asarray(q).shape[0]
+    alpha = np.asarray(alpha, np.float64)
+    g = np.log(alpha).reshape(1, T, H, dk)
+    beta = np.asarray(beta32, np.float64).reshape(T, H, 32).mean(-1)[None]
+    dq, dk_, dv_, dg, db, dh0 = chunk_bwd(
+        np.asarray(q, np.float64).reshape(1, T, H, dk), np.asarray(k, np.float64).reshape(1, T, H, dk),
+        np.asarray(v, np.float64).reshape(1, T, H, dv), g, beta, np.asarray(do, np.float64).reshape(1, T, H, dv),
+        dht=None if dS is None else np.asarray(dS, np.float64)[None], h0=np.asarray(S, np.float64)[None],
+        chunk=chunk)
+    dbeta32 = np.repeat(db[0][..., None] / 32.0, 32, axis=-1).reshape(T, H * 32)
+    return (dq.reshape(T, H * dk), dk_.reshape(T, H * dk), dv_.reshape(T, H * dv),
+            dg.reshape(T, H * dk) / alpha, dbeta32, dh0[0])
 
 
 def chunk_intermediates(q, k, v, g, beta, chunk: int = 64, tile: int = 16, scale: float = 1.0):

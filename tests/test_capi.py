@@ -77,7 +77,7 @@ def varlen_ws_bytes(T, N, H, dk, dv, es):
 def test_header_declares_the_abi():
     names = _lib.header_symbols()
     assert set(names) == set(_lib._SIGNATURES), names
-    assert len(names) == len(set(names)) == 21
+    assert len(names) == len(set(names)) == 23
 
 
 def test_library_exports_every_declared_symbol(L):
@@ -335,3 +335,27 @@ def test_epilogue_bwd_validation(L):
     assert call(eps=float("nan"))[0] == _lib.KDA_ERR_INVALID_ARGUMENT
     assert call(dts=(0, 0, 0, 2))[0] == _lib.KDA_ERR_INVALID_ARGUMENT
     assert call(B=0)[0] == _lib.KDA_ERR_INVALID_ARGUMENT
+
+
+def test_cc_scan_bwd_workspace_and_validation(L):
+    T, H, d = 4096, 4, 128
+    th = T * H
+    want = (_align(th * d * 4) + _align(th * 4) + 4 * _align(th * d * 4) + _align(th * 4)
+            + L.kda_chunk_bwd_workspace(1, T, H, d, d, C))
+    assert L.kda_cc_scan_bwd_workspace(T, H, d, d, 32) == want
+    assert L.kda_cc_scan_bwd_workspace(T, H, 96, 96, 32) == 0
+
+    def call(**kw):
+        a = dict(q=_FAKE, do=_FAKE, T=96, H=2, d=128, tile=16, chunk=32, ws=_FAKE, ws_bytes=1 << 30)
+        a.update(kw)
+        rc = L.kda_cc_scan_bwd(_NULL, a["q"], _FAKE, _FAKE, _FAKE, _FAKE, _FAKE, a["do"], _FAKE,
+                               _FAKE, _FAKE, _FAKE, _FAKE, _FAKE, _FAKE, a["T"], a["H"], a["d"], a["d"],
+                               a["tile"], a["chunk"], a["ws"], a["ws_bytes"])
+        return rc, _lib.last_error()
+    assert call(q=_NULL)[0] == _lib.KDA_ERR_INVALID_ARGUMENT
+    assert call(do=_NULL)[0] == _lib.KDA_ERR_INVALID_ARGUMENT
+    rc, msg = call(chunk=64)
+    assert rc == _lib.KDA_ERR_INVALID_ARGUMENT and "multiple of the chunk width" in msg
+    assert call(tile=17)[0] == _lib.KDA_ERR_INVALID_ARGUMENT
+    assert call(d=96)[0] == _lib.KDA_ERR_UNSUPPORTED
+    assert call(ws_bytes=64)[0] == _lib.KDA_ERR_WORKSPACE

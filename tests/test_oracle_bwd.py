@@ -146,3 +146,37 @@ def test_planted_mistake_fails_the_fd_pin(monkeypatch):
     xm = dict(x); xm["k"] = x["k"] - eps * u
     fd = (_loss(xp, do, dht, 8) - _loss(xm, do, dht, 8)) / (2 * eps)
     assert abs(fd - float((gr["k"] * u).sum())) > 1e-4
+
+
+def test_cc_scan_bwd_matches_finite_differences():
+    """The seam's cotangents (dalpha through g = log alpha, dbeta32 through
+    the 32-column mean) against central differences of the seam's forward."""
+    rng = np.random.default_rng(5)
+    T, H, d = 24, 2, 4
+    q = rng.standard_normal((T, H * d)) * 0.5
+    k = rng.standard_normal((T, H * d)) * 0.5
+    v = rng.standard_normal((T, H * d))
+    alpha = np.exp(-rng.uniform(0.01, 0.8, (T, H * d)))
+    beta32 = rng.uniform(0.1, 0.9, (T, H * 32))          # unequal columns: beta is their mean
+    S = rng.standard_normal((H, d, d)) * 0.3
+    do = rng.standard_normal((T, H * d))
+    dS = rng.standard_normal((H, d, d))
+    x = dict(q=q, k=k, v=v, alpha=alpha, beta32=beta32, S=S)
+
+    def loss(y):
+        o, sn = K.cc_scan(y["q"], y["k"], y["v"], y["alpha"], y["beta32"], y["S"], chunk=8)
+        return float((o * do).sum() + (sn * dS).sum())
+
+    grads = dict(zip(("q", "k", "v", "alpha", "beta32", "S"),
+                     K.cc_scan_bwd(q, k, v, alpha, beta32, S, do, dS, chunk=8)))
+    eps = 1e-6
+    for n in x:
+        u = rng.standard_normal(x[n].shape)
+        xp = dict(x); xp[n] = x[n] + eps * u
+        xm = dict(x); xm[n] = x[n] - eps * u
+        fd = (loss(xp) - loss(xm)) / (2 * eps)
+        an = float((grads[n] * u).sum())
+        assert abs(fd - an) <= 1e-6 * max(1.0, abs(fd)), (n, fd, an)
+    # dbeta32 is constant over a head's 32 columns
+    db = grads["beta32"].reshape(T, H, 32)
+    assert np.array_equal(db, np.repeat(db[..., :1], 32, axis=-1))
