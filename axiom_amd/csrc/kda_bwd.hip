@@ -630,8 +630,8 @@ __global__ __launch_bounds__(kChunkThreads) void kda_bwd_chunk_kernel(BwdArgs a)
   // holds dG until the final reverse cumsum).  Phases 1-3 run on the fp32
   // matrix cores: wave wv owns row tile mt = wv / 2 and the NDT column tiles
   // dt = (wv % 2) NDT + q of every [64][D] product (lane (r, gq) holds rows
-  // 16 mt + 4 gq + i, column 16 dt + r), so its read-modify-writes of phases
-  // 1 and 2 hit its own positions; phase 4 (wave wv owns column tile wv, lane
+  // 16 mt + 4 gq + i, column 16 dt + r), so phase 2 adds to the dk and dG
+  // terms phase 1 left at its own positions; phase 4 (wave wv owns column tile wv, lane
   // rows 4 gq + e of every row tile) and the outputs (thread (rm, cn) owns rows
   // rm + 16i, columns cn + TC j) read what other threads wrote, after the
   // workgroup barriers between the phases.  Pad rows (c >= len) are never
@@ -653,6 +653,11 @@ __global__ __launch_bounds__(kChunkThreads) void kda_bwd_chunk_kernel(BwdArgs a)
 #pragma unroll
   for (int q = 0; q < NDT; ++q) dzp[q] = 0.f;
   float dgc = 0.f;   // thread t < D: sum_n S[t][n] dS'[t][n]
+
+  // Phase 1's dk and dG terms reach phase 2 (same thread, same positions)
+  // through LDS past phase 2's buffers, not through dk and dg in memory.
+  float* const sAcc = sm + kC * PT + 2 * kC * PX;   // [2][64][D]: dk, dG
+  static_assert(kC * PT + 2 * kC * PX + 2 * kC * D <= SMEM_FLOATS, "phase 1 -> 2 accumulators");
 
   // ---- phase 1: dY = v~ dS'^T, dgq = do S^T, dW = -dv~ S^T (K = dv in passes of HW)
   f4 dW[NDT];
@@ -732,11 +737,9 @@ __global__ __launch_bounds__(kChunkThreads) void kda_bwd_chunk_kernel(BwdArgs a)
         const float gam = ex2(gl[i]), lam = ex2(glast - gl[i]);
         const float dz = dY[q][i] * kv[i] * lam;
         dzp[q] += dz;
-        if (c < cr.len) {
-          gq_[in_idx(c, d)] = dgq[q][i] * gam * a.scale;
-          gk_[in_idx(c, d)] = dY[q][i] * lam;
-          gG_[in_idx(c, d)] = dgq[q][i] * qv[i] * gam - dz;
-        }
+        if (c < cr.len) gq_[in_idx(c, d)] = dgq[q][i] * gam * a.scale;
+        sAcc[c * D + d] = dY[q][i] * lam;
+        sAcc[(kC + c) * D + d] = dgq[q][i] * qv[i] * gam - dz;
       }
     }
   }
@@ -785,8 +788,8 @@ __global__ __launch_bounds__(kChunkThreads) void kda_bwd_chunk_kernel(BwdArgs a)
         gl[q] = GL[c * D + d];
         kv[q] = ld_k(c, d);
         vv[q] = ld_v(c, d);
-        oG[q] = live ? gG_[in_idx(c, d)] : 0.f;
-        ok[q] = live ? gk_[in_idx(c, d)] : 0.f;
+        oG[q] = sAcc[(kC + c) * D + d];
+        ok[q] = sAcc[c * D + d];
       }
 #pragma unroll
       for (int q = 0; q < NDT; ++q) {
@@ -800,6 +803,7 @@ __global__ __launch_bounds__(kChunkThreads) void kda_bwd_chunk_kernel(BwdArgs a)
         }
       }
     }
+    __syncthreads();   // sAcc read before phase 3's operands overwrite it
   }
 
   // ---- phase 3: dL = strict(-(Yw W^T + Yu U^T)), dAqk = tril(do v~^T); [64][64]
