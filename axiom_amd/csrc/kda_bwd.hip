@@ -237,12 +237,19 @@ __device__ __forceinline__ f4 mfma4(float a, float b, f4 c) {
   return __builtin_amdgcn_mfma_f32_16x16x4f32(a, b, c, 0, 0, 0);
 }
 
+// The chunk's channels are taken in halves of 64 (d = 128) so the shared
+// memory fits two workgroups per CU: the scores accumulate over the halves in
+// registers, T = (I+L)^-1 is built once, and W, U are formed per half of
+// their columns (the last half's k and G still staged, the other reloaded).
 template <int D, int DTQ, int DTG>
-__global__ __launch_bounds__(kPrepThreads) void kda_bwd_prep_kernel(BwdArgs a) {
-  constexpr int P = D + 2;            // [64][D] pitch: row fragments conflict-free
+__global__ __launch_bounds__(kPrepThreads, 4) void kda_bwd_prep_kernel(BwdArgs a) {
+  constexpr int HD = 64;              // channels per half
+  constexpr int NHALF = D / HD;
+  constexpr int P = HD + 2;           // [64][HD] pitch: row fragments conflict-free
   constexpr int PC = kC + 1;
-  __shared__ float sQ[kC * P], sK[kC * P], sG[kC * P];
-  __shared__ float sL[kC * PC], sT[kC * PC];
+  static_assert(kC * PC <= kC * P, "T shares sQ's buffer");
+  __shared__ float sQ[kC * P], sK[kC * P], sG[kC * P];   // one channel half; sQ then holds T
+  __shared__ float sL[kC * PC];       // L, then one half of beta*v
   __shared__ float sTmp[768];         // the triangular inversion's scratch
   __shared__ float sB[kC];
   constexpr int NTH = kPrepThreads;
@@ -252,61 +259,94 @@ __global__ __launch_bounds__(kPrepThreads) void kda_bwd_prep_kernel(BwdArgs a) {
   const int u = blockIdx.x / H, h = blockIdx.x - u * H;
   const ChunkRows cr = chunk_rows(a, u);
   const int64_t ch = static_cast<int64_t>(u) * H + h;
+  float* const sT = sQ;
 
-  lds_load_in<DTQ, D, D, P, NTH>(sQ, a.q, cr.row0, cr.len, H, h, 0, a.scale);
-  lds_load_in<DTQ, D, D, P, NTH>(sK, a.k, cr.row0, cr.len, H, h, 0, 1.f);
-  lds_load_in<DTG, D, D, P, NTH>(sG, a.g, cr.row0, cr.len, H, h, 0, 1.f);
-  if (t < kC) sB[t] = (t < cr.len) ? ld1<DTG>(a.beta, (cr.row0 + t) * H + h) : 0.f;
-  __syncthreads();
-  // in-chunk inclusive cumsum of g, in log2 units
-  if (t < D) {
-    float col[kC];
+  // k and the in-chunk inclusive cumsum of g (log2 units) of channel half c0
+  auto stage_k_g = [&](int c0) {
+    lds_load_in<DTQ, D, HD, P, NTH>(sK, a.k, cr.row0, cr.len, H, h, c0, 1.f);
+    lds_load_in<DTG, D, HD, P, NTH>(sG, a.g, cr.row0, cr.len, H, h, c0, 1.f);
+  };
+  auto cumsum_g = [&]() {            // 16 rows' loads in flight at a time
+    if (t < HD) {
+      float acc = 0.f;
 #pragma unroll
-    for (int c = 0; c < kC; ++c) col[c] = sG[c * P + t];
-    float acc = 0.f;
+      for (int r0 = 0; r0 < kC; r0 += 16) {
+        float col[16];
 #pragma unroll
-    for (int c = 0; c < kC; ++c) {
-      acc += col[c];
-      sG[c * P + t] = acc * kLog2e;
+        for (int c = 0; c < 16; ++c) col[c] = sG[(r0 + c) * P + t];
+#pragma unroll
+        for (int c = 0; c < 16; ++c) {
+          acc += col[c];
+          sG[(r0 + c) * P + t] = acc * kLog2e;
+        }
+      }
+    }
+  };
+
+  // scores: Aqk (c >= i) to the workspace, L = beta_c Akk (c > i) to LDS,
+  // accumulated over the channel halves.  Off-diagonal tile pairs (row tile
+  // R > key tile s) on the matrix cores, one pair per wave (waves 0..5), the
+  // decay factored at the row tile's first row a: 2^(G_c - G_i) =
+  // 2^(G_c - G_a) 2^(G_a - G_i), both <= 1, applied to each operand element as
+  // it is read.  Diagonal tiles take 2^(G_c - G_i) per element, (c, i) slots
+  // spread over all threads.
+  const int R_off = (wv < 1) ? 1 : (wv < 3) ? 2 : 3;
+  const int sk_off = wv - R_off * (R_off - 1) / 2;
+  f4 accA = {0.f, 0.f, 0.f, 0.f}, accL = {0.f, 0.f, 0.f, 0.f};
+  float dA[2] = {0.f, 0.f}, dL[2] = {0.f, 0.f};
+  for (int hf = 0; hf < NHALF; ++hf) {
+    const int c0 = HD * hf;
+    if (hf > 0) __syncthreads();      // the previous half's reads are done
+    lds_load_in<DTQ, D, HD, P, NTH>(sQ, a.q, cr.row0, cr.len, H, h, c0, a.scale);
+    stage_k_g(c0);
+    if (hf == 0 && t < kC) sB[t] = (t < cr.len) ? ld1<DTG>(a.beta, (cr.row0 + t) * H + h) : 0.f;
+    __syncthreads();
+    cumsum_g();
+    __syncthreads();
+    {
+      float* GL = a.GL + ch * kC * D + c0;
+      float* QG = a.QG + ch * kC * D + c0;
+      float* KL = a.KL + ch * kC * D + c0;
+      for (int e = t; e < kC * HD; e += NTH) {
+        const int c = e / HD, d = e - c * HD;
+        const float gl = sG[c * P + d];
+        const float glast = sG[(kC - 1) * P + d];
+        GL[c * D + d] = gl;
+        QG[c * D + d] = ex2(gl) * sQ[c * P + d];
+        KL[c * D + d] = ex2(glast - gl) * sK[c * P + d];
+      }
+      if (t < HD) a.GCV[ch * D + c0 + t] = ex2(sG[(kC - 1) * P + t]);
+    }
+    if (wv < 6) {
+      const int a0 = 16 * R_off, i = 16 * sk_off + r16;
+#pragma unroll 8
+      for (int k = 0; k < HD / 4; ++k) {
+        const int d = 4 * k + gq;
+        const float ga = sG[a0 * P + d];
+        const float fa = ex2(sG[(a0 + r16) * P + d] - ga);
+        const float bk = sK[i * P + d] * ex2(ga - sG[i * P + d]);
+        accA = mfma4(sQ[(a0 + r16) * P + d] * fa, bk, accA);
+        accL = mfma4(sK[(a0 + r16) * P + d] * fa, bk, accL);
+      }
+    }
+#pragma unroll
+    for (int j = 0; j < 2; ++j) {
+      const int p = t + NTH * j;               // 4 diagonal tiles x 256 slots
+      const int R = p >> 8, rc = (p >> 4) & 15, ri = p & 15;
+      const int c = 16 * R + rc, i = 16 * R + ri;
+      if (ri <= rc) {
+#pragma unroll 4
+        for (int d = 0; d < HD; ++d) {
+          const float ki = sK[i * P + d] * ex2(sG[c * P + d] - sG[i * P + d]);
+          dA[j] = fmaf(sQ[c * P + d], ki, dA[j]);
+          dL[j] = fmaf(sK[c * P + d], ki, dL[j]);
+        }
+      }
     }
   }
-  __syncthreads();
-  {
-    float* GL = a.GL + ch * kC * D;
-    float* QG = a.QG + ch * kC * D;
-    float* KL = a.KL + ch * kC * D;
-    for (int e = t; e < kC * D; e += NTH) {
-      const int c = e / D, d = e - c * D;
-      const float gl = sG[c * P + d];
-      const float glast = sG[(kC - 1) * P + d];
-      GL[e] = gl;
-      QG[e] = ex2(gl) * sQ[c * P + d];
-      KL[e] = ex2(glast - gl) * sK[c * P + d];
-    }
-    if (t < D) a.GCV[ch * D + t] = ex2(sG[(kC - 1) * P + t]);
-  }
-
-  // scores: Aqk (c >= i) to the workspace, L = beta_c Akk (c > i) to LDS.
-  // Off-diagonal tile pairs (row tile R > key tile s) on the matrix cores,
-  // one pair per wave (waves 0..5), the decay factored at the row tile's
-  // first row a: 2^(G_c - G_i) = 2^(G_c - G_a) 2^(G_a - G_i), both <= 1,
-  // applied to each operand element as it is read.  Diagonal tiles take
-  // 2^(G_c - G_i) per element, (c, i) slots spread over all threads.
   float* AQ = a.AQ + ch * kC * kC;
   if (wv < 6) {
-    const int R = (wv < 1) ? 1 : (wv < 3) ? 2 : 3;
-    const int sk = wv - R * (R - 1) / 2;
-    const int a0 = 16 * R, i = 16 * sk + r16;
-    f4 accA = {0.f, 0.f, 0.f, 0.f}, accL = {0.f, 0.f, 0.f, 0.f};
-#pragma unroll 8
-    for (int k = 0; k < D / 4; ++k) {
-      const int d = 4 * k + gq;
-      const float ga = sG[a0 * P + d];
-      const float fa = ex2(sG[(a0 + r16) * P + d] - ga);
-      const float bk = sK[i * P + d] * ex2(ga - sG[i * P + d]);
-      accA = mfma4(sQ[(a0 + r16) * P + d] * fa, bk, accA);
-      accL = mfma4(sK[(a0 + r16) * P + d] * fa, bk, accL);
-    }
+    const int a0 = 16 * R_off, i = 16 * sk_off + r16;
 #pragma unroll
     for (int e = 0; e < 4; ++e) {
       const int c = a0 + 4 * gq + e;
@@ -316,20 +356,11 @@ __global__ __launch_bounds__(kPrepThreads) void kda_bwd_prep_kernel(BwdArgs a) {
   }
 #pragma unroll
   for (int j = 0; j < 2; ++j) {
-    const int p = t + NTH * j;                 // 4 diagonal tiles x 256 slots
+    const int p = t + NTH * j;
     const int R = p >> 8, rc = (p >> 4) & 15, ri = p & 15;
     const int c = 16 * R + rc, i = 16 * R + ri;
-    float accA = 0.f, accL = 0.f;
-    if (ri <= rc) {
-#pragma unroll 4
-      for (int d = 0; d < D; ++d) {
-        const float ki = sK[i * P + d] * ex2(sG[c * P + d] - sG[i * P + d]);
-        accA = fmaf(sQ[c * P + d], ki, accA);
-        accL = fmaf(sK[c * P + d], ki, accL);
-      }
-    }
-    AQ[c * kC + i] = accA;
-    sL[c * PC + i] = (ri < rc) ? accL * sB[c] : 0.f;
+    AQ[c * kC + i] = (ri <= rc) ? dA[j] : 0.f;
+    sL[c * PC + i] = (ri < rc) ? dL[j] * sB[c] : 0.f;
   }
   // blocks above the diagonal: zero
   for (int e = t; e < 6 * 256; e += NTH) {
@@ -342,7 +373,7 @@ __global__ __launch_bounds__(kPrepThreads) void kda_bwd_prep_kernel(BwdArgs a) {
   }
   __syncthreads();
 
-  // T = (I + L)^-1
+  // T = (I + L)^-1 (into sQ's buffer: q is no longer read)
   invert_unit_lower64<PC, NTH>(sL, sT, sTmp);
   {
     float* TM = a.TM + ch * kC * kC;
@@ -351,18 +382,27 @@ __global__ __launch_bounds__(kPrepThreads) void kda_bwd_prep_kernel(BwdArgs a) {
       TM[e] = sT[c * PC + i];
     }
   }
-  // W = T (beta gamma k), U = T (beta v) on the matrix cores: wave wv owns
-  // row tile wv / 2 and column tiles (wv % 2) D/32 + q
-  lds_load_in<DTQ, D, D, P, NTH>(sQ, a.v, cr.row0, cr.len, H, h, 0, 1.f);
-  __syncthreads();
-  for (int e = t; e < kC * D; e += NTH) {
-    const int c = e / D, d = e - c * D;
-    sK[c * P + d] *= sB[c] * ex2(sG[c * P + d]);
-    sQ[c * P + d] *= sB[c];
-  }
-  __syncthreads();
-  {
-    constexpr int NDT = D / 32;
+  // W = T (beta gamma k), U = T (beta v) on the matrix cores, per half of
+  // their columns (the last half first: its k and G are still staged); wave
+  // wv owns row tile wv / 2 and column tiles (wv % 2) HD/32 + q of the half
+  float* const sV = sL;               // beta * v of the half, pitch PC
+  for (int pass = 0; pass < NHALF; ++pass) {
+    const int c0 = HD * (NHALF - 1 - pass);
+    if (pass > 0) {
+      __syncthreads();                // the previous pass's products are done
+      stage_k_g(c0);
+      __syncthreads();
+      cumsum_g();
+    }
+    lds_load_in<DTQ, D, HD, PC, NTH>(sV, a.v, cr.row0, cr.len, H, h, c0, 1.f);
+    __syncthreads();
+    for (int e = t; e < kC * HD; e += NTH) {
+      const int c = e / HD, d = e - c * HD;
+      sK[c * P + d] *= sB[c] * ex2(sG[c * P + d]);
+      sV[c * PC + d] *= sB[c];
+    }
+    __syncthreads();
+    constexpr int NDT = HD / 32;
     const int mt = wv >> 1, dg = wv & 1;
     f4 accW[NDT], accU[NDT];
 #pragma unroll
@@ -374,13 +414,13 @@ __global__ __launch_bounds__(kPrepThreads) void kda_bwd_prep_kernel(BwdArgs a) {
       const float at = sT[(16 * mt + r16) * PC + 4 * k + gq];
 #pragma unroll
       for (int q = 0; q < NDT; ++q) {
-        const int kb = (4 * k + gq) * P + 16 * (dg * NDT + q) + r16;
-        accW[q] = mfma4(at, sK[kb], accW[q]);
-        accU[q] = mfma4(at, sQ[kb], accU[q]);
+        const int col = 16 * (dg * NDT + q) + r16;
+        accW[q] = mfma4(at, sK[(4 * k + gq) * P + col], accW[q]);
+        accU[q] = mfma4(at, sV[(4 * k + gq) * PC + col], accU[q]);
       }
     }
-    float* WM = a.WM + ch * kC * D;
-    float* UM = a.UM + ch * kC * D;
+    float* WM = a.WM + ch * kC * D + c0;
+    float* UM = a.UM + ch * kC * D + c0;
 #pragma unroll
     for (int q = 0; q < NDT; ++q)
 #pragma unroll
