@@ -159,12 +159,13 @@ def _layer_ref(xs, ws, bufs, g, beta, z, h0, dy, dht, H, scale, eps, in_dt, g_dt
                 dbq=db[0], dbk=db[1], dbv=db[2], dh0=dh0)
 
 
-@pytest.mark.parametrize("B,T,H,d,K,prec", [
-    (1, 100, 2, 64, 4, "fp32"),
-    (2, 130, 2, 128, 4, "bf16"),
-    (1, 70, 1, 64, 6, "bf16"),        # K > 4: the forward's prologue runs as its own pass
+@pytest.mark.parametrize("B,T,H,d,K,prec,carried", [
+    (1, 100, 2, 64, 4, "fp32", True),
+    (2, 130, 2, 128, 4, "bf16", True),
+    (1, 70, 1, 64, 6, "bf16", True),      # K > 4: the forward's prologue runs as its own pass
+    (2, 77, 2, 128, 4, "bf16", False),    # no conv buffers, no initial state
 ])
-def test_layer_autograd_matches_oracle(cuda, B, T, H, d, K, prec):
+def test_layer_autograd_matches_oracle(cuda, B, T, H, d, K, prec, carried):
     import axiom_amd
     in_dt = torch.float32 if prec == "fp32" else torch.bfloat16
     x = inputs.make_inputs(B, T, H, d, d, seed=T + K, dtype="fp32", h0_std=0.05)
@@ -183,20 +184,24 @@ def test_layer_autograd_matches_oracle(cuda, B, T, H, d, K, prec):
     g_t, b_t = leaf(x["g"], in_dt), leaf(x["beta"], in_dt)
     z_t = leaf(z, in_dt)
     ws_t = [leaf(a, torch.float32) for a in ws]
-    st = [leaf(a, torch.float32) for a in bufs]
-    h0_t = leaf(x["h0"], torch.float32)
-    y, ht = axiom_amd.kda_layer(*xs_t, g_t, b_t, z_t, *ws_t, conv_state=tuple(st), initial_state=h0_t,
-                                scale=scale, eps=eps)
+    st = [leaf(a, torch.float32) for a in bufs] if carried else None
+    h0_t = leaf(x["h0"], torch.float32) if carried else None
+    y, ht = axiom_amd.kda_layer(*xs_t, g_t, b_t, z_t, *ws_t, conv_state=None if st is None else tuple(st),
+                                initial_state=h0_t, scale=scale, eps=eps)
     assert y.dtype == in_dt and ht.dtype == torch.float32
     loss = (y.float() * torch.from_numpy(dy).to(cuda)).sum() + (ht * torch.from_numpy(dht).to(cuda)).sum()
     loss.backward()
     torch.cuda.synchronize()
     # y.float()'s VJP hands the layer dy rounded to y's dtype
-    ref = _layer_ref(xs, ws, bufs, x["g"], x["beta"], z, x["h0"], _as(dy, in_dt), dht.astype(np.float64),
-                     H, scale, eps, in_dt, in_dt)
+    ref = _layer_ref(xs, ws, bufs if carried else None, x["g"], x["beta"], z, x["h0"] if carried else None,
+                     _as(dy, in_dt), dht.astype(np.float64), H, scale, eps, in_dt, in_dt)
     got = dict(dqp=xs_t[0].grad, dkp=xs_t[1].grad, dvp=xs_t[2].grad, dg=g_t.grad, dbeta=b_t.grad, dgate=z_t.grad,
-               dwq=ws_t[0].grad, dwk=ws_t[1].grad, dwv=ws_t[2].grad, dbq=st[0].grad, dbk=st[1].grad,
-               dbv=st[2].grad, dh0=h0_t.grad)
+               dwq=ws_t[0].grad, dwk=ws_t[1].grad, dwv=ws_t[2].grad)
+    if carried:
+        got.update(dbq=st[0].grad, dbk=st[1].grad, dbv=st[2].grad, dh0=h0_t.grad)
+    else:
+        for n in ("dbq", "dbk", "dbv", "dh0"):
+            ref.pop(n)
     rel, mx = (1e-4, 1e-4) if prec == "fp32" else (1e-2, 5e-2)
     for name, r in ref.items():
         assert got[name] is not None, name
