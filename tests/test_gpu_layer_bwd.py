@@ -159,15 +159,17 @@ def _layer_ref(xs, ws, bufs, g, beta, z, h0, dy, dht, H, scale, eps, in_dt, g_dt
                 dbq=db[0], dbk=db[1], dbv=db[2], dh0=dh0)
 
 
-@pytest.mark.parametrize("B,T,H,d,K,prec,carried", [
-    (1, 100, 2, 64, 4, "fp32", True),
-    (2, 130, 2, 128, 4, "bf16", True),
-    (1, 70, 1, 64, 6, "bf16", True),      # K > 4: the forward's prologue runs as its own pass
-    (2, 77, 2, 128, 4, "bf16", False),    # no conv buffers, no initial state
+@pytest.mark.parametrize("B,T,H,d,K,prec,carried,gates32", [
+    (1, 100, 2, 64, 4, "fp32", True, False),
+    (2, 130, 2, 128, 4, "bf16", True, False),
+    (1, 70, 1, 64, 6, "bf16", True, False),      # K > 4: the forward's prologue runs as its own pass
+    (2, 77, 2, 128, 4, "bf16", False, False),    # no conv buffers, no initial state
+    (1, 90, 2, 128, 3, "bf16", True, True),      # bf16 projections with fp32 g and beta
 ])
-def test_layer_autograd_matches_oracle(cuda, B, T, H, d, K, prec, carried):
+def test_layer_autograd_matches_oracle(cuda, B, T, H, d, K, prec, carried, gates32):
     import axiom_amd
     in_dt = torch.float32 if prec == "fp32" else torch.bfloat16
+    g_dt = torch.float32 if gates32 else in_dt
     x = inputs.make_inputs(B, T, H, d, d, seed=T + K, dtype="fp32", h0_std=0.05)
     xs, ws, bufs, _ = _proj(B, T, H, d, K, seed=T * 3 + K)
     rng = np.random.default_rng(T)
@@ -181,7 +183,7 @@ def test_layer_autograd_matches_oracle(cuda, B, T, H, d, K, prec, carried):
         return torch.from_numpy(np.ascontiguousarray(a)).to(cuda, dt).requires_grad_(True)
 
     xs_t = [leaf(a, in_dt) for a in xs]
-    g_t, b_t = leaf(x["g"], in_dt), leaf(x["beta"], in_dt)
+    g_t, b_t = leaf(x["g"], g_dt), leaf(x["beta"], g_dt)
     z_t = leaf(z, in_dt)
     ws_t = [leaf(a, torch.float32) for a in ws]
     st = [leaf(a, torch.float32) for a in bufs] if carried else None
@@ -194,7 +196,7 @@ def test_layer_autograd_matches_oracle(cuda, B, T, H, d, K, prec, carried):
     torch.cuda.synchronize()
     # y.float()'s VJP hands the layer dy rounded to y's dtype
     ref = _layer_ref(xs, ws, bufs if carried else None, x["g"], x["beta"], z, x["h0"] if carried else None,
-                     _as(dy, in_dt), dht.astype(np.float64), H, scale, eps, in_dt, in_dt)
+                     _as(dy, in_dt), dht.astype(np.float64), H, scale, eps, in_dt, g_dt)
     got = dict(dqp=xs_t[0].grad, dkp=xs_t[1].grad, dvp=xs_t[2].grad, dg=g_t.grad, dbeta=b_t.grad, dgate=z_t.grad,
                dwq=ws_t[0].grad, dwk=ws_t[1].grad, dwv=ws_t[2].grad)
     if carried:
