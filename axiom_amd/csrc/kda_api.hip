@@ -6,6 +6,7 @@
 #include <cstdarg>
 #include <cstdio>
 #include <cstring>
+#include <numeric>
 
 #include "kda_common.h"
 #include "kda_internal.h"
@@ -54,10 +55,15 @@ size_t bytes_per_chunk_head(int dk, int dv, size_t es) {
 // intra-chunk results stay within this budget: on MI355X they are then read
 // back by the state kernel from the 256 MB last-level cache rather than
 // HBM, and the next segment overwrites them there.  Config 1 (B4 T4096 H16
-// d128, 304 MB of results) runs as 3 segments of 22 chunks: 282 us against
-// 305 us unsegmented (2 segments: 287 us; 4: 282 us; 6 or 8: 328 us, the
-// smaller intra grids then leave CUs idle).
+// d128, 304 MB of results) runs as 3 segments (282 us against 305 us
+// unsegmented when introduced; 2 segments: 287 us; 4: 282 us; 6 or 8:
+// 328 us, the smaller intra grids then leave CUs idle).
 constexpr double kSegmentBudgetBytes = 100.0 * 1048576.0;
+// Intra workgroups resident at once (two on each of the MI355X's 256 CUs).
+// A segment's chunk count is rounded up so its B * H * chunks workgroups fill
+// whole rounds of them (config 1: 24 + 24 + 16 chunks, 227.6 us, against
+// 22 + 22 + 20, 232.9 us, whose last round per segment ran a quarter empty).
+constexpr int kIntraSlots = 512;
 
 int dense_segments(int B, int T, int H, int dk, int dv, int in_dtype) {
   const int NT = (T + kC - 1) / kC;
@@ -78,9 +84,16 @@ WsLayout ws_layout(int B, int T, int H, int dk, int dv, int32_t n_seqs, int in_d
   if (n_seqs > 0) {
     units = (static_cast<int64_t>(T) + 63LL * n_seqs) / kC;
   } else {
+    const int NT = L.seg_chunks;
     L.segments = dense_segments(B, T, H, dk, dv, in_dtype);
     L.seg_chunks = (L.seg_chunks + L.segments - 1) / L.segments;
-    L.segments = (L.seg_chunks > 0) ? ((T + kC - 1) / kC + L.seg_chunks - 1) / L.seg_chunks : 1;
+    if (L.segments > 1) {
+      const int64_t bh = static_cast<int64_t>(B) * H;
+      const int m = static_cast<int>(kIntraSlots / std::gcd<int64_t>(kIntraSlots, bh));
+      const int up = (L.seg_chunks + m - 1) / m * m;
+      if (up < NT) L.seg_chunks = up;
+    }
+    L.segments = (L.seg_chunks > 0) ? (NT + L.seg_chunks - 1) / L.seg_chunks : 1;
     units = static_cast<int64_t>(B) * L.seg_chunks;
   }
   L.units_bound = units;

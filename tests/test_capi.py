@@ -10,6 +10,7 @@ CPU tensors (no fallback) is checked too.
 from __future__ import annotations
 
 import ctypes
+import math
 import subprocess
 
 import pytest
@@ -36,6 +37,9 @@ def _align(x):
 SEGMENT_BUDGET = 100 * 1048576   # bytes of intra-chunk results per segment of a dense call
 
 
+INTRA_SLOTS = 512   # intra workgroups resident at once: segments are rounded up to whole rounds
+
+
 def dense_segments(B, T, H, dk, dv, es):
     NT = (T + C - 1) // C
     if NT <= 1:
@@ -43,6 +47,11 @@ def dense_segments(B, T, H, dk, dv, es):
     total = B * NT * H * (C * (3 * dk + dv + C) * es + dk * 4)
     s = min(max(-(-total // SEGMENT_BUDGET), 1), NT)
     seg = -(-NT // s)
+    if s > 1:
+        m = INTRA_SLOTS // math.gcd(INTRA_SLOTS, B * H)
+        up = -(-seg // m) * m
+        if up < NT:
+            seg = up
     return -(-NT // seg), seg
 
 
@@ -60,10 +69,11 @@ def dense_ws_bytes(B, T, H, dk, dv, es):
 
 
 def test_segment_policy():
-    # config 1: 304 MB of intra-chunk results -> 3 segments of 22 chunks
-    assert dense_segments(4, 4096, 16, 128, 128, 2) == (3, 22)
+    # config 1: 304 MB of intra-chunk results -> 3 segments; 22 chunks rounded
+    # up to 24 so each segment's 4 * 16 * 24 = 1536 intra workgroups are whole rounds
+    assert dense_segments(4, 4096, 16, 128, 128, 2) == (3, 24)
     assert dense_segments(2, 1000, 2, 128, 128, 2) == (1, 16)
-    assert dense_segments(1, 65536, 16, 128, 128, 2) == (12, 86)
+    assert dense_segments(1, 65536, 16, 128, 128, 2) == (11, 96)
 
 
 def varlen_ws_bytes(T, N, H, dk, dv, es):
