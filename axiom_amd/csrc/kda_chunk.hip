@@ -98,11 +98,6 @@ struct IntraSmem {
   float fac[4][5][DK];    // per tile: 2^pre, 2^post, 2^-D, M(w,w-2), M(w,w-3)
 };
 
-// slot index (position in a lane-group-major row) of channel d
-__device__ __forceinline__ int channel_slot(int d) {
-  const int jd = d >> 5, wd = d & 31;
-  return 32 * jd + 8 * ((wd & 15) >> 2) + 4 * (wd >> 4) + (wd & 3);
-}
 // channel of slot index s
 __device__ __forceinline__ int slot_index_channel(int s) {
   return slot_channel(s >> 5, (s >> 3) & 3, s & 7);
@@ -1221,10 +1216,6 @@ __device__ __forceinline__ void static_for(F&& f) {
     f(std::integral_constant<int, B>{});
     static_for<B + 1, E>(f);
   }
-}
-
-__device__ __forceinline__ h8 lds_frag(const unsigned char* buf, int f, int l) {
-  return *reinterpret_cast<const h8*>(buf + f * 1024 + l * 16);
 }
 
 // o of row tiles 0..3 (D layout: rows 16ct + 4gq + i, column r of value tile

@@ -35,12 +35,6 @@ __device__ __forceinline__ float pl_ld(const void* p, int64_t i) {
   else return bf16_to_f32(static_cast<const u16*>(p)[i]);
 }
 
-template <int DT>
-__device__ __forceinline__ void pl_st(void* p, int64_t i, float v) {
-  if constexpr (DT == 0) static_cast<float*>(p)[i] = v;
-  else static_cast<u16*>(p)[i] = cvt_bf16(v);
-}
-
 __device__ __forceinline__ float wave_sum(float x) {
 #pragma unroll
   for (int off = 32; off >= 1; off >>= 1) x += __shfl_xor(x, off, 64);
