@@ -252,22 +252,27 @@ int chunk_fwd_impl(hipStream_t stream, const void* q, const void* k, const void*
 // ----------------------------------------------------------------------------
 namespace kda {
 
+// Grid-strided: g element by element (consecutive threads, consecutive
+// elements), beta one token-head per thread (its 32 columns summed in column
+// order).
 __global__ __launch_bounds__(256) void kda_adapt_kernel(AdaptArgs a) {
-  const int64_t i = static_cast<int64_t>(blockIdx.x) * 256 + threadIdx.x;  // token-head
-  if (i >= a.n_tok_heads) return;
-  const float* al = a.alpha + i * a.dk;
-  float* go = a.g_out + i * a.dk;
-  for (int d = 0; d < a.dk; ++d) go[d] = logf(al[d]);
-  const float* b = a.beta32 + i * 32;
-  float s = 0.f;
-  for (int j = 0; j < 32; ++j) s += b[j];
-  a.beta_out[i] = s * (1.0f / 32.0f);
+  const int64_t stride = static_cast<int64_t>(gridDim.x) * 256;
+  const int64_t i0 = static_cast<int64_t>(blockIdx.x) * 256 + threadIdx.x;
+  const int64_t n = a.n_tok_heads * a.dk;
+  for (int64_t i = i0; i < n; i += stride) a.g_out[i] = logf(a.alpha[i]);
+  for (int64_t th = i0; th < a.n_tok_heads; th += stride) {
+    const float* b = a.beta32 + th * 32;
+    float s = 0.f;
+    for (int j = 0; j < 32; ++j) s += b[j];
+    a.beta_out[th] = s * (1.0f / 32.0f);
+  }
 }
 
 hipError_t launch_adapt(const AdaptArgs& a, hipStream_t s) {
   if (a.n_tok_heads == 0) return hipSuccess;
-  const int64_t grid = (a.n_tok_heads + 255) / 256;
-  hipLaunchKernelGGL(kda_adapt_kernel, dim3(static_cast<unsigned>(grid)), dim3(256), 0, s, a);
+  const int64_t need = (a.n_tok_heads * a.dk + 255) / 256;
+  const int grid = static_cast<int>(need < 8192 ? need : 8192);
+  hipLaunchKernelGGL(kda_adapt_kernel, dim3(grid), dim3(256), 0, s, a);
   return hipGetLastError();
 }
 

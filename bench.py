@@ -36,6 +36,9 @@ Also reported on the same JSON line:
 * ``decode_layer``: the layer decode step (prologue, recurrent step,
   epilogue) per token, eager against a HIP graph of 64 tokens, at B=1 and
   B=256;
+* ``cc_scan_seam``: the reference's seam ``cc_scan`` and its backward rule
+  ``cc_scan_bwd`` on one batch element of config 1 (alpha / beta32 operands,
+  the reference's call shape), per call;
 * ``ut_solve``: the standalone unit-triangular solve at the reference's case
   (H=12, C=64, N=dk+dv=256, fp32), both orientations, per call;
 * ``cpu_baseline``: the oracle's fp32 restatement of the reference jax body
@@ -379,6 +382,42 @@ def bench_layer_bwd(args, fwd_inputs, device):
         config="B4 T4096 H16 d128 K4, bf16 projections, gate and dy; the whole backward recomputes q, k, v, o")
 
 
+def bench_cc_scan(args, fwd_inputs, device):
+    """The reference's own seam (``cc_scan`` and its backward rule) on one batch
+    element of config 1 -- how the reference calls it, vmapped over B -- with
+    the alpha / beta32 operands: the adapter (g = log alpha, beta = mean of the
+    32 columns) plus the dense kernels."""
+    import axiom_amd
+    q, k, v, g, beta = fwd_inputs
+    _, T, H, d = q.shape
+    q2, k2, v2 = (x[0].reshape(T, H * d).contiguous() for x in (q, k, v))
+    alpha = torch.exp(g[0].float()).reshape(T, H * d).contiguous()
+    beta32 = beta[0].float().reshape(T, H, 1).expand(T, H, 32).reshape(T, H * 32).contiguous()
+    S = torch.zeros(H, d, d, device=device)
+    gen = torch.Generator(device=device)
+    gen.manual_seed(args.seed + 9)
+    do = torch.randn(T, H * d, device=device, generator=gen)
+    dS = torch.randn(H, d, d, device=device, generator=gen) * 0.1
+    stream = torch.cuda.current_stream(device)
+
+    def timed(f, steps):
+        for _ in range(3):
+            f()
+        torch.cuda.synchronize()
+        e0, e1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+        e0.record(stream)
+        for _ in range(steps):
+            f()
+        e1.record(stream)
+        torch.cuda.synchronize()
+        return e0.elapsed_time(e1) / 1e3 / steps
+    t_f = timed(lambda: axiom_amd.cc_scan(q2, k2, v2, alpha, beta32, S, tile=16, chunk=64), args.steps)
+    t_b = timed(lambda: axiom_amd.cc_scan_bwd(q2, k2, v2, alpha, beta32, S, do, dS, tile=16, chunk=64),
+                args.bwd_steps)
+    return dict(fwd_us_per_call=t_f * 1e6, bwd_us_per_call=t_b * 1e6, tokens_per_s_fwd=T / t_f,
+                config=f"one batch element: T{T} H{H} d{d}, bf16 q/k/v, fp32 alpha/beta32/S (cc_scan, cc_scan_bwd)")
+
+
 def bench_ut_solve(args, device):
     import axiom_amd
     H, C, N = 12, 64, 256
@@ -555,6 +594,7 @@ def main():
     if not args.no_backward:
         line["layer_backward"] = bench_layer_bwd(args, fwd["inputs"], device)
     line["decode_layer"] = bench_decode_layer(args, device)
+    line["cc_scan_seam"] = bench_cc_scan(args, fwd["inputs"], device)
     line["ut_solve"] = bench_ut_solve(args, device)
     if args.other_configs:
         line["other_configs"] = bench_other_configs(args, device)
