@@ -1,7 +1,8 @@
 """The entry points inside HIP graphs (torch.cuda.CUDAGraph on ROCm).
 
 No compute entry point allocates, synchronises or sets memory with
-hipMemsetAsync, so a caller can capture them on its stream.  Each test
+hipMemsetAsync, so a caller can capture them on its stream: the chunked
+forward, a run of layer decode steps, and the layer's backward chain.  Each test
 captures a sequence of calls, replays the graph several times with the
 program's own eager work and synchronisations between the replays, and checks
 every replay against the eager result bit for bit.
@@ -100,3 +101,45 @@ def test_decode_layer_steps_graph_replays_match_eager(cuda):
         for b, br in zip(bufs, bufs_ref):
             assert torch.equal(b, br), f"replay {rep} conv buffer"
         _ = (state * 2.0).sum().item()   # the program's own eager work between replays
+
+
+def test_layer_backward_chain_graph_replays_match_eager(cuda):
+    """kda_epilogue_bwd -> kda_chunk_bwd -> kda_prologue_bwd (the layer's
+    backward after the recompute) captured in one graph."""
+    import axiom_amd
+    from axiom_amd import kda as kmod
+    B, T, H, d, K = 2, 150, 2, 128, 4
+    rng = np.random.default_rng(44)
+    bf = torch.bfloat16
+    xs = [to_dev(rng.standard_normal((B, T, H * d)).astype(np.float32), bf, cuda) for _ in range(3)]
+    ws_ = [to_dev((rng.standard_normal((K, H * d)) * 0.4).astype(np.float32), torch.float32, cuda) for _ in range(3)]
+    bufs = tuple(to_dev(rng.standard_normal((B, K - 1, H * d)).astype(np.float32), torch.float32, cuda)
+                 for _ in range(3))
+    base = inputs.make_inputs(B, T, H, d, d, seed=45, dtype="bf16")
+    g, beta = to_dev(base["g"], bf, cuda), to_dev(base["beta"], bf, cuda)
+    gate = to_dev(rng.standard_normal((B, T, H * d)).astype(np.float32), bf, cuda)
+    dy = to_dev(rng.standard_normal((B, T, H * d)).astype(np.float32), bf, cuda)
+    q, k, v, _ = axiom_amd.kda_prologue(*xs, *ws_, H, conv_state=bufs, return_state=False)
+    o, _ = axiom_amd.kda_chunk_fwd(q, k, v, g, beta, output_final_state=False)
+    bws = torch.empty(kmod.chunk_bwd_workspace_bytes(B, T, H, d, d), dtype=torch.uint8, device=cuda)
+    pws = torch.empty(kmod.prologue_bwd_workspace_bytes(B, T, H, d, K), dtype=torch.uint8, device=cuda)
+
+    def run():
+        do, dgate = axiom_amd.kda_epilogue_bwd(o, gate, dy)
+        dq, dk, dv, dg, dbeta, _ = axiom_amd.kda_chunk_bwd(q, k, v, g, beta, do, need_dh0=False, workspace=bws)
+        dx, dw, db = axiom_amd.kda_prologue_bwd(*xs, *ws_, dq, dk, dv, conv_state=bufs, workspace=pws)
+        return [dgate, dg, dbeta, *dx, *dw, *db]
+
+    ref = [t.clone() for t in run()]
+    torch.cuda.synchronize()
+    graph, outs = _capture(run)
+    for rep in range(3):
+        for t in outs:
+            t.zero_()
+        torch.cuda.synchronize()
+        graph.replay()
+        torch.cuda.synchronize()
+        for i, (got, want) in enumerate(zip(outs, ref)):
+            assert torch.equal(got, want), f"replay {rep} output {i}"
+        run()   # eager work on the same workspaces between replays
+        torch.cuda.synchronize()
