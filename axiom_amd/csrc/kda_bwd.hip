@@ -18,8 +18,10 @@
 //   kda_bwd_chunk_kernel  one workgroup per chunk-head: the rest of the adjoint
 //                         (dY, dgq, dW, the two transposed solves, dL, dAqk, the
 //                         score adjoints, the cumsum adjoint) and the outputs.
-// Every dense product runs on the fp32 matrix cores (v_mfma_f32_16x16x4f32:
-// exact fp32 products, fp32 sums), operands staged through LDS; decay factors
+// The dense products run on the fp32 matrix cores (v_mfma_f32_16x16x4f32:
+// exact fp32 products, fp32 sums), except the forward scan's, which run as
+// bf16 hi/lo triples (about 2^-16 of each product dropped); operands are
+// staged through LDS; decay factors
 // of off-diagonal 16-row tiles are anchored at the row tile's first row
 // (2^(G_c - G_a) * 2^(G_a - G_i), both <= 1), diagonal tiles use
 // 2^(G_c - G_i) directly.  Workspace arrays are fp32, row-major, per
@@ -433,8 +435,9 @@ __global__ __launch_bounds__(kPrepThreads, 4) void kda_bwd_prep_kernel(BwdArgs a
 }
 
 // ---------------------------------------------------------------------------
-// The two scans run their products on the fp32 matrix cores
-// (v_mfma_f32_16x16x4f32, exact fp32 products): lane (r = l & 15, gq = l >> 4)
+// The reverse scan runs its products on the fp32 matrix cores
+// (v_mfma_f32_16x16x4f32, exact fp32 products; the forward scan's bf16 form
+// is described at it): lane (r = l & 15, gq = l >> 4)
 // supplies A[r][4s + gq] and B[4s + gq][r] of K step s and holds D rows
 // 4 gq + i, column r.  Eight waves per workgroup; the 32-column state slice is
 // (D/16) x 2 tiles in accumulators, D/64 tiles per wave; the [64][32] results
@@ -445,14 +448,37 @@ __global__ __launch_bounds__(kPrepThreads, 4) void kda_bwd_prep_kernel(BwdArgs a
 constexpr int kPB = 48;
 constexpr int kPA = kC + 16;
 
-// forward state scan of one (chain, 32-column slice): S_in and v~ per chunk
+// x0, x1 -> packed bf16 pairs hi (round to nearest even) and lo = bf16(x - hi)
+__device__ __forceinline__ void split2_bf16(float x0, float x1, unsigned& h, unsigned& l) {
+  h = pack_bf16x2(x0, x1);
+  l = pack_bf16x2(x0 - __uint_as_float(h << 16), x1 - __uint_as_float(h & 0xFFFF0000u));
+}
+// hi * hi + hi * lo + lo * hi of one 32-wide K block on the bf16 matrix cores
+// (products exact, sums fp32; the dropped lo * lo term and the rounding of lo
+// leave about 2^-16 of each product)
+__device__ __forceinline__ f4 mma3_bf16(f4 acc, const b8& ah, const b8& al, const b8& bh, const b8& bl) {
+  acc = mma32_bf16(acc, ah, bh);
+  acc = mma32_bf16(acc, ah, bl);
+  return mma32_bf16(acc, al, bh);
+}
+
+// forward state scan of one (chain, 32-column slice): S_in and v~ per chunk.
+// The products run as bf16 hi/lo triples (v_mfma_f32_16x16x32_bf16, lane
+// (r, gq) holding K values 8 gq .. 8 gq + 7 of each 32-wide block): W and
+// (lambda k)^T, the state slice S^T and v~^T are kept in LDS as hi and lo
+// bf16 planes with the K index contiguous, so each fragment is one 16-byte
+// read.  The state itself stays fp32 in the accumulators.
 template <int D>
 __global__ __launch_bounds__(kScanThreads) void kda_bwd_fscan_kernel(BwdArgs a) {
-  constexpr int PW = D + 2;
   constexpr int NS = D / 32;
   constexpr int NST = D / 64;   // state tiles per wave
-  __shared__ float sW[kC * PW], sKL[kC * PW];
-  __shared__ float sS[D * kPB], sU[kC * kPB], sV[kC * kPB], sGC[D];
+  constexpr int PW = D + 8;     // bf16 pitch of rows whose K index is a channel
+  constexpr int PK = kC + 8;    // bf16 pitch of rows whose K index is a chunk row
+  __shared__ __attribute__((aligned(16))) __bf16 sWh[kC * PW], sWl[kC * PW];    // W [64][D]
+  __shared__ __attribute__((aligned(16))) __bf16 sKh[D * PK], sKl[D * PK];      // (lambda k)^T [D][64]
+  __shared__ __attribute__((aligned(16))) __bf16 sSh[32 * PW], sSl[32 * PW];    // S^T [32][D]
+  __shared__ __attribute__((aligned(16))) __bf16 sVh[32 * PK], sVl[32 * PK];    // v~^T [32][64]
+  __shared__ float sU[kC * kPB], sGC[D];
   constexpr int NTH = kScanThreads;
   const int t = threadIdx.x, wv = t >> 6, l = t & 63, r = l & 15, gq = l >> 4;
   const int H = a.H;
@@ -474,12 +500,27 @@ __global__ __launch_bounds__(kScanThreads) void kda_bwd_fscan_kernel(BwdArgs a) 
                     : 0.f;
   // chunk n's W, lambda*k and U slice are loaded into registers during
   // chunk n-1's arithmetic
-  Tile<kC, D, NTH> tW, tK;
+  typedef Tile<kC, D, NTH> TD;
+  TD tW;
   Tile<kC, 32, NTH> tU;
+  // lambda*k, fetched for its transposed store: thread t holds rows 2 rp and
+  // 2 rp + 1 (rp = t % 32) of the column groups KCG j + t / 32, so each
+  // transposed row is written as packed row pairs, consecutive lanes at
+  // consecutive words
+  constexpr int KCG = NTH / 32;                    // column groups per pass
+  constexpr int KPER = (D / 4) / KCG;              // float4 column groups per thread
+  static_assert((D / 4) % KCG == 0, "lambda*k column groups");
+  float4 kq[KPER][2];
+  const int rp = t & 31, cg = t >> 5;
   auto fetch = [&](int n) {
     const int64_t ch = (static_cast<int64_t>(b) * a.NT + n) * H + h;
     tW.fetch(a.WM + ch * kC * D, D, 0);
-    tK.fetch(a.KL + ch * kC * D, D, 0);
+    const float* KLp = a.KL + ch * kC * D;
+#pragma unroll
+    for (int j = 0; j < KPER; ++j)
+#pragma unroll
+      for (int y = 0; y < 2; ++y)
+        kq[j][y] = *reinterpret_cast<const float4*>(KLp + (2 * rp + y) * D + 4 * (cg + KCG * j));
     tU.fetch(a.UM + ch * kC * D, D, c0);
   };
   if (a.NT > 0) fetch(0);
@@ -487,37 +528,69 @@ __global__ __launch_bounds__(kScanThreads) void kda_bwd_fscan_kernel(BwdArgs a) 
     const int64_t ch = (static_cast<int64_t>(b) * a.NT + n) * H + h;
     float* SI = a.SI + ch * D * D;
 #pragma unroll
-    for (int q = 0; q < NST; ++q)
+    for (int q = 0; q < NST; ++q) {
+      const int m0 = 16 * rt[q] + 4 * gq, col = 16 * cs[q] + r;
 #pragma unroll
-      for (int i = 0; i < 4; ++i) {
-        const int row = 16 * rt[q] + 4 * gq + i, col = 16 * cs[q] + r;
-        SI[row * D + c0 + col] = S[q][i];
-        sS[row * kPB + col] = S[q][i];
+      for (int i = 0; i < 4; ++i) SI[(m0 + i) * D + c0 + col] = S[q][i];
+      uint2 hh, ll;
+      split2_bf16(S[q][0], S[q][1], hh.x, ll.x);
+      split2_bf16(S[q][2], S[q][3], hh.y, ll.y);
+      *reinterpret_cast<uint2*>(&sSh[col * PW + m0]) = hh;
+      *reinterpret_cast<uint2*>(&sSl[col * PW + m0]) = ll;
+    }
+    // W row-major and lambda*k transposed, as hi / lo planes
+#pragma unroll
+    for (int p = 0; p < TD::PER; ++p) {
+      const int e = t + p * NTH;
+      const int row = e / TD::V, c4 = e - row * TD::V;
+      const float4 w = tW.r[p];
+      uint2 hh, ll;
+      split2_bf16(w.x, w.y, hh.x, ll.x);
+      split2_bf16(w.z, w.w, hh.y, ll.y);
+      *reinterpret_cast<uint2*>(&sWh[row * PW + 4 * c4]) = hh;
+      *reinterpret_cast<uint2*>(&sWl[row * PW + 4 * c4]) = ll;
+    }
+#pragma unroll
+    for (int j = 0; j < KPER; ++j) {
+      const int ch4 = 4 * (cg + KCG * j);
+      const float k0[4] = {kq[j][0].x, kq[j][0].y, kq[j][0].z, kq[j][0].w};
+      const float k1[4] = {kq[j][1].x, kq[j][1].y, kq[j][1].z, kq[j][1].w};
+#pragma unroll
+      for (int e = 0; e < 4; ++e) {
+        unsigned hh, ll;
+        split2_bf16(k0[e], k1[e], hh, ll);     // rows 2 rp, 2 rp + 1 of channel ch4 + e
+        *reinterpret_cast<unsigned*>(&sKh[(ch4 + e) * PK + 2 * rp]) = hh;
+        *reinterpret_cast<unsigned*>(&sKl[(ch4 + e) * PK + 2 * rp]) = ll;
       }
-    tW.template put<PW>(sW);
-    tK.template put<PW>(sKL);
+    }
     tU.template put<kPB>(sU);
     if (t < D) sGC[t] = a.GCV[ch * D + t];
     if (n + 1 < a.NT) fetch(n + 1);
     __syncthreads();
-    // v~ = U - W S (two accumulation chains over K = D)
+    // v~ = U - W S (two accumulation chains over the D / 32 K blocks)
     {
-      f4 acc0, acc1 = {0.f, 0.f, 0.f, 0.f};
+      f4 acc0 = {0.f, 0.f, 0.f, 0.f}, acc1 = {0.f, 0.f, 0.f, 0.f};
 #pragma unroll
-      for (int i = 0; i < 4; ++i) acc0[i] = sU[(16 * mt + 4 * gq + i) * kPB + 16 * ct + r];
-#pragma unroll 8
-      for (int k = 0; k < D / 4; k += 2) {
-        acc0 = mfma4(-sW[(16 * mt + r) * PW + 4 * k + gq], sS[(4 * k + gq) * kPB + 16 * ct + r], acc0);
-        acc1 = mfma4(-sW[(16 * mt + r) * PW + 4 * k + 4 + gq], sS[(4 * k + 4 + gq) * kPB + 16 * ct + r], acc1);
+      for (int kb = 0; kb < D / 32; ++kb) {
+        const int ka = (16 * mt + r) * PW + 32 * kb + 8 * gq, kbb = (16 * ct + r) * PW + 32 * kb + 8 * gq;
+        const b8 ah = *reinterpret_cast<const b8*>(&sWh[ka]), al = *reinterpret_cast<const b8*>(&sWl[ka]);
+        const b8 bh = *reinterpret_cast<const b8*>(&sSh[kbb]), bl = *reinterpret_cast<const b8*>(&sSl[kbb]);
+        if (kb & 1) acc1 = mma3_bf16(acc1, ah, al, bh, bl);
+        else acc0 = mma3_bf16(acc0, ah, al, bh, bl);
       }
       float* VT = a.VT + ch * kC * D;
+      float v[4];
 #pragma unroll
       for (int i = 0; i < 4; ++i) {
         const int row = 16 * mt + 4 * gq + i, col = 16 * ct + r;
-        const float v = acc0[i] + acc1[i];
-        sV[row * kPB + col] = v;
-        VT[row * D + c0 + col] = v;
+        v[i] = sU[row * kPB + col] - (acc0[i] + acc1[i]);
+        VT[row * D + c0 + col] = v[i];
       }
+      uint2 hh, ll;
+      split2_bf16(v[0], v[1], hh.x, ll.x);
+      split2_bf16(v[2], v[3], hh.y, ll.y);
+      *reinterpret_cast<uint2*>(&sVh[(16 * ct + r) * PK + 16 * mt + 4 * gq]) = hh;
+      *reinterpret_cast<uint2*>(&sVl[(16 * ct + r) * PK + 16 * mt + 4 * gq]) = ll;
     }
     __syncthreads();
     // S <- gamma_C S + (lambda k)^T v~
@@ -525,11 +598,14 @@ __global__ __launch_bounds__(kScanThreads) void kda_bwd_fscan_kernel(BwdArgs a) 
     for (int q = 0; q < NST; ++q)
 #pragma unroll
       for (int i = 0; i < 4; ++i) S[q][i] *= sGC[16 * rt[q] + 4 * gq + i];
-#pragma unroll 4
-    for (int k = 0; k < kC / 4; ++k)
 #pragma unroll
-      for (int q = 0; q < NST; ++q)
-        S[q] = mfma4(sKL[(4 * k + gq) * PW + 16 * rt[q] + r], sV[(4 * k + gq) * kPB + 16 * cs[q] + r], S[q]);
+    for (int kb = 0; kb < kC / 32; ++kb)
+#pragma unroll
+      for (int q = 0; q < NST; ++q) {
+        const int ka = (16 * rt[q] + r) * PK + 32 * kb + 8 * gq, kbb = (16 * cs[q] + r) * PK + 32 * kb + 8 * gq;
+        S[q] = mma3_bf16(S[q], *reinterpret_cast<const b8*>(&sKh[ka]), *reinterpret_cast<const b8*>(&sKl[ka]),
+                         *reinterpret_cast<const b8*>(&sVh[kbb]), *reinterpret_cast<const b8*>(&sVl[kbb]));
+      }
     __syncthreads();
   }
 }
