@@ -729,28 +729,18 @@ int kda_decode_layer_step(hipStream_t stream, const void* qp, const void* kp, co
   const size_t need = kda_decode_layer_workspace(B, H, d, in_dtype);
   if (!workspace || workspace_bytes < need)
     return fail(KDA_ERR_WORKSPACE, "workspace of %zu bytes is too small (need %zu)", workspace_bytes, need);
-  const size_t n = static_cast<size_t>(B) * H * d;
-  const size_t es = in_dtype == KDA_DTYPE_F32 ? 4 : 2;
-  unsigned char* ws = static_cast<unsigned char*>(workspace);
-  void* q = ws;
-  void* k = ws + align_up(n * es);
-  void* v = ws + 2 * align_up(n * es);
-  float* o = reinterpret_cast<float*>(ws + 3 * align_up(n * es));
-  const int dt = in_dtype == KDA_DTYPE_F32 ? 0 : 1;
-  kda::PrologueArgs p{};
-  p.qp = qp; p.kp = kp; p.vp = vp; p.wq = wq; p.wk = wk; p.wv = wv;
-  p.bq_in = bq; p.bk_in = bk; p.bv_in = bv; p.bq_out = bq; p.bk_out = bk; p.bv_out = bv;
-  p.q = q; p.k = k; p.v = v; p.B = B; p.T = 1; p.H = H; p.K = K;
-  hipError_t e = kda::launch_prologue(p, d, dt, dt, stream);
-  if (e != hipSuccess) return hip_fail(e, "layer step prologue launch");
-  kda::DecodeArgs a{};
-  a.q = q; a.k = k; a.v = v; a.g = g; a.beta = beta; a.state = state; a.o = o; a.scale = scale;
-  e = kda::launch_decode(a, d, in_dtype, 0, static_cast<int>(static_cast<int64_t>(B) * H), stream);
-  if (e != hipSuccess) return hip_fail(e, "layer step decode launch");
-  kda::EpilogueArgs ep{};
-  ep.o = o; ep.gate = gate; ep.y = y; ep.B = B; ep.T = 1; ep.H = H; ep.eps = eps;
-  e = kda::launch_epilogue(ep, d, 0, dt, out_dtype == KDA_DTYPE_F32 ? 0 : 1, stream);
-  if (e != hipSuccess) return hip_fail(e, "layer step epilogue launch");
+  // one fused launch (the workspace is not touched by it)
+  kda::DecodeLayerArgs la{};
+  la.x[0] = qp; la.x[1] = kp; la.x[2] = vp;
+  la.g = g; la.beta = beta; la.gate = gate;
+  la.w[0] = wq; la.w[1] = wk; la.w[2] = wv;
+  // with K == 1 there are no buffer rows: the kernel reads (and discards) row 0
+  // of a stand-in array and writes nothing
+  la.buf[0] = K > 1 ? bq : state; la.buf[1] = K > 1 ? bk : state; la.buf[2] = K > 1 ? bv : state;
+  la.state = state; la.y = y; la.scale = scale; la.eps = eps; la.B = B; la.H = H; la.K = K;
+  const hipError_t e = kda::launch_decode_layer(la, d, in_dtype == KDA_DTYPE_F32 ? 0 : 1,
+                                                out_dtype == KDA_DTYPE_F32 ? 0 : 1, stream);
+  if (e != hipSuccess) return hip_fail(e, "layer step launch");
   return KDA_OK;
 }
 

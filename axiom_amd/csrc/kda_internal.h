@@ -192,6 +192,23 @@ hipError_t launch_varlen_prep(const int32_t* cu, int N, int T, int32_t* cu_clamp
                               int32_t* chunk_off, int32_t* n_units, int32_t* order,
                               int32_t* flags, hipStream_t s);
 hipError_t launch_decode(const DecodeArgs& a, int d, int dt, int out_dt, int grid, hipStream_t s);
+
+// One decode token of the whole layer in one launch: short conv (buffers
+// shifted in place), swish, L2 norm of q and k, the delta-rule step on the
+// fp32 state in place, head-wise RMSNorm x sigmoid gate.
+struct DecodeLayerArgs {
+  const void* x[3];        // qp, kp, vp [B, H*d]
+  const void* g;           // [B, H, d] log decay
+  const void* beta;        // [B, H]
+  const void* gate;        // [B, H*d] logits
+  const float* w[3];       // conv taps [K, H*d]
+  float* buf[3];           // conv buffers [B, K-1, H*d] (updated in place)
+  float* state;            // [B, H, d, d]
+  void* y;                 // [B, H*d]
+  float scale, eps;
+  int B, H, K;
+};
+hipError_t launch_decode_layer(const DecodeLayerArgs& a, int d, int dt, int out_dt, hipStream_t s);
 hipError_t launch_adapt(const AdaptArgs& a, hipStream_t s);
 
 // cc_scan backward outputs from the dense backward's fp32 results: dq, dk, dv

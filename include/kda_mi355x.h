@@ -288,9 +288,11 @@ KDA_API int kda_epilogue_bwd(hipStream_t stream, const void* o, const void* gate
  * :205-214 without W_o).  qp, kp, vp [B, H*d], g [B,H,d] (log decay), beta
  * [B,H], gate logits [B, H*d] in in_dtype (KDA_DTYPE_F32 or KDA_DTYPE_BF16);
  * conv taps [K, H*d] fp32; buffers [B, K-1, H*d] fp32 and state [B,H,d,d]
- * fp32 updated in place; y [B, H*d] in out_dtype (F32 or BF16).  Three
- * launches (prologue, decode, epilogue) through a caller workspace of
- * kda_decode_layer_workspace bytes.  d in {64, 128}, 1 <= K <= 8.
+ * fp32 updated in place; y [B, H*d] in out_dtype (F32 or BF16).  One fused
+ * launch (a workgroup per (b, h): conv, swish, L2 norm, the state step, the
+ * gated RMSNorm); the caller workspace of kda_decode_layer_workspace bytes is
+ * still required and validated (the ABI is unchanged) but not written.
+ * d in {64, 128}, 1 <= K <= 8.
  */
 KDA_API int kda_decode_layer_step(hipStream_t stream,
                 const void* qp, const void* kp, const void* vp,
