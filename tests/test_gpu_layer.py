@@ -105,15 +105,16 @@ def test_epilogue_matches_oracle(cuda, o_dt, g_dt, y_dt, dv):
     _close(y, ref, o_dt == g_dt == y_dt == torch.float32)
 
 
-@pytest.mark.parametrize("dt,d", [(torch.float32, 128), (torch.bfloat16, 64)])
-def test_decode_layer_steps_equal_the_whole_sequence(cuda, dt, d):
+@pytest.mark.parametrize("dt,d,Kc", [(torch.float32, 128, 4), (torch.bfloat16, 64, 4), (torch.float32, 64, 1),
+                                     (torch.bfloat16, 128, 8), (torch.float32, 128, 2)])
+def test_decode_layer_steps_equal_the_whole_sequence(cuda, dt, d, Kc):
     """T layer steps (conv buffers and state carried in place) == prologue over the
     T tokens, the recurrence, and the epilogue (the decode == chunked invariant of
     the reference's generation path, net/kda.py:277-295)."""
     import axiom_amd
     from oracle import inputs, kda_oracle as K
-    B, T, H, Kc = 2, 12, 2, 4
-    rng = np.random.default_rng(d)
+    B, T, H = 2, 12, 2
+    rng = np.random.default_rng(d + Kc)
     xs, ws, _ = _proj(B, T, H, d, Kc, seed=d + 1)
     base = inputs.make_inputs(B, T, H, d, d, seed=d + 2, dtype="fp32")
     gate = rng.standard_normal((B, T, H * d)).astype(np.float32)
@@ -144,4 +145,5 @@ def test_decode_layer_steps_equal_the_whole_sequence(cuda, dt, d):
         assert np.linalg.norm(y - y_ref) / np.linalg.norm(y_ref) <= 1e-2
         assert np.linalg.norm(state.cpu().numpy() - hT) / np.linalg.norm(hT) <= 1e-2
     for buf, x in zip(bufs, xs_r):
-        np.testing.assert_allclose(buf.cpu().numpy(), x[:, T - (Kc - 1):], rtol=0, atol=0)
+        np.testing.assert_allclose(buf.cpu().numpy(), x[:, T - (Kc - 1):] if Kc > 1 else x[:, :0],
+                                   rtol=0, atol=0)
