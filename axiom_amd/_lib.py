@@ -57,7 +57,7 @@ _SIGNATURES = {
     "kda_prologue_bwd": (_i, [_vp] * 22 + [_i, _i, _i, _i, _i, _i, _vp, _sz]),
     "kda_prologue_bwd_workspace": (_sz, [_i, _i, _i, _i, _i]),
     "kda_epilogue_bwd": (_i, [_vp] * 6 + [_i, _i, _i, _i, _f, _i, _i, _i, _i]),
-    "kda_layer_fwd": (_i, [_vp] * 19 + [_i, _i, _i, _i, _i, _f, _f, _i, _i, _i, _vp, _sz]),
+    "kda_layer_fwd": (_i, [_vp] * 20 + [_i, _i, _i, _i, _i, _f, _f, _i, _i, _i, _vp, _sz]),
     "kda_layer_fwd_workspace": (_sz, [_i, _i, _i, _i, _i, _i]),
     "kda_last_error": (ctypes.c_char_p, []),
     "kda_abi_version": (_i, []),

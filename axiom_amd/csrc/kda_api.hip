@@ -338,7 +338,7 @@ int ut_check(const void* a, const void* b, const void* x, int H, int C, int N, i
 
 extern "C" {
 
-int kda_abi_version(void) { return 100; }
+int kda_abi_version(void) { return 101; }
 
 const char* kda_last_error(void) { return g_err; }
 
@@ -787,7 +787,7 @@ int kda_layer_fwd(hipStream_t stream, const void* qp, const void* kp, const void
                   const float* wq, const float* wk, const float* wv,
                   const float* bq_in, const float* bk_in, const float* bv_in,
                   float* bq_out, float* bk_out, float* bv_out,
-                  const float* h0, float* ht, void* y,
+                  const float* h0, float* ht, void* y, float* o_out,
                   int B, int T, int H, int d, int K, float scale, float eps,
                   int in_dtype, int gate_dtype, int out_dtype, void* workspace, size_t workspace_bytes) {
   g_err[0] = 0;
@@ -809,7 +809,7 @@ int kda_layer_fwd(hipStream_t stream, const void* qp, const void* kp, const void
   if (!workspace || workspace_bytes < L.total)
     return fail(KDA_ERR_WORKSPACE, "workspace of %zu bytes is too small (need %zu)", workspace_bytes, L.total);
   unsigned char* ws = static_cast<unsigned char*>(workspace);
-  float* o = reinterpret_cast<float*>(ws + L.o);
+  float* o = o_out != nullptr ? o_out : reinterpret_cast<float*>(ws + L.o);   // the scan's fp32 output
   const size_t chunk_bytes = L.o;
   kda::PrologueArgs p{};
   p.qp = qp; p.kp = kp; p.vp = vp; p.wq = wq; p.wk = wk; p.wv = wv;

@@ -436,7 +436,7 @@ def layer_fwd_workspace_bytes(B, T, H, d, K, in_code=_lib.KDA_DTYPE_BF16) -> int
 
 def kda_layer_fwd(qp, kp, vp, g, beta, gate, wq, wk, wv, conv_state=None, initial_state=None,
                   scale: float = 1.0, eps: float = 1e-6, output_final_state: bool = True,
-                  return_conv_state: bool = True, out_dtype=torch.bfloat16, workspace=None):
+                  return_conv_state: bool = True, out_dtype=torch.bfloat16, workspace=None, o_out=None):
     """The chunked KDA layer between its projections and ``W_o``.
 
     ``net/kda.py:790-853`` (short conv -> postprocess -> chunked scan -> output
@@ -447,7 +447,8 @@ def kda_layer_fwd(qp, kp, vp, g, beta, gate, wq, wk, wv, conv_state=None, initia
     or bf16), ``wq, wk, wv [K, H*d]`` fp32 conv taps, ``conv_state`` None or
     three fp32 ``[B, K-1, H*d]`` buffers, ``initial_state`` None or fp32
     ``[B, H, d, d]``.  Returns ``(y [B, T, H*d] in out_dtype, final_state or
-    None, new_conv_state or None)``.
+    None, new_conv_state or None)``.  ``o_out``: None, or a fp32 ``[B, T, H, d]``
+    tensor that receives the scan's output o (the epilogue's input).
     """
     what = "kda_layer_fwd"
     if qp.dim() != 3 or kp.shape != qp.shape or vp.shape != qp.shape or gate.shape != qp.shape:
@@ -481,8 +482,10 @@ def kda_layer_fwd(qp, kp, vp, g, beta, gate, wq, wk, wv, conv_state=None, initia
     if initial_state is not None and (initial_state.dtype != torch.float32 or
                                       tuple(initial_state.shape) != (B, H, d, d)):
         raise ValueError(f"{what}: initial_state must be fp32 [{B},{H},{d},{d}]")
+    if o_out is not None and (o_out.dtype != torch.float32 or tuple(o_out.shape) != (B, T, H, d)):
+        raise ValueError(f"{what}: o_out must be fp32 [{B},{T},{H},{d}]")
     tensors = [qp, kp, vp, g, beta, gate, wq, wk, wv] + list(conv_state or []) + \
-        ([initial_state] if initial_state is not None else [])
+        ([initial_state] if initial_state is not None else []) + ([o_out] if o_out is not None else [])
     for i, t in enumerate(tensors):
         _contig(f"arg{i}", t)
     dev = _require_gpu(tensors, what)
@@ -499,7 +502,7 @@ def kda_layer_fwd(qp, kp, vp, g, beta, gate, wq, wk, wv, conv_state=None, initia
     bin_ = conv_state if conv_state is not None else (None, None, None)
     rc = L.kda_layer_fwd(_stream(dev), _ptr(qp), _ptr(kp), _ptr(vp), _ptr(g), _ptr(beta), _ptr(gate),
                          _ptr(wq), _ptr(wk), _ptr(wv), *(_ptr(b) for b in bin_), *(_ptr(b) for b in new),
-                         _ptr(initial_state), _ptr(ht), _ptr(y), B, T, H, d, K, float(scale), float(eps),
+                         _ptr(initial_state), _ptr(ht), _ptr(y), _ptr(o_out), B, T, H, d, K, float(scale), float(eps),
                          code, _OUT_CODES[gate.dtype], _OUT_CODES[out_dtype], _ptr(workspace), need)
     _lib.check(rc, what)
     return y, ht, (new if return_conv_state else None)
@@ -598,22 +601,25 @@ def kda_epilogue_bwd(o, gate, dy, eps: float = 1e-6, dgate_dtype=None):
 
 class _KDALayer(torch.autograd.Function):
     """``(y, final_state)`` of :func:`kda_layer_fwd` with a backward that runs on
-    the HIP kernels: q, k, v and o recomputed (prologue, chunked forward), then
-    epilogue backward -> chunked backward -> prologue backward."""
+    the HIP kernels: the forward keeps the scan's output o (fp32) for the
+    epilogue backward; q, k, v are recomputed by the prologue; then epilogue
+    backward -> chunked backward -> prologue backward."""
 
     @staticmethod
     def forward(ctx, qp, kp, vp, g, beta, gate, wq, wk, wv, bq, bk, bv, initial_state, scale, eps):
         conv_state = None if bq is None else (bq, bk, bv)
+        B, T, H, d = g.shape
+        o = torch.empty((B, T, H, d), dtype=torch.float32, device=qp.device)   # kept for the epilogue backward
         y, ht, _ = kda_layer_fwd(qp, kp, vp, g, beta, gate, wq, wk, wv, conv_state=conv_state,
                                  initial_state=initial_state, scale=scale, eps=eps, return_conv_state=False,
-                                 out_dtype=qp.dtype)
-        ctx.save_for_backward(qp, kp, vp, g, beta, gate, wq, wk, wv, bq, bk, bv, initial_state)
+                                 out_dtype=qp.dtype, o_out=o)
+        ctx.save_for_backward(qp, kp, vp, g, beta, gate, wq, wk, wv, bq, bk, bv, initial_state, o)
         ctx.scale, ctx.eps = scale, eps
         return y, ht
 
     @staticmethod
     def backward(ctx, dy, dht):
-        qp, kp, vp, g, beta, gate, wq, wk, wv, bq, bk, bv, h0 = ctx.saved_tensors
+        qp, kp, vp, g, beta, gate, wq, wk, wv, bq, bk, bv, h0, o = ctx.saved_tensors
         conv_state = None if bq is None else (bq, bk, bv)
         B, T, H, d = g.shape
         if dy is None:
@@ -623,7 +629,6 @@ class _KDALayer(torch.autograd.Function):
             dy = dy.float()
         q, k, v, _ = kda_prologue(qp, kp, vp, wq, wk, wv, H, conv_state=conv_state, return_state=False,
                                   out_dtype=qp.dtype)
-        o, _ = kda_chunk_fwd(q, k, v, g, beta, initial_state=h0, scale=ctx.scale, output_final_state=False)
         do, dgate = kda_epilogue_bwd(o, gate, dy, eps=ctx.eps)
         dht = None if dht is None else dht.float().contiguous()
         dq, dk, dv, dg, dbeta, dh0 = kda_chunk_bwd(q, k, v, g, beta, do, dht=dht, initial_state=h0,

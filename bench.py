@@ -325,9 +325,9 @@ def bench_layer(args, fwd_inputs, device):
 
 def bench_layer_bwd(args, fwd_inputs, device):
     """The layer backward at config-1 shapes (K = 4, bf16 projections, gate and
-    dy): the two new entry points on their own, and the whole backward of
-    ``kda_layer`` (recompute q, k, v and o, epilogue backward, chunked
-    backward, prologue backward)."""
+    dy): the prologue and epilogue adjoints on their own, and the whole
+    backward of ``kda_layer`` (q, k, v recomputed, o kept by the forward;
+    epilogue backward, chunked backward, prologue backward)."""
     import axiom_amd
     from axiom_amd import kda as kmod
     q, k, v, g, beta = fwd_inputs
@@ -343,7 +343,6 @@ def bench_layer_bwd(args, fwd_inputs, device):
     dqkv = [torch.randn(B, T, H, d, device=device, generator=gen) for _ in range(3)]
     o = torch.randn(B, T, H, d, device=device, generator=gen)
     pws = torch.empty(kmod.prologue_bwd_workspace_bytes(B, T, H, d, K), dtype=torch.uint8, device=device)
-    cws = torch.empty(kmod.chunk_fwd_workspace_bytes(B, T, H, d, d), dtype=torch.uint8, device=device)
     bws = torch.empty(kmod.chunk_bwd_workspace_bytes(B, T, H, d, d), dtype=torch.uint8, device=device)
     stream = torch.cuda.current_stream(device)
 
@@ -359,10 +358,9 @@ def bench_layer_bwd(args, fwd_inputs, device):
         torch.cuda.synchronize()
         return e0.elapsed_time(e1) / 1e3 / steps
 
-    def whole():
+    def whole():   # the forward kept o (kda_layer_fwd's o_out): q, k, v are recomputed
         qq, kk, vv, _ = axiom_amd.kda_prologue(*xs, *ws_, H, out_dtype=bf, return_state=False)
-        oo, _ = axiom_amd.kda_chunk_fwd(qq, kk, vv, g, beta, output_final_state=False, workspace=cws)
-        do, _ = axiom_amd.kda_epilogue_bwd(oo, gate, dy)
+        do, _ = axiom_amd.kda_epilogue_bwd(o, gate, dy)
         dq, dk, dv, _, _, _ = axiom_amd.kda_chunk_bwd(qq, kk, vv, g, beta, do, need_dh0=False, workspace=bws)
         return axiom_amd.kda_prologue_bwd(*xs, *ws_, dq, dk, dv, workspace=pws)
 
@@ -379,7 +377,8 @@ def bench_layer_bwd(args, fwd_inputs, device):
         epilogue_bwd={"us_per_call": t_epi * 1e6, "algorithmic_bytes": epi_bytes,
                       "gbps": epi_bytes / t_epi / 1e9, "frac": epi_bytes / t_epi / 1e9 / HBM_PEAK_GBPS},
         layer_bwd_us_per_call=t_all * 1e6, layer_bwd_tokens_per_s=B * T / t_all,
-        config="B4 T4096 H16 d128 K4, bf16 projections, gate and dy; the whole backward recomputes q, k, v, o")
+        config="B4 T4096 H16 d128 K4, bf16 projections, gate and dy; the whole backward recomputes q, k, v "
+               "(o kept by the forward)")
 
 
 def bench_cc_scan(args, fwd_inputs, device):

@@ -318,7 +318,10 @@ KDA_API size_t kda_decode_layer_workspace(int B, int H, int d, int in_dtype);
  * With bf16 projections and K <= 4 the prologue runs inside the intra kernel
  * (no q, k, v round trip through memory; results equal kda_prologue followed
  * by kda_chunk_fwd and kda_epilogue bit for bit); otherwise it is its own pass.
- * Caller workspace of kda_layer_fwd_workspace bytes.  d in {64, 128}.
+ * o_out: NULL, or [B,T,H,d] fp32 that receives the scan's output o (the
+ * epilogue's input; a training caller keeps it for kda_epilogue_bwd instead
+ * of recomputing it).  Caller workspace of kda_layer_fwd_workspace bytes.
+ * d in {64, 128}.
  */
 KDA_API int kda_layer_fwd(hipStream_t stream,
                 const void* qp, const void* kp, const void* vp,
@@ -326,7 +329,7 @@ KDA_API int kda_layer_fwd(hipStream_t stream,
                 const float* wq, const float* wk, const float* wv,
                 const float* bq_in, const float* bk_in, const float* bv_in,
                 float* bq_out, float* bk_out, float* bv_out,
-                const float* h0, float* ht, void* y,
+                const float* h0, float* ht, void* y, float* o_out,
                 int B, int T, int H, int d, int K, float scale, float eps,
                 int in_dtype, int gate_dtype, int out_dtype, void* workspace, size_t workspace_bytes);
 

@@ -101,7 +101,7 @@ def test_library_exports_every_declared_symbol(L):
 
 
 def test_abi_version(L):
-    assert L.kda_abi_version() == 100
+    assert L.kda_abi_version() == 101
 
 
 @pytest.mark.parametrize("B,T,H,d", [(1, 512, 4, 64), (4, 4096, 16, 128), (2, 1, 3, 128),

@@ -52,23 +52,24 @@ def _tensors(cuda, c, dt, gdt):
     return xs, ws, bs, _dev(cuda, c["g"], gdt), _dev(cuda, c["beta"], gdt), _dev(cuda, c["gate"], dt), S0
 
 
-def _layer(cuda, c, dt, gdt, out_dtype=torch.float32):
+def _layer(cuda, c, dt, gdt, out_dtype=torch.float32, with_o=False):
     import axiom_amd
     xs, ws, bs, g, beta, gate, S0 = _tensors(cuda, c, dt, gdt)
+    o = torch.full(g.shape, float("nan"), device=cuda) if with_o else None
     y, ht, new = axiom_amd.kda_layer_fwd(*xs, g, beta, gate, *ws, conv_state=bs, initial_state=S0,
-                                         out_dtype=out_dtype)
+                                         out_dtype=out_dtype, o_out=o)
     torch.cuda.synchronize()
-    return y, ht, new
+    return (y, ht, new, o) if with_o else (y, ht, new)
 
 
-def _unfused(cuda, c, dt, gdt, out_dtype=torch.float32):
+def _unfused(cuda, c, dt, gdt, out_dtype=torch.float32, with_o=False):
     import axiom_amd
     xs, ws, bs, g, beta, gate, S0 = _tensors(cuda, c, dt, gdt)
     q, k, v, new = axiom_amd.kda_prologue(*xs, *ws, c["H"], conv_state=bs, out_dtype=dt)
     o, ht = axiom_amd.kda_chunk_fwd(q, k, v, g, beta, initial_state=S0)
     y = axiom_amd.kda_epilogue(o, gate, eps=1e-6, out_dtype=out_dtype)
     torch.cuda.synchronize()
-    return y, ht, new
+    return (y, ht, new, o) if with_o else (y, ht, new)
 
 
 def _oracle(c, dt, gdt):
@@ -93,10 +94,11 @@ def _oracle(c, dt, gdt):
 def test_fused_layer_equals_the_three_entry_points(cuda, B, T, H, d, Kc, gdt, bufs, h0):
     c = _case(B, T, H, d, Kc, seed=T + d + Kc, bufs=bufs, h0=h0)
     print(f"[layer fused vs unfused] B={B} T={T} H={H} d={d} K={Kc} gates={gdt}", flush=True)
-    y, ht, new = _layer(cuda, c, torch.bfloat16, gdt)
-    y2, ht2, new2 = _unfused(cuda, c, torch.bfloat16, gdt)
+    y, ht, new, o = _layer(cuda, c, torch.bfloat16, gdt, with_o=True)
+    y2, ht2, new2, o2 = _unfused(cuda, c, torch.bfloat16, gdt, with_o=True)
     assert torch.equal(y, y2), (y - y2).abs().max().item()
     assert torch.equal(ht, ht2)
+    assert torch.equal(o, o2)          # o_out: the scan's output, as kda_chunk_fwd's
     for a, b in zip(new, new2):
         assert torch.equal(a, b)
 
