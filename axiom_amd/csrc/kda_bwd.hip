@@ -715,6 +715,52 @@ __global__ __launch_bounds__(kScanThreads) void kda_bwd_rscan_kernel(BwdArgs a) 
   }
 }
 
+// A fetched fp32 tile into LDS as hi / lo bf16 planes (row pitch PB bf16).
+template <int PB, int ROWS, int COLS, int NTH>
+__device__ __forceinline__ void put_hl(const Tile<ROWS, COLS, NTH>& tl, __bf16* h, __bf16* l) {
+  typedef Tile<ROWS, COLS, NTH> TT;
+#pragma unroll
+  for (int p = 0; p < TT::PER; ++p) {
+    const int e = threadIdx.x + p * NTH;
+    if (TT::N % NTH == 0 || e < TT::N) {
+      const int row = e / TT::V, c4 = e - row * TT::V;
+      uint2 hh, ll;
+      split2_bf16(tl.r[p].x, tl.r[p].y, hh.x, ll.x);
+      split2_bf16(tl.r[p].z, tl.r[p].w, hh.y, ll.y);
+      *reinterpret_cast<uint2*>(&h[row * PB + 4 * c4]) = hh;
+      *reinterpret_cast<uint2*>(&l[row * PB + 4 * c4]) = ll;
+    }
+  }
+}
+template <int PB, int DT, int D, int COLS, int NTH>
+__device__ __forceinline__ void put_hl(const InTile<DT, D, COLS, NTH>& tl, __bf16* h, __bf16* l) {
+  typedef InTile<DT, D, COLS, NTH> TT;
+#pragma unroll
+  for (int p = 0; p < TT::PER; ++p) {
+    const int e = threadIdx.x + p * NTH;
+    if (TT::N % NTH == 0 || e < TT::N) {
+      const int r = e / TT::V, c8 = e - r * TT::V;
+      float x[8];
+      if constexpr (DT == 0) {
+        const uint4 a = tl.w[2 * p], b = tl.w[2 * p + 1];
+        x[0] = __uint_as_float(a.x); x[1] = __uint_as_float(a.y); x[2] = __uint_as_float(a.z); x[3] = __uint_as_float(a.w);
+        x[4] = __uint_as_float(b.x); x[5] = __uint_as_float(b.y); x[6] = __uint_as_float(b.z); x[7] = __uint_as_float(b.w);
+      } else {
+        const f4 lo = unpack4<DT>(make_uint2(tl.w[p].x, tl.w[p].y)), hi = unpack4<DT>(make_uint2(tl.w[p].z, tl.w[p].w));
+#pragma unroll
+        for (int q = 0; q < 4; ++q) { x[q] = lo[q]; x[4 + q] = hi[q]; }
+      }
+      uint4 hh, ll;
+      split2_bf16(x[0], x[1], hh.x, ll.x);
+      split2_bf16(x[2], x[3], hh.y, ll.y);
+      split2_bf16(x[4], x[5], hh.z, ll.z);
+      split2_bf16(x[6], x[7], hh.w, ll.w);
+      *reinterpret_cast<uint4*>(&h[r * PB + 8 * c8]) = hh;
+      *reinterpret_cast<uint4*>(&l[r * PB + 8 * c8]) = ll;
+    }
+  }
+}
+
 // ---------------------------------------------------------------------------
 // per chunk-head adjoint
 // ---------------------------------------------------------------------------
@@ -730,7 +776,7 @@ __global__ __launch_bounds__(kChunkThreads) void kda_bwd_chunk_kernel(BwdArgs a)
   // phase 4 is the largest: dL, dAqk [64][65]; q, k, G [64][P]; three [16][PF]
   constexpr int PF = D + 16;          // column-fragment pitch of phase 4's factored operands
   constexpr int SMEM_FLOATS = 2 * kC * PC + 3 * kC * P + 3 * 16 * PF + kC;
-  __shared__ float sm[SMEM_FLOATS];
+  __shared__ __attribute__((aligned(16))) float sm[SMEM_FLOATS];
   const int t = threadIdx.x, rm = t / TC, cn = t % TC;
   const int H = a.H;
   const int u = blockIdx.x / H, h = blockIdx.x - u * H;
@@ -758,7 +804,6 @@ __global__ __launch_bounds__(kChunkThreads) void kda_bwd_chunk_kernel(BwdArgs a)
   constexpr int NDT = D / 32;          // column tiles per wave of a [64][D] product
   const int wv = t >> 6, l = t & 63, r16 = l & 15, gq = l >> 4;
   const int mt = wv >> 1, dg_ = wv & 1;
-  constexpr int PH = HW + 2;           // row-fragment pitch of phase 1's [*][HW] tiles
   constexpr int PR = D + 2;            // row-fragment pitch of [64][D] operands
   constexpr int PX = D + 16;           // column-fragment pitch of [64][D] operands
   constexpr int PT = kC + 16;          // column-fragment pitch of T
@@ -776,6 +821,10 @@ __global__ __launch_bounds__(kChunkThreads) void kda_bwd_chunk_kernel(BwdArgs a)
   static_assert(kC * PT + 2 * kC * PX + 2 * kC * D <= SMEM_FLOATS, "phase 1 -> 2 accumulators");
 
   // ---- phase 1: dY = v~ dS'^T, dgq = do S^T, dW = -dv~ S^T (K = dv in passes of HW)
+  // The operands go to LDS as hi / lo bf16 planes (K contiguous) and each
+  // product runs as three bf16 MFMAs per 32-wide K block (hi hi + hi lo +
+  // lo hi, about 2^-16 of each product dropped); dW accumulates +dv~ S^T and
+  // is negated where phase 2 takes it.
   f4 dW[NDT];
   Tile<kC, kC, NTH> tT;      // phase 2's T and dv~, loaded during phase 1's last pass
   Tile<kC, D, NTH> tY;
@@ -785,11 +834,18 @@ __global__ __launch_bounds__(kChunkThreads) void kda_bwd_chunk_kernel(BwdArgs a)
     for (int q = 0; q < NDT; ++q)
 #pragma unroll
       for (int i = 0; i < 4; ++i) dY[q][i] = dgq[q][i] = dW[q][i] = 0.f;
-    float* sVt = sm;
-    float* sDo = sVt + kC * PH;
-    float* sDv = sDo + kC * PH;
-    float* sS = sDv + kC * PH;
-    float* sDS = sS + D * PH;
+    constexpr int PB = HW + 8;         // bf16 pitch: rows of 32-wide K blocks start 16-byte aligned
+    static_assert((6 * kC + 4 * D) * PB / 2 <= SMEM_FLOATS, "phase 1 LDS");
+    __bf16* const sVh = reinterpret_cast<__bf16*>(sm);
+    __bf16* const sVl = sVh + kC * PB;
+    __bf16* const sOh = sVl + kC * PB;
+    __bf16* const sOl = sOh + kC * PB;
+    __bf16* const sUh = sOl + kC * PB;   // dv~
+    __bf16* const sUl = sUh + kC * PB;
+    __bf16* const sSh = sUl + kC * PB;
+    __bf16* const sSl = sSh + D * PB;
+    __bf16* const sDh = sSl + D * PB;    // dS'
+    __bf16* const sDl = sDh + D * PB;
     // a pass's operands are loaded during the previous pass's products
     Tile<kC, HW, NTH> pV, pDv;
     Tile<D, HW, NTH> pS, pDS;
@@ -803,32 +859,43 @@ __global__ __launch_bounds__(kChunkThreads) void kda_bwd_chunk_kernel(BwdArgs a)
     };
     fetch_pass(0);
     for (int hp = 0; hp < NH; ++hp) {
-      pV.template put<PH>(sVt);
-      pDv.template put<PH>(sDv);
-      pS.template put<PH>(sS);
-      pDS.template put<PH>(sDS);
-      pDo.template put<PH>(sDo, 1.f);
+      put_hl<PB>(pV, sVh, sVl);
+      put_hl<PB>(pDv, sUh, sUl);
+      put_hl<PB>(pS, sSh, sSl);
+      put_hl<PB>(pDS, sDh, sDl);
+      put_hl<PB>(pDo, sOh, sOl);
       __syncthreads();
       if (hp + 1 < NH) fetch_pass(HW * (hp + 1));
       else {   // phase 2's operands
         tT.fetch(a.TM + ch * kC * kC, kC, 0);
         tY.fetch(a.DVT + ch * kC * D, D, 0);
       }
-#pragma unroll 4
-      for (int k = 0; k < HW / 4; ++k) {
-        const int ka = (16 * mt + r16) * PH + 4 * k + gq;
-        const float av = sVt[ka], ao = sDo[ka], aw = -sDv[ka];
+#pragma unroll
+      for (int kb = 0; kb < HW / 32; ++kb) {
+        const int ka = (16 * mt + r16) * PB + 32 * kb + 8 * gq;
+        const b8 vh = *reinterpret_cast<const b8*>(&sVh[ka]), vl = *reinterpret_cast<const b8*>(&sVl[ka]);
+        const b8 oh = *reinterpret_cast<const b8*>(&sOh[ka]), ol = *reinterpret_cast<const b8*>(&sOl[ka]);
+        const b8 uh = *reinterpret_cast<const b8*>(&sUh[ka]), ul = *reinterpret_cast<const b8*>(&sUl[ka]);
 #pragma unroll
         for (int q = 0; q < NDT; ++q) {
-          const int kb = (16 * (dg_ * NDT + q) + r16) * PH + 4 * k + gq;
-          const float bs = sS[kb];
-          dY[q] = mfma4(av, sDS[kb], dY[q]);
-          dgq[q] = mfma4(ao, bs, dgq[q]);
-          dW[q] = mfma4(aw, bs, dW[q]);
+          const int kbb = (16 * (dg_ * NDT + q) + r16) * PB + 32 * kb + 8 * gq;
+          const b8 sh = *reinterpret_cast<const b8*>(&sSh[kbb]), sl = *reinterpret_cast<const b8*>(&sSl[kbb]);
+          const b8 dh = *reinterpret_cast<const b8*>(&sDh[kbb]), dl = *reinterpret_cast<const b8*>(&sDl[kbb]);
+          dY[q] = mma3_bf16(dY[q], vh, vl, dh, dl);
+          dgq[q] = mma3_bf16(dgq[q], oh, ol, sh, sl);
+          dW[q] = mma3_bf16(dW[q], uh, ul, sh, sl);
         }
       }
       if (t < D) {
-        for (int nn = 0; nn < HW; ++nn) dgc = fmaf(sS[t * PH + nn], sDS[t * PH + nn], dgc);
+#pragma unroll 2
+        for (int n8 = 0; n8 < HW; n8 += 8) {
+          const b8 sh = *reinterpret_cast<const b8*>(&sSh[t * PB + n8]), sl = *reinterpret_cast<const b8*>(&sSl[t * PB + n8]);
+          const b8 dh = *reinterpret_cast<const b8*>(&sDh[t * PB + n8]), dl = *reinterpret_cast<const b8*>(&sDl[t * PB + n8]);
+#pragma unroll
+          for (int e = 0; e < 8; ++e)
+            dgc = fmaf(static_cast<float>(sh[e]) + static_cast<float>(sl[e]),
+                       static_cast<float>(dh[e]) + static_cast<float>(dl[e]), dgc);
+        }
       }
       __syncthreads();
     }
@@ -870,7 +937,7 @@ __global__ __launch_bounds__(kChunkThreads) void kda_bwd_chunk_kernel(BwdArgs a)
 #pragma unroll
     for (int q = 0; q < NDT; ++q)
 #pragma unroll
-      for (int i = 0; i < 4; ++i) sX[(16 * mt + 4 * gq + i) * PX + 16 * (dg_ * NDT + q) + r16] = dW[q][i];
+      for (int i = 0; i < 4; ++i) sX[(16 * mt + 4 * gq + i) * PX + 16 * (dg_ * NDT + q) + r16] = -dW[q][i];
     tT.template put<PT>(sT);
     tY.template put<PX>(sY);
     __syncthreads();
@@ -924,7 +991,6 @@ __global__ __launch_bounds__(kChunkThreads) void kda_bwd_chunk_kernel(BwdArgs a)
 
   // ---- phase 3: dL = strict(-(Yw W^T + Yu U^T)), dAqk = tril(do v~^T); [64][64]
   // outputs, two 16 x 16 tiles per wave: row tile mt, key tiles 2 (wv % 2) + q
-  static_assert(3 * kC * PH + 2 * D * PH <= SMEM_FLOATS, "phase 1 LDS");
   static_assert(kC * PT + 2 * kC * PX <= SMEM_FLOATS, "phase 2 LDS");
   static_assert(4 * kC * PR <= SMEM_FLOATS, "phase 3 LDS");
   float* const sDL = sm;                 // phase 4's operands, written at the end of phase 3
