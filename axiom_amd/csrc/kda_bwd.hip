@@ -19,8 +19,9 @@
 //                         (dY, dgq, dW, the two transposed solves, dL, dAqk, the
 //                         score adjoints, the cumsum adjoint) and the outputs.
 // The dense products run on the fp32 matrix cores (v_mfma_f32_16x16x4f32:
-// exact fp32 products, fp32 sums), except the forward scan's, which run as
-// bf16 hi/lo triples (about 2^-16 of each product dropped); operands are
+// exact fp32 products, fp32 sums), except the forward scan's and the chunk
+// kernel's phase 1 (dY, dgq, dW), which run as bf16 hi/lo triples (about
+// 2^-16 of each product dropped); operands are
 // staged through LDS; decay factors
 // of off-diagonal 16-row tiles are anchored at the row tile's first row
 // (2^(G_c - G_a) * 2^(G_a - G_i), both <= 1), diagonal tiles use
