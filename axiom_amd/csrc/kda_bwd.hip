@@ -20,8 +20,8 @@
 //                         score adjoints, the cumsum adjoint) and the outputs.
 // The dense products run on the fp32 matrix cores (v_mfma_f32_16x16x4f32:
 // exact fp32 products, fp32 sums), except the forward scan's and the chunk
-// kernel's phase 1 (dY, dgq, dW), which run as bf16 hi/lo triples (about
-// 2^-16 of each product dropped); operands are
+// kernel's phases 1 (dY, dgq, dW) and 3 (dL, dAqk), which run as bf16 hi/lo
+// triples (about 2^-16 of each product dropped); operands are
 // staged through LDS; decay factors
 // of off-diagonal 16-row tiles are anchored at the row tile's first row
 // (2^(G_c - G_a) * 2^(G_a - G_i), both <= 1), diagonal tiles use
@@ -762,6 +762,26 @@ __device__ __forceinline__ void put_hl(const InTile<DT, D, COLS, NTH>& tl, __bf1
   }
 }
 
+// A 16 x 16 accumulator tile (lane (r, gq): rows 4 gq + i, column r) into
+// row-major hi / lo bf16 planes of pitch PB at (row0, col0): lanes r and r ^ 1
+// swap one value of each row pair, so each lane writes packed column pairs
+// (columns r & ~1, r | 1) of rows 4 gq + (r & 1) and 4 gq + 2 + (r & 1).
+template <int PB>
+__device__ __forceinline__ void acc_put_hl(const f4& v, int row0, int col0, __bf16* h, __bf16* l) {
+  const int lane = threadIdx.x & 63, r = lane & 15, gq = lane >> 4;
+  const bool odd = (r & 1) != 0;
+  const float x0 = __shfl_xor(odd ? v[0] : v[1], 1, 64);
+  const float x1 = __shfl_xor(odd ? v[2] : v[3], 1, 64);
+  const int o = (row0 + 4 * gq + (odd ? 1 : 0)) * PB + col0 + (r & ~1);
+  unsigned hh, ll;
+  split2_bf16(odd ? x0 : v[0], odd ? v[1] : x0, hh, ll);
+  *reinterpret_cast<unsigned*>(&h[o]) = hh;
+  *reinterpret_cast<unsigned*>(&l[o]) = ll;
+  split2_bf16(odd ? x1 : v[2], odd ? v[3] : x1, hh, ll);
+  *reinterpret_cast<unsigned*>(&h[o + 2 * PB]) = hh;
+  *reinterpret_cast<unsigned*>(&l[o + 2 * PB]) = ll;
+}
+
 // ---------------------------------------------------------------------------
 // per chunk-head adjoint
 // ---------------------------------------------------------------------------
@@ -790,12 +810,13 @@ __global__ __launch_bounds__(kChunkThreads) void kda_bwd_chunk_kernel(BwdArgs a)
   auto ld_v = [&](int c, int d) { return (c < cr.len) ? ld1<DTQ>(a.v, in_idx(c, d)) : 0.f; };
   auto ld_b = [&](int c) { return (c < cr.len) ? ld1<DTG>(a.beta, (cr.row0 + c) * H + h) : 0.f; };
   // The gradients of q, k and G accumulate in place in dq, dk and dg (dg
-  // holds dG until the final reverse cumsum).  Phases 1-3 run on the fp32
-  // matrix cores: wave wv owns row tile mt = wv / 2 and the NDT column tiles
-  // dt = (wv % 2) NDT + q of every [64][D] product (lane (r, gq) holds rows
-  // 16 mt + 4 gq + i, column 16 dt + r), so phase 2 adds to the dk and dG
-  // terms phase 1 left at its own positions; phase 4 (wave wv owns column tile wv, lane
-  // rows 4 gq + e of every row tile) and the outputs (thread (rm, cn) owns rows
+  // holds dG until the final reverse cumsum).  Phases 1-3 run on the matrix
+  // cores (phases 1 and 3 as bf16 hi / lo triples, phase 2 in fp32): wave wv
+  // owns row tile mt = wv / 2 and the NDT column tiles dt = (wv % 2) NDT + q
+  // of every [64][D] product (lane (r, gq) holds rows 16 mt + 4 gq + i,
+  // column 16 dt + r), so phase 2 adds to the dk and dG terms phase 1 left at
+  // its own positions; phase 4 (wave wv owns column tile wv, lane rows
+  // 4 gq + e of every row tile) and the outputs (thread (rm, cn) owns rows
   // rm + 16i, columns cn + TC j) read what other threads wrote, after the
   // workgroup barriers between the phases.  Pad rows (c >= len) are never
   // stored (their dG is zero: every term carries a factor q_c or k_c).
@@ -805,7 +826,7 @@ __global__ __launch_bounds__(kChunkThreads) void kda_bwd_chunk_kernel(BwdArgs a)
   constexpr int NDT = D / 32;          // column tiles per wave of a [64][D] product
   const int wv = t >> 6, l = t & 63, r16 = l & 15, gq = l >> 4;
   const int mt = wv >> 1, dg_ = wv & 1;
-  constexpr int PR = D + 2;            // row-fragment pitch of [64][D] operands
+  const int mts = __builtin_amdgcn_readfirstlane(mt);   // mt as a wave-uniform (scalar) value
   constexpr int PX = D + 16;           // column-fragment pitch of [64][D] operands
   constexpr int PT = kC + 16;          // column-fragment pitch of T
 
@@ -948,8 +969,9 @@ __global__ __launch_bounds__(kChunkThreads) void kda_bwd_chunk_kernel(BwdArgs a)
     for (int q = 0; q < NDT; ++q)
 #pragma unroll
       for (int i = 0; i < 4; ++i) Yw[q][i] = Yu[q][i] = 0.f;
+    // T[c][m] is zero for c < m: row tile mt needs K steps c >= 16 mt only
 #pragma unroll 4
-    for (int k = 0; k < kC / 4; ++k) {
+    for (int k = 4 * mts; k < kC / 4; ++k) {
       const float at = sT[(4 * k + gq) * PT + 16 * mt + r16];   // (T^T)[c][m] = T[m][c]
 #pragma unroll
       for (int q = 0; q < NDT; ++q) {
@@ -991,64 +1013,84 @@ __global__ __launch_bounds__(kChunkThreads) void kda_bwd_chunk_kernel(BwdArgs a)
   }
 
   // ---- phase 3: dL = strict(-(Yw W^T + Yu U^T)), dAqk = tril(do v~^T); [64][64]
-  // outputs, two 16 x 16 tiles per wave: row tile mt, key tiles 2 (wv % 2) + q
+  // outputs, two 16 x 16 tiles per wave: row tile mt, key tiles 2 (wv % 2) + q,
+  // as bf16 hi / lo triples (operands row-major with the channel, the K index,
+  // contiguous); key tiles above the row tile are masked to zero and skipped.
   static_assert(kC * PT + 2 * kC * PX <= SMEM_FLOATS, "phase 2 LDS");
-  static_assert(4 * kC * PR <= SMEM_FLOATS, "phase 3 LDS");
   float* const sDL = sm;                 // phase 4's operands, written at the end of phase 3
   float* const sDA = sDL + kC * PC;
   InTile<DTQ, D, D, NTH> tQ4, tK4;
   Tile<kC, D, NTH> tG4;
   {
-    float* sA = sm;                      // Yw, then do
-    float* sB = sA + kC * PR;            // Yu, then v~
-    float* sW = sB + kC * PR;
-    float* sU = sW + kC * PR;
+    constexpr int PB = D + 8;            // bf16 pitch: 16-byte aligned K blocks, rows 4 banks apart
+    static_assert(8 * kC * PB / 2 <= SMEM_FLOATS, "phase 3 LDS");
+    __bf16* const sAh = reinterpret_cast<__bf16*>(sm);   // Yw, then do
+    __bf16* const sAl = sAh + kC * PB;
+    __bf16* const sBh = sAl + kC * PB;                   // Yu, then v~
+    __bf16* const sBl = sBh + kC * PB;
+    __bf16* const sWh = sBl + kC * PB;
+    __bf16* const sWl = sWh + kC * PB;
+    __bf16* const sUh = sWl + kC * PB;
+    __bf16* const sUl = sUh + kC * PB;
 #pragma unroll
-    for (int q = 0; q < NDT; ++q)
-#pragma unroll
-      for (int i = 0; i < 4; ++i) {
-        const int o = (16 * mt + 4 * gq + i) * PR + 16 * (dg_ * NDT + q) + r16;
-        sA[o] = Yw[q][i];
-        sB[o] = Yu[q][i];
-      }
-    tW3.template put<PR>(sW);
-    tU3.template put<PR>(sU);
+    for (int q = 0; q < NDT; ++q) {
+      acc_put_hl<PB>(Yw[q], 16 * mt, 16 * (dg_ * NDT + q), sAh, sAl);
+      acc_put_hl<PB>(Yu[q], 16 * mt, 16 * (dg_ * NDT + q), sBh, sBl);
+    }
+    put_hl<PB>(tW3, sWh, sWl);
+    put_hl<PB>(tU3, sUh, sUl);
     __syncthreads();
     f4 dLa[2], dAa[2];
 #pragma unroll
     for (int q = 0; q < 2; ++q)
 #pragma unroll
       for (int i = 0; i < 4; ++i) dLa[q][i] = dAa[q][i] = 0.f;
+    const int kt0 = 2 * (wv & 1);
+    const bool live0 = kt0 <= mts, live1 = kt0 + 1 <= mts;   // wave-uniform
     InTile<DO, D, D, NTH> tDo;            // do and v~ for dAqk, during the dL products
     Tile<kC, D, NTH> tVt;
     tDo.fetch(a.dout, cr.row0, cr.len, H, h, 0);
     tVt.fetch(a.VT + ch * kC * D, D, 0);
-#pragma unroll 4
-    for (int k = 0; k < D / 4; ++k) {
-      const int ka = (16 * mt + r16) * PR + 4 * k + gq;
-      const float yw = sA[ka], yu = sB[ka];
+    if (live0) {
 #pragma unroll
-      for (int q = 0; q < 2; ++q) {
-        const int kb = (16 * (2 * dg_ + q) + r16) * PR + 4 * k + gq;
-        dLa[q] = mfma4(yw, sW[kb], dLa[q]);
-        dLa[q] = mfma4(yu, sU[kb], dLa[q]);
+      for (int kb = 0; kb < D / 32; ++kb) {
+        const int ka = (16 * mt + r16) * PB + 32 * kb + 8 * gq;
+        const b8 ywh = *reinterpret_cast<const b8*>(&sAh[ka]), ywl = *reinterpret_cast<const b8*>(&sAl[ka]);
+        const b8 yuh = *reinterpret_cast<const b8*>(&sBh[ka]), yul = *reinterpret_cast<const b8*>(&sBl[ka]);
+#pragma unroll
+        for (int q = 0; q < 2; ++q) {
+          if (q == 1 && !live1) continue;
+          const int kbb = (16 * (kt0 + q) + r16) * PB + 32 * kb + 8 * gq;
+          dLa[q] = mma3_bf16(dLa[q], ywh, ywl, *reinterpret_cast<const b8*>(&sWh[kbb]),
+                             *reinterpret_cast<const b8*>(&sWl[kbb]));
+          dLa[q] = mma3_bf16(dLa[q], yuh, yul, *reinterpret_cast<const b8*>(&sUh[kbb]),
+                             *reinterpret_cast<const b8*>(&sUl[kbb]));
+        }
       }
     }
     __syncthreads();
     // do and v~ into the Yw / Yu slots
-    tDo.template put<PR>(sA, 1.f);
-    tVt.template put<PR>(sB);
+    put_hl<PB>(tDo, sAh, sAl);
+    put_hl<PB>(tVt, sBh, sBl);
     __syncthreads();
     tQ4.fetch(a.q, cr.row0, cr.len, H, h, 0);   // phase 4's q, k, G, during the dAqk products
     tK4.fetch(a.k, cr.row0, cr.len, H, h, 0);
     tG4.fetch(GL, D, 0);
-#pragma unroll 4
-    for (int k = 0; k < D / 4; ++k) {
-      const float ao = sA[(16 * mt + r16) * PR + 4 * k + gq];
+    if (live0) {
 #pragma unroll
-      for (int q = 0; q < 2; ++q) dAa[q] = mfma4(ao, sB[(16 * (2 * dg_ + q) + r16) * PR + 4 * k + gq], dAa[q]);
+      for (int kb = 0; kb < D / 32; ++kb) {
+        const int ka = (16 * mt + r16) * PB + 32 * kb + 8 * gq;
+        const b8 oh = *reinterpret_cast<const b8*>(&sAh[ka]), ol = *reinterpret_cast<const b8*>(&sAl[ka]);
+#pragma unroll
+        for (int q = 0; q < 2; ++q) {
+          if (q == 1 && !live1) continue;
+          const int kbb = (16 * (kt0 + q) + r16) * PB + 32 * kb + 8 * gq;
+          dAa[q] = mma3_bf16(dAa[q], oh, ol, *reinterpret_cast<const b8*>(&sBh[kbb]),
+                             *reinterpret_cast<const b8*>(&sBl[kbb]));
+        }
+      }
     }
-    __syncthreads();   // every read of sA, sB done before sDL, sDA overwrite them
+    __syncthreads();   // every read of the planes done before sDL, sDA overwrite them
     // phase 4's masked operands
 #pragma unroll
     for (int q = 0; q < 2; ++q)
