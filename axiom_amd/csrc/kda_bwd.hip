@@ -20,8 +20,8 @@
 //                         score adjoints, the cumsum adjoint) and the outputs.
 // The dense products run on the fp32 matrix cores (v_mfma_f32_16x16x4f32:
 // exact fp32 products, fp32 sums), except the forward scan's and the chunk
-// kernel's phases 1 (dY, dgq, dW) and 3 (dL, dAqk), which run as bf16 hi/lo
-// triples (about 2^-16 of each product dropped); operands are
+// kernel's phases 1-3 (dY, dgq, dW; Yw, Yu; dL, dAqk), which run as bf16
+// hi/lo triples (about 2^-16 of each product dropped); operands are
 // staged through LDS; decay factors
 // of off-diagonal 16-row tiles are anchored at the row tile's first row
 // (2^(G_c - G_a) * 2^(G_a - G_i), both <= 1), diagonal tiles use
@@ -762,6 +762,45 @@ __device__ __forceinline__ void put_hl(const InTile<DT, D, COLS, NTH>& tl, __bf1
   }
 }
 
+// A [64][COLS] fp32 tile fetched for a transposed store into hi / lo bf16
+// planes [COLS][64] (the source row index becomes the contiguous K index):
+// thread t holds rows 2 rp and 2 rp + 1 (rp = t % 32) of the float4 column
+// groups t / 32 + (NTH / 32) j, so each transposed row is written as packed
+// row pairs, consecutive lanes at consecutive words.
+template <int COLS, int NTH>
+struct TTile {
+  static constexpr int G = NTH / 32;
+  static constexpr int PER = (COLS / 4) / G;
+  static_assert(NTH % 32 == 0 && (COLS / 4) % G == 0, "transposed tile mapping");
+  float4 r[PER][2];
+  __device__ __forceinline__ void fetch(const float* src, int src_ld, int col0) {
+    const int rp = threadIdx.x & 31, cg = threadIdx.x >> 5;
+#pragma unroll
+    for (int j = 0; j < PER; ++j)
+#pragma unroll
+      for (int y = 0; y < 2; ++y)
+        r[j][y] = *reinterpret_cast<const float4*>(src + static_cast<int64_t>(2 * rp + y) * src_ld + col0 +
+                                                   4 * (cg + G * j));
+  }
+  template <int PB>
+  __device__ __forceinline__ void put_hl(__bf16* h, __bf16* l) const {
+    const int rp = threadIdx.x & 31, cg = threadIdx.x >> 5;
+#pragma unroll
+    for (int j = 0; j < PER; ++j) {
+      const int c4 = 4 * (cg + G * j);
+      const float x0[4] = {r[j][0].x, r[j][0].y, r[j][0].z, r[j][0].w};
+      const float x1[4] = {r[j][1].x, r[j][1].y, r[j][1].z, r[j][1].w};
+#pragma unroll
+      for (int e = 0; e < 4; ++e) {
+        unsigned hh, ll;
+        split2_bf16(x0[e], x1[e], hh, ll);
+        *reinterpret_cast<unsigned*>(&h[(c4 + e) * PB + 2 * rp]) = hh;
+        *reinterpret_cast<unsigned*>(&l[(c4 + e) * PB + 2 * rp]) = ll;
+      }
+    }
+  }
+};
+
 // A 16 x 16 accumulator tile (lane (r, gq): rows 4 gq + i, column r) into
 // row-major hi / lo bf16 planes of pitch PB at (row0, col0): lanes r and r ^ 1
 // swap one value of each row pair, so each lane writes packed column pairs
@@ -811,7 +850,7 @@ __global__ __launch_bounds__(kChunkThreads) void kda_bwd_chunk_kernel(BwdArgs a)
   auto ld_b = [&](int c) { return (c < cr.len) ? ld1<DTG>(a.beta, (cr.row0 + c) * H + h) : 0.f; };
   // The gradients of q, k and G accumulate in place in dq, dk and dg (dg
   // holds dG until the final reverse cumsum).  Phases 1-3 run on the matrix
-  // cores (phases 1 and 3 as bf16 hi / lo triples, phase 2 in fp32): wave wv
+  // cores as bf16 hi / lo triples: wave wv
   // owns row tile mt = wv / 2 and the NDT column tiles dt = (wv % 2) NDT + q
   // of every [64][D] product (lane (r, gq) holds rows 16 mt + 4 gq + i,
   // column 16 dt + r), so phase 2 adds to the dk and dG terms phase 1 left at
@@ -827,8 +866,7 @@ __global__ __launch_bounds__(kChunkThreads) void kda_bwd_chunk_kernel(BwdArgs a)
   const int wv = t >> 6, l = t & 63, r16 = l & 15, gq = l >> 4;
   const int mt = wv >> 1, dg_ = wv & 1;
   const int mts = __builtin_amdgcn_readfirstlane(mt);   // mt as a wave-uniform (scalar) value
-  constexpr int PX = D + 16;           // column-fragment pitch of [64][D] operands
-  constexpr int PT = kC + 16;          // column-fragment pitch of T
+  constexpr int ACC0 = (2 * kC + 4 * D) * (kC + 8) / 2;   // floats of phase 2's bf16 planes
 
   float dbrD[4], dzp[NDT];             // dbeta partials (rows 16 mt + 4 gq + i), dz partials
 #pragma unroll
@@ -839,8 +877,8 @@ __global__ __launch_bounds__(kChunkThreads) void kda_bwd_chunk_kernel(BwdArgs a)
 
   // Phase 1's dk and dG terms reach phase 2 (same thread, same positions)
   // through LDS past phase 2's buffers, not through dk and dg in memory.
-  float* const sAcc = sm + kC * PT + 2 * kC * PX;   // [2][64][D]: dk, dG
-  static_assert(kC * PT + 2 * kC * PX + 2 * kC * D <= SMEM_FLOATS, "phase 1 -> 2 accumulators");
+  float* const sAcc = sm + ACC0;   // [2][64][D]: dk, dG
+  static_assert(ACC0 + 2 * kC * D <= SMEM_FLOATS, "phase 1 -> 2 accumulators");
 
   // ---- phase 1: dY = v~ dS'^T, dgq = do S^T, dW = -dv~ S^T (K = dv in passes of HW)
   // The operands go to LDS as hi / lo bf16 planes (K contiguous) and each
@@ -848,8 +886,8 @@ __global__ __launch_bounds__(kChunkThreads) void kda_bwd_chunk_kernel(BwdArgs a)
   // lo hi, about 2^-16 of each product dropped); dW accumulates +dv~ S^T and
   // is negated where phase 2 takes it.
   f4 dW[NDT];
-  Tile<kC, kC, NTH> tT;      // phase 2's T and dv~, loaded during phase 1's last pass
-  Tile<kC, D, NTH> tY;
+  TTile<kC, NTH> tT;         // phase 2's T and dv~, loaded during phase 1's last pass
+  TTile<D, NTH> tY;
   {
     f4 dY[NDT], dgq[NDT];
 #pragma unroll
@@ -949,19 +987,32 @@ __global__ __launch_bounds__(kChunkThreads) void kda_bwd_chunk_kernel(BwdArgs a)
     }
   }
 
-  // ---- phase 2: Yw = T^T dW, Yu = T^T dv~ (K = the chunk's 64 rows)
+  // ---- phase 2: Yw = T^T dW, Yu = T^T dv~ (K = the chunk's 64 rows), as
+  // bf16 hi / lo triples: T^T, (-dW)^T and dv~^T in LDS with the chunk row
+  // contiguous; T[c][m] is zero for c < m, so row tile mt starts at the
+  // K block holding row 16 mt.
   f4 Yw[NDT], Yu[NDT];
   Tile<kC, D, NTH> tW3, tU3;
   {
-    float* sT = sm;
-    float* sX = sT + kC * PT;
-    float* sY = sX + kC * PX;
+    constexpr int PB = kC + 8;
+    static_assert((2 * kC + 4 * D) * PB / 2 <= ACC0, "phase 2 planes end below sAcc");
+    __bf16* const sTh = reinterpret_cast<__bf16*>(sm);   // T^T [64][64]
+    __bf16* const sTl = sTh + kC * PB;
+    __bf16* const sXh = sTl + kC * PB;                   // (-dW)^T [D][64]
+    __bf16* const sXl = sXh + D * PB;
+    __bf16* const sYh = sXl + D * PB;                    // dv~^T [D][64]
+    __bf16* const sYl = sYh + D * PB;
 #pragma unroll
-    for (int q = 0; q < NDT; ++q)
-#pragma unroll
-      for (int i = 0; i < 4; ++i) sX[(16 * mt + 4 * gq + i) * PX + 16 * (dg_ * NDT + q) + r16] = -dW[q][i];
-    tT.template put<PT>(sT);
-    tY.template put<PX>(sY);
+    for (int q = 0; q < NDT; ++q) {
+      const int o = (16 * (dg_ * NDT + q) + r16) * PB + 16 * mt + 4 * gq;
+      uint2 hh, ll;
+      split2_bf16(-dW[q][0], -dW[q][1], hh.x, ll.x);
+      split2_bf16(-dW[q][2], -dW[q][3], hh.y, ll.y);
+      *reinterpret_cast<uint2*>(&sXh[o]) = hh;
+      *reinterpret_cast<uint2*>(&sXl[o]) = ll;
+    }
+    tT.template put_hl<PB>(sTh, sTl);
+    tY.template put_hl<PB>(sYh, sYl);
     __syncthreads();
     tW3.fetch(a.WM + ch * kC * D, D, 0);     // phase 3's operands, during the products
     tU3.fetch(a.UM + ch * kC * D, D, 0);
@@ -969,15 +1020,16 @@ __global__ __launch_bounds__(kChunkThreads) void kda_bwd_chunk_kernel(BwdArgs a)
     for (int q = 0; q < NDT; ++q)
 #pragma unroll
       for (int i = 0; i < 4; ++i) Yw[q][i] = Yu[q][i] = 0.f;
-    // T[c][m] is zero for c < m: row tile mt needs K steps c >= 16 mt only
-#pragma unroll 4
-    for (int k = 4 * mts; k < kC / 4; ++k) {
-      const float at = sT[(4 * k + gq) * PT + 16 * mt + r16];   // (T^T)[c][m] = T[m][c]
+    for (int kb = mts >> 1; kb < kC / 32; ++kb) {
+      const int ka = (16 * mt + r16) * PB + 32 * kb + 8 * gq;
+      const b8 th = *reinterpret_cast<const b8*>(&sTh[ka]), tl = *reinterpret_cast<const b8*>(&sTl[ka]);
 #pragma unroll
       for (int q = 0; q < NDT; ++q) {
-        const int kb = (4 * k + gq) * PX + 16 * (dg_ * NDT + q) + r16;
-        Yw[q] = mfma4(at, sX[kb], Yw[q]);
-        Yu[q] = mfma4(at, sY[kb], Yu[q]);
+        const int kbb = (16 * (dg_ * NDT + q) + r16) * PB + 32 * kb + 8 * gq;
+        Yw[q] = mma3_bf16(Yw[q], th, tl, *reinterpret_cast<const b8*>(&sXh[kbb]),
+                          *reinterpret_cast<const b8*>(&sXl[kbb]));
+        Yu[q] = mma3_bf16(Yu[q], th, tl, *reinterpret_cast<const b8*>(&sYh[kbb]),
+                          *reinterpret_cast<const b8*>(&sYl[kbb]));
       }
     }
     __syncthreads();
@@ -1016,7 +1068,6 @@ __global__ __launch_bounds__(kChunkThreads) void kda_bwd_chunk_kernel(BwdArgs a)
   // outputs, two 16 x 16 tiles per wave: row tile mt, key tiles 2 (wv % 2) + q,
   // as bf16 hi / lo triples (operands row-major with the channel, the K index,
   // contiguous); key tiles above the row tile are masked to zero and skipped.
-  static_assert(kC * PT + 2 * kC * PX <= SMEM_FLOATS, "phase 2 LDS");
   float* const sDL = sm;                 // phase 4's operands, written at the end of phase 3
   float* const sDA = sDL + kC * PC;
   InTile<DTQ, D, D, NTH> tQ4, tK4;
