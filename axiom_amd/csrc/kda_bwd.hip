@@ -19,7 +19,7 @@
 //                         (dY, dgq, dW, the two transposed solves, dL, dAqk, the
 //                         score adjoints, the cumsum adjoint) and the outputs.
 // The dense products run on the fp32 matrix cores (v_mfma_f32_16x16x4f32:
-// exact fp32 products, fp32 sums), except the forward scan's and the chunk
+// exact fp32 products, fp32 sums), except the two scans' and the chunk
 // kernel's phases 1-3 (dY, dgq, dW; Yw, Yu; dL, dAqk), which run as bf16
 // hi/lo triples (about 2^-16 of each product dropped); operands are
 // staged through LDS; decay factors
@@ -436,18 +436,16 @@ __global__ __launch_bounds__(kPrepThreads, 4) void kda_bwd_prep_kernel(BwdArgs a
 }
 
 // ---------------------------------------------------------------------------
-// The reverse scan runs its products on the fp32 matrix cores
-// (v_mfma_f32_16x16x4f32, exact fp32 products; the forward scan's bf16 form
-// is described at it): lane (r = l & 15, gq = l >> 4)
-// supplies A[r][4s + gq] and B[4s + gq][r] of K step s and holds D rows
-// 4 gq + i, column r.  Eight waves per workgroup; the 32-column state slice is
-// (D/16) x 2 tiles in accumulators, D/64 tiles per wave; the [64][32] results
-// of a chunk are 8 tiles, one per wave.  LDS pitches: PW = D + 2 for [64][D]
-// operands (row fragments conflict-free, column fragments 2-way), PB = 48 for
-// [*][32] B operands, PA = 80 for Aqk read by columns.
+// The scans run their products on the bf16 matrix cores as hi/lo triples
+// (v_mfma_f32_16x16x32_bf16): lane (r = l & 15, gq = l >> 4) supplies
+// A[r][32 s + 8 gq .. + 7] and B[32 s + 8 gq .. + 7][r] of K block s and
+// holds D rows 4 gq + i, column r.  Eight waves per workgroup; the 32-column
+// state slice is (D/16) x 2 tiles in accumulators, D/64 tiles per wave; the
+// [64][32] results of a chunk are 8 tiles, one per wave.  Operands sit in LDS
+// as hi and lo bf16 planes with the K index contiguous, so each fragment is
+// one 16-byte read.
 // ---------------------------------------------------------------------------
-constexpr int kPB = 48;
-constexpr int kPA = kC + 16;
+constexpr int kPB = 48;   // fp32 pitch of the forward scan's [64][32] U slice
 
 // x0, x1 -> packed bf16 pairs hi (round to nearest even) and lo = bf16(x - hi)
 __device__ __forceinline__ void split2_bf16(float x0, float x1, unsigned& h, unsigned& l) {
@@ -462,6 +460,91 @@ __device__ __forceinline__ f4 mma3_bf16(f4 acc, const b8& ah, const b8& al, cons
   acc = mma32_bf16(acc, ah, bl);
   return mma32_bf16(acc, al, bh);
 }
+
+// A fetched fp32 tile into LDS as hi / lo bf16 planes (row pitch PB bf16).
+template <int PB, int ROWS, int COLS, int NTH>
+__device__ __forceinline__ void put_hl(const Tile<ROWS, COLS, NTH>& tl, __bf16* h, __bf16* l) {
+  typedef Tile<ROWS, COLS, NTH> TT;
+#pragma unroll
+  for (int p = 0; p < TT::PER; ++p) {
+    const int e = threadIdx.x + p * NTH;
+    if (TT::N % NTH == 0 || e < TT::N) {
+      const int row = e / TT::V, c4 = e - row * TT::V;
+      uint2 hh, ll;
+      split2_bf16(tl.r[p].x, tl.r[p].y, hh.x, ll.x);
+      split2_bf16(tl.r[p].z, tl.r[p].w, hh.y, ll.y);
+      *reinterpret_cast<uint2*>(&h[row * PB + 4 * c4]) = hh;
+      *reinterpret_cast<uint2*>(&l[row * PB + 4 * c4]) = ll;
+    }
+  }
+}
+template <int PB, int DT, int D, int COLS, int NTH>
+__device__ __forceinline__ void put_hl(const InTile<DT, D, COLS, NTH>& tl, __bf16* h, __bf16* l) {
+  typedef InTile<DT, D, COLS, NTH> TT;
+#pragma unroll
+  for (int p = 0; p < TT::PER; ++p) {
+    const int e = threadIdx.x + p * NTH;
+    if (TT::N % NTH == 0 || e < TT::N) {
+      const int r = e / TT::V, c8 = e - r * TT::V;
+      float x[8];
+      if constexpr (DT == 0) {
+        const uint4 a = tl.w[2 * p], b = tl.w[2 * p + 1];
+        x[0] = __uint_as_float(a.x); x[1] = __uint_as_float(a.y); x[2] = __uint_as_float(a.z); x[3] = __uint_as_float(a.w);
+        x[4] = __uint_as_float(b.x); x[5] = __uint_as_float(b.y); x[6] = __uint_as_float(b.z); x[7] = __uint_as_float(b.w);
+      } else {
+        const f4 lo = unpack4<DT>(make_uint2(tl.w[p].x, tl.w[p].y)), hi = unpack4<DT>(make_uint2(tl.w[p].z, tl.w[p].w));
+#pragma unroll
+        for (int q = 0; q < 4; ++q) { x[q] = lo[q]; x[4 + q] = hi[q]; }
+      }
+      uint4 hh, ll;
+      split2_bf16(x[0], x[1], hh.x, ll.x);
+      split2_bf16(x[2], x[3], hh.y, ll.y);
+      split2_bf16(x[4], x[5], hh.z, ll.z);
+      split2_bf16(x[6], x[7], hh.w, ll.w);
+      *reinterpret_cast<uint4*>(&h[r * PB + 8 * c8]) = hh;
+      *reinterpret_cast<uint4*>(&l[r * PB + 8 * c8]) = ll;
+    }
+  }
+}
+
+// A [64][COLS] fp32 tile fetched for a transposed store into hi / lo bf16
+// planes [COLS][64] (the source row index becomes the contiguous K index):
+// thread t holds rows 2 rp and 2 rp + 1 (rp = t % 32) of the float4 column
+// groups t / 32 + (NTH / 32) j, so each transposed row is written as packed
+// row pairs, consecutive lanes at consecutive words.
+template <int COLS, int NTH>
+struct TTile {
+  static constexpr int G = NTH / 32;
+  static constexpr int PER = (COLS / 4) / G;
+  static_assert(NTH % 32 == 0 && (COLS / 4) % G == 0, "transposed tile mapping");
+  float4 r[PER][2];
+  __device__ __forceinline__ void fetch(const float* src, int src_ld, int col0) {
+    const int rp = threadIdx.x & 31, cg = threadIdx.x >> 5;
+#pragma unroll
+    for (int j = 0; j < PER; ++j)
+#pragma unroll
+      for (int y = 0; y < 2; ++y)
+        r[j][y] = *reinterpret_cast<const float4*>(src + static_cast<int64_t>(2 * rp + y) * src_ld + col0 +
+                                                   4 * (cg + G * j));
+  }
+  template <int PB>
+  __device__ __forceinline__ void put_hl(__bf16* h, __bf16* l) const {
+    const int rp = threadIdx.x & 31, cg = threadIdx.x >> 5;
+#pragma unroll
+    for (int j = 0; j < PER; ++j) {
+      const int c4 = 4 * (cg + G * j);
+      const float x0[4] = {r[j][0].x, r[j][0].y, r[j][0].z, r[j][0].w};
+      const float x1[4] = {r[j][1].x, r[j][1].y, r[j][1].z, r[j][1].w};
+#pragma unroll
+      for (int e = 0; e < 4; ++e) {
+        unsigned hh, ll;
+        split2_bf16(x0[e], x1[e], hh, ll);
+        *reinterpret_cast<unsigned*>(&h[(c4 + e) * PB + 2 * rp]) = hh;
+        *reinterpret_cast<unsigned*>(&l[(c4 + e) * PB + 2 * rp]) = ll;
+      }
+    }
+  }
+};
 
 // forward state scan of one (chain, 32-column slice): S_in and v~ per chunk.
 // The products run as bf16 hi/lo triples (v_mfma_f32_16x16x32_bf16, lane
@@ -611,14 +694,34 @@ __global__ __launch_bounds__(kScanThreads) void kda_bwd_fscan_kernel(BwdArgs a) 
   }
 }
 
-// reverse scan of one (chain, 32-column slice): dS per chunk, dv~, dh0
+// reverse scan of one (chain, 32-column slice): dS per chunk, dv~, dh0.
+// The products run as bf16 hi/lo triples, as in the forward scan: lambda k
+// and the state cotangent slice dS^T with the channel as the K index; Aqk^T,
+// do^T, (gamma q)^T, W^T and (-dv~)^T with the chunk row as the K index
+// (transposed stores of row pairs).  dS itself stays fp32 in the accumulators.
 template <int D, int DO>
 __global__ __launch_bounds__(kScanThreads) void kda_bwd_rscan_kernel(BwdArgs a) {
-  constexpr int PW = D + 2;
   constexpr int NS = D / 32;
   constexpr int NST = D / 64;
-  __shared__ float sX[kC * PW], sY[kC * PW], sA[kC * kPA];
-  __shared__ float sS[D * kPB], sDo[kC * kPB], sDv[kC * kPB], sGC[D];
+  constexpr int PW = D + 8;     // bf16 pitch of rows whose K index is a channel
+  constexpr int PK = kC + 8;    // bf16 pitch of rows whose K index is a chunk row
+  // region R: lambda k [64][PW] and Aqk^T [64][PK] for dv~, then
+  // (gamma q)^T [D][PK] and W^T [D][PK] for the dS update
+  constexpr int RA = 2 * kC * PW + 2 * kC * PK, RB = 4 * D * PK;
+  constexpr int RN = RA > RB ? RA : RB;
+  __shared__ __attribute__((aligned(16))) __bf16 sR[RN];
+  __shared__ __attribute__((aligned(16))) __bf16 sSh[32 * PW], sSl[32 * PW];   // dS^T [32][D]
+  __shared__ __attribute__((aligned(16))) __bf16 sOh[32 * PK], sOl[32 * PK];   // do^T [32][64]
+  __shared__ __attribute__((aligned(16))) __bf16 sVh[32 * PK], sVl[32 * PK];   // (-dv~)^T [32][64]
+  __shared__ float sGC[D];
+  __bf16* const sLh = sR;
+  __bf16* const sLl = sLh + kC * PW;
+  __bf16* const sAh = sLl + kC * PW;
+  __bf16* const sAl = sAh + kC * PK;
+  __bf16* const sQh = sR;
+  __bf16* const sQl = sQh + D * PK;
+  __bf16* const sWh = sQl + D * PK;
+  __bf16* const sWl = sWh + D * PK;
   constexpr int NTH = kScanThreads;
   const int t = threadIdx.x, wv = t >> 6, l = t & 63, r = l & 15, gq = l >> 4;
   const int H = a.H;
@@ -627,6 +730,7 @@ __global__ __launch_bounds__(kScanThreads) void kda_bwd_rscan_kernel(BwdArgs a) 
   const int b = chain / H, h = chain - b * H;
   const int c0 = 32 * split;
   const int mt = wv >> 1, ct = wv & 1;
+  const int mts = __builtin_amdgcn_readfirstlane(mt);
   int rt[NST], cs[NST];
 #pragma unroll
   for (int q = 0; q < NST; ++q) { rt[q] = (wv * NST + q) >> 1; cs[q] = (wv * NST + q) & 1; }
@@ -641,11 +745,12 @@ __global__ __launch_bounds__(kScanThreads) void kda_bwd_rscan_kernel(BwdArgs a) 
   // Operands of the two products of a chunk, loaded into registers one
   // product ahead: lambda*k and Aqk (for dv~) during the previous chunk's dS
   // update, gamma*q and W (for dS) during this chunk's dv~.
-  Tile<kC, D, NTH> tX, tY;
-  Tile<kC, kC, NTH> tA;
+  Tile<kC, D, NTH> tL;
+  TTile<kC, NTH> tA;
+  TTile<D, NTH> tQ, tW;
   auto fetch_a = [&](int n) {
     const int64_t ch = (static_cast<int64_t>(b) * a.NT + n) * H + h;
-    tX.fetch(a.KL + ch * kC * D, D, 0);
+    tL.fetch(a.KL + ch * kC * D, D, 0);
     tA.fetch(a.AQ + ch * kC * kC, kC, 0);
   };
   if (a.NT > 0) fetch_a(a.NT - 1);
@@ -655,41 +760,74 @@ __global__ __launch_bounds__(kScanThreads) void kda_bwd_rscan_kernel(BwdArgs a) 
     const ChunkRows cr = chunk_rows(a, u);
     float* DS = a.DS + ch * D * D;
 #pragma unroll
-    for (int q = 0; q < NST; ++q)
+    for (int q = 0; q < NST; ++q) {
+      const int m0 = 16 * rt[q] + 4 * gq, col = 16 * cs[q] + r;
 #pragma unroll
-      for (int i = 0; i < 4; ++i) {
-        const int row = 16 * rt[q] + 4 * gq + i, col = 16 * cs[q] + r;
-        DS[row * D + c0 + col] = dS[q][i];
-        sS[row * kPB + col] = dS[q][i];
+      for (int i = 0; i < 4; ++i) DS[(m0 + i) * D + c0 + col] = dS[q][i];
+      uint2 hh, ll;
+      split2_bf16(dS[q][0], dS[q][1], hh.x, ll.x);
+      split2_bf16(dS[q][2], dS[q][3], hh.y, ll.y);
+      *reinterpret_cast<uint2*>(&sSh[col * PW + m0]) = hh;
+      *reinterpret_cast<uint2*>(&sSl[col * PW + m0]) = ll;
+    }
+    put_hl<PW>(tL, sLh, sLl);
+    tA.template put_hl<PK>(sAh, sAl);
+    // do^T of the slice: thread t < 256 holds rows 2 rp, 2 rp + 1 of
+    // columns c0 + 4 cg .. + 3 (rows past len read as zero)
+    if (t < 256) {
+      const int rp = t & 31, cg = t >> 5;
+      f4 x[2];
+#pragma unroll
+      for (int y = 0; y < 2; ++y) {
+        const int row = 2 * rp + y;
+        const bool ok = row < cr.len;
+        const f4 v = ld4<DO>(a.dout, ((cr.row0 + (ok ? row : 0)) * H + h) * D + c0 + 4 * cg);
+#pragma unroll
+        for (int e = 0; e < 4; ++e) x[y][e] = ok ? v[e] : 0.f;
       }
-    tX.template put<PW>(sX);
-    tA.template put<kPA>(sA);
-    lds_load_in<DO, D, 32, kPB, NTH>(sDo, a.dout, cr.row0, cr.len, H, h, c0, 1.f);
-    if (t < D) sGC[t] = a.GCV[ch * D + t];
-    tX.fetch(a.QG + ch * kC * D, D, 0);
-    tY.fetch(a.WM + ch * kC * D, D, 0);
-    __syncthreads();
-    // dv~ = (lambda k) dS + Aqk^T do
-    {
-      f4 acc0 = {0.f, 0.f, 0.f, 0.f}, acc1 = {0.f, 0.f, 0.f, 0.f};
-#pragma unroll 8
-      for (int k = 0; k < D / 4; ++k)
-        acc0 = mfma4(sX[(16 * mt + r) * PW + 4 * k + gq], sS[(4 * k + gq) * kPB + 16 * ct + r], acc0);
-#pragma unroll 8
-      for (int k = 0; k < kC / 4; ++k)
-        acc1 = mfma4(sA[(4 * k + gq) * kPA + 16 * mt + r], sDo[(4 * k + gq) * kPB + 16 * ct + r], acc1);
-      float* DVT = a.DVT + ch * kC * D;
 #pragma unroll
-      for (int i = 0; i < 4; ++i) {
-        const int row = 16 * mt + 4 * gq + i, col = 16 * ct + r;
-        const float v = acc0[i] + acc1[i];
-        sDv[row * kPB + col] = v;
-        DVT[row * D + c0 + col] = v;
+      for (int e = 0; e < 4; ++e) {
+        unsigned hh, ll;
+        split2_bf16(x[0][e], x[1][e], hh, ll);
+        *reinterpret_cast<unsigned*>(&sOh[(4 * cg + e) * PK + 2 * rp]) = hh;
+        *reinterpret_cast<unsigned*>(&sOl[(4 * cg + e) * PK + 2 * rp]) = ll;
       }
     }
+    if (t < D) sGC[t] = a.GCV[ch * D + t];
+    tQ.fetch(a.QG + ch * kC * D, D, 0);
+    tW.fetch(a.WM + ch * kC * D, D, 0);
     __syncthreads();
-    tX.template put<PW>(sX);
-    tY.template put<PW>(sY);
+    // dv~ = (lambda k) dS + Aqk^T do; Aqk[j][m] is zero for j < m, so row
+    // tile mt starts at the K block holding row 16 mt
+    {
+      f4 acc0 = {0.f, 0.f, 0.f, 0.f}, acc1 = {0.f, 0.f, 0.f, 0.f};
+#pragma unroll
+      for (int kb = 0; kb < D / 32; ++kb) {
+        const int ka = (16 * mt + r) * PW + 32 * kb + 8 * gq, kbb = (16 * ct + r) * PW + 32 * kb + 8 * gq;
+        acc0 = mma3_bf16(acc0, *reinterpret_cast<const b8*>(&sLh[ka]), *reinterpret_cast<const b8*>(&sLl[ka]),
+                         *reinterpret_cast<const b8*>(&sSh[kbb]), *reinterpret_cast<const b8*>(&sSl[kbb]));
+      }
+      for (int kb = mts >> 1; kb < kC / 32; ++kb) {
+        const int ka = (16 * mt + r) * PK + 32 * kb + 8 * gq, kbb = (16 * ct + r) * PK + 32 * kb + 8 * gq;
+        acc1 = mma3_bf16(acc1, *reinterpret_cast<const b8*>(&sAh[ka]), *reinterpret_cast<const b8*>(&sAl[ka]),
+                         *reinterpret_cast<const b8*>(&sOh[kbb]), *reinterpret_cast<const b8*>(&sOl[kbb]));
+      }
+      float* DVT = a.DVT + ch * kC * D;
+      float v[4];
+#pragma unroll
+      for (int i = 0; i < 4; ++i) {
+        v[i] = acc0[i] + acc1[i];
+        DVT[(16 * mt + 4 * gq + i) * D + c0 + 16 * ct + r] = v[i];
+      }
+      uint2 hh, ll;
+      split2_bf16(-v[0], -v[1], hh.x, ll.x);
+      split2_bf16(-v[2], -v[3], hh.y, ll.y);
+      *reinterpret_cast<uint2*>(&sVh[(16 * ct + r) * PK + 16 * mt + 4 * gq]) = hh;
+      *reinterpret_cast<uint2*>(&sVl[(16 * ct + r) * PK + 16 * mt + 4 * gq]) = ll;
+    }
+    __syncthreads();
+    tQ.template put_hl<PK>(sQh, sQl);
+    tW.template put_hl<PK>(sWh, sWl);
     if (n > 0) fetch_a(n - 1);
     __syncthreads();
     // dS <- gamma_C dS + (gamma q)^T do - W^T dv~
@@ -697,13 +835,15 @@ __global__ __launch_bounds__(kScanThreads) void kda_bwd_rscan_kernel(BwdArgs a) 
     for (int q = 0; q < NST; ++q)
 #pragma unroll
       for (int i = 0; i < 4; ++i) dS[q][i] *= sGC[16 * rt[q] + 4 * gq + i];
-#pragma unroll 4
-    for (int k = 0; k < kC / 4; ++k)
+#pragma unroll
+    for (int kb = 0; kb < kC / 32; ++kb)
 #pragma unroll
       for (int q = 0; q < NST; ++q) {
-        const int kr = (4 * k + gq) * PW + 16 * rt[q] + r, kb = (4 * k + gq) * kPB + 16 * cs[q] + r;
-        dS[q] = mfma4(sX[kr], sDo[kb], dS[q]);
-        dS[q] = mfma4(-sY[kr], sDv[kb], dS[q]);
+        const int ka = (16 * rt[q] + r) * PK + 32 * kb + 8 * gq, kbb = (16 * cs[q] + r) * PK + 32 * kb + 8 * gq;
+        dS[q] = mma3_bf16(dS[q], *reinterpret_cast<const b8*>(&sQh[ka]), *reinterpret_cast<const b8*>(&sQl[ka]),
+                          *reinterpret_cast<const b8*>(&sOh[kbb]), *reinterpret_cast<const b8*>(&sOl[kbb]));
+        dS[q] = mma3_bf16(dS[q], *reinterpret_cast<const b8*>(&sWh[ka]), *reinterpret_cast<const b8*>(&sWl[ka]),
+                          *reinterpret_cast<const b8*>(&sVh[kbb]), *reinterpret_cast<const b8*>(&sVl[kbb]));
       }
     __syncthreads();
   }
@@ -715,91 +855,6 @@ __global__ __launch_bounds__(kScanThreads) void kda_bwd_rscan_kernel(BwdArgs a) 
         a.dh0[(static_cast<int64_t>(chain) * D + 16 * rt[q] + 4 * gq + i) * D + c0 + 16 * cs[q] + r] = dS[q][i];
   }
 }
-
-// A fetched fp32 tile into LDS as hi / lo bf16 planes (row pitch PB bf16).
-template <int PB, int ROWS, int COLS, int NTH>
-__device__ __forceinline__ void put_hl(const Tile<ROWS, COLS, NTH>& tl, __bf16* h, __bf16* l) {
-  typedef Tile<ROWS, COLS, NTH> TT;
-#pragma unroll
-  for (int p = 0; p < TT::PER; ++p) {
-    const int e = threadIdx.x + p * NTH;
-    if (TT::N % NTH == 0 || e < TT::N) {
-      const int row = e / TT::V, c4 = e - row * TT::V;
-      uint2 hh, ll;
-      split2_bf16(tl.r[p].x, tl.r[p].y, hh.x, ll.x);
-      split2_bf16(tl.r[p].z, tl.r[p].w, hh.y, ll.y);
-      *reinterpret_cast<uint2*>(&h[row * PB + 4 * c4]) = hh;
-      *reinterpret_cast<uint2*>(&l[row * PB + 4 * c4]) = ll;
-    }
-  }
-}
-template <int PB, int DT, int D, int COLS, int NTH>
-__device__ __forceinline__ void put_hl(const InTile<DT, D, COLS, NTH>& tl, __bf16* h, __bf16* l) {
-  typedef InTile<DT, D, COLS, NTH> TT;
-#pragma unroll
-  for (int p = 0; p < TT::PER; ++p) {
-    const int e = threadIdx.x + p * NTH;
-    if (TT::N % NTH == 0 || e < TT::N) {
-      const int r = e / TT::V, c8 = e - r * TT::V;
-      float x[8];
-      if constexpr (DT == 0) {
-        const uint4 a = tl.w[2 * p], b = tl.w[2 * p + 1];
-        x[0] = __uint_as_float(a.x); x[1] = __uint_as_float(a.y); x[2] = __uint_as_float(a.z); x[3] = __uint_as_float(a.w);
-        x[4] = __uint_as_float(b.x); x[5] = __uint_as_float(b.y); x[6] = __uint_as_float(b.z); x[7] = __uint_as_float(b.w);
-      } else {
-        const f4 lo = unpack4<DT>(make_uint2(tl.w[p].x, tl.w[p].y)), hi = unpack4<DT>(make_uint2(tl.w[p].z, tl.w[p].w));
-#pragma unroll
-        for (int q = 0; q < 4; ++q) { x[q] = lo[q]; x[4 + q] = hi[q]; }
-      }
-      uint4 hh, ll;
-      split2_bf16(x[0], x[1], hh.x, ll.x);
-      split2_bf16(x[2], x[3], hh.y, ll.y);
-      split2_bf16(x[4], x[5], hh.z, ll.z);
-      split2_bf16(x[6], x[7], hh.w, ll.w);
-      *reinterpret_cast<uint4*>(&h[r * PB + 8 * c8]) = hh;
-      *reinterpret_cast<uint4*>(&l[r * PB + 8 * c8]) = ll;
-    }
-  }
-}
-
-// A [64][COLS] fp32 tile fetched for a transposed store into hi / lo bf16
-// planes [COLS][64] (the source row index becomes the contiguous K index):
-// thread t holds rows 2 rp and 2 rp + 1 (rp = t % 32) of the float4 column
-// groups t / 32 + (NTH / 32) j, so each transposed row is written as packed
-// row pairs, consecutive lanes at consecutive words.
-template <int COLS, int NTH>
-struct TTile {
-  static constexpr int G = NTH / 32;
-  static constexpr int PER = (COLS / 4) / G;
-  static_assert(NTH % 32 == 0 && (COLS / 4) % G == 0, "transposed tile mapping");
-  float4 r[PER][2];
-  __device__ __forceinline__ void fetch(const float* src, int src_ld, int col0) {
-    const int rp = threadIdx.x & 31, cg = threadIdx.x >> 5;
-#pragma unroll
-    for (int j = 0; j < PER; ++j)
-#pragma unroll
-      for (int y = 0; y < 2; ++y)
-        r[j][y] = *reinterpret_cast<const float4*>(src + static_cast<int64_t>(2 * rp + y) * src_ld + col0 +
-                                                   4 * (cg + G * j));
-  }
-  template <int PB>
-  __device__ __forceinline__ void put_hl(__bf16* h, __bf16* l) const {
-    const int rp = threadIdx.x & 31, cg = threadIdx.x >> 5;
-#pragma unroll
-    for (int j = 0; j < PER; ++j) {
-      const int c4 = 4 * (cg + G * j);
-      const float x0[4] = {r[j][0].x, r[j][0].y, r[j][0].z, r[j][0].w};
-      const float x1[4] = {r[j][1].x, r[j][1].y, r[j][1].z, r[j][1].w};
-#pragma unroll
-      for (int e = 0; e < 4; ++e) {
-        unsigned hh, ll;
-        split2_bf16(x0[e], x1[e], hh, ll);
-        *reinterpret_cast<unsigned*>(&h[(c4 + e) * PB + 2 * rp]) = hh;
-        *reinterpret_cast<unsigned*>(&l[(c4 + e) * PB + 2 * rp]) = ll;
-      }
-    }
-  }
-};
 
 // A 16 x 16 accumulator tile (lane (r, gq): rows 4 gq + i, column r) into
 // row-major hi / lo bf16 planes of pitch PB at (row0, col0): lanes r and r ^ 1
