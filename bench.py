@@ -211,7 +211,7 @@ def bench_backward(args, fwd_inputs, device):
     return dict(us_per_call=t_call * 1e6, tokens_per_s=B * T / t_call, calls=args.bwd_steps,
                 roofline={"bound": "hbm", "achieved": gbps, "peak": HBM_PEAK_GBPS, "unit": "GB/s",
                           "frac": gbps / HBM_PEAK_GBPS, "algorithmic_bytes_per_call": nbytes},
-                kernels="kda_bwd_prep + kda_bwd_fscan + kda_bwd_rscan + kda_bwd_chunk (fp32)",
+                kernels="kda_bwd_prep + kda_bwd_fscan + kda_bwd_rscan + kda_bwd_chunk (fp32 arithmetic, bf16 hi/lo products)",
                 config="B4 T4096 H16 d128 bf16 inputs, fp32 do and dht, zero h0")
 
 
