@@ -407,13 +407,15 @@ __global__ __launch_bounds__(kPrepThreads, 4) void kda_bwd_prep_kernel(BwdArgs a
     __syncthreads();
     constexpr int NDT = HD / 32;
     const int mt = wv >> 1, dg = wv & 1;
+    const int mts = __builtin_amdgcn_readfirstlane(mt);
     f4 accW[NDT], accU[NDT];
 #pragma unroll
     for (int q = 0; q < NDT; ++q)
 #pragma unroll
       for (int e = 0; e < 4; ++e) accW[q][e] = accU[q][e] = 0.f;
+    // T[c][i] is zero for i > c: row tile mt needs K steps i < 16 (mt + 1) only
 #pragma unroll 4
-    for (int k = 0; k < kC / 4; ++k) {
+    for (int k = 0; k < 4 * (mts + 1); ++k) {
       const float at = sT[(16 * mt + r16) * PC + 4 * k + gq];
 #pragma unroll
       for (int q = 0; q < NDT; ++q) {
