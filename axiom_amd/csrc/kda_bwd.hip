@@ -59,6 +59,8 @@ struct BwdDims {
   static constexpr int NJ = D / 16;   // columns per thread of a [64][D] product
 };
 
+constexpr int cmax(int a, int b) { return a > b ? a : b; }
+
 // Token row of chunk row c (dense layout) and whether it exists.
 struct ChunkRows {
   int64_t row0;   // b * T + n * 64
@@ -890,9 +892,12 @@ __global__ __launch_bounds__(kChunkThreads) void kda_bwd_chunk_kernel(BwdArgs a)
   constexpr int NJ = D / TC;          // columns per thread of a [64][D] product
   constexpr int HW = 64;             // value columns per pass of phase 1
   constexpr int NH = D / HW;
-  // phase 4 is the largest: dL, dAqk [64][65]; q, k, G [64][P]; three [16][PF]
-  constexpr int PF = D + 16;          // column-fragment pitch of phase 4's factored operands
-  constexpr int SMEM_FLOATS = 2 * kC * PC + 3 * kC * P + 3 * 16 * PF + kC;
+  // LDS of the largest phase: phase 1's bf16 planes, phase 2's planes plus
+  // the dk, dG hand-off, phase 3's planes, phase 4's dL, dAqk [64][PC] and
+  // q, k, G [64][P] plus beta
+  constexpr int ACC0 = (2 * kC + 4 * D) * (kC + 8) / 2;   // floats of phase 2's bf16 planes
+  constexpr int SMEM_FLOATS = cmax(cmax((6 * kC + 4 * D) * (HW + 8) / 2, ACC0 + 2 * kC * D),
+                                   cmax(8 * kC * (D + 8) / 2, 2 * kC * PC + 3 * kC * P + kC));
   __shared__ __attribute__((aligned(16))) float sm[SMEM_FLOATS];
   const int t = threadIdx.x, rm = t / TC, cn = t % TC;
   const int H = a.H;
@@ -923,7 +928,6 @@ __global__ __launch_bounds__(kChunkThreads) void kda_bwd_chunk_kernel(BwdArgs a)
   const int wv = t >> 6, l = t & 63, r16 = l & 15, gq = l >> 4;
   const int mt = wv >> 1, dg_ = wv & 1;
   const int mts = __builtin_amdgcn_readfirstlane(mt);   // mt as a wave-uniform (scalar) value
-  constexpr int ACC0 = (2 * kC + 4 * D) * (kC + 8) / 2;   // floats of phase 2's bf16 planes
 
   float dbrD[4], dzp[NDT];             // dbeta partials (rows 16 mt + 4 gq + i), dz partials
 #pragma unroll
@@ -1228,10 +1232,7 @@ __global__ __launch_bounds__(kChunkThreads) void kda_bwd_chunk_kernel(BwdArgs a)
     float* sQ = sDA + kC * PC;       // q * scale
     float* sK = sQ + kC * P;
     float* sG = sK + kC * P;
-    float* sXq = sG + kC * P;        // [16][PF] q_c 2^(G_c - G_a), rows of tile R
-    float* sXk = sXq + 16 * PF;      // [16][PF] beta_c k_c 2^(G_c - G_a)
-    float* sKf = sXk + 16 * PF;      // [16][PF] k_i 2^(G_a - G_i), rows of key tile s
-    float* sB = sKf + 16 * PF;
+    float* sB = sG + kC * P;
     tQ4.template put<P>(sQ, a.scale);
     tK4.template put<P>(sK, 1.f);
     tG4.template put<P>(sG);
@@ -1241,7 +1242,10 @@ __global__ __launch_bounds__(kChunkThreads) void kda_bwd_chunk_kernel(BwdArgs a)
     const int d = 16 * (wv % NCT) + r16;
     // Row tiles in descending order: when tile R is finished (its diagonal and
     // the read-modify-write of its rows), every row tile below it has already
-    // added its column-side terms to colS[R].
+    // added its column-side terms to colS[R].  Each lane forms the factored
+    // operands it feeds to the matrix cores itself (rows 4 k + gq of a tile,
+    // its column d), so the loop reads only LDS written before it and needs
+    // no barrier.
     f4 colS[3];
 #pragma unroll
     for (int q = 0; q < 3; ++q)
@@ -1252,37 +1256,32 @@ __global__ __launch_bounds__(kChunkThreads) void kda_bwd_chunk_kernel(BwdArgs a)
     for (int R = 3; R >= 0; --R) {
       const int a0 = 16 * R;
       f4 accA = {0.f, 0.f, 0.f, 0.f}, accK = {0.f, 0.f, 0.f, 0.f};
-      if (R > 0) {
-        for (int e = t; e < 16 * D; e += NTH) {
-          const int rr = e / D, dd = e - rr * D;
-          const float fr = ex2(sG[(a0 + rr) * P + dd] - sG[a0 * P + dd]);
-          sXq[rr * PF + dd] = sQ[(a0 + rr) * P + dd] * fr;
-          sXk[rr * PF + dd] = sK[(a0 + rr) * P + dd] * sB[a0 + rr] * fr;
-        }
-      }
+      if (mine && R > 0) {
+        const float ga = sG[a0 * P + d];
+        float xq[4], xk[4];      // q_c 2^(G_c - G_a), beta_c k_c 2^(G_c - G_a): rows a0 + 4 k + gq
 #pragma unroll
-      for (int sk = 0; sk < R; ++sk) {
-        for (int e = t; e < 16 * D; e += NTH) {
-          const int ii = e / D, dd = e - ii * D;
-          sKf[ii * PF + dd] = sK[(16 * sk + ii) * P + dd] * ex2(sG[a0 * P + dd] - sG[(16 * sk + ii) * P + dd]);
+        for (int k = 0; k < 4; ++k) {
+          const int c = a0 + 4 * k + gq;
+          const float fr = ex2(sG[c * P + d] - ga);
+          xq[k] = sQ[c * P + d] * fr;
+          xk[k] = sK[c * P + d] * sB[c] * fr;
         }
-        __syncthreads();
-        if (mine) {
+#pragma unroll
+        for (int sk = 0; sk < R; ++sk) {
           f4 cS = {0.f, 0.f, 0.f, 0.f};
 #pragma unroll
           for (int k = 0; k < 4; ++k) {
-            const int kr = (4 * k + gq) * PF + 16 * wv + r16;
-            const float kb = sKf[kr];
+            const int i = 16 * sk + 4 * k + gq;
+            const float kb = sK[i * P + d] * ex2(ga - sG[i * P + d]);   // k_i 2^(G_a - G_i)
             accA = mfma4(sDA[(a0 + r16) * PC + 16 * sk + 4 * k + gq], kb, accA);
             accK = mfma4(sDL[(a0 + r16) * PC + 16 * sk + 4 * k + gq], kb, accK);
-            cS = mfma4(sDA[(a0 + 4 * k + gq) * PC + 16 * sk + r16], sXq[kr], cS);
-            cS = mfma4(sDL[(a0 + 4 * k + gq) * PC + 16 * sk + r16], sXk[kr], cS);
+            cS = mfma4(sDA[(a0 + 4 * k + gq) * PC + 16 * sk + r16], xq[k], cS);
+            cS = mfma4(sDL[(a0 + 4 * k + gq) * PC + 16 * sk + r16], xk[k], cS);
           }
 #pragma unroll
           for (int e = 0; e < 4; ++e)
-            colS[sk][e] += cS[e] * ex2(sG[a0 * P + d] - sG[(16 * sk + 4 * gq + e) * P + d]);
+            colS[sk][e] += cS[e] * ex2(ga - sG[(16 * sk + 4 * gq + e) * P + d]);
         }
-        __syncthreads();   // sKf, and after the last key tile sXq / sXk, free again
       }
       if (mine) {
         float gd[16], kd[16], qd[16];
