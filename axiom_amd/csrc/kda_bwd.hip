@@ -1256,6 +1256,19 @@ __global__ __launch_bounds__(kChunkThreads) void kda_bwd_chunk_kernel(BwdArgs a)
     for (int R = 3; R >= 0; --R) {
       const int a0 = 16 * R;
       f4 accA = {0.f, 0.f, 0.f, 0.f}, accK = {0.f, 0.f, 0.f, 0.f};
+      // this tile's partial dq, dG, dk, loaded before its arithmetic (pad
+      // rows read row 0 and are not stored)
+      float oq[4], oG[4], ok[4];
+      if (mine) {
+#pragma unroll
+        for (int e = 0; e < 4; ++e) {
+          const int c = a0 + 4 * gq + e;
+          const int64_t o = in_idx(c < cr.len ? c : 0, d);
+          oq[e] = gq_[o];
+          oG[e] = gG_[o];
+          ok[e] = gk_[o];
+        }
+      }
       if (mine && R > 0) {
         const float ga = sG[a0 * P + d];
         float xq[4], xk[4];      // q_c 2^(G_c - G_a), beta_c k_c 2^(G_c - G_a): rows a0 + 4 k + gq
@@ -1284,44 +1297,48 @@ __global__ __launch_bounds__(kChunkThreads) void kda_bwd_chunk_kernel(BwdArgs a)
         }
       }
       if (mine) {
-        float gd[16], kd[16], qd[16];
+        // With G non-increasing (g <= 0), the pair (c, a0 + y) of the row
+        // side (y <= x) decays by 2^(G_c - G_y) and the pair (a0 + y, c) of
+        // the column side (y >= x) by 2^(G_y - G_c): both are 2^-|G_c - G_y|,
+        // and the masked cotangents zero the side a given y does not belong to.
+        // Row y's G, k, q, beta are read once for the lane's four rows c.
+        float gc[4], rA[4], rK[4], cS[4];
 #pragma unroll
+        for (int e = 0; e < 4; ++e) {
+          gc[e] = sG[(a0 + 4 * gq + e) * P + d];
+          rA[e] = rK[e] = cS[e] = 0.f;
+        }
+#pragma unroll 4
         for (int y = 0; y < 16; ++y) {
-          gd[y] = sG[(a0 + y) * P + d];
-          kd[y] = sK[(a0 + y) * P + d];
-          qd[y] = sQ[(a0 + y) * P + d];
+          const float gy = sG[(a0 + y) * P + d], ky = sK[(a0 + y) * P + d];
+          const float qy = sQ[(a0 + y) * P + d], by = sB[a0 + y];
+#pragma unroll
+          for (int e = 0; e < 4; ++e) {
+            const int c = a0 + 4 * gq + e;
+            const float ev = ex2(-fabsf(gc[e] - gy));
+            const float kr = ky * ev;
+            rA[e] = fmaf(sDA[c * PC + a0 + y], kr, rA[e]);
+            rK[e] = fmaf(sDL[c * PC + a0 + y], kr, rK[e]);
+            cS[e] = fmaf(sDA[(a0 + y) * PC + c], qy * ev, cS[e]);
+            cS[e] = fmaf(sDL[(a0 + y) * PC + c], by * kr, cS[e]);
+          }
         }
 #pragma unroll
         for (int e = 0; e < 4; ++e) {
           const int c = a0 + 4 * gq + e;
-          const float gc = sG[c * P + d], kc = sK[c * P + d], qc = sQ[c * P + d], bc = sB[c];
-          float rA = 0.f, rK = 0.f, cS = 0.f;
-          // With G non-increasing (g <= 0), the pair (c, a0 + y) of the row
-          // side (y <= x) decays by 2^(G_c - G_y) and the pair (a0 + y, c) of
-          // the column side (y >= x) by 2^(G_y - G_c): both are 2^-|G_c - G_y|,
-          // and the masked cotangents zero the side a given y does not belong to.
-#pragma unroll
-          for (int y = 0; y < 16; ++y) {
-            const float ev = ex2(-fabsf(gc - gd[y]));
-            const float kr = kd[y] * ev;
-            rA = fmaf(sDA[c * PC + a0 + y], kr, rA);
-            rK = fmaf(sDL[c * PC + a0 + y], kr, rK);
-            cS = fmaf(sDA[(a0 + y) * PC + c], qd[y] * ev, cS);
-            cS = fmaf(sDL[(a0 + y) * PC + c], sB[a0 + y] * kr, cS);
-          }
+          const float kc = sK[c * P + d], qc = sQ[c * P + d], bc = sB[c];
           if (R > 0) {
-            const float f = ex2(sG[c * P + d] - sG[a0 * P + d]);
-            rA = fmaf(accA[e], f, rA);
-            rK = fmaf(accK[e], f, rK);
+            const float f = ex2(gc[e] - sG[a0 * P + d]);
+            rA[e] = fmaf(accA[e], f, rA[e]);
+            rK[e] = fmaf(accK[e], f, rK[e]);
           }
-          if (R < 3) cS += colS[R < 3 ? R : 0][e];
-          dbq[R][e] = rK * kc;
+          if (R < 3) cS[e] += colS[R < 3 ? R : 0][e];
+          dbq[R][e] = rK[e] * kc;
           if (c < cr.len) {
             const int64_t o = in_idx(c, d);
-            const float oq = gq_[o], oG = gG_[o], ok = gk_[o];
-            gq_[o] = oq + rA * a.scale;
-            gG_[o] = oG + rA * qc + rK * kc * bc - cS * kc;
-            gk_[o] = ok + rK * bc + cS;
+            gq_[o] = oq[e] + rA[e] * a.scale;
+            gG_[o] = oG[e] + rA[e] * qc + rK[e] * kc * bc - cS[e] * kc;
+            gk_[o] = ok[e] + rK[e] * bc + cS[e];
           }
         }
       }
