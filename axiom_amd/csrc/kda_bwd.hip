@@ -888,8 +888,6 @@ __global__ __launch_bounds__(kChunkThreads) void kda_bwd_chunk_kernel(BwdArgs a)
   typedef BwdDims<D> BD;
   constexpr int P = BD::P, PC = BD::PC;
   constexpr int NTH = kChunkThreads;
-  constexpr int TC = NTH / 16;        // threads per row group: columns cn + TC j
-  constexpr int NJ = D / TC;          // columns per thread of a [64][D] product
   constexpr int HW = 64;             // value columns per pass of phase 1
   constexpr int NH = D / HW;
   // LDS of the largest phase: phase 1's bf16 planes, phase 2's planes plus
@@ -899,7 +897,7 @@ __global__ __launch_bounds__(kChunkThreads) void kda_bwd_chunk_kernel(BwdArgs a)
   constexpr int SMEM_FLOATS = cmax(cmax((6 * kC + 4 * D) * (HW + 8) / 2, ACC0 + 2 * kC * D),
                                    cmax(8 * kC * (D + 8) / 2, 2 * kC * PC + 3 * kC * P + kC));
   __shared__ __attribute__((aligned(16))) float sm[SMEM_FLOATS];
-  const int t = threadIdx.x, rm = t / TC, cn = t % TC;
+  const int t = threadIdx.x;
   const int H = a.H;
   const int u = blockIdx.x / H, h = blockIdx.x - u * H;
   const ChunkRows cr = chunk_rows(a, u);
@@ -911,16 +909,15 @@ __global__ __launch_bounds__(kChunkThreads) void kda_bwd_chunk_kernel(BwdArgs a)
   auto ld_v = [&](int c, int d) { return (c < cr.len) ? ld1<DTQ>(a.v, in_idx(c, d)) : 0.f; };
   auto ld_b = [&](int c) { return (c < cr.len) ? ld1<DTG>(a.beta, (cr.row0 + c) * H + h) : 0.f; };
   // The gradients of q, k and G accumulate in place in dq, dk and dg (dg
-  // holds dG until the final reverse cumsum).  Phases 1-3 run on the matrix
-  // cores as bf16 hi / lo triples: wave wv
-  // owns row tile mt = wv / 2 and the NDT column tiles dt = (wv % 2) NDT + q
-  // of every [64][D] product (lane (r, gq) holds rows 16 mt + 4 gq + i,
-  // column 16 dt + r), so phase 2 adds to the dk and dG terms phase 1 left at
-  // its own positions; phase 4 (wave wv owns column tile wv, lane rows
-  // 4 gq + e of every row tile) and the outputs (thread (rm, cn) owns rows
-  // rm + 16i, columns cn + TC j) read what other threads wrote, after the
-  // workgroup barriers between the phases.  Pad rows (c >= len) are never
-  // stored (their dG is zero: every term carries a factor q_c or k_c).
+  // holds dG until phase 4 turns it into its reverse cumsum).  Phases 1-3
+  // run on the matrix cores as bf16 hi / lo triples: wave wv owns row tile
+  // mt = wv / 2 and the NDT column tiles dt = (wv % 2) NDT + q of every
+  // [64][D] product (lane (r, gq) holds rows 16 mt + 4 gq + i, column
+  // 16 dt + r), so phase 2 adds to the dk and dG terms phase 1 left at its
+  // own positions; phase 4 (wave wv owns column tile wv, lane rows 4 gq + e
+  // of every row tile) reads what other threads wrote, after the workgroup
+  // barriers between the phases.  Pad rows (c >= len) are never stored
+  // (their dG is zero: every term carries a factor q_c or k_c).
   float* const gq_ = a.dq;
   float* const gk_ = a.dk;
   float* const gG_ = a.dg;
@@ -1131,6 +1128,11 @@ __global__ __launch_bounds__(kChunkThreads) void kda_bwd_chunk_kernel(BwdArgs a)
   // contiguous); key tiles above the row tile are masked to zero and skipped.
   float* const sDL = sm;                 // phase 4's operands, written at the end of phase 3
   float* const sDA = sDL + kC * PC;
+  // past phase 4's dL, dAqk, q, k, G, beta: [16][D] dz partials, then the
+  // per-column base of dg [D]
+  float* const sRed4 = sm + 2 * kC * PC + 3 * kC * P + kC;
+  float* const sBase = sRed4 + 16 * D;
+  static_assert(2 * kC * PC + 3 * kC * P + kC + 17 * D <= SMEM_FLOATS, "phase 4 LDS");
   InTile<DTQ, D, D, NTH> tQ4, tK4;
   Tile<kC, D, NTH> tG4;
   {
@@ -1212,6 +1214,9 @@ __global__ __launch_bounds__(kChunkThreads) void kda_bwd_chunk_kernel(BwdArgs a)
         sDL[c * PC + ii] = (ii < c) ? -dLa[q][i] : 0.f;
         sDA[c * PC + ii] = (ii <= c) ? dAa[q][i] : 0.f;
       }
+    // dz column partials (slot 4 mt + gq) for the per-column base of dg
+#pragma unroll
+    for (int q = 0; q < NDT; ++q) sRed4[(4 * mt + gq) * D + 16 * (dg_ * NDT + q) + r16] = dzp[q];
     __syncthreads();
   }
 
@@ -1237,6 +1242,11 @@ __global__ __launch_bounds__(kChunkThreads) void kda_bwd_chunk_kernel(BwdArgs a)
     tK4.template put<P>(sK, 1.f);
     tG4.template put<P>(sG);
     if (t < kC) sB[t] = ld_b(t);
+    if (t < D) {   // dg[c] = base + sum_{c' >= c} dG[c']: the G_C terms and the dz terms
+      float acc = dgc * ex2(GL[(kC - 1) * D + t]);
+      for (int r = 0; r < 16; ++r) acc += sRed4[r * D + t];
+      sBase[t] = acc;
+    }
     __syncthreads();
     const bool mine = wv < NCT;
     const int d = 16 * (wv % NCT) + r16;
@@ -1252,6 +1262,7 @@ __global__ __launch_bounds__(kChunkThreads) void kda_bwd_chunk_kernel(BwdArgs a)
 #pragma unroll
       for (int e = 0; e < 4; ++e) colS[q][e] = 0.f;
     float dbq[4][4];
+    float carry = 0.f;   // sum of dG over the rows of the tiles already finished (below)
 #pragma unroll
     for (int R = 3; R >= 0; --R) {
       const int a0 = 16 * R;
@@ -1323,6 +1334,7 @@ __global__ __launch_bounds__(kChunkThreads) void kda_bwd_chunk_kernel(BwdArgs a)
             cS[e] = fmaf(sDL[(a0 + y) * PC + c], by * kr, cS[e]);
           }
         }
+        float gn[4];   // this tile's dG (zero on pad rows)
 #pragma unroll
         for (int e = 0; e < 4; ++e) {
           const int c = a0 + 4 * gq + e;
@@ -1334,13 +1346,32 @@ __global__ __launch_bounds__(kChunkThreads) void kda_bwd_chunk_kernel(BwdArgs a)
           }
           if (R < 3) cS[e] += colS[R < 3 ? R : 0][e];
           dbq[R][e] = rK[e] * kc;
+          gn[e] = (c < cr.len) ? oG[e] + rA[e] * qc + rK[e] * kc * bc - cS[e] * kc : 0.f;
           if (c < cr.len) {
             const int64_t o = in_idx(c, d);
             gq_[o] = oq[e] + rA[e] * a.scale;
-            gG_[o] = oG[e] + rA[e] * qc + rK[e] * kc * bc - cS[e] * kc;
             gk_[o] = ok[e] + rK[e] * bc + cS[e];
           }
         }
+        // reverse cumsum down the column: within the lane's four rows, then
+        // over the row groups gq' > gq of the tile (lanes 16 gq' + r16), then
+        // the tiles already finished
+        float sfx[4];
+        sfx[3] = gn[3];
+        sfx[2] = gn[2] + sfx[3];
+        sfx[1] = gn[1] + sfx[2];
+        sfx[0] = gn[0] + sfx[1];
+        const float x1 = __shfl_down(sfx[0], 16, 64), x2 = __shfl_down(sfx[0], 32, 64);
+        const float x3 = __shfl_down(sfx[0], 48, 64);
+        const float above = (gq < 3 ? x1 : 0.f) + (gq < 2 ? x2 : 0.f) + (gq < 1 ? x3 : 0.f);
+        const float tile = __shfl(sfx[0] + above, r16, 64);   // lane r16 is row group 0
+        const float base = sBase[d] + carry + above;
+#pragma unroll
+        for (int e = 0; e < 4; ++e) {
+          const int c = a0 + 4 * gq + e;
+          if (c < cr.len) gG_[in_idx(c, d)] = base + sfx[e];
+        }
+        carry += tile;
       }
       asm volatile("" ::: "memory");   // keep each row tile's loads inside its iteration
     }
@@ -1366,33 +1397,13 @@ __global__ __launch_bounds__(kChunkThreads) void kda_bwd_chunk_kernel(BwdArgs a)
     }
   }
 
-  // ---- outputs: dbeta, dg (reverse cumsum of dG plus the G_C terms)
+  // ---- outputs: dbeta (dg is final after phase 4)
   {
-    float* sDG = sm;                   // [64][P]
-    float* sRed = sDG + kC * P;        // [16][D] column partial sums of dz (slot 4 mt + gq)
-    float* sDbD = sRed + 16 * D;       // [64][32] row partial sums of dbeta (phase 2)
+    float* sDbD = sm + kC * P + 16 * D;   // [64][32] row partial sums of dbeta (phase 2)
     // sDb4 = sDbD + 64 * 32: [64][8] row partial sums of dbeta (phase 4), written above
 #pragma unroll
-    for (int i = 0; i < 4; ++i) {
-      const int c = rm + 16 * i;
-#pragma unroll
-      for (int j = 0; j < NJ; ++j) {
-        const int d = cn + TC * j;
-        sDG[c * P + d] = (c < cr.len) ? gG_[in_idx(c, d)] : 0.f;
-      }
-      sDbD[(16 * mt + 4 * gq + i) * 32 + 16 * dg_ + r16] = dbrD[i];
-    }
-#pragma unroll
-    for (int q = 0; q < NDT; ++q) sRed[(4 * mt + gq) * D + 16 * (dg_ * NDT + q) + r16] = dzp[q];
+    for (int i = 0; i < 4; ++i) sDbD[(16 * mt + 4 * gq + i) * 32 + 16 * dg_ + r16] = dbrD[i];
     __syncthreads();
-    if (t < D) {
-      float acc = dgc * ex2(GL[(kC - 1) * D + t]);
-      for (int r = 0; r < 16; ++r) acc += sRed[r * D + t];
-      for (int c = kC - 1; c >= 0; --c) {
-        acc += sDG[c * P + t];
-        if (c < cr.len) a.dg[in_idx(c, t)] = acc;
-      }
-    }
     if (t < kC && t < cr.len) {
       float acc = 0.f;
       for (int j = 0; j < NCT; ++j) acc += sDb4[t * 8 + j];
