@@ -600,8 +600,10 @@ __global__ __launch_bounds__(kScanThreads) void kda_bwd_fscan_kernel(BwdArgs a) 
   static_assert((D / 4) % KCG == 0, "lambda*k column groups");
   float4 kq[KPER][2];
   const int rp = t & 31, cg = t >> 5;
+  float pgc;   // gamma_C of the chunk, loaded with its operands (every thread; t < D stores it)
   auto fetch = [&](int n) {
     const int64_t ch = (static_cast<int64_t>(b) * a.NT + n) * H + h;
+    pgc = a.GCV[ch * D + (t & (D - 1))];
     tW.fetch(a.WM + ch * kC * D, D, 0);
     const float* KLp = a.KL + ch * kC * D;
 #pragma unroll
@@ -652,7 +654,7 @@ __global__ __launch_bounds__(kScanThreads) void kda_bwd_fscan_kernel(BwdArgs a) 
       }
     }
     tU.template put<kPB>(sU);
-    if (t < D) sGC[t] = a.GCV[ch * D + t];
+    if (t < D) sGC[t] = pgc;
     if (n + 1 < a.NT) fetch(n + 1);
     __syncthreads();
     // v~ = U - W S (two accumulation chains over the D / 32 K blocks)
