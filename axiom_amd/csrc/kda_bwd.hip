@@ -267,9 +267,14 @@ __global__ __launch_bounds__(kPrepThreads, 4) void kda_bwd_prep_kernel(BwdArgs a
   float* const sT = sQ;
 
   // k and the in-chunk inclusive cumsum of g (log2 units) of channel half c0
+  // (both tiles' loads issued before either is stored)
   auto stage_k_g = [&](int c0) {
-    lds_load_in<DTQ, D, HD, P, NTH>(sK, a.k, cr.row0, cr.len, H, h, c0, 1.f);
-    lds_load_in<DTG, D, HD, P, NTH>(sG, a.g, cr.row0, cr.len, H, h, c0, 1.f);
+    InTile<DTQ, D, HD, NTH> ik;
+    InTile<DTG, D, HD, NTH> ig;
+    ik.fetch(a.k, cr.row0, cr.len, H, h, c0);
+    ig.fetch(a.g, cr.row0, cr.len, H, h, c0);
+    ik.template put<P>(sK, 1.f);
+    ig.template put<P>(sG, 1.f);
   };
   auto cumsum_g = [&]() {            // 16 rows' loads in flight at a time
     if (t < HD) {
@@ -302,9 +307,19 @@ __global__ __launch_bounds__(kPrepThreads, 4) void kda_bwd_prep_kernel(BwdArgs a
   for (int hf = 0; hf < NHALF; ++hf) {
     const int c0 = HD * hf;
     if (hf > 0) __syncthreads();      // the previous half's reads are done
-    lds_load_in<DTQ, D, HD, P, NTH>(sQ, a.q, cr.row0, cr.len, H, h, c0, a.scale);
-    stage_k_g(c0);
-    if (hf == 0 && t < kC) sB[t] = (t < cr.len) ? ld1<DTG>(a.beta, (cr.row0 + t) * H + h) : 0.f;
+    {   // q, k, g of the half and beta: every load issued before the stores
+      InTile<DTQ, D, HD, NTH> iq, ik;
+      InTile<DTG, D, HD, NTH> ig;
+      iq.fetch(a.q, cr.row0, cr.len, H, h, c0);
+      ik.fetch(a.k, cr.row0, cr.len, H, h, c0);
+      ig.fetch(a.g, cr.row0, cr.len, H, h, c0);
+      const int tb = t & (kC - 1);
+      const float bv = ld1<DTG>(a.beta, (cr.row0 + (tb < cr.len ? tb : 0)) * H + h);
+      iq.template put<P>(sQ, a.scale);
+      ik.template put<P>(sK, 1.f);
+      ig.template put<P>(sG, 1.f);
+      if (hf == 0 && t < kC) sB[t] = (t < cr.len) ? bv : 0.f;
+    }
     __syncthreads();
     cumsum_g();
     __syncthreads();
@@ -906,10 +921,24 @@ __global__ __launch_bounds__(kChunkThreads) void kda_bwd_chunk_kernel(BwdArgs a)
   const int64_t ch = static_cast<int64_t>(u) * H + h;
   const float* GL = a.GL + ch * kC * D;
   auto in_idx = [&](int c, int d) { return ((cr.row0 + c) * H + h) * D + d; };
-  auto ld_q = [&](int c, int d) { return (c < cr.len) ? ld1<DTQ>(a.q, in_idx(c, d)) * a.scale : 0.f; };
-  auto ld_k = [&](int c, int d) { return (c < cr.len) ? ld1<DTQ>(a.k, in_idx(c, d)) : 0.f; };
-  auto ld_v = [&](int c, int d) { return (c < cr.len) ? ld1<DTQ>(a.v, in_idx(c, d)) : 0.f; };
-  auto ld_b = [&](int c) { return (c < cr.len) ? ld1<DTG>(a.beta, (cr.row0 + c) * H + h) : 0.f; };
+  // loads from pad rows (c >= len) read row 0 and are zeroed where used, so
+  // no load sits inside a branch (whose end would wait for it)
+  auto ld_q = [&](int c, int d) {
+    const float x = ld1<DTQ>(a.q, in_idx(c < cr.len ? c : 0, d));
+    return (c < cr.len) ? x * a.scale : 0.f;
+  };
+  auto ld_k = [&](int c, int d) {
+    const float x = ld1<DTQ>(a.k, in_idx(c < cr.len ? c : 0, d));
+    return (c < cr.len) ? x : 0.f;
+  };
+  auto ld_v = [&](int c, int d) {
+    const float x = ld1<DTQ>(a.v, in_idx(c < cr.len ? c : 0, d));
+    return (c < cr.len) ? x : 0.f;
+  };
+  auto ld_b = [&](int c) {
+    const float x = ld1<DTG>(a.beta, (cr.row0 + (c < cr.len ? c : 0)) * H + h);
+    return (c < cr.len) ? x : 0.f;
+  };
   // The gradients of q, k and G accumulate in place in dq, dk and dg (dg
   // holds dG until phase 4 turns it into its reverse cumsum).  Phases 1-3
   // run on the matrix cores as bf16 hi / lo triples: wave wv owns row tile
