@@ -161,22 +161,24 @@ __device__ __forceinline__ void lds_load_in(float* dst, const void* src, int64_t
   constexpr int N = kC * V;
   constexpr int PER = (N + NTH - 1) / NTH;
   static_assert(COLS % 8 == 0, "8-element loads");
+  // every thread loads (masked ones from row 0 of the chunk) and zeroes
+  // where it stores, so no load sits inside a branch
   float tmp[PER][8];
 #pragma unroll
   for (int p = 0; p < PER; ++p) {
     const int e = threadIdx.x + p * NTH;
     const int r = e / V, c8 = e - r * V;
-#pragma unroll
-    for (int x = 0; x < 8; ++x) tmp[p][x] = 0.f;
-    if ((N % NTH == 0 || e < N) && r < len) ld8<DT>(src, ((row0 + r) * H + h) * D + col0 + 8 * c8, tmp[p]);
+    const bool ok = (N % NTH == 0 || e < N) && r < len;
+    ld8<DT>(src, ((row0 + (ok ? r : 0)) * H + h) * D + col0 + 8 * (ok ? c8 : 0), tmp[p]);
   }
 #pragma unroll
   for (int p = 0; p < PER; ++p) {
     const int e = threadIdx.x + p * NTH;
     if (N % NTH == 0 || e < N) {
       const int r = e / V, c8 = e - r * V;
+      const bool ok = r < len;
 #pragma unroll
-      for (int x = 0; x < 8; ++x) dst[r * PITCH + 8 * c8 + x] = tmp[p][x] * mul;
+      for (int x = 0; x < 8; ++x) dst[r * PITCH + 8 * c8 + x] = ok ? tmp[p][x] * mul : 0.f;
     }
   }
 }
@@ -769,10 +771,12 @@ __global__ __launch_bounds__(kScanThreads) void kda_bwd_rscan_kernel(BwdArgs a) 
   Tile<kC, D, NTH> tL;
   TTile<kC, NTH> tA;
   TTile<D, NTH> tQ, tW;
+  float pgc;   // gamma_C of the chunk, loaded with lambda*k and Aqk (every thread; t < D stores it)
   auto fetch_a = [&](int n) {
     const int64_t ch = (static_cast<int64_t>(b) * a.NT + n) * H + h;
     tL.fetch(a.KL + ch * kC * D, D, 0);
     tA.fetch(a.AQ + ch * kC * kC, kC, 0);
+    pgc = a.GCV[ch * D + (t & (D - 1))];
   };
   if (a.NT > 0) fetch_a(a.NT - 1);
   for (int n = a.NT - 1; n >= 0; --n) {
@@ -814,7 +818,7 @@ __global__ __launch_bounds__(kScanThreads) void kda_bwd_rscan_kernel(BwdArgs a) 
         *reinterpret_cast<unsigned*>(&sOl[(4 * cg + e) * PK + 2 * rp]) = ll;
       }
     }
-    if (t < D) sGC[t] = a.GCV[ch * D + t];
+    if (t < D) sGC[t] = pgc;
     tQ.fetch(a.QG + ch * kC * D, D, 0);
     tW.fetch(a.WM + ch * kC * D, D, 0);
     __syncthreads();
