@@ -395,7 +395,10 @@ __global__ __launch_bounds__(kPrepThreads, 4) void kda_bwd_prep_kernel(BwdArgs a
   }
   __syncthreads();
 
-  // T = (I + L)^-1 (into sQ's buffer: q is no longer read)
+  // T = (I + L)^-1 (into sQ's buffer: q is no longer read); the first W/U
+  // pass's v half is loaded during the inversion
+  InTile<DTQ, D, HD, NTH> iv;
+  iv.fetch(a.v, cr.row0, cr.len, H, h, HD * (NHALF - 1));
   invert_unit_lower64<PC, NTH>(sL, sT, sTmp);
   {
     float* TM = a.TM + ch * kC * kC;
@@ -412,11 +415,12 @@ __global__ __launch_bounds__(kPrepThreads, 4) void kda_bwd_prep_kernel(BwdArgs a
     const int c0 = HD * (NHALF - 1 - pass);
     if (pass > 0) {
       __syncthreads();                // the previous pass's products are done
+      iv.fetch(a.v, cr.row0, cr.len, H, h, c0);   // in flight during the k, g staging
       stage_k_g(c0);
       __syncthreads();
       cumsum_g();
     }
-    lds_load_in<DTQ, D, HD, PC, NTH>(sV, a.v, cr.row0, cr.len, H, h, c0, 1.f);
+    iv.template put<PC>(sV, 1.f);
     __syncthreads();
     for (int e = t; e < kC * HD; e += NTH) {
       const int c = e / HD, d = e - c * HD;
