@@ -252,10 +252,12 @@ template <int D, int DTQ, int DTG>
 __global__ __launch_bounds__(kPrepThreads, 4) void kda_bwd_prep_kernel(BwdArgs a) {
   constexpr int HD = 64;              // channels per half
   constexpr int NHALF = D / HD;
-  constexpr int P = HD + 2;           // [64][HD] pitch: row fragments conflict-free
+  // [64][HD] pitch: row fragments conflict-free (rows 4 banks apart), rows
+  // 16-byte aligned for the diagonal tiles' vector reads
+  constexpr int P = HD + 4;
   constexpr int PC = kC + 1;
   static_assert(kC * PC <= kC * P, "T shares sQ's buffer");
-  __shared__ float sQ[kC * P], sK[kC * P], sG[kC * P];   // one channel half; sQ then holds T
+  __shared__ __attribute__((aligned(16))) float sQ[kC * P], sK[kC * P], sG[kC * P];   // one channel half; sQ then holds T
   __shared__ float sL[kC * PC];       // L, then one half of beta*v
   __shared__ float sTmp[768];         // the triangular inversion's scratch
   __shared__ float sB[kC];
@@ -357,11 +359,21 @@ __global__ __launch_bounds__(kPrepThreads, 4) void kda_bwd_prep_kernel(BwdArgs a
       const int R = p >> 8, rc = (p >> 4) & 15, ri = p & 15;
       const int c = 16 * R + rc, i = 16 * R + ri;
       if (ri <= rc) {
-#pragma unroll 4
-        for (int d = 0; d < HD; ++d) {
-          const float ki = sK[i * P + d] * ex2(sG[c * P + d] - sG[i * P + d]);
-          dA[j] = fmaf(sQ[c * P + d], ki, dA[j]);
-          dL[j] = fmaf(sK[c * P + d], ki, dL[j]);
+#pragma unroll 2
+        for (int d4 = 0; d4 < HD; d4 += 4) {
+          const float4 kI = *reinterpret_cast<const float4*>(&sK[i * P + d4]);
+          const float4 gI = *reinterpret_cast<const float4*>(&sG[i * P + d4]);
+          const float4 gC = *reinterpret_cast<const float4*>(&sG[c * P + d4]);
+          const float4 qC = *reinterpret_cast<const float4*>(&sQ[c * P + d4]);
+          const float4 kC4 = *reinterpret_cast<const float4*>(&sK[c * P + d4]);
+          const float ki[4] = {kI.x * ex2(gC.x - gI.x), kI.y * ex2(gC.y - gI.y), kI.z * ex2(gC.z - gI.z),
+                               kI.w * ex2(gC.w - gI.w)};
+          const float qc[4] = {qC.x, qC.y, qC.z, qC.w}, kc[4] = {kC4.x, kC4.y, kC4.z, kC4.w};
+#pragma unroll
+          for (int e = 0; e < 4; ++e) {
+            dA[j] = fmaf(qc[e], ki[e], dA[j]);
+            dL[j] = fmaf(kc[e], ki[e], dL[j]);
+          }
         }
       }
     }
