@@ -923,7 +923,8 @@ __device__ __forceinline__ void acc_put_hl(const f4& v, int row0, int col0, __bf
 template <int D, int DTQ, int DTG, int DO>
 __global__ __launch_bounds__(kChunkThreads) void kda_bwd_chunk_kernel(BwdArgs a) {
   typedef BwdDims<D> BD;
-  constexpr int P = BD::P, PC = BD::PC;
+  constexpr int P = BD::P;
+  constexpr int PC = kC + 4;          // [64][64] pitch: 16-byte aligned rows, row fragments conflict-free
   constexpr int NTH = kChunkThreads;
   constexpr int HW = 64;             // value columns per pass of phase 1
   constexpr int NH = D / HW;
@@ -1370,19 +1371,30 @@ __global__ __launch_bounds__(kChunkThreads) void kda_bwd_chunk_kernel(BwdArgs a)
           gc[e] = sG[(a0 + 4 * gq + e) * P + d];
           rA[e] = rK[e] = cS[e] = 0.f;
         }
-#pragma unroll 4
-        for (int y = 0; y < 16; ++y) {
-          const float gy = sG[(a0 + y) * P + d], ky = sK[(a0 + y) * P + d];
-          const float qy = sQ[(a0 + y) * P + d], by = sB[a0 + y];
+#pragma unroll 1
+        for (int y4 = 0; y4 < 16; y4 += 4) {
+          f4 rowA[4], rowL[4];   // dA[c][a0 + y4 .. + 3], dL likewise, for the lane's rows c
 #pragma unroll
           for (int e = 0; e < 4; ++e) {
             const int c = a0 + 4 * gq + e;
-            const float ev = ex2(-fabsf(gc[e] - gy));
-            const float kr = ky * ev;
-            rA[e] = fmaf(sDA[c * PC + a0 + y], kr, rA[e]);
-            rK[e] = fmaf(sDL[c * PC + a0 + y], kr, rK[e]);
-            cS[e] = fmaf(sDA[(a0 + y) * PC + c], qy * ev, cS[e]);
-            cS[e] = fmaf(sDL[(a0 + y) * PC + c], by * kr, cS[e]);
+            rowA[e] = *reinterpret_cast<const f4*>(&sDA[c * PC + a0 + y4]);
+            rowL[e] = *reinterpret_cast<const f4*>(&sDL[c * PC + a0 + y4]);
+          }
+#pragma unroll
+          for (int yy = 0; yy < 4; ++yy) {
+            const int y = y4 + yy;
+            const float gy = sG[(a0 + y) * P + d], ky = sK[(a0 + y) * P + d];
+            const float qy = sQ[(a0 + y) * P + d], by = sB[a0 + y];
+#pragma unroll
+            for (int e = 0; e < 4; ++e) {
+              const int c = a0 + 4 * gq + e;
+              const float ev = ex2(-fabsf(gc[e] - gy));
+              const float kr = ky * ev;
+              rA[e] = fmaf(rowA[e][yy], kr, rA[e]);
+              rK[e] = fmaf(rowL[e][yy], kr, rK[e]);
+              cS[e] = fmaf(sDA[(a0 + y) * PC + c], qy * ev, cS[e]);
+              cS[e] = fmaf(sDL[(a0 + y) * PC + c], by * kr, cS[e]);
+            }
           }
         }
         float gn[4];   // this tile's dG (zero on pad rows)
