@@ -331,13 +331,19 @@ __global__ __launch_bounds__(kPrepThreads, 4) void kda_bwd_prep_kernel(BwdArgs a
       float* GL = a.GL + ch * kC * D + c0;
       float* QG = a.QG + ch * kC * D + c0;
       float* KL = a.KL + ch * kC * D + c0;
-      for (int e = t; e < kC * HD; e += NTH) {
-        const int c = e / HD, d = e - c * HD;
-        const float gl = sG[c * P + d];
-        const float glast = sG[(kC - 1) * P + d];
-        GL[c * D + d] = gl;
-        QG[c * D + d] = ex2(gl) * sQ[c * P + d];
-        KL[c * D + d] = ex2(glast - gl) * sK[c * P + d];
+      constexpr int V4 = HD / 4;      // float4 groups per row
+      for (int e = t; e < kC * V4; e += NTH) {
+        const int c = e / V4, d = 4 * (e - c * V4);
+        const float4 gl = *reinterpret_cast<const float4*>(&sG[c * P + d]);
+        const float4 gz = *reinterpret_cast<const float4*>(&sG[(kC - 1) * P + d]);
+        const float4 qv = *reinterpret_cast<const float4*>(&sQ[c * P + d]);
+        const float4 kv = *reinterpret_cast<const float4*>(&sK[c * P + d]);
+        const float4 qg = make_float4(ex2(gl.x) * qv.x, ex2(gl.y) * qv.y, ex2(gl.z) * qv.z, ex2(gl.w) * qv.w);
+        const float4 kl = make_float4(ex2(gz.x - gl.x) * kv.x, ex2(gz.y - gl.y) * kv.y, ex2(gz.z - gl.z) * kv.z,
+                                      ex2(gz.w - gl.w) * kv.w);
+        *reinterpret_cast<float4*>(&GL[c * D + d]) = gl;
+        *reinterpret_cast<float4*>(&QG[c * D + d]) = qg;
+        *reinterpret_cast<float4*>(&KL[c * D + d]) = kl;
       }
       if (t < HD) a.GCV[ch * D + c0 + t] = ex2(sG[(kC - 1) * P + t]);
     }
