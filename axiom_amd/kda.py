@@ -77,14 +77,15 @@ def chunk_fwd_workspace_bytes(B, T, H, dk, dv, n_seqs=0, in_code=_lib.KDA_DTYPE_
 
 def kda_chunk_fwd(q, k, v, g, beta, initial_state=None, cu_seqlens=None, chunk_size: int = 64,
                   scale: float = 1.0, output_final_state: bool = True,
-                  out_dtype=torch.float32, workspace=None):
+                  out_dtype=torch.float32, workspace=None, out=None, final_state=None):
     """Chunked KDA forward; returns ``(o, final_state)`` (``final_state`` None if not requested).
 
     ``q, k, g [B,T,H,dk]``, ``v [B,T,H,dv]``, ``beta [B,T,H]``; q/k/v share one
     dtype (bf16, fp16 or fp32).  g and beta have the same dtype as q, or fp32
     with bf16 q/k/v.  ``initial_state [N,H,dk,dv]`` fp32 or None (zeros);
     ``cu_seqlens`` int32 ``[N+1]`` on the device (requires B == 1).  fp32
-    inputs select the exact (fp32 MFMA) kernels.
+    inputs select the exact (fp32 MFMA) kernels.  ``out`` / ``final_state``:
+    optional preallocated outputs (contiguous, the shapes and dtypes returned).
     """
     what = "kda_chunk_fwd"
     if q.dim() != 4 or k.shape != q.shape or g.shape != q.shape:
@@ -131,8 +132,23 @@ def kda_chunk_fwd(q, k, v, g, beta, initial_state=None, cu_seqlens=None, chunk_s
         raise ValueError(f"{what}: unsupported configuration")
     if workspace is None or workspace.numel() * workspace.element_size() < ws_bytes:
         workspace = torch.empty(ws_bytes, dtype=torch.uint8, device=dev)
-    o = torch.empty((B, T, H, dv), dtype=out_dtype, device=dev)
-    ht = torch.empty((N, H, dk, dv), dtype=torch.float32, device=dev) if output_final_state else None
+    if out is not None:
+        if tuple(out.shape) != (B, T, H, dv) or out.dtype != out_dtype or out.device != dev:
+            raise ValueError(f"{what}: out must be {out_dtype} [{B},{T},{H},{dv}] on {dev}")
+        _contig("out", out)
+        o = out
+    else:
+        o = torch.empty((B, T, H, dv), dtype=out_dtype, device=dev)
+    if not output_final_state:
+        ht = None
+    elif final_state is not None:
+        if tuple(final_state.shape) != (N, H, dk, dv) or final_state.dtype != torch.float32 \
+                or final_state.device != dev:
+            raise ValueError(f"{what}: final_state must be fp32 [{N},{H},{dk},{dv}] on {dev}")
+        _contig("final_state", final_state)
+        ht = final_state
+    else:
+        ht = torch.empty((N, H, dk, dv), dtype=torch.float32, device=dev)
     rc = L.kda_chunk_fwd(_stream(dev), _ptr(q), _ptr(k), _ptr(v), _ptr(g), _ptr(beta),
                          _ptr(initial_state), _ptr(cu_seqlens), n_seqs, _ptr(o), _ptr(ht),
                          B, T, H, dk, dv, CHUNK, float(scale), in_code, _OUT_CODES[out_dtype],

@@ -4,10 +4,12 @@
 Headline (the ``value``): chunked KDA forward throughput in tokens/s at
 B=4, T=4096, H=16, dk=dv=128, C=64, bf16 inputs, fp32 o and fp32 final state
 (``configs[1]`` of the benchmark definition), inputs resident in HBM.  One
-"step" = one ``kda_chunk_fwd`` over the whole batch.  The default warm-up is
-100 untimed steps (~25 ms): after idle the GPU's clocks ramp up over the first
-~80 calls (336 us per call for the first 20, 244 us from the 80th on), and the
-timed steps are meant to see the steady state.
+"step" = one ``kda_chunk_fwd`` over the whole batch into preallocated o and
+final-state buffers.  Before the ``--warmup`` steps, a fixed clock ramp of
+``CLOCK_RAMP_CALLS`` untimed calls runs whatever ``--warmup`` is: after idle
+the GPU's clocks ramp up over the first ~80 calls (336 us per call for the
+first 20, 244 us from the 80th on), and the timed steps are meant to see the
+steady state.  The JSON line reports the ramp as ``clock_ramp_calls``.
 
 Also reported on the same JSON line:
 * TFLOP/s and % of bf16 dense MFMA peak with the algorithmic count
@@ -66,6 +68,8 @@ TRAFFIC_PROFILE = os.path.join(os.path.dirname(os.path.abspath(__file__)), "prof
 MFMA_BF16_PEAK_TFLOPS = 2516.6
 
 CFG = dict(B=4, T=4096, H=16, dk=128, dv=128, C=64)
+# untimed forward calls before the warm-up proper (clock ramp after idle)
+CLOCK_RAMP_CALLS = 150
 
 
 def flops_per_token_head(C, d):
@@ -135,8 +139,18 @@ def bench_forward(args, device):
     B, T, H, dk, dv, C = (CFG[k] for k in ("B", "T", "H", "dk", "dv", "C"))
     q, k, v, g, beta = make_inputs_gpu(B, T, H, dk, dv, args.seed, device)
     ws = torch.empty(kmod.chunk_fwd_workspace_bytes(B, T, H, dk, dv), dtype=torch.uint8, device=device)
+    o = torch.empty(B, T, H, dv, dtype=torch.float32, device=device)
+    ht = torch.empty(B, H, dk, dv, dtype=torch.float32, device=device)
+
+    def call():
+        return axiom_amd.kda_chunk_fwd(q, k, v, g, beta, workspace=ws, out=o, final_state=ht)
+
+    # clock ramp: after idle the GPU's clocks take ~80 calls to reach steady
+    # state; these calls are untimed and independent of --warmup
+    for _ in range(CLOCK_RAMP_CALLS):
+        call()
     for _ in range(args.warmup):
-        axiom_amd.kda_chunk_fwd(q, k, v, g, beta, workspace=ws)
+        call()
     torch.cuda.synchronize()
     stream = torch.cuda.current_stream(device)
     ev = [(torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True))
@@ -144,7 +158,7 @@ def bench_forward(args, device):
     t0 = time.perf_counter()
     for i in range(args.steps):
         ev[i][0].record(stream)
-        o, ht = axiom_amd.kda_chunk_fwd(q, k, v, g, beta, workspace=ws)
+        call()
         ev[i][1].record(stream)
     torch.cuda.synchronize()
     wall = time.perf_counter() - t0
@@ -525,7 +539,7 @@ def main():
     ap = argparse.ArgumentParser(description=__doc__.split("\n")[0])
     ap.add_argument("--gpus", type=int, default=1)
     ap.add_argument("--steps", type=int, default=20)
-    ap.add_argument("--warmup", type=int, default=100)
+    ap.add_argument("--warmup", type=int, default=10)
     ap.add_argument("--decode-steps", type=int, default=128)
     ap.add_argument("--seed", type=int, default=0)
     ap.add_argument("--cpu-seconds", type=float, default=10.0)
@@ -563,6 +577,7 @@ def main():
         "n_gpus": 1,
         "steps": steps,
         "warmup": args.warmup,
+        "clock_ramp_calls": CLOCK_RAMP_CALLS,
         "ms_per_step": ms_per_step,
         "higher_is_better": True,
         "scaling": "weak",

@@ -44,6 +44,15 @@ How each is pinned (tests/test_oracle.py)
 * UT solve: ``scipy.linalg.solve_triangular(unit_diagonal=True)`` and the
   Neumann product identity (``net/kernels/kda_ut_solve.py:20-27``);
 * varlen: packed == per-sequence; decode: T decode steps == chunked forward.
+* ``chunk_intermediates``: the per-chunk W, U, Aqk, gamma*q, lambda*k and
+  gamma_C alone rebuild o and the final state of the token recurrence (fp64,
+  1e-10, ragged tail and h0 included), ``T (I + L) = I`` with ``L`` built by
+  brute force from its definition, and planted slips (lambda*k transposed,
+  an exclusive gamma, a strict Aqk, W without beta, gamma_C of one row, U of
+  the wrong chunk) each fail the rebuild.
+* ``cc_tile``: the values of ``net/kda.py:577-585`` (16 at ``g_min = -5``,
+  8 at -10, 16 at 0, ...) and the rule they follow (the widest tile <= 16
+  with ``tile * |g_min| <= 80``).
 * ``cc_scan`` / ``cc_scan_bwd`` (the seam's operands: alpha, beta32 as a
   32-column mean): the backward against central finite differences of the
   forward in every input, with unequal beta32 columns (tests/test_oracle_bwd.py).

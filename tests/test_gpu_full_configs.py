@@ -48,14 +48,20 @@ def test_config1_full(cuda):
         o_ref, ht_ref = K.chunk_fwd(hc["q"], hc["k"], hc["v"], hc["g"], hc["beta"], chunk=64)
         assert_close(f"o[b={b}]", o[b:b + 1][:, :, heads], o_ref, TOL["bf16"])
         assert_close(f"ht[b={b}]", ht[b:b + 1][:, heads], ht_ref, TOL["bf16"])
-    # The whole call runs in 3 segments of 22 chunks (its intra-chunk results
-    # exceed the per-segment budget); four calls of 16 chunks each run whole
-    # and carry the state between them: same result bit for bit.
+    # The whole call runs in segments of chunks (its intra-chunk results
+    # exceed the per-segment budget); four calls of 16 chunks each carry the
+    # state between them: same result bit for bit.
     h, outs = None, []
     for t0 in range(0, T, 1024):
         oi, h = _fwd(_slice(d, t0, t0 + 1024), h0=h)
         outs.append(oi)
     assert torch.equal(torch.cat(outs, dim=1), o) and torch.equal(h, ht)
+    # Without a final-state output the segments carry the state through the
+    # workspace instead of ht: o is the same bit for bit.
+    import axiom_amd
+    o_nf, ht_nf = axiom_amd.kda_chunk_fwd(d["q"], d["k"], d["v"], d["g"], d["beta"], output_final_state=False)
+    torch.cuda.synchronize()
+    assert ht_nf is None and torch.equal(o_nf, o)
 
 
 def test_config2_full(cuda):

@@ -3,6 +3,7 @@
 from __future__ import annotations
 
 import numpy as np
+import pytest
 
 from oracle import layer as Lr
 
@@ -119,3 +120,121 @@ def test_l2_norm_gradient_at_a_zero_row_is_zero():
     u = np.random.default_rng(13).standard_normal((2, 4))
     fd = (np.sum(Lr.l2_norm(x[[0, 2]] + 1e-6 * u)) - np.sum(Lr.l2_norm(x[[0, 2]] - 1e-6 * u))) / 2e-6
     np.testing.assert_allclose(np.sum(g[[0, 2]] * u), fd, rtol=1e-6)
+
+
+# ---------------------------------------------------------------------------
+# composition order of the prologue and epilogue (net/kda.py:194-214)
+# ---------------------------------------------------------------------------
+
+
+def _indep_swish_conv(x, w):
+    """swish(causal depthwise conv) of one sequence (T, D) by numpy.convolve and
+    scipy's logistic function, independent of the oracle's own routines."""
+    from scipy.special import expit
+    T, D = x.shape
+    a = np.stack([np.convolve(x[:, c], w[:, c])[:T] for c in range(D)], axis=1)
+    return a * expit(a)
+
+
+def test_prologue_order_conv_swish_then_l2_on_q_k_only():
+    """q and k are swish(conv(x)) / (||.|| + 1e-12) per head row; v is swish(conv(x))
+    with no norm.  Catches: L2 before swish (rows not unit norm), v normalised,
+    the norm taken over H*d instead of per head."""
+    rng = np.random.default_rng(7)
+    B, T, H, d, K = 1, 9, 3, 8, 4
+    xs = [rng.standard_normal((B, T, H * d)) * (1.0 + 2.0 * n) for n in range(3)]
+    ws = [rng.standard_normal((K, H * d)) for _ in range(3)]
+    q, k, v, _ = Lr.prologue(*xs, *ws, H)
+    for n, got in enumerate((q, k, v)):
+        s = _indep_swish_conv(xs[n][0], ws[n]).reshape(T, H, d)
+        if n < 2:
+            nrm = np.linalg.norm(s, axis=-1, keepdims=True)
+            np.testing.assert_allclose(got[0], s / (nrm + 1e-12), rtol=1e-12, atol=1e-14)
+            np.testing.assert_allclose(np.linalg.norm(got[0], axis=-1), 1.0, rtol=1e-10)
+        else:
+            np.testing.assert_allclose(got[0], s, rtol=1e-12, atol=1e-14)
+            assert np.max(np.abs(np.linalg.norm(got[0], axis=-1) - 1.0)) > 0.1
+
+
+def test_l2_eps_is_added_to_the_norm_not_under_the_root():
+    """x / (||x|| + 1e-12) (net/norm.py:53-66): a row of norm 1e-12 comes out
+    with norm 1/2; x / sqrt(||x||^2 + 1e-12) would give ~1e-6."""
+    x = np.zeros((2, 16))
+    x[0, 3] = 1e-12
+    x[1, :4] = 0.5e-12
+    np.testing.assert_allclose(np.linalg.norm(Lr.l2_norm(x), axis=-1), 0.5, rtol=1e-12)
+
+
+def test_epilogue_rms_eps_sigmoid_gate_and_per_head_norm():
+    """y = sigmoid(z) * o / sqrt(mean_head(o^2) + 1e-6) (net/kda.py:205-214,
+    net/norm.py:69-73): per-head RMS of y equals sigmoid(z) for o >> eps; a
+    head with mean(o^2) = 1e-6 is divided by sqrt(2e-6) (eps under the root,
+    added to the mean, not to the sum); the gate multiplies after the norm."""
+    rng = np.random.default_rng(8)
+    B, T, H, dv = 1, 3, 2, 16
+    o = rng.standard_normal((B, T, H, dv))
+    o[:, :, 1] *= 100.0                                  # heads on different scales
+    z = np.zeros((B, T, H * dv))
+    y = Lr.epilogue(o, z).reshape(B, T, H, dv)
+    rms = np.sqrt(np.mean(y * y, axis=-1))
+    np.testing.assert_allclose(rms, 0.5, rtol=1e-5)      # sigmoid(0) = 1/2
+    tiny = np.full((1, 1, 1, dv), 1e-3)                  # mean(o^2) = 1e-6
+    yt = Lr.epilogue(tiny, np.full((1, 1, dv), 50.0))    # sigmoid(50) = 1 in fp64 to 2e-22
+    np.testing.assert_allclose(yt, 1e-3 / np.sqrt(2e-6), rtol=1e-12)
+    zz = rng.standard_normal((B, T, H * dv))
+    from scipy.special import expit
+    np.testing.assert_allclose(Lr.epilogue(o, zz), expit(zz) * Lr.epilogue(o, np.full_like(zz, 50.0)),
+                               rtol=1e-12)
+
+
+def _prologue_variant(variant):
+    def prologue(qp, kp, vp, wq, wk, wv, H, bufs=None):
+        outs = []
+        for n, (x, w) in enumerate(((qp, wq), (kp, wk), (vp, wv))):
+            x = np.asarray(x, np.float64)
+            B, T, HD = x.shape
+            y = np.stack([Lr.short_conv(x[b], w)[0] for b in range(B)])
+            if variant == "l2_before_swish" and n < 2:
+                y = Lr.swish(Lr.l2_norm(y.reshape(B, T, H, HD // H)))
+            else:
+                y = Lr.swish(y).reshape(B, T, H, HD // H)
+                if n < 2 or variant == "v_normalised":
+                    y = Lr.l2_norm(y)
+                if variant == "norm_over_all_heads" and n < 2:
+                    s = Lr.swish(np.stack([Lr.short_conv(x[b], w)[0] for b in range(B)]))
+                    y = (s / (np.linalg.norm(s, axis=-1, keepdims=True) + 1e-12)).reshape(B, T, H, HD // H)
+            outs.append(y)
+        return outs[0], outs[1], outs[2], None
+    return prologue
+
+
+@pytest.mark.parametrize("variant", ["l2_before_swish", "v_normalised", "norm_over_all_heads"])
+def test_mutated_prologue_is_caught(monkeypatch, variant):
+    monkeypatch.setattr(Lr, "prologue", _prologue_variant(variant))
+    with pytest.raises(AssertionError):
+        test_prologue_order_conv_swish_then_l2_on_q_k_only()
+
+
+def test_mutated_l2_eps_is_caught(monkeypatch):
+    monkeypatch.setattr(Lr, "l2_norm", lambda x, eps=1e-12: x / np.sqrt(np.sum(x * x, -1, keepdims=True) + eps))
+    with pytest.raises(AssertionError):
+        test_l2_eps_is_added_to_the_norm_not_under_the_root()
+
+
+@pytest.mark.parametrize("variant", ["eps_outside_root", "eps_on_sum", "gate_before_norm"])
+def test_mutated_epilogue_is_caught(monkeypatch, variant):
+    def epilogue(o, gate_logits, eps=1e-6):
+        o = np.asarray(o, np.float64)
+        B, T, H, dv = o.shape
+        g = 1.0 / (1.0 + np.exp(-np.asarray(gate_logits, np.float64))).reshape(B, T, H, dv)
+        if variant == "eps_outside_root":
+            y = o / (np.sqrt(np.mean(o * o, -1, keepdims=True)) + eps)
+        elif variant == "eps_on_sum":
+            y = o * np.sqrt(dv) / np.sqrt(np.sum(o * o, -1, keepdims=True) + eps)
+        else:
+            go = g * o
+            return Lr.headwise_rms_norm(go, eps).reshape(B, T, H * dv)
+        return (g * y).reshape(B, T, H * dv)
+    monkeypatch.setattr(Lr, "epilogue", epilogue)
+    with pytest.raises(AssertionError):
+        test_epilogue_rms_eps_sigmoid_gate_and_per_head_norm()

@@ -289,3 +289,121 @@ def test_mutated_decode_is_caught(monkeypatch):
     monkeypatch.setattr(K, "decode_step", bad)
     with pytest.raises(AssertionError):
         test_decode_step_equals_literal_eq1()
+
+
+# ---------------------------------------------------------------------------
+# per-chunk intermediates (the GPU workspace is checked against these)
+# ---------------------------------------------------------------------------
+
+
+def _rebuild_from_intermediates(it, h0):
+    """o and the final state from the per-chunk W, U, Aqk, gamma*q, lambda*k,
+    gamma_C alone: v~ = U - W S, o = (gamma q) S + Aqk v~,
+    S' = gamma_C S + (lambda k)^T v~ (the state recurrence of net/kda.py:689-702)."""
+    B, H, n, C, dv = it["U"].shape
+    S = np.array(h0, np.float64)
+    o = np.zeros((B, H, n, C, dv))
+    for i in range(n):
+        vt = it["U"][:, :, i] - it["W"][:, :, i] @ S
+        o[:, :, i] = it["GQ"][:, :, i] @ S + it["Aqk"][:, :, i] @ vt
+        S = it["GC"][:, :, i][..., None] * S + np.swapaxes(it["LK"][:, :, i], -1, -2) @ vt
+    return o, S
+
+
+def _intermediates_case(T=150, C=32, dk=16, dv=12, seed=4):
+    d = _small(T=T, dk=dk, dv=dv, seed=seed)
+    it = K.chunk_intermediates(d["q"], d["k"], d["v"], d["g"], d["beta"], chunk=C)
+    o_r, s_r = K.recurrent_fwd(d["q"], d["k"], d["v"], d["g"], d["beta"], h0=d["h0"])
+    return d, it, o_r, s_r
+
+
+def _rebuild_error(d, it, o_r, s_r):
+    o, S = _rebuild_from_intermediates(it, d["h0"])
+    B, H, n, C, dv = o.shape
+    T = o_r.shape[1]
+    o = np.transpose(o.reshape(B, H, n * C, dv), (0, 2, 1, 3))[:, :T]
+    return max(K.max_abs(o, o_r), K.max_abs(S, s_r))
+
+
+@pytest.mark.parametrize("C", [16, 32, 64])
+def test_chunk_intermediates_rebuild_the_recurrence(C):
+    """The per-chunk intermediates alone reproduce the token recurrence (fp64),
+    ragged tail included (T = 150 is not a multiple of C)."""
+    d, it, o_r, s_r = _intermediates_case(C=C)
+    assert _rebuild_error(d, it, o_r, s_r) <= 1e-10
+
+
+def test_chunk_intermediates_T_inverts_I_plus_L():
+    """T (I + L) = I with L built by brute force from its definition
+    L[c,i] = beta_c sum_d k_c k_i exp(G_c - G_i), c > i (net/kda.py:678-681)."""
+    d = _small(T=64, dk=16, dv=12, seed=5)
+    it = K.chunk_intermediates(d["q"], d["k"], d["v"], d["g"], d["beta"], chunk=32)
+    B, T, H, dk = d["k"].shape
+    for b in range(B):
+        for h in range(H):
+            for n in range(2):
+                sl = slice(32 * n, 32 * n + 32)
+                k = d["k"][b, sl, h].astype(np.float64)
+                G = np.cumsum(d["g"][b, sl, h].astype(np.float64), axis=0)
+                beta = d["beta"][b, sl, h].astype(np.float64)
+                L = np.zeros((32, 32))
+                for c in range(32):
+                    for i in range(c):
+                        L[c, i] = beta[c] * np.sum(k[c] * k[i] * np.exp(G[c] - G[i]))
+                Tm = it["T"][b, h, n]
+                np.testing.assert_allclose(Tm @ (np.eye(32) + L), np.eye(32), rtol=0, atol=1e-12)
+
+
+@pytest.mark.parametrize("mistake", ["lk_transposed", "gq_exclusive", "aqk_strict", "w_without_beta",
+                                     "gc_first_row", "u_shifted_chunk"])
+def test_mutated_intermediates_are_caught(mistake):
+    """A plausible slip in chunk_intermediates fails the rebuild pin.  The
+    transposed lambda*k needs a square [C, dk] block, so that case runs at
+    C = dk = 16."""
+    C = 16 if mistake == "lk_transposed" else 32
+    d, it, o_r, s_r = _intermediates_case(C=C)
+    assert _rebuild_error(d, it, o_r, s_r) <= 1e-10
+    it = {n: v.copy() for n, v in it.items()}
+    if mistake == "lk_transposed":
+        it["LK"] = np.swapaxes(it["LK"], -1, -2).copy()
+    elif mistake == "gq_exclusive":
+        # gamma of the previous row (exclusive cumsum) instead of the row's own
+        g = np.transpose(np.asarray(d["g"], np.float64), (0, 2, 1, 3))
+        B, H, n, Cc, dk = it["GQ"].shape
+        gp = np.zeros((B, H, n * Cc, dk))
+        gp[:, :, :g.shape[2]] = g
+        it["GQ"] = it["GQ"] * np.exp(-gp.reshape(B, H, n, Cc, dk))
+    elif mistake == "aqk_strict":
+        it["Aqk"] = np.tril(it["Aqk"], -1)
+    elif mistake == "w_without_beta":
+        beta = np.transpose(np.asarray(d["beta"], np.float64), (0, 2, 1))
+        B, H, n, Cc, dk = it["W"].shape
+        bp = np.ones((B, H, n * Cc))
+        bp[:, :, :beta.shape[2]] = beta
+        # undo the beta scaling of the right-hand side (beta > 0 on every real row)
+        it["W"] = it["T"] @ (np.linalg.solve(it["T"], it["W"]) / bp.reshape(B, H, n, Cc)[..., None])
+    elif mistake == "gc_first_row":
+        it["GC"] = it["GQ"][..., 0, :] * 0 + np.exp(np.transpose(np.asarray(d["g"], np.float64), (0, 2, 1, 3))
+                                                    [:, :, ::C][:, :, :it["GC"].shape[2]])
+    elif mistake == "u_shifted_chunk":
+        it["U"] = np.roll(it["U"], 1, axis=2)
+    assert _rebuild_error(d, it, o_r, s_r) > 1e-4, f"mistake {mistake} not caught"
+
+
+# ---------------------------------------------------------------------------
+# tile width rule
+# ---------------------------------------------------------------------------
+
+
+@pytest.mark.parametrize("g_min,expect", [(-5.0, 16), (-10.0, 8), (0.0, 16), (-3.0, 16), (-20.0, 4),
+                                          (-30.0, 2), (-100.0, 1)])
+def test_cc_tile_values(g_min, expect):
+    """net/kda.py:577-585: the widest tile (at most 16) whose column factor
+    exp(|g_min| * tile) stays inside the exponent budget of 80, at least 1."""
+    t = K.cc_tile(g_min)
+    assert t == expect
+    step = abs(g_min)
+    assert 1 <= t <= 16
+    if t > 1:
+        assert t * step <= 80.0
+    assert t == 16 or (t + 1) * step > 80.0 or t == 1
