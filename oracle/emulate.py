@@ -122,39 +122,42 @@ def _chunk(rd: _Round, q, k, v, g, beta, S, diag: str):
             a = rd.h(kc[:, cols])
             Akk[:, rows, cols] = _scores_tile_pair(rd, rd.h(rd.f(kr[:, rows] * M[:, None])), a)
             Aqk[:, rows, cols] = _scores_tile_pair(rd, rd.h(rd.f(qr[:, rows] * M[:, None])), a)
-        # diagonal tile
+        # diagonal tile; the operand path is chosen per chain (per chunk-head,
+        # as each workgroup decides for its own tile)
         Dr = D[r]
-        extreme = bool((Dr < -100).any())
+        extreme = (Dr < -100).any(1)                                     # [N]
         iD = rd.f(torch.exp2(-Dr))[:, None]
-        if not extreme:
-            ad = kc[:, rows]
-            bk = rd.f(kr[:, rows] * iD)
-            bq = rd.f(qr[:, rows] * iD)
-        else:
+        ad = kc[:, rows]
+        bk = rd.f(kr[:, rows] * iD)
+        bq = rd.f(qr[:, rows] * iD)
+        if bool(extreme.any()):
             g7 = Gt[:, 16 * r + 7][:, None]
             gt = Gt[:, rows]
             fr = rd.f(torch.exp2(rd.f(gt - g7)))
-            ad = rd.f(k[:, rows] * rd.f(torch.exp2(rd.f(g7 - gt))))
-            bk = rd.f(k[:, rows] * fr)
-            bq = rd.f(q[:, rows] * fr)
+            x_ = extreme[:, None, None]
+            ad = torch.where(x_, rd.f(k[:, rows] * rd.f(torch.exp2(rd.f(g7 - gt)))), ad)
+            bk = torch.where(x_, rd.f(k[:, rows] * fr), bk)
+            bq = torch.where(x_, rd.f(q[:, rows] * fr), bq)
         mx = torch.stack([kc[:, rows].abs().amax((1, 2)), kr[:, rows].abs().amax((1, 2)),
                           qr[:, rows].abs().amax((1, 2))]).amax(0)
-        fp16_ok = (not extreme) and bool((Dr > -12).all()) and bool((mx <= 8).all())
+        fp16_ok = (~extreme) & (Dr > -12).all(1) & (mx <= 8)             # [N]
         if diag == "fp32" or rd.exact:
             blk_k = rd.mm(bk, ad.transpose(1, 2))
             blk_q = rd.mm(bq, ad.transpose(1, 2))
         elif diag == "bf16":
             blk_k = rd.mm(rd.b(bk), rd.b(ad).transpose(1, 2))
             blk_q = rd.mm(rd.b(bq), rd.b(ad).transpose(1, 2))
-        elif fp16_ok:
-            blk_k = rd.mm(rd.h(bk), rd.h(ad).transpose(1, 2))
-            blk_q = rd.mm(rd.h(bq), rd.h(ad).transpose(1, 2))
         else:
             ah, al = rd.hilo(ad)
             kh, kl = rd.hilo(bk)
             qh, ql = rd.hilo(bq)
-            blk_k = rd.f(kh @ ah.transpose(1, 2) + kl @ ah.transpose(1, 2) + kh @ al.transpose(1, 2))
-            blk_q = rd.f(qh @ ah.transpose(1, 2) + ql @ ah.transpose(1, 2) + qh @ al.transpose(1, 2))
+            hl_k = rd.f(kh @ ah.transpose(1, 2) + kl @ ah.transpose(1, 2) + kh @ al.transpose(1, 2))
+            hl_q = rd.f(qh @ ah.transpose(1, 2) + ql @ ah.transpose(1, 2) + qh @ al.transpose(1, 2))
+            f16_k = rd.mm(rd.h(bk), rd.h(ad).transpose(1, 2))
+            f16_q = rd.mm(rd.h(bq), rd.h(ad).transpose(1, 2))
+            ok = fp16_ok[:, None, None]
+            blk_k = torch.where(ok, f16_k, hl_k)
+            blk_q = torch.where(ok, f16_q, hl_q)
         zero = torch.zeros((), dtype=F64)
         Akk[:, rows, rows] = torch.where(ri > ci, blk_k, zero)
         Aqk[:, rows, rows] = torch.where(ri >= ci, blk_q, zero)
