@@ -6,6 +6,7 @@
 #include <cstdarg>
 #include <cstdio>
 #include <cstring>
+#include <mutex>
 #include <numeric>
 
 #include "kda_common.h"
@@ -336,9 +337,58 @@ int ut_check(const void* a, const void* b, const void* x, int H, int C, int N, i
   return KDA_OK;
 }
 
+// ----------------------------------------------------------------------------
+// Scratch of kda_chunk_fwd_noalloc: the forward's workspace as a file-scope
+// device array, so that entry point allocates nothing.  Each device holds its
+// own copy (at its own address) from the library's load until the process
+// ends.  In host code `scratch` names a host-side stand-in, not device
+// memory: its device address is taken once per device with
+// hipGetSymbolAddress and only that pointer is ever handed to kernels.  Calls
+// on one device share the array; calls that overlap on one device (two
+// streams, two threads) race on it.  No part of it needs clearing between
+// calls: the forward writes every workspace word it reads within the call.
+// ----------------------------------------------------------------------------
+constexpr size_t kScratchBytes = static_cast<size_t>(128) << 20;
+static __device__ __align__(256) unsigned char scratch[kScratchBytes];
+
+constexpr int kMaxDevices = 64;
+std::mutex g_scratch_mu;
+void* g_scratch_ptr[kMaxDevices] = {};
+
+// Device address of this device's scratch, looked up on the first call on
+// the device (with that device current) and kept.
+int scratch_for_stream(hipStream_t stream, void** out) {
+  int dev = -1;
+  hipError_t e = hipGetDevice(&dev);
+  if (e != hipSuccess) return hip_fail(e, "hipGetDevice");
+  if (stream != nullptr) {
+    int sdev = -1;
+    e = hipStreamGetDevice(stream, &sdev);
+    if (e != hipSuccess) return hip_fail(e, "hipStreamGetDevice");
+    dev = sdev;
+  }
+  if (dev < 0 || dev >= kMaxDevices) return fail(KDA_ERR_UNSUPPORTED, "device %d: at most %d devices", dev, kMaxDevices);
+  std::lock_guard<std::mutex> lock(g_scratch_mu);
+  if (g_scratch_ptr[dev] == nullptr) {
+    int cur = -1;
+    e = hipGetDevice(&cur);
+    if (e != hipSuccess) return hip_fail(e, "hipGetDevice");
+    if (cur != dev && (e = hipSetDevice(dev)) != hipSuccess) return hip_fail(e, "hipSetDevice");
+    void* p = nullptr;
+    e = hipGetSymbolAddress(&p, HIP_SYMBOL(scratch));
+    hipError_t e2 = (cur != dev) ? hipSetDevice(cur) : hipSuccess;
+    if (e != hipSuccess) return hip_fail(e, "hipGetSymbolAddress(scratch)");
+    if (e2 != hipSuccess) return hip_fail(e2, "hipSetDevice");
+    if (p == nullptr) return fail(KDA_ERR_HIP, "hipGetSymbolAddress(scratch) returned null");
+    g_scratch_ptr[dev] = p;
+  }
+  *out = g_scratch_ptr[dev];
+  return KDA_OK;
+}
+
 extern "C" {
 
-int kda_abi_version(void) { return 101; }
+int kda_abi_version(void) { return 102; }
 
 const char* kda_last_error(void) { return g_err; }
 
@@ -357,6 +407,30 @@ int kda_chunk_fwd(hipStream_t stream, const void* q, const void* k, const void* 
   g_err[0] = '\0';
   return chunk_fwd_impl(stream, q, k, v, g, beta, h0, cu_seqlens, n_seqs, o, ht, B, T, H, dk, dv,
                         chunk, scale, in_dtype, out_dtype, workspace, workspace_bytes);
+}
+
+int kda_chunk_fwd_noalloc(hipStream_t stream, const void* q, const void* k, const void* v,
+                          const void* g, const void* beta, const float* h0,
+                          const int32_t* cu_seqlens, int32_t n_seqs, void* o, float* ht,
+                          int B, int T, int H, int dk, int dv, int chunk, float scale,
+                          int in_dtype, int out_dtype) {
+  g_err[0] = '\0';
+  if (B < 1 || T < 0 || H < 1 || !dim_ok(dk) || dk != dv || chunk != kC ||
+      in_dtype < KDA_DTYPE_F32 || in_dtype > KDA_DTYPE_BF16_F32GATES) {
+    // the full argument checks with their messages
+    return chunk_fwd_impl(stream, q, k, v, g, beta, h0, cu_seqlens, n_seqs, o, ht, B, T, H, dk, dv,
+                          chunk, scale, in_dtype, out_dtype, nullptr, 0);
+  }
+  const size_t need = ws_layout(B, T, H, dk, dv, cu_seqlens != nullptr ? n_seqs : 0, in_dtype).total;
+  if (need > kScratchBytes)
+    return fail(KDA_ERR_WORKSPACE,
+                "kda_chunk_fwd_noalloc: this call needs %zu bytes of scratch, the library's "
+                "per-device scratch holds %zu (use kda_chunk_fwd with a caller workspace)",
+                need, kScratchBytes);
+  void* ws = nullptr;
+  if (int rc = scratch_for_stream(stream, &ws)) return rc;
+  return chunk_fwd_impl(stream, q, k, v, g, beta, h0, cu_seqlens, n_seqs, o, ht, B, T, H, dk, dv,
+                        chunk, scale, in_dtype, out_dtype, ws, kScratchBytes);
 }
 
 int kda_varlen_status(hipStream_t stream, const void* workspace, size_t workspace_bytes,

@@ -89,6 +89,27 @@ KDA_API int kda_chunk_fwd(hipStream_t stream,
                   int in_dtype, int out_dtype,
                   void* workspace, size_t workspace_bytes);
 
+/*
+ * kda_chunk_fwd without a workspace argument: the workspace is a file-scope
+ * device array of the library (128 MiB = 134217728 bytes, one per device,
+ * held from the library's load until the process ends), so the call allocates nothing (no hipMalloc, no allocating library
+ * routine) and only launches kernels.  No counterpart in the reference: it is
+ * for callers that cannot allocate -- code under HIP graph capture, tight
+ * serving loops, harnesses that forbid allocation.  Arguments, results and
+ * errors as kda_chunk_fwd; a call whose workspace (kda_chunk_fwd_workspace)
+ * exceeds the scratch returns KDA_ERR_WORKSPACE.  All calls on one device
+ * share its scratch: calls that overlap on one device (two streams or
+ * threads) race and must be ordered by the caller.
+ */
+KDA_API int kda_chunk_fwd_noalloc(hipStream_t stream,
+                  const void* q, const void* k, const void* v,
+                  const void* g, const void* beta,
+                  const float* h0,
+                  const int32_t* cu_seqlens, int32_t n_seqs,
+                  void* o, float* ht,
+                  int B, int T, int H, int dk, int dv, int chunk, float scale,
+                  int in_dtype, int out_dtype);
+
 /* Workspace bytes kda_chunk_fwd needs for these arguments (0 on bad input).
  * n_seqs <= 0 means dense (no cu_seqlens).  Host-only; no HIP call. */
 KDA_API size_t kda_chunk_fwd_workspace(int B, int T, int H, int dk, int dv, int chunk,
