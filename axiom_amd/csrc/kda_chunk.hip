@@ -1425,6 +1425,289 @@ void kda_state_col_kernel(StateArgs a) {
 }
 
 // ----------------------------------------------------------------------------
+// State kernel, whole-chain form (fp16 operands)
+//
+// One workgroup of eight waves owns a whole chain (all dv columns): compute
+// wave w (0..3) owns value tiles w*DV/64 .. (w+1)*DV/64 - 1 for all dk
+// channels, so every shared fragment it reads from LDS feeds one MFMA per
+// value tile it owns; producer waves 4..7 copy the chunk's shared operands,
+// gamma_C and the whole U into one of two LDS buffers one chunk ahead.  The
+// compute waves store o straight from their accumulators: they issue no
+// loads, so their stores queue behind nothing.  Against the 32-column form
+// the shared operands of a chunk are copied into LDS once per chain instead
+// of once per slice, and each LDS read feeds twice the MFMA work.
+// ----------------------------------------------------------------------------
+template <int DK, int DV>
+struct FullLayout {
+  typedef ColLayout<DK> CL;
+  static constexpr int NF = CL::NF;
+  static constexpr int OFF_G = NF * 1024;                       // gamma_C (DK floats)
+  static constexpr int OFF_U = NF * 1024 + DK * 4;              // U [ct][vt][64][4] fp16
+  static constexpr int BYTES = OFF_U + 4 * (DV / 16) * 512;
+};
+
+template <int DK, int DV>
+struct FullSmem {
+  alignas(16) unsigned char buf[2][FullLayout<DK, DV>::BYTES];
+};
+
+constexpr int kFullCompute = 4;     // compute waves of a whole-chain workgroup
+constexpr int kFullProducers = 4;   // producer waves
+
+// Producer P's share of chunk-head ch: every fourth shared fragment, U row
+// tile P of every value tile, and (last producer) gamma_C.
+template <int DK, int DV, int P>
+__device__ __forceinline__ void full_stage(const StateArgs& a, int64_t ch, unsigned char* dst, int l) {
+  typedef ColLayout<DK> LY;
+  typedef FullLayout<DK, DV> FL;
+  const _Float16* iW = static_cast<const _Float16*>(a.W);
+  const _Float16* iQ = static_cast<const _Float16*>(a.GQ);
+  const _Float16* iL = static_cast<const _Float16*>(a.LK);
+  const _Float16* iA = static_cast<const _Float16*>(a.AQ);
+#pragma unroll
+  for (int f = P; f < LY::NF; f += kFullProducers) {
+    const _Float16* src;
+    if (f < LY::OFF_Q) src = iW + (ch * LY::FW + f) * 512;
+    else if (f < LY::OFF_L) src = iQ + (ch * LY::FW + (f - LY::OFF_Q)) * 512;
+    else if (f < LY::OFF_A) src = iL + (ch * LY::FL + (f - LY::OFF_L)) * 512;
+    else {
+      const int ai = f - LY::OFF_A;                 // 0..5 -> (ct, jj) = 00 10 20 21 30 31
+      const int gidx = (ai < 2) ? 2 * ai : ai + 2;  // index ct*2 + jj in the workspace
+      src = iA + (ch * 8 + gidx) * 512;
+    }
+    __builtin_amdgcn_global_load_lds(src + l * 8, dst + f * 1024, 16, 0, 0);
+  }
+  static_assert(kFullProducers == 4, "one U row tile per producer");
+#pragma unroll
+  for (int i = 0; i < DV / 32; ++i) {
+    // value tiles 2i, 2i+1 of row tile P: 1 KiB, contiguous in the workspace
+    const _Float16* usrc = static_cast<const _Float16*>(a.U) +
+                           (ch * 4 * (DV / 16) + P * (DV / 16) + 2 * i) * 256 + l * 8;
+    __builtin_amdgcn_global_load_lds(usrc, dst + FL::OFF_U + (P * (DV / 16) + 2 * i) * 512, 16, 0, 0);
+  }
+  if constexpr (P == kFullProducers - 1) {
+    const _Float16* gsrc = reinterpret_cast<const _Float16*>(a.GC + ch * DK + l * 4);
+    if (l < DK / 4) __builtin_amdgcn_global_load_lds(gsrc, dst + FL::OFF_G, 16, 0, 0);
+  }
+}
+
+template <int DK, int DV, int P>
+__device__ __forceinline__ void full_producer(const StateArgs& a, FullSmem<DK, DV>& sm, int seq, int h) {
+  const ChainRef c = chain_ref(a.geom, seq);
+  const int H = a.geom.H;
+  const int l = threadIdx.x & 63;
+  if (c.nchunks <= 0) return;
+  full_stage<DK, DV, P>(a, static_cast<int64_t>(c.u0) * H + h, sm.buf[0], l);
+  wait_vmem_all();
+  lds_barrier();
+  for (int n = 0; n < c.nchunks; ++n) {
+    if (n + 1 < c.nchunks)
+      full_stage<DK, DV, P>(a, static_cast<int64_t>(c.u0 + n + 1) * H + h, sm.buf[(n + 1) & 1], l);
+    wait_vmem_all();
+    lds_barrier();
+  }
+}
+
+template <int DK, int DV, int OUT_DT, int W>
+__device__ __forceinline__ void full_chain(const StateArgs& a, FullSmem<DK, DV>& sm, int seq, int h) {
+  typedef ColLayout<DK> LY;
+  typedef FullLayout<DK, DV> FL;
+  constexpr int NJ = DK / 32;
+  constexpr int NT = DK / 16;
+  constexpr int NVT = DV / 16;                  // value tiles of the chain
+  constexpr int NC = NVT / kFullCompute;        // value tiles of this wave
+  const Geom& G = a.geom;
+  const int H = G.H;
+  const int l = threadIdx.x & 63, r = l & 15, gq = l >> 4;
+  const int tile0 = W * NC;
+  const ChainRef c = chain_ref(G, seq);
+  const int nchunks = c.nchunks;
+
+  f4 S[NC][NT];
+  const int64_t sbase = (static_cast<int64_t>(seq) * H + h) * DK * DV;
+#pragma unroll
+  for (int cc = 0; cc < NC; ++cc)
+#pragma unroll
+    for (int dt = 0; dt < NT; ++dt)
+#pragma unroll
+      for (int i = 0; i < 4; ++i)
+        S[cc][dt][i] = (a.h0 != nullptr)
+                           ? a.h0[sbase + static_cast<int64_t>(16 * dt + 4 * gq + i) * DV + 16 * (tile0 + cc) + r]
+                           : 0.f;
+
+  if (nchunks > 0) lds_barrier();  // chunk 0 staged by the producer waves
+  for (int n = 0; n < nchunks; ++n) {
+    const unsigned char* cur = sm.buf[n & 1];
+    // Item stream of the step, 16-byte LDS reads consumed in order (each
+    // fragment feeds one MFMA per value tile of this wave):
+    //   items 0 .. 8*NJ-1   W and gamma*q fragments of row tile ct = i / (2*NJ)
+    //                       (alternating: the P and O products of K step j),
+    //   next FA items       Aqk fragments,
+    //   last 3*NT items     per channel tile dt: gamma_C (one float4 per
+    //                       lane), then the lambda*k fragments of K steps 0, 1.
+    constexpr int N_ROW = 8 * NJ;
+    constexpr int I_AQ = N_ROW;
+    constexpr int I_LK = I_AQ + LY::FA;
+    constexpr int NIT = I_LK + 3 * NT;
+    constexpr int DEPTH = 6;
+    constexpr int RING = DEPTH + 1;
+    auto item_read = [&](auto ic) -> uint4 {
+      constexpr int i = decltype(ic)::value;
+      const unsigned char* p;
+      if constexpr (i < N_ROW) {
+        constexpr int ct = i / (2 * NJ), j = (i % (2 * NJ)) >> 1;
+        p = cur + (((i & 1) ? LY::OFF_Q : 0) + ct * NJ + j) * 1024 + l * 16;
+      } else if constexpr (i < I_LK) {
+        p = cur + (LY::OFF_A + (i - I_AQ)) * 1024 + l * 16;
+      } else {
+        constexpr int dt = (i - I_LK) / 3, k3 = (i - I_LK) % 3;
+        if constexpr (k3 == 0) p = cur + FL::OFF_G + (16 * dt + 4 * gq) * 4;
+        else p = cur + (LY::OFF_L + 2 * dt + (k3 - 1)) * 1024 + l * 16;
+      }
+      return *reinterpret_cast<const uint4*>(p);
+    };
+    uint4 ring[RING];
+    static_for<0, DEPTH>([&](auto ic) { ring[decltype(ic)::value % RING] = item_read(ic); });
+    h4 Ucur[NC][4];
+#pragma unroll
+    for (int cc = 0; cc < NC; ++cc)
+#pragma unroll
+      for (int ct = 0; ct < 4; ++ct)
+        Ucur[cc][ct] = *reinterpret_cast<const h4*>(cur + FL::OFF_U + (ct * NVT + tile0 + cc) * 512 + l * 8);
+    // S as B fragments over channels
+    h8 Sb[NC][NJ];
+#pragma unroll
+    for (int cc = 0; cc < NC; ++cc)
+#pragma unroll
+      for (int j = 0; j < NJ; ++j)
+#pragma unroll
+        for (int i = 0; i < 4; ++i) {
+          Sb[cc][j][i] = static_cast<_Float16>(S[cc][2 * j][i]);
+          Sb[cc][j][4 + i] = static_cast<_Float16>(S[cc][2 * j + 1][i]);
+        }
+    f4 O[NC][4], P[NC], Gc;
+    h4 Vh[NC][4];
+    h8 Vb[NC][2];
+#pragma unroll
+    for (int cc = 0; cc < NC; ++cc)
+#pragma unroll
+      for (int ct = 0; ct < 4; ++ct) O[cc][ct] = f4{0, 0, 0, 0};
+    static_for<0, NIT>([&](auto ic) {
+      constexpr int i = decltype(ic)::value;
+      if constexpr (i + DEPTH < NIT) ring[(i + DEPTH) % RING] = item_read(std::integral_constant<int, i + DEPTH>{});
+      __builtin_amdgcn_sched_barrier(0);
+      const uint4 it = ring[i % RING];
+      if constexpr (i < N_ROW) {
+        // P = W S and O = (gamma q) S, row tile ct; v~ = U - P once P is complete
+        constexpr int ct = i / (2 * NJ), j = (i % (2 * NJ)) >> 1;
+        const h8 A = __builtin_bit_cast(h8, it);
+#pragma unroll
+        for (int cc = 0; cc < NC; ++cc) {
+          if constexpr (i & 1) {
+            O[cc][ct] = mma32(O[cc][ct], A, Sb[cc][j]);
+          } else {
+            if constexpr (j == 0) P[cc] = mma32(f4{0, 0, 0, 0}, A, Sb[cc][j]);
+            else P[cc] = mma32(P[cc], A, Sb[cc][j]);
+          }
+        }
+        if constexpr (i % (2 * NJ) == 2 * NJ - 1) {
+#pragma unroll
+          for (int cc = 0; cc < NC; ++cc)
+#pragma unroll
+            for (int e = 0; e < 4; ++e)
+              Vh[cc][ct][e] = static_cast<_Float16>(static_cast<float>(Ucur[cc][ct][e]) - P[cc][e]);
+        }
+      } else if constexpr (i < I_LK) {
+        // O += Aqk v~ (keys at or before the row tile); fragments (ct,jj) = 00 10 20 21 30 31
+        constexpr int f = i - I_AQ;
+        if constexpr (f == 0) {
+#pragma unroll
+          for (int cc = 0; cc < NC; ++cc)
+#pragma unroll
+            for (int jj = 0; jj < 2; ++jj)
+#pragma unroll
+              for (int e = 0; e < 4; ++e) {
+                Vb[cc][jj][e] = Vh[cc][2 * jj][e];
+                Vb[cc][jj][4 + e] = Vh[cc][2 * jj + 1][e];
+              }
+        }
+        constexpr int ct = (f < 2) ? f : 2 + ((f - 2) >> 1);
+        constexpr int jj = (f < 2) ? 0 : ((f - 2) & 1);
+        const h8 A = __builtin_bit_cast(h8, it);
+#pragma unroll
+        for (int cc = 0; cc < NC; ++cc) O[cc][ct] = mma32(O[cc][ct], A, Vb[cc][jj]);
+      } else {
+        // S <- gamma_C S + (lambda k)^T v~ for channel tile dt
+        constexpr int dt = (i - I_LK) / 3, k3 = (i - I_LK) % 3;
+        if constexpr (k3 == 0) {
+          Gc = __builtin_bit_cast(f4, it);
+        } else {
+          const h8 A = __builtin_bit_cast(h8, it);
+#pragma unroll
+          for (int cc = 0; cc < NC; ++cc) {
+            if constexpr (k3 == 1) S[cc][dt] = S[cc][dt] * Gc;
+            S[cc][dt] = mma32(S[cc][dt], A, Vb[cc][k3 - 1]);
+          }
+        }
+      }
+    });
+
+    // o of this chunk straight from the accumulators (rows past the end skipped)
+    const int64_t row0 = c.tok0 + static_cast<int64_t>(n) * kC;
+    const int len = min(kC, c.seq_len - n * kC);
+#pragma unroll
+    for (int cc = 0; cc < NC; ++cc)
+#pragma unroll
+      for (int ct = 0; ct < 4; ++ct)
+#pragma unroll
+        for (int i = 0; i < 4; ++i) {
+          const int row = 16 * ct + 4 * gq + i;
+          if (row < len) {
+            const int64_t oi = ((row0 + row) * H + h) * static_cast<int64_t>(DV) + 16 * (tile0 + cc) + r;
+            if constexpr (OUT_DT == 0) static_cast<float*>(a.o)[oi] = O[cc][ct][i];
+            else static_cast<u16*>(a.o)[oi] = f32_to_bf16_bits(O[cc][ct][i]);
+          }
+        }
+    // the producers have landed the next buffer; this one is refilled only
+    // after every compute wave has passed this barrier
+    lds_barrier();
+  }
+
+  if (a.ht != nullptr) {
+#pragma unroll
+    for (int cc = 0; cc < NC; ++cc)
+#pragma unroll
+      for (int dt = 0; dt < NT; ++dt)
+#pragma unroll
+        for (int i = 0; i < 4; ++i)
+          a.ht[sbase + static_cast<int64_t>(16 * dt + 4 * gq + i) * DV + 16 * (tile0 + cc) + r] = S[cc][dt][i];
+  }
+}
+
+template <int DK, int DV, int OUT_DT>
+__global__ __launch_bounds__(64 * (kFullCompute + kFullProducers), 1)
+void kda_state_full_kernel(StateArgs a) {
+  __shared__ FullSmem<DK, DV> sm;
+  const Geom& G = a.geom;
+  const int H = G.H;
+  const int chain = blockIdx.x;
+  if (chain >= G.N * H) return;
+  const int seq_rank = chain / H;
+  const int h = chain - seq_rank * H;
+  const int seq = (G.order != nullptr) ? G.order[seq_rank] : seq_rank;
+  switch (threadIdx.x >> 6) {
+    case 0: full_chain<DK, DV, OUT_DT, 0>(a, sm, seq, h); break;
+    case 1: full_chain<DK, DV, OUT_DT, 1>(a, sm, seq, h); break;
+    case 2: full_chain<DK, DV, OUT_DT, 2>(a, sm, seq, h); break;
+    case 3: full_chain<DK, DV, OUT_DT, 3>(a, sm, seq, h); break;
+    case 4: full_producer<DK, DV, 0>(a, sm, seq, h); break;
+    case 5: full_producer<DK, DV, 1>(a, sm, seq, h); break;
+    case 6: full_producer<DK, DV, 2>(a, sm, seq, h); break;
+    default: full_producer<DK, DV, 3>(a, sm, seq, h); break;
+  }
+}
+
+// ----------------------------------------------------------------------------
 // host-side launchers
 // ----------------------------------------------------------------------------
 template <int DK, int DV, int DTQ, int DTG, bool EXACT, bool PRO = false>
@@ -1433,13 +1716,23 @@ static hipError_t launch_intra_t(const IntraArgs& a, int grid, hipStream_t s) {
   return hipGetLastError();
 }
 
+// The whole-chain state kernel runs a chunk step in ~2.3 us against ~1.4 us
+// for the 32-column slices, but with four times the work per CU: it pays
+// when there are enough chains to fill the CUs (one workgroup per CU), and
+// the slices pay when the serial chain is the critical path.
+constexpr int kFullStateMinChains = 256;
 template <int DK, int DV, bool EXACT, int OUT>
 static hipError_t launch_state_t(const StateArgs& a, int grid, hipStream_t s) {
   if constexpr (EXACT) {
     hipLaunchKernelGGL((kda_state_kernel<DK, DV, EXACT, OUT>), dim3(grid), dim3(256), 0, s, a);
   } else {
-    hipLaunchKernelGGL((kda_state_col_kernel<DK, DV, OUT>), dim3(grid), dim3(64 * (kColComputeWaves + kColProducers)), 0,
-                       s, a);
+    if (DK == 128 && a.geom.N * a.geom.H >= kFullStateMinChains) {
+      hipLaunchKernelGGL((kda_state_full_kernel<DK, DV, OUT>), dim3(a.geom.N * a.geom.H),
+                         dim3(64 * (kFullCompute + kFullProducers)), 0, s, a);
+    } else {
+      hipLaunchKernelGGL((kda_state_col_kernel<DK, DV, OUT>), dim3(grid), dim3(64 * (kColComputeWaves + kColProducers)), 0,
+                         s, a);
+    }
   }
   return hipGetLastError();
 }
