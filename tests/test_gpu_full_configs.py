@@ -132,3 +132,23 @@ def test_config4_decode_full(cuda):
     o_got = torch.stack([o[bs, hs] for o in outs]).cpu().numpy()[:, :, None]
     assert_close("o", o_got, o_ref, (1e-5, 1e-5))
     assert_close("S", torch.stack([S[b, h] for b, h in pick]).cpu().numpy()[:, None], S_ref, (1e-5, 1e-5))
+
+
+def test_long_two_chain_call_against_oracle(cuda):
+    """B1 T50000 H2 d128 with h0: two chains whose intra-chunk results exceed
+    one segment (the call runs in segments); both chains against the oracle,
+    and the final-state-free call gives the same o bit for bit."""
+    import axiom_amd
+    B, T, H, dd = 1, 50000, 2, 128
+    d = make_inputs_device(B, T, H, dd, dd, seed=106, device=cuda, h0_std=0.02)
+    print("[full] long two-chain call", flush=True)
+    o, ht = _fwd(d, h0=d["h0"])
+    hc = host_chains(d, 0, [0, 1])
+    o_ref, ht_ref = K.chunk_fwd(hc["q"], hc["k"], hc["v"], hc["g"], hc["beta"], h0=d["h0"].cpu().numpy(),
+                                chunk=64)
+    assert_close("o", o, o_ref, TOL["bf16"])
+    assert_close("ht", ht, ht_ref, TOL["bf16"])
+    o2, _ = axiom_amd.kda_chunk_fwd(d["q"], d["k"], d["v"], d["g"], d["beta"], initial_state=d["h0"],
+                                    output_final_state=False)
+    torch.cuda.synchronize()
+    assert torch.equal(o2, o)
