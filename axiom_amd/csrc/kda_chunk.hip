@@ -1425,47 +1425,47 @@ void kda_state_col_kernel(StateArgs a) {
 }
 
 // ----------------------------------------------------------------------------
-// State kernel, whole-chain form (fp16 operands)
+// State kernel, wide-slice form (fp16 operands)
 //
-// One workgroup of eight waves owns a whole chain (all dv columns): compute
-// wave w (0..3) owns value tiles w*DV/64 .. (w+1)*DV/64 - 1 for all dk
-// channels, so every shared fragment it reads from LDS feeds one MFMA per
-// value tile it owns; producer waves 4..7 copy the chunk's shared operands,
-// gamma_C and the whole U into one of two LDS buffers one chunk ahead.  The
-// compute waves store o straight from their accumulators: they issue no
-// loads, so their stores queue behind nothing.  Against the 32-column form
-// the shared operands of a chunk are copied into LDS once per chain instead
-// of once per slice, and each LDS read feeds twice the MFMA work.
+// A workgroup owns VT value tiles (16 columns each) of one chain: compute
+// wave w owns VT / CW of them for all dk channels, so every shared fragment
+// it reads from LDS feeds one MFMA per value tile it owns; four producer
+// waves copy the chunk's shared operands, gamma_C and the workgroup's U into
+// one of two LDS buffers one chunk ahead.  The compute waves store o straight
+// from their accumulators: they issue no loads, so their stores queue behind
+// nothing.  Against the 32-column form, the shared operands of a chunk are
+// copied into LDS once per VT value tiles instead of once per two, and each
+// LDS read feeds more MFMA work; the serial step is longer.  VT = 8 (the
+// whole chain) pays when the chains fill the CUs, VT = 4 in between.
 // ----------------------------------------------------------------------------
-template <int DK, int DV>
-struct FullLayout {
+template <int DK, int VT>
+struct WideLayout {
   typedef ColLayout<DK> CL;
   static constexpr int NF = CL::NF;
   static constexpr int OFF_G = NF * 1024;                       // gamma_C (DK floats)
-  static constexpr int OFF_U = NF * 1024 + DK * 4;              // U [ct][vt][64][4] fp16
-  static constexpr int BYTES = OFF_U + 4 * (DV / 16) * 512;
+  static constexpr int OFF_U = NF * 1024 + DK * 4;              // U [ct][VT][64][4] fp16
+  static constexpr int BYTES = OFF_U + 4 * VT * 512;
 };
 
-template <int DK, int DV>
-struct FullSmem {
-  alignas(16) unsigned char buf[2][FullLayout<DK, DV>::BYTES];
+template <int DK, int VT>
+struct WideSmem {
+  alignas(16) unsigned char buf[2][WideLayout<DK, VT>::BYTES];
 };
 
-constexpr int kFullCompute = 4;     // compute waves of a whole-chain workgroup
-constexpr int kFullProducers = 4;   // producer waves
+constexpr int kWideProducers = 4;
 
 // Producer P's share of chunk-head ch: every fourth shared fragment, U row
-// tile P of every value tile, and (last producer) gamma_C.
-template <int DK, int DV, int P>
-__device__ __forceinline__ void full_stage(const StateArgs& a, int64_t ch, unsigned char* dst, int l) {
+// tile P of the workgroup's value tiles, and (last producer) gamma_C.
+template <int DK, int DV, int VT, int P>
+__device__ __forceinline__ void wide_stage(const StateArgs& a, int64_t ch, int split, unsigned char* dst, int l) {
   typedef ColLayout<DK> LY;
-  typedef FullLayout<DK, DV> FL;
+  typedef WideLayout<DK, VT> WL;
   const _Float16* iW = static_cast<const _Float16*>(a.W);
   const _Float16* iQ = static_cast<const _Float16*>(a.GQ);
   const _Float16* iL = static_cast<const _Float16*>(a.LK);
   const _Float16* iA = static_cast<const _Float16*>(a.AQ);
 #pragma unroll
-  for (int f = P; f < LY::NF; f += kFullProducers) {
+  for (int f = P; f < LY::NF; f += kWideProducers) {
     const _Float16* src;
     if (f < LY::OFF_Q) src = iW + (ch * LY::FW + f) * 512;
     else if (f < LY::OFF_L) src = iQ + (ch * LY::FW + (f - LY::OFF_Q)) * 512;
@@ -1477,49 +1477,49 @@ __device__ __forceinline__ void full_stage(const StateArgs& a, int64_t ch, unsig
     }
     __builtin_amdgcn_global_load_lds(src + l * 8, dst + f * 1024, 16, 0, 0);
   }
-  static_assert(kFullProducers == 4, "one U row tile per producer");
+  static_assert(kWideProducers == 4, "one U row tile per producer");
 #pragma unroll
-  for (int i = 0; i < DV / 32; ++i) {
-    // value tiles 2i, 2i+1 of row tile P: 1 KiB, contiguous in the workspace
+  for (int i = 0; i < VT / 2; ++i) {
+    // value tiles 2i, 2i+1 of the workgroup, row tile P: 1 KiB, contiguous in the workspace
     const _Float16* usrc = static_cast<const _Float16*>(a.U) +
-                           (ch * 4 * (DV / 16) + P * (DV / 16) + 2 * i) * 256 + l * 8;
-    __builtin_amdgcn_global_load_lds(usrc, dst + FL::OFF_U + (P * (DV / 16) + 2 * i) * 512, 16, 0, 0);
+                           (ch * 4 * (DV / 16) + P * (DV / 16) + split * VT + 2 * i) * 256 + l * 8;
+    __builtin_amdgcn_global_load_lds(usrc, dst + WL::OFF_U + (P * VT + 2 * i) * 512, 16, 0, 0);
   }
-  if constexpr (P == kFullProducers - 1) {
+  if constexpr (P == kWideProducers - 1) {
     const _Float16* gsrc = reinterpret_cast<const _Float16*>(a.GC + ch * DK + l * 4);
-    if (l < DK / 4) __builtin_amdgcn_global_load_lds(gsrc, dst + FL::OFF_G, 16, 0, 0);
+    if (l < DK / 4) __builtin_amdgcn_global_load_lds(gsrc, dst + WL::OFF_G, 16, 0, 0);
   }
 }
 
-template <int DK, int DV, int P>
-__device__ __forceinline__ void full_producer(const StateArgs& a, FullSmem<DK, DV>& sm, int seq, int h) {
+template <int DK, int DV, int VT, int P>
+__device__ __forceinline__ void wide_producer(const StateArgs& a, WideSmem<DK, VT>& sm, int seq, int h, int split) {
   const ChainRef c = chain_ref(a.geom, seq);
   const int H = a.geom.H;
   const int l = threadIdx.x & 63;
   if (c.nchunks <= 0) return;
-  full_stage<DK, DV, P>(a, static_cast<int64_t>(c.u0) * H + h, sm.buf[0], l);
+  wide_stage<DK, DV, VT, P>(a, static_cast<int64_t>(c.u0) * H + h, split, sm.buf[0], l);
   wait_vmem_all();
   lds_barrier();
   for (int n = 0; n < c.nchunks; ++n) {
     if (n + 1 < c.nchunks)
-      full_stage<DK, DV, P>(a, static_cast<int64_t>(c.u0 + n + 1) * H + h, sm.buf[(n + 1) & 1], l);
+      wide_stage<DK, DV, VT, P>(a, static_cast<int64_t>(c.u0 + n + 1) * H + h, split, sm.buf[(n + 1) & 1], l);
     wait_vmem_all();
     lds_barrier();
   }
 }
 
-template <int DK, int DV, int OUT_DT, int W>
-__device__ __forceinline__ void full_chain(const StateArgs& a, FullSmem<DK, DV>& sm, int seq, int h) {
+template <int DK, int DV, int VT, int CW, int OUT_DT, int W>
+__device__ __forceinline__ void wide_chain(const StateArgs& a, WideSmem<DK, VT>& sm, int seq, int h, int split) {
   typedef ColLayout<DK> LY;
-  typedef FullLayout<DK, DV> FL;
+  typedef WideLayout<DK, VT> WL;
   constexpr int NJ = DK / 32;
   constexpr int NT = DK / 16;
-  constexpr int NVT = DV / 16;                  // value tiles of the chain
-  constexpr int NC = NVT / kFullCompute;        // value tiles of this wave
+  constexpr int NC = VT / CW;                   // value tiles of this wave
   const Geom& G = a.geom;
   const int H = G.H;
   const int l = threadIdx.x & 63, r = l & 15, gq = l >> 4;
-  const int tile0 = W * NC;
+  const int tile0 = W * NC;                     // first value tile of this wave inside the workgroup
+  const int col0 = 16 * (split * VT + tile0);   // its first value column in the chain
   const ChainRef c = chain_ref(G, seq);
   const int nchunks = c.nchunks;
 
@@ -1532,7 +1532,7 @@ __device__ __forceinline__ void full_chain(const StateArgs& a, FullSmem<DK, DV>&
 #pragma unroll
       for (int i = 0; i < 4; ++i)
         S[cc][dt][i] = (a.h0 != nullptr)
-                           ? a.h0[sbase + static_cast<int64_t>(16 * dt + 4 * gq + i) * DV + 16 * (tile0 + cc) + r]
+                           ? a.h0[sbase + static_cast<int64_t>(16 * dt + 4 * gq + i) * DV + col0 + 16 * cc + r]
                            : 0.f;
 
   if (nchunks > 0) lds_barrier();  // chunk 0 staged by the producer waves
@@ -1561,7 +1561,7 @@ __device__ __forceinline__ void full_chain(const StateArgs& a, FullSmem<DK, DV>&
         p = cur + (LY::OFF_A + (i - I_AQ)) * 1024 + l * 16;
       } else {
         constexpr int dt = (i - I_LK) / 3, k3 = (i - I_LK) % 3;
-        if constexpr (k3 == 0) p = cur + FL::OFF_G + (16 * dt + 4 * gq) * 4;
+        if constexpr (k3 == 0) p = cur + WL::OFF_G + (16 * dt + 4 * gq) * 4;
         else p = cur + (LY::OFF_L + 2 * dt + (k3 - 1)) * 1024 + l * 16;
       }
       return *reinterpret_cast<const uint4*>(p);
@@ -1573,7 +1573,7 @@ __device__ __forceinline__ void full_chain(const StateArgs& a, FullSmem<DK, DV>&
     for (int cc = 0; cc < NC; ++cc)
 #pragma unroll
       for (int ct = 0; ct < 4; ++ct)
-        Ucur[cc][ct] = *reinterpret_cast<const h4*>(cur + FL::OFF_U + (ct * NVT + tile0 + cc) * 512 + l * 8);
+        Ucur[cc][ct] = *reinterpret_cast<const h4*>(cur + WL::OFF_U + (ct * VT + tile0 + cc) * 512 + l * 8);
     // S as B fragments over channels
     h8 Sb[NC][NJ];
 #pragma unroll
@@ -1663,7 +1663,7 @@ __device__ __forceinline__ void full_chain(const StateArgs& a, FullSmem<DK, DV>&
         for (int i = 0; i < 4; ++i) {
           const int row = 16 * ct + 4 * gq + i;
           if (row < len) {
-            const int64_t oi = ((row0 + row) * H + h) * static_cast<int64_t>(DV) + 16 * (tile0 + cc) + r;
+            const int64_t oi = ((row0 + row) * H + h) * static_cast<int64_t>(DV) + col0 + 16 * cc + r;
             if constexpr (OUT_DT == 0) static_cast<float*>(a.o)[oi] = O[cc][ct][i];
             else static_cast<u16*>(a.o)[oi] = f32_to_bf16_bits(O[cc][ct][i]);
           }
@@ -1680,30 +1680,40 @@ __device__ __forceinline__ void full_chain(const StateArgs& a, FullSmem<DK, DV>&
       for (int dt = 0; dt < NT; ++dt)
 #pragma unroll
         for (int i = 0; i < 4; ++i)
-          a.ht[sbase + static_cast<int64_t>(16 * dt + 4 * gq + i) * DV + 16 * (tile0 + cc) + r] = S[cc][dt][i];
+          a.ht[sbase + static_cast<int64_t>(16 * dt + 4 * gq + i) * DV + col0 + 16 * cc + r] = S[cc][dt][i];
   }
 }
 
-template <int DK, int DV, int OUT_DT>
-__global__ __launch_bounds__(64 * (kFullCompute + kFullProducers), 1)
-void kda_state_full_kernel(StateArgs a) {
-  __shared__ FullSmem<DK, DV> sm;
+template <int DK, int DV, int VT, int CW, int OUT_DT>
+__global__ __launch_bounds__(64 * (CW + kWideProducers), 1)
+void kda_state_wide_kernel(StateArgs a) {
+  constexpr int SPL = DV / 16 / VT;   // workgroups per chain
+  __shared__ WideSmem<DK, VT> sm;
   const Geom& G = a.geom;
   const int H = G.H;
-  const int chain = blockIdx.x;
+  // XCD-aware mapping: the SPL workgroups of one chain share an XCD (and L2)
+  const int x = blockIdx.x;
+  const int xcd = x & 7;
+  const int kk = x >> 3;
+  const int slot = kk / SPL;
+  const int split = kk - slot * SPL;
+  const int chain = slot * 8 + xcd;
   if (chain >= G.N * H) return;
   const int seq_rank = chain / H;
   const int h = chain - seq_rank * H;
   const int seq = (G.order != nullptr) ? G.order[seq_rank] : seq_rank;
-  switch (threadIdx.x >> 6) {
-    case 0: full_chain<DK, DV, OUT_DT, 0>(a, sm, seq, h); break;
-    case 1: full_chain<DK, DV, OUT_DT, 1>(a, sm, seq, h); break;
-    case 2: full_chain<DK, DV, OUT_DT, 2>(a, sm, seq, h); break;
-    case 3: full_chain<DK, DV, OUT_DT, 3>(a, sm, seq, h); break;
-    case 4: full_producer<DK, DV, 0>(a, sm, seq, h); break;
-    case 5: full_producer<DK, DV, 1>(a, sm, seq, h); break;
-    case 6: full_producer<DK, DV, 2>(a, sm, seq, h); break;
-    default: full_producer<DK, DV, 3>(a, sm, seq, h); break;
+  const int wave = threadIdx.x >> 6;
+  if (wave < CW) {
+    static_for<0, CW>([&](auto wc) {
+      if (wave == decltype(wc)::value) wide_chain<DK, DV, VT, CW, OUT_DT, decltype(wc)::value>(a, sm, seq, h, split);
+    });
+  } else {
+    switch (wave - CW) {
+      case 0: wide_producer<DK, DV, VT, 0>(a, sm, seq, h, split); break;
+      case 1: wide_producer<DK, DV, VT, 1>(a, sm, seq, h, split); break;
+      case 2: wide_producer<DK, DV, VT, 2>(a, sm, seq, h, split); break;
+      default: wide_producer<DK, DV, VT, 3>(a, sm, seq, h, split); break;
+    }
   }
 }
 
@@ -1716,19 +1726,28 @@ static hipError_t launch_intra_t(const IntraArgs& a, int grid, hipStream_t s) {
   return hipGetLastError();
 }
 
-// The whole-chain state kernel runs a chunk step in ~2.3 us against ~1.4 us
-// for the 32-column slices, but with four times the work per CU: it pays
-// when there are enough chains to fill the CUs (one workgroup per CU), and
-// the slices pay when the serial chain is the critical path.
+// The whole-chain state kernel (VT = 8) runs a chunk step in ~2.3 us against
+// ~1.4 us for the 32-column slices, with four times the work per CU: it pays
+// when there are enough chains to fill the CUs (config 3, 1 024 chains:
+// 4 575 -> 4 025 us per call), and the 32-column slices pay when the serial
+// chain is the critical path.  64-column slices (VT = 4, two compute waves of
+// two value tiles) lost at every measured shape (config 1 229 -> 277 us,
+// config 2 1 569 -> 2 465 us), so calls with fewer chains keep the 32-column
+// slices.
 constexpr int kFullStateMinChains = 256;
+constexpr int kHalfStateMinChains = 1 << 30;   // 64-column slices: never chosen (see above)
 template <int DK, int DV, bool EXACT, int OUT>
 static hipError_t launch_state_t(const StateArgs& a, int grid, hipStream_t s) {
   if constexpr (EXACT) {
     hipLaunchKernelGGL((kda_state_kernel<DK, DV, EXACT, OUT>), dim3(grid), dim3(256), 0, s, a);
   } else {
-    if (DK == 128 && a.geom.N * a.geom.H >= kFullStateMinChains) {
-      hipLaunchKernelGGL((kda_state_full_kernel<DK, DV, OUT>), dim3(a.geom.N * a.geom.H),
-                         dim3(64 * (kFullCompute + kFullProducers)), 0, s, a);
+    const int64_t chains = static_cast<int64_t>(a.geom.N) * a.geom.H;
+    if (DK == 128 && chains >= kFullStateMinChains) {
+      hipLaunchKernelGGL((kda_state_wide_kernel<DK, DV, DV / 16, 4, OUT>), dim3(((chains + 7) / 8) * 8),
+                         dim3(64 * (4 + kWideProducers)), 0, s, a);
+    } else if (DK == 128 && kHalfStateMinChains <= chains) {
+      hipLaunchKernelGGL((kda_state_wide_kernel<DK, DV, 4, 2, OUT>), dim3(((chains + 7) / 8) * 8 * (DV / 64)),
+                         dim3(64 * (2 + kWideProducers)), 0, s, a);
     } else {
       hipLaunchKernelGGL((kda_state_col_kernel<DK, DV, OUT>), dim3(grid), dim3(64 * (kColComputeWaves + kColProducers)), 0,
                          s, a);
