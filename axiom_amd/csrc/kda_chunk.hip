@@ -1735,7 +1735,6 @@ static hipError_t launch_intra_t(const IntraArgs& a, int grid, hipStream_t s) {
 // config 2 1 569 -> 2 465 us), so calls with fewer chains keep the 32-column
 // slices.
 constexpr int kFullStateMinChains = 256;
-constexpr int kHalfStateMinChains = 1 << 30;   // 64-column slices: never chosen (see above)
 template <int DK, int DV, bool EXACT, int OUT>
 static hipError_t launch_state_t(const StateArgs& a, int grid, hipStream_t s) {
   if constexpr (EXACT) {
@@ -1745,9 +1744,6 @@ static hipError_t launch_state_t(const StateArgs& a, int grid, hipStream_t s) {
     if (DK == 128 && chains >= kFullStateMinChains) {
       hipLaunchKernelGGL((kda_state_wide_kernel<DK, DV, DV / 16, 4, OUT>), dim3(((chains + 7) / 8) * 8),
                          dim3(64 * (4 + kWideProducers)), 0, s, a);
-    } else if (DK == 128 && kHalfStateMinChains <= chains) {
-      hipLaunchKernelGGL((kda_state_wide_kernel<DK, DV, 4, 2, OUT>), dim3(((chains + 7) / 8) * 8 * (DV / 64)),
-                         dim3(64 * (2 + kWideProducers)), 0, s, a);
     } else {
       hipLaunchKernelGGL((kda_state_col_kernel<DK, DV, OUT>), dim3(grid), dim3(64 * (kColComputeWaves + kColProducers)), 0,
                          s, a);
