@@ -25,6 +25,8 @@ KDA_DTYPE_BF16 = 1
 KDA_DTYPE_F16 = 2
 KDA_DTYPE_BF16_F32GATES = 3
 
+KDA_STATUS_NONFINITE = 65536
+
 _vp = ctypes.c_void_p
 _i = ctypes.c_int
 _i32 = ctypes.c_int32
@@ -39,6 +41,8 @@ _SIGNATURES = {
                                    _i, _i, _i, _i, _i, _i, _f, _i, _i]),
     "kda_varlen_status": (_i, [_vp, _vp, _sz, _i, _i, _i, _i, _i, _i, _i32, _i,
                                ctypes.POINTER(_i32)]),
+    "kda_chunk_fwd_status": (_i, [_vp, _vp, _sz, _i, _i, _i, _i, _i, _i, _i32, _i,
+                                  ctypes.POINTER(_i32)]),
     "kda_recurrent_step": (_i, [_vp, _vp, _vp, _vp, _vp, _vp, _vp, _vp,
                                 _i, _i, _i, _i, _f, _i, _i]),
     "kda_cc_scan": (_i, [_vp, _vp, _vp, _vp, _vp, _vp, _vp, _vp, _vp,

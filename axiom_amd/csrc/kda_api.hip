@@ -37,6 +37,7 @@ struct WsLayout {
   size_t W, U, AQ, GQ, LK, GC;
   size_t cu_clamped, chunk_off, n_units, order, flags;
   size_t state;          // carried state between segments (segmented dense calls)
+  size_t status;         // int32 status word of the call (kda::kStatusNonFinite)
   size_t total;
   int64_t units_bound;   // workspace chunk units (per segment when segmented)
   int segments;          // dense: launches along T (1 = whole sequence at once)
@@ -115,6 +116,7 @@ WsLayout ws_layout(int B, int T, int H, int dk, int dv, int32_t n_seqs, int in_d
     L.flags = take(4);
   }
   if (L.segments > 1) L.state = take(static_cast<size_t>(B) * H * dk * dv * 4);
+  L.status = take(4);
   L.total = off;
   return L;
 }
@@ -211,10 +213,16 @@ int chunk_fwd_impl(hipStream_t stream, const void* q, const void* k, const void*
     ia.K = pro->K;
   }
 
+  // the call's status word: zeroed by the first intra launch, set by the
+  // 16-bit state kernels on a non-finite o or final state value
+  int* const status = at<int>(ws, L.status);
+  ia.status_clear = status;
+
   kda::StateArgs sa{};
   sa.geom = G;
   sa.W = ia.W; sa.U = ia.U; sa.AQ = ia.AQ; sa.GQ = ia.GQ; sa.LK = ia.LK; sa.GC = ia.GC;
   sa.o = o;
+  sa.status = exact ? nullptr : status;
   const int splits = dv / 32;
   const int64_t chains = static_cast<int64_t>(G.N) * H;
   const int64_t state_grid = ((chains + 7) / 8) * 8 * splits;
@@ -236,12 +244,18 @@ int chunk_fwd_impl(hipStream_t stream, const void* q, const void* k, const void*
       hipError_t e = (pro != nullptr) ? kda::launch_intra_prologue(ia, dk, dtg, static_cast<int>(intra_grid), stream)
                                       : kda::launch_intra(ia, dk, dtq, dtg, static_cast<int>(intra_grid), stream);
       if (e != hipSuccess) return hip_fail(e, "intra kernel launch");
+      ia.status_clear = nullptr;
     }
     sa.h0 = (sgi == 0) ? h0 : carry;
     sa.ht = (L.segments > 1) ? carry : ht;
     hipError_t e = kda::launch_state(sa, dk, exact, out_dtype == KDA_DTYPE_BF16 ? 1 : 0,
                                      static_cast<int>(state_grid), stream);
     if (e != hipSuccess) return hip_fail(e, "state kernel launch");
+  }
+  if (ia.status_clear != nullptr) {
+    // no intra launch ran (T == 0): clear the status word by a kernel
+    hipError_t e = kda::launch_copy_or_zero(reinterpret_cast<float*>(status), nullptr, 1, stream);
+    if (e != hipSuccess) return hip_fail(e, "status clear launch");
   }
   return KDA_OK;
 }
@@ -431,6 +445,34 @@ int kda_chunk_fwd_noalloc(hipStream_t stream, const void* q, const void* k, cons
   if (int rc = scratch_for_stream(stream, &ws)) return rc;
   return chunk_fwd_impl(stream, q, k, v, g, beta, h0, cu_seqlens, n_seqs, o, ht, B, T, H, dk, dv,
                         chunk, scale, in_dtype, out_dtype, ws, kScratchBytes);
+}
+
+int kda_chunk_fwd_status(hipStream_t stream, const void* workspace, size_t workspace_bytes,
+                         int B, int T, int H, int dk, int dv, int chunk, int32_t n_seqs,
+                         int in_dtype, int32_t* flags_out) {
+  g_err[0] = '\0';
+  if (!flags_out) return fail(KDA_ERR_INVALID_ARGUMENT, "null pointer");
+  const size_t need = kda_chunk_fwd_workspace(B, T, H, dk, dv, chunk, n_seqs, in_dtype);
+  if (need == 0) return fail(KDA_ERR_INVALID_ARGUMENT, "invalid call arguments");
+  const void* ws = workspace;
+  if (ws == nullptr) {
+    // the call ran through kda_chunk_fwd_noalloc: its workspace is this device's scratch
+    void* p = nullptr;
+    if (int rc = scratch_for_stream(stream, &p)) return rc;
+    ws = p;
+    workspace_bytes = kScratchBytes;
+  }
+  if (workspace_bytes < need) return fail(KDA_ERR_WORKSPACE, "workspace does not match");
+  const WsLayout L = ws_layout(B, T, H, dk, dv, n_seqs > 0 ? n_seqs : 0, in_dtype);
+  int32_t words[2] = {0, 0};
+  hipError_t e = hipMemcpyAsync(&words[0], static_cast<const char*>(ws) + L.status, 4, hipMemcpyDeviceToHost, stream);
+  if (e == hipSuccess && n_seqs > 0)
+    e = hipMemcpyAsync(&words[1], static_cast<const char*>(ws) + L.flags, 4, hipMemcpyDeviceToHost, stream);
+  if (e != hipSuccess) return hip_fail(e, "status copy");
+  e = hipStreamSynchronize(stream);
+  if (e != hipSuccess) return hip_fail(e, "stream synchronize");
+  *flags_out = words[0] | words[1];
+  return KDA_OK;
 }
 
 int kda_varlen_status(hipStream_t stream, const void* workspace, size_t workspace_bytes,

@@ -45,6 +45,19 @@ namespace kda {
 constexpr int kC = 64;
 
 // ----------------------------------------------------------------------------
+// non-finite detection of the results (fp16 operand range)
+// ----------------------------------------------------------------------------
+__device__ __forceinline__ bool f32_bits_nonfinite(uint32_t w) { return (w & 0x7F800000u) == 0x7F800000u; }
+__device__ __forceinline__ bool bf16x2_bits_nonfinite(uint32_t w) {
+  return (w & 0x7F80u) == 0x7F80u || (w & 0x7F800000u) == 0x7F800000u;
+}
+// sets the call's status bit from one lane when any lane of the wave saw a
+// non-finite result
+__device__ __forceinline__ void report_nonfinite(int* status, bool bad) {
+  if (status != nullptr && __any(bad) && (threadIdx.x & 63) == 0) atomicOr(status, kStatusNonFinite);
+}
+
+// ----------------------------------------------------------------------------
 // chunk-unit geometry
 // ----------------------------------------------------------------------------
 struct UnitRef {
@@ -787,6 +800,7 @@ void kda_intra_kernel(IntraArgs a) {
   __shared__ __attribute__((aligned(16))) unsigned char lds[IntraLds<DK, DV, EXACT, PRO>::kBytes];
   IntraSmem<DK, DV, EXACT>& sm = *reinterpret_cast<IntraSmem<DK, DV, EXACT>*>(lds);
   const int H = a.geom.H;
+  if (a.status_clear != nullptr && blockIdx.x == 0 && threadIdx.x == 0) *a.status_clear = 0;
   const int u = blockIdx.x / H;
   const int h = blockIdx.x - u * H;
   if (a.geom.cu != nullptr && u >= *a.geom.n_units) return;  // uniform per workgroup
@@ -1138,7 +1152,7 @@ __device__ __forceinline__ void col_stage(const StateArgs& a, int64_t ch, int sp
 // per lane, rows past the chunk's end skipped.
 template <int DV, int OUT_DT, int P>
 __device__ __forceinline__ void col_store_rows(const StateArgs& a, const unsigned char* ob, int64_t row0,
-                                               int len, int h, int split, int l) {
+                                               int len, int h, int split, int l, bool& bad) {
   constexpr int ES = (OUT_DT == 0) ? 4 : 2;
   constexpr int LPR = 32 * ES / 16;            // lanes per row
   constexpr int RPI = 64 / LPR;                // rows per instruction
@@ -1150,6 +1164,11 @@ __device__ __forceinline__ void col_store_rows(const StateArgs& a, const unsigne
     const int cb = (l % LPR) * 16;             // byte offset inside the 32-column row
     const uint4 v = *reinterpret_cast<const uint4*>(ob + row * (32 * ES) + cb);
     if (row < len) {
+      if constexpr (OUT_DT == 0)
+        bad |= f32_bits_nonfinite(v.x) | f32_bits_nonfinite(v.y) | f32_bits_nonfinite(v.z) | f32_bits_nonfinite(v.w);
+      else
+        bad |= bf16x2_bits_nonfinite(v.x) | bf16x2_bits_nonfinite(v.y) | bf16x2_bits_nonfinite(v.z) |
+               bf16x2_bits_nonfinite(v.w);
       unsigned char* dst = static_cast<unsigned char*>(a.o) +
                            (((row0 + row) * H + h) * static_cast<int64_t>(DV) + 32 * split) * ES + cb;
       *reinterpret_cast<uint4*>(dst) = v;
@@ -1191,13 +1210,14 @@ __device__ __forceinline__ void col_producer(const StateArgs& a, ColSmem<DK>& sm
   const int H = a.geom.H;
   const int l = threadIdx.x & 63;
   if (c.nchunks <= 0) return;
+  bool bad = false;
   col_stage<DK, DV, P>(a, static_cast<int64_t>(c.u0) * H + h, split, sm.buf[0], l);
   wait_vmem_all();
   lds_barrier();
   for (int n = 0; n < c.nchunks; ++n) {
     if (n > 0)
       col_store_rows<DV, OUT_DT, P>(a, sm.obuf[(n - 1) & 1], c.tok0 + static_cast<int64_t>(n - 1) * kC,
-                                    min(kC, c.seq_len - (n - 1) * kC), h, split, l);
+                                    min(kC, c.seq_len - (n - 1) * kC), h, split, l, bad);
     if (n + 1 < c.nchunks)
       col_stage<DK, DV, P>(a, static_cast<int64_t>(c.u0 + n + 1) * H + h, split, sm.buf[(n + 1) & 1], l);
     wait_vmem_all();
@@ -1205,7 +1225,8 @@ __device__ __forceinline__ void col_producer(const StateArgs& a, ColSmem<DK>& sm
   }
   const int nl = c.nchunks - 1;
   col_store_rows<DV, OUT_DT, P>(a, sm.obuf[nl & 1], c.tok0 + static_cast<int64_t>(nl) * kC,
-                                min(kC, c.seq_len - nl * kC), h, split, l);
+                                min(kC, c.seq_len - nl * kC), h, split, l, bad);
+  report_nonfinite(a.status, bad);
 }
 
 // Calls f(std::integral_constant<int, I>{}) for I = B .. E-1, expanded at
@@ -1380,14 +1401,18 @@ __device__ __forceinline__ void col_chain(const StateArgs& a, ColSmem<DK>& sm, i
   }
 
   if (a.ht != nullptr) {
+    bool bad = false;
 #pragma unroll
     for (int cc = 0; cc < NC; ++cc)
 #pragma unroll
       for (int dt = 0; dt < NT; ++dt)
 #pragma unroll
-        for (int i = 0; i < 4; ++i)
+        for (int i = 0; i < 4; ++i) {
+          bad |= f32_bits_nonfinite(__float_as_uint(S[cc][dt][i]));
           a.ht[sbase + static_cast<int64_t>(16 * dt + 4 * gq + i) * DV + 16 * (2 * split + tile0 + cc) + r] =
               S[cc][dt][i];
+        }
+    report_nonfinite(a.status, bad);
   }
 }
 
@@ -1535,6 +1560,7 @@ __device__ __forceinline__ void wide_chain(const StateArgs& a, WideSmem<DK, VT>&
                            ? a.h0[sbase + static_cast<int64_t>(16 * dt + 4 * gq + i) * DV + col0 + 16 * cc + r]
                            : 0.f;
 
+  bool bad = false;
   if (nchunks > 0) lds_barrier();  // chunk 0 staged by the producer waves
   for (int n = 0; n < nchunks; ++n) {
     const unsigned char* cur = sm.buf[n & 1];
@@ -1664,6 +1690,7 @@ __device__ __forceinline__ void wide_chain(const StateArgs& a, WideSmem<DK, VT>&
           const int row = 16 * ct + 4 * gq + i;
           if (row < len) {
             const int64_t oi = ((row0 + row) * H + h) * static_cast<int64_t>(DV) + col0 + 16 * cc + r;
+            bad |= f32_bits_nonfinite(__float_as_uint(O[cc][ct][i]));
             if constexpr (OUT_DT == 0) static_cast<float*>(a.o)[oi] = O[cc][ct][i];
             else static_cast<u16*>(a.o)[oi] = f32_to_bf16_bits(O[cc][ct][i]);
           }
@@ -1679,9 +1706,12 @@ __device__ __forceinline__ void wide_chain(const StateArgs& a, WideSmem<DK, VT>&
 #pragma unroll
       for (int dt = 0; dt < NT; ++dt)
 #pragma unroll
-        for (int i = 0; i < 4; ++i)
+        for (int i = 0; i < 4; ++i) {
+          bad |= f32_bits_nonfinite(__float_as_uint(S[cc][dt][i]));
           a.ht[sbase + static_cast<int64_t>(16 * dt + 4 * gq + i) * DV + col0 + 16 * cc + r] = S[cc][dt][i];
+        }
   }
+  report_nonfinite(a.status, bad);
 }
 
 template <int DK, int DV, int VT, int CW, int OUT_DT>

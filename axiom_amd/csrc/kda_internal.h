@@ -42,6 +42,7 @@ struct IntraArgs {
   const float* cw[3];
   const float* cb[3];
   int K;
+  int* status_clear;   // non-null: the launch zeroes the call's status word
 };
 
 struct StateArgs {
@@ -55,7 +56,14 @@ struct StateArgs {
   const float* h0;
   void* o;
   float* ht;
+  // non-null (16-bit inputs): bit kStatusNonFinite is set when an o or final
+  // state value of the call is not finite
+  int* status;
 };
+
+// status word of a chunked forward call: a non-finite o or final state value
+// (an fp16 operand out of range, or non-finite inputs)
+constexpr int kStatusNonFinite = 1 << 16;
 
 struct DecodeArgs {
   const void* q;

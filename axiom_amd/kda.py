@@ -77,7 +77,8 @@ def chunk_fwd_workspace_bytes(B, T, H, dk, dv, n_seqs=0, in_code=_lib.KDA_DTYPE_
 
 def kda_chunk_fwd(q, k, v, g, beta, initial_state=None, cu_seqlens=None, chunk_size: int = 64,
                   scale: float = 1.0, output_final_state: bool = True,
-                  out_dtype=torch.float32, workspace=None, out=None, final_state=None):
+                  out_dtype=torch.float32, workspace=None, out=None, final_state=None,
+                  check_finite: bool = False):
     """Chunked KDA forward; returns ``(o, final_state)`` (``final_state`` None if not requested).
 
     ``q, k, g [B,T,H,dk]``, ``v [B,T,H,dv]``, ``beta [B,T,H]``; q/k/v share one
@@ -86,6 +87,10 @@ def kda_chunk_fwd(q, k, v, g, beta, initial_state=None, cu_seqlens=None, chunk_s
     ``cu_seqlens`` int32 ``[N+1]`` on the device (requires B == 1).  fp32
     inputs select the exact (fp32 MFMA) kernels.  ``out`` / ``final_state``:
     optional preallocated outputs (contiguous, the shapes and dtypes returned).
+    16-bit inputs run on fp16 matrix-core operands: unit-norm q and k rows
+    and |v|, the state and the intermediate U below 2^15 are supported; with
+    ``check_finite`` the call synchronises and raises ``ValueError`` when a
+    result is not finite (an operand left that range; ``kda_chunk_fwd_status``).
     """
     what = "kda_chunk_fwd"
     if q.dim() != 4 or k.shape != q.shape or g.shape != q.shape:
@@ -154,6 +159,14 @@ def kda_chunk_fwd(q, k, v, g, beta, initial_state=None, cu_seqlens=None, chunk_s
                          B, T, H, dk, dv, CHUNK, float(scale), in_code, _OUT_CODES[out_dtype],
                          _ptr(workspace), ws_bytes)
     _lib.check(rc, what)
+    if check_finite:
+        flags = ctypes.c_int32(0)
+        rc = L.kda_chunk_fwd_status(_stream(dev), _ptr(workspace), ws_bytes, B, T, H, dk, dv, CHUNK,
+                                    n_seqs, in_code, ctypes.byref(flags))
+        _lib.check(rc, "kda_chunk_fwd_status")
+        if flags.value & _lib.KDA_STATUS_NONFINITE:
+            raise ValueError(f"{what}: non-finite result: an fp16 operand left its range (16-bit inputs "
+                             "need unit-norm q, k and |v|, |U|, |state| < 2^15; fp32 inputs run exact)")
     return o, ht
 
 

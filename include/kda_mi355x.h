@@ -78,6 +78,14 @@ typedef enum kda_dtype_t {
  * cu_seqlens values are clamped on the device into a non-decreasing sequence
  * inside [0, T] so no access can leave the tensors; kda_varlen_status reports
  * whether a repair was needed.
+ * Operand range of 16-bit inputs (BF16, F16, BF16_F32GATES): the matrix-core
+ * operands are fp16 (range +-65504).  Supported: q and k rows of unit L2
+ * norm as the reference's layer produces them (net/kda.py:200-201), |q scale|
+ * and |k| below 2^15 per element, and |v|, U = (I + L)^-1 (beta v), the
+ * state (h0 and its evolution) and v~ = U - W S below 2^15 in magnitude.
+ * Outside this range a result is not finite; the state kernels detect it and
+ * kda_chunk_fwd_status reports KDA_STATUS_NONFINITE.  fp32 inputs (exact
+ * mode) have fp32 range.
  */
 KDA_API int kda_chunk_fwd(hipStream_t stream,
                   const void* q, const void* k, const void* v,
@@ -114,6 +122,20 @@ KDA_API int kda_chunk_fwd_noalloc(hipStream_t stream,
  * n_seqs <= 0 means dense (no cu_seqlens).  Host-only; no HIP call. */
 KDA_API size_t kda_chunk_fwd_workspace(int B, int T, int H, int dk, int dv, int chunk,
                                int32_t n_seqs, int in_dtype);
+
+/*
+ * Status of the last kda_chunk_fwd (or kda_chunk_fwd_noalloc: pass
+ * workspace = NULL) on `stream` with these arguments, copied to *flags_out
+ * (synchronising the stream).  Bits: 1, 2, 4, 8 as kda_varlen_status (varlen
+ * calls); 65536 (KDA_STATUS_NONFINITE) an o or final state value of a 16-bit
+ * input call is not finite: an fp16 operand left its range (see the
+ * precondition of kda_chunk_fwd) or the inputs were not finite.  No
+ * counterpart in the reference, whose bf16 operands have fp32 range.
+ */
+#define KDA_STATUS_NONFINITE 65536
+KDA_API int kda_chunk_fwd_status(hipStream_t stream, const void* workspace, size_t workspace_bytes,
+                         int B, int T, int H, int dk, int dv, int chunk, int32_t n_seqs,
+                         int in_dtype, int32_t* flags_out);
 
 /*
  * After a varlen kda_chunk_fwd on `stream`, copy the device-side validation

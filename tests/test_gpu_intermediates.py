@@ -34,7 +34,8 @@ def ws_offsets(B, T, H, dk, dv, es):
     ch = units * H
     off, res = 0, {}
     for name, nbytes in (("W", ch * C * dk * es), ("GQ", ch * C * dk * es), ("LK", ch * C * dk * es),
-                         ("U", ch * C * dv * es), ("AQ", ch * C * C * es), ("GC", ch * dk * 4)):
+                         ("U", ch * C * dv * es), ("AQ", ch * C * C * es), ("GC", ch * dk * 4),
+                         ("status", 4)):
         res[name] = off
         off = _align(off + nbytes)
     res["total"] = off
