@@ -50,6 +50,11 @@ _SIGNATURES = {
     "kda_cc_scan_workspace": (_sz, [_i, _i, _i, _i, _i]),
     "kda_cc_scan_bwd": (_i, [_vp] * 15 + [_i, _i, _i, _i, _i, _i, _vp, _sz]),
     "kda_cc_scan_bwd_workspace": (_sz, [_i, _i, _i, _i, _i]),
+    "kda_cc_scan_batched": (_i, [_vp, _vp, _vp, _vp, _vp, _vp, _vp, _vp, _vp,
+                                 _i, _i, _i, _i, _i, _i, _i, _vp, _sz]),
+    "kda_cc_scan_batched_workspace": (_sz, [_i, _i, _i, _i, _i, _i]),
+    "kda_cc_scan_bwd_batched": (_i, [_vp] * 15 + [_i, _i, _i, _i, _i, _i, _i, _vp, _sz]),
+    "kda_cc_scan_bwd_batched_workspace": (_sz, [_i, _i, _i, _i, _i, _i]),
     "kda_chunk_bwd": (_i, [_vp, _vp, _vp, _vp, _vp, _vp, _vp, _vp, _vp,
                            _vp, _vp, _vp, _vp, _vp, _vp,
                            _i, _i, _i, _i, _i, _i, _f, _i, _i, _vp, _sz]),

@@ -516,20 +516,25 @@ int kda_recurrent_step(hipStream_t stream, const void* q, const void* k, const v
   return KDA_OK;
 }
 
-size_t kda_cc_scan_workspace(int T, int H, int dk, int dv, int chunk) {
-  if (T < 0 || H < 1 || !dim_ok(dk) || dk != dv || chunk < 1) return 0;
-  const size_t adapt = align_up(static_cast<size_t>(T) * H * dk * 4) +
-                       align_up(static_cast<size_t>(T) * H * 4);
-  return adapt + ws_layout(1, T, H, dk, dv, 0, KDA_DTYPE_BF16_F32GATES).total;
+size_t kda_cc_scan_batched_workspace(int B, int T, int H, int dk, int dv, int chunk) {
+  if (B < 1 || T < 0 || H < 1 || !dim_ok(dk) || dk != dv || chunk < 1) return 0;
+  const size_t th = static_cast<size_t>(B) * T * H;
+  const size_t adapt = align_up(th * dk * 4) + align_up(th * 4);
+  return adapt + ws_layout(B, T, H, dk, dv, 0, KDA_DTYPE_BF16_F32GATES).total;
 }
 
-int kda_cc_scan(hipStream_t stream, const void* q, const void* k, const void* v,
-                const float* alpha, const float* beta32, const float* S_in,
-                float* o, float* S_out, int T, int H, int dk, int dv, int tile, int chunk,
-                void* workspace, size_t workspace_bytes) {
+size_t kda_cc_scan_workspace(int T, int H, int dk, int dv, int chunk) {
+  return kda_cc_scan_batched_workspace(1, T, H, dk, dv, chunk);
+}
+
+int kda_cc_scan_batched(hipStream_t stream, const void* q, const void* k, const void* v,
+                        const float* alpha, const float* beta32, const float* S_in,
+                        float* o, float* S_out, int B, int T, int H, int dk, int dv, int tile, int chunk,
+                        void* workspace, size_t workspace_bytes) {
   g_err[0] = '\0';
   if (!q || !k || !v || !alpha || !beta32 || !S_in || !o || !S_out)
     return fail(KDA_ERR_INVALID_ARGUMENT, "null pointer");
+  if (B < 1) return fail(KDA_ERR_INVALID_ARGUMENT, "B=%d must be >= 1", B);
   if (T < 0) return fail(KDA_ERR_INVALID_ARGUMENT, "T=%d must be >= 0", T);
   if (chunk < 1) return fail(KDA_ERR_INVALID_ARGUMENT, "chunk=%d must be >= 1", chunk);
   if (T % chunk)
@@ -537,23 +542,33 @@ int kda_cc_scan(hipStream_t stream, const void* q, const void* k, const void* v,
   if (tile < 1 || tile > 16)
     return fail(KDA_ERR_INVALID_ARGUMENT, "tile=%d outside [1, 16] (the _cc_tile bound)", tile);
   if (int rc = check_dims(H, dk, dv)) return rc;
-  const size_t need = kda_cc_scan_workspace(T, H, dk, dv, chunk);
+  const size_t need = kda_cc_scan_batched_workspace(B, T, H, dk, dv, chunk);
   if (workspace == nullptr || workspace_bytes < need)
     return fail(KDA_ERR_WORKSPACE, "workspace of %zu bytes is too small (need %zu)", workspace_bytes, need);
-  const size_t g_bytes = align_up(static_cast<size_t>(T) * H * dk * 4);
-  const size_t b_bytes = align_up(static_cast<size_t>(T) * H * 4);
+  const size_t th = static_cast<size_t>(B) * T * H;
+  const size_t g_bytes = align_up(th * dk * 4);
+  const size_t b_bytes = align_up(th * 4);
   float* g32 = reinterpret_cast<float*>(workspace);
   float* b32 = reinterpret_cast<float*>(static_cast<char*>(workspace) + g_bytes);
   kda::AdaptArgs aa{};
   aa.alpha = alpha; aa.beta32 = beta32; aa.g_out = g32; aa.beta_out = b32;
-  aa.n_tok_heads = static_cast<int64_t>(T) * H;
+  aa.n_tok_heads = static_cast<int64_t>(th);
   aa.dk = dk;
   hipError_t e = kda::launch_adapt(aa, stream);
   if (e != hipSuccess) return hip_fail(e, "cc_scan adapter launch");
+  // the (B, T, H*d) operands are the [B, T, H, d] layout of the chunked forward
   void* rest = static_cast<char*>(workspace) + g_bytes + b_bytes;
-  return chunk_fwd_impl(stream, q, k, v, g32, b32, S_in, nullptr, 0, o, S_out, 1, T, H, dk, dv,
+  return chunk_fwd_impl(stream, q, k, v, g32, b32, S_in, nullptr, 0, o, S_out, B, T, H, dk, dv,
                         kC, 1.0f, KDA_DTYPE_BF16_F32GATES, KDA_DTYPE_F32, rest,
                         workspace_bytes - g_bytes - b_bytes);
+}
+
+int kda_cc_scan(hipStream_t stream, const void* q, const void* k, const void* v,
+                const float* alpha, const float* beta32, const float* S_in,
+                float* o, float* S_out, int T, int H, int dk, int dv, int tile, int chunk,
+                void* workspace, size_t workspace_bytes) {
+  return kda_cc_scan_batched(stream, q, k, v, alpha, beta32, S_in, o, S_out, 1, T, H, dk, dv, tile, chunk,
+                             workspace, workspace_bytes);
 }
 
 size_t kda_chunk_bwd_workspace(int B, int T, int H, int dk, int dv, int chunk) {
@@ -621,21 +636,26 @@ int kda_chunk_bwd(hipStream_t stream, const void* q, const void* k, const void* 
 }
 
 
-size_t kda_cc_scan_bwd_workspace(int T, int H, int dk, int dv, int chunk) {
-  if (T < 0 || H < 1 || !dim_ok(dk) || dk != dv || chunk < 1) return 0;
-  const size_t th = static_cast<size_t>(T) * H;
+size_t kda_cc_scan_bwd_batched_workspace(int B, int T, int H, int dk, int dv, int chunk) {
+  if (B < 1 || T < 0 || H < 1 || !dim_ok(dk) || dk != dv || chunk < 1) return 0;
+  const size_t th = static_cast<size_t>(B) * T * H;
   // g, beta (adapter) + dq, dk, dv, dg fp32 + dbeta fp32 + the dense backward's workspace
   return align_up(th * dk * 4) + align_up(th * 4) + 4 * align_up(th * dk * 4) + align_up(th * 4) +
-         kda_chunk_bwd_workspace(1, T, H, dk, dv, kC);
+         kda_chunk_bwd_workspace(B, T, H, dk, dv, kC);
 }
 
-int kda_cc_scan_bwd(hipStream_t stream, const void* q, const void* k, const void* v,
-                    const float* alpha, const float* beta32, const float* S_in,
-                    const float* d_o, const float* dS, void* dq, void* dk, void* dv,
-                    float* dalpha, float* dbeta32, float* dS_in,
-                    int T, int H, int dk_dim, int dv_dim, int tile, int chunk,
-                    void* workspace, size_t workspace_bytes) {
+size_t kda_cc_scan_bwd_workspace(int T, int H, int dk, int dv, int chunk) {
+  return kda_cc_scan_bwd_batched_workspace(1, T, H, dk, dv, chunk);
+}
+
+int kda_cc_scan_bwd_batched(hipStream_t stream, const void* q, const void* k, const void* v,
+                            const float* alpha, const float* beta32, const float* S_in,
+                            const float* d_o, const float* dS, void* dq, void* dk, void* dv,
+                            float* dalpha, float* dbeta32, float* dS_in,
+                            int B, int T, int H, int dk_dim, int dv_dim, int tile, int chunk,
+                            void* workspace, size_t workspace_bytes) {
   g_err[0] = '\0';
+  if (B < 1) return fail(KDA_ERR_INVALID_ARGUMENT, "B=%d must be >= 1", B);
   if (!q || !k || !v || !alpha || !beta32 || !S_in || !d_o || !dS || !dq || !dk || !dv || !dalpha ||
       !dbeta32 || !dS_in)
     return fail(KDA_ERR_INVALID_ARGUMENT, "null pointer");
@@ -646,10 +666,10 @@ int kda_cc_scan_bwd(hipStream_t stream, const void* q, const void* k, const void
   if (tile < 1 || tile > 16)
     return fail(KDA_ERR_INVALID_ARGUMENT, "tile=%d outside [1, 16] (the _cc_tile bound)", tile);
   if (int rc = check_dims(H, dk_dim, dv_dim)) return rc;
-  const size_t need = kda_cc_scan_bwd_workspace(T, H, dk_dim, dv_dim, chunk);
+  const size_t need = kda_cc_scan_bwd_batched_workspace(B, T, H, dk_dim, dv_dim, chunk);
   if (workspace == nullptr || workspace_bytes < need)
     return fail(KDA_ERR_WORKSPACE, "workspace of %zu bytes is too small (need %zu)", workspace_bytes, need);
-  const size_t th = static_cast<size_t>(T) * H;
+  const size_t th = static_cast<size_t>(B) * T * H;
   unsigned char* ws = static_cast<unsigned char*>(workspace);
   float* g32 = reinterpret_cast<float*>(ws);
   ws += align_up(th * dk_dim * 4);
@@ -669,9 +689,9 @@ int kda_cc_scan_bwd(hipStream_t stream, const void* q, const void* k, const void
   aa.dk = dk_dim;
   hipError_t e = kda::launch_adapt(aa, stream);
   if (e != hipSuccess) return hip_fail(e, "cc_scan backward adapter launch");
-  // the dense backward on the [1, T, H, d] view (the same memory layout)
+  // the dense backward on the [B, T, H, d] view (the same memory layout)
   const int rc = kda_chunk_bwd(stream, q, k, v, g32, b32, S_in, d_o, dS, f[0], f[1], f[2], f[3], dbeta, dS_in,
-                               1, T, H, dk_dim, dv_dim, kC, 1.0f, KDA_DTYPE_BF16_F32GATES, KDA_DTYPE_F32, ws, rest);
+                               B, T, H, dk_dim, dv_dim, kC, 1.0f, KDA_DTYPE_BF16_F32GATES, KDA_DTYPE_F32, ws, rest);
   if (rc != KDA_OK) return rc;
   kda::CcFinishArgs fa{};
   fa.dq32 = f[0]; fa.dk32 = f[1]; fa.dv32 = f[2]; fa.dg = f[3]; fa.dbeta = dbeta; fa.alpha = alpha;
@@ -681,6 +701,16 @@ int kda_cc_scan_bwd(hipStream_t stream, const void* q, const void* k, const void
   e = kda::launch_cc_finish(fa, stream);
   if (e != hipSuccess) return hip_fail(e, "cc_scan backward finish launch");
   return KDA_OK;
+}
+
+int kda_cc_scan_bwd(hipStream_t stream, const void* q, const void* k, const void* v,
+                    const float* alpha, const float* beta32, const float* S_in,
+                    const float* d_o, const float* dS, void* dq, void* dk, void* dv,
+                    float* dalpha, float* dbeta32, float* dS_in,
+                    int T, int H, int dk_dim, int dv_dim, int tile, int chunk,
+                    void* workspace, size_t workspace_bytes) {
+  return kda_cc_scan_bwd_batched(stream, q, k, v, alpha, beta32, S_in, d_o, dS, dq, dk, dv, dalpha, dbeta32,
+                                 dS_in, 1, T, H, dk_dim, dv_dim, tile, chunk, workspace, workspace_bytes);
 }
 
 int kda_ut_solve(hipStream_t stream, const void* a, const void* b, void* x, int H, int C, int N,

@@ -725,10 +725,22 @@ def kda_recurrent_step(q, k, v, g, beta, state, scale: float = 1.0, out_dtype=to
 
 
 def _cc_check(q, k, v, alpha, beta32, S, tile, chunk, what, dtype_msg):
-    T = q.shape[0]
-    if S.dim() != 3:
-        raise ValueError(f"{what}: S must be (H, dk, dv)")
-    H, dk, dv = S.shape
+    """Validates the seam's operands, unbatched (T, H*d) or with a leading batch
+    axis (B, T, H*d) -- the vmapped caller of net/model.py:341-347; returns
+    (B, T, H, dk, dv, C) with B = 0 for the unbatched form."""
+    batched = q.dim() == 3
+    if batched:
+        if S.dim() != 4:
+            raise ValueError(f"{what}: with batched operands S must be (B, H, dk, dv)")
+        B, H, dk, dv = S.shape
+        T = q.shape[1]
+        lead = (B, T)
+    else:
+        if S.dim() != 3:
+            raise ValueError(f"{what}: S must be (H, dk, dv)")
+        H, dk, dv = S.shape
+        B, T = 0, q.shape[0]
+        lead = (T,)
     dt = q.dtype
     if v.dtype != dt or dt != torch.bfloat16:
         raise ValueError(f"{dtype_msg}; got q.dtype={dt}, v.dtype={v.dtype}")
@@ -738,28 +750,30 @@ def _cc_check(q, k, v, alpha, beta32, S, tile, chunk, what, dtype_msg):
     if not (1 <= int(tile) <= 16):
         raise ValueError(f"{what}: tile={tile} outside [1, 16]")
     _check_dims(dk, dv, what)
-    if (tuple(q.shape) != (T, H * dk) or tuple(k.shape) != (T, H * dk) or k.dtype != dt
-            or tuple(v.shape) != (T, H * dv) or tuple(alpha.shape) != (T, H * dk)
-            or tuple(beta32.shape) != (T, H * 32)):
-        raise ValueError(f"{what}: shapes must be q,k,alpha (T,H*dk), v (T,H*dv), beta32 (T,H*32)")
+    if (tuple(q.shape) != lead + (H * dk,) or tuple(k.shape) != lead + (H * dk,) or k.dtype != dt
+            or tuple(v.shape) != lead + (H * dv,) or tuple(alpha.shape) != lead + (H * dk,)
+            or tuple(beta32.shape) != lead + (H * 32,)):
+        raise ValueError(f"{what}: shapes must be q,k,alpha ([B,] T,H*dk), v ([B,] T,H*dv), "
+                         "beta32 ([B,] T,H*32)")
     if alpha.dtype != torch.float32 or beta32.dtype != torch.float32 or S.dtype != torch.float32:
         raise ValueError(f"{what}: alpha, beta32 and S must be fp32")
     for name, t in (("q", q), ("k", k), ("v", v), ("alpha", alpha), ("beta32", beta32), ("S", S)):
         _contig(name, t)
-    return T, H, dk, dv, C
+    return B, T, H, dk, dv, C
 
 
 def _cc_scan_fwd(q, k, v, alpha, beta32, S, tile, chunk):
-    T, H, dk, dv, C = _cc_check(q, k, v, alpha, beta32, S, tile, chunk, "cc_scan",
-                                "persistent kernel consumes bf16 q/k/v")
+    B, T, H, dk, dv, C = _cc_check(q, k, v, alpha, beta32, S, tile, chunk, "cc_scan",
+                                   "persistent kernel consumes bf16 q/k/v")
     dev = _require_gpu([q, k, v, alpha, beta32, S], "cc_scan")
     L = _lib.lib()
-    ws_bytes = int(L.kda_cc_scan_workspace(T, H, dk, dv, C))
+    nb = max(B, 1)
+    ws_bytes = int(L.kda_cc_scan_batched_workspace(nb, T, H, dk, dv, C))
     workspace = torch.empty(max(ws_bytes, 1), dtype=torch.uint8, device=dev)
-    o = torch.empty((T, H * dv), dtype=torch.float32, device=dev)
-    S_new = torch.empty((H, dk, dv), dtype=torch.float32, device=dev)
-    rc = L.kda_cc_scan(_stream(dev), _ptr(q), _ptr(k), _ptr(v), _ptr(alpha), _ptr(beta32), _ptr(S),
-                       _ptr(o), _ptr(S_new), T, H, dk, dv, int(tile), C, _ptr(workspace), ws_bytes)
+    o = torch.empty(q.shape[:-1] + (H * dv,), dtype=torch.float32, device=dev)
+    S_new = torch.empty_like(S)
+    rc = L.kda_cc_scan_batched(_stream(dev), _ptr(q), _ptr(k), _ptr(v), _ptr(alpha), _ptr(beta32), _ptr(S),
+                               _ptr(o), _ptr(S_new), nb, T, H, dk, dv, int(tile), C, _ptr(workspace), ws_bytes)
     _lib.check(rc, "cc_scan")
     return o, S_new
 
@@ -767,28 +781,29 @@ def _cc_scan_fwd(q, k, v, alpha, beta32, S, tile, chunk):
 def cc_scan_bwd(q, k, v, alpha, beta32, S, do, dS=None, tile: int = 16, chunk: int = 32):
     """The seam's backward rule ``kernel_bwd`` (``net/kernels/kda_cc_fused_persist.py:1710``).
 
-    ``(q, k, v, alpha, beta32, S)`` as :func:`cc_scan`, ``do (T, H*dv)`` and
-    ``dS (H, dk, dv)`` (None = 0) the cotangents of ``o`` and ``S_new``.
+    ``(q, k, v, alpha, beta32, S)`` as :func:`cc_scan`, ``do ([B,] T, H*dv)`` and
+    ``dS ([B,] H, dk, dv)`` (None = 0) the cotangents of ``o`` and ``S_new``.
     Returns ``(dq, dk, dv, dalpha, dbeta32, dS_in)`` in the primal dtypes:
     bf16 ``dq, dk, dv``, fp32 ``dalpha`` (``= d(log alpha) / alpha``),
     ``dbeta32`` (the beta cotangent / 32 on each of the 32 columns) and
     ``dS_in``.
     """
     what = "cc_scan_bwd"
-    T, H, dk, dv, C = _cc_check(q, k, v, alpha, beta32, S, tile, chunk, what,
-                                "persistent backward kernel consumes bf16 q/k/v (the same operand "
-                                "path as the forward kernel)")
-    if tuple(do.shape) != (T, H * dv):
-        raise ValueError(f"{what}: do must be (T, H*dv) = {(T, H * dv)}")
+    B, T, H, dk, dv, C = _cc_check(q, k, v, alpha, beta32, S, tile, chunk, what,
+                                   "persistent backward kernel consumes bf16 q/k/v (the same operand "
+                                   "path as the forward kernel)")
+    if tuple(do.shape) != tuple(q.shape[:-1]) + (H * dv,):
+        raise ValueError(f"{what}: do must be ([B,] T, H*dv) = {tuple(q.shape[:-1]) + (H * dv,)}")
     do = do.float().contiguous()
     if dS is None:
         dS = torch.zeros_like(S)
-    if tuple(dS.shape) != (H, dk, dv):
-        raise ValueError(f"{what}: dS must be (H, dk, dv)")
+    if tuple(dS.shape) != tuple(S.shape):
+        raise ValueError(f"{what}: dS must be shaped as S ([B,] H, dk, dv)")
     dS = dS.float().contiguous()
     dev = _require_gpu([q, k, v, alpha, beta32, S, do, dS], what)
     L = _lib.lib()
-    ws_bytes = int(L.kda_cc_scan_bwd_workspace(T, H, dk, dv, C))
+    nb = max(B, 1)
+    ws_bytes = int(L.kda_cc_scan_bwd_batched_workspace(nb, T, H, dk, dv, C))
     workspace = torch.empty(max(ws_bytes, 1), dtype=torch.uint8, device=dev)
     dq = torch.empty_like(q)
     dk_ = torch.empty_like(k)
@@ -796,9 +811,10 @@ def cc_scan_bwd(q, k, v, alpha, beta32, S, do, dS=None, tile: int = 16, chunk: i
     dalpha = torch.empty_like(alpha)
     dbeta32 = torch.empty_like(beta32)
     dS_in = torch.empty_like(S)
-    rc = L.kda_cc_scan_bwd(_stream(dev), _ptr(q), _ptr(k), _ptr(v), _ptr(alpha), _ptr(beta32), _ptr(S),
-                           _ptr(do), _ptr(dS), _ptr(dq), _ptr(dk_), _ptr(dv_), _ptr(dalpha), _ptr(dbeta32),
-                           _ptr(dS_in), T, H, dk, dv, int(tile), C, _ptr(workspace), ws_bytes)
+    rc = L.kda_cc_scan_bwd_batched(_stream(dev), _ptr(q), _ptr(k), _ptr(v), _ptr(alpha), _ptr(beta32), _ptr(S),
+                                   _ptr(do), _ptr(dS), _ptr(dq), _ptr(dk_), _ptr(dv_), _ptr(dalpha),
+                                   _ptr(dbeta32), _ptr(dS_in), nb, T, H, dk, dv, int(tile), C,
+                                   _ptr(workspace), ws_bytes)
     _lib.check(rc, what)
     return dq, dk_, dv_, dalpha, dbeta32, dS_in
 
@@ -818,7 +834,7 @@ class _CCScan(torch.autograd.Function):
     def backward(ctx, do, dS):
         q, k, v, alpha, beta32, S = ctx.saved_tensors
         if do is None:
-            do = torch.zeros((q.shape[0], v.shape[1]), dtype=torch.float32, device=q.device)
+            do = torch.zeros(v.shape, dtype=torch.float32, device=q.device)
         grads = cc_scan_bwd(q, k, v, alpha, beta32, S, do, dS, tile=ctx.tile, chunk=ctx.chunk)
         return (*grads, None, None)
 
@@ -828,7 +844,9 @@ def cc_scan(q, k, v, alpha, beta32, S, tile: int = 16, chunk: int = 32):
 
     ``q, k (T, H*dk)`` bf16, ``v (T, H*dv)`` bf16, ``alpha (T, H*dk)`` fp32,
     ``beta32 (T, H*32)`` fp32, ``S (H, dk, dv)`` fp32.  Returns
-    ``(o (T, H*dv) fp32, S_new (H, dk, dv) fp32)``.  Raises ``ValueError`` for
+    ``(o (T, H*dv) fp32, S_new (H, dk, dv) fp32)``.  Every operand may carry a
+    leading batch axis B (the vmapped caller, ``net/model.py:341-347``): the
+    batch then runs in one launch.  Raises ``ValueError`` for
     a non-bf16 q/v (``:737-740``), ``T % chunk != 0`` (``:741-742``) or an
     unsupported configuration (``:743-749``), ``RuntimeError`` without a GPU.
     Differentiable: gradients reach all six inputs through

@@ -40,7 +40,8 @@ Also reported on the same JSON line:
   B=256;
 * ``cc_scan_seam``: the reference's seam ``cc_scan`` and its backward rule
   ``cc_scan_bwd`` on one batch element of config 1 (alpha / beta32 operands,
-  the reference's call shape), per call;
+  the reference's call shape), per call, and (``batched``) on the whole
+  batch in one call with a leading batch axis;
 * ``ut_solve``: the standalone unit-triangular solve at the reference's case
   (H=12, C=64, N=dk+dv=256, fp32), both orientations, per call;
 * ``cpu_baseline``: the oracle's fp32 restatement of the reference jax body
@@ -427,8 +428,22 @@ def bench_cc_scan(args, fwd_inputs, device):
     t_f = timed(lambda: axiom_amd.cc_scan(q2, k2, v2, alpha, beta32, S, tile=16, chunk=64), args.steps)
     t_b = timed(lambda: axiom_amd.cc_scan_bwd(q2, k2, v2, alpha, beta32, S, do, dS, tile=16, chunk=64),
                 args.bwd_steps)
+    # the whole batch in one call (the vmapped caller's form)
+    B = q.shape[0]
+    qb, kb, vb = (x.reshape(B, T, H * d) for x in (q, k, v))
+    alpha_b = torch.exp(g.float()).reshape(B, T, H * d).contiguous()
+    beta32_b = beta.float().reshape(B, T, H, 1).expand(B, T, H, 32).reshape(B, T, H * 32).contiguous()
+    S_b = torch.zeros(B, H, d, d, device=device)
+    do_b = torch.randn(B, T, H * d, device=device, generator=gen)
+    dS_b = torch.randn(B, H, d, d, device=device, generator=gen) * 0.1
+    t_fb = timed(lambda: axiom_amd.cc_scan(qb, kb, vb, alpha_b, beta32_b, S_b, tile=16, chunk=64), args.steps)
+    t_bb = timed(lambda: axiom_amd.cc_scan_bwd(qb, kb, vb, alpha_b, beta32_b, S_b, do_b, dS_b, tile=16, chunk=64),
+                 args.bwd_steps)
     return dict(fwd_us_per_call=t_f * 1e6, bwd_us_per_call=t_b * 1e6, tokens_per_s_fwd=T / t_f,
-                config=f"one batch element: T{T} H{H} d{d}, bf16 q/k/v, fp32 alpha/beta32/S (cc_scan, cc_scan_bwd)")
+                config=f"one batch element: T{T} H{H} d{d}, bf16 q/k/v, fp32 alpha/beta32/S (cc_scan, cc_scan_bwd)",
+                batched=dict(fwd_us_per_call=t_fb * 1e6, bwd_us_per_call=t_bb * 1e6,
+                             tokens_per_s_fwd=B * T / t_fb,
+                             config=f"whole batch in one call: B{B} T{T} H{H} d{d} (leading batch axis)"))
 
 
 def bench_ut_solve(args, device):

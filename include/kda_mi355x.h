@@ -207,6 +207,32 @@ KDA_API int kda_cc_scan_bwd(hipStream_t stream,
 KDA_API size_t kda_cc_scan_bwd_workspace(int T, int H, int dk, int dv, int chunk);
 
 /*
+ * The seam for its vmapped caller: net/model.py:341-347 maps cc_scan over the
+ * batch (jax.vmap), so the custom call sees a leading batch axis.  These take
+ * the seam's operands with that axis -- q, k, alpha (B, T, H*dk), v (B, T,
+ * H*dv), beta32 (B, T, H*32), S_in (B, H, dk, dv) -- and run the B elements
+ * in one launch each (the batch folded into the kernels' grids), with the
+ * results, errors and cotangents of B separate kda_cc_scan /
+ * kda_cc_scan_bwd calls.  An XLA FFI handler registered with
+ * vmap_method="expand_dims" binds them directly (B = 1 is kda_cc_scan).
+ */
+KDA_API int kda_cc_scan_batched(hipStream_t stream,
+                const void* q, const void* k, const void* v,
+                const float* alpha, const float* beta32, const float* S_in,
+                float* o, float* S_out,
+                int B, int T, int H, int dk, int dv, int tile, int chunk,
+                void* workspace, size_t workspace_bytes);
+KDA_API size_t kda_cc_scan_batched_workspace(int B, int T, int H, int dk, int dv, int chunk);
+KDA_API int kda_cc_scan_bwd_batched(hipStream_t stream,
+                const void* q, const void* k, const void* v,
+                const float* alpha, const float* beta32, const float* S_in,
+                const float* d_o, const float* dS,
+                void* dq, void* dk, void* dv, float* dalpha, float* dbeta32, float* dS_in,
+                int B, int T, int H, int dk_dim, int dv_dim, int tile, int chunk,
+                void* workspace, size_t workspace_bytes);
+KDA_API size_t kda_cc_scan_bwd_batched_workspace(int B, int T, int H, int dk, int dv, int chunk);
+
+/*
  * Chunked backward: gradients of (o, final state) = kda_chunk_fwd(q, k, v, g,
  * beta, h0) for dense [B,T,H,d] inputs (no cu_seqlens).  Replaces the
  * reference's backward rule of the cc_scan custom_vjp,
