@@ -77,6 +77,18 @@ def flops_per_token_head(C, d):
     return 8 * C * d + 6 * d * d
 
 
+def reference_cost_flops_per_token_head(C, dk, dv, tile=16):
+    """The reference's executed-work convention, ``cost()`` of
+    ``net/kernels/kda_cc_fused_persist.py:298-318``, per token-head: the chunk's
+    score matrices, their tile-wise rebuild, the solve's right-hand side and
+    power chain, w·S / inter, intra and the state update, divided by C.
+    344,064 at C = 64, d = 128, tile = 16."""
+    ntile = -(-C // tile)
+    per_chunk = (4 * C * C * dk + 4 * ntile * C * C * dk + 4 * C * C * (dk + dv)
+                 + 2 * C * (dk + dv) * dk + 2 * C * dv * C + 2 * dk * dv * C)
+    return per_chunk // C
+
+
 def fwd_bytes(B, T, H, dk, dv, in_bytes=2, o_bytes=4):
     n = B * T * H
     return n * (3 * dk + dv) * in_bytes + n * in_bytes + n * dv * o_bytes + B * H * dk * dv * 4
@@ -605,6 +617,8 @@ def main():
         "tflops": tflops,
         "mfma_peak_frac": tflops / MFMA_BF16_PEAK_TFLOPS,
         "us_per_launch": t_launch * 1e6,
+        # secondary: the reference's own cost() FLOP convention over the same launch
+        "reference_cost_tflops": tokens * H * reference_cost_flops_per_token_head(C, dk, dv) / t_launch / 1e12,
         "roofline": {"bound": "hbm", "achieved": achieved, "peak": HBM_PEAK_GBPS, "unit": "GB/s",
                      "frac": achieved / HBM_PEAK_GBPS,
                      "traffic": measured_traffic("traffic_bytes_per_call"),
