@@ -46,14 +46,28 @@ constexpr int kC = 64;
 
 // ----------------------------------------------------------------------------
 // non-finite detection of the results (fp16 operand range)
+//
+// Each lane keeps the sum of the magnitudes of the values it stores: an inf
+// or NaN among them makes the sum non-finite, and one add per value (with
+// the |x| source modifier) is all the checking the store paths pay.  Inside
+// the supported operand range a sum of finite values stays far below fp32's
+// limit (|o| < 2^23 per element for unit-norm q, k; a lane stores a few
+// values per chunk).
 // ----------------------------------------------------------------------------
-__device__ __forceinline__ bool f32_bits_nonfinite(uint32_t w) { return (w & 0x7F800000u) == 0x7F800000u; }
-__device__ __forceinline__ bool bf16x2_bits_nonfinite(uint32_t w) {
-  return (w & 0x7F80u) == 0x7F80u || (w & 0x7F800000u) == 0x7F800000u;
+__device__ __forceinline__ float abs_sum_f32x4(const uint4 v) {
+  return (fabsf(__uint_as_float(v.x)) + fabsf(__uint_as_float(v.y))) +
+         (fabsf(__uint_as_float(v.z)) + fabsf(__uint_as_float(v.w)));
 }
-// sets the call's status bit from one lane when any lane of the wave saw a
-// non-finite result
-__device__ __forceinline__ void report_nonfinite(int* status, bool bad) {
+__device__ __forceinline__ float abs_sum_bf16x2(const uint32_t w) {
+  return fabsf(__uint_as_float(w << 16)) + fabsf(__uint_as_float(w & 0xFFFF0000u));
+}
+__device__ __forceinline__ float abs_sum_bf16x8(const uint4 v) {
+  return (abs_sum_bf16x2(v.x) + abs_sum_bf16x2(v.y)) + (abs_sum_bf16x2(v.z) + abs_sum_bf16x2(v.w));
+}
+// sets the call's status bit from one lane when any lane of the wave holds a
+// non-finite magnitude sum
+__device__ __forceinline__ void report_nonfinite(int* status, float mag) {
+  const bool bad = !(mag <= 3.402823466e38f);   // inf or NaN
   if (status != nullptr && __any(bad) && (threadIdx.x & 63) == 0) atomicOr(status, kStatusNonFinite);
 }
 
@@ -1149,31 +1163,54 @@ __device__ __forceinline__ void col_stage(const StateArgs& a, int64_t ch, int sp
 
 // Producer P's share of the o rows of one chunk: LDS [64 rows][32 columns]
 // (fp32, or bf16 when OUT_DT == 1) to the workgroup's 32 columns of o, 16 B
-// per lane, rows past the chunk's end skipped.
+// per lane, rows past the chunk's end skipped.  The stored values are kept
+// in `vs` (and whether each was stored in `ok`) for the caller's range check,
+// which it runs once the next chunk's copies are in flight.
+template <int OUT_DT>
+struct ColStoreShape {
+  static constexpr int ES = (OUT_DT == 0) ? 4 : 2;
+  static constexpr int LPR = 32 * ES / 16;     // lanes per row
+  static constexpr int RPI = 64 / LPR;         // rows per instruction
+  static constexpr int NI = kC / RPI;          // instructions per chunk
+  static constexpr int NS = (NI + kColProducers - 1) / kColProducers;  // per producer
+};
+
 template <int DV, int OUT_DT, int P>
 __device__ __forceinline__ void col_store_rows(const StateArgs& a, const unsigned char* ob, int64_t row0,
-                                               int len, int h, int split, int l, bool& bad) {
-  constexpr int ES = (OUT_DT == 0) ? 4 : 2;
-  constexpr int LPR = 32 * ES / 16;            // lanes per row
-  constexpr int RPI = 64 / LPR;                // rows per instruction
-  constexpr int NI = kC / RPI;                 // instructions per chunk
+                                               int len, int h, int split, int l,
+                                               uint4 (&vs)[ColStoreShape<OUT_DT>::NS],
+                                               bool (&ok)[ColStoreShape<OUT_DT>::NS]) {
+  typedef ColStoreShape<OUT_DT> SS;
   const int H = a.geom.H;
 #pragma unroll
-  for (int ins = P; ins < NI; ins += kColProducers) {
-    const int row = RPI * ins + l / LPR;
-    const int cb = (l % LPR) * 16;             // byte offset inside the 32-column row
-    const uint4 v = *reinterpret_cast<const uint4*>(ob + row * (32 * ES) + cb);
-    if (row < len) {
-      if constexpr (OUT_DT == 0)
-        bad |= f32_bits_nonfinite(v.x) | f32_bits_nonfinite(v.y) | f32_bits_nonfinite(v.z) | f32_bits_nonfinite(v.w);
-      else
-        bad |= bf16x2_bits_nonfinite(v.x) | bf16x2_bits_nonfinite(v.y) | bf16x2_bits_nonfinite(v.z) |
-               bf16x2_bits_nonfinite(v.w);
-      unsigned char* dst = static_cast<unsigned char*>(a.o) +
-                           (((row0 + row) * H + h) * static_cast<int64_t>(DV) + 32 * split) * ES + cb;
-      *reinterpret_cast<uint4*>(dst) = v;
+  for (int k = 0; k < SS::NS; ++k) {
+    const int ins = P + kColProducers * k;
+    ok[k] = false;
+    vs[k] = uint4{0, 0, 0, 0};
+    if (ins < SS::NI) {
+      const int row = SS::RPI * ins + l / SS::LPR;
+      const int cb = (l % SS::LPR) * 16;       // byte offset inside the 32-column row
+      vs[k] = *reinterpret_cast<const uint4*>(ob + row * (32 * SS::ES) + cb);
+      ok[k] = row < len;
+      if (ok[k]) {
+        unsigned char* dst = static_cast<unsigned char*>(a.o) +
+                             (((row0 + row) * H + h) * static_cast<int64_t>(DV) + 32 * split) * SS::ES + cb;
+        *reinterpret_cast<uint4*>(dst) = vs[k];
+      }
     }
   }
+}
+
+// magnitude sum of the values col_store_rows stored
+template <int OUT_DT, int NS>
+__device__ __forceinline__ float col_stored_mag(const uint4 (&vs)[NS], const bool (&ok)[NS]) {
+  float m = 0.f;
+#pragma unroll
+  for (int k = 0; k < NS; ++k) {
+    const float x = (OUT_DT == 0) ? abs_sum_f32x4(vs[k]) : abs_sum_bf16x8(vs[k]);
+    m += ok[k] ? x : 0.f;
+  }
+  return m;
 }
 
 struct ChainRef {
@@ -1210,23 +1247,31 @@ __device__ __forceinline__ void col_producer(const StateArgs& a, ColSmem<DK>& sm
   const int H = a.geom.H;
   const int l = threadIdx.x & 63;
   if (c.nchunks <= 0) return;
-  bool bad = false;
+  constexpr int NS = ColStoreShape<OUT_DT>::NS;
+  uint4 vs[NS];
+  bool ok[NS];
+  float mag = 0.f;
   col_stage<DK, DV, P>(a, static_cast<int64_t>(c.u0) * H + h, split, sm.buf[0], l);
   wait_vmem_all();
   lds_barrier();
   for (int n = 0; n < c.nchunks; ++n) {
-    if (n > 0)
+    const bool st = n > 0;
+    if (st)
       col_store_rows<DV, OUT_DT, P>(a, sm.obuf[(n - 1) & 1], c.tok0 + static_cast<int64_t>(n - 1) * kC,
-                                    min(kC, c.seq_len - (n - 1) * kC), h, split, l, bad);
+                                    min(kC, c.seq_len - (n - 1) * kC), h, split, l, vs, ok);
     if (n + 1 < c.nchunks)
       col_stage<DK, DV, P>(a, static_cast<int64_t>(c.u0 + n + 1) * H + h, split, sm.buf[(n + 1) & 1], l);
+    // the range check of the stored o rows runs while the copies are in flight
+    __builtin_amdgcn_sched_barrier(0);
+    if (st) mag += col_stored_mag<OUT_DT>(vs, ok);
     wait_vmem_all();
     lds_barrier();
   }
   const int nl = c.nchunks - 1;
   col_store_rows<DV, OUT_DT, P>(a, sm.obuf[nl & 1], c.tok0 + static_cast<int64_t>(nl) * kC,
-                                min(kC, c.seq_len - nl * kC), h, split, l, bad);
-  report_nonfinite(a.status, bad);
+                                min(kC, c.seq_len - nl * kC), h, split, l, vs, ok);
+  mag += col_stored_mag<OUT_DT>(vs, ok);
+  report_nonfinite(a.status, mag);
 }
 
 // Calls f(std::integral_constant<int, I>{}) for I = B .. E-1, expanded at
@@ -1401,18 +1446,18 @@ __device__ __forceinline__ void col_chain(const StateArgs& a, ColSmem<DK>& sm, i
   }
 
   if (a.ht != nullptr) {
-    bool bad = false;
+    float mag = 0.f;
 #pragma unroll
     for (int cc = 0; cc < NC; ++cc)
 #pragma unroll
       for (int dt = 0; dt < NT; ++dt)
 #pragma unroll
         for (int i = 0; i < 4; ++i) {
-          bad |= f32_bits_nonfinite(__float_as_uint(S[cc][dt][i]));
+          mag += fabsf(S[cc][dt][i]);
           a.ht[sbase + static_cast<int64_t>(16 * dt + 4 * gq + i) * DV + 16 * (2 * split + tile0 + cc) + r] =
               S[cc][dt][i];
         }
-    report_nonfinite(a.status, bad);
+    report_nonfinite(a.status, mag);
   }
 }
 
@@ -1560,7 +1605,7 @@ __device__ __forceinline__ void wide_chain(const StateArgs& a, WideSmem<DK, VT>&
                            ? a.h0[sbase + static_cast<int64_t>(16 * dt + 4 * gq + i) * DV + col0 + 16 * cc + r]
                            : 0.f;
 
-  bool bad = false;
+  float mag = 0.f;
   if (nchunks > 0) lds_barrier();  // chunk 0 staged by the producer waves
   for (int n = 0; n < nchunks; ++n) {
     const unsigned char* cur = sm.buf[n & 1];
@@ -1690,7 +1735,7 @@ __device__ __forceinline__ void wide_chain(const StateArgs& a, WideSmem<DK, VT>&
           const int row = 16 * ct + 4 * gq + i;
           if (row < len) {
             const int64_t oi = ((row0 + row) * H + h) * static_cast<int64_t>(DV) + col0 + 16 * cc + r;
-            bad |= f32_bits_nonfinite(__float_as_uint(O[cc][ct][i]));
+            mag += fabsf(O[cc][ct][i]);
             if constexpr (OUT_DT == 0) static_cast<float*>(a.o)[oi] = O[cc][ct][i];
             else static_cast<u16*>(a.o)[oi] = f32_to_bf16_bits(O[cc][ct][i]);
           }
@@ -1707,11 +1752,11 @@ __device__ __forceinline__ void wide_chain(const StateArgs& a, WideSmem<DK, VT>&
       for (int dt = 0; dt < NT; ++dt)
 #pragma unroll
         for (int i = 0; i < 4; ++i) {
-          bad |= f32_bits_nonfinite(__float_as_uint(S[cc][dt][i]));
+          mag += fabsf(S[cc][dt][i]);
           a.ht[sbase + static_cast<int64_t>(16 * dt + 4 * gq + i) * DV + col0 + 16 * cc + r] = S[cc][dt][i];
         }
   }
-  report_nonfinite(a.status, bad);
+  report_nonfinite(a.status, mag);
 }
 
 template <int DK, int DV, int VT, int CW, int OUT_DT>
