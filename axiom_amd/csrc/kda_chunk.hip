@@ -117,12 +117,26 @@ struct IntraSmem {
   // region 1, two lives: k*Cf (scores) -> (beta*gamma*k)^T (W product)
   st r1[R1];
   st BVt[DV * PC];        // (beta*v)^T, rows = channel
-  st Tm[kC * PC];         // T = (I+L)^-1; wave w writes row block w
-  st Lmb[6][16][20];      // off-diagonal L blocks, row-major; block (R,j) at R(R-1)/2+j
-  st Tdg[4][16][20];      // diagonal T blocks, row-major
-  float Ld[4][16][20];    // diagonal L blocks, fp32
+  // T = (I+L)^-1 (wave w writes row block w after barrier #2).  Before that
+  // barrier the same bytes hold each wave's per-tile factors and, once its
+  // score tiles are done, its diagonal L block (both wave-local).
+  st Tm[kC * PC];
+  st Lmb[6][16][16];      // off-diagonal L blocks, row-major; block (R,j) at R(R-1)/2+j
+  st Tdg[4][16][16];      // diagonal T blocks, row-major
   float tot[4][DK];       // per-tile log2 decay totals, slot order
-  float fac[4][5][DK];    // per tile: 2^pre, 2^post, 2^-D, M(w,w-2), M(w,w-3)
+  // Factor rows of wave w (2^pre, 2^post, 2^-D, then M(w,w-2) from w = 2 on
+  // and M(w,w-3) from w = 3 on): rows FR0[w] .. FR0[w+1]-1 of DK floats.
+  static constexpr int FR0[5] = {0, 3, 6, 10, 15};
+  __device__ float* fac(int w, int k) { return reinterpret_cast<float*>(Tm) + (FR0[w] + k) * DK; }
+  // the diagonal L block of wave w, fp32 [16][20]: over the wave's own factor
+  // rows when they are large enough, else after all factor rows
+  static constexpr bool LD_IN_FAC = 3 * DK >= 16 * 20;
+  __device__ float (*Ld(int w))[20] {
+    float* base = LD_IN_FAC ? fac(w, 0) : reinterpret_cast<float*>(Tm) + FR0[4] * DK + w * 16 * 20;
+    return reinterpret_cast<float (*)[20]>(base);
+  }
+  static_assert(sizeof(st) * kC * PC >= sizeof(float) * (FR0[4] * DK + (LD_IN_FAC ? 0 : 4 * 16 * 20)),
+                "factor rows and diagonal L blocks exceed the T buffer");
 };
 
 // channel of slot index s
@@ -169,7 +183,9 @@ __device__ __forceinline__ void intra_chunk(const IntraArgs& a, const UnitRef& U
   constexpr int ROWB = DK * 2;          // bytes per staged row
   constexpr int NCH = ROWB / 16;        // 16-byte chunks per row
   constexpr int RPI = 1024 / ROWB;      // rows per copy instruction
-  static_assert(PRO || !(STQ || STG) || sizeof(SM) >= 4 * kC * ROWB, "staging area exceeds the shared buffers");
+  // Without the fused prologue three [64][DK] 16-bit tensors are staged at a
+  // time: q, k and g, then v in g's rows once the wave has read its g.
+  static_assert(PRO || !(STQ || STG) || sizeof(SM) >= 3 * kC * ROWB, "staging area exceeds the shared buffers");
   static_assert(DK == DV, "staging assumes dk == dv");
   static_assert(!PRO || (DTQ == 1 && !EXACT), "the fused prologue stages bf16 projections");
   unsigned char* const stg = reinterpret_cast<unsigned char*>(&sm);
@@ -183,7 +199,7 @@ __device__ __forceinline__ void intra_chunk(const IntraArgs& a, const UnitRef& U
       const int tt = (t == 3) ? 2 : t;   // q, k, v
       return stg + (kC + (tt * 4 + W) * HR + (row - 16 * W + RPI)) * ROWB;
     } else {
-      return stg + (t * kC + row) * ROWB;
+      return stg + ((t == 3 ? 2 : t) * kC + row) * ROWB;   // v over g
     }
   };
   // beta first: its latency hides behind the row copies.  Copy order g, k, q,
@@ -242,27 +258,34 @@ __device__ __forceinline__ void intra_chunk(const IntraArgs& a, const UnitRef& U
       }
     }
   }
+  // direct global->LDS copies of this wave's rows of tensor t
+  auto stage_rows = [&](const int t) {
+    const u16* src = static_cast<const u16*>(t == 0 ? a.q : t == 1 ? a.k : t == 2 ? a.g : a.v);
+    const int nc = (t == 2) ? NPER : NQKV;
+    const int r0 = (PRO && t != 2) ? 16 * W - RPI : 16 * W;         // first row copied
+#pragma unroll
+    for (int i = 0; i < nc; ++i) {
+      const int row = r0 + RPI * i + l / NCH;                       // chunk row this lane copies
+      const int cidx = (l % NCH) ^ (row & (NCH - 1));               // source chunk of LDS chunk l % NCH
+      // rows past the end re-read a valid row; history rows before a
+      // sequence's first chunk (replaced by the carried inputs) read row 0
+      int rv = min(row, U.len - 1);
+      if (PRO && U.n == 0) rv = max(rv, 0);
+      const int64_t srow = U.row0 + rv;
+      const u16* gsrc = src + (srow * H + h) * DK + cidx * 8;
+      unsigned char* ldst = stg_row(t, r0 + RPI * i);
+      __builtin_amdgcn_global_load_lds(gsrc, ldst, 16, 0, 0);
+    }
+  };
+  // v goes into g's rows once the wave has read its g (below) when g is staged
+  constexpr bool V_LATE = !PRO && STG;
   if constexpr (STQ || STG) {
 #pragma unroll
     for (int oi = 0; oi < 4; ++oi) {
       const int t = (oi == 0) ? 2 : (oi == 1) ? 1 : (oi == 2) ? 0 : 3;  // 0 q, 1 k, 2 g, 3 v
       if ((t == 2) ? !STG : !STQ) continue;
-      const u16* src = static_cast<const u16*>(t == 0 ? a.q : t == 1 ? a.k : t == 2 ? a.g : a.v);
-      const int nc = (t == 2) ? NPER : NQKV;
-      const int r0 = (PRO && t != 2) ? 16 * W - RPI : 16 * W;       // first row copied
-#pragma unroll
-      for (int i = 0; i < nc; ++i) {
-        const int row = r0 + RPI * i + l / NCH;                     // chunk row this lane copies
-        const int cidx = (l % NCH) ^ (row & (NCH - 1));             // source chunk of LDS chunk l % NCH
-        // rows past the end re-read a valid row; history rows before a
-        // sequence's first chunk (replaced by the carried inputs) read row 0
-        int rv = min(row, U.len - 1);
-        if (PRO && U.n == 0) rv = max(rv, 0);
-        const int64_t srow = U.row0 + rv;
-        const u16* gsrc = src + (srow * H + h) * DK + cidx * 8;
-        unsigned char* ldst = stg_row(t, r0 + RPI * i);
-        __builtin_amdgcn_global_load_lds(gsrc, ldst, 16, 0, 0);
-      }
+      if (V_LATE && t == 3) continue;
+      stage_rows(t);
     }
     if constexpr (!SPLIT) {
       wait_vmem_all();
@@ -291,11 +314,15 @@ __device__ __forceinline__ void intra_chunk(const IntraArgs& a, const UnitRef& U
 
   // g -> log2 decay, then the tile-local inclusive scan
   if constexpr (SPLIT) {
-    wait_vmem<3 * NQKV>();
+    wait_vmem<(V_LATE ? 2 : 3) * NQKV>();
     __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "workgroup", "local");
   }
   uint2 sw[2 * NJ];
   if constexpr (STG) stg_read_all(2, sw);
+  // g is in registers (settled): v's copies may now overwrite its rows; they
+  // are the newest copies, so the waits below for k, q and then v are as
+  // before
+  if constexpr (V_LATE) stage_rows(3);
 #pragma unroll
   for (int j = 0; j < NJ; ++j)
 #pragma unroll
@@ -515,11 +542,11 @@ __device__ __forceinline__ void intra_chunk(const IntraArgs& a, const UnitRef& U
       if (t < W) pre += tt[t];
       if (t > W) post += tt[t];
     }
-    sm.fac[W][0][s0] = fast_exp2(pre);
-    sm.fac[W][1][s0] = fast_exp2(post);
-    sm.fac[W][2][s0] = fast_exp2(-tt[W]);
-    if constexpr (W >= 2) sm.fac[W][3][s0] = fast_exp2(tt[W - 1]);
-    if constexpr (W >= 3) sm.fac[W][4][s0] = fast_exp2(tt[W - 1] + tt[W - 2]);
+    sm.fac(W, 0)[s0] = fast_exp2(pre);
+    sm.fac(W, 1)[s0] = fast_exp2(post);
+    sm.fac(W, 2)[s0] = fast_exp2(-tt[W]);
+    if constexpr (W >= 2) sm.fac(W, 3)[s0] = fast_exp2(tt[W - 1]);
+    if constexpr (W >= 3) sm.fac(W, 4)[s0] = fast_exp2(tt[W - 1] + tt[W - 2]);
     if constexpr (W == 0) a.GC[chead * DK + slot_index_channel(s0)] = fast_exp2(tt[0] + tt[1] + tt[2] + tt[3]);
   }
   __builtin_amdgcn_wave_barrier();  // this wave reads back its own fac[W] below
@@ -528,15 +555,15 @@ __device__ __forceinline__ void intra_chunk(const IntraArgs& a, const UnitRef& U
   f4 accK[W + 1], accQ[W + 1];
 #pragma unroll
   for (int s = 0; s <= W; ++s) { accK[s] = f4{0, 0, 0, 0}; accQ[s] = f4{0, 0, 0, 0}; }
-  st lk[NJ][8];  // lambda*k
-  st bw[NJ][8];  // beta*gamma*k
+  v8 lk[NJ];  // lambda*k, packed operand precision
+  v8 bw[NJ];  // beta*gamma*k, packed operand precision
 
 #pragma unroll
   for (int j = 0; j < NJ; ++j) {
     const int sb = 32 * j + 8 * gq;
-    const f8 P = *reinterpret_cast<const f8*>(&sm.fac[W][0][sb]);
-    const f8 Q = *reinterpret_cast<const f8*>(&sm.fac[W][1][sb]);
-    const f8 iD = *reinterpret_cast<const f8*>(&sm.fac[W][2][sb]);
+    const f8 P = *reinterpret_cast<const f8*>(&sm.fac(W, 0)[sb]);
+    const f8 Q = *reinterpret_cast<const f8*>(&sm.fac(W, 1)[sb]);
+    const f8 iD = *reinterpret_cast<const f8*>(&sm.fac(W, 2)[sb]);
     f8 krj, qrj;
 #pragma unroll
     for (int e = 0; e < 8; ++e) { krj[e] = kr[j][e]; qrj[e] = qr[j][e]; }
@@ -550,14 +577,14 @@ __device__ __forceinline__ void intra_chunk(const IntraArgs& a, const UnitRef& U
     }
     if constexpr (W >= 2) {
       constexpr int s = W - 2;
-      const f8 M2 = *reinterpret_cast<const f8*>(&sm.fac[W][3][sb]);
+      const f8 M2 = *reinterpret_cast<const f8*>(&sm.fac(W, 3)[sb]);
       const v8 A = *reinterpret_cast<const v8*>(&sm.r1[(16 * s + r) * PK + sb]);
       accK[s] = mma32(accK[s], A, cvt8<EXACT>(krj * M2));
       accQ[s] = mma32(accQ[s], A, cvt8<EXACT>(qrj * M2));
     }
     if constexpr (W >= 3) {
       constexpr int s = W - 3;
-      const f8 M3 = *reinterpret_cast<const f8*>(&sm.fac[W][4][sb]);
+      const f8 M3 = *reinterpret_cast<const f8*>(&sm.fac(W, 4)[sb]);
       const v8 A = *reinterpret_cast<const v8*>(&sm.r1[(16 * s + r) * PK + sb]);
       accK[s] = mma32(accK[s], A, cvt8<EXACT>(krj * M3));
       accQ[s] = mma32(accQ[s], A, cvt8<EXACT>(qrj * M3));
@@ -569,16 +596,18 @@ __device__ __forceinline__ void intra_chunk(const IntraArgs& a, const UnitRef& U
 #pragma unroll
         for (int e = 0; e < 8; ++e) { ad[e] = kc[j][e]; bk[e] = krj[e] * iD[e]; bqd[e] = qrj[e] * iD[e]; }
       } else {
-        // mid-tile anchor: 2^(Gt_c - Gt_7) * 2^(Gt_7 - Gt_i); k and q are reloaded
+        // mid-tile anchor: 2^(Gt_c - Gt_7) * 2^(Gt_7 - Gt_i); k, q and g are
+        // reloaded and the tile-local cumsum is recomputed (the same scan, so
+        // the same values), which keeps Gt out of the registers live here
 #pragma unroll
         for (int hf = 0; hf < 2; ++hf) {
           const int ch0 = 32 * j + 4 * gq + 16 * hf;
-          f4 x = {0, 0, 0, 0}, y = {0, 0, 0, 0};
-          if (valid) { x = ld4<DTQ>(a.q, bq + ch0); y = ld4<DTQ>(a.k, bq + ch0); }
+          f4 x = {0, 0, 0, 0}, y = {0, 0, 0, 0}, z = {0, 0, 0, 0};
+          if (valid) { x = ld4<DTQ>(a.q, bq + ch0); y = ld4<DTQ>(a.k, bq + ch0); z = ld4<DTG>(a.g, bq + ch0); }
 #pragma unroll
           for (int e = 0; e < 4; ++e) {
             const int ee = 4 * hf + e;
-            const float gt = Gt[j][ee];
+            const float gt = row_scan16(valid ? z[e] * kLog2e : 0.f);
             const float g7 = row_bcast<7>(gt);
             const float fr = fast_exp2(gt - g7);
             ad[ee] = y[e] * fast_exp2(g7 - gt);
@@ -612,14 +641,16 @@ __device__ __forceinline__ void intra_chunk(const IntraArgs& a, const UnitRef& U
     }
 
     // q*gamma -> GQ (fragment order); beta*gamma*k and lambda*k kept
-    f8 gqv;
+    f8 gqv, lkf, bwf;
     const float bc = beta_c;
 #pragma unroll
     for (int e = 0; e < 8; ++e) {
       gqv[e] = qrj[e] * P[e];
-      lk[j][e] = st(kc[j][e] * Q[e]);
-      bw[j][e] = st(krj[e] * (bc * P[e]));
+      lkf[e] = kc[j][e] * Q[e];
+      bwf[e] = krj[e] * (bc * P[e]);
     }
+    lk[j] = cvt8<EXACT>(lkf);
+    bw[j] = cvt8<EXACT>(bwf);
     *reinterpret_cast<v8*>(oGQ + (chead * (kC / 16) * NJ + (W * NJ + j)) * 512 + l * 8) =
         cvt8<EXACT>(gqv);
   }
@@ -671,22 +702,35 @@ __device__ __forceinline__ void intra_chunk(const IntraArgs& a, const UnitRef& U
 #pragma unroll
   for (int s = 0; s < W; ++s)
     *reinterpret_cast<v4*>(&sm.Lmb[W * (W - 1) / 2 + s][r][4 * gq]) = cvt4<EXACT>(Lk[s]);
-  *reinterpret_cast<f4*>(&sm.Ld[W][r][4 * gq]) = Lk[W];
+  *reinterpret_cast<f4*>(&sm.Ld(W)[r][4 * gq]) = Lk[W];
   __builtin_amdgcn_wave_barrier();
 
-  // diagonal block inverse: column r of T_WW by forward substitution
+  // diagonal block inverse: column r of T_WW by forward substitution.  The
+  // L rows of four substitution steps are read from LDS together before
+  // those steps (one LDS round trip per four rows, not one per row); the
+  // products are summed in the same order either way.
   float x[16];
 #pragma unroll
-  for (int i = 0; i < 16; ++i) {
-    float acc = 0.f;
+  for (int b = 0; b < 4; ++b) {
+    f4 Lb[4][4];
 #pragma unroll
-    for (int m4 = 0; m4 < i; m4 += 4) {
-      const f4 Lrow = *reinterpret_cast<const f4*>(&sm.Ld[W][i][m4]);
+    for (int ii = 0; ii < 4; ++ii)
 #pragma unroll
-      for (int t = 0; t < 4; ++t)
-        if (m4 + t < i) acc += Lrow[t] * x[m4 + t];
+      for (int q = 0; q < 4; ++q)
+        if (4 * q < 4 * b + ii) Lb[ii][q] = *reinterpret_cast<const f4*>(&sm.Ld(W)[4 * b + ii][4 * q]);
+#pragma unroll
+    for (int ii = 0; ii < 4; ++ii) {
+      const int i = 4 * b + ii;
+      float acc = 0.f;
+#pragma unroll
+      for (int m4 = 0; m4 < i; m4 += 4) {
+        const f4 Lrow = Lb[ii][m4 >> 2];
+#pragma unroll
+        for (int t = 0; t < 4; ++t)
+          if (m4 + t < i) acc += Lrow[t] * x[m4 + t];
+      }
+      x[i] = (i < r) ? 0.f : ((i == r) ? 1.f : -acc);
     }
-    x[i] = (i < r) ? 0.f : ((i == r) ? 1.f : -acc);
   }
   if (gq == 0) {
 #pragma unroll
