@@ -42,6 +42,8 @@ struct WsLayout {
   int64_t units_bound;   // workspace chunk units (per segment when segmented)
   int segments;          // dense: launches along T (1 = whole sequence at once)
   int seg_chunks;        // dense: chunks per segment
+  int bufs;              // 2: segments alternate between two sets of intra results
+  size_t sz_W, sz_U, sz_AQ, sz_GQ, sz_LK, sz_GC;  // bytes of one set
 };
 
 bool is_exact(int in_dtype) { return in_dtype == KDA_DTYPE_F32; }
@@ -67,12 +69,33 @@ constexpr double kSegmentBudgetBytes = 100.0 * 1048576.0;
 // 22 + 22 + 20, 232.9 us, whose last round per segment ran a quarter empty).
 constexpr int kIntraSlots = 512;
 
+// Overlapped segments (the state scan of segment s in the same launch as the
+// intra-chunk work of segment s+1) when the state kernel's grid leaves most
+// of the chip free: at most this many 32-column state workgroups (each holds a
+// CU for the whole segment; 24 chains at dv = 128).  Both segments' intra
+// results then live at once, next to the inputs the intra work streams, so a
+// segment's budget is smaller: config 2 (B1 T65536 H16) runs 1 530 us in
+// sequential 100 MiB segments, 1 915 us overlapped at 100 MiB (the two sets
+// and the inputs overflow the 256 MB memory-side cache and the serial scan
+// waits on HBM), 1 239 us overlapped at 48 MiB (32: 1 295, 40: 1 263,
+// 56: 1 263, 64: 1 274).  At 128 state workgroups (32 chains) overlapping
+// gains nothing (1 085 against 1 085 us), at 96 (24 chains) 1 855 -> 1 770 us.
+constexpr int64_t kOverlapMaxStateWgs = 96;
+constexpr double kOverlapSegmentBudgetBytes = 48.0 * 1048576.0;
+
+int64_t col_state_grid(int64_t chains, int dv) { return ((chains + 7) / 8) * 8 * (dv / 32); }
+
+bool overlap_eligible(int B, int H, int dv, int in_dtype) {
+  return !is_exact(in_dtype) && col_state_grid(static_cast<int64_t>(B) * H, dv) <= kOverlapMaxStateWgs;
+}
+
 int dense_segments(int B, int T, int H, int dk, int dv, int in_dtype) {
   const int NT = (T + kC - 1) / kC;
   if (NT <= 1) return 1;
   const size_t es = is_exact(in_dtype) ? 4 : 2;
   const double total = static_cast<double>(B) * NT * H * bytes_per_chunk_head(dk, dv, es);
-  const int s = static_cast<int>(std::ceil(total / kSegmentBudgetBytes));
+  const double budget = overlap_eligible(B, H, dv, in_dtype) ? kOverlapSegmentBudgetBytes : kSegmentBudgetBytes;
+  const int s = static_cast<int>(std::ceil(total / budget));
   return s < 1 ? 1 : (s > NT ? NT : s);
 }
 
@@ -89,7 +112,7 @@ WsLayout ws_layout(int B, int T, int H, int dk, int dv, int32_t n_seqs, int in_d
     const int NT = L.seg_chunks;
     L.segments = dense_segments(B, T, H, dk, dv, in_dtype);
     L.seg_chunks = (L.seg_chunks + L.segments - 1) / L.segments;
-    if (L.segments > 1) {
+    if (L.segments > 1 && !overlap_eligible(B, H, dv, in_dtype)) {
       const int64_t bh = static_cast<int64_t>(B) * H;
       const int m = static_cast<int>(kIntraSlots / std::gcd<int64_t>(kIntraSlots, bh));
       const int up = (L.seg_chunks + m - 1) / m * m;
@@ -99,15 +122,20 @@ WsLayout ws_layout(int B, int T, int H, int dk, int dv, int32_t n_seqs, int in_d
     units = static_cast<int64_t>(B) * L.seg_chunks;
   }
   L.units_bound = units;
+  L.bufs = (n_seqs <= 0 && L.segments > 1 && overlap_eligible(B, H, dv, in_dtype)) ? 2 : 1;
   const int64_t ch = units * H;
   size_t off = 0;
   auto take = [&](size_t bytes) { size_t at = off; off = align_up(off + bytes); return at; };
-  L.W = take(static_cast<size_t>(ch) * kC * dk * es);
-  L.GQ = take(static_cast<size_t>(ch) * kC * dk * es);
-  L.LK = take(static_cast<size_t>(ch) * kC * dk * es);
-  L.U = take(static_cast<size_t>(ch) * kC * dv * es);
-  L.AQ = take(static_cast<size_t>(ch) * kC * kC * es);
-  L.GC = take(static_cast<size_t>(ch) * dk * 4);
+  L.sz_W = L.sz_GQ = L.sz_LK = align_up(static_cast<size_t>(ch) * kC * dk * es);
+  L.sz_U = align_up(static_cast<size_t>(ch) * kC * dv * es);
+  L.sz_AQ = align_up(static_cast<size_t>(ch) * kC * kC * es);
+  L.sz_GC = align_up(static_cast<size_t>(ch) * dk * 4);
+  L.W = take(L.sz_W * L.bufs);
+  L.GQ = take(L.sz_GQ * L.bufs);
+  L.LK = take(L.sz_LK * L.bufs);
+  L.U = take(L.sz_U * L.bufs);
+  L.AQ = take(L.sz_AQ * L.bufs);
+  L.GC = take(L.sz_GC * L.bufs);
   if (n_seqs > 0) {
     L.cu_clamped = take(static_cast<size_t>(n_seqs + 1) * 4);
     L.chunk_off = take(static_cast<size_t>(n_seqs + 1) * 4);
@@ -223,15 +251,57 @@ int chunk_fwd_impl(hipStream_t stream, const void* q, const void* k, const void*
   sa.W = ia.W; sa.U = ia.U; sa.AQ = ia.AQ; sa.GQ = ia.GQ; sa.LK = ia.LK; sa.GC = ia.GC;
   sa.o = o;
   sa.status = exact ? nullptr : status;
-  const int splits = dv / 32;
   const int64_t chains = static_cast<int64_t>(G.N) * H;
-  const int64_t state_grid = ((chains + 7) / 8) * 8 * splits;
+  const int64_t state_grid = col_state_grid(chains, dv);
   if (state_grid > 0x7FFFFFFFLL) return fail(KDA_ERR_INVALID_ARGUMENT, "too many chains");
 
   // Segments along T (dense only): the state leaves one segment in `carry`
   // and enters the next from it (each state workgroup reads its slice before
   // writing it, so the same buffer serves as both).
   float* carry = (L.segments > 1) ? (ht != nullptr ? ht : at<float>(ws, L.state)) : ht;
+  const int out_dt = out_dtype == KDA_DTYPE_BF16 ? 1 : 0;
+  if (!varlen && pro == nullptr && L.bufs == 2) {
+    // Overlapped segments: intra(0); then per launch the state scan of
+    // segment s (results set s % 2) and the intra work of segment s+1 (set
+    // (s+1) % 2); then the state scan of the last segment.
+    auto set_bufs = [&](int b) {
+      ia.W = at<char>(ws, L.W) + b * L.sz_W;
+      ia.GQ = at<char>(ws, L.GQ) + b * L.sz_GQ;
+      ia.LK = at<char>(ws, L.LK) + b * L.sz_LK;
+      ia.U = at<char>(ws, L.U) + b * L.sz_U;
+      ia.AQ = at<char>(ws, L.AQ) + b * L.sz_AQ;
+      ia.GC = reinterpret_cast<float*>(at<char>(ws, L.GC) + b * L.sz_GC);
+    };
+    auto seg_geom = [&](int sgi) {
+      kda::Geom g2 = G;
+      g2.n0 = sgi * L.seg_chunks;
+      g2.NTS = std::min(L.seg_chunks, G.NT - g2.n0);
+      return g2;
+    };
+    set_bufs(0);
+    ia.geom = seg_geom(0);
+    hipError_t e = kda::launch_intra(ia, dk, dtq, dtg, static_cast<int>(static_cast<int64_t>(B) * ia.geom.NTS * H),
+                                     stream);
+    if (e != hipSuccess) return hip_fail(e, "intra kernel launch");
+    ia.status_clear = nullptr;
+    for (int sgi = 0; sgi < L.segments; ++sgi) {
+      sa.geom = seg_geom(sgi);
+      sa.W = ia.W; sa.U = ia.U; sa.AQ = ia.AQ; sa.GQ = ia.GQ; sa.LK = ia.LK; sa.GC = ia.GC;
+      sa.h0 = (sgi == 0) ? h0 : carry;
+      sa.ht = carry;
+      if (sgi + 1 < L.segments) {
+        set_bufs((sgi + 1) & 1);
+        ia.geom = seg_geom(sgi + 1);
+        e = kda::launch_overlap(ia, sa, dk, dtq, dtg, out_dt, static_cast<int>(state_grid),
+                                static_cast<int>(static_cast<int64_t>(B) * ia.geom.NTS * H), stream);
+        if (e != hipSuccess) return hip_fail(e, "overlapped segment launch");
+      } else {
+        e = kda::launch_state(sa, dk, exact, out_dt, static_cast<int>(state_grid), stream);
+        if (e != hipSuccess) return hip_fail(e, "state kernel launch");
+      }
+    }
+    return KDA_OK;
+  }
   for (int sgi = 0; sgi < L.segments; ++sgi) {
     if (!varlen) {
       G.n0 = sgi * L.seg_chunks;
@@ -248,8 +318,7 @@ int chunk_fwd_impl(hipStream_t stream, const void* q, const void* k, const void*
     }
     sa.h0 = (sgi == 0) ? h0 : carry;
     sa.ht = (L.segments > 1) ? carry : ht;
-    hipError_t e = kda::launch_state(sa, dk, exact, out_dtype == KDA_DTYPE_BF16 ? 1 : 0,
-                                     static_cast<int>(state_grid), stream);
+    hipError_t e = kda::launch_state(sa, dk, exact, out_dt, static_cast<int>(state_grid), stream);
     if (e != hipSuccess) return hip_fail(e, "state kernel launch");
   }
   if (ia.status_clear != nullptr) {

@@ -1837,6 +1837,87 @@ void kda_state_wide_kernel(StateArgs a) {
 }
 
 // ----------------------------------------------------------------------------
+// Overlapped segments: the state scan of segment s and the intra-chunk work
+// of segment s+1 in one launch (fp16 operands).
+//
+// With few chains the 32-column state workgroups occupy few CUs (one each:
+// 133 KiB of LDS) and the serial chain leaves the rest of the chip idle.
+// Workgroups below `n_state` take the state role (kda_state_col_kernel's
+// mapping; they are dispatched first and land one per CU); the others take
+// two chunk-heads of the next segment each (waves 0-3 and 4-7, one
+// IntraSmem each, in step: both run the same barriers).  The two segments use
+// different halves of a double workspace, so no workgroup waits for another.
+// ----------------------------------------------------------------------------
+// barriers of intra_chunk on the staged 16-bit path: the staging barrier and #1-#3
+constexpr int kIntraBarriers = 4;
+
+template <int DK, int DV>
+struct OverlapLds {
+  static constexpr size_t kIntra = 2 * sizeof(IntraSmem<DK, DV, false>);
+  static constexpr size_t kState = sizeof(ColSmem<DK>);
+  static constexpr size_t kBytes = kIntra > kState ? kIntra : kState;
+};
+
+template <int DK, int DV, int DTQ, int DTG, int OUT_DT>
+__global__ __launch_bounds__(512, 1)
+void kda_overlap_kernel(IntraArgs ia, StateArgs sa, int n_state) {
+  __shared__ __attribute__((aligned(16))) unsigned char lds[OverlapLds<DK, DV>::kBytes];
+  const int wave = threadIdx.x >> 6;
+  if (static_cast<int>(blockIdx.x) < n_state) {
+    constexpr int SPLITS = DV / 32;
+    ColSmem<DK>& sm = *reinterpret_cast<ColSmem<DK>*>(lds);
+    const Geom& G = sa.geom;
+    const int H = G.H;
+    const int x = blockIdx.x;
+    const int xcd = x & 7;
+    const int kk = x >> 3;
+    const int slot = kk / SPLITS;
+    const int split = kk - slot * SPLITS;
+    const int chain = slot * 8 + xcd;
+    if (chain >= G.N * H) return;  // uniform per workgroup
+    const int seq_rank = chain / H;
+    const int h = chain - seq_rank * H;
+    const int seq = (G.order != nullptr) ? G.order[seq_rank] : seq_rank;
+    static_assert(kColComputeWaves == 2 && kColProducers == 4, "six working waves");
+    switch (wave) {
+      case 0: col_chain<DK, DV, OUT_DT, 0>(sa, sm, seq, h, split); break;
+      case 1: col_chain<DK, DV, OUT_DT, 1>(sa, sm, seq, h, split); break;
+      case 2: col_producer<DK, DV, OUT_DT, 0>(sa, sm, seq, h, split); break;
+      case 3: col_producer<DK, DV, OUT_DT, 1>(sa, sm, seq, h, split); break;
+      case 4: col_producer<DK, DV, OUT_DT, 2>(sa, sm, seq, h, split); break;
+      case 5: col_producer<DK, DV, OUT_DT, 3>(sa, sm, seq, h, split); break;
+      default: {
+        // the two spare waves join every barrier of the state role
+        const int nb = chain_ref(G, seq).nchunks;
+        for (int i = 0; i < (nb > 0 ? nb + 1 : 0); ++i) lds_barrier();
+        break;
+      }
+    }
+  } else {
+    const int grp = wave >> 2;
+    IntraSmem<DK, DV, false>& sm =
+        *reinterpret_cast<IntraSmem<DK, DV, false>*>(lds + grp * sizeof(IntraSmem<DK, DV, false>));
+    const int H = ia.geom.H;
+    const int x = 2 * (static_cast<int>(blockIdx.x) - n_state) + grp;
+    if (x < ia.total) {
+      const int u = x / H;
+      const int h = x - u * H;
+      const UnitRef U = unit_ref(ia.geom, u);
+      const int64_t chead = static_cast<int64_t>(u) * H + h;
+      switch (wave & 3) {
+        case 0: intra_chunk<DK, DV, DTQ, DTG, false, 0, false>(ia, U, h, chead, sm); break;
+        case 1: intra_chunk<DK, DV, DTQ, DTG, false, 1, false>(ia, U, h, chead, sm); break;
+        case 2: intra_chunk<DK, DV, DTQ, DTG, false, 2, false>(ia, U, h, chead, sm); break;
+        default: intra_chunk<DK, DV, DTQ, DTG, false, 3, false>(ia, U, h, chead, sm); break;
+      }
+    } else {
+      // no chunk-head for this group: join the other group's barriers
+      for (int i = 0; i < kIntraBarriers; ++i) lds_barrier();
+    }
+  }
+}
+
+// ----------------------------------------------------------------------------
 // host-side launchers
 // ----------------------------------------------------------------------------
 template <int DK, int DV, int DTQ, int DTG, bool EXACT, bool PRO = false>
@@ -1892,6 +1973,35 @@ hipError_t launch_intra_prologue(const IntraArgs& a, int d, int dtg, int grid, h
   if (d == 128 && dtg == 0) return launch_intra_t<128, 128, 1, 0, false, true>(a, grid, s);
   if (d == 64 && dtg == 1) return launch_intra_t<64, 64, 1, 1, false, true>(a, grid, s);
   if (d == 64 && dtg == 0) return launch_intra_t<64, 64, 1, 0, false, true>(a, grid, s);
+  return hipErrorInvalidValue;
+}
+
+// One launch: the state role for segment s (n_state workgroups, the 32-column
+// state kernel's grid) and the intra role for segment s+1 (ia.total
+// chunk-heads, two per workgroup).
+hipError_t launch_overlap(const IntraArgs& ia0, const StateArgs& sa, int d, int dtq, int dtg, int out_dt,
+                          int n_state, int intra_units, hipStream_t s) {
+  IntraArgs ia = ia0;
+  ia.total = intra_units;
+  const int grid = n_state + (intra_units + 1) / 2;
+#define KDA_OVL(D, Q, G, O)                                                                            \
+  if (d == D && dtq == Q && dtg == G && out_dt == O) {                                                 \
+    hipLaunchKernelGGL((kda_overlap_kernel<D, D, Q, G, O>), dim3(grid), dim3(512), 0, s, ia, sa, n_state); \
+    return hipGetLastError();                                                                          \
+  }
+  KDA_OVL(128, 1, 1, 0)
+  KDA_OVL(128, 1, 1, 1)
+  KDA_OVL(128, 2, 2, 0)
+  KDA_OVL(128, 2, 2, 1)
+  KDA_OVL(128, 1, 0, 0)
+  KDA_OVL(128, 1, 0, 1)
+  KDA_OVL(64, 1, 1, 0)
+  KDA_OVL(64, 1, 1, 1)
+  KDA_OVL(64, 2, 2, 0)
+  KDA_OVL(64, 2, 2, 1)
+  KDA_OVL(64, 1, 0, 0)
+  KDA_OVL(64, 1, 0, 1)
+#undef KDA_OVL
   return hipErrorInvalidValue;
 }
 

@@ -43,6 +43,7 @@ struct IntraArgs {
   const float* cb[3];
   int K;
   int* status_clear;   // non-null: the launch zeroes the call's status word
+  int total;           // chunk-heads of the launch (overlapped-segment launch only)
 };
 
 struct StateArgs {
@@ -196,6 +197,11 @@ hipError_t launch_intra(const IntraArgs& a, int d, int dtq, int dtg, int grid, h
 hipError_t launch_intra_prologue(const IntraArgs& a, int d, int dtg, int grid, hipStream_t s);
 constexpr int kFusedConvTaps = 4;
 hipError_t launch_state(const StateArgs& a, int d, bool exact, int out_dt, int grid, hipStream_t s);
+// state scan of one segment (n_state workgroups of the 32-column state
+// kernel's grid) and intra-chunk work of the next (intra_units chunk-heads)
+// in one launch; fp16 operands, no fused prologue
+hipError_t launch_overlap(const IntraArgs& ia, const StateArgs& sa, int d, int dtq, int dtg, int out_dt,
+                          int n_state, int intra_units, hipStream_t s);
 hipError_t launch_varlen_prep(const int32_t* cu, int N, int T, int32_t* cu_clamped,
                               int32_t* chunk_off, int32_t* n_units, int32_t* order,
                               int32_t* flags, hipStream_t s);

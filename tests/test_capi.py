@@ -39,15 +39,26 @@ SEGMENT_BUDGET = 100 * 1048576   # bytes of intra-chunk results per segment of a
 
 INTRA_SLOTS = 512   # intra workgroups resident at once: segments are rounded up to whole rounds
 
+# Calls whose 32-column state grid is at most 96 workgroups overlap each
+# segment's state scan with the next segment's intra work: two sets of intra
+# results, 48 MiB segments, no rounding to whole intra rounds.
+OVERLAP_BUDGET = 48 * 1048576
+OVERLAP_MAX_STATE_WGS = 96
+
+
+def overlap_eligible(B, H, dv, es):
+    return es == 2 and -(-(B * H) // 8) * 8 * (dv // 32) <= OVERLAP_MAX_STATE_WGS
+
 
 def dense_segments(B, T, H, dk, dv, es):
     NT = (T + C - 1) // C
     if NT <= 1:
         return 1, NT
     total = B * NT * H * (C * (3 * dk + dv + C) * es + dk * 4)
-    s = min(max(-(-total // SEGMENT_BUDGET), 1), NT)
+    ovl = overlap_eligible(B, H, dv, es)
+    s = min(max(-(-total // (OVERLAP_BUDGET if ovl else SEGMENT_BUDGET)), 1), NT)
     seg = -(-NT // s)
-    if s > 1:
+    if s > 1 and not ovl:
         m = INTRA_SLOTS // math.gcd(INTRA_SLOTS, B * H)
         up = -(-seg // m) * m
         if up < NT:
@@ -58,11 +69,13 @@ def dense_segments(B, T, H, dk, dv, es):
 def dense_ws_bytes(B, T, H, dk, dv, es):
     """Dense workspace size: W, gamma*q, lambda*k [units*H][C][dk], U [..][C][dv],
     Aqk [..][C][C] in operand precision, gamma_C [..][dk] fp32, each 256-B aligned,
-    for one segment's units; plus the carried state when the call is segmented."""
+    for one segment's units (two sets when segments overlap); plus the carried
+    state when the call is segmented."""
     segments, seg = dense_segments(B, T, H, dk, dv, es)
     ch = B * seg * H
-    arrays = [ch * C * dk * es, ch * C * dk * es, ch * C * dk * es, ch * C * dv * es, ch * C * C * es,
-              ch * dk * 4]
+    bufs = 2 if (segments > 1 and overlap_eligible(B, H, dv, es)) else 1
+    arrays = [bufs * _align(n) for n in (ch * C * dk * es, ch * C * dk * es, ch * C * dk * es, ch * C * dv * es,
+                                         ch * C * C * es, ch * dk * 4)]
     if segments > 1:
         arrays.append(B * H * dk * dv * 4)
     arrays.append(4)   # the call's status word
@@ -74,7 +87,11 @@ def test_segment_policy():
     # up to 24 so each segment's 4 * 16 * 24 = 1536 intra workgroups are whole rounds
     assert dense_segments(4, 4096, 16, 128, 128, 2) == (3, 24)
     assert dense_segments(2, 1000, 2, 128, 128, 2) == (1, 16)
-    assert dense_segments(1, 65536, 16, 128, 128, 2) == (11, 96)
+    # config 2 (16 chains: 64 state workgroups) overlaps its segments: 48 MiB
+    # each, 25 segments of 41 chunks (the last 40)
+    assert overlap_eligible(1, 16, 128, 2) and not overlap_eligible(4, 16, 128, 2)
+    assert dense_segments(1, 65536, 16, 128, 128, 2) == (25, 41)
+    assert not overlap_eligible(1, 16, 128, 4)   # exact mode never overlaps
 
 
 def varlen_ws_bytes(T, N, H, dk, dv, es):
@@ -106,7 +123,8 @@ def test_abi_version(L):
 
 
 @pytest.mark.parametrize("B,T,H,d", [(1, 512, 4, 64), (4, 4096, 16, 128), (2, 1, 3, 128),
-                                     (3, 65, 2, 64), (1, 0, 1, 64)])
+                                     (3, 65, 2, 64), (1, 0, 1, 64), (1, 65536, 16, 128),
+                                     (1, 100000, 3, 128), (1, 100000, 3, 64), (2, 32768, 16, 128)])
 @pytest.mark.parametrize("code,es", [(0, 4), (1, 2), (2, 2), (3, 2)])
 def test_dense_workspace_size(L, B, T, H, d, code, es):
     assert L.kda_chunk_fwd_workspace(B, T, H, d, d, C, 0, code) == dense_ws_bytes(B, T, H, d, d, es)

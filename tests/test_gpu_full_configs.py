@@ -152,3 +152,38 @@ def test_long_two_chain_call_against_oracle(cuda):
                                     output_final_state=False)
     torch.cuda.synchronize()
     assert torch.equal(o2, o)
+
+
+@pytest.mark.parametrize("dd", [128, 64])
+def test_overlapped_segments_odd_chunk_heads(cuda, dd):
+    """B1 T100000 H3: three chains, few enough that each segment's state scan
+    runs in one launch with the next segment's intra work; every segment holds
+    an odd number of chunk-heads (the last workgroup's second group idles).
+    Two chains against the oracle; the call split in two with the state carried
+    across gives the same o and final state bit for bit; bf16 o is the fp32 o
+    rounded."""
+    import axiom_amd
+    from tests.test_capi import dense_segments, overlap_eligible
+    B, T, H = 1, 100000, 3
+    segments, seg = dense_segments(B, T, H, dd, dd, 2)
+    NT = -(-T // 64)
+    # some segment after the first (their intra work runs in the overlapped
+    # launches) has an odd number of chunk-heads
+    assert overlap_eligible(B, H, dd, 2) and segments > 1
+    assert any(B * min(seg, NT - i * seg) * H % 2 == 1 for i in range(1, segments))
+    d = make_inputs_device(B, T, H, dd, dd, seed=107 + dd, device=cuda, h0_std=0.02)
+    print(f"[full] overlapped segments d={dd}", flush=True)
+    o, ht = _fwd(d, h0=d["h0"])
+    hc = host_chains(d, 0, [0, 2])
+    o_ref, ht_ref = K.chunk_fwd(hc["q"], hc["k"], hc["v"], hc["g"], hc["beta"],
+                                h0=d["h0"][:, [0, 2]].cpu().numpy(), chunk=64)
+    assert_close("o", o[:, :, [0, 2]], o_ref, TOL["bf16"])
+    assert_close("ht", ht[:, [0, 2]], ht_ref, TOL["bf16"])
+    half = 64 * 781
+    o1, h1 = _fwd(_slice(d, 0, half), h0=d["h0"])
+    o2, h2 = _fwd(_slice(d, half, T), h0=h1)
+    assert torch.equal(torch.cat([o1, o2], dim=1), o) and torch.equal(h2, ht)
+    ob, _ = axiom_amd.kda_chunk_fwd(d["q"], d["k"], d["v"], d["g"], d["beta"], initial_state=d["h0"],
+                                    out_dtype=torch.bfloat16)
+    torch.cuda.synchronize()
+    assert torch.equal(ob, o.to(torch.bfloat16))
