@@ -154,8 +154,8 @@ def test_long_two_chain_call_against_oracle(cuda):
     assert torch.equal(o2, o)
 
 
-@pytest.mark.parametrize("dd", [128, 64])
-def test_overlapped_segments_odd_chunk_heads(cuda, dd):
+@pytest.mark.parametrize("dd,prec", [(128, "bf16"), (64, "bf16"), (128, "fp16"), (128, "bf16_f32gates")])
+def test_overlapped_segments_odd_chunk_heads(cuda, dd, prec):
     """B1 T100000 H3: three chains, few enough that each segment's state scan
     runs in one launch with the next segment's intra work; every segment holds
     an odd number of chunk-heads (the last workgroup's second group idles).
@@ -172,13 +172,18 @@ def test_overlapped_segments_odd_chunk_heads(cuda, dd):
     assert overlap_eligible(B, H, dd, 2) and segments > 1
     assert any(B * min(seg, NT - i * seg) * H % 2 == 1 for i in range(1, segments))
     d = make_inputs_device(B, T, H, dd, dd, seed=107 + dd, device=cuda, h0_std=0.02)
-    print(f"[full] overlapped segments d={dd}", flush=True)
+    if prec == "fp16":
+        d.update({n: d[n].to(torch.float16) for n in ("q", "k", "v", "g", "beta")})
+    elif prec == "bf16_f32gates":
+        d.update({n: d[n].float() for n in ("g", "beta")})
+    print(f"[full] overlapped segments d={dd} {prec}", flush=True)
     o, ht = _fwd(d, h0=d["h0"])
     hc = host_chains(d, 0, [0, 2])
     o_ref, ht_ref = K.chunk_fwd(hc["q"], hc["k"], hc["v"], hc["g"], hc["beta"],
                                 h0=d["h0"][:, [0, 2]].cpu().numpy(), chunk=64)
-    assert_close("o", o[:, :, [0, 2]], o_ref, TOL["bf16"])
-    assert_close("ht", ht[:, [0, 2]], ht_ref, TOL["bf16"])
+    tol = TOL["fp16" if prec == "fp16" else "bf16"]
+    assert_close("o", o[:, :, [0, 2]], o_ref, tol)
+    assert_close("ht", ht[:, [0, 2]], ht_ref, tol)
     half = 64 * 781
     o1, h1 = _fwd(_slice(d, 0, half), h0=d["h0"])
     o2, h2 = _fwd(_slice(d, half, T), h0=h1)
