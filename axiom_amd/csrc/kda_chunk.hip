@@ -665,9 +665,11 @@ __device__ __forceinline__ void intra_chunk(const IntraArgs& a, const UnitRef& U
   f4 Lk[W + 1];
 #pragma unroll
   for (int s = 0; s <= W; ++s) Lk[s] = accK[s] * beta_c;
-  // Aqk fragments for the state kernel: row tile W, K step jj pairs key tiles (2jj, 2jj+1)
+  // Aqk fragments for the state kernel: row tile W, K step jj pairs key tiles
+  // (2jj, 2jj+1).  Row tiles 0 and 1 have no keys in tiles 2 and 3: their
+  // jj = 1 fragment is zero, is never read, and is not stored.
 #pragma unroll
-  for (int jj = 0; jj < 2; ++jj) {
+  for (int jj = 0; jj < ((W < 2) ? 1 : 2); ++jj) {
     f8 x;
 #pragma unroll
     for (int hf = 0; hf < 2; ++hf) {
