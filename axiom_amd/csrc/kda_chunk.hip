@@ -1129,11 +1129,13 @@ void kda_state_kernel(StateArgs a) {
 //   * v~ row tiles, two at a time, are the B fragment over 32 keys.
 // Only the dv-independent A operands (W, gamma*q, Aqk, lambda*k) and gamma_C
 // are shared: per chunk four producer-only waves copy them once per
-// workgroup from the workspace into one of two LDS buffers by direct
-// global->LDS loads (16 B per lane, fragment order, so every LDS read is a
-// conflict-free 16 B per lane), one chunk ahead.  The compute waves issue no
-// copies of their own (a wave issues memory instructions in order, so a deep
-// copy queue would stall its MFMAs).  One barrier per chunk.
+// workgroup from the workspace into one of two LDS buffers (16 B per lane,
+// fragment order, so every LDS read is a conflict-free 16 B per lane).  The
+// copy runs two chunks ahead: a producer loads chunk n+2 into registers
+// while the compute waves work on chunk n, and writes chunk n+1 (loaded one
+// step earlier) into the free LDS buffer.  The compute waves issue no copies
+// of their own (a wave issues memory instructions in order, so a deep copy
+// queue would stall its MFMAs).  One barrier per chunk.
 // ----------------------------------------------------------------------------
 template <int DK>
 struct ColLayout {
@@ -1168,48 +1170,10 @@ constexpr int kColProducers = 4;
 constexpr int kColComputeWaves = 2;
 constexpr int kColTilesPerWave = 2 / kColComputeWaves;
 
-// Copy producer P's share of the operands of chunk-head ch into an LDS buffer
-// (fragment-ordered 1 KiB blocks: lane l moves bytes 16l..16l+15): every
-// fourth shared fragment, the U block of row tile P for this workgroup's two
-// value tiles, and (last producer) gamma_C.
-template <int DK, int DV, int P>
-__device__ __forceinline__ void col_stage(const StateArgs& a, int64_t ch, int split, unsigned char* dst,
-                                          int l) {
-  typedef ColLayout<DK> LY;
-  const _Float16* iW = static_cast<const _Float16*>(a.W);
-  const _Float16* iQ = static_cast<const _Float16*>(a.GQ);
-  const _Float16* iL = static_cast<const _Float16*>(a.LK);
-  const _Float16* iA = static_cast<const _Float16*>(a.AQ);
-#pragma unroll
-  for (int f = P; f < LY::NF; f += kColProducers) {
-    const _Float16* src;
-    if (f < LY::OFF_Q) src = iW + (ch * LY::FW + f) * 512;
-    else if (f < LY::OFF_L) src = iQ + (ch * LY::FW + (f - LY::OFF_Q)) * 512;
-    else if (f < LY::OFF_A) src = iL + (ch * LY::FL + (f - LY::OFF_L)) * 512;
-    else {
-      const int ai = f - LY::OFF_A;                 // 0..5 -> (ct, jj) = 00 10 20 21 30 31
-      const int gidx = (ai < 2) ? 2 * ai : ai + 2;  // index ct*2 + jj in the workspace
-      src = iA + (ch * 8 + gidx) * 512;
-    }
-    __builtin_amdgcn_global_load_lds(src + l * 8, dst + f * 1024, 16, 0, 0);
-  }
-  {
-    static_assert(kColProducers == 4, "one U row tile per producer");
-    const _Float16* usrc = static_cast<const _Float16*>(a.U) +
-                           (ch * 4 * (DV / 16) + P * (DV / 16) + 2 * split) * 256 + l * 8;
-    unsigned char* udst = dst + LY::OFF_U + P * 1024;
-    __builtin_amdgcn_global_load_lds(usrc, udst, 16, 0, 0);
-  }
-  if constexpr (P == kColProducers - 1) {
-    const _Float16* gsrc = reinterpret_cast<const _Float16*>(a.GC + ch * DK + l * 4);
-    unsigned char* gdst = dst + LY::OFF_G;
-    if (l < DK / 4) __builtin_amdgcn_global_load_lds(gsrc, gdst, 16, 0, 0);
-  }
-}
-
 // Producer P's share of the o rows of one chunk: LDS [64 rows][32 columns]
-// (fp32, or bf16 when OUT_DT == 1) to the workgroup's 32 columns of o, 16 B
-// per lane, rows past the chunk's end skipped.  The stored values are kept
+// (fp32, or bf16 when OUT_DT == 1; the 16-byte chunks of rows with bit 2 set
+// are swapped between the row's halves, see col_put_o) to the workgroup's 32
+// columns of o, 16 B per lane, rows past the chunk's end skipped.  The stored values are kept
 // in `vs` (and whether each was stored in `ok`) for the caller's range check,
 // which it runs once the next chunk's copies are in flight.
 template <int OUT_DT>
@@ -1236,7 +1200,8 @@ __device__ __forceinline__ void col_store_rows(const StateArgs& a, const unsigne
     if (ins < SS::NI) {
       const int row = SS::RPI * ins + l / SS::LPR;
       const int cb = (l % SS::LPR) * 16;       // byte offset inside the 32-column row
-      vs[k] = *reinterpret_cast<const uint4*>(ob + row * (32 * SS::ES) + cb);
+      const int pcb = ((l % SS::LPR) ^ ((SS::LPR / 2) * ((row >> 2) & 1))) * 16;   // swizzled chunk
+      vs[k] = *reinterpret_cast<const uint4*>(ob + row * (32 * SS::ES) + pcb);
       ok[k] = row < len;
       if (ok[k]) {
         unsigned char* dst = static_cast<unsigned char*>(a.o) +
@@ -1280,46 +1245,6 @@ __device__ __forceinline__ ChainRef chain_ref(const Geom& G, int seq) {
   return c;
 }
 
-// Producer wave P: while the compute waves work on chunk n it stores o of
-// chunk n-1 (from LDS) and fills its share of the buffer of chunk n+1, then
-// joins the one barrier per chunk once all of it has landed.  The compute
-// waves issue no global memory operation inside the chunk loop: a wave issues
-// memory instructions in order, so queueing behind these copies would stall
-// their MFMAs.
-template <int DK, int DV, int OUT_DT, int P>
-__device__ __forceinline__ void col_producer(const StateArgs& a, ColSmem<DK>& sm, int seq, int h,
-                                             int split) {
-  const ChainRef c = chain_ref(a.geom, seq);
-  const int H = a.geom.H;
-  const int l = threadIdx.x & 63;
-  if (c.nchunks <= 0) return;
-  constexpr int NS = ColStoreShape<OUT_DT>::NS;
-  uint4 vs[NS];
-  bool ok[NS];
-  float mag = 0.f;
-  col_stage<DK, DV, P>(a, static_cast<int64_t>(c.u0) * H + h, split, sm.buf[0], l);
-  wait_vmem_all();
-  lds_barrier();
-  for (int n = 0; n < c.nchunks; ++n) {
-    const bool st = n > 0;
-    if (st)
-      col_store_rows<DV, OUT_DT, P>(a, sm.obuf[(n - 1) & 1], c.tok0 + static_cast<int64_t>(n - 1) * kC,
-                                    min(kC, c.seq_len - (n - 1) * kC), h, split, l, vs, ok);
-    if (n + 1 < c.nchunks)
-      col_stage<DK, DV, P>(a, static_cast<int64_t>(c.u0 + n + 1) * H + h, split, sm.buf[(n + 1) & 1], l);
-    // the range check of the stored o rows runs while the copies are in flight
-    __builtin_amdgcn_sched_barrier(0);
-    if (st) mag += col_stored_mag<OUT_DT>(vs, ok);
-    wait_vmem_all();
-    lds_barrier();
-  }
-  const int nl = c.nchunks - 1;
-  col_store_rows<DV, OUT_DT, P>(a, sm.obuf[nl & 1], c.tok0 + static_cast<int64_t>(nl) * kC,
-                                min(kC, c.seq_len - nl * kC), h, split, l, vs, ok);
-  mag += col_stored_mag<OUT_DT>(vs, ok);
-  report_nonfinite(a.status, mag);
-}
-
 // Calls f(std::integral_constant<int, I>{}) for I = B .. E-1, expanded at
 // compile time (a loop over a long, branchy body is not always unrolled).
 template <int B, int E, typename F>
@@ -1328,6 +1253,121 @@ __device__ __forceinline__ void static_for(F&& f) {
     f(std::integral_constant<int, B>{});
     static_for<B + 1, E>(f);
   }
+}
+
+// One chunk's share of producer P (every fourth shared fragment, the U block
+// of row tile P for the workgroup's two value tiles, and for the last
+// producer gamma_C), held in registers between its global load and its
+// write into an LDS buffer.
+typedef unsigned int u32x4 __attribute__((ext_vector_type(4)));
+template <int DK, int P>
+struct ColRegs {
+  static constexpr int NFP = (ColLayout<DK>::NF - P + kColProducers - 1) / kColProducers;
+  u32x4 f[NFP];
+  u32x4 u;
+  u32x4 g;
+};
+
+template <int DK, int DV, int P>
+__device__ __forceinline__ void col_load_regs(const StateArgs& a, int64_t ch, int split, int l,
+                                              ColRegs<DK, P>& R) {
+  typedef ColLayout<DK> LY;
+  const _Float16* iW = static_cast<const _Float16*>(a.W);
+  const _Float16* iQ = static_cast<const _Float16*>(a.GQ);
+  const _Float16* iL = static_cast<const _Float16*>(a.LK);
+  const _Float16* iA = static_cast<const _Float16*>(a.AQ);
+  static_for<0, ColRegs<DK, P>::NFP>([&](auto kc) {
+    constexpr int f = P + kColProducers * decltype(kc)::value;
+    const _Float16* src;
+    if constexpr (f < LY::OFF_Q) src = iW + (ch * LY::FW + f) * 512;
+    else if constexpr (f < LY::OFF_L) src = iQ + (ch * LY::FW + (f - LY::OFF_Q)) * 512;
+    else if constexpr (f < LY::OFF_A) src = iL + (ch * LY::FL + (f - LY::OFF_L)) * 512;
+    else {
+      constexpr int ai = f - LY::OFF_A;                 // 0..5 -> (ct, jj) = 00 10 20 21 30 31
+      constexpr int gidx = (ai < 2) ? 2 * ai : ai + 2;  // index ct*2 + jj in the workspace
+      src = iA + (ch * 8 + gidx) * 512;
+    }
+    R.f[decltype(kc)::value] = *reinterpret_cast<const u32x4*>(src + l * 8);
+  });
+  static_assert(kColProducers == 4, "one U row tile per producer");
+  R.u = *reinterpret_cast<const u32x4*>(static_cast<const _Float16*>(a.U) +
+                                        (ch * 4 * (DV / 16) + P * (DV / 16) + 2 * split) * 256 + l * 8);
+  if constexpr (P == kColProducers - 1) {
+    R.g = u32x4{0, 0, 0, 0};
+    if (l < DK / 4) R.g = *reinterpret_cast<const u32x4*>(a.GC + ch * DK + l * 4);
+  }
+}
+
+// The registers of one chunk into an LDS buffer, in the fragment order the
+// compute waves read (lane l's 16 bytes at byte 16 l of each 1 KiB block).
+template <int DK, int P>
+__device__ __forceinline__ void col_write_regs(unsigned char* dst, int l, const ColRegs<DK, P>& R) {
+  typedef ColLayout<DK> LY;
+  static_for<0, ColRegs<DK, P>::NFP>([&](auto kc) {
+    constexpr int k = decltype(kc)::value;
+    *reinterpret_cast<u32x4*>(dst + (P + kColProducers * k) * 1024 + l * 16) = R.f[k];
+  });
+  *reinterpret_cast<u32x4*>(dst + LY::OFF_U + P * 1024 + l * 16) = R.u;
+  if constexpr (P == kColProducers - 1)
+    if (l < DK / 4) *reinterpret_cast<u32x4*>(dst + LY::OFF_G + l * 16) = R.g;
+}
+
+// One chunk step of producer P while the compute waves work on chunk n: store
+// o of chunk n-1 (from LDS), load chunk n+2 into Rn (which held chunk n, in
+// LDS since the last barrier; past the chain's end the last chunk is loaded
+// again), write chunk n+1 from Rn1 into the free buffer, then join the one
+// barrier per chunk.  The write waits only for Rn1's loads, issued a step
+// earlier, so each load has two chunk steps to arrive.
+template <int DK, int DV, int OUT_DT, int P>
+__device__ __forceinline__ void col_producer_step(const StateArgs& a, ColSmem<DK>& sm, const ChainRef& c, int H,
+                                                  int h, int split, int l, int n, ColRegs<DK, P>& Rn,
+                                                  ColRegs<DK, P>& Rn1, float& mag) {
+  constexpr int NS = ColStoreShape<OUT_DT>::NS;
+  uint4 vs[NS];
+  bool ok[NS];
+  const bool st = n > 0;
+  if (st)
+    col_store_rows<DV, OUT_DT, P>(a, sm.obuf[(n - 1) & 1], c.tok0 + static_cast<int64_t>(n - 1) * kC,
+                                  min(kC, c.seq_len - (n - 1) * kC), h, split, l, vs, ok);
+  col_load_regs<DK, DV, P>(a, static_cast<int64_t>(c.u0 + min(n + 2, c.nchunks - 1)) * H + h, split, l, Rn);
+  // the range check of the stored o rows runs while the loads are in flight
+  __builtin_amdgcn_sched_barrier(0);
+  if (st) mag += col_stored_mag<OUT_DT>(vs, ok);
+  if (n + 1 < c.nchunks) col_write_regs<DK, P>(sm.buf[(n + 1) & 1], l, Rn1);
+  lds_barrier();
+}
+
+// Producer wave P of a state workgroup.  The compute waves issue no global
+// memory operation inside the chunk loop: a wave issues memory instructions
+// in order, so queueing behind these copies would stall their MFMAs.
+template <int DK, int DV, int OUT_DT, int P>
+__device__ __forceinline__ void col_producer(const StateArgs& a, ColSmem<DK>& sm, int seq, int h,
+                                             int split) {
+  const ChainRef c = chain_ref(a.geom, seq);
+  const int H = a.geom.H;
+  const int l = threadIdx.x & 63;
+  if (c.nchunks <= 0) return;
+  float mag = 0.f;
+  const int last = c.nchunks - 1;
+  ColRegs<DK, P> R0, R1;
+  col_load_regs<DK, DV, P>(a, static_cast<int64_t>(c.u0) * H + h, split, l, R0);
+  col_load_regs<DK, DV, P>(a, static_cast<int64_t>(c.u0 + min(1, last)) * H + h, split, l, R1);
+  col_write_regs<DK, P>(sm.buf[0], l, R0);
+  lds_barrier();  // chunk 0 staged
+  int n = 0;
+  for (; n + 1 < c.nchunks; n += 2) {
+    col_producer_step<DK, DV, OUT_DT, P>(a, sm, c, H, h, split, l, n, R0, R1, mag);
+    col_producer_step<DK, DV, OUT_DT, P>(a, sm, c, H, h, split, l, n + 1, R1, R0, mag);
+  }
+  if (n < c.nchunks) col_producer_step<DK, DV, OUT_DT, P>(a, sm, c, H, h, split, l, n, R0, R1, mag);
+  wait_vmem_all();
+  constexpr int NS = ColStoreShape<OUT_DT>::NS;
+  uint4 vs[NS];
+  bool ok[NS];
+  col_store_rows<DV, OUT_DT, P>(a, sm.obuf[last & 1], c.tok0 + static_cast<int64_t>(last) * kC,
+                                min(kC, c.seq_len - last * kC), h, split, l, vs, ok);
+  mag += col_stored_mag<OUT_DT>(vs, ok);
+  report_nonfinite(a.status, mag);
 }
 
 // o of row tiles 0..3 (D layout: rows 16ct + 4gq + i, column r of value tile
@@ -1339,8 +1379,14 @@ __device__ __forceinline__ void col_put_o(unsigned char* ob, const f4 (&O)[4], i
 #pragma unroll
     for (int i = 0; i < 4; ++i) {
       const int row = 16 * ct + 4 * gq + i;
-      if constexpr (OUT_DT == 0) reinterpret_cast<float*>(ob)[row * 32 + 16 * tile + r] = O[ct][i];
-      else reinterpret_cast<u16*>(ob)[row * 32 + 16 * tile + r] = f32_to_bf16_bits(O[ct][i]);
+      // 16-byte chunks of rows with bit 2 set swap halves, so that in each
+      // 32-lane half of a write (gq 0 and 1, gq 2 and 3) the lanes hit
+      // distinct banks
+      constexpr int EPC = (OUT_DT == 0) ? 4 : 8;   // elements per 16-byte chunk
+      const int col = 16 * tile + r;
+      const int pc = ((col / EPC) ^ ((16 / EPC) * ((row >> 2) & 1))) * EPC + col % EPC;
+      if constexpr (OUT_DT == 0) reinterpret_cast<float*>(ob)[row * 32 + pc] = O[ct][i];
+      else reinterpret_cast<u16*>(ob)[row * 32 + pc] = f32_to_bf16_bits(O[ct][i]);
     }
 }
 
