@@ -28,7 +28,14 @@ typedef _Float16 h8 __attribute__((ext_vector_type(8)));
 typedef __bf16 b8 __attribute__((ext_vector_type(8)));
 typedef float f4 __attribute__((ext_vector_type(4)));
 typedef float f8 __attribute__((ext_vector_type(8)));
+typedef unsigned int u32x4 __attribute__((ext_vector_type(4)));
 typedef uint16_t u16;
+
+// Cache policy of a direct global->LDS copy (the aux operand of
+// __builtin_amdgcn_global_load_lds): non-temporal, for data read once and
+// not again by this launch (the copy does not keep the lines in L2, where
+// they would displace lines other workgroups still read).
+constexpr int kCpolStream = 2;
 
 constexpr float kLog2e = 1.4426950408889634f;
 
