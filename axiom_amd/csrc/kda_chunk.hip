@@ -1619,7 +1619,9 @@ struct WideSmem {
 constexpr int kWideProducers = 4;
 
 // Producer P's share of chunk-head ch: every fourth shared fragment, U row
-// tile P of the workgroup's value tiles, and (last producer) gamma_C.
+// tile P of the workgroup's value tiles, and (last producer) gamma_C.  The
+// copies are non-temporal: one workgroup owns the whole chain, so no other
+// workgroup reads these lines (config 3 3 990 -> 3 930 us when introduced).
 template <int DK, int DV, int VT, int P>
 __device__ __forceinline__ void wide_stage(const StateArgs& a, int64_t ch, int split, unsigned char* dst, int l) {
   typedef ColLayout<DK> LY;
@@ -1639,7 +1641,7 @@ __device__ __forceinline__ void wide_stage(const StateArgs& a, int64_t ch, int s
       const int gidx = (ai < 2) ? 2 * ai : ai + 2;  // index ct*2 + jj in the workspace
       src = iA + (ch * 8 + gidx) * 512;
     }
-    __builtin_amdgcn_global_load_lds(src + l * 8, dst + f * 1024, 16, 0, 0);
+    __builtin_amdgcn_global_load_lds(src + l * 8, dst + f * 1024, 16, 0, kCpolStream);
   }
   static_assert(kWideProducers == 4, "one U row tile per producer");
 #pragma unroll
@@ -1647,11 +1649,11 @@ __device__ __forceinline__ void wide_stage(const StateArgs& a, int64_t ch, int s
     // value tiles 2i, 2i+1 of the workgroup, row tile P: 1 KiB, contiguous in the workspace
     const _Float16* usrc = static_cast<const _Float16*>(a.U) +
                            (ch * 4 * (DV / 16) + P * (DV / 16) + split * VT + 2 * i) * 256 + l * 8;
-    __builtin_amdgcn_global_load_lds(usrc, dst + WL::OFF_U + (P * VT + 2 * i) * 512, 16, 0, 0);
+    __builtin_amdgcn_global_load_lds(usrc, dst + WL::OFF_U + (P * VT + 2 * i) * 512, 16, 0, kCpolStream);
   }
   if constexpr (P == kWideProducers - 1) {
     const _Float16* gsrc = reinterpret_cast<const _Float16*>(a.GC + ch * DK + l * 4);
-    if (l < DK / 4) __builtin_amdgcn_global_load_lds(gsrc, dst + WL::OFF_G, 16, 0, 0);
+    if (l < DK / 4) __builtin_amdgcn_global_load_lds(gsrc, dst + WL::OFF_G, 16, 0, kCpolStream);
   }
 }
 
