@@ -59,14 +59,17 @@ size_t bytes_per_chunk_head(int dk, int dv, size_t es) {
 // intra-chunk results stay within this budget: on MI355X they are then read
 // back by the state kernel from the 256 MB last-level cache rather than
 // HBM, and the next segment overwrites them there.  Config 1 (B4 T4096 H16
-// d128, 304 MB of results) runs as 3 segments (282 us against 305 us
-// unsegmented when introduced; 2 segments: 287 us; 4: 282 us; 6 or 8:
-// 328 us, the smaller intra grids then leave CUs idle).
-constexpr double kSegmentBudgetBytes = 100.0 * 1048576.0;
+// d128, 304 MB of results) runs as 2 segments of 32 chunks: 206 us against
+// 212 us as 3 (24 + 24 + 16) and 241 us unsegmented, measured once the
+// intra kernel's input copies were non-temporal (they no longer compete
+// with the results for the cache; before that 3 segments were best: 282 us
+// against 287 for 2 and 305 unsegmented).
+constexpr double kSegmentBudgetBytes = 160.0 * 1048576.0;
 // Intra workgroups resident at once (two on each of the MI355X's 256 CUs).
 // A segment's chunk count is rounded up so its B * H * chunks workgroups fill
-// whole rounds of them (config 1: 24 + 24 + 16 chunks, 227.6 us, against
-// 22 + 22 + 20, 232.9 us, whose last round per segment ran a quarter empty).
+// whole rounds of them (measured when config 1 ran 3 segments: 24 + 24 + 16
+// chunks, 227.6 us, against 22 + 22 + 20, 232.9 us, whose last round per
+// segment ran a quarter empty).
 constexpr int kIntraSlots = 512;
 
 // Overlapped segments (the state scan of segment s in the same launch as the
@@ -74,14 +77,16 @@ constexpr int kIntraSlots = 512;
 // of the chip free: at most this many 32-column state workgroups (each holds a
 // CU for the whole segment; 24 chains at dv = 128).  Both segments' intra
 // results then live at once, next to the inputs the intra work streams, so a
-// segment's budget is smaller: config 2 (B1 T65536 H16) runs 1 530 us in
-// sequential 100 MiB segments, 1 915 us overlapped at 100 MiB (the two sets
-// and the inputs overflow the 256 MB memory-side cache and the serial scan
-// waits on HBM), 1 239 us overlapped at 48 MiB (32: 1 295, 40: 1 263,
-// 56: 1 263, 64: 1 274).  At 128 state workgroups (32 chains) overlapping
-// gains nothing (1 085 against 1 085 us), at 96 (24 chains) 1 855 -> 1 770 us.
+// segment's budget is smaller.  Config 2 (B1 T65536 H16), with the intra
+// kernel's input copies non-temporal: 1 134 us overlapped at 96 MiB (48:
+// 1 166, 56: 1 161, 64: 1 148, 80: 1 143, 112: 1 136, 128: 1 141); before
+// those copies were non-temporal the inputs competed for the 256 MB
+// memory-side cache and 48 MiB was best (1 239 us; 100 MiB: 1 915 us, the
+// serial scan waiting on HBM; sequential 100 MiB segments: 1 530 us).  At
+// 128 state workgroups (32 chains) overlapping gained nothing (1 085 against
+// 1 085 us), at 96 (24 chains) 1 855 -> 1 770 us.
 constexpr int64_t kOverlapMaxStateWgs = 96;
-constexpr double kOverlapSegmentBudgetBytes = 48.0 * 1048576.0;
+constexpr double kOverlapSegmentBudgetBytes = 96.0 * 1048576.0;
 
 int64_t col_state_grid(int64_t chains, int dv) { return ((chains + 7) / 8) * 8 * (dv / 32); }
 
@@ -431,7 +436,10 @@ int ut_check(const void* a, const void* b, const void* x, int H, int C, int N, i
 // streams, two threads) race on it.  No part of it needs clearing between
 // calls: the forward writes every workspace word it reads within the call.
 // ----------------------------------------------------------------------------
-constexpr size_t kScratchBytes = static_cast<size_t>(128) << 20;
+// 192 MiB: the dense config-1 workspace (two segments of 160 MiB budget: 149
+// MiB with the carried state) and the overlapped config-2 one (two 96 MiB
+// sets: 180 MiB) fit.
+constexpr size_t kScratchBytes = static_cast<size_t>(192) << 20;
 static __device__ __align__(256) unsigned char scratch[kScratchBytes];
 
 constexpr int kMaxDevices = 64;

@@ -99,7 +99,7 @@ KDA_API int kda_chunk_fwd(hipStream_t stream,
 
 /*
  * kda_chunk_fwd without a workspace argument: the workspace is a file-scope
- * device array of the library (128 MiB = 134217728 bytes, one per device,
+ * device array of the library (192 MiB = 201326592 bytes, one per device,
  * held from the library's load until the process ends), so the call allocates nothing (no hipMalloc, no allocating library
  * routine) and only launches kernels.  No counterpart in the reference: it is
  * for callers that cannot allocate -- code under HIP graph capture, tight

@@ -34,15 +34,15 @@ def _align(x):
     return (x + 255) // 256 * 256
 
 
-SEGMENT_BUDGET = 100 * 1048576   # bytes of intra-chunk results per segment of a dense call
+SEGMENT_BUDGET = 160 * 1048576   # bytes of intra-chunk results per segment of a dense call
 
 
 INTRA_SLOTS = 512   # intra workgroups resident at once: segments are rounded up to whole rounds
 
 # Calls whose 32-column state grid is at most 96 workgroups overlap each
 # segment's state scan with the next segment's intra work: two sets of intra
-# results, 48 MiB segments, no rounding to whole intra rounds.
-OVERLAP_BUDGET = 48 * 1048576
+# results, 96 MiB segments, no rounding to whole intra rounds.
+OVERLAP_BUDGET = 96 * 1048576
 OVERLAP_MAX_STATE_WGS = 96
 
 
@@ -83,14 +83,16 @@ def dense_ws_bytes(B, T, H, dk, dv, es):
 
 
 def test_segment_policy():
-    # config 1: 304 MB of intra-chunk results -> 3 segments; 22 chunks rounded
-    # up to 24 so each segment's 4 * 16 * 24 = 1536 intra workgroups are whole rounds
-    assert dense_segments(4, 4096, 16, 128, 128, 2) == (3, 24)
+    # config 1: 304 MB of intra-chunk results -> 2 segments of 32 chunks, each
+    # segment's 4 * 16 * 32 = 2048 intra workgroups whole rounds of 512
+    assert dense_segments(4, 4096, 16, 128, 128, 2) == (2, 32)
     assert dense_segments(2, 1000, 2, 128, 128, 2) == (1, 16)
-    # config 2 (16 chains: 64 state workgroups) overlaps its segments: 48 MiB
-    # each, 25 segments of 41 chunks (the last 40)
+    # 70 chunks: 2 segments of 35 chunks rounded up to 40 (whole rounds)
+    assert dense_segments(4, 70 * 64, 16, 128, 128, 2) == (2, 40)
+    # config 2 (16 chains: 64 state workgroups) overlaps its segments: 96 MiB
+    # each, 13 segments of 79 chunks (the last 76)
     assert overlap_eligible(1, 16, 128, 2) and not overlap_eligible(4, 16, 128, 2)
-    assert dense_segments(1, 65536, 16, 128, 128, 2) == (25, 41)
+    assert dense_segments(1, 65536, 16, 128, 128, 2) == (13, 79)
     assert not overlap_eligible(1, 16, 128, 4)   # exact mode never overlaps
 
 

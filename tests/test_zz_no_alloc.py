@@ -83,4 +83,4 @@ def test_noalloc_refuses_a_call_beyond_its_scratch(cuda):
     torch.cuda.synchronize()
     assert rc == _lib.KDA_ERR_WORKSPACE
     msg = _lib.last_error()
-    assert "scratch" in msg and "134217728" in msg, msg
+    assert "scratch" in msg and "201326592" in msg, msg
