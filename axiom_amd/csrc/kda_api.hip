@@ -343,31 +343,79 @@ namespace kda {
 
 // Grid-strided: g element by element (consecutive threads, consecutive
 // elements), beta one token-head per thread (its 32 columns summed in column
-// order).
+// order).  VEC (every pointer 16-byte aligned): four elements per thread and
+// 16-byte non-temporal loads and stores (each value is touched once), the
+// beta columns read four at a time and summed in the same order.
+template <bool VEC>
 __global__ __launch_bounds__(256) void kda_adapt_kernel(AdaptArgs a) {
   const int64_t stride = static_cast<int64_t>(gridDim.x) * 256;
   const int64_t i0 = static_cast<int64_t>(blockIdx.x) * 256 + threadIdx.x;
   const int64_t n = a.n_tok_heads * a.dk;
-  for (int64_t i = i0; i < n; i += stride) a.g_out[i] = logf(a.alpha[i]);
-  for (int64_t th = i0; th < a.n_tok_heads; th += stride) {
-    const float* b = a.beta32 + th * 32;
-    float s = 0.f;
-    for (int j = 0; j < 32; ++j) s += b[j];
-    a.beta_out[th] = s * (1.0f / 32.0f);
+  if constexpr (VEC) {
+    const f4* al = reinterpret_cast<const f4*>(a.alpha);
+    f4* go = reinterpret_cast<f4*>(a.g_out);
+    for (int64_t i = i0; i < n / 4; i += stride) {
+      const f4 x = __builtin_nontemporal_load(al + i);
+      __builtin_nontemporal_store(f4{logf(x[0]), logf(x[1]), logf(x[2]), logf(x[3])}, go + i);
+    }
+    for (int64_t th = i0; th < a.n_tok_heads; th += stride) {
+      const f4* b = reinterpret_cast<const f4*>(a.beta32 + th * 32);
+      float s = 0.f;
+#pragma unroll
+      for (int j = 0; j < 8; ++j) {
+        const f4 v = __builtin_nontemporal_load(b + j);
+        s += v[0];
+        s += v[1];
+        s += v[2];
+        s += v[3];
+      }
+      a.beta_out[th] = s * (1.0f / 32.0f);
+    }
+  } else {
+    for (int64_t i = i0; i < n; i += stride) a.g_out[i] = logf(a.alpha[i]);
+    for (int64_t th = i0; th < a.n_tok_heads; th += stride) {
+      const float* b = a.beta32 + th * 32;
+      float s = 0.f;
+      for (int j = 0; j < 32; ++j) s += b[j];
+      a.beta_out[th] = s * (1.0f / 32.0f);
+    }
   }
 }
 
 hipError_t launch_adapt(const AdaptArgs& a, hipStream_t s) {
   if (a.n_tok_heads == 0) return hipSuccess;
-  const int64_t need = (a.n_tok_heads * a.dk + 255) / 256;
+  const bool vec = a.dk % 4 == 0 &&
+                   ((reinterpret_cast<uintptr_t>(a.alpha) | reinterpret_cast<uintptr_t>(a.beta32) |
+                     reinterpret_cast<uintptr_t>(a.g_out)) & 15) == 0;
+  const int64_t need = (a.n_tok_heads * a.dk / (vec ? 4 : 1) + 255) / 256;
   const int grid = static_cast<int>(need < 8192 ? need : 8192);
-  hipLaunchKernelGGL(kda_adapt_kernel, dim3(grid), dim3(256), 0, s, a);
+  if (vec) hipLaunchKernelGGL(kda_adapt_kernel<true>, dim3(grid), dim3(256), 0, s, a);
+  else hipLaunchKernelGGL(kda_adapt_kernel<false>, dim3(grid), dim3(256), 0, s, a);
   return hipGetLastError();
 }
 
+// One element (VEC: four, with 16-byte non-temporal loads of the fp32 inputs
+// and non-temporal stores; every pointer 16-byte aligned) per thread, and one
+// dbeta32 value per thread.
+template <bool VEC>
 __global__ __launch_bounds__(256) void kda_cc_finish_kernel(CcFinishArgs a) {
   const int64_t i = static_cast<int64_t>(blockIdx.x) * 256 + threadIdx.x;
-  if (i < a.n) {
+  if constexpr (VEC) {
+    if (i < a.n / 4) {
+      typedef unsigned int u2v __attribute__((ext_vector_type(2)));
+      auto bf4 = [](const f4 x) { return u2v{pack_bf16x2(x[0], x[1]), pack_bf16x2(x[2], x[3])}; };
+      __builtin_nontemporal_store(bf4(__builtin_nontemporal_load(reinterpret_cast<const f4*>(a.dq32) + i)),
+                                  reinterpret_cast<u2v*>(a.dq) + i);
+      __builtin_nontemporal_store(bf4(__builtin_nontemporal_load(reinterpret_cast<const f4*>(a.dk32) + i)),
+                                  reinterpret_cast<u2v*>(a.dk) + i);
+      __builtin_nontemporal_store(bf4(__builtin_nontemporal_load(reinterpret_cast<const f4*>(a.dv32) + i)),
+                                  reinterpret_cast<u2v*>(a.dv) + i);
+      const f4 g = __builtin_nontemporal_load(reinterpret_cast<const f4*>(a.dg) + i);
+      const f4 al = __builtin_nontemporal_load(reinterpret_cast<const f4*>(a.alpha) + i);
+      __builtin_nontemporal_store(f4{g[0] / al[0], g[1] / al[1], g[2] / al[2], g[3] / al[3]},
+                                  reinterpret_cast<f4*>(a.dalpha) + i);
+    }
+  } else if (i < a.n) {
     static_cast<u16*>(a.dq)[i] = cvt_bf16(a.dq32[i]);
     static_cast<u16*>(a.dk)[i] = cvt_bf16(a.dk32[i]);
     static_cast<u16*>(a.dv)[i] = cvt_bf16(a.dv32[i]);
@@ -377,9 +425,18 @@ __global__ __launch_bounds__(256) void kda_cc_finish_kernel(CcFinishArgs a) {
 }
 
 hipError_t launch_cc_finish(const CcFinishArgs& a, hipStream_t s) {
-  const int64_t n = a.n > a.n_tok_heads * 32 ? a.n : a.n_tok_heads * 32;
+  const uintptr_t any = reinterpret_cast<uintptr_t>(a.dq32) | reinterpret_cast<uintptr_t>(a.dk32) |
+                        reinterpret_cast<uintptr_t>(a.dv32) | reinterpret_cast<uintptr_t>(a.dg) |
+                        reinterpret_cast<uintptr_t>(a.alpha) | reinterpret_cast<uintptr_t>(a.dalpha);
+  const uintptr_t any8 = reinterpret_cast<uintptr_t>(a.dq) | reinterpret_cast<uintptr_t>(a.dk) |
+                         reinterpret_cast<uintptr_t>(a.dv);
+  const bool vec = a.n % 4 == 0 && (any & 15) == 0 && (any8 & 7) == 0;
+  const int64_t ne = vec ? a.n / 4 : a.n;
+  const int64_t n = ne > a.n_tok_heads * 32 ? ne : a.n_tok_heads * 32;
   if (n == 0) return hipSuccess;
-  hipLaunchKernelGGL(kda_cc_finish_kernel, dim3(static_cast<unsigned>((n + 255) / 256)), dim3(256), 0, s, a);
+  const dim3 grid(static_cast<unsigned>((n + 255) / 256));
+  if (vec) hipLaunchKernelGGL(kda_cc_finish_kernel<true>, grid, dim3(256), 0, s, a);
+  else hipLaunchKernelGGL(kda_cc_finish_kernel<false>, grid, dim3(256), 0, s, a);
   return hipGetLastError();
 }
 
