@@ -180,7 +180,7 @@ int chunk_fwd_impl(hipStream_t stream, const void* q, const void* k, const void*
                    const int32_t* cu_seqlens, int32_t n_seqs, void* o, float* ht,
                    int B, int T, int H, int dk, int dv, int chunk, float scale,
                    int in_dtype, int out_dtype, void* ws, size_t ws_bytes,
-                   const FusedPrologue* pro = nullptr) {
+                   const FusedPrologue* pro = nullptr, bool gates_alpha = false) {
   if (!q || !k || !v || !g || !beta) return fail(KDA_ERR_INVALID_ARGUMENT, "null input pointer");
   if (!o && T > 0) return fail(KDA_ERR_INVALID_ARGUMENT, "null output pointer o");
   if (B < 1) return fail(KDA_ERR_INVALID_ARGUMENT, "B=%d must be >= 1", B);
@@ -235,6 +235,7 @@ int chunk_fwd_impl(hipStream_t stream, const void* q, const void* k, const void*
   ia.geom = G;
   ia.q = q; ia.k = k; ia.v = v; ia.g = g; ia.beta = beta;
   ia.scale = scale;
+  ia.gates_alpha = gates_alpha ? 1 : 0;
   ia.W = at<void>(ws, L.W);
   ia.U = at<void>(ws, L.U);
   ia.AQ = at<void>(ws, L.AQ);
@@ -682,19 +683,15 @@ int kda_cc_scan_batched(hipStream_t stream, const void* q, const void* k, const 
   const size_t th = static_cast<size_t>(B) * T * H;
   const size_t g_bytes = align_up(th * dk * 4);
   const size_t b_bytes = align_up(th * 4);
-  float* g32 = reinterpret_cast<float*>(workspace);
-  float* b32 = reinterpret_cast<float*>(static_cast<char*>(workspace) + g_bytes);
-  kda::AdaptArgs aa{};
-  aa.alpha = alpha; aa.beta32 = beta32; aa.g_out = g32; aa.beta_out = b32;
-  aa.n_tok_heads = static_cast<int64_t>(th);
-  aa.dk = dk;
-  hipError_t e = kda::launch_adapt(aa, stream);
-  if (e != hipSuccess) return hip_fail(e, "cc_scan adapter launch");
-  // the (B, T, H*d) operands are the [B, T, H, d] layout of the chunked forward
+  // The (B, T, H*d) operands are the [B, T, H, d] layout of the chunked
+  // forward; its intra kernel takes g = log(alpha) and beta = mean(beta32)
+  // itself (the arithmetic of kda_adapt_kernel, which the backward runs).
+  // The workspace keeps the adapter's g and beta areas unused, so both
+  // directions size it the same way.
   void* rest = static_cast<char*>(workspace) + g_bytes + b_bytes;
-  return chunk_fwd_impl(stream, q, k, v, g32, b32, S_in, nullptr, 0, o, S_out, B, T, H, dk, dv,
+  return chunk_fwd_impl(stream, q, k, v, alpha, beta32, S_in, nullptr, 0, o, S_out, B, T, H, dk, dv,
                         kC, 1.0f, KDA_DTYPE_BF16_F32GATES, KDA_DTYPE_F32, rest,
-                        workspace_bytes - g_bytes - b_bytes);
+                        workspace_bytes - g_bytes - b_bytes, nullptr, true);
 }
 
 int kda_cc_scan(hipStream_t stream, const void* q, const void* k, const void* v,

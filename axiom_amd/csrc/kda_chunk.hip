@@ -211,7 +211,22 @@ __device__ __forceinline__ void intra_chunk(const IntraArgs& a, const UnitRef& U
   constexpr int NQKV = PRO ? NPER + 1 : NPER;   // copies per q, k, v (PRO: one of history rows)
   // (unconditional load of a valid row, masked after the waits: a load
   // inside a branch is waited for at the branch's end)
-  float beta_c = ld1<DTG>(a.beta, (U.row0 + min(c, U.len - 1)) * H + h);
+  float beta_c;
+  if constexpr (DTG == 0) {
+    const int64_t bi = (U.row0 + min(c, U.len - 1)) * H + h;
+    if (a.gates_alpha) {
+      // cc_scan's beta32 row: the mean of its 32 columns, summed in order
+      const float* b32 = static_cast<const float*>(a.beta) + bi * 32;
+      float sb = 0.f;
+#pragma unroll
+      for (int j = 0; j < 32; ++j) sb += b32[j];
+      beta_c = sb * (1.0f / 32.0f);
+    } else {
+      beta_c = ld1<DTG>(a.beta, bi);
+    }
+  } else {
+    beta_c = ld1<DTG>(a.beta, (U.row0 + min(c, U.len - 1)) * H + h);
+  }
   // PRO: conv taps of this lane's channels PL*l .. PL*l + PL-1 and, for the
   // first chunk of a sequence (wave 0), the carried inputs before it; loaded
   // before the row copies, so the copies' partial waits cover them
@@ -332,6 +347,12 @@ __device__ __forceinline__ void intra_chunk(const IntraArgs& a, const UnitRef& U
       f4 z = {0, 0, 0, 0};
       if constexpr (STG) z = unpack4<DTG>(sw[2 * j + hf]);
       else if (valid) z = ld4<DTG>(a.g, bq + 32 * j + 4 * gq + 16 * hf);
+      if constexpr (!STG) {
+        if (a.gates_alpha) {
+#pragma unroll
+          for (int e = 0; e < 4; ++e) z[e] = logf(z[e]);   // g = log(alpha)
+        }
+      }
 #pragma unroll
       for (int e = 0; e < 4; ++e) Gt[j][4 * hf + e] = valid ? z[e] * kLog2e : 0.f;
     }
@@ -606,6 +627,12 @@ __device__ __forceinline__ void intra_chunk(const IntraArgs& a, const UnitRef& U
           const int ch0 = 32 * j + 4 * gq + 16 * hf;
           f4 x = {0, 0, 0, 0}, y = {0, 0, 0, 0}, z = {0, 0, 0, 0};
           if (valid) { x = ld4<DTQ>(a.q, bq + ch0); y = ld4<DTQ>(a.k, bq + ch0); z = ld4<DTG>(a.g, bq + ch0); }
+          if constexpr (DTG == 0) {
+            if (a.gates_alpha) {
+#pragma unroll
+              for (int e = 0; e < 4; ++e) z[e] = logf(z[e]);
+            }
+          }
 #pragma unroll
           for (int e = 0; e < 4; ++e) {
             const int ee = 4 * hf + e;
