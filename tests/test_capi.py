@@ -56,7 +56,10 @@ def dense_segments(B, T, H, dk, dv, es):
         return 1, NT
     total = B * NT * H * (C * (3 * dk + dv + C) * es + dk * 4)
     ovl = overlap_eligible(B, H, dv, es)
-    s = min(max(-(-total // (OVERLAP_BUDGET if ovl else SEGMENT_BUDGET)), 1), NT)
+    s = -(-total // (OVERLAP_BUDGET if ovl else SEGMENT_BUDGET))
+    if ovl and s < 2 and NT >= 32:
+        s = 2   # an overlapped call of 32 or more chunks runs at least two segments
+    s = min(max(s, 1), NT)
     seg = -(-NT // s)
     if s > 1 and not ovl:
         m = INTRA_SLOTS // math.gcd(INTRA_SLOTS, B * H)
@@ -93,6 +96,9 @@ def test_segment_policy():
     # each, 13 segments of 79 chunks (the last 76)
     assert overlap_eligible(1, 16, 128, 2) and not overlap_eligible(4, 16, 128, 2)
     assert dense_segments(1, 65536, 16, 128, 128, 2) == (13, 79)
+    # one segment's worth of results, overlapped: still two segments
+    assert dense_segments(1, 4096, 16, 128, 128, 2) == (2, 32)
+    assert dense_segments(1, 31 * 64, 16, 128, 128, 2) == (1, 31)
     assert not overlap_eligible(1, 16, 128, 4)   # exact mode never overlaps
 
 
