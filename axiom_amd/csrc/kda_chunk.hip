@@ -30,10 +30,16 @@
 // Kernels:
 //  * kda_intra_kernel -- one workgroup per chunk-head; writes W, U, Aqk,
 //    gamma*q, lambda*k and gamma_C to the workspace in MFMA fragment order.
-//  * kda_state_kernel -- one workgroup per (chain, 32-column dv slice); walks
-//    the chunks of its chain with the fp32 state slice in MFMA accumulators,
-//    prefetching three chunks ahead, and emits o and the final state.
-// Exact mode (fp32 inputs) runs the same code with fp32 operands.
+//  * kda_state_col_kernel (16-bit inputs) -- one workgroup per (chain,
+//    32-column dv slice): two compute waves hold the fp32 state slice in MFMA
+//    accumulators and walk the chain's chunks while four producer waves copy
+//    each chunk's operands into LDS two chunks ahead and store o.
+//  * kda_state_wide_kernel (16-bit inputs, >= 256 chains) -- the same with one
+//    workgroup per whole chain.
+//  * kda_overlap_kernel (16-bit inputs, <= 24 chains) -- one segment's
+//    state-slice workgroups and the next segment's intra work in one launch.
+//  * kda_state_kernel (exact mode, fp32 inputs) -- one workgroup per (chain,
+//    32-column dv slice) with fp32 operands.
 
 #include <type_traits>
 
