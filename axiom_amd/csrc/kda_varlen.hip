@@ -77,9 +77,12 @@ void kda_varlen_prep_kernel(const int32_t* cu, int N, int T, int32_t* cu_clamped
     __syncthreads();
   }
   if (tid == 0) { chunk_off[N] = carry; *n_units = carry; flags[0] = bad; }
-  // longest-first order (bitonic sort of (-len, idx)); identity for large N
+  // longest-first order (bitonic sort of (-len, idx) over the next power of
+  // two >= N); identity for large N
   if (N <= 2048) {
-    for (int i = tid; i < 2048; i += 1024) {
+    int P = 2;
+    while (P < N) P <<= 1;
+    for (int i = tid; i < P; i += 1024) {
       if (i < N) {
         const int64_t len = cu_clamped[i + 1] - cu_clamped[i];
         keys[i] = ((int64_t)(0x7FFFFFFF - len) << 32) | (uint32_t)i;
@@ -88,9 +91,9 @@ void kda_varlen_prep_kernel(const int32_t* cu, int N, int T, int32_t* cu_clamped
       }
     }
     __syncthreads();
-    for (int k = 2; k <= 2048; k <<= 1) {
+    for (int k = 2; k <= P; k <<= 1) {
       for (int j = k >> 1; j > 0; j >>= 1) {
-        for (int i = tid; i < 2048; i += 1024) {
+        for (int i = tid; i < P; i += 1024) {
           const int ixj = i ^ j;
           if (ixj > i) {
             const bool up = ((i & k) == 0);
