@@ -134,6 +134,28 @@ def test_config4_decode_full(cuda):
     assert_close("S", torch.stack([S[b, h] for b, h in pick]).cpu().numpy()[:, None], S_ref, (1e-5, 1e-5))
 
 
+def test_two_segment_minimum_overlapped(cuda):
+    """B1 T4096 H16 d128 with h0 (the cc_scan seam's per-element shape): one
+    segment's worth of intra results, run as two overlapped segments; two
+    chains against the oracle, the call split at the segment boundary and at
+    another point gives the same o and final state bit for bit."""
+    from tests.test_capi import dense_segments, overlap_eligible
+    B, T, H, dd = 1, 4096, 16, 128
+    assert overlap_eligible(B, H, dd, 2) and dense_segments(B, T, H, dd, dd, 2) == (2, 32)
+    d = make_inputs_device(B, T, H, dd, dd, seed=111, device=cuda, h0_std=0.02)
+    print("[full] two-segment minimum", flush=True)
+    o, ht = _fwd(d, h0=d["h0"])
+    hc = host_chains(d, 0, [3, 12])
+    o_ref, ht_ref = K.chunk_fwd(hc["q"], hc["k"], hc["v"], hc["g"], hc["beta"],
+                                h0=d["h0"][:, [3, 12]].cpu().numpy(), chunk=64)
+    assert_close("o", o[:, :, [3, 12]], o_ref, TOL["bf16"])
+    assert_close("ht", ht[:, [3, 12]], ht_ref, TOL["bf16"])
+    for cut in (2048, 64 * 13):
+        o1, h1 = _fwd(_slice(d, 0, cut), h0=d["h0"])
+        o2, h2 = _fwd(_slice(d, cut, T), h0=h1)
+        assert torch.equal(torch.cat([o1, o2], dim=1), o) and torch.equal(h2, ht), cut
+
+
 def test_long_two_chain_call_against_oracle(cuda):
     """B1 T50000 H2 d128 with h0: two chains whose intra-chunk results exceed
     one segment (the call runs in segments); both chains against the oracle,
