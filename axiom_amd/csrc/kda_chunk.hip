@@ -221,11 +221,22 @@ __device__ __forceinline__ void intra_chunk(const IntraArgs& a, const UnitRef& U
   if constexpr (DTG == 0) {
     const int64_t bi = (U.row0 + min(c, U.len - 1)) * H + h;
     if (a.gates_alpha) {
-      // cc_scan's beta32 row: the mean of its 32 columns, summed in order
-      const float* b32 = static_cast<const float*>(a.beta) + bi * 32;
-      float sb = 0.f;
+      // cc_scan's beta32 row: the mean of its 32 columns, summed in column
+      // order.  Lane group gq loads columns 8 gq .. 8 gq + 7 (two 16-byte
+      // loads), and the running sum passes from group to group: at step s
+      // group s adds its eight columns to the sum of the groups before it.
+      const f4* b32 = reinterpret_cast<const f4*>(static_cast<const float*>(a.beta) + bi * 32 + 8 * gq);
+      const f4 bl = b32[0], bh = b32[1];
+      float sb = 0.f, t = 0.f;
 #pragma unroll
-      for (int j = 0; j < 32; ++j) sb += b32[j];
+      for (int st = 0; st < 4; ++st) {
+        t = sb;
+#pragma unroll
+        for (int e = 0; e < 4; ++e) t += bl[e];
+#pragma unroll
+        for (int e = 0; e < 4; ++e) t += bh[e];
+        sb = __shfl(t, r + 16 * st, 64);
+      }
       beta_c = sb * (1.0f / 32.0f);
     } else {
       beta_c = ld1<DTG>(a.beta, bi);
