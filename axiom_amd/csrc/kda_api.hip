@@ -160,6 +160,11 @@ WsLayout ws_layout(int B, int T, int H, int dk, int dv, int32_t n_seqs, int in_d
 
 bool dim_ok(int d) { return d == 64 || d == 128; }
 
+// The kernels move rows, fragments and state slices 16 bytes (bf16 v in
+// decode: 8 bytes) per lane access, so those pointers must be aligned to
+// that; a null pointer is left to the null checks.
+bool misaligned(const void* p, uintptr_t bytes) { return (reinterpret_cast<uintptr_t>(p) & (bytes - 1)) != 0; }
+
 int check_dims(int H, int dk, int dv) {
   if (H < 1) return fail(KDA_ERR_INVALID_ARGUMENT, "H=%d must be >= 1", H);
   if (dk < 1 || dv < 1) return fail(KDA_ERR_INVALID_ARGUMENT, "dk=%d, dv=%d must be >= 1", dk, dv);
@@ -203,6 +208,10 @@ int chunk_fwd_impl(hipStream_t stream, const void* q, const void* k, const void*
   }
   const int64_t elems = static_cast<int64_t>(B) * T * H * (dk > dv ? dk : dv);
   if (elems >= (1LL << 40)) return fail(KDA_ERR_INVALID_ARGUMENT, "problem too large");
+  if (misaligned(q, 16) || misaligned(k, 16) || misaligned(v, 16) || misaligned(g, 16) || misaligned(o, 16) ||
+      misaligned(ws, 16) || (gates_alpha && misaligned(beta, 16)))
+    return fail(KDA_ERR_INVALID_ARGUMENT, "q, k, v, g%s, o and the workspace must be 16-byte aligned",
+                gates_alpha ? ", beta32" : "");
   const WsLayout L = ws_layout(B, T, H, dk, dv, varlen ? n_seqs : 0, in_dtype);
   if (L.units_bound * H > 0x7FFFFFFFLL) return fail(KDA_ERR_INVALID_ARGUMENT, "too many chunk-heads");
   if (ws == nullptr || ws_bytes < L.total)
@@ -644,6 +653,9 @@ int kda_recurrent_step(hipStream_t stream, const void* q, const void* k, const v
   if (out_dtype != KDA_DTYPE_F32 && out_dtype != KDA_DTYPE_BF16)
     return fail(KDA_ERR_INVALID_ARGUMENT, "out_dtype=%d: o is emitted as F32 or BF16", out_dtype);
   if (!std::isfinite(scale)) return fail(KDA_ERR_INVALID_ARGUMENT, "scale must be finite");
+  if (misaligned(state, 16) || misaligned(v, in_dtype == KDA_DTYPE_F32 ? 16 : 8) ||
+      misaligned(o, out_dtype == KDA_DTYPE_F32 ? 16 : 8))
+    return fail(KDA_ERR_INVALID_ARGUMENT, "state must be 16-byte aligned, v and o aligned to 4 elements");
   const int64_t grid = static_cast<int64_t>(B) * H;
   if (grid > 0x3FFFFFFFLL) return fail(KDA_ERR_INVALID_ARGUMENT, "B*H too large");
   kda::DecodeArgs a{};

@@ -222,6 +222,9 @@ def _chunk_fwd(L, **kw):
     (dict(cu=_FAKE, n_seqs=0), _lib.KDA_ERR_INVALID_ARGUMENT, "n_seqs=0"),
     (dict(ws=_NULL), _lib.KDA_ERR_WORKSPACE, "workspace"),
     (dict(ws_bytes=100), _lib.KDA_ERR_WORKSPACE, "too small"),
+    (dict(q=ctypes.c_void_p(0x1008)), _lib.KDA_ERR_INVALID_ARGUMENT, "16-byte aligned"),
+    (dict(o=ctypes.c_void_p(0x1004)), _lib.KDA_ERR_INVALID_ARGUMENT, "16-byte aligned"),
+    (dict(ws=ctypes.c_void_p(0x1002)), _lib.KDA_ERR_INVALID_ARGUMENT, "16-byte aligned"),
 ])
 def test_chunk_fwd_validation(L, kw, status, needle):
     rc, msg = _chunk_fwd(L, **kw)
@@ -250,6 +253,8 @@ def test_recurrent_step_validation(L):
     rc, msg = call(in_dt=3)
     assert rc == _lib.KDA_ERR_INVALID_ARGUMENT and "decode takes" in msg
     assert call(out_dt=2)[0] == _lib.KDA_ERR_INVALID_ARGUMENT
+    rc, msg = call(state=ctypes.c_void_p(0x1008))
+    assert rc == _lib.KDA_ERR_INVALID_ARGUMENT and "16-byte aligned" in msg
 
 
 def test_cc_scan_validation_messages(L):
