@@ -7,6 +7,7 @@
 #include <cstdio>
 #include <cstring>
 #include <mutex>
+#include <initializer_list>
 #include <numeric>
 
 #include "kda_common.h"
@@ -164,6 +165,17 @@ bool dim_ok(int d) { return d == 64 || d == 128; }
 // decode: 8 bytes) per lane access, so those pointers must be aligned to
 // that; a null pointer is left to the null checks.
 bool misaligned(const void* p, uintptr_t bytes) { return (reinterpret_cast<uintptr_t>(p) & (bytes - 1)) != 0; }
+
+// Every pointer of `ps` aligned to `bytes` (null pointers pass), else a
+// KDA_ERR_INVALID_ARGUMENT naming `what`.
+int require_aligned(uintptr_t bytes, const char* what, std::initializer_list<const void*> ps) {
+  for (const void* p : ps)
+    if (misaligned(p, bytes)) return fail(KDA_ERR_INVALID_ARGUMENT, "%s must be %d-byte aligned", what, static_cast<int>(bytes));
+  return KDA_OK;
+}
+
+// bytes of four elements of a kda_dtype_t that is F32 or BF16
+uintptr_t four_elems(int dtype) { return dtype == KDA_DTYPE_F32 ? 16 : 8; }
 
 int check_dims(int H, int dk, int dv) {
   if (H < 1) return fail(KDA_ERR_INVALID_ARGUMENT, "H=%d must be >= 1", H);
@@ -748,6 +760,9 @@ int kda_chunk_bwd(hipStream_t stream, const void* q, const void* k, const void* 
   if (elems >= (1LL << 40)) return fail(KDA_ERR_INVALID_ARGUMENT, "problem too large");
   const int64_t NT = (T + kC - 1) / kC;
   if (static_cast<int64_t>(B) * NT * H > 0x7FFFFFFFLL) return fail(KDA_ERR_INVALID_ARGUMENT, "too many chunk-heads");
+  if (int rc = require_aligned(16, "q, k, v, g, dout, the gradients, the states and the workspace",
+                               {q, k, v, g, dout, dq, dk, dv, dg, h0, dht, dh0, workspace}))
+    return rc;
   const BwdLayout L = bwd_layout(B, T, H, dk_dim);
   if (!workspace || workspace_bytes < L.total)
     return fail(KDA_ERR_WORKSPACE, "workspace of %zu bytes is too small (need %zu)", workspace_bytes, L.total);
@@ -813,6 +828,10 @@ int kda_cc_scan_bwd_batched(hipStream_t stream, const void* q, const void* k, co
   if (tile < 1 || tile > 16)
     return fail(KDA_ERR_INVALID_ARGUMENT, "tile=%d outside [1, 16] (the _cc_tile bound)", tile);
   if (int rc = check_dims(H, dk_dim, dv_dim)) return rc;
+  // checked here as well as by the dense backward: the adapter launch comes first
+  if (int rc = require_aligned(16, "q, k, v, S_in, do, dS, dS_in and the workspace",
+                               {q, k, v, S_in, d_o, dS, dS_in, workspace}))
+    return rc;
   const size_t need = kda_cc_scan_bwd_batched_workspace(B, T, H, dk_dim, dv_dim, chunk);
   if (workspace == nullptr || workspace_bytes < need)
     return fail(KDA_ERR_WORKSPACE, "workspace of %zu bytes is too small (need %zu)", workspace_bytes, need);
@@ -900,6 +919,8 @@ int kda_prologue(hipStream_t stream, const void* qp, const void* kp, const void*
   if (!wq || !wk || !wv) return fail(KDA_ERR_INVALID_ARGUMENT, "null conv taps");
   if (T > 0 && (!qp || !kp || !vp || !q || !k || !v)) return fail(KDA_ERR_INVALID_ARGUMENT, "null pointer");
   if (static_cast<int64_t>(B) * T * H * 3 / 4 > 0x7FFFFFFFLL) return fail(KDA_ERR_INVALID_ARGUMENT, "too large");
+  if (int rc = require_aligned(four_elems(in_dtype) / 2, "qp, kp, vp (two elements)", {qp, kp, vp})) return rc;
+  if (int rc = require_aligned(four_elems(out_dtype) / 2, "q, k, v (two elements)", {q, k, v})) return rc;
   kda::PrologueArgs a{};
   a.qp = qp; a.kp = kp; a.vp = vp; a.wq = wq; a.wk = wk; a.wv = wv;
   a.bq_in = bq_in; a.bk_in = bk_in; a.bv_in = bv_in; a.bq_out = bq_out; a.bk_out = bk_out; a.bv_out = bv_out;
@@ -921,6 +942,9 @@ int kda_epilogue(hipStream_t stream, const void* o, const void* gate, void* y, i
   if (!(eps >= 0.f) || !std::isfinite(eps)) return fail(KDA_ERR_INVALID_ARGUMENT, "eps must be finite and >= 0");
   if (T > 0 && (!o || !gate || !y)) return fail(KDA_ERR_INVALID_ARGUMENT, "null pointer");
   if (static_cast<int64_t>(B) * T * H / 4 > 0x7FFFFFFFLL) return fail(KDA_ERR_INVALID_ARGUMENT, "too large");
+  if (misaligned(o, four_elems(o_dtype)) || misaligned(gate, four_elems(gate_dtype)) ||
+      misaligned(y, four_elems(out_dtype)))
+    return fail(KDA_ERR_INVALID_ARGUMENT, "o, gate and y must be aligned to 4 elements");
   kda::EpilogueArgs a{};
   a.o = o; a.gate = gate; a.y = y; a.B = B; a.T = T; a.H = H; a.eps = eps;
   const hipError_t e = kda::launch_epilogue(a, dv, o_dtype == KDA_DTYPE_F32 ? 0 : 1,
@@ -954,6 +978,9 @@ int kda_prologue_bwd(hipStream_t stream, const void* qp, const void* kp, const v
   if (!wq || !wk || !wv || !dwq || !dwk || !dwv) return fail(KDA_ERR_INVALID_ARGUMENT, "null conv taps or dw");
   if (T > 0 && (!qp || !kp || !vp || !dq || !dk || !dv || !dqp || !dkp || !dvp))
     return fail(KDA_ERR_INVALID_ARGUMENT, "null pointer");
+  if (int rc = require_aligned(four_elems(in_dtype) / 2, "qp, kp, vp (two elements)", {qp, kp, vp})) return rc;
+  if (int rc = require_aligned(8, "dq, dk, dv, dqp, dkp, dvp (two elements)", {dq, dk, dv, dqp, dkp, dvp}))
+    return rc;
   if (static_cast<int64_t>(B) * T * H * 3 / 4 > 0x7FFFFFFFLL) return fail(KDA_ERR_INVALID_ARGUMENT, "too large");
   const size_t need = kda_prologue_bwd_workspace(B, T, H, d, K);
   if (!workspace || workspace_bytes < need)
@@ -985,6 +1012,9 @@ int kda_epilogue_bwd(hipStream_t stream, const void* o, const void* gate, const 
   if (!(eps >= 0.f) || !std::isfinite(eps)) return fail(KDA_ERR_INVALID_ARGUMENT, "eps must be finite and >= 0");
   if (T > 0 && (!o || !gate || !dy || !dout || !dgate)) return fail(KDA_ERR_INVALID_ARGUMENT, "null pointer");
   if (static_cast<int64_t>(B) * T * H / 4 > 0x7FFFFFFFLL) return fail(KDA_ERR_INVALID_ARGUMENT, "too large");
+  if (misaligned(o, four_elems(o_dtype)) || misaligned(gate, four_elems(gate_dtype)) ||
+      misaligned(dy, four_elems(dy_dtype)) || misaligned(dout, 16) || misaligned(dgate, four_elems(dgate_dtype)))
+    return fail(KDA_ERR_INVALID_ARGUMENT, "o, gate, dy, dout and dgate must be aligned to 4 elements");
   kda::EpilogueBwdArgs a{};
   a.o = o; a.gate = gate; a.dy = dy; a.dout = dout; a.dgate = dgate; a.B = B; a.T = T; a.H = H; a.eps = eps;
   auto c = [](int dt) { return dt == KDA_DTYPE_F32 ? 0 : 1; };
@@ -1019,6 +1049,8 @@ int kda_decode_layer_step(hipStream_t stream, const void* qp, const void* kp, co
   if (!std::isfinite(scale) || !std::isfinite(eps) || !(eps >= 0.f))
     return fail(KDA_ERR_INVALID_ARGUMENT, "scale and eps must be finite (eps >= 0)");
   if (static_cast<int64_t>(B) * H > 0x3FFFFFFFLL) return fail(KDA_ERR_INVALID_ARGUMENT, "B*H too large");
+  if (misaligned(state, 16) || misaligned(y, four_elems(out_dtype)))
+    return fail(KDA_ERR_INVALID_ARGUMENT, "state must be 16-byte aligned and y aligned to 4 elements");
   const size_t need = kda_decode_layer_workspace(B, H, d, in_dtype);
   if (!workspace || workspace_bytes < need)
     return fail(KDA_ERR_WORKSPACE, "workspace of %zu bytes is too small (need %zu)", workspace_bytes, need);
@@ -1098,6 +1130,10 @@ int kda_layer_fwd(hipStream_t stream, const void* qp, const void* kp, const void
   if (!std::isfinite(scale) || !std::isfinite(eps) || !(eps >= 0.f))
     return fail(KDA_ERR_INVALID_ARGUMENT, "scale and eps must be finite (eps >= 0)");
   if (static_cast<int64_t>(B) * T * H * 3 / 4 > 0x7FFFFFFFLL) return fail(KDA_ERR_INVALID_ARGUMENT, "too large");
+  if (int rc = require_aligned(16, "qp, kp, vp, g, o_out and the workspace", {qp, kp, vp, g, o_out, workspace}))
+    return rc;
+  if (misaligned(gate, four_elems(gate_dtype)) || misaligned(y, four_elems(out_dtype)))
+    return fail(KDA_ERR_INVALID_ARGUMENT, "gate and y must be aligned to 4 elements");
   const LayerLayout L = layer_layout(B, T, H, d, K, in_dtype);
   if (!workspace || workspace_bytes < L.total)
     return fail(KDA_ERR_WORKSPACE, "workspace of %zu bytes is too small (need %zu)", workspace_bytes, L.total);

@@ -13,13 +13,16 @@
  *   - g is the per-channel log-decay (g = log alpha <= 0), beta in (0, 1);
  *     no 1/sqrt(d) scale is applied unless `scale` says so (1.0 reproduces
  *     the reference, which applies none: net/kda.py:293, :693-696);
- *   - the kernels move data 16 bytes per lane access: the chunked forward
- *     (kda_chunk_fwd, its no-allocation form, cc_scan and the layer forward)
- *     takes q, k, v, g, o and the workspace (and cc_scan's beta32) 16-byte
- *     aligned, the decode step its state 16-byte aligned and v, o aligned
- *     to 4 elements; other pointers need only element alignment.  Torch
- *     and XLA allocations satisfy this; a misaligned pointer is rejected
- *     with KDA_ERR_INVALID_ARGUMENT;
+ *   - the kernels move several elements per lane access, so pointers are
+ *     aligned to that access: 16 bytes for the chunked forward's (kda_chunk_fwd,
+ *     its no-allocation form, cc_scan, the layer forward) q, k, v, g, o,
+ *     workspace and cc_scan's beta32, the chunked backward's and cc_scan
+ *     backward's inputs, gradients, states and workspace, and every fp32
+ *     state; 4 elements for the decode step's v and o and the epilogues'
+ *     tensors; 2 elements for the prologues' projections and outputs.
+ *     Other pointers need only element alignment.  Torch and XLA
+ *     allocations satisfy this; a misaligned pointer is rejected with
+ *     KDA_ERR_INVALID_ARGUMENT before anything is enqueued;
  *   - return value 0 on success, a negative kda_status_t otherwise; the
  *     message of the last failure on the calling thread is kda_last_error().
  *     Invalid arguments are rejected before anything is enqueued; there is

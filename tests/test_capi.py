@@ -401,3 +401,42 @@ def test_cc_scan_bwd_workspace_and_validation(L):
     assert call(tile=17)[0] == _lib.KDA_ERR_INVALID_ARGUMENT
     assert call(d=96)[0] == _lib.KDA_ERR_UNSUPPORTED
     assert call(ws_bytes=64)[0] == _lib.KDA_ERR_WORKSPACE
+
+
+_ODD = ctypes.c_void_p(0x1004)   # 4-byte aligned only; never dereferenced
+
+
+def _args_with(n, odd_at, ints, tail=()):
+    ptrs = [_FAKE] * n
+    ptrs[odd_at] = _ODD
+    return [_NULL] + ptrs + list(ints) + list(tail)
+
+
+@pytest.mark.parametrize("name,n_ptrs,odd_at,ints,tail", [
+    # kda_chunk_bwd: q misaligned (B, T, H, dk, dv, chunk, scale, in_dt, dout_dt, ws, bytes)
+    ("kda_chunk_bwd", 14, 0, [1, 64, 1, 64, 64, C, 1.0, 1, 0], [_FAKE, 1 << 40]),
+    # kda_cc_scan_bwd_batched: d_o misaligned
+    ("kda_cc_scan_bwd_batched", 14, 6, [1, 64, 1, 64, 64, 16, 32], [_FAKE, 1 << 40]),
+    # kda_prologue: the fp32 projections (two elements per access) misaligned
+    ("kda_prologue", 15, 0, [1, 64, 1, 128, 4, 0, 0], []),
+    # kda_epilogue: o (fp32) misaligned
+    ("kda_epilogue", 3, 0, [1, 64, 1, 128, 1e-6, 0, 1, 1], []),
+    # kda_prologue_bwd: dqp misaligned
+    ("kda_prologue_bwd", 21, 12, [1, 64, 1, 128, 4, 1], [_FAKE, 1 << 40]),
+    # kda_epilogue_bwd: dout misaligned
+    ("kda_epilogue_bwd", 5, 3, [1, 64, 1, 128, 1e-6, 0, 1, 1, 1], []),
+    # kda_decode_layer_step: state misaligned
+    ("kda_decode_layer_step", 14, 12, [1, 1, 128, 4, 1.0, 1e-6, 1, 1], [_FAKE, 1 << 40]),
+    # kda_layer_fwd: g misaligned
+    ("kda_layer_fwd", 19, 3, [1, 64, 1, 128, 4, 1.0, 1e-6, 1, 1, 1], [_FAKE, 1 << 40]),
+])
+def test_misaligned_pointers_are_rejected(L, name, n_ptrs, odd_at, ints, tail):
+    """Pointers the kernels access several elements at a time must be aligned to
+    that access; a misaligned one is rejected before anything is enqueued."""
+    res, argtypes = _lib._SIGNATURES[name]
+    args = _args_with(n_ptrs, odd_at, ints, tail)
+    assert len(args) == len(argtypes), (name, len(args), len(argtypes))
+    rc = getattr(L, name)(*args)
+    msg = _lib.last_error()
+    assert rc == _lib.KDA_ERR_INVALID_ARGUMENT, msg
+    assert "aligned" in msg, msg
