@@ -17,8 +17,8 @@
  *     aligned to that access: 16 bytes for the chunked forward's (kda_chunk_fwd,
  *     its no-allocation form, cc_scan, the layer forward) q, k, v, g, o,
  *     workspace and cc_scan's beta32, the chunked backward's and cc_scan
- *     backward's inputs, gradients, states and workspace, and every fp32
- *     state; 4 elements for the decode step's v and o and the epilogues'
+ *     backward's inputs, gradients, states and workspace, and the decode
+ *     steps' state; 4 elements for the decode step's v and o and the epilogues'
  *     tensors; 2 elements for the prologues' projections and outputs.
  *     Other pointers need only element alignment.  Torch and XLA
  *     allocations satisfy this; a misaligned pointer is rejected with
