@@ -44,6 +44,9 @@ Also reported on the same JSON line:
   batch in one call with a leading batch axis;
 * ``ut_solve``: the standalone unit-triangular solve at the reference's case
   (H=12, C=64, N=dk+dv=256, fp32), both orientations, per call;
+* ``copy_gbps_measured`` and ``gemm_bf16_tflops_measured``: the box's own
+  ceilings beside the datasheet peaks (a 1 GiB device copy; a contiguous
+  8192^3 bf16 ``torch.mm``, fp32 accumulate);
 * ``cpu_baseline``: the oracle's fp32 restatement of the reference jax body
   (torch CPU, all available cores) timed on a bounded sample of the same
   workload on this host.
@@ -129,6 +132,27 @@ def make_inputs_gpu(B, T, H, dk, dv, seed, device, dtype=torch.bfloat16):
     a = torch.rand(H, device=device, generator=gen) * -2.0
     g = (-torch.nn.functional.softplus(gz) * torch.exp(a)[None, None, :, None]).to(dtype)
     return q, k, v, g, beta
+
+
+def gemm_bf16_tflops(device, n=8192, reps=10):
+    """Dense bf16 matrix-core rate the box reaches through the vendor GEMM
+    (torch.mm, contiguous n x n operands, fp32 accumulate): the practical
+    ceiling next to the 2 516.6 TFLOP/s datasheet peak."""
+    gen = torch.Generator(device=device)
+    gen.manual_seed(7)
+    a = torch.randn(n, n, device=device, generator=gen).to(torch.bfloat16)
+    b = torch.randn(n, n, device=device, generator=gen).to(torch.bfloat16)
+    for _ in range(3):
+        torch.mm(a, b)
+    torch.cuda.synchronize()
+    e0, e1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+    e0.record()
+    for _ in range(reps):
+        torch.mm(a, b)
+    e1.record()
+    torch.cuda.synchronize()
+    t = e0.elapsed_time(e1) / 1e3 / reps
+    return 2.0 * n ** 3 / t / 1e12
 
 
 def copy_bandwidth(device, nbytes=1 << 30, reps=10):
@@ -565,7 +589,7 @@ def cpu_baseline(fwd_inputs, seconds):
 def main():
     ap = argparse.ArgumentParser(description=__doc__.split("\n")[0])
     ap.add_argument("--gpus", type=int, default=1)
-    ap.add_argument("--steps", type=int, default=20)
+    ap.add_argument("--steps", type=int, default=50)
     ap.add_argument("--warmup", type=int, default=10)
     ap.add_argument("--decode-steps", type=int, default=128)
     ap.add_argument("--seed", type=int, default=0)
@@ -629,6 +653,10 @@ def main():
         line["copy_gbps_measured"] = copy_bandwidth(device)
     except RuntimeError:
         line["copy_gbps_measured"] = None
+    try:
+        line["gemm_bf16_tflops_measured"] = gemm_bf16_tflops(device)
+    except RuntimeError:
+        line["gemm_bf16_tflops_measured"] = None
     if not args.no_decode:
         line["decode"] = bench_decode(args, device)
     if not args.no_backward:
