@@ -145,6 +145,21 @@ struct IntraSmem {
                 "factor rows and diagonal L blocks exceed the T buffer");
 };
 
+// The intra kernel stages fp32 gate rows through LDS when q, k, v are 16-bit
+// and g is fp32 (BF16_F32GATES, the cc_scan seam), outside the fused
+// prologue and the exact mode.
+template <int DTQ, int DTG, bool EXACT, bool PRO>
+struct IntraG32 {
+  static constexpr bool value = DTG == 0 && DTQ != 0 && !EXACT && !PRO;
+};
+
+// Shared memory of the intra kernel: IntraSmem, or the larger staging area
+// the fused prologue needs (64 rows of g plus 4 waves x 3 tensors x (16 +
+// history) rows) or the fp32-gate staging (64 fp32 g rows, 64 rows of q and
+// of k), whichever is bigger.
+template <int DK, int DV, bool EXACT, bool PRO, bool G32>
+struct IntraLds;
+
 // channel of slot index s
 __device__ __forceinline__ int slot_index_channel(int s) {
   return slot_channel(s >> 5, (s >> 3) & 3, s & 7);
@@ -185,13 +200,20 @@ __device__ __forceinline__ void intra_chunk(const IntraArgs& a, const UnitRef& U
   // aliases the buffers of the later phases (barrier before their first use).
   // fp32 tensors are loaded per lane as before.
   constexpr bool STQ = (DTQ != 0);
-  constexpr bool STG = (DTG != 0);
-  constexpr int ROWB = DK * 2;          // bytes per staged row
+  // fp32 gates with 16-bit q, k, v (G32): g is staged too, in fp32 rows of
+  // twice the bytes, each copy instruction moving RPI / 2 of them
+  constexpr bool G32 = IntraG32<DTQ, DTG, EXACT, PRO>::value;
+  constexpr bool STG = (DTG != 0) || G32;
+  constexpr int ROWB = DK * 2;          // bytes per staged 16-bit row
   constexpr int NCH = ROWB / 16;        // 16-byte chunks per row
   constexpr int RPI = 1024 / ROWB;      // rows per copy instruction
-  // Without the fused prologue three [64][DK] 16-bit tensors are staged at a
-  // time: q, k and g, then v in g's rows once the wave has read its g.
-  static_assert(PRO || !(STQ || STG) || sizeof(SM) >= 3 * kC * ROWB, "staging area exceeds the shared buffers");
+  constexpr int ROWG = G32 ? 2 * ROWB : ROWB;   // bytes per staged g row
+  constexpr int NCHG = ROWG / 16;
+  constexpr int RPIG = 1024 / ROWG;
+  // Without the fused prologue three [64][DK] tensors are staged at a time:
+  // q, k and g, then v in g's rows once the wave has read its g.
+  static_assert(PRO || !(STQ || STG) || IntraLds<DK, DV, EXACT, PRO, G32>::kBytes >= kC * (2 * ROWB + ROWG),
+                "staging area exceeds the shared buffers");
   static_assert(DK == DV, "staging assumes dk == dv");
   static_assert(!PRO || (DTQ == 1 && !EXACT), "the fused prologue stages bf16 projections");
   unsigned char* const stg = reinterpret_cast<unsigned char*>(&sm);
@@ -204,6 +226,11 @@ __device__ __forceinline__ void intra_chunk(const IntraArgs& a, const UnitRef& U
       if (t == 2) return stg + row * ROWB;
       const int tt = (t == 3) ? 2 : t;   // q, k, v
       return stg + (kC + (tt * 4 + W) * HR + (row - 16 * W + RPI)) * ROWB;
+    } else if constexpr (G32) {
+      // g rows first; a wave's 16 v rows, dense, over its own g rows
+      if (t == 2) return stg + row * ROWG;
+      if (t == 3) return stg + (row & ~15) * ROWG + (row & 15) * ROWB;
+      return stg + kC * ROWG + (t * kC + row) * ROWB;
     } else {
       return stg + ((t == 3 ? 2 : t) * kC + row) * ROWB;   // v over g
     }
@@ -294,20 +321,22 @@ __device__ __forceinline__ void intra_chunk(const IntraArgs& a, const UnitRef& U
   // each row is read by this chunk-head only, and kept in L2 it would
   // displace workspace lines; config 1 225 -> 215 us when introduced)
   auto stage_rows = [&](const int t) {
-    const u16* src = static_cast<const u16*>(t == 0 ? a.q : t == 1 ? a.k : t == 2 ? a.g : a.v);
-    const int nc = (t == 2) ? NPER : NQKV;
+    const unsigned char* src = static_cast<const unsigned char*>(t == 0 ? a.q : t == 1 ? a.k : t == 2 ? a.g : a.v);
+    const bool g32 = G32 && t == 2;
+    const int rowb = g32 ? ROWG : ROWB, nch = g32 ? NCHG : NCH, rpi = g32 ? RPIG : RPI;
+    const int nc = (t == 2) ? 16 / rpi : NQKV;
     const int r0 = (PRO && t != 2) ? 16 * W - RPI : 16 * W;         // first row copied
 #pragma unroll
     for (int i = 0; i < nc; ++i) {
-      const int row = r0 + RPI * i + l / NCH;                       // chunk row this lane copies
-      const int cidx = (l % NCH) ^ (row & (NCH - 1));               // source chunk of LDS chunk l % NCH
+      const int row = r0 + rpi * i + l / nch;                       // chunk row this lane copies
+      const int cidx = (l % nch) ^ (row & (nch - 1));               // source chunk of LDS chunk l % nch
       // rows past the end re-read a valid row; history rows before a
       // sequence's first chunk (replaced by the carried inputs) read row 0
       int rv = min(row, U.len - 1);
       if (PRO && U.n == 0) rv = max(rv, 0);
       const int64_t srow = U.row0 + rv;
-      const u16* gsrc = src + (srow * H + h) * DK + cidx * 8;
-      unsigned char* ldst = stg_row(t, r0 + RPI * i);
+      const unsigned char* gsrc = src + (srow * H + h) * static_cast<int64_t>(rowb) + cidx * 16;
+      unsigned char* ldst = stg_row(t, r0 + rpi * i);
       __builtin_amdgcn_global_load_lds(gsrc, ldst, 16, 0, kCpolStream);
     }
   };
@@ -352,7 +381,20 @@ __device__ __forceinline__ void intra_chunk(const IntraArgs& a, const UnitRef& U
     __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "workgroup", "local");
   }
   uint2 sw[2 * NJ];
-  if constexpr (STG) stg_read_all(2, sw);
+  u32x4 sg[G32 ? 2 * NJ : 1];
+  if constexpr (G32) {
+    // four fp32 channels ch0 = 32j + 16hf + 4gq .. +3: one 16-byte chunk
+#pragma unroll
+    for (int j = 0; j < NJ; ++j)
+#pragma unroll
+      for (int hf = 0; hf < 2; ++hf) {
+        const int ci = 8 * j + 4 * hf + gq;
+        sg[2 * j + hf] = ds_read_b128_raw(stg_row(2, c) + (ci ^ (c & (NCHG - 1))) * 16);
+      }
+    lds_settle(sg);
+  } else if constexpr (STG) {
+    stg_read_all(2, sw);
+  }
   // g is in registers (settled): v's copies may now overwrite its rows; they
   // are the newest copies, so the waits below for k, q and then v are as
   // before
@@ -362,9 +404,10 @@ __device__ __forceinline__ void intra_chunk(const IntraArgs& a, const UnitRef& U
 #pragma unroll
     for (int hf = 0; hf < 2; ++hf) {
       f4 z = {0, 0, 0, 0};
-      if constexpr (STG) z = unpack4<DTG>(sw[2 * j + hf]);
+      if constexpr (G32) z = __builtin_bit_cast(f4, sg[2 * j + hf]);
+      else if constexpr (STG) z = unpack4<DTG>(sw[2 * j + hf]);
       else if (valid) z = ld4<DTG>(a.g, bq + 32 * j + 4 * gq + 16 * hf);
-      if constexpr (!STG) {
+      if constexpr (DTG == 0) {
         if (a.gates_alpha) {
 #pragma unroll
           for (int e = 0; e < 4; ++e) z[e] = logf(z[e]);   // g = log(alpha)
@@ -889,21 +932,20 @@ __device__ __forceinline__ void intra_chunk(const IntraArgs& a, const UnitRef& U
   }
 }
 
-// Shared memory of the intra kernel: IntraSmem, or with the fused prologue
-// the larger staging area it needs (64 rows of g plus 4 waves x 3 tensors x
-// (16 + history) rows), whichever is bigger.
-template <int DK, int DV, bool EXACT, bool PRO>
+template <int DK, int DV, bool EXACT, bool PRO, bool G32>
 struct IntraLds {
   static constexpr int ROWB = DK * 2;
   static constexpr int RPI = 1024 / ROWB;
-  static constexpr size_t kStage = PRO ? static_cast<size_t>(kC + 12 * (16 + RPI)) * ROWB : 0;
+  static constexpr size_t kStage = PRO   ? static_cast<size_t>(kC + 12 * (16 + RPI)) * ROWB
+                                   : G32 ? static_cast<size_t>(kC) * 4 * ROWB   // g fp32, q, k
+                                         : 0;
   static constexpr size_t kBytes = sizeof(IntraSmem<DK, DV, EXACT>) > kStage ? sizeof(IntraSmem<DK, DV, EXACT>) : kStage;
 };
 
 template <int DK, int DV, int DTQ, int DTG, bool EXACT, bool PRO>
 __global__ __launch_bounds__(256, EXACT ? 1 : 2)
 void kda_intra_kernel(IntraArgs a) {
-  __shared__ __attribute__((aligned(16))) unsigned char lds[IntraLds<DK, DV, EXACT, PRO>::kBytes];
+  __shared__ __attribute__((aligned(16))) unsigned char lds[IntraLds<DK, DV, EXACT, PRO, IntraG32<DTQ, DTG, EXACT, PRO>::value>::kBytes];
   IntraSmem<DK, DV, EXACT>& sm = *reinterpret_cast<IntraSmem<DK, DV, EXACT>*>(lds);
   const int H = a.geom.H;
   if (a.status_clear != nullptr && blockIdx.x == 0 && threadIdx.x == 0) *a.status_clear = 0;
@@ -1947,9 +1989,9 @@ void kda_state_wide_kernel(StateArgs a) {
 // barriers of intra_chunk on the staged 16-bit path: the staging barrier and #1-#3
 constexpr int kIntraBarriers = 4;
 
-template <int DK, int DV>
+template <int DK, int DV, bool G32>
 struct OverlapLds {
-  static constexpr size_t kIntra = 2 * sizeof(IntraSmem<DK, DV, false>);
+  static constexpr size_t kIntra = 2 * IntraLds<DK, DV, false, false, G32>::kBytes;
   static constexpr size_t kState = sizeof(ColSmem<DK>);
   static constexpr size_t kBytes = kIntra > kState ? kIntra : kState;
 };
@@ -1957,7 +1999,8 @@ struct OverlapLds {
 template <int DK, int DV, int DTQ, int DTG, int OUT_DT>
 __global__ __launch_bounds__(512, 1)
 void kda_overlap_kernel(IntraArgs ia, StateArgs sa, int n_state) {
-  __shared__ __attribute__((aligned(16))) unsigned char lds[OverlapLds<DK, DV>::kBytes];
+  constexpr bool G32 = IntraG32<DTQ, DTG, false, false>::value;
+  __shared__ __attribute__((aligned(16))) unsigned char lds[OverlapLds<DK, DV, G32>::kBytes];
   const int wave = threadIdx.x >> 6;
   if (static_cast<int>(blockIdx.x) < n_state) {
     constexpr int SPLITS = DV / 32;
@@ -1992,7 +2035,7 @@ void kda_overlap_kernel(IntraArgs ia, StateArgs sa, int n_state) {
   } else {
     const int grp = wave >> 2;
     IntraSmem<DK, DV, false>& sm =
-        *reinterpret_cast<IntraSmem<DK, DV, false>*>(lds + grp * sizeof(IntraSmem<DK, DV, false>));
+        *reinterpret_cast<IntraSmem<DK, DV, false>*>(lds + grp * IntraLds<DK, DV, false, false, G32>::kBytes);
     const int H = ia.geom.H;
     const int x = 2 * (static_cast<int>(blockIdx.x) - n_state) + grp;
     if (x < ia.total) {

@@ -209,9 +209,15 @@ __device__ __forceinline__ uint2 ds_read_b64_raw(const void* p) {
   asm volatile("ds_read_b64 %0, %1" : "=v"(v) : "v"(addr));
   return v;
 }
-// 4- and 2-byte forms of the same (the 2-byte read zero-extends), and LDS
-// writes the compiler does not see either (it would otherwise wait for every
-// outstanding direct copy before them too).
+// 16-, 4- and 2-byte forms of the same (the 2-byte read zero-extends), and
+// LDS writes the compiler does not see either (it would otherwise wait for
+// every outstanding direct copy before them too).
+__device__ __forceinline__ u32x4 ds_read_b128_raw(const void* p) {
+  u32x4 v;
+  const unsigned addr = static_cast<unsigned>(reinterpret_cast<uintptr_t>(p));
+  asm volatile("ds_read_b128 %0, %1" : "=v"(v) : "v"(addr));
+  return v;
+}
 __device__ __forceinline__ unsigned ds_read_b32_raw(const void* p) {
   unsigned v;
   const unsigned addr = static_cast<unsigned>(reinterpret_cast<uintptr_t>(p));
@@ -236,6 +242,12 @@ __device__ __forceinline__ void ds_write_b16_raw(void* p, unsigned v) {
 // use of them is scheduled before it.
 template <int N>
 __device__ __forceinline__ void lds_settle(uint2 (&v)[N]) {
+  asm volatile("s_waitcnt lgkmcnt(0)" ::: "memory");
+#pragma unroll
+  for (int i = 0; i < N; ++i) asm volatile("" : "+v"(v[i]));
+}
+template <int N>
+__device__ __forceinline__ void lds_settle(u32x4 (&v)[N]) {
   asm volatile("s_waitcnt lgkmcnt(0)" ::: "memory");
 #pragma unroll
   for (int i = 0; i < N; ++i) asm volatile("" : "+v"(v[i]));
