@@ -374,6 +374,14 @@ __device__ __forceinline__ void intra_chunk(const IntraArgs& a, const UnitRef& U
   // chunk's decay.
   float kr[NJ][8], qr[NJ][8], kc[NJ][8], Gt[NJ][8];
   float vr[NJV][8];
+  // a gate value in log2 units: g log2(e), or with alpha gates (cc_scan:
+  // g holds alpha) log2(alpha) directly by the hardware base-2 logarithm
+  auto decay2 = [&](float z) -> float {
+    if constexpr (DTG == 0) {
+      if (a.gates_alpha) return __builtin_amdgcn_logf(z);
+    }
+    return z * kLog2e;
+  };
 
   // g -> log2 decay, then the tile-local inclusive scan
   if constexpr (SPLIT) {
@@ -407,14 +415,8 @@ __device__ __forceinline__ void intra_chunk(const IntraArgs& a, const UnitRef& U
       if constexpr (G32) z = __builtin_bit_cast(f4, sg[2 * j + hf]);
       else if constexpr (STG) z = unpack4<DTG>(sw[2 * j + hf]);
       else if (valid) z = ld4<DTG>(a.g, bq + 32 * j + 4 * gq + 16 * hf);
-      if constexpr (DTG == 0) {
-        if (a.gates_alpha) {
 #pragma unroll
-          for (int e = 0; e < 4; ++e) z[e] = logf(z[e]);   // g = log(alpha)
-        }
-      }
-#pragma unroll
-      for (int e = 0; e < 4; ++e) Gt[j][4 * hf + e] = valid ? z[e] * kLog2e : 0.f;
+      for (int e = 0; e < 4; ++e) Gt[j][4 * hf + e] = valid ? decay2(z[e]) : 0.f;
     }
 #pragma unroll
   for (int j = 0; j < NJ; ++j)
@@ -687,16 +689,10 @@ __device__ __forceinline__ void intra_chunk(const IntraArgs& a, const UnitRef& U
           const int ch0 = 32 * j + 4 * gq + 16 * hf;
           f4 x = {0, 0, 0, 0}, y = {0, 0, 0, 0}, z = {0, 0, 0, 0};
           if (valid) { x = ld4<DTQ>(a.q, bq + ch0); y = ld4<DTQ>(a.k, bq + ch0); z = ld4<DTG>(a.g, bq + ch0); }
-          if constexpr (DTG == 0) {
-            if (a.gates_alpha) {
-#pragma unroll
-              for (int e = 0; e < 4; ++e) z[e] = logf(z[e]);
-            }
-          }
 #pragma unroll
           for (int e = 0; e < 4; ++e) {
             const int ee = 4 * hf + e;
-            const float gt = row_scan16(valid ? z[e] * kLog2e : 0.f);
+            const float gt = row_scan16(valid ? decay2(z[e]) : 0.f);
             const float g7 = row_bcast<7>(gt);
             const float fr = fast_exp2(gt - g7);
             ad[ee] = y[e] * fast_exp2(g7 - gt);

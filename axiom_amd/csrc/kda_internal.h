@@ -45,7 +45,8 @@ struct IntraArgs {
   int* status_clear;   // non-null: the launch zeroes the call's status word
   int total;           // chunk-heads of the launch (overlapped-segment launch only)
   // cc_scan operands (fp32 gates only): g holds alpha (the decay factor; the
-  // kernel takes logf(alpha)) and beta holds beta32 [T*H][32] (the kernel
+  // kernel takes log2(alpha) by the hardware logarithm, the log-decay in the
+  // base-2 units it works in) and beta holds beta32 [T*H][32] (the kernel
   // takes the mean of the 32 columns, summed in column order)
   int gates_alpha;
 };
