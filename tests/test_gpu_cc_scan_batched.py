@@ -129,3 +129,29 @@ def test_batched_shape_errors(cuda):
         axiom_amd.cc_scan(q, k, v, alpha, beta32[:1].contiguous(), S, chunk=32)
     with pytest.raises(ValueError, match="do must be"):
         axiom_amd.cc_scan_bwd(q, k, v, alpha, beta32, S, do[0], chunk=32)
+
+
+@pytest.mark.parametrize("B", [1, 2])
+def test_seam_at_the_config1_element_shape(cuda, B):
+    """The seam at its production shape, T=4096 H=16 d=128 (one element runs
+    as two overlapped segments, two elements as one sequential launch), with
+    unequal beta32 columns: sampled heads of every element against the oracle's
+    cc_scan on that head alone."""
+    import axiom_amd
+    T, H, d = 4096, 16, 128
+    case = _batch_case(B, T, H, d, seed=4096 + B)
+    ops, _, _ = _dev(case, cuda)
+    if B == 1:
+        o, S_new = axiom_amd.cc_scan(*(t[0].contiguous() for t in ops), tile=16, chunk=64)
+        o, S_new = o[None], S_new[None]
+    else:
+        o, S_new = axiom_amd.cc_scan(*ops, tile=16, chunk=64)
+    torch.cuda.synchronize()
+    qkv, alpha, beta32, S, _, _ = case
+    for b in range(B):
+        for h in (0, H - 1):
+            cols = slice(h * d, (h + 1) * d)
+            o_ref, S_ref = K.cc_scan(*(_bf16_values(x[b][:, cols]) for x in qkv), alpha[b][:, cols],
+                                     beta32[b][:, h * 32:(h + 1) * 32], S[b][h:h + 1], chunk=64)
+            assert_close(f"o[{b}] head {h}", o[b][:, cols], o_ref, TOL["bf16"])
+            assert_close(f"S_new[{b}] head {h}", S_new[b][h:h + 1], S_ref, TOL["bf16"])
