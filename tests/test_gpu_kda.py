@@ -84,8 +84,11 @@ def test_fp16_inputs(cuda):
     assert_close("ht", ht, ht_ref, TOL["fp16"])
 
 
-def test_bf16_with_fp32_gates(cuda):
-    d = inputs.make_inputs(1, 256, 4, 128, 128, seed=6, dtype="bf16")
+@pytest.mark.parametrize("T,dk", [(256, 128), (200, 128), (200, 64)])
+def test_bf16_with_fp32_gates(cuda, T, dk):
+    # fp32 gate rows are staged through LDS like the 16-bit rows (a ragged T
+    # re-reads the last row for the rows past the end)
+    d = inputs.make_inputs(1, T, 4, dk, dk, seed=6, dtype="bf16")
     d["g"] = (d["g"] * np.float32(0.9731)).astype(np.float32)   # not bf16-representable
     o, ht = _run_chunk(cuda, d, "bf16", gates_fp32=True)
     o_ref, ht_ref = _oracle(d)
