@@ -712,10 +712,11 @@ int kda_cc_scan_batched(hipStream_t stream, const void* q, const void* k, const 
   const size_t g_bytes = align_up(th * dk * 4);
   const size_t b_bytes = align_up(th * 4);
   // The (B, T, H*d) operands are the [B, T, H, d] layout of the chunked
-  // forward; its intra kernel takes g = log(alpha) and beta = mean(beta32)
-  // itself (the arithmetic of kda_adapt_kernel, which the backward runs).
-  // The workspace keeps the adapter's g and beta areas unused, so both
-  // directions size it the same way.
+  // forward; its intra kernel takes the log-decay of alpha (log2 alpha, in
+  // its own units) and beta = mean(beta32) (in kda_adapt_kernel's column
+  // order; the backward runs that adapter) itself.  The workspace keeps the
+  // adapter's g and beta areas unused, so both directions size it the same
+  // way.
   void* rest = static_cast<char*>(workspace) + g_bytes + b_bytes;
   return chunk_fwd_impl(stream, q, k, v, alpha, beta32, S_in, nullptr, 0, o, S_out, B, T, H, dk, dv,
                         kC, 1.0f, KDA_DTYPE_BF16_F32GATES, KDA_DTYPE_F32, rest,
