@@ -198,7 +198,8 @@ __device__ __forceinline__ void intra_chunk(const IntraArgs& a, const UnitRef& U
   // wave-local wait suffices; 16-byte chunks are XOR-swizzled by row so the
   // slot-order reads below are spread over the LDS banks.  The staging area
   // aliases the buffers of the later phases (barrier before their first use).
-  // fp32 tensors are loaded per lane as before.
+  // fp32 g rows are staged the same way when q, k, v are 16-bit; the exact
+  // mode's fp32 tensors are loaded per lane.
   constexpr bool STQ = (DTQ != 0);
   // fp32 gates with 16-bit q, k, v (G32): g is staged too, in fp32 rows of
   // twice the bytes, each copy instruction moving RPI / 2 of them
