@@ -440,3 +440,11 @@ def test_misaligned_pointers_are_rejected(L, name, n_ptrs, odd_at, ints, tail):
     msg = _lib.last_error()
     assert rc == _lib.KDA_ERR_INVALID_ARGUMENT, msg
     assert "aligned" in msg, msg
+
+
+def test_cc_scan_rejects_a_misaligned_beta32(L):
+    # the intra kernel reads the seam's beta32 rows 16 bytes at a time
+    rc = L.kda_cc_scan(_NULL, _FAKE, _FAKE, _FAKE, _FAKE, _ODD, _FAKE, _FAKE, _FAKE,
+                       64, 1, 64, 64, 16, 32, _FAKE, 1 << 40)
+    msg = _lib.last_error()
+    assert rc == _lib.KDA_ERR_INVALID_ARGUMENT and "beta32" in msg and "aligned" in msg, msg
