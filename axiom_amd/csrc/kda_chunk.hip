@@ -17,7 +17,9 @@
 //     so both MFMA operands stay in [0, 1] and run in fp16;
 //   diagonal tile (c >= i):  2^(G_c - G_i) = (R_c 2^-D) * Cf_i, operands up
 //     to 2^|D|, run as fp32 MFMA (16x16x4); a tile whose total decay passes
-//     2^-100 takes a slower mid-tile-anchored path with the same result;
+//     2^-100 takes a slower path that splits each pair at the highest bit
+//     where c and i differ, through an anchor row between them, so every
+//     factor stays <= 1 however strong the decay;
 //   gamma = R * 2^(totals before the tile), lambda = Cf * 2^(totals after).
 // The per-channel constants (2^pre, 2^post, 2^-D, M) are computed once per
 // wave into LDS.
@@ -376,10 +378,16 @@ __device__ __forceinline__ void intra_chunk(const IntraArgs& a, const UnitRef& U
   float kr[NJ][8], qr[NJ][8], kc[NJ][8], Gt[NJ][8];
   float vr[NJV][8];
   // a gate value in log2 units: g log2(e), or with alpha gates (cc_scan:
-  // g holds alpha) log2(alpha) directly by the hardware base-2 logarithm
+  // g holds alpha) log2(alpha) directly by the hardware base-2 logarithm.
+  // That instruction flushes a denormal input to zero (log2 = -inf, and
+  // -inf - -inf = NaN in the decay factors): a denormal alpha is scaled by
+  // 2^32 first and 32 taken off the logarithm.
   auto decay2 = [&](float z) -> float {
     if constexpr (DTG == 0) {
-      if (a.gates_alpha) return __builtin_amdgcn_logf(z);
+      if (a.gates_alpha) {
+        const bool dn = z < 1.17549435e-38f;
+        return __builtin_amdgcn_logf(dn ? z * 4294967296.0f : z) - (dn ? 32.0f : 0.0f);
+      }
     }
     return z * kLog2e;
   };
@@ -676,36 +684,14 @@ __device__ __forceinline__ void intra_chunk(const IntraArgs& a, const UnitRef& U
       accQ[s] = mma32(accQ[s], A, cvt8<EXACT>(qrj * M3));
     }
     // diagonal tile in fp32
-    {
+    if (!extreme) {
       f8 ad, bk, bqd;
-      if (!extreme) {
 #pragma unroll
-        for (int e = 0; e < 8; ++e) { ad[e] = kc[j][e]; bk[e] = krj[e] * iD[e]; bqd[e] = qrj[e] * iD[e]; }
-      } else {
-        // mid-tile anchor: 2^(Gt_c - Gt_7) * 2^(Gt_7 - Gt_i); k, q and g are
-        // reloaded and the tile-local cumsum is recomputed (the same scan, so
-        // the same values), which keeps Gt out of the registers live here
-#pragma unroll
-        for (int hf = 0; hf < 2; ++hf) {
-          const int ch0 = 32 * j + 4 * gq + 16 * hf;
-          f4 x = {0, 0, 0, 0}, y = {0, 0, 0, 0}, z = {0, 0, 0, 0};
-          if (valid) { x = ld4<DTQ>(a.q, bq + ch0); y = ld4<DTQ>(a.k, bq + ch0); z = ld4<DTG>(a.g, bq + ch0); }
-#pragma unroll
-          for (int e = 0; e < 4; ++e) {
-            const int ee = 4 * hf + e;
-            const float gt = row_scan16(valid ? decay2(z[e]) : 0.f);
-            const float g7 = row_bcast<7>(gt);
-            const float fr = fast_exp2(gt - g7);
-            ad[ee] = y[e] * fast_exp2(g7 - gt);
-            bk[ee] = y[e] * fr;
-            bqd[ee] = x[e] * a.scale * fr;
-          }
-        }
-      }
+      for (int e = 0; e < 8; ++e) { ad[e] = kc[j][e]; bk[e] = krj[e] * iD[e]; bqd[e] = qrj[e] * iD[e]; }
       if constexpr (EXACT) {
         accK[W] = mma32(accK[W], ad, bk);
         accQ[W] = mma32(accQ[W], ad, bqd);
-      } else if (diag16 && !extreme) {
+      } else if (diag16) {
         const v8 a16 = cvt8<EXACT>(ad);
         accK[W] = mma32(accK[W], a16, cvt8<EXACT>(bk));
         accQ[W] = mma32(accQ[W], a16, cvt8<EXACT>(bqd));
@@ -723,6 +709,66 @@ __device__ __forceinline__ void intra_chunk(const IntraArgs& a, const UnitRef& U
         accQ[W] = mma32_bf16(accQ[W], ah, ql);
         accK[W] = mma32_bf16(accK[W], al, kh);
         accQ[W] = mma32_bf16(accQ[W], al, qh);
+      }
+    } else {
+      // Tile decay past 2^-100: no single row factor pair fits fp32, so the
+      // pair (c, i), c > i, splits at the highest bit h where c and i differ,
+      // through the anchor row a = (i | (2^h - 1)) in [i, c):
+      // 2^(G_c - G_a) * 2^(G_a - G_i), both factors <= 1 whatever the decay.
+      // At level h the key rows with bit h clear carry 2^(G_a - G_i), the
+      // query rows with bit h set 2^(G_c - G_a), every other row 0, and the
+      // level's products are kept for its own pairs only; the diagonal (Aqk)
+      // has factor 1 (pass hb = -1).  Each pass reloads k, q and g and
+      // recomputes the tile-local cumsum (the same scan, so the same values)
+      // and the passes are not unrolled: the rare path keeps its registers
+      // few, so the common path's allocation does not grow.
+#pragma unroll 1
+      for (int hb = -1; hb < 4; ++hb) {
+        const int an = (hb < 0) ? r : (r & ~((2 << hb) - 1)) | ((1 << hb) - 1);   // anchor of this row
+        const bool key = (hb < 0) || ((r >> hb) & 1) == 0;
+        f8 A, Bk, Bq;
+#pragma unroll
+        for (int hf = 0; hf < 2; ++hf) {
+          const int ch0 = 32 * j + 4 * gq + 16 * hf;
+          f4 x = {0, 0, 0, 0}, y = {0, 0, 0, 0}, z = {0, 0, 0, 0};
+          if (valid) { x = ld4<DTQ>(a.q, bq + ch0); y = ld4<DTQ>(a.k, bq + ch0); z = ld4<DTG>(a.g, bq + ch0); }
+#pragma unroll
+          for (int e = 0; e < 4; ++e) {
+            const int ee = 4 * hf + e;
+            const float gt = row_scan16(valid ? decay2(z[e]) : 0.f);
+            const float ga = __shfl(gt, (l & 48) | an, 64);
+            const float f = (hb < 0) ? 1.f : fast_exp2(key ? ga - gt : gt - ga);
+            A[ee] = key ? y[e] * f : 0.f;
+            Bk[ee] = (hb < 0 || key) ? 0.f : y[e] * f;
+            Bq[ee] = (hb < 0) ? x[e] * a.scale : key ? 0.f : x[e] * a.scale * f;
+          }
+        }
+        f4 tK = {0, 0, 0, 0}, tQ = {0, 0, 0, 0};
+        if constexpr (EXACT) {
+          tK = mma32(tK, A, Bk);
+          tQ = mma32(tQ, A, Bq);
+        } else {
+          b8 ah, al, kh, kl;
+          split_bf16(A, ah, al);
+          split_bf16(Bk, kh, kl);
+          tK = mma32_bf16(tK, ah, kh);
+          tK = mma32_bf16(tK, ah, kl);
+          tK = mma32_bf16(tK, al, kh);
+          split_bf16(Bq, kh, kl);
+          tQ = mma32_bf16(tQ, ah, kh);
+          tQ = mma32_bf16(tQ, ah, kl);
+          tQ = mma32_bf16(tQ, al, kh);
+        }
+#pragma unroll
+        for (int i = 0; i < 4; ++i) {
+          const int ii = 4 * gq + i;
+          if (hb < 0) {
+            if (r == ii) accQ[W][i] += tQ[i];
+          } else if (r > ii && ((r ^ ii) >> hb) == 1) {
+            accK[W][i] += tK[i];
+            accQ[W][i] += tQ[i];
+          }
+        }
       }
     }
 

@@ -17,8 +17,10 @@ kernels do (fp32 accumulation of rounded operands):
 * diagonal score tiles: fp16 operands ``k Cf`` and ``(k or q) R 2^-D`` when
   every channel's tile decay is above 2^-12 and the operands are at most 8
   in magnitude, else a three-term bf16 hi/lo split
-  (``hi*hi + hi*lo + lo*hi``); a tile whose decay passes 2^-100 anchors at
-  its row 7 (``2^(Gt_c - Gt_7) 2^(Gt_7 - Gt_i)``) on the hi/lo split;
+  (``hi*hi + hi*lo + lo*hi``); a tile whose decay passes 2^-100 splits each
+  pair (c, i) at the highest bit h where c and i differ, through the anchor
+  row a = i | (2^h - 1) (``2^(Gt_c - Gt_a) 2^(Gt_a - Gt_i)``, both <= 1), one
+  hi/lo product per level;
 * ``L = beta Akk`` fp32; ``T = (I+L)^-1``: diagonal 16x16 blocks inverted in
   fp32 and stored fp16, off-diagonal blocks by the blocked recurrence
   ``T_Rs = -T_RR sum_j L_Rj T_js`` on fp16 operands;
@@ -79,6 +81,39 @@ class _Round:
         return hi, self.b(x - hi)
 
 
+
+def _extreme_diag(rd, kk, qq, gt):
+    """Diagonal 16x16 tile of a tile whose decay passes 2^-100, as the intra
+    kernel forms it: the pair (c, i), c > i, through the anchor row
+    a = i | (2^h - 1) of the highest bit h where c and i differ, with factors
+    2^(G_c - G_a) (query row) and 2^(G_a - G_i) (key row), both <= 1; one
+    product per level h (and one for the diagonal, factor 1), each kept for
+    its own pairs.  Returns the Akk and Aqk blocks [N, 16 (c), 16 (i)]."""
+    def prod(bq, a):
+        if rd.exact:
+            return rd.mm(bq, a.transpose(1, 2))
+        ah, al = rd.hilo(a)
+        h, l_ = rd.hilo(bq)
+        return rd.f(h @ ah.transpose(1, 2) + l_ @ ah.transpose(1, 2) + h @ al.transpose(1, 2))
+    c = torch.arange(16)[:, None]
+    i = torch.arange(16)[None, :]
+    blk_k = torch.zeros(kk.shape[0], 16, 16, dtype=F64)
+    blk_q = torch.where((c == i)[None], prod(qq, kk), blk_k)
+    for hb in range(4):
+        an = torch.tensor([(r & ~((2 << hb) - 1)) | ((1 << hb) - 1) for r in range(16)])
+        key = torch.tensor([((r >> hb) & 1) == 0 for r in range(16)])[None, :, None]
+        ga = gt[:, an]
+        fk = rd.f(torch.exp2(rd.f(ga - gt)))
+        fq = rd.f(torch.exp2(rd.f(gt - ga)))
+        zero = torch.zeros_like(kk)
+        a = torch.where(key, rd.f(kk * fk), zero)
+        bk = torch.where(key, zero, rd.f(kk * fq))
+        bq = torch.where(key, zero, rd.f(qq * fq))
+        keep = ((c > i) & (((c ^ i) >> hb) == 1))[None]
+        blk_k = torch.where(keep, prod(bk, a), blk_k)
+        blk_q = torch.where(keep, prod(bq, a), blk_q)
+    return blk_k, blk_q
+
 def _scores_tile_pair(rd: _Round, row_op, col_op):
     return rd.mm(row_op, col_op.transpose(-1, -2))
 
@@ -130,14 +165,6 @@ def _chunk(rd: _Round, q, k, v, g, beta, S, diag: str):
         ad = kc[:, rows]
         bk = rd.f(kr[:, rows] * iD)
         bq = rd.f(qr[:, rows] * iD)
-        if bool(extreme.any()):
-            g7 = Gt[:, 16 * r + 7][:, None]
-            gt = Gt[:, rows]
-            fr = rd.f(torch.exp2(rd.f(gt - g7)))
-            x_ = extreme[:, None, None]
-            ad = torch.where(x_, rd.f(k[:, rows] * rd.f(torch.exp2(rd.f(g7 - gt)))), ad)
-            bk = torch.where(x_, rd.f(k[:, rows] * fr), bk)
-            bq = torch.where(x_, rd.f(q[:, rows] * fr), bq)
         mx = torch.stack([kc[:, rows].abs().amax((1, 2)), kr[:, rows].abs().amax((1, 2)),
                           qr[:, rows].abs().amax((1, 2))]).amax(0)
         fp16_ok = (~extreme) & (Dr > -12).all(1) & (mx <= 8)             # [N]
@@ -158,6 +185,11 @@ def _chunk(rd: _Round, q, k, v, g, beta, S, diag: str):
             ok = fp16_ok[:, None, None]
             blk_k = torch.where(ok, f16_k, hl_k)
             blk_q = torch.where(ok, f16_q, hl_q)
+        if bool(extreme.any()):
+            bk_x, bq_x = _extreme_diag(rd, k[:, rows], q[:, rows], Gt[:, rows])
+            x_ = extreme[:, None, None]
+            blk_k = torch.where(x_, bk_x, blk_k)
+            blk_q = torch.where(x_, bq_x, blk_q)
         zero = torch.zeros((), dtype=F64)
         Akk[:, rows, rows] = torch.where(ri > ci, blk_k, zero)
         Aqk[:, rows, rows] = torch.where(ri >= ci, blk_q, zero)

@@ -33,12 +33,26 @@ def _ref(x, scale=1.0):
 @pytest.mark.parametrize("B,T,H,d,seed,h0,gm", [
     (1, 200, 2, 64, 0, 0.05, 1.0),      # ragged tail, initial state
     (2, 128, 2, 128, 1, 0.0, 8.0),      # strong decay: hi/lo diagonal tiles
-    (1, 96, 1, 64, 2, 0.02, 40.0),      # tiles past 2^-100: the row-7 anchor
+    (1, 96, 1, 64, 2, 0.02, 40.0),      # tiles past 2^-100: the level anchors
 ])
 def test_exact_mode_equals_float64_oracle(B, T, H, d, seed, h0, gm):
     """With every rounding switched off the emulated kernel algebra (tile
     factorisation, blocked inverse, state step) is the chunk body itself."""
     x = _case(B, T, H, d, seed, h0, gm)
+    o, s = _run(x, exact=True)
+    o_r, s_r = _ref(x)
+    assert K.max_abs(o.numpy(), o_r.numpy()) <= 1e-11 * max(1.0, float(o_r.abs().max()))
+    assert K.max_abs(s.numpy(), s_r.numpy()) <= 1e-11 * max(1.0, float(s_r.abs().max()))
+
+
+def test_exact_mode_with_decay_spikes():
+    """Single steps that decay by e^-150 (past fp32's range in one factor): the
+    extreme tiles' level anchors pair every row with an anchor between, and
+    the algebra still equals the float64 oracle."""
+    x = _case(1, 192, 2, 64, 5, 0.02, 1.0)
+    rng = np.random.default_rng(5)
+    spike = rng.random(x["g"].shape) < 0.03
+    x["g"] = np.where(spike, np.float32(-150.0), x["g"]).astype(np.float32)
     o, s = _run(x, exact=True)
     o_r, s_r = _ref(x)
     assert K.max_abs(o.numpy(), o_r.numpy()) <= 1e-11 * max(1.0, float(o_r.abs().max()))

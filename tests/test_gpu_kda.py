@@ -156,6 +156,31 @@ def test_cc_scan_seam(cuda):
     assert_close("S_new", S_new, s_ref[0], TOL["bf16"])
 
 
+def test_cc_scan_seam_denormal_alpha(cuda):
+    """Denormal alpha values (a gate that has decayed past fp32's normal
+    range) are finite log-decays of -87 to -103, as in the oracle: the
+    forward must not turn them into -inf (and NaN factors)."""
+    import axiom_amd
+    T, H, d = 128, 2, 128
+    dd = inputs.make_inputs(1, T, H, d, d, seed=14, dtype="bf16", h0_std=0.05)
+    alpha = np.exp(dd["g"].astype(np.float64)).astype(np.float32)
+    rng = np.random.default_rng(14)
+    pick = rng.random(alpha.shape) < 0.02
+    alpha[pick] = rng.uniform(1e-44, 1e-38, size=int(pick.sum())).astype(np.float32)
+    assert (alpha[pick] < np.finfo(np.float32).tiny).all() and (alpha > 0).all()
+    g_eff = np.log(alpha.astype(np.float64)).astype(np.float32)
+    beta32 = np.repeat(dd["beta"][..., None], 32, axis=-1).reshape(T, H * 32)
+    q, k, v = (to_dev(dd[n].reshape(T, H * d), torch.bfloat16, cuda) for n in ("q", "k", "v"))
+    S = to_dev(dd["h0"][0], torch.float32, cuda)
+    o, S_new = axiom_amd.cc_scan(q, k, v, to_dev(alpha.reshape(T, H * d), torch.float32, cuda),
+                                 to_dev(beta32, torch.float32, cuda), S, tile=16, chunk=32)
+    torch.cuda.synchronize()
+    assert torch.isfinite(o).all() and torch.isfinite(S_new).all()
+    o_ref, s_ref = K.chunk_fwd(dd["q"], dd["k"], dd["v"], g_eff, dd["beta"], h0=dd["h0"], chunk=64)
+    assert_close("o", o.reshape(1, T, H, d), o_ref, TOL["bf16"])
+    assert_close("S_new", S_new, s_ref[0], TOL["bf16"])
+
+
 def test_cc_scan_errors(cuda):
     import axiom_amd
     T, H, d = 96, 2, 128

@@ -57,6 +57,34 @@ def test_forward_strong_decay(cuda, prec, d):
     assert_close("ht", ht, ht_ref, TOL[prec])
 
 
+@pytest.mark.parametrize("prec,d", [("bf16", 128), ("bf16", 64), ("fp32", 64)])
+def test_forward_decay_spikes(cuda, prec, d):
+    """Single steps that decay by e^-150 (2^-216, past fp32's range in one
+    factor) in 3 % of the gate entries: the extreme tiles' pairs go through
+    anchors between their rows, so o and the final state stay finite and on
+    the oracle."""
+    import axiom_amd
+    x = inputs.make_inputs(2, 192, 2, d, d, seed=41 + d, dtype="fp32", h0_std=0.05)
+    rng = np.random.default_rng(41 + d)
+    x["g"] = np.where(rng.random(x["g"].shape) < 0.03, np.float32(-150.0), x["g"]).astype(np.float32)
+    if prec == "bf16":
+        for n in ("q", "k", "v", "g", "beta"):
+            x[n] = inputs.bf16_round(x[n])
+    dt = TDT[prec]
+    ts = [to_dev(x[n], dt, cuda) for n in ("q", "k", "v", "g", "beta")]
+    h0 = to_dev(x["h0"], torch.float32, cuda)
+    print(f"[decay spikes fwd] {prec} d={d}", flush=True)
+    o, ht = axiom_amd.kda_chunk_fwd(*ts, initial_state=h0)
+    torch.cuda.synchronize()
+    assert torch.isfinite(o).all() and torch.isfinite(ht).all()
+    # the token-by-token oracle: the chunked one forms e^(G_c - G_i) from
+    # e^G and e^-G, which leave float64's range once a channel's decay within
+    # a chunk passes e^-709 (a few spikes in one channel)
+    o_ref, ht_ref = K.recurrent_fwd(x["q"], x["k"], x["v"], x["g"], x["beta"], h0=x["h0"])
+    assert_close("o", o, o_ref, TOL[prec])
+    assert_close("ht", ht, ht_ref, TOL[prec])
+
+
 @pytest.mark.parametrize("prec,d", [("bf16", 128), ("fp32", 64)])
 def test_backward_strong_decay(cuda, prec, d):
     import axiom_amd
