@@ -529,6 +529,29 @@ __device__ __forceinline__ void intra_chunk(const IntraArgs& a, const UnitRef& U
     stg_read_all(0, sq);
     stg_read_all(1, sw);
   }
+  if constexpr (PRO) {
+    // The anchored path of an extreme tile (below) re-reads q and k per
+    // level; with the fused prologue they exist only here (the convolved bf16
+    // rows in LDS are overwritten after the staging barrier).  A wave whose
+    // tile takes that path parks its lane's q and k words in this
+    // chunk-head's gamma*q and W slots of its row tile, which are written
+    // later (gamma*q of K step j at the end of that step, after its last
+    // read; W by the final products, after barrier #3), in the slot order
+    // the path reads them back in.
+    float dm = 0.f;
+#pragma unroll
+    for (int j = 0; j < NJ; ++j)
+#pragma unroll
+      for (int e = 0; e < 8; ++e) dm = fminf(dm, row_bcast<15>(Gt[j][e]));
+    if (__any(dm < -100.f)) {
+#pragma unroll
+      for (int j = 0; j < NJ; ++j) {
+        const int64_t slot = (chead * (kC / 16) * NJ + (W * NJ + j)) * 512 + l * 8;
+        *reinterpret_cast<uint4*>(oGQ + slot) = uint4{sq[2 * j].x, sq[2 * j].y, sq[2 * j + 1].x, sq[2 * j + 1].y};
+        *reinterpret_cast<uint4*>(oW + slot) = uint4{sw[2 * j].x, sw[2 * j].y, sw[2 * j + 1].x, sw[2 * j + 1].y};
+      }
+    }
+  }
 #pragma unroll
   for (int j = 0; j < NJ; ++j)
 #pragma unroll
@@ -720,18 +743,34 @@ __device__ __forceinline__ void intra_chunk(const IntraArgs& a, const UnitRef& U
       // level's products are kept for its own pairs only; the diagonal (Aqk)
       // has factor 1 (pass hb = -1).  Each pass reloads k, q and g and
       // recomputes the tile-local cumsum (the same scan, so the same values)
-      // and the passes are not unrolled: the rare path keeps its registers
-      // few, so the common path's allocation does not grow.
+      // and the passes are not unrolled, which keeps the rare path's own
+      // registers few.  With the fused prologue q and k come from the slots
+      // this wave parked them in (above), g from memory as always.
 #pragma unroll 1
       for (int hb = -1; hb < 4; ++hb) {
         const int an = (hb < 0) ? r : (r & ~((2 << hb) - 1)) | ((1 << hb) - 1);   // anchor of this row
         const bool key = (hb < 0) || ((r >> hb) & 1) == 0;
+        uint4 pq = {0, 0, 0, 0}, pk = {0, 0, 0, 0};
+        if constexpr (PRO) {
+          const int64_t slot = (chead * (kC / 16) * NJ + (W * NJ + j)) * 512 + l * 8;
+          pq = *reinterpret_cast<const uint4*>(oGQ + slot);
+          pk = *reinterpret_cast<const uint4*>(oW + slot);
+        }
         f8 A, Bk, Bq;
 #pragma unroll
         for (int hf = 0; hf < 2; ++hf) {
           const int ch0 = 32 * j + 4 * gq + 16 * hf;
           f4 x = {0, 0, 0, 0}, y = {0, 0, 0, 0}, z = {0, 0, 0, 0};
-          if (valid) { x = ld4<DTQ>(a.q, bq + ch0); y = ld4<DTQ>(a.k, bq + ch0); z = ld4<DTG>(a.g, bq + ch0); }
+          if (valid) {
+            if constexpr (PRO) {
+              x = unpack4<DTQ>(hf ? uint2{pq.z, pq.w} : uint2{pq.x, pq.y});
+              y = unpack4<DTQ>(hf ? uint2{pk.z, pk.w} : uint2{pk.x, pk.y});
+            } else {
+              x = ld4<DTQ>(a.q, bq + ch0);
+              y = ld4<DTQ>(a.k, bq + ch0);
+            }
+            z = ld4<DTG>(a.g, bq + ch0);
+          }
 #pragma unroll
           for (int e = 0; e < 4; ++e) {
             const int ee = 4 * hf + e;
@@ -770,6 +809,9 @@ __device__ __forceinline__ void intra_chunk(const IntraArgs& a, const UnitRef& U
           }
         }
       }
+      // the parked q words are read above, before this step's gamma*q store
+      // below reuses their slot
+      if constexpr (PRO) asm volatile("" ::: "memory");
     }
 
     // q*gamma -> GQ (fragment order); beta*gamma*k and lambda*k kept

@@ -166,3 +166,38 @@ def test_fused_layer_equals_the_three_entry_points_at_config1(cuda):
     torch.cuda.synchronize()
     assert torch.isfinite(y.float()).all()
     assert torch.equal(y, y2) and torch.equal(ht, ht2)
+
+
+@pytest.mark.parametrize("d,gdt", [(128, torch.bfloat16), (64, torch.bfloat16), (128, torch.float32)])
+def test_fused_layer_decay_spikes(cuda, d, gdt):
+    """Single steps that decay by e^-150 in 3 % of the gate entries put some
+    16-row tiles past 2^-100, where the intra kernel takes its anchored path
+    and re-reads q and k per level.  With the fused prologue those are the
+    convolved, normalised rows, which exist only inside the kernel: the
+    fused layer must equal the three entry points (whose scan reads the
+    prologue's q, k from memory) bit for bit, and the oracle chain with the
+    token-by-token recurrence (the chunked oracle leaves float64's range
+    under such decay)."""
+    B, T, H, Kc = 2, 192, 2, 4
+    c = _case(B, T, H, d, Kc, seed=17 + d)
+    rng = np.random.default_rng(23 + d)
+    c["g"] = np.where(rng.random(c["g"].shape) < 0.03, np.float32(-150.0), c["g"]).astype(np.float32)
+    assert (c["g"].reshape(B, T // 16, 16, H, d).sum(axis=2) / np.log(2.0)).min() < -100.0
+    print(f"[layer decay spikes] d={d} gates={gdt}", flush=True)
+    y, ht, new, o = _layer(cuda, c, torch.bfloat16, gdt, with_o=True)
+    y2, ht2, new2, o2 = _unfused(cuda, c, torch.bfloat16, gdt, with_o=True)
+    assert torch.isfinite(y).all() and torch.isfinite(ht).all()
+    assert torch.equal(o, o2), (o - o2).abs().max().item()
+    assert torch.equal(y, y2) and torch.equal(ht, ht2)
+    xs_r = [_as(x, torch.bfloat16) for x in c["xs"]]
+    q, k, v, _ = Lr.prologue(*xs_r, *c["ws"], c["H"], bufs=c["bs"])
+    q, k, v = (_as(x.astype(np.float32), torch.bfloat16) for x in (q, k, v))
+    o_ref, hT_ref = Ko.recurrent_fwd(q, k, v, _as(c["g"], gdt), _as(c["beta"], gdt), h0=c["S0"])
+    o_ref, hT_ref = np.asarray(o_ref), np.asarray(hT_ref)
+    y_ref = Lr.epilogue(o_ref, _as(c["gate"], torch.bfloat16), eps=1e-6)
+    o_np = o.double().cpu().numpy()
+    assert Ko.rel_l2(o_np, o_ref) <= 1e-3 and Ko.max_abs(o_np, o_ref) <= 2e-2, (Ko.rel_l2(o_np, o_ref), Ko.max_abs(o_np, o_ref))
+    y_np = y.double().cpu().numpy()
+    assert Ko.rel_l2(y_np, y_ref) <= 2e-3 and Ko.max_abs(y_np, y_ref) <= 2e-2, (Ko.rel_l2(y_np, y_ref), Ko.max_abs(y_np, y_ref))
+    ht_np = ht.double().cpu().numpy()
+    assert Ko.rel_l2(ht_np, hT_ref) <= 1e-3
