@@ -42,6 +42,11 @@ Also reported on the same JSON line:
   ``cc_scan_bwd`` on one batch element of config 1 (alpha / beta32 operands,
   the reference's call shape), per call, and (``batched``) on the whole
   batch in one call with a leading batch axis;
+* ``config2``, ``config3``: the chunked forward at ``configs[2]`` (B=1,
+  T=65536: 1 024 serial chunks per chain) and ``configs[3]`` (64 sequences
+  of U[128, 8192] tokens packed with cu_seqlens, h0 and final state per
+  sequence), each per call with its own ``roofline`` over its algorithmic
+  bytes;
 * ``ut_solve``: the standalone unit-triangular solve at the reference's case
   (H=12, C=64, N=dk+dv=256, fp32), both orientations, per call;
 * ``copy_gbps_measured`` and ``gemm_bf16_tflops_measured``: the box's own
@@ -513,16 +518,26 @@ def bench_ut_solve(args, device):
     return out
 
 
+def _roofline(nbytes, t, traffic_key=None):
+    achieved = nbytes / t / 1e9
+    return {"bound": "hbm", "achieved": achieved, "peak": HBM_PEAK_GBPS, "unit": "GB/s",
+            "frac": achieved / HBM_PEAK_GBPS,
+            "traffic": measured_traffic(traffic_key) if traffic_key else None,
+            "algorithmic_bytes_per_call": nbytes}
+
+
 def bench_other_configs(args, device):
     """Forward at configs 2 (B1 T65536, 1 024 serial chunks per chain) and 3
-    (64 packed sequences of U[128, 8192] tokens, per-sequence h0): the
-    parity-test configurations, timed on request (``--other-configs``)."""
+    (64 packed sequences of U[128, 8192] tokens, per-sequence h0 and final
+    states): per call with HIP events on the kernels' stream, inputs resident,
+    each with its algorithmic bytes (read q, k, v, g, beta; write o fp32 and
+    the final states; config 3 also reads its h0) against the HBM peak."""
     import axiom_amd
     from axiom_amd import kda as kmod
     from oracle import inputs as oin
     stream = torch.cuda.current_stream(device)
 
-    def timed(f, n=10):
+    def timed(f, n):
         for _ in range(3):
             f()
         torch.cuda.synchronize()
@@ -539,22 +554,34 @@ def bench_other_configs(args, device):
     T2 = 65536
     q, k, v, g, beta = make_inputs_gpu(1, T2, H, d, d, args.seed + 6, device)
     ws = torch.empty(kmod.chunk_fwd_workspace_bytes(1, T2, H, d, d), dtype=torch.uint8, device=device)
-    t = timed(lambda: axiom_amd.kda_chunk_fwd(q, k, v, g, beta, workspace=ws))
+    o = torch.empty(1, T2, H, d, device=device)
+    ht = torch.empty(1, H, d, d, device=device)
+    t = timed(lambda: axiom_amd.kda_chunk_fwd(q, k, v, g, beta, workspace=ws, out=o, final_state=ht),
+              args.config_calls)
     nb = fwd_bytes(1, T2, H, d, d)
-    out["config2"] = dict(us_per_call=t * 1e6, tokens_per_s=T2 / t, hbm_frac=nb / t / 1e9 / HBM_PEAK_GBPS,
-                          workload="B1 T65536 H16 d128 bf16, fp32 o")
-    del q, k, v, g, beta, ws
+    out["config2"] = dict(us_per_call=t * 1e6, tokens_per_s=T2 / t, calls=args.config_calls,
+                          roofline=_roofline(nb, t, "config2_traffic_bytes_per_call"),
+                          workload="B1 T65536 H16 d128 bf16, fp32 o and final state, zero initial state")
+    del q, k, v, g, beta, ws, o, ht
     lengths = oin.make_varlen_lengths(64, 128, 8192, seed=3)
     cu = torch.from_numpy(oin.cu_seqlens_from_lengths(lengths)).to(device)
     T3 = int(lengths.sum())
     q, k, v, g, beta = make_inputs_gpu(1, T3, H, d, d, args.seed + 7, device)
-    h0 = torch.randn(len(lengths), H, d, d, device=device) * 0.02
+    gen = torch.Generator(device=device)
+    gen.manual_seed(args.seed + 8)
+    h0 = torch.randn(len(lengths), H, d, d, device=device, generator=gen) * 0.02
     ws = torch.empty(kmod.chunk_fwd_workspace_bytes(1, T3, H, d, d, n_seqs=len(lengths)), dtype=torch.uint8,
                      device=device)
-    t = timed(lambda: axiom_amd.kda_chunk_fwd(q, k, v, g, beta, initial_state=h0, cu_seqlens=cu, workspace=ws))
+    o = torch.empty(1, T3, H, d, device=device)
+    ht = torch.empty(len(lengths), H, d, d, device=device)
+    t = timed(lambda: axiom_amd.kda_chunk_fwd(q, k, v, g, beta, initial_state=h0, cu_seqlens=cu, workspace=ws,
+                                              out=o, final_state=ht), args.config_calls)
     nb = fwd_bytes(1, T3, H, d, d) + 2 * len(lengths) * H * d * d * 4 - H * d * d * 4
-    out["config3"] = dict(us_per_call=t * 1e6, tokens_per_s=T3 / t, hbm_frac=nb / t / 1e9 / HBM_PEAK_GBPS,
-                          workload=f"varlen 64 sequences U[128, 8192] (T={T3}) H16 d128 bf16, h0 and hT per sequence")
+    out["config3"] = dict(us_per_call=t * 1e6, tokens_per_s=T3 / t, calls=args.config_calls,
+                          roofline=_roofline(nb, t, "config3_traffic_bytes_per_call"),
+                          workspace_bytes=int(ws.numel()),
+                          workload=f"varlen 64 sequences U[128, 8192] (T={T3}) H16 d128 bf16, fp32 o, "
+                                   "h0 and final state per sequence")
     return out
 
 
@@ -605,8 +632,10 @@ def main():
     ap.add_argument("--no-decode", action="store_true")
     ap.add_argument("--bwd-steps", type=int, default=5)
     ap.add_argument("--no-backward", action="store_true")
-    ap.add_argument("--other-configs", action="store_true",
-                    help="also time the forward at configs 2 and 3 (parity-test shapes)")
+    ap.add_argument("--no-other-configs", action="store_true",
+                    help="skip the forward at configs 2 and 3")
+    ap.add_argument("--config-calls", type=int, default=10,
+                    help="timed calls of the forward at configs 2 and 3")
     args = ap.parse_args()
     if args.gpus != 1 or int(os.environ.get("WORLD_SIZE", "1")) != 1:
         print("bench.py measures one GPU only: every (batch, head) chain of this path is "
@@ -674,8 +703,8 @@ def main():
     line["decode_layer"] = bench_decode_layer(args, device)
     line["cc_scan_seam"] = bench_cc_scan(args, fwd["inputs"], device)
     line["ut_solve"] = bench_ut_solve(args, device)
-    if args.other_configs:
-        line["other_configs"] = bench_other_configs(args, device)
+    if not args.no_other_configs:
+        line.update(bench_other_configs(args, device))
     if not args.no_cpu_baseline:
         line["cpu_baseline"] = cpu_baseline(fwd["inputs"], args.cpu_seconds)
     print(json.dumps(line), flush=True)

@@ -490,6 +490,29 @@ def decode_steps(q, k, v, g, beta, S, scale: float = 1.0):
     return np.stack(outs, 0), S
 
 
+def decode_steps_torch(q, k, v, g, beta, S, scale: float = 1.0):
+    """``decode_steps`` for many chains at once: the same equations
+    (``net/kda.py:298-310``, ``:293``) as batched float64 torch products on
+    the host's threads, for checks that cover every chain of a large decode
+    batch.  Inputs ``[steps, ..., d]`` (``beta [steps, ...]``), state
+    ``[..., dk, dv]``; returns numpy ``(o [steps, ..., dv], S)``."""
+    f64 = torch.float64
+    q, k, v, g, beta = (torch.as_tensor(np.asarray(x), dtype=f64) for x in (q, k, v, g, beta))
+    S = torch.as_tensor(np.asarray(S), dtype=f64).clone()
+    lead = S.shape[:-2]
+    dk, dv = S.shape[-2:]
+    S = S.reshape(-1, dk, dv)
+    outs = []
+    for t in range(q.shape[0]):
+        qt, kt, vt = q[t].reshape(-1, dk) * scale, k[t].reshape(-1, dk), v[t].reshape(-1, dv)
+        alpha = torch.exp(g[t].reshape(-1, dk))
+        S.mul_(alpha[:, :, None])                                   # Diag(alpha) S
+        read = torch.bmm(kt[:, None, :], S)[:, 0]                   # (alpha*k)^T S = k^T Diag(alpha) S
+        S.add_((beta[t].reshape(-1)[:, None, None] * kt[:, :, None]) * (vt - read)[:, None, :])
+        outs.append(torch.bmm(qt[:, None, :], S)[:, 0].reshape(*lead, dv))   # S'^T q
+    return torch.stack(outs, 0).numpy(), S.reshape(*lead, dk, dv).numpy()
+
+
 # ---------------------------------------------------------------------------
 # Error metrics used by every parity test
 # ---------------------------------------------------------------------------

@@ -69,3 +69,35 @@ def host_chains(d, b, heads, t0=0, t1=None):
         res[n] = d[n][b:b + 1, sl][:, :, heads].float().cpu().numpy()
     res["beta"] = d["beta"][b:b + 1, sl][:, :, heads].float().cpu().numpy()
     return res
+
+
+def chain_errors(got, ref, chain_axes: tuple[int, ...]):
+    """Relative L2 and max-abs error of every chain: the slices at one index
+    of ``chain_axes``, reduced over the other axes."""
+    got = got.detach().double().cpu().numpy() if isinstance(got, torch.Tensor) else np.asarray(got, np.float64)
+    ref = ref.detach().double().cpu().numpy() if isinstance(ref, torch.Tensor) else np.asarray(ref, np.float64)
+    assert got.shape == ref.shape, f"shape {got.shape} vs {ref.shape}"
+    assert np.all(np.isfinite(got)), "non-finite values"
+    red = tuple(i for i in range(got.ndim) if i not in chain_axes)
+    err = got - ref
+    rel = np.sqrt((err * err).sum(axis=red)) / np.maximum(np.sqrt((ref * ref).sum(axis=red)), 1e-30)
+    return rel, np.abs(err).max(axis=red)
+
+
+def assert_chain_errors(name: str, rel, mx, tol: tuple[float, float]):
+    """Every chain's errors (from chain_errors) within ``tol``; returns the worst."""
+    rel, mx = np.asarray(rel), np.asarray(mx)
+    worst = np.unravel_index(int(np.argmax(rel / tol[0] + mx / tol[1])), rel.shape)
+    assert (rel <= tol[0]).all() and (mx <= tol[1]).all(), (
+        f"{name}: chain {worst} rel_l2={rel[worst]:.3e} max_abs={mx[worst]:.3e} (tol {tol}); "
+        f"{int(((rel > tol[0]) | (mx > tol[1])).sum())} of {rel.size} chains over the bar")
+    print(f"  {name}: {rel.size} chains, worst rel_l2={rel.max():.2e} max_abs={mx.max():.2e}", flush=True)
+    return float(rel.max()), float(mx.max())
+
+
+def assert_chains_close(name: str, got, ref, tol: tuple[float, float], chain_axes: tuple[int, ...]):
+    """Parity per chain: relative L2 and max-abs error of every chain within
+    ``tol``, so that one wrong chain among many cannot hide in a norm over
+    all of them.  Returns the worst relative L2 and max-abs over the chains."""
+    rel, mx = chain_errors(got, ref, chain_axes)
+    return assert_chain_errors(name, rel, mx, tol)

@@ -99,3 +99,90 @@ def test_cc_scan_bwd_errors(cuda):
         axiom_amd.cc_scan_bwd(z.bfloat16(), z.bfloat16(), z.bfloat16(), z, b32, S, z, chunk=64)
     with pytest.raises(ValueError, match="persistent backward kernel consumes bf16"):
         axiom_amd.cc_scan_bwd(z, z, z, z, b32, S, z, chunk=32)
+
+
+def _seam_device(cuda, B, T, H, d, seed):
+    """Seam operands at full size drawn on the GPU (config-1 distributions;
+    beta32's columns unequal), with a leading batch axis when B > 0."""
+    gen = torch.Generator(device=cuda)
+    gen.manual_seed(seed)
+    lead = (B,) if B else ()
+    n = lambda *s: torch.randn(*lead, *s, device=cuda, generator=gen)  # noqa: E731
+    l2 = lambda x: x / (x.norm(dim=-1, keepdim=True) + 1e-12)  # noqa: E731
+    q = l2(n(T, H, d)).reshape(*lead, T, H * d).to(torch.bfloat16)
+    k = l2(n(T, H, d)).reshape(*lead, T, H * d).to(torch.bfloat16)
+    v = n(T, H * d).to(torch.bfloat16)
+    a = torch.rand(H, device=cuda, generator=gen) * -2.0
+    g = -torch.nn.functional.softplus(n(T, H, d)) * torch.exp(a)[:, None]
+    alpha = torch.exp(g).reshape(*lead, T, H * d)
+    beta32 = (torch.sigmoid(n(T, H, 1)) + (torch.rand(*lead, T, H, 32, device=cuda, generator=gen) - 0.5) * 0.1)
+    beta32 = beta32.reshape(*lead, T, H * 32).contiguous()
+    S = n(H, d, d) * 0.05
+    do = n(T, H * d)
+    dS = n(H, d, d) * 0.1
+    return q, k, v, alpha, beta32, S, do, dS
+
+
+def _check_heads(tag, got, ref_fn, heads, H, d):
+    """Each sampled head (chain) of one batch element against the oracle on
+    that head's operands alone (heads are independent chains)."""
+    cols = np.concatenate([np.arange(h * d, (h + 1) * d) for h in heads])
+    cols32 = np.concatenate([np.arange(h * 32, (h + 1) * 32) for h in heads])
+    ref = ref_fn(cols, cols32)
+    T = got[0].shape[0]
+    n = len(heads)
+    for name, g, r, width, rt, at in (("dq", got[0], ref[0], d, 4e-3, 1e-2), ("dk", got[1], ref[1], d, 4e-3, 1e-2),
+                                      ("dv", got[2], ref[2], d, 4e-3, 1e-2), ("dalpha", got[3], ref[3], d, 1e-4, 1e-4),
+                                      ("dbeta32", got[4], ref[4], 32, 1e-4, 1e-4)):
+        gh = g[:, cols if width == d else cols32].double().cpu().numpy().reshape(T, n, width)
+        rh = r.reshape(T, n, width)
+        for j, h in enumerate(heads):
+            _close(f"{tag} {name} head {h}", torch.from_numpy(gh[:, j]), rh[:, j], rt, at)
+    gS = got[5][heads].double().cpu().numpy()
+    for j, h in enumerate(heads):
+        _close(f"{tag} dS_in head {h}", torch.from_numpy(gS[j]), ref[5][j], 1e-4, 1e-4)
+
+
+def test_cc_scan_bwd_at_the_bench_shape(cuda):
+    """The seam's backward rule at the shape bench.py times it at: one batch
+    element of config 1 (T4096 H16 d128), every head against the oracle."""
+    import axiom_amd
+    T, H, d = 4096, 16, 128
+    q, k, v, alpha, beta32, S, do, dS = _seam_device(cuda, 0, T, H, d, seed=41)
+    print("[seam bwd] T4096 H16 d128", flush=True)
+    out = axiom_amd.cc_scan_bwd(q, k, v, alpha, beta32, S, do, dS, tile=16, chunk=64)
+    torch.cuda.synchronize()
+    host = [t.float().cpu().numpy() for t in (q, k, v, alpha, beta32, S, do, dS)]
+
+    def ref_fn(cols, cols32):
+        hs = cols[::d] // d
+        return K.cc_scan_bwd(host[0][:, cols], host[1][:, cols], host[2][:, cols], host[3][:, cols],
+                             host[4][:, cols32], host[5][hs], host[6][:, cols], host[7][hs], chunk=64)
+
+    _check_heads("seam", out, ref_fn, list(range(H)), H, d)
+
+
+def test_cc_scan_bwd_batched_at_the_bench_shape(cuda):
+    """kda_cc_scan_bwd_batched over the whole of config 1 (B4 T4096 H16 d128)
+    in one call, as bench.py times it: four heads of every batch element
+    against the oracle, and element 2 equal bit for bit to its own unbatched
+    call."""
+    import axiom_amd
+    B, T, H, d = 4, 4096, 16, 128
+    q, k, v, alpha, beta32, S, do, dS = _seam_device(cuda, B, T, H, d, seed=43)
+    print("[seam bwd batched] B4 T4096 H16 d128", flush=True)
+    out = axiom_amd.cc_scan_bwd(q, k, v, alpha, beta32, S, do, dS, tile=16, chunk=64)
+    one = axiom_amd.cc_scan_bwd(*(t[2].contiguous() for t in (q, k, v, alpha, beta32, S, do, dS)), tile=16, chunk=64)
+    torch.cuda.synchronize()
+    for a, b in zip(out, one):
+        assert torch.equal(a[2], b)
+    for b in range(B):
+        host = [t[b].float().cpu().numpy() for t in (q, k, v, alpha, beta32, S, do, dS)]
+        heads = [(5 * b + 3 * j) % H for j in range(4)]
+
+        def ref_fn(cols, cols32, host=host):
+            hs = cols[::d] // d
+            return K.cc_scan_bwd(host[0][:, cols], host[1][:, cols], host[2][:, cols], host[3][:, cols],
+                                 host[4][:, cols32], host[5][hs], host[6][:, cols], host[7][hs], chunk=64)
+
+        _check_heads(f"batched b={b}", [t[b] for t in out], ref_fn, heads, H, d)

@@ -1,11 +1,14 @@
 """GPU parity at the full sizes of the benchmark configurations.
 
-The fp64 oracle cannot run these sizes whole, so each test combines
-* exact oracle checks on a sample of chains (heads and sequences are
-  independent chains, so a sample is checked at its full length), and
-* size-independent properties checked on everything: splitting a sequence and
-  carrying the final state across gives the same result bit for bit; a packed
-  varlen run equals the per-sequence runs bit for bit; no non-finite values.
+Each test combines
+* the fp64 oracle on every chain (every (sequence, head) pair, at its full
+  length; the oracle runs these sizes in seconds on the host's threads), each
+  chain held to the bar on its own so that one wrong chain -- a slip in the
+  chain -> workgroup or XCD mapping, the longest-first varlen order, a
+  segment boundary -- cannot hide in a norm over all of them, and
+* size-independent properties: splitting a sequence and carrying the final
+  state across gives the same result bit for bit; a packed varlen run equals
+  the per-sequence runs bit for bit; no non-finite values.
 
 Config 1: B4 T4096 H16 d128; config 2: B1 T65536 H16 d128 (1024 serial
 chunks per chain); config 3: 64 sequences of U[128, 8192] tokens packed with
@@ -20,7 +23,8 @@ import pytest
 import torch
 
 from oracle import inputs, kda_oracle as K
-from tests.kda_testutil import TOL, assert_close, host_chains, make_inputs_device
+from tests.kda_testutil import (TOL, assert_chain_errors, assert_chains_close, assert_close, chain_errors,
+                                host_chains, make_inputs_device)
 
 pytestmark = pytest.mark.gpu
 
@@ -37,17 +41,27 @@ def _slice(d, t0, t1):
     return {n: d[n][:, t0:t1].contiguous() for n in ("q", "k", "v", "g", "beta")}
 
 
+def _host(d):
+    """float32 host copies of the whole inputs (the bf16 values exactly)."""
+    return {n: d[n].float().cpu().numpy() for n in ("q", "k", "v", "g", "beta")}
+
+
+def _all_chains_dense(name, d, o, ht, h0=None):
+    """Every (batch row, head) chain against the fp64 oracle, each on its own."""
+    x = _host(d)
+    o_ref, ht_ref = K.chunk_fwd(x["q"], x["k"], x["v"], x["g"], x["beta"], chunk=64,
+                                h0=None if h0 is None else h0.cpu().numpy())
+    assert_chains_close(f"{name} o", o, o_ref, TOL["bf16"], chain_axes=(0, 2))
+    assert_chains_close(f"{name} ht", ht, ht_ref, TOL["bf16"], chain_axes=(0, 1))
+
+
 def test_config1_full(cuda):
     B, T, H, dd = 4, 4096, 16, 128
     d = make_inputs_device(B, T, H, dd, dd, seed=101, device=cuda)
     print("[full] config 1 forward", flush=True)
     o, ht = _fwd(d)
     assert torch.isfinite(o).all() and torch.isfinite(ht).all()
-    for b, heads in ((0, [0, 7]), (3, [15])):
-        hc = host_chains(d, b, heads)
-        o_ref, ht_ref = K.chunk_fwd(hc["q"], hc["k"], hc["v"], hc["g"], hc["beta"], chunk=64)
-        assert_close(f"o[b={b}]", o[b:b + 1][:, :, heads], o_ref, TOL["bf16"])
-        assert_close(f"ht[b={b}]", ht[b:b + 1][:, heads], ht_ref, TOL["bf16"])
+    _all_chains_dense("config 1", d, o, ht)
     # The whole call runs in segments of chunks (its intra-chunk results
     # exceed the per-segment budget); four calls of 16 chunks each carry the
     # state between them: same result bit for bit.
@@ -70,11 +84,7 @@ def test_config2_full(cuda):
     print("[full] config 2 forward", flush=True)
     o, ht = _fwd(d)
     assert torch.isfinite(o).all() and torch.isfinite(ht).all()
-    heads = [0, 9]
-    hc = host_chains(d, 0, heads)
-    o_ref, ht_ref = K.chunk_fwd(hc["q"], hc["k"], hc["v"], hc["g"], hc["beta"], chunk=64)
-    assert_close("o", o[:, :, heads], o_ref, TOL["bf16"])
-    assert_close("ht", ht[:, heads], ht_ref, TOL["bf16"])
+    _all_chains_dense("config 2", d, o, ht)
     # state carry: [0, T/2) then [T/2, T) from its final state == the whole run
     half = T // 2
     o1, ht1 = _fwd(_slice(d, 0, half))
@@ -100,14 +110,17 @@ def test_config3_varlen_full(cuda):
         oi, hi = _fwd(_slice(d, a, b), h0=d["h0"][i:i + 1].contiguous())
         assert torch.equal(oi, o[:, a:b]), f"sequence {i}: packed o differs from its own run"
         assert torch.equal(hi[0], ht[i]), f"sequence {i}: packed state differs from its own run"
-    for i in (int(order[0]), int(order[-1])):
+    # every (sequence, head) chain against the fp64 oracle, each on its own
+    x = _host(d)
+    o_ref, ht_ref = K.chunk_fwd(x["q"], x["k"], x["v"], x["g"], x["beta"], h0=d["h0"].cpu().numpy(),
+                                cu_seqlens=cu, chunk=64)
+    o_np, o_ref = o.double().cpu().numpy(), o_ref.numpy()
+    rel, mx = np.zeros((len(lengths), H)), np.zeros((len(lengths), H))
+    for i in range(len(lengths)):
         a, b = int(cu[i]), int(cu[i + 1])
-        heads = [2, 13]
-        hc = host_chains(d, 0, heads, a, b)
-        h0 = d["h0"][i:i + 1][:, heads].cpu().numpy()
-        o_ref, ht_ref = K.chunk_fwd(hc["q"], hc["k"], hc["v"], hc["g"], hc["beta"], h0=h0, chunk=64)
-        assert_close(f"o[seq {i}]", o[:, a:b][:, :, heads], o_ref, TOL["bf16"])
-        assert_close(f"ht[seq {i}]", ht[i:i + 1][:, heads], ht_ref, TOL["bf16"])
+        rel[i], mx[i] = chain_errors(o_np[:, a:b], o_ref[:, a:b], chain_axes=(2,))
+    assert_chain_errors("config 3 o", rel, mx, TOL["bf16"])
+    assert_chains_close("config 3 ht", ht, ht_ref, TOL["bf16"], chain_axes=(0, 1))
 
 
 def test_config4_decode_full(cuda):
@@ -117,27 +130,24 @@ def test_config4_decode_full(cuda):
     gen = torch.Generator(device=cuda)
     gen.manual_seed(105)
     S = torch.randn(B, H, dd, dd, device=cuda, generator=gen) * 0.02
-    pick = [(0, 0), (17, 5), (255, 15)]
-    S0 = np.stack([S[b, h].cpu().numpy() for b, h in pick])          # [n, d, d]
+    S0 = S.cpu().numpy()
     print("[full] config 4 decode", flush=True)
     outs = []
     for t in range(steps):
         outs.append(axiom_amd.kda_recurrent_step(d["q"][t], d["k"][t], d["v"][t], d["g"][t], d["beta"][t], S))
     torch.cuda.synchronize()
     assert torch.isfinite(S).all()
-    bs = [b for b, _ in pick]
-    hs = [h for _, h in pick]
-    sub = {n: d[n][:, bs, hs].float().cpu().numpy()[:, :, None] for n in ("q", "k", "v", "g", "beta")}
-    o_ref, S_ref = K.decode_steps(sub["q"], sub["k"], sub["v"], sub["g"], sub["beta"], S0[:, None])
-    o_got = torch.stack([o[bs, hs] for o in outs]).cpu().numpy()[:, :, None]
-    assert_close("o", o_got, o_ref, (1e-5, 1e-5))
-    assert_close("S", torch.stack([S[b, h] for b, h in pick]).cpu().numpy()[:, None], S_ref, (1e-5, 1e-5))
+    # all 4 096 (b, h) chains over the 128 steps, each on its own
+    x = _host(d)
+    o_ref, S_ref = K.decode_steps_torch(x["q"], x["k"], x["v"], x["g"], x["beta"], S0)
+    assert_chains_close("config 4 o", torch.stack(outs), o_ref, (1e-5, 1e-5), chain_axes=(1, 2))
+    assert_chains_close("config 4 S", S, S_ref, (1e-5, 1e-5), chain_axes=(0, 1))
 
 
 def test_two_segment_minimum_overlapped(cuda):
     """B1 T4096 H16 d128 with h0 (the cc_scan seam's per-element shape): one
     segment's worth of intra results, run as two overlapped segments; two
-    chains against the oracle, the call split at the segment boundary and at
+    every chain against the oracle, the call split at the segment boundary and at
     another point gives the same o and final state bit for bit."""
     from tests.test_capi import dense_segments, overlap_eligible
     B, T, H, dd = 1, 4096, 16, 128
@@ -145,11 +155,7 @@ def test_two_segment_minimum_overlapped(cuda):
     d = make_inputs_device(B, T, H, dd, dd, seed=111, device=cuda, h0_std=0.02)
     print("[full] two-segment minimum", flush=True)
     o, ht = _fwd(d, h0=d["h0"])
-    hc = host_chains(d, 0, [3, 12])
-    o_ref, ht_ref = K.chunk_fwd(hc["q"], hc["k"], hc["v"], hc["g"], hc["beta"],
-                                h0=d["h0"][:, [3, 12]].cpu().numpy(), chunk=64)
-    assert_close("o", o[:, :, [3, 12]], o_ref, TOL["bf16"])
-    assert_close("ht", ht[:, [3, 12]], ht_ref, TOL["bf16"])
+    _all_chains_dense("two-segment minimum", d, o, ht, h0=d["h0"])
     for cut in (2048, 64 * 13):
         o1, h1 = _fwd(_slice(d, 0, cut), h0=d["h0"])
         o2, h2 = _fwd(_slice(d, cut, T), h0=h1)
@@ -181,7 +187,7 @@ def test_overlapped_segments_odd_chunk_heads(cuda, dd, prec):
     """B1 T100000 H3: three chains, few enough that each segment's state scan
     runs in one launch with the next segment's intra work; every segment holds
     an odd number of chunk-heads (the last workgroup's second group idles).
-    Two chains against the oracle; the call split in two with the state carried
+    Every chain against the oracle; the call split in two with the state carried
     across gives the same o and final state bit for bit; bf16 o is the fp32 o
     rounded."""
     import axiom_amd
@@ -200,12 +206,11 @@ def test_overlapped_segments_odd_chunk_heads(cuda, dd, prec):
         d.update({n: d[n].float() for n in ("g", "beta")})
     print(f"[full] overlapped segments d={dd} {prec}", flush=True)
     o, ht = _fwd(d, h0=d["h0"])
-    hc = host_chains(d, 0, [0, 2])
-    o_ref, ht_ref = K.chunk_fwd(hc["q"], hc["k"], hc["v"], hc["g"], hc["beta"],
-                                h0=d["h0"][:, [0, 2]].cpu().numpy(), chunk=64)
+    x = _host(d)
+    o_ref, ht_ref = K.chunk_fwd(x["q"], x["k"], x["v"], x["g"], x["beta"], h0=d["h0"].cpu().numpy(), chunk=64)
     tol = TOL["fp16" if prec == "fp16" else "bf16"]
-    assert_close("o", o[:, :, [0, 2]], o_ref, tol)
-    assert_close("ht", ht[:, [0, 2]], ht_ref, tol)
+    assert_chains_close("o", o, o_ref, tol, chain_axes=(0, 2))
+    assert_chains_close("ht", ht, ht_ref, tol, chain_axes=(0, 1))
     half = 64 * 781
     o1, h1 = _fwd(_slice(d, 0, half), h0=d["h0"])
     o2, h2 = _fwd(_slice(d, half, T), h0=h1)

@@ -234,6 +234,27 @@ def test_decode_steps_equal_chunked():
     assert K.max_abs(s_c.numpy(), s_d) <= 1e-10
 
 
+@pytest.mark.parametrize("scale", [1.0, 0.7])
+def test_batched_decode_steps_equal_the_chunked_forward(scale):
+    """decode_steps_torch (the batched form the full-size decode check uses)
+    against the chunked oracle over the same tokens, and against the numpy
+    steps; a step that skips the decay of the read fails the first check."""
+    d = _small(B=2, T=40, seed=16)
+    # (the chunked oracle applies the scale in fp32: ~1e-8 apart from fp64 at 0.7)
+    o_c, s_c = K.chunk_fwd(d["q"], d["k"], d["v"], d["g"], d["beta"], h0=d["h0"], chunk=16, scale=scale)
+    steps = {n: np.moveaxis(d[n], 1, 0) for n in ("q", "k", "v", "g", "beta")}
+    o_t, s_t = K.decode_steps_torch(steps["q"], steps["k"], steps["v"], steps["g"], steps["beta"], d["h0"], scale)
+    bar = 1e-10 if scale == 1.0 else 1e-7
+    assert K.max_abs(o_c.numpy(), np.moveaxis(o_t, 0, 1)) <= bar
+    assert K.max_abs(s_c.numpy(), s_t) <= 1e-10
+    o_n, s_n = K.decode_steps(steps["q"], steps["k"], steps["v"], steps["g"], steps["beta"], d["h0"], scale)
+    assert K.max_abs(o_n, o_t) <= 1e-12 and K.max_abs(s_n, s_t) <= 1e-12
+    # planted: the decay dropped (g taken as zero)
+    o_m, _ = K.decode_steps_torch(steps["q"], steps["k"], steps["v"], np.zeros_like(steps["g"]), steps["beta"],
+                                  d["h0"], scale)
+    assert K.max_abs(o_c.numpy(), np.moveaxis(o_m, 0, 1)) > 1e-3
+
+
 # ---------------------------------------------------------------------------
 # mutation tests: a planted mistake must fail a pin
 # ---------------------------------------------------------------------------
