@@ -16,9 +16,12 @@
 //     M_rs = 2^(sum of the totals of the tiles strictly between) <= 1,
 //     so both MFMA operands stay in [0, 1] and run in fp16;
 //   diagonal tile (c >= i):  2^(G_c - G_i) = (R_c 2^-D) * Cf_i, operands up
-//     to 2^|D|, run as fp32 MFMA (16x16x4); a tile whose total decay passes
-//     2^-100 takes a slower path that splits each pair at the highest bit
-//     where c and i differ, through an anchor row between them, so every
+//     to 2^|D|: on fp16 MFMA when the tile's operands stay below 2^15 (tile
+//     decay above 2^-12, |k Cf|, |k R|, |q R| <= 8), else on the bf16 MFMA
+//     as a three-product hi/lo split (fp32 range, ~16 significant bits),
+//     and on fp32 MFMA (16x16x4) in exact mode; a tile whose total decay
+//     passes 2^-100 takes a slower path that splits each pair at the highest
+//     bit where c and i differ, through an anchor row between them, so every
 //     factor stays <= 1 however strong the decay;
 //   gamma = R * 2^(totals before the tile), lambda = Cf * 2^(totals after).
 // The per-channel constants (2^pre, 2^post, 2^-D, M) are computed once per
@@ -165,6 +168,119 @@ struct IntraLds;
 // channel of slot index s
 __device__ __forceinline__ int slot_index_channel(int s) {
   return slot_channel(s >> 5, (s >> 3) & 3, s & 7);
+}
+
+// Where a wave of the fused-prologue kernel parks its lane's convolved q and
+// k words of K step j (8 bf16 each, the slot order of the score operands)
+// when its tile takes the anchored path: this chunk-head's U and W slots of
+// its own row tile, which the final products write only after barrier #3
+// (every read of the parked words precedes barrier #2).
+template <int DK>
+__device__ __forceinline__ int64_t park_k_slot(int64_t chead, int W, int j, int l) {
+  return (chead * (kC / 16) * (DK / 32) + (W * (DK / 32) + j)) * 512 + l * 8;
+}
+template <int DK>
+__device__ __forceinline__ int64_t park_q_slot(int64_t chead, int W, int j, int l) {
+  return (chead * (kC / 16) * (DK / 16) + (W * (DK / 16) + 2 * j)) * 256 + l * 8;
+}
+
+// One K step (channels 32j .. 32j+31) of the diagonal tile of row tile W when
+// the tile's decay passes 2^-100 in some channel and no single row factor pair
+// fits fp32.  The pair (c, i), c > i, splits at the highest bit h where c and
+// i differ, through the anchor row a = (i | (2^h - 1)) in [i, c):
+// 2^(G_c - G_a) * 2^(G_a - G_i), both factors <= 1 whatever the decay.  At
+// level h the key rows with bit h clear carry 2^(G_a - G_i), the query rows
+// with bit h set 2^(G_c - G_a), every other row 0, and the level's products
+// are kept for its own pairs only; the diagonal (Aqk) has factor 1 (pass
+// hb = -1).  Each pass reloads k, q and g and recomputes the tile-local
+// cumsum (the same scan, so the same values).  With the fused prologue q and
+// k come from the slots the wave parked them in (pq_slot, pk_slot below), g
+// from memory as always.  acc holds the lane's Akk and Aqk accumulators of
+// the tile (4 + 4) and is returned updated.  Not unrolled, and run after the
+// score loop (whose row slices and factors are then dead): the rare path's
+// temporaries do not add to the registers of the common path.
+template <int DK, int DTQ, int DTG, bool EXACT, int W, bool PRO>
+__device__ __forceinline__ f8 extreme_diag_step(const IntraArgs* ap, const int j, const int64_t chead,
+                                               const int len, const int64_t row0, const int h, f8 acc) {
+  typedef typename Prec<EXACT>::st st;
+  constexpr int NJ = DK / 32;
+  const IntraArgs& a = *ap;
+  const int l = threadIdx.x & 63, r = l & 15, gq = l >> 4;
+  const int c = 16 * W + r;
+  const bool valid = c < len;
+  const int64_t bq = ((row0 + c) * a.geom.H + h) * DK;
+  auto decay2 = [&](float z) -> float {
+    if constexpr (DTG == 0) {
+      if (a.gates_alpha) {
+        const bool dn = z < 1.17549435e-38f;
+        return __builtin_amdgcn_logf(dn ? z * 4294967296.0f : z) - (dn ? 32.0f : 0.0f);
+      }
+    }
+    return z * kLog2e;
+  };
+#pragma unroll 1
+  for (int hb = -1; hb < 4; ++hb) {
+    const int an = (hb < 0) ? r : (r & ~((2 << hb) - 1)) | ((1 << hb) - 1);   // anchor of this row
+    const bool key = (hb < 0) || ((r >> hb) & 1) == 0;
+    uint4 pq = {0, 0, 0, 0}, pk = {0, 0, 0, 0};
+    if constexpr (PRO) {
+      pq = *reinterpret_cast<const uint4*>(static_cast<const st*>(a.U) + park_q_slot<DK>(chead, W, j, l));
+      pk = *reinterpret_cast<const uint4*>(static_cast<const st*>(a.W) + park_k_slot<DK>(chead, W, j, l));
+    }
+    f8 A, Bk, Bq;
+#pragma unroll
+    for (int hf = 0; hf < 2; ++hf) {
+      const int ch0 = 32 * j + 4 * gq + 16 * hf;
+      f4 x = {0, 0, 0, 0}, y = {0, 0, 0, 0}, z = {0, 0, 0, 0};
+      if (valid) {
+        if constexpr (PRO) {
+          x = unpack4<DTQ>(hf ? uint2{pq.z, pq.w} : uint2{pq.x, pq.y});
+          y = unpack4<DTQ>(hf ? uint2{pk.z, pk.w} : uint2{pk.x, pk.y});
+        } else {
+          x = ld4<DTQ>(a.q, bq + ch0);
+          y = ld4<DTQ>(a.k, bq + ch0);
+        }
+        z = ld4<DTG>(a.g, bq + ch0);
+      }
+#pragma unroll
+      for (int e = 0; e < 4; ++e) {
+        const int ee = 4 * hf + e;
+        const float gt = row_scan16(valid ? decay2(z[e]) : 0.f);
+        const float ga = __shfl(gt, (l & 48) | an, 64);
+        const float f = (hb < 0) ? 1.f : fast_exp2(key ? ga - gt : gt - ga);
+        A[ee] = key ? y[e] * f : 0.f;
+        Bk[ee] = (hb < 0 || key) ? 0.f : y[e] * f;
+        Bq[ee] = (hb < 0) ? x[e] * a.scale : key ? 0.f : x[e] * a.scale * f;
+      }
+    }
+    f4 tK = {0, 0, 0, 0}, tQ = {0, 0, 0, 0};
+    if constexpr (EXACT) {
+      tK = mma32(tK, A, Bk);
+      tQ = mma32(tQ, A, Bq);
+    } else {
+      b8 ah, al, kh, kl;
+      split_bf16(A, ah, al);
+      split_bf16(Bk, kh, kl);
+      tK = mma32_bf16(tK, ah, kh);
+      tK = mma32_bf16(tK, ah, kl);
+      tK = mma32_bf16(tK, al, kh);
+      split_bf16(Bq, kh, kl);
+      tQ = mma32_bf16(tQ, ah, kh);
+      tQ = mma32_bf16(tQ, ah, kl);
+      tQ = mma32_bf16(tQ, al, kh);
+    }
+#pragma unroll
+    for (int i = 0; i < 4; ++i) {
+      const int ii = 4 * gq + i;
+      if (hb < 0) {
+        if (r == ii) acc[4 + i] += tQ[i];
+      } else if (r > ii && ((r ^ ii) >> hb) == 1) {
+        acc[i] += tK[i];
+        acc[4 + i] += tQ[i];
+      }
+    }
+  }
+  return acc;
 }
 
 template <int DK, int DV, int DTQ, int DTG, bool EXACT, int W, bool PRO>
@@ -431,6 +547,18 @@ __device__ __forceinline__ void intra_chunk(const IntraArgs& a, const UnitRef& U
   for (int j = 0; j < NJ; ++j)
 #pragma unroll
     for (int e = 0; e < 8; ++e) Gt[j][e] = row_scan16(Gt[j][e]);
+  // PRO: whether this wave's tile takes the anchored path (the same test as
+  // `extreme` below), known before the convolution so that the wave can park
+  // its convolved q and k for that path as soon as it reads them
+  bool ext_pro = false;
+  if constexpr (PRO) {
+    float dm = 0.f;
+#pragma unroll
+    for (int j = 0; j < NJ; ++j)
+#pragma unroll
+      for (int e = 0; e < 8; ++e) dm = fminf(dm, row_bcast<15>(Gt[j][e]));
+    ext_pro = __any(dm < -100.f);
+  }
 
   // k, q and the two decay factors.  Each group's results are tied to an
   // empty asm statement before the next group's wait: otherwise the compiler
@@ -533,22 +661,15 @@ __device__ __forceinline__ void intra_chunk(const IntraArgs& a, const UnitRef& U
     // The anchored path of an extreme tile (below) re-reads q and k per
     // level; with the fused prologue they exist only here (the convolved bf16
     // rows in LDS are overwritten after the staging barrier).  A wave whose
-    // tile takes that path parks its lane's q and k words in this
-    // chunk-head's gamma*q and W slots of its row tile, which are written
-    // later (gamma*q of K step j at the end of that step, after its last
-    // read; W by the final products, after barrier #3), in the slot order
-    // the path reads them back in.
-    float dm = 0.f;
-#pragma unroll
-    for (int j = 0; j < NJ; ++j)
-#pragma unroll
-      for (int e = 0; e < 8; ++e) dm = fminf(dm, row_bcast<15>(Gt[j][e]));
-    if (__any(dm < -100.f)) {
+    // tile takes that path parks its lane's q and k words in slots of the
+    // workspace that are written only later (park_q_slot, park_k_slot).
+    if (ext_pro) {
 #pragma unroll
       for (int j = 0; j < NJ; ++j) {
-        const int64_t slot = (chead * (kC / 16) * NJ + (W * NJ + j)) * 512 + l * 8;
-        *reinterpret_cast<uint4*>(oGQ + slot) = uint4{sq[2 * j].x, sq[2 * j].y, sq[2 * j + 1].x, sq[2 * j + 1].y};
-        *reinterpret_cast<uint4*>(oW + slot) = uint4{sw[2 * j].x, sw[2 * j].y, sw[2 * j + 1].x, sw[2 * j + 1].y};
+        *reinterpret_cast<uint4*>(oU + park_q_slot<DK>(chead, W, j, l)) =
+            uint4{sq[2 * j].x, sq[2 * j].y, sq[2 * j + 1].x, sq[2 * j + 1].y};
+        *reinterpret_cast<uint4*>(oW + park_k_slot<DK>(chead, W, j, l)) =
+            uint4{sw[2 * j].x, sw[2 * j].y, sw[2 * j + 1].x, sw[2 * j + 1].y};
       }
     }
   }
@@ -706,7 +827,8 @@ __device__ __forceinline__ void intra_chunk(const IntraArgs& a, const UnitRef& U
       accK[s] = mma32(accK[s], A, cvt8<EXACT>(krj * M3));
       accQ[s] = mma32(accQ[s], A, cvt8<EXACT>(qrj * M3));
     }
-    // diagonal tile in fp32
+    // diagonal tile: fp16, bf16 hi/lo or (exact mode) fp32 operands; an
+    // extreme tile is done after this loop
     if (!extreme) {
       f8 ad, bk, bqd;
 #pragma unroll
@@ -733,85 +855,6 @@ __device__ __forceinline__ void intra_chunk(const IntraArgs& a, const UnitRef& U
         accK[W] = mma32_bf16(accK[W], al, kh);
         accQ[W] = mma32_bf16(accQ[W], al, qh);
       }
-    } else {
-      // Tile decay past 2^-100: no single row factor pair fits fp32, so the
-      // pair (c, i), c > i, splits at the highest bit h where c and i differ,
-      // through the anchor row a = (i | (2^h - 1)) in [i, c):
-      // 2^(G_c - G_a) * 2^(G_a - G_i), both factors <= 1 whatever the decay.
-      // At level h the key rows with bit h clear carry 2^(G_a - G_i), the
-      // query rows with bit h set 2^(G_c - G_a), every other row 0, and the
-      // level's products are kept for its own pairs only; the diagonal (Aqk)
-      // has factor 1 (pass hb = -1).  Each pass reloads k, q and g and
-      // recomputes the tile-local cumsum (the same scan, so the same values)
-      // and the passes are not unrolled, which keeps the rare path's own
-      // registers few.  With the fused prologue q and k come from the slots
-      // this wave parked them in (above), g from memory as always.
-#pragma unroll 1
-      for (int hb = -1; hb < 4; ++hb) {
-        const int an = (hb < 0) ? r : (r & ~((2 << hb) - 1)) | ((1 << hb) - 1);   // anchor of this row
-        const bool key = (hb < 0) || ((r >> hb) & 1) == 0;
-        uint4 pq = {0, 0, 0, 0}, pk = {0, 0, 0, 0};
-        if constexpr (PRO) {
-          const int64_t slot = (chead * (kC / 16) * NJ + (W * NJ + j)) * 512 + l * 8;
-          pq = *reinterpret_cast<const uint4*>(oGQ + slot);
-          pk = *reinterpret_cast<const uint4*>(oW + slot);
-        }
-        f8 A, Bk, Bq;
-#pragma unroll
-        for (int hf = 0; hf < 2; ++hf) {
-          const int ch0 = 32 * j + 4 * gq + 16 * hf;
-          f4 x = {0, 0, 0, 0}, y = {0, 0, 0, 0}, z = {0, 0, 0, 0};
-          if (valid) {
-            if constexpr (PRO) {
-              x = unpack4<DTQ>(hf ? uint2{pq.z, pq.w} : uint2{pq.x, pq.y});
-              y = unpack4<DTQ>(hf ? uint2{pk.z, pk.w} : uint2{pk.x, pk.y});
-            } else {
-              x = ld4<DTQ>(a.q, bq + ch0);
-              y = ld4<DTQ>(a.k, bq + ch0);
-            }
-            z = ld4<DTG>(a.g, bq + ch0);
-          }
-#pragma unroll
-          for (int e = 0; e < 4; ++e) {
-            const int ee = 4 * hf + e;
-            const float gt = row_scan16(valid ? decay2(z[e]) : 0.f);
-            const float ga = __shfl(gt, (l & 48) | an, 64);
-            const float f = (hb < 0) ? 1.f : fast_exp2(key ? ga - gt : gt - ga);
-            A[ee] = key ? y[e] * f : 0.f;
-            Bk[ee] = (hb < 0 || key) ? 0.f : y[e] * f;
-            Bq[ee] = (hb < 0) ? x[e] * a.scale : key ? 0.f : x[e] * a.scale * f;
-          }
-        }
-        f4 tK = {0, 0, 0, 0}, tQ = {0, 0, 0, 0};
-        if constexpr (EXACT) {
-          tK = mma32(tK, A, Bk);
-          tQ = mma32(tQ, A, Bq);
-        } else {
-          b8 ah, al, kh, kl;
-          split_bf16(A, ah, al);
-          split_bf16(Bk, kh, kl);
-          tK = mma32_bf16(tK, ah, kh);
-          tK = mma32_bf16(tK, ah, kl);
-          tK = mma32_bf16(tK, al, kh);
-          split_bf16(Bq, kh, kl);
-          tQ = mma32_bf16(tQ, ah, kh);
-          tQ = mma32_bf16(tQ, ah, kl);
-          tQ = mma32_bf16(tQ, al, kh);
-        }
-#pragma unroll
-        for (int i = 0; i < 4; ++i) {
-          const int ii = 4 * gq + i;
-          if (hb < 0) {
-            if (r == ii) accQ[W][i] += tQ[i];
-          } else if (r > ii && ((r ^ ii) >> hb) == 1) {
-            accK[W][i] += tK[i];
-            accQ[W][i] += tQ[i];
-          }
-        }
-      }
-      // the parked q words are read above, before this step's gamma*q store
-      // below reuses their slot
-      if constexpr (PRO) asm volatile("" ::: "memory");
     }
 
     // q*gamma -> GQ (fragment order); beta*gamma*k and lambda*k kept
@@ -827,6 +870,20 @@ __device__ __forceinline__ void intra_chunk(const IntraArgs& a, const UnitRef& U
     bw[j] = cvt8<EXACT>(bwf);
     *reinterpret_cast<v8*>(oGQ + (chead * (kC / 16) * NJ + (W * NJ + j)) * 512 + l * 8) =
         cvt8<EXACT>(gqv);
+  }
+
+  // Tile decay past 2^-100 in some channel: the diagonal tile by the anchored
+  // passes, K step by K step in the order the loop above would take them
+  if (extreme) {
+#pragma unroll 1
+    for (int j = 0; j < NJ; ++j) {
+      f8 acc;
+#pragma unroll
+      for (int i = 0; i < 4; ++i) { acc[i] = accK[W][i]; acc[4 + i] = accQ[W][i]; }
+      acc = extreme_diag_step<DK, DTQ, DTG, EXACT, W, PRO>(&a, j, chead, U.len, U.row0, h, acc);
+#pragma unroll
+      for (int i = 0; i < 4; ++i) { accK[W][i] = acc[i]; accQ[W][i] = acc[4 + i]; }
+    }
   }
 
   // masks; L = beta_c * Akk stays in registers (Lk[s] = 16x16x16 A fragment of L_{W,s})
