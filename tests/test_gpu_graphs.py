@@ -143,3 +143,63 @@ def test_layer_backward_chain_graph_replays_match_eager(cuda):
             assert torch.equal(got, want), f"replay {rep} output {i}"
         run()   # eager work on the same workspaces between replays
         torch.cuda.synchronize()
+
+
+def test_noalloc_captured_first_call_replays_match_eager(cuda):
+    """kda_chunk_fwd_noalloc captured into a graph with no warm-up call, so its
+    first call on the device -- the lookup of the library scratch's device
+    address -- happens during the capture (no other test of the suite calls
+    it before this one).  Replays, with eager calls of both entry points on
+    the same buffers between them, equal the eager kda_chunk_fwd bit for bit;
+    a second graph of a smaller call reuses the same scratch."""
+    import ctypes
+    from axiom_amd import _lib
+    L = _lib.lib()
+    p = lambda a: ctypes.c_void_p(0 if a is None else a.data_ptr())  # noqa: E731
+
+    def case(B, T, H, seed):
+        d = inputs.make_inputs(B, T, H, 128, 128, seed=seed, dtype="bf16", h0_std=0.05)
+        t = {n: to_dev(d[n], torch.bfloat16, cuda) for n in ("q", "k", "v", "g", "beta")}
+        t["h0"] = to_dev(d["h0"], torch.float32, cuda)
+        t["o"] = torch.zeros(B, T, H, 128, device=cuda)
+        t["ht"] = torch.zeros(B, H, 128, 128, device=cuda)
+        return t
+
+    def args(t, B, T, H, o, ht):
+        stream = ctypes.c_void_p(torch.cuda.current_stream(cuda).cuda_stream)
+        return (stream, p(t["q"]), p(t["k"]), p(t["v"]), p(t["g"]), p(t["beta"]), p(t["h0"]), ctypes.c_void_p(0), 0,
+                p(o), p(ht), B, T, H, 128, 128, 64, 1.0, _lib.KDA_DTYPE_BF16, _lib.KDA_DTYPE_F32)
+
+    def eager_ref(t, B, T, H):
+        o, ht = torch.empty_like(t["o"]), torch.empty_like(t["ht"])
+        nb = int(L.kda_chunk_fwd_workspace(B, T, H, 128, 128, 64, 0, _lib.KDA_DTYPE_BF16))
+        ws = torch.empty(nb, dtype=torch.uint8, device=cuda)
+        assert L.kda_chunk_fwd(*args(t, B, T, H, o, ht), p(ws), nb) == 0, _lib.last_error()
+        torch.cuda.synchronize()
+        return o, ht
+
+    graphs = []
+    for B, T, H, seed in ((2, 1000, 4, 51), (1, 130, 2, 52)):
+        t = case(B, T, H, seed)
+        g = torch.cuda.CUDAGraph()
+        print(f"[graph noalloc] capture B={B} T={T} H={H}", flush=True)
+        with torch.cuda.graph(g):
+            rc = L.kda_chunk_fwd_noalloc(*args(t, B, T, H, t["o"], t["ht"]))
+        torch.cuda.synchronize()
+        assert rc == _lib.KDA_OK, _lib.last_error()
+        graphs.append((g, t, B, T, H))
+    for g, t, B, T, H in graphs:
+        o_ref, ht_ref = eager_ref(t, B, T, H)
+        for rep in range(3):
+            t["o"].zero_()
+            t["ht"].zero_()
+            torch.cuda.synchronize()
+            g.replay()
+            torch.cuda.synchronize()
+            assert torch.equal(t["o"], o_ref) and torch.equal(t["ht"], ht_ref), f"B={B} T={T} replay {rep}"
+            # eager calls between replays, through both entry points
+            o2, ht2 = torch.empty_like(o_ref), torch.empty_like(ht_ref)
+            assert L.kda_chunk_fwd_noalloc(*args(t, B, T, H, o2, ht2)) == 0, _lib.last_error()
+            torch.cuda.synchronize()
+            assert torch.equal(o2, o_ref) and torch.equal(ht2, ht_ref)
+            eager_ref(t, B, T, H)
