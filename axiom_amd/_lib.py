@@ -37,6 +37,7 @@ _SIGNATURES = {
     "kda_chunk_fwd": (_i, [_vp, _vp, _vp, _vp, _vp, _vp, _vp, _vp, _i32, _vp, _vp,
                            _i, _i, _i, _i, _i, _i, _f, _i, _i, _vp, _sz]),
     "kda_chunk_fwd_workspace": (_sz, [_i, _i, _i, _i, _i, _i, _i32, _i]),
+    "kda_chunk_fwd_workspace_min": (_sz, [_i, _i, _i, _i, _i, _i, _i32, _i]),
     "kda_chunk_fwd_noalloc": (_i, [_vp, _vp, _vp, _vp, _vp, _vp, _vp, _vp, _i32, _vp, _vp,
                                    _i, _i, _i, _i, _i, _i, _f, _i, _i]),
     "kda_varlen_status": (_i, [_vp, _vp, _sz, _i, _i, _i, _i, _i, _i, _i32, _i,

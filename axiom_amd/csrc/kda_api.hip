@@ -37,7 +37,10 @@ size_t align_up(size_t x) { return (x + kAlign - 1) / kAlign * kAlign; }
 struct WsLayout {
   size_t W, U, AQ, GQ, LK, GC;
   size_t cu_clamped, chunk_off, n_units, order, flags;
-  size_t state;          // carried state between segments (segmented dense calls)
+  size_t state;          // carried state between segments (segmented calls)
+  size_t pos_off, seg_pos;  // position-major unit tables (segmented varlen calls)
+  int vsegs;             // varlen: launches (1 = every unit at once)
+  int KU;                // varlen, segmented: units per launch
   size_t status;         // int32 status word of the call (kda::kStatusNonFinite)
   size_t total;
   int64_t units_bound;   // workspace chunk units (per segment when segmented)
@@ -87,6 +90,22 @@ constexpr int kIntraSlots = 512;
 // 128 state workgroups (32 chains) overlapping gained nothing (1 085 against
 // 1 085 us), at 96 (24 chains) 1 855 -> 1 770 us.
 constexpr int64_t kOverlapMaxStateWgs = 96;
+
+// A varlen call runs every chunk-head at once when its workspace allows
+// (kda_chunk_fwd_workspace: the fastest schedule), else in segments of KU
+// units of a position-major numbering (every sequence's chunk p before any
+// sequence's chunk p + 1, sequences longest-first), the largest KU whose
+// layout fits the caller's workspace; each chain's state crosses the
+// segment boundaries in ht (or a workspace copy), as in the segmented dense
+// calls.  The least workspace accepted (kda_chunk_fwd_workspace_min) holds
+// this budget of intra-chunk results per segment.  Segmenting trades time
+// for memory: config 3 (64 sequences, T = 309 178) 3 902 us in one launch
+// pair (5.8 GB of workspace), 4 059 / 4 156 / 4 163 / 4 657 us in segments
+// of 1 280 / 640 / 320 / 160 MiB of results (each chain restarts its scan
+// at every boundary and the last positions are walked by few chains).  Needs
+// the longest-first order (at most 2 048 sequences: the prep kernel's sort).
+constexpr double kVarlenSegmentBudgetBytes = 160.0 * 1048576.0;
+constexpr int kVarlenSegmentMaxSeqs = 2048;
 constexpr double kOverlapSegmentBudgetBytes = 96.0 * 1048576.0;
 
 int64_t col_state_grid(int64_t chains, int dv) { return ((chains + 7) / 8) * 8 * (dv / 32); }
@@ -109,15 +128,27 @@ int dense_segments(int B, int T, int H, int dk, int dv, int in_dtype) {
   return s < 1 ? 1 : (s > NT ? NT : s);
 }
 
-// n_seqs <= 0: dense
-WsLayout ws_layout(int B, int T, int H, int dk, int dv, int32_t n_seqs, int in_dtype) {
+// upper bound on a varlen call's chunk units: sum ceil(len_i / C) <= (T + (C-1) N) / C
+int64_t varlen_units(int T, int32_t n_seqs) { return (static_cast<int64_t>(T) + 63LL * n_seqs) / kC; }
+
+// n_seqs <= 0: dense.  Varlen: ku = 0 runs every unit in one launch pair,
+// ku > 0 (below the unit bound; at most 2 048 sequences) runs segments of ku
+// units.
+WsLayout ws_layout(int B, int T, int H, int dk, int dv, int32_t n_seqs, int in_dtype, int64_t ku = 0) {
   WsLayout L{};
   const size_t es = is_exact(in_dtype) ? 4 : 2;
   int64_t units;
   L.segments = 1;
+  L.vsegs = 1;
+  L.KU = 0;
   L.seg_chunks = (T + kC - 1) / kC;
   if (n_seqs > 0) {
-    units = (static_cast<int64_t>(T) + 63LL * n_seqs) / kC;
+    units = varlen_units(T, n_seqs);
+    if (ku > 0 && ku < units && n_seqs <= kVarlenSegmentMaxSeqs) {
+      L.KU = static_cast<int>(ku);
+      L.vsegs = static_cast<int>((units + ku - 1) / ku);
+      units = ku;
+    }
   } else {
     const int NT = L.seg_chunks;
     L.segments = dense_segments(B, T, H, dk, dv, in_dtype);
@@ -152,11 +183,50 @@ WsLayout ws_layout(int B, int T, int H, int dk, int dv, int32_t n_seqs, int in_d
     L.n_units = take(4);
     L.order = take(static_cast<size_t>(n_seqs) * 4);
     L.flags = take(4);
+    if (L.vsegs > 1) {
+      L.pos_off = take((static_cast<size_t>(T + kC - 1) / kC + 2) * 4);
+      L.seg_pos = take(static_cast<size_t>(L.vsegs + 1) * 2 * 4);
+    }
   }
-  if (L.segments > 1) L.state = take(static_cast<size_t>(B) * H * dk * dv * 4);
+  if (L.segments > 1 || L.vsegs > 1)
+    L.state = take(static_cast<size_t>(n_seqs > 0 ? n_seqs : B) * H * dk * dv * 4);
   L.status = take(4);
   L.total = off;
   return L;
+}
+
+// Units per segment of a varlen call's smallest workspace (the budget's
+// worth of intra-chunk results), or 0 when the call runs unsegmented anyway.
+int64_t varlen_min_ku(int T, int H, int dk, int dv, int32_t n_seqs, int in_dtype) {
+  const int64_t units = varlen_units(T, n_seqs);
+  const double per_unit = static_cast<double>(H) * bytes_per_chunk_head(dk, dv, is_exact(in_dtype) ? 4 : 2);
+  if (n_seqs > kVarlenSegmentMaxSeqs || static_cast<double>(units) * per_unit <= kVarlenSegmentBudgetBytes) return 0;
+  return std::max<int64_t>(1, static_cast<int64_t>(kVarlenSegmentBudgetBytes / per_unit));
+}
+
+// The layout a call with ws_bytes of workspace runs: the fastest one when it
+// fits, else (varlen) the segments of the most units that fit.  ok = false:
+// not even the smallest layout fits.
+WsLayout ws_layout_for(int B, int T, int H, int dk, int dv, int32_t n_seqs, int in_dtype, size_t ws_bytes,
+                       bool* ok) {
+  const WsLayout full = ws_layout(B, T, H, dk, dv, n_seqs, in_dtype);
+  *ok = true;
+  if (ws_bytes >= full.total || n_seqs <= 0) {
+    *ok = ws_bytes >= full.total;
+    return full;
+  }
+  const int64_t kmin = varlen_min_ku(T, H, dk, dv, n_seqs, in_dtype);
+  if (kmin == 0 || ws_layout(B, T, H, dk, dv, n_seqs, in_dtype, kmin).total > ws_bytes) {
+    *ok = false;
+    return full;
+  }
+  // largest ku in [kmin, units) whose layout fits (the size grows with ku)
+  int64_t lo = kmin, hi = varlen_units(T, n_seqs) - 1;
+  while (lo < hi) {
+    const int64_t mid = lo + (hi - lo + 1) / 2;
+    if (ws_layout(B, T, H, dk, dv, n_seqs, in_dtype, mid).total <= ws_bytes) lo = mid; else hi = mid - 1;
+  }
+  return ws_layout(B, T, H, dk, dv, n_seqs, in_dtype, lo);
 }
 
 bool dim_ok(int d) { return d == 64 || d == 128; }
@@ -224,10 +294,14 @@ int chunk_fwd_impl(hipStream_t stream, const void* q, const void* k, const void*
       misaligned(ws, 16) || (gates_alpha && misaligned(beta, 16)))
     return fail(KDA_ERR_INVALID_ARGUMENT, "q, k, v, g%s, o and the workspace must be 16-byte aligned",
                 gates_alpha ? ", beta32" : "");
-  const WsLayout L = ws_layout(B, T, H, dk, dv, varlen ? n_seqs : 0, in_dtype);
+  bool fits = false;
+  const WsLayout L = ws_layout_for(B, T, H, dk, dv, varlen ? n_seqs : 0, in_dtype, ws ? ws_bytes : 0, &fits);
   if (L.units_bound * H > 0x7FFFFFFFLL) return fail(KDA_ERR_INVALID_ARGUMENT, "too many chunk-heads");
-  if (ws == nullptr || ws_bytes < L.total)
-    return fail(KDA_ERR_WORKSPACE, "workspace of %zu bytes is too small (need %zu)", ws_bytes, L.total);
+  if (ws == nullptr || !fits) {
+    const int64_t kmin = varlen ? varlen_min_ku(T, H, dk, dv, n_seqs, in_dtype) : 0;
+    const size_t least = kmin > 0 ? ws_layout(B, T, H, dk, dv, n_seqs, in_dtype, kmin).total : L.total;
+    return fail(KDA_ERR_WORKSPACE, "workspace of %zu bytes is too small (need %zu)", ws ? ws_bytes : 0, least);
+  }
 
   const bool exact = is_exact(in_dtype);
   int dtq, dtg;
@@ -250,9 +324,17 @@ int chunk_fwd_impl(hipStream_t stream, const void* q, const void* k, const void*
     G.chunk_off = at<int32_t>(ws, L.chunk_off);
     G.n_units = at<int32_t>(ws, L.n_units);
     G.order = at<int32_t>(ws, L.order);
+    if (L.vsegs > 1) {
+      G.pos_off = at<int32_t>(ws, L.pos_off);
+      G.seg_pos = at<int32_t>(ws, L.seg_pos);
+      G.KU = L.KU;
+    }
     hipError_t e = kda::launch_varlen_prep(cu_seqlens, n_seqs, T, at<int32_t>(ws, L.cu_clamped),
                                            at<int32_t>(ws, L.chunk_off), at<int32_t>(ws, L.n_units),
-                                           at<int32_t>(ws, L.order), at<int32_t>(ws, L.flags), stream);
+                                           at<int32_t>(ws, L.order), at<int32_t>(ws, L.flags),
+                                           L.vsegs > 1 ? at<int32_t>(ws, L.pos_off) : nullptr,
+                                           L.vsegs > 1 ? at<int32_t>(ws, L.seg_pos) : nullptr, L.KU, L.vsegs,
+                                           stream);
     if (e != hipSuccess) return hip_fail(e, "varlen prep launch");
   }
 
@@ -330,6 +412,25 @@ int chunk_fwd_impl(hipStream_t stream, const void* q, const void* k, const void*
         e = kda::launch_state(sa, dk, exact, out_dt, static_cast<int>(state_grid), stream);
         if (e != hipSuccess) return hip_fail(e, "state kernel launch");
       }
+    }
+    return KDA_OK;
+  }
+  if (varlen && L.vsegs > 1) {
+    // Segmented varlen: per segment an intra launch over its KU units and a
+    // state launch that walks each chain's chunks in it, from h0 (a chain's
+    // first chunk) or from the state the previous segment left in `carry`.
+    float* const vcarry = (ht != nullptr) ? ht : at<float>(ws, L.state);
+    for (int sgi = 0; sgi < L.vsegs; ++sgi) {
+      G.seg = sgi;
+      ia.geom = G;
+      sa.geom = G;
+      hipError_t e = kda::launch_intra(ia, dk, dtq, dtg, static_cast<int>(static_cast<int64_t>(L.KU) * H), stream);
+      if (e != hipSuccess) return hip_fail(e, "intra kernel launch");
+      ia.status_clear = nullptr;
+      sa.h0 = h0;
+      sa.ht = vcarry;
+      e = kda::launch_state(sa, dk, exact, out_dt, static_cast<int>(state_grid), stream);
+      if (e != hipSuccess) return hip_fail(e, "state kernel launch");
     }
     return KDA_OK;
   }
@@ -519,10 +620,12 @@ int ut_check(const void* a, const void* b, const void* x, int H, int C, int N, i
 // streams, two threads) race on it.  No part of it needs clearing between
 // calls: the forward writes every workspace word it reads within the call.
 // ----------------------------------------------------------------------------
-// 192 MiB: the dense config-1 workspace (two segments of 160 MiB budget: 149
-// MiB with the carried state) and the overlapped config-2 one (two 96 MiB
-// sets: 180 MiB) fit.
-constexpr size_t kScratchBytes = static_cast<size_t>(192) << 20;
+// 256 MiB: the dense config-1 workspace (two segments of 160 MiB budget: 149
+// MiB with the carried state), the overlapped config-2 one (two 96 MiB sets:
+// 180 MiB) and config 3's least varlen workspace (160 MiB of intra results
+// per segment and 64 MiB of carried state: 225 MiB) fit; a larger varlen
+// call runs in the segments that fit the scratch.
+constexpr size_t kScratchBytes = static_cast<size_t>(256) << 20;
 static __device__ __align__(256) unsigned char scratch[kScratchBytes];
 
 constexpr int kMaxDevices = 64;
@@ -573,6 +676,15 @@ size_t kda_chunk_fwd_workspace(int B, int T, int H, int dk, int dv, int chunk, i
   return ws_layout(B, T, H, dk, dv, n_seqs > 0 ? n_seqs : 0, in_dtype).total;
 }
 
+size_t kda_chunk_fwd_workspace_min(int B, int T, int H, int dk, int dv, int chunk, int32_t n_seqs,
+                                   int in_dtype) {
+  if (B < 1 || T < 0 || H < 1 || !dim_ok(dk) || dk != dv || chunk != kC) return 0;
+  if (in_dtype < KDA_DTYPE_F32 || in_dtype > KDA_DTYPE_BF16_F32GATES) return 0;
+  const int32_t ns = n_seqs > 0 ? n_seqs : 0;
+  const int64_t kmin = ns > 0 ? varlen_min_ku(T, H, dk, dv, ns, in_dtype) : 0;
+  return ws_layout(B, T, H, dk, dv, ns, in_dtype, kmin).total;
+}
+
 int kda_chunk_fwd(hipStream_t stream, const void* q, const void* k, const void* v,
                   const void* g, const void* beta, const float* h0,
                   const int32_t* cu_seqlens, int32_t n_seqs, void* o, float* ht,
@@ -595,7 +707,10 @@ int kda_chunk_fwd_noalloc(hipStream_t stream, const void* q, const void* k, cons
     return chunk_fwd_impl(stream, q, k, v, g, beta, h0, cu_seqlens, n_seqs, o, ht, B, T, H, dk, dv,
                           chunk, scale, in_dtype, out_dtype, nullptr, 0);
   }
-  const size_t need = ws_layout(B, T, H, dk, dv, cu_seqlens != nullptr ? n_seqs : 0, in_dtype).total;
+  // the call runs the fastest layout that fits the scratch (a varlen call
+  // past it in segments: kda_chunk_fwd with a smaller workspace)
+  const size_t need = kda_chunk_fwd_workspace_min(B, T, H, dk, dv, chunk, cu_seqlens != nullptr ? n_seqs : 0,
+                                                  in_dtype);
   if (need > kScratchBytes)
     return fail(KDA_ERR_WORKSPACE,
                 "kda_chunk_fwd_noalloc: this call needs %zu bytes of scratch, the library's "
@@ -622,8 +737,9 @@ int kda_chunk_fwd_status(hipStream_t stream, const void* workspace, size_t works
     ws = p;
     workspace_bytes = kScratchBytes;
   }
-  if (workspace_bytes < need) return fail(KDA_ERR_WORKSPACE, "workspace does not match");
-  const WsLayout L = ws_layout(B, T, H, dk, dv, n_seqs > 0 ? n_seqs : 0, in_dtype);
+  bool fits = false;
+  const WsLayout L = ws_layout_for(B, T, H, dk, dv, n_seqs > 0 ? n_seqs : 0, in_dtype, workspace_bytes, &fits);
+  if (!fits) return fail(KDA_ERR_WORKSPACE, "workspace does not match");
   int32_t words[2] = {0, 0};
   hipError_t e = hipMemcpyAsync(&words[0], static_cast<const char*>(ws) + L.status, 4, hipMemcpyDeviceToHost, stream);
   if (e == hipSuccess && n_seqs > 0)
@@ -642,8 +758,9 @@ int kda_varlen_status(hipStream_t stream, const void* workspace, size_t workspac
   if (!workspace || !flags_out) return fail(KDA_ERR_INVALID_ARGUMENT, "null pointer");
   if (n_seqs < 1) return fail(KDA_ERR_INVALID_ARGUMENT, "n_seqs=%d must be >= 1", n_seqs);
   const size_t need = kda_chunk_fwd_workspace(B, T, H, dk, dv, chunk, n_seqs, in_dtype);
-  if (need == 0 || workspace_bytes < need) return fail(KDA_ERR_WORKSPACE, "workspace does not match");
-  const WsLayout L = ws_layout(B, T, H, dk, dv, n_seqs, in_dtype);
+  bool fits = false;
+  const WsLayout L = ws_layout_for(B, T, H, dk, dv, n_seqs, in_dtype, workspace_bytes, &fits);
+  if (need == 0 || !fits) return fail(KDA_ERR_WORKSPACE, "workspace does not match");
   hipError_t e = hipMemcpyAsync(flags_out, static_cast<const char*>(workspace) + L.flags, 4,
                                 hipMemcpyDeviceToHost, stream);
   if (e != hipSuccess) return hip_fail(e, "flags copy");

@@ -92,8 +92,27 @@ struct UnitRef {
   int len;        // valid rows, 1..64
 };
 
+// u: the launch's unit (its workspace slot); segmented varlen launches map it
+// to the global position-major unit seg * KU + u (the caller has checked that
+// this is below n_units)
 __device__ __forceinline__ UnitRef unit_ref(const Geom& G, int u) {
   UnitRef R;
+  if (G.pos_off != nullptr) {
+    // position p of the unit: the largest p in [P0, P1] with pos_off[p] <= ug
+    // (P0, P1 the positions of this segment's and the next one's first unit)
+    const int ug = G.seg * G.KU + u;
+    int lo = G.seg_pos[2 * G.seg], hi = G.seg_pos[2 * G.seg + 2];
+    while (lo < hi) {
+      const int mid = (lo + hi + 1) >> 1;
+      if (G.pos_off[mid] <= ug) lo = mid; else hi = mid - 1;
+    }
+    R.seq = G.order[ug - G.pos_off[lo]];
+    R.n = lo;
+    const int s0 = G.cu_clamped[R.seq], s1 = G.cu_clamped[R.seq + 1];
+    R.row0 = static_cast<int64_t>(s0) + static_cast<int64_t>(R.n) * kC;
+    R.len = min(kC, static_cast<int>(s1 - R.row0));
+    return R;
+  }
   if (G.cu == nullptr) {
     // dense: units are (sequence, chunk) of the segment [n0, n0 + NTS)
     R.seq = u / G.NTS;
@@ -114,6 +133,65 @@ __device__ __forceinline__ UnitRef unit_ref(const Geom& G, int u) {
     R.len = min(kC, static_cast<int>(s1 - R.row0));
   }
   return R;
+}
+
+// The chunks of one chain that a state launch walks.  chain_unit(G, c, n) is
+// the workspace slot of its n-th chunk in the launch; rows tok0 + 64 n on,
+// seq_len - 64 n of them valid.  The walk starts from h0 (from_h0) or from
+// the state the previous segment left in ht; an inactive chain (a segmented
+// varlen launch holding none of its chunks) touches nothing.
+struct ChainRef {
+  int seq, u0, nchunks, seq_len;
+  int64_t tok0;
+  int rank, p0;   // segmented varlen: longest-first rank, first chunk position
+  bool from_h0, active;
+};
+
+// rank: the chain's sequence slot of the state grid (varlen: its rank in the
+// longest-first order; dense: the batch row)
+__device__ __forceinline__ ChainRef chain_ref(const Geom& G, int rank) {
+  ChainRef c;
+  c.seq = (G.order != nullptr) ? G.order[rank] : rank;
+  c.rank = rank;
+  c.p0 = 0;
+  c.from_h0 = true;
+  c.active = true;
+  if (G.cu == nullptr) {
+    c.u0 = c.seq * G.NTS;
+    c.nchunks = G.NTS;
+    c.tok0 = static_cast<int64_t>(c.seq) * G.T + static_cast<int64_t>(G.n0) * kC;
+    c.seq_len = G.T - G.n0 * kC;
+  } else if (G.pos_off == nullptr) {
+    c.u0 = G.chunk_off[c.seq];
+    c.nchunks = G.chunk_off[c.seq + 1] - c.u0;
+    c.tok0 = G.cu_clamped[c.seq];
+    c.seq_len = G.cu_clamped[c.seq + 1] - G.cu_clamped[c.seq];
+  } else {
+    // The chain's units pos_off[p] + rank increase with p; this segment holds
+    // positions [p_lo, p_hi) of them: from the first segment unit's (P0, R0)
+    // and the next segment's (P1, R1), p_lo = P0 + (rank < R0), p_hi = P1 +
+    // (rank < R1), clamped to the chain's chunk count.
+    const int ni = G.chunk_off[c.seq + 1] - G.chunk_off[c.seq];
+    const int P0 = G.seg_pos[2 * G.seg], R0 = G.seg_pos[2 * G.seg + 1];
+    const int P1 = G.seg_pos[2 * G.seg + 2], R1 = G.seg_pos[2 * G.seg + 3];
+    const int p_lo = P0 + (rank < R0 ? 1 : 0);
+    const int p_hi = min(P1 + (rank < R1 ? 1 : 0), ni);
+    c.p0 = p_lo;
+    c.u0 = 0;
+    c.nchunks = max(p_hi - p_lo, 0);
+    const int s0 = G.cu_clamped[c.seq];
+    c.tok0 = static_cast<int64_t>(s0) + static_cast<int64_t>(p_lo) * kC;
+    c.seq_len = G.cu_clamped[c.seq + 1] - s0 - p_lo * kC;
+    c.from_h0 = (p_lo == 0);
+    // an empty sequence's final state (h0) is written by the first segment
+    c.active = c.nchunks > 0 || (ni == 0 && G.seg == 0);
+  }
+  return c;
+}
+
+__device__ __forceinline__ int chain_unit(const Geom& G, const ChainRef& c, int n) {
+  if (G.pos_off != nullptr) return G.pos_off[c.p0 + n] + c.rank - G.seg * G.KU;
+  return c.u0 + n;
 }
 
 // ----------------------------------------------------------------------------
@@ -1093,7 +1171,7 @@ void kda_intra_kernel(IntraArgs a) {
   if (a.status_clear != nullptr && blockIdx.x == 0 && threadIdx.x == 0) *a.status_clear = 0;
   const int u = blockIdx.x / H;
   const int h = blockIdx.x - u * H;
-  if (a.geom.cu != nullptr && u >= *a.geom.n_units) return;  // uniform per workgroup
+  if (a.geom.cu != nullptr && a.geom.seg * a.geom.KU + u >= *a.geom.n_units) return;  // uniform per workgroup
   const UnitRef U = unit_ref(a.geom, u);
   const int64_t chead = static_cast<int64_t>(u) * H + h;
   switch (threadIdx.x >> 6) {
@@ -1255,22 +1333,14 @@ __device__ __forceinline__ void state_chain(const StateArgs& a, StateSmem<DK, DV
   const Geom& G = a.geom;
   const int H = G.H;
   const int l = threadIdx.x & 63, r = l & 15, gq = l >> 4;
-  int u0, nchunks, seq_len;
-  int64_t tok0;
-  if (G.cu == nullptr) {
-    u0 = seq * G.NTS;
-    nchunks = G.NTS;
-    tok0 = static_cast<int64_t>(seq) * G.T + static_cast<int64_t>(G.n0) * kC;
-    seq_len = G.T - G.n0 * kC;
-  } else {
-    u0 = G.chunk_off[seq];
-    nchunks = G.chunk_off[seq + 1] - u0;
-    tok0 = G.cu_clamped[seq];
-    seq_len = G.cu_clamped[seq + 1] - G.cu_clamped[seq];
-  }
+  const ChainRef c = chain_ref(G, seq);
+  if (!c.active) return;
+  const int nchunks = c.nchunks, seq_len = c.seq_len;
+  const int64_t tok0 = c.tok0;
 
   f4 S[DTW][2];
-  const int64_t sbase = (static_cast<int64_t>(seq) * H + h) * DK * DV;
+  const int64_t sbase = (static_cast<int64_t>(c.seq) * H + h) * DK * DV;
+  const float* const s_in = c.from_h0 ? a.h0 : a.ht;
 #pragma unroll
   for (int t = 0; t < DTW; ++t)
 #pragma unroll
@@ -1279,10 +1349,10 @@ __device__ __forceinline__ void state_chain(const StateArgs& a, StateSmem<DK, DV
       for (int i = 0; i < 4; ++i) {
         const int d = 16 * (W * DTW + t) + 4 * gq + i;
         const int e = 32 * split + 16 * et + r;
-        S[t][et][i] = (a.h0 != nullptr) ? a.h0[sbase + static_cast<int64_t>(d) * DV + e] : 0.f;
+        S[t][et][i] = (s_in != nullptr) ? s_in[sbase + static_cast<int64_t>(d) * DV + e] : 0.f;
       }
 
-  auto chead_of = [&](int n) { return static_cast<int64_t>(u0 + n) * H + h; };
+  auto chead_of = [&](int n) { return static_cast<int64_t>(chain_unit(G, c, n)) * H + h; };
   auto step = [&](const StateFrags<DK, EXACT>& f, int n) {
     const int64_t row0 = tok0 + static_cast<int64_t>(n) * kC;
     const int len = min(kC, seq_len - n * kC);
@@ -1339,7 +1409,7 @@ void kda_state_kernel(StateArgs a) {
   if (chain >= G.N * H) return;
   const int seq_rank = chain / H;
   const int h = chain - seq_rank * H;
-  const int seq = (G.order != nullptr) ? G.order[seq_rank] : seq_rank;
+  const int seq = seq_rank;   // the roles look the sequence up (chain_ref)
   switch (threadIdx.x >> 6) {
     case 0: state_chain<DK, DV, EXACT, OUT_DT, 0>(a, sm, seq, h, split); break;
     case 1: state_chain<DK, DV, EXACT, OUT_DT, 1>(a, sm, seq, h, split); break;
@@ -1455,26 +1525,6 @@ __device__ __forceinline__ float col_stored_mag(const uint4 (&vs)[NS], const boo
   return m;
 }
 
-struct ChainRef {
-  int u0, nchunks, seq_len;
-  int64_t tok0;
-};
-
-__device__ __forceinline__ ChainRef chain_ref(const Geom& G, int seq) {
-  ChainRef c;
-  if (G.cu == nullptr) {
-    c.u0 = seq * G.NTS;
-    c.nchunks = G.NTS;
-    c.tok0 = static_cast<int64_t>(seq) * G.T + static_cast<int64_t>(G.n0) * kC;
-    c.seq_len = G.T - G.n0 * kC;
-  } else {
-    c.u0 = G.chunk_off[seq];
-    c.nchunks = G.chunk_off[seq + 1] - c.u0;
-    c.tok0 = G.cu_clamped[seq];
-    c.seq_len = G.cu_clamped[seq + 1] - G.cu_clamped[seq];
-  }
-  return c;
-}
 
 // Calls f(std::integral_constant<int, I>{}) for I = B .. E-1, expanded at
 // compile time (a loop over a long, branchy body is not always unrolled).
@@ -1559,7 +1609,7 @@ __device__ __forceinline__ void col_producer_step(const StateArgs& a, ColSmem<DK
   if (st)
     col_store_rows<DV, OUT_DT, P>(a, sm.obuf[(n - 1) & 1], c.tok0 + static_cast<int64_t>(n - 1) * kC,
                                   min(kC, c.seq_len - (n - 1) * kC), h, split, l, vs, ok);
-  col_load_regs<DK, DV, P>(a, static_cast<int64_t>(c.u0 + min(n + 2, c.nchunks - 1)) * H + h, split, l, Rn);
+  col_load_regs<DK, DV, P>(a, static_cast<int64_t>(chain_unit(a.geom, c, min(n + 2, c.nchunks - 1))) * H + h, split, l, Rn);
   // the range check of the stored o rows runs while the loads are in flight
   __builtin_amdgcn_sched_barrier(0);
   if (st) mag += col_stored_mag<OUT_DT>(vs, ok);
@@ -1580,8 +1630,8 @@ __device__ __forceinline__ void col_producer(const StateArgs& a, ColSmem<DK>& sm
   float mag = 0.f;
   const int last = c.nchunks - 1;
   ColRegs<DK, P> R0, R1;
-  col_load_regs<DK, DV, P>(a, static_cast<int64_t>(c.u0) * H + h, split, l, R0);
-  col_load_regs<DK, DV, P>(a, static_cast<int64_t>(c.u0 + min(1, last)) * H + h, split, l, R1);
+  col_load_regs<DK, DV, P>(a, static_cast<int64_t>(chain_unit(a.geom, c, 0)) * H + h, split, l, R0);
+  col_load_regs<DK, DV, P>(a, static_cast<int64_t>(chain_unit(a.geom, c, min(1, last))) * H + h, split, l, R1);
   col_write_regs<DK, P>(sm.buf[0], l, R0);
   lds_barrier();  // chunk 0 staged
   int n = 0;
@@ -1631,18 +1681,20 @@ __device__ __forceinline__ void col_chain(const StateArgs& a, ColSmem<DK>& sm, i
   const int l = threadIdx.x & 63, r = l & 15, gq = l >> 4;
   const int tile0 = W * NC;                 // first value tile of this wave inside the workgroup
   const ChainRef c = chain_ref(G, seq);
+  if (!c.active) return;
   const int nchunks = c.nchunks;
 
   f4 S[NC][NT];
-  const int64_t sbase = (static_cast<int64_t>(seq) * H + h) * DK * DV;
+  const int64_t sbase = (static_cast<int64_t>(c.seq) * H + h) * DK * DV;
+  const float* const s_in = c.from_h0 ? a.h0 : a.ht;
 #pragma unroll
   for (int cc = 0; cc < NC; ++cc)
 #pragma unroll
     for (int dt = 0; dt < NT; ++dt)
 #pragma unroll
       for (int i = 0; i < 4; ++i)
-        S[cc][dt][i] = (a.h0 != nullptr)
-                           ? a.h0[sbase + static_cast<int64_t>(16 * dt + 4 * gq + i) * DV +
+        S[cc][dt][i] = (s_in != nullptr)
+                           ? s_in[sbase + static_cast<int64_t>(16 * dt + 4 * gq + i) * DV +
                                   16 * (2 * split + tile0 + cc) + r]
                            : 0.f;
 
@@ -1800,7 +1852,7 @@ void kda_state_col_kernel(StateArgs a) {
   if (chain >= G.N * H) return;
   const int seq_rank = chain / H;
   const int h = chain - seq_rank * H;
-  const int seq = (G.order != nullptr) ? G.order[seq_rank] : seq_rank;
+  const int seq = seq_rank;   // the roles look the sequence up (chain_ref)
   const int wave = threadIdx.x >> 6;
   if (wave < kColComputeWaves) {
     if constexpr (kColComputeWaves == 1) col_chain<DK, DV, OUT_DT, 0>(a, sm, seq, h, split);
@@ -1891,12 +1943,13 @@ __device__ __forceinline__ void wide_producer(const StateArgs& a, WideSmem<DK, V
   const int H = a.geom.H;
   const int l = threadIdx.x & 63;
   if (c.nchunks <= 0) return;
-  wide_stage<DK, DV, VT, P>(a, static_cast<int64_t>(c.u0) * H + h, split, sm.buf[0], l);
+  wide_stage<DK, DV, VT, P>(a, static_cast<int64_t>(chain_unit(a.geom, c, 0)) * H + h, split, sm.buf[0], l);
   wait_vmem_all();
   lds_barrier();
   for (int n = 0; n < c.nchunks; ++n) {
     if (n + 1 < c.nchunks)
-      wide_stage<DK, DV, VT, P>(a, static_cast<int64_t>(c.u0 + n + 1) * H + h, split, sm.buf[(n + 1) & 1], l);
+      wide_stage<DK, DV, VT, P>(a, static_cast<int64_t>(chain_unit(a.geom, c, n + 1)) * H + h, split,
+                                sm.buf[(n + 1) & 1], l);
     wait_vmem_all();
     lds_barrier();
   }
@@ -1915,18 +1968,20 @@ __device__ __forceinline__ void wide_chain(const StateArgs& a, WideSmem<DK, VT>&
   const int tile0 = W * NC;                     // first value tile of this wave inside the workgroup
   const int col0 = 16 * (split * VT + tile0);   // its first value column in the chain
   const ChainRef c = chain_ref(G, seq);
+  if (!c.active) return;
   const int nchunks = c.nchunks;
 
   f4 S[NC][NT];
-  const int64_t sbase = (static_cast<int64_t>(seq) * H + h) * DK * DV;
+  const int64_t sbase = (static_cast<int64_t>(c.seq) * H + h) * DK * DV;
+  const float* const s_in = c.from_h0 ? a.h0 : a.ht;
 #pragma unroll
   for (int cc = 0; cc < NC; ++cc)
 #pragma unroll
     for (int dt = 0; dt < NT; ++dt)
 #pragma unroll
       for (int i = 0; i < 4; ++i)
-        S[cc][dt][i] = (a.h0 != nullptr)
-                           ? a.h0[sbase + static_cast<int64_t>(16 * dt + 4 * gq + i) * DV + col0 + 16 * cc + r]
+        S[cc][dt][i] = (s_in != nullptr)
+                           ? s_in[sbase + static_cast<int64_t>(16 * dt + 4 * gq + i) * DV + col0 + 16 * cc + r]
                            : 0.f;
 
   float mag = 0.f;
@@ -2100,7 +2155,7 @@ void kda_state_wide_kernel(StateArgs a) {
   if (chain >= G.N * H) return;
   const int seq_rank = chain / H;
   const int h = chain - seq_rank * H;
-  const int seq = (G.order != nullptr) ? G.order[seq_rank] : seq_rank;
+  const int seq = seq_rank;   // the roles look the sequence up (chain_ref)
   const int wave = threadIdx.x >> 6;
   if (wave < CW) {
     static_for<0, CW>([&](auto wc) {
@@ -2158,7 +2213,7 @@ void kda_overlap_kernel(IntraArgs ia, StateArgs sa, int n_state) {
     if (chain >= G.N * H) return;  // uniform per workgroup
     const int seq_rank = chain / H;
     const int h = chain - seq_rank * H;
-    const int seq = (G.order != nullptr) ? G.order[seq_rank] : seq_rank;
+    const int seq = seq_rank;   // the roles look the sequence up (chain_ref)
     static_assert(kColComputeWaves == 2 && kColProducers == 4, "six working waves");
     switch (wave) {
       case 0: col_chain<DK, DV, OUT_DT, 0>(sa, sm, seq, h, split); break;

@@ -19,6 +19,17 @@ struct Geom {
   const int32_t* chunk_off;     // [N+1] first chunk unit of each sequence (varlen)
   const int32_t* n_units;       // total chunk units (varlen, device)
   const int32_t* order;         // longest-first sequence order (varlen) or null
+  // Segmented varlen calls (pos_off non-null).  Units are numbered
+  // position-major: every sequence's chunk p precedes every sequence's chunk
+  // p + 1, and at position p the sequences of longest-first rank 0 ..
+  // cnt(p) - 1 (the ones with more than p chunks) hold units pos_off[p] +
+  // rank.  A launch covers units [seg * KU, (seg + 1) * KU); its workspace
+  // slot of unit u is u - seg * KU.  seg_pos[2 s], seg_pos[2 s + 1] are the
+  // position and rank of unit s * KU (the first unit of segment s).
+  const int32_t* pos_off;       // [n_pos + 1], device (prep kernel)
+  const int32_t* seg_pos;       // [2 (n_seg + 1)], device (prep kernel)
+  int seg;                      // segment of this launch
+  int KU;                       // units per segment
 };
 
 struct IntraArgs {
@@ -207,9 +218,13 @@ hipError_t launch_state(const StateArgs& a, int d, bool exact, int out_dt, int g
 // in one launch; fp16 operands, no fused prologue
 hipError_t launch_overlap(const IntraArgs& ia, const StateArgs& sa, int d, int dtq, int dtg, int out_dt,
                           int n_state, int intra_units, hipStream_t s);
+// varlen preparation; pos_off / seg_pos non-null (segmented calls, N <= 2048):
+// also the position-major unit tables of Geom for segments of KU units
+// (n_seg segments)
 hipError_t launch_varlen_prep(const int32_t* cu, int N, int T, int32_t* cu_clamped,
                               int32_t* chunk_off, int32_t* n_units, int32_t* order,
-                              int32_t* flags, hipStream_t s);
+                              int32_t* flags, int32_t* pos_off, int32_t* seg_pos, int KU, int n_seg,
+                              hipStream_t s);
 hipError_t launch_decode(const DecodeArgs& a, int d, int dt, int out_dt, int grid, hipStream_t s);
 
 // One decode token of the whole layer in one launch: short conv (buffers

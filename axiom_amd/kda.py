@@ -72,7 +72,15 @@ def _check_dims(dk, dv, what):
 
 
 def chunk_fwd_workspace_bytes(B, T, H, dk, dv, n_seqs=0, in_code=_lib.KDA_DTYPE_BF16) -> int:
+    """Workspace bytes of the fastest schedule (``kda_chunk_fwd_workspace``)."""
     return int(_lib.lib().kda_chunk_fwd_workspace(B, T, H, dk, dv, CHUNK, n_seqs, in_code))
+
+
+def chunk_fwd_workspace_min_bytes(B, T, H, dk, dv, n_seqs=0, in_code=_lib.KDA_DTYPE_BF16) -> int:
+    """The least workspace a call accepts (``kda_chunk_fwd_workspace_min``):
+    a large varlen call given less than the fastest schedule's runs in
+    segments that fit it."""
+    return int(_lib.lib().kda_chunk_fwd_workspace_min(B, T, H, dk, dv, CHUNK, n_seqs, in_code))
 
 
 def kda_chunk_fwd(q, k, v, g, beta, initial_state=None, cu_seqlens=None, chunk_size: int = 64,
@@ -87,6 +95,9 @@ def kda_chunk_fwd(q, k, v, g, beta, initial_state=None, cu_seqlens=None, chunk_s
     ``cu_seqlens`` int32 ``[N+1]`` on the device (requires B == 1).  fp32
     inputs select the exact (fp32 MFMA) kernels.  ``out`` / ``final_state``:
     optional preallocated outputs (contiguous, the shapes and dtypes returned).
+    ``workspace``: an optional uint8 device buffer of at least
+    ``chunk_fwd_workspace_min_bytes`` (smaller ones are replaced by a new
+    buffer of the fastest schedule's size).
     16-bit inputs run on fp16 matrix-core operands: unit-norm q and k rows
     and |v|, the state and the intermediate U below 2^15 are supported; with
     ``check_finite`` the call synchronises and raises ``ValueError`` when a
@@ -135,7 +146,14 @@ def kda_chunk_fwd(q, k, v, g, beta, initial_state=None, cu_seqlens=None, chunk_s
     ws_bytes = int(L.kda_chunk_fwd_workspace(B, T, H, dk, dv, CHUNK, n_seqs, in_code))
     if ws_bytes == 0:
         raise ValueError(f"{what}: unsupported configuration")
-    if workspace is None or workspace.numel() * workspace.element_size() < ws_bytes:
+    # a caller workspace of at least the minimum is used as it is (a large
+    # varlen call then runs in the segments that fit it); else a new one of
+    # the fastest schedule's size
+    ws_min = int(L.kda_chunk_fwd_workspace_min(B, T, H, dk, dv, CHUNK, n_seqs, in_code))
+    if workspace is not None and workspace.numel() * workspace.element_size() >= ws_min:
+        _contig("workspace", workspace)
+        ws_bytes = min(ws_bytes, workspace.numel() * workspace.element_size())
+    else:
         workspace = torch.empty(ws_bytes, dtype=torch.uint8, device=dev)
     if out is not None:
         if tuple(out.shape) != (B, T, H, dv) or out.dtype != out_dtype or out.device != dev:

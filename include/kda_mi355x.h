@@ -109,13 +109,15 @@ KDA_API int kda_chunk_fwd(hipStream_t stream,
 
 /*
  * kda_chunk_fwd without a workspace argument: the workspace is a file-scope
- * device array of the library (192 MiB = 201326592 bytes, one per device,
+ * device array of the library (256 MiB = 268435456 bytes, one per device,
  * held from the library's load until the process ends), so the call allocates nothing (no hipMalloc, no allocating library
  * routine) and only launches kernels.  No counterpart in the reference: it is
  * for callers that cannot allocate -- code under HIP graph capture, tight
  * serving loops, harnesses that forbid allocation.  Arguments, results and
- * errors as kda_chunk_fwd; a call whose workspace (kda_chunk_fwd_workspace)
- * exceeds the scratch returns KDA_ERR_WORKSPACE.  All calls on one device
+ * errors as kda_chunk_fwd run with the scratch as its workspace (a varlen
+ * call whose fastest schedule needs more runs in the segments that fit);
+ * a call whose least workspace (kda_chunk_fwd_workspace_min) exceeds the
+ * scratch returns KDA_ERR_WORKSPACE.  All calls on one device
  * share its scratch: calls that overlap on one device (two streams or
  * threads) race and must be ordered by the caller.
  */
@@ -128,10 +130,22 @@ KDA_API int kda_chunk_fwd_noalloc(hipStream_t stream,
                   int B, int T, int H, int dk, int dv, int chunk, float scale,
                   int in_dtype, int out_dtype);
 
-/* Workspace bytes kda_chunk_fwd needs for these arguments (0 on bad input).
- * n_seqs <= 0 means dense (no cu_seqlens).  Host-only; no HIP call. */
+/* Workspace bytes of kda_chunk_fwd's fastest schedule for these arguments
+ * (0 on bad input).  n_seqs <= 0 means dense (no cu_seqlens).  Host-only; no
+ * HIP call. */
 KDA_API size_t kda_chunk_fwd_workspace(int B, int T, int H, int dk, int dv, int chunk,
                                int32_t n_seqs, int in_dtype);
+
+/* The least workspace kda_chunk_fwd accepts for these arguments (0 on bad
+ * input).  Equal to kda_chunk_fwd_workspace except for varlen calls (at most
+ * 2048 sequences) whose intra-chunk results exceed 160 MiB: given less than
+ * kda_chunk_fwd_workspace (and at least this), such a call runs in segments
+ * of a position-major unit numbering, the largest that fit its workspace,
+ * with the same results bit for bit and more time (config 3: 3.9 ms with
+ * the 5.8 GB workspace, 4.7 ms with the ~0.23 GB minimum).  No counterpart in
+ * the reference (varlen is absent there).  Host-only; no HIP call. */
+KDA_API size_t kda_chunk_fwd_workspace_min(int B, int T, int H, int dk, int dv, int chunk,
+                                   int32_t n_seqs, int in_dtype);
 
 /*
  * Status of the last kda_chunk_fwd (or kda_chunk_fwd_noalloc: pass

@@ -102,18 +102,59 @@ def test_segment_policy():
     assert not overlap_eligible(1, 16, 128, 4)   # exact mode never overlaps
 
 
-def varlen_ws_bytes(T, N, H, dk, dv, es):
+VARLEN_BUDGET = 160 * 1048576   # intra-chunk results per segment of a varlen call's least workspace
+VARLEN_MAX_SEQS = 2048           # segmented only with the longest-first order
+
+
+def varlen_min_ku(T, N, H, dk, dv, es):
+    """Units per segment of the least workspace, 0 when a call never segments."""
     units = (T + 63 * N) // C   # upper bound on sum(ceil(len_i / C))
+    per_unit = H * (C * (3 * dk + dv + C) * es + dk * 4)
+    if N <= VARLEN_MAX_SEQS and units * per_unit > VARLEN_BUDGET:
+        return max(1, VARLEN_BUDGET // per_unit)
+    return 0
+
+
+def varlen_segments(T, N, H, dk, dv, es):
+    """(launches, units per launch) of a varlen call given its least workspace."""
+    units = (T + 63 * N) // C
+    ku = varlen_min_ku(T, N, H, dk, dv, es)
+    return (-(-units // ku), ku) if ku else (1, units)
+
+
+def varlen_ws_bytes(T, N, H, dk, dv, es, ku=0):
+    """Varlen workspace: the intra-chunk results of one launch's units, the
+    prep kernel's tables (cu_clamped, chunk offsets, unit count, order, flags)
+    and, when segmented (ku units per launch), the position-major unit tables
+    (pos_off over the chunk positions, the segments' first positions) and the
+    carried state."""
+    units = (T + 63 * N) // C
+    segs = -(-units // ku) if 0 < ku < units else 1
+    if segs > 1:
+        units = ku
     ch = units * H
-    arrays = (ch * C * dk * es, ch * C * dk * es, ch * C * dk * es, ch * C * dv * es,
-              ch * C * C * es, ch * dk * 4, (N + 1) * 4, (N + 1) * 4, 4, N * 4, 4, 4)
+    arrays = [ch * C * dk * es, ch * C * dk * es, ch * C * dk * es, ch * C * dv * es,
+              ch * C * C * es, ch * dk * 4, (N + 1) * 4, (N + 1) * 4, 4, N * 4, 4]
+    if segs > 1:
+        arrays += [((T + C - 1) // C + 2) * 4, (segs + 1) * 2 * 4, N * H * dk * dv * 4]
+    arrays.append(4)   # the call's status word
     return sum(_align(n) for n in arrays)
+
+
+def test_varlen_segment_policy():
+    # config 3 (64 sequences, T = 309 178, H 16 d 128): 4 894 units at most;
+    # its least workspace runs segments of 141 units (160 MiB of results), 35 launches
+    assert varlen_segments(309178, 64, 16, 128, 128, 2) == (35, 141)
+    assert varlen_segments(108, 4, 16, 128, 128, 2) == (1, 5)
+    assert varlen_segments(10 ** 6, 3000, 16, 128, 128, 2)[0] == 1   # beyond the sortable count
+    assert varlen_ws_bytes(309178, 64, 16, 128, 128, 2, 141) < 240 * 1048576
+    assert varlen_ws_bytes(309178, 64, 16, 128, 128, 2) > 5 * 10 ** 9
 
 
 def test_header_declares_the_abi():
     names = _lib.header_symbols()
     assert set(names) == set(_lib._SIGNATURES), names
-    assert len(names) == len(set(names)) == 29
+    assert len(names) == len(set(names)) == 30
 
 
 def test_library_exports_every_declared_symbol(L):
@@ -156,9 +197,18 @@ def test_layer_workspace_rejects_unsupported(L, args):
     assert L.kda_layer_fwd_workspace(*args) == 0
 
 
-@pytest.mark.parametrize("T,N", [(262144, 64), (108, 4), (1, 1), (0, 3)])
+@pytest.mark.parametrize("T,N", [(262144, 64), (309178, 64), (108, 4), (1, 1), (0, 3), (10 ** 6, 3000)])
 def test_varlen_workspace_size(L, T, N):
     assert L.kda_chunk_fwd_workspace(1, T, 16, 128, 128, C, N, 1) == varlen_ws_bytes(T, N, 16, 128, 128, 2)
+    ku = varlen_min_ku(T, N, 16, 128, 128, 2)
+    assert L.kda_chunk_fwd_workspace_min(1, T, 16, 128, 128, C, N, 1) == varlen_ws_bytes(T, N, 16, 128, 128, 2, ku)
+
+
+@pytest.mark.parametrize("B,T,H,d", [(4, 4096, 16, 128), (1, 65536, 16, 128), (2, 37, 2, 64)])
+def test_dense_workspace_min_is_the_workspace(L, B, T, H, d):
+    for code in (0, 1, 2, 3):
+        assert L.kda_chunk_fwd_workspace_min(B, T, H, d, d, C, 0, code) == \
+            L.kda_chunk_fwd_workspace(B, T, H, d, d, C, 0, code)
 
 
 def test_varlen_workspace_covers_every_split():

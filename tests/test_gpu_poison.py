@@ -13,7 +13,8 @@ difference between the two runs.
 Layouts covered: dense calls in one segment, in two sequential segments (the
 state carried through the workspace when no final state is asked for) and in
 overlapped segments (two alternating result sets); varlen (the prep kernel's
-offsets and order in the workspace); exact (fp32) mode; the chunked backward;
+offsets and order in the workspace), also in segments (its position tables,
+the state carried through ht or the workspace); exact (fp32) mode; the chunked backward;
 the layer forward (fused prologue); the cc_scan seam, its backward rule and
 their batched forms.  The reference ran its device checks under a poison
 fill of the same kind (evidence/mfu-55/kernels/REPORT-kda-ut-solve.md:20).
@@ -61,7 +62,7 @@ def _u8(n, dev):
     return torch.empty(max(int(n), 1), dtype=torch.uint8, device=dev)
 
 
-def _chunk_fwd_case(cuda, B, T, H, d, dtype, h0, want_ht, cu=None):
+def _chunk_fwd_case(cuda, B, T, H, d, dtype, h0, want_ht, cu=None, least=False):
     L = _lib.lib()
     if dtype == "fp32":
         x = inputs.make_inputs(B, T, H, d, d, seed=T + H, dtype="fp32", h0_std=0.05,
@@ -76,7 +77,7 @@ def _chunk_fwd_case(cuda, B, T, H, d, dtype, h0, want_ht, cu=None):
     n_seqs = 0 if cu is None else len(cu) - 1
     N = B if cu is None else n_seqs
     cu_t = None if cu is None else torch.tensor(cu, dtype=torch.int32, device=cuda)
-    need = int(L.kda_chunk_fwd_workspace(B, T, H, d, d, 64, n_seqs, code))
+    need = int((L.kda_chunk_fwd_workspace_min if least else L.kda_chunk_fwd_workspace)(B, T, H, d, d, 64, n_seqs, code))
     assert need > 0
 
     def make_bufs():
@@ -106,11 +107,16 @@ def test_chunk_fwd_poisoned_workspace(cuda, B, T, H, d, dtype, h0, want_ht):
     _chunk_fwd_case(cuda, B, T, H, d, dtype, h0, want_ht)
 
 
-@pytest.mark.parametrize("lengths,d", [([100, 1, 0, 640, 77, 300], 128), ([64, 129, 5], 64)])
-def test_chunk_fwd_varlen_poisoned_workspace(cuda, lengths, d):
+@pytest.mark.parametrize("lengths,H,d,want_ht", [
+    ([100, 1, 0, 640, 77, 300], 2, 128, True),
+    ([64, 129, 5], 2, 64, True),
+    ([900, 0, 1, 640, 130, 2000, 64, 65], 128, 64, True),    # least workspace, segmented: state in ht
+    ([900, 0, 1, 640, 130, 2000, 64, 65], 128, 64, False),   # segmented: state carried in the workspace
+])
+def test_chunk_fwd_varlen_poisoned_workspace(cuda, lengths, H, d, want_ht):
     cu = [0] + list(np.cumsum(lengths))
-    print(f"[poison varlen] lengths={lengths} d={d}", flush=True)
-    _chunk_fwd_case(cuda, 1, int(cu[-1]), 2, d, "bf16", True, True, cu=cu)
+    print(f"[poison varlen] lengths={lengths} H={H} d={d} ht={want_ht}", flush=True)
+    _chunk_fwd_case(cuda, 1, int(cu[-1]), H, d, "bf16", True, want_ht, cu=cu, least=H > 2)
 
 
 @pytest.mark.parametrize("B,T,H,d", [(1, 200, 2, 128), (2, 130, 2, 64)])
