@@ -43,9 +43,16 @@ constexpr int kThreads = 256;
 // The per-chunk adjoint runs 512 threads (two waves per SIMD): it is bound by
 // latency at one workgroup per CU (its LDS), so the second wave per SIMD hides it.
 constexpr int kChunkThreads = 512;
-// Scan workgroups likewise: one per (chain, 32-column slice), 512 threads, one
-// state column per thread.
-constexpr int kScanThreads = 512;
+// Scan workgroups: one per (chain, 32-column slice).  The scans are bound by
+// the latency of their serial chunk steps (operand splits into LDS, three
+// barriers and two short MFMA chains per step), so d = 128 runs 16 waves (four
+// per SIMD: one state tile and half the operand splitting per wave), d = 64
+// eight.
+template <int D>
+struct ScanThreads {
+  static constexpr int value = (D == 128) ? 1024 : 512;
+};
+constexpr int kScanThreads = 512;   // threads of the 64-column transposed tiles of the scans
 // The prep kernel likewise (the channel sums of a score tile pair split over
 // the two halves of the workgroup).
 constexpr int kPrepThreads = 512;
@@ -596,9 +603,11 @@ struct TTile {
 // bf16 planes with the K index contiguous, so each fragment is one 16-byte
 // read.  The state itself stays fp32 in the accumulators.
 template <int D>
-__global__ __launch_bounds__(kScanThreads) void kda_bwd_fscan_kernel(BwdArgs a) {
+__global__ __launch_bounds__(ScanThreads<D>::value) void kda_bwd_fscan_kernel(BwdArgs a) {
+  constexpr int NTH = ScanThreads<D>::value;
   constexpr int NS = D / 32;
-  constexpr int NST = D / 64;   // state tiles per wave
+  constexpr int NST = (D / 8) / (NTH / 64);   // state tiles per wave (D / 8 tiles of the 32-column slice)
+  static_assert(NST >= 1, "at least one state tile per wave");
   constexpr int PW = D + 8;     // bf16 pitch of rows whose K index is a channel
   constexpr int PK = kC + 8;    // bf16 pitch of rows whose K index is a chunk row
   __shared__ __attribute__((aligned(16))) __bf16 sWh[kC * PW], sWl[kC * PW];    // W [64][D]
@@ -606,14 +615,14 @@ __global__ __launch_bounds__(kScanThreads) void kda_bwd_fscan_kernel(BwdArgs a) 
   __shared__ __attribute__((aligned(16))) __bf16 sSh[32 * PW], sSl[32 * PW];    // S^T [32][D]
   __shared__ __attribute__((aligned(16))) __bf16 sVh[32 * PK], sVl[32 * PK];    // v~^T [32][64]
   __shared__ float sU[kC * kPB], sGC[D];
-  constexpr int NTH = kScanThreads;
   const int t = threadIdx.x, wv = t >> 6, l = t & 63, r = l & 15, gq = l >> 4;
   const int H = a.H;
   int chain, split;
   if (!scan_slot<NS>(a.B * H, chain, split)) return;   // uniform per workgroup
   const int b = chain / H, h = chain - b * H;
   const int c0 = 32 * split;
-  const int mt = wv >> 1, ct = wv & 1;                  // this wave's v~ tile
+  const int mt = wv >> 1, ct = wv & 1;                  // this wave's v~ tile (waves 0-7: 8 tiles)
+  const bool vt_wave = wv < 8;
   int rt[NST], cs[NST];                                 // this wave's state tiles
 #pragma unroll
   for (int q = 0; q < NST; ++q) { rt[q] = (wv * NST + q) >> 1; cs[q] = (wv * NST + q) & 1; }
@@ -697,7 +706,7 @@ __global__ __launch_bounds__(kScanThreads) void kda_bwd_fscan_kernel(BwdArgs a) 
     if (n + 1 < a.NT) fetch(n + 1);
     __syncthreads();
     // v~ = U - W S (two accumulation chains over the D / 32 K blocks)
-    {
+    if (vt_wave) {
       f4 acc0 = {0.f, 0.f, 0.f, 0.f}, acc1 = {0.f, 0.f, 0.f, 0.f};
 #pragma unroll
       for (int kb = 0; kb < D / 32; ++kb) {
@@ -745,9 +754,11 @@ __global__ __launch_bounds__(kScanThreads) void kda_bwd_fscan_kernel(BwdArgs a) 
 // do^T, (gamma q)^T, W^T and (-dv~)^T with the chunk row as the K index
 // (transposed stores of row pairs).  dS itself stays fp32 in the accumulators.
 template <int D, int DO>
-__global__ __launch_bounds__(kScanThreads) void kda_bwd_rscan_kernel(BwdArgs a) {
+__global__ __launch_bounds__(ScanThreads<D>::value) void kda_bwd_rscan_kernel(BwdArgs a) {
+  constexpr int NTH = ScanThreads<D>::value;
   constexpr int NS = D / 32;
-  constexpr int NST = D / 64;
+  constexpr int NST = (D / 8) / (NTH / 64);
+  static_assert(NST >= 1, "at least one state tile per wave");
   constexpr int PW = D + 8;     // bf16 pitch of rows whose K index is a channel
   constexpr int PK = kC + 8;    // bf16 pitch of rows whose K index is a chunk row
   // region R: lambda k [64][PW] and Aqk^T [64][PK] for dv~, then
@@ -767,14 +778,14 @@ __global__ __launch_bounds__(kScanThreads) void kda_bwd_rscan_kernel(BwdArgs a) 
   __bf16* const sQl = sQh + D * PK;
   __bf16* const sWh = sQl + D * PK;
   __bf16* const sWl = sWh + D * PK;
-  constexpr int NTH = kScanThreads;
   const int t = threadIdx.x, wv = t >> 6, l = t & 63, r = l & 15, gq = l >> 4;
   const int H = a.H;
   int chain, split;
   if (!scan_slot<NS>(a.B * H, chain, split)) return;   // uniform per workgroup
   const int b = chain / H, h = chain - b * H;
   const int c0 = 32 * split;
-  const int mt = wv >> 1, ct = wv & 1;
+  const int mt = wv >> 1, ct = wv & 1;                  // this wave's dv~ tile (waves 0-7: 8 tiles)
+  const bool vt_wave = wv < 8;
   const int mts = __builtin_amdgcn_readfirstlane(mt);
   int rt[NST], cs[NST];
 #pragma unroll
@@ -791,13 +802,14 @@ __global__ __launch_bounds__(kScanThreads) void kda_bwd_rscan_kernel(BwdArgs a) 
   // product ahead: lambda*k and Aqk (for dv~) during the previous chunk's dS
   // update, gamma*q and W (for dS) during this chunk's dv~.
   Tile<kC, D, NTH> tL;
-  TTile<kC, NTH> tA;
+  TTile<kC, kScanThreads> tA;   // threads t < kScanThreads
   TTile<D, NTH> tQ, tW;
+  const bool a_thread = t < kScanThreads;
   float pgc;   // gamma_C of the chunk, loaded with lambda*k and Aqk (every thread; t < D stores it)
   auto fetch_a = [&](int n) {
     const int64_t ch = (static_cast<int64_t>(b) * a.NT + n) * H + h;
     tL.fetch(a.KL + ch * kC * D, D, 0);
-    tA.fetch(a.AQ + ch * kC * kC, kC, 0);
+    if (a_thread) tA.fetch(a.AQ + ch * kC * kC, kC, 0);
     pgc = a.GCV[ch * D + (t & (D - 1))];
   };
   if (a.NT > 0) fetch_a(a.NT - 1);
@@ -818,7 +830,7 @@ __global__ __launch_bounds__(kScanThreads) void kda_bwd_rscan_kernel(BwdArgs a) 
       *reinterpret_cast<uint2*>(&sSl[col * PW + m0]) = ll;
     }
     put_hl<PW>(tL, sLh, sLl);
-    tA.template put_hl<PK>(sAh, sAl);
+    if (a_thread) tA.template put_hl<PK>(sAh, sAl);
     // do^T of the slice: thread t < 256 holds rows 2 rp, 2 rp + 1 of
     // columns c0 + 4 cg .. + 3 (rows past len read as zero)
     if (t < 256) {
@@ -846,7 +858,7 @@ __global__ __launch_bounds__(kScanThreads) void kda_bwd_rscan_kernel(BwdArgs a) 
     __syncthreads();
     // dv~ = (lambda k) dS + Aqk^T do; Aqk[j][m] is zero for j < m, so row
     // tile mt starts at the K block holding row 16 mt
-    {
+    if (vt_wave) {
       f4 acc0 = {0.f, 0.f, 0.f, 0.f}, acc1 = {0.f, 0.f, 0.f, 0.f};
 #pragma unroll
       for (int kb = 0; kb < D / 32; ++kb) {
@@ -1490,10 +1502,10 @@ hipError_t launch_bwd_t(const BwdArgs& a, hipStream_t s) {
   hipError_t e = hipGetLastError();
   if (e != hipSuccess) return e;
   const int scan_grid = (chains + 7) / 8 * 8 * (D / 32);
-  hipLaunchKernelGGL((kda_bwd_fscan_kernel<D>), dim3(scan_grid), dim3(kScanThreads), 0, s, a);
+  hipLaunchKernelGGL((kda_bwd_fscan_kernel<D>), dim3(scan_grid), dim3(ScanThreads<D>::value), 0, s, a);
   e = hipGetLastError();
   if (e != hipSuccess) return e;
-  hipLaunchKernelGGL((kda_bwd_rscan_kernel<D, DO>), dim3(scan_grid), dim3(kScanThreads), 0, s, a);
+  hipLaunchKernelGGL((kda_bwd_rscan_kernel<D, DO>), dim3(scan_grid), dim3(ScanThreads<D>::value), 0, s, a);
   e = hipGetLastError();
   if (e != hipSuccess) return e;
   hipLaunchKernelGGL((kda_bwd_chunk_kernel<D, DTQ, DTG, DO>), dim3(chunk_heads), dim3(kChunkThreads), 0, s, a);
