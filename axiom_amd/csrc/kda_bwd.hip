@@ -798,21 +798,49 @@ __global__ __launch_bounds__(ScanThreads<D>::value) void kda_bwd_rscan_kernel(Bw
       dS[q][i] = (a.dht != nullptr)
                      ? a.dht[(static_cast<int64_t>(chain) * D + 16 * rt[q] + 4 * gq + i) * D + c0 + 16 * cs[q] + r]
                      : 0.f;
-  // Operands of the two products of a chunk, loaded into registers one
-  // product ahead: lambda*k and Aqk (for dv~) during the previous chunk's dS
-  // update, gamma*q and W (for dS) during this chunk's dv~.
+  // Operands of a chunk, loaded into registers one chunk step ahead: lambda*k,
+  // Aqk, gamma_C and the do slice (for dv~) right after the previous chunk
+  // has staged its own, gamma*q and W (for the dS update) right after the
+  // previous chunk has staged its own.  Each load then has a whole chunk step
+  // to arrive, and the do slice is held as loaded (raw words) so that no wait
+  // falls at its load.
   Tile<kC, D, NTH> tL;
   TTile<kC, kScanThreads> tA;   // threads t < kScanThreads
   TTile<D, NTH> tQ, tW;
   const bool a_thread = t < kScanThreads;
   float pgc;   // gamma_C of the chunk, loaded with lambda*k and Aqk (every thread; t < D stores it)
+  // do^T of the slice: thread t < 256 holds rows 2 rp, 2 rp + 1 of columns
+  // c0 + 4 cg .. + 3 (rows past the chunk's end are loaded from row 0 and
+  // zeroed where staged)
+  typedef typename std::conditional<DO == 0, uint4, uint2>::type DoWord;
+  DoWord pdo[2];
+  const int drp = t & 31, dcg = t >> 5;
   auto fetch_a = [&](int n) {
-    const int64_t ch = (static_cast<int64_t>(b) * a.NT + n) * H + h;
+    const int u = b * a.NT + n;
+    const int64_t ch = static_cast<int64_t>(u) * H + h;
     tL.fetch(a.KL + ch * kC * D, D, 0);
     if (a_thread) tA.fetch(a.AQ + ch * kC * kC, kC, 0);
     pgc = a.GCV[ch * D + (t & (D - 1))];
+    if (t < 256) {
+      const ChunkRows crn = chunk_rows(a, u);
+#pragma unroll
+      for (int y = 0; y < 2; ++y) {
+        const int row = 2 * drp + y;
+        const int64_t i = ((crn.row0 + (row < crn.len ? row : 0)) * H + h) * D + c0 + 4 * dcg;
+        if constexpr (DO == 0) pdo[y] = *reinterpret_cast<const uint4*>(static_cast<const float*>(a.dout) + i);
+        else pdo[y] = *reinterpret_cast<const uint2*>(static_cast<const u16*>(a.dout) + i);
+      }
+    }
   };
-  if (a.NT > 0) fetch_a(a.NT - 1);
+  auto fetch_qw = [&](int n) {
+    const int64_t ch = (static_cast<int64_t>(b) * a.NT + n) * H + h;
+    tQ.fetch(a.QG + ch * kC * D, D, 0);
+    tW.fetch(a.WM + ch * kC * D, D, 0);
+  };
+  if (a.NT > 0) {
+    fetch_a(a.NT - 1);
+    fetch_qw(a.NT - 1);
+  }
   for (int n = a.NT - 1; n >= 0; --n) {
     const int u = b * a.NT + n;
     const int64_t ch = static_cast<int64_t>(u) * H + h;
@@ -831,16 +859,14 @@ __global__ __launch_bounds__(ScanThreads<D>::value) void kda_bwd_rscan_kernel(Bw
     }
     put_hl<PW>(tL, sLh, sLl);
     if (a_thread) tA.template put_hl<PK>(sAh, sAl);
-    // do^T of the slice: thread t < 256 holds rows 2 rp, 2 rp + 1 of
-    // columns c0 + 4 cg .. + 3 (rows past len read as zero)
     if (t < 256) {
-      const int rp = t & 31, cg = t >> 5;
       f4 x[2];
 #pragma unroll
       for (int y = 0; y < 2; ++y) {
-        const int row = 2 * rp + y;
-        const bool ok = row < cr.len;
-        const f4 v = ld4<DO>(a.dout, ((cr.row0 + (ok ? row : 0)) * H + h) * D + c0 + 4 * cg);
+        const bool ok = 2 * drp + y < cr.len;
+        f4 v;
+        if constexpr (DO == 0) v = __builtin_bit_cast(f4, pdo[y]);
+        else v = unpack4<DO>(pdo[y]);
 #pragma unroll
         for (int e = 0; e < 4; ++e) x[y][e] = ok ? v[e] : 0.f;
       }
@@ -848,13 +874,12 @@ __global__ __launch_bounds__(ScanThreads<D>::value) void kda_bwd_rscan_kernel(Bw
       for (int e = 0; e < 4; ++e) {
         unsigned hh, ll;
         split2_bf16(x[0][e], x[1][e], hh, ll);
-        *reinterpret_cast<unsigned*>(&sOh[(4 * cg + e) * PK + 2 * rp]) = hh;
-        *reinterpret_cast<unsigned*>(&sOl[(4 * cg + e) * PK + 2 * rp]) = ll;
+        *reinterpret_cast<unsigned*>(&sOh[(4 * dcg + e) * PK + 2 * drp]) = hh;
+        *reinterpret_cast<unsigned*>(&sOl[(4 * dcg + e) * PK + 2 * drp]) = ll;
       }
     }
     if (t < D) sGC[t] = pgc;
-    tQ.fetch(a.QG + ch * kC * D, D, 0);
-    tW.fetch(a.WM + ch * kC * D, D, 0);
+    if (n > 0) fetch_a(n - 1);
     __syncthreads();
     // dv~ = (lambda k) dS + Aqk^T do; Aqk[j][m] is zero for j < m, so row
     // tile mt starts at the K block holding row 16 mt
@@ -887,7 +912,7 @@ __global__ __launch_bounds__(ScanThreads<D>::value) void kda_bwd_rscan_kernel(Bw
     __syncthreads();
     tQ.template put_hl<PK>(sQh, sQl);
     tW.template put_hl<PK>(sWh, sWl);
-    if (n > 0) fetch_a(n - 1);
+    if (n > 0) fetch_qw(n - 1);
     __syncthreads();
     // dS <- gamma_C dS + (gamma q)^T do - W^T dv~
 #pragma unroll
