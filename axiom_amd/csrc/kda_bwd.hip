@@ -753,6 +753,17 @@ __global__ __launch_bounds__(ScanThreads<D>::value) void kda_bwd_fscan_kernel(Bw
 // and the state cotangent slice dS^T with the channel as the K index; Aqk^T,
 // do^T, (gamma q)^T, W^T and (-dv~)^T with the chunk row as the K index
 // (transposed stores of row pairs).  dS itself stays fp32 in the accumulators.
+//
+// A chunk step has three phases between workgroup barriers, and every
+// operand has LDS of its own, so each is staged one phase or more before it
+// is read, in the shadow of the products:
+//   A  store dS, stage it as hi / lo planes; dS <- gamma_C dS + (gamma q)^T do
+//      (everything it reads was staged during the previous chunk);
+//   B  dv~ = (lambda k) dS + Aqk^T do on waves 0-7, then every wave stages
+//      W^T of this chunk (read in C) and loads W of the next one;
+//   C  dS <- dS - W^T dv~; every wave stages lambda k, Aqk^T, do^T,
+//      (gamma q)^T and gamma_C of the next chunk (read in its A and B) and
+//      loads the one after.
 template <int D, int DO>
 __global__ __launch_bounds__(ScanThreads<D>::value) void kda_bwd_rscan_kernel(BwdArgs a) {
   constexpr int NTH = ScanThreads<D>::value;
@@ -761,23 +772,14 @@ __global__ __launch_bounds__(ScanThreads<D>::value) void kda_bwd_rscan_kernel(Bw
   static_assert(NST >= 1, "at least one state tile per wave");
   constexpr int PW = D + 8;     // bf16 pitch of rows whose K index is a channel
   constexpr int PK = kC + 8;    // bf16 pitch of rows whose K index is a chunk row
-  // region R: lambda k [64][PW] and Aqk^T [64][PK] for dv~, then
-  // (gamma q)^T [D][PK] and W^T [D][PK] for the dS update
-  constexpr int RA = 2 * kC * PW + 2 * kC * PK, RB = 4 * D * PK;
-  constexpr int RN = RA > RB ? RA : RB;
-  __shared__ __attribute__((aligned(16))) __bf16 sR[RN];
+  __shared__ __attribute__((aligned(16))) __bf16 sLh[kC * PW], sLl[kC * PW];   // lambda k [64][D]
+  __shared__ __attribute__((aligned(16))) __bf16 sAh[kC * PK], sAl[kC * PK];   // Aqk^T [64][64]
+  __shared__ __attribute__((aligned(16))) __bf16 sQh[D * PK], sQl[D * PK];     // (gamma q)^T [D][64]
+  __shared__ __attribute__((aligned(16))) __bf16 sWh[D * PK], sWl[D * PK];     // W^T [D][64]
   __shared__ __attribute__((aligned(16))) __bf16 sSh[32 * PW], sSl[32 * PW];   // dS^T [32][D]
   __shared__ __attribute__((aligned(16))) __bf16 sOh[32 * PK], sOl[32 * PK];   // do^T [32][64]
   __shared__ __attribute__((aligned(16))) __bf16 sVh[32 * PK], sVl[32 * PK];   // (-dv~)^T [32][64]
   __shared__ float sGC[D];
-  __bf16* const sLh = sR;
-  __bf16* const sLl = sLh + kC * PW;
-  __bf16* const sAh = sLl + kC * PW;
-  __bf16* const sAl = sAh + kC * PK;
-  __bf16* const sQh = sR;
-  __bf16* const sQl = sQh + D * PK;
-  __bf16* const sWh = sQl + D * PK;
-  __bf16* const sWl = sWh + D * PK;
   const int t = threadIdx.x, wv = t >> 6, l = t & 63, r = l & 15, gq = l >> 4;
   const int H = a.H;
   int chain, split;
@@ -798,53 +800,74 @@ __global__ __launch_bounds__(ScanThreads<D>::value) void kda_bwd_rscan_kernel(Bw
       dS[q][i] = (a.dht != nullptr)
                      ? a.dht[(static_cast<int64_t>(chain) * D + 16 * rt[q] + 4 * gq + i) * D + c0 + 16 * cs[q] + r]
                      : 0.f;
-  // Operands of a chunk, loaded into registers one chunk step ahead: lambda*k,
-  // Aqk, gamma_C and the do slice (for dv~) right after the previous chunk
-  // has staged its own, gamma*q and W (for the dS update) right after the
-  // previous chunk has staged its own.  Each load then has a whole chunk step
-  // to arrive, and the do slice is held as loaded (raw words) so that no wait
-  // falls at its load.
+  // Operands in registers between their loads and their staging, one set
+  // each: a set is reloaded right after it is staged, so every load has a
+  // whole chunk step to arrive.  The do slice is held as loaded (raw words),
+  // so that no wait falls at its load.
   Tile<kC, D, NTH> tL;
   TTile<kC, kScanThreads> tA;   // threads t < kScanThreads
   TTile<D, NTH> tQ, tW;
   const bool a_thread = t < kScanThreads;
-  float pgc;   // gamma_C of the chunk, loaded with lambda*k and Aqk (every thread; t < D stores it)
-  // do^T of the slice: thread t < 256 holds rows 2 rp, 2 rp + 1 of columns
-  // c0 + 4 cg .. + 3 (rows past the chunk's end are loaded from row 0 and
-  // zeroed where staged)
-  typedef typename std::conditional<DO == 0, uint4, uint2>::type DoWord;
-  DoWord pdo[2];
-  const int drp = t & 31, dcg = t >> 5;
-  auto fetch_a = [&](int n) {
+  float pgc;   // gamma_C of the chunk (every thread; t < D stages it)
+  // do^T of the slice, spread over every thread: thread t holds rows 2 rp,
+  // 2 rp + 1 of the DCPT columns c0 + DCPT cg .. (consecutive threads at
+  // consecutive columns; rows past the chunk's end are loaded from row 0 and
+  // zeroed where staged), as raw words
+  constexpr int DCPT = (kC * 32) / 2 / NTH;   // columns per thread
+  constexpr int DCG = 32 / DCPT;              // column groups
+  static_assert(DCPT >= 1 && DCPT <= 2 && DCG * DCPT == 32 && 2 * DCG * 32 == 2 * NTH, "do slice mapping");
+  uint32_t pdo[2][DCPT];
+  const int dcg = t % DCG, drp = t / DCG;
+  auto do_val = [&](uint32_t w) -> float {
+    if constexpr (DO == 0) return __uint_as_float(w);
+    else if constexpr (DO == 1) return __uint_as_float(w << 16);
+    else return f16bits_to_f32(static_cast<u16>(w));
+  };
+  auto chead = [&](int n) { return (static_cast<int64_t>(b) * a.NT + n) * H + h; };
+  auto fetch_a = [&](int n) {   // lambda k, Aqk, gamma q, gamma_C and do of chunk n
     const int u = b * a.NT + n;
-    const int64_t ch = static_cast<int64_t>(u) * H + h;
+    const int64_t ch = chead(n);
     tL.fetch(a.KL + ch * kC * D, D, 0);
     if (a_thread) tA.fetch(a.AQ + ch * kC * kC, kC, 0);
+    tQ.fetch(a.QG + ch * kC * D, D, 0);
     pgc = a.GCV[ch * D + (t & (D - 1))];
-    if (t < 256) {
-      const ChunkRows crn = chunk_rows(a, u);
+    const ChunkRows crn = chunk_rows(a, u);
 #pragma unroll
-      for (int y = 0; y < 2; ++y) {
-        const int row = 2 * drp + y;
-        const int64_t i = ((crn.row0 + (row < crn.len ? row : 0)) * H + h) * D + c0 + 4 * dcg;
-        if constexpr (DO == 0) pdo[y] = *reinterpret_cast<const uint4*>(static_cast<const float*>(a.dout) + i);
-        else pdo[y] = *reinterpret_cast<const uint2*>(static_cast<const u16*>(a.dout) + i);
+    for (int y = 0; y < 2; ++y) {
+      const int row = 2 * drp + y;
+      const int64_t i = ((crn.row0 + (row < crn.len ? row : 0)) * H + h) * D + c0 + DCPT * dcg;
+#pragma unroll
+      for (int e = 0; e < DCPT; ++e) {
+        if constexpr (DO == 0) pdo[y][e] = static_cast<const uint32_t*>(a.dout)[i + e];
+        else pdo[y][e] = static_cast<const u16*>(a.dout)[i + e];
       }
     }
   };
-  auto fetch_qw = [&](int n) {
-    const int64_t ch = (static_cast<int64_t>(b) * a.NT + n) * H + h;
-    tQ.fetch(a.QG + ch * kC * D, D, 0);
-    tW.fetch(a.WM + ch * kC * D, D, 0);
+  auto put_a = [&](int n) {     // ... staged for chunk n
+    const ChunkRows crn = chunk_rows(a, b * a.NT + n);
+    put_hl<PW>(tL, sLh, sLl);
+    if (a_thread) tA.template put_hl<PK>(sAh, sAl);
+    tQ.template put_hl<PK>(sQh, sQl);
+    const bool ok0 = 2 * drp < crn.len, ok1 = 2 * drp + 1 < crn.len;
+#pragma unroll
+    for (int e = 0; e < DCPT; ++e) {
+      unsigned hh, ll;
+      split2_bf16(ok0 ? do_val(pdo[0][e]) : 0.f, ok1 ? do_val(pdo[1][e]) : 0.f, hh, ll);
+      *reinterpret_cast<unsigned*>(&sOh[(DCPT * dcg + e) * PK + 2 * drp]) = hh;
+      *reinterpret_cast<unsigned*>(&sOl[(DCPT * dcg + e) * PK + 2 * drp]) = ll;
+    }
+    if (t < D) sGC[t] = pgc;
   };
   if (a.NT > 0) {
     fetch_a(a.NT - 1);
-    fetch_qw(a.NT - 1);
+    tW.fetch(a.WM + chead(a.NT - 1) * kC * D, D, 0);
+    put_a(a.NT - 1);
+    if (a.NT > 1) fetch_a(a.NT - 2);
+    __syncthreads();
   }
   for (int n = a.NT - 1; n >= 0; --n) {
-    const int u = b * a.NT + n;
-    const int64_t ch = static_cast<int64_t>(u) * H + h;
-    const ChunkRows cr = chunk_rows(a, u);
+    const int64_t ch = chead(n);
+    // ---- A: store and stage dS; dS <- gamma_C dS + (gamma q)^T do
     float* DS = a.DS + ch * D * D;
 #pragma unroll
     for (int q = 0; q < NST; ++q) {
@@ -857,32 +880,21 @@ __global__ __launch_bounds__(ScanThreads<D>::value) void kda_bwd_rscan_kernel(Bw
       *reinterpret_cast<uint2*>(&sSh[col * PW + m0]) = hh;
       *reinterpret_cast<uint2*>(&sSl[col * PW + m0]) = ll;
     }
-    put_hl<PW>(tL, sLh, sLl);
-    if (a_thread) tA.template put_hl<PK>(sAh, sAl);
-    if (t < 256) {
-      f4 x[2];
 #pragma unroll
-      for (int y = 0; y < 2; ++y) {
-        const bool ok = 2 * drp + y < cr.len;
-        f4 v;
-        if constexpr (DO == 0) v = __builtin_bit_cast(f4, pdo[y]);
-        else v = unpack4<DO>(pdo[y]);
+    for (int q = 0; q < NST; ++q)
 #pragma unroll
-        for (int e = 0; e < 4; ++e) x[y][e] = ok ? v[e] : 0.f;
+      for (int i = 0; i < 4; ++i) dS[q][i] *= sGC[16 * rt[q] + 4 * gq + i];
+#pragma unroll
+    for (int kb = 0; kb < kC / 32; ++kb)
+#pragma unroll
+      for (int q = 0; q < NST; ++q) {
+        const int ka = (16 * rt[q] + r) * PK + 32 * kb + 8 * gq, kbb = (16 * cs[q] + r) * PK + 32 * kb + 8 * gq;
+        dS[q] = mma3_bf16(dS[q], *reinterpret_cast<const b8*>(&sQh[ka]), *reinterpret_cast<const b8*>(&sQl[ka]),
+                          *reinterpret_cast<const b8*>(&sOh[kbb]), *reinterpret_cast<const b8*>(&sOl[kbb]));
       }
-#pragma unroll
-      for (int e = 0; e < 4; ++e) {
-        unsigned hh, ll;
-        split2_bf16(x[0][e], x[1][e], hh, ll);
-        *reinterpret_cast<unsigned*>(&sOh[(4 * dcg + e) * PK + 2 * drp]) = hh;
-        *reinterpret_cast<unsigned*>(&sOl[(4 * dcg + e) * PK + 2 * drp]) = ll;
-      }
-    }
-    if (t < D) sGC[t] = pgc;
-    if (n > 0) fetch_a(n - 1);
     __syncthreads();
-    // dv~ = (lambda k) dS + Aqk^T do; Aqk[j][m] is zero for j < m, so row
-    // tile mt starts at the K block holding row 16 mt
+    // ---- B: dv~ = (lambda k) dS + Aqk^T do; Aqk[j][m] is zero for j < m,
+    // so row tile mt starts at the K block holding row 16 mt
     if (vt_wave) {
       f4 acc0 = {0.f, 0.f, 0.f, 0.f}, acc1 = {0.f, 0.f, 0.f, 0.f};
 #pragma unroll
@@ -909,26 +921,23 @@ __global__ __launch_bounds__(ScanThreads<D>::value) void kda_bwd_rscan_kernel(Bw
       *reinterpret_cast<uint2*>(&sVh[(16 * ct + r) * PK + 16 * mt + 4 * gq]) = hh;
       *reinterpret_cast<uint2*>(&sVl[(16 * ct + r) * PK + 16 * mt + 4 * gq]) = ll;
     }
-    __syncthreads();
-    tQ.template put_hl<PK>(sQh, sQl);
     tW.template put_hl<PK>(sWh, sWl);
-    if (n > 0) fetch_qw(n - 1);
+    if (n > 0) tW.fetch(a.WM + chead(n - 1) * kC * D, D, 0);
     __syncthreads();
-    // dS <- gamma_C dS + (gamma q)^T do - W^T dv~
-#pragma unroll
-    for (int q = 0; q < NST; ++q)
-#pragma unroll
-      for (int i = 0; i < 4; ++i) dS[q][i] *= sGC[16 * rt[q] + 4 * gq + i];
+    // ---- C: dS <- dS - W^T dv~; the next chunk's lambda k, Aqk^T, do^T,
+    // (gamma q)^T and gamma_C staged while the products run
 #pragma unroll
     for (int kb = 0; kb < kC / 32; ++kb)
 #pragma unroll
       for (int q = 0; q < NST; ++q) {
         const int ka = (16 * rt[q] + r) * PK + 32 * kb + 8 * gq, kbb = (16 * cs[q] + r) * PK + 32 * kb + 8 * gq;
-        dS[q] = mma3_bf16(dS[q], *reinterpret_cast<const b8*>(&sQh[ka]), *reinterpret_cast<const b8*>(&sQl[ka]),
-                          *reinterpret_cast<const b8*>(&sOh[kbb]), *reinterpret_cast<const b8*>(&sOl[kbb]));
         dS[q] = mma3_bf16(dS[q], *reinterpret_cast<const b8*>(&sWh[ka]), *reinterpret_cast<const b8*>(&sWl[ka]),
                           *reinterpret_cast<const b8*>(&sVh[kbb]), *reinterpret_cast<const b8*>(&sVl[kbb]));
       }
+    if (n > 0) {
+      put_a(n - 1);
+      if (n > 1) fetch_a(n - 2);
+    }
     __syncthreads();
   }
   if (a.dh0 != nullptr) {
