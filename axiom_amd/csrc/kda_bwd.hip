@@ -86,25 +86,94 @@ __device__ __forceinline__ ChunkRows chunk_rows(const BwdArgs& a, int u) {
 // first column col0) into LDS rows of pitch PITCH.  All of a thread's 16-byte
 // loads are issued before its LDS writes, so they are in flight together.
 // The two halves of lds_load: the loads into registers (a thread's share,
-// Tile::PER 16-byte pieces) and the LDS writes.  Split, a scan kernel issues
-// the next chunk's loads before the current chunk's arithmetic.
-template <int ROWS, int COLS, int NTH = kThreads>
+// Tile::PER pieces of four elements) and the LDS writes.  Split, a scan kernel
+// issues the next chunk's loads before the current chunk's arithmetic.
+//
+// Workspace arrays are fp32 (ET 0) or fp16 (ET 2, see BwdWs); an fp16 tile
+// loads 8 bytes per piece and converts when it is written to LDS, so the wait
+// for the load falls there, not at the fetch.
+template <int ET>
+struct WsPiece {
+  typedef uint2 t;
+};
+template <>
+struct WsPiece<0> {
+  typedef float4 t;
+};
+template <int ET>
+__device__ __forceinline__ float4 ws_unpack(const typename WsPiece<ET>::t& w) {
+  if constexpr (ET == 0) {
+    return w;
+  } else {
+    const f4 v = unpack4<ET>(w);
+    return make_float4(v[0], v[1], v[2], v[3]);
+  }
+}
+// element `off` of a workspace array of element type ET
+template <int ET>
+__device__ __forceinline__ const void* ws_at(const float* base, int64_t off) {
+  if constexpr (ET == 0) return base + off;
+  else return reinterpret_cast<const u16*>(base) + off;
+}
+template <int ET>
+__device__ __forceinline__ void ws_st(float* base, int64_t off, float x) {
+  static_assert(ET == 0 || ET == 2, "workspace arrays are fp32 or fp16");
+  if constexpr (ET == 0) base[off] = x;
+  else reinterpret_cast<u16*>(base)[off] = __builtin_bit_cast(u16, static_cast<_Float16>(x));
+}
+// four consecutive elements (off a multiple of 4)
+template <int ET>
+__device__ __forceinline__ void ws_st4(float* base, int64_t off, float4 x) {
+  if constexpr (ET == 0) {
+    *reinterpret_cast<float4*>(base + off) = x;
+  } else {
+    static_assert(ET == 2, "workspace arrays are fp32 or fp16");
+    typedef _Float16 hv4 __attribute__((ext_vector_type(4)));
+    const hv4 v = {static_cast<_Float16>(x.x), static_cast<_Float16>(x.y), static_cast<_Float16>(x.z),
+                   static_cast<_Float16>(x.w)};
+    *reinterpret_cast<uint2*>(reinterpret_cast<u16*>(base) + off) = __builtin_bit_cast(uint2, v);
+  }
+}
+
+// four fp32 -> packed fp16 (round to nearest even)
+__device__ __forceinline__ uint2 pack_f16x4(const f4& x) {
+  const h4 v = {static_cast<_Float16>(x[0]), static_cast<_Float16>(x[1]), static_cast<_Float16>(x[2]),
+                static_cast<_Float16>(x[3])};
+  return __builtin_bit_cast(uint2, v);
+}
+
+// Element types of the backward's workspace.  fp32 inputs keep every array
+// fp32.  16-bit inputs store six forward-side arrays in fp16 (gamma q,
+// lambda k, Aqk, T, W and the chunk's incoming state S: the operand width the
+// forward's own kernels use for them); G, gamma_C, U, v~ (U - W S cancels, so
+// their rounding would reach the gradients amplified) and the cotangents dS,
+// dv~ (whose scale is the caller's) stay fp32.
+template <bool WS16>
+struct BwdWs {
+  static constexpr int F = WS16 ? 2 : 0;
+};
+
+template <int ROWS, int COLS, int NTH = kThreads, int ET = 0>
 struct Tile {
   static constexpr int V = COLS / 4;
   static constexpr int N = ROWS * V;
   static constexpr int PER = (N + NTH - 1) / NTH;
-  static_assert(COLS % 4 == 0, "16-byte loads");
-  float4 r[PER];
-  __device__ __forceinline__ void fetch(const float* src, int src_ld, int col0) {
+  static_assert(COLS % 4 == 0, "four-element pieces");
+  typedef typename WsPiece<ET>::t Piece;
+  Piece r[PER];
+  __device__ __forceinline__ void fetch(const void* src, int src_ld, int col0) {
 #pragma unroll
     for (int p = 0; p < PER; ++p) {
       const int e = threadIdx.x + p * NTH;
       if (N % NTH == 0 || e < N) {
         const int row = e / V, c4 = e - row * V;
-        r[p] = *reinterpret_cast<const float4*>(src + static_cast<int64_t>(row) * src_ld + col0 + 4 * c4);
+        const int64_t i = static_cast<int64_t>(row) * src_ld + col0 + 4 * c4;
+        if constexpr (ET == 0) r[p] = *reinterpret_cast<const float4*>(static_cast<const float*>(src) + i);
+        else r[p] = *reinterpret_cast<const uint2*>(static_cast<const u16*>(src) + i);
       }
     }
   }
+  __device__ __forceinline__ float4 get(int p) const { return ws_unpack<ET>(r[p]); }
   template <int PITCH>
   __device__ __forceinline__ void put(float* dst) const {
 #pragma unroll
@@ -112,11 +181,12 @@ struct Tile {
       const int e = threadIdx.x + p * NTH;
       if (N % NTH == 0 || e < N) {
         const int row = e / V, c4 = e - row * V;
+        const float4 x = get(p);
         float* d = dst + row * PITCH + 4 * c4;
-        d[0] = r[p].x;
-        d[1] = r[p].y;
-        d[2] = r[p].z;
-        d[3] = r[p].w;
+        d[0] = x.x;
+        d[1] = x.y;
+        d[2] = x.z;
+        d[3] = x.w;
       }
     }
   }
@@ -128,6 +198,12 @@ __device__ __forceinline__ void lds_load(float* dst, const float* src, int src_l
   t.fetch(src, src_ld, col0);
   t.template put<PITCH>(dst);
 }
+
+// Largest in-tile decay (log2 units, one channel) at which the chunk
+// kernel's diagonal score-adjoint tiles run on the matrix cores anchored at
+// the tile's first row: the key factors reach 2^kDiagAnchorLog2, which leaves
+// 2^96 of fp32's range for the cotangent sums they multiply.
+constexpr float kDiagAnchorLog2 = 32.f;
 
 // Workgroup -> (chain, 32-column slice) of the scan kernels: the NS slices
 // of a chain on one XCD (workgroup x runs on XCD x % 8), so the operands all
@@ -257,6 +333,7 @@ __device__ __forceinline__ f4 mfma4(float a, float b, f4 c) {
 // their columns (the last half's k and G still staged, the other reloaded).
 template <int D, int DTQ, int DTG>
 __global__ __launch_bounds__(kPrepThreads, 4) void kda_bwd_prep_kernel(BwdArgs a) {
+  constexpr int EF = BwdWs<DTQ != 0>::F;   // gamma q, lambda k, Aqk, T, W, U
   constexpr int HD = 64;              // channels per half
   constexpr int NHALF = D / HD;
   // [64][HD] pitch: row fragments conflict-free (rows 4 banks apart), rows
@@ -335,9 +412,8 @@ __global__ __launch_bounds__(kPrepThreads, 4) void kda_bwd_prep_kernel(BwdArgs a
     cumsum_g();
     __syncthreads();
     {
-      float* GL = a.GL + ch * kC * D + c0;
-      float* QG = a.QG + ch * kC * D + c0;
-      float* KL = a.KL + ch * kC * D + c0;
+      const int64_t base = ch * kC * D + c0;
+      float* GL = a.GL + base;
       constexpr int V4 = HD / 4;      // float4 groups per row
       for (int e = t; e < kC * V4; e += NTH) {
         const int c = e / V4, d = 4 * (e - c * V4);
@@ -349,8 +425,8 @@ __global__ __launch_bounds__(kPrepThreads, 4) void kda_bwd_prep_kernel(BwdArgs a
         const float4 kl = make_float4(ex2(gz.x - gl.x) * kv.x, ex2(gz.y - gl.y) * kv.y, ex2(gz.z - gl.z) * kv.z,
                                       ex2(gz.w - gl.w) * kv.w);
         *reinterpret_cast<float4*>(&GL[c * D + d]) = gl;
-        *reinterpret_cast<float4*>(&QG[c * D + d]) = qg;
-        *reinterpret_cast<float4*>(&KL[c * D + d]) = kl;
+        ws_st4<EF>(a.QG, base + c * D + d, qg);
+        ws_st4<EF>(a.KL, base + c * D + d, kl);
       }
       if (t < HD) a.GCV[ch * D + c0 + t] = ex2(sG[(kC - 1) * P + t]);
     }
@@ -391,13 +467,13 @@ __global__ __launch_bounds__(kPrepThreads, 4) void kda_bwd_prep_kernel(BwdArgs a
       }
     }
   }
-  float* AQ = a.AQ + ch * kC * kC;
+  const int64_t aq0 = ch * kC * kC;
   if (wv < 6) {
     const int a0 = 16 * R_off, i = 16 * sk_off + r16;
 #pragma unroll
     for (int e = 0; e < 4; ++e) {
       const int c = a0 + 4 * gq + e;
-      AQ[c * kC + i] = accA[e];
+      ws_st<EF>(a.AQ, aq0 + c * kC + i, accA[e]);
       sL[c * PC + i] = accL[e] * sB[c];
     }
   }
@@ -406,7 +482,7 @@ __global__ __launch_bounds__(kPrepThreads, 4) void kda_bwd_prep_kernel(BwdArgs a
     const int p = t + NTH * j;
     const int R = p >> 8, rc = (p >> 4) & 15, ri = p & 15;
     const int c = 16 * R + rc, i = 16 * R + ri;
-    AQ[c * kC + i] = (ri <= rc) ? dA[j] : 0.f;
+    ws_st<EF>(a.AQ, aq0 + c * kC + i, (ri <= rc) ? dA[j] : 0.f);
     sL[c * PC + i] = (ri < rc) ? dL[j] * sB[c] : 0.f;
   }
   // blocks above the diagonal: zero
@@ -415,7 +491,7 @@ __global__ __launch_bounds__(kPrepThreads, 4) void kda_bwd_prep_kernel(BwdArgs a
     const int R = (blk < 3) ? 0 : (blk < 5) ? 1 : 2;             // (0,1) (0,2) (0,3) (1,2) (1,3) (2,3)
     const int sk = (blk < 3) ? blk + 1 : (blk < 5) ? blk - 1 : 3;
     const int c = 16 * R + rc, i = 16 * sk + ri;
-    AQ[c * kC + i] = 0.f;
+    ws_st<EF>(a.AQ, aq0 + c * kC + i, 0.f);
     sL[c * PC + i] = 0.f;
   }
   __syncthreads();
@@ -426,10 +502,9 @@ __global__ __launch_bounds__(kPrepThreads, 4) void kda_bwd_prep_kernel(BwdArgs a
   iv.fetch(a.v, cr.row0, cr.len, H, h, HD * (NHALF - 1));
   invert_unit_lower64<PC, NTH>(sL, sT, sTmp);
   {
-    float* TM = a.TM + ch * kC * kC;
     for (int e = t; e < kC * kC; e += NTH) {
       const int c = e / kC, i = e - c * kC;
-      TM[e] = sT[c * PC + i];
+      ws_st<EF>(a.TM, ch * kC * kC + e, sT[c * PC + i]);
     }
   }
   // W = T (beta gamma k), U = T (beta v) on the matrix cores, per half of
@@ -472,15 +547,14 @@ __global__ __launch_bounds__(kPrepThreads, 4) void kda_bwd_prep_kernel(BwdArgs a
         accU[q] = mfma4(at, sV[(4 * k + gq) * PC + col], accU[q]);
       }
     }
-    float* WM = a.WM + ch * kC * D + c0;
-    float* UM = a.UM + ch * kC * D + c0;
+    const int64_t wu0 = ch * kC * D + c0;
 #pragma unroll
     for (int q = 0; q < NDT; ++q)
 #pragma unroll
       for (int e = 0; e < 4; ++e) {
         const int o = (16 * mt + 4 * gq + e) * D + 16 * (dg * NDT + q) + r16;
-        WM[o] = accW[q][e];
-        UM[o] = accU[q][e];
+        ws_st<EF>(a.WM, wu0 + o, accW[q][e]);
+        a.UM[wu0 + o] = accU[q][e];
       }
   }
 }
@@ -512,17 +586,18 @@ __device__ __forceinline__ f4 mma3_bf16(f4 acc, const b8& ah, const b8& al, cons
 }
 
 // A fetched fp32 tile into LDS as hi / lo bf16 planes (row pitch PB bf16).
-template <int PB, int ROWS, int COLS, int NTH>
-__device__ __forceinline__ void put_hl(const Tile<ROWS, COLS, NTH>& tl, __bf16* h, __bf16* l) {
-  typedef Tile<ROWS, COLS, NTH> TT;
+template <int PB, int ROWS, int COLS, int NTH, int ET>
+__device__ __forceinline__ void put_hl(const Tile<ROWS, COLS, NTH, ET>& tl, __bf16* h, __bf16* l) {
+  typedef Tile<ROWS, COLS, NTH, ET> TT;
 #pragma unroll
   for (int p = 0; p < TT::PER; ++p) {
     const int e = threadIdx.x + p * NTH;
     if (TT::N % NTH == 0 || e < TT::N) {
       const int row = e / TT::V, c4 = e - row * TT::V;
+      const float4 x = tl.get(p);
       uint2 hh, ll;
-      split2_bf16(tl.r[p].x, tl.r[p].y, hh.x, ll.x);
-      split2_bf16(tl.r[p].z, tl.r[p].w, hh.y, ll.y);
+      split2_bf16(x.x, x.y, hh.x, ll.x);
+      split2_bf16(x.z, x.w, hh.y, ll.y);
       *reinterpret_cast<uint2*>(&h[row * PB + 4 * c4]) = hh;
       *reinterpret_cast<uint2*>(&l[row * PB + 4 * c4]) = ll;
     }
@@ -557,25 +632,28 @@ __device__ __forceinline__ void put_hl(const InTile<DT, D, COLS, NTH>& tl, __bf1
   }
 }
 
-// A [64][COLS] fp32 tile fetched for a transposed store into hi / lo bf16
-// planes [COLS][64] (the source row index becomes the contiguous K index):
-// thread t holds rows 2 rp and 2 rp + 1 (rp = t % 32) of the float4 column
-// groups t / 32 + (NTH / 32) j, so each transposed row is written as packed
-// row pairs, consecutive lanes at consecutive words.
-template <int COLS, int NTH>
+// A [64][COLS] tile (element type ET) fetched for a transposed store into
+// hi / lo bf16 planes [COLS][64] (the source row index becomes the contiguous
+// K index): thread t holds rows 2 rp and 2 rp + 1 (rp = t % 32) of the
+// four-column groups t / 32 + (NTH / 32) j, so each transposed row is written
+// as packed row pairs, consecutive lanes at consecutive words.
+template <int COLS, int NTH, int ET = 0>
 struct TTile {
   static constexpr int G = NTH / 32;
   static constexpr int PER = (COLS / 4) / G;
   static_assert(NTH % 32 == 0 && (COLS / 4) % G == 0, "transposed tile mapping");
-  float4 r[PER][2];
-  __device__ __forceinline__ void fetch(const float* src, int src_ld, int col0) {
+  typedef typename WsPiece<ET>::t Piece;
+  Piece r[PER][2];
+  __device__ __forceinline__ void fetch(const void* src, int src_ld, int col0) {
     const int rp = threadIdx.x & 31, cg = threadIdx.x >> 5;
 #pragma unroll
     for (int j = 0; j < PER; ++j)
 #pragma unroll
-      for (int y = 0; y < 2; ++y)
-        r[j][y] = *reinterpret_cast<const float4*>(src + static_cast<int64_t>(2 * rp + y) * src_ld + col0 +
-                                                   4 * (cg + G * j));
+      for (int y = 0; y < 2; ++y) {
+        const int64_t i = static_cast<int64_t>(2 * rp + y) * src_ld + col0 + 4 * (cg + G * j);
+        if constexpr (ET == 0) r[j][y] = *reinterpret_cast<const float4*>(static_cast<const float*>(src) + i);
+        else r[j][y] = *reinterpret_cast<const uint2*>(static_cast<const u16*>(src) + i);
+      }
   }
   template <int PB>
   __device__ __forceinline__ void put_hl(__bf16* h, __bf16* l) const {
@@ -583,8 +661,9 @@ struct TTile {
 #pragma unroll
     for (int j = 0; j < PER; ++j) {
       const int c4 = 4 * (cg + G * j);
-      const float x0[4] = {r[j][0].x, r[j][0].y, r[j][0].z, r[j][0].w};
-      const float x1[4] = {r[j][1].x, r[j][1].y, r[j][1].z, r[j][1].w};
+      const float4 y0 = ws_unpack<ET>(r[j][0]), y1 = ws_unpack<ET>(r[j][1]);
+      const float x0[4] = {y0.x, y0.y, y0.z, y0.w};
+      const float x1[4] = {y1.x, y1.y, y1.z, y1.w};
 #pragma unroll
       for (int e = 0; e < 4; ++e) {
         unsigned hh, ll;
@@ -601,9 +680,14 @@ struct TTile {
 // (r, gq) holding K values 8 gq .. 8 gq + 7 of each 32-wide block): W and
 // (lambda k)^T, the state slice S^T and v~^T are kept in LDS as hi and lo
 // bf16 planes with the K index contiguous, so each fragment is one 16-byte
-// read.  The state itself stays fp32 in the accumulators.
-template <int D>
+// read.  The state itself stays fp32 in the accumulators.  With 16-bit inputs
+// every operand of both products is forward-side and fp16 (W and lambda k as
+// stored; S rounded as it is stored, v~ rounded for the product and stored
+// in fp32), so each product is one fp16 MFMA per K block, the forward
+// kernels' operand precision.
+template <int D, bool WS16>
 __global__ __launch_bounds__(ScanThreads<D>::value) void kda_bwd_fscan_kernel(BwdArgs a) {
+  constexpr int EF = BwdWs<WS16>::F;   // W, lambda k in; S_in out
   constexpr int NTH = ScanThreads<D>::value;
   constexpr int NS = D / 32;
   constexpr int NST = (D / 8) / (NTH / 64);   // state tiles per wave (D / 8 tiles of the 32-column slice)
@@ -636,7 +720,7 @@ __global__ __launch_bounds__(ScanThreads<D>::value) void kda_bwd_fscan_kernel(Bw
                     : 0.f;
   // chunk n's W, lambda*k and U slice are loaded into registers during
   // chunk n-1's arithmetic
-  typedef Tile<kC, D, NTH> TD;
+  typedef Tile<kC, D, NTH, EF> TD;
   TD tW;
   Tile<kC, 32, NTH> tU;
   // lambda*k, fetched for its transposed store: thread t holds rows 2 rp and
@@ -646,59 +730,81 @@ __global__ __launch_bounds__(ScanThreads<D>::value) void kda_bwd_fscan_kernel(Bw
   constexpr int KCG = NTH / 32;                    // column groups per pass
   constexpr int KPER = (D / 4) / KCG;              // float4 column groups per thread
   static_assert((D / 4) % KCG == 0, "lambda*k column groups");
-  float4 kq[KPER][2];
+  typename WsPiece<EF>::t kq[KPER][2];
   const int rp = t & 31, cg = t >> 5;
   float pgc;   // gamma_C of the chunk, loaded with its operands (every thread; t < D stores it)
   auto fetch = [&](int n) {
     const int64_t ch = (static_cast<int64_t>(b) * a.NT + n) * H + h;
     pgc = a.GCV[ch * D + (t & (D - 1))];
-    tW.fetch(a.WM + ch * kC * D, D, 0);
-    const float* KLp = a.KL + ch * kC * D;
+    tW.fetch(ws_at<EF>(a.WM, ch * kC * D), D, 0);
+    const void* KLp = ws_at<EF>(a.KL, ch * kC * D);
 #pragma unroll
     for (int j = 0; j < KPER; ++j)
 #pragma unroll
-      for (int y = 0; y < 2; ++y)
-        kq[j][y] = *reinterpret_cast<const float4*>(KLp + (2 * rp + y) * D + 4 * (cg + KCG * j));
+      for (int y = 0; y < 2; ++y) {
+        const int i = (2 * rp + y) * D + 4 * (cg + KCG * j);
+        if constexpr (EF == 0) kq[j][y] = *reinterpret_cast<const float4*>(static_cast<const float*>(KLp) + i);
+        else kq[j][y] = *reinterpret_cast<const uint2*>(static_cast<const u16*>(KLp) + i);
+      }
     tU.fetch(a.UM + ch * kC * D, D, c0);
   };
   if (a.NT > 0) fetch(0);
   for (int n = 0; n < a.NT; ++n) {
     const int64_t ch = (static_cast<int64_t>(b) * a.NT + n) * H + h;
-    float* SI = a.SI + ch * D * D;
 #pragma unroll
     for (int q = 0; q < NST; ++q) {
       const int m0 = 16 * rt[q] + 4 * gq, col = 16 * cs[q] + r;
 #pragma unroll
-      for (int i = 0; i < 4; ++i) SI[(m0 + i) * D + c0 + col] = S[q][i];
-      uint2 hh, ll;
-      split2_bf16(S[q][0], S[q][1], hh.x, ll.x);
-      split2_bf16(S[q][2], S[q][3], hh.y, ll.y);
-      *reinterpret_cast<uint2*>(&sSh[col * PW + m0]) = hh;
-      *reinterpret_cast<uint2*>(&sSl[col * PW + m0]) = ll;
+      for (int i = 0; i < 4; ++i) ws_st<EF>(a.SI, ch * D * D + (m0 + i) * D + c0 + col, S[q][i]);
+      if constexpr (WS16) {
+        *reinterpret_cast<uint2*>(&sSh[col * PW + m0]) = pack_f16x4(S[q]);
+      } else {
+        uint2 hh, ll;
+        split2_bf16(S[q][0], S[q][1], hh.x, ll.x);
+        split2_bf16(S[q][2], S[q][3], hh.y, ll.y);
+        *reinterpret_cast<uint2*>(&sSh[col * PW + m0]) = hh;
+        *reinterpret_cast<uint2*>(&sSl[col * PW + m0]) = ll;
+      }
     }
-    // W row-major and lambda*k transposed, as hi / lo planes
+    // W row-major and lambda*k transposed, as hi / lo planes (16-bit
+    // workspace: one fp16 plane each, the stored values as they are)
 #pragma unroll
     for (int p = 0; p < TD::PER; ++p) {
       const int e = t + p * NTH;
       const int row = e / TD::V, c4 = e - row * TD::V;
-      const float4 w = tW.r[p];
-      uint2 hh, ll;
-      split2_bf16(w.x, w.y, hh.x, ll.x);
-      split2_bf16(w.z, w.w, hh.y, ll.y);
-      *reinterpret_cast<uint2*>(&sWh[row * PW + 4 * c4]) = hh;
-      *reinterpret_cast<uint2*>(&sWl[row * PW + 4 * c4]) = ll;
+      if constexpr (WS16) {
+        *reinterpret_cast<uint2*>(&sWh[row * PW + 4 * c4]) = tW.r[p];
+      } else {
+        const float4 w = tW.get(p);
+        uint2 hh, ll;
+        split2_bf16(w.x, w.y, hh.x, ll.x);
+        split2_bf16(w.z, w.w, hh.y, ll.y);
+        *reinterpret_cast<uint2*>(&sWh[row * PW + 4 * c4]) = hh;
+        *reinterpret_cast<uint2*>(&sWl[row * PW + 4 * c4]) = ll;
+      }
     }
 #pragma unroll
     for (int j = 0; j < KPER; ++j) {
       const int ch4 = 4 * (cg + KCG * j);
-      const float k0[4] = {kq[j][0].x, kq[j][0].y, kq[j][0].z, kq[j][0].w};
-      const float k1[4] = {kq[j][1].x, kq[j][1].y, kq[j][1].z, kq[j][1].w};
+      if constexpr (WS16) {
+        // channel ch4 + e of rows 2 rp, 2 rp + 1: the e-th halves of the two
+        // rows' pieces, packed low / high
+        const uint2 w0 = kq[j][0], w1 = kq[j][1];
+        const unsigned pr[4] = {(w0.x & 0xFFFFu) | (w1.x << 16), (w0.x >> 16) | (w1.x & 0xFFFF0000u),
+                                (w0.y & 0xFFFFu) | (w1.y << 16), (w0.y >> 16) | (w1.y & 0xFFFF0000u)};
 #pragma unroll
-      for (int e = 0; e < 4; ++e) {
-        unsigned hh, ll;
-        split2_bf16(k0[e], k1[e], hh, ll);     // rows 2 rp, 2 rp + 1 of channel ch4 + e
-        *reinterpret_cast<unsigned*>(&sKh[(ch4 + e) * PK + 2 * rp]) = hh;
-        *reinterpret_cast<unsigned*>(&sKl[(ch4 + e) * PK + 2 * rp]) = ll;
+        for (int e = 0; e < 4; ++e) *reinterpret_cast<unsigned*>(&sKh[(ch4 + e) * PK + 2 * rp]) = pr[e];
+      } else {
+        const float4 y0 = ws_unpack<EF>(kq[j][0]), y1 = ws_unpack<EF>(kq[j][1]);
+        const float k0[4] = {y0.x, y0.y, y0.z, y0.w};
+        const float k1[4] = {y1.x, y1.y, y1.z, y1.w};
+#pragma unroll
+        for (int e = 0; e < 4; ++e) {
+          unsigned hh, ll;
+          split2_bf16(k0[e], k1[e], hh, ll);     // rows 2 rp, 2 rp + 1 of channel ch4 + e
+          *reinterpret_cast<unsigned*>(&sKh[(ch4 + e) * PK + 2 * rp]) = hh;
+          *reinterpret_cast<unsigned*>(&sKl[(ch4 + e) * PK + 2 * rp]) = ll;
+        }
       }
     }
     tU.template put<kPB>(sU);
@@ -711,24 +817,31 @@ __global__ __launch_bounds__(ScanThreads<D>::value) void kda_bwd_fscan_kernel(Bw
 #pragma unroll
       for (int kb = 0; kb < D / 32; ++kb) {
         const int ka = (16 * mt + r) * PW + 32 * kb + 8 * gq, kbb = (16 * ct + r) * PW + 32 * kb + 8 * gq;
-        const b8 ah = *reinterpret_cast<const b8*>(&sWh[ka]), al = *reinterpret_cast<const b8*>(&sWl[ka]);
-        const b8 bh = *reinterpret_cast<const b8*>(&sSh[kbb]), bl = *reinterpret_cast<const b8*>(&sSl[kbb]);
-        if (kb & 1) acc1 = mma3_bf16(acc1, ah, al, bh, bl);
-        else acc0 = mma3_bf16(acc0, ah, al, bh, bl);
+        f4& acc = (kb & 1) ? acc1 : acc0;
+        if constexpr (WS16) {
+          acc = mma32(acc, *reinterpret_cast<const h8*>(&sWh[ka]), *reinterpret_cast<const h8*>(&sSh[kbb]));
+        } else {
+          const b8 ah = *reinterpret_cast<const b8*>(&sWh[ka]), al = *reinterpret_cast<const b8*>(&sWl[ka]);
+          const b8 bh = *reinterpret_cast<const b8*>(&sSh[kbb]), bl = *reinterpret_cast<const b8*>(&sSl[kbb]);
+          acc = mma3_bf16(acc, ah, al, bh, bl);
+        }
       }
-      float* VT = a.VT + ch * kC * D;
       float v[4];
 #pragma unroll
       for (int i = 0; i < 4; ++i) {
         const int row = 16 * mt + 4 * gq + i, col = 16 * ct + r;
         v[i] = sU[row * kPB + col] - (acc0[i] + acc1[i]);
-        VT[row * D + c0 + col] = v[i];
+        a.VT[ch * kC * D + row * D + c0 + col] = v[i];
       }
-      uint2 hh, ll;
-      split2_bf16(v[0], v[1], hh.x, ll.x);
-      split2_bf16(v[2], v[3], hh.y, ll.y);
-      *reinterpret_cast<uint2*>(&sVh[(16 * ct + r) * PK + 16 * mt + 4 * gq]) = hh;
-      *reinterpret_cast<uint2*>(&sVl[(16 * ct + r) * PK + 16 * mt + 4 * gq]) = ll;
+      if constexpr (WS16) {
+        *reinterpret_cast<uint2*>(&sVh[(16 * ct + r) * PK + 16 * mt + 4 * gq]) = pack_f16x4(f4{v[0], v[1], v[2], v[3]});
+      } else {
+        uint2 hh, ll;
+        split2_bf16(v[0], v[1], hh.x, ll.x);
+        split2_bf16(v[2], v[3], hh.y, ll.y);
+        *reinterpret_cast<uint2*>(&sVh[(16 * ct + r) * PK + 16 * mt + 4 * gq]) = hh;
+        *reinterpret_cast<uint2*>(&sVl[(16 * ct + r) * PK + 16 * mt + 4 * gq]) = ll;
+      }
     }
     __syncthreads();
     // S <- gamma_C S + (lambda k)^T v~
@@ -741,8 +854,11 @@ __global__ __launch_bounds__(ScanThreads<D>::value) void kda_bwd_fscan_kernel(Bw
 #pragma unroll
       for (int q = 0; q < NST; ++q) {
         const int ka = (16 * rt[q] + r) * PK + 32 * kb + 8 * gq, kbb = (16 * cs[q] + r) * PK + 32 * kb + 8 * gq;
-        S[q] = mma3_bf16(S[q], *reinterpret_cast<const b8*>(&sKh[ka]), *reinterpret_cast<const b8*>(&sKl[ka]),
-                         *reinterpret_cast<const b8*>(&sVh[kbb]), *reinterpret_cast<const b8*>(&sVl[kbb]));
+        if constexpr (WS16)
+          S[q] = mma32(S[q], *reinterpret_cast<const h8*>(&sKh[ka]), *reinterpret_cast<const h8*>(&sVh[kbb]));
+        else
+          S[q] = mma3_bf16(S[q], *reinterpret_cast<const b8*>(&sKh[ka]), *reinterpret_cast<const b8*>(&sKl[ka]),
+                           *reinterpret_cast<const b8*>(&sVh[kbb]), *reinterpret_cast<const b8*>(&sVl[kbb]));
       }
     __syncthreads();
   }
@@ -764,8 +880,9 @@ __global__ __launch_bounds__(ScanThreads<D>::value) void kda_bwd_fscan_kernel(Bw
 //   C  dS <- dS - W^T dv~; every wave stages lambda k, Aqk^T, do^T,
 //      (gamma q)^T and gamma_C of the next chunk (read in its A and B) and
 //      loads the one after.
-template <int D, int DO>
+template <int D, int DO, bool WS16>
 __global__ __launch_bounds__(ScanThreads<D>::value) void kda_bwd_rscan_kernel(BwdArgs a) {
+  constexpr int EF = BwdWs<WS16>::F;    // lambda k, Aqk, gamma q, W in
   constexpr int NTH = ScanThreads<D>::value;
   constexpr int NS = D / 32;
   constexpr int NST = (D / 8) / (NTH / 64);
@@ -804,9 +921,9 @@ __global__ __launch_bounds__(ScanThreads<D>::value) void kda_bwd_rscan_kernel(Bw
   // each: a set is reloaded right after it is staged, so every load has a
   // whole chunk step to arrive.  The do slice is held as loaded (raw words),
   // so that no wait falls at its load.
-  Tile<kC, D, NTH> tL;
-  TTile<kC, kScanThreads> tA;   // threads t < kScanThreads
-  TTile<D, NTH> tQ, tW;
+  Tile<kC, D, NTH, EF> tL;
+  TTile<kC, kScanThreads, EF> tA;   // threads t < kScanThreads
+  TTile<D, NTH, EF> tQ, tW;
   const bool a_thread = t < kScanThreads;
   float pgc;   // gamma_C of the chunk (every thread; t < D stages it)
   // do^T of the slice, spread over every thread: thread t holds rows 2 rp,
@@ -827,9 +944,9 @@ __global__ __launch_bounds__(ScanThreads<D>::value) void kda_bwd_rscan_kernel(Bw
   auto fetch_a = [&](int n) {   // lambda k, Aqk, gamma q, gamma_C and do of chunk n
     const int u = b * a.NT + n;
     const int64_t ch = chead(n);
-    tL.fetch(a.KL + ch * kC * D, D, 0);
-    if (a_thread) tA.fetch(a.AQ + ch * kC * kC, kC, 0);
-    tQ.fetch(a.QG + ch * kC * D, D, 0);
+    tL.fetch(ws_at<EF>(a.KL, ch * kC * D), D, 0);
+    if (a_thread) tA.fetch(ws_at<EF>(a.AQ, ch * kC * kC), kC, 0);
+    tQ.fetch(ws_at<EF>(a.QG, ch * kC * D), D, 0);
     pgc = a.GCV[ch * D + (t & (D - 1))];
     const ChunkRows crn = chunk_rows(a, u);
 #pragma unroll
@@ -860,7 +977,7 @@ __global__ __launch_bounds__(ScanThreads<D>::value) void kda_bwd_rscan_kernel(Bw
   };
   if (a.NT > 0) {
     fetch_a(a.NT - 1);
-    tW.fetch(a.WM + chead(a.NT - 1) * kC * D, D, 0);
+    tW.fetch(ws_at<EF>(a.WM, chead(a.NT - 1) * kC * D), D, 0);
     put_a(a.NT - 1);
     if (a.NT > 1) fetch_a(a.NT - 2);
     __syncthreads();
@@ -868,12 +985,11 @@ __global__ __launch_bounds__(ScanThreads<D>::value) void kda_bwd_rscan_kernel(Bw
   for (int n = a.NT - 1; n >= 0; --n) {
     const int64_t ch = chead(n);
     // ---- A: store and stage dS; dS <- gamma_C dS + (gamma q)^T do
-    float* DS = a.DS + ch * D * D;
 #pragma unroll
     for (int q = 0; q < NST; ++q) {
       const int m0 = 16 * rt[q] + 4 * gq, col = 16 * cs[q] + r;
 #pragma unroll
-      for (int i = 0; i < 4; ++i) DS[(m0 + i) * D + c0 + col] = dS[q][i];
+      for (int i = 0; i < 4; ++i) a.DS[ch * D * D + (m0 + i) * D + c0 + col] = dS[q][i];
       uint2 hh, ll;
       split2_bf16(dS[q][0], dS[q][1], hh.x, ll.x);
       split2_bf16(dS[q][2], dS[q][3], hh.y, ll.y);
@@ -922,7 +1038,7 @@ __global__ __launch_bounds__(ScanThreads<D>::value) void kda_bwd_rscan_kernel(Bw
       *reinterpret_cast<uint2*>(&sVl[(16 * ct + r) * PK + 16 * mt + 4 * gq]) = ll;
     }
     tW.template put_hl<PK>(sWh, sWl);
-    if (n > 0) tW.fetch(a.WM + chead(n - 1) * kC * D, D, 0);
+    if (n > 0) tW.fetch(ws_at<EF>(a.WM, chead(n - 1) * kC * D), D, 0);
     __syncthreads();
     // ---- C: dS <- dS - W^T dv~; the next chunk's lambda k, Aqk^T, do^T,
     // (gamma q)^T and gamma_C staged while the products run
@@ -1036,6 +1152,7 @@ __global__ __launch_bounds__(kChunkThreads) void kda_bwd_chunk_kernel(BwdArgs a)
 #pragma unroll
   for (int q = 0; q < NDT; ++q) dzp[q] = 0.f;
   float dgc = 0.f;   // thread t < D: sum_n S[t][n] dS'[t][n]
+  constexpr int EF = BwdWs<DTQ != 0>::F;    // S_in, T, W
 
   // Phase 1's dk and dG terms reach phase 2 (same thread, same positions)
   // through LDS past phase 2's buffers, not through dk and dg in memory.
@@ -1048,7 +1165,7 @@ __global__ __launch_bounds__(kChunkThreads) void kda_bwd_chunk_kernel(BwdArgs a)
   // lo hi, about 2^-16 of each product dropped); dW accumulates +dv~ S^T and
   // is negated where phase 2 takes it.
   f4 dW[NDT];
-  TTile<kC, NTH> tT;         // phase 2's T and dv~, loaded during phase 1's last pass
+  TTile<kC, NTH, EF> tT;     // phase 2's T and dv~, loaded during phase 1's last pass
   TTile<D, NTH> tY;
   {
     f4 dY[NDT], dgq[NDT];
@@ -1070,12 +1187,13 @@ __global__ __launch_bounds__(kChunkThreads) void kda_bwd_chunk_kernel(BwdArgs a)
     __bf16* const sDl = sDh + D * PB;
     // a pass's operands are loaded during the previous pass's products
     Tile<kC, HW, NTH> pV, pDv;
-    Tile<D, HW, NTH> pS, pDS;
+    Tile<D, HW, NTH, EF> pS;
+    Tile<D, HW, NTH> pDS;
     InTile<DO, D, HW, NTH> pDo;
     auto fetch_pass = [&](int n0) {
       pV.fetch(a.VT + ch * kC * D, D, n0);
       pDv.fetch(a.DVT + ch * kC * D, D, n0);
-      pS.fetch(a.SI + ch * D * D, D, n0);
+      pS.fetch(ws_at<EF>(a.SI, ch * D * D), D, n0);
       pDS.fetch(a.DS + ch * D * D, D, n0);
       pDo.fetch(a.dout, cr.row0, cr.len, H, h, n0);
     };
@@ -1089,7 +1207,7 @@ __global__ __launch_bounds__(kChunkThreads) void kda_bwd_chunk_kernel(BwdArgs a)
       __syncthreads();
       if (hp + 1 < NH) fetch_pass(HW * (hp + 1));
       else {   // phase 2's operands
-        tT.fetch(a.TM + ch * kC * kC, kC, 0);
+        tT.fetch(ws_at<EF>(a.TM, ch * kC * kC), kC, 0);
         tY.fetch(a.DVT + ch * kC * D, D, 0);
       }
 #pragma unroll
@@ -1154,7 +1272,8 @@ __global__ __launch_bounds__(kChunkThreads) void kda_bwd_chunk_kernel(BwdArgs a)
   // contiguous; T[c][m] is zero for c < m, so row tile mt starts at the
   // K block holding row 16 mt.
   f4 Yw[NDT], Yu[NDT];
-  Tile<kC, D, NTH> tW3, tU3;
+  Tile<kC, D, NTH, EF> tW3;
+  Tile<kC, D, NTH> tU3;
   {
     constexpr int PB = kC + 8;
     static_assert((2 * kC + 4 * D) * PB / 2 <= ACC0, "phase 2 planes end below sAcc");
@@ -1176,7 +1295,7 @@ __global__ __launch_bounds__(kChunkThreads) void kda_bwd_chunk_kernel(BwdArgs a)
     tT.template put_hl<PB>(sTh, sTl);
     tY.template put_hl<PB>(sYh, sYl);
     __syncthreads();
-    tW3.fetch(a.WM + ch * kC * D, D, 0);     // phase 3's operands, during the products
+    tW3.fetch(ws_at<EF>(a.WM, ch * kC * D), D, 0);     // phase 3's operands, during the products
     tU3.fetch(a.UM + ch * kC * D, D, 0);
 #pragma unroll
     for (int q = 0; q < NDT; ++q)
@@ -1332,7 +1451,9 @@ __global__ __launch_bounds__(kChunkThreads) void kda_bwd_chunk_kernel(BwdArgs a)
   // factor the decay at the row tile's first row a, 2^(G_c - G_a) 2^(G_a - G_i),
   // both <= 1, and run on the matrix cores: (16 x 16 block) x (k_i 2^(G_a - G_i))
   // for the row side, (block)^T x (q_c 2^(G_c - G_a)) for the column side.
-  // Diagonal tiles take 2^-|G_c - G_i| per element.  Wave wv < D/16 owns column tile
+  // Diagonal tiles are anchored the same way (their key factors >= 1, bounded
+  // by the tile's decay) unless the tile decays past 2^-kDiagAnchorLog2 in a
+  // column of the wave; those take 2^-|G_c - G_i| per element.  Wave wv < D/16 owns column tile
   // wv: lane (r, gq) rows 4 gq + e of every row tile, column 16 wv + r; each
   // position gets one read-modify-write.
   constexpr int NCT = D / 16;
@@ -1384,9 +1505,9 @@ __global__ __launch_bounds__(kChunkThreads) void kda_bwd_chunk_kernel(BwdArgs a)
           ok[e] = gk_[o];
         }
       }
-      if (mine && R > 0) {
-        const float ga = sG[a0 * P + d];
-        float xq[4], xk[4];      // q_c 2^(G_c - G_a), beta_c k_c 2^(G_c - G_a): rows a0 + 4 k + gq
+      const float ga = sG[a0 * P + d];
+      float xq[4], xk[4];      // q_c 2^(G_c - G_a), beta_c k_c 2^(G_c - G_a): rows a0 + 4 k + gq
+      if (mine) {
 #pragma unroll
         for (int k = 0; k < 4; ++k) {
           const int c = a0 + 4 * k + gq;
@@ -1394,6 +1515,8 @@ __global__ __launch_bounds__(kChunkThreads) void kda_bwd_chunk_kernel(BwdArgs a)
           xq[k] = sQ[c * P + d] * fr;
           xk[k] = sK[c * P + d] * sB[c] * fr;
         }
+      }
+      if (mine && R > 0) {
 #pragma unroll
         for (int sk = 0; sk < R; ++sk) {
           f4 cS = {0.f, 0.f, 0.f, 0.f};
@@ -1412,17 +1535,40 @@ __global__ __launch_bounds__(kChunkThreads) void kda_bwd_chunk_kernel(BwdArgs a)
         }
       }
       if (mine) {
-        // With G non-increasing (g <= 0), the pair (c, a0 + y) of the row
-        // side (y <= x) decays by 2^(G_c - G_y) and the pair (a0 + y, c) of
-        // the column side (y >= x) by 2^(G_y - G_c): both are 2^-|G_c - G_y|,
-        // and the masked cotangents zero the side a given y does not belong to.
-        // Row y's G, k, q, beta are read once for the lane's four rows c.
         float gc[4], rA[4], rK[4], cS[4];
 #pragma unroll
         for (int e = 0; e < 4; ++e) {
           gc[e] = sG[(a0 + 4 * gq + e) * P + d];
           rA[e] = rK[e] = cS[e] = 0.f;
         }
+        // The diagonal tile on the matrix cores, anchored at its first row a
+        // like the off-diagonal ones: row side (block) x (k_y 2^(G_a - G_y)),
+        // column side (block)^T x (q_c 2^(G_c - G_a)), times 2^(G_c - G_a) and
+        // 2^(G_a - G_i) afterwards.  Key factors here are >= 1, up to the
+        // tile's decay in the column; the masked cotangents zero every pair
+        // whose factor would exceed 1 overall.  A tile that decays by more
+        // than 2^-kDiagAnchorLog2 in one of the wave's columns (the factors
+        // would leave fp32 headroom for the cotangents) takes the per-element
+        // form below.
+        if (!__any(ga - sG[(a0 + 15) * P + d] > kDiagAnchorLog2)) {
+          f4 cd = {0.f, 0.f, 0.f, 0.f};
+#pragma unroll
+          for (int k = 0; k < 4; ++k) {
+            const int y = a0 + 4 * k + gq;
+            const float kb = sK[y * P + d] * ex2(ga - sG[y * P + d]);   // k_y 2^(G_a - G_y)
+            accA = mfma4(sDA[(a0 + r16) * PC + y], kb, accA);
+            accK = mfma4(sDL[(a0 + r16) * PC + y], kb, accK);
+            cd = mfma4(sDA[y * PC + a0 + r16], xq[k], cd);
+            cd = mfma4(sDL[y * PC + a0 + r16], xk[k], cd);
+          }
+#pragma unroll
+          for (int e = 0; e < 4; ++e) cS[e] = cd[e] * ex2(ga - gc[e]);
+        } else {
+        // With G non-increasing (g <= 0), the pair (c, a0 + y) of the row
+        // side (y <= x) decays by 2^(G_c - G_y) and the pair (a0 + y, c) of
+        // the column side (y >= x) by 2^(G_y - G_c): both are 2^-|G_c - G_y|,
+        // and the masked cotangents zero the side a given y does not belong to.
+        // Row y's G, k, q, beta are read once for the lane's four rows c.
 #pragma unroll 1
         for (int y4 = 0; y4 < 16; y4 += 4) {
           f4 rowA[4], rowL[4];   // dA[c][a0 + y4 .. + 3], dL likewise, for the lane's rows c
@@ -1449,16 +1595,15 @@ __global__ __launch_bounds__(kChunkThreads) void kda_bwd_chunk_kernel(BwdArgs a)
             }
           }
         }
+        }
         float gn[4];   // this tile's dG (zero on pad rows)
 #pragma unroll
         for (int e = 0; e < 4; ++e) {
           const int c = a0 + 4 * gq + e;
           const float kc = sK[c * P + d], qc = sQ[c * P + d], bc = sB[c];
-          if (R > 0) {
-            const float f = ex2(gc[e] - sG[a0 * P + d]);
-            rA[e] = fmaf(accA[e], f, rA[e]);
-            rK[e] = fmaf(accK[e], f, rK[e]);
-          }
+          const float f = ex2(gc[e] - ga);   // accA, accK: every tile pair but a per-element diagonal
+          rA[e] = fmaf(accA[e], f, rA[e]);
+          rK[e] = fmaf(accK[e], f, rK[e]);
           if (R < 3) cS[e] += colS[R < 3 ? R : 0][e];
           dbq[R][e] = rK[e] * kc;
           gn[e] = (c < cr.len) ? oG[e] + rA[e] * qc + rK[e] * kc * bc - cS[e] * kc : 0.f;
@@ -1536,10 +1681,10 @@ hipError_t launch_bwd_t(const BwdArgs& a, hipStream_t s) {
   hipError_t e = hipGetLastError();
   if (e != hipSuccess) return e;
   const int scan_grid = (chains + 7) / 8 * 8 * (D / 32);
-  hipLaunchKernelGGL((kda_bwd_fscan_kernel<D>), dim3(scan_grid), dim3(ScanThreads<D>::value), 0, s, a);
+  hipLaunchKernelGGL((kda_bwd_fscan_kernel<D, (DTQ != 0)>), dim3(scan_grid), dim3(ScanThreads<D>::value), 0, s, a);
   e = hipGetLastError();
   if (e != hipSuccess) return e;
-  hipLaunchKernelGGL((kda_bwd_rscan_kernel<D, DO>), dim3(scan_grid), dim3(ScanThreads<D>::value), 0, s, a);
+  hipLaunchKernelGGL((kda_bwd_rscan_kernel<D, DO, (DTQ != 0)>), dim3(scan_grid), dim3(ScanThreads<D>::value), 0, s, a);
   e = hipGetLastError();
   if (e != hipSuccess) return e;
   hipLaunchKernelGGL((kda_bwd_chunk_kernel<D, DTQ, DTG, DO>), dim3(chunk_heads), dim3(kChunkThreads), 0, s, a);

@@ -9,7 +9,7 @@ kernels see the same per-chain operands and run the same arithmetic, so the
 comparison is bit for bit.  One element per case is also checked against the
 oracle (``cc_scan`` / ``cc_scan_bwd``) at the unbatched seam's tolerances: the
 forward's bf16 bar (relative L2 <= 1e-3, max-abs <= 2e-2), the backward's
-(relative L2 <= 4e-3 for the bf16 dq, dk, dv; 1e-4 for the fp32 cotangents).
+(relative L2 <= 4e-3 for the bf16 dq, dk, dv; 1e-3 for the fp32 cotangents).
 """
 
 from __future__ import annotations
@@ -100,7 +100,7 @@ def test_batched_backward_equals_per_element_calls(cuda, B, T, H, d, chunk):
     for name, got, r in zip(("dq", "dk", "dv"), grads[:3], ref[:3]):
         _close(name, got[b], r, 4e-3, 1e-2)
     for name, got, r in zip(("dalpha", "dbeta32", "dS_in"), grads[3:], ref[3:]):
-        _close(name, got[b], r, 1e-4, 1e-4)
+        _close(name, got[b], r, 1e-3, 2e-3)
 
 
 def test_batched_autograd_equals_the_backward_rule(cuda):

@@ -3,11 +3,12 @@
 oracle's ``cc_scan_bwd`` (pinned by finite differences of the seam's forward in
 tests/test_oracle_bwd.py), and the differentiable ``cc_scan``.
 
-The HIP backward computes in fp32 from the bf16 q, k, v the seam takes; the
-fp32 cotangents (dalpha, dbeta32, dS_in) are held to the chunked backward's
-bar (relative L2 <= 1e-4, max-abs <= 1e-4 x max(1, max|reference|)); dq, dk,
-dv come back in the primal dtype, bf16, so their bar adds bf16's rounding
-(relative L2 <= 4e-3, max-abs <= 1e-2 x max(1, max|reference|)).
+The HIP backward runs on the bf16 q, k, v the seam takes, with its 16-bit
+workspace (fp16 forward-side arrays, tests/test_gpu_bwd.py); the fp32
+cotangents (dalpha, dbeta32, dS_in) are held to the chunked backward's bar for
+16-bit inputs (relative L2 <= 1e-3, max-abs <= 2e-3 x max(1, max|reference|));
+dq, dk, dv come back in the primal dtype, bf16, so their bar adds bf16's
+rounding (relative L2 <= 4e-3, max-abs <= 1e-2 x max(1, max|reference|)).
 """
 
 from __future__ import annotations
@@ -64,7 +65,7 @@ def test_cc_scan_bwd_matches_oracle(cuda, T, H, d, chunk):
     for name, got, r in zip(("dq", "dk", "dv"), out[:3], ref[:3]):
         _close(name, got, r, 4e-3, 1e-2)
     for name, got, r in zip(("dalpha", "dbeta32", "dS_in"), out[3:], ref[3:]):
-        _close(name, got, r, 1e-4, 1e-4)
+        _close(name, got, r, 1e-3, 2e-3)
 
 
 def test_cc_scan_autograd_equals_the_backward_rule(cuda):
@@ -132,15 +133,15 @@ def _check_heads(tag, got, ref_fn, heads, H, d):
     T = got[0].shape[0]
     n = len(heads)
     for name, g, r, width, rt, at in (("dq", got[0], ref[0], d, 4e-3, 1e-2), ("dk", got[1], ref[1], d, 4e-3, 1e-2),
-                                      ("dv", got[2], ref[2], d, 4e-3, 1e-2), ("dalpha", got[3], ref[3], d, 1e-4, 1e-4),
-                                      ("dbeta32", got[4], ref[4], 32, 1e-4, 1e-4)):
+                                      ("dv", got[2], ref[2], d, 4e-3, 1e-2), ("dalpha", got[3], ref[3], d, 1e-3, 2e-3),
+                                      ("dbeta32", got[4], ref[4], 32, 1e-3, 2e-3)):
         gh = g[:, cols if width == d else cols32].double().cpu().numpy().reshape(T, n, width)
         rh = r.reshape(T, n, width)
         for j, h in enumerate(heads):
             _close(f"{tag} {name} head {h}", torch.from_numpy(gh[:, j]), rh[:, j], rt, at)
     gS = got[5][heads].double().cpu().numpy()
     for j, h in enumerate(heads):
-        _close(f"{tag} dS_in head {h}", torch.from_numpy(gS[j]), ref[5][j], 1e-4, 1e-4)
+        _close(f"{tag} dS_in head {h}", torch.from_numpy(gS[j]), ref[5][j], 1e-3, 2e-3)
 
 
 def test_cc_scan_bwd_at_the_bench_shape(cuda):

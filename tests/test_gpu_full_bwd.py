@@ -7,9 +7,10 @@ length (chains are independent, so a sample is exact for its chains).  The
 sample covers every batch row of the heads it takes, so the conv-tap
 gradients (summed over the batch) of those heads' channels are checked too.
 A small case with B*H = 12 chains exercises the scans' chain -> workgroup
-mapping beyond the first XCD slot.  Bars as tests/test_gpu_bwd.py (chunked:
-relative L2 <= 1e-4, max-abs <= 1e-4 x max|ref|) and
-tests/test_gpu_layer_bwd.py (layer with bf16 projections: 1e-2 / 5e-2).
+mapping beyond the first XCD slot.  Bars as tests/test_gpu_bwd.py (chunked,
+16-bit inputs: relative L2 <= 1e-3, max-abs <= 2e-3 x max|ref| against the
+float64 oracle) and tests/test_gpu_layer_bwd.py (layer with bf16
+projections: 1e-2 / 5e-2).
 """
 
 from __future__ import annotations
@@ -24,6 +25,7 @@ from tests.kda_testutil import make_inputs_device
 pytestmark = pytest.mark.gpu
 
 NAMES = ("dq", "dk", "dv", "dg", "dbeta", "dh0")
+REL16, ABS16 = 1e-3, 2e-3   # chunked backward, 16-bit inputs (tests/test_gpu_bwd.py)
 
 
 def _close(name, got, ref, rel_tol, abs_tol):
@@ -56,7 +58,7 @@ def test_bwd_many_chains(cuda, d):
     ref = K.chunk_bwd(x["q"], x["k"], x["v"], x["g"], x["beta"], do.astype(np.float64),
                       dht=dht.astype(np.float64), h0=x["h0"], chunk=64)
     for n, got, r in zip(NAMES, out, ref):
-        _close(n, got, r, 1e-4, 1e-4)
+        _close(n, got, r, REL16, ABS16)
 
 
 def test_bwd_config1_full(cuda):
@@ -79,7 +81,7 @@ def test_bwd_config1_full(cuda):
                       dht=dht[:, heads].double().cpu().numpy(), chunk=64)
     for n, got, r in zip(NAMES, out, ref):
         sub = got[:, heads] if n == "dh0" else got[:, :, heads]
-        _close(n, sub, r, 1e-4, 1e-4)
+        _close(n, sub, r, REL16, ABS16)
 
 
 def test_layer_bwd_config1_full(cuda):

@@ -5,8 +5,9 @@ diagonal exponentials see products near the fp32 range's ends).
 
 Same bars as the ordinary cases: forward o and final state rel-L2 <= 1e-3 and
 max-abs <= 2e-2 (bf16 inputs), <= 1e-5 (fp32, exact mode); backward every
-gradient rel-L2 <= 1e-4 and max-abs <= 1e-4 x max|reference| against the
-float64 oracle on the same inputs.
+gradient rel-L2 <= 1e-4 and max-abs <= 1e-4 x max|reference| (fp32 inputs),
+<= 1e-3 and <= 2e-3 x max|reference| (bf16 inputs: the 16-bit workspace of
+tests/test_gpu_bwd.py) against the float64 oracle on the same inputs.
 """
 
 from __future__ import annotations
@@ -105,4 +106,5 @@ def test_backward_strong_decay(cuda, prec, d):
         assert np.all(np.isfinite(a)), name
         rel, mx = K.rel_l2(a, b), K.max_abs(a, b)
         print(f"  {name}: rel_l2={rel:.2e} max_abs={mx:.2e}", flush=True)
-        assert rel <= 1e-4 and mx <= 1e-4 * max(1.0, float(np.abs(b).max())), (name, rel, mx)
+        rt, at = (1e-4, 1e-4) if prec == "fp32" else (1e-3, 2e-3)
+        assert rel <= rt and mx <= at * max(1.0, float(np.abs(b).max())), (name, rel, mx)
