@@ -572,9 +572,10 @@ hipError_t launch_cc_finish(const CcFinishArgs& a, hipStream_t s) {
 // ----------------------------------------------------------------------------
 // exported entry points
 // ----------------------------------------------------------------------------
-// Backward workspace: fp32 arrays per chunk-head (see kda_internal.h: BwdArgs).
+// Backward workspace: arrays per chunk-head (see kda_internal.h: BwdArgs),
+// sized for fp32; the fragment arrays FL, FA, FQ, FW (fp16) serve 16-bit inputs.
 struct BwdLayout {
-  size_t GL, QG, KL, GCV, AQ, TM, WM, UM, SI, VT, DS, DVT, total;
+  size_t GL, QG, KL, GCV, AQ, TM, WM, UM, SI, VT, DS, DVT, FL, FA, FQ, FW, total;
 };
 
 BwdLayout bwd_layout(int B, int T, int H, int d) {
@@ -595,6 +596,10 @@ BwdLayout bwd_layout(int B, int T, int H, int d) {
   L.VT = take(cd);
   L.DS = take(dd);
   L.DVT = take(cd);
+  L.FL = take(ch * 4 * (d / 32) * 1024);
+  L.FA = take(ch * 6 * 1024);
+  L.FQ = take(ch * (d / 16) * 2 * 1024);
+  L.FW = take(ch * (d / 16) * 2 * 1024);
   L.total = off;
   return L;
 }
@@ -910,6 +915,10 @@ int kda_chunk_bwd(hipStream_t stream, const void* q, const void* k, const void* 
   a.VT = reinterpret_cast<float*>(ws + L.VT);
   a.DS = reinterpret_cast<float*>(ws + L.DS);
   a.DVT = reinterpret_cast<float*>(ws + L.DVT);
+  a.FL = ws + L.FL;
+  a.FA = ws + L.FA;
+  a.FQ = ws + L.FQ;
+  a.FW = ws + L.FW;
   const hipError_t e = kda::launch_bwd(a, dk_dim, in_dtype, dout_dtype, stream);
   if (e != hipSuccess) return hip_fail(e, "backward kernel launch");
   return KDA_OK;

@@ -327,6 +327,11 @@ __device__ __forceinline__ f4 mfma4(float a, float b, f4 c) {
   return __builtin_amdgcn_mfma_f32_16x16x4f32(a, b, c, 0, 0, 0);
 }
 
+// Index of the stored Aqk^T A fragment (key tile it, K step kb over the query
+// rows): (0,0) (0,1) (1,0) (1,1) (2,1) (3,1); (2,0) and (3,0) are zero and
+// not stored.
+__device__ __forceinline__ int fa_frag(int it, int kb) { return (it < 2) ? 2 * it + kb : it + 2; }
+
 // The chunk's channels are taken in halves of 64 (d = 128) so the shared
 // memory fits two workgroups per CU: the scores accumulate over the halves in
 // registers, T = (I+L)^-1 is built once, and W, U are formed per half of
@@ -425,8 +430,27 @@ __global__ __launch_bounds__(kPrepThreads, 4) void kda_bwd_prep_kernel(BwdArgs a
         const float4 kl = make_float4(ex2(gz.x - gl.x) * kv.x, ex2(gz.y - gl.y) * kv.y, ex2(gz.z - gl.z) * kv.z,
                                       ex2(gz.w - gl.w) * kv.w);
         *reinterpret_cast<float4*>(&GL[c * D + d]) = gl;
-        ws_st4<EF>(a.QG, base + c * D + d, qg);
+        if constexpr (EF == 0) ws_st4<EF>(a.QG, base + c * D + d, qg);
         ws_st4<EF>(a.KL, base + c * D + d, kl);
+      }
+      if constexpr (EF != 0) {
+        // the reverse scan's A fragments of this half's channels, one lane
+        // fragment per thread each (the slot order of kda_internal.h)
+        static_assert(NTH == 512 && HD == 64, "one (gamma q)^T and one lambda k lane fragment per thread");
+        const int ln = t & 63, rr = ln & 15, g4 = ln >> 4, hi = (t >> 6) & 1, tt = t >> 7;
+        h8 vq, vl;
+#pragma unroll
+        for (int e = 0; e < 8; ++e) {
+          // (gamma q)^T: channel tile tt of the half, K step hi over the rows
+          const int c = 32 * hi + 4 * g4 + (e & 3) + 16 * (e >> 2), dq = 16 * tt + rr;
+          vq[e] = static_cast<_Float16>(ex2(sG[c * P + dq]) * sQ[c * P + dq]);
+          // lambda k: row tile tt, K step hi over the half's channels
+          const int row = 16 * tt + rr, dl = 32 * hi + 4 * g4 + (e & 3) + 16 * (e >> 2);
+          vl[e] = static_cast<_Float16>(ex2(sG[(kC - 1) * P + dl] - sG[row * P + dl]) * sK[row * P + dl]);
+        }
+        const int dt = (c0 >> 4) + tt, j = (c0 >> 5) + hi;
+        *reinterpret_cast<h8*>(static_cast<_Float16*>(a.FQ) + (((ch * (D / 16) + dt) * 2 + hi) * 64 + ln) * 8) = vq;
+        *reinterpret_cast<h8*>(static_cast<_Float16*>(a.FL) + (((ch * 4 + tt) * (D / 32) + j) * 64 + ln) * 8) = vl;
       }
       if (t < HD) a.GCV[ch * D + c0 + t] = ex2(sG[(kC - 1) * P + t]);
     }
@@ -473,16 +497,22 @@ __global__ __launch_bounds__(kPrepThreads, 4) void kda_bwd_prep_kernel(BwdArgs a
 #pragma unroll
     for (int e = 0; e < 4; ++e) {
       const int c = a0 + 4 * gq + e;
-      ws_st<EF>(a.AQ, aq0 + c * kC + i, accA[e]);
+      if constexpr (EF == 0) ws_st<EF>(a.AQ, aq0 + c * kC + i, accA[e]);
       sL[c * PC + i] = accL[e] * sB[c];
     }
+    if constexpr (EF != 0)   // Aqk^T fragment (key tile sk_off, K step R_off / 2), half R_off % 2
+      *reinterpret_cast<uint2*>(static_cast<u16*>(a.FA) + ((ch * 6 + fa_frag(sk_off, R_off >> 1)) * 64 + l) * 8 +
+                                4 * (R_off & 1)) = pack_f16x4(accA);
   }
 #pragma unroll
   for (int j = 0; j < 2; ++j) {
     const int p = t + NTH * j;
     const int R = p >> 8, rc = (p >> 4) & 15, ri = p & 15;
     const int c = 16 * R + rc, i = 16 * R + ri;
-    ws_st<EF>(a.AQ, aq0 + c * kC + i, (ri <= rc) ? dA[j] : 0.f);
+    if constexpr (EF == 0) ws_st<EF>(a.AQ, aq0 + c * kC + i, (ri <= rc) ? dA[j] : 0.f);
+    else   // diagonal tile R: Aqk^T fragment (R, R / 2), lane ri + 16 (rc / 4), element 4 (R % 2) + rc % 4
+      static_cast<_Float16*>(a.FA)[((ch * 6 + fa_frag(R, R >> 1)) * 64 + ri + 16 * (rc >> 2)) * 8 + 4 * (R & 1) +
+                                   (rc & 3)] = static_cast<_Float16>((ri <= rc) ? dA[j] : 0.f);
     sL[c * PC + i] = (ri < rc) ? dL[j] * sB[c] : 0.f;
   }
   // blocks above the diagonal: zero
@@ -491,8 +521,16 @@ __global__ __launch_bounds__(kPrepThreads, 4) void kda_bwd_prep_kernel(BwdArgs a
     const int R = (blk < 3) ? 0 : (blk < 5) ? 1 : 2;             // (0,1) (0,2) (0,3) (1,2) (1,3) (2,3)
     const int sk = (blk < 3) ? blk + 1 : (blk < 5) ? blk - 1 : 3;
     const int c = 16 * R + rc, i = 16 * sk + ri;
-    ws_st<EF>(a.AQ, aq0 + c * kC + i, 0.f);
+    if constexpr (EF == 0) ws_st<EF>(a.AQ, aq0 + c * kC + i, 0.f);
     sL[c * PC + i] = 0.f;
+  }
+  if constexpr (EF != 0) {
+    // the zero halves of the stored Aqk^T fragments: key tile 1 against row
+    // tile 0, key tile 3 against row tile 2
+    if (t < 128)
+      *reinterpret_cast<uint2*>(static_cast<u16*>(a.FA) +
+                                ((ch * 6 + (t < 64 ? fa_frag(1, 0) : fa_frag(3, 1))) * 64 + (t & 63)) * 8) =
+          uint2{0u, 0u};
   }
   __syncthreads();
 
@@ -556,6 +594,15 @@ __global__ __launch_bounds__(kPrepThreads, 4) void kda_bwd_prep_kernel(BwdArgs a
         ws_st<EF>(a.WM, wu0 + o, accW[q][e]);
         a.UM[wu0 + o] = accU[q][e];
       }
+    if constexpr (EF != 0) {
+      // W^T fragments: channel tile of column tile q, K step mt / 2, half mt % 2
+#pragma unroll
+      for (int q = 0; q < NDT; ++q) {
+        const int dt = (c0 >> 4) + dg * NDT + q;
+        *reinterpret_cast<uint2*>(static_cast<u16*>(a.FW) + (((ch * (D / 16) + dt) * 2 + (mt >> 1)) * 64 + l) * 8 +
+                                  4 * (mt & 1)) = pack_f16x4(accW[q]);
+      }
+    }
   }
 }
 
@@ -1062,6 +1109,355 @@ __global__ __launch_bounds__(ScanThreads<D>::value) void kda_bwd_rscan_kernel(Bw
 #pragma unroll
       for (int i = 0; i < 4; ++i)
         a.dh0[(static_cast<int64_t>(chain) * D + 16 * rt[q] + 4 * gq + i) * D + c0 + 16 * cs[q] + r] = dS[q][i];
+  }
+}
+
+// ---------------------------------------------------------------------------
+// Reverse scan for 16-bit inputs: one workgroup per (chain, 32-column slice),
+// two compute waves (one 16-column value tile each) and four producer waves,
+// as the forward's state kernel.  Each compute wave owns its tile's columns of
+// dS for every channel, so a chunk step needs no exchange between waves:
+//   dv~ = (lambda k) dS' + Aqk^T do,  dS <- gamma_C dS + (gamma q)^T do - W^T dv~
+// with the forward-side operands (lambda k, Aqk^T, (gamma q)^T, W^T) as the
+// prep kernel's fp16 A fragments, staged by the producers into one of two LDS
+// buffers two chunks ahead, and the cotangent operands (dS', do, dv~) as B
+// fragments formed in registers.  A cotangent's scale is the caller's, so
+// each B column is scaled by a power of two that brings its largest element
+// to [2^14, 2^15) and split into fp16 hi + lo (about 22 significant bits,
+// fp16's range no limit); each product is two fp16 MFMAs per K step, and the
+// column's scale is taken off the accumulator (every lane's D column is its
+// own B column).  One barrier per chunk step.
+// ---------------------------------------------------------------------------
+constexpr int kRsProducers = 4;
+
+template <int D>
+struct RsLayout {
+  static constexpr int NFL = 4 * (D / 32);         // lambda k fragments (row tile, K step over channels)
+  static constexpr int NFA = 6;                    // Aqk^T fragments
+  static constexpr int NFQ = 2 * (D / 16);         // (gamma q)^T fragments (channel tile, K step over rows)
+  static constexpr int OFF_A = NFL;                // in 1 KiB fragments
+  static constexpr int OFF_Q = OFF_A + NFA;
+  static constexpr int OFF_W = OFF_Q + NFQ;
+  static constexpr int NF = OFF_W + NFQ;           // fragments per chunk
+  static constexpr int OFF_GC = NF * 1024;         // gamma_C, D floats
+  static constexpr int OFF_DO = OFF_GC + 4 * D;    // do B fragments [K step][value tile][64][8] fp32
+  static constexpr int BYTES = OFF_DO + 2 * 2 * 64 * 8 * 4;
+};
+
+// One chunk's share of producer P: every kRsProducers-th fragment, two
+// 16-byte pieces of the do rows, and (last producer) gamma_C.
+template <int D, int P>
+struct RsRegs {
+  static constexpr int NFP = (RsLayout<D>::NF - P + kRsProducers - 1) / kRsProducers;
+  u32x4 f[NFP];
+  uint4 d[2];
+  u32x4 g;
+};
+
+template <int D, int DO, int P>
+__device__ __forceinline__ void rs_load(const BwdArgs& a, int b, int n, int h, int c0, int l, RsRegs<D, P>& R) {
+  typedef RsLayout<D> LY;
+  const int H = a.H;
+  const int64_t ch = (static_cast<int64_t>(b) * a.NT + n) * H + h;
+#pragma unroll
+  for (int k = 0; k < RsRegs<D, P>::NFP; ++k) {
+    const int f = P + kRsProducers * k;
+    const _Float16* src;
+    if (f < LY::OFF_A) src = static_cast<const _Float16*>(a.FL) + (ch * LY::NFL + f) * 512;
+    else if (f < LY::OFF_Q) src = static_cast<const _Float16*>(a.FA) + (ch * LY::NFA + (f - LY::OFF_A)) * 512;
+    else if (f < LY::OFF_W) src = static_cast<const _Float16*>(a.FQ) + (ch * LY::NFQ + (f - LY::OFF_Q)) * 512;
+    else src = static_cast<const _Float16*>(a.FW) + (ch * LY::NFQ + (f - LY::OFF_W)) * 512;
+    R.f[k] = *reinterpret_cast<const u32x4*>(src + l * 8);
+  }
+  // do rows of the slice: 64 rows x 32 columns = 512 pieces of four columns,
+  // 128 per producer; rows past the chunk's end load row 0 (zeroed when written)
+  const ChunkRows cr = chunk_rows(a, b * a.NT + n);
+#pragma unroll
+  for (int k = 0; k < 2; ++k) {
+    const int pc = 128 * P + 64 * k + l, row = pc >> 3, c4 = pc & 7;
+    const int64_t i = ((cr.row0 + (row < cr.len ? row : 0)) * H + h) * D + c0 + 4 * c4;
+    if constexpr (DO == 0) R.d[k] = *reinterpret_cast<const uint4*>(static_cast<const float*>(a.dout) + i);
+    else {
+      const uint2 w = *reinterpret_cast<const uint2*>(static_cast<const u16*>(a.dout) + i);
+      R.d[k] = uint4{w.x, w.y, 0u, 0u};
+    }
+  }
+  if constexpr (P == kRsProducers - 1) {
+    R.g = u32x4{0, 0, 0, 0};
+    if (l < D / 4) R.g = *reinterpret_cast<const u32x4*>(a.GCV + ch * D + 4 * l);
+  }
+}
+
+template <int D, int DO, int P>
+__device__ __forceinline__ void rs_write(unsigned char* dst, const BwdArgs& a, int b, int n, int l,
+                                         const RsRegs<D, P>& R) {
+  typedef RsLayout<D> LY;
+#pragma unroll
+  for (int k = 0; k < RsRegs<D, P>::NFP; ++k)
+    *reinterpret_cast<u32x4*>(dst + (P + kRsProducers * k) * 1024 + l * 16) = R.f[k];
+  const int len = chunk_rows(a, b * a.NT + n).len;
+#pragma unroll
+  for (int k = 0; k < 2; ++k) {
+    const int pc = 128 * P + 64 * k + l, row = pc >> 3, c4 = pc & 7;
+    float x[4];
+    if constexpr (DO == 0) {
+      x[0] = __uint_as_float(R.d[k].x); x[1] = __uint_as_float(R.d[k].y);
+      x[2] = __uint_as_float(R.d[k].z); x[3] = __uint_as_float(R.d[k].w);
+    } else {
+      const f4 v = unpack4<1>(uint2{R.d[k].x, R.d[k].y});
+      x[0] = v[0]; x[1] = v[1]; x[2] = v[2]; x[3] = v[3];
+    }
+    // B fragment (K step row / 32, value tile col / 16), lane (col % 16) +
+    // 16 ((row % 16) / 4), element (row % 4) + 4 ((row % 32) / 16)
+    const int kb = row >> 5, rr = row & 31;
+    const int lane_hi = 16 * ((rr & 15) >> 2), e = (rr & 3) + 4 * (rr >> 4);
+#pragma unroll
+    for (int i = 0; i < 4; ++i) {
+      const int col = 4 * c4 + i;
+      float* p = reinterpret_cast<float*>(dst + LY::OFF_DO) +
+                 ((kb * 2 + (col >> 4)) * 64 + (col & 15) + lane_hi) * 8 + e;
+      *p = (row < len) ? x[i] : 0.f;
+    }
+  }
+  if constexpr (P == kRsProducers - 1)
+    if (l < D / 4) *reinterpret_cast<u32x4*>(dst + LY::OFF_GC + l * 16) = R.g;
+}
+
+template <int D, int DO, int P>
+__device__ __forceinline__ void rs_producer(const BwdArgs& a, unsigned char (*buf)[RsLayout<D>::BYTES], int b, int h,
+                                            int c0) {
+  const int l = threadIdx.x & 63;
+  const int NT = a.NT;
+  RsRegs<D, P> R0, R1;
+  // step s works on chunk NT - 1 - s
+  rs_load<D, DO, P>(a, b, NT - 1, h, c0, l, R0);
+  rs_load<D, DO, P>(a, b, max(NT - 2, 0), h, c0, l, R1);
+  rs_write<D, DO, P>(buf[0], a, b, NT - 1, l, R0);
+  lds_barrier();   // chunk of step 0 staged
+  auto step = [&](int s, RsRegs<D, P>& Rn, RsRegs<D, P>& Rn1) {
+    // Rn held step s's chunk (in LDS since the last barrier): load step s+2's;
+    // write step s+1's from Rn1 (loaded a step earlier) into the free buffer
+    rs_load<D, DO, P>(a, b, max(NT - 3 - s, 0), h, c0, l, Rn);
+    if (s + 1 < NT) rs_write<D, DO, P>(buf[(s + 1) & 1], a, b, NT - 2 - s, l, Rn1);
+    lds_barrier();
+  };
+  int s = 0;
+  for (; s + 1 < NT; s += 2) {
+    step(s, R0, R1);
+    step(s + 1, R1, R0);
+  }
+  if (s < NT) step(s, R0, R1);
+  wait_vmem_all();
+}
+
+// A column's scale 2^e, e = 15 - exponent(largest |x|), so the largest
+// scaled element lies in [2^14, 2^15); e is at most 126 (a column below
+// 2^-111 is scaled less than that, which only costs it relative precision it
+// cannot use), and at least 15 - 128 for finite x, so 2^e and 2^-e are normal
+// floats: the scale and its inverse are exact multipliers.
+struct RsScale {
+  float up, down;
+};
+__device__ __forceinline__ RsScale rs_col_scale(float m) {
+  const int e = min(15 - __builtin_amdgcn_frexp_expf(m), 126);
+  return RsScale{__builtin_amdgcn_ldexpf(1.f, e), __builtin_amdgcn_ldexpf(1.f, -e)};
+}
+// eight B values, scaled, as fp16 hi + lo
+__device__ __forceinline__ void rs_split(const float (&x)[8], float up, h8& hi, h8& lo) {
+#pragma unroll
+  for (int i = 0; i < 8; ++i) {
+    const float y = x[i] * up;
+    hi[i] = static_cast<_Float16>(y);
+    lo[i] = static_cast<_Float16>(y - static_cast<float>(hi[i]));
+  }
+}
+// largest |x| of a column over the four lanes (gq) that hold it
+__device__ __forceinline__ float rs_col_max(float m) {
+  m = fmaxf(m, __shfl_xor(m, 16, 64));
+  return fmaxf(m, __shfl_xor(m, 32, 64));
+}
+
+template <int D, int W>
+__device__ __forceinline__ void rs_chain(const BwdArgs& a, unsigned char (*buf)[RsLayout<D>::BYTES], int b, int h,
+                                         int chain, int c0) {
+  typedef RsLayout<D> LY;
+  constexpr int NT_ = D / 16;   // channel tiles
+  constexpr int NJ = D / 32;    // K steps over the channels
+  const int l = threadIdx.x & 63, r = l & 15, gq = l >> 4;
+  const int col = c0 + 16 * W + r;   // this lane's value column
+  const int NT = a.NT;
+  f4 dS[NT_];
+  const int64_t sbase = static_cast<int64_t>(chain) * D * D + (4 * gq) * D + col;   // + (16 dt + i) D
+#pragma unroll
+  for (int dt = 0; dt < NT_; ++dt)
+#pragma unroll
+    for (int i = 0; i < 4; ++i) dS[dt][i] = (a.dht != nullptr) ? a.dht[sbase + (16 * dt + i) * D] : 0.f;
+  lds_barrier();   // chunk of step 0 staged by the producers
+  for (int s = 0; s < NT; ++s) {
+    const int n = NT - 1 - s;
+    const int64_t ch = (static_cast<int64_t>(b) * NT + n) * a.H + h;
+    const unsigned char* cur = buf[s & 1];
+    auto frag = [&](int f) { return *reinterpret_cast<const h8*>(cur + f * 1024 + l * 16); };
+    // the dv~ products' A fragments and the do B values, read ahead of the
+    // arithmetic that forms dS' and do's B fragments
+    h8 AL[4][NJ], AA[6];
+#pragma unroll
+    for (int ct = 0; ct < 4; ++ct)
+#pragma unroll
+      for (int j = 0; j < NJ; ++j) AL[ct][j] = frag(ct * NJ + j);
+#pragma unroll
+    for (int f = 0; f < 6; ++f) AA[f] = frag(LY::OFF_A + f);
+    float dov[2][8];
+#pragma unroll
+    for (int kb = 0; kb < 2; ++kb) {
+      const float* p = reinterpret_cast<const float*>(cur + LY::OFF_DO) + ((kb * 2 + W) * 64 + l) * 8;
+      const f4 lo = *reinterpret_cast<const f4*>(p), hi4 = *reinterpret_cast<const f4*>(p + 4);
+#pragma unroll
+      for (int i = 0; i < 4; ++i) { dov[kb][i] = lo[i]; dov[kb][4 + i] = hi4[i]; }
+    }
+    // (the reads stay here, ahead of the arithmetic below)
+    __builtin_amdgcn_sched_barrier(0);
+    // dS' (the cotangent of the state this chunk leaves) to the workspace
+    float* const dsp = a.DS + ch * D * D + (4 * gq) * D + col;
+#pragma unroll
+    for (int dt = 0; dt < NT_; ++dt)
+#pragma unroll
+      for (int i = 0; i < 4; ++i) dsp[(16 * dt + i) * D] = dS[dt][i];
+    // B fragments: dS' over the channels, do over the rows
+    float m1 = 0.f;
+#pragma unroll
+    for (int dt = 0; dt < NT_; ++dt)
+#pragma unroll
+      for (int i = 0; i < 4; ++i) m1 = fmaxf(m1, fabsf(dS[dt][i]));
+    const RsScale e1 = rs_col_scale(rs_col_max(m1));
+    h8 Sh[NJ], Sl[NJ];
+#pragma unroll
+    for (int j = 0; j < NJ; ++j) {
+      const float x[8] = {dS[2 * j][0], dS[2 * j][1], dS[2 * j][2], dS[2 * j][3],
+                          dS[2 * j + 1][0], dS[2 * j + 1][1], dS[2 * j + 1][2], dS[2 * j + 1][3]};
+      rs_split(x, e1.up, Sh[j], Sl[j]);
+    }
+    float m2 = 0.f;
+#pragma unroll
+    for (int kb = 0; kb < 2; ++kb)
+#pragma unroll
+      for (int i = 0; i < 8; ++i) m2 = fmaxf(m2, fabsf(dov[kb][i]));
+    const RsScale e2 = rs_col_scale(rs_col_max(m2));
+    h8 Dh[2], Dl[2];
+#pragma unroll
+    for (int kb = 0; kb < 2; ++kb) rs_split(dov[kb], e2.up, Dh[kb], Dl[kb]);
+    // dv~ = (lambda k) dS' + Aqk^T do, row tile ct
+    f4 p1[4], p2[4];
+#pragma unroll
+    for (int ct = 0; ct < 4; ++ct) {
+      p1[ct] = f4{0.f, 0.f, 0.f, 0.f};
+      p2[ct] = f4{0.f, 0.f, 0.f, 0.f};
+    }
+    // (consecutive MFMAs feed different accumulators)
+#pragma unroll
+    for (int j = 0; j < NJ; ++j) {
+#pragma unroll
+      for (int ct = 0; ct < 4; ++ct) p1[ct] = mma32(p1[ct], AL[ct][j], Sh[j]);
+#pragma unroll
+      for (int ct = 0; ct < 4; ++ct) p1[ct] = mma32(p1[ct], AL[ct][j], Sl[j]);
+    }
+#pragma unroll
+    for (int kb = 0; kb < 2; ++kb)
+#pragma unroll
+      for (int hl = 0; hl < 2; ++hl)
+#pragma unroll
+        for (int ct = 0; ct < 4; ++ct) {
+          if (ct >= 2 && kb == 0) continue;   // query rows 0..31 hold no pair with keys 32..63
+          p2[ct] = mma32(p2[ct], AA[fa_frag(ct, kb)], hl ? Dl[kb] : Dh[kb]);
+        }
+    // the dS update's (gamma q)^T fragments; (gamma q)^T do does not wait for dv~
+    h8 AQ[NT_][2];
+#pragma unroll
+    for (int dt = 0; dt < NT_; ++dt)
+#pragma unroll
+      for (int kb = 0; kb < 2; ++kb) AQ[dt][kb] = frag(LY::OFF_Q + 2 * dt + kb);
+    f4 pq[NT_];
+#pragma unroll
+    for (int dt = 0; dt < NT_; ++dt) pq[dt] = f4{0.f, 0.f, 0.f, 0.f};
+#pragma unroll
+    for (int kb = 0; kb < 2; ++kb)
+#pragma unroll
+      for (int hl = 0; hl < 2; ++hl)
+#pragma unroll
+        for (int dt = 0; dt < NT_; ++dt) pq[dt] = mma32(pq[dt], AQ[dt][kb], hl ? Dl[kb] : Dh[kb]);
+    h8 AW[NT_][2];
+#pragma unroll
+    for (int dt = 0; dt < NT_; ++dt)
+#pragma unroll
+      for (int kb = 0; kb < 2; ++kb) AW[dt][kb] = frag(LY::OFF_W + 2 * dt + kb);
+    f4 dvt[4];
+#pragma unroll
+    for (int ct = 0; ct < 4; ++ct)
+#pragma unroll
+      for (int i = 0; i < 4; ++i)
+        dvt[ct][i] = fmaf(p1[ct][i], e1.down, p2[ct][i] * e2.down);
+    float* const dvp = a.DVT + ch * kC * D + (4 * gq) * D + col;
+#pragma unroll
+    for (int ct = 0; ct < 4; ++ct)
+#pragma unroll
+      for (int i = 0; i < 4; ++i) dvp[(16 * ct + i) * D] = dvt[ct][i];
+    // dv~ as B fragments over the rows
+    float m3 = 0.f;
+#pragma unroll
+    for (int ct = 0; ct < 4; ++ct)
+#pragma unroll
+      for (int i = 0; i < 4; ++i) m3 = fmaxf(m3, fabsf(dvt[ct][i]));
+    const RsScale e3 = rs_col_scale(rs_col_max(m3));
+    h8 Vh[2], Vl[2];
+#pragma unroll
+    for (int kb = 0; kb < 2; ++kb) {
+      const float x[8] = {dvt[2 * kb][0], dvt[2 * kb][1], dvt[2 * kb][2], dvt[2 * kb][3],
+                          dvt[2 * kb + 1][0], dvt[2 * kb + 1][1], dvt[2 * kb + 1][2], dvt[2 * kb + 1][3]};
+      rs_split(x, e3.up, Vh[kb], Vl[kb]);
+    }
+    // dS <- gamma_C dS + (gamma q)^T do - W^T dv~, channel tile dt
+    f4 pw[NT_];
+#pragma unroll
+    for (int dt = 0; dt < NT_; ++dt) pw[dt] = f4{0.f, 0.f, 0.f, 0.f};
+#pragma unroll
+    for (int kb = 0; kb < 2; ++kb)
+#pragma unroll
+      for (int hl = 0; hl < 2; ++hl)
+#pragma unroll
+        for (int dt = 0; dt < NT_; ++dt) pw[dt] = mma32(pw[dt], AW[dt][kb], hl ? Vl[kb] : Vh[kb]);
+#pragma unroll
+    for (int dt = 0; dt < NT_; ++dt) {
+      const f4 gc = *reinterpret_cast<const f4*>(cur + LY::OFF_GC + (16 * dt + 4 * gq) * 4);
+#pragma unroll
+      for (int i = 0; i < 4; ++i)
+        dS[dt][i] = fmaf(-pw[dt][i], e3.down, fmaf(pq[dt][i], e2.down, dS[dt][i] * gc[i]));
+    }
+    lds_barrier();   // this buffer is free, the next one staged
+  }
+  if (a.dh0 != nullptr) {
+#pragma unroll
+    for (int dt = 0; dt < NT_; ++dt)
+#pragma unroll
+      for (int i = 0; i < 4; ++i) a.dh0[sbase + (16 * dt + i) * D] = dS[dt][i];
+  }
+}
+
+template <int D, int DO>
+__global__ __launch_bounds__(64 * (2 + kRsProducers), 1) void kda_bwd_rscan16_kernel(BwdArgs a) {
+  constexpr int NS = D / 32;
+  __shared__ __attribute__((aligned(16))) unsigned char buf[2][RsLayout<D>::BYTES];
+  int chain, split;
+  if (!scan_slot<NS>(a.B * a.H, chain, split)) return;   // uniform per workgroup
+  const int b = chain / a.H, h = chain - b * a.H;
+  const int c0 = 32 * split;
+  const int wave = threadIdx.x >> 6;
+  switch (wave) {
+    case 0: rs_chain<D, 0>(a, buf, b, h, chain, c0); break;
+    case 1: rs_chain<D, 1>(a, buf, b, h, chain, c0); break;
+    case 2: rs_producer<D, DO, 0>(a, buf, b, h, c0); break;
+    case 3: rs_producer<D, DO, 1>(a, buf, b, h, c0); break;
+    case 4: rs_producer<D, DO, 2>(a, buf, b, h, c0); break;
+    default: rs_producer<D, DO, 3>(a, buf, b, h, c0); break;
   }
 }
 
@@ -1684,7 +2080,10 @@ hipError_t launch_bwd_t(const BwdArgs& a, hipStream_t s) {
   hipLaunchKernelGGL((kda_bwd_fscan_kernel<D, (DTQ != 0)>), dim3(scan_grid), dim3(ScanThreads<D>::value), 0, s, a);
   e = hipGetLastError();
   if (e != hipSuccess) return e;
-  hipLaunchKernelGGL((kda_bwd_rscan_kernel<D, DO, (DTQ != 0)>), dim3(scan_grid), dim3(ScanThreads<D>::value), 0, s, a);
+  if constexpr (DTQ != 0)
+    hipLaunchKernelGGL((kda_bwd_rscan16_kernel<D, DO>), dim3(scan_grid), dim3(64 * (2 + kRsProducers)), 0, s, a);
+  else
+    hipLaunchKernelGGL((kda_bwd_rscan_kernel<D, DO, false>), dim3(scan_grid), dim3(ScanThreads<D>::value), 0, s, a);
   e = hipGetLastError();
   if (e != hipSuccess) return e;
   hipLaunchKernelGGL((kda_bwd_chunk_kernel<D, DTQ, DTG, DO>), dim3(chunk_heads), dim3(kChunkThreads), 0, s, a);

@@ -102,8 +102,11 @@ struct AdaptArgs {
   int dk;
 };
 
-// Chunked backward (dense inputs; all workspace arrays fp32, row-major,
-// per chunk-head ch = (b * NT + n) * H + h).
+// Chunked backward (dense inputs; workspace arrays row-major per chunk-head
+// ch = (b * NT + n) * H + h, fp32, or for 16-bit inputs fp16 where kda_bwd.hip
+// says so; the F* arrays, written and read only with 16-bit inputs, are fp16
+// MFMA A fragments: lane (r = l & 15, gq = l >> 4) of K step s holds M index
+// 16 m + r and K indices 32 s + 4 gq + (e & 3) + 16 (e >> 2), e = 0..7).
 struct BwdArgs {
   int B, T, H, NT;
   const void* q;
@@ -133,6 +136,11 @@ struct BwdArgs {
   float* VT;            // [ch][C][dv] v~
   float* DS;            // [ch][dk][dv] cotangent of the state leaving the chunk
   float* DVT;           // [ch][C][dv] cotangent of v~
+  void* FL;             // [ch][4][dk/32][64][8]  lambda k (M rows, K channels)
+  void* FA;             // [ch][6][64][8]         Aqk^T (M key rows, K query rows): (key tile, K step)
+                        //                        00 01 10 11 21 31 (the others are zero)
+  void* FQ;             // [ch][dk/16][2][64][8]  (gamma q)^T (M channels, K rows)
+  void* FW;             // [ch][dk/16][2][64][8]  W^T (M channels, K rows)
 };
 
 // Standalone unit-triangular solve (kda_ut.hip); a [H][C][C], b/x/xf [H][C][N].
