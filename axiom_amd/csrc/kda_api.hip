@@ -575,7 +575,7 @@ hipError_t launch_cc_finish(const CcFinishArgs& a, hipStream_t s) {
 // Backward workspace: arrays per chunk-head (see kda_internal.h: BwdArgs),
 // sized for fp32; the fragment arrays FL, FA, FQ, FW (fp16) serve 16-bit inputs.
 struct BwdLayout {
-  size_t GL, QG, KL, GCV, AQ, TM, WM, UM, SI, VT, DS, DVT, FL, FA, FQ, FW, total;
+  size_t GL, QG, KL, GCV, AQ, TM, WM, UM, SI, VT, DS, DVT, FL, FA, FQ, FW, FWN, FLT, total;
 };
 
 BwdLayout bwd_layout(int B, int T, int H, int d) {
@@ -600,6 +600,8 @@ BwdLayout bwd_layout(int B, int T, int H, int d) {
   L.FA = take(ch * 6 * 1024);
   L.FQ = take(ch * (d / 16) * 2 * 1024);
   L.FW = take(ch * (d / 16) * 2 * 1024);
+  L.FWN = take(ch * 4 * (d / 32) * 1024);
+  L.FLT = take(ch * (d / 16) * 2 * 1024);
   L.total = off;
   return L;
 }
@@ -919,6 +921,8 @@ int kda_chunk_bwd(hipStream_t stream, const void* q, const void* k, const void* 
   a.FA = ws + L.FA;
   a.FQ = ws + L.FQ;
   a.FW = ws + L.FW;
+  a.FWN = ws + L.FWN;
+  a.FLT = ws + L.FLT;
   const hipError_t e = kda::launch_bwd(a, dk_dim, in_dtype, dout_dtype, stream);
   if (e != hipSuccess) return hip_fail(e, "backward kernel launch");
   return KDA_OK;

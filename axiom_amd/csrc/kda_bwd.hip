@@ -430,26 +430,30 @@ __global__ __launch_bounds__(kPrepThreads, 4) void kda_bwd_prep_kernel(BwdArgs a
         const float4 kl = make_float4(ex2(gz.x - gl.x) * kv.x, ex2(gz.y - gl.y) * kv.y, ex2(gz.z - gl.z) * kv.z,
                                       ex2(gz.w - gl.w) * kv.w);
         *reinterpret_cast<float4*>(&GL[c * D + d]) = gl;
-        if constexpr (EF == 0) ws_st4<EF>(a.QG, base + c * D + d, qg);
-        ws_st4<EF>(a.KL, base + c * D + d, kl);
+        if constexpr (EF == 0) {
+          ws_st4<EF>(a.QG, base + c * D + d, qg);
+          ws_st4<EF>(a.KL, base + c * D + d, kl);
+        }
       }
       if constexpr (EF != 0) {
         // the reverse scan's A fragments of this half's channels, one lane
         // fragment per thread each (the slot order of kda_internal.h)
         static_assert(NTH == 512 && HD == 64, "one (gamma q)^T and one lambda k lane fragment per thread");
         const int ln = t & 63, rr = ln & 15, g4 = ln >> 4, hi = (t >> 6) & 1, tt = t >> 7;
-        h8 vq, vl;
+        h8 vq, vl, vt;
 #pragma unroll
         for (int e = 0; e < 8; ++e) {
-          // (gamma q)^T: channel tile tt of the half, K step hi over the rows
+          // (gamma q)^T and (lambda k)^T: channel tile tt of the half, K step hi over the rows
           const int c = 32 * hi + 4 * g4 + (e & 3) + 16 * (e >> 2), dq = 16 * tt + rr;
           vq[e] = static_cast<_Float16>(ex2(sG[c * P + dq]) * sQ[c * P + dq]);
+          vt[e] = static_cast<_Float16>(ex2(sG[(kC - 1) * P + dq] - sG[c * P + dq]) * sK[c * P + dq]);
           // lambda k: row tile tt, K step hi over the half's channels
           const int row = 16 * tt + rr, dl = 32 * hi + 4 * g4 + (e & 3) + 16 * (e >> 2);
           vl[e] = static_cast<_Float16>(ex2(sG[(kC - 1) * P + dl] - sG[row * P + dl]) * sK[row * P + dl]);
         }
         const int dt = (c0 >> 4) + tt, j = (c0 >> 5) + hi;
         *reinterpret_cast<h8*>(static_cast<_Float16*>(a.FQ) + (((ch * (D / 16) + dt) * 2 + hi) * 64 + ln) * 8) = vq;
+        *reinterpret_cast<h8*>(static_cast<_Float16*>(a.FLT) + (((ch * (D / 16) + dt) * 2 + hi) * 64 + ln) * 8) = vt;
         *reinterpret_cast<h8*>(static_cast<_Float16*>(a.FL) + (((ch * 4 + tt) * (D / 32) + j) * 64 + ln) * 8) = vl;
       }
       if (t < HD) a.GCV[ch * D + c0 + t] = ex2(sG[(kC - 1) * P + t]);
@@ -591,17 +595,30 @@ __global__ __launch_bounds__(kPrepThreads, 4) void kda_bwd_prep_kernel(BwdArgs a
 #pragma unroll
       for (int e = 0; e < 4; ++e) {
         const int o = (16 * mt + 4 * gq + e) * D + 16 * (dg * NDT + q) + r16;
-        ws_st<EF>(a.WM, wu0 + o, accW[q][e]);
+        if constexpr (EF == 0) ws_st<EF>(a.WM, wu0 + o, accW[q][e]);
         a.UM[wu0 + o] = accU[q][e];
       }
     if constexpr (EF != 0) {
-      // W^T fragments: channel tile of column tile q, K step mt / 2, half mt % 2
+      // W^T fragments: channel tile of column tile q, K step mt / 2, half mt % 2;
+      // W fragments (rows x channels) of K step c0 / 32 + dg: the D-layout tile
+      // read as an A fragment is W^T, and its product with the identity lands
+      // row r of W, channels 4 gq .. 4 gq + 3 of the tile, in lane (r, gq)
+      static_assert(NDT == 2, "two column tiles per wave: one 32-channel K step");
+      h4 ident;
+#pragma unroll
+      for (int i = 0; i < 4; ++i) ident[i] = static_cast<_Float16>((4 * gq + i == r16) ? 1.f : 0.f);
+      h8 wn;
 #pragma unroll
       for (int q = 0; q < NDT; ++q) {
         const int dt = (c0 >> 4) + dg * NDT + q;
+        const uint2 w16 = pack_f16x4(accW[q]);
         *reinterpret_cast<uint2*>(static_cast<u16*>(a.FW) + (((ch * (D / 16) + dt) * 2 + (mt >> 1)) * 64 + l) * 8 +
-                                  4 * (mt & 1)) = pack_f16x4(accW[q]);
+                                  4 * (mt & 1)) = w16;
+        const f4 tr = mma16(f4{0.f, 0.f, 0.f, 0.f}, __builtin_bit_cast(h4, w16), ident);
+#pragma unroll
+        for (int i = 0; i < 4; ++i) wn[4 * q + i] = static_cast<_Float16>(tr[i]);
       }
+      *reinterpret_cast<h8*>(static_cast<_Float16*>(a.FWN) + (((ch * 4 + mt) * (D / 32) + (c0 >> 5) + dg) * 64 + l) * 8) = wn;
     }
   }
 }
@@ -1461,6 +1478,259 @@ __global__ __launch_bounds__(64 * (2 + kRsProducers), 1) void kda_bwd_rscan16_ke
   }
 }
 
+// ---------------------------------------------------------------------------
+// Forward state scan for 16-bit inputs, in the form of the reverse scan above
+// (and of the forward's state kernel): per (chain, 32-column slice) two
+// compute waves own a 16-column tile of S each,
+//   v~ = U - W S,  S <- gamma_C S + (lambda k)^T v~,
+// with W and (lambda k)^T as the prep kernel's fp16 A fragments and S, v~
+// handed to the matrix cores as fp16 (the forward kernels' operands); four
+// producer waves stage W, (lambda k)^T, the slice's U tiles (fp32) and gamma_C
+// two chunks ahead.  Each chunk's incoming S is stored fp16 row-major: the
+// D-layout tile read as an A fragment is S^T, and its product with the
+// identity puts four consecutive columns of one row of S in each lane.  The
+// compute waves write S and v~ into a staging area and the producers store
+// them with 16-byte stores a step later, so the compute waves issue no global
+// memory operation inside the chunk loop.
+// ---------------------------------------------------------------------------
+constexpr int kFsProducers = 4;
+
+template <int D>
+struct FsLayout {
+  static constexpr int NFW = 4 * (D / 32);         // W fragments (row tile, K step over channels)
+  static constexpr int NFL = 2 * (D / 16);         // (lambda k)^T fragments (channel tile, K step over rows)
+  static constexpr int NF = NFW + NFL;             // 1 KiB fragments
+  static constexpr int OFF_U = NF * 1024;          // U tiles [row tile][value tile of the slice][64][4] fp32
+  static constexpr int NU = 4 * 2;
+  static constexpr int OFF_GC = OFF_U + NU * 1024; // gamma_C, D floats
+  static constexpr int BYTES = OFF_GC + 4 * D;
+  // the compute waves' outputs of a chunk, stored by the producers a step
+  // later: S fp16 [D][32], v~ fp32 [64][32] of the slice
+  static constexpr int STG_VT = D * 32 * 2;
+  static constexpr int STG = STG_VT + kC * 32 * 4;
+};
+
+// Producer P's share of a chunk: every kFsProducers-th fragment, two four-
+// column pieces of the slice's U rows (64 rows x 8 pieces, 128 per producer)
+// and (last producer) gamma_C.
+template <int D, int P>
+struct FsRegs {
+  static constexpr int NFP = (FsLayout<D>::NF - P + kFsProducers - 1) / kFsProducers;
+  u32x4 f[NFP];
+  f4 u[2];
+  u32x4 g;
+};
+
+template <int D, int P>
+__device__ __forceinline__ void fs_load(const BwdArgs& a, int b, int n, int h, int split, int l, FsRegs<D, P>& R) {
+  typedef FsLayout<D> LY;
+  const int64_t ch = (static_cast<int64_t>(b) * a.NT + n) * a.H + h;
+#pragma unroll
+  for (int k = 0; k < FsRegs<D, P>::NFP; ++k) {
+    const int f = P + kFsProducers * k;
+    const _Float16* src = (f < LY::NFW) ? static_cast<const _Float16*>(a.FWN) + (ch * LY::NFW + f) * 512
+                                        : static_cast<const _Float16*>(a.FLT) + (ch * LY::NFL + (f - LY::NFW)) * 512;
+    R.f[k] = *reinterpret_cast<const u32x4*>(src + l * 8);
+  }
+#pragma unroll
+  for (int k = 0; k < 2; ++k) {
+    const int pc = 128 * P + 64 * k + l, row = pc >> 3, c4 = pc & 7;
+    R.u[k] = *reinterpret_cast<const f4*>(a.UM + ch * kC * D + row * D + 32 * split + 4 * c4);
+  }
+  if constexpr (P == kFsProducers - 1) {
+    R.g = u32x4{0, 0, 0, 0};
+    if (l < D / 4) R.g = *reinterpret_cast<const u32x4*>(a.GCV + ch * D + 4 * l);
+  }
+}
+
+template <int D, int P>
+__device__ __forceinline__ void fs_write(unsigned char* dst, int l, const FsRegs<D, P>& R) {
+  typedef FsLayout<D> LY;
+#pragma unroll
+  for (int k = 0; k < FsRegs<D, P>::NFP; ++k)
+    *reinterpret_cast<u32x4*>(dst + (P + kFsProducers * k) * 1024 + l * 16) = R.f[k];
+  // U piece (row, four columns) into the D-layout tiles [row tile][value
+  // tile]: lane (col % 16) + 16 ((row % 16) / 4), element row % 4
+#pragma unroll
+  for (int k = 0; k < 2; ++k) {
+    const int pc = 128 * P + 64 * k + l, row = pc >> 3, c4 = pc & 7;
+#pragma unroll
+    for (int i = 0; i < 4; ++i) {
+      const int col = 4 * c4 + i;
+      reinterpret_cast<float*>(dst + LY::OFF_U)[(((row >> 4) * 2 + (col >> 4)) * 64 + (col & 15) +
+                                                 16 * ((row & 15) >> 2)) * 4 + (row & 3)] = R.u[k][i];
+    }
+  }
+  if constexpr (P == kFsProducers - 1)
+    if (l < D / 4) *reinterpret_cast<u32x4*>(dst + LY::OFF_GC + l * 16) = R.g;
+}
+
+// Producer P's share of chunk n's outputs from the staging area: 16-byte
+// pieces of the S rows (D rows x 4) and of the v~ rows (64 rows x 8).
+template <int D, int P>
+__device__ __forceinline__ void fs_store(const BwdArgs& a, const unsigned char* stg, int b, int n, int h, int split,
+                                         int l) {
+  typedef FsLayout<D> LY;
+  const int64_t ch = (static_cast<int64_t>(b) * a.NT + n) * a.H + h;
+  constexpr int NSP = D * 4 / (64 * kFsProducers);   // S pieces per lane
+#pragma unroll
+  for (int k = 0; k < NSP; ++k) {
+    const int pc = 64 * (NSP * P + k) + l, row = pc >> 2, c8 = pc & 3;
+    const uint4 v = *reinterpret_cast<const uint4*>(stg + (row * 32 + 8 * c8) * 2);
+    *reinterpret_cast<uint4*>(reinterpret_cast<u16*>(a.SI) + ch * D * D + row * D + 32 * split + 8 * c8) = v;
+  }
+#pragma unroll
+  for (int k = 0; k < 2; ++k) {
+    const int pc = 128 * P + 64 * k + l, row = pc >> 3, c4 = pc & 7;
+    const f4 v = *reinterpret_cast<const f4*>(stg + LY::STG_VT + (row * 32 + 4 * c4) * 4);
+    *reinterpret_cast<f4*>(a.VT + ch * kC * D + row * D + 32 * split + 4 * c4) = v;
+  }
+}
+
+template <int D, int P>
+__device__ __forceinline__ void fs_producer(const BwdArgs& a, unsigned char (*buf)[FsLayout<D>::BYTES],
+                                            unsigned char (*stg)[FsLayout<D>::STG], int b, int h, int split) {
+  const int l = threadIdx.x & 63;
+  const int NT = a.NT;
+  FsRegs<D, P> R0, R1;
+  fs_load<D, P>(a, b, 0, h, split, l, R0);
+  fs_load<D, P>(a, b, min(1, NT - 1), h, split, l, R1);
+  fs_write<D, P>(buf[0], l, R0);
+  lds_barrier();   // chunk 0 staged
+  auto step = [&](int n, FsRegs<D, P>& Rn, FsRegs<D, P>& Rn1) {
+    if (n > 0) fs_store<D, P>(a, stg[(n - 1) & 1], b, n - 1, h, split, l);
+    fs_load<D, P>(a, b, min(n + 2, NT - 1), h, split, l, Rn);
+    if (n + 1 < NT) fs_write<D, P>(buf[(n + 1) & 1], l, Rn1);
+    lds_barrier();
+  };
+  int n = 0;
+  for (; n + 1 < NT; n += 2) {
+    step(n, R0, R1);
+    step(n + 1, R1, R0);
+  }
+  if (n < NT) step(n, R0, R1);
+  fs_store<D, P>(a, stg[(NT - 1) & 1], b, NT - 1, h, split, l);
+  wait_vmem_all();
+}
+
+template <int D, int W>
+__device__ __forceinline__ void fs_chain(const BwdArgs& a, unsigned char (*buf)[FsLayout<D>::BYTES],
+                                         unsigned char (*stg)[FsLayout<D>::STG], int b, int h, int chain, int c0) {
+  typedef FsLayout<D> LY;
+  constexpr int NT_ = D / 16;
+  constexpr int NJ = D / 32;
+  const int l = threadIdx.x & 63, r = l & 15, gq = l >> 4;
+  const int col = c0 + 16 * W + r;
+  const int NT = a.NT;
+  f4 S[NT_];
+#pragma unroll
+  for (int dt = 0; dt < NT_; ++dt)
+#pragma unroll
+    for (int i = 0; i < 4; ++i)
+      S[dt][i] = (a.h0 != nullptr) ? a.h0[(static_cast<int64_t>(chain) * D + 16 * dt + 4 * gq + i) * D + col] : 0.f;
+  h4 ident;
+#pragma unroll
+  for (int i = 0; i < 4; ++i) ident[i] = static_cast<_Float16>((4 * gq + i == r) ? 1.f : 0.f);
+  lds_barrier();   // chunk 0 staged by the producers
+  for (int n = 0; n < NT; ++n) {
+    const int64_t ch = (static_cast<int64_t>(b) * NT + n) * a.H + h;
+    const unsigned char* cur = buf[n & 1];
+    auto frag = [&](int f) { return *reinterpret_cast<const h8*>(cur + f * 1024 + l * 16); };
+    h8 AW[4][NJ];
+#pragma unroll
+    for (int ct = 0; ct < 4; ++ct)
+#pragma unroll
+      for (int j = 0; j < NJ; ++j) AW[ct][j] = frag(ct * NJ + j);
+    f4 Ut[4];
+#pragma unroll
+    for (int ct = 0; ct < 4; ++ct) Ut[ct] = *reinterpret_cast<const f4*>(cur + LY::OFF_U + (2 * ct + W) * 1024 + l * 16);
+    __builtin_amdgcn_sched_barrier(0);
+    // S as fp16: the B fragments over the channels, and the chunk's incoming
+    // state to the workspace (row 16 dt + r, columns 4 gq .. 4 gq + 3 of the tile)
+    h4 Sq[NT_];
+#pragma unroll
+    for (int dt = 0; dt < NT_; ++dt)
+#pragma unroll
+      for (int i = 0; i < 4; ++i) Sq[dt][i] = static_cast<_Float16>(S[dt][i]);
+    unsigned char* const so = stg[n & 1];
+#pragma unroll
+    for (int dt = 0; dt < NT_; ++dt) {
+      const f4 tr = mma16(f4{0.f, 0.f, 0.f, 0.f}, Sq[dt], ident);
+      h4 v;
+#pragma unroll
+      for (int i = 0; i < 4; ++i) v[i] = static_cast<_Float16>(tr[i]);
+      *reinterpret_cast<h4*>(so + ((16 * dt + r) * 32 + 16 * W + 4 * gq) * 2) = v;
+    }
+    h8 Sb[NJ];
+#pragma unroll
+    for (int j = 0; j < NJ; ++j)
+#pragma unroll
+      for (int i = 0; i < 4; ++i) {
+        Sb[j][i] = Sq[2 * j][i];
+        Sb[j][4 + i] = Sq[2 * j + 1][i];
+      }
+    // v~ = U - W S, row tile ct
+    f4 P[4];
+#pragma unroll
+    for (int ct = 0; ct < 4; ++ct) P[ct] = f4{0.f, 0.f, 0.f, 0.f};
+#pragma unroll
+    for (int j = 0; j < NJ; ++j)
+#pragma unroll
+      for (int ct = 0; ct < 4; ++ct) P[ct] = mma32(P[ct], AW[ct][j], Sb[j]);
+    h8 AL[NT_][2];
+#pragma unroll
+    for (int dt = 0; dt < NT_; ++dt)
+#pragma unroll
+      for (int kb = 0; kb < 2; ++kb) AL[dt][kb] = frag(LY::NFW + 2 * dt + kb);
+    f4 vt[4];
+#pragma unroll
+    for (int ct = 0; ct < 4; ++ct) vt[ct] = Ut[ct] - P[ct];
+    float* const vto = reinterpret_cast<float*>(so + LY::STG_VT);
+#pragma unroll
+    for (int ct = 0; ct < 4; ++ct)
+#pragma unroll
+      for (int i = 0; i < 4; ++i) vto[(16 * ct + 4 * gq + i) * 32 + 16 * W + r] = vt[ct][i];
+    h8 Vb[2];
+#pragma unroll
+    for (int kb = 0; kb < 2; ++kb)
+#pragma unroll
+      for (int i = 0; i < 4; ++i) {
+        Vb[kb][i] = static_cast<_Float16>(vt[2 * kb][i]);
+        Vb[kb][4 + i] = static_cast<_Float16>(vt[2 * kb + 1][i]);
+      }
+    // S <- gamma_C S + (lambda k)^T v~, channel tile dt
+#pragma unroll
+    for (int dt = 0; dt < NT_; ++dt) {
+      const f4 gc = *reinterpret_cast<const f4*>(cur + LY::OFF_GC + (16 * dt + 4 * gq) * 4);
+      S[dt] = S[dt] * gc;
+    }
+#pragma unroll
+    for (int kb = 0; kb < 2; ++kb)
+#pragma unroll
+      for (int dt = 0; dt < NT_; ++dt) S[dt] = mma32(S[dt], AL[dt][kb], Vb[kb]);
+    lds_barrier();   // this buffer is free, the next one staged
+  }
+}
+
+template <int D>
+__global__ __launch_bounds__(64 * (2 + kFsProducers), 1) void kda_bwd_fscan16_kernel(BwdArgs a) {
+  constexpr int NS = D / 32;
+  __shared__ __attribute__((aligned(16))) unsigned char buf[2][FsLayout<D>::BYTES];
+  __shared__ __attribute__((aligned(16))) unsigned char stg[2][FsLayout<D>::STG];
+  int chain, split;
+  if (!scan_slot<NS>(a.B * a.H, chain, split)) return;   // uniform per workgroup
+  const int b = chain / a.H, h = chain - b * a.H;
+  const int c0 = 32 * split;
+  switch (threadIdx.x >> 6) {
+    case 0: fs_chain<D, 0>(a, buf, stg, b, h, chain, c0); break;
+    case 1: fs_chain<D, 1>(a, buf, stg, b, h, chain, c0); break;
+    case 2: fs_producer<D, 0>(a, buf, stg, b, h, split); break;
+    case 3: fs_producer<D, 1>(a, buf, stg, b, h, split); break;
+    case 4: fs_producer<D, 2>(a, buf, stg, b, h, split); break;
+    default: fs_producer<D, 3>(a, buf, stg, b, h, split); break;
+  }
+}
+
 // A 16 x 16 accumulator tile (lane (r, gq): rows 4 gq + i, column r) into
 // row-major hi / lo bf16 planes of pitch PB at (row0, col0): lanes r and r ^ 1
 // swap one value of each row pair, so each lane writes packed column pairs
@@ -1480,6 +1750,41 @@ __device__ __forceinline__ void acc_put_hl(const f4& v, int row0, int col0, __bf
   *reinterpret_cast<unsigned*>(&h[o + 2 * PB]) = hh;
   *reinterpret_cast<unsigned*>(&l[o + 2 * PB]) = ll;
 }
+
+// W of a chunk-head from its fp16 A fragments (rows x channels, the slot
+// order of kda_internal.h) into hi / lo bf16 planes [64][PB] with the channel
+// contiguous: each lane fragment is row 16 ct + r, channels 32 j + 4 gq .. + 3
+// and 32 j + 16 + 4 gq .. + 3.
+template <int D, int NTH>
+struct WnTile {
+  static constexpr int N = 4 * (D / 32) * 64;     // lane fragments
+  static constexpr int PER = (N + NTH - 1) / NTH;
+  static_assert(N % NTH == 0, "whole lane fragments per thread");
+  uint4 w[PER];
+  __device__ __forceinline__ void fetch(const void* src) {
+#pragma unroll
+    for (int p = 0; p < PER; ++p)
+      w[p] = *reinterpret_cast<const uint4*>(static_cast<const u16*>(src) + (threadIdx.x + p * NTH) * 8);
+  }
+  template <int PB>
+  __device__ __forceinline__ void put_hl(__bf16* h, __bf16* l) const {
+#pragma unroll
+    for (int p = 0; p < PER; ++p) {
+      const int e = threadIdx.x + p * NTH, f = e >> 6, ln = e & 63;
+      const int ct = f / (D / 32), j = f - ct * (D / 32);
+      const int row = 16 * ct + (ln & 15), ch0 = 32 * j + 4 * (ln >> 4);
+#pragma unroll
+      for (int hf = 0; hf < 2; ++hf) {
+        const f4 v = unpack4<2>(hf ? uint2{w[p].z, w[p].w} : uint2{w[p].x, w[p].y});
+        uint2 hh, ll;
+        split2_bf16(v[0], v[1], hh.x, ll.x);
+        split2_bf16(v[2], v[3], hh.y, ll.y);
+        *reinterpret_cast<uint2*>(&h[row * PB + ch0 + 16 * hf]) = hh;
+        *reinterpret_cast<uint2*>(&l[row * PB + ch0 + 16 * hf]) = ll;
+      }
+    }
+  }
+};
 
 // ---------------------------------------------------------------------------
 // per chunk-head adjoint
@@ -1668,7 +1973,8 @@ __global__ __launch_bounds__(kChunkThreads) void kda_bwd_chunk_kernel(BwdArgs a)
   // contiguous; T[c][m] is zero for c < m, so row tile mt starts at the
   // K block holding row 16 mt.
   f4 Yw[NDT], Yu[NDT];
-  Tile<kC, D, NTH, EF> tW3;
+  // W from its row-major array (fp32 inputs) or its fp16 A fragments (16-bit)
+  typename std::conditional<EF == 0, Tile<kC, D, NTH>, WnTile<D, NTH>>::type tW3;
   Tile<kC, D, NTH> tU3;
   {
     constexpr int PB = kC + 8;
@@ -1691,7 +1997,8 @@ __global__ __launch_bounds__(kChunkThreads) void kda_bwd_chunk_kernel(BwdArgs a)
     tT.template put_hl<PB>(sTh, sTl);
     tY.template put_hl<PB>(sYh, sYl);
     __syncthreads();
-    tW3.fetch(ws_at<EF>(a.WM, ch * kC * D), D, 0);     // phase 3's operands, during the products
+    if constexpr (EF == 0) tW3.fetch(a.WM + ch * kC * D, D, 0);   // phase 3's operands, during the products
+    else tW3.fetch(static_cast<const u16*>(a.FWN) + ch * kC * D);
     tU3.fetch(a.UM + ch * kC * D, D, 0);
 #pragma unroll
     for (int q = 0; q < NDT; ++q)
@@ -1770,7 +2077,8 @@ __global__ __launch_bounds__(kChunkThreads) void kda_bwd_chunk_kernel(BwdArgs a)
       acc_put_hl<PB>(Yw[q], 16 * mt, 16 * (dg_ * NDT + q), sAh, sAl);
       acc_put_hl<PB>(Yu[q], 16 * mt, 16 * (dg_ * NDT + q), sBh, sBl);
     }
-    put_hl<PB>(tW3, sWh, sWl);
+    if constexpr (EF == 0) put_hl<PB>(tW3, sWh, sWl);
+    else tW3.template put_hl<PB>(sWh, sWl);
     put_hl<PB>(tU3, sUh, sUl);
     __syncthreads();
     f4 dLa[2], dAa[2];
@@ -2077,7 +2385,10 @@ hipError_t launch_bwd_t(const BwdArgs& a, hipStream_t s) {
   hipError_t e = hipGetLastError();
   if (e != hipSuccess) return e;
   const int scan_grid = (chains + 7) / 8 * 8 * (D / 32);
-  hipLaunchKernelGGL((kda_bwd_fscan_kernel<D, (DTQ != 0)>), dim3(scan_grid), dim3(ScanThreads<D>::value), 0, s, a);
+  if constexpr (DTQ != 0)
+    hipLaunchKernelGGL((kda_bwd_fscan16_kernel<D>), dim3(scan_grid), dim3(64 * (2 + kFsProducers)), 0, s, a);
+  else
+    hipLaunchKernelGGL((kda_bwd_fscan_kernel<D, false>), dim3(scan_grid), dim3(ScanThreads<D>::value), 0, s, a);
   e = hipGetLastError();
   if (e != hipSuccess) return e;
   if constexpr (DTQ != 0)

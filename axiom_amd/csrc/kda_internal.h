@@ -141,6 +141,8 @@ struct BwdArgs {
                         //                        00 01 10 11 21 31 (the others are zero)
   void* FQ;             // [ch][dk/16][2][64][8]  (gamma q)^T (M channels, K rows)
   void* FW;             // [ch][dk/16][2][64][8]  W^T (M channels, K rows)
+  void* FWN;            // [ch][4][dk/32][64][8]  W (M rows, K channels)
+  void* FLT;            // [ch][dk/16][2][64][8]  (lambda k)^T (M channels, K rows)
 };
 
 // Standalone unit-triangular solve (kda_ut.hip); a [H][C][C], b/x/xf [H][C][N].
