@@ -1,4 +1,4 @@
-// Chunked KDA backward (dense [B, T, H, d] inputs), fp32 throughout.
+// Chunked KDA backward (dense [B, T, H, d] inputs).
 //
 // Gradients of o = chunk_fwd(q, k, v, g, beta, h0) and of the final state
 // with respect to q, k, v, g (the log decay), beta and h0, following the
@@ -8,25 +8,40 @@
 // launches:
 //   kda_bwd_prep_kernel   one workgroup per chunk-head: in-chunk log2 cumsum G,
 //                         gamma*q, lambda*k, gamma_C, Aqk, T = (I+L)^-1, W, U;
-//   kda_bwd_fscan_kernel  one workgroup per (chain, 32 value columns): the
-//                         forward state scan, keeping every chunk's incoming
-//                         state S and its v~ = U - W S;
-//   kda_bwd_rscan_kernel  same grid, chunks in reverse: the state cotangent
+//   forward state scan    one workgroup per (chain, 32 value columns): every
+//                         chunk's incoming state S and its v~ = U - W S;
+//   reverse scan          same grid, chunks in reverse: the state cotangent
 //                         dS entering each chunk from the right, and
 //                         dv~ = (lambda k) dS + Aqk^T do;
 //                         dS <- gamma_C dS + (gamma q)^T do - W^T dv~; dh0;
 //   kda_bwd_chunk_kernel  one workgroup per chunk-head: the rest of the adjoint
 //                         (dY, dgq, dW, the two transposed solves, dL, dAqk, the
 //                         score adjoints, the cumsum adjoint) and the outputs.
-// The dense products run on the fp32 matrix cores (v_mfma_f32_16x16x4f32:
-// exact fp32 products, fp32 sums), except the two scans' and the chunk
-// kernel's phases 1-3 (dY, dgq, dW; Yw, Yu; dL, dAqk), which run as bf16
-// hi/lo triples (about 2^-16 of each product dropped); operands are
-// staged through LDS; decay factors
-// of off-diagonal 16-row tiles are anchored at the row tile's first row
-// (2^(G_c - G_a) * 2^(G_a - G_i), both <= 1), diagonal tiles use
-// 2^(G_c - G_i) directly.  Workspace arrays are fp32, row-major, per
-// chunk-head ch = (b * NT + n) * H + h.
+// Two precisions of the workspace, chosen by the input dtype:
+//  * fp32 inputs: every workspace array fp32 row-major per chunk-head
+//    ch = (b * NT + n) * H + h; scans kda_bwd_fscan_kernel and
+//    kda_bwd_rscan_kernel (16 waves, operands split into bf16 hi/lo planes
+//    in LDS each chunk step).
+//  * 16-bit inputs (bf16, fp16): the forward-side arrays gamma q, lambda k,
+//    Aqk, T, W and the stored state S are fp16 (BwdWs<true>: the operand
+//    width the forward's own kernels give them), and the
+//    prep kernel writes the scans' operands directly as MFMA lane fragments
+//    (FL, FA, FQ, FW, FWN, FLT); G, gamma_C, U, v~ and the cotangents dS', dv~
+//    stay fp32.  Scans kda_bwd_fscan16_kernel and kda_bwd_rscan16_kernel in
+//    the column-owner form: two compute waves (one 16-column tile each of the
+//    32-column slice, the state slice in their accumulators) and four
+//    producer waves that load two chunks ahead into registers, fill a
+//    double-buffered LDS chunk, and store the compute waves' staged outputs
+//    a step later; one barrier per chunk step.
+// Products: fp16 operands on v_mfma_f32_16x16x32_f16 (exact products of the
+// stored values); fp32 operands (cotangents, v~, U, S in the fp32 path) as
+// hi/lo pairs of a 16-bit type, about 2^-16 of each product dropped (the
+// 16-bit scans scale each column's cotangent by a power of two first, so the
+// fp16 pair keeps ~22 bits whatever its range); the rest (prep scores, phase 4
+// of the chunk kernel) on v_mfma_f32_16x16x4f32.  Decay factors of
+// off-diagonal 16-row tiles are anchored at the row tile's first row
+// (2^(G_c - G_a) * 2^(G_a - G_i), both <= 1); diagonal tiles likewise when
+// the tile's decay span allows (kDiagAnchorLog2), else per element.
 #include <hip/hip_runtime.h>
 
 #include <cstdint>
@@ -1159,6 +1174,8 @@ struct RsLayout {
   static constexpr int OFF_GC = NF * 1024;         // gamma_C, D floats
   static constexpr int OFF_DO = OFF_GC + 4 * D;    // do B fragments [K step][value tile][64][8] fp32
   static constexpr int BYTES = OFF_DO + 2 * 2 * 64 * 8 * 4;
+  static constexpr int SROW = 36;                  // staging row stride in floats (rows 4 apart land 16 banks apart)
+  static constexpr int STG = kC * SROW * 4;        // dv~ of the slice, fp32 [64][32], stored a step later
 };
 
 // One chunk's share of producer P: every kRsProducers-th fragment, two
@@ -1240,9 +1257,23 @@ __device__ __forceinline__ void rs_write(unsigned char* dst, const BwdArgs& a, i
     if (l < D / 4) *reinterpret_cast<u32x4*>(dst + LY::OFF_GC + l * 16) = R.g;
 }
 
+// Producer P's share of chunk n's dv~ rows from the staging area (64 rows x
+// 8 pieces of four columns, 16-byte stores).
+template <int D, int P>
+__device__ __forceinline__ void rs_store(const BwdArgs& a, const unsigned char* stg, int b, int n, int h, int c0,
+                                         int l) {
+  const int64_t ch = (static_cast<int64_t>(b) * a.NT + n) * a.H + h;
+#pragma unroll
+  for (int k = 0; k < 2; ++k) {
+    const int pc = 128 * P + 64 * k + l, row = pc >> 3, c4 = pc & 7;
+    const f4 v = *reinterpret_cast<const f4*>(stg + (row * RsLayout<D>::SROW + 4 * c4) * 4);
+    *reinterpret_cast<f4*>(a.DVT + ch * kC * D + row * D + c0 + 4 * c4) = v;
+  }
+}
+
 template <int D, int DO, int P>
-__device__ __forceinline__ void rs_producer(const BwdArgs& a, unsigned char (*buf)[RsLayout<D>::BYTES], int b, int h,
-                                            int c0) {
+__device__ __forceinline__ void rs_producer(const BwdArgs& a, unsigned char (*buf)[RsLayout<D>::BYTES],
+                                            unsigned char (*stg)[RsLayout<D>::STG], int b, int h, int c0) {
   const int l = threadIdx.x & 63;
   const int NT = a.NT;
   RsRegs<D, P> R0, R1;
@@ -1252,8 +1283,10 @@ __device__ __forceinline__ void rs_producer(const BwdArgs& a, unsigned char (*bu
   rs_write<D, DO, P>(buf[0], a, b, NT - 1, l, R0);
   lds_barrier();   // chunk of step 0 staged
   auto step = [&](int s, RsRegs<D, P>& Rn, RsRegs<D, P>& Rn1) {
-    // Rn held step s's chunk (in LDS since the last barrier): load step s+2's;
-    // write step s+1's from Rn1 (loaded a step earlier) into the free buffer
+    // store step s-1's dv~; Rn held step s's chunk (in LDS since the last
+    // barrier): load step s+2's; write step s+1's from Rn1 (loaded a step
+    // earlier) into the free buffer
+    if (s > 0) rs_store<D, P>(a, stg[(s - 1) & 1], b, NT - s, h, c0, l);
     rs_load<D, DO, P>(a, b, max(NT - 3 - s, 0), h, c0, l, Rn);
     if (s + 1 < NT) rs_write<D, DO, P>(buf[(s + 1) & 1], a, b, NT - 2 - s, l, Rn1);
     lds_barrier();
@@ -1264,6 +1297,7 @@ __device__ __forceinline__ void rs_producer(const BwdArgs& a, unsigned char (*bu
     step(s + 1, R1, R0);
   }
   if (s < NT) step(s, R0, R1);
+  rs_store<D, P>(a, stg[(NT - 1) & 1], b, 0, h, c0, l);
   wait_vmem_all();
 }
 
@@ -1295,8 +1329,8 @@ __device__ __forceinline__ float rs_col_max(float m) {
 }
 
 template <int D, int W>
-__device__ __forceinline__ void rs_chain(const BwdArgs& a, unsigned char (*buf)[RsLayout<D>::BYTES], int b, int h,
-                                         int chain, int c0) {
+__device__ __forceinline__ void rs_chain(const BwdArgs& a, unsigned char (*buf)[RsLayout<D>::BYTES],
+                                         unsigned char (*stg)[RsLayout<D>::STG], int b, int h, int chain, int c0) {
   typedef RsLayout<D> LY;
   constexpr int NT_ = D / 16;   // channel tiles
   constexpr int NJ = D / 32;    // K steps over the channels
@@ -1413,11 +1447,11 @@ __device__ __forceinline__ void rs_chain(const BwdArgs& a, unsigned char (*buf)[
 #pragma unroll
       for (int i = 0; i < 4; ++i)
         dvt[ct][i] = fmaf(p1[ct][i], e1.down, p2[ct][i] * e2.down);
-    float* const dvp = a.DVT + ch * kC * D + (4 * gq) * D + col;
+    float* const dvo = reinterpret_cast<float*>(stg[s & 1]);   // stored by the producers a step later
 #pragma unroll
     for (int ct = 0; ct < 4; ++ct)
 #pragma unroll
-      for (int i = 0; i < 4; ++i) dvp[(16 * ct + i) * D] = dvt[ct][i];
+      for (int i = 0; i < 4; ++i) dvo[(16 * ct + 4 * gq + i) * LY::SROW + 16 * W + r] = dvt[ct][i];
     // dv~ as B fragments over the rows
     float m3 = 0.f;
 #pragma unroll
@@ -1463,18 +1497,19 @@ template <int D, int DO>
 __global__ __launch_bounds__(64 * (2 + kRsProducers), 1) void kda_bwd_rscan16_kernel(BwdArgs a) {
   constexpr int NS = D / 32;
   __shared__ __attribute__((aligned(16))) unsigned char buf[2][RsLayout<D>::BYTES];
+  __shared__ __attribute__((aligned(16))) unsigned char stg[2][RsLayout<D>::STG];
   int chain, split;
   if (!scan_slot<NS>(a.B * a.H, chain, split)) return;   // uniform per workgroup
   const int b = chain / a.H, h = chain - b * a.H;
   const int c0 = 32 * split;
   const int wave = threadIdx.x >> 6;
   switch (wave) {
-    case 0: rs_chain<D, 0>(a, buf, b, h, chain, c0); break;
-    case 1: rs_chain<D, 1>(a, buf, b, h, chain, c0); break;
-    case 2: rs_producer<D, DO, 0>(a, buf, b, h, c0); break;
-    case 3: rs_producer<D, DO, 1>(a, buf, b, h, c0); break;
-    case 4: rs_producer<D, DO, 2>(a, buf, b, h, c0); break;
-    default: rs_producer<D, DO, 3>(a, buf, b, h, c0); break;
+    case 0: rs_chain<D, 0>(a, buf, stg, b, h, chain, c0); break;
+    case 1: rs_chain<D, 1>(a, buf, stg, b, h, chain, c0); break;
+    case 2: rs_producer<D, DO, 0>(a, buf, stg, b, h, c0); break;
+    case 3: rs_producer<D, DO, 1>(a, buf, stg, b, h, c0); break;
+    case 4: rs_producer<D, DO, 2>(a, buf, stg, b, h, c0); break;
+    default: rs_producer<D, DO, 3>(a, buf, stg, b, h, c0); break;
   }
 }
 
