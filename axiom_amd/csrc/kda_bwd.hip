@@ -724,15 +724,33 @@ struct TTile {
   typedef typename WsPiece<ET>::t Piece;
   Piece r[PER][2];
   __device__ __forceinline__ void fetch(const void* src, int src_ld, int col0) {
+#pragma unroll
+    for (int j = 0; j < PER; ++j) fetch_block(src, src_ld, col0, j);
+  }
+  // column block j alone: columns col0 + 4 (cg + G j) .. + 3 of the row pair
+  __device__ __forceinline__ void fetch_block(const void* src, int src_ld, int col0, int j) {
     const int rp = threadIdx.x & 31, cg = threadIdx.x >> 5;
 #pragma unroll
-    for (int j = 0; j < PER; ++j)
+    for (int y = 0; y < 2; ++y) {
+      const int64_t i = static_cast<int64_t>(2 * rp + y) * src_ld + col0 + 4 * (cg + G * j);
+      if constexpr (ET == 0) r[j][y] = *reinterpret_cast<const float4*>(static_cast<const float*>(src) + i);
+      else r[j][y] = *reinterpret_cast<const uint2*>(static_cast<const u16*>(src) + i);
+    }
+  }
+  // block j row-major into hi / lo planes of pitch PB, block-local columns
+  // 4 cg .. 4 cg + 3 (a [rows][4 G] pass of a product over the columns)
+  template <int PB>
+  __device__ __forceinline__ void put_rows_hl(int j, __bf16* h, __bf16* l) const {
+    const int rp = threadIdx.x & 31, cg = threadIdx.x >> 5;
 #pragma unroll
-      for (int y = 0; y < 2; ++y) {
-        const int64_t i = static_cast<int64_t>(2 * rp + y) * src_ld + col0 + 4 * (cg + G * j);
-        if constexpr (ET == 0) r[j][y] = *reinterpret_cast<const float4*>(static_cast<const float*>(src) + i);
-        else r[j][y] = *reinterpret_cast<const uint2*>(static_cast<const u16*>(src) + i);
-      }
+    for (int y = 0; y < 2; ++y) {
+      const float4 x = ws_unpack<ET>(r[j][y]);
+      uint2 hh, ll;
+      split2_bf16(x.x, x.y, hh.x, ll.x);
+      split2_bf16(x.z, x.w, hh.y, ll.y);
+      *reinterpret_cast<uint2*>(&h[(2 * rp + y) * PB + 4 * cg]) = hh;
+      *reinterpret_cast<uint2*>(&l[(2 * rp + y) * PB + 4 * cg]) = ll;
+    }
   }
   template <int PB>
   __device__ __forceinline__ void put_hl(__bf16* h, __bf16* l) const {
@@ -1888,6 +1906,11 @@ __global__ __launch_bounds__(kChunkThreads) void kda_bwd_chunk_kernel(BwdArgs a)
 #pragma unroll
   for (int q = 0; q < NDT; ++q) dzp[q] = 0.f;
   float dgc = 0.f;   // thread t < D: sum_n S[t][n] dS'[t][n]
+  // G, k and q (times the scale; zero on pad rows) at this thread's positions
+  // (rows 16 mt + 4 gq + i, columns 16 (dg_ NDT + q) + r16), read once in
+  // phase 1's epilogue: phase 2 shares the positions and phase 4 takes its
+  // LDS copies of G, k, q from them
+  float gH[NDT][4], kH[NDT][4], qH[NDT][4], gLast[NDT];
   constexpr int EF = BwdWs<DTQ != 0>::F;    // S_in, T, W
 
   // Phase 1's dk and dG terms reach phase 2 (same thread, same positions)
@@ -1901,8 +1924,11 @@ __global__ __launch_bounds__(kChunkThreads) void kda_bwd_chunk_kernel(BwdArgs a)
   // lo hi, about 2^-16 of each product dropped); dW accumulates +dv~ S^T and
   // is negated where phase 2 takes it.
   f4 dW[NDT];
-  TTile<kC, NTH, EF> tT;     // phase 2's T and dv~, loaded during phase 1's last pass
+  TTile<kC, NTH, EF> tT;     // phase 2's T, loaded during phase 1's last pass
+  // dv~ in row pairs: column block hp is phase 1's pass hp operand, and the
+  // whole tile phase 2's dv~^T (one read of dv~ serves both)
   TTile<D, NTH> tY;
+  static_assert(TTile<D, NTH>::PER == D / 64 && TTile<D, NTH>::G * 4 == 64, "one column block per pass");
   {
     f4 dY[NDT], dgq[NDT];
 #pragma unroll
@@ -1922,29 +1948,42 @@ __global__ __launch_bounds__(kChunkThreads) void kda_bwd_chunk_kernel(BwdArgs a)
     __bf16* const sDh = sSl + D * PB;    // dS'
     __bf16* const sDl = sDh + D * PB;
     // a pass's operands are loaded during the previous pass's products
-    Tile<kC, HW, NTH> pV, pDv;
+    Tile<kC, HW, NTH> pV;
     Tile<D, HW, NTH, EF> pS;
     Tile<D, HW, NTH> pDS;
     InTile<DO, D, HW, NTH> pDo;
-    auto fetch_pass = [&](int n0) {
+    auto fetch_pass = [&](int hp) {
+      const int n0 = HW * hp;
       pV.fetch(a.VT + ch * kC * D, D, n0);
-      pDv.fetch(a.DVT + ch * kC * D, D, n0);
+      tY.fetch_block(a.DVT + ch * kC * D, D, 0, hp);
       pS.fetch(ws_at<EF>(a.SI, ch * D * D), D, n0);
       pDS.fetch(a.DS + ch * D * D, D, n0);
       pDo.fetch(a.dout, cr.row0, cr.len, H, h, n0);
     };
     fetch_pass(0);
+#pragma unroll
     for (int hp = 0; hp < NH; ++hp) {
       put_hl<PB>(pV, sVh, sVl);
-      put_hl<PB>(pDv, sUh, sUl);
+      tY.template put_rows_hl<PB>(hp, sUh, sUl);
       put_hl<PB>(pS, sSh, sSl);
       put_hl<PB>(pDS, sDh, sDl);
       put_hl<PB>(pDo, sOh, sOl);
       __syncthreads();
-      if (hp + 1 < NH) fetch_pass(HW * (hp + 1));
-      else {   // phase 2's operands
+      if (hp + 1 < NH) fetch_pass(hp + 1);
+      else {   // phase 2's T; the epilogue's G, q, k (all issued before any of its stores)
         tT.fetch(ws_at<EF>(a.TM, ch * kC * kC), kC, 0);
-        tY.fetch(a.DVT + ch * kC * D, D, 0);
+#pragma unroll
+        for (int q = 0; q < NDT; ++q) {
+          const int d = 16 * (dg_ * NDT + q) + r16;
+          gLast[q] = GL[(kC - 1) * D + d];
+#pragma unroll
+          for (int i = 0; i < 4; ++i) {
+            const int c = 16 * mt + 4 * gq + i;
+            gH[q][i] = GL[c * D + d];
+            qH[q][i] = ld_q(c, d);
+            kH[q][i] = ld_k(c, d);
+          }
+        }
       }
 #pragma unroll
       for (int kb = 0; kb < HW / 32; ++kb) {
@@ -1975,30 +2014,21 @@ __global__ __launch_bounds__(kChunkThreads) void kda_bwd_chunk_kernel(BwdArgs a)
       }
       __syncthreads();
     }
-    // dq = dgq gamma; dG = dgq q gamma - dY k lambda; dk = dY lambda.  Loads
-    // of a tile are issued before its stores (the compiler cannot move a load
-    // above a store to a pointer it may alias).
+    // dq = dgq gamma; dG = dgq q gamma - dY k lambda; dk = dY lambda (the
+    // operands loaded during the last pass: a load the compiler finds after a
+    // store to a pointer it may alias waits for it)
 #pragma unroll
     for (int q = 0; q < NDT; ++q) {
       const int d = 16 * (dg_ * NDT + q) + r16;
-      const float glast = GL[(kC - 1) * D + d];
-      float gl[4], qv[4], kv[4];
 #pragma unroll
       for (int i = 0; i < 4; ++i) {
         const int c = 16 * mt + 4 * gq + i;
-        gl[i] = GL[c * D + d];
-        qv[i] = ld_q(c, d);
-        kv[i] = ld_k(c, d);
-      }
-#pragma unroll
-      for (int i = 0; i < 4; ++i) {
-        const int c = 16 * mt + 4 * gq + i;
-        const float gam = ex2(gl[i]), lam = ex2(glast - gl[i]);
-        const float dz = dY[q][i] * kv[i] * lam;
+        const float gam = ex2(gH[q][i]), lam = ex2(gLast[q] - gH[q][i]);
+        const float dz = dY[q][i] * kH[q][i] * lam;
         dzp[q] += dz;
         if (c < cr.len) gq_[in_idx(c, d)] = dgq[q][i] * gam * a.scale;
         sAcc[c * D + d] = dY[q][i] * lam;
-        sAcc[(kC + c) * D + d] = dgq[q][i] * qv[i] * gam - dz;
+        sAcc[(kC + c) * D + d] = dgq[q][i] * qH[q][i] * gam - dz;
       }
     }
   }
@@ -2035,6 +2065,14 @@ __global__ __launch_bounds__(kChunkThreads) void kda_bwd_chunk_kernel(BwdArgs a)
     if constexpr (EF == 0) tW3.fetch(a.WM + ch * kC * D, D, 0);   // phase 3's operands, during the products
     else tW3.fetch(static_cast<const u16*>(a.FWN) + ch * kC * D);
     tU3.fetch(a.UM + ch * kC * D, D, 0);
+    float vH[NDT][4], bH[4];   // the epilogue's v and beta, during the products
+#pragma unroll
+    for (int i = 0; i < 4; ++i) {
+      const int c = 16 * mt + 4 * gq + i;
+      bH[i] = ld_b(c);
+#pragma unroll
+      for (int q = 0; q < NDT; ++q) vH[q][i] = ld_v(c, 16 * (dg_ * NDT + q) + r16);
+    }
 #pragma unroll
     for (int q = 0; q < NDT; ++q)
 #pragma unroll
@@ -2057,21 +2095,20 @@ __global__ __launch_bounds__(kChunkThreads) void kda_bwd_chunk_kernel(BwdArgs a)
     for (int i = 0; i < 4; ++i) {
       const int c = 16 * mt + 4 * gq + i;
       const bool live = c < cr.len;
-      const float bc = ld_b(c);
-      float gl[NDT], kv[NDT], vv[NDT], oG[NDT], ok[NDT];
+      const float bc = bH[i];
+      float kv[NDT], vv[NDT], oG[NDT], ok[NDT];
 #pragma unroll
       for (int q = 0; q < NDT; ++q) {
         const int d = 16 * (dg_ * NDT + q) + r16;
-        gl[q] = GL[c * D + d];
-        kv[q] = ld_k(c, d);
-        vv[q] = ld_v(c, d);
+        kv[q] = kH[q][i];
+        vv[q] = vH[q][i];
         oG[q] = sAcc[(kC + c) * D + d];
         ok[q] = sAcc[c * D + d];
       }
 #pragma unroll
       for (int q = 0; q < NDT; ++q) {
         const int d = 16 * (dg_ * NDT + q) + r16;
-        const float gam = ex2(gl[q]);
+        const float gam = ex2(gH[q][i]);
         dbrD[i] += Yw[q][i] * gam * kv[q] + Yu[q][i] * vv[q];
         if (live) {
           gG_[in_idx(c, d)] = oG[q] + Yw[q][i] * kv[q] * bc * gam;
@@ -2094,8 +2131,6 @@ __global__ __launch_bounds__(kChunkThreads) void kda_bwd_chunk_kernel(BwdArgs a)
   float* const sRed4 = sm + 2 * kC * PC + 3 * kC * P + kC;
   float* const sBase = sRed4 + 16 * D;
   static_assert(2 * kC * PC + 3 * kC * P + kC + 17 * D <= SMEM_FLOATS, "phase 4 LDS");
-  InTile<DTQ, D, D, NTH> tQ4, tK4;
-  Tile<kC, D, NTH> tG4;
   {
     constexpr int PB = D + 8;            // bf16 pitch: 16-byte aligned K blocks, rows 4 banks apart
     static_assert(8 * kC * PB / 2 <= SMEM_FLOATS, "phase 3 LDS");
@@ -2149,9 +2184,6 @@ __global__ __launch_bounds__(kChunkThreads) void kda_bwd_chunk_kernel(BwdArgs a)
     put_hl<PB>(tDo, sAh, sAl);
     put_hl<PB>(tVt, sBh, sBl);
     __syncthreads();
-    tQ4.fetch(a.q, cr.row0, cr.len, H, h, 0);   // phase 4's q, k, G, during the dAqk products
-    tK4.fetch(a.k, cr.row0, cr.len, H, h, 0);
-    tG4.fetch(GL, D, 0);
     if (live0) {
 #pragma unroll
       for (int kb = 0; kb < D / 32; ++kb) {
@@ -2202,18 +2234,39 @@ __global__ __launch_bounds__(kChunkThreads) void kda_bwd_chunk_kernel(BwdArgs a)
     float* sK = sQ + kC * P;
     float* sG = sK + kC * P;
     float* sB = sG + kC * P;
-    tQ4.template put<P>(sQ, a.scale);
-    tK4.template put<P>(sK, 1.f);
-    tG4.template put<P>(sG);
+#pragma unroll
+    for (int q = 0; q < NDT; ++q)
+#pragma unroll
+      for (int i = 0; i < 4; ++i) {
+        const int o = (16 * mt + 4 * gq + i) * P + 16 * (dg_ * NDT + q) + r16;
+        sQ[o] = qH[q][i];
+        sK[o] = kH[q][i];
+        sG[o] = gH[q][i];
+      }
     if (t < kC) sB[t] = ld_b(t);
+    const bool mine = wv < NCT;
+    const int d = 16 * (wv % NCT) + r16;
+    // the partial dq, dG, dk of every row tile, issued here so their latency
+    // passes during the LDS fill (pad rows read row 0 and are not stored)
+    float oq4[4][4], oG4[4][4], ok4[4][4];
+    if (mine) {
+#pragma unroll
+      for (int R = 0; R < 4; ++R)
+#pragma unroll
+        for (int e = 0; e < 4; ++e) {
+          const int c = 16 * R + 4 * gq + e;
+          const int64_t o = in_idx(c < cr.len ? c : 0, d);
+          oq4[R][e] = gq_[o];
+          oG4[R][e] = gG_[o];
+          ok4[R][e] = gk_[o];
+        }
+    }
     if (t < D) {   // dg[c] = base + sum_{c' >= c} dG[c']: the G_C terms and the dz terms
       float acc = dgc * ex2(GL[(kC - 1) * D + t]);
       for (int r = 0; r < 16; ++r) acc += sRed4[r * D + t];
       sBase[t] = acc;
     }
     __syncthreads();
-    const bool mine = wv < NCT;
-    const int d = 16 * (wv % NCT) + r16;
     // Row tiles in descending order: when tile R is finished (its diagonal and
     // the read-modify-write of its rows), every row tile below it has already
     // added its column-side terms to colS[R].  Each lane forms the factored
@@ -2231,19 +2284,9 @@ __global__ __launch_bounds__(kChunkThreads) void kda_bwd_chunk_kernel(BwdArgs a)
     for (int R = 3; R >= 0; --R) {
       const int a0 = 16 * R;
       f4 accA = {0.f, 0.f, 0.f, 0.f}, accK = {0.f, 0.f, 0.f, 0.f};
-      // this tile's partial dq, dG, dk, loaded before its arithmetic (pad
-      // rows read row 0 and are not stored)
-      float oq[4], oG[4], ok[4];
-      if (mine) {
-#pragma unroll
-        for (int e = 0; e < 4; ++e) {
-          const int c = a0 + 4 * gq + e;
-          const int64_t o = in_idx(c < cr.len ? c : 0, d);
-          oq[e] = gq_[o];
-          oG[e] = gG_[o];
-          ok[e] = gk_[o];
-        }
-      }
+      const float* const oq = oq4[R];
+      const float* const oG = oG4[R];
+      const float* const ok = ok4[R];
       const float ga = sG[a0 * P + d];
       float xq[4], xk[4];      // q_c 2^(G_c - G_a), beta_c k_c 2^(G_c - G_a): rows a0 + 4 k + gq
       if (mine) {
