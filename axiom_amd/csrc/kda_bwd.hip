@@ -1855,7 +1855,7 @@ __global__ __launch_bounds__(kChunkThreads) void kda_bwd_chunk_kernel(BwdArgs a)
   // q, k, G [64][P] plus beta
   constexpr int ACC0 = (2 * kC + 4 * D) * (kC + 8) / 2;   // floats of phase 2's bf16 planes
   constexpr int SMEM_FLOATS = cmax(cmax((6 * kC + 4 * D) * (HW + 8) / 2, ACC0 + 2 * kC * D),
-                                   cmax(8 * kC * (D + 8) / 2, 2 * kC * PC + 3 * kC * P + kC));
+                                   cmax(8 * kC * (D + 8) / 2, 2 * kC * PC + 3 * kC * P + kC + 17 * D + 40 * kC));
   __shared__ __attribute__((aligned(16))) float sm[SMEM_FLOATS];
   const int t = threadIdx.x;
   const int H = a.H;
@@ -1882,19 +1882,17 @@ __global__ __launch_bounds__(kChunkThreads) void kda_bwd_chunk_kernel(BwdArgs a)
     const float x = ld1<DTG>(a.beta, (cr.row0 + (c < cr.len ? c : 0)) * H + h);
     return (c < cr.len) ? x : 0.f;
   };
-  // The gradients of q, k and G accumulate in place in dq, dk and dg (dg
-  // holds dG until phase 4 turns it into its reverse cumsum).  Phases 1-3
-  // run on the matrix cores as bf16 hi / lo triples: wave wv owns row tile
-  // mt = wv / 2 and the NDT column tiles dt = (wv % 2) NDT + q of every
-  // [64][D] product (lane (r, gq) holds rows 16 mt + 4 gq + i, column
-  // 16 dt + r), so phase 2 adds to the dk and dG terms phase 1 left at its
-  // own positions; phase 4 (wave wv owns column tile wv, lane rows 4 gq + e
-  // of every row tile) reads what other threads wrote, after the workgroup
-  // barriers between the phases.  Pad rows (c >= len) are never stored
-  // (their dG is zero: every term carries a factor q_c or k_c).
+  // Every phase works in one mapping: wave wv owns row tile mt = wv / 2 and
+  // the NDT column tiles dt = (wv % 2) NDT + q of every [64][D] array (lane
+  // (r, gq) holds rows 16 mt + 4 gq + i, column 16 dt + r), so the gradients
+  // of q, k and G accumulate in registers from phase 1 to phase 4 and each
+  // is stored once.  Phases 1-3 run on the matrix cores as bf16 hi / lo
+  // triples.  Pad rows (c >= len) are never stored (their dG is zero: every
+  // term carries a factor q_c or k_c).
   float* const gq_ = a.dq;
   float* const gk_ = a.dk;
   float* const gG_ = a.dg;
+  float pq[D / 32][4], pk[D / 32][4], pG[D / 32][4];   // partial dq, dk, dG at this thread's positions
   constexpr int NDT = D / 32;          // column tiles per wave of a [64][D] product
   const int wv = t >> 6, l = t & 63, r16 = l & 15, gq = l >> 4;
   const int mt = wv >> 1, dg_ = wv & 1;
@@ -1910,7 +1908,40 @@ __global__ __launch_bounds__(kChunkThreads) void kda_bwd_chunk_kernel(BwdArgs a)
   // (rows 16 mt + 4 gq + i, columns 16 (dg_ NDT + q) + r16), read once in
   // phase 1's epilogue: phase 2 shares the positions and phase 4 takes its
   // LDS copies of G, k, q from them
-  float gH[NDT][4], kH[NDT][4], qH[NDT][4], gLast[NDT];
+  // (q, k held as loaded: 16-bit inputs packed two to a register)
+  typedef typename std::conditional<DTQ == 0, f4, uint2>::type H4;
+  auto hload = [&](const void* src, int d) {   // rows 16 mt + 4 gq + i of column d (pad rows read row 0)
+    H4 hv;
+    if constexpr (DTQ == 0) {
+#pragma unroll
+      for (int i = 0; i < 4; ++i) {
+        const int c = 16 * mt + 4 * gq + i;
+        hv[i] = static_cast<const float*>(src)[in_idx(c < cr.len ? c : 0, d)];
+      }
+    } else {
+      uint32_t b[4];
+#pragma unroll
+      for (int i = 0; i < 4; ++i) {
+        const int c = 16 * mt + 4 * gq + i;
+        b[i] = static_cast<const u16*>(src)[in_idx(c < cr.len ? c : 0, d)];
+      }
+      hv.x = b[0] | (b[1] << 16);
+      hv.y = b[2] | (b[3] << 16);
+    }
+    return hv;
+  };
+  auto hget = [&](const H4& hv, int i) {   // element i, zero on pad rows
+    float x;
+    if constexpr (DTQ == 0) x = hv[i];
+    else {
+      const uint32_t w = (i < 2) ? hv.x : hv.y;
+      const u16 bits = static_cast<u16>((i & 1) ? (w >> 16) : (w & 0xFFFFu));
+      x = (DTQ == 1) ? bf16_to_f32(bits) : f16bits_to_f32(bits);
+    }
+    return (16 * mt + 4 * gq + i < cr.len) ? x : 0.f;
+  };
+  float gH[NDT][4], gLast[NDT];
+  H4 kH[NDT], qH[NDT];
   constexpr int EF = BwdWs<DTQ != 0>::F;    // S_in, T, W
 
   // Phase 1's dk and dG terms reach phase 2 (same thread, same positions)
@@ -1970,21 +2001,7 @@ __global__ __launch_bounds__(kChunkThreads) void kda_bwd_chunk_kernel(BwdArgs a)
       put_hl<PB>(pDo, sOh, sOl);
       __syncthreads();
       if (hp + 1 < NH) fetch_pass(hp + 1);
-      else {   // phase 2's T; the epilogue's G, q, k (all issued before any of its stores)
-        tT.fetch(ws_at<EF>(a.TM, ch * kC * kC), kC, 0);
-#pragma unroll
-        for (int q = 0; q < NDT; ++q) {
-          const int d = 16 * (dg_ * NDT + q) + r16;
-          gLast[q] = GL[(kC - 1) * D + d];
-#pragma unroll
-          for (int i = 0; i < 4; ++i) {
-            const int c = 16 * mt + 4 * gq + i;
-            gH[q][i] = GL[c * D + d];
-            qH[q][i] = ld_q(c, d);
-            kH[q][i] = ld_k(c, d);
-          }
-        }
-      }
+      else tT.fetch(ws_at<EF>(a.TM, ch * kC * kC), kC, 0);   // phase 2's T
 #pragma unroll
       for (int kb = 0; kb < HW / 32; ++kb) {
         const int ka = (16 * mt + r16) * PB + 32 * kb + 8 * gq;
@@ -2014,9 +2031,16 @@ __global__ __launch_bounds__(kChunkThreads) void kda_bwd_chunk_kernel(BwdArgs a)
       }
       __syncthreads();
     }
-    // dq = dgq gamma; dG = dgq q gamma - dY k lambda; dk = dY lambda (the
-    // operands loaded during the last pass: a load the compiler finds after a
-    // store to a pointer it may alias waits for it)
+    // dq = dgq gamma; dG = dgq q gamma - dY k lambda; dk = dY lambda
+#pragma unroll
+    for (int q = 0; q < NDT; ++q) {
+      const int d = 16 * (dg_ * NDT + q) + r16;
+      gLast[q] = GL[(kC - 1) * D + d];
+#pragma unroll
+      for (int i = 0; i < 4; ++i) gH[q][i] = GL[(16 * mt + 4 * gq + i) * D + d];
+      qH[q] = hload(a.q, d);
+      kH[q] = hload(a.k, d);
+    }
 #pragma unroll
     for (int q = 0; q < NDT; ++q) {
       const int d = 16 * (dg_ * NDT + q) + r16;
@@ -2024,11 +2048,11 @@ __global__ __launch_bounds__(kChunkThreads) void kda_bwd_chunk_kernel(BwdArgs a)
       for (int i = 0; i < 4; ++i) {
         const int c = 16 * mt + 4 * gq + i;
         const float gam = ex2(gH[q][i]), lam = ex2(gLast[q] - gH[q][i]);
-        const float dz = dY[q][i] * kH[q][i] * lam;
+        const float dz = dY[q][i] * hget(kH[q], i) * lam;
         dzp[q] += dz;
         if (c < cr.len) gq_[in_idx(c, d)] = dgq[q][i] * gam * a.scale;
         sAcc[c * D + d] = dY[q][i] * lam;
-        sAcc[(kC + c) * D + d] = dgq[q][i] * qH[q][i] * gam - dz;
+        sAcc[(kC + c) * D + d] = dgq[q][i] * (hget(qH[q], i) * a.scale) * gam - dz;
       }
     }
   }
@@ -2062,17 +2086,12 @@ __global__ __launch_bounds__(kChunkThreads) void kda_bwd_chunk_kernel(BwdArgs a)
     tT.template put_hl<PB>(sTh, sTl);
     tY.template put_hl<PB>(sYh, sYl);
     __syncthreads();
-    if constexpr (EF == 0) tW3.fetch(a.WM + ch * kC * D, D, 0);   // phase 3's operands, during the products
-    else tW3.fetch(static_cast<const u16*>(a.FWN) + ch * kC * D);
-    tU3.fetch(a.UM + ch * kC * D, D, 0);
-    float vH[NDT][4], bH[4];   // the epilogue's v and beta, during the products
+    H4 vH[NDT];   // the epilogue's v and beta, during the products
+    float bH[4];
 #pragma unroll
-    for (int i = 0; i < 4; ++i) {
-      const int c = 16 * mt + 4 * gq + i;
-      bH[i] = ld_b(c);
+    for (int i = 0; i < 4; ++i) bH[i] = ld_b(16 * mt + 4 * gq + i);
 #pragma unroll
-      for (int q = 0; q < NDT; ++q) vH[q][i] = ld_v(c, 16 * (dg_ * NDT + q) + r16);
-    }
+    for (int q = 0; q < NDT; ++q) vH[q] = hload(a.v, 16 * (dg_ * NDT + q) + r16);
 #pragma unroll
     for (int q = 0; q < NDT; ++q)
 #pragma unroll
@@ -2100,8 +2119,8 @@ __global__ __launch_bounds__(kChunkThreads) void kda_bwd_chunk_kernel(BwdArgs a)
 #pragma unroll
       for (int q = 0; q < NDT; ++q) {
         const int d = 16 * (dg_ * NDT + q) + r16;
-        kv[q] = kH[q][i];
-        vv[q] = vH[q][i];
+        kv[q] = hget(kH[q], i);
+        vv[q] = hget(vH[q], i);
         oG[q] = sAcc[(kC + c) * D + d];
         ok[q] = sAcc[c * D + d];
       }
@@ -2110,11 +2129,9 @@ __global__ __launch_bounds__(kChunkThreads) void kda_bwd_chunk_kernel(BwdArgs a)
         const int d = 16 * (dg_ * NDT + q) + r16;
         const float gam = ex2(gH[q][i]);
         dbrD[i] += Yw[q][i] * gam * kv[q] + Yu[q][i] * vv[q];
-        if (live) {
-          gG_[in_idx(c, d)] = oG[q] + Yw[q][i] * kv[q] * bc * gam;
-          gk_[in_idx(c, d)] = ok[q] + Yw[q][i] * gam * bc;
-          a.dv[in_idx(c, d)] = Yu[q][i] * bc;
-        }
+        pG[q][i] = oG[q] + Yw[q][i] * kv[q] * bc * gam;
+        pk[q][i] = ok[q] + Yw[q][i] * gam * bc;
+        if (live) a.dv[in_idx(c, d)] = Yu[q][i] * bc;
       }
     }
     __syncthreads();   // sAcc read before phase 3's operands overwrite it
@@ -2124,13 +2141,19 @@ __global__ __launch_bounds__(kChunkThreads) void kda_bwd_chunk_kernel(BwdArgs a)
   // outputs, two 16 x 16 tiles per wave: row tile mt, key tiles 2 (wv % 2) + q,
   // as bf16 hi / lo triples (operands row-major with the channel, the K index,
   // contiguous); key tiles above the row tile are masked to zero and skipped.
+  Tile<kC, D, NTH> tG4;                  // phase 4's G, loaded at the end of phase 3
   float* const sDL = sm;                 // phase 4's operands, written at the end of phase 3
   float* const sDA = sDL + kC * PC;
   // past phase 4's dL, dAqk, q, k, G, beta: [16][D] dz partials, then the
   // per-column base of dg [D]
   float* const sRed4 = sm + 2 * kC * PC + 3 * kC * P + kC;
   float* const sBase = sRed4 + 16 * D;
-  static_assert(2 * kC * PC + 3 * kC * P + kC + 17 * D <= SMEM_FLOATS, "phase 4 LDS");
+  // then the row partial sums of dbeta: [64][32] from phase 2 (written at the
+  // start of phase 3, past its planes), [64][8] from phase 4 (per column tile)
+  float* const sDbD = sBase + D;
+  float* const sDb4 = sDbD + kC * 32;
+  static_assert(2 * kC * PC + 3 * kC * P + kC + 17 * D + 40 * kC <= SMEM_FLOATS, "phase 4 LDS");
+  static_assert(8 * kC * (D + 8) / 2 <= 2 * kC * PC + 3 * kC * P + kC + 17 * D, "phase 3 planes end below sDbD");
   {
     constexpr int PB = D + 8;            // bf16 pitch: 16-byte aligned K blocks, rows 4 banks apart
     static_assert(8 * kC * PB / 2 <= SMEM_FLOATS, "phase 3 LDS");
@@ -2147,9 +2170,14 @@ __global__ __launch_bounds__(kChunkThreads) void kda_bwd_chunk_kernel(BwdArgs a)
       acc_put_hl<PB>(Yw[q], 16 * mt, 16 * (dg_ * NDT + q), sAh, sAl);
       acc_put_hl<PB>(Yu[q], 16 * mt, 16 * (dg_ * NDT + q), sBh, sBl);
     }
+    if constexpr (EF == 0) tW3.fetch(a.WM + ch * kC * D, D, 0);
+    else tW3.fetch(static_cast<const u16*>(a.FWN) + ch * kC * D);
+    tU3.fetch(a.UM + ch * kC * D, D, 0);
     if constexpr (EF == 0) put_hl<PB>(tW3, sWh, sWl);
     else tW3.template put_hl<PB>(sWh, sWl);
     put_hl<PB>(tU3, sUh, sUl);
+#pragma unroll
+    for (int i = 0; i < 4; ++i) sDbD[(16 * mt + 4 * gq + i) * 32 + 16 * dg_ + r16] = dbrD[i];
     __syncthreads();
     f4 dLa[2], dAa[2];
 #pragma unroll
@@ -2163,7 +2191,7 @@ __global__ __launch_bounds__(kChunkThreads) void kda_bwd_chunk_kernel(BwdArgs a)
     tDo.fetch(a.dout, cr.row0, cr.len, H, h, 0);
     tVt.fetch(a.VT + ch * kC * D, D, 0);
     if (live0) {
-#pragma unroll
+#pragma unroll 2
       for (int kb = 0; kb < D / 32; ++kb) {
         const int ka = (16 * mt + r16) * PB + 32 * kb + 8 * gq;
         const b8 ywh = *reinterpret_cast<const b8*>(&sAh[ka]), ywl = *reinterpret_cast<const b8*>(&sAl[ka]);
@@ -2198,6 +2226,7 @@ __global__ __launch_bounds__(kChunkThreads) void kda_bwd_chunk_kernel(BwdArgs a)
         }
       }
     }
+    tG4.fetch(GL, D, 0);   // phase 4's G
     __syncthreads();   // every read of the planes done before sDL, sDA overwrite them
     // phase 4's masked operands
 #pragma unroll
@@ -2224,11 +2253,11 @@ __global__ __launch_bounds__(kChunkThreads) void kda_bwd_chunk_kernel(BwdArgs a)
   // for the row side, (block)^T x (q_c 2^(G_c - G_a)) for the column side.
   // Diagonal tiles are anchored the same way (their key factors >= 1, bounded
   // by the tile's decay) unless the tile decays past 2^-kDiagAnchorLog2 in a
-  // column of the wave; those take 2^-|G_c - G_i| per element.  Wave wv < D/16 owns column tile
-  // wv: lane (r, gq) rows 4 gq + e of every row tile, column 16 wv + r; each
-  // position gets one read-modify-write.
+  // column of the wave; those take 2^-|G_c - G_i| per element.  Wave (mt, half)
+  // forms, for each of its column tiles, the row side of row tile mt (key
+  // tiles s <= mt) and the column side of key tile mt (row tiles R >= mt), so
+  // the results land on the positions whose partial sums it holds.
   constexpr int NCT = D / 16;
-  float* sDb4 = nullptr;             // [64][8] row partial sums of dbeta, per column tile
   {
     float* sQ = sDA + kC * PC;       // q * scale
     float* sK = sQ + kC * P;
@@ -2239,113 +2268,90 @@ __global__ __launch_bounds__(kChunkThreads) void kda_bwd_chunk_kernel(BwdArgs a)
 #pragma unroll
       for (int i = 0; i < 4; ++i) {
         const int o = (16 * mt + 4 * gq + i) * P + 16 * (dg_ * NDT + q) + r16;
-        sQ[o] = qH[q][i];
-        sK[o] = kH[q][i];
-        sG[o] = gH[q][i];
+        sQ[o] = hget(qH[q], i) * a.scale;
+        sK[o] = hget(kH[q], i);
       }
+    tG4.template put<P>(sG);
     if (t < kC) sB[t] = ld_b(t);
-    const bool mine = wv < NCT;
-    const int d = 16 * (wv % NCT) + r16;
-    // the partial dq, dG, dk of every row tile, issued here so their latency
-    // passes during the LDS fill (pad rows read row 0 and are not stored)
-    float oq4[4][4], oG4[4][4], ok4[4][4];
-    if (mine) {
-#pragma unroll
-      for (int R = 0; R < 4; ++R)
-#pragma unroll
-        for (int e = 0; e < 4; ++e) {
-          const int c = 16 * R + 4 * gq + e;
-          const int64_t o = in_idx(c < cr.len ? c : 0, d);
-          oq4[R][e] = gq_[o];
-          oG4[R][e] = gG_[o];
-          ok4[R][e] = gk_[o];
-        }
-    }
     if (t < D) {   // dg[c] = base + sum_{c' >= c} dG[c']: the G_C terms and the dz terms
       float acc = dgc * ex2(GL[(kC - 1) * D + t]);
       for (int r = 0; r < 16; ++r) acc += sRed4[r * D + t];
       sBase[t] = acc;
     }
+    // phase 1's dq terms (stored there: registers are short through phases 2
+    // and 3), loaded during the LDS fill
+#pragma unroll
+    for (int q = 0; q < NDT; ++q)
+#pragma unroll
+      for (int e = 0; e < 4; ++e) {
+        const int c = 16 * mt + 4 * gq + e;
+        pq[q][e] = gq_[in_idx(c < cr.len ? c : 0, 16 * (dg_ * NDT + q) + r16)];
+      }
     __syncthreads();
-    // Row tiles in descending order: when tile R is finished (its diagonal and
-    // the read-modify-write of its rows), every row tile below it has already
-    // added its column-side terms to colS[R].  Each lane forms the factored
-    // operands it feeds to the matrix cores itself (rows 4 k + gq of a tile,
-    // its column d), so the loop reads only LDS written before it and needs
-    // no barrier.
-    f4 colS[3];
+    float* const sTile = sRed4;      // [4][D] dG column sums of each row tile (sRed4 is read above)
+    const int a0 = 16 * mt;
+    float sfx[NDT][4], abv[NDT];
 #pragma unroll
-    for (int q = 0; q < 3; ++q)
-#pragma unroll
-      for (int e = 0; e < 4; ++e) colS[q][e] = 0.f;
-    float dbq[4][4];
-    float carry = 0.f;   // sum of dG over the rows of the tiles already finished (below)
-#pragma unroll
-    for (int R = 3; R >= 0; --R) {
-      const int a0 = 16 * R;
-      f4 accA = {0.f, 0.f, 0.f, 0.f}, accK = {0.f, 0.f, 0.f, 0.f};
-      const float* const oq = oq4[R];
-      const float* const oG = oG4[R];
-      const float* const ok = ok4[R];
+    for (int q = 0; q < NDT; ++q) {
+      const int d = 16 * (dg_ * NDT + q) + r16;
       const float ga = sG[a0 * P + d];
-      float xq[4], xk[4];      // q_c 2^(G_c - G_a), beta_c k_c 2^(G_c - G_a): rows a0 + 4 k + gq
-      if (mine) {
+      f4 accA = {0.f, 0.f, 0.f, 0.f}, accK = {0.f, 0.f, 0.f, 0.f};
+      // row side: key tiles below the row tile
+      for (int sk = 0; sk < mts; ++sk) {
 #pragma unroll
         for (int k = 0; k < 4; ++k) {
-          const int c = a0 + 4 * k + gq;
-          const float fr = ex2(sG[c * P + d] - ga);
-          xq[k] = sQ[c * P + d] * fr;
-          xk[k] = sK[c * P + d] * sB[c] * fr;
+          const int i = 16 * sk + 4 * k + gq;
+          const float kb = sK[i * P + d] * ex2(ga - sG[i * P + d]);   // k_i 2^(G_a - G_i)
+          accA = mfma4(sDA[(a0 + r16) * PC + 16 * sk + 4 * k + gq], kb, accA);
+          accK = mfma4(sDL[(a0 + r16) * PC + 16 * sk + 4 * k + gq], kb, accK);
         }
       }
-      if (mine && R > 0) {
+      // column side: row tiles above the key tile, the furthest first
+      float colS[4] = {0.f, 0.f, 0.f, 0.f};
+      for (int R = 3; R > mts; --R) {
+        const int aR = 16 * R;
+        const float gR = sG[aR * P + d];
+        f4 cS = {0.f, 0.f, 0.f, 0.f};
 #pragma unroll
-        for (int sk = 0; sk < R; ++sk) {
-          f4 cS = {0.f, 0.f, 0.f, 0.f};
-#pragma unroll
-          for (int k = 0; k < 4; ++k) {
-            const int i = 16 * sk + 4 * k + gq;
-            const float kb = sK[i * P + d] * ex2(ga - sG[i * P + d]);   // k_i 2^(G_a - G_i)
-            accA = mfma4(sDA[(a0 + r16) * PC + 16 * sk + 4 * k + gq], kb, accA);
-            accK = mfma4(sDL[(a0 + r16) * PC + 16 * sk + 4 * k + gq], kb, accK);
-            cS = mfma4(sDA[(a0 + 4 * k + gq) * PC + 16 * sk + r16], xq[k], cS);
-            cS = mfma4(sDL[(a0 + 4 * k + gq) * PC + 16 * sk + r16], xk[k], cS);
-          }
-#pragma unroll
-          for (int e = 0; e < 4; ++e)
-            colS[sk][e] += cS[e] * ex2(ga - sG[(16 * sk + 4 * gq + e) * P + d]);
+        for (int k = 0; k < 4; ++k) {
+          const int c = aR + 4 * k + gq;
+          const float fr = ex2(sG[c * P + d] - gR);   // q_c 2^(G_c - G_R), beta_c k_c 2^(G_c - G_R)
+          cS = mfma4(sDA[c * PC + a0 + r16], sQ[c * P + d] * fr, cS);
+          cS = mfma4(sDL[c * PC + a0 + r16], sK[c * P + d] * sB[c] * fr, cS);
         }
+#pragma unroll
+        for (int e = 0; e < 4; ++e) colS[e] += cS[e] * ex2(gR - sG[(a0 + 4 * gq + e) * P + d]);
       }
-      if (mine) {
-        float gc[4], rA[4], rK[4], cS[4];
+      float gc[4], rA[4], rK[4], cS[4];
 #pragma unroll
-        for (int e = 0; e < 4; ++e) {
-          gc[e] = sG[(a0 + 4 * gq + e) * P + d];
-          rA[e] = rK[e] = cS[e] = 0.f;
+      for (int e = 0; e < 4; ++e) {
+        gc[e] = sG[(a0 + 4 * gq + e) * P + d];
+        rA[e] = rK[e] = cS[e] = 0.f;
+      }
+      // The diagonal tile on the matrix cores, anchored at its first row a
+      // like the off-diagonal ones: row side (block) x (k_y 2^(G_a - G_y)),
+      // column side (block)^T x (q_c 2^(G_c - G_a)), times 2^(G_c - G_a) and
+      // 2^(G_a - G_i) afterwards.  Key factors here are >= 1, up to the
+      // tile's decay in the column; the masked cotangents zero every pair
+      // whose factor would exceed 1 overall.  A tile that decays by more
+      // than 2^-kDiagAnchorLog2 in one of the wave's columns (the factors
+      // would leave fp32 headroom for the cotangents) takes the per-element
+      // form below.
+      if (!__any(ga - sG[(a0 + 15) * P + d] > kDiagAnchorLog2)) {
+        f4 cd = {0.f, 0.f, 0.f, 0.f};
+#pragma unroll
+        for (int k = 0; k < 4; ++k) {
+          const int y = a0 + 4 * k + gq;
+          const float fr = ex2(sG[y * P + d] - ga);
+          const float kb = sK[y * P + d] * ex2(ga - sG[y * P + d]);   // k_y 2^(G_a - G_y)
+          accA = mfma4(sDA[(a0 + r16) * PC + y], kb, accA);
+          accK = mfma4(sDL[(a0 + r16) * PC + y], kb, accK);
+          cd = mfma4(sDA[y * PC + a0 + r16], sQ[y * P + d] * fr, cd);
+          cd = mfma4(sDL[y * PC + a0 + r16], sK[y * P + d] * sB[y] * fr, cd);
         }
-        // The diagonal tile on the matrix cores, anchored at its first row a
-        // like the off-diagonal ones: row side (block) x (k_y 2^(G_a - G_y)),
-        // column side (block)^T x (q_c 2^(G_c - G_a)), times 2^(G_c - G_a) and
-        // 2^(G_a - G_i) afterwards.  Key factors here are >= 1, up to the
-        // tile's decay in the column; the masked cotangents zero every pair
-        // whose factor would exceed 1 overall.  A tile that decays by more
-        // than 2^-kDiagAnchorLog2 in one of the wave's columns (the factors
-        // would leave fp32 headroom for the cotangents) takes the per-element
-        // form below.
-        if (!__any(ga - sG[(a0 + 15) * P + d] > kDiagAnchorLog2)) {
-          f4 cd = {0.f, 0.f, 0.f, 0.f};
 #pragma unroll
-          for (int k = 0; k < 4; ++k) {
-            const int y = a0 + 4 * k + gq;
-            const float kb = sK[y * P + d] * ex2(ga - sG[y * P + d]);   // k_y 2^(G_a - G_y)
-            accA = mfma4(sDA[(a0 + r16) * PC + y], kb, accA);
-            accK = mfma4(sDL[(a0 + r16) * PC + y], kb, accK);
-            cd = mfma4(sDA[y * PC + a0 + r16], xq[k], cd);
-            cd = mfma4(sDL[y * PC + a0 + r16], xk[k], cd);
-          }
-#pragma unroll
-          for (int e = 0; e < 4; ++e) cS[e] = cd[e] * ex2(ga - gc[e]);
-        } else {
+        for (int e = 0; e < 4; ++e) cS[e] = cd[e] * ex2(ga - gc[e]);
+      } else {
         // With G non-increasing (g <= 0), the pair (c, a0 + y) of the row
         // side (y <= x) decays by 2^(G_c - G_y) and the pair (a0 + y, c) of
         // the column side (y >= x) by 2^(G_y - G_c): both are 2^-|G_c - G_y|,
@@ -2377,75 +2383,61 @@ __global__ __launch_bounds__(kChunkThreads) void kda_bwd_chunk_kernel(BwdArgs a)
             }
           }
         }
-        }
-        float gn[4];   // this tile's dG (zero on pad rows)
-#pragma unroll
-        for (int e = 0; e < 4; ++e) {
-          const int c = a0 + 4 * gq + e;
-          const float kc = sK[c * P + d], qc = sQ[c * P + d], bc = sB[c];
-          const float f = ex2(gc[e] - ga);   // accA, accK: every tile pair but a per-element diagonal
-          rA[e] = fmaf(accA[e], f, rA[e]);
-          rK[e] = fmaf(accK[e], f, rK[e]);
-          if (R < 3) cS[e] += colS[R < 3 ? R : 0][e];
-          dbq[R][e] = rK[e] * kc;
-          gn[e] = (c < cr.len) ? oG[e] + rA[e] * qc + rK[e] * kc * bc - cS[e] * kc : 0.f;
-          if (c < cr.len) {
-            const int64_t o = in_idx(c, d);
-            gq_[o] = oq[e] + rA[e] * a.scale;
-            gk_[o] = ok[e] + rK[e] * bc + cS[e];
-          }
-        }
-        // reverse cumsum down the column: within the lane's four rows, then
-        // over the row groups gq' > gq of the tile (lanes 16 gq' + r16), then
-        // the tiles already finished
-        float sfx[4];
-        sfx[3] = gn[3];
-        sfx[2] = gn[2] + sfx[3];
-        sfx[1] = gn[1] + sfx[2];
-        sfx[0] = gn[0] + sfx[1];
-        const float x1 = __shfl_down(sfx[0], 16, 64), x2 = __shfl_down(sfx[0], 32, 64);
-        const float x3 = __shfl_down(sfx[0], 48, 64);
-        const float above = (gq < 3 ? x1 : 0.f) + (gq < 2 ? x2 : 0.f) + (gq < 1 ? x3 : 0.f);
-        const float tile = __shfl(sfx[0] + above, r16, 64);   // lane r16 is row group 0
-        const float base = sBase[d] + carry + above;
-#pragma unroll
-        for (int e = 0; e < 4; ++e) {
-          const int c = a0 + 4 * gq + e;
-          if (c < cr.len) gG_[in_idx(c, d)] = base + sfx[e];
-        }
-        carry += tile;
       }
-      asm volatile("" ::: "memory");   // keep each row tile's loads inside its iteration
-    }
-    if (mine) {
-      // dbeta partials: sum over the 16 columns of this wave's tile
+      float gn[4], dbq[4];   // this tile's dG (zero on pad rows), dbeta terms
 #pragma unroll
-      for (int R = 0; R < 4; ++R)
-#pragma unroll
-        for (int e = 0; e < 4; ++e) {
-          float v = dbq[R][e];
-#pragma unroll
-          for (int off = 8; off >= 1; off >>= 1) v += __shfl_xor(v, off, 64);
-          dbq[R][e] = v;
+      for (int e = 0; e < 4; ++e) {
+        const int c = a0 + 4 * gq + e;
+        const float kc = sK[c * P + d], qc = sQ[c * P + d], bc = sB[c];
+        const float f = ex2(gc[e] - ga);   // accA, accK: every tile pair but a per-element diagonal
+        rA[e] = fmaf(accA[e], f, rA[e]);
+        rK[e] = fmaf(accK[e], f, rK[e]);
+        if (mts < 3) cS[e] += colS[e];
+        dbq[e] = rK[e] * kc;
+        gn[e] = (c < cr.len) ? pG[q][e] + rA[e] * qc + rK[e] * kc * bc - cS[e] * kc : 0.f;
+        if (c < cr.len) {
+          const int64_t o = in_idx(c, d);
+          gq_[o] = pq[q][e] + rA[e] * a.scale;
+          gk_[o] = pk[q][e] + rK[e] * bc + cS[e];
         }
+      }
+      // reverse cumsum down the column: within the lane's four rows, then
+      // over the row groups gq' > gq of the tile (lanes 16 gq' + r16); the
+      // tiles below come after the barrier
+      sfx[q][3] = gn[3];
+      sfx[q][2] = gn[2] + sfx[q][3];
+      sfx[q][1] = gn[1] + sfx[q][2];
+      sfx[q][0] = gn[0] + sfx[q][1];
+      const float x1 = __shfl_down(sfx[q][0], 16, 64), x2 = __shfl_down(sfx[q][0], 32, 64);
+      const float x3 = __shfl_down(sfx[q][0], 48, 64);
+      abv[q] = (gq < 3 ? x1 : 0.f) + (gq < 2 ? x2 : 0.f) + (gq < 1 ? x3 : 0.f);
+      if (gq == 0) sTile[mt * D + d] = sfx[q][0] + abv[q];   // the tile's column sum
+      // dbeta partials: sum over the 16 columns of the tile
+#pragma unroll
+      for (int e = 0; e < 4; ++e) {
+        float v = dbq[e];
+#pragma unroll
+        for (int off = 8; off >= 1; off >>= 1) v += __shfl_xor(v, off, 64);
+        if (r16 == 0) sDb4[(a0 + 4 * gq + e) * 8 + dg_ * NDT + q] = v;
+      }
     }
-    __syncthreads();   // phase 4's LDS reads done; every position written
-    sDb4 = sm + kC * P + 16 * D + kC * 32;   // outputs' layout (below)
-    if (mine && r16 == 0) {
+    __syncthreads();   // phase 4's LDS reads done; every tile's column sums written
 #pragma unroll
-      for (int R = 0; R < 4; ++R)
+    for (int q = 0; q < NDT; ++q) {
+      const int d = 16 * (dg_ * NDT + q) + r16;
+      float carry = 0.f;   // the tiles below, the furthest first
+      for (int R = 3; R > mts; --R) carry += sTile[R * D + d];
+      const float base = sBase[d] + carry + abv[q];
 #pragma unroll
-        for (int e = 0; e < 4; ++e) sDb4[(16 * R + 4 * gq + e) * 8 + wv] = dbq[R][e];
+      for (int e = 0; e < 4; ++e) {
+        const int c = a0 + 4 * gq + e;
+        if (c < cr.len) gG_[in_idx(c, d)] = base + sfx[q][e];
+      }
     }
   }
 
-  // ---- outputs: dbeta (dg is final after phase 4)
+  // ---- outputs: dbeta (its row partial sums in LDS before phase 4's last barrier)
   {
-    float* sDbD = sm + kC * P + 16 * D;   // [64][32] row partial sums of dbeta (phase 2)
-    // sDb4 = sDbD + 64 * 32: [64][8] row partial sums of dbeta (phase 4), written above
-#pragma unroll
-    for (int i = 0; i < 4; ++i) sDbD[(16 * mt + 4 * gq + i) * 32 + 16 * dg_ + r16] = dbrD[i];
-    __syncthreads();
     if (t < kC && t < cr.len) {
       float acc = 0.f;
       for (int j = 0; j < NCT; ++j) acc += sDb4[t * 8 + j];
