@@ -402,32 +402,45 @@ __global__ __launch_bounds__(kPrepThreads, 4) void kda_bwd_prep_kernel(BwdArgs a
   };
 
   // scores: Aqk (c >= i) to the workspace, L = beta_c Akk (c > i) to LDS,
-  // accumulated over the channel halves.  Off-diagonal tile pairs (row tile
-  // R > key tile s) on the matrix cores, one pair per wave (waves 0..5), the
-  // decay factored at the row tile's first row a: 2^(G_c - G_i) =
-  // 2^(G_c - G_a) 2^(G_a - G_i), both <= 1, applied to each operand element as
-  // it is read.  Diagonal tiles take 2^(G_c - G_i) per element, (c, i) slots
-  // spread over all threads.
+  // accumulated over the channel halves on the matrix cores, one 16 x 16 tile
+  // pair per wave: waves 0..5 the off-diagonal pairs (row tile R > key tile
+  // s), waves 6 and 7 two diagonal tiles each.  The decay is factored at the
+  // row tile's first row a, 2^(G_c - G_i) = 2^(G_c - G_a) 2^(G_a - G_i), and
+  // applied to each operand element as it is read: both factors <= 1 off the
+  // diagonal; on it the key factor is >= 1, up to the tile's decay, and pairs
+  // where the product would exceed 1 are masked.  A diagonal tile that decays
+  // by more than 2^-kDiagAnchorLog2 in a channel of the half takes
+  // 2^(G_c - G_i) per element for that half instead (lane (r, gq) forming its
+  // own four outputs, rows 4 gq + e, key r).
   const int R_off = (wv < 1) ? 1 : (wv < 3) ? 2 : 3;
   const int sk_off = wv - R_off * (R_off - 1) / 2;
-  f4 accA = {0.f, 0.f, 0.f, 0.f}, accL = {0.f, 0.f, 0.f, 0.f};
-  float dA[2] = {0.f, 0.f}, dL[2] = {0.f, 0.f};
+  const int NPAIR = (wv < 6) ? 1 : 2;   // wave-uniform
+  auto pair_rs = [&](int pi, int& R, int& sk) {
+    if (wv < 6) { R = R_off; sk = sk_off; }
+    else { R = 2 * (wv - 6) + pi; sk = R; }
+  };
+  f4 accA[2], accL[2];
+#pragma unroll
+  for (int pi = 0; pi < 2; ++pi) accA[pi] = accL[pi] = f4{0.f, 0.f, 0.f, 0.f};
+  // the next half's q, k, g and beta, loaded during this half's scores
+  InTile<DTQ, D, HD, NTH> nq, nk;
+  InTile<DTG, D, HD, NTH> ng;
+  float nb = 0.f;
+  auto fetch_half = [&](int c0) {
+    nq.fetch(a.q, cr.row0, cr.len, H, h, c0);
+    nk.fetch(a.k, cr.row0, cr.len, H, h, c0);
+    ng.fetch(a.g, cr.row0, cr.len, H, h, c0);
+    const int tb = t & (kC - 1);
+    nb = ld1<DTG>(a.beta, (cr.row0 + (tb < cr.len ? tb : 0)) * H + h);
+  };
+  fetch_half(0);
   for (int hf = 0; hf < NHALF; ++hf) {
     const int c0 = HD * hf;
     if (hf > 0) __syncthreads();      // the previous half's reads are done
-    {   // q, k, g of the half and beta: every load issued before the stores
-      InTile<DTQ, D, HD, NTH> iq, ik;
-      InTile<DTG, D, HD, NTH> ig;
-      iq.fetch(a.q, cr.row0, cr.len, H, h, c0);
-      ik.fetch(a.k, cr.row0, cr.len, H, h, c0);
-      ig.fetch(a.g, cr.row0, cr.len, H, h, c0);
-      const int tb = t & (kC - 1);
-      const float bv = ld1<DTG>(a.beta, (cr.row0 + (tb < cr.len ? tb : 0)) * H + h);
-      iq.template put<P>(sQ, a.scale);
-      ik.template put<P>(sK, 1.f);
-      ig.template put<P>(sG, 1.f);
-      if (hf == 0 && t < kC) sB[t] = (t < cr.len) ? bv : 0.f;
-    }
+    nq.template put<P>(sQ, a.scale);
+    nk.template put<P>(sK, 1.f);
+    ng.template put<P>(sG, 1.f);
+    if (hf == 0 && t < kC) sB[t] = (t < cr.len) ? nb : 0.f;
     __syncthreads();
     cumsum_g();
     __syncthreads();
@@ -473,66 +486,79 @@ __global__ __launch_bounds__(kPrepThreads, 4) void kda_bwd_prep_kernel(BwdArgs a
       }
       if (t < HD) a.GCV[ch * D + c0 + t] = ex2(sG[(kC - 1) * P + t]);
     }
-    if (wv < 6) {
-      const int a0 = 16 * R_off, i = 16 * sk_off + r16;
-#pragma unroll 8
-      for (int k = 0; k < HD / 4; ++k) {
-        const int d = 4 * k + gq;
-        const float ga = sG[a0 * P + d];
-        const float fa = ex2(sG[(a0 + r16) * P + d] - ga);
-        const float bk = sK[i * P + d] * ex2(ga - sG[i * P + d]);
-        accA = mfma4(sQ[(a0 + r16) * P + d] * fa, bk, accA);
-        accL = mfma4(sK[(a0 + r16) * P + d] * fa, bk, accL);
+    if (hf + 1 < NHALF) fetch_half(c0 + HD);
+#pragma unroll
+    for (int pi = 0; pi < 2; ++pi) {
+      if (pi >= NPAIR) break;
+      int R, sk;
+      pair_rs(pi, R, sk);
+      const int a0 = 16 * R, i = 16 * sk + r16;
+      // a diagonal tile decaying past the anchor's range in a channel of the half
+      bool far = false;
+      if (R == sk) {
+#pragma unroll
+        for (int k = 0; k < HD / 4; ++k) {
+          const int d = 4 * k + gq;
+          far |= sG[a0 * P + d] - sG[(a0 + 15) * P + d] > kDiagAnchorLog2;
+        }
       }
-    }
+      if (!__any(far)) {
+#pragma unroll 8
+        for (int k = 0; k < HD / 4; ++k) {
+          const int d = 4 * k + gq;
+          const float ga = sG[a0 * P + d];
+          const float fa = ex2(sG[(a0 + r16) * P + d] - ga);
+          const float bk = sK[i * P + d] * ex2(ga - sG[i * P + d]);
+          accA[pi] = mfma4(sQ[(a0 + r16) * P + d] * fa, bk, accA[pi]);
+          accL[pi] = mfma4(sK[(a0 + r16) * P + d] * fa, bk, accL[pi]);
+        }
+      } else {
 #pragma unroll
-    for (int j = 0; j < 2; ++j) {
-      const int p = t + NTH * j;               // 4 diagonal tiles x 256 slots
-      const int R = p >> 8, rc = (p >> 4) & 15, ri = p & 15;
-      const int c = 16 * R + rc, i = 16 * R + ri;
-      if (ri <= rc) {
+        for (int e = 0; e < 4; ++e) {
+          const int c = a0 + 4 * gq + e;
+          if (r16 > 4 * gq + e) continue;   // above the diagonal (masked below)
+          float sA = 0.f, sL4 = 0.f;
 #pragma unroll 2
-        for (int d4 = 0; d4 < HD; d4 += 4) {
-          const float4 kI = *reinterpret_cast<const float4*>(&sK[i * P + d4]);
-          const float4 gI = *reinterpret_cast<const float4*>(&sG[i * P + d4]);
-          const float4 gC = *reinterpret_cast<const float4*>(&sG[c * P + d4]);
-          const float4 qC = *reinterpret_cast<const float4*>(&sQ[c * P + d4]);
-          const float4 kC4 = *reinterpret_cast<const float4*>(&sK[c * P + d4]);
-          const float ki[4] = {kI.x * ex2(gC.x - gI.x), kI.y * ex2(gC.y - gI.y), kI.z * ex2(gC.z - gI.z),
-                               kI.w * ex2(gC.w - gI.w)};
-          const float qc[4] = {qC.x, qC.y, qC.z, qC.w}, kc[4] = {kC4.x, kC4.y, kC4.z, kC4.w};
+          for (int d4 = 0; d4 < HD; d4 += 4) {
+            const float4 kI = *reinterpret_cast<const float4*>(&sK[i * P + d4]);
+            const float4 gI = *reinterpret_cast<const float4*>(&sG[i * P + d4]);
+            const float4 gC = *reinterpret_cast<const float4*>(&sG[c * P + d4]);
+            const float4 qC = *reinterpret_cast<const float4*>(&sQ[c * P + d4]);
+            const float4 kC4 = *reinterpret_cast<const float4*>(&sK[c * P + d4]);
+            const float ki[4] = {kI.x * ex2(gC.x - gI.x), kI.y * ex2(gC.y - gI.y), kI.z * ex2(gC.z - gI.z),
+                                 kI.w * ex2(gC.w - gI.w)};
+            const float qc[4] = {qC.x, qC.y, qC.z, qC.w}, kc[4] = {kC4.x, kC4.y, kC4.z, kC4.w};
 #pragma unroll
-          for (int e = 0; e < 4; ++e) {
-            dA[j] = fmaf(qc[e], ki[e], dA[j]);
-            dL[j] = fmaf(kc[e], ki[e], dL[j]);
+            for (int x = 0; x < 4; ++x) {
+              sA = fmaf(qc[x], ki[x], sA);
+              sL4 = fmaf(kc[x], ki[x], sL4);
+            }
           }
+          accA[pi][e] += sA;
+          accL[pi][e] += sL4;
         }
       }
     }
   }
   const int64_t aq0 = ch * kC * kC;
-  if (wv < 6) {
-    const int a0 = 16 * R_off, i = 16 * sk_off + r16;
+#pragma unroll
+  for (int pi = 0; pi < 2; ++pi) {
+    if (pi >= NPAIR) break;
+    int R, sk;
+    pair_rs(pi, R, sk);
+    const int a0 = 16 * R, i = 16 * sk + r16;
+    f4 vA;
 #pragma unroll
     for (int e = 0; e < 4; ++e) {
       const int c = a0 + 4 * gq + e;
-      if constexpr (EF == 0) ws_st<EF>(a.AQ, aq0 + c * kC + i, accA[e]);
-      sL[c * PC + i] = accL[e] * sB[c];
+      const bool diag = R == sk;
+      vA[e] = (!diag || r16 <= 4 * gq + e) ? accA[pi][e] : 0.f;   // Aqk: i <= c
+      if constexpr (EF == 0) ws_st<EF>(a.AQ, aq0 + c * kC + i, vA[e]);
+      sL[c * PC + i] = (!diag || r16 < 4 * gq + e) ? accL[pi][e] * sB[c] : 0.f;   // L: i < c
     }
-    if constexpr (EF != 0)   // Aqk^T fragment (key tile sk_off, K step R_off / 2), half R_off % 2
-      *reinterpret_cast<uint2*>(static_cast<u16*>(a.FA) + ((ch * 6 + fa_frag(sk_off, R_off >> 1)) * 64 + l) * 8 +
-                                4 * (R_off & 1)) = pack_f16x4(accA);
-  }
-#pragma unroll
-  for (int j = 0; j < 2; ++j) {
-    const int p = t + NTH * j;
-    const int R = p >> 8, rc = (p >> 4) & 15, ri = p & 15;
-    const int c = 16 * R + rc, i = 16 * R + ri;
-    if constexpr (EF == 0) ws_st<EF>(a.AQ, aq0 + c * kC + i, (ri <= rc) ? dA[j] : 0.f);
-    else   // diagonal tile R: Aqk^T fragment (R, R / 2), lane ri + 16 (rc / 4), element 4 (R % 2) + rc % 4
-      static_cast<_Float16*>(a.FA)[((ch * 6 + fa_frag(R, R >> 1)) * 64 + ri + 16 * (rc >> 2)) * 8 + 4 * (R & 1) +
-                                   (rc & 3)] = static_cast<_Float16>((ri <= rc) ? dA[j] : 0.f);
-    sL[c * PC + i] = (ri < rc) ? dL[j] * sB[c] : 0.f;
+    if constexpr (EF != 0)   // Aqk^T fragment (key tile sk, K step R / 2), half R % 2
+      *reinterpret_cast<uint2*>(static_cast<u16*>(a.FA) + ((ch * 6 + fa_frag(sk, R >> 1)) * 64 + l) * 8 +
+                                4 * (R & 1)) = pack_f16x4(vA);
   }
   // blocks above the diagonal: zero
   for (int e = t; e < 6 * 256; e += NTH) {
