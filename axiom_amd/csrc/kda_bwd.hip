@@ -1975,12 +1975,21 @@ __global__ __launch_bounds__(kChunkThreads) void kda_bwd_chunk_kernel(BwdArgs a)
   float* const sAcc = sm + ACC0;   // [2][64][D]: dk, dG
   static_assert(ACC0 + 2 * kC * D <= SMEM_FLOATS, "phase 1 -> 2 accumulators");
 
-  // ---- phase 1: dY = v~ dS'^T, dgq = do S^T, dW = -dv~ S^T (K = dv in passes of HW)
+  // ---- phase 1: dY = v~ dS'^T, dgq = do S^T, dW = -dv~ S^T, dAqk = do v~^T
+  // (K = dv in passes of HW)
   // The operands go to LDS as hi / lo bf16 planes (K contiguous) and each
   // product runs as three bf16 MFMAs per 32-wide K block (hi hi + hi lo +
   // lo hi, about 2^-16 of each product dropped); dW accumulates +dv~ S^T and
   // is negated where phase 2 takes it.
   f4 dW[NDT];
+  // dAqk = tril(do v~^T), two 16 x 16 tiles per wave (row tile mt, key tiles
+  // 2 (wv % 2) + q), from phase 1's do and v~ planes: K = the value channels
+  // of each pass; key tiles above the row tile are skipped (masked in phase 3)
+  f4 dAa[2];
+  const int kt0 = 2 * (wv & 1);
+  const bool live0 = kt0 <= mts, live1 = kt0 + 1 <= mts;   // wave-uniform
+#pragma unroll
+  for (int q = 0; q < 2; ++q) dAa[q] = f4{0.f, 0.f, 0.f, 0.f};
   TTile<kC, NTH, EF> tT;     // phase 2's T, loaded during phase 1's last pass
   // dv~ in row pairs: column block hp is phase 1's pass hp operand, and the
   // whole tile phase 2's dv~^T (one read of dv~ serves both)
@@ -2043,6 +2052,15 @@ __global__ __launch_bounds__(kChunkThreads) void kda_bwd_chunk_kernel(BwdArgs a)
           dgq[q] = mma3_bf16(dgq[q], oh, ol, sh, sl);
           dW[q] = mma3_bf16(dW[q], uh, ul, sh, sl);
         }
+        if (live0) {
+#pragma unroll
+          for (int q = 0; q < 2; ++q) {
+            if (q == 1 && !live1) continue;
+            const int kv = (16 * (kt0 + q) + r16) * PB + 32 * kb + 8 * gq;
+            dAa[q] = mma3_bf16(dAa[q], oh, ol, *reinterpret_cast<const b8*>(&sVh[kv]),
+                               *reinterpret_cast<const b8*>(&sVl[kv]));
+          }
+        }
       }
       if (t < D) {
 #pragma unroll 2
@@ -2076,7 +2094,7 @@ __global__ __launch_bounds__(kChunkThreads) void kda_bwd_chunk_kernel(BwdArgs a)
         const float gam = ex2(gH[q][i]), lam = ex2(gLast[q] - gH[q][i]);
         const float dz = dY[q][i] * hget(kH[q], i) * lam;
         dzp[q] += dz;
-        if (c < cr.len) gq_[in_idx(c, d)] = dgq[q][i] * gam * a.scale;
+        pq[q][i] = dgq[q][i] * gam * a.scale;
         sAcc[c * D + d] = dY[q][i] * lam;
         sAcc[(kC + c) * D + d] = dgq[q][i] * (hget(qH[q], i) * a.scale) * gam - dz;
       }
@@ -2163,8 +2181,8 @@ __global__ __launch_bounds__(kChunkThreads) void kda_bwd_chunk_kernel(BwdArgs a)
     __syncthreads();   // sAcc read before phase 3's operands overwrite it
   }
 
-  // ---- phase 3: dL = strict(-(Yw W^T + Yu U^T)), dAqk = tril(do v~^T); [64][64]
-  // outputs, two 16 x 16 tiles per wave: row tile mt, key tiles 2 (wv % 2) + q,
+  // ---- phase 3: dL = strict(-(Yw W^T + Yu U^T)) [64][64] (dAqk came from
+  // phase 1), two 16 x 16 tiles per wave: row tile mt, key tiles 2 (wv % 2) + q,
   // as bf16 hi / lo triples (operands row-major with the channel, the K index,
   // contiguous); key tiles above the row tile are masked to zero and skipped.
   Tile<kC, D, NTH> tG4;                  // phase 4's G, loaded at the end of phase 3
@@ -2183,9 +2201,9 @@ __global__ __launch_bounds__(kChunkThreads) void kda_bwd_chunk_kernel(BwdArgs a)
   {
     constexpr int PB = D + 8;            // bf16 pitch: 16-byte aligned K blocks, rows 4 banks apart
     static_assert(8 * kC * PB / 2 <= SMEM_FLOATS, "phase 3 LDS");
-    __bf16* const sAh = reinterpret_cast<__bf16*>(sm);   // Yw, then do
+    __bf16* const sAh = reinterpret_cast<__bf16*>(sm);   // Yw
     __bf16* const sAl = sAh + kC * PB;
-    __bf16* const sBh = sAl + kC * PB;                   // Yu, then v~
+    __bf16* const sBh = sAl + kC * PB;                   // Yu
     __bf16* const sBl = sBh + kC * PB;
     __bf16* const sWh = sBl + kC * PB;
     __bf16* const sWl = sWh + kC * PB;
@@ -2205,17 +2223,10 @@ __global__ __launch_bounds__(kChunkThreads) void kda_bwd_chunk_kernel(BwdArgs a)
 #pragma unroll
     for (int i = 0; i < 4; ++i) sDbD[(16 * mt + 4 * gq + i) * 32 + 16 * dg_ + r16] = dbrD[i];
     __syncthreads();
-    f4 dLa[2], dAa[2];
+    f4 dLa[2];
 #pragma unroll
-    for (int q = 0; q < 2; ++q)
-#pragma unroll
-      for (int i = 0; i < 4; ++i) dLa[q][i] = dAa[q][i] = 0.f;
-    const int kt0 = 2 * (wv & 1);
-    const bool live0 = kt0 <= mts, live1 = kt0 + 1 <= mts;   // wave-uniform
-    InTile<DO, D, D, NTH> tDo;            // do and v~ for dAqk, during the dL products
-    Tile<kC, D, NTH> tVt;
-    tDo.fetch(a.dout, cr.row0, cr.len, H, h, 0);
-    tVt.fetch(a.VT + ch * kC * D, D, 0);
+    for (int q = 0; q < 2; ++q) dLa[q] = f4{0.f, 0.f, 0.f, 0.f};
+    tG4.fetch(GL, D, 0);   // phase 4's G, during the products
     if (live0) {
 #pragma unroll 2
       for (int kb = 0; kb < D / 32; ++kb) {
@@ -2233,26 +2244,6 @@ __global__ __launch_bounds__(kChunkThreads) void kda_bwd_chunk_kernel(BwdArgs a)
         }
       }
     }
-    __syncthreads();
-    // do and v~ into the Yw / Yu slots
-    put_hl<PB>(tDo, sAh, sAl);
-    put_hl<PB>(tVt, sBh, sBl);
-    __syncthreads();
-    if (live0) {
-#pragma unroll
-      for (int kb = 0; kb < D / 32; ++kb) {
-        const int ka = (16 * mt + r16) * PB + 32 * kb + 8 * gq;
-        const b8 oh = *reinterpret_cast<const b8*>(&sAh[ka]), ol = *reinterpret_cast<const b8*>(&sAl[ka]);
-#pragma unroll
-        for (int q = 0; q < 2; ++q) {
-          if (q == 1 && !live1) continue;
-          const int kbb = (16 * (kt0 + q) + r16) * PB + 32 * kb + 8 * gq;
-          dAa[q] = mma3_bf16(dAa[q], oh, ol, *reinterpret_cast<const b8*>(&sBh[kbb]),
-                             *reinterpret_cast<const b8*>(&sBl[kbb]));
-        }
-      }
-    }
-    tG4.fetch(GL, D, 0);   // phase 4's G
     __syncthreads();   // every read of the planes done before sDL, sDA overwrite them
     // phase 4's masked operands
 #pragma unroll
@@ -2304,15 +2295,6 @@ __global__ __launch_bounds__(kChunkThreads) void kda_bwd_chunk_kernel(BwdArgs a)
       for (int r = 0; r < 16; ++r) acc += sRed4[r * D + t];
       sBase[t] = acc;
     }
-    // phase 1's dq terms (stored there: registers are short through phases 2
-    // and 3), loaded during the LDS fill
-#pragma unroll
-    for (int q = 0; q < NDT; ++q)
-#pragma unroll
-      for (int e = 0; e < 4; ++e) {
-        const int c = 16 * mt + 4 * gq + e;
-        pq[q][e] = gq_[in_idx(c < cr.len ? c : 0, 16 * (dg_ * NDT + q) + r16)];
-      }
     __syncthreads();
     float* const sTile = sRed4;      // [4][D] dG column sums of each row tile (sRed4 is read above)
     const int a0 = 16 * mt;
