@@ -2185,7 +2185,6 @@ __global__ __launch_bounds__(kChunkThreads) void kda_bwd_chunk_kernel(BwdArgs a)
   // phase 1), two 16 x 16 tiles per wave: row tile mt, key tiles 2 (wv % 2) + q,
   // as bf16 hi / lo triples (operands row-major with the channel, the K index,
   // contiguous); key tiles above the row tile are masked to zero and skipped.
-  Tile<kC, D, NTH> tG4;                  // phase 4's G, loaded at the end of phase 3
   float* const sDL = sm;                 // phase 4's operands, written at the end of phase 3
   float* const sDA = sDL + kC * PC;
   // past phase 4's dL, dAqk, q, k, G, beta: [16][D] dz partials, then the
@@ -2226,7 +2225,6 @@ __global__ __launch_bounds__(kChunkThreads) void kda_bwd_chunk_kernel(BwdArgs a)
     f4 dLa[2];
 #pragma unroll
     for (int q = 0; q < 2; ++q) dLa[q] = f4{0.f, 0.f, 0.f, 0.f};
-    tG4.fetch(GL, D, 0);   // phase 4's G, during the products
     if (live0) {
 #pragma unroll 2
       for (int kb = 0; kb < D / 32; ++kb) {
@@ -2287,8 +2285,8 @@ __global__ __launch_bounds__(kChunkThreads) void kda_bwd_chunk_kernel(BwdArgs a)
         const int o = (16 * mt + 4 * gq + i) * P + 16 * (dg_ * NDT + q) + r16;
         sQ[o] = hget(qH[q], i) * a.scale;
         sK[o] = hget(kH[q], i);
+        sG[o] = gH[q][i];
       }
-    tG4.template put<P>(sG);
     if (t < kC) sB[t] = ld_b(t);
     if (t < D) {   // dg[c] = base + sum_{c' >= c} dG[c']: the G_C terms and the dz terms
       float acc = dgc * ex2(GL[(kC - 1) * D + t]);
