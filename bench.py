@@ -259,7 +259,7 @@ def bench_backward(args, fwd_inputs, device):
     dht = torch.randn(B, H, dk, dv, device=device, generator=gen) * 0.1
     ws = torch.empty(kmod.chunk_bwd_workspace_bytes(B, T, H, dk, dv), dtype=torch.uint8, device=device)
     stream = torch.cuda.current_stream(device)
-    for _ in range(2):
+    for _ in range(5):
         axiom_amd.kda_chunk_bwd(q, k, v, g, beta, do, dht=dht, workspace=ws)
     torch.cuda.synchronize()
     e0, e1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
@@ -273,8 +273,10 @@ def bench_backward(args, fwd_inputs, device):
     gbps = nbytes / t_call / 1e9
     return dict(us_per_call=t_call * 1e6, tokens_per_s=B * T / t_call, calls=args.bwd_steps,
                 roofline={"bound": "hbm", "achieved": gbps, "peak": HBM_PEAK_GBPS, "unit": "GB/s",
-                          "frac": gbps / HBM_PEAK_GBPS, "algorithmic_bytes_per_call": nbytes},
-                kernels="kda_bwd_prep + kda_bwd_fscan + kda_bwd_rscan + kda_bwd_chunk (fp32 arithmetic, bf16 hi/lo products)",
+                          "frac": gbps / HBM_PEAK_GBPS, "algorithmic_bytes_per_call": nbytes,
+                          "traffic": measured_traffic("backward_traffic_bytes_per_call")},
+                kernels="kda_bwd_prep + kda_bwd_fscan16 + kda_bwd_rscan16 + kda_bwd_chunk (fp16 forward-side "
+                        "workspace, fp32 cotangents; fp16 and bf16 hi/lo products)",
                 config="B4 T4096 H16 d128 bf16 inputs, fp32 do and dht, zero h0")
 
 
@@ -630,7 +632,7 @@ def main():
     ap.add_argument("--cpu-seconds", type=float, default=10.0)
     ap.add_argument("--no-cpu-baseline", action="store_true")
     ap.add_argument("--no-decode", action="store_true")
-    ap.add_argument("--bwd-steps", type=int, default=5)
+    ap.add_argument("--bwd-steps", type=int, default=20)
     ap.add_argument("--no-backward", action="store_true")
     ap.add_argument("--no-other-configs", action="store_true",
                     help="skip the forward at configs 2 and 3")
