@@ -270,7 +270,12 @@ KDA_API size_t kda_cc_scan_bwd_batched_workspace(int B, int T, int H, int dk, in
  * when dh0 is not null, dh0 [B,H,dk,dv].  dg is the cotangent of the log
  * decay g (the reference's alpha form has dalpha = dg / alpha).  q, k, v, g,
  * beta, in_dtype, scale and chunk as in kda_chunk_fwd; the workspace is
- * caller-owned, kda_chunk_bwd_workspace bytes.
+ * caller-owned, kda_chunk_bwd_workspace bytes.  Precision: fp32 inputs keep
+ * an fp32 workspace (gradients within 1e-4 relative of an fp64 reference);
+ * 16-bit inputs store the forward-side intermediates (gamma q, lambda k, Aqk,
+ * T, W and each chunk's incoming state) in fp16, the width the forward gives
+ * them, with the cotangents, U and v~ kept fp32 (within 1e-3 relative of an
+ * fp64 reference, 1e-4 of an emulation of those roundings).
  */
 KDA_API int kda_chunk_bwd(hipStream_t stream,
                 const void* q, const void* k, const void* v, const void* g, const void* beta,
