@@ -1866,7 +1866,17 @@ struct WnTile {
 };
 
 // ---------------------------------------------------------------------------
-// per chunk-head adjoint
+// per chunk-head adjoint: one 512-thread workgroup per chunk-head, four
+// phases separated by workgroup barriers, every phase in the same thread
+// mapping so the partial dq, dk, dG stay in registers and each output is
+// stored once:
+//   1  dY = v~ dS'^T, dgq = do S^T, dW = dv~ S^T, dAqk = do v~^T (two
+//      passes over the value channels); the epilogue forms dq's and dk's
+//      terms and dG's first terms
+//   2  Yw = T^T (-dW), Yu = T^T dv~; dv, dbeta's first terms, dk and dG
+//   3  dL = -(Yw W^T + Yu U^T)
+//   4  the score adjoints of the wave's row tile (row side) and key tile
+//      (column side); dg's reverse cumsum; dq, dk, dg, dbeta stored
 // ---------------------------------------------------------------------------
 template <int D, int DTQ, int DTG, int DO>
 __global__ __launch_bounds__(kChunkThreads) void kda_bwd_chunk_kernel(BwdArgs a) {
