@@ -575,7 +575,7 @@ hipError_t launch_cc_finish(const CcFinishArgs& a, hipStream_t s) {
 // Backward workspace: arrays per chunk-head (see kda_internal.h: BwdArgs),
 // sized for fp32; the fragment arrays FL, FA, FQ, FW (fp16) serve 16-bit inputs.
 struct BwdLayout {
-  size_t GL, QG, KL, GCV, AQ, TM, WM, UM, SI, VT, DS, DVT, FL, FA, FQ, FW, FWN, FLT, total;
+  size_t QG, KL, GCV, AQ, TM, WM, UM, SI, VT, DS, DVT, FL, FA, FQ, FW, FWN, FLT, total;
 };
 
 BwdLayout bwd_layout(int B, int T, int H, int d) {
@@ -584,7 +584,6 @@ BwdLayout bwd_layout(int B, int T, int H, int d) {
   size_t off = 0;
   auto take = [&](size_t bytes) { size_t at = off; off = align_up(off + bytes); return at; };
   const size_t cd = ch * kC * d * 4, cc = ch * kC * kC * 4, dd = ch * d * d * 4;
-  L.GL = take(cd);
   L.QG = take(cd);
   L.KL = take(cd);
   L.GCV = take(ch * d * 4);
@@ -905,7 +904,6 @@ int kda_chunk_bwd(hipStream_t stream, const void* q, const void* k, const void* 
   a.q = q; a.k = k; a.v = v; a.g = g; a.beta = beta;
   a.h0 = h0; a.dout = dout; a.dht = dht; a.scale = scale;
   a.dq = dq; a.dk = dk; a.dv = dv; a.dg = dg; a.dbeta = dbeta; a.dh0 = dh0;
-  a.GL = reinterpret_cast<float*>(ws + L.GL);
   a.QG = reinterpret_cast<float*>(ws + L.QG);
   a.KL = reinterpret_cast<float*>(ws + L.KL);
   a.GCV = reinterpret_cast<float*>(ws + L.GCV);

@@ -445,25 +445,23 @@ __global__ __launch_bounds__(kPrepThreads, 4) void kda_bwd_prep_kernel(BwdArgs a
     cumsum_g();
     __syncthreads();
     {
-      const int64_t base = ch * kC * D + c0;
-      float* GL = a.GL + base;
-      constexpr int V4 = HD / 4;      // float4 groups per row
-      for (int e = t; e < kC * V4; e += NTH) {
-        const int c = e / V4, d = 4 * (e - c * V4);
-        const float4 gl = *reinterpret_cast<const float4*>(&sG[c * P + d]);
-        const float4 gz = *reinterpret_cast<const float4*>(&sG[(kC - 1) * P + d]);
-        const float4 qv = *reinterpret_cast<const float4*>(&sQ[c * P + d]);
-        const float4 kv = *reinterpret_cast<const float4*>(&sK[c * P + d]);
-        const float4 qg = make_float4(ex2(gl.x) * qv.x, ex2(gl.y) * qv.y, ex2(gl.z) * qv.z, ex2(gl.w) * qv.w);
-        const float4 kl = make_float4(ex2(gz.x - gl.x) * kv.x, ex2(gz.y - gl.y) * kv.y, ex2(gz.z - gl.z) * kv.z,
-                                      ex2(gz.w - gl.w) * kv.w);
-        *reinterpret_cast<float4*>(&GL[c * D + d]) = gl;
-        if constexpr (EF == 0) {
+      if constexpr (EF == 0) {
+        // gamma q and lambda k, row-major
+        const int64_t base = ch * kC * D + c0;
+        constexpr int V4 = HD / 4;      // float4 groups per row
+        for (int e = t; e < kC * V4; e += NTH) {
+          const int c = e / V4, d = 4 * (e - c * V4);
+          const float4 gl = *reinterpret_cast<const float4*>(&sG[c * P + d]);
+          const float4 gz = *reinterpret_cast<const float4*>(&sG[(kC - 1) * P + d]);
+          const float4 qv = *reinterpret_cast<const float4*>(&sQ[c * P + d]);
+          const float4 kv = *reinterpret_cast<const float4*>(&sK[c * P + d]);
+          const float4 qg = make_float4(ex2(gl.x) * qv.x, ex2(gl.y) * qv.y, ex2(gl.z) * qv.z, ex2(gl.w) * qv.w);
+          const float4 kl = make_float4(ex2(gz.x - gl.x) * kv.x, ex2(gz.y - gl.y) * kv.y, ex2(gz.z - gl.z) * kv.z,
+                                        ex2(gz.w - gl.w) * kv.w);
           ws_st4<EF>(a.QG, base + c * D + d, qg);
           ws_st4<EF>(a.KL, base + c * D + d, kl);
         }
-      }
-      if constexpr (EF != 0) {
+      } else {
         // the reverse scan's A fragments of this half's channels, one lane
         // fragment per thread each (the slot order of kda_internal.h)
         static_assert(NTH == 512 && HD == 64, "one (gamma q)^T and one lambda k lane fragment per thread");
@@ -1887,18 +1885,20 @@ __global__ __launch_bounds__(kChunkThreads) void kda_bwd_chunk_kernel(BwdArgs a)
   constexpr int HW = 64;             // value columns per pass of phase 1
   constexpr int NH = D / HW;
   // LDS of the largest phase: phase 1's bf16 planes, phase 2's planes plus
-  // the dk, dG hand-off, phase 3's planes, phase 4's dL, dAqk [64][PC] and
-  // q, k, G [64][P] plus beta
+  // the dk, dG hand-off and the row tiles' sums of g, phase 3's planes,
+  // phase 4's dL, dAqk [64][PC] and q, k, G [64][P] plus beta
   constexpr int ACC0 = (2 * kC + 4 * D) * (kC + 8) / 2;   // floats of phase 2's bf16 planes
-  constexpr int SMEM_FLOATS = cmax(cmax((6 * kC + 4 * D) * (HW + 8) / 2, ACC0 + 2 * kC * D),
-                                   cmax(8 * kC * (D + 8) / 2, 2 * kC * PC + 3 * kC * P + kC + 17 * D + 40 * kC));
+  constexpr int P4 = 2 * kC * PC + 3 * kC * P + kC + 17 * D + 40 * kC;   // floats of phase 4
+  // [4][D] row tiles' sums of g, from phase 1's epilogue to phase 4: past
+  // every buffer of phases 2 to 4
+  constexpr int GS0 = cmax(ACC0 + 2 * kC * D, P4);
+  constexpr int SMEM_FLOATS = cmax(cmax((6 * kC + 4 * D) * (HW + 8) / 2, GS0 + 4 * D), 8 * kC * (D + 8) / 2);
   __shared__ __attribute__((aligned(16))) float sm[SMEM_FLOATS];
   const int t = threadIdx.x;
   const int H = a.H;
   const int u = blockIdx.x / H, h = blockIdx.x - u * H;
   const ChunkRows cr = chunk_rows(a, u);
   const int64_t ch = static_cast<int64_t>(u) * H + h;
-  const float* GL = a.GL + ch * kC * D;
   auto in_idx = [&](int c, int d) { return ((cr.row0 + c) * H + h) * D + d; };
   // loads from pad rows (c >= len) read row 0 and are zeroed where used, so
   // no load sits inside a branch (whose end would wait for it)
@@ -1942,8 +1942,8 @@ __global__ __launch_bounds__(kChunkThreads) void kda_bwd_chunk_kernel(BwdArgs a)
   float dgc = 0.f;   // thread t < D: sum_n S[t][n] dS'[t][n]
   // G, k and q (times the scale; zero on pad rows) at this thread's positions
   // (rows 16 mt + 4 gq + i, columns 16 (dg_ NDT + q) + r16), read once in
-  // phase 1's epilogue: phase 2 shares the positions and phase 4 takes its
-  // LDS copies of G, k, q from them
+  // phase 1's epilogue (G formed there from g): phase 2 shares the positions
+  // and phase 4 takes its LDS copies of G, k, q from them
   // (q, k held as loaded: 16-bit inputs packed two to a register)
   typedef typename std::conditional<DTQ == 0, f4, uint2>::type H4;
   auto hload = [&](const void* src, int d) {   // rows 16 mt + 4 gq + i of column d (pad rows read row 0)
@@ -2085,16 +2085,50 @@ __global__ __launch_bounds__(kChunkThreads) void kda_bwd_chunk_kernel(BwdArgs a)
       }
       __syncthreads();
     }
-    // dq = dgq gamma; dG = dgq q gamma - dY k lambda; dk = dY lambda
+    // G_c = log2(e) sum_{c' <= c} g_c' at this thread's positions, from g:
+    // the prefix over the lane's four rows, plus the lane groups above it in
+    // the row tile (shuffles), plus the row tiles above (their sums through
+    // LDS, past phase 2's buffers).  G_{C-1} sums the four tile sums in the
+    // order the last row's prefix does, so the two agree bit for bit.
+    float* const sGs = sm + GS0;
 #pragma unroll
     for (int q = 0; q < NDT; ++q) {
       const int d = 16 * (dg_ * NDT + q) + r16;
-      gLast[q] = GL[(kC - 1) * D + d];
 #pragma unroll
-      for (int i = 0; i < 4; ++i) gH[q][i] = GL[(16 * mt + 4 * gq + i) * D + d];
+      for (int i = 0; i < 4; ++i) {
+        const int c = 16 * mt + 4 * gq + i;
+        const float x = ld1<DTG>(a.g, in_idx(c < cr.len ? c : 0, d));
+        gH[q][i] = (c < cr.len) ? x : 0.f;
+      }
       qH[q] = hload(a.q, d);
       kH[q] = hload(a.k, d);
     }
+#pragma unroll
+    for (int q = 0; q < NDT; ++q) {
+#pragma unroll
+      for (int i = 1; i < 4; ++i) gH[q][i] += gH[q][i - 1];
+      const float tot = gH[q][3];
+      const float t1 = __shfl_up(tot, 16), t2 = __shfl_up(tot, 32), t3 = __shfl_up(tot, 48);
+      const float ex = (gq >= 1 ? t1 : 0.f) + (gq >= 2 ? t2 : 0.f) + (gq >= 3 ? t3 : 0.f);
+#pragma unroll
+      for (int i = 0; i < 4; ++i) gH[q][i] += ex;
+      if (gq == 3) sGs[mt * D + 16 * (dg_ * NDT + q) + r16] = gH[q][3];
+    }
+    __syncthreads();
+#pragma unroll
+    for (int q = 0; q < NDT; ++q) {
+      const int d = 16 * (dg_ * NDT + q) + r16;
+      float pre = 0.f, run = 0.f;
+#pragma unroll
+      for (int m = 0; m < 4; ++m) {
+        if (m == mts) pre = run;
+        run += sGs[m * D + d];
+      }
+      gLast[q] = run * kLog2e;
+#pragma unroll
+      for (int i = 0; i < 4; ++i) gH[q][i] = (gH[q][i] + pre) * kLog2e;
+    }
+    // dq = dgq gamma; dG = dgq q gamma - dY k lambda; dk = dY lambda
 #pragma unroll
     for (int q = 0; q < NDT; ++q) {
       const int d = 16 * (dg_ * NDT + q) + r16;
@@ -2205,7 +2239,7 @@ __global__ __launch_bounds__(kChunkThreads) void kda_bwd_chunk_kernel(BwdArgs a)
   // start of phase 3, past its planes), [64][8] from phase 4 (per column tile)
   float* const sDbD = sBase + D;
   float* const sDb4 = sDbD + kC * 32;
-  static_assert(2 * kC * PC + 3 * kC * P + kC + 17 * D + 40 * kC <= SMEM_FLOATS, "phase 4 LDS");
+  static_assert(P4 <= GS0 && GS0 + 4 * D <= SMEM_FLOATS, "phase 4 LDS, below the sums of g");
   static_assert(8 * kC * (D + 8) / 2 <= 2 * kC * PC + 3 * kC * P + kC + 17 * D, "phase 3 planes end below sDbD");
   {
     constexpr int PB = D + 8;            // bf16 pitch: 16-byte aligned K blocks, rows 4 banks apart
@@ -2299,7 +2333,8 @@ __global__ __launch_bounds__(kChunkThreads) void kda_bwd_chunk_kernel(BwdArgs a)
       }
     if (t < kC) sB[t] = ld_b(t);
     if (t < D) {   // dg[c] = base + sum_{c' >= c} dG[c']: the G_C terms and the dz terms
-      float acc = dgc * ex2(GL[(kC - 1) * D + t]);
+      const float* sGs = sm + GS0;   // G_{C-1} of column t, summed as in phase 1's epilogue
+      float acc = dgc * ex2((((sGs[t] + sGs[D + t]) + sGs[2 * D + t]) + sGs[3 * D + t]) * kLog2e);
       for (int r = 0; r < 16; ++r) acc += sRed4[r * D + t];
       sBase[t] = acc;
     }

@@ -124,7 +124,6 @@ struct BwdArgs {
   float* dg;            // [B,T,H,dk]
   float* dbeta;         // [B,T,H]
   float* dh0;           // [B,H,dk,dv] or null
-  float* GL;            // [ch][C][dk] in-chunk cumsum of g, log2 units
   float* QG;            // [ch][C][dk] gamma * q (scaled)
   float* KL;            // [ch][C][dk] lambda * k
   float* GCV;           // [ch][dk]    gamma_C

@@ -375,10 +375,10 @@ def test_ut_solve_validation(L, args, status, needle):
 def test_chunk_bwd_workspace_size(L):
     NT = (4096 + 63) // 64
     ch = 4 * NT * 16
-    # fp32 arrays G, gamma q, lambda k, gamma_C, Aqk, T, W, U, S, v~, dS', dv~,
+    # fp32 arrays gamma q, lambda k, gamma_C, Aqk, T, W, U, S, v~, dS', dv~,
     # then the 16-bit inputs' fragment arrays lambda k, Aqk^T, (gamma q)^T, W^T,
     # W and (lambda k)^T
-    expected = sum(_align(n) for n in (ch * 64 * 128 * 4,) * 3 + (ch * 128 * 4, ch * 64 * 64 * 4, ch * 64 * 64 * 4)
+    expected = sum(_align(n) for n in (ch * 64 * 128 * 4,) * 2 + (ch * 128 * 4, ch * 64 * 64 * 4, ch * 64 * 64 * 4)
                    + (ch * 64 * 128 * 4,) * 2 + (ch * 128 * 128 * 4, ch * 64 * 128 * 4, ch * 128 * 128 * 4,
                                                  ch * 64 * 128 * 4)
                    + (ch * 16 * 1024, ch * 6 * 1024, ch * 16 * 1024, ch * 16 * 1024)
