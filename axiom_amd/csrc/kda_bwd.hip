@@ -384,21 +384,24 @@ __global__ __launch_bounds__(kPrepThreads, 4) void kda_bwd_prep_kernel(BwdArgs a
     ik.template put<P>(sK, 1.f);
     ig.template put<P>(sG, 1.f);
   };
-  auto cumsum_g = [&]() {            // 16 rows' loads in flight at a time
-    if (t < HD) {
-      float acc = 0.f;
+  // every thread: channel t % HD, rows 8 s .. 8 s + 7 (s = t / HD): the
+  // prefix over its rows, then the sums of the segments above it (through
+  // sTmp, which the triangular inversion alone uses otherwise); ends with a
+  // barrier before which sG must not be read
+  static_assert(NTH == 8 * HD && kC == 64, "eight 8-row segments per channel");
+  auto cumsum_g = [&]() {
+    const int d = t & (HD - 1), s8 = t / HD;
+    float x[8];
 #pragma unroll
-      for (int r0 = 0; r0 < kC; r0 += 16) {
-        float col[16];
+    for (int j = 0; j < 8; ++j) x[j] = sG[(8 * s8 + j) * P + d];
 #pragma unroll
-        for (int c = 0; c < 16; ++c) col[c] = sG[(r0 + c) * P + t];
+    for (int j = 1; j < 8; ++j) x[j] += x[j - 1];
+    sTmp[s8 * HD + d] = x[7];
+    __syncthreads();
+    float pre = 0.f;
+    for (int k = 0; k < s8; ++k) pre += sTmp[k * HD + d];
 #pragma unroll
-        for (int c = 0; c < 16; ++c) {
-          acc += col[c];
-          sG[(r0 + c) * P + t] = acc * kLog2e;
-        }
-      }
-    }
+    for (int j = 0; j < 8; ++j) sG[(8 * s8 + j) * P + d] = (x[j] + pre) * kLog2e;
   };
 
   // scores: Aqk (c >= i) to the workspace, L = beta_c Akk (c > i) to LDS,
@@ -583,10 +586,12 @@ __global__ __launch_bounds__(kPrepThreads, 4) void kda_bwd_prep_kernel(BwdArgs a
   iv.fetch(a.v, cr.row0, cr.len, H, h, HD * (NHALF - 1));
   invert_unit_lower64<PC, NTH>(sL, sT, sTmp);
   {
-    for (int e = t; e < kC * kC; e += NTH) {
-      const int c = e / kC, i = e - c * kC;
-      ws_st<EF>(a.TM, ch * kC * kC + e, sT[c * PC + i]);
-    }
+    static_assert(kC * kC == 8 * NTH, "eight entries of T per thread");
+    const int c = t >> 3, i0 = 8 * (t & 7);
+    const float* row = sT + c * PC + i0;
+    const int64_t o = ch * kC * kC + c * kC + i0;
+    ws_st4<EF>(a.TM, o, make_float4(row[0], row[1], row[2], row[3]));
+    ws_st4<EF>(a.TM, o + 4, make_float4(row[4], row[5], row[6], row[7]));
   }
   // W = T (beta gamma k), U = T (beta v) on the matrix cores, per half of
   // their columns (the last half first: its k and G are still staged); wave
