@@ -1710,11 +1710,16 @@ __device__ __forceinline__ void col_chain(const StateArgs& a, ColSmem<DK>& sm, i
 
     // The step is one stream of 16-byte LDS reads consumed in order (each
     // fragment feeds one MFMA per value tile of this wave):
-    //   items 0 .. 8*NJ-1    W and gamma*q fragments of row tile ct = i / (2*NJ)
-    //                        (alternating: P and O products of K step j),
+    //   items 0 .. 8*NJ-1    W and gamma*q fragments of K step j = i / 8, row
+    //                        tile ct = (i % 8) / 2 (alternating: P and O
+    //                        products), so consecutive products into one
+    //                        accumulator are eight items apart (measured:
+    //                        config 2 1 127 -> 1 086 us against row-tile-major
+    //                        order, bit-identical),
     //   next FA items        Aqk fragments,
     //   next NT items        gamma_C of channel tile dt (one float4 per lane),
-    //   last 2*NT items      lambda*k fragments of channel tile dt, K steps 0, 1.
+    //   last 2*NT items      lambda*k fragments, K step jj = 0 for every channel
+    //                        tile dt, then K step 1.
     // Each read is issued DEPTH items ahead of its use into a register ring,
     // so up to DEPTH reads are in flight at every wait (the lgkm counter
     // tracks 15), and a scheduling barrier per item keeps that order.
@@ -1729,14 +1734,16 @@ __device__ __forceinline__ void col_chain(const StateArgs& a, ColSmem<DK>& sm, i
       constexpr int i = decltype(ic)::value;
       const unsigned char* p;
       if constexpr (i < N_ROW) {
-        constexpr int ct = i / (2 * NJ), j = (i % (2 * NJ)) >> 1;
+        static_assert(kC == 64, "four row tiles per K step");
+        constexpr int j = i / 8, ct = (i % 8) >> 1;
         p = cur + (((i & 1) ? LY::OFF_Q : 0) + ct * NJ + j) * 1024 + l * 16;
       } else if constexpr (i < I_GC) {
         p = cur + (LY::OFF_A + (i - I_AQ)) * 1024 + l * 16;
       } else if constexpr (i < I_LK) {
         p = cur + LY::OFF_G + (16 * (i - I_GC) + 4 * gq) * 4;
       } else {
-        p = cur + (LY::OFF_L + (i - I_LK)) * 1024 + l * 16;
+        constexpr int jj = (i - I_LK) / NT, dt = (i - I_LK) % NT;
+        p = cur + (LY::OFF_L + 2 * dt + jj) * 1024 + l * 16;
       }
       return *reinterpret_cast<const uint4*>(p);
     };
@@ -1765,19 +1772,22 @@ __device__ __forceinline__ void col_chain(const StateArgs& a, ColSmem<DK>& sm, i
       __builtin_amdgcn_sched_barrier(0);
       const uint4 it = ring[i % RING];
       if constexpr (i < N_ROW) {
-        // P = W S and O = (gamma q) S, row tile ct; v~ = U - P once P is complete
-        constexpr int ct = i / (2 * NJ), j = (i % (2 * NJ)) >> 1;
+        // P = W S and O = (gamma q) S, K step j of row tile ct; v~ = U - P
+        // once every P is complete
+        constexpr int j = i / 8, ct = (i % 8) >> 1;
         const h8 A = __builtin_bit_cast(h8, it);
 #pragma unroll
         for (int cc = 0; cc < NC; ++cc) {
           if constexpr (i & 1) O[cc][ct] = mma32(O[cc][ct], A, Sb[cc][j]);
           else P[cc][ct] = mma32(P[cc][ct], A, Sb[cc][j]);
         }
-        if constexpr (i % (2 * NJ) == 2 * NJ - 1) {
+        if constexpr (i == N_ROW - 1) {
 #pragma unroll
           for (int cc = 0; cc < NC; ++cc)
 #pragma unroll
-            for (int e = 0; e < 4; ++e) Vt[cc][ct][e] = static_cast<float>(Ucur[cc][ct][e]) - P[cc][ct][e];
+            for (int t4 = 0; t4 < 4; ++t4)
+#pragma unroll
+              for (int e = 0; e < 4; ++e) Vt[cc][t4][e] = static_cast<float>(Ucur[cc][t4][e]) - P[cc][t4][e];
         }
       } else if constexpr (i < I_GC) {
         // O += Aqk v~ (keys at or before the row tile); fragments (ct,jj) = 00 10 20 21 30 31
@@ -1801,8 +1811,8 @@ __device__ __forceinline__ void col_chain(const StateArgs& a, ColSmem<DK>& sm, i
       } else if constexpr (i < I_LK) {
         Gc[i - I_GC] = __builtin_bit_cast(f4, it);
       } else {
-        // S <- gamma_C S + (lambda k)^T v~ for channel tile dt
-        constexpr int dt = (i - I_LK) >> 1, jj = (i - I_LK) & 1;
+        // S <- gamma_C S + (lambda k)^T v~, K step jj of channel tile dt
+        constexpr int jj = (i - I_LK) / NT, dt = (i - I_LK) % NT;
         const h8 A = __builtin_bit_cast(h8, it);
 #pragma unroll
         for (int cc = 0; cc < NC; ++cc) {
