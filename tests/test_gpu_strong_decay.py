@@ -86,16 +86,18 @@ def test_forward_decay_spikes(cuda, prec, d):
     assert_close("ht", ht, ht_ref, TOL[prec])
 
 
-@pytest.mark.parametrize("prec,d", [("bf16", 128), ("fp32", 64)])
-def test_backward_strong_decay(cuda, prec, d):
+@pytest.mark.parametrize("prec,d,T", [("bf16", 128, 192), ("fp32", 64, 192), ("bf16", 64, 150)])
+def test_backward_strong_decay(cuda, prec, d, T):
+    # (T = 150: a ragged last chunk, whose pad rows the chunk kernel's
+    # in-kernel cumsum of g must treat as zero decay)
     import axiom_amd
-    x = _strong(1, 192, 2, d, seed=31 + d, dtype=prec)
+    x = _strong(1, T, 2, d, seed=31 + d, dtype=prec)
     rng = np.random.default_rng(5)
-    do = rng.standard_normal((1, 192, 2, d)).astype(np.float32)
+    do = rng.standard_normal((1, T, 2, d)).astype(np.float32)
     dS = (rng.standard_normal((1, 2, d, d)) * 0.1).astype(np.float32)
     dt = TDT[prec]
     ts = [to_dev(x[n], dt, cuda) for n in ("q", "k", "v", "g", "beta")]
-    print(f"[strong decay bwd] {prec} d={d}", flush=True)
+    print(f"[strong decay bwd] {prec} d={d} T={T}", flush=True)
     got = axiom_amd.kda_chunk_bwd(*ts, to_dev(do, torch.float32, cuda), dht=to_dev(dS, torch.float32, cuda),
                                   initial_state=to_dev(x["h0"], torch.float32, cuda))
     torch.cuda.synchronize()
